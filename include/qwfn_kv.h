@@ -1,0 +1,158 @@
+/*
+ * qwfn_kv.h -- C ABI of the MI355X (gfx950) q8_0 KV-cache path.
+ *
+ * This library replaces, behind a plain C boundary, the device work that the
+ * reference engine (thomaskleiven/QwFN-hybrid) hands to ggml-cuda for its
+ * attention layers:
+ *
+ *   ggml_cpy      F32 -> Q8_0   cache append at n_past      qwfn_graph.cpp:376-383, :916-921
+ *   ggml_set_rows F32 -> Q8_0   decode append at write_idx  qwfn_graph.cpp:623-624
+ *   ggml_get_rows on I32 words  raw gather of cache rows    qwfn_graph.cpp:638-645
+ *   ggml_flash_attn_ext         decode / verify / prefill   qwfn_graph.cpp:469-471, :698-699
+ *   ggml_backend_tensor_set/copy snapshot restore           qwfn_engine.cpp:1029-1053
+ *
+ * Conventions
+ *   - Tensors are described ggml-style: ne[4] element counts, nb[4] byte
+ *     strides, a type code using ggml's numbering, and a device address. For
+ *     Q8_0, ne[0] counts values (a multiple of 32) and nb[0] is 34, one block
+ *     { fp16 d; int8 qs[32]; }.
+ *   - Every entry point returns QWFN_OK (0) or a negative QWFN_E* code and sets
+ *     a thread-local message readable with qwfn_last_error(). No exception
+ *     crosses the boundary.
+ *   - Shapes, strides, alignment and host-visible index ranges are validated on
+ *     the host BEFORE anything is launched, so an invalid call never touches
+ *     the GPU. Indices that live in device memory are bounds-checked by the
+ *     kernels: an out-of-range index is skipped (never dereferenced) and raises
+ *     a device flag read by qwfn_device_status().
+ *   - The caller owns all memory. Calls are stream-ordered and asynchronous on
+ *     the given stream (a hipStream_t passed as void*; NULL is the null stream).
+ */
+#ifndef QWFN_KV_H
+#define QWFN_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QWFN_KV_ABI_VERSION 1
+
+/* ggml type numbering (ggml.h: GGML_TYPE_F32 = 0, F16 = 1, Q8_0 = 8, I32 = 26) */
+enum qwfn_type {
+    QWFN_TYPE_F32  = 0,
+    QWFN_TYPE_F16  = 1,
+    QWFN_TYPE_Q8_0 = 8,
+    QWFN_TYPE_I32  = 26,
+};
+
+enum qwfn_status {
+    QWFN_OK      =  0,
+    QWFN_EINVAL  = -1,  /* bad argument, shape or type            */
+    QWFN_ERANGE  = -2,  /* index or row outside the tensor        */
+    QWFN_EALIGN  = -3,  /* misaligned address, stride or row size */
+    QWFN_ENOTSUP = -4,  /* valid in ggml, not supported here      */
+    QWFN_EDEVICE = -5,  /* HIP runtime error                      */
+    QWFN_ENOMEM  = -6,  /* allocation failure / workspace too small */
+    QWFN_ESIZE   = -7,  /* snapshot part count or size mismatch   */
+};
+
+/* q8_0 quantiser rounding variant (ggml-cpu has two; they differ on ties and
+ * on 1-ulp differences of the inverse scale):
+ *   QWFN_Q8_X86 : quantize_row_q8_0 x86 AVX/AVX2 path: id = 127/amax, round half to even
+ *   QWFN_Q8_REF : quantize_row_q8_0_ref:               id = 1/(amax/127), round half away from 0 */
+enum qwfn_q8_variant { QWFN_Q8_REF = 0, QWFN_Q8_X86 = 1 };
+
+typedef struct qwfn_tensor {
+    void *   data;   /* device address of element [0,0,0,0]  */
+    int32_t  type;   /* enum qwfn_type                       */
+    int32_t  pad_;
+    int64_t  ne[4];  /* elements per dimension               */
+    size_t   nb[4];  /* byte stride per dimension            */
+} qwfn_tensor;
+
+/* ----------------------------------------------------------------- runtime */
+
+int          qwfn_abi_version(void);
+const char * qwfn_last_error(void);
+/* Make `device` current for this thread and create the per-device status word. */
+int          qwfn_init(int device);
+/* Synchronise `stream`, then read and clear the device-side error flags
+ * (bit 0: set_rows index out of range; bit 1: get_rows index out of range). */
+int          qwfn_device_status(void * stream, uint32_t * flags);
+
+/* ------------------------------------------------------------ cache append */
+
+/* ggml_set_rows(dst, src, idx): dst Q8_0 [ne0, n_rows] (row stride nb[1]),
+ * src F32 [ne0, n] (nb[0] == 4), idx I32 [n] in device memory. Row i of src is
+ * quantised into row idx[i] of dst. Replaces qwfn_graph.cpp:623-624
+ * (qsa_dec_kv_write) and the MTP head's decode append. */
+int qwfn_set_rows_q8_0(const qwfn_tensor * dst, const qwfn_tensor * src, const qwfn_tensor * idx,
+                       int variant, void * stream);
+
+/* ggml_cpy(src, dst): src F32 [ne0, n], dst Q8_0 [ne0, n] (a view whose rows
+ * start at the append position). Replaces qwfn_graph.cpp:376-383 (kv_append)
+ * and :916-921 (mtp_head_kv). */
+int qwfn_cpy_f32_q8_0(const qwfn_tensor * src, const qwfn_tensor * dst, int variant, void * stream);
+
+/* -------------------------------------------------------------- gather */
+
+/* ggml_get_rows(src, idx) on I32 words: src I32 [ne0, n_rows], idx I32 [n]
+ * (device), dst I32 [ne0, n]. Copies raw cache bytes, no dequantisation.
+ * Replaces qwfn_graph.cpp:638-645 (qsa_gather, raw branch). */
+int qwfn_get_rows_i32(const qwfn_tensor * src, const qwfn_tensor * idx, const qwfn_tensor * dst,
+                      void * stream);
+
+/* Per-segment gather for per-KV-head selections: for each segment s in
+ * [0, n_seg) and i in [0, n_idx), copy seg_bytes bytes starting at byte
+ * seg_off + s*seg_stride of row idx[s*n_idx + i] of src into
+ * dst + s*dst_seg_stride + i*dst_row_stride. idx is device memory.
+ * seg_bytes, offsets and strides must be multiples of 4. No ggml counterpart:
+ * it is the reference's raw get_rows (qwfn_graph.cpp:638-645) applied per KV
+ * head instead of once for both heads. */
+int qwfn_kv_gather_segments(const void * src, size_t src_row_stride, int64_t src_rows,
+                            size_t seg_off, size_t seg_stride, size_t seg_bytes, int32_t n_seg,
+                            const int32_t * idx, int64_t n_idx,
+                            void * dst, size_t dst_row_stride, size_t dst_seg_stride, void * stream);
+
+/* ------------------------------------------------------- flash attention */
+
+/* ggml_flash_attn_ext(q, k, v, mask, scale, max_bias, logit_softcap) with F32
+ * accumulation (ggml_prec_set_acc(.., GGML_PREC_F32), qwfn_graph.cpp:471, :699):
+ *   q    F32  [D, T, n_head, B]          (nb[0] == 4; any other strides)
+ *   k, v Q8_0 [D, n_kv, n_head_kv, B|1] (nb[0] == 34; nb[1] row, nb[2] head stride)
+ *   mask F16  [n_kv', T', mh, mb] or NULL; n_kv' >= n_kv, T' >= T,
+ *             n_head % mh == 0, B % mb == 0 (broadcast as in ggml)
+ *   dst  F32  [D, n_head, T, B] contiguous
+ * D must be 256 (the model's head size). n_head % n_head_kv == 0.
+ * max_bias and logit_softcap must be 0 (the reference never sets them).
+ * Semantics follow ggml-cpu's q8_0 path: Q is requantised to q8_0 with
+ * `variant`, scores are sum_b d_k*d_q*isum_b, masked (-inf) keys are skipped,
+ * softmax is online, V is dequantised q*d. A fully masked row gives 0.
+ * ws: device workspace of at least qwfn_fattn_workspace_size() bytes, or NULL
+ * to use a library-owned buffer (allocated on first use, not graph-capturable). */
+size_t qwfn_fattn_workspace_size(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v);
+int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
+                             const qwfn_tensor * mask, float scale, float max_bias, float logit_softcap,
+                             const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes, void * stream);
+
+/* ------------------------------------------------------ snapshot restore */
+
+enum qwfn_copy_src { QWFN_SRC_DEVICE = 0, QWFN_SRC_HOST = 1 };
+
+/* Restore snapshot parts into n_slots sequence slots:
+ *   for p in [0, n_parts), s in [0, n_slots): copy bytes[p] bytes from src[p]
+ *   to dst[s*n_parts + p].
+ * src_kind QWFN_SRC_DEVICE: one fused kernel reads every source byte once and
+ * writes it to all slots. QWFN_SRC_HOST: src are host pointers (pinned for
+ * asynchronous copies); slot 0 is filled over the host link, slots 1.. by the
+ * device broadcast from slot 0. Replaces the per-part ggml_backend_tensor_set
+ * loop of engine::snapshot_load (qwfn_engine.cpp:1039-1042). */
+int qwfn_state_restore(const void * const * src, const size_t * bytes, void * const * dst,
+                       int32_t n_parts, int32_t n_slots, int32_t src_kind, void * stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

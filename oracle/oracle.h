@@ -1,0 +1,98 @@
+/*
+ * CPU oracle for the q8_0 KV-cache path. TEST INFRASTRUCTURE ONLY.
+ *
+ * This library is the checker: only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py load it. The product path (libqwfn_kv.so) never
+ * links, loads or calls it.
+ *
+ * It restates, in plain C, the ggml-cpu semantics the reference engine relies on
+ * (ggml from unslothai/llama.cpp @ ca1426903, not vendored in the reference tree,
+ * see scripts/build.sh:8-16 and CMakeLists.txt:20-31 of the reference):
+ *   - block_q8_0 = { fp16 d; int8 qs[32]; }  (34 bytes per 32 values)
+ *   - quantize_row_q8_0: scalar "_ref" variant and the x86 AVX/AVX2 variant
+ *   - dequantize_row_q8_0, vec_dot_q8_0_q8_0 (scalar and x86 summation order)
+ *   - set_rows / cpy F32 -> Q8_0 (reference call sites qwfn_graph.cpp:370-384,
+ *     :612-628), get_rows on I32 words (qwfn_graph.cpp:632-645)
+ *   - flash_attn_ext, the CPU one-chunk loop (Q requantised to q8_0, online
+ *     softmax with expf, V dequantised to F32), as called at qwfn_graph.cpp:469
+ *     and :698
+ *   - an fp64 textbook attention used as a second referee
+ *   - snapshot part layout (qwfn_engine.cpp:988-999)
+ *
+ * Pinning status of each function is recorded next to its declaration.
+ */
+#ifndef QWFN_ORACLE_H
+#define QWFN_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ORACLE_QK8_0 32
+#define ORACLE_Q8_0_BLOCK_BYTES 34
+
+enum { ORACLE_Q8_REF = 0, ORACLE_Q8_X86 = 1 };
+
+/* ---- deterministic PRNG: SplitMix64-seeded xoshiro256**, Box-Muller in double ----
+ * Pinned by the published xoshiro256** / SplitMix64 reference outputs (tests). */
+typedef struct { uint64_t s[4]; } oracle_rng;
+void     oracle_rng_seed(oracle_rng * r, uint64_t seed);
+uint64_t oracle_rng_next(oracle_rng * r);
+uint64_t oracle_splitmix64(uint64_t * state);
+/* stream key for per-tensor sub-streams: hash(seed, a, b, c) */
+uint64_t oracle_stream_key(uint64_t seed, uint64_t a, uint64_t b, uint64_t c);
+/* n normal values N(0, stddev^2) rounded to float */
+void oracle_fill_normal(uint64_t key, float * out, int64_t n, double stddev);
+/* n uniform values in [0, 1) as float (top 24 bits) */
+void oracle_fill_uniform(uint64_t key, float * out, int64_t n);
+
+/* ---- fp16 <-> fp32, IEEE round-to-nearest-even (ggml's GGML_FP32_TO_FP16).
+ * Pinned against numpy.float16 over all 2^16 patterns and random floats. */
+uint16_t oracle_fp32_to_fp16(float f);
+float    oracle_fp16_to_fp32(uint16_t h);
+
+/* ---- q8_0 quantisation.  variant: ORACLE_Q8_REF or ORACLE_Q8_X86.
+ * Pinned by closed-form invariants, crafted tie / 1-ulp cases, brute force. */
+void  oracle_quantize_row_q8_0(const float * x, void * y, int64_t k, int variant);
+void  oracle_dequantize_row_q8_0(const void * x, float * y, int64_t k);
+/* variant selects the summation order: REF = scalar, X86 = AVX2 8-lane fma order */
+float oracle_vec_dot_q8_0_q8_0(int64_t n, const void * x, const void * y, int variant);
+
+/* ---- set_rows / cpy / get_rows.  Return 0 or a negative error code. ---- */
+int oracle_set_rows_q8_0(void * dst, size_t dst_nb1, int64_t dst_rows,
+                         const float * src, size_t src_nb1, int64_t ne0,
+                         const int32_t * idx, int64_t n, int variant);
+int oracle_cpy_f32_q8_0(void * dst, size_t dst_nb1, int64_t first_row, int64_t dst_rows,
+                        const float * src, size_t src_nb1, int64_t ne0, int64_t n, int variant);
+int oracle_get_rows(const void * src, size_t src_nb1, int64_t src_rows, size_t row_bytes,
+                    const int32_t * idx, int64_t n, void * dst, size_t dst_nb1);
+
+/* ---- attention ----
+ * A ggml-style view: ne[4] elements, nb[4] byte strides. For q8_0 tensors
+ * ne[0] counts values and nb[0] is 34 (one block). */
+typedef struct {
+    const void * data;
+    int64_t ne[4];
+    size_t  nb[4];
+} oracle_view;
+
+/* ggml flash_attn_ext (CPU one-chunk loop), F32 Q, q8_0 K/V, optional F16 mask.
+ * dst is F32 [DV, n_head, T, B] contiguous.  q_variant / dot_variant select the
+ * quantiser used for Q and the vec_dot summation order.  n_threads >= 1. */
+int oracle_flash_attn_ext_q8_0(const oracle_view * q, const oracle_view * k, const oracle_view * v,
+                               const oracle_view * mask, float scale, float * dst,
+                               int q_variant, int dot_variant, int n_threads);
+
+/* fp64 textbook softmax(Q K^T * scale + mask) V over dequantised K/V.
+ * quantize_q: 0 uses the F32 Q as given, 1/2 requantises Q with REF/X86 first.
+ * Fully masked rows give 0 (as ggml).  dst as above, in double. */
+int oracle_attn_f64(const oracle_view * q, const oracle_view * k, const oracle_view * v,
+                    const oracle_view * mask, double scale, double * dst, int quantize_q);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

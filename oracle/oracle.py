@@ -1,0 +1,249 @@
+"""ctypes binding of the CPU oracle (liboracle.so). TEST INFRASTRUCTURE ONLY.
+
+Only tests/, ``__graft_entry__.smoke()`` and bench.py's cpu_baseline leg import
+this module, and only as the checker. The product library never loads it.
+
+The C sources restate ggml-cpu semantics for the q8_0 KV-cache path; see the
+header of oracle.c for the ggml functions and reference call sites they follow.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+Q8_REF = 0
+Q8_X86 = 1
+QK8_0 = 32
+Q8_0_BLOCK_BYTES = 34
+
+
+class View(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p),
+                ("ne", ctypes.c_int64 * 4),
+                ("nb", ctypes.c_size_t * 4)]
+
+
+_lib = None
+
+
+def build(force: bool = False) -> str:
+    if force or not os.path.exists(LIB_PATH):
+        subprocess.run(["make", "-s", "-C", HERE, "-B" if force else "liboracle.so"], check=True)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        vp, i64, u64, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_uint64, ctypes.c_size_t
+        L.oracle_splitmix64.argtypes = [ctypes.POINTER(u64)]
+        L.oracle_splitmix64.restype = u64
+        L.oracle_rng_seed.argtypes = [vp, u64]
+        L.oracle_rng_next.argtypes = [vp]
+        L.oracle_rng_next.restype = u64
+        L.oracle_stream_key.argtypes = [u64, u64, u64, u64]
+        L.oracle_stream_key.restype = u64
+        L.oracle_fill_normal.argtypes = [u64, vp, i64, ctypes.c_double]
+        L.oracle_fill_uniform.argtypes = [u64, vp, i64]
+        L.oracle_fp32_to_fp16.argtypes = [ctypes.c_float]
+        L.oracle_fp32_to_fp16.restype = ctypes.c_uint16
+        L.oracle_fp16_to_fp32.argtypes = [ctypes.c_uint16]
+        L.oracle_fp16_to_fp32.restype = ctypes.c_float
+        L.oracle_quantize_row_q8_0.argtypes = [vp, vp, i64, ctypes.c_int]
+        L.oracle_dequantize_row_q8_0.argtypes = [vp, vp, i64]
+        L.oracle_vec_dot_q8_0_q8_0.argtypes = [i64, vp, vp, ctypes.c_int]
+        L.oracle_vec_dot_q8_0_q8_0.restype = ctypes.c_float
+        L.oracle_set_rows_q8_0.argtypes = [vp, sz, i64, vp, sz, i64, vp, i64, ctypes.c_int]
+        L.oracle_cpy_f32_q8_0.argtypes = [vp, sz, i64, i64, vp, sz, i64, i64, ctypes.c_int]
+        L.oracle_get_rows.argtypes = [vp, sz, i64, sz, vp, i64, vp, sz]
+        L.oracle_flash_attn_ext_q8_0.argtypes = [ctypes.POINTER(View)] * 4 + [
+            ctypes.c_float, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.oracle_attn_f64.argtypes = [ctypes.POINTER(View)] * 4 + [ctypes.c_double, vp, ctypes.c_int]
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+# ------------------------------------------------------------------ PRNG
+
+def stream_key(seed: int, a: int = 0, b: int = 0, c: int = 0) -> int:
+    return int(lib().oracle_stream_key(seed, a, b, c))
+
+
+def normal(key: int, n: int, stddev: float = 1.0) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    lib().oracle_fill_normal(key, _p(out), n, stddev)
+    return out
+
+
+def uniform(key: int, n: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    lib().oracle_fill_uniform(key, _p(out), n)
+    return out
+
+
+def splitmix64_stream(state: int, n: int) -> list[int]:
+    s = ctypes.c_uint64(state)
+    return [int(lib().oracle_splitmix64(ctypes.byref(s))) for _ in range(n)]
+
+
+def xoshiro_stream(seed: int, n: int) -> list[int]:
+    st = (ctypes.c_uint64 * 4)()
+    lib().oracle_rng_seed(st, seed)
+    return [int(lib().oracle_rng_next(st)) for _ in range(n)]
+
+
+# ------------------------------------------------------------------ q8_0
+
+def fp32_to_fp16_bits(x: np.ndarray) -> np.ndarray:
+    f = lib().oracle_fp32_to_fp16
+    return np.array([f(float(v)) for v in np.asarray(x, np.float32).ravel()], dtype=np.uint16)
+
+
+def fp16_bits_to_fp32(h: np.ndarray) -> np.ndarray:
+    f = lib().oracle_fp16_to_fp32
+    return np.array([f(int(v)) for v in np.asarray(h, np.uint16).ravel()], dtype=np.float32)
+
+
+def quantize(x: np.ndarray, variant: int = Q8_X86) -> np.ndarray:
+    """F32 [..., k] -> q8_0 bytes [..., k/32*34] (uint8)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    k = x.shape[-1]
+    assert k % QK8_0 == 0
+    out = np.empty(x.shape[:-1] + (k // QK8_0 * Q8_0_BLOCK_BYTES,), dtype=np.uint8)
+    lib().oracle_quantize_row_q8_0(_p(x), _p(out), x.size, variant)
+    return out
+
+
+def dequantize(y: np.ndarray) -> np.ndarray:
+    y = np.ascontiguousarray(y, dtype=np.uint8)
+    nbytes = y.shape[-1]
+    assert nbytes % Q8_0_BLOCK_BYTES == 0
+    k = nbytes // Q8_0_BLOCK_BYTES * QK8_0
+    out = np.empty(y.shape[:-1] + (k,), dtype=np.float32)
+    lib().oracle_dequantize_row_q8_0(_p(y), _p(out), out.size)
+    return out
+
+
+def vec_dot(x: np.ndarray, y: np.ndarray, variant: int = Q8_X86) -> float:
+    x = np.ascontiguousarray(x, np.uint8)
+    y = np.ascontiguousarray(y, np.uint8)
+    n = x.size // Q8_0_BLOCK_BYTES * QK8_0
+    return float(lib().oracle_vec_dot_q8_0_q8_0(n, _p(x), _p(y), variant))
+
+
+def set_rows(cache: np.ndarray, src: np.ndarray, idx: np.ndarray, variant: int = Q8_X86) -> None:
+    """In place on a uint8 cache [n_rows, row_bytes]; src F32 [n, ne0]; idx I32 [n]."""
+    src = np.ascontiguousarray(src, np.float32)
+    idx = np.ascontiguousarray(idx, np.int32)
+    rc = lib().oracle_set_rows_q8_0(_p(cache), cache.strides[0], cache.shape[0], _p(src), src.strides[0],
+                                    src.shape[1], _p(idx), idx.size, variant)
+    if rc:
+        raise ValueError(f"oracle set_rows failed ({rc})")
+
+
+def cpy(cache: np.ndarray, src: np.ndarray, first_row: int, variant: int = Q8_X86) -> None:
+    src = np.ascontiguousarray(src, np.float32)
+    rc = lib().oracle_cpy_f32_q8_0(_p(cache), cache.strides[0], first_row, cache.shape[0], _p(src),
+                                   src.strides[0], src.shape[1], src.shape[0], variant)
+    if rc:
+        raise ValueError(f"oracle cpy failed ({rc})")
+
+
+def get_rows(src: np.ndarray, idx: np.ndarray, row_bytes: int | None = None, col_off: int = 0) -> np.ndarray:
+    """Copy row_bytes bytes (from byte col_off) of each indexed row of a uint8 [rows, stride] array."""
+    idx = np.ascontiguousarray(idx, np.int32)
+    rb = src.shape[1] - col_off if row_bytes is None else row_bytes
+    dst = np.zeros((idx.size, rb), dtype=np.uint8)
+    base = src[:, col_off:]
+    rc = lib().oracle_get_rows(base.ctypes.data, src.strides[0], src.shape[0], rb, _p(idx), idx.size,
+                               _p(dst), dst.strides[0])
+    if rc:
+        raise ValueError(f"oracle get_rows failed ({rc})")
+    return dst
+
+
+# ------------------------------------------------------------------ attention
+
+def view(data: np.ndarray, ne, nb) -> View:
+    v = View()
+    v.data = data.ctypes.data
+    for i in range(4):
+        v.ne[i] = int(ne[i]) if i < len(ne) else 1
+    last = 0
+    for i in range(4):
+        if i < len(nb):
+            v.nb[i] = int(nb[i])
+            last = v.nb[i] * v.ne[i]
+        else:
+            v.nb[i] = last
+            last = v.nb[i] * v.ne[i]
+    return v
+
+
+def flash_attn_ext(qv: View, kv: View, vv: View, mv: View | None, scale: float, out_shape,
+                   q_variant: int = Q8_X86, dot_variant: int = Q8_X86, n_threads: int = 1) -> np.ndarray:
+    dst = np.zeros(out_shape, dtype=np.float32)
+    rc = lib().oracle_flash_attn_ext_q8_0(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv),
+                                          ctypes.byref(mv) if mv is not None else None, scale, _p(dst),
+                                          q_variant, dot_variant, n_threads)
+    if rc:
+        raise ValueError(f"oracle flash_attn_ext failed ({rc})")
+    return dst
+
+
+def attn_f64(qv: View, kv: View, vv: View, mv: View | None, scale: float, out_shape,
+             quantize_q: int = 0) -> np.ndarray:
+    dst = np.zeros(out_shape, dtype=np.float64)
+    rc = lib().oracle_attn_f64(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv),
+                               ctypes.byref(mv) if mv is not None else None, scale, _p(dst), quantize_q)
+    if rc:
+        raise ValueError(f"oracle attn_f64 failed ({rc})")
+    return dst
+
+
+def cache_views(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, n_kv: int, n_head_kv: int, hd: int):
+    """ggml views for the reference's layout.
+
+    q: F32 [T, n_head, hd] (the projection's natural order; the graph permutes it
+    to [hd, T, n_head], qwfn_graph.cpp:466); kc/vc: uint8 caches [n_ctx, row_bytes]
+    token-major, KV head h at byte 34*(hd/32)*h (qwfn_graph.cpp:461-464).
+    """
+    T, nh, _ = q.shape
+    seg = hd // QK8_0 * Q8_0_BLOCK_BYTES
+    qv = view(q, (hd, T, nh, 1), (4, nh * hd * 4, hd * 4, T * nh * hd * 4))
+    kv = view(kc, (hd, n_kv, n_head_kv, 1), (Q8_0_BLOCK_BYTES, kc.strides[0], seg, kc.strides[0] * n_kv))
+    vv = view(vc, (hd, n_kv, n_head_kv, 1), (Q8_0_BLOCK_BYTES, vc.strides[0], seg, vc.strides[0] * n_kv))
+    return qv, kv, vv
+
+
+def mask_view(mask_f16_bits: np.ndarray) -> View:
+    """mask: uint16 F16 bits [T, n_kv] (ggml [n_kv, T])."""
+    T, n_kv = mask_f16_bits.shape
+    return view(mask_f16_bits, (n_kv, T, 1, 1), (2, mask_f16_bits.strides[0], mask_f16_bits.strides[0] * T,
+                                                 mask_f16_bits.strides[0] * T))
+
+
+F16_NEG_INF = 0xFC00
+F16_ZERO = 0x0000
+
+
+def causal_mask(T: int, n_past: int, n_kv: int | None = None) -> np.ndarray:
+    """F16 bits [T, n_kv]: query i sees rows <= n_past + i (qwfn_engine.cpp:2093-2098, :1261-1271)."""
+    n_kv = n_past + T if n_kv is None else n_kv
+    m = np.full((T, n_kv), F16_NEG_INF, dtype=np.uint16)
+    for i in range(T):
+        m[i, :min(n_kv, n_past + i + 1)] = F16_ZERO
+    return m

@@ -1,0 +1,235 @@
+// Byte-movement kernels of the KV path: raw row gather and snapshot restore.
+//
+// Gather: ggml_get_rows on the cache viewed as I32 words (qwfn_graph.cpp:638-645)
+// copies whole 544-byte rows of selected cells, no dequantisation; the
+// per-segment form gathers one KV head's 272-byte half rows from per-head
+// index lists. Each lane moves 16 bytes when rows and strides allow it, else 4.
+//
+// Restore: engine::snapshot_load copies each snapshot part into the state with
+// ggml_backend_tensor_set (qwfn_engine.cpp:1039-1042). Here a device-resident
+// snapshot is broadcast into n_slots sequence slots by one kernel that reads
+// each source byte once and writes it n_slots times.
+#include "qwfn_common.h"
+
+#include <algorithm>
+#include <vector>
+
+namespace qwfn {
+namespace {
+
+constexpr int COPY_THREADS = 256;
+
+// ------------------------------------------------------------------ gather
+
+struct gather_args {
+    const char *    src;
+    size_t          src_row_stride;
+    int64_t         src_rows;
+    size_t          seg_off;
+    size_t          seg_stride;
+    const int32_t * idx;       // [n_seg][n_idx]
+    int64_t         n_idx;
+    char *          dst;
+    size_t          dst_row_stride;
+    size_t          dst_seg_stride;
+    int32_t         units;     // copy units (16 or 4 bytes) per segment
+    int32_t         n_seg;
+    uint32_t *      status;
+};
+
+template <typename U>
+__global__ __launch_bounds__(COPY_THREADS) void k_gather(gather_args a) {
+    const int64_t total = (int64_t) a.n_seg * a.n_idx * a.units;
+    for (int64_t u = (int64_t) blockIdx.x * COPY_THREADS + threadIdx.x; u < total;
+         u += (int64_t) gridDim.x * COPY_THREADS) {
+        const int64_t row = u / a.units;               // (seg, i) flattened
+        const int32_t part = (int32_t) (u - row * a.units);
+        const int64_t seg = row / a.n_idx;
+        const int64_t i = row - seg * a.n_idx;
+        const int32_t r = a.idx[row];
+        if (r < 0 || r >= a.src_rows) {
+            if (part == 0) atomicOr(a.status, DEVERR_GET_ROWS_INDEX);
+            continue;
+        }
+        const U * s = (const U *) (a.src + (size_t) r * a.src_row_stride + a.seg_off + (size_t) seg * a.seg_stride) + part;
+        U * d = (U *) (a.dst + (size_t) seg * a.dst_seg_stride + (size_t) i * a.dst_row_stride) + part;
+        *d = *s;
+    }
+}
+
+int launch_gather(gather_args a, size_t seg_bytes, hipStream_t stream) {
+    const bool v16 = seg_bytes % 16 == 0 && a.src_row_stride % 16 == 0 && a.seg_off % 16 == 0 &&
+                     a.seg_stride % 16 == 0 && a.dst_row_stride % 16 == 0 && a.dst_seg_stride % 16 == 0 &&
+                     is_aligned(a.src, 16) && is_aligned(a.dst, 16);
+    a.units = (int32_t) (seg_bytes / (v16 ? 16 : 4));
+    const int64_t total = (int64_t) a.n_seg * a.n_idx * a.units;
+    if (total == 0) return QWFN_OK;
+    const int64_t grid = std::min<int64_t>((total + COPY_THREADS - 1) / COPY_THREADS, 65536);
+    if (v16) hipLaunchKernelGGL(k_gather<uint4>, dim3((unsigned) grid), dim3(COPY_THREADS), 0, stream, a);
+    else     hipLaunchKernelGGL(k_gather<uint32_t>, dim3((unsigned) grid), dim3(COPY_THREADS), 0, stream, a);
+    return hip_check(hipGetLastError(), "gather launch");
+}
+
+// ------------------------------------------------------------------ restore
+
+constexpr int RESTORE_MAX_PARTS = 16;   // per launch
+constexpr int RESTORE_MAX_SLOTS = 8;
+
+struct restore_args {
+    const char * src[RESTORE_MAX_PARTS];
+    char *       dst[RESTORE_MAX_SLOTS][RESTORE_MAX_PARTS];
+    int64_t      start[RESTORE_MAX_PARTS + 1];   // prefix sum of 16-byte units
+    int32_t      n_parts;
+    int32_t      n_slots;
+};
+
+// 16-byte units; each source unit is read once and stored to every slot.
+__global__ __launch_bounds__(COPY_THREADS) void k_restore16(restore_args a) {
+    const int64_t total = a.start[a.n_parts];
+    for (int64_t u = (int64_t) blockIdx.x * COPY_THREADS + threadIdx.x; u < total;
+         u += (int64_t) gridDim.x * COPY_THREADS) {
+        int p = 0;
+        while (p + 1 < a.n_parts && u >= a.start[p + 1]) p++;
+        const int64_t off = u - a.start[p];
+        const uint4 v = ((const uint4 *) a.src[p])[off];
+        for (int s = 0; s < a.n_slots; s++) ((uint4 *) a.dst[s][p])[off] = v;
+    }
+}
+
+// Byte tails and parts that are not 16-byte aligned.
+__global__ __launch_bounds__(COPY_THREADS) void k_restore_bytes(const char * src, char * const * dsts_unused,
+                                                               char * d0, char * d1, char * d2, char * d3,
+                                                               char * d4, char * d5, char * d6, char * d7,
+                                                               int32_t n_slots, int64_t n) {
+    (void) dsts_unused;
+    char * d[RESTORE_MAX_SLOTS] = {d0, d1, d2, d3, d4, d5, d6, d7};
+    for (int64_t i = (int64_t) blockIdx.x * COPY_THREADS + threadIdx.x; i < n; i += (int64_t) gridDim.x * COPY_THREADS) {
+        const char v = src[i];
+        for (int s = 0; s < n_slots; s++) d[s][i] = v;
+    }
+}
+
+int restore_device(const char * const * src, const size_t * bytes, char * const * dst, int n_parts, int n_slots,
+                   int slot0, hipStream_t stream) {
+    // dst is [n_slots_total][n_parts]; slots [slot0, slot0 + n_slots) are written.
+    for (int s0 = 0; s0 < n_slots; s0 += RESTORE_MAX_SLOTS) {
+        const int ns = std::min(RESTORE_MAX_SLOTS, n_slots - s0);
+        int p = 0;
+        while (p < n_parts) {
+            restore_args a{};
+            a.n_slots = ns;
+            int np = 0;
+            int64_t units = 0;
+            for (; p < n_parts && np < RESTORE_MAX_PARTS; p++) {
+                const size_t b = bytes[p];
+                bool aligned = is_aligned(src[p], 16);
+                for (int s = 0; s < ns; s++) aligned = aligned && is_aligned(dst[(size_t) (slot0 + s0 + s) * n_parts + p], 16);
+                const size_t main = aligned ? (b / 16) * 16 : 0;
+                if (main) {
+                    a.src[np] = src[p];
+                    for (int s = 0; s < ns; s++) a.dst[s][np] = dst[(size_t) (slot0 + s0 + s) * n_parts + p];
+                    a.start[np] = units;
+                    units += (int64_t) (main / 16);
+                    np++;
+                }
+                if (main < b) {
+                    char * d[RESTORE_MAX_SLOTS] = {};
+                    for (int s = 0; s < ns; s++) d[s] = dst[(size_t) (slot0 + s0 + s) * n_parts + p] + main;
+                    const int64_t n = (int64_t) (b - main);
+                    const int64_t grid = std::min<int64_t>((n + COPY_THREADS - 1) / COPY_THREADS, 4096);
+                    hipLaunchKernelGGL(k_restore_bytes, dim3((unsigned) grid), dim3(COPY_THREADS), 0, stream,
+                                       src[p] + main, nullptr, d[0], d[1], d[2], d[3], d[4], d[5], d[6], d[7], ns, n);
+                    if (int rc = hip_check(hipGetLastError(), "restore tail launch")) return rc;
+                }
+            }
+            if (np == 0) continue;
+            a.n_parts = np;
+            a.start[np] = units;
+            // Enough workgroups to cover the chip several times over; each lane streams units.
+            const int64_t grid = std::min<int64_t>((units + COPY_THREADS - 1) / COPY_THREADS, 8192);
+            hipLaunchKernelGGL(k_restore16, dim3((unsigned) grid), dim3(COPY_THREADS), 0, stream, a);
+            if (int rc = hip_check(hipGetLastError(), "restore launch")) return rc;
+        }
+    }
+    return QWFN_OK;
+}
+
+}  // namespace
+}  // namespace qwfn
+
+using namespace qwfn;
+
+extern "C" int qwfn_get_rows_i32(const qwfn_tensor * src, const qwfn_tensor * idx, const qwfn_tensor * dst,
+                                 void * stream) {
+    if (!src || !idx || !dst || !src->data || !idx->data || !dst->data)
+        return set_error(QWFN_EINVAL, "get_rows: NULL tensor");
+    if (src->type != QWFN_TYPE_I32 || idx->type != QWFN_TYPE_I32 || dst->type != QWFN_TYPE_I32)
+        return set_error(QWFN_EINVAL, "get_rows: src, idx and dst must be i32");
+    if (src->nb[0] != 4 || dst->nb[0] != 4 || idx->nb[0] != 4)
+        return set_error(QWFN_EINVAL, "get_rows: rows must be contiguous words");
+    if (src->ne[2] != 1 || src->ne[3] != 1 || idx->ne[1] != 1 || idx->ne[2] != 1 || idx->ne[3] != 1 ||
+        dst->ne[2] != 1 || dst->ne[3] != 1)
+        return set_error(QWFN_ENOTSUP, "get_rows: only 2-D src/dst and 1-D idx are supported");
+    if (dst->ne[0] != src->ne[0] || dst->ne[1] != idx->ne[0])
+        return set_error(QWFN_EINVAL, "get_rows: dst must be [src ne[0], idx ne[0]]");
+    if (!is_aligned(src->data, 4) || !is_aligned(dst->data, 4) || !is_aligned(idx->data, 4) ||
+        src->nb[1] % 4 || dst->nb[1] % 4)
+        return set_error(QWFN_EALIGN, "get_rows: 4-byte alignment required");
+    uint32_t * st = nullptr;
+    if (int rc = status_word(&st)) return rc;
+    gather_args a{};
+    a.src = (const char *) src->data; a.src_row_stride = src->nb[1]; a.src_rows = src->ne[1];
+    a.seg_off = 0; a.seg_stride = 0;
+    a.idx = (const int32_t *) idx->data; a.n_idx = idx->ne[0];
+    a.dst = (char *) dst->data; a.dst_row_stride = dst->nb[1]; a.dst_seg_stride = 0;
+    a.n_seg = 1; a.status = st;
+    return launch_gather(a, (size_t) src->ne[0] * 4, as_stream(stream));
+}
+
+extern "C" int qwfn_kv_gather_segments(const void * src, size_t src_row_stride, int64_t src_rows,
+                                       size_t seg_off, size_t seg_stride, size_t seg_bytes, int32_t n_seg,
+                                       const int32_t * idx, int64_t n_idx,
+                                       void * dst, size_t dst_row_stride, size_t dst_seg_stride, void * stream) {
+    if (!src || !idx || !dst) return set_error(QWFN_EINVAL, "gather_segments: NULL pointer");
+    if (n_seg < 1 || n_idx < 0 || src_rows < 0 || seg_bytes == 0)
+        return set_error(QWFN_EINVAL, "gather_segments: empty or negative sizes");
+    if (seg_bytes % 4 || seg_off % 4 || seg_stride % 4 || src_row_stride % 4 || dst_row_stride % 4 ||
+        dst_seg_stride % 4 || !is_aligned(src, 4) || !is_aligned(dst, 4) || !is_aligned(idx, 4))
+        return set_error(QWFN_EALIGN, "gather_segments: sizes, offsets and strides must be multiples of 4");
+    if (seg_off + (size_t) (n_seg - 1) * seg_stride + seg_bytes > src_row_stride)
+        return set_error(QWFN_ERANGE, "gather_segments: segments extend past the source row");
+    if (dst_row_stride < seg_bytes) return set_error(QWFN_EINVAL, "gather_segments: dst rows overlap");
+    uint32_t * st = nullptr;
+    if (int rc = status_word(&st)) return rc;
+    gather_args a{};
+    a.src = (const char *) src; a.src_row_stride = src_row_stride; a.src_rows = src_rows;
+    a.seg_off = seg_off; a.seg_stride = seg_stride;
+    a.idx = idx; a.n_idx = n_idx;
+    a.dst = (char *) dst; a.dst_row_stride = dst_row_stride; a.dst_seg_stride = dst_seg_stride;
+    a.n_seg = n_seg; a.status = st;
+    return launch_gather(a, seg_bytes, as_stream(stream));
+}
+
+extern "C" int qwfn_state_restore(const void * const * src, const size_t * bytes, void * const * dst,
+                                  int32_t n_parts, int32_t n_slots, int32_t src_kind, void * stream) {
+    if (!src || !bytes || !dst) return set_error(QWFN_EINVAL, "state_restore: NULL array");
+    if (n_parts < 0 || n_slots < 1) return set_error(QWFN_EINVAL, "state_restore: need n_parts >= 0 and n_slots >= 1");
+    if (src_kind != QWFN_SRC_DEVICE && src_kind != QWFN_SRC_HOST)
+        return set_error(QWFN_EINVAL, "state_restore: unknown source kind");
+    for (int p = 0; p < n_parts; p++) {
+        if (bytes[p] && !src[p]) return set_error(QWFN_EINVAL, "state_restore: NULL source part " + std::to_string(p));
+        for (int s = 0; s < n_slots; s++)
+            if (bytes[p] && !dst[(size_t) s * n_parts + p])
+                return set_error(QWFN_EINVAL, "state_restore: NULL destination part " + std::to_string(p));
+    }
+    hipStream_t st = as_stream(stream);
+    const char * const * s8 = reinterpret_cast<const char * const *>(src);
+    char * const * d8 = reinterpret_cast<char * const *>(dst);
+    if (src_kind == QWFN_SRC_DEVICE) return restore_device(s8, bytes, d8, n_parts, n_slots, 0, st);
+    for (int p = 0; p < n_parts; p++)
+        if (bytes[p]) QWFN_HIP_TRY(hipMemcpyAsync(d8[p], s8[p], bytes[p], hipMemcpyHostToDevice, st));
+    if (n_slots == 1) return QWFN_OK;
+    // Broadcast slot 0 (now on the device) into slots 1..n_slots-1.
+    std::vector<const char *> s0(d8, d8 + n_parts);
+    return restore_device(s0.data(), bytes, d8, n_parts, n_slots - 1, 1, st);
+}

@@ -1,0 +1,236 @@
+"""Python binding of libqwfn_kv.so (the C ABI declared in include/qwfn_kv.h).
+
+The binding only marshals descriptors: every operation runs in the HIP library.
+PyTorch supplies device memory and the current stream. Loading fails loudly
+when the library has not been built; there is no fallback.
+
+Tensors follow ggml conventions (ne = element counts, nb = byte strides). The
+helpers below build the views the reference engine builds over its per-layer
+caches (qwfn_state.cpp:48-91, qwfn_graph.cpp:461-464): a cache is a uint8
+[n_ctx, row_bytes] array, token-major, KV head h at byte h * 272.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libqwfn_kv.so")
+
+TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_I32 = 0, 1, 8, 26
+Q8_REF, Q8_X86 = 0, 1
+SRC_DEVICE, SRC_HOST = 0, 1
+
+QK8_0 = 32
+Q8_0_BLOCK = 34
+
+OK, EINVAL, ERANGE, EALIGN, ENOTSUP, EDEVICE, ENOMEM, ESIZE = 0, -1, -2, -3, -4, -5, -6, -7
+
+DEVERR_SET_ROWS_INDEX = 1
+DEVERR_GET_ROWS_INDEX = 2
+
+
+class QwfnError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"qwfn error {code}: {msg}")
+        self.code = code
+
+
+class Tensor(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p),
+                ("type", ctypes.c_int32),
+                ("pad_", ctypes.c_int32),
+                ("ne", ctypes.c_int64 * 4),
+                ("nb", ctypes.c_size_t * 4)]
+
+
+EXPORTS = [
+    "qwfn_abi_version", "qwfn_last_error", "qwfn_init", "qwfn_device_status",
+    "qwfn_set_rows_q8_0", "qwfn_cpy_f32_q8_0", "qwfn_get_rows_i32", "qwfn_kv_gather_segments",
+    "qwfn_fattn_workspace_size", "qwfn_flash_attn_ext_q8_0", "qwfn_state_restore",
+]
+
+_lib = None
+
+
+def load(path: str = LIB_PATH):
+    """Load the HIP library; raise if it is missing (no fallback exists)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(f"libqwfn_kv.so not built ({path}); run __graft_entry__.build()")
+    L = ctypes.CDLL(path)
+    vp, i32, i64, sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t
+    T = ctypes.POINTER(Tensor)
+    L.qwfn_abi_version.restype = ctypes.c_int
+    L.qwfn_last_error.restype = ctypes.c_char_p
+    L.qwfn_init.argtypes = [ctypes.c_int]
+    L.qwfn_device_status.argtypes = [vp, ctypes.POINTER(ctypes.c_uint32)]
+    L.qwfn_set_rows_q8_0.argtypes = [T, T, T, ctypes.c_int, vp]
+    L.qwfn_cpy_f32_q8_0.argtypes = [T, T, ctypes.c_int, vp]
+    L.qwfn_get_rows_i32.argtypes = [T, T, T, vp]
+    L.qwfn_kv_gather_segments.argtypes = [vp, sz, i64, sz, sz, sz, i32, vp, i64, vp, sz, sz, vp]
+    L.qwfn_fattn_workspace_size.argtypes = [T, T, T]
+    L.qwfn_fattn_workspace_size.restype = sz
+    L.qwfn_flash_attn_ext_q8_0.argtypes = [T, T, T, T, ctypes.c_float, ctypes.c_float, ctypes.c_float, T,
+                                           ctypes.c_int, vp, sz, vp]
+    L.qwfn_state_restore.argtypes = [ctypes.POINTER(vp), ctypes.POINTER(sz), ctypes.POINTER(vp), i32, i32, i32, vp]
+    for name in EXPORTS:
+        getattr(L, name).restype = getattr(L, name).restype or ctypes.c_int
+    L.qwfn_last_error.restype = ctypes.c_char_p
+    L.qwfn_fattn_workspace_size.restype = sz
+    _lib = L
+    return L
+
+
+def check(rc: int) -> int:
+    if rc != OK:
+        raise QwfnError(rc, load().qwfn_last_error().decode(errors="replace"))
+    return rc
+
+
+def tensor(ptr: int, typ: int, ne, nb) -> Tensor:
+    t = Tensor()
+    t.data = ptr
+    t.type = typ
+    ne = list(ne) + [1] * (4 - len(ne))
+    nb = list(nb)
+    while len(nb) < 4:
+        nb.append(nb[-1] * ne[len(nb) - 1])
+    for i in range(4):
+        t.ne[i] = int(ne[i])
+        t.nb[i] = int(nb[i])
+    return t
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    return int(stream) if not hasattr(stream, "cuda_stream") else stream.cuda_stream
+
+
+# --------------------------------------------------------------------- views
+
+def row_bytes(kv_dim: int) -> int:
+    return kv_dim // QK8_0 * Q8_0_BLOCK
+
+
+def cache_rows_view(cache, n_rows: int | None = None, first_row: int = 0) -> Tensor:
+    """q8_0 [kv_dim, n_rows] view of a uint8 [n_ctx, row_bytes] cache starting at first_row."""
+    n_ctx, rb = cache.shape
+    n = n_ctx - first_row if n_rows is None else n_rows
+    kv_dim = rb // Q8_0_BLOCK * QK8_0
+    return tensor(cache.data_ptr() + first_row * cache.stride(0), TYPE_Q8_0, (kv_dim, n), (Q8_0_BLOCK, cache.stride(0)))
+
+
+def cache_attn_view(cache, n_kv: int, n_head_kv: int, hd: int = 256, batch: int = 1, batch_stride: int = 0) -> Tensor:
+    """ggml view [hd, n_kv, n_head_kv, batch] of a token-major cache (nb1 = row, nb2 = head segment)."""
+    seg = hd // QK8_0 * Q8_0_BLOCK
+    rs = cache.stride(0) if cache.dim() == 2 else cache.stride(-2)
+    return tensor(cache.data_ptr(), TYPE_Q8_0, (hd, n_kv, n_head_kv, batch),
+                  (Q8_0_BLOCK, rs, seg, batch_stride or rs * n_kv))
+
+
+def f32_view(t) -> Tensor:
+    """Contiguous torch float32 tensor in ggml order (reversed torch dims)."""
+    assert t.dtype.itemsize == 4
+    dims = list(t.shape)[::-1]
+    strides = [s * 4 for s in list(t.stride())[::-1]]
+    return tensor(t.data_ptr(), TYPE_F32, dims, strides)
+
+
+def q_view(q) -> Tensor:
+    """Q in the projection's natural order, torch [B, T, n_head, hd] (or [T, n_head, hd]),
+    as the graph's permuted view [hd, T, n_head, B] (qwfn_graph.cpp:466, :697)."""
+    if q.dim() == 3:
+        q = q.unsqueeze(0)
+    B, T, nh, hd = q.shape
+    s = q.stride()
+    return tensor(q.data_ptr(), TYPE_F32, (hd, T, nh, B), (4, s[1] * 4, s[2] * 4, s[0] * 4))
+
+
+def mask_view(mask) -> Tensor:
+    """F16 mask, torch [T, n_kv] (or [B|1, H|1, T, n_kv]) -> ggml [n_kv, T, H, B]."""
+    if mask.dim() == 2:
+        mask = mask.unsqueeze(0).unsqueeze(0)
+    B, H, T, n = mask.shape
+    s = mask.stride()
+    return tensor(mask.data_ptr(), TYPE_F16, (n, T, H, B), (2, s[2] * 2, s[1] * 2, s[0] * 2))
+
+
+def out_view(out) -> Tensor:
+    """Output torch [B, T, n_head, hd] float32 contiguous = ggml [hd, n_head, T, B]."""
+    if out.dim() == 3:
+        out = out.unsqueeze(0)
+    B, T, nh, hd = out.shape
+    return tensor(out.data_ptr(), TYPE_F32, (hd, nh, T, B), (4, hd * 4, hd * nh * 4, hd * nh * T * 4))
+
+
+# --------------------------------------------------------------------- ops
+
+def set_rows_q8_0(cache, src, idx, variant: int = Q8_X86, stream=None, n_rows: int | None = None):
+    """cache uint8 [n_ctx, rb]; src float32 [n, kv_dim]; idx int32 [n] (device)."""
+    L = load()
+    dst = cache_rows_view(cache, n_rows)
+    s = tensor(src.data_ptr(), TYPE_F32, (src.shape[1], src.shape[0]), (4, src.stride(0) * 4))
+    i = tensor(idx.data_ptr(), TYPE_I32, (idx.shape[0],), (4,))
+    return check(L.qwfn_set_rows_q8_0(ctypes.byref(dst), ctypes.byref(s), ctypes.byref(i), variant, _stream(stream)))
+
+
+def cpy_f32_q8_0(src, cache, first_row: int, variant: int = Q8_X86, stream=None):
+    L = load()
+    s = tensor(src.data_ptr(), TYPE_F32, (src.shape[1], src.shape[0]), (4, src.stride(0) * 4))
+    dst = cache_rows_view(cache, src.shape[0], first_row)
+    return check(L.qwfn_cpy_f32_q8_0(ctypes.byref(s), ctypes.byref(dst), variant, _stream(stream)))
+
+
+def get_rows_i32(cache, idx, out, stream=None):
+    """Raw row gather: cache uint8 [n_ctx, rb] viewed as I32 words; out uint8 [n, rb]."""
+    L = load()
+    rb = cache.shape[1]
+    src = tensor(cache.data_ptr(), TYPE_I32, (rb // 4, cache.shape[0]), (4, cache.stride(0)))
+    i = tensor(idx.data_ptr(), TYPE_I32, (idx.shape[0],), (4,))
+    dst = tensor(out.data_ptr(), TYPE_I32, (rb // 4, out.shape[0]), (4, out.stride(0)))
+    return check(L.qwfn_get_rows_i32(ctypes.byref(src), ctypes.byref(i), ctypes.byref(dst), _stream(stream)))
+
+
+def gather_segments(cache, idx, out, seg_off: int, seg_stride: int, seg_bytes: int, stream=None):
+    """idx int32 [n_seg, n_idx]; out uint8 [n_seg, n_idx, seg_bytes]."""
+    L = load()
+    n_seg, n_idx = idx.shape
+    return check(L.qwfn_kv_gather_segments(cache.data_ptr(), cache.stride(0), cache.shape[0], seg_off, seg_stride,
+                                           seg_bytes, n_seg, idx.data_ptr(), n_idx, out.data_ptr(), out.stride(1),
+                                           out.stride(0), _stream(stream)))
+
+
+def flash_attn_ext(qv: Tensor, kv: Tensor, vv: Tensor, mv: Tensor | None, scale: float, ov: Tensor,
+                   variant: int = Q8_X86, ws=None, stream=None, max_bias: float = 0.0, softcap: float = 0.0):
+    L = load()
+    ws_ptr = ws.data_ptr() if ws is not None else None
+    ws_bytes = ws.numel() * ws.element_size() if ws is not None else 0
+    return check(L.qwfn_flash_attn_ext_q8_0(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv),
+                                            ctypes.byref(mv) if mv is not None else None, scale, max_bias, softcap,
+                                            ctypes.byref(ov), variant, ws_ptr, ws_bytes, _stream(stream)))
+
+
+def fattn_workspace_size(qv: Tensor, kv: Tensor, vv: Tensor) -> int:
+    return int(load().qwfn_fattn_workspace_size(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv)))
+
+
+def state_restore(srcs, nbytes, dsts, n_slots: int, src_kind: int = SRC_DEVICE, stream=None):
+    """srcs: list of n_parts pointers; dsts: list of n_slots*n_parts pointers (slot-major)."""
+    L = load()
+    n_parts = len(srcs)
+    S = (ctypes.c_void_p * max(1, n_parts))(*srcs)
+    B = (ctypes.c_size_t * max(1, n_parts))(*nbytes)
+    Dd = (ctypes.c_void_p * max(1, len(dsts)))(*dsts)
+    return check(L.qwfn_state_restore(S, B, Dd, n_parts, n_slots, src_kind, _stream(stream)))
+
+
+def device_status(stream=None) -> int:
+    L = load()
+    f = ctypes.c_uint32(0)
+    check(L.qwfn_device_status(_stream(stream), ctypes.byref(f)))
+    return int(f.value)

@@ -1,0 +1,123 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry point
+declared in include/qwfn_kv.h, and rejects invalid calls on the host before
+anything is launched (the reference's CPU-forcible failure cases)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import qwfn_kv as K
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+FAKE = 0x7F0000000000          # never dereferenced: validation fails first
+
+
+def declared_symbols():
+    hdr = open(os.path.join(ROOT, "include", "qwfn_kv.h")).read()
+    hdr = re.sub(r"/\*.*?\*/", "", hdr, flags=re.S)
+    return sorted(set(re.findall(r"\b(qwfn_[a-z0-9_]+)\s*\(", hdr)))
+
+
+def test_library_exports_header_symbols():
+    L = K.load()
+    syms = declared_symbols()
+    assert len(syms) >= 10
+    for s in syms:
+        assert hasattr(L, s), s
+    assert set(K.EXPORTS) == set(syms)
+    assert L.qwfn_abi_version() == 1
+
+
+def _err(rc, code, needle):
+    assert rc == code, (rc, K.load().qwfn_last_error())
+    assert needle in K.load().qwfn_last_error().decode()
+
+
+def q8(ne0, n, nb1=None):
+    return K.tensor(FAKE, K.TYPE_Q8_0, (ne0, n), (34, nb1 or ne0 // 32 * 34))
+
+
+def f32(ne0, n):
+    return K.tensor(FAKE, K.TYPE_F32, (ne0, n), (4, ne0 * 4))
+
+
+def i32(n):
+    return K.tensor(FAKE, K.TYPE_I32, (n,), (4,))
+
+
+def test_set_rows_validation():
+    L = K.load()
+    r = ctypes.byref
+    _err(L.qwfn_set_rows_q8_0(r(q8(512, 64)), r(f32(500, 1)), r(i32(1)), 1, None), K.EINVAL, "multiple of 32")
+    _err(L.qwfn_set_rows_q8_0(r(q8(512, 64)), r(f32(512, 2)), r(i32(3)), 1, None), K.EINVAL, "idx")
+    bad = K.tensor(FAKE, K.TYPE_F16, (512, 1), (2, 1024))
+    _err(L.qwfn_set_rows_q8_0(r(q8(512, 64)), r(bad), r(i32(1)), 1, None), K.EINVAL, "f32")
+    _err(L.qwfn_set_rows_q8_0(r(q8(512, 64)), r(f32(512, 1)), r(i32(1)), 7, None), K.EINVAL, "variant")
+    _err(L.qwfn_set_rows_q8_0(r(q8(256, 64)), r(f32(512, 1)), r(i32(1)), 1, None), K.EINVAL, "ne[0]")
+    mis = K.tensor(FAKE + 1, K.TYPE_Q8_0, (512, 64), (34, 544))
+    _err(L.qwfn_set_rows_q8_0(r(mis), r(f32(512, 1)), r(i32(1)), 1, None), K.EALIGN, "aligned")
+
+
+def test_cpy_validation():
+    L = K.load()
+    r = ctypes.byref
+    _err(L.qwfn_cpy_f32_q8_0(r(f32(512, 3)), r(q8(512, 2)), 1, None), K.EINVAL, "ne[1]")
+    _err(L.qwfn_cpy_f32_q8_0(r(f32(512, 3)), r(q8(512, 3, nb1=100)), 1, None), K.EINVAL, "overlap")
+
+
+def test_get_rows_and_gather_validation():
+    L = K.load()
+    r = ctypes.byref
+    src = K.tensor(FAKE, K.TYPE_I32, (136, 100), (4, 544))
+    dst = K.tensor(FAKE, K.TYPE_I32, (136, 5), (4, 544))
+    _err(L.qwfn_get_rows_i32(r(src), r(i32(4)), r(dst), None), K.EINVAL, "dst")
+    srcq = K.tensor(FAKE, K.TYPE_Q8_0, (256, 100), (34, 544))
+    _err(L.qwfn_get_rows_i32(r(srcq), r(i32(5)), r(dst), None), K.EINVAL, "i32")
+    _err(L.qwfn_kv_gather_segments(FAKE, 544, 100, 2, 272, 272, 2, FAKE, 10, FAKE, 272, 2720, None),
+         K.EALIGN, "multiples of 4")
+    _err(L.qwfn_kv_gather_segments(FAKE, 544, 100, 0, 272, 276, 2, FAKE, 10, FAKE, 276, 2760, None),
+         K.ERANGE, "past the source row")
+
+
+def _fa_views(hd=256, T=1, nh=16, nh_kv=2, n_kv=100, qtype=K.TYPE_F32):
+    q = K.tensor(FAKE, qtype, (hd, T, nh, 1), (4, nh * hd * 4, hd * 4, T * nh * hd * 4))
+    k = K.tensor(FAKE, K.TYPE_Q8_0, (hd, n_kv, nh_kv, 1), (34, hd // 32 * 34 * nh_kv, hd // 32 * 34, 1 << 20))
+    o = K.tensor(FAKE, K.TYPE_F32, (hd, nh, T, 1), (4, hd * 4, hd * nh * 4, hd * nh * T * 4))
+    return q, k, o
+
+
+def test_flash_attn_validation():
+    L = K.load()
+    r = ctypes.byref
+    q, k, o = _fa_views()
+    _err(L.qwfn_flash_attn_ext_q8_0(r(q), r(k), r(k), None, 0.0625, 8.0, 0.0, r(o), 1, None, 0, None),
+         K.ENOTSUP, "max_bias")
+    _err(L.qwfn_flash_attn_ext_q8_0(r(q), r(k), r(k), None, 0.0625, 0.0, 30.0, r(o), 1, None, 0, None),
+         K.ENOTSUP, "softcap")
+    q2, k2, o2 = _fa_views(hd=128)
+    _err(L.qwfn_flash_attn_ext_q8_0(r(q2), r(k2), r(k2), None, 0.0625, 0.0, 0.0, r(o2), 1, None, 0, None),
+         K.ENOTSUP, "head size")
+    q3, k3, o3 = _fa_views(nh=15)
+    _err(L.qwfn_flash_attn_ext_q8_0(r(q3), r(k3), r(k3), None, 0.0625, 0.0, 0.0, r(o3), 1, None, 0, None),
+         K.EINVAL, "multiple of n_head_kv")
+    m = K.tensor(FAKE, K.TYPE_F16, (50, 1, 1, 1), (2, 100, 100, 100))
+    _err(L.qwfn_flash_attn_ext_q8_0(r(q), r(k), r(k), r(m), 0.0625, 0.0, 0.0, r(o), 1, None, 0, None),
+         K.EINVAL, "mask")
+    kmis = K.tensor(FAKE, K.TYPE_Q8_0, (256, 100, 2, 1), (34, 550, 272, 1 << 20))
+    _err(L.qwfn_flash_attn_ext_q8_0(r(q), r(kmis), r(kmis), None, 0.0625, 0.0, 0.0, r(o), 1, None, 0, None),
+         K.EALIGN, "16-byte")
+    q4, k4, o4 = _fa_views(qtype=K.TYPE_F16)
+    _err(L.qwfn_flash_attn_ext_q8_0(r(q4), r(k4), r(k4), None, 0.0625, 0.0, 0.0, r(o4), 1, None, 0, None),
+         K.EINVAL, "f32")
+
+
+def test_restore_validation():
+    L = K.load()
+    vp = ctypes.c_void_p
+    S = (vp * 2)(FAKE, None)
+    B = (ctypes.c_size_t * 2)(16, 16)
+    D = (vp * 2)(FAKE, FAKE)
+    _err(L.qwfn_state_restore(S, B, D, 2, 1, 0, None), K.EINVAL, "source part 1")
+    _err(L.qwfn_state_restore(S, B, D, 2, 0, 0, None), K.EINVAL, "n_slots")
+    _err(L.qwfn_state_restore(S, B, D, 2, 1, 5, None), K.EINVAL, "source kind")
