@@ -1,5 +1,5 @@
-// Flash attention straight from the raw q8_0 KV cache, for decode and MTP
-// verify (T * n_head/n_head_kv <= 64 query rows per KV head), on gfx950.
+// Flash attention straight from the raw q8_0 KV cache, for decode, MTP verify
+// and (through row groups) longer query blocks, on gfx950.
 //
 // Semantics: ggml_flash_attn_ext with q8_0 K/V and F32 accumulation, as the
 // reference calls it at qwfn_graph.cpp:469-471 (dense / MTP head / QSA-off
@@ -7,24 +7,26 @@
 // one-chunk loop of ggml (the oracle) requantises Q to q8_0, takes
 // s = sum_b d_k[b]*d_q[b]*isum_b, skips keys whose mask is -inf, runs an online
 // softmax and accumulates dequantised V rows. This kernel keeps that arithmetic:
-// Q is requantised with the same quantiser, the integer block dot products are
-// exact (i8 MFMA), only the float accumulation order differs.
+// Q is requantised with the same quantiser and the integer block dot products
+// are exact (i8 MFMA); only the float accumulation order differs. P*d_v enters
+// the f16 PV matrix cores as a hi + lo pair of f16 values (~22 bits).
 //
 // Work decomposition (flash-decoding):
-//   grid   : (batch, KV head, key split), ordered so that the KV heads of one
-//            split run on the same XCD (their rows share cache lines).
-//   block  : 4 wavefronts. A 128-key chunk of K and V rows (272-byte head
-//            segments) is staged into LDS with 16-byte loads; wave w owns keys
-//            [32w, 32w+32) of the chunk.
-//   QK^T   : v_mfma_i32_16x16x32_i8, A = 16 keys x one 32-value block of K,
-//            B = the block of 16 requantised query rows; the int32 tile is
-//            scaled by d_q*d_k per block (one FMA per element) into F32 scores.
-//   softmax: online, base 2, per query row; row max reduced over the 4 lane
-//            groups with cross-lane swaps.
-//   PV     : v_mfma_f32_16x16x32_f16, A = V^T (16 dims x 32 keys, exact int8 ->
-//            f16 via SDWA byte-select conversion), B = P*d_v for one V block.
-//   merge  : the 4 waves merge in LDS; the key splits merge in a second kernel
-//            (LSE merge), or in place when there is a single split.
+//   grid   : (batch, KV head, row group, key split); the KV heads and row groups
+//            of one split are placed on the same XCD, so K/V cache lines they
+//            share are fetched from HBM once.
+//   block  : RTW 16-row query tiles x 2 key halves = 2*RTW wavefronts. Keys are
+//            streamed in 64-key chunks of raw 272-byte head rows, LDS-DMA
+//            (global_load_lds_dwordx4) into two LDS buffers: chunk c+1 is in
+//            flight while chunk c is computed. Wave (tile t, half h) owns query
+//            rows 16t..16t+15 and keys 32h..32h+31 of each chunk.
+//   QK^T   : v_mfma_i32_16x16x32_i8 per 32-value block, A = 16 keys, B = 16
+//            requantised query rows; the int32 tile is scaled by d_q*d_k.
+//   softmax: online, base 2, per query row; row max across the 4 lane groups.
+//   PV     : v_mfma_f32_16x16x32_f16, A = V^T (exact int8 -> f16 by SDWA
+//            byte-select conversion), B = P*d_v of one V block as f16 hi + lo.
+//   merge  : the two key halves merge in LDS; key splits merge in a second
+//            kernel (LSE), or in place when there is a single split.
 #include "q8_device.h"
 #include "qwfn_common.h"
 
@@ -38,17 +40,19 @@ namespace {
 typedef int      v4i __attribute__((ext_vector_type(4)));
 typedef float    v4f __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int D      = 256;            // head size (values per head row)
 constexpr int NBLK   = D / QK;         // 8 q8_0 blocks per head row
 constexpr int SEG    = NBLK * QBLOCK;  // 272 bytes per head row
-constexpr int PIECES = SEG / 16;       // 17 16-byte pieces per head row
-constexpr int WAVES  = 4;
-constexpr int THREADS = WAVES * 64;
-constexpr int KW     = 32;             // keys per wave per chunk
-constexpr int CK     = WAVES * KW;     // keys per chunk
-constexpr int MAX_RW = 32;             // query rows per block (2 MFMA row tiles)
+constexpr int KW     = 32;             // keys per wave per chunk (one PV MFMA depth)
+constexpr int CK     = 2 * KW;         // keys per chunk
+constexpr int CHUNK_BYTES = CK * SEG;  // one tensor's rows of a chunk (17408)
+constexpr int DMA_PER_TENSOR = CHUNK_BYTES / 1024;   // wave-wide 16-byte LDS-DMA loads per tensor (17)
+constexpr int MAX_MROWS = 16;          // mask rows staged per block
+constexpr int MASK_LDS = 4096;         // staged mask values per block (rows x keys of its split)
 constexpr float LOG2E = 1.4426950408889634f;
+static_assert(CHUNK_BYTES % 1024 == 0, "a chunk is whole wave-wide DMA instructions");
 
 struct fa_args {
     const char * q;  size_t q_nb1, q_nb2, q_nb3;
@@ -64,7 +68,7 @@ struct fa_args {
     int32_t  kb, vb;       // K/V batch extents (ne[3]); batch b reads b % kb
     int32_t  ns;           // key splits
     int32_t  split_len;    // keys per split, multiple of CK
-    int32_t  rw;           // query rows per block (row group size)
+    int32_t  rw;           // query rows per block (16 * RTW)
     int32_t  n_rg;         // row groups per KV head
     float    scale;
     int32_t  x86;
@@ -111,36 +115,64 @@ __device__ __forceinline__ float h2f(uint64_t four, int i) {
     return dev::f16_bits_to_f32((uint16_t) (four >> (16 * i)));
 }
 
-typedef __attribute__((address_space(3))) void lds_void;
+// s_waitcnt that waits for vmcnt <= n only (gfx9 encoding: vmcnt[3:0] in
+// bits 3:0, vmcnt[5:4] in bits 15:14, expcnt and lgkmcnt left at their max).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
 
-// LDS layout of one block (bytes).
-struct lds_layout {
-    static constexpr int KS = 0;                          // K rows  [CK][272]
-    static constexpr int VS = KS + CK * SEG;              // V rows  [CK][272]
-    static constexpr int KD = VS + CK * SEG;              // K scales [8][CK] fp16
-    static constexpr int VD = KD + CK * NBLK * 2;         // V scales [8][CK] fp16
-    static constexpr int MS = VD + CK * NBLK * 2;         // mask [n_mrows][CK] fp16
-    static constexpr int MAX_MROWS = 32;
-    static constexpr int END = MS + MAX_MROWS * CK * 2;
-    // Aliases used before / after the key loop.
-    static constexpr int QS = 0;                          // Q int8 [32][256]
-    static constexpr int QD = QS + 32 * D;                // Q scales [32][8] f32
-    static constexpr int OB = 0;                          // merge buffer [32][256] f32
-    static constexpr int ML = OB + 32 * D * 4;            // per-wave (m, l) [4][32]
-};
-static_assert(lds_layout::QD + 32 * NBLK * 4 <= lds_layout::MS, "Q staging fits below the mask");
-static_assert(lds_layout::ML + WAVES * 32 * 8 <= lds_layout::MS, "merge buffer fits below the mask");
-static_assert(CK * PIECES % 64 == 0, "staging is whole wave instructions");
+// One wave-wide LDS-DMA load: each lane copies 16 bytes from gptr to
+// LDS[lds_base + 16 * lane]; lds_base is wave-uniform. Issued as inline asm:
+// the compiler neither reorders memory operations across it nor tracks it, and
+// the kernel waits for it explicitly (vmcnt) before the barrier that publishes
+// the data. No other vector-memory load is in flight while DMAs are, so the
+// explicit counts are exact.
+__device__ __forceinline__ void dma16(const void * gptr, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\t"
+                 "global_load_lds_dwordx4 %0, off"
+                 :: "v"(gptr), "s"(lds_base) : "memory", "m0");
+}
 
-template <int RT>
-__global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_fattn_q8_0(fa_args a) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+__device__ __forceinline__ uint32_t lds_addr(const void * p) {
+    return (uint32_t) (uintptr_t) (const __attribute__((address_space(3))) void *) p;
+}
+
+// Base of staged mask row mr of this block (F16 row over keys), or nullptr.
+// Row mr is query position t0 + mr for a shared mask, query row r0 + mr for a
+// per-head mask.
+__device__ __forceinline__ const uint16_t * mask_row(const fa_args & a, int mr, int t0, int r0, int kvh, int b) {
+    if (!a.mask) return nullptr;
+    int t, hq;
+    if (a.m_ne2 == 1) { t = t0 + mr; hq = 0; }
+    else { const int r = r0 + mr; t = r / a.gqa; hq = (kvh * a.gqa + (r - t * a.gqa)) % a.m_ne2; }
+    return (const uint16_t *) (a.mask + (size_t) t * a.m_nb1 + (size_t) hq * a.m_nb2 + (size_t) (b % a.m_ne3) * a.m_nb3);
+}
+
+template <int RTW>
+__global__ __launch_bounds__(RTW * 128) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void k_fattn_q8_0(fa_args a) {
+    constexpr int WAVES = 2 * RTW;
+    constexpr int THREADS = WAVES * 64;
+    constexpr int ROWS = 16 * RTW;
+    constexpr int DMA_PER_WAVE = (2 * DMA_PER_TENSOR + WAVES - 1) / WAVES;
+    // two chunk buffers, each K rows [CK][272] then V rows [CK][272]
+    __shared__ __attribute__((aligned(16))) uint8_t buf0[2 * CHUNK_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t buf1[2 * CHUNK_BYTES];
+    __shared__ __attribute__((aligned(16))) uint16_t scl[2][NBLK][CK];      // [K|V][block][key] fp16 scales
+    __shared__ __attribute__((aligned(16))) uint16_t msk[MASK_LDS];         // mask of the block's split [row][key]
+    static_assert(ROWS * D + ROWS * NBLK * 4 <= 2 * CHUNK_BYTES, "Q staging fits in buffer 1");
+    static_assert(ROWS * D * 4 + WAVES * 16 * 8 <= 2 * CHUNK_BYTES, "merge buffer fits in buffer 0");
+
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform (SGPR)
     const int ln = lane & 15;       // MFMA row/col within a 16-tile
     const int lg = lane >> 4;       // lane group (k-chunk / output row quad)
+    const int tile = wave % RTW;    // query row tile of this wave
+    const int half = wave / RTW;    // key half of each chunk
 
-    // ---- block -> (b, kvh, row group, split); a split's heads and row groups share an XCD ----
+    // ---- block -> (b, kvh, row group, split) ----
     const int id   = blockIdx.x;
     const int xcd  = id & 7;
     const int j    = id >> 3;
@@ -154,26 +186,84 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
     if (b >= a.B) return;
     const int64_t k_lo = (int64_t) split * a.split_len;
     const int64_t k_hi = std::min<int64_t>(a.n_kv, k_lo + a.split_len);
+    const int n_chunks = (int) ((k_hi - k_lo + CK - 1) / CK);
     const int r0 = rg * a.rw;                          // first query row of this block
     const int RW = std::min(a.rw, a.R - r0);          // rows in this block
     const int t0 = r0 / a.gqa;
     const int n_mrows = a.m_ne2 == 1 ? (r0 + RW - 1) / a.gqa - t0 + 1 : RW;
 
-    // ---- stage Q: requantise the block's query rows to q8_0 ----
-    {
-        uint32_t * qs = (uint32_t *) (lds + lds_layout::QS);
-        float *    qd = (float *) (lds + lds_layout::QD);
-        const int sub = lane & 7;       // 4-value group in a block
-        const int blk = lane >> 3;      // block in the row
-        for (int rl = wave; rl < RT * 16; rl += WAVES) {
-            float x[4] = {0.f, 0.f, 0.f, 0.f};
-            if (rl < RW) {
-                const int r = r0 + rl;
-                const int t = r / a.gqa, h = kvh * a.gqa + (r - t * a.gqa);
-                const float4 v = *(const float4 *) (a.q + (size_t) t * a.q_nb1 + (size_t) h * a.q_nb2 +
-                                                    (size_t) b * a.q_nb3 + (size_t) (blk * QK + sub * 4) * 4);
-                x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+    const char * kbase = a.k + (size_t) (b % a.kb) * a.k_nb3 + (size_t) kvh * a.k_nb2;
+    const char * vbase = a.v + (size_t) (b % a.vb) * a.v_nb3 + (size_t) kvh * a.v_nb2;
+
+    // Issue chunk c's K/V rows into buffer dstb (keys past k_hi repeat the last key).
+    // Every wave issues exactly DMA_PER_WAVE instructions (surplus ones repeat an
+    // instruction another wave covers, writing identical bytes), so the number
+    // of loads in flight is known at compile time. Piece p = 64*i + lane of a
+    // tensor's chunk is byte 16*(p % 17) of key p / 17; keys past k_hi repeat
+    // the last key.
+    auto issue_chunk = [&](int c, uint8_t * dstb) {
+        const int64_t c0 = k_lo + (int64_t) c * CK;
+        const int last = (int) std::min<int64_t>(CK - 1, k_hi - 1 - c0);
+        int ln_o = lane;
+        asm volatile("" : "+v"(ln_o));          // recomputed per chunk: no hoisted per-instruction addresses
+#pragma unroll
+        for (int n = 0; n < DMA_PER_WAVE; n++) {
+            int i = wave + n * WAVES;
+            if (i >= 2 * DMA_PER_TENSOR) i = 2 * DMA_PER_TENSOR - 1 - (i - 2 * DMA_PER_TENSOR);
+            const int tensor = i >= DMA_PER_TENSOR;
+            const int ii = i - tensor * DMA_PER_TENSOR;
+            const int p = ii * 64 + ln_o;
+            const int key = std::min(p / 17, last), part = p % 17;
+            const char * src = (tensor ? vbase + (size_t) (c0 + key) * a.v_nb1 : kbase + (size_t) (c0 + key) * a.k_nb1) + part * 16;
+            dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(dstb + tensor * CHUNK_BYTES + ii * 1024)));
+        }
+    };
+    // The mask of the block's whole key range is staged into LDS once, before
+    // the key loop, so no ordinary load is outstanding while DMAs are.
+    const int span = (int) (k_hi - k_lo);                       // keys of this split (<= split_len)
+    const int mstride = a.split_len;                            // LDS row stride of the staged mask
+    // Prologue: chunk 0's DMA, the block's Q rows and its mask are all put in
+    // flight before anything waits, so they cost one memory round trip together.
+    issue_chunk(0, buf0);
+    const int sub = lane & 7;       // 4-value group of a q8_0 block (Q staging)
+    const int blk = lane >> 3;      // q8_0 block of the row (Q staging)
+    float4 xv[ROWS / WAVES];
+#pragma unroll
+    for (int q = 0; q < ROWS / WAVES; q++) {
+        const int rl = wave + q * WAVES;
+        const int r = r0 + std::min(rl, RW - 1);
+        const int t = r / a.gqa, h = kvh * a.gqa + (r - t * a.gqa);
+        xv[q] = *(const float4 *) (a.q + (size_t) t * a.q_nb1 + (size_t) h * a.q_nb2 + (size_t) b * a.q_nb3 +
+                                   (size_t) (blk * QK + sub * 4) * 4);
+    }
+    if (a.mask) {
+        constexpr int MB = 8;                                   // loads in flight per thread
+        for (int e0 = threadIdx.x; e0 < n_mrows * mstride; e0 += MB * THREADS) {
+            uint16_t mv[MB];
+#pragma unroll
+            for (int q = 0; q < MB; q++) {
+                const int e = e0 + q * THREADS;
+                const int mr = std::min(e / mstride, n_mrows - 1);
+                const int key = std::min(e - (e / mstride) * mstride, span - 1);
+                mv[q] = mask_row(a, mr, t0, r0, kvh, b)[k_lo + key];
             }
+#pragma unroll
+            for (int q = 0; q < MB; q++) {
+                const int e = e0 + q * THREADS;
+                if (e < n_mrows * mstride) msk[e] = mv[q];
+            }
+        }
+    }
+
+    // ---- stage Q in buffer 1: requantise the block's query rows to q8_0 ----
+    {
+        uint32_t * qs = (uint32_t *) buf1;
+        float *    qd = (float *) (buf1 + ROWS * D);
+#pragma unroll
+        for (int q = 0; q < ROWS / WAVES; q++) {
+            const int rl = wave + q * WAVES;
+            const float4 v4 = rl < RW ? xv[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float x[4] = {v4.x, v4.y, v4.z, v4.w};
             uint16_t d16;
             float dq;
             const uint32_t w = dev::q8_quantize_lane4(x, a.x86 != 0, &d16, &dq);
@@ -182,134 +272,100 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
         }
     }
     __syncthreads();
-
-    long  qB[RT][NBLK];
-    float dqr[RT][NBLK];
-    int   mrow[RT];     // staged mask row of this lane's query row; -1 for padding rows
+    long  qB[NBLK];
+    float dqr[NBLK];
+    const int rl_lane = tile * 16 + ln;                 // this lane's query row (as MFMA column)
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++) {
-        const int rl = rt * 16 + ln;
-#pragma unroll
-        for (int bb = 0; bb < NBLK; bb++) {
-            qB[rt][bb] = (long) lds_u64(lds + lds_layout::QS + rl * D + bb * QK + lg * 8);
-            dqr[rt][bb] = ((const float *) (lds + lds_layout::QD))[rl * NBLK + bb];
-        }
-        mrow[rt] = rl >= RW ? -1 : (a.m_ne2 == 1 ? (r0 + rl) / a.gqa - t0 : rl);
+    for (int bb = 0; bb < NBLK; bb++) {
+        qB[bb] = (long) lds_u64(buf1 + rl_lane * D + bb * QK + lg * 8);
+        dqr[bb] = ((const float *) (buf1 + ROWS * D))[rl_lane * NBLK + bb];
     }
+    const int mrow = rl_lane >= RW ? -1 : (a.m_ne2 == 1 ? (r0 + rl_lane) / a.gqa - t0 : rl_lane);
+    __syncthreads();   // buffer 1 is free again
+    if (n_chunks > 1) issue_chunk(1, buf1);
 
-    // ---- online softmax state ----
-    v4f   O[RT][NBLK][2];
-    float m_run[RT], l_run[RT];
+    // ---- online softmax state (one 16-row tile per wave) ----
+    v4f   O[NBLK][2];
+    float m_run = -INFINITY, l_run = 0.f;
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++) {
-        m_run[rt] = -INFINITY;
-        l_run[rt] = 0.f;
-#pragma unroll
-        for (int bb = 0; bb < NBLK; bb++) { O[rt][bb][0] = v4f{0, 0, 0, 0}; O[rt][bb][1] = v4f{0, 0, 0, 0}; }
-    }
+    for (int bb = 0; bb < NBLK; bb++) { O[bb][0] = v4f{0, 0, 0, 0}; O[bb][1] = v4f{0, 0, 0, 0}; }
 
-    const char * kbase = a.k + (size_t) (b % a.kb) * a.k_nb3 + (size_t) kvh * a.k_nb2;
-    const char * vbase = a.v + (size_t) (b % a.vb) * a.v_nb3 + (size_t) kvh * a.v_nb2;
-    const uint16_t * ms = (const uint16_t *) (lds + lds_layout::MS);
-    const int wk = wave * KW;   // this wave's first key in a chunk
+    const int wk = half * KW;   // this wave's first key in a chunk
     int keyj[8];                // k-slot order: j<4 -> key 4g+j, j>=4 -> key 16+4g+j-4
 #pragma unroll
     for (int jj = 0; jj < 8; jj++) keyj[jj] = wk + (jj >> 2) * 16 + lg * 4 + (jj & 3);
     const int aoff = 2 + 4 * (ln & 7) + (ln >> 3);   // V^T row m: dims 4(m%8) (+1 byte for m >= 8)
 
-    for (int64_t c0 = k_lo; c0 < k_hi; c0 += CK) {
-        __syncthreads();   // previous chunk (or Q staging) fully consumed
-        // ---- stage raw K/V rows straight into LDS (keys past k_hi repeat the last key) ----
-        for (int i = wave; i < CK * PIECES / 64; i += WAVES) {
-            const int p = i * 64 + lane;
-            const int key = p / PIECES, part = p - key * PIECES;
-            const int64_t kk = std::min<int64_t>(c0 + key, k_hi - 1);
-            __builtin_amdgcn_global_load_lds((const void *) (kbase + (size_t) kk * a.k_nb1 + part * 16),
-                                             (lds_void *) (lds + lds_layout::KS + i * 1024), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((const void *) (vbase + (size_t) kk * a.v_nb1 + part * 16),
-                                             (lds_void *) (lds + lds_layout::VS + i * 1024), 16, 0, 0);
+    // One chunk: `cur` holds chunk c. Called with buf0 / buf1 literally so the
+    // compiler can tell the buffer being read from the one the DMA is filling.
+    auto chunk_step = [&](int c, uint8_t * cur) {
+        // the mask of chunk c (prefetched into registers) goes to LDS
+        if (c + 1 < n_chunks) {
+            // chunk c+1's DMA is the only one issued after chunk c's: once at most
+            // that many loads are outstanding, chunk c has landed
+            wait_vmcnt<DMA_PER_WAVE>();
+        } else {
+            wait_vmcnt<0>();
         }
-        // ---- stage mask values (F16 bits); keys past k_hi are -inf ----
-        for (int e = threadIdx.x; e < n_mrows * CK; e += THREADS) {
-            const int mr = e / CK, key = e - mr * CK;
-            const int64_t kk = c0 + key;
-            uint16_t mv = 0xFC00;   // -inf
-            if (kk < k_hi) {
-                if (a.mask) {
-                    int t, hq;
-                    if (a.m_ne2 == 1) { t = t0 + mr; hq = 0; }
-                    else { const int r = r0 + mr; t = r / a.gqa; hq = (kvh * a.gqa + (r - t * a.gqa)) % a.m_ne2; }
-                    mv = *(const uint16_t *) (a.mask + (size_t) t * a.m_nb1 + (size_t) hq * a.m_nb2 +
-                                              (size_t) (b % a.m_ne3) * a.m_nb3 + (size_t) kk * 2);
-                } else {
-                    mv = 0;
-                }
-            }
-            ((uint16_t *) (lds + lds_layout::MS))[mr * CK + key] = mv;
-        }
-        __builtin_amdgcn_s_waitcnt(0);   // LDS-DMA writes are counted by vmcnt
         __syncthreads();
-        // ---- per-block scales, transposed to [block][key] ----
+        // per-block scales of chunk c, transposed to [block][key]
         for (int e = threadIdx.x; e < CK * NBLK; e += THREADS) {
             const int key = e >> 3, bb = e & 7;
-            ((uint16_t *) (lds + lds_layout::KD))[bb * CK + key] = *(const uint16_t *) (lds + lds_layout::KS + key * SEG + bb * QBLOCK);
-            ((uint16_t *) (lds + lds_layout::VD))[bb * CK + key] = *(const uint16_t *) (lds + lds_layout::VS + key * SEG + bb * QBLOCK);
+            scl[0][bb][key] = *(const uint16_t *) (cur + key * SEG + bb * QBLOCK);
+            scl[1][bb][key] = *(const uint16_t *) (cur + CHUNK_BYTES + key * SEG + bb * QBLOCK);
         }
         __syncthreads();
+        const uint8_t * ks = cur;
+        const uint8_t * vs = cur + CHUNK_BYTES;
 
         // ---- S = Q K^T for 2 tiles of 16 keys ----
-        float s[RT][2][4];
+        float s[2][4];
 #pragma unroll
         for (int kt = 0; kt < 2; kt++) {
             const int kr = wk + kt * 16 + ln;                 // A-operand key row
             const int k4 = wk + kt * 16 + lg * 4;             // output keys k4..k4+3
 #pragma unroll
-            for (int rt = 0; rt < RT; rt++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) s[rt][kt][i] = 0.f;
+            for (int i = 0; i < 4; i++) s[kt][i] = 0.f;
 #pragma unroll
             for (int bb = 0; bb < NBLK; bb++) {
-                const long kA = (long) lds_u64(lds + lds_layout::KS + kr * SEG + bb * QBLOCK + 2 + lg * 8);
-                const uint64_t dk4 = lds_u64(lds + lds_layout::KD + (bb * CK + k4) * 2);
+                const long kA = (long) lds_u64(ks + kr * SEG + bb * QBLOCK + 2 + lg * 8);
+                const uint64_t dk4 = lds_u64((const uint8_t *) &scl[0][bb][k4]);
+                const v4i cc = __builtin_amdgcn_mfma_i32_16x16x32_i8(kA, qB[bb], v4i{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-                for (int rt = 0; rt < RT; rt++) {
-                    const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(kA, qB[rt][bb], v4i{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        s[rt][kt][i] = __builtin_fmaf((float) c[i], dqr[rt][bb] * h2f(dk4, i), s[rt][kt][i]);
-                }
+                for (int i = 0; i < 4; i++) s[kt][i] = __builtin_fmaf((float) cc[i], dqr[bb] * h2f(dk4, i), s[kt][i]);
             }
         }
 
         // ---- mask, scale, online softmax (base 2) ----
-        float p[RT][8];
-#pragma unroll
-        for (int rt = 0; rt < RT; rt++) {
+        float p[8];
+        {
             float sv[8];
             float mloc = -INFINITY;
 #pragma unroll
             for (int jj = 0; jj < 8; jj++) {
-                const float mv = mrow[rt] >= 0 ? dev::f16_bits_to_f32(ms[mrow[rt] * CK + keyj[jj]]) : -INFINITY;
-                const float x = (mv == -INFINITY) ? -INFINITY : (s[rt][jj >> 2][jj & 3] * a.scale + mv) * LOG2E;
+                const int kin = c * CK + keyj[jj];               // key index within the split
+                float mv = -INFINITY;
+                if (mrow >= 0 && kin < span) mv = a.mask ? dev::f16_bits_to_f32(msk[mrow * mstride + kin]) : 0.f;
+                const float x = (mv == -INFINITY) ? -INFINITY : (s[jj >> 2][jj & 3] * a.scale + mv) * LOG2E;
                 sv[jj] = x;
                 mloc = xmax(mloc, x);
             }
             mloc = xmax(mloc, __shfl_xor(mloc, 16));
             mloc = xmax(mloc, __shfl_xor(mloc, 32));
-            const float m_new = xmax(m_run[rt], mloc);
-            const float alpha = (m_new == -INFINITY) ? 1.f : exp2f(m_run[rt] - m_new);
+            const float m_new = xmax(m_run, mloc);
+            const float alpha = (m_new == -INFINITY) ? 1.f : exp2f(m_run - m_new);
             float lsum = 0.f;
 #pragma unroll
             for (int jj = 0; jj < 8; jj++) {
                 const float pv = (sv[jj] == -INFINITY) ? 0.f : exp2f(sv[jj] - m_new);
-                p[rt][jj] = pv;
+                p[jj] = pv;
                 lsum += pv;
             }
-            l_run[rt] = l_run[rt] * alpha + lsum;
-            m_run[rt] = m_new;
+            l_run = l_run * alpha + lsum;
+            m_run = m_new;
             if (__any(alpha != 1.f)) {
 #pragma unroll
-                for (int bb = 0; bb < NBLK; bb++) { O[rt][bb][0] *= alpha; O[rt][bb][1] *= alpha; }
+                for (int bb = 0; bb < NBLK; bb++) { O[bb][0] *= alpha; O[bb][1] *= alpha; }
             }
         }
 
@@ -318,7 +374,7 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
         for (int bb = 0; bb < NBLK; bb++) {
             uint32_t w[8];
 #pragma unroll
-            for (int jj = 0; jj < 8; jj++) w[jj] = lds_u32(lds + lds_layout::VS + keyj[jj] * SEG + bb * QBLOCK + aoff);
+            for (int jj = 0; jj < 8; jj++) w[jj] = lds_u32(vs + keyj[jj] * SEG + bb * QBLOCK + aoff);
             uint32_t a0[4], a1[4];
 #pragma unroll
             for (int q2 = 0; q2 < 4; q2++) {
@@ -327,73 +383,67 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
             }
             const v8h A0 = __builtin_bit_cast(v8h, uint4{a0[0], a0[1], a0[2], a0[3]});
             const v8h A1 = __builtin_bit_cast(v8h, uint4{a1[0], a1[1], a1[2], a1[3]});
-            const uint64_t dvlo = lds_u64(lds + lds_layout::VD + (bb * CK + keyj[0]) * 2);
-            const uint64_t dvhi = lds_u64(lds + lds_layout::VD + (bb * CK + keyj[4]) * 2);
+            const uint64_t dvlo = lds_u64((const uint8_t *) &scl[1][bb][keyj[0]]);
+            const uint64_t dvhi = lds_u64((const uint8_t *) &scl[1][bb][keyj[4]]);
+            // B = P*d_v split into f16 hi + lo parts (two MFMAs): ~22 significant
+            // bits, so a few dominant keys over large V values stay exact enough
+            v8h Bh, Bl;
 #pragma unroll
-            for (int rt = 0; rt < RT; rt++) {
-                v8h Bp;
-#pragma unroll
-                for (int jj = 0; jj < 8; jj++)
-                    Bp[jj] = (_Float16) (p[rt][jj] * h2f(jj < 4 ? dvlo : dvhi, jj & 3));
-                O[rt][bb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, Bp, O[rt][bb][0], 0, 0, 0);
-                O[rt][bb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, Bp, O[rt][bb][1], 0, 0, 0);
+            for (int jj = 0; jj < 8; jj++) {
+                const float x = p[jj] * h2f(jj < 4 ? dvlo : dvhi, jj & 3);
+                const _Float16 h = (_Float16) x;
+                Bh[jj] = h;
+                Bl[jj] = (_Float16) (x - (float) h);
             }
+            O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, Bh, O[bb][0], 0, 0, 0);
+            O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, Bh, O[bb][1], 0, 0, 0);
+            O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, Bl, O[bb][0], 0, 0, 0);
+            O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, Bl, O[bb][1], 0, 0, 0);
         }
+        __syncthreads();   // chunk c consumed: its buffer, scales and mask may be overwritten
+        if (c + 2 < n_chunks) issue_chunk(c + 2, cur);
+    };
+    for (int c = 0; c < n_chunks; c += 2) {
+        chunk_step(c, buf0);
+        if (c + 1 < n_chunks) chunk_step(c + 1, buf1);
     }
 
-    // ---- merge the 4 waves' partial states in LDS (deterministic order) ----
-    __syncthreads();   // staging area becomes the merge buffer
-    float * ob = (float *) (lds + lds_layout::OB);
-    float2 * ml = (float2 *) (lds + lds_layout::ML);
-#pragma unroll
-    for (int rt = 0; rt < RT; rt++) {
-        float l = l_run[rt];
+    // ---- merge the two key halves in LDS ----
+    float * ob = (float *) buf0;                                  // [ROWS][256] f32
+    float2 * ml = (float2 *) (buf0 + ROWS * D * 4);               // [WAVES][16]
+    {
+        float l = l_run;
         l += __shfl_xor(l, 16);
         l += __shfl_xor(l, 32);
-        l_run[rt] = l;
-        if (lg == 0) ml[wave * 32 + rt * 16 + ln] = make_float2(m_run[rt], l);
+        l_run = l;
+        if (lg == 0) ml[wave * 16 + ln] = make_float2(m_run, l);
     }
     __syncthreads();
-    float mw[RT], lw[RT], fw[RT];
-#pragma unroll
-    for (int rt = 0; rt < RT; rt++) {
-        const int rl = rt * 16 + ln;
-        float M = -INFINITY;
-        for (int w2 = 0; w2 < WAVES; w2++) M = xmax(M, ml[w2 * 32 + rl].x);
-        float L = 0.f;
-        for (int w2 = 0; w2 < WAVES; w2++) {
-            const float2 e = ml[w2 * 32 + rl];
-            L += (e.x == -INFINITY) ? 0.f : e.y * exp2f(e.x - M);
-        }
-        mw[rt] = M;
-        lw[rt] = L;
-        fw[rt] = (m_run[rt] == -INFINITY) ? 0.f : exp2f(m_run[rt] - M);
+    float M, L, fw;
+    {
+        const float2 e0 = ml[tile * 16 + ln], e1 = ml[(RTW + tile) * 16 + ln];
+        M = xmax(e0.x, e1.x);
+        L = (e0.x == -INFINITY ? 0.f : e0.y * exp2f(e0.x - M)) + (e1.x == -INFINITY ? 0.f : e1.y * exp2f(e1.x - M));
+        fw = (m_run == -INFINITY) ? 0.f : exp2f(m_run - M);
     }
-    __syncthreads();   // every wave has read ml before row 0's (M, L) overwrite it below
-    for (int w2 = 0; w2 < WAVES; w2++) {
-        if (wave == w2) {
+    __syncthreads();
+    for (int hh = 0; hh < 2; hh++) {
+        if (half == hh) {
 #pragma unroll
-            for (int rt = 0; rt < RT; rt++) {
-                const int rl = rt * 16 + ln;
+            for (int bb = 0; bb < NBLK; bb++)
 #pragma unroll
-                for (int bb = 0; bb < NBLK; bb++)
-#pragma unroll
-                    for (int e = 0; e < 2; e++) {
-                        float4 * dstp = (float4 *) (ob + rl * D + bb * 32 + e * 16 + lg * 4);
-                        const v4f val = O[rt][bb][e] * fw[rt];
-                        if (w2 == 0) {
-                            *dstp = make_float4(val[0], val[1], val[2], val[3]);
-                        } else {
-                            float4 cur = *dstp;
-                            cur.x += val[0]; cur.y += val[1]; cur.z += val[2]; cur.w += val[3];
-                            *dstp = cur;
-                        }
+                for (int e = 0; e < 2; e++) {
+                    float4 * dstp = (float4 *) (ob + rl_lane * D + bb * 32 + e * 16 + lg * 4);
+                    const v4f val = O[bb][e] * fw;
+                    if (hh == 0) {
+                        *dstp = make_float4(val[0], val[1], val[2], val[3]);
+                    } else {
+                        float4 c4 = *dstp;
+                        c4.x += val[0]; c4.y += val[1]; c4.z += val[2]; c4.w += val[3];
+                        *dstp = c4;
                     }
-            }
-            if (w2 == 0 && lg == 0) {
-#pragma unroll
-                for (int rt = 0; rt < RT; rt++) ml[rt * 16 + ln] = make_float2(mw[rt], lw[rt]);
-            }
+                }
+            if (hh == 0 && lg == 0) ml[tile * 16 + ln] = make_float2(M, L);
         }
         __syncthreads();
     }
@@ -401,64 +451,86 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
     // ---- write the block's result ----
     const size_t bh = (size_t) b * a.nh_kv + kvh;
     if (a.ns == 1) {
-        // single split: normalised final output, dims restored
         for (int e = threadIdx.x; e < RW * D; e += THREADS) {
             const int rl = e / D, pos = e - rl * D;
             const int r = r0 + rl;
             const int t = r / a.gqa, h = kvh * a.gqa + (r - t * a.gqa);
-            const float L = ml[rl].y;
-            const float o = L > 0.f ? ob[rl * D + pos] / L : 0.f;
-            a.dst[(((size_t) b * a.T + t) * a.nh + h) * D + pos_to_dim(pos)] = o;
+            const float Lr = ml[rl].y;
+            a.dst[(((size_t) b * a.T + t) * a.nh + h) * D + pos_to_dim(pos)] = Lr > 0.f ? ob[rl * D + pos] / Lr : 0.f;
         }
     } else {
         float * po = a.part_o + ((bh * a.ns + split) * a.R + r0) * D;
-        for (int e = threadIdx.x; e < RW * D / 4; e += THREADS)
-            ((float4 *) po)[e] = ((const float4 *) ob)[e];
-        for (int rl = threadIdx.x; rl < RW; rl += THREADS)
-            a.part_ml[(bh * a.ns + split) * a.R + r0 + rl] = ml[rl];
+        for (int e = threadIdx.x; e < RW * D / 4; e += THREADS) ((float4 *) po)[e] = ((const float4 *) ob)[e];
+        for (int rl = threadIdx.x; rl < RW; rl += THREADS) a.part_ml[(bh * a.ns + split) * a.R + r0 + rl] = ml[rl];
     }
 }
 
-// One block per (b, kvh, r): LSE merge of the ns split partials.
+// LSE merge of the ns split partials. Block = (row, 64-dim slice); its 256
+// threads are 4 split groups x 64 dims: each thread folds every 4th split of one
+// dim, 4 splits per step with independent loads, then the 4 groups combine
+// through LDS.
+constexpr int MERGE_DIMS = 64;
+constexpr int MERGE_GROUPS = 4;
+constexpr int MERGE_UNROLL = 4;
+
 __global__ __launch_bounds__(256) void k_fattn_merge(fa_args a) {
-    const int row = blockIdx.x;                  // ((b * nh_kv + kvh) * R + r)
+    __shared__ float red_m[MERGE_GROUPS], red_l[MERGE_GROUPS];
+    __shared__ float red_o[MERGE_GROUPS][MERGE_DIMS];
+    const int row = blockIdx.x / (D / MERGE_DIMS);          // ((b * nh_kv + kvh) * R + r)
+    const int slice = blockIdx.x - row * (D / MERGE_DIMS);
     const int r = row % a.R;
     const int bh = row / a.R;
     const int kvh = bh % a.nh_kv, b = bh / a.nh_kv;
+    const int sg = threadIdx.x / MERGE_DIMS, d = threadIdx.x % MERGE_DIMS;
+    const int pos = slice * MERGE_DIMS + d;
     const float2 * ml = a.part_ml + (size_t) bh * a.ns * a.R + r;
-    float M = -INFINITY;
-    for (int s2 = 0; s2 < a.ns; s2++) M = xmax(M, ml[(size_t) s2 * a.R].x);
-    float L = 0.f, acc = 0.f;
-    const int pos = threadIdx.x;
     const float * po = a.part_o + ((size_t) bh * a.ns * a.R + r) * D + pos;
-    for (int s2 = 0; s2 < a.ns; s2++) {
-        const float2 e = ml[(size_t) s2 * a.R];
-        if (e.x == -INFINITY) continue;
-        const float f = exp2f(e.x - M);
-        L += e.y * f;
-        acc += po[(size_t) s2 * a.R * D] * f;
+    float M = -INFINITY;
+    for (int s0 = sg; s0 < a.ns; s0 += MERGE_GROUPS * MERGE_UNROLL) {
+        float mm[MERGE_UNROLL];
+#pragma unroll
+        for (int q = 0; q < MERGE_UNROLL; q++) {
+            const int s2 = s0 + q * MERGE_GROUPS;
+            mm[q] = s2 < a.ns ? ml[(size_t) s2 * a.R].x : -INFINITY;
+        }
+#pragma unroll
+        for (int q = 0; q < MERGE_UNROLL; q++) M = xmax(M, mm[q]);
     }
-    const int t = r / a.gqa, h = kvh * a.gqa + (r - t * a.gqa);
-    a.dst[(((size_t) b * a.T + t) * a.nh + h) * D + pos_to_dim(pos)] = L > 0.f ? acc / L : 0.f;
-}
-
-// Blocks use more than the default 64 KB of dynamic LDS (gfx950 has 160 KB).
-template <int RT>
-int launch_fa(int64_t grid, size_t shmem, hipStream_t st, const fa_args & a) {
-    static bool attr_set = false;
-    if (!attr_set) {
-        QWFN_HIP_TRY(hipFuncSetAttribute((const void *) k_fattn_q8_0<RT>,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds_layout::END));
-        attr_set = true;
+    if (d == 0) red_m[sg] = M;
+    __syncthreads();
+    M = xmax(xmax(red_m[0], red_m[1]), xmax(red_m[2], red_m[3]));
+    float L = 0.f, acc = 0.f;
+    for (int s0 = sg; s0 < a.ns; s0 += MERGE_GROUPS * MERGE_UNROLL) {
+        float2 e[MERGE_UNROLL];
+        float o[MERGE_UNROLL];
+#pragma unroll
+        for (int q = 0; q < MERGE_UNROLL; q++) {
+            const int s2 = s0 + q * MERGE_GROUPS;
+            e[q] = s2 < a.ns ? ml[(size_t) s2 * a.R] : make_float2(-INFINITY, 0.f);
+            o[q] = s2 < a.ns ? po[(size_t) s2 * a.R * D] : 0.f;
+        }
+#pragma unroll
+        for (int q = 0; q < MERGE_UNROLL; q++) {
+            const float f = (e[q].x == -INFINITY) ? 0.f : exp2f(e[q].x - M);
+            L += e[q].y * f;
+            acc += o[q] * f;
+        }
     }
-    hipLaunchKernelGGL(k_fattn_q8_0<RT>, dim3((unsigned) grid), dim3(THREADS), shmem, st, a);
-    return QWFN_OK;
+    red_o[sg][d] = acc;
+    if (d == 0) red_l[sg] = L;
+    __syncthreads();
+    if (sg == 0) {
+        const float Lt = (red_l[0] + red_l[1]) + (red_l[2] + red_l[3]);
+        const float At = (red_o[0][d] + red_o[1][d]) + (red_o[2][d] + red_o[3][d]);
+        const int t = r / a.gqa, h = kvh * a.gqa + (r - t * a.gqa);
+        a.dst[(((size_t) b * a.T + t) * a.nh + h) * D + pos_to_dim(pos)] = Lt > 0.f ? At / Lt : 0.f;
+    }
 }
 
 // ---------------------------------------------------------------- planning
 
 struct fa_plan {
-    int32_t R, RT, gqa, rw, n_rg, ns, split_len, n_mrows;
+    int32_t R, RTW, gqa, rw, n_rg, ns, split_len;
     size_t  ws_bytes;
 };
 
@@ -493,7 +565,7 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
         return set_error(QWFN_EALIGN, "flash_attn_ext: k/v data and strides must be 16-byte aligned");
     if (!is_aligned(q->data, 16) || q->nb[1] % 16 || q->nb[2] % 16 || q->nb[3] % 16)
         return set_error(QWFN_EALIGN, "flash_attn_ext: q data and strides must be 16-byte aligned");
-    int n_mrows = (int) T;
+    bool per_head_mask = false;
     if (mask) {
         if (!mask->data) return set_error(QWFN_EINVAL, "flash_attn_ext: mask has no data");
         if (mask->type != QWFN_TYPE_F16) return set_error(QWFN_EINVAL, "flash_attn_ext: mask must be f16");
@@ -503,28 +575,33 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
         if (mask->ne[2] <= 0 || nh % mask->ne[2] || mask->ne[3] <= 0 || q->ne[3] % mask->ne[3])
             return set_error(QWFN_EINVAL, "flash_attn_ext: mask must broadcast over heads and batch");
         if (!is_aligned(mask->data, 2)) return set_error(QWFN_EALIGN, "flash_attn_ext: mask must be 2-byte aligned");
-        n_mrows = mask->ne[2] == 1 ? (int) T : (int) R;
+        per_head_mask = mask->ne[2] != 1;
     }
-    // Query rows per block: up to 32 (two 16-row MFMA tiles); more rows are
-    // split into row groups that read the same K/V (L2-shared on one XCD).
-    int rw = (int) std::min<int64_t>(R, MAX_RW);
-    if (const int force = env_int("QWFN_FA_ROWS", 0)) rw = std::max(1, std::min(rw, force));
+    // Query rows per block: one or two 16-row tiles. A per-head mask stages one
+    // mask row per query row, so it keeps blocks at 16 rows (<= 16 staged rows).
+    int rw = (R > 16 && !per_head_mask) ? 32 : 16;
+    if (const int force = env_int("QWFN_FA_ROWS", 0)) rw = (force >= 32 && !per_head_mask) ? 32 : 16;
     pl->R = (int32_t) R;
     pl->rw = rw;
+    pl->RTW = rw / 16;
     pl->n_rg = (int32_t) ((R + rw - 1) / rw);
-    pl->RT = (rw + 15) / 16;
     pl->gqa = (int32_t) gqa;
-    pl->n_mrows = (mask && mask->ne[2] != 1) ? rw : (int) std::min<int64_t>(T, (rw + gqa - 1) / gqa + 1);
-    (void) n_mrows;
     const int64_t n_kv = k->ne[1];
     const int64_t B = q->ne[3];
-    // Splits: enough blocks to cover the chip about twice, each at least one chunk.
-    const int64_t target_blocks = env_int("QWFN_FA_BLOCKS", 512);
+    // Splits: about one block per CU (256), each at least one chunk.
+    const int64_t target_blocks = env_int("QWFN_FA_BLOCKS", 256);
     int64_t ns = std::max<int64_t>(1, target_blocks / std::max<int64_t>(1, nh_kv * B * pl->n_rg));
     ns = std::min<int64_t>(ns, std::max<int64_t>(1, (n_kv + CK - 1) / CK));
     if (const int force = env_int("QWFN_FA_SPLITS", 0)) ns = force;
     int64_t split_len = (n_kv + ns - 1) / ns;
     split_len = std::max<int64_t>(CK, (split_len + CK - 1) / CK * CK);
+    if (mask) {
+        // a block stages its split's mask rows in LDS: rows x split_len <= MASK_LDS
+        const int64_t mrows = per_head_mask ? rw : std::min<int64_t>(T, (rw + gqa - 1) / gqa + 1);
+        const int64_t cap = std::max<int64_t>(CK, MASK_LDS / mrows / CK * CK);
+        if (mrows * CK > MASK_LDS) return set_error(QWFN_ENOTSUP, "flash_attn_ext: too many mask rows per block");
+        split_len = std::min(split_len, cap);
+    }
     ns = std::max<int64_t>(1, (n_kv + split_len - 1) / split_len);
     pl->ns = (int32_t) ns;
     pl->split_len = (int32_t) split_len;
@@ -599,16 +676,12 @@ extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor
     const int64_t grid = units * a.nh_kv * a.n_rg;
     if (grid > 0x7fffffff) return set_error(QWFN_EINVAL, "flash_attn_ext: grid too large");
     hipStream_t st = as_stream(stream);
-    const size_t shmem = (size_t) lds_layout::MS + (size_t) pl.n_mrows * CK * 2;
-    if (pl.RT == 1) {
-        if (int rc = launch_fa<1>(grid, shmem, st, a)) return rc;
-    } else {
-        if (int rc = launch_fa<2>(grid, shmem, st, a)) return rc;
-    }
+    if (pl.RTW == 1) hipLaunchKernelGGL(k_fattn_q8_0<1>, dim3((unsigned) grid), dim3(128), 0, st, a);
+    else             hipLaunchKernelGGL(k_fattn_q8_0<2>, dim3((unsigned) grid), dim3(256), 0, st, a);
     if (int rc = hip_check(hipGetLastError(), "flash_attn launch")) return rc;
     if (a.ns > 1) {
-        const int64_t rows = (int64_t) a.B * a.nh_kv * a.R;
-        hipLaunchKernelGGL(k_fattn_merge, dim3((unsigned) rows), dim3(256), 0, st, a);
+        const int64_t blocks = (int64_t) a.B * a.nh_kv * a.R * (D / MERGE_DIMS);
+        hipLaunchKernelGGL(k_fattn_merge, dim3((unsigned) blocks), dim3(256), 0, st, a);
         if (int rc = hip_check(hipGetLastError(), "flash_attn merge launch")) return rc;
     }
     return QWFN_OK;
