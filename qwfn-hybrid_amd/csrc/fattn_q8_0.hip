@@ -98,6 +98,28 @@ __device__ __forceinline__ uint32_t cvt_i8x2_f16_b2(uint32_t a, uint32_t b) {
     return r;
 }
 
+// x * f16 (low or high half of a packed dword), one v_fma_mix_f32.
+__device__ __forceinline__ float mul_f16lo(float x, uint32_t h) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[0,0,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(x), "v"(h));
+    return r;
+}
+__device__ __forceinline__ float mul_f16hi(float x, uint32_t h) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(x), "v"(h));
+    return r;
+}
+// Split two f32 values into f16 hi parts (RNE) and f16 lo = f16(x - hi):
+// returns {hi pair, lo pair} as packed dwords.
+__device__ __forceinline__ uint2 split_f16x2(float x0, float x1) {
+    uint32_t hi, lo;
+    asm("v_cvt_pk_f16_f32 %0, %2, %3\n\t"
+        "v_fma_mixlo_f16 %1, %2, 1.0, -%0 op_sel:[0,0,0] op_sel_hi:[0,0,1]\n\t"
+        "v_fma_mixhi_f16 %1, %3, 1.0, -%0 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+        : "=&v"(hi), "=&v"(lo) : "v"(x0), "v"(x1));
+    return make_uint2(hi, lo);
+}
+
 __device__ __forceinline__ uint32_t lds_u32(const uint8_t * p) {
     uint32_t v;
     __builtin_memcpy(&v, p, 4);   // gfx950 LDS reads any alignment in one ds_read_b32
@@ -150,6 +172,12 @@ __device__ __forceinline__ const uint16_t * mask_row(const fa_args & a, int mr, 
     return (const uint16_t *) (a.mask + (size_t) t * a.m_nb1 + (size_t) hq * a.m_nb2 + (size_t) (b % a.m_ne3) * a.m_nb3);
 }
 
+// f[0 .. n) = 0 (dst is only 4-byte aligned, so plain f32 stores).
+__global__ void k_zero_f32(float * f, int64_t n) {
+    const int64_t stride = (int64_t) gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) f[i] = 0.f;
+}
+
 template <int RTW>
 __global__ __launch_bounds__(RTW * 128) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_fattn_q8_0(fa_args a) {
@@ -162,7 +190,8 @@ void k_fattn_q8_0(fa_args a) {
     __shared__ __attribute__((aligned(16))) uint8_t buf1[2 * CHUNK_BYTES];
     __shared__ __attribute__((aligned(16))) uint16_t scl[2][NBLK][CK];      // [K|V][block][key] fp16 scales
     __shared__ __attribute__((aligned(16))) uint16_t msk[MASK_LDS];         // mask of the block's split [row][key]
-    static_assert(ROWS * D + ROWS * NBLK * 4 <= 2 * CHUNK_BYTES, "Q staging fits in buffer 1");
+    // the block's query rows requantised to q8_0: quants [ROWS][256] then scales [ROWS][8] f32
+    __shared__ __attribute__((aligned(16))) uint8_t qsh[ROWS * D + ROWS * NBLK * 4];
     static_assert(ROWS * D * 4 + WAVES * 16 * 8 <= 2 * CHUNK_BYTES, "merge buffer fits in buffer 0");
 
     const int lane = threadIdx.x & 63;
@@ -225,6 +254,7 @@ void k_fattn_q8_0(fa_args a) {
     // Prologue: chunk 0's DMA, the block's Q rows and its mask are all put in
     // flight before anything waits, so they cost one memory round trip together.
     issue_chunk(0, buf0);
+    if (n_chunks > 1) issue_chunk(1, buf1);
     const int sub = lane & 7;       // 4-value group of a q8_0 block (Q staging)
     const int blk = lane >> 3;      // q8_0 block of the row (Q staging)
     float4 xv[ROWS / WAVES];
@@ -255,10 +285,10 @@ void k_fattn_q8_0(fa_args a) {
         }
     }
 
-    // ---- stage Q in buffer 1: requantise the block's query rows to q8_0 ----
+    // ---- requantise the block's query rows to q8_0 into qsh ----
     {
-        uint32_t * qs = (uint32_t *) buf1;
-        float *    qd = (float *) (buf1 + ROWS * D);
+        uint32_t * qs = (uint32_t *) qsh;
+        float *    qd = (float *) (qsh + ROWS * D);
 #pragma unroll
         for (int q = 0; q < ROWS / WAVES; q++) {
             const int rl = wave + q * WAVES;
@@ -271,18 +301,11 @@ void k_fattn_q8_0(fa_args a) {
             if (sub == 0) qd[rl * NBLK + blk] = dq;
         }
     }
-    __syncthreads();
-    long  qB[NBLK];
-    float dqr[NBLK];
     const int rl_lane = tile * 16 + ln;                 // this lane's query row (as MFMA column)
-#pragma unroll
-    for (int bb = 0; bb < NBLK; bb++) {
-        qB[bb] = (long) lds_u64(buf1 + rl_lane * D + bb * QK + lg * 8);
-        dqr[bb] = ((const float *) (buf1 + ROWS * D))[rl_lane * NBLK + bb];
-    }
+    // Q operands stay in LDS (re-read per key tile) to keep registers for occupancy
+    const uint8_t * qB_lds = qsh + rl_lane * D + lg * 8;
+    const float *   dq_lds = (const float *) (qsh + ROWS * D) + rl_lane * NBLK;
     const int mrow = rl_lane >= RW ? -1 : (a.m_ne2 == 1 ? (r0 + rl_lane) / a.gqa - t0 : rl_lane);
-    __syncthreads();   // buffer 1 is free again
-    if (n_chunks > 1) issue_chunk(1, buf1);
 
     // ---- online softmax state (one 16-row tile per wave) ----
     v4f   O[NBLK][2];
@@ -318,48 +341,58 @@ void k_fattn_q8_0(fa_args a) {
         const uint8_t * ks = cur;
         const uint8_t * vs = cur + CHUNK_BYTES;
 
-        // ---- S = Q K^T for 2 tiles of 16 keys ----
+        // ---- S = Q K^T for 2 tiles of 16 keys: all 8 block MFMAs of a tile in
+        //      flight before the d_q * d_k scaling consumes them ----
         float s[2][4];
 #pragma unroll
         for (int kt = 0; kt < 2; kt++) {
             const int kr = wk + kt * 16 + ln;                 // A-operand key row
             const int k4 = wk + kt * 16 + lg * 4;             // output keys k4..k4+3
-#pragma unroll
-            for (int i = 0; i < 4; i++) s[kt][i] = 0.f;
+            v4i cc[NBLK];
 #pragma unroll
             for (int bb = 0; bb < NBLK; bb++) {
                 const long kA = (long) lds_u64(ks + kr * SEG + bb * QBLOCK + 2 + lg * 8);
-                const uint64_t dk4 = lds_u64((const uint8_t *) &scl[0][bb][k4]);
-                const v4i cc = __builtin_amdgcn_mfma_i32_16x16x32_i8(kA, qB[bb], v4i{0, 0, 0, 0}, 0, 0, 0);
+                cc[bb] = __builtin_amdgcn_mfma_i32_16x16x32_i8(kA, (long) lds_u64(qB_lds + bb * QK), v4i{0, 0, 0, 0}, 0, 0, 0);
+            }
 #pragma unroll
-                for (int i = 0; i < 4; i++) s[kt][i] = __builtin_fmaf((float) cc[i], dqr[bb] * h2f(dk4, i), s[kt][i]);
+            for (int i = 0; i < 4; i++) s[kt][i] = 0.f;
+            const float4 dqa = *(const float4 *) dq_lds, dqb = *(const float4 *) (dq_lds + 4);
+            const float dqr[NBLK] = {dqa.x, dqa.y, dqa.z, dqa.w, dqb.x, dqb.y, dqb.z, dqb.w};
+#pragma unroll
+            for (int bb = 0; bb < NBLK; bb++) {
+                const uint64_t dk4 = lds_u64((const uint8_t *) &scl[0][bb][k4]);   // 4 keys' fp16 d_k
+                const uint32_t d01 = (uint32_t) dk4, d23 = (uint32_t) (dk4 >> 32);
+                s[kt][0] = __builtin_fmaf((float) cc[bb][0], mul_f16lo(dqr[bb], d01), s[kt][0]);
+                s[kt][1] = __builtin_fmaf((float) cc[bb][1], mul_f16hi(dqr[bb], d01), s[kt][1]);
+                s[kt][2] = __builtin_fmaf((float) cc[bb][2], mul_f16lo(dqr[bb], d23), s[kt][2]);
+                s[kt][3] = __builtin_fmaf((float) cc[bb][3], mul_f16hi(dqr[bb], d23), s[kt][3]);
             }
         }
 
-        // ---- mask, scale, online softmax (base 2) ----
+        // ---- mask, scale, online softmax (base 2). A masked key has mv = -inf,
+        //      so its x is -inf and its p is exp2(-inf) = 0 without selects ----
         float p[8];
         {
-            float sv[8];
+            float x[8];
             float mloc = -INFINITY;
 #pragma unroll
             for (int jj = 0; jj < 8; jj++) {
                 const int kin = c * CK + keyj[jj];               // key index within the split
-                float mv = -INFINITY;
-                if (mrow >= 0 && kin < span) mv = a.mask ? dev::f16_bits_to_f32(msk[mrow * mstride + kin]) : 0.f;
-                const float x = (mv == -INFINITY) ? -INFINITY : (s[jj >> 2][jj & 3] * a.scale + mv) * LOG2E;
-                sv[jj] = x;
-                mloc = xmax(mloc, x);
+                float mv = (mrow >= 0 && kin < span) ? 0.f : -INFINITY;
+                if (a.mask && mrow >= 0 && kin < span) mv = dev::f16_bits_to_f32(msk[mrow * mstride + kin]);
+                x[jj] = (s[jj >> 2][jj & 3] * a.scale + mv) * LOG2E;
+                mloc = xmax(mloc, x[jj]);
             }
             mloc = xmax(mloc, __shfl_xor(mloc, 16));
             mloc = xmax(mloc, __shfl_xor(mloc, 32));
             const float m_new = xmax(m_run, mloc);
-            const float alpha = (m_new == -INFINITY) ? 1.f : exp2f(m_run - m_new);
+            const float m_use = (m_new == -INFINITY) ? 0.f : m_new;   // all keys masked so far
+            const float alpha = exp2f(m_run - m_use);
             float lsum = 0.f;
 #pragma unroll
             for (int jj = 0; jj < 8; jj++) {
-                const float pv = (sv[jj] == -INFINITY) ? 0.f : exp2f(sv[jj] - m_new);
-                p[jj] = pv;
-                lsum += pv;
+                p[jj] = exp2f(x[jj] - m_use);
+                lsum += p[jj];
             }
             l_run = l_run * alpha + lsum;
             m_run = m_new;
@@ -369,12 +402,22 @@ void k_fattn_q8_0(fa_args a) {
             }
         }
 
-        // ---- O += V^T P (per V block: B = P * d_v) ----
+        // ---- O += V^T P (per V block: B = P * d_v as f16 hi + lo) ----
 #pragma unroll
         for (int bb = 0; bb < NBLK; bb++) {
             uint32_t w[8];
 #pragma unroll
             for (int jj = 0; jj < 8; jj++) w[jj] = lds_u32(vs + keyj[jj] * SEG + bb * QBLOCK + aoff);
+            const uint64_t dvlo = lds_u64((const uint8_t *) &scl[1][bb][keyj[0]]);
+            const uint64_t dvhi = lds_u64((const uint8_t *) &scl[1][bb][keyj[4]]);
+            const uint32_t dv[4] = {(uint32_t) dvlo, (uint32_t) (dvlo >> 32), (uint32_t) dvhi, (uint32_t) (dvhi >> 32)};
+            uint32_t bh[4], bl[4];
+#pragma unroll
+            for (int q2 = 0; q2 < 4; q2++) {
+                const uint2 hl = split_f16x2(mul_f16lo(p[2 * q2], dv[q2]), mul_f16hi(p[2 * q2 + 1], dv[q2]));
+                bh[q2] = hl.x;
+                bl[q2] = hl.y;
+            }
             uint32_t a0[4], a1[4];
 #pragma unroll
             for (int q2 = 0; q2 < 4; q2++) {
@@ -383,18 +426,8 @@ void k_fattn_q8_0(fa_args a) {
             }
             const v8h A0 = __builtin_bit_cast(v8h, uint4{a0[0], a0[1], a0[2], a0[3]});
             const v8h A1 = __builtin_bit_cast(v8h, uint4{a1[0], a1[1], a1[2], a1[3]});
-            const uint64_t dvlo = lds_u64((const uint8_t *) &scl[1][bb][keyj[0]]);
-            const uint64_t dvhi = lds_u64((const uint8_t *) &scl[1][bb][keyj[4]]);
-            // B = P*d_v split into f16 hi + lo parts (two MFMAs): ~22 significant
-            // bits, so a few dominant keys over large V values stay exact enough
-            v8h Bh, Bl;
-#pragma unroll
-            for (int jj = 0; jj < 8; jj++) {
-                const float x = p[jj] * h2f(jj < 4 ? dvlo : dvhi, jj & 3);
-                const _Float16 h = (_Float16) x;
-                Bh[jj] = h;
-                Bl[jj] = (_Float16) (x - (float) h);
-            }
+            const v8h Bh = __builtin_bit_cast(v8h, uint4{bh[0], bh[1], bh[2], bh[3]});
+            const v8h Bl = __builtin_bit_cast(v8h, uint4{bl[0], bl[1], bl[2], bl[3]});
             O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, Bh, O[bb][0], 0, 0, 0);
             O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, Bh, O[bb][1], 0, 0, 0);
             O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, Bl, O[bb][0], 0, 0, 0);
@@ -539,6 +572,24 @@ int env_int(const char * name, int dflt) {
     return s && *s ? std::atoi(s) : dflt;
 }
 
+// The key loop hand-counts its outstanding vector-memory operations (the LDS
+// DMAs are inline asm the compiler does not see), so a build of the attention
+// kernel that spills to scratch would break that count: refuse to run one.
+int check_no_scratch() {
+    static const int rc = [] {
+        for (const void * f : {(const void *) k_fattn_q8_0<1>, (const void *) k_fattn_q8_0<2>}) {
+            hipFuncAttributes at{};
+            if (int e = hip_check(hipFuncGetAttributes(&at, f), "hipFuncGetAttributes")) return e;
+            if (at.localSizeBytes != 0)
+                return set_error(QWFN_EDEVICE, "flash_attn_ext: attention kernel was built with " +
+                                                   std::to_string(at.localSizeBytes) + " B of scratch per lane");
+        }
+        return (int) QWFN_OK;
+    }();
+    if (rc) set_error(rc, "flash_attn_ext: attention kernel uses scratch memory (build is unusable)");
+    return rc;
+}
+
 int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v, const qwfn_tensor * mask,
                fa_plan * pl) {
     if (!q || !k || !v) return set_error(QWFN_EINVAL, "flash_attn_ext: NULL q/k/v");
@@ -647,9 +698,15 @@ extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor
     }
     const int64_t n_kv = k->ne[1];
     if (n_kv == 0) {
-        QWFN_HIP_TRY(hipMemsetAsync(dst->data, 0, view_bytes(*dst), as_stream(stream)));
-        return QWFN_OK;
+        // no keys: ggml-cpu divides 0 by S = 0 only for rows it visits; the
+        // result of an empty attention is defined here as zeros (a fill kernel,
+        // not a memset node, so the call stays capturable into a HIP graph)
+        const int64_t n = (int64_t) (view_bytes(*dst) / 4);
+        hipLaunchKernelGGL(k_zero_f32, dim3((unsigned) std::max<int64_t>(1, std::min<int64_t>((n + 255) / 256, 4096))),
+                           dim3(256), 0, as_stream(stream), (float *) dst->data, n);
+        return hip_check(hipGetLastError(), "flash_attn zero fill");
     }
+    if (int rc = check_no_scratch()) return rc;
 
     fa_args a{};
     a.q = (const char *) q->data; a.q_nb1 = q->nb[1]; a.q_nb2 = q->nb[2]; a.q_nb3 = q->nb[3];
