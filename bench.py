@@ -237,6 +237,17 @@ def main() -> int:
         except Exception as e:
             log(f"[bench] cpu baseline skipped: {e}")
 
+    # HBM traffic per launch of the attention kernel, measured by the two
+    # rocprofv3 --pmc passes summarised under profiles/ (FETCH_SIZE, WRITE_SIZE,
+    # each scaled by what the counter reads for a plain copy of known size)
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "fattn_q8_0.mtp_verify_16k.traffic.json")
+    if os.path.exists(tpath):
+        tj = json.load(open(tpath))
+        w = tj.get("workload", {})
+        if w.get("depth") == depth and w.get("T") == T:
+            traffic = tj["traffic_bytes"]
+
     best_ms = graph_ms if graph_ms is not None else eager_ms
     value = step_bytes / (best_ms * 1e-3) / 1e9
     achieved = attn_bytes / (attn_us * 1e-6) / 1e9
@@ -261,7 +272,7 @@ def main() -> int:
         "us_per_layer_graph": round(graph_ms * 1e3 / L, 3) if graph_ms is not None else None,
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "flash_attn_ext q8_0 (k_fattn_q8_0 + k_fattn_merge)",
                      "us_per_launch": round(attn_us, 3), "bytes_per_launch": attn_bytes},
         "cpu_baseline": cpu,
