@@ -111,7 +111,7 @@ def main() -> int:
     mv = K.mask_view(mask)
     views = [[(K.cache_attn_view(kc, n_kv, nh_kv), K.cache_attn_view(vc, n_kv, nh_kv)) for kc, vc in st]
              for st in caches]
-    ws_bytes = K.fattn_workspace_size(qv[0], views[0][0][0], views[0][0][1])
+    ws_bytes = K.fattn_workspace_size(qv[0], views[0][0][0], views[0][0][1], mv)
     ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
     scale = 1.0 / 16.0
 

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define QWFN_KV_ABI_VERSION 1
+#define QWFN_KV_ABI_VERSION 2
 
 /* ggml type numbering (ggml.h: GGML_TYPE_F32 = 0, F16 = 1, Q8_0 = 8, I32 = 26) */
 enum qwfn_type {
@@ -130,9 +130,13 @@ int qwfn_kv_gather_segments(const void * src, size_t src_row_stride, int64_t src
  * Semantics follow ggml-cpu's q8_0 path: Q is requantised to q8_0 with
  * `variant`, scores are sum_b d_k*d_q*isum_b, masked (-inf) keys are skipped,
  * softmax is online, V is dequantised q*d. A fully masked row gives 0.
- * ws: device workspace of at least qwfn_fattn_workspace_size() bytes, or NULL
- * to use a library-owned buffer (allocated on first use, not graph-capturable). */
-size_t qwfn_fattn_workspace_size(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v);
+ * ws: device workspace of at least qwfn_fattn_workspace_size(q, k, v, mask)
+ * bytes, or NULL to use a library-owned buffer (allocated on first use, not
+ * graph-capturable). The workspace holds the query operands prepared once per
+ * call, an aligned copy of the mask and, when the keys are split, the split
+ * partials; its contents need not be preserved between calls. */
+size_t qwfn_fattn_workspace_size(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
+                                 const qwfn_tensor * mask);
 int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
                              const qwfn_tensor * mask, float scale, float max_bias, float logit_softcap,
                              const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes, void * stream);

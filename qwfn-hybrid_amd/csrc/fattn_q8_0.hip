@@ -39,6 +39,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
+#include <type_traits>
 
 namespace qwfn {
 namespace {
@@ -46,17 +47,23 @@ namespace {
 typedef int      v4i __attribute__((ext_vector_type(4)));
 typedef float    v4f __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef _Float16 h2  __attribute__((ext_vector_type(2)));
+typedef uint16_t us2 __attribute__((ext_vector_type(2)));
 
 constexpr int D      = 256;            // head size (values per head row)
 constexpr int NBLK   = D / QK;         // 8 q8_0 blocks per head row
 constexpr int SEG    = NBLK * QBLOCK;  // 272 bytes per head row
-constexpr int KW     = 32;             // keys per wave per chunk (one PV MFMA depth)
-constexpr int KG     = 2;              // key groups (waves along the keys of a chunk)
+constexpr int KW     = 16;             // keys per wave per chunk (one QK tile, one PV MFMA depth)
+constexpr int KG     = 4;              // key groups = waves of a block
 constexpr int CK     = KG * KW;        // keys per chunk
 constexpr int CHUNK_BYTES = CK * SEG;  // one tensor's rows of a chunk (17408)
 constexpr int DMA_PER_TENSOR = CHUNK_BYTES / 1024;   // wave-wide 16-byte LDS-DMA loads per tensor (17)
-constexpr int MASK_LDS = 2048;         // staged mask values per block (rows x keys of its split)
+constexpr int MASK_ROWS = 16;          // mask rows a block streams with each chunk
+constexpr int MASK_BYTES = MASK_ROWS * CK * 2;       // a chunk's mask slice in LDS (2048)
+constexpr int STAGE_BYTES = 2 * CHUNK_BYTES + MASK_BYTES;   // one ring stage: K rows, V rows, mask slice
+constexpr int DMA_SLOTS = 2 * DMA_PER_TENSOR + MASK_BYTES / 1024;   // wave-wide DMAs per chunk (36)
+constexpr int QROWS_IMG = 32;          // d_q rows per row group in the query image (one 1 KB DMA)
 constexpr int QWIN   = 64;             // bytes of one block's query window
 constexpr int MAX_SPLITS = 1024;       // key splits per (batch, KV head, row group)
 constexpr float LOG2E = 1.4426950408889634f;
@@ -79,7 +86,11 @@ struct fa_args {
     float *  dst;          // [D, nh, T, B]
     float *  part_o;       // [B][nh_kv][ns][R][D]
     float2 * part_ml;      // [B][nh_kv][ns][R]: (running max in log2 units, sum)
+    uint4 *  qimg;         // [B][nh_kv][n_rg][RT][64 lanes][NBLK]: lane's 16-byte query window slices
+    float *  dqimg;        // [B][nh_kv][n_rg][32 rows][NBLK]: d_q * scale * log2(e)
+    uint16_t * mimg;       // [m_ne3][m_ne2][T][n_kv_pad] F16 mask copy, -inf past n_kv (or null)
     int64_t  n_kv;
+    int64_t  n_kv_pad;     // n_kv rounded up to a chunk
     int32_t  T, nh, nh_kv, gqa, R, B;
     int32_t  kb, vb;       // K/V batch extents (ne[3]); batch b reads b % kb
     int32_t  ns;           // key splits
@@ -91,18 +102,42 @@ struct fa_args {
     int32_t  dst_vec;      // dst is 16-byte aligned: float4 stores
 };
 
-// Two int8 values (byte SEL of a and of b) -> packed f16 pair, exact.
-#define QWFN_CVT_I8X2(NAME, SEL)                                                                  \
-    __device__ __forceinline__ uint32_t NAME(uint32_t a, uint32_t b) {                            \
-        uint32_t r;                                                                               \
-        asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:" SEL  \
-            "\n\tv_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:" SEL \
-            : "=&v"(r) : "v"(a), "v"(b));                                                         \
-        return r;                                                                                 \
-    }
-QWFN_CVT_I8X2(cvt_i8x2_f16_b0, "BYTE_0")
-QWFN_CVT_I8X2(cvt_i8x2_f16_b1, "BYTE_1")
-#undef QWFN_CVT_I8X2
+// The compiler's hazard recognizer does not see the VALU writes inside inline
+// asm, and an MFMA that reads a VGPR needs two wait states after a VALU wrote
+// it. Every asm below whose result can feed an MFMA operand therefore ends
+// with s_nop 1.
+
+// One V block's A operands for the lane's 4 keys: w[q] holds dims 2m, 2m+1
+// of keys 2q (bytes 0-1) and 2q+1 (bytes 2-3); a0[q] = f16 pair (dim 2m of
+// both keys), a1[q] = f16 pair (dim 2m+1). int8 -> f16 is exact.
+__device__ __forceinline__ void cvt_v_block(const uint32_t w[2], uint32_t a0[2], uint32_t a1[2]) {
+#define QWFN_SDWA(D, S, DSEL, UNUSED, SSEL) "v_cvt_f16_i16_sdwa " D ", sext(" S ") dst_sel:" DSEL " dst_unused:" UNUSED " src0_sel:" SSEL "\n\t"
+#define QWFN_PAIR(D, S, B0, B1) QWFN_SDWA(D, S, "WORD_0", "UNUSED_PAD", B0) QWFN_SDWA(D, S, "WORD_1", "UNUSED_PRESERVE", B1)
+    asm volatile(QWFN_PAIR("%0", "%4", "BYTE_0", "BYTE_2") QWFN_PAIR("%1", "%5", "BYTE_0", "BYTE_2")
+                 QWFN_PAIR("%2", "%4", "BYTE_1", "BYTE_3") QWFN_PAIR("%3", "%5", "BYTE_1", "BYTE_3")
+                 "s_nop 1"
+                 : "=&v"(a0[0]), "=&v"(a0[1]), "=&v"(a1[0]), "=&v"(a1[1])
+                 : "v"(w[0]), "v"(w[1]));
+#undef QWFN_PAIR
+#undef QWFN_SDWA
+}
+
+// B operands of one V block: for key pairs q (keys 2q, 2q+1), P*d_v as an f16
+// hi pair, bh[q] = f16(p*d_v) (RNE), and a lo pair, bl[q] = f16(p*d_v - hi),
+// each from one fused v_fma_mix (the product is exact before its rounding).
+// dv[q] holds the two keys' fp16 d_v.
+__device__ __forceinline__ void pdv_hilo(const float p[4], const uint32_t dv[2], uint32_t bh[2], uint32_t bl[2]) {
+#define QWFN_HILO(H, L, P0, P1, DV)                                                                   \
+    "v_fma_mixlo_f16 " H ", " P0 ", " DV ", 0 op_sel:[0,0,0] op_sel_hi:[0,1,0]\n\t"                     \
+    "v_fma_mixhi_f16 " H ", " P1 ", " DV ", 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"                     \
+    "v_fma_mixlo_f16 " L ", " P0 ", " DV ", -" H " op_sel:[0,0,0] op_sel_hi:[0,1,1]\n\t"                \
+    "v_fma_mixhi_f16 " L ", " P1 ", " DV ", -" H " op_sel:[0,1,1] op_sel_hi:[0,1,1]\n\t"
+    asm volatile(QWFN_HILO("%0", "%2", "%4", "%5", "%8") QWFN_HILO("%1", "%3", "%6", "%7", "%9")
+                 "s_nop 1"
+                 : "=&v"(bh[0]), "=&v"(bh[1]), "=&v"(bl[0]), "=&v"(bl[1])
+                 : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]), "v"(dv[0]), "v"(dv[1]));
+#undef QWFN_HILO
+}
 
 // x * f16 (low or high half of a packed dword), one v_fma_mix_f32.
 __device__ __forceinline__ float mul_f16lo(float x, uint32_t h) {
@@ -126,18 +161,33 @@ __device__ __forceinline__ float fma_f16hi(uint32_t h, float c, float x) {
     asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(c), "v"(x));
     return r;
 }
-// Split two f32 values into f16 hi parts (RNE) and f16 lo = f16(x - hi):
-// returns {hi pair, lo pair} as packed dwords.
-__device__ __forceinline__ uint2 split_f16x2(float x0, float x1) {
-    uint32_t hi, lo;
-    asm("v_cvt_pk_f16_f32 %0, %2, %3\n\t"
-        "v_fma_mixlo_f16 %1, %2, 1.0, -%0 op_sel:[0,0,0] op_sel_hi:[0,0,1]\n\t"
-        "v_fma_mixhi_f16 %1, %3, 1.0, -%0 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
-        : "=&v"(hi), "=&v"(lo) : "v"(x0), "v"(x1));
-    return make_uint2(hi, lo);
-}
-
 __device__ __forceinline__ float xmax(float a, float b) { return a > b ? a : b; }
+
+// Reductions over the 4 lanes l, l^16, l^32, l^48 (the four lane groups
+// holding one MFMA column), with gfx950's cross-row swaps instead of LDS
+// permutes: a swap pair holds lanes l and l^16 (or l^32) between its two
+// results. The two results pass through an empty asm: without it the
+// compiler's IR folds the second result into the first (r[0] op r[1] becomes
+// r[0] op r[0]), which silently turns the reduction into x op x.
+template <typename Op>
+__device__ __forceinline__ float reduce_lanes16_32(float x, Op op) {
+    const unsigned u = __builtin_bit_cast(unsigned, x);
+    const auto r16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    unsigned a = r16[0], b = r16[1];
+    asm volatile("" : "+v"(a), "+v"(b));
+    x = op(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+    const unsigned w = __builtin_bit_cast(unsigned, x);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+    unsigned c = r32[0], d = r32[1];
+    asm volatile("" : "+v"(c), "+v"(d));
+    return op(__builtin_bit_cast(float, c), __builtin_bit_cast(float, d));
+}
+__device__ __forceinline__ float xmax_lanes16_32(float x) {
+    return reduce_lanes16_32(x, [](float a, float b) { return xmax(a, b); });
+}
+__device__ __forceinline__ float sum_lanes16_32(float x) {
+    return reduce_lanes16_32(x, [](float a, float b) { return a + b; });
+}
 
 // s_waitcnt that waits for vmcnt <= n only (gfx9 encoding: vmcnt[3:0] in
 // bits 3:0, vmcnt[5:4] in bits 15:14, expcnt and lgkmcnt left at their max).
@@ -171,15 +221,13 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Base of staged mask row mr of this block (F16 row over keys), or nullptr.
-// Row mr is query position t0 + mr for a shared mask, query row r0 + mr for a
-// per-head mask.
-__device__ __forceinline__ const uint16_t * mask_row(const fa_args & a, int mr, int t0, int r0, int kvh, int b) {
-    if (!a.mask) return nullptr;
+// Row of the mask copy that staged row mr of a block reads: query position
+// t0 + mr for a shared mask, query row r0 + mr for a per-head mask.
+__device__ __forceinline__ int64_t mask_img_row(const fa_args & a, int mr, int t0, int r0, int kvh, int b) {
     int t, hq;
     if (a.m_ne2 == 1) { t = t0 + mr; hq = 0; }
     else { const int r = r0 + mr; t = r / a.gqa; hq = (kvh * a.gqa + (r - t * a.gqa)) % a.m_ne2; }
-    return (const uint16_t *) (a.mask + (size_t) t * a.m_nb1 + (size_t) hq * a.m_nb2 + (size_t) (b % a.m_ne3) * a.m_nb3);
+    return ((int64_t) (b % a.m_ne3) * a.m_ne2 + hq) * a.T + t;
 }
 
 // f[0 .. n) = 0 (dst is only 4-byte aligned, so plain f32 stores).
@@ -188,29 +236,102 @@ __global__ void k_zero_f32(float * f, int64_t n) {
     for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) f[i] = 0.f;
 }
 
+// Per-call preparation shared by every key split:
+//  * blocks [0, n_qblocks): one (batch, KV head, row group) each. The query
+//    rows are requantised to q8_0 (ggml-cpu's quantiser, `x86` variant) and
+//    each q8_0 block is laid out on its 64-byte window (zero outside the
+//    block); the result is stored in the order the attention lanes load it as
+//    MFMA B operands, with d_q * scale * log2(e) beside it.
+//  * blocks past that: the F16 mask rows [0, T) of every (head, batch) slice
+//    are copied to a 16-byte aligned image padded with -inf up to n_kv_pad, so
+//    the attention kernel can stream each chunk's slice with the K/V DMA.
 template <int RT>
-__global__ __launch_bounds__(RT * KG * 64)
-void k_fattn_q8_0(fa_args a) {
-    constexpr int WAVES = RT * KG;
-    constexpr int THREADS = WAVES * 64;
+__global__ __launch_bounds__(256) void k_fattn_prep(fa_args a, int n_qblocks) {
     constexpr int ROWS = 16 * RT;
-    constexpr int DPW = (2 * DMA_PER_TENSOR + WAVES - 1) / WAVES;   // DMAs per wave per chunk
-    // two chunk buffers, each K rows [CK][272] then V rows [CK][272]
-    __shared__ __attribute__((aligned(16))) uint8_t ring[2][2 * CHUNK_BYTES];
+    if ((int) blockIdx.x >= n_qblocks) {
+        if (!a.mask) return;
+        const int64_t rows = (int64_t) a.m_ne3 * a.m_ne2 * a.T;
+        const int64_t units = rows * (a.n_kv_pad / 8);            // 8 keys (16 bytes) per unit
+        const int64_t stride = (int64_t) (gridDim.x - n_qblocks) * 256;
+        for (int64_t e = (int64_t) (blockIdx.x - n_qblocks) * 256 + threadIdx.x; e < units; e += stride) {
+            const int64_t row = e / (a.n_kv_pad / 8);
+            const int64_t k0 = (e - row * (a.n_kv_pad / 8)) * 8;
+            const int t = (int) (row % a.T);
+            const int64_t hs = row / a.T;
+            const int hq = (int) (hs % a.m_ne2), bm = (int) (hs / a.m_ne2);
+            const uint16_t * src = (const uint16_t *) (a.mask + (size_t) t * a.m_nb1 + (size_t) hq * a.m_nb2 + (size_t) bm * a.m_nb3);
+            uint16_t v[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = k0 + i < a.n_kv ? src[k0 + i] : (uint16_t) 0xFC00;
+            uint4 w;
+            w.x = v[0] | ((uint32_t) v[1] << 16); w.y = v[2] | ((uint32_t) v[3] << 16);
+            w.z = v[4] | ((uint32_t) v[5] << 16); w.w = v[6] | ((uint32_t) v[7] << 16);
+            *(uint4 *) (a.mimg + row * a.n_kv_pad + k0) = w;
+        }
+        return;
+    }
+    __shared__ __attribute__((aligned(16))) uint8_t qwin[ROWS * NBLK * QWIN];
+    const int bkr = blockIdx.x;                    // (b * nh_kv + kvh) * n_rg + rg
+    const int rg = bkr % a.n_rg, kvh = (bkr / a.n_rg) % a.nh_kv, b = bkr / (a.n_rg * a.nh_kv);
+    const int r0 = rg * a.rw;
+    const int RW = min(a.rw, a.R - r0);
+    for (int e = threadIdx.x; e < ROWS * NBLK * QWIN / 16; e += 256) ((uint4 *) qwin)[e] = make_uint4(0, 0, 0, 0);
+    __syncthreads();
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int sub = lane & 7, blk = lane >> 3;
+    const float fs = a.scale * LOG2E;
+    for (int rl = wave; rl < ROWS; rl += 4) {
+        const int r = r0 + min(rl, RW - 1);
+        const int t = r / a.gqa, h = kvh * a.gqa + (r - t * a.gqa);
+        float4 v4 = *(const float4 *) (a.q + (size_t) t * a.q_nb1 + (size_t) h * a.q_nb2 + (size_t) b * a.q_nb3 +
+                                       (size_t) (blk * QK + sub * 4) * 4);
+        if (rl >= RW) v4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        const float x[4] = {v4.x, v4.y, v4.z, v4.w};
+        uint16_t d16;
+        float dq;
+        const uint32_t w = dev::q8_quantize_lane4(x, a.x86 != 0, &d16, &dq);
+        uint16_t * wp = (uint16_t *) (qwin + (rl * NBLK + blk) * QWIN + win_off(blk) + 4 * sub);
+        wp[0] = (uint16_t) w;
+        wp[1] = (uint16_t) (w >> 16);
+        if (sub == 0) a.dqimg[((size_t) bkr * QROWS_IMG + rl) * NBLK + blk] = dq * fs;
+    }
+    __syncthreads();
+    // lane (ln, lg) of row tile `tile` reads slice lg of row 16*tile + ln's window, per block
+    for (int e = threadIdx.x; e < RT * 64 * NBLK; e += 256) {
+        const int tile = e / (64 * NBLK), ln_ = (e / NBLK) & 63, bb = e % NBLK;
+        const int row = tile * 16 + (ln_ & 15), lg_ = ln_ >> 4;
+        a.qimg[(size_t) bkr * RT * 64 * NBLK + e] = *(const uint4 *) (qwin + (row * NBLK + bb) * QWIN + 16 * lg_);
+    }
+}
+
+// 16-byte global load into registers, issued as inline asm so that its
+// completion is tracked by the kernel's own vmcnt waits (like the LDS DMAs)
+// rather than by compiler-inserted ones.
+__device__ __forceinline__ v4i gload16_asm(const void * p) {
+    v4i r;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p) : "memory");
+    return r;
+}
+
+template <int RT>
+__global__ __launch_bounds__(KG * 64)
+void k_fattn_q8_0(fa_args a) {
+    constexpr int WAVES = KG;
+    constexpr int ROWS = 16 * RT;
+    constexpr int DPW = DMA_SLOTS / WAVES;         // DMAs per wave per chunk
+    static_assert(DMA_SLOTS % WAVES == 0, "every wave issues the same number of DMAs");
+    // two ring stages, each K rows [CK][272], V rows [CK][272], mask [MASK_ROWS][CK] F16
+    __shared__ __attribute__((aligned(16))) uint8_t ring[2][STAGE_BYTES];
     // per-wave scale tables of the current chunk: [K|V][block][key of the wave] fp16
     __shared__ __attribute__((aligned(16))) uint16_t scl[WAVES][2][NBLK][KW];
-    __shared__ __attribute__((aligned(16))) uint16_t msk[MASK_LDS];         // mask of the block's split [row][key]
-    // prologue scratch in ring stage 1 (before chunk 1's DMA): query windows
-    // [ROWS][NBLK][64] int8, then d_q [ROWS][NBLK] f32
-    static_assert(ROWS * NBLK * QWIN + ROWS * NBLK * 4 <= 2 * CHUNK_BYTES, "query scratch fits in stage 1");
-    static_assert(ROWS * D * 4 + WAVES * 16 * 8 <= 2 * CHUNK_BYTES, "merge buffer fits in stage 0");
+    __shared__ __attribute__((aligned(16))) float dql[QROWS_IMG][NBLK];     // d_q * scale * log2(e) per row and block
+    static_assert(ROWS * D * 4 + WAVES * ROWS * 8 <= STAGE_BYTES, "merge buffer fits in stage 0");
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform (SGPR)
     const int ln = lane & 15;       // MFMA row/col within a 16-tile
     const int lg = lane >> 4;       // lane group (k-slice / output row quad)
-    const int tile = wave % RT;     // query row tile of this wave
-    const int kgrp = wave / RT;     // key group of each chunk
+    const int kgrp = wave;          // key group: keys 16*kgrp .. 16*kgrp+15 of every chunk
 
     // ---- block -> (b, kvh, row group, split) ----
     const int id   = blockIdx.x;
@@ -230,312 +351,330 @@ void k_fattn_q8_0(fa_args a) {
     const int r0 = rg * a.rw;                          // first query row of this block
     const int RW = std::min(a.rw, a.R - r0);          // rows in this block
     const int t0 = r0 / a.gqa;
-    const int n_mrows = a.m_ne2 == 1 ? (r0 + RW - 1) / a.gqa - t0 + 1 : RW;
+    const int n_mrows = a.m_ne2 == 1 ? (r0 + RW - 1) / a.gqa - t0 + 1 : RW;   // <= MASK_ROWS (planned)
+    const int bkr = (b * a.nh_kv + kvh) * a.n_rg + rg;
 
     const char * kbase = a.k + (size_t) (b % a.kb) * a.k_nb3 + (size_t) kvh * a.k_nb2;
     const char * vbase = a.v + (size_t) (b % a.vb) * a.v_nb3 + (size_t) kvh * a.v_nb2;
 
-    // Issue chunk c's K/V rows into buffer dstb. Every wave issues exactly DPW
-    // instructions (surplus ones repeat an instruction another wave covers,
-    // writing identical bytes), so the number of loads in flight is known at
-    // compile time. Piece p = 64*i + lane of a tensor's chunk is byte
-    // 16*(p % 17) of key p / 17. Keys past the split are loaded (and masked)
-    // while they exist; past n_kv they repeat the last key.
-    uint32_t doff[DPW];             // per-lane byte offset of piece n within a chunk
-#pragma unroll
-    for (int n = 0; n < DPW; n++) {
-        int i = wave + n * WAVES;
-        if (i >= 2 * DMA_PER_TENSOR) i = 2 * DMA_PER_TENSOR - 1 - (i - 2 * DMA_PER_TENSOR);
-        const int tensor = i >= DMA_PER_TENSOR;
-        const int p = (i - tensor * DMA_PER_TENSOR) * 64 + lane;
-        doff[n] = (uint32_t) ((p / 17) * (tensor ? a.v_nb1 : a.k_nb1) + (p % 17) * 16);
-    }
-    auto issue_chunk = [&](int c, uint8_t * dstb) __attribute__((always_inline)) {
+    // Issue part of chunk c into stage dstb: the chunk is DMA_SLOTS wave-wide
+    // 16-byte DMAs, DPW per wave, issued as slots [n0, n1) of the wave. Wave w
+    // issues slots w, w + WAVES, ...: slots 0-16 are K pieces, 17-33 V pieces
+    // (piece p = 64*i + lane of a tensor's chunk is byte 16*(p % 17) of key
+    // p / 17; keys past the split are loaded and masked while they exist, past
+    // n_kv they repeat the last key), 34-35 the chunk's mask slice, rows 0-7 and
+    // 8-15. Only a wave's last slot can be a mask slot; without a mask it
+    // repeats the wave's first piece.
+    static_assert((DPW - 1) * WAVES + WAVES - 1 < DMA_SLOTS && (DPW - 1) * WAVES <= 2 * DMA_PER_TENSOR,
+                  "the mask slots are the last slot of some waves");
+    auto issue_part = [&](int c, uint8_t * dstb, auto n0c, auto n1c) __attribute__((always_inline)) {
+        constexpr int n0 = decltype(n0c)::value, n1 = decltype(n1c)::value;
         const int64_t c0 = k_lo + (int64_t) c * CK;
         const bool clamp = c0 + CK > a.n_kv;   // the cache's last chunk: no rows past n_kv
         const int last = (int) std::min<int64_t>(CK - 1, a.n_kv - 1 - c0);
-#pragma unroll
-        for (int n = 0; n < DPW; n++) {
-            int i = wave + n * WAVES;
-            if (i >= 2 * DMA_PER_TENSOR) i = 2 * DMA_PER_TENSOR - 1 - (i - 2 * DMA_PER_TENSOR);
+        int ln_o = lane;
+        asm volatile("" : "+v"(ln_o));          // recomputed per chunk: no hoisted per-piece addresses
+        const char * kc0 = kbase + (size_t) c0 * a.k_nb1;
+        const char * vc0 = vbase + (size_t) c0 * a.v_nb1;
+        auto kv_piece = [&](int i) __attribute__((always_inline)) {
             const int tensor = i >= DMA_PER_TENSOR;
             const int ii = i - tensor * DMA_PER_TENSOR;
-            const char * base = tensor ? vbase + (size_t) c0 * a.v_nb1 : kbase + (size_t) c0 * a.k_nb1;
-            uint32_t off = doff[n];
-            if (clamp) {
-                const int p = ii * 64 + lane;
-                off = (uint32_t) (std::min(p / 17, last) * (tensor ? a.v_nb1 : a.k_nb1) + (p % 17) * 16);
-            }
-            dma16(base + off, __builtin_amdgcn_readfirstlane(lds_addr(dstb + tensor * CHUNK_BYTES + ii * 1024)));
+            const unsigned p = (unsigned) (ii * 64) + (unsigned) ln_o;      // < 1088
+            // p / 17 and p % 17 with full-rate 24-bit multiplies: (p * 3856) >> 16
+            // is exact for p < 1088
+            unsigned key = __umul24(p, 3856u) >> 16;
+            const unsigned part = p - __umul24(key, 17u);
+            if (clamp) key = std::min(key, (unsigned) last);
+            // row strides are < 2^24 (checked on the host): 24-bit multiplies suffice
+            const char * src = (tensor ? vc0 + __umul24(key, (unsigned) a.v_nb1) : kc0 + __umul24(key, (unsigned) a.k_nb1)) + part * 16;
+            dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(dstb + tensor * CHUNK_BYTES + ii * 1024)));
+        };
+#pragma unroll
+        for (int n = n0; n < (n1 < DPW - 1 ? n1 : DPW - 1); n++) kv_piece(wave + n * WAVES);
+        if constexpr (n1 < DPW) return;
+        const int il = wave + (DPW - 1) * WAVES;
+        if (il < 2 * DMA_PER_TENSOR) {
+            kv_piece(il);
+        } else if (a.mask) {
+            const int m = il - 2 * DMA_PER_TENSOR;
+            const int mr = std::min(m * 8 + (ln_o >> 3), n_mrows - 1);
+            const uint16_t * src = a.mimg + mask_img_row(a, mr, t0, r0, kvh, b) * a.n_kv_pad + c0 + (ln_o & 7) * 8;
+            dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(dstb + 2 * CHUNK_BYTES + m * 1024)));
+        } else {
+            kv_piece(wave);
         }
     };
-    const int span = (int) (k_hi - k_lo);                       // keys of this split (<= split_len)
-    const int mstride = a.split_len;                            // LDS row stride of the staged mask
 
-    // ---- prologue: chunk 0's DMA first, then the block's Q rows and its mask.
-    //      Waiting for the (later) ordinary loads also lands chunk 0. ----
-    issue_chunk(0, ring[0]);
-    const int sub = lane & 7;       // 4-value group of a q8_0 block (Q staging)
-    const int blk = lane >> 3;      // q8_0 block of the row (Q staging)
-    float4 xv[ROWS / WAVES];
-#pragma unroll
-    for (int q = 0; q < ROWS / WAVES; q++) {
-        const int rl = wave + q * WAVES;
-        const int r = r0 + std::min(rl, RW - 1);
-        const int t = r / a.gqa, h = kvh * a.gqa + (r - t * a.gqa);
-        xv[q] = *(const float4 *) (a.q + (size_t) t * a.q_nb1 + (size_t) h * a.q_nb2 + (size_t) b * a.q_nb3 +
-                                   (size_t) (blk * QK + sub * 4) * 4);
-    }
-    if (a.mask) {
-        constexpr int MB = 8;                                   // loads in flight per thread
-        for (int e0 = threadIdx.x; e0 < n_mrows * mstride; e0 += MB * THREADS) {
-            uint16_t mv[MB];
-#pragma unroll
-            for (int q = 0; q < MB; q++) {
-                const int e = e0 + q * THREADS;
-                const int mr = std::min(e / mstride, n_mrows - 1);
-                const int key = std::min(e - (e / mstride) * mstride, span - 1);
-                mv[q] = mask_row(a, mr, t0, r0, kvh, b)[k_lo + key];
-            }
-#pragma unroll
-            for (int q = 0; q < MB; q++) {
-                const int e = e0 + q * THREADS;
-                if (e < n_mrows * mstride) msk[e] = mv[q];
-            }
-        }
-    }
-
-    // ---- requantise the block's query rows to q8_0 and lay each block out on
-    //      its 64-byte window (zero elsewhere), in ring stage 1 ----
-    uint8_t * qwin = ring[1];
-    float *   dqs  = (float *) (ring[1] + ROWS * NBLK * QWIN);
-    for (int e = threadIdx.x; e < ROWS * NBLK * QWIN / 16; e += THREADS) ((uint4 *) qwin)[e] = make_uint4(0, 0, 0, 0);
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < ROWS / WAVES; q++) {
-        const int rl = wave + q * WAVES;
-        const float4 v4 = rl < RW ? xv[q] : make_float4(0.f, 0.f, 0.f, 0.f);
-        const float x[4] = {v4.x, v4.y, v4.z, v4.w};
-        uint16_t d16;
-        float dq;
-        const uint32_t w = dev::q8_quantize_lane4(x, a.x86 != 0, &d16, &dq);
-        uint16_t * wp = (uint16_t *) (qwin + (rl * NBLK + blk) * QWIN + win_off(blk) + 4 * sub);
-        wp[0] = (uint16_t) w;
-        wp[1] = (uint16_t) (w >> 16);
-        if (sub == 0) dqs[rl * NBLK + blk] = dq;
-    }
-    __syncthreads();
-    const int rl_lane = tile * 16 + ln;                 // this lane's query row (MFMA column)
-    v4i qw[NBLK];                                       // B operand of QK: window slice lg of each block
-#pragma unroll
-    for (int bb = 0; bb < NBLK; bb++) qw[bb] = *(const v4i *) (qwin + (rl_lane * NBLK + bb) * QWIN + 16 * lg);
-    float dqr[NBLK];                                    // d_q * scale * log2(e)
+    // ---- prologue: the lane's query operands (prepared once per call) and
+    //      chunk 0, one wait for both. Chunk c+1 is then issued during chunk c's
+    //      compute, in three parts, so the DMA queue drains while the wave works ----
+    v4i qw[RT][NBLK];                                   // B operands of QK: window slice lg of each block, per row tile
     {
-        const float4 d0 = *(const float4 *) (dqs + rl_lane * NBLK), d1 = *(const float4 *) (dqs + rl_lane * NBLK + 4);
-        const float f = a.scale * LOG2E;
-        dqr[0] = d0.x * f; dqr[1] = d0.y * f; dqr[2] = d0.z * f; dqr[3] = d0.w * f;
-        dqr[4] = d1.x * f; dqr[5] = d1.y * f; dqr[6] = d1.z * f; dqr[7] = d1.w * f;
-    }
-    __syncthreads();                                    // stage 1 is free again
-    if (n_chunks > 1) issue_chunk(1, ring[1]);
-    // padded rows (rl_lane >= RW) read mask row 0: their results are never stored
-    const int mrow = rl_lane >= RW ? 0 : (a.m_ne2 == 1 ? (r0 + rl_lane) / a.gqa - t0 : rl_lane);
-
-    // ---- online softmax state (one 16-row tile per wave) ----
-    v4f   O[NBLK][2];
-    float m_run = -INFINITY, l_run = 0.f;
 #pragma unroll
-    for (int bb = 0; bb < NBLK; bb++) { O[bb][0] = v4f{0, 0, 0, 0}; O[bb][1] = v4f{0, 0, 0, 0}; }
+        for (int t = 0; t < RT; t++) {
+            const uint4 * qp = a.qimg + ((size_t) bkr * RT * 64 + t * 64 + lane) * NBLK;
+#pragma unroll
+            for (int bb = 0; bb < NBLK; bb++) qw[t][bb] = gload16_asm(qp + bb);
+        }
+        if (wave == 0) dma16(a.dqimg + (size_t) bkr * QROWS_IMG * NBLK + lane * 4, __builtin_amdgcn_readfirstlane(lds_addr(&dql[0][0])));
+    }
+    issue_part(0, ring[0], std::integral_constant<int, 0>{}, std::integral_constant<int, DPW>{});
+    wait_vmcnt<0>();
+#pragma unroll
+    for (int t = 0; t < RT; t++)
+#pragma unroll
+        for (int bb = 0; bb < NBLK; bb++) asm volatile("" : "+v"(qw[t][bb]));   // loaded: usable from here on
+    // the lane's query row in tile t is 16t + ln; padded rows (>= RW) read mask
+    // row 0 and are never stored
+    int mrow[RT];
+#pragma unroll
+    for (int t = 0; t < RT; t++) {
+        const int rl = t * 16 + ln;
+        mrow[t] = rl >= RW ? 0 : (a.m_ne2 == 1 ? (r0 + rl) / a.gqa - t0 : rl);
+    }
+
+    // ---- online softmax state per row tile ----
+    v4f   O[RT][NBLK][2];
+    float m_run[RT], l_run[RT];
+#pragma unroll
+    for (int t = 0; t < RT; t++) {
+        m_run[t] = -INFINITY;
+        l_run[t] = 0.f;
+#pragma unroll
+        for (int bb = 0; bb < NBLK; bb++) { O[t][bb][0] = v4f{0, 0, 0, 0}; O[t][bb][1] = v4f{0, 0, 0, 0}; }
+    }
 
     const int wk = kgrp * KW;   // this wave's first key in a chunk
+    const int span = (int) (k_hi - k_lo);                       // keys of this split (<= split_len)
     uint16_t (*sw)[NBLK][KW] = scl[wave];
 
-    // One chunk: `cur` holds chunk c. Called with ring[0] / ring[1] literally so
-    // the compiler can tell the buffer being read from the one the DMA fills.
-    auto chunk_step = [&](int c, uint8_t * cur) __attribute__((always_inline)) {
-        if (c + 1 < n_chunks) {
-            // chunk c+1's DMA is the only one issued after chunk c's: once at most
-            // that many loads are outstanding, chunk c has landed
-            wait_vmcnt<DPW>();
-        } else {
-            wait_vmcnt<0>();
-        }
+    // One chunk: `cur` holds chunk c; chunk c+1 goes to `nxt`. Called with the
+    // ring stages literally so the compiler can tell them apart.
+    constexpr int P1 = DPW / 3, P2 = 2 * DPW / 3;
+    auto chunk_step = [&](int c, uint8_t * cur, uint8_t * nxt) __attribute__((always_inline)) {
+        // chunk c was the last thing issued (during step c-1): wait for all of
+        // it; the barrier publishes it and also tells every wave that `nxt`
+        // (chunk c-1's stage) is no longer read
+        wait_vmcnt<0>();
         __syncthreads();
+        const bool more = c + 1 < n_chunks;
         const uint8_t * ks = cur;
         const uint8_t * vs = cur + CHUNK_BYTES;
-        // this wave's keys' block scales, transposed to [block][key]
+        // this wave's keys' block scales, transposed to [block][key] (all reads
+        // issued before the writes: the two LDS arrays could alias as far as the
+        // compiler knows, so interleaving would serialise them)
+        {
+            // entry n of this lane: tensor n / 2, key (n % 2) * 8 + lane / 8, block lane % 8
+            const uint8_t * src = cur + (wk + (lane >> 3)) * SEG + (lane & 7) * QBLOCK;
+            uint16_t * dstw = &sw[0][lane & 7][lane >> 3];
+            uint16_t sv[4];
 #pragma unroll
-        for (int n = 0; n < 2 * NBLK * KW / 64; n++) {
-            const int e = n * 64 + lane;
-            const int tensor = e / (NBLK * KW), kk = (e / NBLK) % KW, bb = e % NBLK;
-            sw[tensor][bb][kk] = *(const uint16_t *) (cur + tensor * CHUNK_BYTES + (wk + kk) * SEG + bb * QBLOCK);
+            for (int n = 0; n < 4; n++) sv[n] = *(const uint16_t *) (src + (n >> 1) * CHUNK_BYTES + (n & 1) * 8 * SEG);
+#pragma unroll
+            for (int n = 0; n < 4; n++) dstw[(n >> 1) * NBLK * KW + (n & 1) * 8] = sv[n];
         }
         wave_lds_sync();
+        if (more) issue_part(c + 1, nxt, std::integral_constant<int, 0>{}, std::integral_constant<int, P1>{});
 
-        // ---- S = Q K^T for 2 tiles of 16 keys ----
-        float s[2][4];
+        // ---- S = Q K^T: one 16-key tile (the MFMA rows) x RT row tiles ----
+        float s[RT][4];
+        {
+            const uint8_t * krow = ks + (wk + ln) * SEG + 16 * lg;   // A operand: key row ln, slice lg
 #pragma unroll
-        for (int kt = 0; kt < 2; kt++) {
-            const uint8_t * krow = ks + (wk + kt * 16 + ln) * SEG + 16 * lg;   // A operand: key row ln, slice lg
-            v4i cc[NBLK];
+            for (int t = 0; t < RT; t++)
 #pragma unroll
-            for (int bb = 0; bb < NBLK; bb++)
-                cc[bb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(*(const v4i *) (krow + 16 * win_piece(bb)), qw[bb],
-                                                               v4i{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; i++) s[kt][i] = 0.f;
+                for (int i = 0; i < 4; i++) s[t][i] = 0.f;
 #pragma unroll
             for (int bb = 0; bb < NBLK; bb++) {
-                const uint2 dk = *(const uint2 *) &sw[0][bb][kt * 16 + lg * 4];   // 4 keys' fp16 d_k
-                s[kt][0] = __builtin_fmaf((float) cc[bb][0], mul_f16lo(dqr[bb], dk.x), s[kt][0]);
-                s[kt][1] = __builtin_fmaf((float) cc[bb][1], mul_f16hi(dqr[bb], dk.x), s[kt][1]);
-                s[kt][2] = __builtin_fmaf((float) cc[bb][2], mul_f16lo(dqr[bb], dk.y), s[kt][2]);
-                s[kt][3] = __builtin_fmaf((float) cc[bb][3], mul_f16hi(dqr[bb], dk.y), s[kt][3]);
+                const v4i kA = *(const v4i *) (krow + 16 * win_piece(bb));
+                const uint2 dk = *(const uint2 *) &sw[0][bb][lg * 4];   // the lane's 4 keys' fp16 d_k
+#pragma unroll
+                for (int t = 0; t < RT; t++) {
+                    const v4i cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kA, qw[t][bb], v4i{0, 0, 0, 0}, 0, 0, 0);
+                    const float dq = dql[t * 16 + ln][bb];
+                    s[t][0] = __builtin_fmaf((float) cc[0], mul_f16lo(dq, dk.x), s[t][0]);
+                    s[t][1] = __builtin_fmaf((float) cc[1], mul_f16hi(dq, dk.x), s[t][1]);
+                    s[t][2] = __builtin_fmaf((float) cc[2], mul_f16lo(dq, dk.y), s[t][2]);
+                    s[t][3] = __builtin_fmaf((float) cc[3], mul_f16hi(dq, dk.y), s[t][3]);
+                }
             }
-            __builtin_amdgcn_sched_barrier(0);   // one key tile's accumulators live at a time
         }
+        if (more) issue_part(c + 1, nxt, std::integral_constant<int, P1>{}, std::integral_constant<int, P2>{});
 
         // ---- mask, online softmax (base 2; scores are already in log2 units).
         //      A masked key has x = -inf, so its p is exp2(-inf) = 0 ----
-        float p[8];
-        {
-            float x[8];
+        float p[RT][4];
+        const int kin = c * CK + wk + lg * 4;                     // first of the lane's 4 keys in the split
+        const bool tail = (c + 1) * CK > span;                     // keys past the split in this chunk
+#pragma unroll
+        for (int t = 0; t < RT; t++) {
+            uint2 mv = make_uint2(0, 0);
+            if (a.mask) mv = *(const uint2 *) (cur + 2 * CHUNK_BYTES + (mrow[t] * CK + wk + lg * 4) * 2);
+            float x[4];
             float mloc = -INFINITY;
-            const bool tail = (c + 1) * CK > span;                     // keys past the split in this chunk
 #pragma unroll
-            for (int kt = 0; kt < 2; kt++) {
-                const int kin = c * CK + wk + kt * 16 + lg * 4;          // first of the lane's 4 keys in the split
-                uint2 mv = make_uint2(0, 0);
-                if (a.mask) mv = *(const uint2 *) (msk + mrow * mstride + kin);
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const uint32_t mh = i < 2 ? mv.x : mv.y;
-                    float xi = (i & 1) ? fma_f16hi(mh, LOG2E, s[kt][i]) : fma_f16lo(mh, LOG2E, s[kt][i]);
-                    if (tail && kin + i >= span) xi = -INFINITY;
-                    x[kt * 4 + i] = xi;
-                    mloc = xmax(mloc, xi);
-                }
+            for (int i = 0; i < 4; i++) {
+                const uint32_t mh = i < 2 ? mv.x : mv.y;
+                float xi = (i & 1) ? fma_f16hi(mh, LOG2E, s[t][i]) : fma_f16lo(mh, LOG2E, s[t][i]);
+                if (tail && kin + i >= span) xi = -INFINITY;
+                x[i] = xi;
+                mloc = xmax(mloc, xi);
             }
-            mloc = xmax(mloc, __shfl_xor(mloc, 16));
-            mloc = xmax(mloc, __shfl_xor(mloc, 32));
-            const float m_new = xmax(m_run, mloc);
+            mloc = xmax_lanes16_32(mloc);
+            const float m_new = xmax(m_run[t], mloc);
             const float m_use = (m_new == -INFINITY) ? 0.f : m_new;   // all keys masked so far
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+            const float alpha = __builtin_amdgcn_exp2f(m_run[t] - m_use);
             float lsum = 0.f;
 #pragma unroll
-            for (int jj = 0; jj < 8; jj++) {
-                p[jj] = __builtin_amdgcn_exp2f(x[jj] - m_use);
-                lsum += p[jj];
+            for (int i = 0; i < 4; i++) {
+                p[t][i] = __builtin_amdgcn_exp2f(x[i] - m_use);
+                lsum += p[t][i];
             }
-            l_run = l_run * alpha + lsum;
-            m_run = m_new;
+            l_run[t] = l_run[t] * alpha + lsum;
+            m_run[t] = m_new;
             if (__any(alpha != 1.f)) {
 #pragma unroll
-                for (int bb = 0; bb < NBLK; bb++) { O[bb][0] *= alpha; O[bb][1] *= alpha; }
+                for (int bb = 0; bb < NBLK; bb++) { O[t][bb][0] *= alpha; O[t][bb][1] *= alpha; }
             }
         }
+        if (more) issue_part(c + 1, nxt, std::integral_constant<int, P2>{}, std::integral_constant<int, DPW>{});
+
         // ---- O += V^T P per V block. Tile e of block bb holds dims 32bb + 2m + e
         //      (m = MFMA row); the A operand of lane (m, g) is dims 2m, 2m+1 of the
-        //      lane's 8 keys, one naturally aligned 2-byte LDS read per key ----
+        //      lane's 4 keys (4g..4g+3 of the wave's 16), one naturally aligned
+        //      2-byte LDS read per key, shared by every row tile ----
         const uint8_t * vrow = vs + (wk + lg * 4) * SEG + 2 + 2 * ln;
 #pragma unroll
         for (int bb = 0; bb < NBLK; bb++) {
-            uint32_t w[8];
+            // keys 2q and 2q+1 share a register: dims 2m, 2m+1 of key 2q in bytes 0-1,
+            // of key 2q+1 in bytes 2-3
+            uint32_t w[2];
 #pragma unroll
-            for (int jj = 0; jj < 8; jj++)
-                w[jj] = *(const uint16_t *) (vrow + ((jj >> 2) * 16 + (jj & 3)) * SEG + bb * QBLOCK);
-            const uint2 dv0 = *(const uint2 *) &sw[1][bb][lg * 4];
-            const uint2 dv1 = *(const uint2 *) &sw[1][bb][16 + lg * 4];
-            const uint32_t dv[4] = {dv0.x, dv0.y, dv1.x, dv1.y};
-            uint32_t bh[4], bl[4];
-#pragma unroll
-            for (int q2 = 0; q2 < 4; q2++) {
-                const uint2 hl = split_f16x2(mul_f16lo(p[2 * q2], dv[q2]), mul_f16hi(p[2 * q2 + 1], dv[q2]));
-                bh[q2] = hl.x;
-                bl[q2] = hl.y;
+            for (int q2 = 0; q2 < 2; q2++) {
+                const uint8_t * r0p = vrow + (2 * q2) * SEG + bb * QBLOCK;
+                us2 tv;
+                tv.x = *(const uint16_t *) r0p;
+                tv.y = *(const uint16_t *) (r0p + SEG);
+                w[q2] = __builtin_bit_cast(uint32_t, tv);
             }
-            uint32_t a0[4], a1[4];
+            const uint2 dv2 = *(const uint2 *) &sw[1][bb][lg * 4];
+            const uint32_t dv[2] = {dv2.x, dv2.y};
+            uint32_t a0[2], a1[2];
+            cvt_v_block(w, a0, a1);
+            const v4h A0 = __builtin_bit_cast(v4h, make_uint2(a0[0], a0[1]));
+            const v4h A1 = __builtin_bit_cast(v4h, make_uint2(a1[0], a1[1]));
 #pragma unroll
-            for (int q2 = 0; q2 < 4; q2++) {
-                a0[q2] = cvt_i8x2_f16_b0(w[2 * q2], w[2 * q2 + 1]);
-                a1[q2] = cvt_i8x2_f16_b1(w[2 * q2], w[2 * q2 + 1]);
+            for (int t = 0; t < RT; t++) {
+                uint32_t bh[2], bl[2];
+                pdv_hilo(p[t], dv, bh, bl);
+                const v4h Bh = __builtin_bit_cast(v4h, make_uint2(bh[0], bh[1]));
+                const v4h Bl = __builtin_bit_cast(v4h, make_uint2(bl[0], bl[1]));
+                O[t][bb][0] = __builtin_amdgcn_mfma_f32_16x16x16f16(A0, Bh, O[t][bb][0], 0, 0, 0);
+                O[t][bb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A1, Bh, O[t][bb][1], 0, 0, 0);
+                O[t][bb][0] = __builtin_amdgcn_mfma_f32_16x16x16f16(A0, Bl, O[t][bb][0], 0, 0, 0);
+                O[t][bb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A1, Bl, O[t][bb][1], 0, 0, 0);
             }
-            const v8h A0 = __builtin_bit_cast(v8h, uint4{a0[0], a0[1], a0[2], a0[3]});
-            const v8h A1 = __builtin_bit_cast(v8h, uint4{a1[0], a1[1], a1[2], a1[3]});
-            const v8h Bh = __builtin_bit_cast(v8h, uint4{bh[0], bh[1], bh[2], bh[3]});
-            const v8h Bl = __builtin_bit_cast(v8h, uint4{bl[0], bl[1], bl[2], bl[3]});
-            O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, Bh, O[bb][0], 0, 0, 0);
-            O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, Bh, O[bb][1], 0, 0, 0);
-            O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, Bl, O[bb][0], 0, 0, 0);
-            O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, Bl, O[bb][1], 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);   // bound the V reads hoisted ahead
         }
-        __syncthreads();   // chunk c consumed: its buffer may be overwritten
-        if (c + 2 < n_chunks) issue_chunk(c + 2, cur);
     };
     for (int c = 0; c < n_chunks; c += 2) {
-        chunk_step(c, ring[0]);
-        if (c + 1 < n_chunks) chunk_step(c + 1, ring[1]);
+        chunk_step(c, ring[0], ring[1]);
+        if (c + 1 < n_chunks) chunk_step(c + 1, ring[1], ring[0]);
     }
+    __syncthreads();   // every wave is done with the last chunk: stage 0 becomes the merge buffer
 
-    // ---- merge the two key groups in LDS: group 1 adds its weighted O to the
-    //      buffer, group 0 adds its own and writes the block's result ----
+    // ---- merge the 4 key groups in LDS: each wave publishes (max, sum) per row,
+    //      then adds its weighted O into the buffer in turn; wave 0 adds last and
+    //      writes the block's result ----
     float * ob = (float *) ring[0];                                // [ROWS][256] f32, natural dim order
-    float2 * ml = (float2 *) (ring[0] + ROWS * D * 4);             // [WAVES][16]
-    {
-        float l = l_run;
-        l += __shfl_xor(l, 16);
-        l += __shfl_xor(l, 32);
-        l_run = l;
-        if (lg == 0) ml[wave * 16 + ln] = make_float2(m_run, l);
-    }
-    __syncthreads();
-    float M, L, fw;
-    {
-        const float2 e0 = ml[tile * 16 + ln], e1 = ml[(RT + tile) * 16 + ln];
-        M = xmax(e0.x, e1.x);
-        L = (e0.x == -INFINITY ? 0.f : e0.y * exp2f(e0.x - M)) + (e1.x == -INFINITY ? 0.f : e1.y * exp2f(e1.x - M));
-        fw = (m_run == -INFINITY) ? 0.f : exp2f(m_run - M);
-    }
-    // lane (ln, lg) holds, for block bb, dims 32bb + 8lg + 2i + e in O[bb][e][i]
-    float * orow = ob + rl_lane * D + 8 * lg;
-    if (kgrp == 1) {
+    float2 * ml = (float2 *) (ring[0] + ROWS * D * 4);             // [WAVES][ROWS]
 #pragma unroll
-        for (int bb = 0; bb < NBLK; bb++) {
-            const v4f o0 = O[bb][0] * fw, o1 = O[bb][1] * fw;
-            *(float4 *) (orow + 32 * bb)     = make_float4(o0[0], o1[0], o0[1], o1[1]);
-            *(float4 *) (orow + 32 * bb + 4) = make_float4(o0[2], o1[2], o0[3], o1[3]);
-        }
+    for (int t = 0; t < RT; t++) {
+        const float l = sum_lanes16_32(l_run[t]);
+        if (lg == 0) ml[wave * ROWS + t * 16 + ln] = make_float2(m_run[t], l);
     }
     __syncthreads();
-    if (kgrp != 0 || rl_lane >= RW) return;
-    const int r = r0 + rl_lane;
-    const int t = r / a.gqa, h = kvh * a.gqa + (r - t * a.gqa);
-    const size_t bh = (size_t) b * a.nh_kv + kvh;
-    float * out;
-    float oscale;
-    if (a.ns == 1) {
-        out = a.dst + (((size_t) b * a.T + t) * a.nh + h) * D + 8 * lg;
-        oscale = L > 0.f ? 1.f / L : 0.f;
-    } else {
-        out = a.part_o + ((bh * a.ns + split) * a.R + r) * D + 8 * lg;
-        oscale = 1.f;
-        if (lg == 0) a.part_ml[(bh * a.ns + split) * a.R + r] = make_float2(M, L);
+    float M[RT], L[RT], fw[RT];
+#pragma unroll
+    for (int t = 0; t < RT; t++) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int w2 = 0; w2 < WAVES; w2++) mx = xmax(mx, ml[w2 * ROWS + t * 16 + ln].x);
+        float ls = 0.f;
+#pragma unroll
+        for (int w2 = 0; w2 < WAVES; w2++) {
+            const float2 e = ml[w2 * ROWS + t * 16 + ln];
+            ls += e.x == -INFINITY ? 0.f : e.y * exp2f(e.x - mx);
+        }
+        M[t] = mx;
+        L[t] = ls;
+        fw[t] = (m_run[t] == -INFINITY) ? 0.f : exp2f(m_run[t] - mx);
     }
+    // Lane (ln, lg) holds, for row tile t and block bb, dims 32bb + 8lg + 2i + e
+    // of row 16t + ln in O[t][bb][e][i]. Lane indices are re-derived here (an
+    // opaque copy of the thread id), so no output address stays live through
+    // the key loop.
+    int tid_e = (int) threadIdx.x;
+    asm volatile("" : "+v"(tid_e));
+    const int ln_e = tid_e & 15, lg_e = (tid_e >> 4) & 3;
+    for (int w2 = WAVES - 1; w2 >= 1; w2--) {
+        if (wave == w2) {
+#pragma unroll
+            for (int t = 0; t < RT; t++) {
+                float * orow = ob + (t * 16 + ln_e) * D + 8 * lg_e;
+#pragma unroll
+                for (int bb = 0; bb < NBLK; bb++) {
+                    const v4f o0 = O[t][bb][0] * fw[t], o1 = O[t][bb][1] * fw[t];
+                    float4 * d0 = (float4 *) (orow + 32 * bb);
+                    float4 * d1 = (float4 *) (orow + 32 * bb + 4);
+                    if (w2 == WAVES - 1) {
+                        *d0 = make_float4(o0[0], o1[0], o0[1], o1[1]);
+                        *d1 = make_float4(o0[2], o1[2], o0[3], o1[3]);
+                    } else {
+                        float4 x0 = *d0, x1 = *d1;
+                        x0.x += o0[0]; x0.y += o1[0]; x0.z += o0[1]; x0.w += o1[1];
+                        x1.x += o0[2]; x1.y += o1[2]; x1.z += o0[3]; x1.w += o1[3];
+                        *d0 = x0;
+                        *d1 = x1;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    if (wave != 0) return;
+    const size_t bh = (size_t) b * a.nh_kv + kvh;
     const bool vec = a.ns > 1 || a.dst_vec;
 #pragma unroll
-    for (int bb = 0; bb < NBLK; bb++) {
-        const float4 p0 = *(const float4 *) (orow + 32 * bb), p1 = *(const float4 *) (orow + 32 * bb + 4);
-        const v4f o0 = O[bb][0] * fw, o1 = O[bb][1] * fw;
-        const float4 w0 = make_float4((o0[0] + p0.x) * oscale, (o1[0] + p0.y) * oscale, (o0[1] + p0.z) * oscale, (o1[1] + p0.w) * oscale);
-        const float4 w1 = make_float4((o0[2] + p1.x) * oscale, (o1[2] + p1.y) * oscale, (o0[3] + p1.z) * oscale, (o1[3] + p1.w) * oscale);
-        if (vec) {
-            *(float4 *) (out + 32 * bb) = w0;
-            *(float4 *) (out + 32 * bb + 4) = w1;
+    for (int t = 0; t < RT; t++) {
+        const int rl = t * 16 + ln_e;
+        if (rl >= RW) continue;
+        const int r = r0 + rl;
+        const int tq = r / a.gqa, h = kvh * a.gqa + (r - tq * a.gqa);
+        float * out;
+        float oscale;
+        if (a.ns == 1) {
+            out = a.dst + (((size_t) b * a.T + tq) * a.nh + h) * D + 8 * lg_e;
+            oscale = L[t] > 0.f ? 1.f / L[t] : 0.f;
         } else {
-            float * o = out + 32 * bb;
-            o[0] = w0.x; o[1] = w0.y; o[2] = w0.z; o[3] = w0.w;
-            o[4] = w1.x; o[5] = w1.y; o[6] = w1.z; o[7] = w1.w;
+            out = a.part_o + ((bh * a.ns + split) * a.R + r) * D + 8 * lg_e;
+            oscale = 1.f;
+            if (lg_e == 0) a.part_ml[(bh * a.ns + split) * a.R + r] = make_float2(M[t], L[t]);
+        }
+        const float * orow = ob + rl * D + 8 * lg_e;
+#pragma unroll
+        for (int bb = 0; bb < NBLK; bb++) {
+            const float4 p0 = *(const float4 *) (orow + 32 * bb), p1 = *(const float4 *) (orow + 32 * bb + 4);
+            const v4f o0 = O[t][bb][0] * fw[t], o1 = O[t][bb][1] * fw[t];
+            const float4 w0 = make_float4((o0[0] + p0.x) * oscale, (o1[0] + p0.y) * oscale, (o0[1] + p0.z) * oscale, (o1[1] + p0.w) * oscale);
+            const float4 w1 = make_float4((o0[2] + p1.x) * oscale, (o1[2] + p1.y) * oscale, (o0[3] + p1.z) * oscale, (o1[3] + p1.w) * oscale);
+            if (vec) {
+                *(float4 *) (out + 32 * bb) = w0;
+                *(float4 *) (out + 32 * bb + 4) = w1;
+            } else {
+                float * o = out + 32 * bb;
+                o[0] = w0.x; o[1] = w0.y; o[2] = w0.z; o[3] = w0.w;
+                o[4] = w1.x; o[5] = w1.y; o[6] = w1.z; o[7] = w1.w;
+            }
         }
     }
 }
@@ -627,6 +766,8 @@ __global__ __launch_bounds__(256) void k_fattn_merge(fa_args a) {
 
 struct fa_plan {
     int32_t R, RT, gqa, rw, n_rg, ns, split_len;
+    int64_t n_kv_pad;
+    size_t  off_ml, off_qimg, off_dq, off_mimg;   // workspace sections (bytes)
     size_t  ws_bytes;
 };
 
@@ -635,9 +776,12 @@ int env_int(const char * name, int dflt) {
     return s && *s ? std::atoi(s) : dflt;
 }
 
+size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
 // The key loop hand-counts its outstanding vector-memory operations (the LDS
-// DMAs are inline asm the compiler does not see), so a build of the attention
-// kernel that spills to scratch would break that count: refuse to run one.
+// DMAs and the query-operand loads are inline asm the compiler does not see),
+// so a build of the attention kernel that spills to scratch would break that
+// count: refuse to run one.
 int check_no_scratch() {
     static const int rc = [] {
         for (const void * f : {(const void *) k_fattn_q8_0<1>, (const void *) k_fattn_q8_0<2>}) {
@@ -679,7 +823,10 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
         return set_error(QWFN_EALIGN, "flash_attn_ext: k/v data and strides must be 16-byte aligned");
     if (!is_aligned(q->data, 16) || q->nb[1] % 16 || q->nb[2] % 16 || q->nb[3] % 16)
         return set_error(QWFN_EALIGN, "flash_attn_ext: q data and strides must be 16-byte aligned");
+    if (k->nb[1] >= (size_t(1) << 24) || v->nb[1] >= (size_t(1) << 24))
+        return set_error(QWFN_ENOTSUP, "flash_attn_ext: k/v row strides must be below 16 MiB");
     bool per_head_mask = false;
+    int64_t m_slices = 0;
     if (mask) {
         if (!mask->data) return set_error(QWFN_EINVAL, "flash_attn_ext: mask has no data");
         if (mask->type != QWFN_TYPE_F16) return set_error(QWFN_EINVAL, "flash_attn_ext: mask must be f16");
@@ -690,11 +837,14 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
             return set_error(QWFN_EINVAL, "flash_attn_ext: mask must broadcast over heads and batch");
         if (!is_aligned(mask->data, 2)) return set_error(QWFN_EALIGN, "flash_attn_ext: mask must be 2-byte aligned");
         per_head_mask = mask->ne[2] != 1;
+        m_slices = mask->ne[2] * mask->ne[3];
     }
-    // Query rows per block: one or two 16-row tiles. A per-head mask stages one
-    // mask row per query row, so it keeps blocks at 16 rows.
-    int rw = (R > 16 && !per_head_mask) ? 32 : 16;
-    if (const int force = env_int("QWFN_FA_ROWS", 0)) rw = (force >= 32 && !per_head_mask) ? 32 : 16;
+    // Query rows per block: one or two 16-row tiles. A block streams at most
+    // MASK_ROWS mask rows per chunk: one per query row for a per-head mask, one
+    // per query position for a shared one.
+    int rw = R > 16 ? 32 : 16;
+    if (const int force = env_int("QWFN_FA_ROWS", 0)) rw = force >= 32 ? 32 : 16;
+    if (mask && rw == 32 && (per_head_mask || (32 + gqa - 1) / gqa + 1 > MASK_ROWS)) rw = 16;
     pl->R = (int32_t) R;
     pl->rw = rw;
     pl->RT = rw / 16;
@@ -702,6 +852,7 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
     pl->gqa = (int32_t) gqa;
     const int64_t n_kv = k->ne[1];
     const int64_t B = q->ne[3];
+    pl->n_kv_pad = (n_kv + CK - 1) / CK * CK;
     // Splits: about one block per CU (256), each at least one chunk.
     const int64_t target_blocks = env_int("QWFN_FA_BLOCKS", 256);
     int64_t ns = std::max<int64_t>(1, target_blocks / std::max<int64_t>(1, nh_kv * B * pl->n_rg));
@@ -709,23 +860,25 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
     if (const int force = env_int("QWFN_FA_SPLITS", 0)) ns = force;
     int64_t split_len = (n_kv + ns - 1) / ns;
     split_len = std::max<int64_t>(CK, (split_len + CK - 1) / CK * CK);
-    if (mask) {
-        // a block stages its split's mask rows in LDS: rows x split_len <= MASK_LDS
-        const int64_t mrows = per_head_mask ? rw : std::min<int64_t>(T, (rw + gqa - 1) / gqa + 1);
-        if (mrows * CK > MASK_LDS) return set_error(QWFN_ENOTSUP, "flash_attn_ext: too many mask rows per block");
-        const int64_t cap = std::max<int64_t>(CK, MASK_LDS / mrows / CK * CK);
-        split_len = std::min(split_len, cap);
-    }
     ns = std::max<int64_t>(1, (n_kv + split_len - 1) / split_len);
-    if (ns > MAX_SPLITS) {
-        // long caches with a mask: widen the splits (the mask cap above) no further
-        // than MAX_SPLITS allows; such a call is refused rather than truncated
-        return set_error(QWFN_ENOTSUP, "flash_attn_ext: " + std::to_string(ns) + " key splits needed, at most " +
+    if (ns > MAX_SPLITS)
+        return set_error(QWFN_ENOTSUP, "flash_attn_ext: " + std::to_string(ns) + " key splits requested, at most " +
                                            std::to_string(MAX_SPLITS) + " supported");
-    }
     pl->ns = (int32_t) ns;
     pl->split_len = (int32_t) split_len;
-    pl->ws_bytes = ns > 1 ? (size_t) (B * nh_kv * ns * R) * (D * sizeof(float) + sizeof(float2)) + 256 : 0;
+    // workspace: split partials (when ns > 1), the query image, the mask image
+    const int64_t n_bkr = B * nh_kv * pl->n_rg;
+    const size_t n_part = ns > 1 ? (size_t) (B * nh_kv * ns * R) : 0;
+    size_t off = align256(n_part * D * sizeof(float));
+    pl->off_ml = off;
+    off = align256(off + n_part * sizeof(float2));
+    pl->off_qimg = off;
+    off = align256(off + (size_t) n_bkr * pl->RT * 64 * NBLK * 16);
+    pl->off_dq = off;
+    off = align256(off + (size_t) n_bkr * QROWS_IMG * NBLK * sizeof(float));
+    pl->off_mimg = off;
+    off = align256(off + (size_t) m_slices * T * pl->n_kv_pad * 2);
+    pl->ws_bytes = off;
     return QWFN_OK;
 }
 
@@ -734,9 +887,10 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
 
 using namespace qwfn;
 
-extern "C" size_t qwfn_fattn_workspace_size(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v) {
+extern "C" size_t qwfn_fattn_workspace_size(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
+                                            const qwfn_tensor * mask) {
     fa_plan pl{};
-    if (plan_fattn(q, k, v, nullptr, &pl)) return 0;
+    if (plan_fattn(q, k, v, mask, &pl)) return 0;
     return pl.ws_bytes;
 }
 
@@ -757,14 +911,6 @@ extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor
         dst->nb[3] != dst->nb[2] * (size_t) dst->ne[2])
         return set_error(QWFN_EINVAL, "flash_attn_ext: dst must be contiguous");
     if (!is_aligned(dst->data, 4)) return set_error(QWFN_EALIGN, "flash_attn_ext: dst must be 4-byte aligned");
-    if (pl.ns > 1) {
-        if (ws) {
-            if (ws_bytes < pl.ws_bytes) return set_error(QWFN_ENOMEM, "flash_attn_ext: workspace too small");
-            if (!is_aligned(ws, 256)) return set_error(QWFN_EALIGN, "flash_attn_ext: workspace must be 256-byte aligned");
-        } else if (int rc = library_workspace(pl.ws_bytes, &ws)) {
-            return rc;
-        }
-    }
     const int64_t n_kv = k->ne[1];
     if (n_kv == 0) {
         // no keys: ggml-cpu divides 0 by S = 0 only for rows it visits; the
@@ -775,23 +921,33 @@ extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor
                            dim3(256), 0, as_stream(stream), (float *) dst->data, n);
         return hip_check(hipGetLastError(), "flash_attn zero fill");
     }
+    if (ws) {
+        if (ws_bytes < pl.ws_bytes) return set_error(QWFN_ENOMEM, "flash_attn_ext: workspace too small");
+        if (!is_aligned(ws, 256)) return set_error(QWFN_EALIGN, "flash_attn_ext: workspace must be 256-byte aligned");
+    } else if (int rc = library_workspace(pl.ws_bytes, &ws)) {
+        return rc;
+    }
     if (int rc = check_no_scratch()) return rc;
 
     fa_args a{};
     a.q = (const char *) q->data; a.q_nb1 = q->nb[1]; a.q_nb2 = q->nb[2]; a.q_nb3 = q->nb[3];
     a.k = (const char *) k->data; a.k_nb1 = k->nb[1]; a.k_nb2 = k->nb[2]; a.k_nb3 = k->nb[3];
     a.v = (const char *) v->data; a.v_nb1 = v->nb[1]; a.v_nb2 = v->nb[2]; a.v_nb3 = v->nb[3];
+    char * w = (char *) ws;
     if (mask) {
         a.mask = (const char *) mask->data; a.m_nb1 = mask->nb[1]; a.m_nb2 = mask->nb[2]; a.m_nb3 = mask->nb[3];
         a.m_ne2 = (int32_t) mask->ne[2]; a.m_ne3 = (int32_t) mask->ne[3];
+        a.mimg = (uint16_t *) (w + pl.off_mimg);
     } else {
-        a.mask = nullptr; a.m_ne2 = 1; a.m_ne3 = 1;
+        a.mask = nullptr; a.m_ne2 = 1; a.m_ne3 = 1; a.mimg = nullptr;
     }
     a.dst = (float *) dst->data;
-    const size_t n_part = (size_t) q->ne[3] * k->ne[2] * pl.ns * pl.R;
-    a.part_o = (float *) ws;
-    a.part_ml = ws ? (float2 *) ((char *) ws + n_part * D * sizeof(float)) : nullptr;
+    a.part_o = (float *) w;
+    a.part_ml = (float2 *) (w + pl.off_ml);
+    a.qimg = (uint4 *) (w + pl.off_qimg);
+    a.dqimg = (float *) (w + pl.off_dq);
     a.n_kv = n_kv;
+    a.n_kv_pad = pl.n_kv_pad;
     a.T = (int32_t) q->ne[1]; a.nh = (int32_t) q->ne[2]; a.nh_kv = (int32_t) k->ne[2];
     a.gqa = pl.gqa; a.R = pl.R; a.B = (int32_t) q->ne[3];
     a.kb = (int32_t) k->ne[3]; a.vb = (int32_t) v->ne[3];
@@ -803,8 +959,13 @@ extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor
     const int64_t grid = units * a.nh_kv * a.n_rg;
     if (grid > 0x7fffffff) return set_error(QWFN_EINVAL, "flash_attn_ext: grid too large");
     hipStream_t st = as_stream(stream);
-    if (pl.RT == 1) hipLaunchKernelGGL(k_fattn_q8_0<1>, dim3((unsigned) grid), dim3(1 * KG * 64), 0, st, a);
-    else            hipLaunchKernelGGL(k_fattn_q8_0<2>, dim3((unsigned) grid), dim3(2 * KG * 64), 0, st, a);
+    const int n_qblocks = a.B * a.nh_kv * a.n_rg;
+    const int n_mblocks = mask ? 64 : 0;
+    if (pl.RT == 1) hipLaunchKernelGGL(k_fattn_prep<1>, dim3(n_qblocks + n_mblocks), dim3(256), 0, st, a, n_qblocks);
+    else            hipLaunchKernelGGL(k_fattn_prep<2>, dim3(n_qblocks + n_mblocks), dim3(256), 0, st, a, n_qblocks);
+    if (int rc = hip_check(hipGetLastError(), "flash_attn prep launch")) return rc;
+    if (pl.RT == 1) hipLaunchKernelGGL(k_fattn_q8_0<1>, dim3((unsigned) grid), dim3(KG * 64), 0, st, a);
+    else            hipLaunchKernelGGL(k_fattn_q8_0<2>, dim3((unsigned) grid), dim3(KG * 64), 0, st, a);
     if (int rc = hip_check(hipGetLastError(), "flash_attn launch")) return rc;
     if (a.ns > 1) {
         const int64_t blocks = (int64_t) a.B * a.nh_kv * a.R;

@@ -71,7 +71,7 @@ def load(path: str = LIB_PATH):
     L.qwfn_cpy_f32_q8_0.argtypes = [T, T, ctypes.c_int, vp]
     L.qwfn_get_rows_i32.argtypes = [T, T, T, vp]
     L.qwfn_kv_gather_segments.argtypes = [vp, sz, i64, sz, sz, sz, i32, vp, i64, vp, sz, sz, vp]
-    L.qwfn_fattn_workspace_size.argtypes = [T, T, T]
+    L.qwfn_fattn_workspace_size.argtypes = [T, T, T, T]
     L.qwfn_fattn_workspace_size.restype = sz
     L.qwfn_flash_attn_ext_q8_0.argtypes = [T, T, T, T, ctypes.c_float, ctypes.c_float, ctypes.c_float, T,
                                            ctypes.c_int, vp, sz, vp]
@@ -215,8 +215,9 @@ def flash_attn_ext(qv: Tensor, kv: Tensor, vv: Tensor, mv: Tensor | None, scale:
                                             ctypes.byref(ov), variant, ws_ptr, ws_bytes, _stream(stream)))
 
 
-def fattn_workspace_size(qv: Tensor, kv: Tensor, vv: Tensor) -> int:
-    return int(load().qwfn_fattn_workspace_size(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv)))
+def fattn_workspace_size(qv: Tensor, kv: Tensor, vv: Tensor, mv: Tensor | None = None) -> int:
+    return int(load().qwfn_fattn_workspace_size(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv),
+                                                ctypes.byref(mv) if mv is not None else None))
 
 
 def state_restore(srcs, nbytes, dsts, n_slots: int, src_kind: int = SRC_DEVICE, stream=None):

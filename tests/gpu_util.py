@@ -48,7 +48,7 @@ def gpu_attn(K, q: np.ndarray, kc: np.ndarray, vc: np.ndarray, n_kv: int, nh_kv:
     out = torch.full((B, T, nh, hd), float("nan"), dtype=torch.float32, device="cuda")
     wst = None
     if ws:
-        n = K.fattn_workspace_size(K.q_view(qd), kv, vv)
+        n = K.fattn_workspace_size(K.q_view(qd), kv, vv, mv)
         wst = torch.empty(max(n, 256), dtype=torch.uint8, device="cuda")
     K.flash_attn_ext(K.q_view(qd), kv, vv, mv, scale, K.out_view(out), variant, ws=wst)
     o = host(out)

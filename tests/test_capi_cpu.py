@@ -26,7 +26,7 @@ def test_library_exports_header_symbols():
     for s in syms:
         assert hasattr(L, s), s
     assert set(K.EXPORTS) == set(syms)
-    assert L.qwfn_abi_version() == 1
+    assert L.qwfn_abi_version() == 2
 
 
 def _err(rc, code, needle):
