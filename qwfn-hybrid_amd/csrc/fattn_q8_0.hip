@@ -11,28 +11,32 @@
 // are exact (i8 MFMA); only the float accumulation order differs. P*d_v enters
 // the f16 PV matrix cores as a hi + lo pair of f16 values (~22 bits).
 //
-// Work decomposition (flash-decoding):
+// Work decomposition (flash-decoding), one launch plus a split merge:
 //   grid   : (batch, KV head, row group, key split); the KV heads and row
 //            groups of one split sit on the same XCD and are dispatched next to
 //            each other, so the cache lines two heads share (a 272-byte head row
 //            is not line aligned) come from one L2.
-//   block  : RT 16-row query tiles x 2 key groups = 2*RT wavefronts. Keys are
-//            streamed in 64-key chunks of raw 272-byte head rows with gfx950's
-//            LDS DMA (global_load_lds_dwordx4) into a two-stage ring: chunk c+1
-//            is in flight while chunk c is computed. Wave (tile t, group g) owns
-//            query rows 16t..16t+15 and keys 32g..32g+31 of every chunk.
+//   block  : 8 wavefronts (two per SIMD), RT 16-row query tiles x 8/RT key
+//            groups of 16 keys. Keys are streamed in chunks of 16*8/RT raw
+//            272-byte head rows with gfx950's LDS DMA (global_load_lds_dwordx4,
+//            SGPR base + per-lane offset) into a two-stage ring: chunk c+1 is in
+//            flight while chunk c is computed. The block requantises its own
+//            query rows into LDS while chunk 0 loads.
 //   QK^T   : v_mfma_i32_16x16x64_i8 per q8_0 block. The A operand is four
 //            16-byte aligned pieces of the raw K row that cover the block's 32
 //            quants (a 64-byte window); the B operand is the requantised query
 //            laid out on the same window, zero outside the block, so the integer
 //            sum is exactly the block's dot product and no LDS read is ever
 //            misaligned. The int32 tile is scaled by d_q*d_k.
-//   softmax: online, base 2, per query row; row max across the 4 lane groups.
-//   PV     : v_mfma_f32_16x16x32_f16, A = V^T (int8 -> f16 exact, SDWA byte
+//   softmax: online, base 2, per query row; row max across the 4 lane groups
+//            with cross-row lane swaps. The running max may lag the true max by
+//            up to 2^8 (p <= 256), so the accumulators are rescaled only when
+//            the max jumps by more than that.
+//   PV     : v_mfma_f32_16x16x16_f16, A = V^T (int8 -> f16 exact, SDWA byte
 //            select from naturally aligned 2-byte LDS reads), B = P*d_v of one V
 //            block as f16 hi + lo.
-//   merge  : the two key groups merge in LDS; key splits merge in a second
-//            kernel (log-sum-exp weights).
+//   merge  : the key groups of a block merge in LDS; key splits merge in a
+//            second kernel (log-sum-exp weights), one block per quarter row.
 #include "q8_device.h"
 #include "qwfn_common.h"
 
@@ -46,28 +50,36 @@ namespace {
 
 typedef int      v4i __attribute__((ext_vector_type(4)));
 typedef float    v4f __attribute__((ext_vector_type(4)));
-typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
-typedef _Float16 h2  __attribute__((ext_vector_type(2)));
 typedef uint16_t us2 __attribute__((ext_vector_type(2)));
 
 constexpr int D      = 256;            // head size (values per head row)
 constexpr int NBLK   = D / QK;         // 8 q8_0 blocks per head row
 constexpr int SEG    = NBLK * QBLOCK;  // 272 bytes per head row
 constexpr int KW     = 16;             // keys per wave per chunk (one QK tile, one PV MFMA depth)
-constexpr int KG     = 4;              // key groups = waves of a block
-constexpr int CK     = KG * KW;        // keys per chunk
-constexpr int CHUNK_BYTES = CK * SEG;  // one tensor's rows of a chunk (17408)
-constexpr int DMA_PER_TENSOR = CHUNK_BYTES / 1024;   // wave-wide 16-byte LDS-DMA loads per tensor (17)
-constexpr int MASK_ROWS = 16;          // mask rows a block streams with each chunk
-constexpr int MASK_BYTES = MASK_ROWS * CK * 2;       // a chunk's mask slice in LDS (2048)
-constexpr int STAGE_BYTES = 2 * CHUNK_BYTES + MASK_BYTES;   // one ring stage: K rows, V rows, mask slice
-constexpr int DMA_SLOTS = 2 * DMA_PER_TENSOR + MASK_BYTES / 1024;   // wave-wide DMAs per chunk (36)
-constexpr int QROWS_IMG = 32;          // d_q rows per row group in the query image (one 1 KB DMA)
+constexpr int WAVES  = 8;              // wavefronts per block (two per SIMD)
 constexpr int QWIN   = 64;             // bytes of one block's query window
 constexpr int MAX_SPLITS = 1024;       // key splits per (batch, KV head, row group)
 constexpr float LOG2E = 1.4426950408889634f;
-static_assert(CHUNK_BYTES % 1024 == 0, "a chunk is whole wave-wide DMA instructions");
+constexpr float RESCALE_SLACK = 8.f;   // log2 units the running max may lag the true max
+constexpr int MASK_LDS = 8192;         // LDS bytes for a block's mask rows over its whole split
+enum { MASK_NONE = 0, MASK_SPLIT = 1, MASK_CHUNK = 2 };
+
+// Chunk geometry for RT query tiles per block.
+template <int RT>
+struct fa_cfg {
+    static constexpr int ROWS  = 16 * RT;                   // query rows per block
+    static constexpr int KG    = WAVES / RT;                // key groups
+    static constexpr int CK    = KG * KW;                   // keys per chunk (64 or 128)
+    static constexpr int CHUNK = CK * SEG;                  // one tensor's rows of a chunk
+    static constexpr int DMA_T = CHUNK / 1024;              // wave-wide 16-byte DMAs per tensor
+    static constexpr int STAGE = 2 * CHUNK;                 // one ring stage: K rows, V rows
+    static constexpr int SLOTS = 2 * DMA_T;                 // DMAs per chunk
+    static constexpr int SPW   = (SLOTS + WAVES - 1) / WAVES;   // DMA slots per wave
+    static constexpr int NS    = RT == 2 ? 3 : 2;           // ring stages (chunks in flight + 1)
+    static_assert(CHUNK % 1024 == 0, "a chunk is whole wave-wide DMAs");
+    static_assert(SPW * WAVES - SLOTS < WAVES, "only a wave's last slot can be absent");
+};
 
 // First 16-byte piece of the 64-byte window of block b inside a 272-byte head
 // row. Block b's quants occupy bytes [34b+2, 34b+34); the window
@@ -81,20 +93,18 @@ struct fa_args {
     const char * q;  size_t q_nb1, q_nb2, q_nb3;
     const char * k;  size_t k_nb1, k_nb2, k_nb3;
     const char * v;  size_t v_nb1, v_nb2, v_nb3;
-    const char * mask; size_t m_nb1, m_nb2, m_nb3;
+    const char * mask; size_t m_nb1, m_nb2, m_nb3;   // F16 [n_kv, T, m_ne2, m_ne3] or null
     int32_t m_ne2, m_ne3;
+    uint32_t m_slice;      // bytes of one batch slice of the mask (last row's end)
+    int32_t  mask_mode;    // MASK_NONE, MASK_SPLIT (whole split in LDS) or MASK_CHUNK (per chunk)
     float *  dst;          // [D, nh, T, B]
     float *  part_o;       // [B][nh_kv][ns][R][D]
     float2 * part_ml;      // [B][nh_kv][ns][R]: (running max in log2 units, sum)
-    uint4 *  qimg;         // [B][nh_kv][n_rg][RT][64 lanes][NBLK]: lane's 16-byte query window slices
-    float *  dqimg;        // [B][nh_kv][n_rg][32 rows][NBLK]: d_q * scale * log2(e)
-    uint16_t * mimg;       // [m_ne3][m_ne2][T][n_kv_pad] F16 mask copy, -inf past n_kv (or null)
     int64_t  n_kv;
-    int64_t  n_kv_pad;     // n_kv rounded up to a chunk
     int32_t  T, nh, nh_kv, gqa, R, B;
     int32_t  kb, vb;       // K/V batch extents (ne[3]); batch b reads b % kb
     int32_t  ns;           // key splits
-    int32_t  split_len;    // keys per split, multiple of CK
+    int32_t  split_len;    // keys per split, multiple of the chunk
     int32_t  rw;           // query rows per block (16 * RT)
     int32_t  n_rg;         // row groups per KV head
     float    scale;
@@ -196,17 +206,40 @@ __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
+// The same for a wave-uniform runtime count (the counts a wave can leave in
+// flight; anything else waits for everything).
+__device__ __forceinline__ void wait_vmcnt_n(int n) {
+    switch (n) {
+        case 4: wait_vmcnt<4>(); break;
+        case 5: wait_vmcnt<5>(); break;
+        case 8: wait_vmcnt<8>(); break;
+        case 9: wait_vmcnt<9>(); break;
+        default: wait_vmcnt<0>(); break;
+    }
+}
 
-// One wave-wide LDS-DMA load: each lane copies 16 bytes from gptr to
-// LDS[lds_base + 16 * lane]; lds_base is wave-uniform. Issued as inline asm:
-// the compiler neither reorders memory operations across it nor tracks it, and
-// the kernel waits for it explicitly (vmcnt) before the barrier that publishes
-// the data. No other vector-memory load is in flight while DMAs are, so the
-// explicit counts are exact.
-__device__ __forceinline__ void dma16(const void * gptr, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %1\n\t"
-                 "global_load_lds_dwordx4 %0, off"
-                 :: "v"(gptr), "s"(lds_base) : "memory");
+// Buffer resource of `bytes` bytes at base (raw, 32-bit data format). Loads
+// at offsets past `bytes` return zeros instead of touching memory.
+__device__ __forceinline__ v4i make_rsrc(const void * base, uint32_t bytes) {
+    const uint64_t p = (uint64_t) (uintptr_t) base;
+    v4i r;
+    r[0] = (int) (uint32_t) p;
+    r[1] = (int) ((uint32_t) (p >> 32) & 0xffffu);   // stride 0
+    r[2] = (int) bytes;
+    r[3] = 0x00020000;                               // DATA_FORMAT 32
+    return r;
+}
+
+// One wave-wide LDS-DMA load: lane i copies the 16 bytes at offset off of the
+// buffer to LDS[lds_base + 16 * i] (zeros past the buffer's size). Issued as
+// inline asm: the compiler neither reorders memory operations across it nor
+// tracks it, and the kernel waits for it explicitly (vmcnt) before the barrier
+// that publishes the data. No other vector-memory load is in flight while DMAs
+// are, so the explicit counts are exact.
+__device__ __forceinline__ void dma16_buf(v4i rsrc, uint32_t off, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\t"
+                 "buffer_load_dwordx4 %0, %1, 0 offen lds"
+                 :: "v"(off), "s"(rsrc), "s"(lds_base) : "memory");
 }
 
 __device__ __forceinline__ uint32_t lds_addr(const void * p) {
@@ -221,117 +254,32 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Row of the mask copy that staged row mr of a block reads: query position
-// t0 + mr for a shared mask, query row r0 + mr for a per-head mask.
-__device__ __forceinline__ int64_t mask_img_row(const fa_args & a, int mr, int t0, int r0, int kvh, int b) {
-    int t, hq;
-    if (a.m_ne2 == 1) { t = t0 + mr; hq = 0; }
-    else { const int r = r0 + mr; t = r / a.gqa; hq = (kvh * a.gqa + (r - t * a.gqa)) % a.m_ne2; }
-    return ((int64_t) (b % a.m_ne3) * a.m_ne2 + hq) * a.T + t;
-}
-
 // f[0 .. n) = 0 (dst is only 4-byte aligned, so plain f32 stores).
 __global__ void k_zero_f32(float * f, int64_t n) {
     const int64_t stride = (int64_t) gridDim.x * blockDim.x;
     for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) f[i] = 0.f;
 }
 
-// Per-call preparation shared by every key split:
-//  * blocks [0, n_qblocks): one (batch, KV head, row group) each. The query
-//    rows are requantised to q8_0 (ggml-cpu's quantiser, `x86` variant) and
-//    each q8_0 block is laid out on its 64-byte window (zero outside the
-//    block); the result is stored in the order the attention lanes load it as
-//    MFMA B operands, with d_q * scale * log2(e) beside it.
-//  * blocks past that: the F16 mask rows [0, T) of every (head, batch) slice
-//    are copied to a 16-byte aligned image padded with -inf up to n_kv_pad, so
-//    the attention kernel can stream each chunk's slice with the K/V DMA.
 template <int RT>
-__global__ __launch_bounds__(256) void k_fattn_prep(fa_args a, int n_qblocks) {
-    constexpr int ROWS = 16 * RT;
-    if ((int) blockIdx.x >= n_qblocks) {
-        if (!a.mask) return;
-        const int64_t rows = (int64_t) a.m_ne3 * a.m_ne2 * a.T;
-        const int64_t units = rows * (a.n_kv_pad / 8);            // 8 keys (16 bytes) per unit
-        const int64_t stride = (int64_t) (gridDim.x - n_qblocks) * 256;
-        for (int64_t e = (int64_t) (blockIdx.x - n_qblocks) * 256 + threadIdx.x; e < units; e += stride) {
-            const int64_t row = e / (a.n_kv_pad / 8);
-            const int64_t k0 = (e - row * (a.n_kv_pad / 8)) * 8;
-            const int t = (int) (row % a.T);
-            const int64_t hs = row / a.T;
-            const int hq = (int) (hs % a.m_ne2), bm = (int) (hs / a.m_ne2);
-            const uint16_t * src = (const uint16_t *) (a.mask + (size_t) t * a.m_nb1 + (size_t) hq * a.m_nb2 + (size_t) bm * a.m_nb3);
-            uint16_t v[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++) v[i] = k0 + i < a.n_kv ? src[k0 + i] : (uint16_t) 0xFC00;
-            uint4 w;
-            w.x = v[0] | ((uint32_t) v[1] << 16); w.y = v[2] | ((uint32_t) v[3] << 16);
-            w.z = v[4] | ((uint32_t) v[5] << 16); w.w = v[6] | ((uint32_t) v[7] << 16);
-            *(uint4 *) (a.mimg + row * a.n_kv_pad + k0) = w;
-        }
-        return;
-    }
-    __shared__ __attribute__((aligned(16))) uint8_t qwin[ROWS * NBLK * QWIN];
-    const int bkr = blockIdx.x;                    // (b * nh_kv + kvh) * n_rg + rg
-    const int rg = bkr % a.n_rg, kvh = (bkr / a.n_rg) % a.nh_kv, b = bkr / (a.n_rg * a.nh_kv);
-    const int r0 = rg * a.rw;
-    const int RW = min(a.rw, a.R - r0);
-    for (int e = threadIdx.x; e < ROWS * NBLK * QWIN / 16; e += 256) ((uint4 *) qwin)[e] = make_uint4(0, 0, 0, 0);
-    __syncthreads();
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int sub = lane & 7, blk = lane >> 3;
-    const float fs = a.scale * LOG2E;
-    for (int rl = wave; rl < ROWS; rl += 4) {
-        const int r = r0 + min(rl, RW - 1);
-        const int t = r / a.gqa, h = kvh * a.gqa + (r - t * a.gqa);
-        float4 v4 = *(const float4 *) (a.q + (size_t) t * a.q_nb1 + (size_t) h * a.q_nb2 + (size_t) b * a.q_nb3 +
-                                       (size_t) (blk * QK + sub * 4) * 4);
-        if (rl >= RW) v4 = make_float4(0.f, 0.f, 0.f, 0.f);
-        const float x[4] = {v4.x, v4.y, v4.z, v4.w};
-        uint16_t d16;
-        float dq;
-        const uint32_t w = dev::q8_quantize_lane4(x, a.x86 != 0, &d16, &dq);
-        uint16_t * wp = (uint16_t *) (qwin + (rl * NBLK + blk) * QWIN + win_off(blk) + 4 * sub);
-        wp[0] = (uint16_t) w;
-        wp[1] = (uint16_t) (w >> 16);
-        if (sub == 0) a.dqimg[((size_t) bkr * QROWS_IMG + rl) * NBLK + blk] = dq * fs;
-    }
-    __syncthreads();
-    // lane (ln, lg) of row tile `tile` reads slice lg of row 16*tile + ln's window, per block
-    for (int e = threadIdx.x; e < RT * 64 * NBLK; e += 256) {
-        const int tile = e / (64 * NBLK), ln_ = (e / NBLK) & 63, bb = e % NBLK;
-        const int row = tile * 16 + (ln_ & 15), lg_ = ln_ >> 4;
-        a.qimg[(size_t) bkr * RT * 64 * NBLK + e] = *(const uint4 *) (qwin + (row * NBLK + bb) * QWIN + 16 * lg_);
-    }
-}
-
-// 16-byte global load into registers, issued as inline asm so that its
-// completion is tracked by the kernel's own vmcnt waits (like the LDS DMAs)
-// rather than by compiler-inserted ones.
-__device__ __forceinline__ v4i gload16_asm(const void * p) {
-    v4i r;
-    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p) : "memory");
-    return r;
-}
-
-template <int RT>
-__global__ __launch_bounds__(KG * 64)
-void k_fattn_q8_0(fa_args a) {
-    constexpr int WAVES = KG;
-    constexpr int ROWS = 16 * RT;
-    constexpr int DPW = DMA_SLOTS / WAVES;         // DMAs per wave per chunk
-    static_assert(DMA_SLOTS % WAVES == 0, "every wave issues the same number of DMAs");
-    // two ring stages, each K rows [CK][272], V rows [CK][272], mask [MASK_ROWS][CK] F16
-    __shared__ __attribute__((aligned(16))) uint8_t ring[2][STAGE_BYTES];
+__global__ __launch_bounds__(WAVES * 64) void k_fattn_q8_0(fa_args a) {
+    using C = fa_cfg<RT>;
+    constexpr int ROWS = C::ROWS, KG = C::KG, CK = C::CK, CHUNK = C::CHUNK, DMA_T = C::DMA_T;
+    constexpr int SLOTS = C::SLOTS, SPW = C::SPW, NS = C::NS;
+    // NS ring stages, each K rows [CK][272] and V rows [CK][272]
+    __shared__ __attribute__((aligned(16))) uint8_t ring[NS][C::STAGE];
     // per-wave scale tables of the current chunk: [K|V][block][key of the wave] fp16
     __shared__ __attribute__((aligned(16))) uint16_t scl[WAVES][2][NBLK][KW];
-    __shared__ __attribute__((aligned(16))) float dql[QROWS_IMG][NBLK];     // d_q * scale * log2(e) per row and block
-    static_assert(ROWS * D * 4 + WAVES * ROWS * 8 <= STAGE_BYTES, "merge buffer fits in stage 0");
+    // the block's mask rows over its whole split (MASK_SPLIT mode): [row][split_len] F16
+    __shared__ __attribute__((aligned(16))) uint16_t mlds[MASK_LDS / 2];
+    static_assert(ROWS * NBLK * QWIN + ROWS * NBLK * 4 <= C::STAGE, "query image fits in the last stage");
+    static_assert(ROWS * (D + 4) * 4 + WAVES * 16 * 8 <= C::STAGE, "merge buffer fits in stage 0");
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform (SGPR)
     const int ln = lane & 15;       // MFMA row/col within a 16-tile
     const int lg = lane >> 4;       // lane group (k-slice / output row quad)
-    const int kgrp = wave;          // key group: keys 16*kgrp .. 16*kgrp+15 of every chunk
+    const int tile = wave % RT;     // query rows 16*tile .. 16*tile+15 of the block
+    const int kg = wave / RT;       // keys 16*kg .. 16*kg+15 of every chunk
 
     // ---- block -> (b, kvh, row group, split) ----
     const int id   = blockIdx.x;
@@ -351,199 +299,267 @@ void k_fattn_q8_0(fa_args a) {
     const int r0 = rg * a.rw;                          // first query row of this block
     const int RW = std::min(a.rw, a.R - r0);          // rows in this block
     const int t0 = r0 / a.gqa;
-    const int n_mrows = a.m_ne2 == 1 ? (r0 + RW - 1) / a.gqa - t0 + 1 : RW;   // <= MASK_ROWS (planned)
-    const int bkr = (b * a.nh_kv + kvh) * a.n_rg + rg;
 
     const char * kbase = a.k + (size_t) (b % a.kb) * a.k_nb3 + (size_t) kvh * a.k_nb2;
     const char * vbase = a.v + (size_t) (b % a.vb) * a.v_nb3 + (size_t) kvh * a.v_nb2;
-
-    // Issue part of chunk c into stage dstb: the chunk is DMA_SLOTS wave-wide
-    // 16-byte DMAs, DPW per wave, issued as slots [n0, n1) of the wave. Wave w
-    // issues slots w, w + WAVES, ...: slots 0-16 are K pieces, 17-33 V pieces
-    // (piece p = 64*i + lane of a tensor's chunk is byte 16*(p % 17) of key
-    // p / 17; keys past the split are loaded and masked while they exist, past
-    // n_kv they repeat the last key), 34-35 the chunk's mask slice, rows 0-7 and
-    // 8-15. Only a wave's last slot can be a mask slot; without a mask it
-    // repeats the wave's first piece.
-    static_assert((DPW - 1) * WAVES + WAVES - 1 < DMA_SLOTS && (DPW - 1) * WAVES <= 2 * DMA_PER_TENSOR,
-                  "the mask slots are the last slot of some waves");
-    auto issue_part = [&](int c, uint8_t * dstb, auto n0c, auto n1c) __attribute__((always_inline)) {
-        constexpr int n0 = decltype(n0c)::value, n1 = decltype(n1c)::value;
-        const int64_t c0 = k_lo + (int64_t) c * CK;
-        const bool clamp = c0 + CK > a.n_kv;   // the cache's last chunk: no rows past n_kv
-        const int last = (int) std::min<int64_t>(CK - 1, a.n_kv - 1 - c0);
-        int ln_o = lane;
-        asm volatile("" : "+v"(ln_o));          // recomputed per chunk: no hoisted per-piece addresses
-        const char * kc0 = kbase + (size_t) c0 * a.k_nb1;
-        const char * vc0 = vbase + (size_t) c0 * a.v_nb1;
-        auto kv_piece = [&](int i) __attribute__((always_inline)) {
-            const int tensor = i >= DMA_PER_TENSOR;
-            const int ii = i - tensor * DMA_PER_TENSOR;
-            const unsigned p = (unsigned) (ii * 64) + (unsigned) ln_o;      // < 1088
-            // p / 17 and p % 17 with full-rate 24-bit multiplies: (p * 3856) >> 16
-            // is exact for p < 1088
-            unsigned key = __umul24(p, 3856u) >> 16;
-            const unsigned part = p - __umul24(key, 17u);
-            if (clamp) key = std::min(key, (unsigned) last);
-            // row strides are < 2^24 (checked on the host): 24-bit multiplies suffice
-            const char * src = (tensor ? vc0 + __umul24(key, (unsigned) a.v_nb1) : kc0 + __umul24(key, (unsigned) a.k_nb1)) + part * 16;
-            dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(dstb + tensor * CHUNK_BYTES + ii * 1024)));
-        };
+    // A chunk is SLOTS wave-wide 16-byte DMAs; slot s lands at byte 1024*s of
+    // the stage: slots [0, DMA_T) are the K rows (piece p = 64*s + lane is byte
+    // 16*(p % 17) of key p / 17), the next DMA_T the V rows. Wave w issues slots
+    // w, w + 8, ...; only its last slot can be absent. The lane offsets within
+    // a chunk are the same for every chunk.
+    auto slot_off = [&](int slot) -> uint32_t {
+        const int tensor = slot >= DMA_T;
+        const unsigned p = (unsigned) ((slot - tensor * DMA_T) * 64 + lane);
+        const unsigned key = p / 17u, part = p - key * 17u;
+        return key * (unsigned) (tensor ? a.v_nb1 : a.k_nb1) + part * 16u;
+    };
+    uint32_t doff[SPW];
 #pragma unroll
-        for (int n = n0; n < (n1 < DPW - 1 ? n1 : DPW - 1); n++) kv_piece(wave + n * WAVES);
-        if constexpr (n1 < DPW) return;
-        const int il = wave + (DPW - 1) * WAVES;
-        if (il < 2 * DMA_PER_TENSOR) {
-            kv_piece(il);
-        } else if (a.mask) {
-            const int m = il - 2 * DMA_PER_TENSOR;
-            const int mr = std::min(m * 8 + (ln_o >> 3), n_mrows - 1);
-            const uint16_t * src = a.mimg + mask_img_row(a, mr, t0, r0, kvh, b) * a.n_kv_pad + c0 + (ln_o & 7) * 8;
-            dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(dstb + 2 * CHUNK_BYTES + m * 1024)));
-        } else {
-            kv_piece(wave);
+    for (int s = 0; s < SPW; s++) doff[s] = slot_off(wave + WAVES * s);
+    // vector-memory operations this wave issues per chunk (DMAs, plus the mask
+    // loads in MASK_CHUNK mode): the count a wait leaves in flight for the
+    // chunk issued after the one it waits for
+    const int ops_per_chunk = (SLOTS - wave + WAVES - 1) / WAVES + (a.mask_mode == MASK_CHUNK ? 4 : 0);
+
+    // Chunk c is read through buffer resources based at its first key, sized
+    // to the bytes that exist: rows past n_kv arrive as zeros, and those keys
+    // are past the split, so they are masked.
+    const int64_t k_bytes = a.n_kv * (int64_t) a.k_nb1, v_bytes = a.n_kv * (int64_t) a.v_nb1;
+    auto issue_chunk = [&](int c, uint8_t * dstb) __attribute__((always_inline)) {
+        const int64_t c0 = k_lo + (int64_t) c * CK;
+        const int64_t kc = c0 * (int64_t) a.k_nb1, vc = c0 * (int64_t) a.v_nb1;
+        const v4i rk = make_rsrc(kbase + kc, (uint32_t) std::min<int64_t>(k_bytes - kc, 0xffffffffll));
+        const v4i rv = make_rsrc(vbase + vc, (uint32_t) std::min<int64_t>(v_bytes - vc, 0xffffffffll));
+#pragma unroll
+        for (int s = 0; s < SPW; s++) {
+            const int slot = wave + WAVES * s;
+            if (s == SPW - 1 && slot >= SLOTS) break;
+            const v4i r = slot < DMA_T ? rk : rv;
+            dma16_buf(r, doff[s], __builtin_amdgcn_readfirstlane(lds_addr(dstb + slot * 1024)));
         }
     };
 
-    // ---- prologue: the lane's query operands (prepared once per call) and
-    //      chunk 0, one wait for both. Chunk c+1 is then issued during chunk c's
-    //      compute, in three parts, so the DMA queue drains while the wave works ----
-    v4i qw[RT][NBLK];                                   // B operands of QK: window slice lg of each block, per row tile
-    {
+    // Mask values. MASK_SPLIT: the block's mask rows over its whole split are
+    // loaded into LDS once, in the prologue. MASK_CHUNK (rows too many for
+    // that): the lane's 4 keys of a chunk in its own mask row are loaded with
+    // the chunk's DMAs (and waited for with them), one F16 value per register
+    // so nothing consumes them early. Both go through a buffer resource over
+    // the batch's mask slice: keys past n_kv read a neighbouring row's values
+    // or zeros (past the slice), and they are masked anyway.
+    const __amdgpu_buffer_rsrc_t mrsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void *) (a.mask ? a.mask + (size_t) (b % a.m_ne3) * a.m_nb3 : a.q), (short) 0, (int) a.m_slice, 0x00020000);
+    uint32_t mrow_off = 0;
+    if (a.mask) {
+        const int rl_m = 16 * tile + ln;
+        const int r = r0 + std::min(rl_m, RW - 1), t = r / a.gqa;   // padded rows read row RW - 1
+        const int hq = (kvh * a.gqa + (r - t * a.gqa)) % a.m_ne2;
+        mrow_off = (uint32_t) ((size_t) t * a.m_nb1 + (size_t) hq * a.m_nb2);
+    }
+    auto load_mask = [&](int c, uint32_t (&m)[4]) __attribute__((always_inline)) {
+        if (a.mask_mode != MASK_CHUNK) return;
+        const uint32_t off = mrow_off + 2u * (uint32_t) (k_lo + (int64_t) c * CK + kg * KW + lg * 4);
 #pragma unroll
-        for (int t = 0; t < RT; t++) {
-            const uint4 * qp = a.qimg + ((size_t) bkr * RT * 64 + t * 64 + lane) * NBLK;
+        for (int i = 0; i < 4; i++) m[i] = __builtin_amdgcn_raw_buffer_load_b16(mrsrc, off + 2u * i, 0, 0);
+    };
+
+    // ---- prologue: chunks 0 .. NS-2 in flight while the block requantises
+    //      its query rows into the last stage (no DMA writes there before
+    //      chunk NS-1 is issued) ----
+    // Order: chunk 0, then the block's own loads (query rows, MASK_SPLIT rows;
+    // waiting for them waits for chunk 0 as well, the counter being in
+    // order), then chunk 1, which stays in flight through the requantisation.
+    uint32_t mreg[NS][4] = {};                                 // MASK_CHUNK values, one set per stage
+    issue_chunk(0, ring[0]);
+    load_mask(0, mreg[0]);
+    // MASK_SPLIT rows: query position t0 + mr (shared mask) or query row r0 + mr
+    // (per head); loaded to registers here, stored to LDS once they arrive
+    constexpr int MIT = MASK_LDS / 2 / (WAVES * 64);
+    const int n_mval = a.mask_mode == MASK_SPLIT ? ((a.m_ne2 == 1 ? (r0 + RW - 1) / a.gqa - t0 + 1 : RW) * a.split_len) : 0;
+    uint16_t mpre[MIT];
 #pragma unroll
-            for (int bb = 0; bb < NBLK; bb++) qw[t][bb] = gload16_asm(qp + bb);
+    for (int it = 0; it < MIT; it++) {
+        const int e = (int) threadIdx.x + it * WAVES * 64;
+        mpre[it] = 0;
+        if (e < n_mval) {
+            const int mr = e / a.split_len, j = e - mr * a.split_len;
+            int t = t0 + mr, hq = 0;
+            if (a.m_ne2 != 1) {
+                const int r = r0 + mr;
+                t = r / a.gqa;
+                hq = (kvh * a.gqa + (r - t * a.gqa)) % a.m_ne2;
+            }
+            const uint32_t off = (uint32_t) ((size_t) t * a.m_nb1 + (size_t) hq * a.m_nb2) +
+                                 2u * (uint32_t) std::min<int64_t>(k_lo + j, a.n_kv - 1);
+            mpre[it] = __builtin_amdgcn_raw_buffer_load_b16(mrsrc, off, 0, 0);
         }
-        if (wave == 0) dma16(a.dqimg + (size_t) bkr * QROWS_IMG * NBLK + lane * 4, __builtin_amdgcn_readfirstlane(lds_addr(&dql[0][0])));
     }
-    issue_part(0, ring[0], std::integral_constant<int, 0>{}, std::integral_constant<int, DPW>{});
-    wait_vmcnt<0>();
+    uint8_t * qwin = ring[NS - 1];                                  // [ROWS][NBLK][QWIN] windows
+    float * dql = (float *) (ring[NS - 1] + ROWS * NBLK * QWIN);    // [ROWS][NBLK] d_q * scale * log2(e)
+    for (int e = threadIdx.x; e < ROWS * NBLK * QWIN / 16; e += WAVES * 64) ((uint4 *) qwin)[e] = make_uint4(0, 0, 0, 0);
+    __syncthreads();
+    {
+        // 8 lanes per (row, block), 4 values each; every load of the thread is
+        // in flight before the first is used
+        constexpr int QIT = ROWS * NBLK * 8 / (WAVES * 64);
+        static_assert(ROWS * NBLK * 8 % (WAVES * 64) == 0, "whole query iterations");
+        float4 v4[QIT];
 #pragma unroll
-    for (int t = 0; t < RT; t++)
+        for (int it = 0; it < QIT; it++) {
+            const int e = (int) threadIdx.x + it * WAVES * 64;
+            const int unit = e >> 3, sub = e & 7;
+            const int rl = unit / NBLK, blk = unit % NBLK;
+            const int r = r0 + std::min(rl, RW - 1);
+            const int t = r / a.gqa, h = kvh * a.gqa + (r - t * a.gqa);
+            v4[it] = *(const float4 *) (a.q + (size_t) t * a.q_nb1 + (size_t) h * a.q_nb2 + (size_t) b * a.q_nb3 +
+                                        (size_t) (blk * QK + sub * 4) * 4);
+        }
+        // every query and mask value of this thread has arrived (and chunk 0);
+        // the compiler sees this wait, so no later one stalls on chunk 1
+        wait_vmcnt<0>();
 #pragma unroll
-        for (int bb = 0; bb < NBLK; bb++) asm volatile("" : "+v"(qw[t][bb]));   // loaded: usable from here on
-    // the lane's query row in tile t is 16t + ln; padded rows (>= RW) read mask
-    // row 0 and are never stored
-    int mrow[RT];
+        for (int it = 0; it < MIT; it++) {
+            const int e = (int) threadIdx.x + it * WAVES * 64;
+            if (e < n_mval) mlds[e] = mpre[it];
+        }
+        if constexpr (NS > 2) {
+            if (n_chunks > 1) {
+                issue_chunk(1, ring[1]);
+                load_mask(1, mreg[1]);
+            }
+        }
+        const float fs = a.scale * LOG2E;
 #pragma unroll
-    for (int t = 0; t < RT; t++) {
-        const int rl = t * 16 + ln;
-        mrow[t] = rl >= RW ? 0 : (a.m_ne2 == 1 ? (r0 + rl) / a.gqa - t0 : rl);
+        for (int it = 0; it < QIT; it++) {
+            const int e = (int) threadIdx.x + it * WAVES * 64;
+            const int unit = e >> 3, sub = e & 7;
+            const int rl = unit / NBLK, blk = unit % NBLK;
+            const float x[4] = {v4[it].x, v4[it].y, v4[it].z, v4[it].w};
+            const float z[4] = {0.f, 0.f, 0.f, 0.f};
+            uint16_t d16;
+            float dq;
+            const uint32_t w = dev::q8_quantize_lane4(rl < RW ? x : z, a.x86 != 0, &d16, &dq);
+            uint16_t * wp = (uint16_t *) (qwin + (rl * NBLK + blk) * QWIN + win_off(blk) + 4 * sub);
+            wp[0] = (uint16_t) w;
+            wp[1] = (uint16_t) (w >> 16);
+            if (sub == 0) dql[rl * NBLK + blk] = dq * fs;
+        }
     }
+    __syncthreads();
+    const int rl_lane = 16 * tile + ln;                 // this lane's query row (MFMA column)
+    v4i qw[NBLK];                                       // B operands of QK: window slice lg of each block
+    float dq[NBLK];
+#pragma unroll
+    for (int bb = 0; bb < NBLK; bb++) {
+        qw[bb] = *(const v4i *) (qwin + (rl_lane * NBLK + bb) * QWIN + 16 * lg);
+        dq[bb] = dql[rl_lane * NBLK + bb];
+    }
+#pragma unroll
+    for (int bb = 0; bb < NBLK; bb++) asm volatile("" : "+v"(qw[bb]), "+v"(dq[bb]));   // read before the stage is reused
+    // the lane's row in the MASK_SPLIT rows (padded rows read row 0; never stored)
+    const int mrow = rl_lane >= RW ? 0 : (a.m_ne2 == 1 ? (r0 + rl_lane) / a.gqa - t0 : rl_lane);
 
-    // ---- online softmax state per row tile ----
-    v4f   O[RT][NBLK][2];
-    float m_run[RT], l_run[RT];
+    // ---- online softmax state of the lane's row ----
+    v4f   O[NBLK][2];
+    float m_run = -INFINITY, l_run = 0.f;
 #pragma unroll
-    for (int t = 0; t < RT; t++) {
-        m_run[t] = -INFINITY;
-        l_run[t] = 0.f;
-#pragma unroll
-        for (int bb = 0; bb < NBLK; bb++) { O[t][bb][0] = v4f{0, 0, 0, 0}; O[t][bb][1] = v4f{0, 0, 0, 0}; }
-    }
+    for (int bb = 0; bb < NBLK; bb++) { O[bb][0] = v4f{0, 0, 0, 0}; O[bb][1] = v4f{0, 0, 0, 0}; }
 
-    const int wk = kgrp * KW;   // this wave's first key in a chunk
-    const int span = (int) (k_hi - k_lo);                       // keys of this split (<= split_len)
+    const int span = (int) (k_hi - k_lo);               // keys of this split
     uint16_t (*sw)[NBLK][KW] = scl[wave];
 
-    // One chunk: `cur` holds chunk c; chunk c+1 goes to `nxt`. Called with the
-    // ring stages literally so the compiler can tell them apart.
-    constexpr int P1 = DPW / 3, P2 = 2 * DPW / 3;
-    auto chunk_step = [&](int c, uint8_t * cur, uint8_t * nxt) __attribute__((always_inline)) {
-        // chunk c was the last thing issued (during step c-1): wait for all of
-        // it; the barrier publishes it and also tells every wave that `nxt`
-        // (chunk c-1's stage) is no longer read
-        wait_vmcnt<0>();
+    // One chunk: `cur` holds chunk c; chunk c+NS-1 goes to `nxt` (chunk c-1's
+    // stage), its MASK_CHUNK values to `mnext`. Called with the ring stages
+    // and mask registers literally (no register copy that would wait for the
+    // loads in flight).
+    auto chunk_step = [&](int c, uint8_t * cur, uint8_t * nxt, const uint32_t (&mcur)[4], uint32_t (&mnext)[4])
+                          __attribute__((always_inline)) {
+        // Wait for chunk c; with three stages chunk c+1 (issued one step
+        // earlier) may stay in flight. The barrier publishes every wave's part
+        // and tells all of them that `nxt` is no longer read.
+        if (NS > 2 && c + 1 < n_chunks) wait_vmcnt_n(ops_per_chunk);
+        else wait_vmcnt<0>();
         __syncthreads();
-        const bool more = c + 1 < n_chunks;
-        const uint8_t * ks = cur;
-        const uint8_t * vs = cur + CHUNK_BYTES;
-        // this wave's keys' block scales, transposed to [block][key] (all reads
-        // issued before the writes: the two LDS arrays could alias as far as the
-        // compiler knows, so interleaving would serialise them)
+        if (c + NS - 1 < n_chunks) {
+            issue_chunk(c + NS - 1, nxt);
+            load_mask(c + NS - 1, mnext);
+        }
+        // this wave's keys' block scales, transposed to [block][key]: entry n of
+        // a lane is tensor n / 2, key (n % 2) * 8 + lane / 8, block lane % 8
         {
-            // entry n of this lane: tensor n / 2, key (n % 2) * 8 + lane / 8, block lane % 8
-            const uint8_t * src = cur + (wk + (lane >> 3)) * SEG + (lane & 7) * QBLOCK;
+            const uint8_t * src = cur + (kg * KW + (lane >> 3)) * SEG + (lane & 7) * QBLOCK;
             uint16_t * dstw = &sw[0][lane & 7][lane >> 3];
             uint16_t sv[4];
 #pragma unroll
-            for (int n = 0; n < 4; n++) sv[n] = *(const uint16_t *) (src + (n >> 1) * CHUNK_BYTES + (n & 1) * 8 * SEG);
+            for (int n = 0; n < 4; n++) sv[n] = *(const uint16_t *) (src + (n >> 1) * CHUNK + (n & 1) * 8 * SEG);
 #pragma unroll
             for (int n = 0; n < 4; n++) dstw[(n >> 1) * NBLK * KW + (n & 1) * 8] = sv[n];
         }
         wave_lds_sync();
-        if (more) issue_part(c + 1, nxt, std::integral_constant<int, 0>{}, std::integral_constant<int, P1>{});
 
-        // ---- S = Q K^T: one 16-key tile (the MFMA rows) x RT row tiles ----
-        float s[RT][4];
+        // ---- S = Q K^T for the wave's 16 keys (MFMA rows) x 16 query rows ----
+        float s[4] = {0.f, 0.f, 0.f, 0.f};
         {
-            const uint8_t * krow = ks + (wk + ln) * SEG + 16 * lg;   // A operand: key row ln, slice lg
-#pragma unroll
-            for (int t = 0; t < RT; t++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) s[t][i] = 0.f;
+            const uint8_t * krow = cur + (kg * KW + ln) * SEG + 16 * lg;   // A operand: key row ln, slice lg
 #pragma unroll
             for (int bb = 0; bb < NBLK; bb++) {
                 const v4i kA = *(const v4i *) (krow + 16 * win_piece(bb));
                 const uint2 dk = *(const uint2 *) &sw[0][bb][lg * 4];   // the lane's 4 keys' fp16 d_k
-#pragma unroll
-                for (int t = 0; t < RT; t++) {
-                    const v4i cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kA, qw[t][bb], v4i{0, 0, 0, 0}, 0, 0, 0);
-                    const float dq = dql[t * 16 + ln][bb];
-                    s[t][0] = __builtin_fmaf((float) cc[0], mul_f16lo(dq, dk.x), s[t][0]);
-                    s[t][1] = __builtin_fmaf((float) cc[1], mul_f16hi(dq, dk.x), s[t][1]);
-                    s[t][2] = __builtin_fmaf((float) cc[2], mul_f16lo(dq, dk.y), s[t][2]);
-                    s[t][3] = __builtin_fmaf((float) cc[3], mul_f16hi(dq, dk.y), s[t][3]);
-                }
+                const v4i cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kA, qw[bb], v4i{0, 0, 0, 0}, 0, 0, 0);
+                s[0] = __builtin_fmaf((float) cc[0], mul_f16lo(dq[bb], dk.x), s[0]);
+                s[1] = __builtin_fmaf((float) cc[1], mul_f16hi(dq[bb], dk.x), s[1]);
+                s[2] = __builtin_fmaf((float) cc[2], mul_f16lo(dq[bb], dk.y), s[2]);
+                s[3] = __builtin_fmaf((float) cc[3], mul_f16hi(dq[bb], dk.y), s[3]);
             }
         }
-        if (more) issue_part(c + 1, nxt, std::integral_constant<int, P1>{}, std::integral_constant<int, P2>{});
 
         // ---- mask, online softmax (base 2; scores are already in log2 units).
         //      A masked key has x = -inf, so its p is exp2(-inf) = 0 ----
-        float p[RT][4];
-        const int kin = c * CK + wk + lg * 4;                     // first of the lane's 4 keys in the split
-        const bool tail = (c + 1) * CK > span;                     // keys past the split in this chunk
-#pragma unroll
-        for (int t = 0; t < RT; t++) {
-            uint2 mv = make_uint2(0, 0);
-            if (a.mask) mv = *(const uint2 *) (cur + 2 * CHUNK_BYTES + (mrow[t] * CK + wk + lg * 4) * 2);
+        float p[4];
+        {
+            const int kin = c * CK + kg * KW + lg * 4;           // first of the lane's 4 keys in the split
+            const bool tail = (c + 1) * CK > span;                // keys past the split in this chunk
             float x[4];
             float mloc = -INFINITY;
+            uint32_t mv[4] = {mcur[0], mcur[1], mcur[2], mcur[3]};
+            if (a.mask_mode == MASK_SPLIT) {
+                const uint2 m2 = *(const uint2 *) &mlds[mrow * a.split_len + c * CK + kg * KW + lg * 4];
+                mv[0] = m2.x; mv[1] = m2.x >> 16; mv[2] = m2.y; mv[3] = m2.y >> 16;
+            }
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const uint32_t mh = i < 2 ? mv.x : mv.y;
-                float xi = (i & 1) ? fma_f16hi(mh, LOG2E, s[t][i]) : fma_f16lo(mh, LOG2E, s[t][i]);
+                float xi = a.mask_mode != MASK_NONE ? fma_f16lo(mv[i], LOG2E, s[i]) : s[i];
                 if (tail && kin + i >= span) xi = -INFINITY;
                 x[i] = xi;
                 mloc = xmax(mloc, xi);
             }
             mloc = xmax_lanes16_32(mloc);
-            const float m_new = xmax(m_run[t], mloc);
-            const float m_use = (m_new == -INFINITY) ? 0.f : m_new;   // all keys masked so far
-            const float alpha = __builtin_amdgcn_exp2f(m_run[t] - m_use);
+            // the running max moves only when the chunk's max exceeds it by more
+            // than RESCALE_SLACK (or it is still -inf), so p <= 2^RESCALE_SLACK
+            const bool grow = mloc > m_run + RESCALE_SLACK;
+            float alpha = 1.f;
+            if (grow) {
+                alpha = __builtin_amdgcn_exp2f(m_run - mloc);
+                m_run = mloc;
+            }
+            const float m_use = m_run == -INFINITY ? 0.f : m_run;   // all keys masked so far
             float lsum = 0.f;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                p[t][i] = __builtin_amdgcn_exp2f(x[i] - m_use);
-                lsum += p[t][i];
+                p[i] = __builtin_amdgcn_exp2f(x[i] - m_use);
+                lsum += p[i];
             }
-            l_run[t] = l_run[t] * alpha + lsum;
-            m_run[t] = m_new;
-            if (__any(alpha != 1.f)) {
+            l_run = l_run * alpha + lsum;
+            if (__any(grow)) {
 #pragma unroll
-                for (int bb = 0; bb < NBLK; bb++) { O[t][bb][0] *= alpha; O[t][bb][1] *= alpha; }
+                for (int bb = 0; bb < NBLK; bb++) { O[bb][0] *= alpha; O[bb][1] *= alpha; }
             }
         }
-        if (more) issue_part(c + 1, nxt, std::integral_constant<int, P2>{}, std::integral_constant<int, DPW>{});
 
         // ---- O += V^T P per V block. Tile e of block bb holds dims 32bb + 2m + e
         //      (m = MFMA row); the A operand of lane (m, g) is dims 2m, 2m+1 of the
         //      lane's 4 keys (4g..4g+3 of the wave's 16), one naturally aligned
-        //      2-byte LDS read per key, shared by every row tile ----
-        const uint8_t * vrow = vs + (wk + lg * 4) * SEG + 2 + 2 * ln;
+        //      2-byte LDS read per key ----
+        const uint8_t * vrow = cur + CHUNK + (kg * KW + lg * 4) * SEG + 2 + 2 * ln;
 #pragma unroll
         for (int bb = 0; bb < NBLK; bb++) {
             // keys 2q and 2q+1 share a register: dims 2m, 2m+1 of key 2q in bytes 0-1,
@@ -559,147 +575,136 @@ void k_fattn_q8_0(fa_args a) {
             }
             const uint2 dv2 = *(const uint2 *) &sw[1][bb][lg * 4];
             const uint32_t dv[2] = {dv2.x, dv2.y};
-            uint32_t a0[2], a1[2];
+            uint32_t a0[2], a1[2], bh[2], bl[2];
             cvt_v_block(w, a0, a1);
+            pdv_hilo(p, dv, bh, bl);
             const v4h A0 = __builtin_bit_cast(v4h, make_uint2(a0[0], a0[1]));
             const v4h A1 = __builtin_bit_cast(v4h, make_uint2(a1[0], a1[1]));
-#pragma unroll
-            for (int t = 0; t < RT; t++) {
-                uint32_t bh[2], bl[2];
-                pdv_hilo(p[t], dv, bh, bl);
-                const v4h Bh = __builtin_bit_cast(v4h, make_uint2(bh[0], bh[1]));
-                const v4h Bl = __builtin_bit_cast(v4h, make_uint2(bl[0], bl[1]));
-                O[t][bb][0] = __builtin_amdgcn_mfma_f32_16x16x16f16(A0, Bh, O[t][bb][0], 0, 0, 0);
-                O[t][bb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A1, Bh, O[t][bb][1], 0, 0, 0);
-                O[t][bb][0] = __builtin_amdgcn_mfma_f32_16x16x16f16(A0, Bl, O[t][bb][0], 0, 0, 0);
-                O[t][bb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A1, Bl, O[t][bb][1], 0, 0, 0);
-            }
+            const v4h Bh = __builtin_bit_cast(v4h, make_uint2(bh[0], bh[1]));
+            const v4h Bl = __builtin_bit_cast(v4h, make_uint2(bl[0], bl[1]));
+            O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x16f16(A0, Bh, O[bb][0], 0, 0, 0);
+            O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A1, Bh, O[bb][1], 0, 0, 0);
+            O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x16f16(A0, Bl, O[bb][0], 0, 0, 0);
+            O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A1, Bl, O[bb][1], 0, 0, 0);
         }
     };
-    for (int c = 0; c < n_chunks; c += 2) {
-        chunk_step(c, ring[0], ring[1]);
-        if (c + 1 < n_chunks) chunk_step(c + 1, ring[1], ring[0]);
+    if constexpr (NS == 3) {
+        for (int c = 0; c < n_chunks; c += 3) {
+            chunk_step(c, ring[0], ring[2], mreg[0], mreg[2]);
+            if (c + 1 < n_chunks) chunk_step(c + 1, ring[1], ring[0], mreg[1], mreg[0]);
+            if (c + 2 < n_chunks) chunk_step(c + 2, ring[2], ring[1], mreg[2], mreg[1]);
+        }
+    } else {
+        for (int c = 0; c < n_chunks; c += 2) {
+            chunk_step(c, ring[0], ring[1], mreg[0], mreg[1]);
+            if (c + 1 < n_chunks) chunk_step(c + 1, ring[1], ring[0], mreg[1], mreg[0]);
+        }
     }
     __syncthreads();   // every wave is done with the last chunk: stage 0 becomes the merge buffer
 
-    // ---- merge the 4 key groups in LDS: each wave publishes (max, sum) per row,
-    //      then adds its weighted O into the buffer in turn; wave 0 adds last and
-    //      writes the block's result ----
-    float * ob = (float *) ring[0];                                // [ROWS][256] f32, natural dim order
-    float2 * ml = (float2 *) (ring[0] + ROWS * D * 4);             // [WAVES][ROWS]
-#pragma unroll
-    for (int t = 0; t < RT; t++) {
-        const float l = sum_lanes16_32(l_run[t]);
-        if (lg == 0) ml[wave * ROWS + t * 16 + ln] = make_float2(m_run[t], l);
+    // ---- merge the key groups of each row tile in LDS: every wave publishes
+    //      (max, sum) per row, then the groups add their weighted O into the
+    //      buffer in turn; group 0 adds last and writes the block's result ----
+    // [ROWS][OBS] f32, natural dim order; the padded row stride puts the 16
+    // rows a float4 access touches on different banks
+    constexpr int OBS = D + 4;
+    float * ob = (float *) ring[0];
+    float2 * ml = (float2 *) (ring[0] + ROWS * OBS * 4);           // [WAVES][16]
+    {
+        const float l = sum_lanes16_32(l_run);
+        if (lg == 0) ml[wave * 16 + ln] = make_float2(m_run, l);
     }
     __syncthreads();
-    float M[RT], L[RT], fw[RT];
+    float M = -INFINITY, L = 0.f;
 #pragma unroll
-    for (int t = 0; t < RT; t++) {
-        float mx = -INFINITY;
+    for (int k2 = 0; k2 < KG; k2++) M = xmax(M, ml[(k2 * RT + tile) * 16 + ln].x);
 #pragma unroll
-        for (int w2 = 0; w2 < WAVES; w2++) mx = xmax(mx, ml[w2 * ROWS + t * 16 + ln].x);
-        float ls = 0.f;
-#pragma unroll
-        for (int w2 = 0; w2 < WAVES; w2++) {
-            const float2 e = ml[w2 * ROWS + t * 16 + ln];
-            ls += e.x == -INFINITY ? 0.f : e.y * exp2f(e.x - mx);
-        }
-        M[t] = mx;
-        L[t] = ls;
-        fw[t] = (m_run[t] == -INFINITY) ? 0.f : exp2f(m_run[t] - mx);
+    for (int k2 = 0; k2 < KG; k2++) {
+        const float2 e = ml[(k2 * RT + tile) * 16 + ln];
+        L += e.x == -INFINITY ? 0.f : e.y * exp2f(e.x - M);
     }
-    // Lane (ln, lg) holds, for row tile t and block bb, dims 32bb + 8lg + 2i + e
-    // of row 16t + ln in O[t][bb][e][i]. Lane indices are re-derived here (an
-    // opaque copy of the thread id), so no output address stays live through
-    // the key loop.
+    const float fw = m_run == -INFINITY ? 0.f : exp2f(m_run - M);
+    // Lane (ln, lg) holds dims 32bb + 8lg + 2i + e of row 16*tile + ln in
+    // O[bb][e][i]. Lane indices are re-derived here (an opaque copy of the
+    // thread id), so no output address stays live through the key loop.
     int tid_e = (int) threadIdx.x;
     asm volatile("" : "+v"(tid_e));
     const int ln_e = tid_e & 15, lg_e = (tid_e >> 4) & 3;
-    for (int w2 = WAVES - 1; w2 >= 1; w2--) {
-        if (wave == w2) {
+    const int rl = 16 * tile + ln_e;
+    float * orow = ob + rl * OBS + 8 * lg_e;
+    for (int k2 = KG - 1; k2 >= 1; k2--) {
+        if (kg == k2) {
 #pragma unroll
-            for (int t = 0; t < RT; t++) {
-                float * orow = ob + (t * 16 + ln_e) * D + 8 * lg_e;
-#pragma unroll
-                for (int bb = 0; bb < NBLK; bb++) {
-                    const v4f o0 = O[t][bb][0] * fw[t], o1 = O[t][bb][1] * fw[t];
-                    float4 * d0 = (float4 *) (orow + 32 * bb);
-                    float4 * d1 = (float4 *) (orow + 32 * bb + 4);
-                    if (w2 == WAVES - 1) {
-                        *d0 = make_float4(o0[0], o1[0], o0[1], o1[1]);
-                        *d1 = make_float4(o0[2], o1[2], o0[3], o1[3]);
-                    } else {
-                        float4 x0 = *d0, x1 = *d1;
-                        x0.x += o0[0]; x0.y += o1[0]; x0.z += o0[1]; x0.w += o1[1];
-                        x1.x += o0[2]; x1.y += o1[2]; x1.z += o0[3]; x1.w += o1[3];
-                        *d0 = x0;
-                        *d1 = x1;
-                    }
+            for (int bb = 0; bb < NBLK; bb++) {
+                const v4f o0 = O[bb][0] * fw, o1 = O[bb][1] * fw;
+                float4 * d0 = (float4 *) (orow + 32 * bb);
+                float4 * d1 = (float4 *) (orow + 32 * bb + 4);
+                if (k2 == KG - 1) {
+                    *d0 = make_float4(o0[0], o1[0], o0[1], o1[1]);
+                    *d1 = make_float4(o0[2], o1[2], o0[3], o1[3]);
+                } else {
+                    float4 x0 = *d0, x1 = *d1;
+                    x0.x += o0[0]; x0.y += o1[0]; x0.z += o0[1]; x0.w += o1[1];
+                    x1.x += o0[2]; x1.y += o1[2]; x1.z += o0[3]; x1.w += o1[3];
+                    *d0 = x0;
+                    *d1 = x1;
                 }
             }
         }
         __syncthreads();
     }
-    if (wave != 0) return;
+    if (kg != 0 || rl >= RW) return;
     const size_t bh = (size_t) b * a.nh_kv + kvh;
     const bool vec = a.ns > 1 || a.dst_vec;
+    const int r = r0 + rl;
+    const int tq = r / a.gqa, h = kvh * a.gqa + (r - tq * a.gqa);
+    float * out;
+    float oscale;
+    if (a.ns == 1) {
+        out = a.dst + (((size_t) b * a.T + tq) * a.nh + h) * D + 8 * lg_e;
+        oscale = L > 0.f ? 1.f / L : 0.f;
+    } else {
+        out = a.part_o + ((bh * a.ns + split) * a.R + r) * D + 8 * lg_e;
+        oscale = 1.f;
+        if (lg_e == 0) a.part_ml[(bh * a.ns + split) * a.R + r] = make_float2(M, L);
+    }
 #pragma unroll
-    for (int t = 0; t < RT; t++) {
-        const int rl = t * 16 + ln_e;
-        if (rl >= RW) continue;
-        const int r = r0 + rl;
-        const int tq = r / a.gqa, h = kvh * a.gqa + (r - tq * a.gqa);
-        float * out;
-        float oscale;
-        if (a.ns == 1) {
-            out = a.dst + (((size_t) b * a.T + tq) * a.nh + h) * D + 8 * lg_e;
-            oscale = L[t] > 0.f ? 1.f / L[t] : 0.f;
+    for (int bb = 0; bb < NBLK; bb++) {
+        const float4 p0 = *(const float4 *) (orow + 32 * bb), p1 = *(const float4 *) (orow + 32 * bb + 4);
+        const v4f o0 = O[bb][0] * fw, o1 = O[bb][1] * fw;
+        const float4 w0 = make_float4((o0[0] + p0.x) * oscale, (o1[0] + p0.y) * oscale, (o0[1] + p0.z) * oscale, (o1[1] + p0.w) * oscale);
+        const float4 w1 = make_float4((o0[2] + p1.x) * oscale, (o1[2] + p1.y) * oscale, (o0[3] + p1.z) * oscale, (o1[3] + p1.w) * oscale);
+        if (vec) {
+            *(float4 *) (out + 32 * bb) = w0;
+            *(float4 *) (out + 32 * bb + 4) = w1;
         } else {
-            out = a.part_o + ((bh * a.ns + split) * a.R + r) * D + 8 * lg_e;
-            oscale = 1.f;
-            if (lg_e == 0) a.part_ml[(bh * a.ns + split) * a.R + r] = make_float2(M[t], L[t]);
-        }
-        const float * orow = ob + rl * D + 8 * lg_e;
-#pragma unroll
-        for (int bb = 0; bb < NBLK; bb++) {
-            const float4 p0 = *(const float4 *) (orow + 32 * bb), p1 = *(const float4 *) (orow + 32 * bb + 4);
-            const v4f o0 = O[t][bb][0] * fw[t], o1 = O[t][bb][1] * fw[t];
-            const float4 w0 = make_float4((o0[0] + p0.x) * oscale, (o1[0] + p0.y) * oscale, (o0[1] + p0.z) * oscale, (o1[1] + p0.w) * oscale);
-            const float4 w1 = make_float4((o0[2] + p1.x) * oscale, (o1[2] + p1.y) * oscale, (o0[3] + p1.z) * oscale, (o1[3] + p1.w) * oscale);
-            if (vec) {
-                *(float4 *) (out + 32 * bb) = w0;
-                *(float4 *) (out + 32 * bb + 4) = w1;
-            } else {
-                float * o = out + 32 * bb;
-                o[0] = w0.x; o[1] = w0.y; o[2] = w0.z; o[3] = w0.w;
-                o[4] = w1.x; o[5] = w1.y; o[6] = w1.z; o[7] = w1.w;
-            }
+            float * o = out + 32 * bb;
+            o[0] = w0.x; o[1] = w0.y; o[2] = w0.z; o[3] = w0.w;
+            o[4] = w1.x; o[5] = w1.y; o[6] = w1.z; o[7] = w1.w;
         }
     }
 }
 
-// LSE merge of the ns split partials of one query row. All (max, sum) pairs
-// are read into LDS at once while the partial rows are already in flight;
-// thread (group g, quad q) then folds splits g, g+4, ... of dims 4q..4q+3 and
-// the four groups add up through LDS.
-constexpr int MERGE_GROUPS = 4;
+// LSE merge of the ns split partials. One block per (query row, quarter of
+// the head dims): thread (group g, quad q) folds splits g, g + 16, ... of dims
+// 4q..4q+3 of the quarter, with the first 8 partials of each group in flight
+// before the weights are known; the 16 groups add up through LDS.
+constexpr int MERGE_GROUPS = 16;
 constexpr int MERGE_BATCH = 8;
 
 __global__ __launch_bounds__(256) void k_fattn_merge(fa_args a) {
     __shared__ float wsh[MAX_SPLITS];
-    __shared__ float red[256 / 64];
-    __shared__ float4 acc_sh[MERGE_GROUPS - 1][64];
-    const int row = blockIdx.x;                               // (b * nh_kv + kvh) * R + r
+    __shared__ float red[4];
+    __shared__ float4 acc_sh[MERGE_GROUPS][16];
+    const int row = blockIdx.x >> 2, quarter = blockIdx.x & 3;   // row = (b * nh_kv + kvh) * R + r
     const int r = row % a.R;
     const int bh = row / a.R;
     const int kvh = bh % a.nh_kv, b = bh / a.nh_kv;
-    const int g = threadIdx.x >> 6, q = threadIdx.x & 63;
+    const int g = threadIdx.x >> 4, q = threadIdx.x & 15;
     const float2 * ml = a.part_ml + (size_t) bh * a.ns * a.R + r;
-    const float4 * po = (const float4 *) (a.part_o + ((size_t) bh * a.ns * a.R + r) * D) + q;
+    const float4 * po = (const float4 *) (a.part_o + ((size_t) bh * a.ns * a.R + r) * D + 64 * quarter) + q;
     const size_t sstride = (size_t) a.R * D / 4;              // float4s between splits
 
-    // first batch of partial rows in flight before the weights are known
     float4 ob[MERGE_BATCH];
 #pragma unroll
     for (int i = 0; i < MERGE_BATCH; i++) {
@@ -745,15 +750,19 @@ __global__ __launch_bounds__(256) void k_fattn_merge(fa_args a) {
             acc.x += w * ob[i].x; acc.y += w * ob[i].y; acc.z += w * ob[i].z; acc.w += w * ob[i].w;
         }
     }
-    if (g > 0) acc_sh[g - 1][q] = acc;
+    acc_sh[g][q] = acc;
     __syncthreads();
     if (g == 0) {
-        const float4 a1 = acc_sh[0][q], a2 = acc_sh[1][q], a3 = acc_sh[2][q];
+        float4 o = acc_sh[0][q];
+#pragma unroll
+        for (int g2 = 1; g2 < MERGE_GROUPS; g2++) {
+            const float4 e = acc_sh[g2][q];
+            o.x += e.x; o.y += e.y; o.z += e.z; o.w += e.w;
+        }
         const float inv = L > 0.f ? 1.f / L : 0.f;
-        const float4 o = make_float4(((acc.x + a1.x) + (a2.x + a3.x)) * inv, ((acc.y + a1.y) + (a2.y + a3.y)) * inv,
-                                     ((acc.z + a1.z) + (a2.z + a3.z)) * inv, ((acc.w + a1.w) + (a2.w + a3.w)) * inv);
+        o.x *= inv; o.y *= inv; o.z *= inv; o.w *= inv;
         const int t = r / a.gqa, h = kvh * a.gqa + (r - t * a.gqa);
-        float * d = a.dst + (((size_t) b * a.T + t) * a.nh + h) * D + 4 * q;
+        float * d = a.dst + (((size_t) b * a.T + t) * a.nh + h) * D + 64 * quarter + 4 * q;
         if (a.dst_vec) {
             *(float4 *) d = o;
         } else {
@@ -766,8 +775,7 @@ __global__ __launch_bounds__(256) void k_fattn_merge(fa_args a) {
 
 struct fa_plan {
     int32_t R, RT, gqa, rw, n_rg, ns, split_len;
-    int64_t n_kv_pad;
-    size_t  off_ml, off_qimg, off_dq, off_mimg;   // workspace sections (bytes)
+    size_t  off_ml;                   // workspace section of the split (max, sum) pairs (bytes)
     size_t  ws_bytes;
 };
 
@@ -778,10 +786,14 @@ int env_int(const char * name, int dflt) {
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
+// Bytes from the start of a mask batch slice to the end of its last row.
+size_t mask_slice_bytes(const qwfn_tensor & m) {
+    return (size_t) (m.ne[1] - 1) * m.nb[1] + (size_t) (m.ne[2] - 1) * m.nb[2] + (size_t) m.ne[0] * 2;
+}
+
 // The key loop hand-counts its outstanding vector-memory operations (the LDS
-// DMAs and the query-operand loads are inline asm the compiler does not see),
-// so a build of the attention kernel that spills to scratch would break that
-// count: refuse to run one.
+// DMAs are inline asm the compiler does not see), so a build of the attention
+// kernel that spills to scratch would break that count: refuse to run one.
 int check_no_scratch() {
     static const int rc = [] {
         for (const void * f : {(const void *) k_fattn_q8_0<1>, (const void *) k_fattn_q8_0<2>}) {
@@ -825,60 +837,49 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
         return set_error(QWFN_EALIGN, "flash_attn_ext: q data and strides must be 16-byte aligned");
     if (k->nb[1] >= (size_t(1) << 24) || v->nb[1] >= (size_t(1) << 24))
         return set_error(QWFN_ENOTSUP, "flash_attn_ext: k/v row strides must be below 16 MiB");
-    bool per_head_mask = false;
-    int64_t m_slices = 0;
+    const int64_t n_kv = k->ne[1];
     if (mask) {
         if (!mask->data) return set_error(QWFN_EINVAL, "flash_attn_ext: mask has no data");
         if (mask->type != QWFN_TYPE_F16) return set_error(QWFN_EINVAL, "flash_attn_ext: mask must be f16");
         if (mask->nb[0] != 2) return set_error(QWFN_EINVAL, "flash_attn_ext: mask rows must be contiguous");
-        if (mask->ne[0] < k->ne[1] || mask->ne[1] < T)
+        if (mask->ne[0] < n_kv || mask->ne[1] < T)
             return set_error(QWFN_EINVAL, "flash_attn_ext: mask must be at least [n_kv, T]");
         if (mask->ne[2] <= 0 || nh % mask->ne[2] || mask->ne[3] <= 0 || q->ne[3] % mask->ne[3])
             return set_error(QWFN_EINVAL, "flash_attn_ext: mask must broadcast over heads and batch");
         if (!is_aligned(mask->data, 2)) return set_error(QWFN_EALIGN, "flash_attn_ext: mask must be 2-byte aligned");
-        per_head_mask = mask->ne[2] != 1;
-        m_slices = mask->ne[2] * mask->ne[3];
+        // per-lane mask offsets are 32-bit within one batch slice (plus a chunk of slack)
+        if (mask_slice_bytes(*mask) >= (size_t(1) << 31))
+            return set_error(QWFN_ENOTSUP, "flash_attn_ext: mask batch slices must be below 2 GiB");
     }
-    // Query rows per block: one or two 16-row tiles. A block streams at most
-    // MASK_ROWS mask rows per chunk: one per query row for a per-head mask, one
-    // per query position for a shared one.
+    // Query rows per block: one or two 16-row tiles.
     int rw = R > 16 ? 32 : 16;
     if (const int force = env_int("QWFN_FA_ROWS", 0)) rw = force >= 32 ? 32 : 16;
-    if (mask && rw == 32 && (per_head_mask || (32 + gqa - 1) / gqa + 1 > MASK_ROWS)) rw = 16;
     pl->R = (int32_t) R;
     pl->rw = rw;
     pl->RT = rw / 16;
     pl->n_rg = (int32_t) ((R + rw - 1) / rw);
     pl->gqa = (int32_t) gqa;
-    const int64_t n_kv = k->ne[1];
+    const int64_t ck = pl->RT == 1 ? fa_cfg<1>::CK : fa_cfg<2>::CK;
     const int64_t B = q->ne[3];
-    pl->n_kv_pad = (n_kv + CK - 1) / CK * CK;
     // Splits: about one block per CU (256), each at least one chunk.
     const int64_t target_blocks = env_int("QWFN_FA_BLOCKS", 256);
     int64_t ns = std::max<int64_t>(1, target_blocks / std::max<int64_t>(1, nh_kv * B * pl->n_rg));
-    ns = std::min<int64_t>(ns, std::max<int64_t>(1, (n_kv + CK - 1) / CK));
+    ns = std::min<int64_t>(ns, std::max<int64_t>(1, (n_kv + ck - 1) / ck));
     if (const int force = env_int("QWFN_FA_SPLITS", 0)) ns = force;
     int64_t split_len = (n_kv + ns - 1) / ns;
-    split_len = std::max<int64_t>(CK, (split_len + CK - 1) / CK * CK);
+    split_len = std::max<int64_t>(ck, (split_len + ck - 1) / ck * ck);
     ns = std::max<int64_t>(1, (n_kv + split_len - 1) / split_len);
     if (ns > MAX_SPLITS)
         return set_error(QWFN_ENOTSUP, "flash_attn_ext: " + std::to_string(ns) + " key splits requested, at most " +
                                            std::to_string(MAX_SPLITS) + " supported");
     pl->ns = (int32_t) ns;
     pl->split_len = (int32_t) split_len;
-    // workspace: split partials (when ns > 1), the query image, the mask image
-    const int64_t n_bkr = B * nh_kv * pl->n_rg;
+    // workspace: split partials (when ns > 1)
     const size_t n_part = ns > 1 ? (size_t) (B * nh_kv * ns * R) : 0;
     size_t off = align256(n_part * D * sizeof(float));
     pl->off_ml = off;
     off = align256(off + n_part * sizeof(float2));
-    pl->off_qimg = off;
-    off = align256(off + (size_t) n_bkr * pl->RT * 64 * NBLK * 16);
-    pl->off_dq = off;
-    off = align256(off + (size_t) n_bkr * QROWS_IMG * NBLK * sizeof(float));
-    pl->off_mimg = off;
-    off = align256(off + (size_t) m_slices * T * pl->n_kv_pad * 2);
-    pl->ws_bytes = off;
+    pl->ws_bytes = std::max<size_t>(off, 256);
     return QWFN_OK;
 }
 
@@ -934,21 +935,21 @@ extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor
     a.k = (const char *) k->data; a.k_nb1 = k->nb[1]; a.k_nb2 = k->nb[2]; a.k_nb3 = k->nb[3];
     a.v = (const char *) v->data; a.v_nb1 = v->nb[1]; a.v_nb2 = v->nb[2]; a.v_nb3 = v->nb[3];
     char * w = (char *) ws;
+    a.n_kv = n_kv;
+    a.T = (int32_t) q->ne[1]; a.nh = (int32_t) q->ne[2]; a.nh_kv = (int32_t) k->ne[2];
     if (mask) {
         a.mask = (const char *) mask->data; a.m_nb1 = mask->nb[1]; a.m_nb2 = mask->nb[2]; a.m_nb3 = mask->nb[3];
         a.m_ne2 = (int32_t) mask->ne[2]; a.m_ne3 = (int32_t) mask->ne[3];
-        a.mimg = (uint16_t *) (w + pl.off_mimg);
+        a.m_slice = (uint32_t) mask_slice_bytes(*mask);
+        const int64_t mrows = mask->ne[2] == 1 ? ((int64_t) pl.rw + pl.gqa - 1) / pl.gqa + 1 : pl.rw;
+        a.mask_mode = mrows * pl.split_len * 2 <= MASK_LDS ? MASK_SPLIT : MASK_CHUNK;
+        if (const int force = env_int("QWFN_FA_MASK_CHUNK", 0)) a.mask_mode = MASK_CHUNK;
     } else {
-        a.mask = nullptr; a.m_ne2 = 1; a.m_ne3 = 1; a.mimg = nullptr;
+        a.mask = nullptr; a.m_ne2 = 1; a.m_ne3 = 1; a.m_slice = 0; a.mask_mode = MASK_NONE;
     }
     a.dst = (float *) dst->data;
     a.part_o = (float *) w;
     a.part_ml = (float2 *) (w + pl.off_ml);
-    a.qimg = (uint4 *) (w + pl.off_qimg);
-    a.dqimg = (float *) (w + pl.off_dq);
-    a.n_kv = n_kv;
-    a.n_kv_pad = pl.n_kv_pad;
-    a.T = (int32_t) q->ne[1]; a.nh = (int32_t) q->ne[2]; a.nh_kv = (int32_t) k->ne[2];
     a.gqa = pl.gqa; a.R = pl.R; a.B = (int32_t) q->ne[3];
     a.kb = (int32_t) k->ne[3]; a.vb = (int32_t) v->ne[3];
     a.ns = pl.ns; a.split_len = pl.split_len; a.rw = pl.rw; a.n_rg = pl.n_rg;
@@ -959,16 +960,12 @@ extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor
     const int64_t grid = units * a.nh_kv * a.n_rg;
     if (grid > 0x7fffffff) return set_error(QWFN_EINVAL, "flash_attn_ext: grid too large");
     hipStream_t st = as_stream(stream);
-    const int n_qblocks = a.B * a.nh_kv * a.n_rg;
-    const int n_mblocks = mask ? 64 : 0;
-    if (pl.RT == 1) hipLaunchKernelGGL(k_fattn_prep<1>, dim3(n_qblocks + n_mblocks), dim3(256), 0, st, a, n_qblocks);
-    else            hipLaunchKernelGGL(k_fattn_prep<2>, dim3(n_qblocks + n_mblocks), dim3(256), 0, st, a, n_qblocks);
-    if (int rc = hip_check(hipGetLastError(), "flash_attn prep launch")) return rc;
-    if (pl.RT == 1) hipLaunchKernelGGL(k_fattn_q8_0<1>, dim3((unsigned) grid), dim3(KG * 64), 0, st, a);
-    else            hipLaunchKernelGGL(k_fattn_q8_0<2>, dim3((unsigned) grid), dim3(KG * 64), 0, st, a);
+    if (pl.RT == 1) hipLaunchKernelGGL(k_fattn_q8_0<1>, dim3((unsigned) grid), dim3(WAVES * 64), 0, st, a);
+    else            hipLaunchKernelGGL(k_fattn_q8_0<2>, dim3((unsigned) grid), dim3(WAVES * 64), 0, st, a);
     if (int rc = hip_check(hipGetLastError(), "flash_attn launch")) return rc;
     if (a.ns > 1) {
-        const int64_t blocks = (int64_t) a.B * a.nh_kv * a.R;
+        const int64_t blocks = (int64_t) a.B * a.nh_kv * a.R * 4;
+        if (blocks > 0x7fffffff) return set_error(QWFN_EINVAL, "flash_attn_ext: merge grid too large");
         hipLaunchKernelGGL(k_fattn_merge, dim3((unsigned) blocks), dim3(256), 0, st, a);
         if (int rc = hip_check(hipGetLastError(), "flash_attn merge launch")) return rc;
     }
