@@ -49,6 +49,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--long-depth", type=int, default=65536,
+                    help="also time the attention op alone at this depth (0: skip)")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="also run one device copy of this many MiB (counter calibration)")
     return ap.parse_args()
@@ -205,6 +207,47 @@ def main() -> int:
         graph_ms = e0.elapsed_time(e1) / args.steps
         log(f"[bench] graph: {graph_ms * 1e3 / L:.2f} us/layer")
 
+    # ---- the attention op alone at a long context (the 64K decode/verify target) ----
+    long_ctx = None
+    if args.long_depth:
+        ld = args.long_depth
+        n_kv_l = ld + T
+        n_sets_l = 4                                   # 4 x 71 MB: more than the Infinity Cache holds
+        lcaches = []
+        for s in range(n_sets_l):
+            kc = torch.zeros((n_kv_l, ROW), dtype=torch.uint8, device=dev)
+            vc = torch.zeros((n_kv_l, ROW), dtype=torch.uint8, device=dev)
+            for c in (kc, vc):
+                for r0 in range(0, n_kv_l, chunk):
+                    n = min(chunk, n_kv_l - r0)
+                    K.cpy_f32_q8_0(torch.randn((n, kv_dim), generator=gen, device=dev) * scale_vec, c, r0)
+            lcaches.append((K.cache_attn_view(kc, n_kv_l, nh_kv), K.cache_attn_view(vc, n_kv_l, nh_kv), kc, vc))
+        lmask_np = np.full((T, n_kv_l), 0xFC00, np.uint16)
+        for i in range(T):
+            lmask_np[i, :ld + i + 1] = 0
+        lmask = torch.from_numpy(lmask_np.view(np.float16)).to(dev)
+        lmv = K.mask_view(lmask)
+        lws_bytes = K.fattn_workspace_size(qv[0], lcaches[0][0], lcaches[0][1], lmv)
+        lws = torch.empty(max(lws_bytes, 256), dtype=torch.uint8, device=dev)
+        for s in range(n_sets_l):
+            K.flash_attn_ext(qv[0], lcaches[s][0], lcaches[s][1], lmv, scale, ov[0], ws=lws)
+        torch.cuda.synchronize()
+        reps = max(40, args.steps)
+        e0.record(stream)
+        for k in range(reps):
+            s = k % n_sets_l
+            K.flash_attn_ext(qv[0], lcaches[s][0], lcaches[s][1], lmv, scale, ov[0], ws=lws)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        l_us = e0.elapsed_time(e1) * 1e3 / reps
+        l_bytes = n_kv_l * 2 * ROW + 2 * T * nh * hd * 4 + T * n_kv_l * 2
+        long_ctx = {"depth": ld, "T": T, "us_per_launch": round(l_us, 3), "bytes_per_launch": l_bytes,
+                    "GBs": round(l_bytes / (l_us * 1e-6) / 1e9, 1),
+                    "frac": round(l_bytes / (l_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        log(f"[bench] attention op at depth {ld}: {l_us:.2f} us/launch, {long_ctx['GBs']} GB/s")
+        del lcaches, lws
+        torch.cuda.empty_cache()
+
     if args.calib_copy_mb:
         n = args.calib_copy_mb << 20
         a = torch.empty(n, dtype=torch.uint8, device=dev)
@@ -276,6 +319,7 @@ def main() -> int:
                      "kernel": "flash_attn_ext q8_0 (k_fattn_q8_0 + k_fattn_merge)",
                      "us_per_launch": round(attn_us, 3), "bytes_per_launch": attn_bytes},
         "cpu_baseline": cpu,
+        "long_context": long_ctx,
         "parity_max_abs": parity[0] if parity else None,
     }
     print(json.dumps(res), flush=True)
