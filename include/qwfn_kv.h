@@ -132,9 +132,10 @@ int qwfn_kv_gather_segments(const void * src, size_t src_row_stride, int64_t src
  * softmax is online, V is dequantised q*d. A fully masked row gives 0.
  * ws: device workspace of at least qwfn_fattn_workspace_size(q, k, v, mask)
  * bytes, or NULL to use a library-owned buffer (allocated on first use, not
- * graph-capturable). The workspace holds the query operands prepared once per
- * call, an aligned copy of the mask and, when the keys are split, the split
- * partials; its contents need not be preserved between calls. */
+ * graph-capturable). The workspace holds the split partials when the keys
+ * are split across workgroups (at least 256 bytes are asked for otherwise);
+ * its contents need not be preserved between calls. Calls that run at the
+ * same time need distinct workspaces. */
 size_t qwfn_fattn_workspace_size(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
                                  const qwfn_tensor * mask);
 int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
