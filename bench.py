@@ -51,9 +51,182 @@ def parse():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--long-depth", type=int, default=65536,
                     help="also time the attention op alone at this depth (0: skip)")
+    ap.add_argument("--no-rows", action="store_true",
+                    help="skip the per-row measurements (append, gather, restore, batch decode, prefill)")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="also run one device copy of this many MiB (counter calibration)")
     return ap.parse_args()
+
+
+def timed(torch, fn, reps: int) -> float:
+    """Average µs per call of fn(k) over reps back-to-back calls on the current stream."""
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    fn(0)                                        # warm-up
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for k in range(reps):
+        fn(k)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps
+
+
+def timed_graph(torch, fn, per_graph: int, reps: int) -> float:
+    """Average µs per call of fn(k) with per_graph calls captured in one HIP graph and the
+    graph replayed reps times: for launches shorter than the host's per-call cost."""
+    stream = torch.cuda.current_stream()
+    fn(0)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            for k in range(per_graph):
+                fn(k)
+    stream.wait_stream(side)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * per_graph)
+
+
+def measure_rows(K, torch, np, dev, gen) -> dict:
+    """The other rows of the path on their own workloads: append of a 512-row prefill chunk,
+    the per-KV-head sparse gather at 64K, snapshot restore into 4 slots, batch-4 ragged decode
+    and a 512-query causal prefill chunk. Synthetic seeded inputs; each timed back to back
+    with HIP events after a warm-up."""
+    rows = {}
+    kv_dim, nh, nh_kv, hd = 512, 16, 2, 256
+    gbs = lambda b, us: round(b / (us * 1e-6) / 1e9, 1)
+
+    # ---- append: cpy of a 512-row F32 chunk into the q8_0 cache (K and V: 2 launches) ----
+    n_ctx, d0, T = 16384 + 512, 16384, 512
+    caches = [torch.zeros((n_ctx, ROW), dtype=torch.uint8, device=dev) for _ in range(8)]
+    srcs = [torch.randn((T, kv_dim), generator=gen, device=dev) for _ in range(8)]
+    us = timed_graph(torch, lambda k: K.cpy_f32_q8_0(srcs[k % 8], caches[(k * 3) % 8], d0), 64, 10)
+    b = T * (kv_dim * 4 + ROW)
+    rows["append_512"] = {"us_per_launch": round(us, 3), "bytes_per_launch": b, "GBs": gbs(b, us),
+                          "frac": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    idx = torch.arange(d0, d0 + 3, dtype=torch.int32, device=dev)
+    us = timed_graph(torch, lambda k: K.set_rows_q8_0(caches[k % 8], srcs[k % 8][:3], idx), 64, 10)
+    rows["append_3_rows"] = {"us_per_launch": round(us, 3), "bytes_per_launch": 3 * (kv_dim * 4 + ROW)}
+    del caches, srcs
+
+    # ---- sparse gather: per KV head, top-128 of 1024 blocks of 64 positions by uniform
+    #      scores plus the last 512 positions, as 272-byte half rows (K and V) ----
+    n_ctx = 65536
+    sets = 4
+    kvs = [(torch.randint(0, 256, (n_ctx, ROW), dtype=torch.uint8, device=dev, generator=gen),
+            torch.randint(0, 256, (n_ctx, ROW), dtype=torch.uint8, device=dev, generator=gen)) for _ in range(sets)]
+    rng = np.random.default_rng(4)
+    lists = []
+    for h in range(nh_kv):
+        sc = rng.random(1024)
+        top = np.argsort(-sc, kind="stable")[:128]
+        pos = np.unique(np.concatenate([(top[:, None] * 64 + np.arange(64)).ravel(), np.arange(n_ctx - 512, n_ctx)]))
+        lists.append(pos)
+    m = max(len(x) for x in lists)
+    idx = torch.from_numpy(np.stack([np.concatenate([x, np.repeat(x[-1:], m - len(x))]) for x in lists])
+                           .astype(np.int32)).to(dev)
+    gk = torch.zeros((nh_kv, m, 272), dtype=torch.uint8, device=dev)
+    gv = torch.zeros((nh_kv, m, 272), dtype=torch.uint8, device=dev)
+
+    def gather(k):
+        kc, vc = kvs[k % sets]
+        K.gather_segments(kc, idx, gk, 0, 272, 272)
+        K.gather_segments(vc, idx, gv, 0, 272, 272)
+    us = timed_graph(torch, gather, 16, 10)
+    moved = sum(len(x) for x in lists) * 272 * 2
+    rows["gather_64k"] = {"us_per_op": round(us, 3), "positions_per_head": [len(x) for x in lists],
+                          "bytes_read": moved, "bytes_written": moved, "GBs": gbs(2 * moved, us),
+                          "frac": round(2 * moved / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    del kvs, gk, gv
+
+    # ---- snapshot restore: 12 layers x 8192 rows of K and V + 36 DeltaNet states
+    #      [32,128,128] f32 into 4 slots, from device memory and from pinned host memory ----
+    n_layers, n_dn, keep, slot_rows = 12, 36, 8192, 73728
+    parts_b = [keep * ROW] * (2 * n_layers) + [32 * 128 * 128 * 4] * n_dn
+    src = [torch.randint(0, 256, (pb,), dtype=torch.uint8, device=dev, generator=gen) for pb in parts_b]
+    kv_dst = [torch.empty((4, slot_rows, ROW), dtype=torch.uint8, device=dev) for _ in range(2 * n_layers)]
+    dn_dst = [torch.empty((4, 32 * 128 * 128 * 4), dtype=torch.uint8, device=dev) for _ in range(n_dn)]
+    dsts = []
+    for sl in range(4):
+        dsts += [kv_dst[i][sl].data_ptr() for i in range(2 * n_layers)] + [dn_dst[i][sl].data_ptr() for i in range(n_dn)]
+    src_ptrs = [x.data_ptr() for x in src]
+    us = timed(torch, lambda k: K.state_restore(src_ptrs, parts_b, dsts, 4, K.SRC_DEVICE), 10)
+    per_slot = sum(parts_b)
+    rows["restore_device"] = {"us_per_op": round(us, 1), "bytes_per_slot": per_slot, "slots": 4,
+                              "bytes_written": 4 * per_slot, "GBs_written": gbs(4 * per_slot, us)}
+    host = [torch.empty((pb,), dtype=torch.uint8, pin_memory=True) for pb in parts_b]
+    for h_, d_ in zip(host, src):
+        h_.copy_(d_.cpu())
+    host_ptrs = [x.data_ptr() for x in host]
+    us = timed(torch, lambda k: K.state_restore(host_ptrs, parts_b, dsts, 4, K.SRC_HOST), 5)
+    rows["restore_pinned_host"] = {"us_per_op": round(us, 1), "bytes_per_slot": per_slot, "slots": 4,
+                                   "host_link_GBs": gbs(per_slot, us)}
+    del src, kv_dst, dn_dst, host
+
+    # ---- batch-4 ragged decode: one query per slot at depths 8192..65536 (mask [n_kv,1,1,4]) ----
+    depths = [8192, 16384, 32768, 65536]
+    n_kv = max(depths)
+    bsets = 2
+    bc = []
+    for _ in range(bsets):
+        kc = torch.randint(0, 256, (4, n_kv, ROW), dtype=torch.uint8, device=dev, generator=gen)
+        vc = torch.randint(0, 256, (4, n_kv, ROW), dtype=torch.uint8, device=dev, generator=gen)
+        for c in (kc, vc):                       # valid fp16 scales: re-quantise a few rows' worth
+            c.view(-1, 34)[:, 0] = 0x20
+            c.view(-1, 34)[:, 1] = 0x14
+        bc.append((kc, vc))
+    mask_np = np.full((4, 1, 1, n_kv), 0xFC00, np.uint16)
+    for s_, dp in enumerate(depths):
+        mask_np[s_, 0, 0, :dp] = 0
+    bmask = torch.from_numpy(mask_np.view(np.float16)).to(dev)
+    bq = torch.randn((4, 1, nh, hd), generator=gen, device=dev)
+    bout = torch.zeros((4, 1, nh, hd), dtype=torch.float32, device=dev)
+    bviews = [(K.cache_attn_view(kc, n_kv, nh_kv, batch=4, batch_stride=n_kv * ROW),
+               K.cache_attn_view(vc, n_kv, nh_kv, batch=4, batch_stride=n_kv * ROW)) for kc, vc in bc]
+    bmv = K.mask_view(bmask)
+    bws = torch.empty(max(256, K.fattn_workspace_size(K.q_view(bq), bviews[0][0], bviews[0][1], bmv)),
+                      dtype=torch.uint8, device=dev)
+    us = timed(torch, lambda k: K.flash_attn_ext(K.q_view(bq), bviews[k % bsets][0], bviews[k % bsets][1], bmv,
+                                                1 / 16, K.out_view(bout), ws=bws), 20)
+    b = sum(depths) * 2 * ROW
+    rows["batch4_decode"] = {"depths": depths, "us_per_launch": round(us, 3), "bytes_per_launch": b,
+                             "GBs": gbs(b, us), "frac": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    del bc, bws
+
+    # ---- prefill chunk: 512 causal queries at depth 16384 through the same op ----
+    d0, T = 16384, 512
+    n_kv = d0 + T
+    kc = torch.randint(0, 256, (n_kv, ROW), dtype=torch.uint8, device=dev, generator=gen)
+    vc = torch.randint(0, 256, (n_kv, ROW), dtype=torch.uint8, device=dev, generator=gen)
+    for c in (kc, vc):
+        c.view(-1, 34)[:, 0] = 0x20
+        c.view(-1, 34)[:, 1] = 0x14
+    pm = np.full((T, n_kv), 0xFC00, np.uint16)
+    for i in range(T):
+        pm[i, :d0 + i + 1] = 0
+    pmask = torch.from_numpy(pm.view(np.float16)).to(dev)
+    pq = torch.randn((1, T, nh, hd), generator=gen, device=dev)
+    pout = torch.zeros((1, T, nh, hd), dtype=torch.float32, device=dev)
+    pk, pv, pmv = K.cache_attn_view(kc, n_kv, nh_kv), K.cache_attn_view(vc, n_kv, nh_kv), K.mask_view(pmask)
+    pws = torch.empty(max(256, K.fattn_workspace_size(K.q_view(pq), pk, pv, pmv)), dtype=torch.uint8, device=dev)
+    us = timed(torch, lambda k: K.flash_attn_ext(K.q_view(pq), pk, pv, pmv, 1 / 16, K.out_view(pout), ws=pws), 3)
+    flops = 4 * nh * hd * (T * d0 + T * (T + 1) // 2)      # causal count, QK^T and PV
+    rows["prefill_512_at_16k"] = {"us_per_launch": round(us, 1), "flops": flops,
+                                  "TFLOPs": round(flops / (us * 1e-6) / 1e12, 2),
+                                  "frac_of_f16_mfma_peak": round(flops / (us * 1e-6) / 2.5e15, 4)}
+    del kc, vc, pws
+    torch.cuda.empty_cache()
+    return rows
 
 
 def main() -> int:
@@ -248,6 +421,11 @@ def main() -> int:
         del lcaches, lws
         torch.cuda.empty_cache()
 
+    rows = None
+    if not args.no_rows:
+        rows = measure_rows(K, torch, np, dev, gen)
+        log(f"[bench] rows: {json.dumps(rows)}")
+
     if args.calib_copy_mb:
         n = args.calib_copy_mb << 20
         a = torch.empty(n, dtype=torch.uint8, device=dev)
@@ -320,6 +498,7 @@ def main() -> int:
                      "us_per_launch": round(attn_us, 3), "bytes_per_launch": attn_bytes},
         "cpu_baseline": cpu,
         "long_context": long_ctx,
+        "rows": rows,
         "parity_max_abs": parity[0] if parity else None,
     }
     print(json.dumps(res), flush=True)

@@ -62,6 +62,7 @@ constexpr int QWIN   = 64;             // bytes of one block's query window
 constexpr int MAX_SPLITS = 1024;       // key splits per (batch, KV head, row group)
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float RESCALE_SLACK = 8.f;   // log2 units the running max may lag the true max
+constexpr int PV_BATCH = 4;            // V blocks whose LDS reads are issued together
 constexpr int MASK_LDS = 8192;         // LDS bytes for a block's mask rows over its whole split
 enum { MASK_NONE = 0, MASK_SPLIT = 1, MASK_CHUNK = 2 };
 
@@ -117,17 +118,17 @@ struct fa_args {
 // it. Every asm below whose result can feed an MFMA operand therefore ends
 // with s_nop 1.
 
-// One V block's A operands for the lane's 4 keys: w[q] holds dims 2m, 2m+1
-// of keys 2q (bytes 0-1) and 2q+1 (bytes 2-3); a0[q] = f16 pair (dim 2m of
-// both keys), a1[q] = f16 pair (dim 2m+1). int8 -> f16 is exact.
-__device__ __forceinline__ void cvt_v_block(const uint32_t w[2], uint32_t a0[2], uint32_t a1[2]) {
+// One V block's A operands for the lane's 4 keys: v[j] holds dims 2m, 2m+1 of
+// key j in its low two bytes (one 2-byte LDS read each); a0[q] = f16 pair
+// (dim 2m of keys 2q, 2q+1), a1[q] = f16 pair (dim 2m+1). int8 -> f16 is exact.
+__device__ __forceinline__ void cvt_v_block(const uint32_t v[4], uint32_t a0[2], uint32_t a1[2]) {
 #define QWFN_SDWA(D, S, DSEL, UNUSED, SSEL) "v_cvt_f16_i16_sdwa " D ", sext(" S ") dst_sel:" DSEL " dst_unused:" UNUSED " src0_sel:" SSEL "\n\t"
-#define QWFN_PAIR(D, S, B0, B1) QWFN_SDWA(D, S, "WORD_0", "UNUSED_PAD", B0) QWFN_SDWA(D, S, "WORD_1", "UNUSED_PRESERVE", B1)
-    asm volatile(QWFN_PAIR("%0", "%4", "BYTE_0", "BYTE_2") QWFN_PAIR("%1", "%5", "BYTE_0", "BYTE_2")
-                 QWFN_PAIR("%2", "%4", "BYTE_1", "BYTE_3") QWFN_PAIR("%3", "%5", "BYTE_1", "BYTE_3")
-                 "s_nop 1"
-                 : "=&v"(a0[0]), "=&v"(a0[1]), "=&v"(a1[0]), "=&v"(a1[1])
-                 : "v"(w[0]), "v"(w[1]));
+#define QWFN_PAIR(D, S0, S1, B) QWFN_SDWA(D, S0, "WORD_0", "UNUSED_PAD", B) QWFN_SDWA(D, S1, "WORD_1", "UNUSED_PRESERVE", B)
+    asm(QWFN_PAIR("%0", "%4", "%5", "BYTE_0") QWFN_PAIR("%1", "%6", "%7", "BYTE_0")
+        QWFN_PAIR("%2", "%4", "%5", "BYTE_1") QWFN_PAIR("%3", "%6", "%7", "BYTE_1")
+        "s_nop 1"
+        : "=&v"(a0[0]), "=&v"(a0[1]), "=&v"(a1[0]), "=&v"(a1[1])
+        : "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]));
 #undef QWFN_PAIR
 #undef QWFN_SDWA
 }
@@ -142,7 +143,7 @@ __device__ __forceinline__ void pdv_hilo(const float p[4], const uint32_t dv[2],
     "v_fma_mixhi_f16 " H ", " P1 ", " DV ", 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"                     \
     "v_fma_mixlo_f16 " L ", " P0 ", " DV ", -" H " op_sel:[0,0,0] op_sel_hi:[0,1,1]\n\t"                \
     "v_fma_mixhi_f16 " L ", " P1 ", " DV ", -" H " op_sel:[0,1,1] op_sel_hi:[0,1,1]\n\t"
-    asm volatile(QWFN_HILO("%0", "%2", "%4", "%5", "%8") QWFN_HILO("%1", "%3", "%6", "%7", "%9")
+    asm(QWFN_HILO("%0", "%2", "%4", "%5", "%8") QWFN_HILO("%1", "%3", "%6", "%7", "%9")
                  "s_nop 1"
                  : "=&v"(bh[0]), "=&v"(bh[1]), "=&v"(bl[0]), "=&v"(bl[1])
                  : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]), "v"(dv[0]), "v"(dv[1]));
@@ -560,32 +561,34 @@ __global__ __launch_bounds__(WAVES * 64) void k_fattn_q8_0(fa_args a) {
         //      lane's 4 keys (4g..4g+3 of the wave's 16), one naturally aligned
         //      2-byte LDS read per key ----
         const uint8_t * vrow = cur + CHUNK + (kg * KW + lg * 4) * SEG + 2 + 2 * ln;
+        // four blocks at a time: all their LDS reads first (one 2-byte read per
+        // key and block, each in its own register), so their latencies overlap
 #pragma unroll
-        for (int bb = 0; bb < NBLK; bb++) {
-            // keys 2q and 2q+1 share a register: dims 2m, 2m+1 of key 2q in bytes 0-1,
-            // of key 2q+1 in bytes 2-3
-            uint32_t w[2];
+        for (int b0 = 0; b0 < NBLK; b0 += PV_BATCH) {
+            uint32_t w[PV_BATCH][4];
+            uint2 dv2[PV_BATCH];
 #pragma unroll
-            for (int q2 = 0; q2 < 2; q2++) {
-                const uint8_t * r0p = vrow + (2 * q2) * SEG + bb * QBLOCK;
-                us2 tv;
-                tv.x = *(const uint16_t *) r0p;
-                tv.y = *(const uint16_t *) (r0p + SEG);
-                w[q2] = __builtin_bit_cast(uint32_t, tv);
+            for (int u = 0; u < PV_BATCH; u++) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) w[u][j] = *(const uint16_t *) (vrow + j * SEG + (b0 + u) * QBLOCK);
+                dv2[u] = *(const uint2 *) &sw[1][b0 + u][lg * 4];
             }
-            const uint2 dv2 = *(const uint2 *) &sw[1][bb][lg * 4];
-            const uint32_t dv[2] = {dv2.x, dv2.y};
-            uint32_t a0[2], a1[2], bh[2], bl[2];
-            cvt_v_block(w, a0, a1);
-            pdv_hilo(p, dv, bh, bl);
-            const v4h A0 = __builtin_bit_cast(v4h, make_uint2(a0[0], a0[1]));
-            const v4h A1 = __builtin_bit_cast(v4h, make_uint2(a1[0], a1[1]));
-            const v4h Bh = __builtin_bit_cast(v4h, make_uint2(bh[0], bh[1]));
-            const v4h Bl = __builtin_bit_cast(v4h, make_uint2(bl[0], bl[1]));
-            O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x16f16(A0, Bh, O[bb][0], 0, 0, 0);
-            O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A1, Bh, O[bb][1], 0, 0, 0);
-            O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x16f16(A0, Bl, O[bb][0], 0, 0, 0);
-            O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A1, Bl, O[bb][1], 0, 0, 0);
+#pragma unroll
+            for (int u = 0; u < PV_BATCH; u++) {
+                const int bb = b0 + u;
+                const uint32_t dv[2] = {dv2[u].x, dv2[u].y};
+                uint32_t a0[2], a1[2], bh[2], bl[2];
+                cvt_v_block(w[u], a0, a1);
+                pdv_hilo(p, dv, bh, bl);
+                const v4h A0 = __builtin_bit_cast(v4h, make_uint2(a0[0], a0[1]));
+                const v4h A1 = __builtin_bit_cast(v4h, make_uint2(a1[0], a1[1]));
+                const v4h Bh = __builtin_bit_cast(v4h, make_uint2(bh[0], bh[1]));
+                const v4h Bl = __builtin_bit_cast(v4h, make_uint2(bl[0], bl[1]));
+                O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x16f16(A0, Bh, O[bb][0], 0, 0, 0);
+                O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A1, Bh, O[bb][1], 0, 0, 0);
+                O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x16f16(A0, Bl, O[bb][0], 0, 0, 0);
+                O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A1, Bl, O[bb][1], 0, 0, 0);
+            }
         }
     };
     if constexpr (NS == 3) {
