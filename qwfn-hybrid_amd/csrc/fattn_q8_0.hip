@@ -64,7 +64,7 @@ constexpr float LOG2E = 1.4426950408889634f;
 constexpr float RESCALE_SLACK = 8.f;   // log2 units the running max may lag the true max
 constexpr int PV_BATCH = 4;            // V blocks whose LDS reads are issued together
 constexpr int MASK_LDS = 8192;         // LDS bytes for a block's mask rows over its whole split
-enum { MASK_NONE = 0, MASK_SPLIT = 1, MASK_CHUNK = 2 };
+enum { MASK_NONE = 0, MASK_SPLIT = 1, MASK_TILE = 2 };
 
 // Chunk geometry for RT query tiles per block.
 template <int RT>
@@ -74,8 +74,14 @@ struct fa_cfg {
     static constexpr int CK    = KG * KW;                   // keys per chunk (64 or 128)
     static constexpr int CHUNK = CK * SEG;                  // one tensor's rows of a chunk
     static constexpr int DMA_T = CHUNK / 1024;              // wave-wide 16-byte DMAs per tensor
-    static constexpr int STAGE = 2 * CHUNK;                 // one ring stage: K rows, V rows
-    static constexpr int SLOTS = 2 * DMA_T;                 // DMAs per chunk
+    // MASK_TILE: a chunk's mask rows travel with it as 16-byte granules from
+    // the 16-byte aligned address at or below each row's first key
+    static constexpr int MGR   = 2 * CK / 16 + 1;           // granules per mask row
+    static constexpr int MROWS = ROWS;                      // mask rows of a block, at most
+    static constexpr int MDMA  = (MROWS * MGR + 63) / 64;   // wave-wide DMAs for them
+    static constexpr int MTILE = MDMA * 1024;               // their bytes in a stage
+    static constexpr int STAGE = 2 * CHUNK + MTILE;         // one ring stage: K rows, V rows, mask tile
+    static constexpr int SLOTS = 2 * DMA_T + MDMA;          // DMAs per chunk (the mask ones as needed)
     static constexpr int SPW   = (SLOTS + WAVES - 1) / WAVES;   // DMA slots per wave
     static constexpr int NS    = RT == 2 ? 3 : 2;           // ring stages (chunks in flight + 1)
     static_assert(CHUNK % 1024 == 0, "a chunk is whole wave-wide DMAs");
@@ -97,7 +103,7 @@ struct fa_args {
     const char * mask; size_t m_nb1, m_nb2, m_nb3;   // F16 [n_kv, T, m_ne2, m_ne3] or null
     int32_t m_ne2, m_ne3;
     uint32_t m_slice;      // bytes of one batch slice of the mask (last row's end)
-    int32_t  mask_mode;    // MASK_NONE, MASK_SPLIT (whole split in LDS) or MASK_CHUNK (per chunk)
+    int32_t  mask_mode;    // MASK_NONE, MASK_SPLIT (whole split in LDS) or MASK_TILE (with each chunk)
     float *  dst;          // [D, nh, T, B]
     float *  part_o;       // [B][nh_kv][ns][R][D]
     float2 * part_ml;      // [B][nh_kv][ns][R]: (running max in log2 units, sum)
@@ -213,8 +219,7 @@ __device__ __forceinline__ void wait_vmcnt_n(int n) {
     switch (n) {
         case 4: wait_vmcnt<4>(); break;
         case 5: wait_vmcnt<5>(); break;
-        case 8: wait_vmcnt<8>(); break;
-        case 9: wait_vmcnt<9>(); break;
+        case 6: wait_vmcnt<6>(); break;
         default: wait_vmcnt<0>(); break;
     }
 }
@@ -282,15 +287,22 @@ __global__ __launch_bounds__(WAVES * 64) void k_fattn_q8_0(fa_args a) {
     const int tile = wave % RT;     // query rows 16*tile .. 16*tile+15 of the block
     const int kg = wave / RT;       // keys 16*kg .. 16*kg+15 of every chunk
 
-    // ---- block -> (b, kvh, row group, split) ----
+    // ---- block -> (b, kvh, row group, split). With at least 8 (batch, split)
+    //      units, the KV heads and row groups of one unit go to one XCD
+    //      (blockIdx % 8); with fewer, consecutive blocks spread them ----
     const int id   = blockIdx.x;
-    const int xcd  = id & 7;
-    const int j    = id >> 3;
     const int hgn  = a.nh_kv * a.n_rg;
-    const int hg   = j % hgn;
+    int hg, u;
+    if (a.B * a.ns >= 8) {
+        const int j = id >> 3;
+        hg = j % hgn;
+        u  = (j / hgn) * 8 + (id & 7);
+    } else {
+        hg = id % hgn;
+        u  = id / hgn;
+    }
     const int kvh  = hg / a.n_rg;
     const int rg   = hg - kvh * a.n_rg;
-    const int u    = (j / hgn) * 8 + xcd;
     const int b    = u / a.ns;
     const int split = u - b * a.ns;
     if (b >= a.B) return;
@@ -303,24 +315,59 @@ __global__ __launch_bounds__(WAVES * 64) void k_fattn_q8_0(fa_args a) {
 
     const char * kbase = a.k + (size_t) (b % a.kb) * a.k_nb3 + (size_t) kvh * a.k_nb2;
     const char * vbase = a.v + (size_t) (b % a.vb) * a.v_nb3 + (size_t) kvh * a.v_nb2;
+    // Mask rows of this block: query position t0 + mr for a shared mask, query
+    // row r0 + mr for a per-head one. Byte offset of row mr from the mask's
+    // batch slice (`mslice`, its start rounded down to 16 bytes).
+    const int n_mrows = a.mask_mode == MASK_NONE ? 0 : (a.m_ne2 == 1 ? (r0 + RW - 1) / a.gqa - t0 + 1 : RW);
+    const char * mslice = a.mask + (size_t) (b % a.m_ne3) * a.m_nb3;
+    const char * mslice_al = (const char *) ((uintptr_t) mslice & ~(uintptr_t) 15);
+    auto mrow_off = [&](int mr) -> uint32_t {
+        int t = t0 + mr, hq = 0;
+        if (a.m_ne2 != 1) {
+            const int r = r0 + mr;
+            t = r / a.gqa;
+            hq = (kvh * a.gqa + (r - t * a.gqa)) % a.m_ne2;
+        }
+        return (uint32_t) (mslice - mslice_al) + (uint32_t) ((size_t) t * a.m_nb1 + (size_t) hq * a.m_nb2);
+    };
+    const int n_mdma = a.mask_mode == MASK_TILE ? (n_mrows * C::MGR + 63) / 64 : 0;
+
     // A chunk is SLOTS wave-wide 16-byte DMAs; slot s lands at byte 1024*s of
     // the stage: slots [0, DMA_T) are the K rows (piece p = 64*s + lane is byte
-    // 16*(p % 17) of key p / 17), the next DMA_T the V rows. Wave w issues slots
-    // w, w + 8, ...; only its last slot can be absent. The lane offsets within
-    // a chunk are the same for every chunk.
+    // 16*(p % 17) of key p / 17), the next DMA_T the V rows, then (MASK_TILE)
+    // the mask rows, granule G = 64*m + lane being granule G % MGR of row
+    // G / MGR. Wave w issues slots w, w + 8, ... The lane offsets within a chunk
+    // are the same for every chunk.
     auto slot_off = [&](int slot) -> uint32_t {
-        const int tensor = slot >= DMA_T;
-        const unsigned p = (unsigned) ((slot - tensor * DMA_T) * 64 + lane);
-        const unsigned key = p / 17u, part = p - key * 17u;
-        return key * (unsigned) (tensor ? a.v_nb1 : a.k_nb1) + part * 16u;
+        if (slot < 2 * DMA_T) {
+            const int tensor = slot >= DMA_T;
+            const unsigned p = (unsigned) ((slot - tensor * DMA_T) * 64 + lane);
+            const unsigned key = p / 17u, part = p - key * 17u;
+            return key * (unsigned) (tensor ? a.v_nb1 : a.k_nb1) + part * 16u;
+        }
+        if (slot < SLOTS && n_mdma > 0) {
+            const int g = (slot - 2 * DMA_T) * 64 + lane;
+            const int mr = std::min(g / C::MGR, n_mrows - 1);   // lanes past the rows re-read the last one
+            return (mrow_off(mr) & ~15u) + 16u * (unsigned) (g % C::MGR);
+        }
+        return 0u;
+    };
+    auto slot_live = [&](int slot) -> bool {
+        return slot < 2 * DMA_T || (slot < SLOTS && slot - 2 * DMA_T < n_mdma);
     };
     uint32_t doff[SPW];
 #pragma unroll
     for (int s = 0; s < SPW; s++) doff[s] = slot_off(wave + WAVES * s);
-    // vector-memory operations this wave issues per chunk (DMAs, plus the mask
-    // loads in MASK_CHUNK mode): the count a wait leaves in flight for the
-    // chunk issued after the one it waits for
-    const int ops_per_chunk = (SLOTS - wave + WAVES - 1) / WAVES + (a.mask_mode == MASK_CHUNK ? 4 : 0);
+    // DMAs this wave issues per chunk: the count a wait leaves in flight for
+    // the chunk issued after the one it waits for
+    int ops_per_chunk = 0;
+#pragma unroll
+    for (int s = 0; s < SPW; s++) ops_per_chunk += slot_live(wave + WAVES * s) ? 1 : 0;
+    // the lane's own mask row in a MASK_TILE stage: row start plus the row's
+    // offset from its 16-byte granule
+    const int rl_lane0 = 16 * tile + ln;
+    const int mrow0 = rl_lane0 >= RW ? 0 : (a.m_ne2 == 1 ? (r0 + rl_lane0) / a.gqa - t0 : rl_lane0);
+    const uint32_t mtile_off = n_mdma > 0 ? (uint32_t) (mrow0 * C::MGR * 16) + (mrow_off(mrow0) & 15u) : 0u;
 
     // Chunk c is read through buffer resources based at its first key, sized
     // to the bytes that exist: rows past n_kv arrive as zeros, and those keys
@@ -334,34 +381,26 @@ __global__ __launch_bounds__(WAVES * 64) void k_fattn_q8_0(fa_args a) {
 #pragma unroll
         for (int s = 0; s < SPW; s++) {
             const int slot = wave + WAVES * s;
-            if (s == SPW - 1 && slot >= SLOTS) break;
-            const v4i r = slot < DMA_T ? rk : rv;
-            dma16_buf(r, doff[s], __builtin_amdgcn_readfirstlane(lds_addr(dstb + slot * 1024)));
+            if (slot >= 2 * DMA_T) continue;
+            dma16_buf(slot < DMA_T ? rk : rv, doff[s], __builtin_amdgcn_readfirstlane(lds_addr(dstb + slot * 1024)));
+        }
+        if (n_mdma > 0) {
+            // mask granules: the chunk's first key is 128-byte aligned within a row
+            const v4i rm = make_rsrc(mslice_al + c0 * 2, (uint32_t) (a.m_slice + (uint32_t) (mslice - mslice_al) - c0 * 2));
+#pragma unroll
+            for (int s = 0; s < SPW; s++) {
+                const int slot = wave + WAVES * s;
+                if (slot < 2 * DMA_T || !slot_live(slot)) continue;
+                dma16_buf(rm, doff[s], __builtin_amdgcn_readfirstlane(lds_addr(dstb + slot * 1024)));
+            }
         }
     };
 
-    // Mask values. MASK_SPLIT: the block's mask rows over its whole split are
-    // loaded into LDS once, in the prologue. MASK_CHUNK (rows too many for
-    // that): the lane's 4 keys of a chunk in its own mask row are loaded with
-    // the chunk's DMAs (and waited for with them), one F16 value per register
-    // so nothing consumes them early. Both go through a buffer resource over
-    // the batch's mask slice: keys past n_kv read a neighbouring row's values
-    // or zeros (past the slice), and they are masked anyway.
+    // MASK_SPLIT: the block's mask rows over its whole split are loaded into
+    // LDS once, in the prologue, through a buffer resource over the batch's
+    // mask slice (keys past n_kv read their row's last key).
     const __amdgpu_buffer_rsrc_t mrsrc = __builtin_amdgcn_make_buffer_rsrc(
-        (void *) (a.mask ? a.mask + (size_t) (b % a.m_ne3) * a.m_nb3 : a.q), (short) 0, (int) a.m_slice, 0x00020000);
-    uint32_t mrow_off = 0;
-    if (a.mask) {
-        const int rl_m = 16 * tile + ln;
-        const int r = r0 + std::min(rl_m, RW - 1), t = r / a.gqa;   // padded rows read row RW - 1
-        const int hq = (kvh * a.gqa + (r - t * a.gqa)) % a.m_ne2;
-        mrow_off = (uint32_t) ((size_t) t * a.m_nb1 + (size_t) hq * a.m_nb2);
-    }
-    auto load_mask = [&](int c, uint32_t (&m)[4]) __attribute__((always_inline)) {
-        if (a.mask_mode != MASK_CHUNK) return;
-        const uint32_t off = mrow_off + 2u * (uint32_t) (k_lo + (int64_t) c * CK + kg * KW + lg * 4);
-#pragma unroll
-        for (int i = 0; i < 4; i++) m[i] = __builtin_amdgcn_raw_buffer_load_b16(mrsrc, off + 2u * i, 0, 0);
-    };
+        (void *) (a.mask ? mslice : a.q), (short) 0, (int) a.m_slice, 0x00020000);
 
     // ---- prologue: chunks 0 .. NS-2 in flight while the block requantises
     //      its query rows into the last stage (no DMA writes there before
@@ -369,13 +408,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_fattn_q8_0(fa_args a) {
     // Order: chunk 0, then the block's own loads (query rows, MASK_SPLIT rows;
     // waiting for them waits for chunk 0 as well, the counter being in
     // order), then chunk 1, which stays in flight through the requantisation.
-    uint32_t mreg[NS][4] = {};                                 // MASK_CHUNK values, one set per stage
     issue_chunk(0, ring[0]);
-    load_mask(0, mreg[0]);
-    // MASK_SPLIT rows: query position t0 + mr (shared mask) or query row r0 + mr
-    // (per head); loaded to registers here, stored to LDS once they arrive
+    // MASK_SPLIT rows, loaded to registers here and stored to LDS once they
+    // arrive
     constexpr int MIT = MASK_LDS / 2 / (WAVES * 64);
-    const int n_mval = a.mask_mode == MASK_SPLIT ? ((a.m_ne2 == 1 ? (r0 + RW - 1) / a.gqa - t0 + 1 : RW) * a.split_len) : 0;
+    const int n_mval = a.mask_mode == MASK_SPLIT ? n_mrows * a.split_len : 0;
     uint16_t mpre[MIT];
 #pragma unroll
     for (int it = 0; it < MIT; it++) {
@@ -391,6 +428,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_fattn_q8_0(fa_args a) {
             }
             const uint32_t off = (uint32_t) ((size_t) t * a.m_nb1 + (size_t) hq * a.m_nb2) +
                                  2u * (uint32_t) std::min<int64_t>(k_lo + j, a.n_kv - 1);
+            (void) mr;
             mpre[it] = __builtin_amdgcn_raw_buffer_load_b16(mrsrc, off, 0, 0);
         }
     }
@@ -423,10 +461,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_fattn_q8_0(fa_args a) {
             if (e < n_mval) mlds[e] = mpre[it];
         }
         if constexpr (NS > 2) {
-            if (n_chunks > 1) {
-                issue_chunk(1, ring[1]);
-                load_mask(1, mreg[1]);
-            }
+            if (n_chunks > 1) issue_chunk(1, ring[1]);
         }
         const float fs = a.scale * LOG2E;
 #pragma unroll
@@ -456,8 +491,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_fattn_q8_0(fa_args a) {
     }
 #pragma unroll
     for (int bb = 0; bb < NBLK; bb++) asm volatile("" : "+v"(qw[bb]), "+v"(dq[bb]));   // read before the stage is reused
-    // the lane's row in the MASK_SPLIT rows (padded rows read row 0; never stored)
-    const int mrow = rl_lane >= RW ? 0 : (a.m_ne2 == 1 ? (r0 + rl_lane) / a.gqa - t0 : rl_lane);
+
 
     // ---- online softmax state of the lane's row ----
     v4f   O[NBLK][2];
@@ -469,20 +503,32 @@ __global__ __launch_bounds__(WAVES * 64) void k_fattn_q8_0(fa_args a) {
     uint16_t (*sw)[NBLK][KW] = scl[wave];
 
     // One chunk: `cur` holds chunk c; chunk c+NS-1 goes to `nxt` (chunk c-1's
-    // stage), its MASK_CHUNK values to `mnext`. Called with the ring stages
-    // and mask registers literally (no register copy that would wait for the
-    // loads in flight).
-    auto chunk_step = [&](int c, uint8_t * cur, uint8_t * nxt, const uint32_t (&mcur)[4], uint32_t (&mnext)[4])
-                          __attribute__((always_inline)) {
+    // stage). Called with the ring stages literally so the compiler can tell
+    // them apart.
+    auto chunk_step = [&](int c, uint8_t * cur, uint8_t * nxt) __attribute__((always_inline)) {
         // Wait for chunk c; with three stages chunk c+1 (issued one step
         // earlier) may stay in flight. The barrier publishes every wave's part
         // and tells all of them that `nxt` is no longer read.
         if (NS > 2 && c + 1 < n_chunks) wait_vmcnt_n(ops_per_chunk);
         else wait_vmcnt<0>();
         __syncthreads();
-        if (c + NS - 1 < n_chunks) {
-            issue_chunk(c + NS - 1, nxt);
-            load_mask(c + NS - 1, mnext);
+        if (c + NS - 1 < n_chunks) issue_chunk(c + NS - 1, nxt);
+
+        // A wave whose 16 keys are all past the split, or (MASK_TILE, where
+        // long causal masks come) all masked (-inf) for all its rows, has
+        // nothing to add for this chunk.
+        const int kin = c * CK + kg * KW + lg * 4;               // first of the lane's 4 keys in the split
+        uint32_t mv[4] = {0, 0, 0, 0};
+        if (a.mask_mode == MASK_TILE) {
+            const uint8_t * mp = cur + 2 * CHUNK + mtile_off + 2 * (kg * KW + lg * 4);
+#pragma unroll
+            for (int i = 0; i < 4; i++) mv[i] = *(const uint16_t *) (mp + 2 * i);
+            bool live = false;
+#pragma unroll
+            for (int i = 0; i < 4; i++) live |= kin + i < span && mv[i] != 0xFC00u;
+            if (!__any(live)) return;
+        } else if (c * CK + kg * KW >= span) {
+            return;
         }
         // this wave's keys' block scales, transposed to [block][key]: entry n of
         // a lane is tensor n / 2, key (n % 2) * 8 + lane / 8, block lane % 8
@@ -517,14 +563,12 @@ __global__ __launch_bounds__(WAVES * 64) void k_fattn_q8_0(fa_args a) {
         //      A masked key has x = -inf, so its p is exp2(-inf) = 0 ----
         float p[4];
         {
-            const int kin = c * CK + kg * KW + lg * 4;           // first of the lane's 4 keys in the split
             const bool tail = (c + 1) * CK > span;                // keys past the split in this chunk
             float x[4];
             float mloc = -INFINITY;
-            uint32_t mv[4] = {mcur[0], mcur[1], mcur[2], mcur[3]};
             if (a.mask_mode == MASK_SPLIT) {
-                const uint2 m2 = *(const uint2 *) &mlds[mrow * a.split_len + c * CK + kg * KW + lg * 4];
-                mv[0] = m2.x; mv[1] = m2.x >> 16; mv[2] = m2.y; mv[3] = m2.y >> 16;
+                const uint2 m2 = *(const uint2 *) &mlds[mrow0 * a.split_len + kin];
+                mv[0] = m2.x & 0xffffu; mv[1] = m2.x >> 16; mv[2] = m2.y & 0xffffu; mv[3] = m2.y >> 16;
             }
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -593,14 +637,14 @@ __global__ __launch_bounds__(WAVES * 64) void k_fattn_q8_0(fa_args a) {
     };
     if constexpr (NS == 3) {
         for (int c = 0; c < n_chunks; c += 3) {
-            chunk_step(c, ring[0], ring[2], mreg[0], mreg[2]);
-            if (c + 1 < n_chunks) chunk_step(c + 1, ring[1], ring[0], mreg[1], mreg[0]);
-            if (c + 2 < n_chunks) chunk_step(c + 2, ring[2], ring[1], mreg[2], mreg[1]);
+            chunk_step(c, ring[0], ring[2]);
+            if (c + 1 < n_chunks) chunk_step(c + 1, ring[1], ring[0]);
+            if (c + 2 < n_chunks) chunk_step(c + 2, ring[2], ring[1]);
         }
     } else {
         for (int c = 0; c < n_chunks; c += 2) {
-            chunk_step(c, ring[0], ring[1], mreg[0], mreg[1]);
-            if (c + 1 < n_chunks) chunk_step(c + 1, ring[1], ring[0], mreg[1], mreg[0]);
+            chunk_step(c, ring[0], ring[1]);
+            if (c + 1 < n_chunks) chunk_step(c + 1, ring[1], ring[0]);
         }
     }
     __syncthreads();   // every wave is done with the last chunk: stage 0 becomes the merge buffer
@@ -945,8 +989,8 @@ extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor
         a.m_ne2 = (int32_t) mask->ne[2]; a.m_ne3 = (int32_t) mask->ne[3];
         a.m_slice = (uint32_t) mask_slice_bytes(*mask);
         const int64_t mrows = mask->ne[2] == 1 ? ((int64_t) pl.rw + pl.gqa - 1) / pl.gqa + 1 : pl.rw;
-        a.mask_mode = mrows * pl.split_len * 2 <= MASK_LDS ? MASK_SPLIT : MASK_CHUNK;
-        if (const int force = env_int("QWFN_FA_MASK_CHUNK", 0)) a.mask_mode = MASK_CHUNK;
+        a.mask_mode = mrows * pl.split_len * 2 <= MASK_LDS ? MASK_SPLIT : MASK_TILE;
+        if (const int force = env_int("QWFN_FA_MASK_TILE", 0)) a.mask_mode = MASK_TILE;
     } else {
         a.mask = nullptr; a.m_ne2 = 1; a.m_ne3 = 1; a.m_slice = 0; a.mask_mode = MASK_NONE;
     }
@@ -959,7 +1003,7 @@ extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor
     a.scale = scale; a.x86 = variant == QWFN_Q8_X86;
     a.dst_vec = is_aligned(dst->data, 16) ? 1 : 0;
 
-    const int64_t units = ((int64_t) a.B * a.ns + 7) / 8 * 8;
+    const int64_t units = (int64_t) a.B * a.ns >= 8 ? ((int64_t) a.B * a.ns + 7) / 8 * 8 : (int64_t) a.B * a.ns;
     const int64_t grid = units * a.nh_kv * a.n_rg;
     if (grid > 0x7fffffff) return set_error(QWFN_EINVAL, "flash_attn_ext: grid too large");
     hipStream_t st = as_stream(stream);
