@@ -66,8 +66,9 @@ constexpr int PV_BATCH = 4;            // V blocks whose LDS reads are issued to
 constexpr int MASK_LDS = 8192;         // LDS bytes for a block's mask rows over its whole split
 enum { MASK_NONE = 0, MASK_SPLIT = 1, MASK_TILE = 2 };
 
-// Chunk geometry for RT query tiles per block.
-template <int RT>
+// Chunk geometry for RT query tiles per block; MT: the mask travels with
+// each chunk (MASK_TILE).
+template <int RT, bool MT>
 struct fa_cfg {
     static constexpr int ROWS  = 16 * RT;                   // query rows per block
     static constexpr int KG    = WAVES / RT;                // key groups
@@ -78,7 +79,7 @@ struct fa_cfg {
     // the 16-byte aligned address at or below each row's first key
     static constexpr int MGR   = 2 * CK / 16 + 1;           // granules per mask row
     static constexpr int MROWS = ROWS;                      // mask rows of a block, at most
-    static constexpr int MDMA  = (MROWS * MGR + 63) / 64;   // wave-wide DMAs for them
+    static constexpr int MDMA  = MT ? (MROWS * MGR + 63) / 64 : 0;   // wave-wide DMAs for them
     static constexpr int MTILE = MDMA * 1024;               // their bytes in a stage
     static constexpr int STAGE = 2 * CHUNK + MTILE;         // one ring stage: K rows, V rows, mask tile
     static constexpr int SLOTS = 2 * DMA_T + MDMA;          // DMAs per chunk (the mask ones as needed)
@@ -266,9 +267,9 @@ __global__ void k_zero_f32(float * f, int64_t n) {
     for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) f[i] = 0.f;
 }
 
-template <int RT>
+template <int RT, bool MT>
 __global__ __launch_bounds__(WAVES * 64) void k_fattn_q8_0(fa_args a) {
-    using C = fa_cfg<RT>;
+    using C = fa_cfg<RT, MT>;
     constexpr int ROWS = C::ROWS, KG = C::KG, CK = C::CK, CHUNK = C::CHUNK, DMA_T = C::DMA_T;
     constexpr int SLOTS = C::SLOTS, SPW = C::SPW, NS = C::NS;
     // NS ring stages, each K rows [CK][272] and V rows [CK][272]
@@ -330,7 +331,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_fattn_q8_0(fa_args a) {
         }
         return (uint32_t) (mslice - mslice_al) + (uint32_t) ((size_t) t * a.m_nb1 + (size_t) hq * a.m_nb2);
     };
-    const int n_mdma = a.mask_mode == MASK_TILE ? (n_mrows * C::MGR + 63) / 64 : 0;
+    const int n_mdma = MT ? (n_mrows * C::MGR + 63) / 64 : 0;
 
     // A chunk is SLOTS wave-wide 16-byte DMAs; slot s lands at byte 1024*s of
     // the stage: slots [0, DMA_T) are the K rows (piece p = 64*s + lane is byte
@@ -345,7 +346,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_fattn_q8_0(fa_args a) {
             const unsigned key = p / 17u, part = p - key * 17u;
             return key * (unsigned) (tensor ? a.v_nb1 : a.k_nb1) + part * 16u;
         }
-        if (slot < SLOTS && n_mdma > 0) {
+        if (MT && slot < SLOTS) {
             const int g = (slot - 2 * DMA_T) * 64 + lane;
             const int mr = std::min(g / C::MGR, n_mrows - 1);   // lanes past the rows re-read the last one
             return (mrow_off(mr) & ~15u) + 16u * (unsigned) (g % C::MGR);
@@ -353,7 +354,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_fattn_q8_0(fa_args a) {
         return 0u;
     };
     auto slot_live = [&](int slot) -> bool {
-        return slot < 2 * DMA_T || (slot < SLOTS && slot - 2 * DMA_T < n_mdma);
+        return slot < 2 * DMA_T || (MT && slot < SLOTS && slot - 2 * DMA_T < n_mdma);
     };
     uint32_t doff[SPW];
 #pragma unroll
@@ -367,7 +368,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_fattn_q8_0(fa_args a) {
     // offset from its 16-byte granule
     const int rl_lane0 = 16 * tile + ln;
     const int mrow0 = rl_lane0 >= RW ? 0 : (a.m_ne2 == 1 ? (r0 + rl_lane0) / a.gqa - t0 : rl_lane0);
-    const uint32_t mtile_off = n_mdma > 0 ? (uint32_t) (mrow0 * C::MGR * 16) + (mrow_off(mrow0) & 15u) : 0u;
+    const uint32_t mtile_off = MT ? (uint32_t) (mrow0 * C::MGR * 16) + (mrow_off(mrow0) & 15u) : 0u;
 
     // Chunk c is read through buffer resources based at its first key, sized
     // to the bytes that exist: rows past n_kv arrive as zeros, and those keys
@@ -384,7 +385,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_fattn_q8_0(fa_args a) {
             if (slot >= 2 * DMA_T) continue;
             dma16_buf(slot < DMA_T ? rk : rv, doff[s], __builtin_amdgcn_readfirstlane(lds_addr(dstb + slot * 1024)));
         }
-        if (n_mdma > 0) {
+        if constexpr (MT) {
             // mask granules: the chunk's first key is 128-byte aligned within a row
             const v4i rm = make_rsrc(mslice_al + c0 * 2, (uint32_t) (a.m_slice + (uint32_t) (mslice - mslice_al) - c0 * 2));
 #pragma unroll
@@ -519,7 +520,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_fattn_q8_0(fa_args a) {
         // nothing to add for this chunk.
         const int kin = c * CK + kg * KW + lg * 4;               // first of the lane's 4 keys in the split
         uint32_t mv[4] = {0, 0, 0, 0};
-        if (a.mask_mode == MASK_TILE) {
+        if constexpr (MT) {
             const uint8_t * mp = cur + 2 * CHUNK + mtile_off + 2 * (kg * KW + lg * 4);
 #pragma unroll
             for (int i = 0; i < 4; i++) mv[i] = *(const uint16_t *) (mp + 2 * i);
@@ -843,7 +844,8 @@ size_t mask_slice_bytes(const qwfn_tensor & m) {
 // kernel that spills to scratch would break that count: refuse to run one.
 int check_no_scratch() {
     static const int rc = [] {
-        for (const void * f : {(const void *) k_fattn_q8_0<1>, (const void *) k_fattn_q8_0<2>}) {
+        for (const void * f : {(const void *) k_fattn_q8_0<1, false>, (const void *) k_fattn_q8_0<2, false>,
+                               (const void *) k_fattn_q8_0<1, true>, (const void *) k_fattn_q8_0<2, true>}) {
             hipFuncAttributes at{};
             if (int e = hip_check(hipFuncGetAttributes(&at, f), "hipFuncGetAttributes")) return e;
             if (at.localSizeBytes != 0)
@@ -906,7 +908,7 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
     pl->RT = rw / 16;
     pl->n_rg = (int32_t) ((R + rw - 1) / rw);
     pl->gqa = (int32_t) gqa;
-    const int64_t ck = pl->RT == 1 ? fa_cfg<1>::CK : fa_cfg<2>::CK;
+    const int64_t ck = pl->RT == 1 ? fa_cfg<1, false>::CK : fa_cfg<2, false>::CK;
     const int64_t B = q->ne[3];
     // Splits: about one block per CU (256), each at least one chunk.
     const int64_t target_blocks = env_int("QWFN_FA_BLOCKS", 256);
@@ -1007,8 +1009,14 @@ extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor
     const int64_t grid = units * a.nh_kv * a.n_rg;
     if (grid > 0x7fffffff) return set_error(QWFN_EINVAL, "flash_attn_ext: grid too large");
     hipStream_t st = as_stream(stream);
-    if (pl.RT == 1) hipLaunchKernelGGL(k_fattn_q8_0<1>, dim3((unsigned) grid), dim3(WAVES * 64), 0, st, a);
-    else            hipLaunchKernelGGL(k_fattn_q8_0<2>, dim3((unsigned) grid), dim3(WAVES * 64), 0, st, a);
+    const bool mt = a.mask_mode == MASK_TILE;
+    if (pl.RT == 1) {
+        if (mt) hipLaunchKernelGGL((k_fattn_q8_0<1, true>), dim3((unsigned) grid), dim3(WAVES * 64), 0, st, a);
+        else    hipLaunchKernelGGL((k_fattn_q8_0<1, false>), dim3((unsigned) grid), dim3(WAVES * 64), 0, st, a);
+    } else {
+        if (mt) hipLaunchKernelGGL((k_fattn_q8_0<2, true>), dim3((unsigned) grid), dim3(WAVES * 64), 0, st, a);
+        else    hipLaunchKernelGGL((k_fattn_q8_0<2, false>), dim3((unsigned) grid), dim3(WAVES * 64), 0, st, a);
+    }
     if (int rc = hip_check(hipGetLastError(), "flash_attn launch")) return rc;
     if (a.ns > 1) {
         const int64_t blocks = (int64_t) a.B * a.nh_kv * a.R * 4;
