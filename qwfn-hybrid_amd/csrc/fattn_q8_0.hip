@@ -411,26 +411,26 @@ __global__ __launch_bounds__(WAVES * 64) void k_fattn_q8_0(fa_args a) {
     // order), then chunk 1, which stays in flight through the requantisation.
     issue_chunk(0, ring[0]);
     // MASK_SPLIT rows, loaded to registers here and stored to LDS once they
-    // arrive
+    // arrive: value e = tid + 512*it is key e % split_len of row e / split_len,
+    // stepped without a division
     constexpr int MIT = MASK_LDS / 2 / (WAVES * 64);
     const int n_mval = a.mask_mode == MASK_SPLIT ? n_mrows * a.split_len : 0;
     uint16_t mpre[MIT];
+    {
+        int mr = 0, j = (int) threadIdx.x;
+        if (n_mval > 0)
+            while (j >= a.split_len) { j -= a.split_len; mr++; }
 #pragma unroll
-    for (int it = 0; it < MIT; it++) {
-        const int e = (int) threadIdx.x + it * WAVES * 64;
-        mpre[it] = 0;
-        if (e < n_mval) {
-            const int mr = e / a.split_len, j = e - mr * a.split_len;
-            int t = t0 + mr, hq = 0;
-            if (a.m_ne2 != 1) {
-                const int r = r0 + mr;
-                t = r / a.gqa;
-                hq = (kvh * a.gqa + (r - t * a.gqa)) % a.m_ne2;
+        for (int it = 0; it < MIT; it++) {
+            mpre[it] = 0;
+            if (mr < n_mrows && n_mval > 0) {
+                const uint32_t roff = mrow_off(mr) - (uint32_t) (mslice - mslice_al);
+                mpre[it] = __builtin_amdgcn_raw_buffer_load_b16(
+                    mrsrc, roff + 2u * (uint32_t) std::min<int64_t>(k_lo + j, a.n_kv - 1), 0, 0);
             }
-            const uint32_t off = (uint32_t) ((size_t) t * a.m_nb1 + (size_t) hq * a.m_nb2) +
-                                 2u * (uint32_t) std::min<int64_t>(k_lo + j, a.n_kv - 1);
-            (void) mr;
-            mpre[it] = __builtin_amdgcn_raw_buffer_load_b16(mrsrc, off, 0, 0);
+            j += WAVES * 64;
+            if (n_mval > 0)
+                while (j >= a.split_len) { j -= a.split_len; mr++; }
         }
     }
     uint8_t * qwin = ring[NS - 1];                                  // [ROWS][NBLK][QWIN] windows
@@ -469,12 +469,13 @@ __global__ __launch_bounds__(WAVES * 64) void k_fattn_q8_0(fa_args a) {
         for (int it = 0; it < QIT; it++) {
             const int e = (int) threadIdx.x + it * WAVES * 64;
             const int unit = e >> 3, sub = e & 7;
-            const int rl = unit / NBLK, blk = unit % NBLK;
+            const int rl = unit / NBLK, blk = unit % NBLK;   // one row per wave and iteration
+            if (rl >= RW) continue;                          // padding rows stay zero
             const float x[4] = {v4[it].x, v4[it].y, v4[it].z, v4[it].w};
-            const float z[4] = {0.f, 0.f, 0.f, 0.f};
             uint16_t d16;
             float dq;
-            const uint32_t w = dev::q8_quantize_lane4(rl < RW ? x : z, a.x86 != 0, &d16, &dq);
+            const uint32_t w = a.x86 ? dev::q8_quantize_lane4(x, true, &d16, &dq)
+                                     : dev::q8_quantize_lane4(x, false, &d16, &dq);
             uint16_t * wp = (uint16_t *) (qwin + (rl * NBLK + blk) * QWIN + win_off(blk) + 4 * sub);
             wp[0] = (uint16_t) w;
             wp[1] = (uint16_t) (w >> 16);
