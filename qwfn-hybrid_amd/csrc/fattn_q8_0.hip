@@ -57,7 +57,8 @@ constexpr int D      = 256;            // head size (values per head row)
 constexpr int NBLK   = D / QK;         // 8 q8_0 blocks per head row
 constexpr int SEG    = NBLK * QBLOCK;  // 272 bytes per head row
 constexpr int KW     = 16;             // keys per wave per chunk (one QK tile, one PV MFMA depth)
-constexpr int WAVES  = 8;              // wavefronts per block (two per SIMD)
+constexpr int WAVES  = 8;              // wavefronts per block, one block per CU (two per SIMD)
+constexpr int WAVES_PAIR = 4;          // wavefronts per block, two blocks per CU
 constexpr int QWIN   = 64;             // bytes of one block's query window
 constexpr int MAX_SPLITS = 1024;       // key splits per (batch, KV head, row group)
 constexpr float LOG2E = 1.4426950408889634f;
@@ -66,12 +67,12 @@ constexpr int PV_BATCH = 4;            // V blocks whose LDS reads are issued to
 constexpr int MASK_LDS = 8192;         // LDS bytes for a block's mask rows over its whole split
 enum { MASK_NONE = 0, MASK_SPLIT = 1, MASK_TILE = 2 };
 
-// Chunk geometry for RT query tiles per block; MT: the mask travels with
-// each chunk (MASK_TILE).
-template <int RT, bool MT>
+// Chunk geometry for RT query tiles per block of NW waves; MT: the mask
+// travels with each chunk (MASK_TILE).
+template <int RT, bool MT, int NW>
 struct fa_cfg {
     static constexpr int ROWS  = 16 * RT;                   // query rows per block
-    static constexpr int KG    = WAVES / RT;                // key groups
+    static constexpr int KG    = NW / RT;                   // key groups
     static constexpr int CK    = KG * KW;                   // keys per chunk (64 or 128)
     static constexpr int CHUNK = CK * SEG;                  // one tensor's rows of a chunk
     static constexpr int DMA_T = CHUNK / 1024;              // wave-wide 16-byte DMAs per tensor
@@ -83,10 +84,10 @@ struct fa_cfg {
     static constexpr int MTILE = MDMA * 1024;               // their bytes in a stage
     static constexpr int STAGE = 2 * CHUNK + MTILE;         // one ring stage: K rows, V rows, mask tile
     static constexpr int SLOTS = 2 * DMA_T + MDMA;          // DMAs per chunk (the mask ones as needed)
-    static constexpr int SPW   = (SLOTS + WAVES - 1) / WAVES;   // DMA slots per wave
+    static constexpr int SPW   = (SLOTS + NW - 1) / NW;     // DMA slots per wave
     static constexpr int NS    = RT == 2 ? 3 : 2;           // ring stages (chunks in flight + 1)
     static_assert(CHUNK % 1024 == 0, "a chunk is whole wave-wide DMAs");
-    static_assert(SPW * WAVES - SLOTS < WAVES, "only a wave's last slot can be absent");
+    static_assert(SPW * NW - SLOTS < NW, "only a wave's last slot can be absent");
 };
 
 // First 16-byte piece of the 64-byte window of block b inside a 272-byte head
@@ -267,9 +268,10 @@ __global__ void k_zero_f32(float * f, int64_t n) {
     for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) f[i] = 0.f;
 }
 
-template <int RT, bool MT>
-__global__ __launch_bounds__(WAVES * 64) void k_fattn_q8_0(fa_args a) {
-    using C = fa_cfg<RT, MT>;
+template <int RT, bool MT, int NW>
+__global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
+    using C = fa_cfg<RT, MT, NW>;
+    constexpr int WAVES = NW;
     constexpr int ROWS = C::ROWS, KG = C::KG, CK = C::CK, CHUNK = C::CHUNK, DMA_T = C::DMA_T;
     constexpr int SLOTS = C::SLOTS, SPW = C::SPW, NS = C::NS;
     // NS ring stages, each K rows [CK][272] and V rows [CK][272]
@@ -824,6 +826,7 @@ __global__ __launch_bounds__(256) void k_fattn_merge(fa_args a) {
 
 struct fa_plan {
     int32_t R, RT, gqa, rw, n_rg, ns, split_len;
+    bool    pair;                     // 16-row blocks of 4 waves, two per CU
     size_t  off_ml;                   // workspace section of the split (max, sum) pairs (bytes)
     size_t  ws_bytes;
 };
@@ -845,8 +848,10 @@ size_t mask_slice_bytes(const qwfn_tensor & m) {
 // kernel that spills to scratch would break that count: refuse to run one.
 int check_no_scratch() {
     static const int rc = [] {
-        for (const void * f : {(const void *) k_fattn_q8_0<1, false>, (const void *) k_fattn_q8_0<2, false>,
-                               (const void *) k_fattn_q8_0<1, true>, (const void *) k_fattn_q8_0<2, true>}) {
+        for (const void * f : {(const void *) k_fattn_q8_0<1, false, WAVES>, (const void *) k_fattn_q8_0<2, false, WAVES>,
+                               (const void *) k_fattn_q8_0<1, true, WAVES>, (const void *) k_fattn_q8_0<2, true, WAVES>,
+                               (const void *) k_fattn_q8_0<1, false, WAVES_PAIR>,
+                               (const void *) k_fattn_q8_0<1, true, WAVES_PAIR>}) {
             hipFuncAttributes at{};
             if (int e = hip_check(hipFuncGetAttributes(&at, f), "hipFuncGetAttributes")) return e;
             if (at.localSizeBytes != 0)
@@ -904,15 +909,21 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
     // Query rows per block: one or two 16-row tiles.
     int rw = R > 16 ? 32 : 16;
     if (const int force = env_int("QWFN_FA_ROWS", 0)) rw = force >= 32 ? 32 : 16;
+    // One 16-row tile: 4-wave blocks, two per CU (their prologues and phases
+    // overlap); two tiles: 8-wave blocks sharing each chunk between the tiles.
+    pl->pair = rw == 16;
+    if (const char * f = std::getenv("QWFN_FA_PAIR"); f && *f) pl->pair = std::atoi(f) != 0;
+    if (pl->pair) rw = 16;
     pl->R = (int32_t) R;
     pl->rw = rw;
     pl->RT = rw / 16;
     pl->n_rg = (int32_t) ((R + rw - 1) / rw);
     pl->gqa = (int32_t) gqa;
-    const int64_t ck = pl->RT == 1 ? fa_cfg<1, false>::CK : fa_cfg<2, false>::CK;
+    const int64_t ck = pl->pair ? fa_cfg<1, false, WAVES_PAIR>::CK
+                     : pl->RT == 1 ? fa_cfg<1, false, WAVES>::CK : fa_cfg<2, false, WAVES>::CK;
     const int64_t B = q->ne[3];
     // Splits: about one block per CU (256), each at least one chunk.
-    const int64_t target_blocks = env_int("QWFN_FA_BLOCKS", 256);
+    const int64_t target_blocks = env_int("QWFN_FA_BLOCKS", pl->pair ? 512 : 256);
     int64_t ns = std::max<int64_t>(1, target_blocks / std::max<int64_t>(1, nh_kv * B * pl->n_rg));
     ns = std::min<int64_t>(ns, std::max<int64_t>(1, (n_kv + ck - 1) / ck));
     if (const int force = env_int("QWFN_FA_SPLITS", 0)) ns = force;
@@ -1011,12 +1022,15 @@ extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor
     if (grid > 0x7fffffff) return set_error(QWFN_EINVAL, "flash_attn_ext: grid too large");
     hipStream_t st = as_stream(stream);
     const bool mt = a.mask_mode == MASK_TILE;
-    if (pl.RT == 1) {
-        if (mt) hipLaunchKernelGGL((k_fattn_q8_0<1, true>), dim3((unsigned) grid), dim3(WAVES * 64), 0, st, a);
-        else    hipLaunchKernelGGL((k_fattn_q8_0<1, false>), dim3((unsigned) grid), dim3(WAVES * 64), 0, st, a);
+    if (pl.pair) {
+        if (mt) hipLaunchKernelGGL((k_fattn_q8_0<1, true, WAVES_PAIR>), dim3((unsigned) grid), dim3(WAVES_PAIR * 64), 0, st, a);
+        else    hipLaunchKernelGGL((k_fattn_q8_0<1, false, WAVES_PAIR>), dim3((unsigned) grid), dim3(WAVES_PAIR * 64), 0, st, a);
+    } else if (pl.RT == 1) {
+        if (mt) hipLaunchKernelGGL((k_fattn_q8_0<1, true, WAVES>), dim3((unsigned) grid), dim3(WAVES * 64), 0, st, a);
+        else    hipLaunchKernelGGL((k_fattn_q8_0<1, false, WAVES>), dim3((unsigned) grid), dim3(WAVES * 64), 0, st, a);
     } else {
-        if (mt) hipLaunchKernelGGL((k_fattn_q8_0<2, true>), dim3((unsigned) grid), dim3(WAVES * 64), 0, st, a);
-        else    hipLaunchKernelGGL((k_fattn_q8_0<2, false>), dim3((unsigned) grid), dim3(WAVES * 64), 0, st, a);
+        if (mt) hipLaunchKernelGGL((k_fattn_q8_0<2, true, WAVES>), dim3((unsigned) grid), dim3(WAVES * 64), 0, st, a);
+        else    hipLaunchKernelGGL((k_fattn_q8_0<2, false, WAVES>), dim3((unsigned) grid), dim3(WAVES * 64), 0, st, a);
     }
     if (int rc = hip_check(hipGetLastError(), "flash_attn launch")) return rc;
     if (a.ns > 1) {
