@@ -51,29 +51,33 @@ namespace {
 typedef int      v4i __attribute__((ext_vector_type(4)));
 typedef float    v4f __attribute__((ext_vector_type(4)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef uint16_t us2 __attribute__((ext_vector_type(2)));
 
 constexpr int D      = 256;            // head size (values per head row)
 constexpr int NBLK   = D / QK;         // 8 q8_0 blocks per head row
 constexpr int SEG    = NBLK * QBLOCK;  // 272 bytes per head row
-constexpr int KW     = 16;             // keys per wave per chunk (one QK tile, one PV MFMA depth)
 constexpr int WAVES  = 8;              // wavefronts per block, one block per CU (two per SIMD)
 constexpr int WAVES_PAIR = 4;          // wavefronts per block, two blocks per CU
 constexpr int QWIN   = 64;             // bytes of one block's query window
 constexpr int MAX_SPLITS = 1024;       // key splits per (batch, KV head, row group)
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float RESCALE_SLACK = 8.f;   // log2 units the running max may lag the true max
-constexpr int PV_BATCH = 4;            // V blocks whose LDS reads are issued together
+constexpr int PV_BATCH = 4;            // 16-key V block tiles whose LDS reads are issued together
 constexpr int MASK_LDS = 8192;         // LDS bytes for a block's mask rows over its whole split
 enum { MASK_NONE = 0, MASK_SPLIT = 1, MASK_TILE = 2 };
 
 // Chunk geometry for RT query tiles per block of NW waves; MT: the mask
 // travels with each chunk (MASK_TILE).
-template <int RT, bool MT, int NW>
+template <int RT, bool MT, int NW, int KWV>
 struct fa_cfg {
     static constexpr int ROWS  = 16 * RT;                   // query rows per block
     static constexpr int KG    = NW / RT;                   // key groups
-    static constexpr int CK    = KG * KW;                   // keys per chunk (64 or 128)
+    static constexpr int NKT   = KWV / 16;                  // 16-key tiles per wave
+    static constexpr int CK    = KG * KWV;                  // keys per chunk (64 or 128)
+    // MASK_SPLIT bytes (none with MASK_TILE; half where 32-key waves leave
+    // two blocks per CU no more room)
+    static constexpr int MLDS  = MT ? 16 : KWV == 32 ? MASK_LDS / 2 : MASK_LDS;
     static constexpr int CHUNK = CK * SEG;                  // one tensor's rows of a chunk
     static constexpr int DMA_T = CHUNK / 1024;              // wave-wide 16-byte DMAs per tensor
     // MASK_TILE: a chunk's mask rows travel with it as 16-byte granules from
@@ -85,9 +89,10 @@ struct fa_cfg {
     static constexpr int STAGE = 2 * CHUNK + MTILE;         // one ring stage: K rows, V rows, mask tile
     static constexpr int SLOTS = 2 * DMA_T + MDMA;          // DMAs per chunk (the mask ones as needed)
     static constexpr int SPW   = (SLOTS + NW - 1) / NW;     // DMA slots per wave
-    static constexpr int NS    = RT == 2 ? 3 : 2;           // ring stages (chunks in flight + 1)
+    static constexpr int NS    = RT == 2 && NW == WAVES ? 3 : 2;   // ring stages (chunks in flight + 1)
     static_assert(CHUNK % 1024 == 0, "a chunk is whole wave-wide DMAs");
     static_assert(SPW * NW - SLOTS < NW, "only a wave's last slot can be absent");
+    static_assert(KWV == 16 || KWV == 32, "one or two 16-key tiles per wave");
 };
 
 // First 16-byte piece of the 64-byte window of block b inside a 272-byte head
@@ -268,10 +273,12 @@ __global__ void k_zero_f32(float * f, int64_t n) {
     for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) f[i] = 0.f;
 }
 
-template <int RT, bool MT, int NW>
+template <int RT, bool MT, int NW, int KWV>
 __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
-    using C = fa_cfg<RT, MT, NW>;
+    using C = fa_cfg<RT, MT, NW, KWV>;
     constexpr int WAVES = NW;
+    constexpr int KW = KWV;              // keys per wave per chunk
+    constexpr int NKT = C::NKT;
     constexpr int ROWS = C::ROWS, KG = C::KG, CK = C::CK, CHUNK = C::CHUNK, DMA_T = C::DMA_T;
     constexpr int SLOTS = C::SLOTS, SPW = C::SPW, NS = C::NS;
     // NS ring stages, each K rows [CK][272] and V rows [CK][272]
@@ -279,7 +286,7 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
     // per-wave scale tables of the current chunk: [K|V][block][key of the wave] fp16
     __shared__ __attribute__((aligned(16))) uint16_t scl[WAVES][2][NBLK][KW];
     // the block's mask rows over its whole split (MASK_SPLIT mode): [row][split_len] F16
-    __shared__ __attribute__((aligned(16))) uint16_t mlds[MASK_LDS / 2];
+    __shared__ __attribute__((aligned(16))) uint16_t mlds[C::MLDS / 2];
     static_assert(ROWS * NBLK * QWIN + ROWS * NBLK * 4 <= C::STAGE, "query image fits in the last stage");
     static_assert(ROWS * (D + 4) * 4 + WAVES * 16 * 8 <= C::STAGE, "merge buffer fits in stage 0");
 
@@ -415,9 +422,9 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
     // MASK_SPLIT rows, loaded to registers here and stored to LDS once they
     // arrive: value e = tid + 512*it is key e % split_len of row e / split_len,
     // stepped without a division
-    constexpr int MIT = MASK_LDS / 2 / (WAVES * 64);
-    const int n_mval = a.mask_mode == MASK_SPLIT ? n_mrows * a.split_len : 0;
-    uint16_t mpre[MIT];
+    constexpr int MIT = C::MLDS / 2 / (WAVES * 64);
+    const int n_mval = !MT && a.mask_mode == MASK_SPLIT ? n_mrows * a.split_len : 0;
+    uint16_t mpre[MIT > 0 ? MIT : 1];
     {
         int mr = 0, j = (int) threadIdx.x;
         if (n_mval > 0)
@@ -518,69 +525,99 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
         __syncthreads();
         if (c + NS - 1 < n_chunks) issue_chunk(c + NS - 1, nxt);
 
-        // A wave whose 16 keys are all past the split, or (MASK_TILE, where
-        // long causal masks come) all masked (-inf) for all its rows, has
-        // nothing to add for this chunk.
-        const int kin = c * CK + kg * KW + lg * 4;               // first of the lane's 4 keys in the split
-        uint32_t mv[4] = {0, 0, 0, 0};
+        // A wave whose keys are all past the split, or (MASK_TILE, where long
+        // causal masks come) all masked (-inf) for all its rows, has nothing
+        // to add for this chunk. The lane's keys are 16*kt + 4*lg + i of the
+        // wave's KW (key tile kt, i = 0..3).
+        const int kin = c * CK + kg * KW + lg * 4;               // the lane's first key of tile 0 in the split
+        uint32_t mv[NKT][4];
+#pragma unroll
+        for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) mv[kt][i] = 0;
         if constexpr (MT) {
             const uint8_t * mp = cur + 2 * CHUNK + mtile_off + 2 * (kg * KW + lg * 4);
 #pragma unroll
-            for (int i = 0; i < 4; i++) mv[i] = *(const uint16_t *) (mp + 2 * i);
+            for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) mv[kt][i] = *(const uint16_t *) (mp + 32 * kt + 2 * i);
             bool live = false;
 #pragma unroll
-            for (int i = 0; i < 4; i++) live |= kin + i < span && mv[i] != 0xFC00u;
+            for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) live |= kin + 16 * kt + i < span && mv[kt][i] != 0xFC00u;
             if (!__any(live)) return;
         } else if (c * CK + kg * KW >= span) {
             return;
         }
         // this wave's keys' block scales, transposed to [block][key]: entry n of
-        // a lane is tensor n / 2, key (n % 2) * 8 + lane / 8, block lane % 8
+        // a lane is tensor n / (2 NKT), key (n % (2 NKT)) * 8 + lane / 8, block lane % 8
         {
+            constexpr int NE = 4 * NKT;
             const uint8_t * src = cur + (kg * KW + (lane >> 3)) * SEG + (lane & 7) * QBLOCK;
             uint16_t * dstw = &sw[0][lane & 7][lane >> 3];
-            uint16_t sv[4];
+            uint16_t sv[NE];
 #pragma unroll
-            for (int n = 0; n < 4; n++) sv[n] = *(const uint16_t *) (src + (n >> 1) * CHUNK + (n & 1) * 8 * SEG);
+            for (int n = 0; n < NE; n++) sv[n] = *(const uint16_t *) (src + (n / (2 * NKT)) * CHUNK + (n % (2 * NKT)) * 8 * SEG);
 #pragma unroll
-            for (int n = 0; n < 4; n++) dstw[(n >> 1) * NBLK * KW + (n & 1) * 8] = sv[n];
+            for (int n = 0; n < NE; n++) dstw[(n / (2 * NKT)) * NBLK * KW + (n % (2 * NKT)) * 8] = sv[n];
         }
         wave_lds_sync();
 
-        // ---- S = Q K^T for the wave's 16 keys (MFMA rows) x 16 query rows ----
-        float s[4] = {0.f, 0.f, 0.f, 0.f};
-        {
-            const uint8_t * krow = cur + (kg * KW + ln) * SEG + 16 * lg;   // A operand: key row ln, slice lg
+        // ---- S = Q K^T for the wave's key tiles (MFMA rows) x 16 query rows ----
+        float s[NKT][4];
 #pragma unroll
-            for (int bb = 0; bb < NBLK; bb++) {
+        for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) s[kt][i] = 0.f;
+#pragma unroll
+        for (int bb = 0; bb < NBLK; bb++) {
+#pragma unroll
+            for (int kt = 0; kt < NKT; kt++) {
+                // A operand: key row 16*kt + ln of the wave, window slice lg
+                const uint8_t * krow = cur + (kg * KW + 16 * kt + ln) * SEG + 16 * lg;
                 const v4i kA = *(const v4i *) (krow + 16 * win_piece(bb));
-                const uint2 dk = *(const uint2 *) &sw[0][bb][lg * 4];   // the lane's 4 keys' fp16 d_k
+                const uint2 dk = *(const uint2 *) &sw[0][bb][16 * kt + lg * 4];   // the lane's 4 keys' fp16 d_k
                 const v4i cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kA, qw[bb], v4i{0, 0, 0, 0}, 0, 0, 0);
-                s[0] = __builtin_fmaf((float) cc[0], mul_f16lo(dq[bb], dk.x), s[0]);
-                s[1] = __builtin_fmaf((float) cc[1], mul_f16hi(dq[bb], dk.x), s[1]);
-                s[2] = __builtin_fmaf((float) cc[2], mul_f16lo(dq[bb], dk.y), s[2]);
-                s[3] = __builtin_fmaf((float) cc[3], mul_f16hi(dq[bb], dk.y), s[3]);
+                if constexpr (NKT == 1) {
+                    s[kt][0] = __builtin_fmaf((float) cc[0], mul_f16lo(dq[bb], dk.x), s[kt][0]);
+                    s[kt][1] = __builtin_fmaf((float) cc[1], mul_f16hi(dq[bb], dk.x), s[kt][1]);
+                    s[kt][2] = __builtin_fmaf((float) cc[2], mul_f16lo(dq[bb], dk.y), s[kt][2]);
+                    s[kt][3] = __builtin_fmaf((float) cc[3], mul_f16hi(dq[bb], dk.y), s[kt][3]);
+                } else {
+                    // (sum * d_q) * d_k: every step depends on the product, so
+                    // no scale product is formed (and held) ahead of it
+                    s[kt][0] = fma_f16lo(dk.x, (float) cc[0] * dq[bb], s[kt][0]);
+                    s[kt][1] = fma_f16hi(dk.x, (float) cc[1] * dq[bb], s[kt][1]);
+                    s[kt][2] = fma_f16lo(dk.y, (float) cc[2] * dq[bb], s[kt][2]);
+                    s[kt][3] = fma_f16hi(dk.y, (float) cc[3] * dq[bb], s[kt][3]);
+                }
             }
         }
 
         // ---- mask, online softmax (base 2; scores are already in log2 units).
         //      A masked key has x = -inf, so its p is exp2(-inf) = 0 ----
-        float p[4];
+        float p[NKT][4];
         {
             const bool tail = (c + 1) * CK > span;                // keys past the split in this chunk
-            float x[4];
+            float x[NKT][4];
             float mloc = -INFINITY;
-            if (a.mask_mode == MASK_SPLIT) {
-                const uint2 m2 = *(const uint2 *) &mlds[mrow0 * a.split_len + kin];
-                mv[0] = m2.x & 0xffffu; mv[1] = m2.x >> 16; mv[2] = m2.y & 0xffffu; mv[3] = m2.y >> 16;
+            if (!MT && a.mask_mode == MASK_SPLIT) {
+#pragma unroll
+                for (int kt = 0; kt < NKT; kt++) {
+                    const uint2 m2 = *(const uint2 *) &mlds[mrow0 * a.split_len + kin + 16 * kt];
+                    mv[kt][0] = m2.x & 0xffffu; mv[kt][1] = m2.x >> 16; mv[kt][2] = m2.y & 0xffffu; mv[kt][3] = m2.y >> 16;
+                }
             }
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                float xi = a.mask_mode != MASK_NONE ? fma_f16lo(mv[i], LOG2E, s[i]) : s[i];
-                if (tail && kin + i >= span) xi = -INFINITY;
-                x[i] = xi;
-                mloc = xmax(mloc, xi);
-            }
+            for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    float xi = a.mask_mode != MASK_NONE ? fma_f16lo(mv[kt][i], LOG2E, s[kt][i]) : s[kt][i];
+                    if (tail && kin + 16 * kt + i >= span) xi = -INFINITY;
+                    x[kt][i] = xi;
+                    mloc = xmax(mloc, xi);
+                }
             mloc = xmax_lanes16_32(mloc);
             // the running max moves only when the chunk's max exceeds it by more
             // than RESCALE_SLACK (or it is still -inf), so p <= 2^RESCALE_SLACK
@@ -593,10 +630,12 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
             const float m_use = m_run == -INFINITY ? 0.f : m_run;   // all keys masked so far
             float lsum = 0.f;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                p[i] = __builtin_amdgcn_exp2f(x[i] - m_use);
-                lsum += p[i];
-            }
+            for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    p[kt][i] = __builtin_amdgcn_exp2f(x[kt][i] - m_use);
+                    lsum += p[kt][i];
+                }
             l_run = l_run * alpha + lsum;
             if (__any(grow)) {
 #pragma unroll
@@ -606,36 +645,56 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
 
         // ---- O += V^T P per V block. Tile e of block bb holds dims 32bb + 2m + e
         //      (m = MFMA row); the A operand of lane (m, g) is dims 2m, 2m+1 of the
-        //      lane's 4 keys (4g..4g+3 of the wave's 16), one naturally aligned
-        //      2-byte LDS read per key ----
+        //      lane's keys (16kt + 4g .. 16kt + 4g + 3), one naturally aligned
+        //      2-byte LDS read per key. With two key tiles the reduction index
+        //      4kt + i of the 16x16x32 MFMA is key 16kt + 4g + i, in the A and the
+        //      B operand alike ----
         const uint8_t * vrow = cur + CHUNK + (kg * KW + lg * 4) * SEG + 2 + 2 * ln;
-        // four blocks at a time: all their LDS reads first (one 2-byte read per
+        // PVB blocks at a time: all their LDS reads first (one 2-byte read per
         // key and block, each in its own register), so their latencies overlap
+        constexpr int PVB = PV_BATCH;
 #pragma unroll
-        for (int b0 = 0; b0 < NBLK; b0 += PV_BATCH) {
-            uint32_t w[PV_BATCH][4];
-            uint2 dv2[PV_BATCH];
+        for (int b0 = 0; b0 < NBLK; b0 += PVB) {
+            uint32_t w[PVB][NKT][4];
+            uint2 dv2[PVB][NKT];
 #pragma unroll
-            for (int u = 0; u < PV_BATCH; u++) {
+            for (int u = 0; u < PVB; u++)
 #pragma unroll
-                for (int j = 0; j < 4; j++) w[u][j] = *(const uint16_t *) (vrow + j * SEG + (b0 + u) * QBLOCK);
-                dv2[u] = *(const uint2 *) &sw[1][b0 + u][lg * 4];
-            }
+                for (int kt = 0; kt < NKT; kt++) {
 #pragma unroll
-            for (int u = 0; u < PV_BATCH; u++) {
+                    for (int j = 0; j < 4; j++)
+                        w[u][kt][j] = *(const uint16_t *) (vrow + (16 * kt + j) * SEG + (b0 + u) * QBLOCK);
+                    dv2[u][kt] = *(const uint2 *) &sw[1][b0 + u][16 * kt + lg * 4];
+                }
+#pragma unroll
+            for (int u = 0; u < PVB; u++) {
                 const int bb = b0 + u;
-                const uint32_t dv[2] = {dv2[u].x, dv2[u].y};
-                uint32_t a0[2], a1[2], bh[2], bl[2];
-                cvt_v_block(w[u], a0, a1);
-                pdv_hilo(p, dv, bh, bl);
-                const v4h A0 = __builtin_bit_cast(v4h, make_uint2(a0[0], a0[1]));
-                const v4h A1 = __builtin_bit_cast(v4h, make_uint2(a1[0], a1[1]));
-                const v4h Bh = __builtin_bit_cast(v4h, make_uint2(bh[0], bh[1]));
-                const v4h Bl = __builtin_bit_cast(v4h, make_uint2(bl[0], bl[1]));
-                O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x16f16(A0, Bh, O[bb][0], 0, 0, 0);
-                O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A1, Bh, O[bb][1], 0, 0, 0);
-                O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x16f16(A0, Bl, O[bb][0], 0, 0, 0);
-                O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A1, Bl, O[bb][1], 0, 0, 0);
+                uint32_t a0[NKT][2], a1[NKT][2], bh[NKT][2], bl[NKT][2];
+#pragma unroll
+                for (int kt = 0; kt < NKT; kt++) {
+                    const uint32_t dv[2] = {dv2[u][kt].x, dv2[u][kt].y};
+                    cvt_v_block(w[u][kt], a0[kt], a1[kt]);
+                    pdv_hilo(p[kt], dv, bh[kt], bl[kt]);
+                }
+                if constexpr (NKT == 1) {
+                    const v4h A0 = __builtin_bit_cast(v4h, make_uint2(a0[0][0], a0[0][1]));
+                    const v4h A1 = __builtin_bit_cast(v4h, make_uint2(a1[0][0], a1[0][1]));
+                    const v4h Bh = __builtin_bit_cast(v4h, make_uint2(bh[0][0], bh[0][1]));
+                    const v4h Bl = __builtin_bit_cast(v4h, make_uint2(bl[0][0], bl[0][1]));
+                    O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x16f16(A0, Bh, O[bb][0], 0, 0, 0);
+                    O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A1, Bh, O[bb][1], 0, 0, 0);
+                    O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x16f16(A0, Bl, O[bb][0], 0, 0, 0);
+                    O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A1, Bl, O[bb][1], 0, 0, 0);
+                } else {
+                    const v8h A0 = __builtin_bit_cast(v8h, make_uint4(a0[0][0], a0[0][1], a0[1][0], a0[1][1]));
+                    const v8h A1 = __builtin_bit_cast(v8h, make_uint4(a1[0][0], a1[0][1], a1[1][0], a1[1][1]));
+                    const v8h Bh = __builtin_bit_cast(v8h, make_uint4(bh[0][0], bh[0][1], bh[1][0], bh[1][1]));
+                    const v8h Bl = __builtin_bit_cast(v8h, make_uint4(bl[0][0], bl[0][1], bl[1][0], bl[1][1]));
+                    O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, Bh, O[bb][0], 0, 0, 0);
+                    O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, Bh, O[bb][1], 0, 0, 0);
+                    O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, Bl, O[bb][0], 0, 0, 0);
+                    O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, Bl, O[bb][1], 0, 0, 0);
+                }
             }
         }
     };
@@ -824,9 +883,17 @@ __global__ __launch_bounds__(256) void k_fattn_merge(fa_args a) {
 
 // ---------------------------------------------------------------- planning
 
+// Attention kernel shapes: waves per block, query tiles, keys per wave.
+enum fa_kind {
+    FA_W8_T1,     // 8 waves, one 16-row tile, 128-key chunks, one block per CU
+    FA_W8_T2,     // 8 waves, two tiles sharing each 64-key chunk, one block per CU
+    FA_P4_T1,     // 4 waves, one tile, 64-key chunks, two blocks per CU
+    FA_P4_T2,     // 4 waves, two tiles, 32 keys per wave, two blocks per CU (no MASK_TILE)
+};
+
 struct fa_plan {
     int32_t R, RT, gqa, rw, n_rg, ns, split_len;
-    bool    pair;                     // 16-row blocks of 4 waves, two per CU
+    fa_kind kind;
     size_t  off_ml;                   // workspace section of the split (max, sum) pairs (bytes)
     size_t  ws_bytes;
 };
@@ -848,10 +915,11 @@ size_t mask_slice_bytes(const qwfn_tensor & m) {
 // kernel that spills to scratch would break that count: refuse to run one.
 int check_no_scratch() {
     static const int rc = [] {
-        for (const void * f : {(const void *) k_fattn_q8_0<1, false, WAVES>, (const void *) k_fattn_q8_0<2, false, WAVES>,
-                               (const void *) k_fattn_q8_0<1, true, WAVES>, (const void *) k_fattn_q8_0<2, true, WAVES>,
-                               (const void *) k_fattn_q8_0<1, false, WAVES_PAIR>,
-                               (const void *) k_fattn_q8_0<1, true, WAVES_PAIR>}) {
+        for (const void * f : {(const void *) k_fattn_q8_0<1, false, WAVES, 16>, (const void *) k_fattn_q8_0<2, false, WAVES, 16>,
+                               (const void *) k_fattn_q8_0<1, true, WAVES, 16>, (const void *) k_fattn_q8_0<2, true, WAVES, 16>,
+                               (const void *) k_fattn_q8_0<1, false, WAVES_PAIR, 16>,
+                               (const void *) k_fattn_q8_0<1, true, WAVES_PAIR, 16>,
+                               (const void *) k_fattn_q8_0<2, false, WAVES_PAIR, 32>}) {
             hipFuncAttributes at{};
             if (int e = hip_check(hipFuncGetAttributes(&at, f), "hipFuncGetAttributes")) return e;
             if (at.localSizeBytes != 0)
@@ -909,21 +977,23 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
     // Query rows per block: one or two 16-row tiles.
     int rw = R > 16 ? 32 : 16;
     if (const int force = env_int("QWFN_FA_ROWS", 0)) rw = force >= 32 ? 32 : 16;
-    // One 16-row tile: 4-wave blocks, two per CU (their prologues and phases
-    // overlap); two tiles: 8-wave blocks sharing each chunk between the tiles.
-    pl->pair = rw == 16;
-    if (const char * f = std::getenv("QWFN_FA_PAIR"); f && *f) pl->pair = std::atoi(f) != 0;
-    if (pl->pair) rw = 16;
+    // 4-wave blocks, two per CU (their prologues and phases overlap), or
+    // 8-wave blocks, one per CU. QWFN_FA_PAIR=0 forces 8 waves, =1 4 waves.
+    const int pair_env = env_int("QWFN_FA_PAIR", -1);
+    const bool pair = pair_env >= 0 ? pair_env != 0 : rw == 16;
+    pl->kind = rw == 16 ? (pair ? FA_P4_T1 : FA_W8_T1) : (pair ? FA_P4_T2 : FA_W8_T2);
     pl->R = (int32_t) R;
     pl->rw = rw;
     pl->RT = rw / 16;
     pl->n_rg = (int32_t) ((R + rw - 1) / rw);
     pl->gqa = (int32_t) gqa;
-    const int64_t ck = pl->pair ? fa_cfg<1, false, WAVES_PAIR>::CK
-                     : pl->RT == 1 ? fa_cfg<1, false, WAVES>::CK : fa_cfg<2, false, WAVES>::CK;
+    const int64_t ck = pl->kind == FA_W8_T1 ? fa_cfg<1, false, WAVES, 16>::CK
+                     : pl->kind == FA_W8_T2 ? fa_cfg<2, false, WAVES, 16>::CK
+                     : pl->kind == FA_P4_T1 ? fa_cfg<1, false, WAVES_PAIR, 16>::CK
+                                            : fa_cfg<2, false, WAVES_PAIR, 32>::CK;
     const int64_t B = q->ne[3];
-    // Splits: about one block per CU (256), each at least one chunk.
-    const int64_t target_blocks = env_int("QWFN_FA_BLOCKS", pl->pair ? 512 : 256);
+    // Splits: about one block per CU slot (256 or 512), each at least one chunk.
+    const int64_t target_blocks = env_int("QWFN_FA_BLOCKS", pair ? 512 : 256);
     int64_t ns = std::max<int64_t>(1, target_blocks / std::max<int64_t>(1, nh_kv * B * pl->n_rg));
     ns = std::min<int64_t>(ns, std::max<int64_t>(1, (n_kv + ck - 1) / ck));
     if (const int force = env_int("QWFN_FA_SPLITS", 0)) ns = force;
@@ -1003,7 +1073,8 @@ extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor
         a.m_ne2 = (int32_t) mask->ne[2]; a.m_ne3 = (int32_t) mask->ne[3];
         a.m_slice = (uint32_t) mask_slice_bytes(*mask);
         const int64_t mrows = mask->ne[2] == 1 ? ((int64_t) pl.rw + pl.gqa - 1) / pl.gqa + 1 : pl.rw;
-        a.mask_mode = mrows * pl.split_len * 2 <= MASK_LDS ? MASK_SPLIT : MASK_TILE;
+        const int64_t mlds = pl.kind == FA_P4_T2 ? fa_cfg<2, false, WAVES_PAIR, 32>::MLDS : MASK_LDS;
+        a.mask_mode = mrows * pl.split_len * 2 <= mlds ? MASK_SPLIT : MASK_TILE;
         if (const int force = env_int("QWFN_FA_MASK_TILE", 0)) a.mask_mode = MASK_TILE;
     } else {
         a.mask = nullptr; a.m_ne2 = 1; a.m_ne3 = 1; a.m_slice = 0; a.mask_mode = MASK_NONE;
@@ -1022,15 +1093,26 @@ extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor
     if (grid > 0x7fffffff) return set_error(QWFN_EINVAL, "flash_attn_ext: grid too large");
     hipStream_t st = as_stream(stream);
     const bool mt = a.mask_mode == MASK_TILE;
-    if (pl.pair) {
-        if (mt) hipLaunchKernelGGL((k_fattn_q8_0<1, true, WAVES_PAIR>), dim3((unsigned) grid), dim3(WAVES_PAIR * 64), 0, st, a);
-        else    hipLaunchKernelGGL((k_fattn_q8_0<1, false, WAVES_PAIR>), dim3((unsigned) grid), dim3(WAVES_PAIR * 64), 0, st, a);
-    } else if (pl.RT == 1) {
-        if (mt) hipLaunchKernelGGL((k_fattn_q8_0<1, true, WAVES>), dim3((unsigned) grid), dim3(WAVES * 64), 0, st, a);
-        else    hipLaunchKernelGGL((k_fattn_q8_0<1, false, WAVES>), dim3((unsigned) grid), dim3(WAVES * 64), 0, st, a);
-    } else {
-        if (mt) hipLaunchKernelGGL((k_fattn_q8_0<2, true, WAVES>), dim3((unsigned) grid), dim3(WAVES * 64), 0, st, a);
-        else    hipLaunchKernelGGL((k_fattn_q8_0<2, false, WAVES>), dim3((unsigned) grid), dim3(WAVES * 64), 0, st, a);
+    const dim3 g((unsigned) grid), b8(WAVES * 64), b4(WAVES_PAIR * 64);
+    switch (pl.kind) {
+        case FA_P4_T1:
+            if (mt) hipLaunchKernelGGL((k_fattn_q8_0<1, true, WAVES_PAIR, 16>), g, b4, 0, st, a);
+            else    hipLaunchKernelGGL((k_fattn_q8_0<1, false, WAVES_PAIR, 16>), g, b4, 0, st, a);
+            break;
+        case FA_P4_T2:
+            // a mask tile in each stage leaves no room for two blocks per CU:
+            // those calls take the 8-wave kernel over the same 64-key chunks
+            if (mt) hipLaunchKernelGGL((k_fattn_q8_0<2, true, WAVES, 16>), g, b8, 0, st, a);
+            else    hipLaunchKernelGGL((k_fattn_q8_0<2, false, WAVES_PAIR, 32>), g, b4, 0, st, a);
+            break;
+        case FA_W8_T1:
+            if (mt) hipLaunchKernelGGL((k_fattn_q8_0<1, true, WAVES, 16>), g, b8, 0, st, a);
+            else    hipLaunchKernelGGL((k_fattn_q8_0<1, false, WAVES, 16>), g, b8, 0, st, a);
+            break;
+        case FA_W8_T2:
+            if (mt) hipLaunchKernelGGL((k_fattn_q8_0<2, true, WAVES, 16>), g, b8, 0, st, a);
+            else    hipLaunchKernelGGL((k_fattn_q8_0<2, false, WAVES, 16>), g, b8, 0, st, a);
+            break;
     }
     if (int rc = hip_check(hipGetLastError(), "flash_attn launch")) return rc;
     if (a.ns > 1) {
