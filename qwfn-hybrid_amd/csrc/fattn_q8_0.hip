@@ -124,7 +124,17 @@ struct fa_args {
     float    scale;
     int32_t  x86;
     int32_t  dst_vec;      // dst is 16-byte aligned: float4 stores
+    uint32_t q_slice;      // bytes of one batch slice of q (last row's end)
+    uint32_t gqa_mul;      // ceil(2^32 / gqa): r / gqa = mulhi(r, gqa_mul) for gqa > 1
+    int32_t  m_gran;       // MASK_SPLIT: 16-byte granules per mask row of a split (split_len / 8 + 1)
+    uint32_t m_gran_mul;   // ceil(2^32 / m_gran)
 };
+
+// r / gqa for the row indices of a call (r * gqa < 2^32, checked by the host):
+// with m = ceil(2^32 / d), floor(r * m / 2^32) = floor(r / d) while r * d < 2^32.
+__device__ __forceinline__ uint32_t div_gqa(const fa_args & a, uint32_t r) {
+    return a.gqa == 1 ? r : __umulhi(r, a.gqa_mul);
+}
 
 // The compiler's hazard recognizer does not see the VALU writes inside inline
 // asm, and an MFMA that reads a VGPR needs two wait states after a VALU wrote
@@ -220,8 +230,22 @@ __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
-// The same for a wave-uniform runtime count (the counts a wave can leave in
-// flight; anything else waits for everything).
+// The same for a wave-uniform runtime count below 32 (a compare chain: for
+// the prologue's one wait).
+template <int N = 0>
+__device__ __forceinline__ void wait_vmcnt_upto(int n) {
+    if constexpr (N < 32) {
+        if (n == N) {
+            wait_vmcnt<N>();
+            return;
+        }
+        wait_vmcnt_upto<N + 1>(n);
+    } else {
+        wait_vmcnt<0>();
+    }
+}
+// The counts a wave can leave in flight in the key loop (anything else waits
+// for everything).
 __device__ __forceinline__ void wait_vmcnt_n(int n) {
     switch (n) {
         case 4: wait_vmcnt<4>(); break;
@@ -321,21 +345,21 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
     const int n_chunks = (int) ((k_hi - k_lo + CK - 1) / CK);
     const int r0 = rg * a.rw;                          // first query row of this block
     const int RW = std::min(a.rw, a.R - r0);          // rows in this block
-    const int t0 = r0 / a.gqa;
+    const int t0 = (int) div_gqa(a, (uint32_t) r0);
 
     const char * kbase = a.k + (size_t) (b % a.kb) * a.k_nb3 + (size_t) kvh * a.k_nb2;
     const char * vbase = a.v + (size_t) (b % a.vb) * a.v_nb3 + (size_t) kvh * a.v_nb2;
     // Mask rows of this block: query position t0 + mr for a shared mask, query
     // row r0 + mr for a per-head one. Byte offset of row mr from the mask's
     // batch slice (`mslice`, its start rounded down to 16 bytes).
-    const int n_mrows = a.mask_mode == MASK_NONE ? 0 : (a.m_ne2 == 1 ? (r0 + RW - 1) / a.gqa - t0 + 1 : RW);
+    const int n_mrows = a.mask_mode == MASK_NONE ? 0 : (a.m_ne2 == 1 ? (int) div_gqa(a, (uint32_t) (r0 + RW - 1)) - t0 + 1 : RW);
     const char * mslice = a.mask + (size_t) (b % a.m_ne3) * a.m_nb3;
     const char * mslice_al = (const char *) ((uintptr_t) mslice & ~(uintptr_t) 15);
     auto mrow_off = [&](int mr) -> uint32_t {
         int t = t0 + mr, hq = 0;
         if (a.m_ne2 != 1) {
             const int r = r0 + mr;
-            t = r / a.gqa;
+            t = (int) div_gqa(a, (uint32_t) r);
             hq = (kvh * a.gqa + (r - t * a.gqa)) % a.m_ne2;
         }
         return (uint32_t) (mslice - mslice_al) + (uint32_t) ((size_t) t * a.m_nb1 + (size_t) hq * a.m_nb2);
@@ -376,7 +400,7 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
     // the lane's own mask row in a MASK_TILE stage: row start plus the row's
     // offset from its 16-byte granule
     const int rl_lane0 = 16 * tile + ln;
-    const int mrow0 = rl_lane0 >= RW ? 0 : (a.m_ne2 == 1 ? (r0 + rl_lane0) / a.gqa - t0 : rl_lane0);
+    const int mrow0 = rl_lane0 >= RW ? 0 : (a.m_ne2 == 1 ? (int) div_gqa(a, (uint32_t) (r0 + rl_lane0)) - t0 : rl_lane0);
     const uint32_t mtile_off = MT ? (uint32_t) (mrow0 * C::MGR * 16) + (mrow_off(mrow0) & 15u) : 0u;
 
     // Chunk c is read through buffer resources based at its first key, sized
@@ -406,89 +430,102 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
         }
     };
 
-    // MASK_SPLIT: the block's mask rows over its whole split are loaded into
-    // LDS once, in the prologue, through a buffer resource over the batch's
-    // mask slice (keys past n_kv read their row's last key).
-    const __amdgpu_buffer_rsrc_t mrsrc = __builtin_amdgcn_make_buffer_rsrc(
-        (void *) (a.mask ? mslice : a.q), (short) 0, (int) a.m_slice, 0x00020000);
-
-    // ---- prologue: chunks 0 .. NS-2 in flight while the block requantises
-    //      its query rows into the last stage (no DMA writes there before
-    //      chunk NS-1 is issued) ----
-    // Order: chunk 0, then the block's own loads (query rows, MASK_SPLIT rows;
-    // waiting for them waits for chunk 0 as well, the counter being in
-    // order), then chunk 1, which stays in flight through the requantisation.
-    issue_chunk(0, ring[0]);
-    // MASK_SPLIT rows, loaded to registers here and stored to LDS once they
-    // arrive: value e = tid + 512*it is key e % split_len of row e / split_len,
-    // stepped without a division
-    constexpr int MIT = C::MLDS / 2 / (WAVES * 64);
-    const int n_mval = !MT && a.mask_mode == MASK_SPLIT ? n_mrows * a.split_len : 0;
-    uint16_t mpre[MIT > 0 ? MIT : 1];
+    // ---- prologue. What the block needs before its key loop travels as LDS
+    //      DMA, in this order: its query rows (f32, into the last ring stage),
+    //      its MASK_SPLIT mask rows, chunk 0 (and chunk 1 with three stages).
+    //      One wait that leaves the chunk DMAs in flight covers the first two
+    //      (the counter is in order), and the block requantises its query rows
+    //      while the chunks arrive ----
+    uint8_t * qstage = ring[NS - 1];    // [ROWS][D] f32 query rows, then the window image below
     {
-        int mr = 0, j = (int) threadIdx.x;
-        if (n_mval > 0)
-            while (j >= a.split_len) { j -= a.split_len; mr++; }
+        // one wave-wide DMA (1 KB) per query row; wave w takes rows w, w + NW, ...
+        const v4i rq = make_rsrc(a.q + (size_t) b * a.q_nb3, a.q_slice);
 #pragma unroll
-        for (int it = 0; it < MIT; it++) {
-            mpre[it] = 0;
-            if (mr < n_mrows && n_mval > 0) {
-                const uint32_t roff = mrow_off(mr) - (uint32_t) (mslice - mslice_al);
-                mpre[it] = __builtin_amdgcn_raw_buffer_load_b16(
-                    mrsrc, roff + 2u * (uint32_t) std::min<int64_t>(k_lo + j, a.n_kv - 1), 0, 0);
-            }
-            j += WAVES * 64;
-            if (n_mval > 0)
-                while (j >= a.split_len) { j -= a.split_len; mr++; }
+        for (int j = 0; j < ROWS / WAVES; j++) {
+            const int rl = wave + WAVES * j;
+            if (rl >= RW) break;
+            const uint32_t r = (uint32_t) (r0 + rl);
+            const uint32_t t = div_gqa(a, r), h = (uint32_t) (kvh * a.gqa) + (r - t * (uint32_t) a.gqa);
+            dma16_buf(rq, t * (uint32_t) a.q_nb1 + h * (uint32_t) a.q_nb2 + 16u * (uint32_t) lane,
+                      __builtin_amdgcn_readfirstlane(lds_addr(qstage + rl * 1024)));
         }
     }
-    uint8_t * qwin = ring[NS - 1];                                  // [ROWS][NBLK][QWIN] windows
-    float * dql = (float *) (ring[NS - 1] + ROWS * NBLK * QWIN);    // [ROWS][NBLK] d_q * scale * log2(e)
-    for (int e = threadIdx.x; e < ROWS * NBLK * QWIN / 16; e += WAVES * 64) ((uint4 *) qwin)[e] = make_uint4(0, 0, 0, 0);
-    __syncthreads();
+    // MASK_SPLIT: mask row mr of the split lands at byte mr * mstride of mlds as
+    // the 16-byte granules from the aligned address at or below its first key,
+    // which sits `mis` bytes into the LDS row. Granule g = 64m + lane is granule
+    // g % m_gran of row g / m_gran; lanes past the last granule re-read it, so
+    // every LDS byte a DMA writes lies inside mlds.
+    const bool msplit = !MT && a.mask_mode == MASK_SPLIT;
+    const uint32_t mstride = 16u * (uint32_t) a.m_gran;
+    uint32_t mlds_row = 0;                              // byte of the lane's first mask key of the split in mlds
+    if (msplit) {
+        const int n_g = n_mrows * a.m_gran;
+        const v4i rm = make_rsrc(mslice_al, a.m_slice + (uint32_t) (mslice - mslice_al));
+        for (int m = wave; m * 64 < n_g; m += WAVES) {
+            const uint32_t g = (uint32_t) std::min(m * 64 + lane, n_g - 1);
+            const uint32_t row = __umulhi(g, a.m_gran_mul);
+            const uint32_t k = g - row * (uint32_t) a.m_gran;
+            const uint32_t src = ((mrow_off((int) row) + 2u * (uint32_t) k_lo) & ~15u) + 16u * k;
+            dma16_buf(rm, src, __builtin_amdgcn_readfirstlane(lds_addr((uint8_t *) mlds + m * 1024)));
+        }
+        mlds_row = (uint32_t) mrow0 * mstride + ((mrow_off(mrow0) + 2u * (uint32_t) k_lo) & 15u);
+    }
+    issue_chunk(0, ring[0]);
+    int chunk_ops = ops_per_chunk;
+    if constexpr (NS > 2) {
+        if (n_chunks > 1) {
+            issue_chunk(1, ring[1]);
+            chunk_ops += ops_per_chunk;
+        }
+    }
+    wait_vmcnt_upto(chunk_ops);   // this wave's query and mask DMAs have landed
+    __syncthreads();              // ... and every wave's
+
+    // Requantisation: QL lanes per (row, block), QV values each; wave w takes
+    // blocks w, w + NW, ... for all rows (QL * ROWS = 64 lanes).
+    constexpr int QL = 64 / ROWS, QV = 32 / QL, QIT = NBLK / WAVES;
+    static_assert(QL * ROWS == 64 && NBLK % WAVES == 0, "one block of all rows per wave and iteration");
+    const int qrl = lane / QL, qh = lane % QL;
+    float qx[QIT][QV];
+#pragma unroll
+    for (int it = 0; it < QIT; it++) {
+        const float4 * src = (const float4 *) (qstage + qrl * 1024 + (QK * (wave + WAVES * it) + QV * qh) * 4);
+#pragma unroll
+        for (int m = 0; m < QV / 4; m++) {
+            const float4 v = qrl < RW ? src[m] : make_float4(0.f, 0.f, 0.f, 0.f);
+            qx[it][4 * m] = v.x; qx[it][4 * m + 1] = v.y; qx[it][4 * m + 2] = v.z; qx[it][4 * m + 3] = v.w;
+        }
+    }
+    __syncthreads();   // every query value is in registers: the stage becomes the window image
+
+    uint8_t * qwin = qstage;                                        // [ROWS][NBLK][QWIN] windows
+    float * dql = (float *) (qstage + ROWS * NBLK * QWIN);          // [ROWS][NBLK] d_q * scale * log2(e)
     {
-        // 8 lanes per (row, block), 4 values each; every load of the thread is
-        // in flight before the first is used
-        constexpr int QIT = ROWS * NBLK * 8 / (WAVES * 64);
-        static_assert(ROWS * NBLK * 8 % (WAVES * 64) == 0, "whole query iterations");
-        float4 v4[QIT];
-#pragma unroll
-        for (int it = 0; it < QIT; it++) {
-            const int e = (int) threadIdx.x + it * WAVES * 64;
-            const int unit = e >> 3, sub = e & 7;
-            const int rl = unit / NBLK, blk = unit % NBLK;
-            const int r = r0 + std::min(rl, RW - 1);
-            const int t = r / a.gqa, h = kvh * a.gqa + (r - t * a.gqa);
-            v4[it] = *(const float4 *) (a.q + (size_t) t * a.q_nb1 + (size_t) h * a.q_nb2 + (size_t) b * a.q_nb3 +
-                                        (size_t) (blk * QK + sub * 4) * 4);
-        }
-        // every query and mask value of this thread has arrived (and chunk 0);
-        // the compiler sees this wait, so no later one stalls on chunk 1
-        wait_vmcnt<0>();
-#pragma unroll
-        for (int it = 0; it < MIT; it++) {
-            const int e = (int) threadIdx.x + it * WAVES * 64;
-            if (e < n_mval) mlds[e] = mpre[it];
-        }
-        if constexpr (NS > 2) {
-            if (n_chunks > 1) issue_chunk(1, ring[1]);
-        }
         const float fs = a.scale * LOG2E;
 #pragma unroll
         for (int it = 0; it < QIT; it++) {
-            const int e = (int) threadIdx.x + it * WAVES * 64;
-            const int unit = e >> 3, sub = e & 7;
-            const int rl = unit / NBLK, blk = unit % NBLK;   // one row per wave and iteration
-            if (rl >= RW) continue;                          // padding rows stay zero
-            const float x[4] = {v4[it].x, v4[it].y, v4[it].z, v4[it].w};
+            const int blk = wave + WAVES * it;
+            uint8_t * wrow = qwin + (qrl * NBLK + blk) * QWIN;
+            // the lane's share of the window is zeroed first; the quants that
+            // follow (written by lanes of this wave, whose LDS writes complete
+            // in order) overwrite their part of it
+#pragma unroll
+            for (int z = 0; z < 4 / QL; z++) ((uint4 *) wrow)[qh * (4 / QL) + z] = make_uint4(0, 0, 0, 0);
+            wave_lds_sync();
+            uint32_t w[QV / 4];
             uint16_t d16;
-            float dq;
-            const uint32_t w = a.x86 ? dev::q8_quantize_lane4(x, true, &d16, &dq)
-                                     : dev::q8_quantize_lane4(x, false, &d16, &dq);
-            uint16_t * wp = (uint16_t *) (qwin + (rl * NBLK + blk) * QWIN + win_off(blk) + 4 * sub);
-            wp[0] = (uint16_t) w;
-            wp[1] = (uint16_t) (w >> 16);
-            if (sub == 0) dql[rl * NBLK + blk] = dq * fs;
+            float dq = 0.f;
+            if (a.x86) dev::q8_quantize_lanes<QV>(qx[it], true, w, &d16, &dq);
+            else       dev::q8_quantize_lanes<QV>(qx[it], false, w, &d16, &dq);
+            if (qrl < RW) {                                     // padding rows keep zero windows
+                uint16_t * wp = (uint16_t *) (wrow + win_off(blk) + QV * qh);
+#pragma unroll
+                for (int m = 0; m < QV / 4; m++) {
+                    wp[2 * m] = (uint16_t) w[m];
+                    wp[2 * m + 1] = (uint16_t) (w[m] >> 16);
+                }
+            }
+            if (qh == 0) dql[qrl * NBLK + blk] = qrl < RW ? dq * fs : 0.f;
         }
     }
     __syncthreads();
@@ -602,12 +639,12 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
             const bool tail = (c + 1) * CK > span;                // keys past the split in this chunk
             float x[NKT][4];
             float mloc = -INFINITY;
-            if (!MT && a.mask_mode == MASK_SPLIT) {
+            if (msplit) {
+                const uint16_t * mp = (const uint16_t *) ((const uint8_t *) mlds + mlds_row) + kin;
 #pragma unroll
-                for (int kt = 0; kt < NKT; kt++) {
-                    const uint2 m2 = *(const uint2 *) &mlds[mrow0 * a.split_len + kin + 16 * kt];
-                    mv[kt][0] = m2.x & 0xffffu; mv[kt][1] = m2.x >> 16; mv[kt][2] = m2.y & 0xffffu; mv[kt][3] = m2.y >> 16;
-                }
+                for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) mv[kt][i] = mp[16 * kt + i];
             }
 #pragma unroll
             for (int kt = 0; kt < NKT; kt++)
@@ -767,7 +804,7 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
     const size_t bh = (size_t) b * a.nh_kv + kvh;
     const bool vec = a.ns > 1 || a.dst_vec;
     const int r = r0 + rl;
-    const int tq = r / a.gqa, h = kvh * a.gqa + (r - tq * a.gqa);
+    const int tq = (int) div_gqa(a, (uint32_t) r), h = kvh * a.gqa + (r - tq * a.gqa);
     float * out;
     float oscale;
     if (a.ns == 1) {
@@ -871,7 +908,7 @@ __global__ __launch_bounds__(256) void k_fattn_merge(fa_args a) {
         }
         const float inv = L > 0.f ? 1.f / L : 0.f;
         o.x *= inv; o.y *= inv; o.z *= inv; o.w *= inv;
-        const int t = r / a.gqa, h = kvh * a.gqa + (r - t * a.gqa);
+        const int t = (int) div_gqa(a, (uint32_t) r), h = kvh * a.gqa + (r - t * a.gqa);
         float * d = a.dst + (((size_t) b * a.T + t) * a.nh + h) * D + 64 * quarter + 4 * q;
         if (a.dst_vec) {
             *(float4 *) d = o;
@@ -908,6 +945,16 @@ size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 // Bytes from the start of a mask batch slice to the end of its last row.
 size_t mask_slice_bytes(const qwfn_tensor & m) {
     return (size_t) (m.ne[1] - 1) * m.nb[1] + (size_t) (m.ne[2] - 1) * m.nb[2] + (size_t) m.ne[0] * 2;
+}
+
+// Bytes from the start of a q batch slice to the end of its last row.
+size_t q_slice_bytes(const qwfn_tensor & q) {
+    return (size_t) (q.ne[1] - 1) * q.nb[1] + (size_t) (q.ne[2] - 1) * q.nb[2] + (size_t) q.ne[0] * 4;
+}
+
+// ceil(2^32 / d) for d > 1 (0 for d = 1, which divides without it).
+uint32_t recip32(int64_t d) {
+    return d > 1 ? (uint32_t) (((uint64_t(1) << 32) + (uint64_t) d - 1) / (uint64_t) d) : 0u;
 }
 
 // The key loop hand-counts its outstanding vector-memory operations (the LDS
@@ -952,6 +999,11 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
     if (T <= 0 || nh <= 0 || q->ne[3] <= 0) return set_error(QWFN_EINVAL, "flash_attn_ext: empty q");
     const int64_t gqa = nh / nh_kv;
     const int64_t R = T * gqa;
+    // row indices divide by gqa through a 32-bit reciprocal (exact while R * gqa < 2^32)
+    if (R * gqa >= (int64_t(1) << 32)) return set_error(QWFN_ENOTSUP, "flash_attn_ext: T * n_head * gqa too large");
+    // query rows travel as 32-bit offsets within one batch slice
+    if (q_slice_bytes(*q) >= (size_t(1) << 32))
+        return set_error(QWFN_ENOTSUP, "flash_attn_ext: q batch slices must be below 4 GiB");
     // 16-byte aligned rows and heads: the kernel stages K/V with 16-byte loads.
     if (!is_aligned(k->data, 16) || !is_aligned(v->data, 16) || k->nb[1] % 16 || k->nb[2] % 16 || k->nb[3] % 16 ||
         v->nb[1] % 16 || v->nb[2] % 16 || v->nb[3] % 16)
@@ -1072,10 +1124,14 @@ extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor
         a.mask = (const char *) mask->data; a.m_nb1 = mask->nb[1]; a.m_nb2 = mask->nb[2]; a.m_nb3 = mask->nb[3];
         a.m_ne2 = (int32_t) mask->ne[2]; a.m_ne3 = (int32_t) mask->ne[3];
         a.m_slice = (uint32_t) mask_slice_bytes(*mask);
+        // MASK_SPLIT: each mask row of a split as 16-byte granules from the
+        // aligned address at or below its first key, all in LDS at once
         const int64_t mrows = mask->ne[2] == 1 ? ((int64_t) pl.rw + pl.gqa - 1) / pl.gqa + 1 : pl.rw;
         const int64_t mlds = pl.kind == FA_P4_T2 ? fa_cfg<2, false, WAVES_PAIR, 32>::MLDS : MASK_LDS;
-        a.mask_mode = mrows * pl.split_len * 2 <= mlds ? MASK_SPLIT : MASK_TILE;
-        if (const int force = env_int("QWFN_FA_MASK_TILE", 0)) a.mask_mode = MASK_TILE;
+        a.m_gran = pl.split_len / 8 + 1;
+        a.m_gran_mul = recip32(a.m_gran);
+        a.mask_mode = mrows * 16 * a.m_gran <= mlds ? MASK_SPLIT : MASK_TILE;
+        if (env_int("QWFN_FA_MASK_TILE", 0)) a.mask_mode = MASK_TILE;
     } else {
         a.mask = nullptr; a.m_ne2 = 1; a.m_ne3 = 1; a.m_slice = 0; a.mask_mode = MASK_NONE;
     }
@@ -1087,6 +1143,8 @@ extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor
     a.ns = pl.ns; a.split_len = pl.split_len; a.rw = pl.rw; a.n_rg = pl.n_rg;
     a.scale = scale; a.x86 = variant == QWFN_Q8_X86;
     a.dst_vec = is_aligned(dst->data, 16) ? 1 : 0;
+    a.q_slice = (uint32_t) q_slice_bytes(*q);
+    a.gqa_mul = recip32(pl.gqa);
 
     const int64_t units = (int64_t) a.B * a.ns >= 8 ? ((int64_t) a.B * a.ns + 7) / 8 * 8 : (int64_t) a.B * a.ns;
     const int64_t grid = units * a.nh_kv * a.n_rg;

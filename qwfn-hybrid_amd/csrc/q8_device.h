@@ -18,16 +18,6 @@ __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
     return (uint32_t) __builtin_amdgcn_update_dpp((int) v, (int) v, CTRL, 0xF, 0xF, false);
 }
 
-// Max of a non-negative float (given as its bit pattern) over aligned groups of
-// 8 lanes: quad butterfly, then the two quads of each half-row. Non-negative
-// IEEE floats order like their bit patterns, so an unsigned max is exact.
-__device__ __forceinline__ uint32_t max8_u32(uint32_t v) {
-    v = max(v, dpp_u32<DPP_QUAD_1032>(v));
-    v = max(v, dpp_u32<DPP_QUAD_2301>(v));
-    v = max(v, dpp_u32<DPP_HALF_MIRROR>(v));
-    return v;
-}
-
 // x86 AVX/AVX2 quantize_row_q8_0 element: _mm256_round_ps(NEAREST) (ties to
 // even) then _mm256_cvtps_epi32 (out of int32 range or NaN -> 0x80000000) and
 // the two saturating packs to int8.
@@ -80,20 +70,38 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
     return (float) __builtin_bit_cast(_Float16, h);
 }
 
-// Quantise 4 consecutive values held by this lane as part of a 32-value block
-// spread over 8 consecutive lanes (lane % 8 == position of the 4-value group).
-// Returns the packed int8 quads; *d16 gets the block's fp16 scale bits and
-// *dq its fp32 value (fp16 -> fp32, as ggml's vec_dot reads it).
-__device__ __forceinline__ uint32_t q8_quantize_lane4(const float x[4], bool x86, uint16_t * d16, float * dq) {
+// Quantise V consecutive values held by this lane as part of a 32-value block
+// spread over L = 32 / V consecutive lanes (lane % L == position of the group).
+// w[m] gets the packed int8 quads of values 4m .. 4m+3; *d16 the block's fp16
+// scale bits and *dq its fp32 value (fp16 -> fp32, as ggml's vec_dot reads it).
+template <int V>
+__device__ __forceinline__ void q8_quantize_lanes(const float (&x)[V], bool x86, uint32_t (&w)[V / 4], uint16_t * d16,
+                                                  float * dq) {
+    static_assert(V == 4 || V == 8 || V == 16 || V == 32, "a block is 32 values");
+    constexpr int L = 32 / V;
+    // |x| max over the block: non-negative IEEE floats order like their bit
+    // patterns, so an unsigned max is exact; the lanes of a block combine by
+    // quad butterfly, then the two quads of each half-row
     uint32_t am = 0;
 #pragma unroll
-    for (int j = 0; j < 4; j++) am = max(am, __builtin_bit_cast(uint32_t, x[j]) & 0x7fffffffu);
-    am = max8_u32(am);
+    for (int j = 0; j < V; j++) am = max(am, __builtin_bit_cast(uint32_t, x[j]) & 0x7fffffffu);
+    if constexpr (L >= 2) am = max(am, dpp_u32<DPP_QUAD_1032>(am));
+    if constexpr (L >= 4) am = max(am, dpp_u32<DPP_QUAD_2301>(am));
+    if constexpr (L >= 8) am = max(am, dpp_u32<DPP_HALF_MIRROR>(am));
     const float amax = __builtin_bit_cast(float, am);
     const q8_scale s = q8_block_scale(amax, x86);
     *d16 = f32_to_f16_bits(s.d);
     *dq = f16_bits_to_f32(*d16);
-    return q8_pack4(x, s.id, x86);
+#pragma unroll
+    for (int m = 0; m < V / 4; m++) w[m] = q8_pack4(&x[4 * m], s.id, x86);
+}
+
+// The same for 4 values per lane over 8 lanes; returns the packed quad.
+__device__ __forceinline__ uint32_t q8_quantize_lane4(const float x[4], bool x86, uint16_t * d16, float * dq) {
+    const float (&xv)[4] = *reinterpret_cast<const float (*)[4]>(x);
+    uint32_t w[1];
+    q8_quantize_lanes<4>(xv, x86, w, d16, dq);
+    return w[0];
 }
 
 }  // namespace dev

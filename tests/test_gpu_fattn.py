@@ -166,6 +166,19 @@ def test_gqa12_and_multiple_row_groups(gpu, oracle):
     check(got, ref)
 
 
+def test_gqa1_rows_one_head_each(gpu, oracle):
+    """One query head per KV head (gqa 1: row r is position r), 5 positions, causal."""
+    K = gpu
+    T, n_past = 5, 900
+    kc, vc = layer(12, n_past + T)
+    q = KD.q_rows(12, 0, T, 2)[0]
+    mask = O.causal_mask(T, n_past)
+    say("gqa 1, T=5")
+    got = gpu_attn(K, q, kc, vc, n_past + T, 2, mask, 1 / 16)
+    ref = KD.oracle_attn(q, kc, vc, n_past + T, 2, mask, 1 / 16)
+    check(got, ref)
+
+
 def test_batched_ragged_depths(gpu, oracle):
     """Config 5 in miniature: 4 sequences in 4 cache slots, depths differ, one query each;
     keys past a sequence's depth are masked (mask [n_kv, 1, 1, 4])."""
