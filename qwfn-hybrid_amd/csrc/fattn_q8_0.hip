@@ -341,7 +341,8 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
     const int split = u - b * a.ns;
     if (b >= a.B) return;
     const int64_t k_lo = (int64_t) split * a.split_len;
-    const int64_t k_hi = std::min<int64_t>(a.n_kv, k_lo + a.split_len);
+    // the last split runs to n_kv (it may hold up to one chunk more than split_len)
+    const int64_t k_hi = split == a.ns - 1 ? a.n_kv : std::min<int64_t>(a.n_kv, k_lo + a.split_len);
     const int n_chunks = (int) ((k_hi - k_lo + CK - 1) / CK);
     const int r0 = rg * a.rw;                          // first query row of this block
     const int RW = std::min(a.rw, a.R - r0);          // rows in this block
@@ -930,6 +931,7 @@ enum fa_kind {
 
 struct fa_plan {
     int32_t R, RT, gqa, rw, n_rg, ns, split_len;
+    int32_t max_span;                 // keys of the longest split, whole chunks
     fa_kind kind;
     size_t  off_ml;                   // workspace section of the split (max, sum) pairs (bytes)
     size_t  ws_bytes;
@@ -1030,9 +1032,14 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
     int rw = R > 16 ? 32 : 16;
     if (const int force = env_int("QWFN_FA_ROWS", 0)) rw = force >= 32 ? 32 : 16;
     // 4-wave blocks, two per CU (their prologues and phases overlap), or
-    // 8-wave blocks, one per CU. QWFN_FA_PAIR=0 forces 8 waves, =1 4 waves.
+    // 8-wave blocks, one per CU. One tile: 4 waves. Two tiles: 4 waves of 32
+    // keys each when 8-wave blocks (one per CU) would get fewer than 4 chunks
+    // each, else 8 waves. QWFN_FA_PAIR=0 forces 8 waves, =1 4 waves.
+    const int64_t B = q->ne[3];
     const int pair_env = env_int("QWFN_FA_PAIR", -1);
-    const bool pair = pair_env >= 0 ? pair_env != 0 : rw == 16;
+    const int64_t groups = nh_kv * B * ((R + rw - 1) / rw);
+    const int64_t splits8 = std::max<int64_t>(1, 256 / groups);
+    const bool pair = pair_env >= 0 ? pair_env != 0 : rw == 16 || n_kv < 4 * 64 * splits8;
     pl->kind = rw == 16 ? (pair ? FA_P4_T1 : FA_W8_T1) : (pair ? FA_P4_T2 : FA_W8_T2);
     pl->R = (int32_t) R;
     pl->rw = rw;
@@ -1043,15 +1050,22 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
                      : pl->kind == FA_W8_T2 ? fa_cfg<2, false, WAVES, 16>::CK
                      : pl->kind == FA_P4_T1 ? fa_cfg<1, false, WAVES_PAIR, 16>::CK
                                             : fa_cfg<2, false, WAVES_PAIR, 32>::CK;
-    const int64_t B = q->ne[3];
     // Splits: about one block per CU slot (256 or 512), each at least one chunk.
     const int64_t target_blocks = env_int("QWFN_FA_BLOCKS", pair ? 512 : 256);
     int64_t ns = std::max<int64_t>(1, target_blocks / std::max<int64_t>(1, nh_kv * B * pl->n_rg));
     ns = std::min<int64_t>(ns, std::max<int64_t>(1, (n_kv + ck - 1) / ck));
     if (const int force = env_int("QWFN_FA_SPLITS", 0)) ns = force;
-    int64_t split_len = (n_kv + ns - 1) / ns;
-    split_len = std::max<int64_t>(ck, (split_len + ck - 1) / ck * ck);
-    ns = std::max<int64_t>(1, (n_kv + split_len - 1) / split_len);
+    // Splits of whole chunks. When the keys exceed two or more whole chunks
+    // per split by less than one chunk (n_kv = 2^k + T), the last split takes
+    // the rest; otherwise every split gets one chunk more and there are fewer.
+    int64_t split_len = n_kv / (ns * ck) * ck;
+    if (split_len < 2 * ck || n_kv - ns * split_len >= ck || !env_int("QWFN_FA_ABSORB", 1)) {
+        split_len = (n_kv + ns - 1) / ns;
+        split_len = std::max<int64_t>(ck, (split_len + ck - 1) / ck * ck);
+        ns = std::max<int64_t>(1, (n_kv + split_len - 1) / split_len);
+    }
+    pl->max_span = n_kv - (ns - 1) * split_len;
+    pl->max_span = std::max<int64_t>(split_len, (pl->max_span + ck - 1) / ck * ck);
     if (ns > MAX_SPLITS)
         return set_error(QWFN_ENOTSUP, "flash_attn_ext: " + std::to_string(ns) + " key splits requested, at most " +
                                            std::to_string(MAX_SPLITS) + " supported");
@@ -1128,7 +1142,7 @@ extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor
         // aligned address at or below its first key, all in LDS at once
         const int64_t mrows = mask->ne[2] == 1 ? ((int64_t) pl.rw + pl.gqa - 1) / pl.gqa + 1 : pl.rw;
         const int64_t mlds = pl.kind == FA_P4_T2 ? fa_cfg<2, false, WAVES_PAIR, 32>::MLDS : MASK_LDS;
-        a.m_gran = pl.split_len / 8 + 1;
+        a.m_gran = pl.max_span / 8 + 1;
         a.m_gran_mul = recip32(a.m_gran);
         a.mask_mode = mrows * 16 * a.m_gran <= mlds ? MASK_SPLIT : MASK_TILE;
         if (env_int("QWFN_FA_MASK_TILE", 0)) a.mask_mode = MASK_TILE;
