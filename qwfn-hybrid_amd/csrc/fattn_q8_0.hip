@@ -840,6 +840,27 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
 constexpr int MERGE_GROUPS = 16;
 constexpr int MERGE_BATCH = 8;
 
+// Wave-wide reduction without LDS: a butterfly within each row of 16 lanes
+// (DPP: lane ^ 1, lane ^ 2, the mirrored half of 8, the mirrored row of 16),
+// then the four rows' results through scalar reads.
+template <typename Op>
+__device__ __forceinline__ float wave_reduce(float x, Op op) {
+    auto dpp = [](float v, auto ctrl) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), decltype(ctrl)::value,
+                                                                     0xF, 0xF, false));
+    };
+    x = op(x, dpp(x, std::integral_constant<int, 0xB1>{}));    // quad_perm [1,0,3,2]
+    x = op(x, dpp(x, std::integral_constant<int, 0x4E>{}));    // quad_perm [2,3,0,1]
+    x = op(x, dpp(x, std::integral_constant<int, 0x141>{}));   // row_half_mirror
+    x = op(x, dpp(x, std::integral_constant<int, 0x140>{}));   // row_mirror
+    const int u = __builtin_bit_cast(int, x);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(u, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(u, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(u, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(u, 48));
+    return op(op(r0, r1), op(r2, r3));
+}
+
 __global__ __launch_bounds__(256) void k_fattn_merge(fa_args a) {
     __shared__ float wsh[MAX_SPLITS];
     __shared__ float red[4];
@@ -853,30 +874,37 @@ __global__ __launch_bounds__(256) void k_fattn_merge(fa_args a) {
     const float4 * po = (const float4 *) (a.part_o + ((size_t) bh * a.ns * a.R + r) * D + 64 * quarter) + q;
     const size_t sstride = (size_t) a.R * D / 4;              // float4s between splits
 
+    // every split's (max, sum), read once: thread i holds splits i + 256 j.
+    // All loads are unconditional (indices clamped to the last split) so the
+    // counter waits stay exact: the (max, sum) pairs first, then the first
+    // MERGE_BATCH partials of the thread's group, which stay in flight while
+    // the weights are formed.
+    constexpr int MLJ = MAX_SPLITS / 256;
+    float2 e[MLJ];
+#pragma unroll
+    for (int j = 0; j < MLJ; j++) e[j] = ml[(size_t) std::min((int) threadIdx.x + 256 * j, a.ns - 1) * a.R];
     float4 ob[MERGE_BATCH];
 #pragma unroll
-    for (int i = 0; i < MERGE_BATCH; i++) {
-        const int s = g + i * MERGE_GROUPS;
-        ob[i] = s < a.ns ? po[(size_t) s * sstride] : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+    for (int i = 0; i < MERGE_BATCH; i++) ob[i] = po[(size_t) std::min(g + i * MERGE_GROUPS, a.ns - 1) * sstride];
     float mloc = -INFINITY;
-    for (int s = threadIdx.x; s < a.ns; s += 256) {
-        const float2 e = ml[(size_t) s * a.R];
-        wsh[s] = e.x;
-        mloc = xmax(mloc, e.x);
+#pragma unroll
+    for (int j = 0; j < MLJ; j++) {
+        if ((int) threadIdx.x + 256 * j >= a.ns) e[j] = make_float2(-INFINITY, 0.f);
+        mloc = xmax(mloc, e[j].x);
     }
-    for (int o = 32; o >= 1; o >>= 1) mloc = xmax(mloc, __shfl_xor(mloc, o));
+    mloc = wave_reduce(mloc, [](float x, float y) { return xmax(x, y); });
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mloc;
     __syncthreads();
     const float M = xmax(xmax(red[0], red[1]), xmax(red[2], red[3]));
     float lpart = 0.f;
-    for (int s = threadIdx.x; s < a.ns; s += 256) {
-        const float m = wsh[s];
-        const float w = m == -INFINITY ? 0.f : exp2f(m - M);
-        lpart += w * ml[(size_t) s * a.R].y;
-        wsh[s] = w;
+#pragma unroll
+    for (int j = 0; j < MLJ; j++) {
+        const int s = (int) threadIdx.x + 256 * j;
+        const float w = e[j].x == -INFINITY ? 0.f : exp2f(e[j].x - M);
+        lpart += w * e[j].y;
+        if (s < a.ns) wsh[s] = w;
     }
-    for (int o = 32; o >= 1; o >>= 1) lpart += __shfl_xor(lpart, o);
+    lpart = wave_reduce(lpart, [](float x, float y) { return x + y; });
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = lpart;
     __syncthreads();
@@ -886,10 +914,7 @@ __global__ __launch_bounds__(256) void k_fattn_merge(fa_args a) {
     for (int s0 = 0; s0 < a.ns; s0 += MERGE_GROUPS * MERGE_BATCH) {
         if (s0 > 0) {
 #pragma unroll
-            for (int i = 0; i < MERGE_BATCH; i++) {
-                const int s = s0 + g + i * MERGE_GROUPS;
-                ob[i] = s < a.ns ? po[(size_t) s * sstride] : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
+            for (int i = 0; i < MERGE_BATCH; i++) ob[i] = po[(size_t) std::min(s0 + g + i * MERGE_GROUPS, a.ns - 1) * sstride];
         }
 #pragma unroll
         for (int i = 0; i < MERGE_BATCH; i++) {
