@@ -128,12 +128,20 @@ struct fa_args {
     uint32_t gqa_mul;      // ceil(2^32 / gqa): r / gqa = mulhi(r, gqa_mul) for gqa > 1
     int32_t  m_gran;       // MASK_SPLIT: 16-byte granules per mask row of a split (split_len / 8 + 1)
     uint32_t m_gran_mul;   // ceil(2^32 / m_gran)
+    uint32_t ns_mul, hgn_mul, nrg_mul;   // ceil(2^32 / d) for ns, nh_kv * n_rg, n_rg
 };
 
-// r / gqa for the row indices of a call (r * gqa < 2^32, checked by the host):
-// with m = ceil(2^32 / d), floor(r * m / 2^32) = floor(r / d) while r * d < 2^32.
+// x / d through m = ceil(2^32 / d): floor(x * m / 2^32) = floor(x / d) while
+// x * d < 2^32 (the host checks the ranges of a call); d = 1 needs no m.
+__device__ __forceinline__ uint32_t udiv(uint32_t x, uint32_t d, uint32_t m) {
+    return d == 1 ? x : __umulhi(x, m);
+}
 __device__ __forceinline__ uint32_t div_gqa(const fa_args & a, uint32_t r) {
-    return a.gqa == 1 ? r : __umulhi(r, a.gqa_mul);
+    return udiv(r, (uint32_t) a.gqa, a.gqa_mul);
+}
+// b % n for a batch index b and a broadcast extent n (n is 1 or B in practice)
+__device__ __forceinline__ int bmod(int b, int n) {
+    return b < n ? b : b % n;
 }
 
 // The compiler's hazard recognizer does not see the VALU writes inside inline
@@ -274,7 +282,9 @@ __device__ __forceinline__ v4i make_rsrc(const void * base, uint32_t bytes) {
 // that publishes the data. No other vector-memory load is in flight while DMAs
 // are, so the explicit counts are exact.
 __device__ __forceinline__ void dma16_buf(v4i rsrc, uint32_t off, uint32_t lds_base) {
+    // an LDS DMA reads M0 one wait state after the SALU write at the earliest
     asm volatile("s_mov_b32 m0, %2\n\t"
+                 "s_nop 0\n\t"
                  "buffer_load_dwordx4 %0, %1, 0 offen lds"
                  :: "v"(off), "s"(rsrc), "s"(lds_base) : "memory");
 }
@@ -291,6 +301,11 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// 16-byte store marked non-temporal (p 16-byte aligned).
+__device__ __forceinline__ void store_nt4(float * p, float4 v) {
+    __builtin_nontemporal_store(v4f{v.x, v.y, v.z, v.w}, (v4f *) p);
+}
+
 // f[0 .. n) = 0 (dst is only 4-byte aligned, so plain f32 stores).
 __global__ void k_zero_f32(float * f, int64_t n) {
     const int64_t stride = (int64_t) gridDim.x * blockDim.x;
@@ -300,6 +315,9 @@ __global__ void k_zero_f32(float * f, int64_t n) {
 template <int RT, bool MT, int NW, int KWV>
 __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
     using C = fa_cfg<RT, MT, NW, KWV>;
+    // the argument block's pointers are loaded with the rest, in one round of
+    // scalar loads (not a second round after the exit of padding blocks)
+    asm volatile("" :: "s"(a.q), "s"(a.k), "s"(a.v), "s"(a.mask), "s"(a.m_ne2), "s"(a.mask_mode), "s"(a.part_o));
     constexpr int WAVES = NW;
     constexpr int KW = KWV;              // keys per wave per chunk
     constexpr int NKT = C::NKT;
@@ -329,15 +347,16 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
     int hg, u;
     if (a.B * a.ns >= 8) {
         const int j = id >> 3;
-        hg = j % hgn;
-        u  = (j / hgn) * 8 + (id & 7);
+        const int jq = (int) udiv((uint32_t) j, (uint32_t) hgn, a.hgn_mul);
+        hg = j - jq * hgn;
+        u  = jq * 8 + (id & 7);
     } else {
-        hg = id % hgn;
-        u  = id / hgn;
+        u  = (int) udiv((uint32_t) id, (uint32_t) hgn, a.hgn_mul);
+        hg = id - u * hgn;
     }
-    const int kvh  = hg / a.n_rg;
+    const int kvh  = (int) udiv((uint32_t) hg, (uint32_t) a.n_rg, a.nrg_mul);
     const int rg   = hg - kvh * a.n_rg;
-    const int b    = u / a.ns;
+    const int b    = (int) udiv((uint32_t) u, (uint32_t) a.ns, a.ns_mul);
     const int split = u - b * a.ns;
     if (b >= a.B) return;
     const int64_t k_lo = (int64_t) split * a.split_len;
@@ -348,13 +367,13 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
     const int RW = std::min(a.rw, a.R - r0);          // rows in this block
     const int t0 = (int) div_gqa(a, (uint32_t) r0);
 
-    const char * kbase = a.k + (size_t) (b % a.kb) * a.k_nb3 + (size_t) kvh * a.k_nb2;
-    const char * vbase = a.v + (size_t) (b % a.vb) * a.v_nb3 + (size_t) kvh * a.v_nb2;
+    const char * kbase = a.k + (size_t) bmod(b, a.kb) * a.k_nb3 + (size_t) kvh * a.k_nb2;
+    const char * vbase = a.v + (size_t) bmod(b, a.vb) * a.v_nb3 + (size_t) kvh * a.v_nb2;
     // Mask rows of this block: query position t0 + mr for a shared mask, query
     // row r0 + mr for a per-head one. Byte offset of row mr from the mask's
     // batch slice (`mslice`, its start rounded down to 16 bytes).
     const int n_mrows = a.mask_mode == MASK_NONE ? 0 : (a.m_ne2 == 1 ? (int) div_gqa(a, (uint32_t) (r0 + RW - 1)) - t0 + 1 : RW);
-    const char * mslice = a.mask + (size_t) (b % a.m_ne3) * a.m_nb3;
+    const char * mslice = a.mask + (size_t) bmod(b, a.m_ne3) * a.m_nb3;
     const char * mslice_al = (const char *) ((uintptr_t) mslice & ~(uintptr_t) 15);
     auto mrow_off = [&](int mr) -> uint32_t {
         int t = t0 + mr, hq = 0;
@@ -366,6 +385,45 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
         return (uint32_t) (mslice - mslice_al) + (uint32_t) ((size_t) t * a.m_nb1 + (size_t) hq * a.m_nb2);
     };
     const int n_mdma = MT ? (n_mrows * C::MGR + 63) / 64 : 0;
+
+    // ---- prologue. What the block needs before its key loop travels as LDS
+    //      DMA, in this order: its query rows (f32, into the last ring stage),
+    //      its MASK_SPLIT mask rows, chunk 0 (and chunk 1 with three stages).
+    //      One wait that leaves the chunk DMAs in flight covers the first two
+    //      (the counter is in order), and the block requantises its query rows
+    //      while the chunks arrive ----
+    uint8_t * qstage = ring[NS - 1];    // [ROWS][D] f32 query rows, then the window image below
+    {
+        // one wave-wide DMA (1 KB) per query row; wave w takes rows w, w + NW, ...
+        const v4i rq = make_rsrc(a.q + (size_t) b * a.q_nb3, a.q_slice);
+#pragma unroll
+        for (int j = 0; j < ROWS / WAVES; j++) {
+            const int rl = wave + WAVES * j;
+            if (rl >= RW) break;
+            const uint32_t r = (uint32_t) (r0 + rl);
+            const uint32_t t = div_gqa(a, r), h = (uint32_t) (kvh * a.gqa) + (r - t * (uint32_t) a.gqa);
+            dma16_buf(rq, t * (uint32_t) a.q_nb1 + h * (uint32_t) a.q_nb2 + 16u * (uint32_t) lane,
+                      __builtin_amdgcn_readfirstlane(lds_addr(qstage + rl * 1024)));
+        }
+    }
+    // MASK_SPLIT: mask row mr of the split lands at byte mr * mstride of mlds as
+    // the 16-byte granules from the aligned address at or below its first key,
+    // which sits `mis` bytes into the LDS row. Granule g = 64m + lane is granule
+    // g % m_gran of row g / m_gran; lanes past the last granule re-read it, so
+    // every LDS byte a DMA writes lies inside mlds.
+    const bool msplit = !MT && a.mask_mode == MASK_SPLIT;
+    const uint32_t mstride = 16u * (uint32_t) a.m_gran;
+    if (msplit) {
+        const int n_g = n_mrows * a.m_gran;
+        const v4i rm = make_rsrc(mslice_al, a.m_slice + (uint32_t) (mslice - mslice_al));
+        for (int m = wave; m * 64 < n_g; m += WAVES) {
+            const uint32_t g = (uint32_t) std::min(m * 64 + lane, n_g - 1);
+            const uint32_t row = __umulhi(g, a.m_gran_mul);
+            const uint32_t k = g - row * (uint32_t) a.m_gran;
+            const uint32_t src = ((mrow_off((int) row) + 2u * (uint32_t) k_lo) & ~15u) + 16u * k;
+            dma16_buf(rm, src, __builtin_amdgcn_readfirstlane(lds_addr((uint8_t *) mlds + m * 1024)));
+        }
+    }
 
     // A chunk is SLOTS wave-wide 16-byte DMAs; slot s lands at byte 1024*s of
     // the stage: slots [0, DMA_T) are the K rows (piece p = 64*s + lane is byte
@@ -403,6 +461,8 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
     const int rl_lane0 = 16 * tile + ln;
     const int mrow0 = rl_lane0 >= RW ? 0 : (a.m_ne2 == 1 ? (int) div_gqa(a, (uint32_t) (r0 + rl_lane0)) - t0 : rl_lane0);
     const uint32_t mtile_off = MT ? (uint32_t) (mrow0 * C::MGR * 16) + (mrow_off(mrow0) & 15u) : 0u;
+    // the lane's mask row in mlds (MASK_SPLIT)
+    const uint32_t mlds_row = msplit ? (uint32_t) mrow0 * mstride + ((mrow_off(mrow0) + 2u * (uint32_t) k_lo) & 15u) : 0u;
 
     // Chunk c is read through buffer resources based at its first key, sized
     // to the bytes that exist: rows past n_kv arrive as zeros, and those keys
@@ -431,46 +491,6 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
         }
     };
 
-    // ---- prologue. What the block needs before its key loop travels as LDS
-    //      DMA, in this order: its query rows (f32, into the last ring stage),
-    //      its MASK_SPLIT mask rows, chunk 0 (and chunk 1 with three stages).
-    //      One wait that leaves the chunk DMAs in flight covers the first two
-    //      (the counter is in order), and the block requantises its query rows
-    //      while the chunks arrive ----
-    uint8_t * qstage = ring[NS - 1];    // [ROWS][D] f32 query rows, then the window image below
-    {
-        // one wave-wide DMA (1 KB) per query row; wave w takes rows w, w + NW, ...
-        const v4i rq = make_rsrc(a.q + (size_t) b * a.q_nb3, a.q_slice);
-#pragma unroll
-        for (int j = 0; j < ROWS / WAVES; j++) {
-            const int rl = wave + WAVES * j;
-            if (rl >= RW) break;
-            const uint32_t r = (uint32_t) (r0 + rl);
-            const uint32_t t = div_gqa(a, r), h = (uint32_t) (kvh * a.gqa) + (r - t * (uint32_t) a.gqa);
-            dma16_buf(rq, t * (uint32_t) a.q_nb1 + h * (uint32_t) a.q_nb2 + 16u * (uint32_t) lane,
-                      __builtin_amdgcn_readfirstlane(lds_addr(qstage + rl * 1024)));
-        }
-    }
-    // MASK_SPLIT: mask row mr of the split lands at byte mr * mstride of mlds as
-    // the 16-byte granules from the aligned address at or below its first key,
-    // which sits `mis` bytes into the LDS row. Granule g = 64m + lane is granule
-    // g % m_gran of row g / m_gran; lanes past the last granule re-read it, so
-    // every LDS byte a DMA writes lies inside mlds.
-    const bool msplit = !MT && a.mask_mode == MASK_SPLIT;
-    const uint32_t mstride = 16u * (uint32_t) a.m_gran;
-    uint32_t mlds_row = 0;                              // byte of the lane's first mask key of the split in mlds
-    if (msplit) {
-        const int n_g = n_mrows * a.m_gran;
-        const v4i rm = make_rsrc(mslice_al, a.m_slice + (uint32_t) (mslice - mslice_al));
-        for (int m = wave; m * 64 < n_g; m += WAVES) {
-            const uint32_t g = (uint32_t) std::min(m * 64 + lane, n_g - 1);
-            const uint32_t row = __umulhi(g, a.m_gran_mul);
-            const uint32_t k = g - row * (uint32_t) a.m_gran;
-            const uint32_t src = ((mrow_off((int) row) + 2u * (uint32_t) k_lo) & ~15u) + 16u * k;
-            dma16_buf(rm, src, __builtin_amdgcn_readfirstlane(lds_addr((uint8_t *) mlds + m * 1024)));
-        }
-        mlds_row = (uint32_t) mrow0 * mstride + ((mrow_off(mrow0) + 2u * (uint32_t) k_lo) & 15u);
-    }
     issue_chunk(0, ring[0]);
     int chunk_ops = ops_per_chunk;
     if constexpr (NS > 2) {
@@ -814,7 +834,11 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
     } else {
         out = a.part_o + ((bh * a.ns + split) * a.R + r) * D + 8 * lg_e;
         oscale = 1.f;
-        if (lg_e == 0) a.part_ml[(bh * a.ns + split) * a.R + r] = make_float2(M, L);
+        if (lg_e == 0) {
+            float2 * mlp = &a.part_ml[(bh * a.ns + split) * a.R + r];
+            __builtin_nontemporal_store(M, &mlp->x);
+            __builtin_nontemporal_store(L, &mlp->y);
+        }
     }
 #pragma unroll
     for (int bb = 0; bb < NBLK; bb++) {
@@ -822,7 +846,11 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
         const v4f o0 = O[bb][0] * fw, o1 = O[bb][1] * fw;
         const float4 w0 = make_float4((o0[0] + p0.x) * oscale, (o1[0] + p0.y) * oscale, (o0[1] + p0.z) * oscale, (o1[1] + p0.w) * oscale);
         const float4 w1 = make_float4((o0[2] + p1.x) * oscale, (o1[2] + p1.y) * oscale, (o0[3] + p1.z) * oscale, (o1[3] + p1.w) * oscale);
-        if (vec) {
+        if (a.ns > 1) {
+            // split partials are read once, by the merge: streamed past the caches
+            store_nt4(out + 32 * bb, w0);
+            store_nt4(out + 32 * bb + 4, w1);
+        } else if (vec) {
             *(float4 *) (out + 32 * bb) = w0;
             *(float4 *) (out + 32 * bb + 4) = w1;
         } else {
@@ -1186,8 +1214,14 @@ extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor
     a.gqa_mul = recip32(pl.gqa);
 
     const int64_t units = (int64_t) a.B * a.ns >= 8 ? ((int64_t) a.B * a.ns + 7) / 8 * 8 : (int64_t) a.B * a.ns;
-    const int64_t grid = units * a.nh_kv * a.n_rg;
-    if (grid > 0x7fffffff) return set_error(QWFN_EINVAL, "flash_attn_ext: grid too large");
+    const int64_t hgn = (int64_t) a.nh_kv * a.n_rg;
+    const int64_t grid = units * hgn;
+    // block indices divide by ns, nh_kv * n_rg and n_rg through 32-bit reciprocals
+    if (grid * hgn >= (int64_t(1) << 32) || units * a.ns >= (int64_t(1) << 32))
+        return set_error(QWFN_ENOTSUP, "flash_attn_ext: grid too large");
+    a.ns_mul = recip32(a.ns);
+    a.hgn_mul = recip32(hgn);
+    a.nrg_mul = recip32(a.n_rg);
     hipStream_t st = as_stream(stream);
     const bool mt = a.mask_mode == MASK_TILE;
     const dim3 g((unsigned) grid), b8(WAVES * 64), b4(WAVES_PAIR * 64);
