@@ -306,6 +306,11 @@ __device__ __forceinline__ void store_nt4(float * p, float4 v) {
     __builtin_nontemporal_store(v4f{v.x, v.y, v.z, v.w}, (v4f *) p);
 }
 
+__device__ __forceinline__ float4 load_nt4(const float4 * p) {
+    const v4f v = __builtin_nontemporal_load((const v4f *) p);
+    return make_float4(v[0], v[1], v[2], v[3]);
+}
+
 // f[0 .. n) = 0 (dst is only 4-byte aligned, so plain f32 stores).
 __global__ void k_zero_f32(float * f, int64_t n) {
     const int64_t stride = (int64_t) gridDim.x * blockDim.x;
@@ -768,27 +773,27 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
             if (c + 1 < n_chunks) chunk_step(c + 1, ring[1], ring[0]);
         }
     }
-    __syncthreads();   // every wave is done with the last chunk: stage 0 becomes the merge buffer
-
-    // ---- merge the key groups of each row tile in LDS: every wave publishes
-    //      (max, sum) per row, then the groups add their weighted O into the
-    //      buffer in turn; group 0 adds last and writes the block's result ----
-    // [ROWS][OBS] f32, natural dim order; the padded row stride puts the 16
-    // rows a float4 access touches on different banks
-    constexpr int OBS = D + 4;
-    float * ob = (float *) ring[0];
-    float2 * ml = (float2 *) (ring[0] + ROWS * OBS * 4);           // [WAVES][16]
+    // ---- merge the key groups of each row tile: every wave publishes (max,
+    //      sum) per row in its own scale table (no other wave uses it), and
+    //      after one barrier the groups 1 .. KG-1 store their weighted O into
+    //      buffers of their own in the ring; after a second, group 0 adds them
+    //      to its own and writes the block's result ----
     {
         const float l = sum_lanes16_32(l_run);
-        if (lg == 0) ml[wave * 16 + ln] = make_float2(m_run, l);
+        float2 * mlw = (float2 *) &scl[wave][0][0][0];
+        if (lg == 0) mlw[ln] = make_float2(m_run, l);
     }
-    __syncthreads();
+    __syncthreads();   // every wave is done with the last chunk, and its (max, sum) are out
+    // [KG-1][ROWS][OBS] f32, natural dim order; the padded row stride puts the
+    // 16 rows a float4 access touches on different banks
+    constexpr int OBS = D + 4;
+    static_assert((KG - 1) * ROWS * OBS * 4 <= NS * C::STAGE, "group buffers fit in the ring");
     float M = -INFINITY, L = 0.f;
 #pragma unroll
-    for (int k2 = 0; k2 < KG; k2++) M = xmax(M, ml[(k2 * RT + tile) * 16 + ln].x);
+    for (int k2 = 0; k2 < KG; k2++) M = xmax(M, ((const float2 *) &scl[k2 * RT + tile][0][0][0])[ln].x);
 #pragma unroll
     for (int k2 = 0; k2 < KG; k2++) {
-        const float2 e = ml[(k2 * RT + tile) * 16 + ln];
+        const float2 e = ((const float2 *) &scl[k2 * RT + tile][0][0][0])[ln];
         L += e.x == -INFINITY ? 0.f : e.y * exp2f(e.x - M);
     }
     const float fw = m_run == -INFINITY ? 0.f : exp2f(m_run - M);
@@ -799,28 +804,18 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
     asm volatile("" : "+v"(tid_e));
     const int ln_e = tid_e & 15, lg_e = (tid_e >> 4) & 3;
     const int rl = 16 * tile + ln_e;
-    float * orow = ob + rl * OBS + 8 * lg_e;
-    for (int k2 = KG - 1; k2 >= 1; k2--) {
-        if (kg == k2) {
+    float * ob = (float *) &ring[0][0];
+    const int orow = rl * OBS + 8 * lg_e;          // the lane's first float in a group buffer
+    if (kg != 0) {
+        float * d = ob + (kg - 1) * ROWS * OBS + orow;
 #pragma unroll
-            for (int bb = 0; bb < NBLK; bb++) {
-                const v4f o0 = O[bb][0] * fw, o1 = O[bb][1] * fw;
-                float4 * d0 = (float4 *) (orow + 32 * bb);
-                float4 * d1 = (float4 *) (orow + 32 * bb + 4);
-                if (k2 == KG - 1) {
-                    *d0 = make_float4(o0[0], o1[0], o0[1], o1[1]);
-                    *d1 = make_float4(o0[2], o1[2], o0[3], o1[3]);
-                } else {
-                    float4 x0 = *d0, x1 = *d1;
-                    x0.x += o0[0]; x0.y += o1[0]; x0.z += o0[1]; x0.w += o1[1];
-                    x1.x += o0[2]; x1.y += o1[2]; x1.z += o0[3]; x1.w += o1[3];
-                    *d0 = x0;
-                    *d1 = x1;
-                }
-            }
+        for (int bb = 0; bb < NBLK; bb++) {
+            const v4f o0 = O[bb][0] * fw, o1 = O[bb][1] * fw;
+            *(float4 *) (d + 32 * bb) = make_float4(o0[0], o1[0], o0[1], o1[1]);
+            *(float4 *) (d + 32 * bb + 4) = make_float4(o0[2], o1[2], o0[3], o1[3]);
         }
-        __syncthreads();
     }
+    __syncthreads();
     if (kg != 0 || rl >= RW) return;
     const size_t bh = (size_t) b * a.nh_kv + kvh;
     const bool vec = a.ns > 1 || a.dst_vec;
@@ -842,10 +837,17 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
     }
 #pragma unroll
     for (int bb = 0; bb < NBLK; bb++) {
-        const float4 p0 = *(const float4 *) (orow + 32 * bb), p1 = *(const float4 *) (orow + 32 * bb + 4);
         const v4f o0 = O[bb][0] * fw, o1 = O[bb][1] * fw;
-        const float4 w0 = make_float4((o0[0] + p0.x) * oscale, (o1[0] + p0.y) * oscale, (o0[1] + p0.z) * oscale, (o1[1] + p0.w) * oscale);
-        const float4 w1 = make_float4((o0[2] + p1.x) * oscale, (o1[2] + p1.y) * oscale, (o0[3] + p1.z) * oscale, (o1[3] + p1.w) * oscale);
+        float4 p0 = make_float4(o0[0], o1[0], o0[1], o1[1]), p1 = make_float4(o0[2], o1[2], o0[3], o1[3]);
+#pragma unroll
+        for (int k2 = 1; k2 < KG; k2++) {
+            const float * src = ob + (k2 - 1) * ROWS * OBS + orow + 32 * bb;
+            const float4 x0 = *(const float4 *) src, x1 = *(const float4 *) (src + 4);
+            p0.x += x0.x; p0.y += x0.y; p0.z += x0.z; p0.w += x0.w;
+            p1.x += x1.x; p1.y += x1.y; p1.z += x1.z; p1.w += x1.w;
+        }
+        const float4 w0 = make_float4(p0.x * oscale, p0.y * oscale, p0.z * oscale, p0.w * oscale);
+        const float4 w1 = make_float4(p1.x * oscale, p1.y * oscale, p1.z * oscale, p1.w * oscale);
         if (a.ns > 1) {
             // split partials are read once, by the merge: streamed past the caches
             store_nt4(out + 32 * bb, w0);
@@ -913,7 +915,7 @@ __global__ __launch_bounds__(256) void k_fattn_merge(fa_args a) {
     for (int j = 0; j < MLJ; j++) e[j] = ml[(size_t) std::min((int) threadIdx.x + 256 * j, a.ns - 1) * a.R];
     float4 ob[MERGE_BATCH];
 #pragma unroll
-    for (int i = 0; i < MERGE_BATCH; i++) ob[i] = po[(size_t) std::min(g + i * MERGE_GROUPS, a.ns - 1) * sstride];
+    for (int i = 0; i < MERGE_BATCH; i++) ob[i] = load_nt4(po + (size_t) std::min(g + i * MERGE_GROUPS, a.ns - 1) * sstride);
     float mloc = -INFINITY;
 #pragma unroll
     for (int j = 0; j < MLJ; j++) {
@@ -942,7 +944,7 @@ __global__ __launch_bounds__(256) void k_fattn_merge(fa_args a) {
     for (int s0 = 0; s0 < a.ns; s0 += MERGE_GROUPS * MERGE_BATCH) {
         if (s0 > 0) {
 #pragma unroll
-            for (int i = 0; i < MERGE_BATCH; i++) ob[i] = po[(size_t) std::min(s0 + g + i * MERGE_GROUPS, a.ns - 1) * sstride];
+            for (int i = 0; i < MERGE_BATCH; i++) ob[i] = load_nt4(po + (size_t) std::min(s0 + g + i * MERGE_GROUPS, a.ns - 1) * sstride);
         }
 #pragma unroll
         for (int i = 0; i < MERGE_BATCH; i++) {
