@@ -79,18 +79,18 @@ struct fa_cfg {
     // two blocks per CU no more room)
     static constexpr int MLDS  = MT ? 16 : KWV == 32 ? MASK_LDS / 2 : MASK_LDS;
     static constexpr int CHUNK = CK * SEG;                  // one tensor's rows of a chunk
-    static constexpr int DMA_T = CHUNK / 1024;              // wave-wide 16-byte DMAs per tensor
+    static constexpr int DMA_T = (CHUNK + 1023) / 1024;     // wave-wide 16-byte DMAs per tensor
+    static constexpr int VOFF  = DMA_T * 1024;              // V rows' offset in a stage (K rows padded to whole DMAs)
     // MASK_TILE: a chunk's mask rows travel with it as 16-byte granules from
     // the 16-byte aligned address at or below each row's first key
     static constexpr int MGR   = 2 * CK / 16 + 1;           // granules per mask row
     static constexpr int MROWS = ROWS;                      // mask rows of a block, at most
     static constexpr int MDMA  = MT ? (MROWS * MGR + 63) / 64 : 0;   // wave-wide DMAs for them
     static constexpr int MTILE = MDMA * 1024;               // their bytes in a stage
-    static constexpr int STAGE = 2 * CHUNK + MTILE;         // one ring stage: K rows, V rows, mask tile
+    static constexpr int STAGE = 2 * VOFF + MTILE;          // one ring stage: K rows, V rows, mask tile
     static constexpr int SLOTS = 2 * DMA_T + MDMA;          // DMAs per chunk (the mask ones as needed)
     static constexpr int SPW   = (SLOTS + NW - 1) / NW;     // DMA slots per wave
-    static constexpr int NS    = RT == 2 && NW == WAVES ? 3 : 2;   // ring stages (chunks in flight + 1)
-    static_assert(CHUNK % 1024 == 0, "a chunk is whole wave-wide DMAs");
+    static constexpr int NS    = RT == 2 && NW == WAVES && KWV == 16 ? 3 : 2;   // ring stages (chunks in flight + 1)
     static_assert(SPW * NW - SLOTS < NW, "only a wave's last slot can be absent");
     static_assert(KWV == 16 || KWV == 32, "one or two 16-key tiles per wave");
 };
@@ -118,7 +118,7 @@ struct fa_args {
     int32_t  T, nh, nh_kv, gqa, R, B;
     int32_t  kb, vb;       // K/V batch extents (ne[3]); batch b reads b % kb
     int32_t  ns;           // key splits
-    int32_t  split_len;    // keys per split, multiple of the chunk
+    int32_t  split_len;    // keys per split, a multiple of the chunk (the last split runs to n_kv)
     int32_t  rw;           // query rows per block (16 * RT)
     int32_t  n_rg;         // row groups per KV head
     float    scale;
@@ -318,7 +318,7 @@ __global__ void k_zero_f32(float * f, int64_t n) {
 }
 
 template <int RT, bool MT, int NW, int KWV>
-__global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
+__global__ __launch_bounds__(NW * 64, NW / 4 > 2 ? NW / 4 : 2) void k_fattn_q8_0(fa_args a) {
     using C = fa_cfg<RT, MT, NW, KWV>;
     // the argument block's pointers are loaded with the rest, in one round of
     // scalar loads (not a second round after the exit of padding blocks)
@@ -326,7 +326,7 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
     constexpr int WAVES = NW;
     constexpr int KW = KWV;              // keys per wave per chunk
     constexpr int NKT = C::NKT;
-    constexpr int ROWS = C::ROWS, KG = C::KG, CK = C::CK, CHUNK = C::CHUNK, DMA_T = C::DMA_T;
+    constexpr int ROWS = C::ROWS, KG = C::KG, CK = C::CK, VOFF = C::VOFF, DMA_T = C::DMA_T;
     constexpr int SLOTS = C::SLOTS, SPW = C::SPW, NS = C::NS;
     // NS ring stages, each K rows [CK][272] and V rows [CK][272]
     __shared__ __attribute__((aligned(16))) uint8_t ring[NS][C::STAGE];
@@ -402,7 +402,7 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
         // one wave-wide DMA (1 KB) per query row; wave w takes rows w, w + NW, ...
         const v4i rq = make_rsrc(a.q + (size_t) b * a.q_nb3, a.q_slice);
 #pragma unroll
-        for (int j = 0; j < ROWS / WAVES; j++) {
+        for (int j = 0; j < (ROWS + WAVES - 1) / WAVES; j++) {
             const int rl = wave + WAVES * j;
             if (rl >= RW) break;
             const uint32_t r = (uint32_t) (r0 + rl);
@@ -432,10 +432,12 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
 
     // A chunk is SLOTS wave-wide 16-byte DMAs; slot s lands at byte 1024*s of
     // the stage: slots [0, DMA_T) are the K rows (piece p = 64*s + lane is byte
-    // 16*(p % 17) of key p / 17), the next DMA_T the V rows, then (MASK_TILE)
-    // the mask rows, granule G = 64*m + lane being granule G % MGR of row
-    // G / MGR. Wave w issues slots w, w + 8, ... The lane offsets within a chunk
-    // are the same for every chunk.
+    // 16*(p % 17) of key p / 17; when the rows end inside the last DMA, its
+    // remaining lanes read the next rows into the padding before VOFF), the
+    // next DMA_T the V rows, then (MASK_TILE) the mask rows, granule
+    // G = 64*m + lane being granule G % MGR of row G / MGR. Wave w issues slots
+    // w, w + NW, ... The lane offsets within a chunk are the same for every
+    // chunk.
     auto slot_off = [&](int slot) -> uint32_t {
         if (slot < 2 * DMA_T) {
             const int tensor = slot >= DMA_T;
@@ -469,10 +471,10 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
     // the lane's mask row in mlds (MASK_SPLIT)
     const uint32_t mlds_row = msplit ? (uint32_t) mrow0 * mstride + ((mrow_off(mrow0) + 2u * (uint32_t) k_lo) & 15u) : 0u;
 
-    // Chunk c is read through buffer resources based at its first key, sized
-    // to the bytes that exist: rows past n_kv arrive as zeros, and those keys
-    // are past the split, so they are masked.
-    const int64_t k_bytes = a.n_kv * (int64_t) a.k_nb1, v_bytes = a.n_kv * (int64_t) a.v_nb1;
+    // Chunk c is read through buffer resources based at its first key and
+    // ending at the split's last key: rows past the split arrive as zeros
+    // without a memory access, and those keys are masked.
+    const int64_t k_bytes = k_hi * (int64_t) a.k_nb1, v_bytes = k_hi * (int64_t) a.v_nb1;
     auto issue_chunk = [&](int c, uint8_t * dstb) __attribute__((always_inline)) {
         const int64_t c0 = k_lo + (int64_t) c * CK;
         const int64_t kc = c0 * (int64_t) a.k_nb1, vc = c0 * (int64_t) a.v_nb1;
@@ -485,7 +487,7 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
             dma16_buf(slot < DMA_T ? rk : rv, doff[s], __builtin_amdgcn_readfirstlane(lds_addr(dstb + slot * 1024)));
         }
         if constexpr (MT) {
-            // mask granules: the chunk's first key is 128-byte aligned within a row
+            // mask granules: the chunk's first key (a multiple of 8) is 16-byte aligned within a row
             const v4i rm = make_rsrc(mslice_al + c0 * 2, (uint32_t) (a.m_slice + (uint32_t) (mslice - mslice_al) - c0 * 2));
 #pragma unroll
             for (int s = 0; s < SPW; s++) {
@@ -509,13 +511,14 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
 
     // Requantisation: QL lanes per (row, block), QV values each; wave w takes
     // blocks w, w + NW, ... for all rows (QL * ROWS = 64 lanes).
-    constexpr int QL = 64 / ROWS, QV = 32 / QL, QIT = NBLK / WAVES;
-    static_assert(QL * ROWS == 64 && NBLK % WAVES == 0, "one block of all rows per wave and iteration");
+    constexpr int QL = 64 / ROWS, QV = 32 / QL, QIT = (NBLK + WAVES - 1) / WAVES;
+    static_assert(QL * ROWS == 64 && (NBLK % WAVES == 0 || WAVES > NBLK), "one block of all rows per wave and iteration");
     const int qrl = lane / QL, qh = lane % QL;
     float qx[QIT][QV];
 #pragma unroll
     for (int it = 0; it < QIT; it++) {
-        const float4 * src = (const float4 *) (qstage + qrl * 1024 + (QK * (wave + WAVES * it) + QV * qh) * 4);
+        const int blk = std::min(wave + WAVES * it, NBLK - 1);      // waves past the blocks read one, unused
+        const float4 * src = (const float4 *) (qstage + qrl * 1024 + (QK * blk + QV * qh) * 4);
 #pragma unroll
         for (int m = 0; m < QV / 4; m++) {
             const float4 v = qrl < RW ? src[m] : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -531,6 +534,7 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
 #pragma unroll
         for (int it = 0; it < QIT; it++) {
             const int blk = wave + WAVES * it;
+            if (WAVES > NBLK && blk >= NBLK) break;
             uint8_t * wrow = qwin + (qrl * NBLK + blk) * QWIN;
             // the lane's share of the window is zeroed first; the quants that
             // follow (written by lanes of this wave, whose LDS writes complete
@@ -599,7 +603,7 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
 #pragma unroll
             for (int i = 0; i < 4; i++) mv[kt][i] = 0;
         if constexpr (MT) {
-            const uint8_t * mp = cur + 2 * CHUNK + mtile_off + 2 * (kg * KW + lg * 4);
+            const uint8_t * mp = cur + 2 * VOFF + mtile_off + 2 * (kg * KW + lg * 4);
 #pragma unroll
             for (int kt = 0; kt < NKT; kt++)
 #pragma unroll
@@ -621,7 +625,7 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
             uint16_t * dstw = &sw[0][lane & 7][lane >> 3];
             uint16_t sv[NE];
 #pragma unroll
-            for (int n = 0; n < NE; n++) sv[n] = *(const uint16_t *) (src + (n / (2 * NKT)) * CHUNK + (n % (2 * NKT)) * 8 * SEG);
+            for (int n = 0; n < NE; n++) sv[n] = *(const uint16_t *) (src + (n / (2 * NKT)) * VOFF + (n % (2 * NKT)) * 8 * SEG);
 #pragma unroll
             for (int n = 0; n < NE; n++) dstw[(n / (2 * NKT)) * NBLK * KW + (n % (2 * NKT)) * 8] = sv[n];
         }
@@ -649,7 +653,8 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
                     s[kt][3] = __builtin_fmaf((float) cc[3], mul_f16hi(dq[bb], dk.y), s[kt][3]);
                 } else {
                     // (sum * d_q) * d_k: every step depends on the product, so
-                    // no scale product is formed (and held) ahead of it
+                    // no scale product is formed (and held) ahead of it (the
+                    // register budget of 32-key waves)
                     s[kt][0] = fma_f16lo(dk.x, (float) cc[0] * dq[bb], s[kt][0]);
                     s[kt][1] = fma_f16hi(dk.x, (float) cc[1] * dq[bb], s[kt][1]);
                     s[kt][2] = fma_f16lo(dk.y, (float) cc[2] * dq[bb], s[kt][2]);
@@ -712,7 +717,7 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
         //      2-byte LDS read per key. With two key tiles the reduction index
         //      4kt + i of the 16x16x32 MFMA is key 16kt + 4g + i, in the A and the
         //      B operand alike ----
-        const uint8_t * vrow = cur + CHUNK + (kg * KW + lg * 4) * SEG + 2 + 2 * ln;
+        const uint8_t * vrow = cur + VOFF + (kg * KW + lg * 4) * SEG + 2 + 2 * ln;
         // PVB blocks at a time: all their LDS reads first (one 2-byte read per
         // key and block, each in its own register), so their latencies overlap
         constexpr int PVB = PV_BATCH;
@@ -784,10 +789,13 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
         if (lg == 0) mlw[ln] = make_float2(m_run, l);
     }
     __syncthreads();   // every wave is done with the last chunk, and its (max, sum) are out
-    // [KG-1][ROWS][OBS] f32, natural dim order; the padded row stride puts the
-    // 16 rows a float4 access touches on different banks
+    // [NBUF][ROWS][OBS] f32, natural dim order; the padded row stride puts the
+    // 16 rows a float4 access touches on different banks. With more groups
+    // than buffers fit in the ring, they take turns (ROUNDS).
     constexpr int OBS = D + 4;
-    static_assert((KG - 1) * ROWS * OBS * 4 <= NS * C::STAGE, "group buffers fit in the ring");
+    constexpr int NBUF = std::min(KG - 1, NS * C::STAGE / (ROWS * OBS * 4));
+    constexpr int ROUNDS = KG == 1 ? 0 : (KG - 1 + NBUF - 1) / NBUF;
+    static_assert(KG == 1 || NBUF >= 1, "a group buffer fits in the ring");
     float M = -INFINITY, L = 0.f;
 #pragma unroll
     for (int k2 = 0; k2 < KG; k2++) M = xmax(M, ((const float2 *) &scl[k2 * RT + tile][0][0][0])[ln].x);
@@ -806,16 +814,38 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
     const int rl = 16 * tile + ln_e;
     float * ob = (float *) &ring[0][0];
     const int orow = rl * OBS + 8 * lg_e;          // the lane's first float in a group buffer
-    if (kg != 0) {
-        float * d = ob + (kg - 1) * ROWS * OBS + orow;
+    // the lane's 8 dims of block bb in natural order: acc[bb][0] dims 0..3, acc[bb][1] dims 4..7
+    float4 acc[NBLK][2];
 #pragma unroll
-        for (int bb = 0; bb < NBLK; bb++) {
-            const v4f o0 = O[bb][0] * fw, o1 = O[bb][1] * fw;
-            *(float4 *) (d + 32 * bb) = make_float4(o0[0], o1[0], o0[1], o1[1]);
-            *(float4 *) (d + 32 * bb + 4) = make_float4(o0[2], o1[2], o0[3], o1[3]);
-        }
+    for (int bb = 0; bb < NBLK; bb++) {
+        const v4f o0 = O[bb][0] * fw, o1 = O[bb][1] * fw;
+        acc[bb][0] = make_float4(o0[0], o1[0], o0[1], o1[1]);
+        acc[bb][1] = make_float4(o0[2], o1[2], o0[3], o1[3]);
     }
-    __syncthreads();
+    for (int rd = 0; rd < ROUNDS; rd++) {
+        if (kg != 0 && (kg - 1) / NBUF == rd) {
+            float * d = ob + ((kg - 1) % NBUF) * ROWS * OBS + orow;
+#pragma unroll
+            for (int bb = 0; bb < NBLK; bb++) {
+                *(float4 *) (d + 32 * bb) = acc[bb][0];
+                *(float4 *) (d + 32 * bb + 4) = acc[bb][1];
+            }
+        }
+        __syncthreads();
+        if (kg == 0 && rl < RW) {
+            const int nb = std::min(NBUF, KG - 1 - rd * NBUF);
+            for (int k2 = 0; k2 < nb; k2++) {
+#pragma unroll
+                for (int bb = 0; bb < NBLK; bb++) {
+                    const float * src = ob + k2 * ROWS * OBS + orow + 32 * bb;
+                    const float4 x0 = *(const float4 *) src, x1 = *(const float4 *) (src + 4);
+                    acc[bb][0].x += x0.x; acc[bb][0].y += x0.y; acc[bb][0].z += x0.z; acc[bb][0].w += x0.w;
+                    acc[bb][1].x += x1.x; acc[bb][1].y += x1.y; acc[bb][1].z += x1.z; acc[bb][1].w += x1.w;
+                }
+            }
+        }
+        if (rd + 1 < ROUNDS) __syncthreads();   // the buffers are read before the next round overwrites them
+    }
     if (kg != 0 || rl >= RW) return;
     const size_t bh = (size_t) b * a.nh_kv + kvh;
     const bool vec = a.ns > 1 || a.dst_vec;
@@ -837,15 +867,7 @@ __global__ __launch_bounds__(NW * 64, 2) void k_fattn_q8_0(fa_args a) {
     }
 #pragma unroll
     for (int bb = 0; bb < NBLK; bb++) {
-        const v4f o0 = O[bb][0] * fw, o1 = O[bb][1] * fw;
-        float4 p0 = make_float4(o0[0], o1[0], o0[1], o1[1]), p1 = make_float4(o0[2], o1[2], o0[3], o1[3]);
-#pragma unroll
-        for (int k2 = 1; k2 < KG; k2++) {
-            const float * src = ob + (k2 - 1) * ROWS * OBS + orow + 32 * bb;
-            const float4 x0 = *(const float4 *) src, x1 = *(const float4 *) (src + 4);
-            p0.x += x0.x; p0.y += x0.y; p0.z += x0.z; p0.w += x0.w;
-            p1.x += x1.x; p1.y += x1.y; p1.z += x1.z; p1.w += x1.w;
-        }
+        const float4 p0 = acc[bb][0], p1 = acc[bb][1];
         const float4 w0 = make_float4(p0.x * oscale, p0.y * oscale, p0.z * oscale, p0.w * oscale);
         const float4 w1 = make_float4(p1.x * oscale, p1.y * oscale, p1.z * oscale, p1.w * oscale);
         if (a.ns > 1) {
@@ -1106,21 +1128,22 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
                      : pl->kind == FA_P4_T1 ? fa_cfg<1, false, WAVES_PAIR, 16>::CK
                                             : fa_cfg<2, false, WAVES_PAIR, 32>::CK;
     // Splits: about one block per CU slot (256 or 512), each at least one chunk.
-    const int64_t target_blocks = env_int("QWFN_FA_BLOCKS", pair ? 512 : 256);
+    const int64_t target_blocks = env_int("QWFN_FA_BLOCKS", pl->kind == FA_P4_T1 || pl->kind == FA_P4_T2 ? 512 : 256);
     int64_t ns = std::max<int64_t>(1, target_blocks / std::max<int64_t>(1, nh_kv * B * pl->n_rg));
     ns = std::min<int64_t>(ns, std::max<int64_t>(1, (n_kv + ck - 1) / ck));
     if (const int force = env_int("QWFN_FA_SPLITS", 0)) ns = force;
-    // Splits of whole chunks. When the keys exceed two or more whole chunks
-    // per split by less than one chunk (n_kv = 2^k + T), the last split takes
-    // the rest; otherwise every split gets one chunk more and there are fewer.
+    // Splits are whole chunks. When the keys exceed two or more chunks per
+    // split by less than one chunk (n_kv = 2^k + T), the last split takes the
+    // rest; otherwise every split rounds up and there are fewer.
     int64_t split_len = n_kv / (ns * ck) * ck;
     if (split_len < 2 * ck || n_kv - ns * split_len >= ck || !env_int("QWFN_FA_ABSORB", 1)) {
         split_len = (n_kv + ns - 1) / ns;
         split_len = std::max<int64_t>(ck, (split_len + ck - 1) / ck * ck);
         ns = std::max<int64_t>(1, (n_kv + split_len - 1) / split_len);
     }
-    pl->max_span = n_kv - (ns - 1) * split_len;
-    pl->max_span = std::max<int64_t>(split_len, (pl->max_span + ck - 1) / ck * ck);
+    // keys of the longest split (the last may be longer), rounded up to whole chunks
+    pl->max_span = std::max<int64_t>(split_len, n_kv - (ns - 1) * split_len);
+    pl->max_span = (pl->max_span + ck - 1) / ck * ck;
     if (ns > MAX_SPLITS)
         return set_error(QWFN_ENOTSUP, "flash_attn_ext: " + std::to_string(ns) + " key splits requested, at most " +
                                            std::to_string(MAX_SPLITS) + " supported");
