@@ -637,30 +637,50 @@ __global__ __launch_bounds__(NW * 64, NW / 4 > 2 ? NW / 4 : 2) void k_fattn_q8_0
         for (int kt = 0; kt < NKT; kt++)
 #pragma unroll
             for (int i = 0; i < 4; i++) s[kt][i] = 0.f;
+        // QKB blocks at a time: their K and scale reads, then their MFMAs, then
+        // the scaling, so the reads' and the MFMAs' latencies overlap (with two
+        // key tiles, all eight blocks at once would not fit the registers)
+        constexpr int QKB = NKT == 1 ? NBLK : NBLK / 2;
 #pragma unroll
-        for (int bb = 0; bb < NBLK; bb++) {
+        for (int b0 = 0; b0 < NBLK; b0 += QKB) {
+            v4i kA[QKB][NKT];
+            uint2 dk[QKB][NKT];
 #pragma unroll
-            for (int kt = 0; kt < NKT; kt++) {
-                // A operand: key row 16*kt + ln of the wave, window slice lg
-                const uint8_t * krow = cur + (kg * KW + 16 * kt + ln) * SEG + 16 * lg;
-                const v4i kA = *(const v4i *) (krow + 16 * win_piece(bb));
-                const uint2 dk = *(const uint2 *) &sw[0][bb][16 * kt + lg * 4];   // the lane's 4 keys' fp16 d_k
-                const v4i cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kA, qw[bb], v4i{0, 0, 0, 0}, 0, 0, 0);
-                if constexpr (NKT == 1) {
-                    s[kt][0] = __builtin_fmaf((float) cc[0], mul_f16lo(dq[bb], dk.x), s[kt][0]);
-                    s[kt][1] = __builtin_fmaf((float) cc[1], mul_f16hi(dq[bb], dk.x), s[kt][1]);
-                    s[kt][2] = __builtin_fmaf((float) cc[2], mul_f16lo(dq[bb], dk.y), s[kt][2]);
-                    s[kt][3] = __builtin_fmaf((float) cc[3], mul_f16hi(dq[bb], dk.y), s[kt][3]);
-                } else {
-                    // (sum * d_q) * d_k: every step depends on the product, so
-                    // no scale product is formed (and held) ahead of it (the
-                    // register budget of 32-key waves)
-                    s[kt][0] = fma_f16lo(dk.x, (float) cc[0] * dq[bb], s[kt][0]);
-                    s[kt][1] = fma_f16hi(dk.x, (float) cc[1] * dq[bb], s[kt][1]);
-                    s[kt][2] = fma_f16lo(dk.y, (float) cc[2] * dq[bb], s[kt][2]);
-                    s[kt][3] = fma_f16hi(dk.y, (float) cc[3] * dq[bb], s[kt][3]);
+            for (int u = 0; u < QKB; u++)
+#pragma unroll
+                for (int kt = 0; kt < NKT; kt++) {
+                    // A operand: key row 16*kt + ln of the wave, window slice lg
+                    const uint8_t * krow = cur + (kg * KW + 16 * kt + ln) * SEG + 16 * lg;
+                    kA[u][kt] = *(const v4i *) (krow + 16 * win_piece(b0 + u));
+                    dk[u][kt] = *(const uint2 *) &sw[0][b0 + u][16 * kt + lg * 4];   // the lane's 4 keys' fp16 d_k
                 }
-            }
+            v4i cc[QKB][NKT];
+#pragma unroll
+            for (int u = 0; u < QKB; u++)
+#pragma unroll
+                for (int kt = 0; kt < NKT; kt++)
+                    cc[u][kt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kA[u][kt], qw[b0 + u], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int u = 0; u < QKB; u++)
+#pragma unroll
+                for (int kt = 0; kt < NKT; kt++) {
+                    const float d = dq[b0 + u];
+                    if constexpr (NKT == 1) {
+                        s[kt][0] = __builtin_fmaf((float) cc[u][kt][0], mul_f16lo(d, dk[u][kt].x), s[kt][0]);
+                        s[kt][1] = __builtin_fmaf((float) cc[u][kt][1], mul_f16hi(d, dk[u][kt].x), s[kt][1]);
+                        s[kt][2] = __builtin_fmaf((float) cc[u][kt][2], mul_f16lo(d, dk[u][kt].y), s[kt][2]);
+                        s[kt][3] = __builtin_fmaf((float) cc[u][kt][3], mul_f16hi(d, dk[u][kt].y), s[kt][3]);
+                    } else {
+                        // (sum * d_q) * d_k: no scale product is formed (and
+                        // held) ahead of the MFMA results (the register budget
+                        // of 32-key waves)
+                        s[kt][0] = fma_f16lo(dk[u][kt].x, (float) cc[u][kt][0] * d, s[kt][0]);
+                        s[kt][1] = fma_f16hi(dk[u][kt].x, (float) cc[u][kt][1] * d, s[kt][1]);
+                        s[kt][2] = fma_f16lo(dk[u][kt].y, (float) cc[u][kt][2] * d, s[kt][2]);
+                        s[kt][3] = fma_f16hi(dk[u][kt].y, (float) cc[u][kt][3] * d, s[kt][3]);
+                    }
+                }
+            if (b0 + QKB < NBLK) __builtin_amdgcn_sched_barrier(0);
         }
 
         // ---- mask, online softmax (base 2; scores are already in log2 units).
