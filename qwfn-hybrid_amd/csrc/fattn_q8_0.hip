@@ -16,12 +16,14 @@
 //            groups of one split sit on the same XCD and are dispatched next to
 //            each other, so the cache lines two heads share (a 272-byte head row
 //            is not line aligned) come from one L2.
-//   block  : 8 wavefronts (two per SIMD), RT 16-row query tiles x 8/RT key
-//            groups of 16 keys. Keys are streamed in chunks of 16*8/RT raw
-//            272-byte head rows with gfx950's LDS DMA (global_load_lds_dwordx4,
-//            SGPR base + per-lane offset) into a two-stage ring: chunk c+1 is in
-//            flight while chunk c is computed. The block requantises its own
-//            query rows into LDS while chunk 0 loads.
+//   block  : 4 wavefronts, two blocks per CU (RT 16-row query tiles x 4/RT
+//            key groups of 16 or 32 keys), or 8 wavefronts, one block per CU
+//            (8/RT key groups of 16 keys). Keys stream in chunks of raw 272-byte
+//            head rows through gfx950's LDS DMA (buffer_load_dwordx4 ... lds)
+//            into a ring of 2 or 3 stages, so one or two chunks are in flight
+//            while one is computed. Query rows and split masks arrive by the
+//            same DMA ahead of the first chunks, and the block requantises its
+//            query rows while those chunks load.
 //   QK^T   : v_mfma_i32_16x16x64_i8 per q8_0 block. The A operand is four
 //            16-byte aligned pieces of the raw K row that cover the block's 32
 //            quants (a 64-byte window); the B operand is the requantised query
@@ -32,9 +34,10 @@
 //            with cross-row lane swaps. The running max may lag the true max by
 //            up to 2^8 (p <= 256), so the accumulators are rescaled only when
 //            the max jumps by more than that.
-//   PV     : v_mfma_f32_16x16x16_f16, A = V^T (int8 -> f16 exact, SDWA byte
-//            select from naturally aligned 2-byte LDS reads), B = P*d_v of one V
-//            block as f16 hi + lo.
+//   PV     : v_mfma_f32_16x16x16_f16 (16-key waves) or 16x16x32 (32-key
+//            waves), A = V^T (int8 -> f16 exact, SDWA byte select from
+//            naturally aligned 2-byte LDS reads), B = P*d_v of one V block as
+//            f16 hi + lo.
 //   merge  : the key groups of a block merge in LDS; key splits merge in a
 //            second kernel (log-sum-exp weights), one block per quarter row.
 #include "q8_device.h"
@@ -1129,14 +1132,9 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
     int rw = R > 16 ? 32 : 16;
     if (const int force = env_int("QWFN_FA_ROWS", 0)) rw = force >= 32 ? 32 : 16;
     // 4-wave blocks, two per CU (their prologues and phases overlap), or
-    // 8-wave blocks, one per CU. One tile: 4 waves. Two tiles: 4 waves of 32
-    // keys each when 8-wave blocks (one per CU) would get fewer than 4 chunks
-    // each, else 8 waves. QWFN_FA_PAIR=0 forces 8 waves, =1 4 waves.
+    // 8-wave blocks, one per CU. QWFN_FA_PAIR=0 forces 8 waves.
     const int64_t B = q->ne[3];
-    const int pair_env = env_int("QWFN_FA_PAIR", -1);
-    const int64_t groups = nh_kv * B * ((R + rw - 1) / rw);
-    const int64_t splits8 = std::max<int64_t>(1, 256 / groups);
-    const bool pair = pair_env >= 0 ? pair_env != 0 : rw == 16 || n_kv < 4 * 64 * splits8;
+    const bool pair = env_int("QWFN_FA_PAIR", 1) != 0;
     pl->kind = rw == 16 ? (pair ? FA_P4_T1 : FA_W8_T1) : (pair ? FA_P4_T2 : FA_W8_T2);
     pl->R = (int32_t) R;
     pl->rw = rw;
