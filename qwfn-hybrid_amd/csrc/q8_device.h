@@ -51,16 +51,34 @@ __device__ __forceinline__ q8_scale q8_block_scale(float amax, bool x86) {
     return s;
 }
 
+// The low bytes of four int32 in one dword (byte j from q[j]): two byte
+// permutes and an or.
+__device__ __forceinline__ uint32_t pack_low_bytes(const int32_t q[4]) {
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t) q[1], (uint32_t) q[0], 0x0c0c0400u);   // q0.b0, q1.b0, 0, 0
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t) q[3], (uint32_t) q[2], 0x04000c0cu);   // 0, 0, q2.b0, q3.b0
+    return lo | hi;
+}
+
 __device__ __forceinline__ uint32_t q8_pack4(const float x[4], float id, bool x86) {
-    uint32_t w = 0;
+    int32_t q[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const float v = x[j] * id;
-        const int32_t q = x86 ? q8_round_x86(v) : q8_round_ref(v);
-        w |= ((uint32_t) (q & 0xff)) << (8 * j);
+        q[j] = x86 ? q8_round_x86(v) : q8_round_ref(v);
     }
-    return w;
+    return pack_low_bytes(q);
 }
+
+// x86 element for a block whose amax is a finite float of at least 2^-100:
+// then |x * id| <= 127 * (1 + 2^-22), so rint lands in [-127, 127] and neither
+// the range check nor the saturation of q8_round_x86 can act.
+__device__ __forceinline__ uint32_t q8_pack4_x86_normal(const float x[4], float id) {
+    int32_t q[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) q[j] = (int32_t) __builtin_rintf(x[j] * id);
+    return pack_low_bytes(q);
+}
+constexpr uint32_t Q8_AMAX_NORMAL_MIN = 0x0d800000u;   // 2^-100 as float bits
 
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
     return __builtin_bit_cast(uint16_t, (_Float16) f);
@@ -92,8 +110,13 @@ __device__ __forceinline__ void q8_quantize_lanes(const float (&x)[V], bool x86,
     const q8_scale s = q8_block_scale(amax, x86);
     *d16 = f32_to_f16_bits(s.d);
     *dq = f16_bits_to_f32(*d16);
+    if (x86 && am >= Q8_AMAX_NORMAL_MIN && am < 0x7f800000u) {
 #pragma unroll
-    for (int m = 0; m < V / 4; m++) w[m] = q8_pack4(&x[4 * m], s.id, x86);
+        for (int m = 0; m < V / 4; m++) w[m] = q8_pack4_x86_normal(&x[4 * m], s.id);
+    } else {
+#pragma unroll
+        for (int m = 0; m < V / 4; m++) w[m] = q8_pack4(&x[4 * m], s.id, x86);
+    }
 }
 
 // The same for 4 values per lane over 8 lanes; returns the packed quad.
