@@ -620,6 +620,11 @@ __global__ __launch_bounds__(NW * 64, NW / 4 > 2 ? NW / 4 : 2) void k_fattn_q8_0
         } else if (c * CK + kg * KW >= span) {
             return;
         }
+        // The rest of the step, for the wave's first NL key tiles: a tile
+        // whose keys are all past the split (the last chunk of a split) is
+        // neither multiplied nor converted.
+        auto compute = [&](auto nl_tag) __attribute__((always_inline)) {
+        constexpr int NL = decltype(nl_tag)::value;
         // this wave's keys' block scales, transposed to [block][key]: entry n of
         // a lane is tensor n / (2 NKT), key (n % (2 NKT)) * 8 + lane / 8, block lane % 8
         {
@@ -651,7 +656,7 @@ __global__ __launch_bounds__(NW * 64, NW / 4 > 2 ? NW / 4 : 2) void k_fattn_q8_0
 #pragma unroll
             for (int u = 0; u < QKB; u++)
 #pragma unroll
-                for (int kt = 0; kt < NKT; kt++) {
+                for (int kt = 0; kt < NL; kt++) {
                     // A operand: key row 16*kt + ln of the wave, window slice lg
                     const uint8_t * krow = cur + (kg * KW + 16 * kt + ln) * SEG + 16 * lg;
                     kA[u][kt] = *(const v4i *) (krow + 16 * win_piece(b0 + u));
@@ -661,12 +666,12 @@ __global__ __launch_bounds__(NW * 64, NW / 4 > 2 ? NW / 4 : 2) void k_fattn_q8_0
 #pragma unroll
             for (int u = 0; u < QKB; u++)
 #pragma unroll
-                for (int kt = 0; kt < NKT; kt++)
+                for (int kt = 0; kt < NL; kt++)
                     cc[u][kt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kA[u][kt], qw[b0 + u], v4i{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
             for (int u = 0; u < QKB; u++)
 #pragma unroll
-                for (int kt = 0; kt < NKT; kt++) {
+                for (int kt = 0; kt < NL; kt++) {
                     const float d = dq[b0 + u];
                     if constexpr (NKT == 1) {
                         s[kt][0] = __builtin_fmaf((float) cc[u][kt][0], mul_f16lo(d, dk[u][kt].x), s[kt][0]);
@@ -751,7 +756,7 @@ __global__ __launch_bounds__(NW * 64, NW / 4 > 2 ? NW / 4 : 2) void k_fattn_q8_0
 #pragma unroll
             for (int u = 0; u < PVB; u++)
 #pragma unroll
-                for (int kt = 0; kt < NKT; kt++) {
+                for (int kt = 0; kt < NL; kt++) {
 #pragma unroll
                     for (int j = 0; j < 4; j++)
                         w[u][kt][j] = *(const uint16_t *) (vrow + (16 * kt + j) * SEG + (b0 + u) * QBLOCK);
@@ -763,9 +768,15 @@ __global__ __launch_bounds__(NW * 64, NW / 4 > 2 ? NW / 4 : 2) void k_fattn_q8_0
                 uint32_t a0[NKT][2], a1[NKT][2], bh[NKT][2], bl[NKT][2];
 #pragma unroll
                 for (int kt = 0; kt < NKT; kt++) {
-                    const uint32_t dv[2] = {dv2[u][kt].x, dv2[u][kt].y};
-                    cvt_v_block(w[u][kt], a0[kt], a1[kt]);
-                    pdv_hilo(p[kt], dv, bh[kt], bl[kt]);
+                    if (kt < NL) {
+                        const uint32_t dv[2] = {dv2[u][kt].x, dv2[u][kt].y};
+                        cvt_v_block(w[u][kt], a0[kt], a1[kt]);
+                        pdv_hilo(p[kt], dv, bh[kt], bl[kt]);
+                    } else {
+                        // a key tile wholly past the split: zero operands
+                        a0[kt][0] = a0[kt][1] = a1[kt][0] = a1[kt][1] = 0u;
+                        bh[kt][0] = bh[kt][1] = bl[kt][0] = bl[kt][1] = 0u;
+                    }
                 }
                 if constexpr (NKT == 1) {
                     const v4h A0 = __builtin_bit_cast(v4h, make_uint2(a0[0][0], a0[0][1]));
@@ -788,6 +799,14 @@ __global__ __launch_bounds__(NW * 64, NW / 4 > 2 ? NW / 4 : 2) void k_fattn_q8_0
                 }
             }
         }
+        };
+        if constexpr (NKT == 2) {
+            if (c * CK + kg * KW + 16 >= span) {
+                compute(std::integral_constant<int, 1>{});
+                return;
+            }
+        }
+        compute(std::integral_constant<int, NKT>{});
     };
     if constexpr (NS == 3) {
         for (int c = 0; c < n_chunks; c += 3) {
