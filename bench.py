@@ -106,17 +106,20 @@ def measure_rows(K, torch, np, dev, gen) -> dict:
     kv_dim, nh, nh_kv, hd = 512, 16, 2, 256
     gbs = lambda b, us: round(b / (us * 1e-6) / 1e9, 1)
 
-    # ---- append: cpy of a 512-row F32 chunk into the q8_0 cache (K and V: 2 launches) ----
+    # ---- append: cpy of a 512-row F32 chunk of K and of V into the q8_0 caches
+    #      (one launch), and the decode step's 3-row set_rows of K and V ----
     n_ctx, d0, T = 16384 + 512, 16384, 512
     caches = [torch.zeros((n_ctx, ROW), dtype=torch.uint8, device=dev) for _ in range(8)]
     srcs = [torch.randn((T, kv_dim), generator=gen, device=dev) for _ in range(8)]
-    us = timed_graph(torch, lambda k: K.cpy_f32_q8_0(srcs[k % 8], caches[(k * 3) % 8], d0), 64, 10)
-    b = T * (kv_dim * 4 + ROW)
-    rows["append_512"] = {"us_per_launch": round(us, 3), "bytes_per_launch": b, "GBs": gbs(b, us),
-                          "frac": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    us = timed_graph(torch, lambda k: K.cpy_f32_q8_0_kv(srcs[k % 8], caches[(k * 3) % 8], srcs[(k + 1) % 8],
+                                                        caches[(k * 3 + 1) % 8], d0), 64, 10)
+    b = 2 * T * (kv_dim * 4 + ROW)
+    rows["append_kv_512"] = {"us_per_launch": round(us, 3), "bytes_per_launch": b, "GBs": gbs(b, us),
+                             "frac": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
     idx = torch.arange(d0, d0 + 3, dtype=torch.int32, device=dev)
-    us = timed_graph(torch, lambda k: K.set_rows_q8_0(caches[k % 8], srcs[k % 8][:3], idx), 64, 10)
-    rows["append_3_rows"] = {"us_per_launch": round(us, 3), "bytes_per_launch": 3 * (kv_dim * 4 + ROW)}
+    us = timed_graph(torch, lambda k: K.set_rows_q8_0_kv(caches[k % 8], srcs[k % 8][:3], caches[(k + 1) % 8],
+                                                         srcs[(k + 1) % 8][:3], idx), 64, 10)
+    rows["append_kv_3_rows"] = {"us_per_launch": round(us, 3), "bytes_per_launch": 2 * 3 * (kv_dim * 4 + ROW)}
     del caches, srcs
 
     # ---- sparse gather: per KV head, top-128 of 1024 blocks of 64 positions by uniform
@@ -297,8 +300,7 @@ def main() -> int:
     def step(s):
         for l in range(L):
             kc, vc = caches[s][l]
-            K.set_rows_q8_0(kc, newk[l], idx)
-            K.set_rows_q8_0(vc, newv[l], idx)
+            K.set_rows_q8_0_kv(kc, newk[l], vc, newv[l], idx)   # the layer's K and V set_rows, one launch
             attn(s, l)
 
     # algorithmic bytes: every cached K/V row read once, the appended rows
@@ -318,8 +320,7 @@ def main() -> int:
     try:
         import kvdata as KD
         kc, vc = caches[0][0]
-        K.set_rows_q8_0(kc, newk[0], idx)
-        K.set_rows_q8_0(vc, newv[0], idx)
+        K.set_rows_q8_0_kv(kc, newk[0], vc, newv[0], idx)
         attn(0, 0)
         torch.cuda.synchronize()
         got = out[0].cpu().numpy()[0]

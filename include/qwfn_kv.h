@@ -96,6 +96,17 @@ int qwfn_set_rows_q8_0(const qwfn_tensor * dst, const qwfn_tensor * src, const q
  * and :916-921 (mtp_head_kv). */
 int qwfn_cpy_f32_q8_0(const qwfn_tensor * src, const qwfn_tensor * dst, int variant, void * stream);
 
+/* The K and the V append of one layer in one launch: the two adjacent
+ * ggml_set_rows nodes with the same idx at qwfn_graph.cpp:623-624
+ * (qsa_dec_kv_write), or the two adjacent ggml_cpy nodes at :376-383
+ * (kv_append) and :916-921 (mtp_head_kv). Each pair is checked as two calls of
+ * the single-tensor entry point would be, and src_k and src_v must have the
+ * same shape; the result is byte-identical to those two calls. */
+int qwfn_set_rows_q8_0_kv(const qwfn_tensor * dst_k, const qwfn_tensor * src_k, const qwfn_tensor * dst_v,
+                          const qwfn_tensor * src_v, const qwfn_tensor * idx, int variant, void * stream);
+int qwfn_cpy_f32_q8_0_kv(const qwfn_tensor * src_k, const qwfn_tensor * dst_k, const qwfn_tensor * src_v,
+                         const qwfn_tensor * dst_v, int variant, void * stream);
+
 /* -------------------------------------------------------------- gather */
 
 /* ggml_get_rows(src, idx) on I32 words: src I32 [ne0, n_rows], idx I32 [n]

@@ -34,7 +34,7 @@ struct append_args {
 };
 
 template <bool VEC4>
-__global__ __launch_bounds__(APPEND_THREADS) void k_append_q8_0(append_args a) {
+__device__ __forceinline__ void append_rows(const append_args & a) {
     const int64_t gblk = (int64_t) blockIdx.x * (APPEND_THREADS / 8) + (threadIdx.x >> 3);
     const int     sub  = threadIdx.x & 7;               // 4-value group within the block
     const int64_t total = a.n * a.bpr;
@@ -76,6 +76,17 @@ __global__ __launch_bounds__(APPEND_THREADS) void k_append_q8_0(append_args a) {
     if (sub == 0) *(uint16_t *) bp = d16;
 }
 
+template <bool VEC4>
+__global__ __launch_bounds__(APPEND_THREADS) void k_append_q8_0(append_args a) {
+    append_rows<VEC4>(a);
+}
+
+// The K and the V rows of one append in one launch: blockIdx.y picks the tensor.
+template <bool VEC4>
+__global__ __launch_bounds__(APPEND_THREADS) void k_append_q8_0_kv(append_args k, append_args v) {
+    append_rows<VEC4>(blockIdx.y ? v : k);
+}
+
 int launch_append(const append_args & a, bool vec4, hipStream_t stream) {
     const int64_t blocks = a.n * a.bpr;
     if (blocks == 0) return QWFN_OK;
@@ -83,6 +94,17 @@ int launch_append(const append_args & a, bool vec4, hipStream_t stream) {
     if (grid > 0x7fffffff) return set_error(QWFN_EINVAL, "append: too many rows");
     if (vec4) hipLaunchKernelGGL(k_append_q8_0<true>, dim3((unsigned) grid), dim3(APPEND_THREADS), 0, stream, a);
     else      hipLaunchKernelGGL(k_append_q8_0<false>, dim3((unsigned) grid), dim3(APPEND_THREADS), 0, stream, a);
+    return hip_check(hipGetLastError(), "append launch");
+}
+
+// k and v have the same n and bpr (checked by the callers).
+int launch_append_kv(const append_args & k, const append_args & v, bool vec4, hipStream_t stream) {
+    const int64_t blocks = k.n * k.bpr;
+    if (blocks == 0) return QWFN_OK;
+    const int64_t grid = (blocks + APPEND_THREADS / 8 - 1) / (APPEND_THREADS / 8);
+    if (grid > 0x7fffffff) return set_error(QWFN_EINVAL, "append: too many rows");
+    if (vec4) hipLaunchKernelGGL(k_append_q8_0_kv<true>, dim3((unsigned) grid, 2), dim3(APPEND_THREADS), 0, stream, k, v);
+    else      hipLaunchKernelGGL(k_append_q8_0_kv<false>, dim3((unsigned) grid, 2), dim3(APPEND_THREADS), 0, stream, k, v);
     return hip_check(hipGetLastError(), "append launch");
 }
 
@@ -107,13 +129,11 @@ int check_dst_q8(const qwfn_tensor * dst, int64_t ne0, const char * op) {
     return QWFN_OK;
 }
 
-}  // namespace
-}  // namespace qwfn
 
-using namespace qwfn;
-
-extern "C" int qwfn_set_rows_q8_0(const qwfn_tensor * dst, const qwfn_tensor * src, const qwfn_tensor * idx,
-                                  int variant, void * stream) {
+// Checks one ggml_set_rows(dst, src, idx) and fills its arguments (all but the
+// status word, taken once every check of a call has passed).
+int set_rows_args(const qwfn_tensor * dst, const qwfn_tensor * src, const qwfn_tensor * idx, int variant,
+                  append_args * a, bool * vec4) {
     if (int rc = check_src_f32(src, "set_rows")) return rc;
     if (int rc = check_dst_q8(dst, src->ne[0], "set_rows")) return rc;
     if (!idx || !idx->data) return set_error(QWFN_EINVAL, "set_rows: idx is NULL");
@@ -122,33 +142,81 @@ extern "C" int qwfn_set_rows_q8_0(const qwfn_tensor * dst, const qwfn_tensor * s
         return set_error(QWFN_EINVAL, "set_rows: idx must be [n] with n == src ne[1]");
     if (!is_aligned(idx->data, 4) || idx->nb[0] % 4) return set_error(QWFN_EALIGN, "set_rows: idx must be 4-byte aligned");
     if (variant != QWFN_Q8_REF && variant != QWFN_Q8_X86) return set_error(QWFN_EINVAL, "set_rows: unknown rounding variant");
-    uint32_t * st = nullptr;
-    if (int rc = status_word(&st)) return rc;
-    append_args a{};
-    a.src = (const char *) src->data; a.src_nb1 = src->nb[1];
-    a.dst = (char *) dst->data;       a.dst_nb1 = dst->nb[1];
-    a.dst_rows = dst->ne[1];
-    a.idx = (const int32_t *) idx->data; a.idx_nb0 = idx->nb[0];
-    a.n = src->ne[1]; a.bpr = (int32_t) (src->ne[0] / QK); a.x86 = variant == QWFN_Q8_X86;
-    a.status = st;
-    const bool vec4 = is_aligned(src->data, 16) && src->nb[1] % 16 == 0;
-    return launch_append(a, vec4, as_stream(stream));
+    *a = append_args{};
+    a->src = (const char *) src->data; a->src_nb1 = src->nb[1];
+    a->dst = (char *) dst->data;       a->dst_nb1 = dst->nb[1];
+    a->dst_rows = dst->ne[1];
+    a->idx = (const int32_t *) idx->data; a->idx_nb0 = idx->nb[0];
+    a->n = src->ne[1]; a->bpr = (int32_t) (src->ne[0] / QK); a->x86 = variant == QWFN_Q8_X86;
+    *vec4 = is_aligned(src->data, 16) && src->nb[1] % 16 == 0;
+    return QWFN_OK;
 }
 
-extern "C" int qwfn_cpy_f32_q8_0(const qwfn_tensor * src, const qwfn_tensor * dst, int variant, void * stream) {
+// Checks one ggml_cpy(src, dst) F32 -> Q8_0 and fills its arguments (all but
+// the status word).
+int cpy_args(const qwfn_tensor * src, const qwfn_tensor * dst, int variant, append_args * a, bool * vec4) {
     if (int rc = check_src_f32(src, "cpy")) return rc;
     if (int rc = check_dst_q8(dst, src->ne[0], "cpy")) return rc;
     if (dst->ne[1] != src->ne[1]) return set_error(QWFN_EINVAL, "cpy: dst ne[1] != src ne[1]");
     if (variant != QWFN_Q8_REF && variant != QWFN_Q8_X86) return set_error(QWFN_EINVAL, "cpy: unknown rounding variant");
-    uint32_t * st = nullptr;
-    if (int rc = status_word(&st)) return rc;
-    append_args a{};
-    a.src = (const char *) src->data; a.src_nb1 = src->nb[1];
-    a.dst = (char *) dst->data;       a.dst_nb1 = dst->nb[1];
-    a.dst_rows = dst->ne[1];
-    a.idx = nullptr; a.idx_nb0 = 0;
-    a.n = src->ne[1]; a.bpr = (int32_t) (src->ne[0] / QK); a.x86 = variant == QWFN_Q8_X86;
-    a.status = st;
-    const bool vec4 = is_aligned(src->data, 16) && src->nb[1] % 16 == 0;
+    *a = append_args{};
+    a->src = (const char *) src->data; a->src_nb1 = src->nb[1];
+    a->dst = (char *) dst->data;       a->dst_nb1 = dst->nb[1];
+    a->dst_rows = dst->ne[1];
+    a->idx = nullptr; a->idx_nb0 = 0;
+    a->n = src->ne[1]; a->bpr = (int32_t) (src->ne[0] / QK); a->x86 = variant == QWFN_Q8_X86;
+    *vec4 = is_aligned(src->data, 16) && src->nb[1] % 16 == 0;
+    return QWFN_OK;
+}
+
+int same_shape(const qwfn_tensor * k, const qwfn_tensor * v, const char * op) {
+    if (k->ne[0] != v->ne[0] || k->ne[1] != v->ne[1])
+        return set_error(QWFN_EINVAL, std::string(op) + ": the K and V sources must have the same shape");
+    return QWFN_OK;
+}
+
+}  // namespace
+}  // namespace qwfn
+
+using namespace qwfn;
+
+extern "C" int qwfn_set_rows_q8_0(const qwfn_tensor * dst, const qwfn_tensor * src, const qwfn_tensor * idx,
+                                  int variant, void * stream) {
+    append_args a;
+    bool vec4;
+    if (int rc = set_rows_args(dst, src, idx, variant, &a, &vec4)) return rc;
+    if (int rc = status_word(&a.status)) return rc;
     return launch_append(a, vec4, as_stream(stream));
+}
+
+extern "C" int qwfn_cpy_f32_q8_0(const qwfn_tensor * src, const qwfn_tensor * dst, int variant, void * stream) {
+    append_args a;
+    bool vec4;
+    if (int rc = cpy_args(src, dst, variant, &a, &vec4)) return rc;
+    if (int rc = status_word(&a.status)) return rc;
+    return launch_append(a, vec4, as_stream(stream));
+}
+
+extern "C" int qwfn_set_rows_q8_0_kv(const qwfn_tensor * dst_k, const qwfn_tensor * src_k, const qwfn_tensor * dst_v,
+                                     const qwfn_tensor * src_v, const qwfn_tensor * idx, int variant, void * stream) {
+    append_args k, v;
+    bool vk, vv;
+    if (int rc = set_rows_args(dst_k, src_k, idx, variant, &k, &vk)) return rc;
+    if (int rc = set_rows_args(dst_v, src_v, idx, variant, &v, &vv)) return rc;
+    if (int rc = same_shape(src_k, src_v, "set_rows_kv")) return rc;
+    if (int rc = status_word(&k.status)) return rc;
+    v.status = k.status;
+    return launch_append_kv(k, v, vk && vv, as_stream(stream));
+}
+
+extern "C" int qwfn_cpy_f32_q8_0_kv(const qwfn_tensor * src_k, const qwfn_tensor * dst_k, const qwfn_tensor * src_v,
+                                    const qwfn_tensor * dst_v, int variant, void * stream) {
+    append_args k, v;
+    bool vk, vv;
+    if (int rc = cpy_args(src_k, dst_k, variant, &k, &vk)) return rc;
+    if (int rc = cpy_args(src_v, dst_v, variant, &v, &vv)) return rc;
+    if (int rc = same_shape(src_k, src_v, "cpy_kv")) return rc;
+    if (int rc = status_word(&k.status)) return rc;
+    v.status = k.status;
+    return launch_append_kv(k, v, vk && vv, as_stream(stream));
 }

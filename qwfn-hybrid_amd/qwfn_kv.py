@@ -46,7 +46,7 @@ class Tensor(ctypes.Structure):
 
 EXPORTS = [
     "qwfn_abi_version", "qwfn_last_error", "qwfn_init", "qwfn_device_status",
-    "qwfn_set_rows_q8_0", "qwfn_cpy_f32_q8_0", "qwfn_get_rows_i32", "qwfn_kv_gather_segments",
+    "qwfn_set_rows_q8_0", "qwfn_cpy_f32_q8_0", "qwfn_set_rows_q8_0_kv", "qwfn_cpy_f32_q8_0_kv", "qwfn_get_rows_i32", "qwfn_kv_gather_segments",
     "qwfn_fattn_workspace_size", "qwfn_flash_attn_ext_q8_0", "qwfn_state_restore",
 ]
 
@@ -69,6 +69,8 @@ def load(path: str = LIB_PATH):
     L.qwfn_device_status.argtypes = [vp, ctypes.POINTER(ctypes.c_uint32)]
     L.qwfn_set_rows_q8_0.argtypes = [T, T, T, ctypes.c_int, vp]
     L.qwfn_cpy_f32_q8_0.argtypes = [T, T, ctypes.c_int, vp]
+    L.qwfn_set_rows_q8_0_kv.argtypes = [T, T, T, T, T, ctypes.c_int, vp]
+    L.qwfn_cpy_f32_q8_0_kv.argtypes = [T, T, T, T, ctypes.c_int, vp]
     L.qwfn_get_rows_i32.argtypes = [T, T, T, vp]
     L.qwfn_kv_gather_segments.argtypes = [vp, sz, i64, sz, sz, sz, i32, vp, i64, vp, sz, sz, vp]
     L.qwfn_fattn_workspace_size.argtypes = [T, T, T, T]
@@ -184,6 +186,28 @@ def cpy_f32_q8_0(src, cache, first_row: int, variant: int = Q8_X86, stream=None)
     s = tensor(src.data_ptr(), TYPE_F32, (src.shape[1], src.shape[0]), (4, src.stride(0) * 4))
     dst = cache_rows_view(cache, src.shape[0], first_row)
     return check(L.qwfn_cpy_f32_q8_0(ctypes.byref(s), ctypes.byref(dst), variant, _stream(stream)))
+
+
+def set_rows_q8_0_kv(kcache, ksrc, vcache, vsrc, idx, variant: int = Q8_X86, stream=None, n_rows: int | None = None):
+    """The K and the V set_rows of one layer in one launch (same idx)."""
+    L = load()
+    dk, dv = cache_rows_view(kcache, n_rows), cache_rows_view(vcache, n_rows)
+    sk = tensor(ksrc.data_ptr(), TYPE_F32, (ksrc.shape[1], ksrc.shape[0]), (4, ksrc.stride(0) * 4))
+    sv = tensor(vsrc.data_ptr(), TYPE_F32, (vsrc.shape[1], vsrc.shape[0]), (4, vsrc.stride(0) * 4))
+    i = tensor(idx.data_ptr(), TYPE_I32, (idx.shape[0],), (4,))
+    return check(L.qwfn_set_rows_q8_0_kv(ctypes.byref(dk), ctypes.byref(sk), ctypes.byref(dv), ctypes.byref(sv),
+                                         ctypes.byref(i), variant, _stream(stream)))
+
+
+def cpy_f32_q8_0_kv(ksrc, kcache, vsrc, vcache, first_row: int, variant: int = Q8_X86, stream=None):
+    """The K and the V cpy of one append in one launch."""
+    L = load()
+    sk = tensor(ksrc.data_ptr(), TYPE_F32, (ksrc.shape[1], ksrc.shape[0]), (4, ksrc.stride(0) * 4))
+    sv = tensor(vsrc.data_ptr(), TYPE_F32, (vsrc.shape[1], vsrc.shape[0]), (4, vsrc.stride(0) * 4))
+    dk = cache_rows_view(kcache, ksrc.shape[0], first_row)
+    dv = cache_rows_view(vcache, vsrc.shape[0], first_row)
+    return check(L.qwfn_cpy_f32_q8_0_kv(ctypes.byref(sk), ctypes.byref(dk), ctypes.byref(sv), ctypes.byref(dv),
+                                        variant, _stream(stream)))
 
 
 def get_rows_i32(cache, idx, out, stream=None):

@@ -66,6 +66,21 @@ def test_cpy_validation():
     _err(L.qwfn_cpy_f32_q8_0(r(f32(512, 3)), r(q8(512, 3, nb1=100)), 1, None), K.EINVAL, "overlap")
 
 
+def test_fused_kv_append_validation():
+    """The fused K+V entry points check each pair like the single calls, and the K and V
+    sources must have the same shape."""
+    L = K.load()
+    r = ctypes.byref
+    _err(L.qwfn_set_rows_q8_0_kv(r(q8(512, 64)), r(f32(512, 2)), r(q8(512, 64)), r(f32(512, 3)), r(i32(2)), 1, None),
+         K.EINVAL, "idx")
+    _err(L.qwfn_set_rows_q8_0_kv(r(q8(512, 64)), r(f32(512, 2)), r(q8(512, 64)), r(f32(500, 2)), r(i32(2)), 1, None),
+         K.EINVAL, "multiple of 32")
+    _err(L.qwfn_cpy_f32_q8_0_kv(r(f32(512, 3)), r(q8(512, 3)), r(f32(256, 3)), r(q8(256, 3)), 1, None),
+         K.EINVAL, "same shape")
+    _err(L.qwfn_cpy_f32_q8_0_kv(r(f32(512, 3)), r(q8(512, 3)), r(f32(512, 3)), r(q8(512, 2)), 1, None),
+         K.EINVAL, "ne[1]")
+
+
 def test_get_rows_and_gather_validation():
     L = K.load()
     r = ctypes.byref

@@ -101,6 +101,46 @@ def test_set_rows_out_of_range_index_is_flagged(gpu, oracle):
     assert K.device_status() == 0                           # flags clear on read
 
 
+@pytest.mark.parametrize("variant", [O.Q8_REF, O.Q8_X86])
+def test_fused_kv_append_bit_exact(gpu, oracle, variant):
+    """The K and V appends of one layer in one launch equal two single appends, and the oracle:
+    set_rows with crafted rows and one out-of-range index, and a 3-row cpy at a depth."""
+    K = gpu
+    rng = np.random.default_rng(300 + variant)
+    n_ctx = 512
+    kc = rng.integers(0, 256, (n_ctx, 544), dtype=np.uint8)
+    vc = rng.integers(0, 256, (n_ctx, 544), dtype=np.uint8)
+    ks = np.concatenate([crafted_rows(rng), rng.standard_normal((40, 512)).astype(np.float32)])
+    vs = (rng.standard_normal(ks.shape) * 7).astype(np.float32)
+    idx = rng.permutation(n_ctx)[:ks.shape[0]].astype(np.int32)
+    idx[5] = n_ctx + 3                                       # flagged, row skipped
+    say(f"set_rows_kv variant={variant} n={ks.shape[0]}")
+    kd, vd = dev(kc), dev(vc)
+    K.set_rows_q8_0_kv(kd, dev(ks), vd, dev(vs), dev(idx), variant)
+    assert K.device_status() & K.DEVERR_SET_ROWS_INDEX
+    keep = np.arange(ks.shape[0]) != 5
+    for got, cache, src in ((host(kd), kc, ks), (host(vd), vc, vs)):
+        exp = cache.copy()
+        O.set_rows(exp, src[keep], idx[keep], variant)
+        np.testing.assert_array_equal(got, exp)
+    # the same through two single calls
+    k2, v2 = dev(kc), dev(vc)
+    K.set_rows_q8_0(k2, dev(ks), dev(idx), variant)
+    K.set_rows_q8_0(v2, dev(vs), dev(idx), variant)
+    K.device_status()
+    np.testing.assert_array_equal(host(kd), host(k2))
+    np.testing.assert_array_equal(host(vd), host(v2))
+    # cpy of 3 rows at depth 300
+    say(f"cpy_kv 3 rows at 300 variant={variant}")
+    kd, vd = dev(kc), dev(vc)
+    K.cpy_f32_q8_0_kv(dev(ks[:3]), kd, dev(vs[:3]), vd, 300, variant)
+    for got, cache, src in ((host(kd), kc, ks[:3]), (host(vd), vc, vs[:3])):
+        exp = cache.copy()
+        O.cpy(exp, src, 300, variant)
+        np.testing.assert_array_equal(got, exp)
+    assert K.device_status() == 0
+
+
 def test_get_rows_raw_cells(gpu, oracle):
     # qsa_gather raw: 2052 cells padded to 2304 with duplicates (qwfn_graph.cpp:681-693)
     K = gpu
