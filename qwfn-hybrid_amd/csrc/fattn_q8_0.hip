@@ -68,6 +68,7 @@ constexpr float LOG2E = 1.4426950408889634f;
 constexpr float RESCALE_SLACK = 8.f;   // log2 units the running max may lag the true max
 constexpr int PV_BATCH = 4;            // 16-key V block tiles whose LDS reads are issued together
 constexpr int MASK_LDS = 8192;         // LDS bytes for a block's mask rows over its whole split
+constexpr int MASK_ROWS_PAIR = 7;      // mask-tile rows of a 4-wave two-tile block
 enum { MASK_NONE = 0, MASK_SPLIT = 1, MASK_TILE = 2 };
 
 // Chunk geometry for RT query tiles per block of NW waves; MT: the mask
@@ -87,7 +88,10 @@ struct fa_cfg {
     // MASK_TILE: a chunk's mask rows travel with it as 16-byte granules from
     // the 16-byte aligned address at or below each row's first key
     static constexpr int MGR   = 2 * CK / 16 + 1;           // granules per mask row
-    static constexpr int MROWS = ROWS;                      // mask rows of a block, at most
+    // mask rows of a block, at most: every row, except for 4-wave blocks of two
+    // tiles, which take mask tiles only for masks shared by the heads (a
+    // block's rows then span at most MASK_ROWS_PAIR query positions)
+    static constexpr int MROWS = NW == WAVES_PAIR && KWV == 32 ? MASK_ROWS_PAIR : ROWS;
     static constexpr int MDMA  = MT ? (MROWS * MGR + 63) / 64 : 0;   // wave-wide DMAs for them
     static constexpr int MTILE = MDMA * 1024;               // their bytes in a stage
     static constexpr int STAGE = 2 * VOFF + MTILE;          // one ring stage: K rows, V rows, mask tile
@@ -1087,7 +1091,8 @@ int check_no_scratch() {
                                (const void *) k_fattn_q8_0<1, true, WAVES, 16>, (const void *) k_fattn_q8_0<2, true, WAVES, 16>,
                                (const void *) k_fattn_q8_0<1, false, WAVES_PAIR, 16>,
                                (const void *) k_fattn_q8_0<1, true, WAVES_PAIR, 16>,
-                               (const void *) k_fattn_q8_0<2, false, WAVES_PAIR, 32>}) {
+                               (const void *) k_fattn_q8_0<2, false, WAVES_PAIR, 32>,
+                               (const void *) k_fattn_q8_0<2, true, WAVES_PAIR, 32>}) {
             hipFuncAttributes at{};
             if (int e = hip_check(hipFuncGetAttributes(&at, f), "hipFuncGetAttributes")) return e;
             if (at.localSizeBytes != 0)
@@ -1249,13 +1254,14 @@ extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor
     char * w = (char *) ws;
     a.n_kv = n_kv;
     a.T = (int32_t) q->ne[1]; a.nh = (int32_t) q->ne[2]; a.nh_kv = (int32_t) k->ne[2];
+    int64_t mrows = 0;    // mask rows a block can span, at most
     if (mask) {
         a.mask = (const char *) mask->data; a.m_nb1 = mask->nb[1]; a.m_nb2 = mask->nb[2]; a.m_nb3 = mask->nb[3];
         a.m_ne2 = (int32_t) mask->ne[2]; a.m_ne3 = (int32_t) mask->ne[3];
         a.m_slice = (uint32_t) mask_slice_bytes(*mask);
         // MASK_SPLIT: each mask row of a split as 16-byte granules from the
         // aligned address at or below its first key, all in LDS at once
-        const int64_t mrows = mask->ne[2] == 1 ? ((int64_t) pl.rw + pl.gqa - 1) / pl.gqa + 1 : pl.rw;
+        mrows = mask->ne[2] == 1 ? ((int64_t) pl.rw + pl.gqa - 1) / pl.gqa + 1 : pl.rw;
         const int64_t mlds = pl.kind == FA_P4_T2 ? fa_cfg<2, false, WAVES_PAIR, 32>::MLDS : MASK_LDS;
         a.m_gran = pl.max_span / 8 + 1;
         a.m_gran_mul = recip32(a.m_gran);
@@ -1293,9 +1299,11 @@ extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor
             else    hipLaunchKernelGGL((k_fattn_q8_0<1, false, WAVES_PAIR, 16>), g, b4, 0, st, a);
             break;
         case FA_P4_T2:
-            // a mask tile in each stage leaves no room for two blocks per CU:
-            // those calls take the 8-wave kernel over the same 64-key chunks
-            if (mt) hipLaunchKernelGGL((k_fattn_q8_0<2, true, WAVES, 16>), g, b8, 0, st, a);
+            // mask tiles of at most MASK_ROWS_PAIR rows fit next to two stages;
+            // more rows (per-head masks, small gqa) take the 8-wave kernel over
+            // the same 64-key chunks
+            if (mt && mrows > MASK_ROWS_PAIR) hipLaunchKernelGGL((k_fattn_q8_0<2, true, WAVES, 16>), g, b8, 0, st, a);
+            else if (mt) hipLaunchKernelGGL((k_fattn_q8_0<2, true, WAVES_PAIR, 32>), g, b4, 0, st, a);
             else    hipLaunchKernelGGL((k_fattn_q8_0<2, false, WAVES_PAIR, 32>), g, b4, 0, st, a);
             break;
         case FA_W8_T1:
