@@ -1,0 +1,216 @@
+/*
+ * qwfn_state.h -- C ABI of the per-sequence state around the q8_0 KV path:
+ * the cache/recurrent-state owner, its reset, MTP-verify rollback, session
+ * snapshots, and the small per-step inputs of the attention layers (masks and
+ * the decode-time sparse-attention inputs), all built on the device.
+ *
+ *   qwfn::state (init, k_cache/v_cache/idx_cache/rs_state/rs_conv/ple_conv,
+ *                reset, bytes, summary, n_ctx)          qwfn_state.h:28-92, qwfn_state.cpp:21-173
+ *   engine::init_state rollback slots                  qwfn_engine.cpp:343-374
+ *   engine::rollback_n                                  qwfn_engine.cpp:3629-3660
+ *   snapshot_parts / snapshot_save / snapshot_load      qwfn_engine.cpp:988-1053
+ *   engine::reset                                       qwfn_engine.cpp:1055-1066
+ *   decode cell mask and padded cell list               qwfn_graph.cpp:668-675, :681-693
+ *   causal masks of prefill chunks, steps, MTP drafts   qwfn_engine.cpp:1261-1271, :2093-2098, :3415-3440
+ *   qsa_decode_prepare / _k, qsa_pool_rebuild (bias),
+ *   init_qsa_tables                                     qwfn_engine.cpp:1072-1105, :3582-3614, :1107-1125, :672-684
+ *
+ * Conventions are those of qwfn_kv.h: QWFN_OK or a negative code with a
+ * thread-local message (qwfn_last_error), host-side validation before any
+ * launch, stream-ordered asynchronous device work, caller-owned buffers except
+ * the state's own arenas.
+ */
+#ifndef QWFN_STATE_H
+#define QWFN_STATE_H
+
+#include "qwfn_kv.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------ state owner */
+
+/* Hyper-parameters that size the state (hparams fields of qwfn_hparams.h:14-80
+ * that qwfn_state.cpp:48-91 reads) and the state_config fields. */
+typedef struct qwfn_state_config {
+    uint32_t n_ctx;                    /* state_config::n_ctx                        */
+    uint32_t n_layer;                  /* 48                                         */
+    uint32_t full_attention_interval;  /* 4: layer il is attention if (il+1) % 4 == 0 */
+    uint32_t n_head_kv;                /* 2                                          */
+    uint32_t n_embd_head_k;            /* 256                                        */
+    uint32_t n_embd_head_v;            /* 256                                        */
+    uint32_t idx_key_len;              /* 128                                        */
+    uint32_t ssm_d_state;              /* 128                                        */
+    uint32_t ssm_n_group;              /* 16                                         */
+    uint32_t ssm_dt_rank;              /* 48                                         */
+    uint32_t ssm_d_conv;               /* 4                                          */
+    uint32_t hc_count;                 /* 4                                          */
+    uint32_t n_embd;                   /* 2560                                       */
+    uint32_t ple_n_head;               /* 16; 0 = no PLE convolution history         */
+    uint32_t ple_conv_kernel;          /* 4                                          */
+    uint32_t ple_ngram_size;           /* 3                                          */
+    int32_t  type_k;                   /* QWFN_TYPE_Q8_0 or QWFN_TYPE_F16            */
+    int32_t  type_v;                   /* QWFN_TYPE_Q8_0 or QWFN_TYPE_F16            */
+    int32_t  type_idx;                 /* QWFN_TYPE_F16 or QWFN_TYPE_F32             */
+    uint32_t kv_host;                  /* K/V caches in pinned host memory           */
+    uint32_t idx_host;                 /* indexer caches in pinned host memory       */
+    uint32_t n_rollback;               /* rollback slots (engine's rb_nsnap_); 0 = none */
+} qwfn_state_config;
+
+/* The model's values above (qwfn_hparams.h comments), with n_ctx, q8_0 K/V,
+ * F16 indexer keys and no rollback slots. */
+void qwfn_state_config_default(qwfn_state_config * cfg, uint32_t n_ctx);
+
+typedef struct qwfn_state qwfn_state;
+
+/* Create a state on `device` and zero its recurrent part (state::init). All
+ * device tensors live in one arena, each 256-byte aligned; the recurrent
+ * tensors (rs and conv of every DeltaNet layer, then the PLE history) are
+ * contiguous, and each rollback slot is a separate image of that region with
+ * the same layout. device = QWFN_LAYOUT_ONLY allocates nothing: tensor
+ * descriptors then carry byte offsets from 0 instead of addresses, which is
+ * enough for sizes, summaries and snapshot part lists (no device needed). */
+#define QWFN_LAYOUT_ONLY (-1)
+int  qwfn_state_create(const qwfn_state_config * cfg, int device, qwfn_state ** out);
+void qwfn_state_destroy(qwfn_state * st);
+
+enum qwfn_state_kind {
+    QWFN_STATE_K        = 0,  /* q8_0/f16 1-D [kv_dim * n_ctx], attention layers */
+    QWFN_STATE_V        = 1,
+    QWFN_STATE_IDX      = 2,  /* f16 1-D [idx_key_len * n_ctx], attention layers */
+    QWFN_STATE_RS       = 3,  /* f32 [d_state, d_state, dt_rank], DeltaNet layers */
+    QWFN_STATE_CONV     = 4,  /* f32 [d_conv - 1, conv_dim], DeltaNet layers      */
+    QWFN_STATE_PLE_CONV = 5,  /* f32 [(kernel - 1) * ngram, hc_count * n_embd]    */
+};
+
+/* Descriptor of a state tensor. slot = -1: the live tensor; slot s >= 0: the
+ * tensor's image in rollback slot s (RS, CONV, PLE_CONV only; slot s holds the
+ * state s+1 tokens back). Returns 1 and fills *out when the tensor exists, 0
+ * (and a zeroed *out) when the layer has no such tensor -- k_cache() etc.
+ * returning null in qwfn_state.cpp:123-148 -- or a negative code. */
+int      qwfn_state_tensor(const qwfn_state * st, int32_t kind, uint32_t il, int32_t slot, qwfn_tensor * out);
+size_t   qwfn_state_bytes(const qwfn_state * st);           /* device arena, without rollback slots */
+size_t   qwfn_state_host_bytes(const qwfn_state * st);      /* pinned host arena (kv_host / idx_host) */
+size_t   qwfn_state_rollback_bytes(const qwfn_state * st);  /* all rollback slots */
+uint32_t qwfn_state_n_ctx(const qwfn_state * st);
+/* state::summary(); writes at most cap bytes including the terminating NUL and
+ * returns the full length (snprintf convention), or a negative code. */
+int      qwfn_state_summary(const qwfn_state * st, char * buf, size_t cap);
+
+/* ------------------------------------------------- position bookkeeping */
+
+int32_t qwfn_state_n_past(const qwfn_state * st);
+int32_t qwfn_state_rollback_depth(const qwfn_state * st);
+/* After a step of T positions (eval_batch, qwfn_engine.cpp:2033-2035):
+ * n_past += T; the rollback depth becomes min(T-1, n_rollback) for a verified
+ * decode step of T >= 2 positions, else 0. QWFN_ERANGE if n_past + T > n_ctx. */
+int qwfn_state_step_done(qwfn_state * st, int32_t T, int32_t verified);
+
+/* engine::reset minus the engine-only flags: zero the recurrent tensors (one
+ * fill kernel; the caches are not cleared), n_past = 0, rollback depth 0. */
+int qwfn_state_reset(qwfn_state * st, void * stream);
+
+/* engine::rollback_n: copy rollback slot n_back-1 over the live recurrent
+ * tensors (one contiguous device copy), n_past -= n_back, depth 0.
+ * QWFN_ERANGE (message "rollback: no snapshot of the state N tokens back")
+ * unless 1 <= n_back <= rollback depth. */
+int qwfn_state_rollback(qwfn_state * st, int32_t n_back, void * stream);
+
+/* ---------------------------------------------------------- snapshots */
+
+typedef struct qwfn_part {
+    void * data;    /* device address (or arena offset for QWFN_LAYOUT_ONLY) */
+    size_t bytes;   /* bytes of the part that belong to the first n_past positions */
+} qwfn_part;
+
+enum qwfn_mem_kind { QWFN_MEM_DEVICE = 0, QWFN_MEM_HOST = 1 };
+
+/* snapshot_parts (qwfn_engine.cpp:990-999) over the states in order (the
+ * trunk, then the MTP head's state): per layer K, V, idx with
+ * min(nbytes, n_past * row bytes), then rs and conv whole; then the PLE
+ * history. Writes up to max_parts entries and sets *n_parts to the count
+ * (call with max_parts = 0 to size the array). */
+int qwfn_snapshot_parts(const qwfn_state * const * sts, int32_t n_sts, int32_t n_past,
+                        qwfn_part * parts, int32_t max_parts, int32_t * n_parts);
+
+/* snapshot_save: copy every part of the states' first n_past positions
+ * (n_past of sts[0]; all states must agree) into dst[k] (dst_bytes[k] must
+ * equal the part's size; n_dst the part count). dst_kind QWFN_MEM_DEVICE: one
+ * batched device copy; QWFN_MEM_HOST: host buffers (pinned ones make the copy
+ * asynchronous). Stream-ordered: synchronise before reading dst. */
+int qwfn_snapshot_save(const qwfn_state * const * sts, int32_t n_sts, void * const * dst,
+                       const size_t * dst_bytes, int32_t n_dst, int32_t dst_kind,
+                       int32_t * n_past_out, void * stream);
+
+/* snapshot_load: reset every state first (as the reference does, so a
+ * rejected snapshot leaves a reset state), then QWFN_ESIZE if n_src differs
+ * from the part count for n_past or any src_bytes[k] from its part's size;
+ * else copy each part in and set n_past on every state. */
+int qwfn_snapshot_load(qwfn_state * const * sts, int32_t n_sts, int32_t n_past, const void * const * src,
+                       const size_t * src_bytes, int32_t n_src, int32_t src_kind, void * stream);
+
+/* ---------------------------------------------------------------- masks */
+
+/* Causal F16 mask of T query rows over n_kv keys, row i at byte i*row_stride:
+ * key j is visible (0x0000) iff j <= n_past + i, else -inf (0xFC00); keys
+ * n_kv .. row_stride/2 - 1 of a padded row are -inf. The masks of
+ * build_attn_inputs (qwfn_engine.cpp:1261-1271), build_step_inputs (:2093-2098)
+ * and mtp_mask (:3415-3421) with n_past = n_past_c / n_past / pos. */
+int qwfn_causal_mask_f16(uint16_t * mask, int64_t n_kv, int64_t T, int64_t n_past, size_t row_stride,
+                         void * stream);
+
+/* Decode cell mask (qwfn_graph.cpp:668-675, :681-693): for j < n_pad,
+ * mask[j] = 0 if j < n_cells and cells[j] <= n_past, else -inf; and, when
+ * gcells is not NULL, the padded cell list gcells[j] = cells[j] for
+ * j < n_cells, cells[j - n_cells] after (the reference's concat of the list
+ * with its own head; needs n_pad <= 2 n_cells). cells, mask and gcells are
+ * device memory. */
+int qwfn_cell_mask_f16(const int32_t * cells, int64_t n_cells, int64_t n_pad, int32_t n_past,
+                       uint16_t * mask, int32_t * gcells, void * stream);
+
+/* ------------------------------------------- decode-time sparse-attention inputs */
+
+/* qsa_decode_inputs (qwfn_graph.h:71-84): device tensors written per token. */
+typedef struct qwfn_qsa_inputs {
+    float *   bias;          /* F32 [n_blocks_max]                         */
+    int32_t * write_idx;     /* I32 [1]                                    */
+    int32_t * member_idx;    /* I32 [ratio]                                */
+    int32_t * blk_pos;       /* I32 [4]                                    */
+    int32_t * blk_idx;       /* I32 [1]                                    */
+    float *   npast_f;       /* F32 [1]                                    */
+    int32_t   ratio;         /* cells per block                            */
+    int32_t   pad_;
+    int64_t   n_blocks_max;  /* bias ne[0] (NBmax)                         */
+} qwfn_qsa_inputs;
+
+/* The block bucket the decode graph is shaped for at n_past:
+ * clamp(roundup256(n_past / ratio + 1), 768, n_blocks_max)
+ * (qwfn_engine.cpp:1099-1101). Host only. */
+int64_t qwfn_qsa_bucket(int32_t n_past, int32_t ratio, int64_t n_blocks_max);
+
+/* qsa_decode_prepare (prev_bias NULL; the bias window around the block of
+ * n_past is updated in place) or qsa_decode_prepare_k (prev_bias = the
+ * previous position's bias: copied, then this position's window on top), in
+ * one launch: write_idx = n_past, member_idx = the cells of n_past's block,
+ * blk_pos = 4 x its first cell, blk_idx, npast_f; bias 0 for whole blocks,
+ * 1e9 for the incomplete block of n_past, -inf past it. */
+int qwfn_qsa_decode_prepare(const qwfn_qsa_inputs * qd, const float * prev_bias, int32_t n_past, void * stream);
+
+/* The full bias rewrite of qsa_pool_rebuild (qwfn_engine.cpp:1115-1120):
+ * 0 for blocks < (n_past+1)/ratio, the block of n_past 0 or 1e9, -inf after.
+ * n_past = -1 writes -inf everywhere (engine::reset, init_qsa_tables). */
+int qwfn_qsa_bias_rebuild(float * bias, int64_t n_blocks_max, int32_t n_past, int32_t ratio, void * stream);
+
+/* Static tables of init_qsa_tables (qwfn_engine.cpp:676-681) and the block
+ * positions of qsa_pool_rebuild (:1121-1124), any pointer may be NULL:
+ * blk_cells[b*ratio + k] = b*ratio + k for b < n_blocks_max; cell_pos[i] = i
+ * (F32) for i < n_ctx; blk_pos_all[s*n_whole + b] = b*ratio for s < 4,
+ * b < n_whole. */
+int qwfn_qsa_tables(int32_t * blk_cells, int64_t n_blocks_max, int32_t ratio, float * cell_pos, int64_t n_ctx,
+                    int32_t * blk_pos_all, int64_t n_whole, void * stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -109,6 +109,8 @@ __global__ __launch_bounds__(COPY_THREADS) void k_restore_bytes(const char * src
     }
 }
 
+}  // namespace
+
 int restore_device(const char * const * src, const size_t * bytes, char * const * dst, int n_parts, int n_slots,
                    int slot0, hipStream_t stream) {
     // dst is [n_slots_total][n_parts]; slots [slot0, slot0 + n_slots) are written.
@@ -154,7 +156,6 @@ int restore_device(const char * const * src, const size_t * bytes, char * const 
     return QWFN_OK;
 }
 
-}  // namespace
 }  // namespace qwfn
 
 using namespace qwfn;

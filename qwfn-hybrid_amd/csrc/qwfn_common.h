@@ -26,6 +26,11 @@ int  hip_check(hipError_t e, const char * what);
 int  status_word(uint32_t ** out);
 // Library-owned workspace of at least `bytes` on the current device.
 int  library_workspace(size_t bytes, void ** out);
+// Device-to-device copy of n_parts parts into n_slots slots (kv_copy.hip):
+// dst is [slots][n_parts], slots slot0 .. slot0+n_slots-1 are written; each
+// source byte is read once. Parts that are not 16-byte aligned go bytewise.
+int  restore_device(const char * const * src, const size_t * bytes, char * const * dst, int n_parts, int n_slots,
+                    int slot0, hipStream_t stream);
 
 inline hipStream_t as_stream(void * s) { return reinterpret_cast<hipStream_t>(s); }
 

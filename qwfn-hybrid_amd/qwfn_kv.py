@@ -44,10 +44,38 @@ class Tensor(ctypes.Structure):
                 ("nb", ctypes.c_size_t * 4)]
 
 
+class StateConfig(ctypes.Structure):
+    """qwfn_state_config (include/qwfn_state.h)."""
+    _fields_ = [(n, ctypes.c_uint32) for n in (
+        "n_ctx", "n_layer", "full_attention_interval", "n_head_kv", "n_embd_head_k", "n_embd_head_v",
+        "idx_key_len", "ssm_d_state", "ssm_n_group", "ssm_dt_rank", "ssm_d_conv", "hc_count", "n_embd",
+        "ple_n_head", "ple_conv_kernel", "ple_ngram_size")] + [
+        ("type_k", ctypes.c_int32), ("type_v", ctypes.c_int32), ("type_idx", ctypes.c_int32),
+        ("kv_host", ctypes.c_uint32), ("idx_host", ctypes.c_uint32), ("n_rollback", ctypes.c_uint32)]
+
+
+class Part(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("bytes", ctypes.c_size_t)]
+
+
+class QsaInputs(ctypes.Structure):
+    """qwfn_qsa_inputs: device addresses of the per-token decode inputs."""
+    _fields_ = [("bias", ctypes.c_void_p), ("write_idx", ctypes.c_void_p), ("member_idx", ctypes.c_void_p),
+                ("blk_pos", ctypes.c_void_p), ("blk_idx", ctypes.c_void_p), ("npast_f", ctypes.c_void_p),
+                ("ratio", ctypes.c_int32), ("pad_", ctypes.c_int32), ("n_blocks_max", ctypes.c_int64)]
+
+
 EXPORTS = [
     "qwfn_abi_version", "qwfn_last_error", "qwfn_init", "qwfn_device_status",
     "qwfn_set_rows_q8_0", "qwfn_cpy_f32_q8_0", "qwfn_set_rows_q8_0_kv", "qwfn_cpy_f32_q8_0_kv", "qwfn_get_rows_i32", "qwfn_kv_gather_segments",
     "qwfn_fattn_workspace_size", "qwfn_flash_attn_ext_q8_0", "qwfn_state_restore",
+    # include/qwfn_state.h
+    "qwfn_state_config_default", "qwfn_state_create", "qwfn_state_destroy", "qwfn_state_tensor",
+    "qwfn_state_bytes", "qwfn_state_host_bytes", "qwfn_state_rollback_bytes", "qwfn_state_n_ctx",
+    "qwfn_state_summary", "qwfn_state_n_past", "qwfn_state_rollback_depth", "qwfn_state_step_done",
+    "qwfn_state_reset", "qwfn_state_rollback", "qwfn_snapshot_parts", "qwfn_snapshot_save", "qwfn_snapshot_load",
+    "qwfn_causal_mask_f16", "qwfn_cell_mask_f16", "qwfn_qsa_bucket", "qwfn_qsa_decode_prepare",
+    "qwfn_qsa_bias_rebuild", "qwfn_qsa_tables",
 ]
 
 _lib = None
@@ -78,8 +106,40 @@ def load(path: str = LIB_PATH):
     L.qwfn_flash_attn_ext_q8_0.argtypes = [T, T, T, T, ctypes.c_float, ctypes.c_float, ctypes.c_float, T,
                                            ctypes.c_int, vp, sz, vp]
     L.qwfn_state_restore.argtypes = [ctypes.POINTER(vp), ctypes.POINTER(sz), ctypes.POINTER(vp), i32, i32, i32, vp]
+    # include/qwfn_state.h
+    u32, PV, PS = ctypes.c_uint32, ctypes.POINTER(vp), ctypes.POINTER(sz)
+    L.qwfn_state_config_default.argtypes = [ctypes.POINTER(StateConfig), u32]
+    L.qwfn_state_config_default.restype = None
+    L.qwfn_state_create.argtypes = [ctypes.POINTER(StateConfig), ctypes.c_int, PV]
+    L.qwfn_state_destroy.argtypes = [vp]
+    L.qwfn_state_destroy.restype = None
+    L.qwfn_state_tensor.argtypes = [vp, i32, u32, i32, T]
+    for f in ("qwfn_state_bytes", "qwfn_state_host_bytes", "qwfn_state_rollback_bytes"):
+        getattr(L, f).argtypes = [vp]
+        getattr(L, f).restype = sz
+    L.qwfn_state_n_ctx.argtypes = [vp]
+    L.qwfn_state_n_ctx.restype = u32
+    L.qwfn_state_summary.argtypes = [vp, ctypes.c_char_p, sz]
+    L.qwfn_state_n_past.argtypes = [vp]
+    L.qwfn_state_n_past.restype = i32
+    L.qwfn_state_rollback_depth.argtypes = [vp]
+    L.qwfn_state_rollback_depth.restype = i32
+    L.qwfn_state_step_done.argtypes = [vp, i32, i32]
+    L.qwfn_state_reset.argtypes = [vp, vp]
+    L.qwfn_state_rollback.argtypes = [vp, i32, vp]
+    L.qwfn_snapshot_parts.argtypes = [PV, i32, i32, ctypes.POINTER(Part), i32, ctypes.POINTER(i32)]
+    L.qwfn_snapshot_save.argtypes = [PV, i32, PV, PS, i32, i32, ctypes.POINTER(i32), vp]
+    L.qwfn_snapshot_load.argtypes = [PV, i32, i32, PV, PS, i32, i32, vp]
+    L.qwfn_causal_mask_f16.argtypes = [vp, i64, i64, i64, sz, vp]
+    L.qwfn_cell_mask_f16.argtypes = [vp, i64, i64, i32, vp, vp, vp]
+    L.qwfn_qsa_bucket.argtypes = [i32, i32, i64]
+    L.qwfn_qsa_bucket.restype = i64
+    L.qwfn_qsa_decode_prepare.argtypes = [ctypes.POINTER(QsaInputs), vp, i32, vp]
+    L.qwfn_qsa_bias_rebuild.argtypes = [vp, i64, i32, i32, vp]
+    L.qwfn_qsa_tables.argtypes = [vp, i64, i32, vp, i64, vp, i64, vp]
     for name in EXPORTS:
-        getattr(L, name).restype = getattr(L, name).restype or ctypes.c_int
+        if name not in ("qwfn_state_config_default", "qwfn_state_destroy"):
+            getattr(L, name).restype = getattr(L, name).restype or ctypes.c_int
     L.qwfn_last_error.restype = ctypes.c_char_p
     L.qwfn_fattn_workspace_size.restype = sz
     _lib = L

@@ -1,0 +1,266 @@
+"""Python mirror of the reference's state interface over libqwfn_kv.so
+(include/qwfn_state.h). Every operation runs in the HIP library; PyTorch only
+supplies caller-owned device buffers and the current stream.
+
+  State            qwfn::state (qwfn_state.h:39-92): init, k_cache, v_cache,
+                   idx_cache, rs_state, rs_conv, ple_conv, reset, bytes,
+                   summary, n_ctx; plus the engine's position bookkeeping
+                   (n_past, rollback depth, rollback_n, qwfn_engine.cpp:3629-3660)
+  snapshot_*       engine::snapshot_save / snapshot_load (qwfn_engine.cpp:988-1053)
+  causal_mask_f16, cell_mask_f16
+                   the masks of qwfn_engine.cpp:1261-1271, :2093-2098,
+                   :3415-3421 and qwfn_graph.cpp:668-693
+  QsaDecodeInputs  qsa_decode_inputs and qsa_decode_prepare(_k)
+                   (qwfn_graph.h:71-84, qwfn_engine.cpp:1072-1105, :3582-3614)
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+
+import qwfn_kv as K
+
+STATE_K, STATE_V, STATE_IDX, STATE_RS, STATE_CONV, STATE_PLE_CONV = range(6)
+MEM_DEVICE, MEM_HOST = 0, 1
+LAYOUT_ONLY = -1
+
+
+def config(n_ctx: int, **overrides) -> K.StateConfig:
+    """The model's configuration (qwfn_state_config_default) with overrides."""
+    c = K.StateConfig()
+    K.load().qwfn_state_config_default(ctypes.byref(c), n_ctx)
+    for k, v in overrides.items():
+        if not hasattr(c, k):
+            raise KeyError(k)
+        setattr(c, k, int(v))
+    return c
+
+
+class State:
+    """qwfn::state: owns the caches and recurrent state of one sequence."""
+
+    def __init__(self):
+        self._h = ctypes.c_void_p(None)
+
+    def init(self, cfg: K.StateConfig, device: int = 0) -> tuple[bool, str]:
+        """state::init: (True, "") or (False, message), as bool + std::string& err."""
+        if self._h:
+            raise RuntimeError("state initialised once")
+        L = K.load()
+        rc = L.qwfn_state_create(ctypes.byref(cfg), device, ctypes.byref(self._h))
+        if rc != K.OK:
+            return False, L.qwfn_last_error().decode(errors="replace")
+        return True, ""
+
+    def close(self):
+        if self._h:
+            K.load().qwfn_state_destroy(self._h)
+            self._h = ctypes.c_void_p(None)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def handle(self):
+        return self._h
+
+    # -- tensors (null for the wrong layer kind, as in qwfn_state.cpp:123-148)
+    def tensor(self, kind: int, il: int = 0, slot: int = -1) -> K.Tensor | None:
+        t = K.Tensor()
+        rc = K.load().qwfn_state_tensor(self._h, kind, il, slot, ctypes.byref(t))
+        if rc < 0:
+            K.check(rc)
+        return t if rc == 1 else None
+
+    def k_cache(self, il: int):
+        return self.tensor(STATE_K, il)
+
+    def v_cache(self, il: int):
+        return self.tensor(STATE_V, il)
+
+    def idx_cache(self, il: int):
+        return self.tensor(STATE_IDX, il)
+
+    def rs_state(self, il: int):
+        return self.tensor(STATE_RS, il)
+
+    def rs_conv(self, il: int):
+        return self.tensor(STATE_CONV, il)
+
+    def ple_conv(self):
+        return self.tensor(STATE_PLE_CONV, 0)
+
+    def rollback_slot(self, kind: int, il: int, slot: int):
+        """The image of a recurrent tensor in rollback slot `slot` (the state slot+1 tokens back)."""
+        return self.tensor(kind, il, slot)
+
+    # -- sizes
+    def bytes(self) -> int:
+        return int(K.load().qwfn_state_bytes(self._h))
+
+    def host_bytes(self) -> int:
+        return int(K.load().qwfn_state_host_bytes(self._h))
+
+    def rollback_bytes(self) -> int:
+        return int(K.load().qwfn_state_rollback_bytes(self._h))
+
+    def n_ctx(self) -> int:
+        return int(K.load().qwfn_state_n_ctx(self._h))
+
+    def summary(self) -> str:
+        L = K.load()
+        n = L.qwfn_state_summary(self._h, None, 0)
+        K.check(min(n, 0))
+        buf = ctypes.create_string_buffer(n + 1)
+        L.qwfn_state_summary(self._h, buf, n + 1)
+        return buf.value.decode()
+
+    # -- bookkeeping
+    def n_past(self) -> int:
+        return int(K.load().qwfn_state_n_past(self._h))
+
+    def rollback_depth(self) -> int:
+        return int(K.load().qwfn_state_rollback_depth(self._h))
+
+    def step_done(self, T: int, verified: bool = False):
+        K.check(K.load().qwfn_state_step_done(self._h, T, int(verified)))
+
+    def reset(self, stream=None):
+        K.check(K.load().qwfn_state_reset(self._h, K._stream(stream)))
+
+    def rollback_n(self, n_back: int, stream=None) -> tuple[bool, str]:
+        """engine::rollback_n: (True, "") or (False, message)."""
+        L = K.load()
+        rc = L.qwfn_state_rollback(self._h, n_back, K._stream(stream))
+        if rc != K.OK:
+            return False, L.qwfn_last_error().decode(errors="replace")
+        return True, ""
+
+
+def _handles(states):
+    return (ctypes.c_void_p * len(states))(*[s.handle for s in states])
+
+
+def snapshot_parts(states, n_past: int) -> list[tuple[int, int]]:
+    """(address, bytes) of each snapshot part, in snapshot_parts order."""
+    L = K.load()
+    H = _handles(states)
+    n = ctypes.c_int32(0)
+    K.check(L.qwfn_snapshot_parts(H, len(states), n_past, None, 0, ctypes.byref(n)))
+    P = (K.Part * max(1, n.value))()
+    K.check(L.qwfn_snapshot_parts(H, len(states), n_past, P, n.value, ctypes.byref(n)))
+    return [(P[i].data or 0, int(P[i].bytes)) for i in range(n.value)]
+
+
+@dataclass
+class Snapshot:
+    """engine::state_snapshot: n_past and one blob per part (torch uint8 tensors)."""
+    n_past: int = 0
+    blobs: list = field(default_factory=list)
+
+    def bytes(self) -> int:
+        return sum(int(b.numel()) for b in self.blobs)
+
+
+def snapshot_save(states, where: int = MEM_HOST, stream=None, sync: bool = True) -> Snapshot:
+    """engine::snapshot_save into pinned host blobs (MEM_HOST) or device blobs."""
+    import torch
+    parts = snapshot_parts(states, states[0].n_past())
+    dev = torch.device("cuda")
+    blobs = [torch.empty(b, dtype=torch.uint8, device=dev) if where == MEM_DEVICE
+             else torch.empty(b, dtype=torch.uint8, pin_memory=True) for _, b in parts]
+    D = (ctypes.c_void_p * max(1, len(blobs)))(*[b.data_ptr() if b.numel() else None for b in blobs])
+    B = (ctypes.c_size_t * max(1, len(blobs)))(*[b.numel() for b in blobs])
+    n_past = ctypes.c_int32(0)
+    H = _handles(states)
+    K.check(K.load().qwfn_snapshot_save(H, len(states), D, B, len(blobs), where, ctypes.byref(n_past),
+                                        K._stream(stream)))
+    if sync:
+        torch.cuda.current_stream().synchronize() if stream is None else stream.synchronize()
+    return Snapshot(int(n_past.value), blobs)
+
+
+def snapshot_load(states, snap: Snapshot, stream=None) -> tuple[bool, str]:
+    """engine::snapshot_load: (False, message) on a part count or size mismatch
+    (the states are reset either way)."""
+    L = K.load()
+    if not snap.blobs:
+        kind = MEM_HOST
+    else:
+        kind = MEM_DEVICE if snap.blobs[0].is_cuda else MEM_HOST
+    S = (ctypes.c_void_p * max(1, len(snap.blobs)))(*[b.data_ptr() if b.numel() else None for b in snap.blobs])
+    B = (ctypes.c_size_t * max(1, len(snap.blobs)))(*[b.numel() for b in snap.blobs])
+    rc = L.qwfn_snapshot_load(_handles(states), len(states), snap.n_past, S, B, len(snap.blobs), kind,
+                              K._stream(stream))
+    if rc != K.OK:
+        if rc != K.ESIZE:
+            K.check(rc)
+        return False, L.qwfn_last_error().decode(errors="replace")
+    return True, ""
+
+
+# ------------------------------------------------------------------- masks
+
+def causal_mask_f16(mask, n_kv: int, T: int, n_past: int, stream=None):
+    """mask: a CUDA uint16/float16 tensor [T, row]; key j of row i is visible iff j <= n_past + i."""
+    row_stride = mask.stride(0) * mask.element_size() if mask.dim() == 2 else n_kv * 2
+    K.check(K.load().qwfn_causal_mask_f16(mask.data_ptr(), n_kv, T, n_past, row_stride, K._stream(stream)))
+
+
+def cell_mask_f16(cells, n_past: int, n_pad: int, mask, gcells=None, stream=None):
+    K.check(K.load().qwfn_cell_mask_f16(cells.data_ptr(), cells.numel(), n_pad, n_past, mask.data_ptr(),
+                                        gcells.data_ptr() if gcells is not None else None, K._stream(stream)))
+
+
+# ------------------------------------------- decode-time sparse-attention inputs
+
+class QsaDecodeInputs:
+    """qsa_decode_inputs (qwfn_graph.h:71-84): the per-token device tensors."""
+
+    def __init__(self, ratio: int, n_blocks_max: int, device="cuda"):
+        import torch
+        self.ratio, self.n_blocks_max = ratio, n_blocks_max
+        self.bias = torch.full((n_blocks_max,), float("-inf"), dtype=torch.float32, device=device)
+        self.write_idx = torch.zeros(1, dtype=torch.int32, device=device)
+        self.member_idx = torch.zeros(ratio, dtype=torch.int32, device=device)
+        self.blk_pos = torch.zeros(4, dtype=torch.int32, device=device)
+        self.blk_idx = torch.zeros(1, dtype=torch.int32, device=device)
+        self.npast_f = torch.zeros(1, dtype=torch.float32, device=device)
+        self.n_bucket = 0
+
+    def _c(self) -> K.QsaInputs:
+        q = K.QsaInputs()
+        q.bias, q.write_idx, q.member_idx = self.bias.data_ptr(), self.write_idx.data_ptr(), self.member_idx.data_ptr()
+        q.blk_pos, q.blk_idx, q.npast_f = self.blk_pos.data_ptr(), self.blk_idx.data_ptr(), self.npast_f.data_ptr()
+        q.ratio, q.n_blocks_max = self.ratio, self.n_blocks_max
+        return q
+
+    def bucket(self, n_past: int) -> int:
+        return int(K.load().qwfn_qsa_bucket(n_past, self.ratio, self.n_blocks_max))
+
+    def prepare(self, n_past: int, prev: "QsaDecodeInputs | None" = None, stream=None):
+        """qsa_decode_prepare (prev None) or qsa_decode_prepare_k (prev = the previous position's inputs)."""
+        q = self._c()
+        K.check(K.load().qwfn_qsa_decode_prepare(ctypes.byref(q), prev.bias.data_ptr() if prev is not None else None,
+                                                 n_past, K._stream(stream)))
+        nb = self.bucket(n_past)
+        self.n_bucket = nb if prev is None else max(prev.n_bucket, nb)
+        if prev is not None:
+            prev.n_bucket = self.n_bucket
+
+    def rebuild_bias(self, n_past: int, stream=None):
+        """qsa_pool_rebuild's bias rewrite; n_past = -1 resets it to -inf."""
+        K.check(K.load().qwfn_qsa_bias_rebuild(self.bias.data_ptr(), self.n_blocks_max, n_past, self.ratio,
+                                               K._stream(stream)))
+
+
+def qsa_tables(blk_cells, ratio: int, cell_pos=None, blk_pos_all=None, n_whole: int = 0, stream=None):
+    n_blocks_max = blk_cells.numel() // ratio if blk_cells is not None else 0
+    K.check(K.load().qwfn_qsa_tables(blk_cells.data_ptr() if blk_cells is not None else None, n_blocks_max, ratio,
+                                     cell_pos.data_ptr() if cell_pos is not None else None,
+                                     cell_pos.numel() if cell_pos is not None else 0,
+                                     blk_pos_all.data_ptr() if blk_pos_all is not None else None, n_whole,
+                                     K._stream(stream)))

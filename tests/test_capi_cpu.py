@@ -1,5 +1,5 @@
 """C-ABI checks that need no GPU: the library loads, exports every entry point
-declared in include/qwfn_kv.h, and rejects invalid calls on the host before
+declared in include/*.h, and rejects invalid calls on the host before
 anything is launched (the reference's CPU-forcible failure cases)."""
 import ctypes
 import os
@@ -14,9 +14,13 @@ FAKE = 0x7F0000000000          # never dereferenced: validation fails first
 
 
 def declared_symbols():
-    hdr = open(os.path.join(ROOT, "include", "qwfn_kv.h")).read()
-    hdr = re.sub(r"/\*.*?\*/", "", hdr, flags=re.S)
-    return sorted(set(re.findall(r"\b(qwfn_[a-z0-9_]+)\s*\(", hdr)))
+    syms = set()
+    for name in sorted(os.listdir(os.path.join(ROOT, "include"))):
+        if name.endswith(".h"):
+            hdr = open(os.path.join(ROOT, "include", name)).read()
+            hdr = re.sub(r"/\*.*?\*/", "", hdr, flags=re.S)
+            syms |= set(re.findall(r"\b(qwfn_[a-z0-9_]+)\s*\(", hdr))
+    return sorted(syms)
 
 
 def test_library_exports_header_symbols():

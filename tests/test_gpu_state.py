@@ -1,0 +1,330 @@
+"""GPU tests of the state rows through the C ABI: the state owner (layout,
+initial zero, reset), MTP-verify rollback, session snapshots (device and host
+blobs, part checks), and the device-built step inputs (causal and cell masks,
+decode sparse-attention inputs) against the oracle restatement, bit-exact.
+Mirrors the reference's snapshot check (tools/qwfn_snaptest.cpp:67-82): save,
+run an unrelated sequence, load, and the state must be what was saved."""
+import numpy as np
+import pytest
+
+import qwfn_kv as K
+import qwfn_state as S
+from gpu_util import dev, host, say
+from oracle import state_oracle as SO
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN_SUMMARY_73728 = ("state @ 73728 ctx: KV 0.962593 GB (q8_0), indexer 0.226492 GB, deltanet 113.246 MB "
+                        "(constant), conv 4.79232 MB  =>  total 1.30712 GB on the device")
+
+
+def small_cfg(n_ctx=1024, **kw):
+    d = dict(n_layer=8, ssm_d_state=16, ssm_n_group=2, ssm_dt_rank=4, hc_count=2, n_embd=64, n_rollback=2)
+    d.update(kw)
+    return S.config(n_ctx, **d)
+
+
+def new_state(cfg):
+    st = S.State()
+    ok, err = st.init(cfg, 0)
+    assert ok, err
+    return st
+
+
+def read(addr, n):
+    import torch
+    buf = torch.empty(max(n, 1), dtype=torch.uint8, device="cuda")
+    if n:
+        K.state_restore([addr], [n], [buf.data_ptr()], 1)
+    return host(buf)[:n]
+
+
+def write(addr, data):
+    t = dev(np.ascontiguousarray(data).view(np.uint8).ravel())
+    K.state_restore([t.data_ptr()], [t.numel()], [addr], 1)
+    host(t)   # synchronise before t is freed
+
+
+def nbytes(t):
+    return t.nb[3] * t.ne[3]
+
+
+def all_tensors(st, cfg):
+    out = []
+    for il in range(cfg.n_layer):
+        for k in (S.STATE_K, S.STATE_V, S.STATE_IDX, S.STATE_RS, S.STATE_CONV):
+            t = st.tensor(k, il)
+            if t is not None:
+                out.append(((k, il), t))
+    t = st.ple_conv()
+    if t is not None:
+        out.append(((S.STATE_PLE_CONV, 0), t))
+    return out
+
+
+def recurrent(key):
+    return key[0] in (S.STATE_RS, S.STATE_CONV, S.STATE_PLE_CONV)
+
+
+def scribble(st, cfg, rng):
+    """Random bytes into every tensor; returns {key: bytes}."""
+    data = {}
+    for key, t in all_tensors(st, cfg):
+        data[key] = rng.integers(0, 256, nbytes(t), dtype=np.uint8)
+        write(t.data, data[key])
+    return data
+
+
+def test_full_model_state_layout_and_initial_zero(gpu):
+    say("state: full model at 73728 positions, 2 rollback slots")
+    cfg = S.config(73728, n_rollback=2)
+    st = new_state(cfg)
+    assert st.summary() == GOLDEN_SUMMARY_73728
+    assert st.bytes() == 1307123712
+    rec = [t for key, t in all_tensors(st, cfg) if recurrent(key)]
+    lo = min(t.data for t in rec)
+    hi = max(t.data + nbytes(t) for t in rec)
+    assert hi - lo == sum(nbytes(t) for t in rec)          # one contiguous region
+    assert st.rollback_bytes() == 2 * (hi - lo)
+    assert not read(lo, hi - lo).any()                      # state::init zeroes it
+    st.close()
+
+
+def test_reset_zeroes_recurrent_only(gpu):
+    rng = np.random.default_rng(1)
+    cfg = small_cfg()
+    st = new_state(cfg)
+    data = scribble(st, cfg, rng)
+    st.step_done(100)
+    say("state: reset")
+    st.reset()
+    for key, t in all_tensors(st, cfg):
+        got = read(t.data, nbytes(t))
+        if recurrent(key):
+            assert not got.any(), key
+        else:
+            np.testing.assert_array_equal(got, data[key])   # the caches are not cleared
+    assert st.n_past() == 0 and st.rollback_depth() == 0
+
+
+def test_rollback_restores_the_slot(gpu):
+    rng = np.random.default_rng(2)
+    cfg = small_cfg()
+    st = new_state(cfg)
+    scribble(st, cfg, rng)
+    rec = [(key, t) for key, t in all_tensors(st, cfg) if recurrent(key)]
+    slots = []
+    for s in range(2):
+        img = {}
+        for key, t in rec:
+            img[key] = rng.integers(0, 256, nbytes(t), dtype=np.uint8)
+            write(st.rollback_slot(key[0], key[1], s).data, img[key])
+        slots.append(img)
+    st.step_done(40)
+    st.step_done(3, verified=True)
+    assert st.rollback_depth() == 2 and st.n_past() == 43
+    say("state: rollback 2")
+    ok, err = st.rollback_n(2)
+    assert ok, err
+    for key, t in rec:
+        np.testing.assert_array_equal(read(t.data, nbytes(t)), slots[1][key])
+    assert st.n_past() == 41 and st.rollback_depth() == 0
+    ok, err = st.rollback_n(1)
+    assert not ok and err == "rollback: no snapshot of the state 1 tokens back"
+    st.step_done(3, verified=True)
+    say("state: rollback 1")
+    assert st.rollback_n(1)[0]
+    for key, t in rec:
+        np.testing.assert_array_equal(read(t.data, nbytes(t)), slots[0][key])
+    assert st.n_past() == 43
+
+
+@pytest.mark.parametrize("where", ["device", "pinned", "pageable"])
+def test_snapshot_save_unrelated_load(gpu, where):
+    import torch
+    rng = np.random.default_rng(3)
+    cfg = small_cfg()
+    head_cfg = small_cfg(n_layer=4, full_attention_interval=4, ple_n_head=0, n_rollback=0)
+    trunk, head = new_state(cfg), new_state(head_cfg)
+    states = [trunk, head]
+    saved = [scribble(trunk, cfg, rng), scribble(head, head_cfg, rng)]
+    n_past = 777
+    for s in states:
+        s.step_done(n_past)
+    say(f"snapshot: save ({where})")
+    snap = S.snapshot_save(states, S.MEM_DEVICE if where == "device" else S.MEM_HOST)
+    if where == "pageable":
+        snap = S.Snapshot(snap.n_past, [b.cpu().clone() for b in snap.blobs])
+        assert not snap.blobs[0].is_pinned()
+    want = SO.snapshot_parts([{**SO.config_default(1024), **_cfg_dict(cfg)},
+                              {**SO.config_default(1024), **_cfg_dict(head_cfg)}], n_past)
+    assert snap.n_past == n_past and [b.numel() for b in snap.blobs] == [p[3] for p in want]
+    # an unrelated sequence in between
+    scribble(trunk, cfg, rng)
+    scribble(head, head_cfg, rng)
+    for s in states:
+        s.step_done(5)
+    say(f"snapshot: load ({where})")
+    ok, err = S.snapshot_load(states, snap)
+    assert ok, err
+    torch.cuda.synchronize()
+    for s, c, sv in ((trunk, cfg, saved[0]), (head, head_cfg, saved[1])):
+        assert s.n_past() == n_past
+        for key, t in all_tensors(s, c):
+            n = nbytes(t) if recurrent(key) else min(nbytes(t), n_past * (t.nb[1] // cfg.n_ctx))
+            np.testing.assert_array_equal(read(t.data, n), sv[key][:n], err_msg=str(key))
+
+
+def _cfg_dict(c):
+    return {f: getattr(c, f) for f, _ in K.StateConfig._fields_}
+
+
+def test_snapshot_mismatch_is_rejected_after_reset(gpu):
+    rng = np.random.default_rng(4)
+    cfg = small_cfg()
+    st = new_state(cfg)
+    scribble(st, cfg, rng)
+    st.step_done(64)
+    snap = S.snapshot_save([st], S.MEM_DEVICE)
+    short = S.Snapshot(snap.n_past, snap.blobs[:-1])
+    say("snapshot: part count mismatch")
+    ok, err = S.snapshot_load([st], short)
+    assert not ok and "parts given" in err
+    assert st.n_past() == 0
+    for key, t in all_tensors(st, cfg):
+        if recurrent(key):
+            assert not read(t.data, nbytes(t)).any()        # reset before the check, as the reference
+    bad = S.Snapshot(snap.n_past + 1, snap.blobs)            # positional parts one row short
+    ok, err = S.snapshot_load([st], bad)
+    assert not ok and "expected" in err
+    ok, err = S.snapshot_load([st], snap)
+    assert ok and st.n_past() == 64
+
+
+def test_host_resident_caches_snapshot(gpu):
+    rng = np.random.default_rng(5)
+    cfg = small_cfg(n_ctx=512, kv_host=1, idx_host=1)
+    st = new_state(cfg)
+    assert st.host_bytes() > 0 and "pinned host memory" in st.summary()
+    data = scribble(st, cfg, rng)
+    st.step_done(300)
+    say("snapshot: host-resident caches")
+    snap = S.snapshot_save([st], S.MEM_DEVICE)
+    scribble(st, cfg, rng)
+    assert S.snapshot_load([st], snap)[0]
+    for key, t in all_tensors(st, cfg):
+        n = nbytes(t) if recurrent(key) else min(nbytes(t), 300 * (t.nb[1] // 512))
+        np.testing.assert_array_equal(read(t.data, n), data[key][:n], err_msg=str(key))
+
+
+def test_state_caches_feed_attention(gpu):
+    """The state's K/V caches are the reference's views: appending into them and
+    attending over them gives the bytes and outputs of a separately held cache."""
+    import torch
+    import kvdata as KD
+    from gpu_util import gpu_attn
+    cfg = S.config(2048)
+    st = new_state(cfg)
+    il = 3
+    kt, vt = st.k_cache(il), st.v_cache(il)
+    n = 700
+    krows = KD.kv_rows(7, il, KD.K_KIND, n)
+    vrows = KD.kv_rows(7, il, KD.V_KIND, n)
+    idx = dev(np.arange(n, dtype=np.int32))
+    rb = 544
+    say("state: set_rows into the state's caches, then attention")
+    import ctypes
+    iv = K.tensor(idx.data_ptr(), K.TYPE_I32, (n,), (4,))
+    for t, rows in ((kt, krows), (vt, vrows)):
+        dst = K.tensor(t.data, K.TYPE_Q8_0, (512, 2048), (34, rb))
+        src = dev(rows)
+        K.check(K.load().qwfn_set_rows_q8_0(ctypes.byref(dst), ctypes.byref(K.f32_view(src)), ctypes.byref(iv),
+                                            K.Q8_X86, K._stream(None)))
+        host(src)
+    kc = read(kt.data, n * rb).reshape(n, rb)
+    vc = read(vt.data, n * rb).reshape(n, rb)
+    from oracle import oracle as O
+    ref_k = np.zeros((n, rb), np.uint8)
+    ref_v = np.zeros((n, rb), np.uint8)
+    O.set_rows(ref_k, krows, np.arange(n, dtype=np.int32))
+    O.set_rows(ref_v, vrows, np.arange(n, dtype=np.int32))
+    np.testing.assert_array_equal(kc, ref_k)
+    np.testing.assert_array_equal(vc, ref_v)
+    q = KD.q_rows(7, il, 3, 16)[0]
+    mask = SO.attn_inputs_mask(n - 3, 3)
+    out = torch.empty((1, 3, 16, 256), dtype=torch.float32, device="cuda")
+    qd = dev(q[None].astype(np.float32))
+    md = dev(mask.view(np.float16))
+    kv = K.tensor(kt.data, K.TYPE_Q8_0, (256, n, 2, 1), (34, rb, 272, n * rb))
+    vv = K.tensor(vt.data, K.TYPE_Q8_0, (256, n, 2, 1), (34, rb, 272, n * rb))
+    K.flash_attn_ext(K.q_view(qd), kv, vv, K.mask_view(md), 1 / 16, K.out_view(out), K.Q8_X86)
+    got = host(out)[0]
+    np.testing.assert_array_equal(got, gpu_attn(K, q, kc, vc, n, 2, mask, 1 / 16))
+    del torch
+
+
+@pytest.mark.parametrize("n_kv,T,n_past,row", [(19, 3, 16, 19), (1027, 5, 1022, 1088), (4608, 512, 4096, 4608),
+                                               (16387, 3, 16384, 16387), (8, 1, 7, 8), (40, 2, 0, 64)])
+def test_causal_mask_matches_oracle(gpu, n_kv, T, n_past, row):
+    import torch
+    m = torch.full((T, row), 0x1234, dtype=torch.int16, device="cuda")
+    say(f"causal mask n_kv={n_kv} T={T} n_past={n_past} row={row}")
+    K.check(K.load().qwfn_causal_mask_f16(m.data_ptr(), n_kv, T, n_past, row * 2, K._stream(None)))
+    got = host(m).view(np.uint16)
+    want = np.full((T, row), SO.F16_NEG_INF, np.uint16)
+    vis = np.arange(row)[None, :] <= (n_past + np.arange(T))[:, None]
+    want[(vis) & (np.arange(row)[None, :] < n_kv)] = SO.F16_ZERO
+    if n_kv == n_past + T:
+        np.testing.assert_array_equal(want[:, :n_kv], SO.attn_inputs_mask(n_past, T))
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("n_cells,n_pad,n_past", [(2052, 2304, 65535), (2052, 2304, 100), (256, 256, 0), (5, 9, 3)])
+def test_cell_mask_matches_oracle(gpu, n_cells, n_pad, n_past):
+    import torch
+    rng = np.random.default_rng(n_cells + n_past)
+    cells = np.sort(rng.choice(max(n_past + 50, n_cells + 10), n_cells, replace=False)).astype(np.int32)
+    cd = dev(cells)
+    m = torch.full((n_pad,), 0x1234, dtype=torch.int16, device="cuda")
+    g = torch.full((n_pad,), -7, dtype=torch.int32, device="cuda")
+    say(f"cell mask n_cells={n_cells} n_pad={n_pad} n_past={n_past}")
+    S.cell_mask_f16(cd, n_past, n_pad, m, g)
+    want_m, want_g = SO.cell_mask(cells, n_past, n_pad)
+    np.testing.assert_array_equal(host(m).view(np.uint16), want_m)
+    np.testing.assert_array_equal(host(g), want_g)
+
+
+def test_qsa_decode_inputs_match_oracle(gpu):
+    ratio, nb_max = 4, 64
+    qd = S.QsaDecodeInputs(ratio, nb_max)
+    qk = S.QsaDecodeInputs(ratio, nb_max)
+    bias = SO.qsa_reset_bias(nb_max)
+    say("qsa decode inputs: positions 0..259")
+    for n in range(0, 260):
+        qd.prepare(n)
+        o = SO.qsa_decode_prepare(bias, n, ratio)
+        for f in ("write_idx", "member_idx", "blk_pos", "blk_idx", "npast_f", "bias"):
+            np.testing.assert_array_equal(host(getattr(qd, f)), o[f], err_msg=f"{f} at {n}")
+        qk.prepare(n + 1, prev=qd)
+        ok_ = SO.qsa_decode_prepare_k(bias, n + 1, ratio)
+        for f in ("write_idx", "member_idx", "blk_pos", "blk_idx", "npast_f", "bias"):
+            np.testing.assert_array_equal(host(getattr(qk, f)), ok_[f], err_msg=f"k {f} at {n}")
+        assert qk.n_bucket == qd.n_bucket == max(SO.qsa_bucket(n, ratio, nb_max), SO.qsa_bucket(n + 1, ratio, nb_max))
+    for n in (-1, 0, 3, 4, 100, 255, 256, 10 ** 5):
+        qd.rebuild_bias(n)
+        want = SO.qsa_reset_bias(nb_max) if n < 0 else SO.qsa_pool_rebuild_bias(nb_max, n, ratio)
+        np.testing.assert_array_equal(host(qd.bias), want, err_msg=str(n))
+
+
+def test_qsa_tables_match_oracle(gpu):
+    import torch
+    ratio, nb_max, n_ctx, n_whole = 4, 300, 1200, 77
+    bc = torch.full((nb_max * ratio,), -1, dtype=torch.int32, device="cuda")
+    cp = torch.full((n_ctx,), -1.0, dtype=torch.float32, device="cuda")
+    bp = torch.full((4 * n_whole,), -1, dtype=torch.int32, device="cuda")
+    say("qsa tables")
+    S.qsa_tables(bc, ratio, cp, bp, n_whole)
+    w_bc, w_cp, w_bp = SO.qsa_tables(nb_max, ratio, n_ctx, n_whole)
+    np.testing.assert_array_equal(host(bc), w_bc)
+    np.testing.assert_array_equal(host(cp), w_cp)
+    np.testing.assert_array_equal(host(bp), w_bp)

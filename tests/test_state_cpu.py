@@ -1,0 +1,256 @@
+"""CPU tests of the state rows: the oracle restatement pinned against the
+reference's logged numbers and its own independent code paths, and the
+library's layout-only state, bookkeeping and host-side validation (no GPU)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import qwfn_kv as K
+import qwfn_state as S
+from oracle import state_oracle as SO
+
+# The summary line every run in the reference's benchmark logs prints at 73728
+# positions (bench/evidence/raw/llamabench/*.log, engine::memory_summary).
+GOLDEN_SUMMARY_73728 = ("state @ 73728 ctx: KV 0.962593 GB (q8_0), indexer 0.226492 GB, deltanet 113.246 MB "
+                        "(constant), conv 4.79232 MB  =>  total 1.30712 GB on the device")
+
+
+def layout_state(n_ctx, **kw):
+    st = S.State()
+    ok, err = st.init(S.config(n_ctx, **kw), S.LAYOUT_ONLY)
+    assert ok, err
+    return st
+
+
+def small_cfg(**kw):
+    d = dict(n_layer=8, ssm_d_state=16, ssm_n_group=2, ssm_dt_rank=4, hc_count=2, n_embd=64, n_rollback=2)
+    d.update(kw)
+    return d
+
+
+# ------------------------------------------------------------------ oracle pins
+
+def test_oracle_summary_matches_reference_log():
+    cfg = SO.config_default(73728)
+    total = sum(t["nbytes"] for t in SO.declare_tensors(cfg))
+    assert SO.summary(cfg, total) == GOLDEN_SUMMARY_73728
+
+
+def test_oracle_sizes_match_reference_comments():
+    # qwfn_state.h:4-8: KV @128K q8_0 1.71 GB (f16 3.22 GB), indexer @128K f16
+    # 0.40 GB, 113 MB f32 of DeltaNet state for all 36 layers
+    for typ, gb in ((SO.TYPE_Q8_0, 1.71), (SO.TYPE_F16, 3.22)):
+        cfg = SO.config_default(131072)
+        cfg["type_k"] = cfg["type_v"] = typ
+        ts = SO.declare_tensors(cfg)
+        kv = sum(t["nbytes"] for t in ts if t["kind"] in (SO.K, SO.V))
+        assert round(kv / 1e9, 2) == gb
+        assert round(sum(t["nbytes"] for t in ts if t["kind"] == SO.IDX) / 1e9, 2) == 0.40
+        assert round(sum(t["nbytes"] for t in ts if t["kind"] == SO.RS) / 1e6) == 113
+    # 12 attention layers, 36 DeltaNet layers (qwfn_hparams.h:30)
+    ts = SO.declare_tensors(SO.config_default(1024))
+    assert sum(t["kind"] == SO.K for t in ts) == 12 and sum(t["kind"] == SO.RS for t in ts) == 36
+
+
+def test_oracle_snapshot_parts_closed_form():
+    cfg = SO.config_default(73728)
+    parts = SO.snapshot_parts([cfg], 8192)
+    assert len(parts) == 12 * 3 + 36 * 2 + 1
+    kv = sum(b for _, k, _, b in parts if k in (SO.K, SO.V))
+    assert kv == 12 * 8192 * 1088                            # 106.95 MB per slot
+    assert sum(b for _, k, _, b in parts if k == SO.IDX) == 12 * 8192 * 256   # 25.2 MB
+    # positional parts are capped at the tensor, recurrent parts are whole
+    full = SO.snapshot_parts([cfg], 10 ** 6)
+    assert sum(b for _, k, _, b in full if k == SO.K) == 12 * 73728 * 544
+    assert all(b == 0 for _, k, _, b in SO.snapshot_parts([cfg], 0) if k in (SO.K, SO.V, SO.IDX))
+    # order: layer by layer, K V idx or rs conv, the PLE history last; a second state follows
+    kinds = [k for _, k, _, _ in parts]
+    assert kinds[:6] == [SO.RS, SO.CONV] * 3 and kinds[6:9] == [SO.K, SO.V, SO.IDX] and kinds[-1] == SO.PLE_CONV
+    two = SO.snapshot_parts([cfg, cfg], 5)
+    assert two[:len(two) // 2] == [(0,) + p[1:] for p in SO.snapshot_parts([cfg], 5)]
+    assert {p[0] for p in two[len(two) // 2:]} == {1}
+
+
+def test_oracle_causal_mask_builders_agree():
+    from oracle import oracle as O
+    for n_past in (0, 1, 7, 64):
+        for T in (1, 2, 3, 9):
+            a = SO.attn_inputs_mask(n_past, T)
+            assert np.array_equal(a, SO.step_inputs_mask(n_past, T))
+            assert np.array_equal(a, SO.mtp_mask(n_past, T))
+            assert np.array_equal(a, O.causal_mask(T, n_past))
+            # the last row sees every key, the first n_past + 1
+            assert (a[-1] == SO.F16_ZERO).all() and (a[0] == SO.F16_ZERO).sum() == n_past + 1
+
+
+def test_oracle_cell_mask_op_chain_is_an_integer_compare():
+    rng = np.random.default_rng(5)
+    for n_past in (0, 3, 1000, 73727):
+        cells = np.concatenate([rng.integers(0, 73728, 200), [n_past, n_past + 1, max(n_past - 1, 0)]]).astype(np.int32)
+        mask, g = SO.cell_mask(cells, n_past, 256)
+        ref = np.where(cells <= n_past, SO.F16_ZERO, SO.F16_NEG_INF)
+        assert np.array_equal(mask[:cells.size], ref)
+        assert (mask[cells.size:] == SO.F16_NEG_INF).all()
+        assert np.array_equal(g[:cells.size], cells) and np.array_equal(g[cells.size:], cells[:256 - cells.size])
+
+
+def test_oracle_bias_window_equals_full_rebuild():
+    # Applying the per-token window from a reset bias for positions 0..n gives
+    # qsa_pool_rebuild's full bias at n: two separate reference functions.
+    for ratio in (1, 4, 5):
+        nb_max = 40
+        bias = SO.qsa_reset_bias(nb_max)
+        for n in range(ratio * nb_max + 3):
+            SO.qsa_decode_prepare(bias, n, ratio)
+            assert np.array_equal(bias, SO.qsa_pool_rebuild_bias(nb_max, n, ratio)), (ratio, n)
+            prev = bias.copy()
+            k = SO.qsa_decode_prepare_k(prev, n + 1, ratio)["bias"]
+            assert np.array_equal(k, SO.qsa_pool_rebuild_bias(nb_max, n + 1, ratio)), (ratio, n)
+
+
+def test_oracle_decode_inputs_and_bucket():
+    o = SO.qsa_decode_prepare(SO.qsa_reset_bias(16), 13, 4)
+    assert o["write_idx"][0] == 13 and o["blk_idx"][0] == 3
+    assert list(o["member_idx"]) == [12, 13, 14, 15] and list(o["blk_pos"]) == [12] * 4
+    assert o["npast_f"][0] == 13.0
+    assert list(o["bias"][:5]) == [-np.inf, -np.inf, 0.0, 1e9, -np.inf]   # only the window is written
+    assert SO.qsa_bucket(0, 4, 18432) == 768
+    assert SO.qsa_bucket(4 * 767, 4, 18432) == 768 and SO.qsa_bucket(4 * 768, 4, 18432) == 1024
+    assert SO.qsa_bucket(73727, 4, 18432) == 18432 and SO.qsa_bucket(10 ** 6, 4, 1000) == 1000
+
+
+def test_oracle_rollback_bookkeeping():
+    assert SO.rollback_depth_after_step(3, True, 2) == 2
+    assert SO.rollback_depth_after_step(3, True, 1) == 1
+    assert SO.rollback_depth_after_step(1, True, 2) == 0
+    assert SO.rollback_depth_after_step(3, False, 2) == 0
+    assert SO.rollback_depth_after_step(3, True, 0) == 0
+    assert not SO.rollback_ok(0, 2) and SO.rollback_ok(2, 2) and not SO.rollback_ok(3, 2)
+
+
+# ------------------------------------------------------- library, layout only
+
+def test_library_summary_matches_reference_log():
+    st = layout_state(73728)
+    assert st.summary() == GOLDEN_SUMMARY_73728
+    assert st.bytes() == 1307123712 and st.n_ctx() == 73728 and st.host_bytes() == 0
+
+
+@pytest.mark.parametrize("n_ctx,kw", [(73728, {}), (1000, small_cfg()), (4096, small_cfg(type_k=1, type_v=1)),
+                                      (512, small_cfg(ple_n_head=0, full_attention_interval=2, type_idx=0)),
+                                      (300, small_cfg(kv_host=1, idx_host=1))])
+def test_library_layout_matches_oracle(n_ctx, kw):
+    st = layout_state(n_ctx, **kw)
+    cfg = SO.config_default(n_ctx)
+    cfg.update(kw)
+    ts = SO.declare_tensors(cfg)
+    seen = []
+    for t in ts:
+        d = st.tensor(t["kind"], t["il"])
+        assert d is not None and d.type == t["type"] and list(d.ne) == t["ne"]
+        assert d.nb[3] * d.ne[3] == t["nbytes"] and (d.data or 0) % 256 == 0
+        seen.append((bool(kw.get("kv_host") if t["kind"] in (0, 1) else kw.get("idx_host") if t["kind"] == 2 else 0),
+                     d.data or 0, t["nbytes"]))
+    for arena in (False, True):                 # no overlaps within an arena
+        spans = sorted((a, a + n) for h, a, n in seen if h == arena)
+        assert all(e0 <= a1 for (_, e0), (a1, _) in zip(spans, spans[1:]))
+    # the wrong layer kind gives null, like k_cache() on a DeltaNet layer
+    assert st.k_cache(0) is None and st.rs_state(cfg["full_attention_interval"] - 1) is None
+    assert st.tensor(S.STATE_K, 10 ** 6) is None
+    dev_total = sum(n for h, _, n in seen if not h)
+    host_total = sum(n for h, _, n in seen if h)
+    assert dev_total <= st.bytes() <= dev_total + 256 * len(ts)
+    assert host_total <= st.host_bytes() <= host_total + 256 * len(ts)
+    assert st.summary() == SO.summary(cfg, st.bytes(), st.host_bytes())
+    # snapshot parts: the oracle's order and sizes
+    for n_past in (0, 1, 77, n_ctx, n_ctx + 5):
+        got = S.snapshot_parts([st, st], n_past)
+        want = SO.snapshot_parts([cfg, cfg], n_past)
+        assert [b for _, b in got] == [p[3] for p in want]
+
+
+def test_library_rollback_slots_layout():
+    # each rollback slot is an image of the live recurrent region, same layout
+    st = layout_state(256, **small_cfg(n_rollback=3))
+    rec = [(k, il) for il in range(8) for k in (S.STATE_RS, S.STATE_CONV) if st.tensor(k, il) is not None]
+    rec.append((S.STATE_PLE_CONV, 0))
+    live = {r: st.tensor(*r) for r in rec}
+    base = min(t.data or 0 for t in live.values())
+    span = st.rollback_bytes() // 3
+    assert span * 3 == st.rollback_bytes() and span >= sum(t.nb[3] * t.ne[3] for t in live.values())
+    for r, t in live.items():
+        for s in range(3):
+            d = st.rollback_slot(r[0], r[1], s)
+            assert (d.data or 0) == s * span + (t.data or 0) - base and list(d.ne) == list(t.ne)
+    with pytest.raises(K.QwfnError):
+        st.rollback_slot(S.STATE_RS, 0, 3)
+    with pytest.raises(K.QwfnError):
+        st.rollback_slot(S.STATE_K, 3, 0)
+
+
+def test_library_bookkeeping_and_rollback_guard():
+    st = layout_state(64, **small_cfg(n_rollback=2))
+    st.step_done(10)
+    assert st.n_past() == 10 and st.rollback_depth() == 0
+    st.step_done(3, verified=True)
+    assert st.n_past() == 13 and st.rollback_depth() == 2
+    ok, err = st.rollback_n(3, stream=0)
+    assert not ok and err == "rollback: no snapshot of the state 3 tokens back"
+    ok, err = st.rollback_n(0, stream=0)
+    assert not ok and "0 tokens back" in err
+    ok, err = st.rollback_n(1, stream=0)         # guard passes; no memory without a device
+    assert not ok and "no rollback memory" in err
+    with pytest.raises(K.QwfnError, match="context exhausted"):
+        st.step_done(64 - 13 + 1)
+    st.step_done(64 - 13)
+    assert st.n_past() == 64
+    with pytest.raises(K.QwfnError, match="QWFN_LAYOUT_ONLY"):
+        st.reset(stream=0)
+
+
+def test_library_config_validation():
+    for kw, needle in ((dict(n_ctx=0), "n_ctx"), (dict(type_k=26), "type_k"), (dict(type_idx=8), "type_idx"),
+                       (dict(n_head_kv=3, n_embd_head_k=8, n_embd_head_v=8), "32-value"),
+                       (dict(ssm_d_conv=1), "d_conv"), (dict(n_rollback=65), "rollback")):
+        cfg = S.config(kw.pop("n_ctx", 128), **kw)
+        ok, err = S.State().init(cfg, S.LAYOUT_ONLY)
+        assert not ok and needle in err, (kw, err)
+
+
+def test_library_bucket():
+    L = K.load()
+    for n_past, ratio, nb in ((0, 4, 18432), (3067, 4, 18432), (3072, 4, 18432), (73727, 4, 18432), (10 ** 6, 4, 1000),
+                              (5, 1, 700)):
+        assert L.qwfn_qsa_bucket(n_past, ratio, nb) == SO.qsa_bucket(n_past, ratio, nb)
+
+
+def test_step_input_validation():
+    L = K.load()
+    FAKE = 0x7F0000000000
+
+    def err(rc, code, needle):
+        assert rc == code, (rc, L.qwfn_last_error())
+        assert needle in L.qwfn_last_error().decode()
+
+    err(L.qwfn_causal_mask_f16(None, 4, 1, 0, 8, None), K.EINVAL, "NULL")
+    err(L.qwfn_causal_mask_f16(FAKE, 4, 1, 0, 6, None), K.EALIGN, "row_stride")
+    err(L.qwfn_causal_mask_f16(FAKE, 4, 1, 0, 9, None), K.EALIGN, "row_stride")
+    err(L.qwfn_cell_mask_f16(FAKE, 10, 21, 0, FAKE, None, None), K.EINVAL, "n_pad")
+    err(L.qwfn_cell_mask_f16(FAKE, 10, 9, 0, FAKE, None, None), K.EINVAL, "n_pad")
+    err(L.qwfn_cell_mask_f16(FAKE, 10, 16, -1, FAKE, None, None), K.EINVAL, "n_past")
+    q = K.QsaInputs()
+    err(L.qwfn_qsa_decode_prepare(ctypes.byref(q), None, 0, None), K.EINVAL, "NULL")
+    for f in ("bias", "write_idx", "member_idx", "blk_pos", "blk_idx", "npast_f"):
+        setattr(q, f, FAKE)
+    q.ratio, q.n_blocks_max = 0, 16
+    err(L.qwfn_qsa_decode_prepare(ctypes.byref(q), None, 0, None), K.EINVAL, "ratio")
+    err(L.qwfn_qsa_bias_rebuild(FAKE, 16, -2, 4, None), K.EINVAL, "sizes")
+    err(L.qwfn_qsa_tables(FAKE, 1 << 30, 4, None, 0, None, 0, None), K.ERANGE, "int32")
+    # snapshot calls need states with memory
+    st = layout_state(64, **small_cfg())
+    H = (ctypes.c_void_p * 1)(st.handle)
+    err(L.qwfn_snapshot_save(H, 1, None, None, 0, 0, None, None), K.EINVAL, "no memory")
+    err(L.qwfn_snapshot_load(H, 1, 0, None, None, 0, 0, None), K.EINVAL, "no memory")
+    n = ctypes.c_int32(0)
+    err(L.qwfn_snapshot_parts(H, 1, -1, None, 0, ctypes.byref(n)), K.EINVAL, "position")
