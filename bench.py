@@ -97,6 +97,81 @@ def timed_graph(torch, fn, per_graph: int, reps: int) -> float:
     return e0.elapsed_time(e1) * 1e3 / (reps * per_graph)
 
 
+def measure_state_rows(K, torch, np, dev, gbs) -> dict:
+    """The state rows on the model's own state (48 layers, 73728 positions, 2 rollback
+    slots): reset of the recurrent region, an MTP-verify rollback, snapshot save and
+    load of an 8192-position prefix with device blobs (and save into pinned host
+    blobs), the 512-query causal mask of a prefill chunk, and one decode step's
+    sparse-attention inputs and cell mask."""
+    import ctypes
+    import qwfn_state as S
+    rows = {}
+    frac = lambda b, us: round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+    st = S.State()
+    ok, err = st.init(S.config(73728, n_rollback=2), 0)
+    if not ok:
+        raise RuntimeError(err)
+    rec = st.rollback_bytes() // 2
+    us = timed(torch, lambda k: st.reset(), 10)
+    rows["state_reset"] = {"us_per_op": round(us, 1), "bytes_written": rec, "GBs": gbs(rec, us), "frac": frac(rec, us)}
+
+    def rollback(k):
+        # alternate the two slots: one slot image read every time would stay in the 256 MB cache
+        st.step_done(3, verified=True)
+        ok_, err_ = st.rollback_n(1 + (k & 1))
+        if not ok_:
+            raise RuntimeError(err_)
+    us = timed(torch, rollback, 10)
+    rows["state_rollback"] = {"us_per_op": round(us, 1), "bytes_read": rec, "bytes_written": rec,
+                              "GBs": gbs(2 * rec, us), "frac": frac(2 * rec, us)}
+
+    st.reset()
+    st.step_done(8192)
+    parts = S.snapshot_parts([st], 8192)
+    snap_b = sum(b for _, b in parts)
+    blobs = [torch.empty(max(b, 1), dtype=torch.uint8, device=dev) for _, b in parts]
+    H = (ctypes.c_void_p * 1)(st.handle)
+    P = (ctypes.c_void_p * len(parts))(*[x.data_ptr() for x in blobs])
+    B = (ctypes.c_size_t * len(parts))(*[b for _, b in parts])
+    L = K.load()
+    stream = lambda: K._stream(None)
+    us = timed(torch, lambda k: K.check(L.qwfn_snapshot_save(H, 1, P, B, len(parts), S.MEM_DEVICE, None, stream())), 10)
+    rows["snapshot_save_device"] = {"us_per_op": round(us, 1), "positions": 8192, "parts": len(parts),
+                                    "bytes": snap_b, "GBs": gbs(2 * snap_b, us), "frac": frac(2 * snap_b, us)}
+    us = timed(torch, lambda k: K.check(L.qwfn_snapshot_load(H, 1, 8192, P, B, len(parts), S.MEM_DEVICE, stream())), 10)
+    moved = 2 * snap_b + rec                       # the load resets the recurrent region first
+    rows["snapshot_load_device"] = {"us_per_op": round(us, 1), "bytes": snap_b, "GBs": gbs(moved, us),
+                                    "frac": frac(moved, us)}
+    hb = [torch.empty(max(b, 1), dtype=torch.uint8, pin_memory=True) for _, b in parts]
+    PH = (ctypes.c_void_p * len(parts))(*[x.data_ptr() for x in hb])
+    us = timed(torch, lambda k: K.check(L.qwfn_snapshot_save(H, 1, PH, B, len(parts), S.MEM_HOST, None, stream())), 3)
+    rows["snapshot_save_pinned_host"] = {"us_per_op": round(us, 1), "bytes": snap_b, "host_link_GBs": gbs(snap_b, us)}
+    del blobs, hb
+    st.close()
+
+    T, d0 = 512, 16384
+    mask = torch.empty((T, d0 + T), dtype=torch.float16, device=dev)
+    us = timed_graph(torch, lambda k: S.causal_mask_f16(mask, d0 + T, T, d0), 16, 10)
+    rows["causal_mask_512_at_16k"] = {"us_per_op": round(us, 2), "bytes_written": mask.numel() * 2,
+                                      "GBs": gbs(mask.numel() * 2, us), "frac": frac(mask.numel() * 2, us)}
+    del mask
+    nb_max = 73728 // 4
+    qd, qk = S.QsaDecodeInputs(4, nb_max), S.QsaDecodeInputs(4, nb_max)
+    cells = torch.randint(0, 65536, (2052,), dtype=torch.int32, device=dev)
+    cmask = torch.empty(2304, dtype=torch.float16, device=dev)
+    gcells = torch.empty(2304, dtype=torch.int32, device=dev)
+
+    def decode_inputs(k):
+        qd.prepare(65533 + (k & 1))
+        qk.prepare(65534 + (k & 1), prev=qd)
+        S.cell_mask_f16(cells, 65533, 2304, cmask, gcells)
+    us = timed_graph(torch, decode_inputs, 16, 10)
+    rows["decode_step_inputs"] = {"us_per_step": round(us, 2), "launches": 3,
+                                  "what": "qsa_decode_prepare, qsa_decode_prepare_k (18432-block bias), cell mask 2052->2304"}
+    torch.cuda.empty_cache()
+    return rows
+
+
 def measure_rows(K, torch, np, dev, gen) -> dict:
     """The other rows of the path on their own workloads: append of a 512-row prefill chunk,
     the per-KV-head sparse gather at 64K, snapshot restore into 4 slots, batch-4 ragged decode
@@ -175,6 +250,8 @@ def measure_rows(K, torch, np, dev, gen) -> dict:
     rows["restore_pinned_host"] = {"us_per_op": round(us, 1), "bytes_per_slot": per_slot, "slots": 4,
                                    "host_link_GBs": gbs(per_slot, us)}
     del src, kv_dst, dn_dst, host
+
+    rows.update(measure_state_rows(K, torch, np, dev, gbs))
 
     # ---- batch-4 ragged decode: one query per slot at depths 8192..65536 (mask [n_kv,1,1,4]) ----
     depths = [8192, 16384, 32768, 65536]
