@@ -147,6 +147,21 @@ def measure_state_rows(K, torch, np, dev, gbs) -> dict:
     us = timed(torch, lambda k: K.check(L.qwfn_snapshot_save(H, 1, PH, B, len(parts), S.MEM_HOST, None, stream())), 3)
     rows["snapshot_save_pinned_host"] = {"us_per_op": round(us, 1), "bytes": snap_b, "host_link_GBs": gbs(snap_b, us)}
     del blobs, hb
+    # the server's switch between two conversations of 8192 positions (restore_or_reset):
+    # the current one is set aside in the HBM pool and the other restored
+    pool = S.SnapPool(1024 << 20, 4, 0)
+    convs = [[7] * 8192, [9] * 8192]
+    pool.save_seq([st], convs[1])
+
+    def switch(k):
+        n = pool.restore_or_reset([st], convs[k & 1], convs[(k + 1) & 1] + [1])
+        if n != 8192:
+            raise RuntimeError("pool: the conversation was not restored")
+    us = timed(torch, switch, 10)
+    moved = 4 * snap_b + rec                       # save (read + write), reset, load (read + write)
+    rows["pool_switch_conversation"] = {"us_per_op": round(us, 1), "positions": 8192, "GBs": gbs(moved, us),
+                                        "frac": frac(moved, us)}
+    pool.close()
     st.close()
 
     T, d0 = 512, 16384

@@ -10,6 +10,7 @@
  *   engine::rollback_n                                  qwfn_engine.cpp:3629-3660
  *   snapshot_parts / snapshot_save / snapshot_load      qwfn_engine.cpp:988-1053
  *   engine::reset                                       qwfn_engine.cpp:1055-1066
+ *   saved-sequence pool of the server                   tools/qwfn_server.cpp:767-793, :1380-1424
  *   decode cell mask and padded cell list               qwfn_graph.cpp:668-675, :681-693
  *   causal masks of prefill chunks, steps, MTP drafts   qwfn_engine.cpp:1261-1271, :2093-2098, :3415-3440
  *   qsa_decode_prepare / _k, qsa_pool_rebuild (bias),
@@ -108,7 +109,8 @@ int32_t qwfn_state_rollback_depth(const qwfn_state * st);
 int qwfn_state_step_done(qwfn_state * st, int32_t T, int32_t verified);
 
 /* engine::reset minus the engine-only flags: zero the recurrent tensors (one
- * fill kernel; the caches are not cleared), n_past = 0, rollback depth 0. */
+ * fill kernel; the caches are not cleared), n_past = 0, rollback depth 0. A
+ * QWFN_LAYOUT_ONLY state only has its bookkeeping reset. */
 int qwfn_state_reset(qwfn_state * st, void * stream);
 
 /* engine::rollback_n: copy rollback slot n_back-1 over the live recurrent
@@ -149,6 +151,50 @@ int qwfn_snapshot_save(const qwfn_state * const * sts, int32_t n_sts, void * con
  * else copy each part in and set n_past on every state. */
 int qwfn_snapshot_load(qwfn_state * const * sts, int32_t n_sts, int32_t n_past, const void * const * src,
                        const size_t * src_bytes, int32_t n_src, int32_t src_kind, void * stream);
+
+/* ------------------------------------------------- saved-sequence pool */
+
+/* The server's saved sequences (saved_seq, save_seq, best_saved,
+ * tools/qwfn_server.cpp:767-793; restore_or_reset, :1380-1400;
+ * shared_prefix_split, :1401-1424) with the snapshots held in HBM instead of
+ * host vectors. At most max_entries (the reference: 4) sequences whose
+ * snapshot bytes sum to at most cap_bytes (QWFN_SNAP_MB), least recently used
+ * first. The pool arena is 2 x (cap + slack) bytes of device memory, allocated
+ * once; device = QWFN_LAYOUT_ONLY keeps the bookkeeping and copies nothing. */
+typedef struct qwfn_snap_pool qwfn_snap_pool;
+int     qwfn_snap_pool_create(size_t cap_bytes, int32_t max_entries, int device, qwfn_snap_pool ** out);
+void    qwfn_snap_pool_destroy(qwfn_snap_pool * pool);
+int32_t qwfn_snap_pool_count(const qwfn_snap_pool * pool);
+size_t  qwfn_snap_pool_bytes(const qwfn_snap_pool * pool);   /* snapshot bytes held */
+/* Entry k (0 = least recently used): token count, n_past, snapshot bytes, and
+ * up to tok_cap of its tokens. */
+int     qwfn_snap_pool_entry(const qwfn_snap_pool * pool, int32_t k, int32_t * n_tok, int32_t * n_past,
+                             size_t * bytes, int32_t * tok, int32_t tok_cap);
+/* save_seq: snapshot the states (at their n_past) under the token sequence.
+ * Returns 1 if kept, 0 if larger than the cap (not kept), or a negative code.
+ * An entry with the same tokens is replaced, then the least recently used go
+ * until the count and the bytes are within the limits. */
+int     qwfn_snap_pool_save(qwfn_snap_pool * pool, const qwfn_state * const * sts, int32_t n_sts,
+                            const int32_t * tok, int32_t n_tok, void * stream);
+/* best_saved: the longest saved sequence the prompt strictly extends, or -1
+ * (always -1 for a prompt with images). */
+int32_t qwfn_snap_pool_best(const qwfn_snap_pool * pool, const int32_t * tok, int32_t n_tok, int32_t has_images);
+/* snapshot_load of entry k into the states (reset first; QWFN_ESIZE if the
+ * states' parts differ from the saved ones); the entry becomes the most
+ * recently used. */
+int     qwfn_snap_pool_load(qwfn_snap_pool * pool, int32_t k, qwfn_state * const * sts, int32_t n_sts, void * stream);
+/* shared_prefix_split: where a fresh prefill of `prompt` should stop once so
+ * that its prefix shared with a saved sequence can be saved; 0 for none. */
+int32_t qwfn_snap_pool_split(const qwfn_snap_pool * pool, const int32_t * prompt, int32_t n_prompt, int32_t n_consumed,
+                             int32_t has_images);
+/* restore_or_reset: save the consumed sequence when it has >= 2048 tokens and
+ * no images, then load the best saved sequence the prompt extends (*n_restored
+ * = its token count; it is now the last entry), or reset the states
+ * (*n_restored = 0). The states' n_past must equal n_consumed. */
+int     qwfn_snap_pool_restore_or_reset(qwfn_snap_pool * pool, qwfn_state * const * sts, int32_t n_sts,
+                                        const int32_t * consumed, int32_t n_consumed, int32_t consumed_has_images,
+                                        const int32_t * prompt, int32_t n_prompt, int32_t prompt_has_images,
+                                        int32_t * n_restored, void * stream);
 
 /* ---------------------------------------------------------------- masks */
 

@@ -11,13 +11,17 @@ Each function follows the reference file:line named in its docstring:
                                  :1107-1125 (qsa_pool_rebuild), :672-684 (init_qsa_tables)
 * masks                          qwfn_engine.cpp:1261-1271, :2093-2098, :3415-3421;
                                  qwfn_graph.cpp:668-675, :681-693 (cell mask, padding)
+* saved-sequence pool            tools/qwfn_server.cpp:767-793, :1380-1424
 
-How each is pinned (tests/test_state_oracle.py): the layout and summary by the
+How each is pinned (tests/test_state_cpu.py): the layout and summary by the
 summary line the reference's own runs logged at 73728 positions and by the
 sizes in qwfn_state.h:4-8; the part list by closed-form byte counts; the bias
 window by its equality with the full rebuild after every decode position; the
 three causal-mask builders by their agreement with each other; the cell mask's
-ggml op chain (float arithmetic) by the integer comparison it reduces to.
+ggml op chain (float arithmetic) by the integer comparison it reduces to; the
+pool by scripted cases whose outcomes follow from the server's rules (count
+and byte caps, replacement of an equal sequence, strict extension, the split
+conditions) and by the invariants the server asserts.
 """
 from __future__ import annotations
 
@@ -264,3 +268,75 @@ def cell_mask(cells: np.ndarray, n_past: int, n_pad: int) -> tuple[np.ndarray, n
     mask = _f16_bits(ok * np.float32(1e30) - np.float32(1e30))
     gcells = np.concatenate([cells, cells[:n_pad - n]])
     return mask, gcells
+
+
+# ------------------------------------------------------- saved-sequence pool
+
+class SnapPool:
+    """The server's saved sequences (tools/qwfn_server.cpp:767-793) and the
+    decisions around them (restore_or_reset :1380-1400, shared_prefix_split
+    :1401-1424). Entries are (tokens, n_past, bytes), least recently used first."""
+
+    def __init__(self, cap: int, max_entries: int = 4):
+        self.cap, self.max_entries = cap, max_entries
+        self.saved: list[tuple[tuple, int, int]] = []
+
+    def save_seq(self, tok, n_past: int, nbytes: int) -> bool:
+        """save_seq (:771-780): a snapshot larger than the cap is not kept; an
+        equal token sequence is replaced; the oldest go first."""
+        if nbytes > self.cap:
+            return False
+        tok = tuple(tok)
+        for k, e in enumerate(self.saved):
+            if e[0] == tok:
+                del self.saved[k]
+                break
+        self.saved.append((tok, n_past, nbytes))
+        total = sum(e[2] for e in self.saved)
+        while len(self.saved) > self.max_entries or total > self.cap:
+            total -= self.saved[0][2]
+            del self.saved[0]
+        assert len(self.saved) <= self.max_entries and total <= self.cap
+        return True
+
+    def best_saved(self, tok, has_images: bool = False) -> int:
+        """best_saved (:782-793): the longest saved sequence the prompt strictly extends."""
+        if has_images:
+            return -1
+        tok = tuple(tok)
+        best = -1
+        for k, (t, _, _) in enumerate(self.saved):
+            if len(t) < len(tok) and tok[:len(t)] == t and (best < 0 or len(t) > len(self.saved[best][0])):
+                best = k
+        return best
+
+    def load(self, k: int):
+        """snapshot_load of entry k, then most recently used last (:1395)."""
+        e = self.saved[k]
+        self.saved = self.saved[:k] + self.saved[k + 1:] + [e]
+        return e
+
+    def restore_or_reset(self, consumed, consumed_bytes: int, consumed_has_images: bool, prompt,
+                         prompt_has_images: bool = False) -> int:
+        """restore_or_reset (:1380-1400): the restored token count, 0 after a reset."""
+        if len(consumed) >= 2048 and not consumed_has_images:
+            self.save_seq(consumed, len(consumed), consumed_bytes)
+        best = self.best_saved(prompt, prompt_has_images)
+        if best >= 0:
+            return len(self.load(best)[0])
+        return 0
+
+    def shared_prefix_split(self, prompt, n_consumed: int, has_images: bool = False) -> int:
+        """shared_prefix_split (:1406-1424)."""
+        if has_images or n_consumed >= 2048:
+            return 0
+        prompt = tuple(prompt)
+        L = 0
+        for t, _, _ in self.saved:
+            m = min(len(t), len(prompt))
+            l = 0
+            while l < m and t[l] == prompt[l]:
+                l += 1
+            L = max(L, l)
+        have = any(len(t) == L and prompt[:L] == t for t, _, _ in self.saved)
+        return L if (L >= 2048 and L + 16 < len(prompt) and L >= n_consumed + 2 and not have) else 0

@@ -19,6 +19,7 @@
 // kernel arguments, so a decode step sends nothing over the host link.
 #include "qwfn_common.h"
 #include "qwfn_state.h"
+#include "state_internal.h"
 
 #include <algorithm>
 #include <cmath>
@@ -165,20 +166,6 @@ unsigned grid_for(int64_t n) {
     return (unsigned) std::max<int64_t>(1, std::min<int64_t>((n + FILL_THREADS - 1) / FILL_THREADS, 4096));
 }
 
-// Makes a device current for the scope of a call and restores the previous one.
-struct device_scope {
-    int prev = -1;
-    int rc = QWFN_OK;
-    explicit device_scope(int dev) {
-        if (dev < 0) return;
-        hipError_t e = hipGetDevice(&prev);
-        if (e == hipSuccess && prev != dev) e = hipSetDevice(dev);
-        else if (e == hipSuccess) prev = -1;
-        if (e != hipSuccess) { rc = hip_check(e, "hipSetDevice"); prev = -1; }
-    }
-    ~device_scope() { if (prev >= 0) (void) hipSetDevice(prev); }
-};
-
 }  // namespace
 }  // namespace qwfn
 
@@ -186,51 +173,7 @@ using namespace qwfn;
 
 // ------------------------------------------------------------ state owner
 
-struct qwfn_state {
-    struct entry {
-        int32_t kind;
-        uint32_t il;
-        bool    host;      // in the pinned host arena
-        size_t  off;       // offset in its arena (recurrent tensors: in the device arena)
-        size_t  bytes;     // ggml_nbytes
-        int32_t type;
-        int64_t ne[4];
-        size_t  nb[4];
-    };
-    qwfn_state_config cfg{};
-    int device = QWFN_LAYOUT_ONLY;
-    std::vector<entry> entries;
-    std::vector<int> k, v, idx, rs, conv;   // entry index per layer, -1 if absent
-    int ple = -1;
-    size_t dev_bytes = 0, host_bytes = 0, rec_off = 0, rec_bytes = 0;
-    char * dev = nullptr;     // device arena
-    char * host = nullptr;    // pinned host arena (host address)
-    char * host_dev = nullptr;  // its device-side address
-    char * rb = nullptr;      // rollback slots
-    int32_t n_past = 0, rb_depth = 0;
-
-    ~qwfn_state() {
-        device_scope ds(device);
-        if (dev) (void) hipFree(dev);
-        if (rb) (void) hipFree(rb);
-        if (host) (void) hipHostFree(host);
-    }
-    bool is_attn(uint32_t il) const {
-        return cfg.full_attention_interval > 0 && ((il + 1) % cfg.full_attention_interval) == 0;
-    }
-    // device-visible address of an entry (its arena offset without memory)
-    char * addr(const entry & e, int32_t slot) const {
-        const size_t off = slot >= 0 ? (size_t) slot * rec_bytes + (e.off - rec_off) : e.off;
-        const char * base = slot >= 0 ? rb : e.host ? host_dev : dev;
-        return reinterpret_cast<char *>(reinterpret_cast<uintptr_t>(base) + off);
-    }
-    // row bytes of a positional cache (ggml_row_size(type, ne0 / n_ctx))
-    size_t row_bytes(const entry & e) const {
-        const int64_t per = e.ne[0] / (int64_t) cfg.n_ctx;
-        return (size_t) (per / type_blck(e.type)) * type_size(e.type);
-    }
-};
-
+namespace qwfn {
 namespace {
 
 int add_entry(qwfn_state & st, int32_t kind, uint32_t il, bool host, int32_t type, std::initializer_list<int64_t> ne,
@@ -319,10 +262,14 @@ void plan(qwfn_state & st) {
     st.host_bytes = align_up(hcur, ARENA_ALIGN);
 }
 
+}  // namespace
+
 int zero_recurrent(qwfn_state & st, hipStream_t stream) {
     if (!st.dev) return set_error(QWFN_EINVAL, "state: created with QWFN_LAYOUT_ONLY, it has no memory");
     return launch_zero(st.dev + st.rec_off, st.rec_bytes, stream);
 }
+
+namespace {
 
 void fill_desc(const qwfn_state & st, const qwfn_state::entry & e, int32_t slot, qwfn_tensor * out) {
     *out = qwfn_tensor{};
@@ -332,6 +279,8 @@ void fill_desc(const qwfn_state & st, const qwfn_state::entry & e, int32_t slot,
 }
 
 // snapshot_parts over one state (qwfn_engine.cpp:990-999)
+}  // namespace
+
 void parts_of(const qwfn_state & st, int32_t n, std::vector<qwfn_part> & out, std::vector<bool> * host_side) {
     auto push = [&](int ei, bool positional) {
         if (ei < 0) return;
@@ -381,7 +330,7 @@ int check_states(const qwfn_state * const * sts, int32_t n_sts, bool need_memory
     return QWFN_OK;
 }
 
-}  // namespace
+}  // namespace qwfn
 
 extern "C" {
 
@@ -525,7 +474,8 @@ int qwfn_state_reset(qwfn_state * st, void * stream) {
     if (!st) return set_error(QWFN_EINVAL, "state_reset: NULL state");
     device_scope ds(st->device);
     if (ds.rc) return ds.rc;
-    if (int rc = zero_recurrent(*st, as_stream(stream))) return rc;
+    if (st->dev)   // a QWFN_LAYOUT_ONLY state has only its bookkeeping
+        if (int rc = zero_recurrent(*st, as_stream(stream))) return rc;
     st->n_past = 0;
     st->rb_depth = 0;
     return QWFN_OK;

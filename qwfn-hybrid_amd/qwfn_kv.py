@@ -76,6 +76,9 @@ EXPORTS = [
     "qwfn_state_reset", "qwfn_state_rollback", "qwfn_snapshot_parts", "qwfn_snapshot_save", "qwfn_snapshot_load",
     "qwfn_causal_mask_f16", "qwfn_cell_mask_f16", "qwfn_qsa_bucket", "qwfn_qsa_decode_prepare",
     "qwfn_qsa_bias_rebuild", "qwfn_qsa_tables",
+    "qwfn_snap_pool_create", "qwfn_snap_pool_destroy", "qwfn_snap_pool_count", "qwfn_snap_pool_bytes",
+    "qwfn_snap_pool_entry", "qwfn_snap_pool_save", "qwfn_snap_pool_best", "qwfn_snap_pool_load",
+    "qwfn_snap_pool_split", "qwfn_snap_pool_restore_or_reset",
 ]
 
 _lib = None
@@ -137,8 +140,24 @@ def load(path: str = LIB_PATH):
     L.qwfn_qsa_decode_prepare.argtypes = [ctypes.POINTER(QsaInputs), vp, i32, vp]
     L.qwfn_qsa_bias_rebuild.argtypes = [vp, i64, i32, i32, vp]
     L.qwfn_qsa_tables.argtypes = [vp, i64, i32, vp, i64, vp, i64, vp]
+    PI = ctypes.POINTER(i32)
+    L.qwfn_snap_pool_create.argtypes = [sz, i32, ctypes.c_int, PV]
+    L.qwfn_snap_pool_destroy.argtypes = [vp]
+    L.qwfn_snap_pool_destroy.restype = None
+    L.qwfn_snap_pool_count.argtypes = [vp]
+    L.qwfn_snap_pool_count.restype = i32
+    L.qwfn_snap_pool_bytes.argtypes = [vp]
+    L.qwfn_snap_pool_bytes.restype = sz
+    L.qwfn_snap_pool_entry.argtypes = [vp, i32, PI, PI, ctypes.POINTER(sz), PI, i32]
+    L.qwfn_snap_pool_save.argtypes = [vp, PV, i32, PI, i32, vp]
+    L.qwfn_snap_pool_best.argtypes = [vp, PI, i32, i32]
+    L.qwfn_snap_pool_best.restype = i32
+    L.qwfn_snap_pool_load.argtypes = [vp, i32, PV, i32, vp]
+    L.qwfn_snap_pool_split.argtypes = [vp, PI, i32, i32, i32]
+    L.qwfn_snap_pool_split.restype = i32
+    L.qwfn_snap_pool_restore_or_reset.argtypes = [vp, PV, i32, PI, i32, i32, PI, i32, i32, PI, vp]
     for name in EXPORTS:
-        if name not in ("qwfn_state_config_default", "qwfn_state_destroy"):
+        if name not in ("qwfn_state_config_default", "qwfn_state_destroy", "qwfn_snap_pool_destroy"):
             getattr(L, name).restype = getattr(L, name).restype or ctypes.c_int
     L.qwfn_last_error.restype = ctypes.c_char_p
     L.qwfn_fattn_workspace_size.restype = sz

@@ -264,3 +264,78 @@ def qsa_tables(blk_cells, ratio: int, cell_pos=None, blk_pos_all=None, n_whole: 
                                      cell_pos.numel() if cell_pos is not None else 0,
                                      blk_pos_all.data_ptr() if blk_pos_all is not None else None, n_whole,
                                      K._stream(stream)))
+
+
+# ------------------------------------------------------- saved-sequence pool
+
+def _i32(seq):
+    seq = list(seq)
+    return (ctypes.c_int32 * max(1, len(seq)))(*seq), len(seq)
+
+
+class SnapPool:
+    """The server's saved sequences (tools/qwfn_server.cpp:767-793) in HBM."""
+
+    def __init__(self, cap_bytes: int, max_entries: int = 4, device: int = 0):
+        self._h = ctypes.c_void_p(None)
+        K.check(K.load().qwfn_snap_pool_create(cap_bytes, max_entries, device, ctypes.byref(self._h)))
+
+    def close(self):
+        if self._h:
+            K.load().qwfn_snap_pool_destroy(self._h)
+            self._h = ctypes.c_void_p(None)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def count(self) -> int:
+        return int(K.load().qwfn_snap_pool_count(self._h))
+
+    def bytes(self) -> int:
+        return int(K.load().qwfn_snap_pool_bytes(self._h))
+
+    def entry(self, k: int) -> tuple[list[int], int, int]:
+        """(tokens, n_past, bytes) of entry k, least recently used first."""
+        L = K.load()
+        n, npast, b = ctypes.c_int32(0), ctypes.c_int32(0), ctypes.c_size_t(0)
+        K.check(L.qwfn_snap_pool_entry(self._h, k, ctypes.byref(n), ctypes.byref(npast), ctypes.byref(b), None, 0))
+        tok = (ctypes.c_int32 * max(1, n.value))()
+        K.check(L.qwfn_snap_pool_entry(self._h, k, None, None, None, tok, n.value))
+        return list(tok[:n.value]), int(npast.value), int(b.value)
+
+    def save_seq(self, states, tok, stream=None) -> bool:
+        T, n = _i32(tok)
+        rc = K.load().qwfn_snap_pool_save(self._h, _handles(states), len(states), T, n, K._stream(stream))
+        if rc < 0:
+            K.check(rc)
+        return rc == 1
+
+    def best_saved(self, tok, has_images: bool = False) -> int:
+        T, n = _i32(tok)
+        return int(K.load().qwfn_snap_pool_best(self._h, T, n, int(has_images)))
+
+    def load(self, k: int, states, stream=None) -> tuple[bool, str]:
+        L = K.load()
+        rc = L.qwfn_snap_pool_load(self._h, k, _handles(states), len(states), K._stream(stream))
+        if rc != K.OK:
+            if rc != K.ESIZE:
+                K.check(rc)
+            return False, L.qwfn_last_error().decode(errors="replace")
+        return True, ""
+
+    def shared_prefix_split(self, prompt, n_consumed: int, has_images: bool = False) -> int:
+        T, n = _i32(prompt)
+        return int(K.load().qwfn_snap_pool_split(self._h, T, n, n_consumed, int(has_images)))
+
+    def restore_or_reset(self, states, consumed, prompt, consumed_has_images: bool = False,
+                         prompt_has_images: bool = False, stream=None) -> int:
+        C, nc = _i32(consumed)
+        P, n_p = _i32(prompt)
+        out = ctypes.c_int32(0)
+        K.check(K.load().qwfn_snap_pool_restore_or_reset(self._h, _handles(states), len(states), C, nc,
+                                                         int(consumed_has_images), P, n_p, int(prompt_has_images),
+                                                         ctypes.byref(out), K._stream(stream)))
+        return int(out.value)

@@ -328,3 +328,77 @@ def test_qsa_tables_match_oracle(gpu):
     np.testing.assert_array_equal(host(bc), w_bc)
     np.testing.assert_array_equal(host(cp), w_cp)
     np.testing.assert_array_equal(host(bp), w_bp)
+
+
+# ------------------------------------------------------- saved-sequence pool
+
+def _pool_pair(n_ctx=4096):
+    cfg = small_cfg(n_ctx=n_ctx, n_rollback=0)
+    head_cfg = small_cfg(n_ctx=n_ctx, n_layer=4, ple_n_head=0, n_rollback=0)
+    return [new_state(cfg), new_state(head_cfg)], [cfg, head_cfg]
+
+
+def _fill(states, cfgs, n_past, rng):
+    for s in states:
+        s.reset()
+        s.step_done(n_past)
+    return [scribble(s, c, rng) for s, c in zip(states, cfgs)]
+
+
+def _check(states, cfgs, data, n_past, what):
+    for s, c, sv in zip(states, cfgs, data):
+        assert s.n_past() == n_past
+        for key, t in all_tensors(s, c):
+            n = nbytes(t) if recurrent(key) else min(nbytes(t), n_past * (t.nb[1] // c.n_ctx))
+            np.testing.assert_array_equal(read(t.data, n), sv[key][:n], err_msg=f"{what} {key}")
+
+
+def test_pool_keeps_snapshots_across_compaction(gpu):
+    """Four saved sequences; replacing one by a longer snapshot leaves no gap
+    large enough, so the pool compacts into its other half. Every saved
+    sequence then restores byte for byte."""
+    rng = np.random.default_rng(21)
+    states, cfgs = _pool_pair()
+    size = lambda n: sum(b for _, b in S.snapshot_parts(states, n))
+    # 4 x size(1000) fit; after replacing one by size(1500) the free tail is too small
+    cap = 3 * size(1000) + size(1500) + 4096
+    pool = S.SnapPool(cap, 4, 0)
+    seqs = {name: [i] * 1000 for i, name in enumerate("abcd")}
+    saved = {}
+    for name, tok in seqs.items():
+        saved[name] = (_fill(states, cfgs, 1000, rng), 1000)
+        say(f"pool: save {name}")
+        assert pool.save_seq(states, tok)
+    b2 = [1] * 1000                                           # b's tokens, a longer state
+    saved["b"] = (_fill(states, cfgs, 1500, rng), 1500)
+    say("pool: replace b (compaction)")
+    assert pool.save_seq(states, b2)
+    assert [pool.entry(k)[0][0] for k in range(4)] == [0, 2, 3, 1]
+    scribble(states[0], cfgs[0], rng)
+    for k in range(4):
+        name = "abcd"[pool.entry(0)[0][0]]
+        say(f"pool: load {name}")
+        ok, err = pool.load(0, states)
+        assert ok, err
+        _check(states, cfgs, saved[name][0], saved[name][1], name)
+
+
+def test_pool_restore_or_reset_round_trip(gpu):
+    """The server's flow: a long conversation is set aside when a side request
+    arrives, and restored when the conversation continues."""
+    rng = np.random.default_rng(22)
+    states, cfgs = _pool_pair()
+    pool = S.SnapPool(64 << 20, 4, 0)
+    conv = [int(x) for x in rng.integers(0, 1000, 3000)]
+    data = _fill(states, cfgs, 3000, rng)
+    say("pool: set aside, reset for a side request")
+    assert pool.restore_or_reset(states, conv, [5, 6, 7]) == 0
+    assert states[0].n_past() == 0 and pool.count() == 1
+    for key, t in all_tensors(states[0], cfgs[0]):
+        if recurrent(key):
+            assert not read(t.data, nbytes(t)).any()
+    side = [int(x) for x in rng.integers(0, 1000, 100)]
+    _fill(states, cfgs, 100, rng)
+    say("pool: restore the conversation")
+    assert pool.restore_or_reset(states, side, conv + [1, 2]) == 3000
+    _check(states, cfgs, data, 3000, "restored")

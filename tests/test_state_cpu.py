@@ -205,8 +205,8 @@ def test_library_bookkeeping_and_rollback_guard():
         st.step_done(64 - 13 + 1)
     st.step_done(64 - 13)
     assert st.n_past() == 64
-    with pytest.raises(K.QwfnError, match="QWFN_LAYOUT_ONLY"):
-        st.reset(stream=0)
+    st.reset(stream=0)                           # bookkeeping only without memory
+    assert st.n_past() == 0 and st.rollback_depth() == 0
 
 
 def test_library_config_validation():
@@ -254,3 +254,135 @@ def test_step_input_validation():
     err(L.qwfn_snapshot_load(H, 1, 0, None, None, 0, 0, None), K.EINVAL, "no memory")
     n = ctypes.c_int32(0)
     err(L.qwfn_snapshot_parts(H, 1, -1, None, 0, ctypes.byref(n)), K.EINVAL, "position")
+
+
+# ------------------------------------------------------- saved-sequence pool
+
+def _toks(n, seed=0, prefix=()):
+    rng = np.random.default_rng(seed)
+    return list(prefix) + [int(x) for x in rng.integers(0, 248000, n - len(prefix))]
+
+
+def test_oracle_pool_scripted():
+    P = SO.SnapPool(cap=100, max_entries=4)
+    for i in range(5):
+        assert P.save_seq([i] * 3, 3, 10)
+    assert [e[0] for e in P.saved] == [(1,) * 3, (2,) * 3, (3,) * 3, (4,) * 3]   # at most four, oldest gone
+    assert not P.save_seq([9], 1, 101) and len(P.saved) == 4                      # larger than the cap: not kept
+    assert P.save_seq([2] * 3, 3, 10) and P.saved[-1][0] == (2,) * 3 and len(P.saved) == 4   # replaced, now newest
+    assert P.save_seq([7], 1, 75)                                                 # the byte cap evicts the oldest
+    assert [e[0] for e in P.saved] == [(4,) * 3, (2,) * 3, (7,)] and sum(e[2] for e in P.saved) <= 100
+    # best_saved: the longest sequence the prompt strictly extends
+    Q = SO.SnapPool(cap=10 ** 9)
+    Q.save_seq([1, 2], 2, 1)
+    Q.save_seq([1, 2, 3], 3, 1)
+    Q.save_seq([1, 2, 3, 4], 4, 1)
+    assert Q.best_saved([1, 2, 3, 4, 5]) == 2 and Q.best_saved([1, 2, 3, 4]) == 1   # equal length is not an extension
+    assert Q.best_saved([1, 2, 3, 9, 9]) == 1 and Q.best_saved([2, 2, 3]) == -1
+    assert Q.best_saved([1, 2, 3, 4, 5], has_images=True) == -1
+    Q.load(0)
+    assert Q.saved[-1][0] == (1, 2)                                               # most recently used last
+
+
+def test_oracle_pool_restore_and_split():
+    P = SO.SnapPool(cap=10 ** 9)
+    a = _toks(3000, 1)
+    assert P.restore_or_reset(a, 10, False, _toks(10, 2)) == 0 and len(P.saved) == 1   # set aside, reset
+    assert P.restore_or_reset(_toks(2047, 3), 10, False, a + [5]) == 3000    # short one not saved; a restored
+    assert len(P.saved) == 1
+    assert P.restore_or_reset(_toks(2500, 4), 10, True, a + [5]) == 3000     # images: not set aside
+    assert len(P.saved) == 1
+    # the split: a shared prefix of >= 2048 tokens past what the engine holds, the prompt going on
+    sys_prompt = _toks(2500, 5)
+    P2 = SO.SnapPool(cap=10 ** 9)
+    P2.save_seq(sys_prompt + _toks(600, 6), 3100, 1)
+    prompt = sys_prompt + _toks(400, 7)
+    assert P2.shared_prefix_split(prompt, 0) == 2500
+    assert P2.shared_prefix_split(prompt, 2499) == 0                    # not 2 past what the engine holds
+    assert P2.shared_prefix_split(prompt, 2048) == 0                    # the engine holds >= 2048: no split
+    assert P2.shared_prefix_split(prompt[:2510], 0) == 0                # fewer than 16 tokens after it
+    assert P2.shared_prefix_split(prompt, 0, has_images=True) == 0
+    P2.save_seq(sys_prompt, 2500, 1)
+    assert P2.shared_prefix_split(prompt, 0) == 0                       # already saved at that point
+    assert P2.shared_prefix_split(_toks(3000, 8), 0) == 0               # nothing shared
+
+
+def _pool_states(n_ctx=4096):
+    return [layout_state(n_ctx, **small_cfg(n_rollback=0)),
+            layout_state(n_ctx, **small_cfg(n_layer=4, ple_n_head=0, n_rollback=0))]
+
+
+def _set_past(states, n):
+    for s in states:
+        if s.n_past() > n:
+            s.reset(stream=0)
+        s.step_done(n - s.n_past()) if n > s.n_past() else None
+
+
+def test_library_pool_matches_oracle_dry():
+    states = _pool_states()
+    size = lambda n: sum(b for _, b in S.snapshot_parts(states, n))
+    rng = np.random.default_rng(11)
+    for cap_n, max_e in ((4096 * 3, 4), (2500, 2), (10 ** 6, 3)):
+        cap = size(cap_n) if cap_n < 10 ** 6 else 1 << 40
+        pool = S.SnapPool(cap, max_e, S.LAYOUT_ONLY)
+        ref = SO.SnapPool(cap, max_e)
+        seqs = [_toks(int(n), int(i)) for i, n in enumerate(rng.integers(1, 4000, 8))]
+        seqs += [seqs[0][:2100] + _toks(50, 99), seqs[1] + [7, 7]]
+        for step in range(60):
+            op = rng.integers(0, 4)
+            t = seqs[int(rng.integers(0, len(seqs)))]
+            if op == 0:
+                _set_past(states, len(t))
+                assert pool.save_seq(states, t, stream=0) == ref.save_seq(t, len(t), size(len(t)))
+            elif op == 1:
+                assert pool.best_saved(t) == ref.best_saved(t)
+                nc = int(rng.integers(0, 3000))
+                assert pool.shared_prefix_split(t, nc) == ref.shared_prefix_split(t, nc)
+            elif op == 2 and ref.saved:
+                k = int(rng.integers(0, len(ref.saved)))
+                ok, err = pool.load(k, states, stream=0)
+                assert ok, err
+                e = ref.load(k)
+                assert states[0].n_past() == e[1] and states[1].n_past() == e[1]
+            else:
+                _set_past(states, len(t))
+                prompt = seqs[int(rng.integers(0, len(seqs)))]
+                prompt = prompt + [1, 2, 3] if rng.integers(0, 2) else prompt
+                got = pool.restore_or_reset(states, t, prompt, stream=0)
+                want = ref.restore_or_reset(t, size(len(t)), False, prompt)
+                assert got == want and states[0].n_past() == want
+            assert pool.count() == len(ref.saved)
+            assert [pool.entry(k)[0] for k in range(pool.count())] == [list(e[0]) for e in ref.saved]
+            assert pool.bytes() == sum(e[2] for e in ref.saved)
+
+
+def test_library_pool_split_matches_oracle():
+    pool = S.SnapPool(1 << 40, 4, S.LAYOUT_ONLY)
+    ref = SO.SnapPool(1 << 40, 4)
+    states = _pool_states()
+    sys_prompt = _toks(2500, 5)
+    for t in (sys_prompt + _toks(600, 6), _toks(3000, 8)):
+        _set_past(states, len(t))
+        assert pool.save_seq(states, t, stream=0) and ref.save_seq(t, len(t), 1)
+    prompt = sys_prompt + _toks(400, 7)
+    for n_consumed in (0, 100, 2497, 2498, 2499, 2048, 3000):
+        for p in (prompt, prompt[:2516], prompt[:2517], _toks(3000, 8) + [1] * 20):
+            for img in (False, True):
+                assert pool.shared_prefix_split(p, n_consumed, img) == ref.shared_prefix_split(p, n_consumed, img)
+
+
+def test_library_pool_validation():
+    L = K.load()
+    h = ctypes.c_void_p(None)
+    assert L.qwfn_snap_pool_create(1 << 20, 0, S.LAYOUT_ONLY, ctypes.byref(h)) == K.EINVAL
+    assert L.qwfn_snap_pool_create(1 << 20, 65, S.LAYOUT_ONLY, ctypes.byref(h)) == K.EINVAL
+    pool = S.SnapPool(1 << 20, 4, S.LAYOUT_ONLY)
+    with pytest.raises(K.QwfnError, match="no such entry"):
+        pool.entry(0)
+    states = _pool_states()
+    states[0].step_done(10)
+    with pytest.raises(K.QwfnError, match="disagree"):
+        pool.save_seq(states, [1] * 10, stream=0)
+    with pytest.raises(K.QwfnError, match="positions"):
+        pool.restore_or_reset(states[:1], [1] * 9, [1] * 20, stream=0)
