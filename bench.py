@@ -153,10 +153,18 @@ def measure_state_rows(K, torch, np, dev, gbs) -> dict:
     convs = [[7] * 8192, [9] * 8192]
     pool.save_seq([st], convs[1])
 
+    held = [0]                                     # the conversation the state holds
+    ctoks = [(ctypes.c_int32 * 8192)(*c) for c in convs]
+    ptoks = [(ctypes.c_int32 * 8193)(*(c + [1])) for c in convs]
+    n_out = ctypes.c_int32(0)
+
     def switch(k):
-        n = pool.restore_or_reset([st], convs[k & 1], convs[(k + 1) & 1] + [1])
-        if n != 8192:
+        cur = held[0]
+        K.check(L.qwfn_snap_pool_restore_or_reset(pool._h, H, 1, ctoks[cur], 8192, 0, ptoks[1 - cur], 8193, 0,
+                                                  ctypes.byref(n_out), stream()))
+        if n_out.value != 8192:
             raise RuntimeError("pool: the conversation was not restored")
+        held[0] = 1 - cur
     us = timed(torch, switch, 10)
     moved = 4 * snap_b + rec                       # save (read + write), reset, load (read + write)
     rows["pool_switch_conversation"] = {"us_per_op": round(us, 1), "positions": 8192, "GBs": gbs(moved, us),
