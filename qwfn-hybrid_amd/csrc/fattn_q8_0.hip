@@ -172,19 +172,21 @@ __device__ __forceinline__ void cvt_v_block(const uint32_t v[4], uint32_t a0[2],
 }
 
 // B operands of one V block: for key pairs q (keys 2q, 2q+1), P*d_v as an f16
-// hi pair, bh[q] = f16(p*d_v) (RNE), and a lo pair, bl[q] = f16(p*d_v - hi),
-// each from one fused v_fma_mix (the product is exact before its rounding).
-// dv[q] holds the two keys' fp16 d_v.
-__device__ __forceinline__ void pdv_hilo(const float p[4], const uint32_t dv[2], uint32_t bh[2], uint32_t bl[2]) {
-#define QWFN_HILO(H, L, P0, P1, DV)                                                                   \
-    "v_fma_mixlo_f16 " H ", " P0 ", " DV ", 0 op_sel:[0,0,0] op_sel_hi:[0,1,0]\n\t"                     \
-    "v_fma_mixhi_f16 " H ", " P1 ", " DV ", 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"                     \
+// hi pair and an f16 lo pair. hi = f16(P16 * d_v) with P16 = P rounded toward
+// zero to f16 (one packed multiply per pair; p16[q] is computed once per
+// chunk); lo = f16(p*d_v - hi), each from one fused v_fma_mix on the f32 p, so
+// hi + lo carries p*d_v to about 2^-21 whatever the rounding of hi. dv[q] holds
+// the two keys' fp16 d_v.
+__device__ __forceinline__ void pdv_hilo(const float p[4], const uint32_t p16[2], const uint32_t dv[2], uint32_t bh[2],
+                                         uint32_t bl[2]) {
+#define QWFN_HILO(H, L, P0, P1, P16, DV)                                                              \
+    "v_pk_mul_f16 " H ", " P16 ", " DV "\n\t"                                                           \
     "v_fma_mixlo_f16 " L ", " P0 ", " DV ", -" H " op_sel:[0,0,0] op_sel_hi:[0,1,1]\n\t"                \
     "v_fma_mixhi_f16 " L ", " P1 ", " DV ", -" H " op_sel:[0,1,1] op_sel_hi:[0,1,1]\n\t"
-    asm(QWFN_HILO("%0", "%2", "%4", "%5", "%8") QWFN_HILO("%1", "%3", "%6", "%7", "%9")
+    asm(QWFN_HILO("%0", "%2", "%4", "%5", "%8", "%10") QWFN_HILO("%1", "%3", "%6", "%7", "%9", "%11")
                  "s_nop 1"
                  : "=&v"(bh[0]), "=&v"(bh[1]), "=&v"(bl[0]), "=&v"(bl[1])
-                 : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]), "v"(dv[0]), "v"(dv[1]));
+                 : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]), "v"(p16[0]), "v"(p16[1]), "v"(dv[0]), "v"(dv[1]));
 #undef QWFN_HILO
 }
 
@@ -211,6 +213,14 @@ __device__ __forceinline__ float fma_f16hi(uint32_t h, float c, float x) {
     return r;
 }
 __device__ __forceinline__ float xmax(float a, float b) { return a > b ? a : b; }
+// max of two scores (finite or -inf, never NaN) in one v_max_f32: fmaxf on an
+// asm result gets both operands canonicalised first, and the ternary above is
+// a compare plus a select
+__device__ __forceinline__ float vmax(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
 
 // Reductions over the 4 lanes l, l^16, l^32, l^48 (the four lane groups
 // holding one MFMA column), with gfx950's cross-row swaps instead of LDS
@@ -232,7 +242,7 @@ __device__ __forceinline__ float reduce_lanes16_32(float x, Op op) {
     return op(__builtin_bit_cast(float, c), __builtin_bit_cast(float, d));
 }
 __device__ __forceinline__ float xmax_lanes16_32(float x) {
-    return reduce_lanes16_32(x, [](float a, float b) { return xmax(a, b); });
+    return reduce_lanes16_32(x, [](float a, float b) { return vmax(a, b); });
 }
 __device__ __forceinline__ float sum_lanes16_32(float x) {
     return reduce_lanes16_32(x, [](float a, float b) { return a + b; });
@@ -698,6 +708,7 @@ __global__ __launch_bounds__(NW * 64, NW / 4 > 2 ? NW / 4 : 2) void k_fattn_q8_0
         // ---- mask, online softmax (base 2; scores are already in log2 units).
         //      A masked key has x = -inf, so its p is exp2(-inf) = 0 ----
         float p[NKT][4];
+        uint32_t p16[NKT][2];   // p rounded toward zero to f16, key pairs (0,1), (2,3)
         {
             const bool tail = (c + 1) * CK > span;                // keys past the split in this chunk
             float x[NKT][4];
@@ -712,12 +723,19 @@ __global__ __launch_bounds__(NW * 64, NW / 4 > 2 ? NW / 4 : 2) void k_fattn_q8_0
 #pragma unroll
             for (int kt = 0; kt < NKT; kt++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    float xi = a.mask_mode != MASK_NONE ? fma_f16lo(mv[kt][i], LOG2E, s[kt][i]) : s[kt][i];
-                    if (tail && kin + 16 * kt + i >= span) xi = -INFINITY;
-                    x[kt][i] = xi;
-                    mloc = xmax(mloc, xi);
-                }
+                for (int i = 0; i < 4; i++)
+                    x[kt][i] = a.mask_mode != MASK_NONE ? fma_f16lo(mv[kt][i], LOG2E, s[kt][i]) : s[kt][i];
+            if (tail) {   // uniform: only the last chunk of a split has keys past its end
+#pragma unroll
+                for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        if (kin + 16 * kt + i >= span) x[kt][i] = -INFINITY;
+            }
+#pragma unroll
+            for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) mloc = vmax(mloc, x[kt][i]);
             mloc = xmax_lanes16_32(mloc);
             // the running max moves only when the chunk's max exceeds it by more
             // than RESCALE_SLACK (or it is still -inf), so p <= 2^RESCALE_SLACK
@@ -737,6 +755,11 @@ __global__ __launch_bounds__(NW * 64, NW / 4 > 2 ? NW / 4 : 2) void k_fattn_q8_0
                     lsum += p[kt][i];
                 }
             l_run = l_run * alpha + lsum;
+#pragma unroll
+            for (int kt = 0; kt < NKT; kt++) {
+                p16[kt][0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p[kt][0], p[kt][1]));
+                p16[kt][1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p[kt][2], p[kt][3]));
+            }
             if (__any(grow)) {
 #pragma unroll
                 for (int bb = 0; bb < NBLK; bb++) { O[bb][0] *= alpha; O[bb][1] *= alpha; }
@@ -775,7 +798,7 @@ __global__ __launch_bounds__(NW * 64, NW / 4 > 2 ? NW / 4 : 2) void k_fattn_q8_0
                     if (kt < NL) {
                         const uint32_t dv[2] = {dv2[u][kt].x, dv2[u][kt].y};
                         cvt_v_block(w[u][kt], a0[kt], a1[kt]);
-                        pdv_hilo(p[kt], dv, bh[kt], bl[kt]);
+                        pdv_hilo(p[kt], p16[kt], dv, bh[kt], bl[kt]);
                     } else {
                         // a key tile wholly past the split: zero operands
                         a0[kt][0] = a0[kt][1] = a1[kt][0] = a1[kt][1] = 0u;
