@@ -49,6 +49,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--separate-append", action="store_true",
+                    help="append K/V with its own launch before the attention launch (default: fused into it)")
     ap.add_argument("--long-depth", type=int, default=65536,
                     help="also time the attention op alone at this depth (0: skip)")
     ap.add_argument("--no-rows", action="store_true",
@@ -400,8 +402,12 @@ def main() -> int:
     def step(s):
         for l in range(L):
             kc, vc = caches[s][l]
-            K.set_rows_q8_0_kv(kc, newk[l], vc, newv[l], idx)   # the layer's K and V set_rows, one launch
-            attn(s, l)
+            if args.separate_append:
+                K.set_rows_q8_0_kv(kc, newk[l], vc, newv[l], idx)   # the layer's K and V set_rows, one launch
+                attn(s, l)
+            else:                                                  # append + attention in one launch
+                kv, vv = views[s][l]
+                K.flash_attn_ext_append(qv[l], kv, vv, mv, scale, ov[l], newk[l], newv[l], n_kv - T, ws=ws)
 
     # algorithmic bytes: every cached K/V row read once, the appended rows
     # (F32 in, q8_0 out), Q and output, and the F16 mask.
@@ -420,8 +426,12 @@ def main() -> int:
     try:
         import kvdata as KD
         kc, vc = caches[0][0]
-        K.set_rows_q8_0_kv(kc, newk[0], vc, newv[0], idx)
-        attn(0, 0)
+        if args.separate_append:
+            K.set_rows_q8_0_kv(kc, newk[0], vc, newv[0], idx)
+            attn(0, 0)
+        else:
+            kv0, vv0 = views[0][0]
+            K.flash_attn_ext_append(qv[0], kv0, vv0, mv, scale, ov[0], newk[0], newv[0], n_kv - T, ws=ws)
         torch.cuda.synchronize()
         got = out[0].cpu().numpy()[0]
         ref = KD.oracle_attn(q[0].cpu().numpy()[0], kc.cpu().numpy(), vc.cpu().numpy(), n_kv, nh_kv, mask_np,
@@ -588,7 +598,8 @@ def main() -> int:
         "data": "synthetic (seeded N(0,1) K/V with 4 x8 outlier channels per KV head, N(0,1) Q)",
         "config": {"workload": f"MTP verify decode: {L} layers, depth {depth}, T={T} (1+{T - 1} drafts, causal), "
                                f"n_head {nh}, n_head_kv {nh_kv}, head 256, q8_0 KV, append {T} rows/layer",
-                   "layers": L, "depth": depth, "T": T, "cache_sets": args.sets},
+                   "layers": L, "depth": depth, "T": T, "cache_sets": args.sets,
+                   "append": "own launch" if args.separate_append else "fused into the attention launch"},
         "us_per_layer": round(best_ms * 1e3 / L, 3),
         "us_per_layer_eager": round(eager_ms * 1e3 / L, 3),
         "us_per_layer_graph": round(graph_ms * 1e3 / L, 3) if graph_ms is not None else None,

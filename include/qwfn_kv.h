@@ -153,6 +153,24 @@ int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor * k, const
                              const qwfn_tensor * mask, float scale, float max_bias, float logit_softcap,
                              const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes, void * stream);
 
+/* The layer's K and V append followed by its attention, in one launch: the
+ * two ggml_cpy / ggml_set_rows nodes that write the step's rows
+ * (qwfn_graph.cpp:376-383, :623-624, :916-921) and the ggml_flash_attn_ext
+ * that reads them (:469-471, :697-701), adjacent in the graph. src_k and src_v
+ * are F32 [256 * n_head_kv, n] (n <= 64, 16-byte aligned rows); they are
+ * quantised with `variant` into rows first_row .. first_row + n - 1 of the
+ * caches that k and v view (heads as consecutive 272-byte segments of a row,
+ * as in the reference's cache), which must lie inside the attended keys; then
+ * the attention runs as qwfn_flash_attn_ext_q8_0. The cache bytes and dst are
+ * identical to qwfn_cpy_f32_q8_0_kv followed by qwfn_flash_attn_ext_q8_0.
+ * One sequence (B = 1). The blocks whose keys hold the new rows write them
+ * before reading, so no separate append launch is needed. */
+int qwfn_flash_attn_ext_q8_0_append(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
+                                    const qwfn_tensor * mask, float scale, float max_bias, float logit_softcap,
+                                    const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes,
+                                    const qwfn_tensor * src_k, const qwfn_tensor * src_v, int64_t first_row,
+                                    void * stream);
+
 /* ------------------------------------------------------ snapshot restore */
 
 enum qwfn_copy_src { QWFN_SRC_DEVICE = 0, QWFN_SRC_HOST = 1 };

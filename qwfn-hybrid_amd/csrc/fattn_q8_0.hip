@@ -136,6 +136,13 @@ struct fa_args {
     int32_t  m_gran;       // MASK_SPLIT: 16-byte granules per mask row of a split (split_len / 8 + 1)
     uint32_t m_gran_mul;   // ceil(2^32 / m_gran)
     uint32_t ns_mul, hgn_mul, nrg_mul;   // ceil(2^32 / d) for ns, nh_kv * n_rg, n_rg
+    // fused append (app_n > 0): F32 rows [nh_kv * D] of K and V quantised into
+    // cache rows app_row0 .. app_row0 + app_n - 1 before they are attended
+    const char * app_k;
+    const char * app_v;
+    size_t   app_nb1;
+    int64_t  app_row0;
+    int32_t  app_n;
 };
 
 // x / d through m = ceil(2^32 / d): floor(x * m / 2^32) = floor(x / d) while
@@ -514,6 +521,41 @@ __global__ __launch_bounds__(NW * 64, NW / 4 > 2 ? NW / 4 : 2) void k_fattn_q8_0
             }
         }
     };
+
+    // Fused append: a block whose keys include appended rows quantises its KV
+    // head's part of them into the cache (the arithmetic of k_append_q8_0, 8
+    // lanes per q8_0 block) and waits for the stores before any of its chunk
+    // DMAs, which then read the new rows from memory. Blocks of other row
+    // groups write the same bytes; each reads only after its own stores.
+    if (a.app_n > 0) {
+        const int64_t alo = std::max<int64_t>(a.app_row0, k_lo), ahi = std::min<int64_t>(a.app_row0 + a.app_n, k_hi);
+        if (alo < ahi) {
+            const int units = (int) (ahi - alo) * NBLK * 2;   // rows x blocks x {K, V}
+            const int sub = threadIdx.x & 7;
+            for (int u0 = 0; u0 < units; u0 += WAVES * 8) {
+                const int u = u0 + (int) (threadIdx.x >> 3);
+                const bool live = u < units;                  // whole 8-lane groups: DPP partners exist
+                const int uu = live ? u : 0;
+                const int tensor = uu & 1, jb = (uu >> 1) % NBLK;
+                const int64_t row = alo + (uu >> 1) / NBLK;
+                const float4 xv = *(const float4 *) ((tensor ? a.app_v : a.app_k) + (size_t) (row - a.app_row0) * a.app_nb1 +
+                                                     (size_t) (kvh * D + QK * jb + 4 * sub) * 4);
+                float x[4] = {xv.x, xv.y, xv.z, xv.w};
+                uint16_t d16;
+                float dqa;
+                const uint32_t q4 = dev::q8_quantize_lane4(x, a.x86 != 0, &d16, &dqa);
+                if (live) {
+                    char * bp = (char *) (tensor ? vbase + (size_t) row * a.v_nb1 : kbase + (size_t) row * a.k_nb1) + jb * QBLOCK;
+                    uint16_t * qp = (uint16_t *) (bp + 2 + sub * 4);
+                    qp[0] = (uint16_t) (q4 & 0xffffu);
+                    qp[1] = (uint16_t) (q4 >> 16);
+                    if (sub == 0) *(uint16_t *) bp = d16;
+                }
+            }
+            wait_vmcnt<0>();      // this wave's stores (and its query DMAs) are done
+            __syncthreads();      // ... and every wave's
+        }
+    }
 
     issue_chunk(0, ring[0]);
     int chunk_ops = ops_per_chunk;
@@ -1235,16 +1277,47 @@ extern "C" size_t qwfn_fattn_workspace_size(const qwfn_tensor * q, const qwfn_te
     return pl.ws_bytes;
 }
 
-extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
-                                        const qwfn_tensor * mask, float scale, float max_bias, float logit_softcap,
-                                        const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes,
-                                        void * stream) {
+namespace {
+
+struct fa_append {
+    const qwfn_tensor * src_k;
+    const qwfn_tensor * src_v;
+    int64_t first_row;
+};
+
+int check_append(const fa_append & ap, const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v) {
+    const qwfn_tensor * srcs[2] = {ap.src_k, ap.src_v};
+    for (const qwfn_tensor * s : srcs) {
+        if (!s || !s->data) return set_error(QWFN_EINVAL, "flash_attn_ext_append: src is NULL");
+        if (s->type != QWFN_TYPE_F32 || s->nb[0] != 4) return set_error(QWFN_EINVAL, "flash_attn_ext_append: src must be contiguous f32 rows");
+        if (s->ne[2] != 1 || s->ne[3] != 1) return set_error(QWFN_ENOTSUP, "flash_attn_ext_append: src must be 2-D");
+        if (s->ne[0] != (int64_t) D * k->ne[2]) return set_error(QWFN_EINVAL, "flash_attn_ext_append: src rows must hold every KV head (256 * n_head_kv values)");
+        if (!is_aligned(s->data, 16) || s->nb[1] % 16) return set_error(QWFN_EALIGN, "flash_attn_ext_append: src rows must be 16-byte aligned");
+    }
+    if (ap.src_k->ne[1] != ap.src_v->ne[1] || ap.src_k->nb[1] != ap.src_v->nb[1])
+        return set_error(QWFN_EINVAL, "flash_attn_ext_append: src_k and src_v must have the same shape");
+    const int64_t n = ap.src_k->ne[1];
+    if (n < 1 || n > 64) return set_error(QWFN_ENOTSUP, "flash_attn_ext_append: 1 to 64 appended rows");
+    if (ap.first_row < 0 || ap.first_row + n > k->ne[1])
+        return set_error(QWFN_ERANGE, "flash_attn_ext_append: the appended rows must lie inside the attended keys");
+    if (q->ne[3] != 1 || k->ne[3] != 1 || v->ne[3] != 1) return set_error(QWFN_ENOTSUP, "flash_attn_ext_append: one sequence (B = 1)");
+    const size_t seg = (size_t) D / QK * QBLOCK;
+    if (k->nb[2] != seg || v->nb[2] != seg)
+        return set_error(QWFN_EINVAL, "flash_attn_ext_append: K/V heads must be consecutive 272-byte segments of a cache row");
+    return QWFN_OK;
+}
+
+int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v, const qwfn_tensor * mask, float scale,
+              float max_bias, float logit_softcap, const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes,
+              void * stream, const fa_append * app) {
     if (max_bias != 0.0f) return set_error(QWFN_ENOTSUP, "flash_attn_ext: max_bias (ALiBi) is not supported");
     if (logit_softcap != 0.0f) return set_error(QWFN_ENOTSUP, "flash_attn_ext: logit_softcap is not supported");
     if (!(std::isfinite(scale))) return set_error(QWFN_EINVAL, "flash_attn_ext: scale must be finite");
     if (variant != QWFN_Q8_REF && variant != QWFN_Q8_X86) return set_error(QWFN_EINVAL, "flash_attn_ext: unknown variant");
     fa_plan pl{};
     if (int rc = plan_fattn(q, k, v, mask, &pl)) return rc;
+    if (app)
+        if (int rc = check_append(*app, q, k, v)) return rc;
     if (!dst || !dst->data || dst->type != QWFN_TYPE_F32) return set_error(QWFN_EINVAL, "flash_attn_ext: dst must be f32");
     if (dst->ne[0] != D || dst->ne[1] != q->ne[2] || dst->ne[2] != q->ne[1] || dst->ne[3] != q->ne[3])
         return set_error(QWFN_EINVAL, "flash_attn_ext: dst must be [256, n_head, T, B]");
@@ -1303,6 +1376,13 @@ extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor
     a.dst_vec = is_aligned(dst->data, 16) ? 1 : 0;
     a.q_slice = (uint32_t) q_slice_bytes(*q);
     a.gqa_mul = recip32(pl.gqa);
+    if (app) {
+        a.app_k = (const char *) app->src_k->data;
+        a.app_v = (const char *) app->src_v->data;
+        a.app_nb1 = app->src_k->nb[1];
+        a.app_row0 = app->first_row;
+        a.app_n = (int32_t) app->src_k->ne[1];
+    }
 
     const int64_t units = (int64_t) a.B * a.ns >= 8 ? ((int64_t) a.B * a.ns + 7) / 8 * 8 : (int64_t) a.B * a.ns;
     const int64_t hgn = (int64_t) a.nh_kv * a.n_rg;
@@ -1346,4 +1426,22 @@ extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor
         if (int rc = hip_check(hipGetLastError(), "flash_attn merge launch")) return rc;
     }
     return QWFN_OK;
+}
+
+}  // namespace
+
+extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
+                                        const qwfn_tensor * mask, float scale, float max_bias, float logit_softcap,
+                                        const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes,
+                                        void * stream) {
+    return fattn_run(q, k, v, mask, scale, max_bias, logit_softcap, dst, variant, ws, ws_bytes, stream, nullptr);
+}
+
+extern "C" int qwfn_flash_attn_ext_q8_0_append(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
+                                               const qwfn_tensor * mask, float scale, float max_bias, float logit_softcap,
+                                               const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes,
+                                               const qwfn_tensor * src_k, const qwfn_tensor * src_v, int64_t first_row,
+                                               void * stream) {
+    const fa_append app{src_k, src_v, first_row};
+    return fattn_run(q, k, v, mask, scale, max_bias, logit_softcap, dst, variant, ws, ws_bytes, stream, &app);
 }

@@ -68,7 +68,7 @@ class QsaInputs(ctypes.Structure):
 EXPORTS = [
     "qwfn_abi_version", "qwfn_last_error", "qwfn_init", "qwfn_device_status",
     "qwfn_set_rows_q8_0", "qwfn_cpy_f32_q8_0", "qwfn_set_rows_q8_0_kv", "qwfn_cpy_f32_q8_0_kv", "qwfn_get_rows_i32", "qwfn_kv_gather_segments",
-    "qwfn_fattn_workspace_size", "qwfn_flash_attn_ext_q8_0", "qwfn_state_restore",
+    "qwfn_fattn_workspace_size", "qwfn_flash_attn_ext_q8_0", "qwfn_flash_attn_ext_q8_0_append", "qwfn_state_restore",
     # include/qwfn_state.h
     "qwfn_state_config_default", "qwfn_state_create", "qwfn_state_destroy", "qwfn_state_tensor",
     "qwfn_state_bytes", "qwfn_state_host_bytes", "qwfn_state_rollback_bytes", "qwfn_state_n_ctx",
@@ -108,6 +108,8 @@ def load(path: str = LIB_PATH):
     L.qwfn_fattn_workspace_size.restype = sz
     L.qwfn_flash_attn_ext_q8_0.argtypes = [T, T, T, T, ctypes.c_float, ctypes.c_float, ctypes.c_float, T,
                                            ctypes.c_int, vp, sz, vp]
+    L.qwfn_flash_attn_ext_q8_0_append.argtypes = [T, T, T, T, ctypes.c_float, ctypes.c_float, ctypes.c_float, T,
+                                                  ctypes.c_int, vp, sz, T, T, i64, vp]
     L.qwfn_state_restore.argtypes = [ctypes.POINTER(vp), ctypes.POINTER(sz), ctypes.POINTER(vp), i32, i32, i32, vp]
     # include/qwfn_state.h
     u32, PV, PS = ctypes.c_uint32, ctypes.POINTER(vp), ctypes.POINTER(sz)
@@ -316,6 +318,19 @@ def flash_attn_ext(qv: Tensor, kv: Tensor, vv: Tensor, mv: Tensor | None, scale:
     return check(L.qwfn_flash_attn_ext_q8_0(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv),
                                             ctypes.byref(mv) if mv is not None else None, scale, max_bias, softcap,
                                             ctypes.byref(ov), variant, ws_ptr, ws_bytes, _stream(stream)))
+
+
+def flash_attn_ext_append(qv: Tensor, kv: Tensor, vv: Tensor, mv: Tensor | None, scale: float, ov: Tensor,
+                          ksrc, vsrc, first_row: int, variant: int = Q8_X86, ws=None, stream=None):
+    """K/V append (ksrc, vsrc: torch f32 [n, 256 * n_head_kv]) at first_row, then attention, one launch."""
+    L = load()
+    ws_ptr = ws.data_ptr() if ws is not None else None
+    ws_bytes = ws.numel() * ws.element_size() if ws is not None else 0
+    sk, sv = f32_view(ksrc), f32_view(vsrc)
+    return check(L.qwfn_flash_attn_ext_q8_0_append(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv),
+                                                   ctypes.byref(mv) if mv is not None else None, scale, 0.0, 0.0,
+                                                   ctypes.byref(ov), variant, ws_ptr, ws_bytes, ctypes.byref(sk),
+                                                   ctypes.byref(sv), first_row, _stream(stream)))
 
 
 def fattn_workspace_size(qv: Tensor, kv: Tensor, vv: Tensor, mv: Tensor | None = None) -> int:

@@ -140,3 +140,20 @@ def test_restore_validation():
     _err(L.qwfn_state_restore(S, B, D, 2, 1, 0, None), K.EINVAL, "source part 1")
     _err(L.qwfn_state_restore(S, B, D, 2, 0, 0, None), K.EINVAL, "n_slots")
     _err(L.qwfn_state_restore(S, B, D, 2, 1, 5, None), K.EINVAL, "source kind")
+
+
+def test_fused_append_attention_validation():
+    L = K.load()
+    r = ctypes.byref
+    q4, k4, o4 = _fa_views()
+    src = K.tensor(FAKE, K.TYPE_F32, (512, 3), (4, 2048))
+    call = lambda sk, sv, first, q=q4, k=k4: L.qwfn_flash_attn_ext_q8_0_append(
+        r(q), r(k), r(k), None, 0.0625, 0.0, 0.0, r(o4), 1, None, 0, r(sk), r(sv), first, None)
+    _err(call(src, src, 10 ** 9), K.ERANGE, "inside the attended keys")
+    _err(call(src, src, -1), K.ERANGE, "inside the attended keys")
+    _err(call(K.tensor(FAKE, K.TYPE_F32, (256, 3), (4, 1024)), src, 0), K.EINVAL, "every KV head")
+    _err(call(K.tensor(FAKE, K.TYPE_F32, (512, 65), (4, 2048)), K.tensor(FAKE, K.TYPE_F32, (512, 65), (4, 2048)), 0),
+         K.ENOTSUP, "1 to 64")
+    _err(call(K.tensor(FAKE + 4, K.TYPE_F32, (512, 3), (4, 2048)), src, 0), K.EALIGN, "16-byte")
+    _err(call(src, K.tensor(FAKE, K.TYPE_F32, (512, 2), (4, 2048)), 0), K.EINVAL, "same shape")
+    _err(call(K.tensor(FAKE, K.TYPE_F16, (512, 3), (2, 1024)), src, 0), K.EINVAL, "f32")

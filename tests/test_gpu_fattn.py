@@ -259,3 +259,46 @@ def test_gathered_inputs_padded(gpu, oracle):
             vh = np.ascontiguousarray(vc[sel][:, (h // 8) * 272:(h // 8 + 1) * 272])
             ref = KD.oracle_attn(q[t:t + 1, h:h + 1], kh, vh, len(sel), 1, None, 1 / 16)
             check(got[t, h], ref[0, 0])
+
+
+@pytest.mark.parametrize("n_past,T,nh,variant,first_off", [(100, 1, 16, O.Q8_X86, 0), (16384, 3, 16, O.Q8_X86, 0),
+                                                           (16384, 3, 24, O.Q8_REF, 0), (65536, 3, 16, O.Q8_X86, 0),
+                                                           (4094, 3, 16, O.Q8_X86, -2)])
+def test_fused_append_equals_separate_calls(gpu, oracle, n_past, T, nh, variant, first_off):
+    """qwfn_flash_attn_ext_q8_0_append writes the same cache bytes and returns the
+    same output bits as the two-tensor append followed by the attention call;
+    first_off < 0 puts the new rows before the last keys (across a split edge)."""
+    K = gpu
+    import torch
+    n_kv = n_past + T
+    first = n_past + first_off
+    kc, vc = layer(31, n_kv, n_kv + 64, outliers=True)
+    newk = KD.kv_rows(31, 1, KD.K_KIND, T, first_row=first, outliers=True)
+    newv = KD.kv_rows(31, 1, KD.V_KIND, T, first_row=first, outliers=True)
+    q = KD.q_rows(31, 0, T, nh)[0]
+    mask = O.causal_mask(T, n_past) if T > 1 else None
+    outs, caches = [], []
+    for fused in (False, True):
+        kd, vd = dev(kc), dev(vc)
+        ks, vs = dev(newk.astype(np.float32)), dev(newv.astype(np.float32))
+        qd = dev(q[None].astype(np.float32))
+        out = torch.full((1, T, nh, 256), float("nan"), dtype=torch.float32, device="cuda")
+        kv = K.cache_attn_view(kd, n_kv, 2)
+        vv = K.cache_attn_view(vd, n_kv, 2)
+        md = dev(mask.view(np.float16)) if mask is not None else None
+        mv = K.mask_view(md) if md is not None else None
+        say(f"fused append={fused} n_past={n_past} T={T} nh={nh} first={first}")
+        if fused:
+            K.flash_attn_ext_append(K.q_view(qd), kv, vv, mv, 1 / 16, K.out_view(out), ks, vs, first, variant=variant)
+        else:
+            K.cpy_f32_q8_0_kv(ks, kd, vs, vd, first, variant=variant)
+            K.flash_attn_ext(K.q_view(qd), kv, vv, mv, 1 / 16, K.out_view(out), variant=variant)
+        outs.append(host(out)[0])
+        caches.append((host(kd), host(vd)))
+    np.testing.assert_array_equal(caches[1][0], caches[0][0])
+    np.testing.assert_array_equal(caches[1][1], caches[0][1])
+    np.testing.assert_array_equal(outs[1], outs[0])
+    # and the appended rows are the oracle's quantisation
+    ref_k = kc.copy()
+    O.cpy(ref_k, newk, first, variant)
+    np.testing.assert_array_equal(caches[1][0], ref_k)
