@@ -304,9 +304,17 @@ def measure_rows(K, torch, np, dev, gen) -> dict:
     us = timed(torch, lambda k: K.flash_attn_ext(K.q_view(bq), bviews[k % bsets][0], bviews[k % bsets][1], bmv,
                                                 1 / 16, K.out_view(bout), ws=bws), 20)
     b = sum(depths) * 2 * ROW
+    rows["batch4_decode_mask_only"] = {"depths": depths, "us_per_launch": round(us, 3), "bytes_per_launch": b,
+                                       "GBs": gbs(b, us), "frac": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    # the same batch with the depths given per sequence (qwfn_flash_attn_ext_q8_0_seq)
+    sws = torch.empty(max(256, K.fattn_workspace_size_seq(K.q_view(bq), bviews[0][0], bviews[0][1], None, depths)),
+                      dtype=torch.uint8, device=dev)
+    us = timed(torch, lambda k: K.flash_attn_ext_seq(K.q_view(bq), bviews[k % bsets][0], bviews[k % bsets][1], None,
+                                                    1 / 16, K.out_view(bout), depths, ws=sws), 20)
     rows["batch4_decode"] = {"depths": depths, "us_per_launch": round(us, 3), "bytes_per_launch": b,
-                             "GBs": gbs(b, us), "frac": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
-    del bc, bws
+                             "GBs": gbs(b, us), "frac": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                             "entry": "qwfn_flash_attn_ext_q8_0_seq"}
+    del bc, bws, sws
 
     # ---- prefill chunk: 512 causal queries at depth 16384 through the same op ----
     d0, T = 16384, 512

@@ -153,6 +153,22 @@ int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor * k, const
                              const qwfn_tensor * mask, float scale, float max_bias, float logit_softcap,
                              const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes, void * stream);
 
+/* Batched decode over sequences of different depths: as
+ * qwfn_flash_attn_ext_q8_0, except that sequence b (q batch index) attends
+ * only keys [0, seq_n_kv[b]) -- the same result as masking its later keys with
+ * -inf, which is how a mask-only call expresses ragged batches (a [n_kv, 1,
+ * 1, B] mask of 0 then -inf). seq_n_kv is a host array of B counts in
+ * [0, n_kv], B <= 16. The keys are split per sequence in proportion to its
+ * count, so every workgroup streams about the same number of chunks and no
+ * workgroup reads keys past its sequence's end. A mask, if given, still
+ * applies. Size ws with qwfn_fattn_workspace_size_seq. */
+size_t qwfn_fattn_workspace_size_seq(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
+                                     const qwfn_tensor * mask, const int64_t * seq_n_kv);
+int qwfn_flash_attn_ext_q8_0_seq(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
+                                 const qwfn_tensor * mask, float scale, float max_bias, float logit_softcap,
+                                 const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes,
+                                 const int64_t * seq_n_kv, void * stream);
+
 /* The layer's K and V append followed by its attention, in one launch: the
  * two ggml_cpy / ggml_set_rows nodes that write the step's rows
  * (qwfn_graph.cpp:376-383, :623-624, :916-921) and the ggml_flash_attn_ext

@@ -64,6 +64,7 @@ constexpr int WAVES  = 8;              // wavefronts per block, one block per CU
 constexpr int WAVES_PAIR = 4;          // wavefronts per block, two blocks per CU
 constexpr int QWIN   = 64;             // bytes of one block's query window
 constexpr int MAX_SPLITS = 1024;       // key splits per (batch, KV head, row group)
+constexpr int RAGGED_MAX_B = 16;       // sequences of a call with per-sequence key counts
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float RESCALE_SLACK = 8.f;   // log2 units the running max may lag the true max
 constexpr int PV_BATCH = 4;            // 16-key V block tiles whose LDS reads are issued together
@@ -143,6 +144,16 @@ struct fa_args {
     size_t   app_nb1;
     int64_t  app_row0;
     int32_t  app_n;
+    // per-sequence key counts (ragged != 0): sequence b attends keys
+    // [0, r_n_kv[b]) in r_ns[b] splits of r_split_len[b] keys, which are units
+    // r_ustart[b] .. r_ustart[b+1]-1; ns above is the largest r_ns (the stride
+    // of the split partials)
+    int32_t  ragged;
+    int32_t  r_units;      // units of all sequences (r_ustart[B])
+    int32_t  r_ustart[RAGGED_MAX_B + 1];
+    int32_t  r_ns[RAGGED_MAX_B];
+    int32_t  r_split_len[RAGGED_MAX_B];
+    int64_t  r_n_kv[RAGGED_MAX_B];
 };
 
 // x / d through m = ceil(2^32 / d): floor(x * m / 2^32) = floor(x / d) while
@@ -373,8 +384,9 @@ __global__ __launch_bounds__(NW * 64, NW / 4 > 2 ? NW / 4 : 2) void k_fattn_q8_0
     //      (blockIdx % 8); with fewer, consecutive blocks spread them ----
     const int id   = blockIdx.x;
     const int hgn  = a.nh_kv * a.n_rg;
+    const int n_units = a.ragged ? a.r_units : a.B * a.ns;
     int hg, u;
-    if (a.B * a.ns >= 8) {
+    if (n_units >= 8) {
         const int j = id >> 3;
         const int jq = (int) udiv((uint32_t) j, (uint32_t) hgn, a.hgn_mul);
         hg = j - jq * hgn;
@@ -385,12 +397,32 @@ __global__ __launch_bounds__(NW * 64, NW / 4 > 2 ? NW / 4 : 2) void k_fattn_q8_0
     }
     const int kvh  = (int) udiv((uint32_t) hg, (uint32_t) a.n_rg, a.nrg_mul);
     const int rg   = hg - kvh * a.n_rg;
-    const int b    = (int) udiv((uint32_t) u, (uint32_t) a.ns, a.ns_mul);
-    const int split = u - b * a.ns;
-    if (b >= a.B) return;
-    const int64_t k_lo = (int64_t) split * a.split_len;
-    // the last split runs to n_kv (it may hold up to one chunk more than split_len)
-    const int64_t k_hi = split == a.ns - 1 ? a.n_kv : std::min<int64_t>(a.n_kv, k_lo + a.split_len);
+    if (u >= n_units) return;                      // padding of the XCD mapping
+    int b, split;
+    int64_t k_lo, k_hi;
+    if (a.ragged) {
+        // the sequence whose units hold u; constant indices keep the table
+        // reads scalar (an indexed read of the argument block is not)
+        int32_t us = 0, nsb = 1, slb = 0;
+        int64_t nkb = 0;
+        b = 0;
+#pragma unroll
+        for (int i = 0; i < RAGGED_MAX_B; i++)
+            if (i < a.B && u >= a.r_ustart[i]) {
+                b = i; us = a.r_ustart[i]; nsb = a.r_ns[i]; slb = a.r_split_len[i]; nkb = a.r_n_kv[i];
+            }
+        split = u - us;
+        k_lo = (int64_t) split * slb;
+        const int64_t e = k_lo + slb;     // ternaries, not std::min: its reference result put a copy on the stack
+        k_hi = split == nsb - 1 ? nkb : (nkb < e ? nkb : e);
+    } else {
+        b = (int) udiv((uint32_t) u, (uint32_t) a.ns, a.ns_mul);
+        split = u - b * a.ns;
+        k_lo = (int64_t) split * a.split_len;
+        // the last split runs to n_kv (it may hold up to one chunk more than split_len)
+        const int64_t e = k_lo + a.split_len;
+        k_hi = split == a.ns - 1 ? a.n_kv : (a.n_kv < e ? a.n_kv : e);
+    }
     const int n_chunks = (int) ((k_hi - k_lo + CK - 1) / CK);
     const int r0 = rg * a.rw;                          // first query row of this block
     const int RW = std::min(a.rw, a.R - r0);          // rows in this block
@@ -1032,6 +1064,12 @@ __global__ __launch_bounds__(256) void k_fattn_merge(fa_args a) {
     const int r = row % a.R;
     const int bh = row / a.R;
     const int kvh = bh % a.nh_kv, b = bh / a.nh_kv;
+    int ns = a.ns;                                               // this sequence's splits (a.ns is the stride)
+    if (a.ragged) {
+#pragma unroll
+        for (int i = 0; i < RAGGED_MAX_B; i++)
+            if (i == b) ns = a.r_ns[i];
+    }
     const int g = threadIdx.x >> 4, q = threadIdx.x & 15;
     const float2 * ml = a.part_ml + (size_t) bh * a.ns * a.R + r;
     const float4 * po = (const float4 *) (a.part_o + ((size_t) bh * a.ns * a.R + r) * D + 64 * quarter) + q;
@@ -1045,14 +1083,14 @@ __global__ __launch_bounds__(256) void k_fattn_merge(fa_args a) {
     constexpr int MLJ = MAX_SPLITS / 256;
     float2 e[MLJ];
 #pragma unroll
-    for (int j = 0; j < MLJ; j++) e[j] = ml[(size_t) std::min((int) threadIdx.x + 256 * j, a.ns - 1) * a.R];
+    for (int j = 0; j < MLJ; j++) e[j] = ml[(size_t) std::min((int) threadIdx.x + 256 * j, ns - 1) * a.R];
     float4 ob[MERGE_BATCH];
 #pragma unroll
-    for (int i = 0; i < MERGE_BATCH; i++) ob[i] = load_nt4(po + (size_t) std::min(g + i * MERGE_GROUPS, a.ns - 1) * sstride);
+    for (int i = 0; i < MERGE_BATCH; i++) ob[i] = load_nt4(po + (size_t) std::min(g + i * MERGE_GROUPS, ns - 1) * sstride);
     float mloc = -INFINITY;
 #pragma unroll
     for (int j = 0; j < MLJ; j++) {
-        if ((int) threadIdx.x + 256 * j >= a.ns) e[j] = make_float2(-INFINITY, 0.f);
+        if ((int) threadIdx.x + 256 * j >= ns) e[j] = make_float2(-INFINITY, 0.f);
         mloc = xmax(mloc, e[j].x);
     }
     mloc = wave_reduce(mloc, [](float x, float y) { return xmax(x, y); });
@@ -1065,7 +1103,7 @@ __global__ __launch_bounds__(256) void k_fattn_merge(fa_args a) {
         const int s = (int) threadIdx.x + 256 * j;
         const float w = e[j].x == -INFINITY ? 0.f : exp2f(e[j].x - M);
         lpart += w * e[j].y;
-        if (s < a.ns) wsh[s] = w;
+        if (s < ns) wsh[s] = w;
     }
     lpart = wave_reduce(lpart, [](float x, float y) { return x + y; });
     __syncthreads();
@@ -1074,15 +1112,15 @@ __global__ __launch_bounds__(256) void k_fattn_merge(fa_args a) {
     const float L = (red[0] + red[1]) + (red[2] + red[3]);
 
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s0 = 0; s0 < a.ns; s0 += MERGE_GROUPS * MERGE_BATCH) {
+    for (int s0 = 0; s0 < ns; s0 += MERGE_GROUPS * MERGE_BATCH) {
         if (s0 > 0) {
 #pragma unroll
-            for (int i = 0; i < MERGE_BATCH; i++) ob[i] = load_nt4(po + (size_t) std::min(s0 + g + i * MERGE_GROUPS, a.ns - 1) * sstride);
+            for (int i = 0; i < MERGE_BATCH; i++) ob[i] = load_nt4(po + (size_t) std::min(s0 + g + i * MERGE_GROUPS, ns - 1) * sstride);
         }
 #pragma unroll
         for (int i = 0; i < MERGE_BATCH; i++) {
             const int s = s0 + g + i * MERGE_GROUPS;
-            const float w = s < a.ns ? wsh[s] : 0.f;
+            const float w = s < ns ? wsh[s] : 0.f;
             acc.x += w * ob[i].x; acc.y += w * ob[i].y; acc.z += w * ob[i].z; acc.w += w * ob[i].w;
         }
     }
@@ -1123,6 +1161,10 @@ struct fa_plan {
     fa_kind kind;
     size_t  off_ml;                   // workspace section of the split (max, sum) pairs (bytes)
     size_t  ws_bytes;
+    // per-sequence key counts: splits of each sequence (ns is the largest)
+    int32_t ragged;
+    int32_t r_ustart[RAGGED_MAX_B + 1], r_ns[RAGGED_MAX_B], r_split_len[RAGGED_MAX_B];
+    int64_t r_n_kv[RAGGED_MAX_B];
 };
 
 int env_int(const char * name, int dflt) {
@@ -1171,7 +1213,7 @@ int check_no_scratch() {
 }
 
 int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v, const qwfn_tensor * mask,
-               fa_plan * pl) {
+               fa_plan * pl, const int64_t * seq_n_kv = nullptr) {
     if (!q || !k || !v) return set_error(QWFN_EINVAL, "flash_attn_ext: NULL q/k/v");
     if (q->type != QWFN_TYPE_F32) return set_error(QWFN_EINVAL, "flash_attn_ext: q must be f32");
     if (k->type != QWFN_TYPE_Q8_0 || v->type != QWFN_TYPE_Q8_0)
@@ -1251,6 +1293,42 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
     // keys of the longest split (the last may be longer), rounded up to whole chunks
     pl->max_span = std::max<int64_t>(split_len, n_kv - (ns - 1) * split_len);
     pl->max_span = (pl->max_span + ck - 1) / ck * ck;
+    pl->ragged = 0;
+    if (seq_n_kv) {
+        // Per-sequence key counts: each sequence gets splits in proportion to its
+        // keys, so every block streams about the same number of chunks whatever
+        // the spread of the depths. Splits round up to whole chunks.
+        if (B > RAGGED_MAX_B)
+            return set_error(QWFN_ENOTSUP, "flash_attn_ext_seq: at most " + std::to_string(RAGGED_MAX_B) + " sequences");
+        int64_t total = 0;
+        for (int64_t b = 0; b < B; b++) {
+            if (seq_n_kv[b] < 0 || seq_n_kv[b] > n_kv)
+                return set_error(QWFN_ERANGE, "flash_attn_ext_seq: sequence key counts must lie in [0, n_kv]");
+            total += seq_n_kv[b];
+        }
+        const int64_t units = std::max<int64_t>(1, target_blocks / std::max<int64_t>(1, nh_kv * pl->n_rg));
+        int64_t ns_max = 1, span = ck, ustart = 0;
+        for (int64_t b = 0; b < B; b++) {
+            const int64_t nk = seq_n_kv[b];
+            int64_t nsb = total > 0 ? std::max<int64_t>(1, (units * nk + total / 2) / total) : 1;
+            nsb = std::min<int64_t>(nsb, std::max<int64_t>(1, (nk + ck - 1) / ck));
+            int64_t sl = (nk + nsb - 1) / nsb;
+            sl = std::max<int64_t>(ck, (sl + ck - 1) / ck * ck);
+            nsb = std::max<int64_t>(1, (nk + sl - 1) / sl);
+            pl->r_ustart[b] = (int32_t) ustart;
+            pl->r_ns[b] = (int32_t) nsb;
+            pl->r_split_len[b] = (int32_t) sl;
+            pl->r_n_kv[b] = nk;
+            ustart += nsb;
+            ns_max = std::max(ns_max, nsb);
+            span = std::max(span, sl);
+        }
+        pl->r_ustart[B] = (int32_t) ustart;
+        pl->ragged = 1;
+        ns = ns_max;
+        split_len = span;
+        pl->max_span = (int32_t) span;
+    }
     if (ns > MAX_SPLITS)
         return set_error(QWFN_ENOTSUP, "flash_attn_ext: " + std::to_string(ns) + " key splits requested, at most " +
                                            std::to_string(MAX_SPLITS) + " supported");
@@ -1309,13 +1387,13 @@ int check_append(const fa_append & ap, const qwfn_tensor * q, const qwfn_tensor 
 
 int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v, const qwfn_tensor * mask, float scale,
               float max_bias, float logit_softcap, const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes,
-              void * stream, const fa_append * app) {
+              void * stream, const fa_append * app, const int64_t * seq_n_kv = nullptr) {
     if (max_bias != 0.0f) return set_error(QWFN_ENOTSUP, "flash_attn_ext: max_bias (ALiBi) is not supported");
     if (logit_softcap != 0.0f) return set_error(QWFN_ENOTSUP, "flash_attn_ext: logit_softcap is not supported");
     if (!(std::isfinite(scale))) return set_error(QWFN_EINVAL, "flash_attn_ext: scale must be finite");
     if (variant != QWFN_Q8_REF && variant != QWFN_Q8_X86) return set_error(QWFN_EINVAL, "flash_attn_ext: unknown variant");
     fa_plan pl{};
-    if (int rc = plan_fattn(q, k, v, mask, &pl)) return rc;
+    if (int rc = plan_fattn(q, k, v, mask, &pl, seq_n_kv)) return rc;
     if (app)
         if (int rc = check_append(*app, q, k, v)) return rc;
     if (!dst || !dst->data || dst->type != QWFN_TYPE_F32) return set_error(QWFN_EINVAL, "flash_attn_ext: dst must be f32");
@@ -1372,6 +1450,14 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
     a.gqa = pl.gqa; a.R = pl.R; a.B = (int32_t) q->ne[3];
     a.kb = (int32_t) k->ne[3]; a.vb = (int32_t) v->ne[3];
     a.ns = pl.ns; a.split_len = pl.split_len; a.rw = pl.rw; a.n_rg = pl.n_rg;
+    a.ragged = pl.ragged;
+    if (pl.ragged) {
+        for (int b = 0; b <= a.B; b++) a.r_ustart[b] = pl.r_ustart[b];
+        a.r_units = pl.r_ustart[a.B];
+        for (int b = 0; b < a.B; b++) {
+            a.r_ns[b] = pl.r_ns[b]; a.r_split_len[b] = pl.r_split_len[b]; a.r_n_kv[b] = pl.r_n_kv[b];
+        }
+    }
     a.scale = scale; a.x86 = variant == QWFN_Q8_X86;
     a.dst_vec = is_aligned(dst->data, 16) ? 1 : 0;
     a.q_slice = (uint32_t) q_slice_bytes(*q);
@@ -1384,7 +1470,8 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
         a.app_n = (int32_t) app->src_k->ne[1];
     }
 
-    const int64_t units = (int64_t) a.B * a.ns >= 8 ? ((int64_t) a.B * a.ns + 7) / 8 * 8 : (int64_t) a.B * a.ns;
+    const int64_t n_units = a.ragged ? (int64_t) a.r_units : (int64_t) a.B * a.ns;
+    const int64_t units = n_units >= 8 ? (n_units + 7) / 8 * 8 : n_units;
     const int64_t hgn = (int64_t) a.nh_kv * a.n_rg;
     const int64_t grid = units * hgn;
     // block indices divide by ns, nh_kv * n_rg and n_rg through 32-bit reciprocals
@@ -1435,6 +1522,21 @@ extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor
                                         const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes,
                                         void * stream) {
     return fattn_run(q, k, v, mask, scale, max_bias, logit_softcap, dst, variant, ws, ws_bytes, stream, nullptr);
+}
+
+extern "C" size_t qwfn_fattn_workspace_size_seq(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
+                                                const qwfn_tensor * mask, const int64_t * seq_n_kv) {
+    fa_plan pl{};
+    if (!seq_n_kv || plan_fattn(q, k, v, mask, &pl, seq_n_kv)) return 0;
+    return pl.ws_bytes;
+}
+
+extern "C" int qwfn_flash_attn_ext_q8_0_seq(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
+                                            const qwfn_tensor * mask, float scale, float max_bias, float logit_softcap,
+                                            const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes,
+                                            const int64_t * seq_n_kv, void * stream) {
+    if (!seq_n_kv) return set_error(QWFN_EINVAL, "flash_attn_ext_seq: seq_n_kv is NULL");
+    return fattn_run(q, k, v, mask, scale, max_bias, logit_softcap, dst, variant, ws, ws_bytes, stream, nullptr, seq_n_kv);
 }
 
 extern "C" int qwfn_flash_attn_ext_q8_0_append(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,

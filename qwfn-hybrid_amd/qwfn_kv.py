@@ -68,7 +68,8 @@ class QsaInputs(ctypes.Structure):
 EXPORTS = [
     "qwfn_abi_version", "qwfn_last_error", "qwfn_init", "qwfn_device_status",
     "qwfn_set_rows_q8_0", "qwfn_cpy_f32_q8_0", "qwfn_set_rows_q8_0_kv", "qwfn_cpy_f32_q8_0_kv", "qwfn_get_rows_i32", "qwfn_kv_gather_segments",
-    "qwfn_fattn_workspace_size", "qwfn_flash_attn_ext_q8_0", "qwfn_flash_attn_ext_q8_0_append", "qwfn_state_restore",
+    "qwfn_fattn_workspace_size", "qwfn_flash_attn_ext_q8_0", "qwfn_flash_attn_ext_q8_0_append",
+    "qwfn_fattn_workspace_size_seq", "qwfn_flash_attn_ext_q8_0_seq", "qwfn_state_restore",
     # include/qwfn_state.h
     "qwfn_state_config_default", "qwfn_state_create", "qwfn_state_destroy", "qwfn_state_tensor",
     "qwfn_state_bytes", "qwfn_state_host_bytes", "qwfn_state_rollback_bytes", "qwfn_state_n_ctx",
@@ -108,6 +109,11 @@ def load(path: str = LIB_PATH):
     L.qwfn_fattn_workspace_size.restype = sz
     L.qwfn_flash_attn_ext_q8_0.argtypes = [T, T, T, T, ctypes.c_float, ctypes.c_float, ctypes.c_float, T,
                                            ctypes.c_int, vp, sz, vp]
+    PL = ctypes.POINTER(i64)
+    L.qwfn_fattn_workspace_size_seq.argtypes = [T, T, T, T, PL]
+    L.qwfn_fattn_workspace_size_seq.restype = sz
+    L.qwfn_flash_attn_ext_q8_0_seq.argtypes = [T, T, T, T, ctypes.c_float, ctypes.c_float, ctypes.c_float, T,
+                                               ctypes.c_int, vp, sz, PL, vp]
     L.qwfn_flash_attn_ext_q8_0_append.argtypes = [T, T, T, T, ctypes.c_float, ctypes.c_float, ctypes.c_float, T,
                                                   ctypes.c_int, vp, sz, T, T, i64, vp]
     L.qwfn_state_restore.argtypes = [ctypes.POINTER(vp), ctypes.POINTER(sz), ctypes.POINTER(vp), i32, i32, i32, vp]
@@ -163,6 +169,7 @@ def load(path: str = LIB_PATH):
             getattr(L, name).restype = getattr(L, name).restype or ctypes.c_int
     L.qwfn_last_error.restype = ctypes.c_char_p
     L.qwfn_fattn_workspace_size.restype = sz
+    L.qwfn_fattn_workspace_size_seq.restype = sz
     _lib = L
     return L
 
@@ -318,6 +325,24 @@ def flash_attn_ext(qv: Tensor, kv: Tensor, vv: Tensor, mv: Tensor | None, scale:
     return check(L.qwfn_flash_attn_ext_q8_0(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv),
                                             ctypes.byref(mv) if mv is not None else None, scale, max_bias, softcap,
                                             ctypes.byref(ov), variant, ws_ptr, ws_bytes, _stream(stream)))
+
+
+def flash_attn_ext_seq(qv: Tensor, kv: Tensor, vv: Tensor, mv: Tensor | None, scale: float, ov: Tensor, seq_n_kv,
+                       variant: int = Q8_X86, ws=None, stream=None):
+    """Batched attention where sequence b attends its first seq_n_kv[b] keys."""
+    L = load()
+    n = (ctypes.c_int64 * len(seq_n_kv))(*[int(x) for x in seq_n_kv])
+    ws_ptr = ws.data_ptr() if ws is not None else None
+    ws_bytes = ws.numel() * ws.element_size() if ws is not None else 0
+    return check(L.qwfn_flash_attn_ext_q8_0_seq(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv),
+                                                ctypes.byref(mv) if mv is not None else None, scale, 0.0, 0.0,
+                                                ctypes.byref(ov), variant, ws_ptr, ws_bytes, n, _stream(stream)))
+
+
+def fattn_workspace_size_seq(qv: Tensor, kv: Tensor, vv: Tensor, mv: Tensor | None, seq_n_kv) -> int:
+    n = (ctypes.c_int64 * len(seq_n_kv))(*[int(x) for x in seq_n_kv])
+    return int(load().qwfn_fattn_workspace_size_seq(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv),
+                                                    ctypes.byref(mv) if mv is not None else None, n))
 
 
 def flash_attn_ext_append(qv: Tensor, kv: Tensor, vv: Tensor, mv: Tensor | None, scale: float, ov: Tensor,

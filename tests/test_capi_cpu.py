@@ -157,3 +157,22 @@ def test_fused_append_attention_validation():
     _err(call(K.tensor(FAKE + 4, K.TYPE_F32, (512, 3), (4, 2048)), src, 0), K.EALIGN, "16-byte")
     _err(call(src, K.tensor(FAKE, K.TYPE_F32, (512, 2), (4, 2048)), 0), K.EINVAL, "same shape")
     _err(call(K.tensor(FAKE, K.TYPE_F16, (512, 3), (2, 1024)), src, 0), K.EINVAL, "f32")
+
+
+def test_ragged_batch_validation():
+    L = K.load()
+    r = ctypes.byref
+    q4, k4, o4 = _fa_views()
+    seq = (ctypes.c_int64 * 1)(101)
+    _err(L.qwfn_flash_attn_ext_q8_0_seq(r(q4), r(k4), r(k4), None, 0.0625, 0.0, 0.0, r(o4), 1, None, 0, seq, None),
+         K.ERANGE, "[0, n_kv]")
+    _err(L.qwfn_flash_attn_ext_q8_0_seq(r(q4), r(k4), r(k4), None, 0.0625, 0.0, 0.0, r(o4), 1, None, 0, None, None),
+         K.EINVAL, "NULL")
+    B = 17
+    q = K.tensor(FAKE, K.TYPE_F32, (256, 1, 16, B), (4, 16 * 1024, 1024, 16 * 1024))
+    k = K.tensor(FAKE, K.TYPE_Q8_0, (256, 100, 2, B), (34, 544, 272, 1 << 20))
+    o = K.tensor(FAKE, K.TYPE_F32, (256, 16, 1, B), (4, 1024, 16 * 1024, 16 * 1024))
+    seq = (ctypes.c_int64 * B)(*([50] * B))
+    _err(L.qwfn_flash_attn_ext_q8_0_seq(r(q), r(k), r(k), None, 0.0625, 0.0, 0.0, r(o), 1, None, 0, seq, None),
+         K.ENOTSUP, "at most 16")
+    assert L.qwfn_fattn_workspace_size_seq(r(q4), r(k4), r(k4), None, None) == 0

@@ -302,3 +302,69 @@ def test_fused_append_equals_separate_calls(gpu, oracle, n_past, T, nh, variant,
     ref_k = kc.copy()
     O.cpy(ref_k, newk, first, variant)
     np.testing.assert_array_equal(caches[1][0], ref_k)
+
+
+def _seq_attn(K, q, kc, vc, n_ctx, seq, mask=None, nh_kv=2):
+    import torch
+    B, T, nh, hd = q.shape
+    qd = dev(q.astype(np.float32))
+    kd, vd = dev(kc), dev(vc)
+    rb = kc.shape[-1]
+    kv = K.tensor(kd.data_ptr(), K.TYPE_Q8_0, (hd, n_ctx, nh_kv, B), (34, rb, hd // 32 * 34, n_ctx * rb))
+    vv = K.tensor(vd.data_ptr(), K.TYPE_Q8_0, (hd, n_ctx, nh_kv, B), (34, rb, hd // 32 * 34, n_ctx * rb))
+    md = dev(mask.view(np.float16)) if mask is not None else None
+    mv = K.mask_view(md) if md is not None else None
+    out = torch.full((B, T, nh, hd), float("nan"), dtype=torch.float32, device="cuda")
+    n = K.fattn_workspace_size_seq(K.q_view(qd), kv, vv, mv, seq)
+    ws = torch.empty(max(n, 256), dtype=torch.uint8, device="cuda")
+    K.flash_attn_ext_seq(K.q_view(qd), kv, vv, mv, 1 / 16, K.out_view(out), seq, ws=ws)
+    return host(out)
+
+
+@pytest.mark.parametrize("depths,nh", [([300, 1200, 2500, 4096], 16), ([4096, 0, 65, 4000], 16), ([1, 2049, 4096], 24)])
+def test_ragged_batch_per_sequence_counts(gpu, oracle, depths, nh):
+    """qwfn_flash_attn_ext_q8_0_seq: sequence b attends its first depths[b] keys,
+    split in proportion to its depth; the result is the oracle's attention over
+    those keys (a sequence of 0 keys gives zeros), and matches the mask-only call."""
+    K = gpu
+    B, n_ctx = len(depths), 4096
+    kcs, vcs = [], []
+    for s in range(B):
+        kc, vc = layer(40 + s, n_ctx, n_ctx, outliers=True)
+        kcs.append(kc)
+        vcs.append(vc)
+    kc, vc = np.stack(kcs), np.stack(vcs)
+    q = KD.q_rows(9, 0, 1, nh, batch=B)
+    say(f"ragged seq counts {depths} nh={nh}")
+    got = _seq_attn(K, q, kc, vc, n_ctx, depths)
+    mask = np.full((B, 1, 1, n_ctx), O.F16_NEG_INF, np.uint16)
+    for s, dpt in enumerate(depths):
+        mask[s, 0, 0, :dpt] = 0
+    via_mask = gpu_attn(K, q, kc, vc, n_ctx, 2, mask, 1 / 16)
+    for s, dpt in enumerate(depths):
+        if dpt == 0:
+            assert (got[s] == 0).all()
+            continue
+        ref = KD.oracle_attn(q[s, :], kcs[s], vcs[s], dpt, 2, None, 1 / 16)
+        check(got[s], ref)
+        assert np.abs(got[s] - via_mask[s]).max() <= TIGHT
+
+
+def test_ragged_batch_with_mask(gpu, oracle):
+    """Per-sequence counts and a mask together: both apply."""
+    K = gpu
+    depths, n_ctx, T = [1000, 3072], 3072, 3
+    kcs, vcs = [], []
+    for s in range(2):
+        kc, vc = layer(60 + s, n_ctx, n_ctx)
+        kcs.append(kc)
+        vcs.append(vc)
+    kc, vc = np.stack(kcs), np.stack(vcs)
+    q = KD.q_rows(11, 0, T, 16, batch=2)
+    mask = np.stack([O.causal_mask(T, n_ctx - T, n_ctx)[None] for _ in range(2)])   # [2, 1, T, n_ctx]
+    say("ragged seq counts + causal mask")
+    got = _seq_attn(K, q, kc, vc, n_ctx, depths, mask)
+    for s, dpt in enumerate(depths):
+        m = mask[s, 0][:, :dpt].copy()
+        ref = KD.oracle_attn(q[s], kcs[s], vcs[s], dpt, 2, m, 1 / 16)
+        check(got[s], ref)
