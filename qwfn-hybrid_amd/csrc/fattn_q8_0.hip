@@ -352,7 +352,9 @@ __global__ void k_zero_f32(float * f, int64_t n) {
     for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) f[i] = 0.f;
 }
 
-template <int RT, bool MT, int NW, int KWV>
+// RG: per-sequence splits (the ragged table of fa_args); a template parameter
+// so that the block mapping of the other calls carries none of it
+template <int RT, bool MT, int NW, int KWV, bool RG>
 __global__ __launch_bounds__(NW * 64, NW / 4 > 2 ? NW / 4 : 2) void k_fattn_q8_0(fa_args a) {
     using C = fa_cfg<RT, MT, NW, KWV>;
     // the argument block's pointers are loaded with the rest, in one round of
@@ -384,7 +386,7 @@ __global__ __launch_bounds__(NW * 64, NW / 4 > 2 ? NW / 4 : 2) void k_fattn_q8_0
     //      (blockIdx % 8); with fewer, consecutive blocks spread them ----
     const int id   = blockIdx.x;
     const int hgn  = a.nh_kv * a.n_rg;
-    const int n_units = a.ragged ? a.r_units : a.B * a.ns;
+    const int n_units = RG ? a.r_units : a.B * a.ns;
     int hg, u;
     if (n_units >= 8) {
         const int j = id >> 3;
@@ -400,7 +402,7 @@ __global__ __launch_bounds__(NW * 64, NW / 4 > 2 ? NW / 4 : 2) void k_fattn_q8_0
     if (u >= n_units) return;                      // padding of the XCD mapping
     int b, split;
     int64_t k_lo, k_hi;
-    if (a.ragged) {
+    if constexpr (RG) {
         // the sequence whose units hold u; constant indices keep the table
         // reads scalar (an indexed read of the argument block is not)
         int32_t us = 0, nsb = 1, slb = 0;
@@ -1056,6 +1058,7 @@ __device__ __forceinline__ float wave_reduce(float x, Op op) {
     return op(op(r0, r1), op(r2, r3));
 }
 
+template <bool RG>
 __global__ __launch_bounds__(256) void k_fattn_merge(fa_args a) {
     __shared__ float wsh[MAX_SPLITS];
     __shared__ float red[4];
@@ -1065,7 +1068,7 @@ __global__ __launch_bounds__(256) void k_fattn_merge(fa_args a) {
     const int bh = row / a.R;
     const int kvh = bh % a.nh_kv, b = bh / a.nh_kv;
     int ns = a.ns;                                               // this sequence's splits (a.ns is the stride)
-    if (a.ragged) {
+    if constexpr (RG) {
 #pragma unroll
         for (int i = 0; i < RAGGED_MAX_B; i++)
             if (i == b) ns = a.r_ns[i];
@@ -1194,12 +1197,17 @@ uint32_t recip32(int64_t d) {
 // kernel that spills to scratch would break that count: refuse to run one.
 int check_no_scratch() {
     static const int rc = [] {
-        for (const void * f : {(const void *) k_fattn_q8_0<1, false, WAVES, 16>, (const void *) k_fattn_q8_0<2, false, WAVES, 16>,
-                               (const void *) k_fattn_q8_0<1, true, WAVES, 16>, (const void *) k_fattn_q8_0<2, true, WAVES, 16>,
-                               (const void *) k_fattn_q8_0<1, false, WAVES_PAIR, 16>,
-                               (const void *) k_fattn_q8_0<1, true, WAVES_PAIR, 16>,
-                               (const void *) k_fattn_q8_0<2, false, WAVES_PAIR, 32>,
-                               (const void *) k_fattn_q8_0<2, true, WAVES_PAIR, 32>}) {
+        for (const void * f : {(const void *) k_fattn_q8_0<1, false, WAVES, 16, false>, (const void *) k_fattn_q8_0<2, false, WAVES, 16, false>,
+                               (const void *) k_fattn_q8_0<1, true, WAVES, 16, false>, (const void *) k_fattn_q8_0<2, true, WAVES, 16, false>,
+                               (const void *) k_fattn_q8_0<1, false, WAVES_PAIR, 16, false>,
+                               (const void *) k_fattn_q8_0<1, true, WAVES_PAIR, 16, false>,
+                               (const void *) k_fattn_q8_0<2, false, WAVES_PAIR, 32, false>,
+                               (const void *) k_fattn_q8_0<2, true, WAVES_PAIR, 32, false>,
+                               (const void *) k_fattn_q8_0<1, false, WAVES_PAIR, 16, true>,
+                               (const void *) k_fattn_q8_0<1, true, WAVES_PAIR, 16, true>,
+                               (const void *) k_fattn_q8_0<2, false, WAVES_PAIR, 32, true>,
+                               (const void *) k_fattn_q8_0<2, true, WAVES_PAIR, 32, true>,
+                               (const void *) k_fattn_q8_0<2, true, WAVES, 16, true>}) {
             hipFuncAttributes at{};
             if (int e = hip_check(hipFuncGetAttributes(&at, f), "hipFuncGetAttributes")) return e;
             if (at.localSizeBytes != 0)
@@ -1265,7 +1273,7 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
     // 4-wave blocks, two per CU (their prologues and phases overlap), or
     // 8-wave blocks, one per CU. QWFN_FA_PAIR=0 forces 8 waves.
     const int64_t B = q->ne[3];
-    const bool pair = env_int("QWFN_FA_PAIR", 1) != 0;
+    const bool pair = seq_n_kv || env_int("QWFN_FA_PAIR", 1) != 0;   // per-sequence splits: 4-wave kernels
     pl->kind = rw == 16 ? (pair ? FA_P4_T1 : FA_W8_T1) : (pair ? FA_P4_T2 : FA_W8_T2);
     pl->R = (int32_t) R;
     pl->rw = rw;
@@ -1483,33 +1491,49 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
     hipStream_t st = as_stream(stream);
     const bool mt = a.mask_mode == MASK_TILE;
     const dim3 g((unsigned) grid), b8(WAVES * 64), b4(WAVES_PAIR * 64);
+    if (a.ragged) {
+        // per-sequence splits: the 4-wave kernels (and the 8-wave mask-tile one)
+        switch (pl.kind) {
+            case FA_P4_T1:
+                if (mt) hipLaunchKernelGGL((k_fattn_q8_0<1, true, WAVES_PAIR, 16, true>), g, b4, 0, st, a);
+                else    hipLaunchKernelGGL((k_fattn_q8_0<1, false, WAVES_PAIR, 16, true>), g, b4, 0, st, a);
+                break;
+            default:
+                if (mt && mrows > MASK_ROWS_PAIR) hipLaunchKernelGGL((k_fattn_q8_0<2, true, WAVES, 16, true>), g, b8, 0, st, a);
+                else if (mt) hipLaunchKernelGGL((k_fattn_q8_0<2, true, WAVES_PAIR, 32, true>), g, b4, 0, st, a);
+                else    hipLaunchKernelGGL((k_fattn_q8_0<2, false, WAVES_PAIR, 32, true>), g, b4, 0, st, a);
+                break;
+        }
+    } else {
     switch (pl.kind) {
         case FA_P4_T1:
-            if (mt) hipLaunchKernelGGL((k_fattn_q8_0<1, true, WAVES_PAIR, 16>), g, b4, 0, st, a);
-            else    hipLaunchKernelGGL((k_fattn_q8_0<1, false, WAVES_PAIR, 16>), g, b4, 0, st, a);
+            if (mt) hipLaunchKernelGGL((k_fattn_q8_0<1, true, WAVES_PAIR, 16, false>), g, b4, 0, st, a);
+            else    hipLaunchKernelGGL((k_fattn_q8_0<1, false, WAVES_PAIR, 16, false>), g, b4, 0, st, a);
             break;
         case FA_P4_T2:
             // mask tiles of at most MASK_ROWS_PAIR rows fit next to two stages;
             // more rows (per-head masks, small gqa) take the 8-wave kernel over
             // the same 64-key chunks
-            if (mt && mrows > MASK_ROWS_PAIR) hipLaunchKernelGGL((k_fattn_q8_0<2, true, WAVES, 16>), g, b8, 0, st, a);
-            else if (mt) hipLaunchKernelGGL((k_fattn_q8_0<2, true, WAVES_PAIR, 32>), g, b4, 0, st, a);
-            else    hipLaunchKernelGGL((k_fattn_q8_0<2, false, WAVES_PAIR, 32>), g, b4, 0, st, a);
+            if (mt && mrows > MASK_ROWS_PAIR) hipLaunchKernelGGL((k_fattn_q8_0<2, true, WAVES, 16, false>), g, b8, 0, st, a);
+            else if (mt) hipLaunchKernelGGL((k_fattn_q8_0<2, true, WAVES_PAIR, 32, false>), g, b4, 0, st, a);
+            else    hipLaunchKernelGGL((k_fattn_q8_0<2, false, WAVES_PAIR, 32, false>), g, b4, 0, st, a);
             break;
         case FA_W8_T1:
-            if (mt) hipLaunchKernelGGL((k_fattn_q8_0<1, true, WAVES, 16>), g, b8, 0, st, a);
-            else    hipLaunchKernelGGL((k_fattn_q8_0<1, false, WAVES, 16>), g, b8, 0, st, a);
+            if (mt) hipLaunchKernelGGL((k_fattn_q8_0<1, true, WAVES, 16, false>), g, b8, 0, st, a);
+            else    hipLaunchKernelGGL((k_fattn_q8_0<1, false, WAVES, 16, false>), g, b8, 0, st, a);
             break;
         case FA_W8_T2:
-            if (mt) hipLaunchKernelGGL((k_fattn_q8_0<2, true, WAVES, 16>), g, b8, 0, st, a);
-            else    hipLaunchKernelGGL((k_fattn_q8_0<2, false, WAVES, 16>), g, b8, 0, st, a);
+            if (mt) hipLaunchKernelGGL((k_fattn_q8_0<2, true, WAVES, 16, false>), g, b8, 0, st, a);
+            else    hipLaunchKernelGGL((k_fattn_q8_0<2, false, WAVES, 16, false>), g, b8, 0, st, a);
             break;
+    }
     }
     if (int rc = hip_check(hipGetLastError(), "flash_attn launch")) return rc;
     if (a.ns > 1) {
         const int64_t blocks = (int64_t) a.B * a.nh_kv * a.R * 4;
         if (blocks > 0x7fffffff) return set_error(QWFN_EINVAL, "flash_attn_ext: merge grid too large");
-        hipLaunchKernelGGL(k_fattn_merge, dim3((unsigned) blocks), dim3(256), 0, st, a);
+        if (a.ragged) hipLaunchKernelGGL(k_fattn_merge<true>, dim3((unsigned) blocks), dim3(256), 0, st, a);
+        else          hipLaunchKernelGGL(k_fattn_merge<false>, dim3((unsigned) blocks), dim3(256), 0, st, a);
         if (int rc = hip_check(hipGetLastError(), "flash_attn merge launch")) return rc;
     }
     return QWFN_OK;
