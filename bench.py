@@ -191,6 +191,22 @@ def measure_state_rows(K, torch, np, dev, gbs) -> dict:
         qk.prepare(65534 + (k & 1), prev=qd)
         S.cell_mask_f16(cells, 65533, 2304, cmask, gcells)
     us = timed_graph(torch, decode_inputs, 16, 10)
+    # the decode step's block selection (qsa_dec_cells) for a 3-position verify step at
+    # 73728 positions: 18432 pooled f16 keys scored against 4 indexer heads, top 513
+    nb, kb = 73728 // 4, 513
+    gsel = torch.Generator(device=dev)
+    gsel.manual_seed(7)
+    pool = (torch.randn((nb, 128), generator=gsel, device=dev) * 0.5).to(torch.float16)
+    qsel = torch.randn((3, 4, 128), generator=gsel, device=dev)
+    bsel = torch.zeros((3, nb), dtype=torch.float32, device=dev)
+    bcells = torch.arange(nb * 4, dtype=torch.int32, device=dev)
+    csel = torch.empty((3, kb * 4), dtype=torch.int32, device=dev)
+    wsel = torch.empty(K.load().qwfn_qsa_select_workspace_size(nb, 3), dtype=torch.uint8, device=dev)
+    us_sel = timed_graph(torch, lambda k: S.qsa_select_cells(pool, qsel, bsel, kb, bcells, 4, csel, ws=wsel), 8, 10)
+    sel_bytes = nb * 128 * 2 * 3 + 3 * nb * 4 * 2 + 3 * kb * 4 * 4
+    rows["qsa_select_cells"] = {"us_per_call": round(us_sel, 2), "blocks": nb, "k_blocks": kb, "queries": 3,
+                                "bytes": sel_bytes, "GBs": gbs(sel_bytes, us_sel), "frac": frac(sel_bytes, us_sel)}
+    del pool, qsel, bsel, bcells, csel, wsel
     rows["decode_step_inputs"] = {"us_per_step": round(us, 2), "launches": 3,
                                   "what": "qsa_decode_prepare, qsa_decode_prepare_k (18432-block bias), cell mask 2052->2304"}
     torch.cuda.empty_cache()

@@ -11,6 +11,7 @@
  *   snapshot_parts / snapshot_save / snapshot_load      qwfn_engine.cpp:988-1053
  *   engine::reset                                       qwfn_engine.cpp:1055-1066
  *   saved-sequence pool of the server                   tools/qwfn_server.cpp:767-793, :1380-1424
+ *   block scores, top-k and cells of the decode QSA     qwfn_graph.cpp:556-581
  *   decode cell mask and padded cell list               qwfn_graph.cpp:668-675, :681-693
  *   causal masks of prefill chunks, steps, MTP drafts   qwfn_engine.cpp:1261-1271, :2093-2098, :3415-3440
  *   qsa_decode_prepare / _k, qsa_pool_rebuild (bias),
@@ -195,6 +196,25 @@ int     qwfn_snap_pool_restore_or_reset(qwfn_snap_pool * pool, qwfn_state * cons
                                         const int32_t * consumed, int32_t n_consumed, int32_t consumed_has_images,
                                         const int32_t * prompt, int32_t n_prompt, int32_t prompt_has_images,
                                         int32_t * n_restored, void * stream);
+
+/* ------------------------------------------------- sparse block selection */
+
+/* qsa_dec_cells (qwfn_graph.cpp:556-581) for T queries: for query t,
+ *   score[b] = sum_h relu(pool[b] . f16(q[t][h])) + bias[t][b]   (b < n_blocks)
+ *   top      = the k_blocks best blocks, best first            (ggml_top_k)
+ *   cells[t][j * ratio + m] = blk_cells[top[j] * ratio + m]
+ * pool: F16 [128] per block at pool_nb1 bytes (the pooled, normed, roped block
+ * keys of the layer's pool cache); q: F32 [128, n_heads] per query at q_nb2
+ * bytes (the roped indexer query, n_heads <= 8); bias: F32 [n_blocks] per query
+ * at bias_nb1 bytes; blk_cells: I32 [n_blocks * ratio]; top (optional): I32
+ * [T][k_blocks]. k_blocks <= min(n_blocks, 1024). Equal scores keep the lower
+ * block first. ws: at least qwfn_qsa_select_workspace_size(n_blocks, T) bytes
+ * of device memory (the scores). All pointers are device memory. */
+size_t qwfn_qsa_select_workspace_size(int64_t n_blocks, int32_t T);
+int qwfn_qsa_select_cells(const uint16_t * pool, size_t pool_nb1, int64_t n_blocks, const float * q, int32_t n_heads,
+                          size_t q_nb2, const float * bias, size_t bias_nb1, int32_t T, int32_t k_blocks,
+                          const int32_t * blk_cells, int32_t ratio, int32_t * cells, int32_t * top, void * ws,
+                          size_t ws_bytes, void * stream);
 
 /* ---------------------------------------------------------------- masks */
 

@@ -340,3 +340,26 @@ class SnapPool:
             L = max(L, l)
         have = any(len(t) == L and prompt[:L] == t for t, _, _ in self.saved)
         return L if (L >= 2048 and L + 16 < len(prompt) and L >= n_consumed + 2 and not have) else 0
+
+
+# ------------------------------------------------- sparse block selection
+
+def qsa_scores(pool_f16: np.ndarray, q: np.ndarray, bias: np.ndarray) -> np.ndarray:
+    """qsa_dec_cells' scores (qwfn_graph.cpp:570-576) for one query: ggml's F16
+    mul_mat rounds the F32 query to f16 and accumulates the products in f32
+    (here in f64, the order-free sum); relu; the sum over indexer heads; the bias."""
+    k = pool_f16.astype(np.float64)                       # [n_blocks, 128]
+    q16 = q.astype(np.float16).astype(np.float64)         # [n_heads, 128]
+    d = k @ q16.T                                         # [n_blocks, n_heads]
+    return np.maximum(d, 0.0).sum(axis=1) + bias.astype(np.float64)
+
+
+def qsa_top_k(score: np.ndarray, k: int) -> np.ndarray:
+    """ggml_top_k (qwfn_graph.cpp:577): the k best blocks, best first; equal
+    scores keep the lower block first (the order a stable descending sort gives)."""
+    return np.argsort(-score, kind="stable")[:k].astype(np.int32)
+
+
+def qsa_cells(top: np.ndarray, blk_cells: np.ndarray, ratio: int) -> np.ndarray:
+    """get_rows(blk_cells, top) reshaped to [k * ratio] (qwfn_graph.cpp:578-579)."""
+    return np.concatenate([blk_cells[b * ratio:(b + 1) * ratio] for b in top]).astype(np.int32)

@@ -80,6 +80,7 @@ EXPORTS = [
     "qwfn_snap_pool_create", "qwfn_snap_pool_destroy", "qwfn_snap_pool_count", "qwfn_snap_pool_bytes",
     "qwfn_snap_pool_entry", "qwfn_snap_pool_save", "qwfn_snap_pool_best", "qwfn_snap_pool_load",
     "qwfn_snap_pool_split", "qwfn_snap_pool_restore_or_reset",
+    "qwfn_qsa_select_workspace_size", "qwfn_qsa_select_cells",
 ]
 
 _lib = None
@@ -164,12 +165,16 @@ def load(path: str = LIB_PATH):
     L.qwfn_snap_pool_split.argtypes = [vp, PI, i32, i32, i32]
     L.qwfn_snap_pool_split.restype = i32
     L.qwfn_snap_pool_restore_or_reset.argtypes = [vp, PV, i32, PI, i32, i32, PI, i32, i32, PI, vp]
+    L.qwfn_qsa_select_workspace_size.argtypes = [i64, i32]
+    L.qwfn_qsa_select_workspace_size.restype = sz
+    L.qwfn_qsa_select_cells.argtypes = [vp, sz, i64, vp, i32, sz, vp, sz, i32, i32, vp, i32, vp, vp, vp, sz, vp]
     for name in EXPORTS:
         if name not in ("qwfn_state_config_default", "qwfn_state_destroy", "qwfn_snap_pool_destroy"):
             getattr(L, name).restype = getattr(L, name).restype or ctypes.c_int
     L.qwfn_last_error.restype = ctypes.c_char_p
     L.qwfn_fattn_workspace_size.restype = sz
     L.qwfn_fattn_workspace_size_seq.restype = sz
+    L.qwfn_qsa_select_workspace_size.restype = sz
     _lib = L
     return L
 

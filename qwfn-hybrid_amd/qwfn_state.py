@@ -339,3 +339,23 @@ class SnapPool:
                                                          int(consumed_has_images), P, n_p, int(prompt_has_images),
                                                          ctypes.byref(out), K._stream(stream)))
         return int(out.value)
+
+
+# ------------------------------------------------- sparse block selection
+
+def qsa_select_cells(pool, q, bias, k_blocks: int, blk_cells, ratio: int, cells, top=None, ws=None, stream=None):
+    """qsa_dec_cells for T queries. pool: f16 [n_blocks, 128] (CUDA, uint16 or float16);
+    q: f32 [T, n_heads, 128]; bias: f32 [T, n_blocks]; blk_cells: i32 [>= n_blocks * ratio];
+    cells: i32 [T, k_blocks * ratio]; top: optional i32 [T, k_blocks]."""
+    import torch
+    L = K.load()
+    n_blocks = pool.shape[0]
+    T = q.shape[0]
+    need = int(L.qwfn_qsa_select_workspace_size(n_blocks, T))
+    if ws is None:
+        ws = torch.empty(need, dtype=torch.uint8, device=pool.device)
+    K.check(L.qwfn_qsa_select_cells(pool.data_ptr(), pool.stride(0) * pool.element_size(), n_blocks, q.data_ptr(),
+                                    q.shape[1], q.stride(0) * 4, bias.data_ptr(), bias.stride(0) * 4, T, k_blocks,
+                                    blk_cells.data_ptr(), ratio, cells.data_ptr(),
+                                    top.data_ptr() if top is not None else None, ws.data_ptr(), ws.numel(),
+                                    K._stream(stream)))

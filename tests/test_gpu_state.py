@@ -402,3 +402,74 @@ def test_pool_restore_or_reset_round_trip(gpu):
     say("pool: restore the conversation")
     assert pool.restore_or_reset(states, side, conv + [1, 2]) == 3000
     _check(states, cfgs, data, 3000, "restored")
+
+
+# ------------------------------------------------- sparse block selection
+
+def _select(pool, q, bias, k, blk_cells, ratio):
+    import torch
+    T = q.shape[0]
+    pd = dev(pool.view(np.uint16))
+    qd, bd, cd = dev(q.astype(np.float32)), dev(bias.astype(np.float32)), dev(blk_cells.astype(np.int32))
+    cells = torch.full((T, k * ratio), -1, dtype=torch.int32, device="cuda")
+    top = torch.full((T, k), -1, dtype=torch.int32, device="cuda")
+    S.qsa_select_cells(pd, qd, bd, k, cd, ratio, cells, top)
+    return host(cells), host(top)
+
+
+def _bias(nb, n_past, ratio):
+    return SO.qsa_pool_rebuild_bias(nb, n_past, ratio)
+
+
+def test_qsa_select_closed_forms(gpu):
+    rng = np.random.default_rng(70)
+    nb, ratio, k = 768, 4, 513
+    blk_cells, _, _ = SO.qsa_tables(nb, ratio, 1, 0)
+    pool = rng.standard_normal((nb, 128)).astype(np.float16)
+    # a zero query: every relu term is 0, the score is the bias: the incomplete
+    # block of n_past (1e9) first, then the whole blocks lowest first
+    n_past = 4 * 600 + 1
+    b = _bias(nb, n_past, ratio)
+    say("qsa select: zero query")
+    cells, top = _select(pool, np.zeros((1, 4, 128), np.float32), b[None], k, blk_cells, ratio)
+    assert top[0][0] == 600 and list(top[0][1:]) == list(range(512))
+    assert list(cells[0][:4]) == [2400, 2401, 2402, 2403]
+    # planted scores: block j's key is j * e0 and the query e0: score j, best first
+    pool2 = np.zeros((nb, 128), np.float16)
+    pool2[:, 0] = np.arange(nb) / 64.0
+    q2 = np.zeros((2, 4, 128), np.float32)
+    q2[:, 0, 0] = 1.0
+    say("qsa select: planted scores, two queries")
+    _, top2 = _select(pool2, q2, np.zeros((2, nb), np.float32), k, blk_cells, ratio)
+    assert list(top2[0]) == list(range(nb - 1, nb - 1 - k, -1)) and list(top2[1]) == list(top2[0])
+    # relu: a query opposite to every key scores 0 everywhere, blocks in order
+    say("qsa select: relu")
+    _, top3 = _select(pool2, -q2[:1], np.zeros((1, nb), np.float32), 5, blk_cells, ratio)
+    assert list(top3[0]) == [0, 1, 2, 3, 4]
+
+
+@pytest.mark.parametrize("nb,k,T,n_past", [(768, 513, 1, 3000), (18432, 513, 3, 73000), (4096, 1, 2, 9000),
+                                           (1024, 1024, 1, 4095)])
+def test_qsa_select_matches_oracle(gpu, nb, k, T, n_past):
+    rng = np.random.default_rng(nb + k)
+    ratio = 4
+    blk_cells, _, _ = SO.qsa_tables(nb, ratio, 1, 0)
+    pool = (rng.standard_normal((nb, 128)) * 0.5).astype(np.float16)
+    q = rng.standard_normal((T, 4, 128)).astype(np.float32)
+    bias = np.stack([_bias(nb, n_past + t, ratio) for t in range(T)])
+    say(f"qsa select nb={nb} k={k} T={T}")
+    cells, top = _select(pool, q, bias, k, blk_cells, ratio)
+    for t in range(T):
+        sc = SO.qsa_scores(pool, q[t], bias[t])
+        want = SO.qsa_top_k(sc, k)
+        got = top[t]
+        # the same blocks, best first, except where scores tie within float
+        # rounding at the k-th place (a sum of 512 f32 products)
+        kth = sc[want[-1]]
+        tol = 1e-5 * max(1.0, abs(kth)) if np.isfinite(kth) else 0.0
+        sure = set(int(b) for b in want if sc[b] > kth + tol)
+        assert sure <= set(int(b) for b in got)
+        assert all(sc[b] >= kth - tol for b in got)
+        assert len(set(got.tolist())) == k
+        assert np.all(np.diff(sc[got]) <= tol + 1e-12 * np.abs(sc[got][1:]))   # best first
+        np.testing.assert_array_equal(cells[t], SO.qsa_cells(got, blk_cells, ratio))

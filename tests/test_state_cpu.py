@@ -386,3 +386,27 @@ def test_library_pool_validation():
         pool.save_seq(states, [1] * 10, stream=0)
     with pytest.raises(K.QwfnError, match="positions"):
         pool.restore_or_reset(states[:1], [1] * 9, [1] * 20, stream=0)
+
+
+def test_qsa_select_validation():
+    L = K.load()
+    FAKE = 0x7F0000000000
+
+    def err(rc, code, needle):
+        assert rc == code, (rc, L.qwfn_last_error())
+        assert needle in L.qwfn_last_error().decode()
+
+    ws = L.qwfn_qsa_select_workspace_size(768, 1)
+    assert ws == 768 * 4
+    call = lambda **kw: L.qwfn_qsa_select_cells(
+        kw.get("pool", FAKE), kw.get("pool_nb1", 256), kw.get("nb", 768), FAKE, kw.get("nh", 4), 2048, FAKE,
+        3072, kw.get("T", 1), kw.get("k", 513), FAKE, 4, FAKE, None, FAKE, kw.get("ws", ws), None)
+    err(call(pool=None), K.EINVAL, "NULL")
+    err(call(k=769), K.EINVAL, "k_blocks")
+    err(call(k=1025, nb=2000, ws=8000), K.EINVAL, "k_blocks")
+    err(call(nh=9), K.ENOTSUP, "heads")
+    err(call(pool_nb1=200), K.EALIGN, "16-byte")
+    err(call(ws=100), K.ENOMEM, "workspace")
+    # the oracle's tie rule on a closed form: equal scores keep the lower block first
+    sc = np.array([1.0, 3.0, 3.0, 2.0, 3.0])
+    assert list(SO.qsa_top_k(sc, 3)) == [1, 2, 4] and list(SO.qsa_top_k(sc, 4)) == [1, 2, 4, 3]
