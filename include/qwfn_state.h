@@ -205,11 +205,13 @@ int     qwfn_snap_pool_restore_or_reset(qwfn_snap_pool * pool, qwfn_state * cons
  *   cells[t][j * ratio + m] = blk_cells[top[j] * ratio + m]
  * pool: F16 [128] per block at pool_nb1 bytes (the pooled, normed, roped block
  * keys of the layer's pool cache); q: F32 [128, n_heads] per query at q_nb2
- * bytes (the roped indexer query, n_heads <= 8); bias: F32 [n_blocks] per query
- * at bias_nb1 bytes; blk_cells: I32 [n_blocks * ratio]; top (optional): I32
- * [T][k_blocks]. k_blocks <= min(n_blocks, 1024). Equal scores keep the lower
- * block first. ws: at least qwfn_qsa_select_workspace_size(n_blocks, T) bytes
- * of device memory (the scores). All pointers are device memory. */
+ * bytes, 16-byte aligned (the roped indexer query, n_heads <= 8); bias: F32
+ * [n_blocks] per query at bias_nb1 bytes; blk_cells: I32 [n_blocks * ratio],
+ * ratio <= 16; top (optional): I32
+ * [T][k_blocks]. k_blocks <= min(n_blocks, 1024), n_blocks <= 49152. Equal
+ * scores keep the lower block first. ws: at least
+ * qwfn_qsa_select_workspace_size(n_blocks, T) bytes of 16-byte aligned device
+ * memory (the scores). All pointers are device memory. */
 size_t qwfn_qsa_select_workspace_size(int64_t n_blocks, int32_t T);
 int qwfn_qsa_select_cells(const uint16_t * pool, size_t pool_nb1, int64_t n_blocks, const float * q, int32_t n_heads,
                           size_t q_nb2, const float * bias, size_t bias_nb1, int32_t T, int32_t k_blocks,

@@ -9,14 +9,14 @@
 // q16 is the query rounded to f16: ggml's mul_mat of an F16 matrix converts
 // its F32 operand to F16 before the dot products, which accumulate in f32.
 //
-// Two kernels. k_qsa_score spreads the pool cache (n_blocks x 128 f16, up to
-// 4.7 MB per query) over many workgroups: 16 lanes per block, 16 bytes of the
-// key each, 4 heads' partial dots reduced across the 16 lanes with DPP. The
-// scores land in a workspace. k_qsa_topk, one workgroup per query, finds the
-// k-th largest score by a radix select over order-preserving keys of the
-// float bits (histograms in LDS), gathers the blocks above it and as many
-// equal to it as needed, lowest block first, sorts those by score, best first
-// (ties: lower block first), and writes their cells.
+// Two kernels. k_qsa_score reads the pool cache (n_blocks x 128 f16, 4.7 MB
+// at 18432 blocks) once for up to 8 queries and computes the dot products on
+// the matrix cores, one wave per 16 blocks; the scores land in a workspace.
+// k_qsa_topk, one workgroup per query, holds the scores in registers, finds
+// the k-th largest by a radix select over order-preserving keys of the float
+// bits (histograms in LDS), keeps the blocks above it and as many equal to it
+// as needed, lowest block first, orders those by score, best first (ties:
+// lower block first), and writes their cells.
 #include "qwfn_common.h"
 #include "qwfn_state.h"
 
@@ -28,9 +28,16 @@ namespace {
 constexpr int IDX_DIM = 128;             // indexer key length (hparams::idx_key_len)
 constexpr int MAX_IDX_HEADS = 8;
 constexpr int SCORE_THREADS = 256;        // 16 blocks per workgroup pass
+constexpr int SCORE_T = 8;                // queries scored per pass over the pool
 constexpr int TOPK_THREADS = 1024;
 constexpr int TOPK_MAX = 1024;            // k_blocks per query, at most
+constexpr int TOPK_MAX_KPT = 48;          // scores per thread: n_blocks <= 49152
 constexpr int RADIX_BITS = 8;
+constexpr int RATIO_MAX = 16;             // cells per block, at most
+constexpr int SUBH_LD = 36;               // words per bin of the sub-histograms: 32 counts + 4, rows 16-byte aligned
+
+// scores of query t sit at score[t * ld + b]; ld is n_blocks rounded up to 64
+__host__ __device__ constexpr int64_t score_ld(int64_t n) { return (n + 63) / 64 * 64; }
 
 struct score_args {
     const uint16_t * pool;        // F16 [IDX_DIM] per block, block stride pool_nb1 bytes
@@ -39,50 +46,108 @@ struct score_args {
     const float *    q;           // F32 [IDX_DIM][n_heads] per query, query stride q_nb2 bytes
     size_t           q_nb2;
     int32_t          n_heads;
+    int32_t          head_bits;   // columns per query: 2^head_bits >= n_heads
+    int32_t          T;
     const float *    bias;        // F32 [n_blocks] per query, query stride bias_nb1 bytes
     size_t           bias_nb1;
-    float *          score;       // [T][n_blocks]
+    float *          score;       // [T][score_ld(n_blocks)]
 };
 
-__device__ __forceinline__ float h2f(uint16_t h) { return (float) __builtin_bit_cast(_Float16, h); }
+// sum over the 16 lanes of a DPP row, the same tree as butterflies over lane
+// masks 1, 2, 4, 8 (quad swaps, then half-row and row mirrors), so every lane
+// of the row holds the same sum
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
 
-// q16: the query rounded to f16 (the conversion of ggml's F16 mul_mat), then
-// back to f32 for the products.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t x) {
+    return (uint32_t) __builtin_amdgcn_update_dpp(0, (int) x, CTRL, ROW_MASK, 0xf, false);
+}
+
+// inclusive prefix sum over the 64 lanes of a wave: shifts within rows of 16,
+// then row 0's total into row 1, row 2's into row 3, lanes 0-31's into rows 2-3
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+    v += dpp_u<0x111>(v);          // row_shr:1
+    v += dpp_u<0x112>(v);          // row_shr:2
+    v += dpp_u<0x114>(v);          // row_shr:4
+    v += dpp_u<0x118>(v);          // row_shr:8
+    v += dpp_u<0x142, 0xa>(v);     // row_bcast:15, rows 1 and 3
+    v += dpp_u<0x143, 0xc>(v);     // row_bcast:31, rows 2 and 3
+    return v;
+}
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float    v4f __attribute__((ext_vector_type(4)));
+
+// Scores as a GEMM on the matrix cores: D[block][col] = pool[block] . q16[col]
+// with v_mfma_f32_16x16x32_f16, one wave per 16 blocks. The columns of a tile
+// are (query, head) pairs, 2^head_bits columns per query (heads past n_heads
+// are zero), so a query's heads are adjacent lanes of a DPP row. A (the keys)
+// comes from global memory straight into registers: lane (lg, ln) holds dims
+// [32 s + 8 lg, +8) of block ln for k-step s; B (the query heads, rounded to
+// f16) likewise for column ln. D: lane (lg, ln) holds blocks 4 lg + r of
+// column ln. relu, then the sum over a query's heads across its lanes; the
+// first lane of each query adds the bias and writes 4 scores. No LDS, no
+// barriers: a wave past the last block leaves at once.
 __global__ __launch_bounds__(SCORE_THREADS) void k_qsa_score(score_args a) {
-    __shared__ float qs[MAX_IDX_HEADS][IDX_DIM];
-    const int t = blockIdx.y;
-    const float * q = (const float *) ((const char *) a.q + (size_t) t * a.q_nb2);
-    for (int i = threadIdx.x; i < a.n_heads * IDX_DIM; i += SCORE_THREADS)
-        qs[i / IDX_DIM][i % IDX_DIM] = (float) (_Float16) q[i];   // round to nearest even
-    __syncthreads();
-    const int sub = threadIdx.x & 15;                  // 8 dims of the key
-    const int64_t step = (int64_t) gridDim.x * (SCORE_THREADS / 16);
-    for (int64_t b = (int64_t) blockIdx.x * (SCORE_THREADS / 16) + (threadIdx.x >> 4); b < a.n_blocks; b += step) {
-        const uint4 raw = *(const uint4 *) ((const char *) a.pool + (size_t) b * a.pool_nb1 + 16 * sub);
-        float k[8];
-        k[0] = h2f(raw.x & 0xffff); k[1] = h2f(raw.x >> 16); k[2] = h2f(raw.y & 0xffff); k[3] = h2f(raw.y >> 16);
-        k[4] = h2f(raw.z & 0xffff); k[5] = h2f(raw.z >> 16); k[6] = h2f(raw.w & 0xffff); k[7] = h2f(raw.w >> 16);
-        float s = 0.f;
-        for (int h = 0; h < a.n_heads; h++) {
-            float d = 0.f;
+    const int lane = threadIdx.x & 63;
+    const int ln = lane & 15, lg = lane >> 4;
+    const int64_t n = a.n_blocks;
+    const int64_t m0 = ((int64_t) blockIdx.x * (SCORE_THREADS / 64) + (threadIdx.x >> 6)) * 16;
+    if (m0 >= n) return;
+    const int t0 = blockIdx.y * SCORE_T;
+    const int nt = a.T - t0 < SCORE_T ? a.T - t0 : SCORE_T;
+    const int hb = a.head_bits, Hp = 1 << hb;
+    const int QT = 16 >> hb;                                      // queries per tile of 16 columns
+    const int n_tiles = (nt + QT - 1) / QT;
+    const int64_t blk = m0 + ln;
+    v8h kr[4];
 #pragma unroll
-            for (int i = 0; i < 8; i++) d = fmaf(k[i], qs[h][8 * sub + i], d);
-            // sum over the 16 lanes of the block: butterflies within 16-lane rows
-            d += __shfl_xor(d, 1, 16);
-            d += __shfl_xor(d, 2, 16);
-            d += __shfl_xor(d, 4, 16);
-            d += __shfl_xor(d, 8, 16);
-            s += d > 0.f ? d : 0.f;                   // relu, then the sum over heads
+    for (int st = 0; st < 4; st++) {
+        uint4 raw = make_uint4(0u, 0u, 0u, 0u);
+        if (blk < n) raw = *(const uint4 *) ((const char *) a.pool + (size_t) blk * a.pool_nb1 + (32 * st + 8 * lg) * 2);
+        kr[st] = __builtin_bit_cast(v8h, raw);
+    }
+    const int64_t ld = score_ld(n);
+    const int64_t ob = m0 + 4 * lg;                               // blocks ob .. ob + 3 of this lane's D rows
+    for (int tile = 0; tile < n_tiles; tile++) {
+        const int tl = tile * QT + (ln >> hb);                    // query of this lane's column
+        const int h = ln & (Hp - 1);
+        const bool colv = tl < nt && h < a.n_heads;
+        const bool writer = h == 0 && tl < nt;
+        const float * qp = (const float *) ((const char *) a.q + (size_t) (t0 + (tl < nt ? tl : 0)) * a.q_nb2)
+                           + h * IDX_DIM + 8 * lg;
+        v8h qb[4];
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            float4 x = make_float4(0.f, 0.f, 0.f, 0.f), y = x;
+            if (colv) { x = *(const float4 *) (qp + 32 * st); y = *(const float4 *) (qp + 32 * st + 4); }
+            qb[st] = v8h{(_Float16) x.x, (_Float16) x.y, (_Float16) x.z, (_Float16) x.w,
+                         (_Float16) y.x, (_Float16) y.y, (_Float16) y.z, (_Float16) y.w};   // round to nearest even
         }
-        if (sub == 0) {
-            const float bb = *(const float *) ((const char *) a.bias + (size_t) t * a.bias_nb1 + (size_t) b * 4);
-            a.score[(size_t) t * a.n_blocks + b] = s + bb;
+        float bias4[4];
+        const char * brow = (const char *) a.bias + (size_t) (t0 + (tl < nt ? tl : 0)) * a.bias_nb1;
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            bias4[r] = (writer && ob + r < n) ? *(const float *) (brow + (size_t) (ob + r) * 4) : 0.f;
+        v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int st = 0; st < 4; st++) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr[st], qb[st], acc, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float v = acc[r] > 0.f ? acc[r] : 0.f;                // relu per head
+            if (hb >= 1) v += dpp_f<0xB1>(v);                     // quad_perm 1,0,3,2
+            if (hb >= 2) v += dpp_f<0x4E>(v);                     // quad_perm 2,3,0,1
+            if (hb >= 3) v += dpp_f<0x141>(v);                    // row_half_mirror
+            if (writer && ob + r < n) a.score[(size_t) (t0 + tl) * ld + ob + r] = v + bias4[r];
         }
     }
 }
 
 struct topk_args {
-    const float *   score;        // [T][n_blocks]
+    const float *   score;        // [T][score_ld(n_blocks)]
     int64_t         n_blocks;
     int32_t         k;            // blocks kept
     const int32_t * blk_cells;    // [n_blocks_max * ratio]
@@ -98,109 +163,194 @@ __device__ __forceinline__ uint32_t okey(float f) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// exclusive prefix over the workgroup of (x, y), in thread order
+__device__ __forceinline__ void block_scan2(uint32_t x, uint32_t y, uint32_t & ex, uint32_t & ey, uint2 * wsum) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint32_t ix = wave_incl_scan(x), iy = wave_incl_scan(y);
+    if (lane == 63) wsum[w] = make_uint2(ix, iy);
+    __syncthreads();
+    uint32_t bx = 0, by = 0;
+#pragma unroll
+    for (int w2 = 0; w2 < TOPK_THREADS / 64; w2++) {
+        const uint2 t = wsum[w2];
+        if (w2 < w) { bx += t.x; by += t.y; }
+    }
+    ex = bx + ix - x;
+    ey = by + iy - y;
+}
+
+// One workgroup per query. Thread i holds scores [i * KPT, i * KPT + KPT) as
+// order-preserving keys in registers. A radix select (8-bit digits, most
+// significant first) finds the k-th largest key `kth` and how many keys equal
+// to it are kept (`keep`, the lowest blocks). Each pass counts digits into 32
+// sub-histograms, one per lane mod 32, whose rows are SUBH_LD words apart: lanes
+// with the same digit hit distinct banks, so clustered digits (the exponent
+// byte of similar scores) cost no serialised atomics. A pass whose boundary
+// bin is kept whole ends the select early. Keys above kth, then the kept equal
+// keys, are placed by an exclusive scan of per-thread counts (block order),
+// packed with their block as (key << 32 | ~block), so the larger packed value
+// comes first, and sorted: runs of 64 per wave, then merged by rank.
+template <int KPT>
 __global__ __launch_bounds__(TOPK_THREADS) void k_qsa_topk(topk_args a) {
+    __shared__ __align__(16) uint32_t sub_hist[(1 << RADIX_BITS) * SUBH_LD];
     __shared__ uint32_t hist[1 << RADIX_BITS];
-    __shared__ uint32_t sel_key[TOPK_MAX];
-    __shared__ int32_t  sel_idx[TOPK_MAX];
-    __shared__ uint32_t s_prefix, s_need, n_above, n_equal;
-    const int t = blockIdx.x;
-    const float * sc = a.score + (size_t) t * a.n_blocks;
+    __shared__ uint32_t s_digit, s_need, s_done;
+    __shared__ __align__(16) uint2 wsum[TOPK_THREADS / 64];
+    __shared__ __align__(16) uint64_t sel[TOPK_MAX];
+    __shared__ int32_t order[TOPK_MAX];
+    const int tid = threadIdx.x, lane = tid & 63;
     const int64_t n = a.n_blocks;
     const int k = a.k;
+    const int64_t base = (int64_t) tid * KPT;
+    const float * sc = a.score + (size_t) blockIdx.x * score_ld(n);
 
-    // radix select, most significant digit first: the k-th largest key
+    for (int i = tid; i < (1 << RADIX_BITS) * SUBH_LD / 4; i += TOPK_THREADS)
+        ((uint4 *) sub_hist)[i] = make_uint4(0u, 0u, 0u, 0u);
+    uint32_t key[KPT];
+#pragma unroll
+    for (int j = 0; j < KPT; j += 4) {
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (base + j < n) v = *(const float4 *) (sc + base + j);   // score_ld keeps the float4 inside the row
+        key[j] = okey(v.x); key[j + 1] = okey(v.y); key[j + 2] = okey(v.z); key[j + 3] = okey(v.w);
+    }
+    const int nv = base >= n ? 0 : (n - base < KPT ? (int) (n - base) : KPT);   // valid keys of this thread
+    __syncthreads();
+
     uint32_t prefix = 0, mask = 0, need = (uint32_t) k;
+    uint32_t kth = 0, keep = 0;
+#pragma unroll 1
     for (int shift = 32 - RADIX_BITS; shift >= 0; shift -= RADIX_BITS) {
-        for (int i = threadIdx.x; i < (1 << RADIX_BITS); i += TOPK_THREADS) hist[i] = 0;
+        uint32_t * mine = sub_hist + (lane & 31);
+#pragma unroll
+        for (int j = 0; j < KPT; j++)
+            if (j < nv && (key[j] & mask) == prefix)
+                atomicAdd(&mine[((key[j] >> shift) & ((1u << RADIX_BITS) - 1)) * SUBH_LD], 1u);
         __syncthreads();
-        for (int64_t i = threadIdx.x; i < n; i += TOPK_THREADS) {
-            const uint32_t key = okey(sc[i]);
-            if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & ((1u << RADIX_BITS) - 1)], 1u);
+        {
+            // 4 threads per bin sum its 32 counts and clear them for the next pass
+            const int bin = tid >> 2, qq = tid & 3;
+            uint4 * p = (uint4 *) (sub_hist + bin * SUBH_LD + qq * 8);
+            const uint4 x = p[0], y = p[1];
+            p[0] = make_uint4(0u, 0u, 0u, 0u);
+            p[1] = make_uint4(0u, 0u, 0u, 0u);
+            uint32_t c = x.x + x.y + x.z + x.w + y.x + y.y + y.z + y.w;
+            c += dpp_u<0xB1>(c);                          // quad_perm 1,0,3,2
+            c += dpp_u<0x4E>(c);                          // quad_perm 2,3,0,1
+            if (qq == 0) hist[bin] = c;
         }
         __syncthreads();
-        if (threadIdx.x == 0) {
-            uint32_t acc = 0;
-            int d = (1 << RADIX_BITS) - 1;
-            for (; d > 0; d--) {                       // from the largest digit down
-                if (acc + hist[d] >= need) break;
-                acc += hist[d];
-            }
-            s_prefix = prefix | ((uint32_t) d << shift);
-            s_need = need - acc;
-        }
-        __syncthreads();
-        prefix = s_prefix;
-        need = s_need;
-        mask |= ((1u << RADIX_BITS) - 1) << shift;
-        __syncthreads();
-    }
-    // prefix is the k-th largest key; `need` of the keys equal to it are kept
-    // (the lowest blocks), every key above it is kept
-    if (threadIdx.x == 0) { n_above = 0; n_equal = 0; }
-    __syncthreads();
-    const uint32_t kth = prefix;
-    const uint32_t keep_equal = need;
-    for (int64_t i0 = 0; i0 < n; i0 += TOPK_THREADS) {
-        const int64_t i = i0 + threadIdx.x;
-        const uint32_t key = i < n ? okey(sc[i]) : 0u;
-        if (i < n && key > kth) {
-            const uint32_t slot = atomicAdd(&n_above, 1u);
-            sel_key[slot] = key;
-            sel_idx[slot] = (int32_t) i;
-        }
-        // equal keys in block order: a ballot per wave, waves in order
-        const bool eq = i < n && key == kth;
-        const unsigned long long bal = __ballot(eq);
-        __shared__ uint32_t wave_eq[TOPK_THREADS / 64];
-        const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-        if (lane == 0) wave_eq[w] = (uint32_t) __popcll(bal);
-        __syncthreads();
-        uint32_t before = n_equal;
-        for (int w2 = 0; w2 < w; w2++) before += wave_eq[w2];
-        const uint32_t rank = before + (uint32_t) __popcll(bal & ((1ull << lane) - 1ull));
-        if (eq && rank < keep_equal) {
-            const uint32_t slot = (uint32_t) k - keep_equal + rank;   // after the keys above
-            sel_key[slot] = key;
-            sel_idx[slot] = (int32_t) i;
-        }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            uint32_t tot = 0;
-            for (int w2 = 0; w2 < TOPK_THREADS / 64; w2++) tot += wave_eq[w2];
-            n_equal += tot;
-        }
-        __syncthreads();
-    }
-    // sort the k kept blocks by key, best first, lower block first on ties
-    // (bitonic over the next power of two; padding sorts last)
-    int np = 1;
-    while (np < k) np <<= 1;
-    for (int i = k + threadIdx.x; i < np; i += TOPK_THREADS) { sel_key[i] = 0u; sel_idx[i] = 0x7fffffff; }
-    __syncthreads();
-    for (int size = 2; size <= np; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int i = threadIdx.x; i < np; i += TOPK_THREADS) {
-                const int j = i ^ stride;
-                if (j > i) {
-                    const bool desc = (i & size) == 0;
-                    const uint32_t ki = sel_key[i], kj = sel_key[j];
-                    const int32_t ii = sel_idx[i], ij = sel_idx[j];
-                    // "i before j" in the final order: larger key, then lower block
-                    const bool i_first = ki > kj || (ki == kj && ii < ij);
-                    if (desc ? !i_first : i_first) {
-                        sel_key[i] = kj; sel_key[j] = ki;
-                        sel_idx[i] = ij; sel_idx[j] = ii;
+        if (tid < 64) {
+            // lane l holds bins 255-4l down to 252-4l; s = keys in bins >= 252-4l
+            const int top = 255 - 4 * lane;
+            const uint32_t c3 = hist[top], c2 = hist[top - 1], c1 = hist[top - 2], c0 = hist[top - 3];
+            const uint32_t tot = c0 + c1 + c2 + c3;
+            const uint32_t s = wave_incl_scan(tot);
+            const uint32_t above = s - tot;           // keys in bins above this lane's
+            if (above < need && need <= s) {          // the one lane whose bins hold the need-th key
+                uint32_t acc = above, d, cd;
+                if (acc + c3 >= need) { d = 3; cd = c3; }
+                else {
+                    acc += c3;
+                    if (acc + c2 >= need) { d = 2; cd = c2; }
+                    else {
+                        acc += c2;
+                        if (acc + c1 >= need) { d = 1; cd = c1; }
+                        else { acc += c1; d = 0; cd = c0; }
                     }
                 }
+                s_digit = (uint32_t) (top - 3) + d;
+                s_need = need - acc;
+                s_done = (need - acc == cd) ? 1u : 0u;   // the whole bin is kept
             }
-            __syncthreads();
+        }
+        __syncthreads();
+        prefix |= s_digit << shift;
+        need = s_need;
+        mask |= ((1u << RADIX_BITS) - 1) << shift;
+        if (s_done) {
+            // keep every key >= prefix (the bin's keys have prefix's top bits and
+            // any low bits): the keys above prefix - 1, and none equal to it;
+            // valid keys are never 0, so prefix 0 keeps them all
+            kth = prefix ? prefix - 1 : 0u;
+            keep = 0;
+            break;
+        }
+        kth = prefix;
+        keep = need;
+    }
+    uint32_t na = 0, ne = 0;
+#pragma unroll
+    for (int j = 0; j < KPT; j++) {
+        na += (j < nv && key[j] > kth) ? 1u : 0u;
+        ne += (j < nv && key[j] == kth) ? 1u : 0u;
+    }
+    uint32_t pa, pe;
+    block_scan2(na, ne, pa, pe, wsum);
+    const uint32_t first_equal = (uint32_t) k - keep;        // the keys above take the slots before
+#pragma unroll
+    for (int j = 0; j < KPT; j++) {
+        const uint64_t packed = ((uint64_t) key[j] << 32) | (uint32_t) ~(uint32_t) (base + j);
+        if (j < nv && key[j] > kth) {
+            if (pa < first_equal) sel[pa] = packed;
+            pa++;
+        } else if (j < nv && key[j] == kth) {
+            if (pe < keep && first_equal + pe < (uint32_t) k) sel[first_equal + pe] = packed;
+            pe++;
         }
     }
-    for (int j = threadIdx.x; j < k; j += TOPK_THREADS) {
-        const int32_t blk = sel_idx[j];
-        if (a.top) a.top[(size_t) t * k + j] = blk;
-        for (int m = 0; m < a.ratio; m++)
-            a.cells[((size_t) t * k + j) * a.ratio + m] = a.blk_cells[(size_t) blk * a.ratio + m];
+    // order: every wave sorts a run of 64 values in registers (bitonic over
+    // lane swaps, best first); then each value's place is its index in its
+    // run plus, for every other run, the number of values above it there
+    // (a binary search). Padding (0) sorts last and is never placed.
+    const int kpad = (k + 63) & ~63;
+    const int n_runs = kpad >> 6;
+    for (int j = k + tid; j < kpad; j += TOPK_THREADS) sel[j] = 0;
+    __syncthreads();
+    const int wv = tid >> 6;
+    if (wv < n_runs) {                                            // wave-uniform
+        uint64_t x = sel[tid];
+#pragma unroll
+        for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+            for (int d = size >> 1; d > 0; d >>= 1) {
+                const uint32_t ylo = (uint32_t) __shfl_xor((int) (uint32_t) x, d);
+                const uint32_t yhi = (uint32_t) __shfl_xor((int) (uint32_t) (x >> 32), d);
+                const uint64_t y = ((uint64_t) yhi << 32) | ylo;
+                const bool take_max = ((lane & d) == 0) == ((lane & size) == 0);
+                x = take_max ? (x > y ? x : y) : (x < y ? x : y);
+            }
+        }
+        sel[tid] = x;
+    }
+    __syncthreads();
+    if (wv < n_runs) {
+        const uint64_t v = sel[tid];
+        uint32_t rank = (uint32_t) lane;
+        for (int r = 0; r < n_runs; r++) {
+            if (r == wv) continue;
+            const uint64_t * run = sel + 64 * r;
+            int pos = 0;
+#pragma unroll
+            for (int step = 32; step >= 1; step >>= 1)
+                if (run[pos + step - 1] > v) pos += step;
+            pos += run[pos] > v ? 1 : 0;                          // pos <= 63 here: all 64 above
+            rank += (uint32_t) pos;
+        }
+        if (v != 0 && rank < (uint32_t) k) order[rank] = (int32_t) ~(uint32_t) v;
+    }
+    __syncthreads();
+    if (tid < k) {
+        const int32_t ix = order[tid];
+        const size_t o = (size_t) blockIdx.x * k + tid;
+        const bool ok = ix >= 0 && ix < n;                      // always, for distinct ranks; never read outside blk_cells
+        // all of the block's cells are loaded before any is stored (cells may alias blk_cells)
+        int32_t c[RATIO_MAX];
+#pragma unroll
+        for (int m = 0; m < RATIO_MAX; m++) c[m] = (ok && m < a.ratio) ? a.blk_cells[(size_t) ix * a.ratio + m] : -1;
+        if (a.top) a.top[o] = ok ? ix : -1;
+#pragma unroll
+        for (int m = 0; m < RATIO_MAX; m++)
+            if (m < a.ratio) a.cells[o * a.ratio + m] = c[m];
     }
 }
 
@@ -210,7 +360,7 @@ __global__ __launch_bounds__(TOPK_THREADS) void k_qsa_topk(topk_args a) {
 using namespace qwfn;
 
 extern "C" size_t qwfn_qsa_select_workspace_size(int64_t n_blocks, int32_t T) {
-    return (size_t) std::max<int64_t>(1, n_blocks) * (size_t) std::max(1, T) * sizeof(float);
+    return (size_t) score_ld(std::max<int64_t>(1, n_blocks)) * (size_t) std::max(1, T) * sizeof(float);
 }
 
 extern "C" int qwfn_qsa_select_cells(const uint16_t * pool, size_t pool_nb1, int64_t n_blocks, const float * q,
@@ -219,23 +369,32 @@ extern "C" int qwfn_qsa_select_cells(const uint16_t * pool, size_t pool_nb1, int
                                      int32_t * top, void * ws, size_t ws_bytes, void * stream) {
     if (!pool || !q || !bias || !blk_cells || !cells) return set_error(QWFN_EINVAL, "qsa_select_cells: NULL pointer");
     if (n_blocks < 1 || T < 1 || ratio < 1) return set_error(QWFN_EINVAL, "qsa_select_cells: empty input");
+    if (ratio > RATIO_MAX) return set_error(QWFN_ENOTSUP, "qsa_select_cells: at most 16 cells per block");
     if (n_heads < 1 || n_heads > MAX_IDX_HEADS) return set_error(QWFN_ENOTSUP, "qsa_select_cells: 1 to 8 indexer heads");
     if (k_blocks < 1 || k_blocks > n_blocks || k_blocks > TOPK_MAX)
         return set_error(QWFN_EINVAL, "qsa_select_cells: need 1 <= k_blocks <= min(n_blocks, 1024)");
     if (pool_nb1 < IDX_DIM * 2 || pool_nb1 % 16 || !is_aligned(pool, 16))
         return set_error(QWFN_EALIGN, "qsa_select_cells: pooled keys must be 128 f16 at a 16-byte aligned stride");
-    if (q_nb2 < (size_t) n_heads * IDX_DIM * 4 || !is_aligned(q, 4) || q_nb2 % 4 || bias_nb1 % 4 || !is_aligned(bias, 4))
+    if (q_nb2 < (size_t) n_heads * IDX_DIM * 4 || !is_aligned(q, 16) || q_nb2 % 16 || bias_nb1 % 4 || !is_aligned(bias, 4))
         return set_error(QWFN_EALIGN, "qsa_select_cells: q [128, n_heads] f32 per query, f32 bias");
-    if (!ws || ws_bytes < qwfn_qsa_select_workspace_size(n_blocks, T) || !is_aligned(ws, 4))
+    if (!ws || ws_bytes < qwfn_qsa_select_workspace_size(n_blocks, T))
         return set_error(QWFN_ENOMEM, "qsa_select_cells: workspace too small");
+    if (!is_aligned(ws, 16)) return set_error(QWFN_EALIGN, "qsa_select_cells: workspace must be 16-byte aligned");
+    if (n_blocks > (int64_t) TOPK_THREADS * TOPK_MAX_KPT)
+        return set_error(QWFN_ENOTSUP, "qsa_select_cells: at most 49152 blocks");
     if (n_blocks * ratio > INT32_MAX) return set_error(QWFN_ERANGE, "qsa_select_cells: too many cells");
     hipStream_t st = as_stream(stream);
-    score_args sa{pool, pool_nb1, n_blocks, q, q_nb2, n_heads, bias, bias_nb1, (float *) ws};
-    const int64_t per = SCORE_THREADS / 16;
-    const unsigned gx = (unsigned) std::max<int64_t>(1, std::min<int64_t>((n_blocks + per - 1) / per, 1024));
-    hipLaunchKernelGGL(k_qsa_score, dim3(gx, (unsigned) T), dim3(SCORE_THREADS), 0, st, sa);
+    int head_bits = 0;
+    while ((1 << head_bits) < n_heads) head_bits++;
+    score_args sa{pool, pool_nb1, n_blocks, q, q_nb2, n_heads, head_bits, T, bias, bias_nb1, (float *) ws};
+    const int64_t per = SCORE_THREADS / 64 * 16;                 // blocks per workgroup: 16 per wave
+    const unsigned gx = (unsigned) ((n_blocks + per - 1) / per);
+    hipLaunchKernelGGL(k_qsa_score, dim3(gx, (unsigned) ((T + SCORE_T - 1) / SCORE_T)), dim3(SCORE_THREADS), 0, st, sa);
     if (int rc = hip_check(hipGetLastError(), "qsa score launch")) return rc;
     topk_args ta{(const float *) ws, n_blocks, k_blocks, blk_cells, ratio, cells, top};
-    hipLaunchKernelGGL(k_qsa_topk, dim3((unsigned) T), dim3(TOPK_THREADS), 0, st, ta);
+    const int64_t kpt = (n_blocks + TOPK_THREADS - 1) / TOPK_THREADS;
+    auto topk = kpt <= 8 ? k_qsa_topk<8> : kpt <= 16 ? k_qsa_topk<16> : kpt <= 24 ? k_qsa_topk<24>
+              : kpt <= 32 ? k_qsa_topk<32> : k_qsa_topk<48>;
+    hipLaunchKernelGGL(topk, dim3((unsigned) T), dim3(TOPK_THREADS), 0, st, ta);
     return hip_check(hipGetLastError(), "qsa top-k launch");
 }
