@@ -203,7 +203,8 @@ def measure_state_rows(K, torch, np, dev, gbs) -> dict:
     csel = torch.empty((3, kb * 4), dtype=torch.int32, device=dev)
     wsel = torch.empty(K.load().qwfn_qsa_select_workspace_size(nb, 3), dtype=torch.uint8, device=dev)
     us_sel = timed_graph(torch, lambda k: S.qsa_select_cells(pool, qsel, bsel, kb, bcells, 4, csel, ws=wsel), 8, 10)
-    sel_bytes = nb * 128 * 2 * 3 + 3 * nb * 4 * 2 + 3 * kb * 4 * 4
+    # compulsory bytes: the pool once, the bias rows, the cells written
+    sel_bytes = nb * 128 * 2 + 3 * nb * 4 + 3 * kb * 4 * 4
     rows["qsa_select_cells"] = {"us_per_call": round(us_sel, 2), "blocks": nb, "k_blocks": kb, "queries": 3,
                                 "bytes": sel_bytes, "GBs": gbs(sel_bytes, us_sel), "frac": frac(sel_bytes, us_sel)}
     del pool, qsel, bsel, bcells, csel, wsel

@@ -399,14 +399,59 @@ def test_qsa_select_validation():
     ws = L.qwfn_qsa_select_workspace_size(768, 1)
     assert ws == 768 * 4
     call = lambda **kw: L.qwfn_qsa_select_cells(
-        kw.get("pool", FAKE), kw.get("pool_nb1", 256), kw.get("nb", 768), FAKE, kw.get("nh", 4), 2048, FAKE,
-        3072, kw.get("T", 1), kw.get("k", 513), FAKE, 4, FAKE, None, FAKE, kw.get("ws", ws), None)
+        kw.get("pool", FAKE), kw.get("pool_nb1", 256), kw.get("nb", 768), kw.get("q", FAKE), kw.get("nh", 4), 2048,
+        FAKE, 3072, kw.get("T", 1), kw.get("k", 513), FAKE, kw.get("ratio", 4), FAKE, None, FAKE, kw.get("ws", ws), None)
     err(call(pool=None), K.EINVAL, "NULL")
     err(call(k=769), K.EINVAL, "k_blocks")
     err(call(k=1025, nb=2000, ws=8000), K.EINVAL, "k_blocks")
     err(call(nh=9), K.ENOTSUP, "heads")
     err(call(pool_nb1=200), K.EALIGN, "16-byte")
     err(call(ws=100), K.ENOMEM, "workspace")
+    err(call(ratio=17), K.ENOTSUP, "16 cells")
+    err(call(nb=49153, ws=L.qwfn_qsa_select_workspace_size(49153, 1)), K.ENOTSUP, "49152")
+    err(call(q=FAKE + 4), K.EALIGN, "q [128")
+    # scores of query t sit at rows of n_blocks rounded up to 64 floats
+    assert L.qwfn_qsa_select_workspace_size(1000, 3) == 1024 * 3 * 4
     # the oracle's tie rule on a closed form: equal scores keep the lower block first
     sc = np.array([1.0, 3.0, 3.0, 2.0, 3.0])
     assert list(SO.qsa_top_k(sc, 3)) == [1, 2, 4] and list(SO.qsa_top_k(sc, 4)) == [1, 2, 4, 3]
+
+
+def test_oracle_qsa_selection_pins():
+    """The selection oracle against closed forms and a brute force over tiny inputs."""
+    rng = np.random.default_rng(11)
+    nb, H = 40, 3
+    pool = rng.standard_normal((nb, 128)).astype(np.float16)
+    bias = rng.standard_normal(nb).astype(np.float32)
+    # a zero query: every head's dot product is 0, relu keeps 0: the score is the bias
+    np.testing.assert_array_equal(SO.qsa_scores(pool, np.zeros((H, 128), np.float32), bias), bias.astype(np.float64))
+    # planted keys: block j holds j/8 in dim 5; a query 1 in dim 5 of head 0 and -1 in
+    # head 1 scores j/8 (head 1 is clipped by relu)
+    planted = np.zeros((nb, 128), np.float16)
+    planted[:, 5] = np.arange(nb) / 8.0
+    q = np.zeros((H, 128), np.float32)
+    q[0, 5], q[1, 5] = 1.0, -1.0
+    np.testing.assert_array_equal(SO.qsa_scores(planted, q, np.zeros(nb, np.float32)), np.arange(nb) / 8.0)
+    # the query is rounded to f16 before the products: 1 + 2^-12 is 1.0 in f16
+    q[0, 5] = 1.0 + 2.0 ** -12
+    np.testing.assert_array_equal(SO.qsa_scores(planted, q, np.zeros(nb, np.float32)), np.arange(nb) / 8.0)
+    # brute force: explicit loops over blocks, heads and dims
+    qr = rng.standard_normal((H, 128)).astype(np.float32)
+    got = SO.qsa_scores(pool, qr, bias)
+    for b in range(0, nb, 7):
+        tot = 0.0
+        for h in range(H):
+            d = 0.0
+            for i in range(128):
+                d += float(pool[b, i]) * float(np.float16(qr[h, i]))
+            tot += d if d > 0.0 else 0.0
+        assert abs(got[b] - (tot + float(bias[b]))) <= 1e-9 * max(1.0, abs(tot))
+    # top-k: a brute-force selection by (score descending, block ascending)
+    sc = np.round(rng.standard_normal(64) * 2.0) / 2.0            # many ties
+    for k in (1, 7, 33, 64):
+        want = sorted(range(64), key=lambda b: (-sc[b], b))[:k]
+        assert list(SO.qsa_top_k(sc, k)) == want
+    # cells: the table of a 1-sequence layout maps block b to cells b*ratio .. b*ratio+ratio-1
+    blk_cells, _, _ = SO.qsa_tables(16, 4, 1, 0)
+    top = np.array([5, 0, 15], np.int32)
+    assert list(SO.qsa_cells(top, blk_cells, 4)) == [20, 21, 22, 23, 0, 1, 2, 3, 60, 61, 62, 63]
