@@ -448,16 +448,17 @@ def test_qsa_select_closed_forms(gpu):
     assert list(top3[0]) == [0, 1, 2, 3, 4]
 
 
-@pytest.mark.parametrize("nb,k,T,n_past", [(768, 513, 1, 3000), (18432, 513, 3, 73000), (4096, 1, 2, 9000),
-                                           (1024, 1024, 1, 4095)])
-def test_qsa_select_matches_oracle(gpu, nb, k, T, n_past):
+@pytest.mark.parametrize("nb,k,T,n_past,H", [(768, 513, 1, 3000, 4), (18432, 513, 3, 73000, 4), (4096, 1, 2, 9000, 4),
+                                             (1024, 1024, 1, 4095, 4), (777, 776, 1, 3100, 1), (1000, 100, 9, 3000, 3),
+                                             (5000, 300, 2, 19000, 8), (4100, 64, 12, 16000, 2)])
+def test_qsa_select_matches_oracle(gpu, nb, k, T, n_past, H):
     rng = np.random.default_rng(nb + k)
     ratio = 4
     blk_cells, _, _ = SO.qsa_tables(nb, ratio, 1, 0)
     pool = (rng.standard_normal((nb, 128)) * 0.5).astype(np.float16)
-    q = rng.standard_normal((T, 4, 128)).astype(np.float32)
+    q = rng.standard_normal((T, H, 128)).astype(np.float32)
     bias = np.stack([_bias(nb, n_past + t, ratio) for t in range(T)])
-    say(f"qsa select nb={nb} k={k} T={T}")
+    say(f"qsa select nb={nb} k={k} T={T} heads={H}")
     cells, top = _select(pool, q, bias, k, blk_cells, ratio)
     for t in range(T):
         sc = SO.qsa_scores(pool, q[t], bias[t])
