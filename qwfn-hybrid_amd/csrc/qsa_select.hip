@@ -393,8 +393,10 @@ extern "C" int qwfn_qsa_select_cells(const uint16_t * pool, size_t pool_nb1, int
     if (int rc = hip_check(hipGetLastError(), "qsa score launch")) return rc;
     topk_args ta{(const float *) ws, n_blocks, k_blocks, blk_cells, ratio, cells, top};
     const int64_t kpt = (n_blocks + TOPK_THREADS - 1) / TOPK_THREADS;
-    auto topk = kpt <= 8 ? k_qsa_topk<8> : kpt <= 16 ? k_qsa_topk<16> : kpt <= 24 ? k_qsa_topk<24>
-              : kpt <= 32 ? k_qsa_topk<32> : k_qsa_topk<48>;
+    // the smallest multiple of 4 that holds n_blocks / 1024 (18432 blocks: 20)
+    auto topk = kpt <= 8 ? k_qsa_topk<8> : kpt <= 12 ? k_qsa_topk<12> : kpt <= 16 ? k_qsa_topk<16>
+              : kpt <= 20 ? k_qsa_topk<20> : kpt <= 24 ? k_qsa_topk<24> : kpt <= 32 ? k_qsa_topk<32>
+              : kpt <= 40 ? k_qsa_topk<40> : k_qsa_topk<48>;
     hipLaunchKernelGGL(topk, dim3((unsigned) T), dim3(TOPK_THREADS), 0, st, ta);
     return hip_check(hipGetLastError(), "qsa top-k launch");
 }

@@ -450,7 +450,11 @@ def test_qsa_select_closed_forms(gpu):
 
 @pytest.mark.parametrize("nb,k,T,n_past,H", [(768, 513, 1, 3000, 4), (18432, 513, 3, 73000, 4), (4096, 1, 2, 9000, 4),
                                              (1024, 1024, 1, 4095, 4), (777, 776, 1, 3100, 1), (1000, 100, 9, 3000, 3),
-                                             (5000, 300, 2, 19000, 8), (4100, 64, 12, 16000, 2)])
+                                             (5000, 300, 2, 19000, 8), (4100, 64, 12, 16000, 2),
+                                             # scores per thread 12, 16, 24, 32, 40, 48
+                                             (10000, 200, 1, 40000, 4), (16000, 513, 2, 64000, 4),
+                                             (24000, 513, 1, 96000, 4), (30000, 513, 1, 120000, 4),
+                                             (36000, 700, 1, 144000, 4), (45000, 1000, 1, 180000, 4)])
 def test_qsa_select_matches_oracle(gpu, nb, k, T, n_past, H):
     rng = np.random.default_rng(nb + k)
     ratio = 4
