@@ -351,6 +351,20 @@ def qsa_select_cells(pool, q, bias, k_blocks: int, blk_cells, ratio: int, cells,
     L = K.load()
     n_blocks = pool.shape[0]
     T = q.shape[0]
+    # the C ABI takes rows at a stride with contiguous elements; the sizes it cannot see are checked here
+    if pool.dim() != 2 or pool.shape[1] != 128 or pool.stride(1) != 1 or pool.element_size() != 2:
+        raise ValueError("qsa_select_cells: pool must be [n_blocks, 128] f16 rows")
+    if q.dim() != 3 or q.dtype != torch.float32 or q.shape[2] != 128 or q.stride(2) != 1 or q.stride(1) != 128:
+        raise ValueError("qsa_select_cells: q must be f32 [T, n_heads, 128] with contiguous heads")
+    if bias.dim() != 2 or bias.dtype != torch.float32 or bias.shape[0] != T or bias.shape[1] < n_blocks \
+            or bias.stride(1) != 1:
+        raise ValueError("qsa_select_cells: bias must be f32 [T, >= n_blocks] rows")
+    if blk_cells.dtype != torch.int32 or not blk_cells.is_contiguous() or blk_cells.numel() < n_blocks * ratio:
+        raise ValueError("qsa_select_cells: blk_cells must be contiguous i32 with n_blocks * ratio entries")
+    if cells.dtype != torch.int32 or not cells.is_contiguous() or cells.numel() < T * k_blocks * ratio:
+        raise ValueError("qsa_select_cells: cells must be contiguous i32 [T, k_blocks * ratio]")
+    if top is not None and (top.dtype != torch.int32 or not top.is_contiguous() or top.numel() < T * k_blocks):
+        raise ValueError("qsa_select_cells: top must be contiguous i32 [T, k_blocks]")
     need = int(L.qwfn_qsa_select_workspace_size(n_blocks, T))
     if ws is None:
         ws = torch.empty(need, dtype=torch.uint8, device=pool.device)

@@ -455,3 +455,22 @@ def test_oracle_qsa_selection_pins():
     blk_cells, _, _ = SO.qsa_tables(16, 4, 1, 0)
     top = np.array([5, 0, 15], np.int32)
     assert list(SO.qsa_cells(top, blk_cells, 4)) == [20, 21, 22, 23, 0, 1, 2, 3, 60, 61, 62, 63]
+
+
+def test_qsa_select_wrapper_checks_shapes():
+    """The Python wrapper refuses tensors whose sizes the C ABI cannot see (CPU tensors: no call is made)."""
+    import torch
+    nb, k, T, ratio = 64, 8, 2, 4
+    pool = torch.zeros((nb, 128), dtype=torch.float16)
+    q = torch.zeros((T, 4, 128), dtype=torch.float32)
+    bias = torch.zeros((T, nb), dtype=torch.float32)
+    blk = torch.zeros(nb * ratio, dtype=torch.int32)
+    cells = torch.zeros((T, k * ratio), dtype=torch.int32)
+    bad = [dict(blk_cells=blk[: nb * ratio - 1]), dict(cells=cells[:, :-1].contiguous()),
+           dict(q=q.transpose(1, 2).contiguous().transpose(1, 2)), dict(bias=bias.double()),
+           dict(pool=pool[:, :64]), dict(top=torch.zeros((T, k - 1), dtype=torch.int32))]
+    for kw in bad:
+        args = dict(pool=pool, q=q, bias=bias, k_blocks=k, blk_cells=blk, ratio=ratio, cells=cells, stream=0)
+        args.update(kw)
+        with pytest.raises(ValueError):
+            S.qsa_select_cells(**args)
