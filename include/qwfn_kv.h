@@ -142,16 +142,27 @@ int qwfn_kv_gather_segments(const void * src, size_t src_row_stride, int64_t src
  * `variant`, scores are sum_b d_k*d_q*isum_b, masked (-inf) keys are skipped,
  * softmax is online, V is dequantised q*d. A fully masked row gives 0.
  * ws: device workspace of at least qwfn_fattn_workspace_size(q, k, v, mask)
- * bytes, or NULL to use a library-owned buffer (allocated on first use, not
- * graph-capturable). The workspace holds the split partials when the keys
- * are split across workgroups (at least 256 bytes are asked for otherwise);
- * its contents need not be preserved between calls. Calls that run at the
- * same time need distinct workspaces. */
+ * bytes, or NULL to use a library-owned buffer: one per device, allocated on
+ * first use and regrown (after a device synchronisation) when a call needs
+ * more. ws == NULL returns QWFN_EINVAL while `stream` is being captured into
+ * a graph, and every ws == NULL call on a device shares that one buffer, so
+ * such calls must not overlap (serialise them on one stream). The workspace
+ * holds the split partials when the keys are split across workgroups (at
+ * least 256 bytes are asked for otherwise); its contents need not be
+ * preserved between calls. Calls that run at the same time need distinct
+ * workspaces. */
 size_t qwfn_fattn_workspace_size(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
                                  const qwfn_tensor * mask);
 int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
                              const qwfn_tensor * mask, float scale, float max_bias, float logit_softcap,
                              const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes, void * stream);
+
+/* Force the key-split count of later attention calls in this process (any
+ * thread; 0 returns to the planner's choice, values are capped at 1024). For
+ * split-invariance tests and tuning sweeps; the results do not depend on it
+ * beyond float rounding. No counterpart in the reference (ggml picks its own
+ * partition). */
+void qwfn_fattn_force_splits(int32_t n_splits);
 
 /* Batched decode over sequences of different depths: as
  * qwfn_flash_attn_ext_q8_0, except that sequence b (q batch index) attends

@@ -45,6 +45,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <atomic>
 #include <cstdlib>
 #include <type_traits>
 
@@ -1152,10 +1153,9 @@ __global__ __launch_bounds__(256) void k_fattn_merge(fa_args a) {
 
 // Attention kernel shapes: waves per block, query tiles, keys per wave.
 enum fa_kind {
-    FA_W8_T1,     // 8 waves, one 16-row tile, 128-key chunks, one block per CU
-    FA_W8_T2,     // 8 waves, two tiles sharing each 64-key chunk, one block per CU
     FA_P4_T1,     // 4 waves, one tile, 64-key chunks, two blocks per CU
-    FA_P4_T2,     // 4 waves, two tiles, 32 keys per wave, two blocks per CU (no MASK_TILE)
+    FA_P4_T2,     // 4 waves, two tiles, 32 keys per wave, two blocks per CU; mask tiles of
+                  // more than MASK_ROWS_PAIR rows go to 8 waves over the same 64-key chunks
 };
 
 struct fa_plan {
@@ -1170,10 +1170,9 @@ struct fa_plan {
     int64_t r_n_kv[RAGGED_MAX_B];
 };
 
-int env_int(const char * name, int dflt) {
-    const char * s = std::getenv(name);
-    return s && *s ? std::atoi(s) : dflt;
-}
+// A forced key-split count for later calls (0: the planner's choice); set by
+// qwfn_fattn_force_splits, read once per call.
+std::atomic<int32_t> g_force_splits{0};
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
@@ -1197,8 +1196,7 @@ uint32_t recip32(int64_t d) {
 // kernel that spills to scratch would break that count: refuse to run one.
 int check_no_scratch() {
     static const int rc = [] {
-        for (const void * f : {(const void *) k_fattn_q8_0<1, false, WAVES, 16, false>, (const void *) k_fattn_q8_0<2, false, WAVES, 16, false>,
-                               (const void *) k_fattn_q8_0<1, true, WAVES, 16, false>, (const void *) k_fattn_q8_0<2, true, WAVES, 16, false>,
+        for (const void * f : {(const void *) k_fattn_q8_0<2, true, WAVES, 16, false>,
                                (const void *) k_fattn_q8_0<1, false, WAVES_PAIR, 16, false>,
                                (const void *) k_fattn_q8_0<1, true, WAVES_PAIR, 16, false>,
                                (const void *) k_fattn_q8_0<2, false, WAVES_PAIR, 32, false>,
@@ -1267,33 +1265,27 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
         if (mask_slice_bytes(*mask) >= (size_t(1) << 31))
             return set_error(QWFN_ENOTSUP, "flash_attn_ext: mask batch slices must be below 2 GiB");
     }
-    // Query rows per block: one or two 16-row tiles.
-    int rw = R > 16 ? 32 : 16;
-    if (const int force = env_int("QWFN_FA_ROWS", 0)) rw = force >= 32 ? 32 : 16;
-    // 4-wave blocks, two per CU (their prologues and phases overlap), or
-    // 8-wave blocks, one per CU. QWFN_FA_PAIR=0 forces 8 waves.
+    // Query rows per block: one or two 16-row tiles, in 4-wave blocks, two per
+    // CU (their prologues and phases overlap).
+    const int rw = R > 16 ? 32 : 16;
     const int64_t B = q->ne[3];
-    const bool pair = seq_n_kv || env_int("QWFN_FA_PAIR", 1) != 0;   // per-sequence splits: 4-wave kernels
-    pl->kind = rw == 16 ? (pair ? FA_P4_T1 : FA_W8_T1) : (pair ? FA_P4_T2 : FA_W8_T2);
+    pl->kind = rw == 16 ? FA_P4_T1 : FA_P4_T2;
     pl->R = (int32_t) R;
     pl->rw = rw;
     pl->RT = rw / 16;
     pl->n_rg = (int32_t) ((R + rw - 1) / rw);
     pl->gqa = (int32_t) gqa;
-    const int64_t ck = pl->kind == FA_W8_T1 ? fa_cfg<1, false, WAVES, 16>::CK
-                     : pl->kind == FA_W8_T2 ? fa_cfg<2, false, WAVES, 16>::CK
-                     : pl->kind == FA_P4_T1 ? fa_cfg<1, false, WAVES_PAIR, 16>::CK
-                                            : fa_cfg<2, false, WAVES_PAIR, 32>::CK;
-    // Splits: about one block per CU slot (256 or 512), each at least one chunk.
-    const int64_t target_blocks = env_int("QWFN_FA_BLOCKS", pl->kind == FA_P4_T1 || pl->kind == FA_P4_T2 ? 512 : 256);
+    const int64_t ck = pl->kind == FA_P4_T1 ? fa_cfg<1, false, WAVES_PAIR, 16>::CK : fa_cfg<2, false, WAVES_PAIR, 32>::CK;
+    // Splits: about one block per CU slot (512), each at least one chunk.
+    const int64_t target_blocks = 512;
     int64_t ns = std::max<int64_t>(1, target_blocks / std::max<int64_t>(1, nh_kv * B * pl->n_rg));
     ns = std::min<int64_t>(ns, std::max<int64_t>(1, (n_kv + ck - 1) / ck));
-    if (const int force = env_int("QWFN_FA_SPLITS", 0)) ns = force;
+    if (const int32_t force = g_force_splits.load(std::memory_order_relaxed)) ns = force;
     // Splits are whole chunks. When the keys exceed two or more chunks per
     // split by less than one chunk (n_kv = 2^k + T), the last split takes the
     // rest; otherwise every split rounds up and there are fewer.
     int64_t split_len = n_kv / (ns * ck) * ck;
-    if (split_len < 2 * ck || n_kv - ns * split_len >= ck || !env_int("QWFN_FA_ABSORB", 1)) {
+    if (split_len < 2 * ck || n_kv - ns * split_len >= ck) {
         split_len = (n_kv + ns - 1) / ns;
         split_len = std::max<int64_t>(ck, (split_len + ck - 1) / ck * ck);
         ns = std::max<int64_t>(1, (n_kv + split_len - 1) / split_len);
@@ -1358,9 +1350,11 @@ using namespace qwfn;
 
 extern "C" size_t qwfn_fattn_workspace_size(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
                                             const qwfn_tensor * mask) {
-    fa_plan pl{};
-    if (plan_fattn(q, k, v, mask, &pl)) return 0;
-    return pl.ws_bytes;
+    return ::qwfn::abi_value<size_t>("fattn_workspace_size", 0, [&]() -> size_t {
+        fa_plan pl{};
+        if (plan_fattn(q, k, v, mask, &pl)) return 0;
+        return pl.ws_bytes;
+    });
 }
 
 namespace {
@@ -1424,7 +1418,7 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
     if (ws) {
         if (ws_bytes < pl.ws_bytes) return set_error(QWFN_ENOMEM, "flash_attn_ext: workspace too small");
         if (!is_aligned(ws, 256)) return set_error(QWFN_EALIGN, "flash_attn_ext: workspace must be 256-byte aligned");
-    } else if (int rc = library_workspace(pl.ws_bytes, &ws)) {
+    } else if (int rc = library_workspace(pl.ws_bytes, as_stream(stream), &ws)) {
         return rc;
     }
     if (int rc = check_no_scratch()) return rc;
@@ -1448,7 +1442,6 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
         a.m_gran = pl.max_span / 8 + 1;
         a.m_gran_mul = recip32(a.m_gran);
         a.mask_mode = mrows * 16 * a.m_gran <= mlds ? MASK_SPLIT : MASK_TILE;
-        if (env_int("QWFN_FA_MASK_TILE", 0)) a.mask_mode = MASK_TILE;
     } else {
         a.mask = nullptr; a.m_ne2 = 1; a.m_ne3 = 1; a.m_slice = 0; a.mask_mode = MASK_NONE;
     }
@@ -1518,14 +1511,6 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
             else if (mt) hipLaunchKernelGGL((k_fattn_q8_0<2, true, WAVES_PAIR, 32, false>), g, b4, 0, st, a);
             else    hipLaunchKernelGGL((k_fattn_q8_0<2, false, WAVES_PAIR, 32, false>), g, b4, 0, st, a);
             break;
-        case FA_W8_T1:
-            if (mt) hipLaunchKernelGGL((k_fattn_q8_0<1, true, WAVES, 16, false>), g, b8, 0, st, a);
-            else    hipLaunchKernelGGL((k_fattn_q8_0<1, false, WAVES, 16, false>), g, b8, 0, st, a);
-            break;
-        case FA_W8_T2:
-            if (mt) hipLaunchKernelGGL((k_fattn_q8_0<2, true, WAVES, 16, false>), g, b8, 0, st, a);
-            else    hipLaunchKernelGGL((k_fattn_q8_0<2, false, WAVES, 16, false>), g, b8, 0, st, a);
-            break;
     }
     }
     if (int rc = hip_check(hipGetLastError(), "flash_attn launch")) return rc;
@@ -1545,22 +1530,28 @@ extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor
                                         const qwfn_tensor * mask, float scale, float max_bias, float logit_softcap,
                                         const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes,
                                         void * stream) {
-    return fattn_run(q, k, v, mask, scale, max_bias, logit_softcap, dst, variant, ws, ws_bytes, stream, nullptr);
+    return ::qwfn::abi_call("flash_attn_ext_q8_0", [&]() -> int {
+        return fattn_run(q, k, v, mask, scale, max_bias, logit_softcap, dst, variant, ws, ws_bytes, stream, nullptr);
+    });
 }
 
 extern "C" size_t qwfn_fattn_workspace_size_seq(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
                                                 const qwfn_tensor * mask, const int64_t * seq_n_kv) {
-    fa_plan pl{};
-    if (!seq_n_kv || plan_fattn(q, k, v, mask, &pl, seq_n_kv)) return 0;
-    return pl.ws_bytes;
+    return ::qwfn::abi_value<size_t>("fattn_workspace_size_seq", 0, [&]() -> size_t {
+        fa_plan pl{};
+        if (!seq_n_kv || plan_fattn(q, k, v, mask, &pl, seq_n_kv)) return 0;
+        return pl.ws_bytes;
+    });
 }
 
 extern "C" int qwfn_flash_attn_ext_q8_0_seq(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
                                             const qwfn_tensor * mask, float scale, float max_bias, float logit_softcap,
                                             const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes,
                                             const int64_t * seq_n_kv, void * stream) {
-    if (!seq_n_kv) return set_error(QWFN_EINVAL, "flash_attn_ext_seq: seq_n_kv is NULL");
-    return fattn_run(q, k, v, mask, scale, max_bias, logit_softcap, dst, variant, ws, ws_bytes, stream, nullptr, seq_n_kv);
+    return ::qwfn::abi_call("flash_attn_ext_q8_0_seq", [&]() -> int {
+        if (!seq_n_kv) return set_error(QWFN_EINVAL, "flash_attn_ext_seq: seq_n_kv is NULL");
+        return fattn_run(q, k, v, mask, scale, max_bias, logit_softcap, dst, variant, ws, ws_bytes, stream, nullptr, seq_n_kv);
+    });
 }
 
 extern "C" int qwfn_flash_attn_ext_q8_0_append(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
@@ -1568,6 +1559,12 @@ extern "C" int qwfn_flash_attn_ext_q8_0_append(const qwfn_tensor * q, const qwfn
                                                const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes,
                                                const qwfn_tensor * src_k, const qwfn_tensor * src_v, int64_t first_row,
                                                void * stream) {
-    const fa_append app{src_k, src_v, first_row};
-    return fattn_run(q, k, v, mask, scale, max_bias, logit_softcap, dst, variant, ws, ws_bytes, stream, &app);
+    return ::qwfn::abi_call("flash_attn_ext_q8_0_append", [&]() -> int {
+        const fa_append app{src_k, src_v, first_row};
+        return fattn_run(q, k, v, mask, scale, max_bias, logit_softcap, dst, variant, ws, ws_bytes, stream, &app);
+    });
+}
+
+extern "C" void qwfn_fattn_force_splits(int32_t n_splits) {
+    g_force_splits.store(n_splits > 0 ? std::min<int32_t>(n_splits, MAX_SPLITS) : 0, std::memory_order_relaxed);
 }

@@ -182,41 +182,49 @@ using namespace qwfn;
 
 extern "C" int qwfn_set_rows_q8_0(const qwfn_tensor * dst, const qwfn_tensor * src, const qwfn_tensor * idx,
                                   int variant, void * stream) {
-    append_args a;
-    bool vec4;
-    if (int rc = set_rows_args(dst, src, idx, variant, &a, &vec4)) return rc;
-    if (int rc = status_word(&a.status)) return rc;
-    return launch_append(a, vec4, as_stream(stream));
+    return ::qwfn::abi_call("set_rows_q8_0", [&]() -> int {
+        append_args a;
+        bool vec4;
+        if (int rc = set_rows_args(dst, src, idx, variant, &a, &vec4)) return rc;
+        if (int rc = status_word(&a.status)) return rc;
+        return launch_append(a, vec4, as_stream(stream));
+    });
 }
 
 extern "C" int qwfn_cpy_f32_q8_0(const qwfn_tensor * src, const qwfn_tensor * dst, int variant, void * stream) {
-    append_args a;
-    bool vec4;
-    if (int rc = cpy_args(src, dst, variant, &a, &vec4)) return rc;
-    if (int rc = status_word(&a.status)) return rc;
-    return launch_append(a, vec4, as_stream(stream));
+    return ::qwfn::abi_call("cpy_f32_q8_0", [&]() -> int {
+        append_args a;
+        bool vec4;
+        if (int rc = cpy_args(src, dst, variant, &a, &vec4)) return rc;
+        if (int rc = status_word(&a.status)) return rc;
+        return launch_append(a, vec4, as_stream(stream));
+    });
 }
 
 extern "C" int qwfn_set_rows_q8_0_kv(const qwfn_tensor * dst_k, const qwfn_tensor * src_k, const qwfn_tensor * dst_v,
                                      const qwfn_tensor * src_v, const qwfn_tensor * idx, int variant, void * stream) {
-    append_args k, v;
-    bool vk, vv;
-    if (int rc = set_rows_args(dst_k, src_k, idx, variant, &k, &vk)) return rc;
-    if (int rc = set_rows_args(dst_v, src_v, idx, variant, &v, &vv)) return rc;
-    if (int rc = same_shape(src_k, src_v, "set_rows_kv")) return rc;
-    if (int rc = status_word(&k.status)) return rc;
-    v.status = k.status;
-    return launch_append_kv(k, v, vk && vv, as_stream(stream));
+    return ::qwfn::abi_call("set_rows_q8_0_kv", [&]() -> int {
+        append_args k, v;
+        bool vk, vv;
+        if (int rc = set_rows_args(dst_k, src_k, idx, variant, &k, &vk)) return rc;
+        if (int rc = set_rows_args(dst_v, src_v, idx, variant, &v, &vv)) return rc;
+        if (int rc = same_shape(src_k, src_v, "set_rows_kv")) return rc;
+        if (int rc = status_word(&k.status)) return rc;
+        v.status = k.status;
+        return launch_append_kv(k, v, vk && vv, as_stream(stream));
+    });
 }
 
 extern "C" int qwfn_cpy_f32_q8_0_kv(const qwfn_tensor * src_k, const qwfn_tensor * dst_k, const qwfn_tensor * src_v,
                                     const qwfn_tensor * dst_v, int variant, void * stream) {
-    append_args k, v;
-    bool vk, vv;
-    if (int rc = cpy_args(src_k, dst_k, variant, &k, &vk)) return rc;
-    if (int rc = cpy_args(src_v, dst_v, variant, &v, &vv)) return rc;
-    if (int rc = same_shape(src_k, src_v, "cpy_kv")) return rc;
-    if (int rc = status_word(&k.status)) return rc;
-    v.status = k.status;
-    return launch_append_kv(k, v, vk && vv, as_stream(stream));
+    return ::qwfn::abi_call("cpy_f32_q8_0_kv", [&]() -> int {
+        append_args k, v;
+        bool vk, vv;
+        if (int rc = cpy_args(src_k, dst_k, variant, &k, &vk)) return rc;
+        if (int rc = cpy_args(src_v, dst_v, variant, &v, &vv)) return rc;
+        if (int rc = same_shape(src_k, src_v, "cpy_kv")) return rc;
+        if (int rc = status_word(&k.status)) return rc;
+        v.status = k.status;
+        return launch_append_kv(k, v, vk && vv, as_stream(stream));
+    });
 }

@@ -204,75 +204,81 @@ using namespace qwfn;
 
 extern "C" int qwfn_get_rows_i32(const qwfn_tensor * src, const qwfn_tensor * idx, const qwfn_tensor * dst,
                                  void * stream) {
-    if (!src || !idx || !dst || !src->data || !idx->data || !dst->data)
-        return set_error(QWFN_EINVAL, "get_rows: NULL tensor");
-    if (src->type != QWFN_TYPE_I32 || idx->type != QWFN_TYPE_I32 || dst->type != QWFN_TYPE_I32)
-        return set_error(QWFN_EINVAL, "get_rows: src, idx and dst must be i32");
-    if (src->nb[0] != 4 || dst->nb[0] != 4 || idx->nb[0] != 4)
-        return set_error(QWFN_EINVAL, "get_rows: rows must be contiguous words");
-    if (src->ne[2] != 1 || src->ne[3] != 1 || idx->ne[1] != 1 || idx->ne[2] != 1 || idx->ne[3] != 1 ||
-        dst->ne[2] != 1 || dst->ne[3] != 1)
-        return set_error(QWFN_ENOTSUP, "get_rows: only 2-D src/dst and 1-D idx are supported");
-    if (dst->ne[0] != src->ne[0] || dst->ne[1] != idx->ne[0])
-        return set_error(QWFN_EINVAL, "get_rows: dst must be [src ne[0], idx ne[0]]");
-    if (!is_aligned(src->data, 4) || !is_aligned(dst->data, 4) || !is_aligned(idx->data, 4) ||
-        src->nb[1] % 4 || dst->nb[1] % 4)
-        return set_error(QWFN_EALIGN, "get_rows: 4-byte alignment required");
-    uint32_t * st = nullptr;
-    if (int rc = status_word(&st)) return rc;
-    gather_args a{};
-    a.src = (const char *) src->data; a.src_row_stride = src->nb[1]; a.src_rows = src->ne[1];
-    a.seg_off = 0; a.seg_stride = 0;
-    a.idx = (const int32_t *) idx->data; a.n_idx = idx->ne[0];
-    a.dst = (char *) dst->data; a.dst_row_stride = dst->nb[1]; a.dst_seg_stride = 0;
-    a.n_seg = 1; a.status = st;
-    return launch_gather(a, (size_t) src->ne[0] * 4, as_stream(stream));
+    return ::qwfn::abi_call("get_rows_i32", [&]() -> int {
+        if (!src || !idx || !dst || !src->data || !idx->data || !dst->data)
+            return set_error(QWFN_EINVAL, "get_rows: NULL tensor");
+        if (src->type != QWFN_TYPE_I32 || idx->type != QWFN_TYPE_I32 || dst->type != QWFN_TYPE_I32)
+            return set_error(QWFN_EINVAL, "get_rows: src, idx and dst must be i32");
+        if (src->nb[0] != 4 || dst->nb[0] != 4 || idx->nb[0] != 4)
+            return set_error(QWFN_EINVAL, "get_rows: rows must be contiguous words");
+        if (src->ne[2] != 1 || src->ne[3] != 1 || idx->ne[1] != 1 || idx->ne[2] != 1 || idx->ne[3] != 1 ||
+            dst->ne[2] != 1 || dst->ne[3] != 1)
+            return set_error(QWFN_ENOTSUP, "get_rows: only 2-D src/dst and 1-D idx are supported");
+        if (dst->ne[0] != src->ne[0] || dst->ne[1] != idx->ne[0])
+            return set_error(QWFN_EINVAL, "get_rows: dst must be [src ne[0], idx ne[0]]");
+        if (!is_aligned(src->data, 4) || !is_aligned(dst->data, 4) || !is_aligned(idx->data, 4) ||
+            src->nb[1] % 4 || dst->nb[1] % 4)
+            return set_error(QWFN_EALIGN, "get_rows: 4-byte alignment required");
+        uint32_t * st = nullptr;
+        if (int rc = status_word(&st)) return rc;
+        gather_args a{};
+        a.src = (const char *) src->data; a.src_row_stride = src->nb[1]; a.src_rows = src->ne[1];
+        a.seg_off = 0; a.seg_stride = 0;
+        a.idx = (const int32_t *) idx->data; a.n_idx = idx->ne[0];
+        a.dst = (char *) dst->data; a.dst_row_stride = dst->nb[1]; a.dst_seg_stride = 0;
+        a.n_seg = 1; a.status = st;
+        return launch_gather(a, (size_t) src->ne[0] * 4, as_stream(stream));
+    });
 }
 
 extern "C" int qwfn_kv_gather_segments(const void * src, size_t src_row_stride, int64_t src_rows,
                                        size_t seg_off, size_t seg_stride, size_t seg_bytes, int32_t n_seg,
                                        const int32_t * idx, int64_t n_idx,
                                        void * dst, size_t dst_row_stride, size_t dst_seg_stride, void * stream) {
-    if (!src || !idx || !dst) return set_error(QWFN_EINVAL, "gather_segments: NULL pointer");
-    if (n_seg < 1 || n_idx < 0 || src_rows < 0 || seg_bytes == 0)
-        return set_error(QWFN_EINVAL, "gather_segments: empty or negative sizes");
-    if (seg_bytes % 4 || seg_off % 4 || seg_stride % 4 || src_row_stride % 4 || dst_row_stride % 4 ||
-        dst_seg_stride % 4 || !is_aligned(src, 4) || !is_aligned(dst, 4) || !is_aligned(idx, 4))
-        return set_error(QWFN_EALIGN, "gather_segments: sizes, offsets and strides must be multiples of 4");
-    if (seg_off + (size_t) (n_seg - 1) * seg_stride + seg_bytes > src_row_stride)
-        return set_error(QWFN_ERANGE, "gather_segments: segments extend past the source row");
-    if (dst_row_stride < seg_bytes) return set_error(QWFN_EINVAL, "gather_segments: dst rows overlap");
-    uint32_t * st = nullptr;
-    if (int rc = status_word(&st)) return rc;
-    gather_args a{};
-    a.src = (const char *) src; a.src_row_stride = src_row_stride; a.src_rows = src_rows;
-    a.seg_off = seg_off; a.seg_stride = seg_stride;
-    a.idx = idx; a.n_idx = n_idx;
-    a.dst = (char *) dst; a.dst_row_stride = dst_row_stride; a.dst_seg_stride = dst_seg_stride;
-    a.n_seg = n_seg; a.status = st;
-    return launch_gather(a, seg_bytes, as_stream(stream));
+    return ::qwfn::abi_call("kv_gather_segments", [&]() -> int {
+        if (!src || !idx || !dst) return set_error(QWFN_EINVAL, "gather_segments: NULL pointer");
+        if (n_seg < 1 || n_idx < 0 || src_rows < 0 || seg_bytes == 0)
+            return set_error(QWFN_EINVAL, "gather_segments: empty or negative sizes");
+        if (seg_bytes % 4 || seg_off % 4 || seg_stride % 4 || src_row_stride % 4 || dst_row_stride % 4 ||
+            dst_seg_stride % 4 || !is_aligned(src, 4) || !is_aligned(dst, 4) || !is_aligned(idx, 4))
+            return set_error(QWFN_EALIGN, "gather_segments: sizes, offsets and strides must be multiples of 4");
+        if (seg_off + (size_t) (n_seg - 1) * seg_stride + seg_bytes > src_row_stride)
+            return set_error(QWFN_ERANGE, "gather_segments: segments extend past the source row");
+        if (dst_row_stride < seg_bytes) return set_error(QWFN_EINVAL, "gather_segments: dst rows overlap");
+        uint32_t * st = nullptr;
+        if (int rc = status_word(&st)) return rc;
+        gather_args a{};
+        a.src = (const char *) src; a.src_row_stride = src_row_stride; a.src_rows = src_rows;
+        a.seg_off = seg_off; a.seg_stride = seg_stride;
+        a.idx = idx; a.n_idx = n_idx;
+        a.dst = (char *) dst; a.dst_row_stride = dst_row_stride; a.dst_seg_stride = dst_seg_stride;
+        a.n_seg = n_seg; a.status = st;
+        return launch_gather(a, seg_bytes, as_stream(stream));
+    });
 }
 
 extern "C" int qwfn_state_restore(const void * const * src, const size_t * bytes, void * const * dst,
                                   int32_t n_parts, int32_t n_slots, int32_t src_kind, void * stream) {
-    if (!src || !bytes || !dst) return set_error(QWFN_EINVAL, "state_restore: NULL array");
-    if (n_parts < 0 || n_slots < 1) return set_error(QWFN_EINVAL, "state_restore: need n_parts >= 0 and n_slots >= 1");
-    if (src_kind != QWFN_SRC_DEVICE && src_kind != QWFN_SRC_HOST)
-        return set_error(QWFN_EINVAL, "state_restore: unknown source kind");
-    for (int p = 0; p < n_parts; p++) {
-        if (bytes[p] && !src[p]) return set_error(QWFN_EINVAL, "state_restore: NULL source part " + std::to_string(p));
-        for (int s = 0; s < n_slots; s++)
-            if (bytes[p] && !dst[(size_t) s * n_parts + p])
-                return set_error(QWFN_EINVAL, "state_restore: NULL destination part " + std::to_string(p));
-    }
-    hipStream_t st = as_stream(stream);
-    const char * const * s8 = reinterpret_cast<const char * const *>(src);
-    char * const * d8 = reinterpret_cast<char * const *>(dst);
-    if (src_kind == QWFN_SRC_DEVICE) return restore_device(s8, bytes, d8, n_parts, n_slots, 0, st);
-    for (int p = 0; p < n_parts; p++)
-        if (bytes[p]) QWFN_HIP_TRY(hipMemcpyAsync(d8[p], s8[p], bytes[p], hipMemcpyHostToDevice, st));
-    if (n_slots == 1) return QWFN_OK;
-    // Broadcast slot 0 (now on the device) into slots 1..n_slots-1.
-    std::vector<const char *> s0(d8, d8 + n_parts);
-    return restore_device(s0.data(), bytes, d8, n_parts, n_slots - 1, 1, st);
+    return ::qwfn::abi_call("state_restore", [&]() -> int {
+        if (!src || !bytes || !dst) return set_error(QWFN_EINVAL, "state_restore: NULL array");
+        if (n_parts < 0 || n_slots < 1) return set_error(QWFN_EINVAL, "state_restore: need n_parts >= 0 and n_slots >= 1");
+        if (src_kind != QWFN_SRC_DEVICE && src_kind != QWFN_SRC_HOST)
+            return set_error(QWFN_EINVAL, "state_restore: unknown source kind");
+        for (int p = 0; p < n_parts; p++) {
+            if (bytes[p] && !src[p]) return set_error(QWFN_EINVAL, "state_restore: NULL source part " + std::to_string(p));
+            for (int s = 0; s < n_slots; s++)
+                if (bytes[p] && !dst[(size_t) s * n_parts + p])
+                    return set_error(QWFN_EINVAL, "state_restore: NULL destination part " + std::to_string(p));
+        }
+        hipStream_t st = as_stream(stream);
+        const char * const * s8 = reinterpret_cast<const char * const *>(src);
+        char * const * d8 = reinterpret_cast<char * const *>(dst);
+        if (src_kind == QWFN_SRC_DEVICE) return restore_device(s8, bytes, d8, n_parts, n_slots, 0, st);
+        for (int p = 0; p < n_parts; p++)
+            if (bytes[p]) QWFN_HIP_TRY(hipMemcpyAsync(d8[p], s8[p], bytes[p], hipMemcpyHostToDevice, st));
+        if (n_slots == 1) return QWFN_OK;
+        // Broadcast slot 0 (now on the device) into slots 1..n_slots-1.
+        std::vector<const char *> s0(d8, d8 + n_parts);
+        return restore_device(s0.data(), bytes, d8, n_parts, n_slots - 1, 1, st);
+    });
 }

@@ -360,43 +360,47 @@ __global__ __launch_bounds__(TOPK_THREADS) void k_qsa_topk(topk_args a) {
 using namespace qwfn;
 
 extern "C" size_t qwfn_qsa_select_workspace_size(int64_t n_blocks, int32_t T) {
-    return (size_t) score_ld(std::max<int64_t>(1, n_blocks)) * (size_t) std::max(1, T) * sizeof(float);
+    return ::qwfn::abi_value<size_t>("qsa_select_workspace_size", 0, [&]() -> size_t {
+        return (size_t) score_ld(std::max<int64_t>(1, n_blocks)) * (size_t) std::max(1, T) * sizeof(float);
+    });
 }
 
 extern "C" int qwfn_qsa_select_cells(const uint16_t * pool, size_t pool_nb1, int64_t n_blocks, const float * q,
                                      int32_t n_heads, size_t q_nb2, const float * bias, size_t bias_nb1, int32_t T,
                                      int32_t k_blocks, const int32_t * blk_cells, int32_t ratio, int32_t * cells,
                                      int32_t * top, void * ws, size_t ws_bytes, void * stream) {
-    if (!pool || !q || !bias || !blk_cells || !cells) return set_error(QWFN_EINVAL, "qsa_select_cells: NULL pointer");
-    if (n_blocks < 1 || T < 1 || ratio < 1) return set_error(QWFN_EINVAL, "qsa_select_cells: empty input");
-    if (ratio > RATIO_MAX) return set_error(QWFN_ENOTSUP, "qsa_select_cells: at most 16 cells per block");
-    if (n_heads < 1 || n_heads > MAX_IDX_HEADS) return set_error(QWFN_ENOTSUP, "qsa_select_cells: 1 to 8 indexer heads");
-    if (k_blocks < 1 || k_blocks > n_blocks || k_blocks > TOPK_MAX)
-        return set_error(QWFN_EINVAL, "qsa_select_cells: need 1 <= k_blocks <= min(n_blocks, 1024)");
-    if (pool_nb1 < IDX_DIM * 2 || pool_nb1 % 16 || !is_aligned(pool, 16))
-        return set_error(QWFN_EALIGN, "qsa_select_cells: pooled keys must be 128 f16 at a 16-byte aligned stride");
-    if (q_nb2 < (size_t) n_heads * IDX_DIM * 4 || !is_aligned(q, 16) || q_nb2 % 16 || bias_nb1 % 4 || !is_aligned(bias, 4))
-        return set_error(QWFN_EALIGN, "qsa_select_cells: q [128, n_heads] f32 per query, f32 bias");
-    if (!ws || ws_bytes < qwfn_qsa_select_workspace_size(n_blocks, T))
-        return set_error(QWFN_ENOMEM, "qsa_select_cells: workspace too small");
-    if (!is_aligned(ws, 16)) return set_error(QWFN_EALIGN, "qsa_select_cells: workspace must be 16-byte aligned");
-    if (n_blocks > (int64_t) TOPK_THREADS * TOPK_MAX_KPT)
-        return set_error(QWFN_ENOTSUP, "qsa_select_cells: at most 49152 blocks");
-    if (n_blocks * ratio > INT32_MAX) return set_error(QWFN_ERANGE, "qsa_select_cells: too many cells");
-    hipStream_t st = as_stream(stream);
-    int head_bits = 0;
-    while ((1 << head_bits) < n_heads) head_bits++;
-    score_args sa{pool, pool_nb1, n_blocks, q, q_nb2, n_heads, head_bits, T, bias, bias_nb1, (float *) ws};
-    const int64_t per = SCORE_THREADS / 64 * 16;                 // blocks per workgroup: 16 per wave
-    const unsigned gx = (unsigned) ((n_blocks + per - 1) / per);
-    hipLaunchKernelGGL(k_qsa_score, dim3(gx, (unsigned) ((T + SCORE_T - 1) / SCORE_T)), dim3(SCORE_THREADS), 0, st, sa);
-    if (int rc = hip_check(hipGetLastError(), "qsa score launch")) return rc;
-    topk_args ta{(const float *) ws, n_blocks, k_blocks, blk_cells, ratio, cells, top};
-    const int64_t kpt = (n_blocks + TOPK_THREADS - 1) / TOPK_THREADS;
-    // the smallest multiple of 4 that holds n_blocks / 1024 (18432 blocks: 20)
-    auto topk = kpt <= 8 ? k_qsa_topk<8> : kpt <= 12 ? k_qsa_topk<12> : kpt <= 16 ? k_qsa_topk<16>
-              : kpt <= 20 ? k_qsa_topk<20> : kpt <= 24 ? k_qsa_topk<24> : kpt <= 32 ? k_qsa_topk<32>
-              : kpt <= 40 ? k_qsa_topk<40> : k_qsa_topk<48>;
-    hipLaunchKernelGGL(topk, dim3((unsigned) T), dim3(TOPK_THREADS), 0, st, ta);
-    return hip_check(hipGetLastError(), "qsa top-k launch");
+    return ::qwfn::abi_call("qsa_select_cells", [&]() -> int {
+        if (!pool || !q || !bias || !blk_cells || !cells) return set_error(QWFN_EINVAL, "qsa_select_cells: NULL pointer");
+        if (n_blocks < 1 || T < 1 || ratio < 1) return set_error(QWFN_EINVAL, "qsa_select_cells: empty input");
+        if (ratio > RATIO_MAX) return set_error(QWFN_ENOTSUP, "qsa_select_cells: at most 16 cells per block");
+        if (n_heads < 1 || n_heads > MAX_IDX_HEADS) return set_error(QWFN_ENOTSUP, "qsa_select_cells: 1 to 8 indexer heads");
+        if (k_blocks < 1 || k_blocks > n_blocks || k_blocks > TOPK_MAX)
+            return set_error(QWFN_EINVAL, "qsa_select_cells: need 1 <= k_blocks <= min(n_blocks, 1024)");
+        if (pool_nb1 < IDX_DIM * 2 || pool_nb1 % 16 || !is_aligned(pool, 16))
+            return set_error(QWFN_EALIGN, "qsa_select_cells: pooled keys must be 128 f16 at a 16-byte aligned stride");
+        if (q_nb2 < (size_t) n_heads * IDX_DIM * 4 || !is_aligned(q, 16) || q_nb2 % 16 || bias_nb1 % 4 || !is_aligned(bias, 4))
+            return set_error(QWFN_EALIGN, "qsa_select_cells: q [128, n_heads] f32 per query, f32 bias");
+        if (!ws || ws_bytes < qwfn_qsa_select_workspace_size(n_blocks, T))
+            return set_error(QWFN_ENOMEM, "qsa_select_cells: workspace too small");
+        if (!is_aligned(ws, 16)) return set_error(QWFN_EALIGN, "qsa_select_cells: workspace must be 16-byte aligned");
+        if (n_blocks > (int64_t) TOPK_THREADS * TOPK_MAX_KPT)
+            return set_error(QWFN_ENOTSUP, "qsa_select_cells: at most 49152 blocks");
+        if (n_blocks * ratio > INT32_MAX) return set_error(QWFN_ERANGE, "qsa_select_cells: too many cells");
+        hipStream_t st = as_stream(stream);
+        int head_bits = 0;
+        while ((1 << head_bits) < n_heads) head_bits++;
+        score_args sa{pool, pool_nb1, n_blocks, q, q_nb2, n_heads, head_bits, T, bias, bias_nb1, (float *) ws};
+        const int64_t per = SCORE_THREADS / 64 * 16;                 // blocks per workgroup: 16 per wave
+        const unsigned gx = (unsigned) ((n_blocks + per - 1) / per);
+        hipLaunchKernelGGL(k_qsa_score, dim3(gx, (unsigned) ((T + SCORE_T - 1) / SCORE_T)), dim3(SCORE_THREADS), 0, st, sa);
+        if (int rc = hip_check(hipGetLastError(), "qsa score launch")) return rc;
+        topk_args ta{(const float *) ws, n_blocks, k_blocks, blk_cells, ratio, cells, top};
+        const int64_t kpt = (n_blocks + TOPK_THREADS - 1) / TOPK_THREADS;
+        // the smallest multiple of 4 that holds n_blocks / 1024 (18432 blocks: 20)
+        auto topk = kpt <= 8 ? k_qsa_topk<8> : kpt <= 12 ? k_qsa_topk<12> : kpt <= 16 ? k_qsa_topk<16>
+                  : kpt <= 20 ? k_qsa_topk<20> : kpt <= 24 ? k_qsa_topk<24> : kpt <= 32 ? k_qsa_topk<32>
+                  : kpt <= 40 ? k_qsa_topk<40> : k_qsa_topk<48>;
+        hipLaunchKernelGGL(topk, dim3((unsigned) T), dim3(TOPK_THREADS), 0, st, ta);
+        return hip_check(hipGetLastError(), "qsa top-k launch");
+    });
 }

@@ -5,6 +5,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <new>
 #include <string>
 
 #include "qwfn_kv.h"
@@ -20,12 +21,46 @@ constexpr uint32_t DEVERR_SET_ROWS_INDEX = 1u << 0;
 constexpr uint32_t DEVERR_GET_ROWS_INDEX = 1u << 1;
 
 // ---- host-side error plumbing (runtime.cpp) ----
-int  set_error(int code, const std::string & msg);
-int  hip_check(hipError_t e, const char * what);
+// The message goes into a fixed thread-local buffer: recording an error never
+// allocates and never throws.
+int  set_error(int code, const char * msg) noexcept;
+int  set_error(int code, const std::string & msg) noexcept;
+int  set_error2(int code, const char * what, const char * msg) noexcept;
+int  hip_check(hipError_t e, const char * what) noexcept;
 // Per-device status word (uint32 flags); created by qwfn_init or on first use.
 int  status_word(uint32_t ** out);
-// Library-owned workspace of at least `bytes` on the current device.
-int  library_workspace(size_t bytes, void ** out);
+// Library-owned workspace of at least `bytes` on the current device, shared by
+// every call on that device that passes no workspace. Refused while `stream`
+// is being captured into a graph (a later, larger call frees the buffer).
+int  library_workspace(size_t bytes, hipStream_t stream, void ** out);
+
+// The body of an extern "C" entry point: no C++ exception crosses the ABI. A
+// host allocation failure returns QWFN_ENOMEM (as the reference's
+// engine::snapshot_save returns false on std::bad_alloc, qwfn_engine.cpp:1022-1025);
+// any other exception QWFN_EDEVICE.
+template <typename F>
+int abi_call(const char * what, F && body) noexcept {
+    try {
+        return body();
+    } catch (const std::bad_alloc &) {
+        return set_error2(QWFN_ENOMEM, what, ": out of host memory");
+    } catch (...) {
+        return set_error2(QWFN_EDEVICE, what, ": unexpected host exception");
+    }
+}
+// The same for entry points that return a value (a size, a count): `fallback`
+// on an exception, with the error recorded.
+template <typename R, typename F>
+R abi_value(const char * what, R fallback, F && body) noexcept {
+    try {
+        return body();
+    } catch (const std::bad_alloc &) {
+        set_error2(QWFN_ENOMEM, what, ": out of host memory");
+    } catch (...) {
+        set_error2(QWFN_EDEVICE, what, ": unexpected host exception");
+    }
+    return fallback;
+}
 // Device-to-device copy of n_parts parts into n_slots slots (kv_copy.hip):
 // dst is [slots][n_parts], slots slot0 .. slot0+n_slots-1 are written; each
 // source byte is read once. Parts that are not 16-byte aligned go bytewise.

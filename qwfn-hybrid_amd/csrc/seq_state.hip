@@ -300,22 +300,29 @@ void parts_of(const qwfn_state & st, int32_t n, std::vector<qwfn_part> & out, st
 }
 
 // Copies parts between state tensors and caller buffers: device<->device parts
-// in one batched kernel, anything that touches host memory with the copy engine.
+// in batched kernels, anything that touches host memory with the copy engine.
+// Allocates nothing (callers rely on that after they have changed their own
+// bookkeeping).
 int copy_parts(const std::vector<const char *> & src, const std::vector<char *> & dst, const std::vector<size_t> & bytes,
                const std::vector<bool> & host_side, hipStream_t stream) {
-    std::vector<const char *> ks;
-    std::vector<char *> kd;
-    std::vector<size_t> kb;
+    constexpr int BATCH = 96;   // one launch of the single-destination copy kernel
+    const char * ks[BATCH];
+    char * kd[BATCH];
+    size_t kb[BATCH];
+    int n = 0;
     for (size_t k = 0; k < src.size(); k++) {
         if (!bytes[k]) continue;
         if (host_side[k]) {
             QWFN_HIP_TRY(hipMemcpyAsync(dst[k], src[k], bytes[k], hipMemcpyDefault, stream));
-        } else {
-            ks.push_back(src[k]); kd.push_back(dst[k]); kb.push_back(bytes[k]);
+            continue;
+        }
+        ks[n] = src[k]; kd[n] = dst[k]; kb[n] = bytes[k];
+        if (++n == BATCH) {
+            if (int rc = restore_device(ks, kb, kd, n, 1, 0, stream)) return rc;
+            n = 0;
         }
     }
-    if (ks.empty()) return QWFN_OK;
-    return restore_device(ks.data(), kb.data(), kd.data(), (int) ks.size(), 1, 0, stream);
+    return n ? restore_device(ks, kb, kd, n, 1, 0, stream) : QWFN_OK;
 }
 
 int check_states(const qwfn_state * const * sts, int32_t n_sts, bool need_memory, const char * what) {
@@ -359,72 +366,76 @@ void qwfn_state_config_default(qwfn_state_config * c, uint32_t n_ctx) {
 }
 
 int qwfn_state_create(const qwfn_state_config * cfg, int device, qwfn_state ** out) {
-    if (!cfg || !out) return set_error(QWFN_EINVAL, "state_create: NULL argument");
-    *out = nullptr;
-    if (int rc = validate_config(*cfg)) return rc;
-    if (device < QWFN_LAYOUT_ONLY) return set_error(QWFN_EINVAL, "state_create: bad device");
-    std::unique_ptr<qwfn_state> st(new (std::nothrow) qwfn_state());
-    if (!st) return set_error(QWFN_ENOMEM, "state_create: out of host memory");
-    st->cfg = *cfg;
-    plan(*st);
-    if (device == QWFN_LAYOUT_ONLY) {
+    return ::qwfn::abi_call("state_create", [&]() -> int {
+        if (!cfg || !out) return set_error(QWFN_EINVAL, "state_create: NULL argument");
+        *out = nullptr;
+        if (int rc = validate_config(*cfg)) return rc;
+        if (device < QWFN_LAYOUT_ONLY) return set_error(QWFN_EINVAL, "state_create: bad device");
+        std::unique_ptr<qwfn_state> st(new (std::nothrow) qwfn_state());
+        if (!st) return set_error(QWFN_ENOMEM, "state_create: out of host memory");
+        st->cfg = *cfg;
+        plan(*st);
+        if (device == QWFN_LAYOUT_ONLY) {
+            *out = st.release();
+            return QWFN_OK;
+        }
+        int n = 0;
+        QWFN_HIP_TRY(hipGetDeviceCount(&n));
+        if (device >= n) return set_error(QWFN_EINVAL, "state_create: device " + std::to_string(device) + " of " + std::to_string(n));
+        st->device = device;
+        device_scope ds(device);
+        if (ds.rc) return ds.rc;
+        void * p = nullptr;
+        if (hipMalloc(&p, std::max<size_t>(st->dev_bytes, ARENA_ALIGN)) != hipSuccess)
+            return set_error(QWFN_ENOMEM, "failed to allocate state buffer");
+        st->dev = (char *) p;
+        if (st->host_bytes) {
+            // mapped so that the device kernels can address the caches over the host link
+            if (hipHostMalloc(&p, st->host_bytes, hipHostMallocMapped | hipHostMallocPortable) != hipSuccess)
+                return set_error(QWFN_ENOMEM, "failed to allocate the host state buffer");
+            st->host = (char *) p;
+            void * dp = nullptr;
+            QWFN_HIP_TRY(hipHostGetDevicePointer(&dp, p, 0));
+            st->host_dev = (char *) dp;
+        }
+        if (cfg->n_rollback) {
+            if (hipMalloc(&p, (size_t) cfg->n_rollback * std::max<size_t>(st->rec_bytes, ARENA_ALIGN)) != hipSuccess)
+                return set_error(QWFN_ENOMEM, "no device memory for the rollback snapshots");
+            st->rb = (char *) p;
+        }
+        // recurrent state and conv history start at zero; the caches need not
+        if (int rc = zero_recurrent(*st, nullptr)) return rc;
+        QWFN_HIP_TRY(hipStreamSynchronize(nullptr));
         *out = st.release();
         return QWFN_OK;
-    }
-    int n = 0;
-    QWFN_HIP_TRY(hipGetDeviceCount(&n));
-    if (device >= n) return set_error(QWFN_EINVAL, "state_create: device " + std::to_string(device) + " of " + std::to_string(n));
-    st->device = device;
-    device_scope ds(device);
-    if (ds.rc) return ds.rc;
-    void * p = nullptr;
-    if (hipMalloc(&p, std::max<size_t>(st->dev_bytes, ARENA_ALIGN)) != hipSuccess)
-        return set_error(QWFN_ENOMEM, "failed to allocate state buffer");
-    st->dev = (char *) p;
-    if (st->host_bytes) {
-        // mapped so that the device kernels can address the caches over the host link
-        if (hipHostMalloc(&p, st->host_bytes, hipHostMallocMapped | hipHostMallocPortable) != hipSuccess)
-            return set_error(QWFN_ENOMEM, "failed to allocate the host state buffer");
-        st->host = (char *) p;
-        void * dp = nullptr;
-        QWFN_HIP_TRY(hipHostGetDevicePointer(&dp, p, 0));
-        st->host_dev = (char *) dp;
-    }
-    if (cfg->n_rollback) {
-        if (hipMalloc(&p, (size_t) cfg->n_rollback * std::max<size_t>(st->rec_bytes, ARENA_ALIGN)) != hipSuccess)
-            return set_error(QWFN_ENOMEM, "no device memory for the rollback snapshots");
-        st->rb = (char *) p;
-    }
-    // recurrent state and conv history start at zero; the caches need not
-    if (int rc = zero_recurrent(*st, nullptr)) return rc;
-    QWFN_HIP_TRY(hipStreamSynchronize(nullptr));
-    *out = st.release();
-    return QWFN_OK;
+    });
 }
 
 void qwfn_state_destroy(qwfn_state * st) { delete st; }
 
 int qwfn_state_tensor(const qwfn_state * st, int32_t kind, uint32_t il, int32_t slot, qwfn_tensor * out) {
-    if (!st || !out) return set_error(QWFN_EINVAL, "state_tensor: NULL argument");
-    *out = qwfn_tensor{};
-    const bool recurrent = kind == QWFN_STATE_RS || kind == QWFN_STATE_CONV || kind == QWFN_STATE_PLE_CONV;
-    if (kind < QWFN_STATE_K || kind > QWFN_STATE_PLE_CONV) return set_error(QWFN_EINVAL, "state_tensor: unknown kind");
-    if (slot < -1 || (slot >= 0 && (!recurrent || slot >= (int32_t) st->cfg.n_rollback)))
-        return set_error(QWFN_ERANGE, "state_tensor: no such rollback slot");
-    int ei = -1;
-    if (kind == QWFN_STATE_PLE_CONV) ei = st->ple;
-    else if (il < st->cfg.n_layer) {
-        switch (kind) {
-            case QWFN_STATE_K:    ei = st->k[il]; break;
-            case QWFN_STATE_V:    ei = st->v[il]; break;
-            case QWFN_STATE_IDX:  ei = st->idx[il]; break;
-            case QWFN_STATE_RS:   ei = st->rs[il]; break;
-            default:              ei = st->conv[il]; break;
+    return ::qwfn::abi_call("state_tensor", [&]() -> int {
+        if (!st || !out) return set_error(QWFN_EINVAL, "state_tensor: NULL argument");
+        *out = qwfn_tensor{};
+        const bool recurrent = kind == QWFN_STATE_RS || kind == QWFN_STATE_CONV || kind == QWFN_STATE_PLE_CONV;
+        if (kind < QWFN_STATE_K || kind > QWFN_STATE_PLE_CONV) return set_error(QWFN_EINVAL, "state_tensor: unknown kind");
+        if (slot < -1 || (slot >= 0 && (!recurrent || slot >= (int32_t) st->cfg.n_rollback)))
+            return set_error(QWFN_ERANGE, "state_tensor: no such rollback slot");
+        int ei = -1;
+        if (kind == QWFN_STATE_PLE_CONV) ei = st->ple;
+        else if (il < st->cfg.n_layer) {
+            switch (kind) {
+                case QWFN_STATE_K:    ei = st->k[il]; break;
+                case QWFN_STATE_V:    ei = st->v[il]; break;
+                case QWFN_STATE_IDX:  ei = st->idx[il]; break;
+                case QWFN_STATE_RS:   ei = st->rs[il]; break;
+                default:              ei = st->conv[il]; break;
+            }
         }
-    }
-    if (ei < 0) return 0;
-    fill_desc(*st, st->entries[(size_t) ei], slot, out);
-    return 1;
+        if (ei < 0) return 0;
+        fill_desc(*st, st->entries[(size_t) ei], slot, out);
+        return 1;
+    });
 }
 
 size_t qwfn_state_bytes(const qwfn_state * st) { return st ? st->dev_bytes : 0; }
@@ -435,217 +446,243 @@ int32_t qwfn_state_n_past(const qwfn_state * st) { return st ? st->n_past : 0; }
 int32_t qwfn_state_rollback_depth(const qwfn_state * st) { return st ? st->rb_depth : 0; }
 
 int qwfn_state_summary(const qwfn_state * st, char * buf, size_t cap) {
-    if (!st || (!buf && cap)) return set_error(QWFN_EINVAL, "state_summary: NULL argument");
-    size_t kv = 0, ix = 0, rs = 0, cv = 0;
-    for (const auto & e : st->entries) {
-        if (e.kind == QWFN_STATE_K || e.kind == QWFN_STATE_V) kv += e.bytes;
-        else if (e.kind == QWFN_STATE_IDX) ix += e.bytes;
-        else if (e.kind == QWFN_STATE_RS) rs += e.bytes;
-        else cv += e.bytes;
-    }
-    // qwfn_state.cpp:154-173; doubles printed as an ostream does by default (%g)
-    std::string s = "state @ " + std::to_string(st->cfg.n_ctx) + " ctx: ";
-    char tmp[512];
-    snprintf(tmp, sizeof tmp, "KV %g GB (%s), indexer %g GB, deltanet %g MB (constant), conv %g MB  =>  total %g GB on the device",
-             kv / 1e9, type_name(st->cfg.type_k), ix / 1e9, rs / 1e6, cv / 1e6, st->dev_bytes / 1e9);
-    s += tmp;
-    if (st->host_bytes) {
-        snprintf(tmp, sizeof tmp, " + %g GB in pinned host memory", st->host_bytes / 1e9);
+    return ::qwfn::abi_call("state_summary", [&]() -> int {
+        if (!st || (!buf && cap)) return set_error(QWFN_EINVAL, "state_summary: NULL argument");
+        size_t kv = 0, ix = 0, rs = 0, cv = 0;
+        for (const auto & e : st->entries) {
+            if (e.kind == QWFN_STATE_K || e.kind == QWFN_STATE_V) kv += e.bytes;
+            else if (e.kind == QWFN_STATE_IDX) ix += e.bytes;
+            else if (e.kind == QWFN_STATE_RS) rs += e.bytes;
+            else cv += e.bytes;
+        }
+        // qwfn_state.cpp:154-173; doubles printed as an ostream does by default (%g)
+        std::string s = "state @ " + std::to_string(st->cfg.n_ctx) + " ctx: ";
+        char tmp[512];
+        snprintf(tmp, sizeof tmp, "KV %g GB (%s), indexer %g GB, deltanet %g MB (constant), conv %g MB  =>  total %g GB on the device",
+                 kv / 1e9, type_name(st->cfg.type_k), ix / 1e9, rs / 1e6, cv / 1e6, st->dev_bytes / 1e9);
         s += tmp;
-    }
-    if (cap) {
-        const size_t n = std::min(cap - 1, s.size());
-        memcpy(buf, s.data(), n);
-        buf[n] = '\0';
-    }
-    return (int) s.size();
+        if (st->host_bytes) {
+            snprintf(tmp, sizeof tmp, " + %g GB in pinned host memory", st->host_bytes / 1e9);
+            s += tmp;
+        }
+        if (cap) {
+            const size_t n = std::min(cap - 1, s.size());
+            memcpy(buf, s.data(), n);
+            buf[n] = '\0';
+        }
+        return (int) s.size();
+    });
 }
 
 int qwfn_state_step_done(qwfn_state * st, int32_t T, int32_t verified) {
-    if (!st) return set_error(QWFN_EINVAL, "state_step_done: NULL state");
-    if (T < 1) return set_error(QWFN_EINVAL, "state_step_done: a step has at least one position");
-    if ((int64_t) st->n_past + T > (int64_t) st->cfg.n_ctx) return set_error(QWFN_ERANGE, "context exhausted");
-    st->rb_depth = (verified && T >= 2 && st->cfg.n_rollback > 0) ? std::min<int32_t>(T - 1, (int32_t) st->cfg.n_rollback) : 0;
-    st->n_past += T;
-    return QWFN_OK;
+    return ::qwfn::abi_call("state_step_done", [&]() -> int {
+        if (!st) return set_error(QWFN_EINVAL, "state_step_done: NULL state");
+        if (T < 1) return set_error(QWFN_EINVAL, "state_step_done: a step has at least one position");
+        if ((int64_t) st->n_past + T > (int64_t) st->cfg.n_ctx) return set_error(QWFN_ERANGE, "context exhausted");
+        st->rb_depth = (verified && T >= 2 && st->cfg.n_rollback > 0) ? std::min<int32_t>(T - 1, (int32_t) st->cfg.n_rollback) : 0;
+        st->n_past += T;
+        return QWFN_OK;
+    });
 }
 
 int qwfn_state_reset(qwfn_state * st, void * stream) {
-    if (!st) return set_error(QWFN_EINVAL, "state_reset: NULL state");
-    device_scope ds(st->device);
-    if (ds.rc) return ds.rc;
-    if (st->dev)   // a QWFN_LAYOUT_ONLY state has only its bookkeeping
-        if (int rc = zero_recurrent(*st, as_stream(stream))) return rc;
-    st->n_past = 0;
-    st->rb_depth = 0;
-    return QWFN_OK;
+    return ::qwfn::abi_call("state_reset", [&]() -> int {
+        if (!st) return set_error(QWFN_EINVAL, "state_reset: NULL state");
+        device_scope ds(st->device);
+        if (ds.rc) return ds.rc;
+        if (st->dev)   // a QWFN_LAYOUT_ONLY state has only its bookkeeping
+            if (int rc = zero_recurrent(*st, as_stream(stream))) return rc;
+        st->n_past = 0;
+        st->rb_depth = 0;
+        return QWFN_OK;
+    });
 }
 
 int qwfn_state_rollback(qwfn_state * st, int32_t n_back, void * stream) {
-    if (!st) return set_error(QWFN_EINVAL, "state_rollback: NULL state");
-    if (n_back < 1 || n_back > st->rb_depth)
-        return set_error(QWFN_ERANGE, "rollback: no snapshot of the state " + std::to_string(n_back) + " tokens back");
-    if (!st->dev || !st->rb) return set_error(QWFN_EINVAL, "state_rollback: the state has no rollback memory");
-    device_scope ds(st->device);
-    if (ds.rc) return ds.rc;
-    const char * src = st->rb + (size_t) (n_back - 1) * st->rec_bytes;
-    char * dst = st->dev + st->rec_off;
-    const size_t b = st->rec_bytes;
-    if (int rc = restore_device(&src, &b, &dst, 1, 1, 0, as_stream(stream))) return rc;
-    st->n_past -= n_back;
-    st->rb_depth = 0;
-    return QWFN_OK;
+    return ::qwfn::abi_call("state_rollback", [&]() -> int {
+        if (!st) return set_error(QWFN_EINVAL, "state_rollback: NULL state");
+        if (n_back < 1 || n_back > st->rb_depth)
+            return set_error(QWFN_ERANGE, "rollback: no snapshot of the state " + std::to_string(n_back) + " tokens back");
+        if (!st->dev || !st->rb) return set_error(QWFN_EINVAL, "state_rollback: the state has no rollback memory");
+        device_scope ds(st->device);
+        if (ds.rc) return ds.rc;
+        const char * src = st->rb + (size_t) (n_back - 1) * st->rec_bytes;
+        char * dst = st->dev + st->rec_off;
+        const size_t b = st->rec_bytes;
+        if (int rc = restore_device(&src, &b, &dst, 1, 1, 0, as_stream(stream))) return rc;
+        st->n_past -= n_back;
+        st->rb_depth = 0;
+        return QWFN_OK;
+    });
 }
 
 int qwfn_snapshot_parts(const qwfn_state * const * sts, int32_t n_sts, int32_t n_past, qwfn_part * parts,
                         int32_t max_parts, int32_t * n_parts) {
-    if (!n_parts || (max_parts > 0 && !parts) || max_parts < 0) return set_error(QWFN_EINVAL, "snapshot_parts: bad output array");
-    if (int rc = check_states(sts, n_sts, false, "snapshot_parts")) return rc;
-    if (n_past < 0) return set_error(QWFN_EINVAL, "snapshot_parts: a position count");
-    std::vector<qwfn_part> all;
-    for (int32_t i = 0; i < n_sts; i++) parts_of(*sts[i], n_past, all, nullptr);
-    *n_parts = (int32_t) all.size();
-    for (int32_t k = 0; k < std::min<int32_t>(max_parts, (int32_t) all.size()); k++) parts[k] = all[(size_t) k];
-    return QWFN_OK;
+    return ::qwfn::abi_call("snapshot_parts", [&]() -> int {
+        if (!n_parts || (max_parts > 0 && !parts) || max_parts < 0) return set_error(QWFN_EINVAL, "snapshot_parts: bad output array");
+        if (int rc = check_states(sts, n_sts, false, "snapshot_parts")) return rc;
+        if (n_past < 0) return set_error(QWFN_EINVAL, "snapshot_parts: a position count");
+        std::vector<qwfn_part> all;
+        for (int32_t i = 0; i < n_sts; i++) parts_of(*sts[i], n_past, all, nullptr);
+        *n_parts = (int32_t) all.size();
+        for (int32_t k = 0; k < std::min<int32_t>(max_parts, (int32_t) all.size()); k++) parts[k] = all[(size_t) k];
+        return QWFN_OK;
+    });
 }
 
 int qwfn_snapshot_save(const qwfn_state * const * sts, int32_t n_sts, void * const * dst, const size_t * dst_bytes,
                        int32_t n_dst, int32_t dst_kind, int32_t * n_past_out, void * stream) {
-    if (int rc = check_states(sts, n_sts, true, "snapshot_save")) return rc;
-    if (dst_kind != QWFN_MEM_DEVICE && dst_kind != QWFN_MEM_HOST) return set_error(QWFN_EINVAL, "snapshot_save: unknown destination kind");
-    const int32_t n_past = sts[0]->n_past;
-    for (int32_t i = 1; i < n_sts; i++)
-        if (sts[i]->n_past != n_past) return set_error(QWFN_EINVAL, "snapshot_save: the states disagree on n_past");
-    std::vector<qwfn_part> parts;
-    std::vector<bool> host_side;
-    for (int32_t i = 0; i < n_sts; i++) parts_of(*sts[i], n_past, parts, &host_side);
-    if (n_dst != (int32_t) parts.size() || (n_dst && (!dst || !dst_bytes)))
-        return set_error(QWFN_ESIZE, "snapshot_save: " + std::to_string(parts.size()) + " parts, " + std::to_string(n_dst) + " buffers");
-    std::vector<const char *> src;
-    std::vector<char *> d;
-    std::vector<size_t> b;
-    for (size_t k = 0; k < parts.size(); k++) {
-        if (dst_bytes[k] != parts[k].bytes)
-            return set_error(QWFN_ESIZE, "snapshot_save: buffer " + std::to_string(k) + " has " + std::to_string(dst_bytes[k]) +
-                                             " bytes, the part " + std::to_string(parts[k].bytes));
-        if (parts[k].bytes && !dst[k]) return set_error(QWFN_EINVAL, "snapshot_save: NULL buffer " + std::to_string(k));
-        src.push_back((const char *) parts[k].data);
-        d.push_back((char *) dst[k]);
-        b.push_back(parts[k].bytes);
-        if (dst_kind == QWFN_MEM_HOST) host_side[k] = true;
-    }
-    device_scope ds(sts[0]->device);
-    if (ds.rc) return ds.rc;
-    if (int rc = copy_parts(src, d, b, host_side, as_stream(stream))) return rc;
-    if (n_past_out) *n_past_out = n_past;
-    return QWFN_OK;
+    return ::qwfn::abi_call("snapshot_save", [&]() -> int {
+        if (int rc = check_states(sts, n_sts, true, "snapshot_save")) return rc;
+        if (dst_kind != QWFN_MEM_DEVICE && dst_kind != QWFN_MEM_HOST) return set_error(QWFN_EINVAL, "snapshot_save: unknown destination kind");
+        const int32_t n_past = sts[0]->n_past;
+        for (int32_t i = 1; i < n_sts; i++)
+            if (sts[i]->n_past != n_past) return set_error(QWFN_EINVAL, "snapshot_save: the states disagree on n_past");
+        std::vector<qwfn_part> parts;
+        std::vector<bool> host_side;
+        for (int32_t i = 0; i < n_sts; i++) parts_of(*sts[i], n_past, parts, &host_side);
+        if (n_dst != (int32_t) parts.size() || (n_dst && (!dst || !dst_bytes)))
+            return set_error(QWFN_ESIZE, "snapshot_save: " + std::to_string(parts.size()) + " parts, " + std::to_string(n_dst) + " buffers");
+        std::vector<const char *> src;
+        std::vector<char *> d;
+        std::vector<size_t> b;
+        for (size_t k = 0; k < parts.size(); k++) {
+            if (dst_bytes[k] != parts[k].bytes)
+                return set_error(QWFN_ESIZE, "snapshot_save: buffer " + std::to_string(k) + " has " + std::to_string(dst_bytes[k]) +
+                                                 " bytes, the part " + std::to_string(parts[k].bytes));
+            if (parts[k].bytes && !dst[k]) return set_error(QWFN_EINVAL, "snapshot_save: NULL buffer " + std::to_string(k));
+            src.push_back((const char *) parts[k].data);
+            d.push_back((char *) dst[k]);
+            b.push_back(parts[k].bytes);
+            if (dst_kind == QWFN_MEM_HOST) host_side[k] = true;
+        }
+        device_scope ds(sts[0]->device);
+        if (ds.rc) return ds.rc;
+        if (int rc = copy_parts(src, d, b, host_side, as_stream(stream))) return rc;
+        if (n_past_out) *n_past_out = n_past;
+        return QWFN_OK;
+    });
 }
 
 int qwfn_snapshot_load(qwfn_state * const * sts, int32_t n_sts, int32_t n_past, const void * const * src,
                        const size_t * src_bytes, int32_t n_src, int32_t src_kind, void * stream) {
-    if (int rc = check_states(sts, n_sts, true, "snapshot_load")) return rc;
-    if (src_kind != QWFN_MEM_DEVICE && src_kind != QWFN_MEM_HOST) return set_error(QWFN_EINVAL, "snapshot_load: unknown source kind");
-    for (int32_t i = 0; i < n_sts; i++)
-        if (n_past < 0 || n_past > (int32_t) sts[i]->cfg.n_ctx) return set_error(QWFN_ERANGE, "snapshot_load: n_past outside the context");
-    device_scope ds(sts[0]->device);
-    if (ds.rc) return ds.rc;
-    hipStream_t s = as_stream(stream);
-    // engine::snapshot_load resets before it checks the parts (qwfn_engine.cpp:1034-1040)
-    for (int32_t i = 0; i < n_sts; i++)
-        if (int rc = qwfn_state_reset(sts[i], stream)) return rc;
-    std::vector<qwfn_part> parts;
-    std::vector<bool> host_side;
-    for (int32_t i = 0; i < n_sts; i++) parts_of(*sts[i], n_past, parts, &host_side);
-    if (n_src != (int32_t) parts.size() || (n_src && (!src || !src_bytes)))
-        return set_error(QWFN_ESIZE, "snapshot_load: " + std::to_string(n_src) + " parts given, " + std::to_string(parts.size()) + " expected");
-    std::vector<const char *> sp;
-    std::vector<char *> dp;
-    std::vector<size_t> b;
-    for (size_t k = 0; k < parts.size(); k++) {
-        if (src_bytes[k] != parts[k].bytes)
-            return set_error(QWFN_ESIZE, "snapshot_load: part " + std::to_string(k) + " has " + std::to_string(src_bytes[k]) +
-                                             " bytes, expected " + std::to_string(parts[k].bytes));
-        if (parts[k].bytes && !src[k]) return set_error(QWFN_EINVAL, "snapshot_load: NULL part " + std::to_string(k));
-        sp.push_back((const char *) src[k]);
-        dp.push_back((char *) parts[k].data);
-        b.push_back(parts[k].bytes);
-        if (src_kind == QWFN_MEM_HOST) host_side[k] = true;
-    }
-    if (int rc = copy_parts(sp, dp, b, host_side, s)) return rc;
-    for (int32_t i = 0; i < n_sts; i++) sts[i]->n_past = n_past;
-    return QWFN_OK;
+    return ::qwfn::abi_call("snapshot_load", [&]() -> int {
+        if (int rc = check_states(sts, n_sts, true, "snapshot_load")) return rc;
+        if (src_kind != QWFN_MEM_DEVICE && src_kind != QWFN_MEM_HOST) return set_error(QWFN_EINVAL, "snapshot_load: unknown source kind");
+        for (int32_t i = 0; i < n_sts; i++)
+            if (n_past < 0 || n_past > (int32_t) sts[i]->cfg.n_ctx) return set_error(QWFN_ERANGE, "snapshot_load: n_past outside the context");
+        device_scope ds(sts[0]->device);
+        if (ds.rc) return ds.rc;
+        hipStream_t s = as_stream(stream);
+        // engine::snapshot_load resets before it checks the parts (qwfn_engine.cpp:1034-1040)
+        for (int32_t i = 0; i < n_sts; i++)
+            if (int rc = qwfn_state_reset(sts[i], stream)) return rc;
+        std::vector<qwfn_part> parts;
+        std::vector<bool> host_side;
+        for (int32_t i = 0; i < n_sts; i++) parts_of(*sts[i], n_past, parts, &host_side);
+        if (n_src != (int32_t) parts.size() || (n_src && (!src || !src_bytes)))
+            return set_error(QWFN_ESIZE, "snapshot_load: " + std::to_string(n_src) + " parts given, " + std::to_string(parts.size()) + " expected");
+        std::vector<const char *> sp;
+        std::vector<char *> dp;
+        std::vector<size_t> b;
+        for (size_t k = 0; k < parts.size(); k++) {
+            if (src_bytes[k] != parts[k].bytes)
+                return set_error(QWFN_ESIZE, "snapshot_load: part " + std::to_string(k) + " has " + std::to_string(src_bytes[k]) +
+                                                 " bytes, expected " + std::to_string(parts[k].bytes));
+            if (parts[k].bytes && !src[k]) return set_error(QWFN_EINVAL, "snapshot_load: NULL part " + std::to_string(k));
+            sp.push_back((const char *) src[k]);
+            dp.push_back((char *) parts[k].data);
+            b.push_back(parts[k].bytes);
+            if (src_kind == QWFN_MEM_HOST) host_side[k] = true;
+        }
+        if (int rc = copy_parts(sp, dp, b, host_side, s)) return rc;
+        for (int32_t i = 0; i < n_sts; i++) sts[i]->n_past = n_past;
+        return QWFN_OK;
+    });
 }
 
 // ---------------------------------------------------------------- masks
 
 int qwfn_causal_mask_f16(uint16_t * mask, int64_t n_kv, int64_t T, int64_t n_past, size_t row_stride, void * stream) {
-    if (!mask) return set_error(QWFN_EINVAL, "causal_mask: NULL mask");
-    if (n_kv < 0 || T < 0 || n_past < 0) return set_error(QWFN_EINVAL, "causal_mask: negative size");
-    if (row_stride % 2 || row_stride < (size_t) n_kv * 2 || !is_aligned(mask, 2))
-        return set_error(QWFN_EALIGN, "causal_mask: row_stride must be even and hold n_kv keys");
-    const int64_t groups = (int64_t) ((row_stride / 2 + 7) / 8);
-    const int64_t total = T * groups;
-    if (total == 0) return QWFN_OK;
-    hipLaunchKernelGGL(k_causal_mask, dim3(grid_for(total)), dim3(FILL_THREADS), 0, as_stream(stream), (char *) mask, n_kv, T,
-                       n_past, row_stride, groups);
-    return hip_check(hipGetLastError(), "causal_mask launch");
+    return ::qwfn::abi_call("causal_mask_f16", [&]() -> int {
+        if (!mask) return set_error(QWFN_EINVAL, "causal_mask: NULL mask");
+        if (n_kv < 0 || T < 0 || n_past < 0) return set_error(QWFN_EINVAL, "causal_mask: negative size");
+        if (row_stride % 2 || row_stride < (size_t) n_kv * 2 || !is_aligned(mask, 2))
+            return set_error(QWFN_EALIGN, "causal_mask: row_stride must be even and hold n_kv keys");
+        const int64_t groups = (int64_t) ((row_stride / 2 + 7) / 8);
+        const int64_t total = T * groups;
+        if (total == 0) return QWFN_OK;
+        hipLaunchKernelGGL(k_causal_mask, dim3(grid_for(total)), dim3(FILL_THREADS), 0, as_stream(stream), (char *) mask, n_kv, T,
+                           n_past, row_stride, groups);
+        return hip_check(hipGetLastError(), "causal_mask launch");
+    });
 }
 
 int qwfn_cell_mask_f16(const int32_t * cells, int64_t n_cells, int64_t n_pad, int32_t n_past, uint16_t * mask,
                        int32_t * gcells, void * stream) {
-    if (!cells || !mask) return set_error(QWFN_EINVAL, "cell_mask: NULL pointer");
-    if (n_cells < 1 || n_pad < n_cells || n_pad > 2 * n_cells)
-        return set_error(QWFN_EINVAL, "cell_mask: need 1 <= n_cells <= n_pad <= 2 n_cells");
-    if (n_past < 0) return set_error(QWFN_EINVAL, "cell_mask: negative n_past");
-    if (!is_aligned(cells, 4) || !is_aligned(mask, 2) || (gcells && !is_aligned(gcells, 4)))
-        return set_error(QWFN_EALIGN, "cell_mask: misaligned pointer");
-    hipLaunchKernelGGL(k_cell_mask, dim3(grid_for(n_pad)), dim3(FILL_THREADS), 0, as_stream(stream), cells, n_cells, n_pad,
-                       n_past, mask, gcells);
-    return hip_check(hipGetLastError(), "cell_mask launch");
+    return ::qwfn::abi_call("cell_mask_f16", [&]() -> int {
+        if (!cells || !mask) return set_error(QWFN_EINVAL, "cell_mask: NULL pointer");
+        if (n_cells < 1 || n_pad < n_cells || n_pad > 2 * n_cells)
+            return set_error(QWFN_EINVAL, "cell_mask: need 1 <= n_cells <= n_pad <= 2 n_cells");
+        if (n_past < 0) return set_error(QWFN_EINVAL, "cell_mask: negative n_past");
+        if (!is_aligned(cells, 4) || !is_aligned(mask, 2) || (gcells && !is_aligned(gcells, 4)))
+            return set_error(QWFN_EALIGN, "cell_mask: misaligned pointer");
+        hipLaunchKernelGGL(k_cell_mask, dim3(grid_for(n_pad)), dim3(FILL_THREADS), 0, as_stream(stream), cells, n_cells, n_pad,
+                           n_past, mask, gcells);
+        return hip_check(hipGetLastError(), "cell_mask launch");
+    });
 }
 
 // ------------------------------------------- decode-time sparse-attention inputs
 
 int64_t qwfn_qsa_bucket(int32_t n_past, int32_t ratio, int64_t n_blocks_max) {
-    if (ratio < 1 || n_past < 0 || n_blocks_max < 1) return 0;
-    const int64_t b_last = n_past / ratio;
-    int64_t nb = (b_last + 1 + 255) / 256 * 256;
-    nb = std::max<int64_t>(nb, 768);
-    return std::min<int64_t>(nb, n_blocks_max);
+    return ::qwfn::abi_value<int64_t>("qsa_bucket", 0, [&]() -> int64_t {
+        if (ratio < 1 || n_past < 0 || n_blocks_max < 1) return 0;
+        const int64_t b_last = n_past / ratio;
+        int64_t nb = (b_last + 1 + 255) / 256 * 256;
+        nb = std::max<int64_t>(nb, 768);
+        return std::min<int64_t>(nb, n_blocks_max);
+    });
 }
 
 int qwfn_qsa_decode_prepare(const qwfn_qsa_inputs * qd, const float * prev_bias, int32_t n_past, void * stream) {
-    if (!qd || !qd->bias || !qd->write_idx || !qd->member_idx || !qd->blk_pos || !qd->blk_idx || !qd->npast_f)
-        return set_error(QWFN_EINVAL, "qsa_decode_prepare: NULL tensor");
-    if (qd->ratio < 1 || qd->n_blocks_max < 1 || n_past < 0)
-        return set_error(QWFN_EINVAL, "qsa_decode_prepare: need ratio >= 1, n_blocks_max >= 1, n_past >= 0");
-    qsa_prep_args a{};
-    a.qd = *qd;
-    a.prev = prev_bias == qd->bias ? nullptr : prev_bias;
-    a.n_past = n_past;
-    const int64_t n = std::max<int64_t>(a.prev ? qd->n_blocks_max : 4, qd->ratio);
-    hipLaunchKernelGGL(k_qsa_prepare, dim3(grid_for(n)), dim3(FILL_THREADS), 0, as_stream(stream), a);
-    return hip_check(hipGetLastError(), "qsa_decode_prepare launch");
+    return ::qwfn::abi_call("qsa_decode_prepare", [&]() -> int {
+        if (!qd || !qd->bias || !qd->write_idx || !qd->member_idx || !qd->blk_pos || !qd->blk_idx || !qd->npast_f)
+            return set_error(QWFN_EINVAL, "qsa_decode_prepare: NULL tensor");
+        if (qd->ratio < 1 || qd->n_blocks_max < 1 || n_past < 0)
+            return set_error(QWFN_EINVAL, "qsa_decode_prepare: need ratio >= 1, n_blocks_max >= 1, n_past >= 0");
+        qsa_prep_args a{};
+        a.qd = *qd;
+        a.prev = prev_bias == qd->bias ? nullptr : prev_bias;
+        a.n_past = n_past;
+        const int64_t n = std::max<int64_t>(a.prev ? qd->n_blocks_max : 4, qd->ratio);
+        hipLaunchKernelGGL(k_qsa_prepare, dim3(grid_for(n)), dim3(FILL_THREADS), 0, as_stream(stream), a);
+        return hip_check(hipGetLastError(), "qsa_decode_prepare launch");
+    });
 }
 
 int qwfn_qsa_bias_rebuild(float * bias, int64_t n_blocks_max, int32_t n_past, int32_t ratio, void * stream) {
-    if (!bias) return set_error(QWFN_EINVAL, "qsa_bias_rebuild: NULL bias");
-    if (n_blocks_max < 1 || ratio < 1 || n_past < -1) return set_error(QWFN_EINVAL, "qsa_bias_rebuild: bad sizes");
-    hipLaunchKernelGGL(k_qsa_bias, dim3(grid_for(n_blocks_max)), dim3(FILL_THREADS), 0, as_stream(stream), bias,
-                       n_blocks_max, n_past, ratio);
-    return hip_check(hipGetLastError(), "qsa_bias_rebuild launch");
+    return ::qwfn::abi_call("qsa_bias_rebuild", [&]() -> int {
+        if (!bias) return set_error(QWFN_EINVAL, "qsa_bias_rebuild: NULL bias");
+        if (n_blocks_max < 1 || ratio < 1 || n_past < -1) return set_error(QWFN_EINVAL, "qsa_bias_rebuild: bad sizes");
+        hipLaunchKernelGGL(k_qsa_bias, dim3(grid_for(n_blocks_max)), dim3(FILL_THREADS), 0, as_stream(stream), bias,
+                           n_blocks_max, n_past, ratio);
+        return hip_check(hipGetLastError(), "qsa_bias_rebuild launch");
+    });
 }
 
 int qwfn_qsa_tables(int32_t * blk_cells, int64_t n_blocks_max, int32_t ratio, float * cell_pos, int64_t n_ctx,
                     int32_t * blk_pos_all, int64_t n_whole, void * stream) {
-    if (ratio < 1 || n_blocks_max < 0 || n_ctx < 0 || n_whole < 0) return set_error(QWFN_EINVAL, "qsa_tables: bad sizes");
-    if (n_blocks_max * ratio > INT32_MAX || n_ctx > (int64_t) 1 << 24 || n_whole * ratio > INT32_MAX)
-        return set_error(QWFN_ERANGE, "qsa_tables: cell ids must fit int32 (positions exact in f32)");
-    qsa_tables_args a{blk_cells, n_blocks_max, ratio, cell_pos, n_ctx, blk_pos_all, n_whole};
-    const int64_t n = std::max({blk_cells ? n_blocks_max * ratio : 0, cell_pos ? n_ctx : 0, blk_pos_all ? 4 * n_whole : 0});
-    if (n == 0) return QWFN_OK;
-    hipLaunchKernelGGL(k_qsa_tables, dim3(grid_for(n)), dim3(FILL_THREADS), 0, as_stream(stream), a);
-    return hip_check(hipGetLastError(), "qsa_tables launch");
+    return ::qwfn::abi_call("qsa_tables", [&]() -> int {
+        if (ratio < 1 || n_blocks_max < 0 || n_ctx < 0 || n_whole < 0) return set_error(QWFN_EINVAL, "qsa_tables: bad sizes");
+        if (n_blocks_max * ratio > INT32_MAX || n_ctx > (int64_t) 1 << 24 || n_whole * ratio > INT32_MAX)
+            return set_error(QWFN_ERANGE, "qsa_tables: cell ids must fit int32 (positions exact in f32)");
+        qsa_tables_args a{blk_cells, n_blocks_max, ratio, cell_pos, n_ctx, blk_pos_all, n_whole};
+        const int64_t n = std::max({blk_cells ? n_blocks_max * ratio : 0, cell_pos ? n_ctx : 0, blk_pos_all ? 4 * n_whole : 0});
+        if (n == 0) return QWFN_OK;
+        hipLaunchKernelGGL(k_qsa_tables, dim3(grid_for(n)), dim3(FILL_THREADS), 0, as_stream(stream), a);
+        return hip_check(hipGetLastError(), "qsa_tables launch");
+    });
 }
 
 }  // extern "C"

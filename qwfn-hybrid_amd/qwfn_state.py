@@ -351,8 +351,10 @@ def qsa_select_cells(pool, q, bias, k_blocks: int, blk_cells, ratio: int, cells,
     L = K.load()
     n_blocks = pool.shape[0]
     T = q.shape[0]
-    # the C ABI takes rows at a stride with contiguous elements; the sizes it cannot see are checked here
-    if pool.dim() != 2 or pool.shape[1] != 128 or pool.stride(1) != 1 or pool.element_size() != 2:
+    # the C ABI takes raw device pointers and rows at a stride with contiguous
+    # elements; what it cannot see (device, dtype, sizes) is checked here
+    f16_types = (torch.float16,) + ((torch.uint16,) if hasattr(torch, "uint16") else ())
+    if pool.dim() != 2 or pool.shape[1] != 128 or pool.stride(1) != 1 or pool.dtype not in f16_types:
         raise ValueError("qsa_select_cells: pool must be [n_blocks, 128] f16 rows")
     if q.dim() != 3 or q.dtype != torch.float32 or q.shape[2] != 128 or q.stride(2) != 1 or q.stride(1) != 128:
         raise ValueError("qsa_select_cells: q must be f32 [T, n_heads, 128] with contiguous heads")
@@ -365,11 +367,17 @@ def qsa_select_cells(pool, q, bias, k_blocks: int, blk_cells, ratio: int, cells,
         raise ValueError("qsa_select_cells: cells must be contiguous i32 [T, k_blocks * ratio]")
     if top is not None and (top.dtype != torch.int32 or not top.is_contiguous() or top.numel() < T * k_blocks):
         raise ValueError("qsa_select_cells: top must be contiguous i32 [T, k_blocks]")
+    for name, t in (("pool", pool), ("q", q), ("bias", bias), ("blk_cells", blk_cells), ("cells", cells),
+                    ("top", top), ("ws", ws)):
+        if t is not None and (not t.is_cuda or t.device != pool.device):
+            raise ValueError(f"qsa_select_cells: {name} must be a GPU tensor on the pool's device")
     need = int(L.qwfn_qsa_select_workspace_size(n_blocks, T))
     if ws is None:
         ws = torch.empty(need, dtype=torch.uint8, device=pool.device)
+    elif ws.numel() * ws.element_size() < need or ws.data_ptr() % 256 or not ws.is_contiguous():
+        raise ValueError(f"qsa_select_cells: ws must be a contiguous 256-byte aligned buffer of >= {need} bytes")
     K.check(L.qwfn_qsa_select_cells(pool.data_ptr(), pool.stride(0) * pool.element_size(), n_blocks, q.data_ptr(),
                                     q.shape[1], q.stride(0) * 4, bias.data_ptr(), bias.stride(0) * 4, T, k_blocks,
                                     blk_cells.data_ptr(), ratio, cells.data_ptr(),
-                                    top.data_ptr() if top is not None else None, ws.data_ptr(), ws.numel(),
+                                    top.data_ptr() if top is not None else None, ws.data_ptr(), ws.numel() * ws.element_size(),
                                     K._stream(stream)))

@@ -115,12 +115,12 @@ def test_split_count_invariance(gpu, oracle):
     ref = KD.oracle_attn(q, kc, vc, 9000, 2, mask, 1 / 16)
     outs = []
     for ns in (1, 3, 17, 70):
-        os.environ["QWFN_FA_SPLITS"] = str(ns)
+        K.load().qwfn_fattn_force_splits(ns)
         try:
             say(f"splits={ns}")
             outs.append(gpu_attn(K, q, kc, vc, 9000, 2, mask, 1 / 16, ws=(ns == 17)))
         finally:
-            del os.environ["QWFN_FA_SPLITS"]
+            K.load().qwfn_fattn_force_splits(0)
         check(outs[-1], ref)
     for o in outs[1:]:
         assert KD.err_stats(o, outs[0])[0] < 2e-5

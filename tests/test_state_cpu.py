@@ -469,8 +469,12 @@ def test_qsa_select_wrapper_checks_shapes():
     bad = [dict(blk_cells=blk[: nb * ratio - 1]), dict(cells=cells[:, :-1].contiguous()),
            dict(q=q.transpose(1, 2).contiguous().transpose(1, 2)), dict(bias=bias.double()),
            dict(pool=pool[:, :64]), dict(top=torch.zeros((T, k - 1), dtype=torch.int32))]
+    bad.append(dict(pool=pool.to(torch.bfloat16)))
     for kw in bad:
         args = dict(pool=pool, q=q, bias=bias, k_blocks=k, blk_cells=blk, ratio=ratio, cells=cells, stream=0)
         args.update(kw)
-        with pytest.raises(ValueError):
+        with pytest.raises(ValueError, match="must be"):
             S.qsa_select_cells(**args)
+    # well-shaped host tensors: the kernels would read host addresses, so the wrapper refuses them
+    with pytest.raises(ValueError, match="GPU tensor"):
+        S.qsa_select_cells(pool=pool, q=q, bias=bias, k_blocks=k, blk_cells=blk, ratio=ratio, cells=cells, stream=0)
