@@ -1,0 +1,228 @@
+"""GPU parity at the full sizes of the path's workloads, through the C ABI,
+against the oracle (bit-exact bytes; attention within 2e-3 max / 1e-3 mean of
+ggml-cpu semantics, and 1e-4 max as observed):
+
+* prefill chunk: 512 new K/V rows appended at depth 0, 4096 and 16384 and a
+  512-query causal attention over the chunk; every token's 16 heads are
+  computed on the GPU, a subset of tokens is held to the oracle;
+* prefix restore: 12 layers of q8_0 K/V at 8192 positions plus 36 DeltaNet
+  states restored into 4 slots of a 73728-position cache (device and pinned
+  host sources), and the recurrent parts into 10 slots; then batch-4 decode
+  with the slots at 8192, 16384, 32768 and 65536 positions, per-sequence key
+  counts and the mask-only form;
+* sparse selection: per-KV-head lists of the top 128 of 1024 blocks of 64
+  positions plus the last 512 positions of a 65536-position cache, gathered
+  and attended by 3 queries.
+"""
+import numpy as np
+import pytest
+import torch
+
+import kvdata as KD
+from gpu_util import dev, host, say
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+TIGHT = 1e-4
+SEG = 272
+ROW = 544
+
+
+def check(got, ref, tight=TIGHT):
+    mx, mean = KD.err_stats(got, ref)
+    print(f"  max abs {mx:.3e}  mean abs {mean:.3e}", flush=True)
+    assert np.isfinite(got).all()
+    assert mx <= KD.MAX_ABS_TOL and mean <= KD.MEAN_ABS_TOL
+    assert mx <= tight
+
+
+# ------------------------------------------------------------- prefill chunk
+
+@pytest.mark.parametrize("depth", [0, 4096, 16384])
+def test_prefill_chunk_append_and_attention(gpu, oracle, depth):
+    K = gpu
+    T, nh, seed = 512, 16, 3
+    n_kv = depth + T
+    kc = KD.make_cache(KD.kv_rows(seed, 0, KD.K_KIND, depth), n_kv) if depth else np.zeros((n_kv, ROW), np.uint8)
+    vc = KD.make_cache(KD.kv_rows(seed, 0, KD.V_KIND, depth), n_kv) if depth else np.zeros((n_kv, ROW), np.uint8)
+    newk = KD.kv_rows(seed, 0, KD.K_KIND, T, first_row=depth)
+    newv = KD.kv_rows(seed, 0, KD.V_KIND, T, first_row=depth)
+    q = KD.q_rows(seed, 1, T, nh)[0]
+    mask = O.causal_mask(T, depth)                     # [T, n_kv], the reference's unpadded shape
+    say(f"prefill chunk: append {T} rows at {depth}, attention {T} x {nh} heads over {n_kv} keys")
+    kd, vd = dev(kc), dev(vc)
+    K.cpy_f32_q8_0_kv(dev(newk), kd, dev(newv), vd, depth)
+    out = torch.full((1, T, nh, 256), float("nan"), dtype=torch.float32, device="cuda")
+    md = dev(mask.view(np.float16))
+    qd = dev(q[None].astype(np.float32))     # held: the descriptors below carry raw pointers
+    K.flash_attn_ext(K.q_view(qd), K.cache_attn_view(kd, n_kv, 2), K.cache_attn_view(vd, n_kv, 2), K.mask_view(md),
+                     1 / 16, K.out_view(out))
+    got = host(out)[0]
+    kc[depth:] = O.quantize(newk, O.Q8_X86)
+    vc[depth:] = O.quantize(newv, O.Q8_X86)
+    np.testing.assert_array_equal(host(kd), kc)
+    np.testing.assert_array_equal(host(vd), vc)
+    assert np.isfinite(got).all()
+    for t in (0, 1, 63, 255, 256, 257, 510, 511):
+        ref = KD.oracle_attn(q[t:t + 1], kc, vc, depth + t + 1, 2, None, 1 / 16)
+        check(got[t:t + 1], ref)
+
+
+# ------------------------------------------------- restore + batch decode
+
+N_CTX5 = 73728
+PREFIX = 8192
+
+
+def _prefix_parts():
+    """The snapshot of config 5: per layer K and V (8192 rows each), then 36 DeltaNet states."""
+    parts = []
+    for il in range(12):
+        parts.append(KD.make_cache(KD.kv_rows(5, il, KD.K_KIND, PREFIX), PREFIX).reshape(-1))
+        parts.append(KD.make_cache(KD.kv_rows(5, il, KD.V_KIND, PREFIX), PREFIX).reshape(-1))
+    for il in range(36):
+        parts.append(KD.normal(5, il, KD.STATE_KIND, 32 * 128 * 128, std=0.02).view(np.uint8))
+    return parts
+
+
+@pytest.mark.parametrize("src_kind", [0, 1])
+def test_prefix_restore_full_size(gpu, src_kind):
+    K = gpu
+    parts = _prefix_parts()
+    sizes = [p.size for p in parts]
+    assert sum(sizes) == 182452224
+    n_slots = 4
+    # slot caches: 12 layers of K and V at 73728 rows (962.6 MB per slot), DeltaNet states after them
+    caches = [torch.zeros((24, N_CTX5 * ROW), dtype=torch.uint8, device="cuda") for _ in range(n_slots)]
+    states = [torch.zeros((36, 32 * 128 * 128 * 4), dtype=torch.uint8, device="cuda") for _ in range(n_slots)]
+    if src_kind == 0:
+        src = [dev(p) for p in parts]
+    else:
+        src = [torch.from_numpy(p).pin_memory() for p in parts]
+    dsts = []
+    for s in range(n_slots):
+        dsts += [caches[s][i].data_ptr() for i in range(24)] + [states[s][i].data_ptr() for i in range(36)]
+    say(f"restore 182 MB x {n_slots} slots, src_kind={src_kind}")
+    K.state_restore([t.data_ptr() for t in src], sizes, dsts, n_slots, src_kind)
+    torch.cuda.synchronize()
+    for s in range(n_slots):
+        for i in range(24):
+            ref = src[i] if src_kind == 0 else src[i].cuda()
+            assert torch.equal(caches[s][i][:sizes[i]], ref), (s, i)
+            assert not caches[s][i][sizes[i]:sizes[i] + ROW * 64].any()
+        ref = torch.stack([src[24 + i] if src_kind == 0 else src[24 + i].cuda() for i in range(36)])
+        assert torch.equal(states[s], ref), s
+    del caches
+    if src_kind == 0:
+        # the recurrent parts into 10 slots (the broadcast runs in launches of at most 8 slots)
+        many = [torch.zeros((36, 32 * 128 * 128 * 4), dtype=torch.uint8, device="cuda") for _ in range(10)]
+        say("restore 36 DeltaNet states x 10 slots")
+        K.state_restore([t.data_ptr() for t in src[24:]], sizes[24:],
+                        [many[s][i].data_ptr() for s in range(10) for i in range(36)], 10, 0)
+        torch.cuda.synchronize()
+        ref = torch.stack(src[24:])
+        for s in range(10):
+            assert torch.equal(many[s], ref), s
+
+
+def test_batch_decode_restored_slots(gpu, oracle):
+    """Config 5's decode: 4 slots share the restored 8192-position prefix and run
+    on to 8192, 16384, 32768 and 65536 positions; one query per slot."""
+    K = gpu
+    depths = [8192, 16384, 32768, 65536]
+    B, nh, n_kv = 4, 16, max(depths)
+    prefix_k = KD.make_cache(KD.kv_rows(5, 0, KD.K_KIND, PREFIX), PREFIX)
+    prefix_v = KD.make_cache(KD.kv_rows(5, 0, KD.V_KIND, PREFIX), PREFIX)
+    kc = torch.zeros((B, N_CTX5, ROW), dtype=torch.uint8, device="cuda")
+    vc = torch.zeros((B, N_CTX5, ROW), dtype=torch.uint8, device="cuda")
+    pk, pv = dev(prefix_k), dev(prefix_v)
+    say("restore the layer-0 prefix into 4 slots")
+    K.state_restore([pk.data_ptr(), pv.data_ptr()], [pk.numel(), pv.numel()],
+                    [p for b in range(B) for p in (kc[b].data_ptr(), vc[b].data_ptr())], B, 0)
+    host_k, host_v = [], []
+    for b, d in enumerate(depths):
+        ek = KD.make_cache(KD.kv_rows(50 + b, 0, KD.K_KIND, d - PREFIX, first_row=PREFIX), d - PREFIX)
+        ev = KD.make_cache(KD.kv_rows(50 + b, 0, KD.V_KIND, d - PREFIX, first_row=PREFIX), d - PREFIX)
+        if d > PREFIX:
+            kc[b, PREFIX:d] = dev(ek)
+            vc[b, PREFIX:d] = dev(ev)
+        host_k.append(np.concatenate([prefix_k, ek]) if d > PREFIX else prefix_k)
+        host_v.append(np.concatenate([prefix_v, ev]) if d > PREFIX else prefix_v)
+    q = KD.q_rows(5, 1, 1, nh, batch=B)                     # [B, 1, nh, 256]
+    qd = dev(q.astype(np.float32))
+    kv = K.tensor(kc.data_ptr(), K.TYPE_Q8_0, (256, n_kv, 2, B), (34, ROW, SEG, N_CTX5 * ROW))
+    vv = K.tensor(vc.data_ptr(), K.TYPE_Q8_0, (256, n_kv, 2, B), (34, ROW, SEG, N_CTX5 * ROW))
+    refs = [KD.oracle_attn(q[b], host_k[b], host_v[b], depths[b], 2, None, 1 / 16) for b in range(B)]
+    out = torch.full((B, 1, nh, 256), float("nan"), dtype=torch.float32, device="cuda")
+    say("batch-4 decode, per-sequence key counts")
+    K.flash_attn_ext_seq(K.q_view(qd), kv, vv, None, 1 / 16, K.out_view(out), depths)
+    got = host(out)
+    for b in range(B):
+        check(got[b], refs[b])
+    # the same batch as one n_kv with each sequence's later keys masked
+    mask = np.full((B, 1, 1, n_kv), O.F16_NEG_INF, np.uint16)
+    for b, d in enumerate(depths):
+        mask[b, 0, 0, :d] = 0
+    md = dev(mask.view(np.float16))
+    mv = K.tensor(md.data_ptr(), K.TYPE_F16, (n_kv, 1, 1, B), (2, 2 * n_kv, 2 * n_kv, 2 * n_kv))
+    out.fill_(float("nan"))
+    say("batch-4 decode, mask only")
+    K.flash_attn_ext(K.q_view(qd), kv, vv, mv, 1 / 16, K.out_view(out))
+    got = host(out)
+    for b in range(B):
+        check(got[b], refs[b])
+
+
+# ------------------------------------------------------- sparse selection
+
+def _selection_lists(n_ctx=65536, blocks=1024, bsz=64, top=128, tail=512):
+    """Per KV head: top-`top` blocks by seeded uniform scores (ties to the lower block) and the last `tail` positions."""
+    lists = []
+    for h in range(2):
+        u = O.uniform(O.stream_key(4, 0, KD.SCORE_KIND, h), blocks)
+        order = np.argsort(-u, kind="stable")[:top]
+        pos = (order[:, None] * bsz + np.arange(bsz)[None, :]).reshape(-1)
+        lists.append(np.union1d(pos, np.arange(n_ctx - tail, n_ctx)).astype(np.int32))
+    return lists
+
+
+def test_sparse_selection_gather_and_attention(gpu, oracle):
+    K = gpu
+    n_ctx, T, nh = 65536, 3, 16
+    lists = _selection_lists(n_ctx)
+    assert [len(x) for x in lists] == [8576, 8640]
+    kc = KD.make_cache(KD.kv_rows(4, 0, KD.K_KIND, n_ctx), n_ctx)
+    vc = KD.make_cache(KD.kv_rows(4, 0, KD.V_KIND, n_ctx), n_ctx)
+    m = ((max(len(x) for x in lists) + 255) // 256) * 256
+    idx = np.stack([np.concatenate([x, np.repeat(x[-1:], m - len(x))]) for x in lists]).astype(np.int32)
+    gk = torch.zeros((2, m, SEG), dtype=torch.uint8, device="cuda")
+    gv = torch.zeros((2, m, SEG), dtype=torch.uint8, device="cuda")
+    kd, vd = dev(kc), dev(vc)
+    say(f"gather 2 x {m} half rows at 65536")
+    K.gather_segments(kd, dev(idx), gk, 0, SEG, SEG)
+    K.gather_segments(vd, dev(idx), gv, 0, SEG, SEG)
+    for h in range(2):
+        np.testing.assert_array_equal(host(gk)[h], kc[idx[h], h * SEG:(h + 1) * SEG])
+        np.testing.assert_array_equal(host(gv)[h], vc[idx[h], h * SEG:(h + 1) * SEG])
+    qpos = np.arange(n_ctx - T, n_ctx)
+    mask = np.full((1, nh, T, m), O.F16_NEG_INF, np.uint16)
+    for h in range(nh):
+        lst = lists[h // 8]
+        for t in range(T):
+            mask[0, h, t, :len(lst)][lst <= qpos[t]] = 0
+    q = KD.q_rows(4, 1, T, nh)[0]
+    out = torch.full((1, T, nh, 256), float("nan"), dtype=torch.float32, device="cuda")
+    kview = K.tensor(gk.data_ptr(), K.TYPE_Q8_0, (256, m, 2, 1), (34, SEG, m * SEG, 2 * m * SEG))
+    vview = K.tensor(gv.data_ptr(), K.TYPE_Q8_0, (256, m, 2, 1), (34, SEG, m * SEG, 2 * m * SEG))
+    say("attention over the gathered rows")
+    qd, md = dev(q[None].astype(np.float32)), dev(mask.view(np.float16))   # held while the call runs
+    K.flash_attn_ext(K.q_view(qd), kview, vview, K.mask_view(md), 1 / 16, K.out_view(out))
+    got = host(out)[0]
+    for h in range(nh):
+        lst = lists[h // 8]
+        for t in range(T):
+            sel = lst[lst <= qpos[t]]
+            kh = np.ascontiguousarray(kc[sel][:, (h // 8) * SEG:(h // 8 + 1) * SEG])
+            vh = np.ascontiguousarray(vc[sel][:, (h // 8) * SEG:(h // 8 + 1) * SEG])
+            ref = KD.oracle_attn(q[t:t + 1, h:h + 1], kh, vh, len(sel), 1, None, 1 / 16)
+            check(got[t, h], ref[0, 0])
