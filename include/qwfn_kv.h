@@ -157,6 +157,19 @@ int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor * k, const
                              const qwfn_tensor * mask, float scale, float max_bias, float logit_softcap,
                              const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes, void * stream);
 
+/* qwfn_flash_attn_ext_q8_0 without a workspace argument and without any
+ * device allocation: no counterpart in the reference; for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). The split partials go to a 16 MiB scratch array inside the
+ * library's code object (one per GPU, held until the process ends); when a
+ * call's partials would not fit, it uses fewer key splits (the result then
+ * differs from qwfn_flash_attn_ext_q8_0's only by float rounding). Every call on
+ * a GPU shares that GPU's scratch: calls that overlap on one GPU (two streams,
+ * or two threads) race and give wrong results. */
+int qwfn_flash_attn_ext_q8_0_noalloc(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
+                                     const qwfn_tensor * mask, float scale, float max_bias, float logit_softcap,
+                                     const qwfn_tensor * dst, int variant, void * stream);
+
 /* Force the key-split count of later attention calls in this process (any
  * thread; 0 returns to the planner's choice, values are capped at 1024). For
  * split-invariance tests and tuning sweeps; the results do not depend on it

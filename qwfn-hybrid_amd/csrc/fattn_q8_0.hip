@@ -47,6 +47,7 @@
 #include <cmath>
 #include <atomic>
 #include <cstdlib>
+#include <mutex>
 #include <type_traits>
 
 namespace qwfn {
@@ -1219,7 +1220,7 @@ int check_no_scratch() {
 }
 
 int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v, const qwfn_tensor * mask,
-               fa_plan * pl, const int64_t * seq_n_kv = nullptr) {
+               fa_plan * pl, const int64_t * seq_n_kv = nullptr, int64_t ns_cap = MAX_SPLITS) {
     if (!q || !k || !v) return set_error(QWFN_EINVAL, "flash_attn_ext: NULL q/k/v");
     if (q->type != QWFN_TYPE_F32) return set_error(QWFN_EINVAL, "flash_attn_ext: q must be f32");
     if (k->type != QWFN_TYPE_Q8_0 || v->type != QWFN_TYPE_Q8_0)
@@ -1281,6 +1282,7 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
     int64_t ns = std::max<int64_t>(1, target_blocks / std::max<int64_t>(1, nh_kv * B * pl->n_rg));
     ns = std::min<int64_t>(ns, std::max<int64_t>(1, (n_kv + ck - 1) / ck));
     if (const int32_t force = g_force_splits.load(std::memory_order_relaxed)) ns = force;
+    ns = std::min<int64_t>(ns, std::max<int64_t>(1, ns_cap));
     // Splits are whole chunks. When the keys exceed two or more chunks per
     // split by less than one chunk (n_kv = 2^k + T), the last split takes the
     // rest; otherwise every split rounds up and there are fewer.
@@ -1306,7 +1308,8 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
                 return set_error(QWFN_ERANGE, "flash_attn_ext_seq: sequence key counts must lie in [0, n_kv]");
             total += seq_n_kv[b];
         }
-        const int64_t units = std::max<int64_t>(1, target_blocks / std::max<int64_t>(1, nh_kv * pl->n_rg));
+        const int64_t units = std::max<int64_t>(1, std::min<int64_t>(target_blocks / std::max<int64_t>(1, nh_kv * pl->n_rg),
+                                                                     ns_cap * B));
         int64_t ns_max = 1, span = ck, ustart = 0;
         for (int64_t b = 0; b < B; b++) {
             const int64_t nk = seq_n_kv[b];
@@ -1387,15 +1390,55 @@ int check_append(const fa_append & ap, const qwfn_tensor * q, const qwfn_tensor 
     return QWFN_OK;
 }
 
+// Workspace of the allocation-free entry point (qwfn_flash_attn_ext_q8_0_noalloc):
+// device memory of the library's code object, one copy per GPU, held until
+// the process ends. In host code `scratch` only names the symbol; its device
+// address on the current GPU comes from hipGetSymbolAddress (scratch_address).
+constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(16) << 20;
+__device__ __align__(256) static char scratch[NOALLOC_SCRATCH_BYTES];
+
+constexpr int SCRATCH_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void *     g_scratch_addr[SCRATCH_MAX_DEVICES];   // scratch's address on each device, once looked up
+
+// scratch's device address on the current device: looked up once per device
+// (with that device current) on the first call there.
+int scratch_address(void ** out) {
+    int dev = 0;
+    QWFN_HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= SCRATCH_MAX_DEVICES) return set_error(QWFN_ENOTSUP, "flash_attn_ext_noalloc: device index beyond the library's table");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_addr[dev]) {
+        void * p = nullptr;
+        QWFN_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p || !is_aligned(p, 256)) return set_error(QWFN_EDEVICE, "flash_attn_ext_noalloc: scratch has no usable device address");
+        g_scratch_addr[dev] = p;
+    }
+    *out = g_scratch_addr[dev];
+    return QWFN_OK;
+}
+
+// Where the split partials go: the caller's workspace (or the library-owned
+// buffer when ws is NULL), or the library's static scratch.
+enum ws_mode { WS_CALLER, WS_SCRATCH };
+
 int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v, const qwfn_tensor * mask, float scale,
               float max_bias, float logit_softcap, const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes,
-              void * stream, const fa_append * app, const int64_t * seq_n_kv = nullptr) {
+              void * stream, const fa_append * app, const int64_t * seq_n_kv = nullptr, ws_mode wsm = WS_CALLER) {
     if (max_bias != 0.0f) return set_error(QWFN_ENOTSUP, "flash_attn_ext: max_bias (ALiBi) is not supported");
     if (logit_softcap != 0.0f) return set_error(QWFN_ENOTSUP, "flash_attn_ext: logit_softcap is not supported");
     if (!(std::isfinite(scale))) return set_error(QWFN_EINVAL, "flash_attn_ext: scale must be finite");
     if (variant != QWFN_Q8_REF && variant != QWFN_Q8_X86) return set_error(QWFN_EINVAL, "flash_attn_ext: unknown variant");
     fa_plan pl{};
     if (int rc = plan_fattn(q, k, v, mask, &pl, seq_n_kv)) return rc;
+    if (wsm == WS_SCRATCH && pl.ws_bytes > NOALLOC_SCRATCH_BYTES) {
+        // fewer key splits, so that their partials fit the scratch
+        const size_t per_split = (size_t) q->ne[3] * k->ne[2] * pl.R * (D * sizeof(float) + sizeof(float2));
+        const int64_t cap = std::max<int64_t>(1, (int64_t) ((NOALLOC_SCRATCH_BYTES - 512) / std::max<size_t>(per_split, 1)));
+        if (int rc = plan_fattn(q, k, v, mask, &pl, seq_n_kv, cap)) return rc;
+        if (pl.ws_bytes > NOALLOC_SCRATCH_BYTES)
+            return set_error(QWFN_ENOMEM, "flash_attn_ext_noalloc: the split partials need more than the 16 MiB scratch");
+    }
     if (app)
         if (int rc = check_append(*app, q, k, v)) return rc;
     if (!dst || !dst->data || dst->type != QWFN_TYPE_F32) return set_error(QWFN_EINVAL, "flash_attn_ext: dst must be f32");
@@ -1415,7 +1458,9 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
                            dim3(256), 0, as_stream(stream), (float *) dst->data, n);
         return hip_check(hipGetLastError(), "flash_attn zero fill");
     }
-    if (ws) {
+    if (wsm == WS_SCRATCH) {
+        if (int rc = scratch_address(&ws)) return rc;
+    } else if (ws) {
         if (ws_bytes < pl.ws_bytes) return set_error(QWFN_ENOMEM, "flash_attn_ext: workspace too small");
         if (!is_aligned(ws, 256)) return set_error(QWFN_EALIGN, "flash_attn_ext: workspace must be 256-byte aligned");
     } else if (int rc = library_workspace(pl.ws_bytes, as_stream(stream), &ws)) {
@@ -1532,6 +1577,15 @@ extern "C" int qwfn_flash_attn_ext_q8_0(const qwfn_tensor * q, const qwfn_tensor
                                         void * stream) {
     return ::qwfn::abi_call("flash_attn_ext_q8_0", [&]() -> int {
         return fattn_run(q, k, v, mask, scale, max_bias, logit_softcap, dst, variant, ws, ws_bytes, stream, nullptr);
+    });
+}
+
+extern "C" int qwfn_flash_attn_ext_q8_0_noalloc(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
+                                                const qwfn_tensor * mask, float scale, float max_bias,
+                                                float logit_softcap, const qwfn_tensor * dst, int variant, void * stream) {
+    return ::qwfn::abi_call("flash_attn_ext_q8_0_noalloc", [&]() -> int {
+        return fattn_run(q, k, v, mask, scale, max_bias, logit_softcap, dst, variant, nullptr, 0, stream, nullptr, nullptr,
+                         WS_SCRATCH);
     });
 }
 

@@ -68,7 +68,7 @@ class QsaInputs(ctypes.Structure):
 EXPORTS = [
     "qwfn_abi_version", "qwfn_last_error", "qwfn_init", "qwfn_device_status",
     "qwfn_set_rows_q8_0", "qwfn_cpy_f32_q8_0", "qwfn_set_rows_q8_0_kv", "qwfn_cpy_f32_q8_0_kv", "qwfn_get_rows_i32", "qwfn_kv_gather_segments",
-    "qwfn_fattn_workspace_size", "qwfn_fattn_force_splits", "qwfn_flash_attn_ext_q8_0", "qwfn_flash_attn_ext_q8_0_append",
+    "qwfn_fattn_workspace_size", "qwfn_fattn_force_splits", "qwfn_flash_attn_ext_q8_0", "qwfn_flash_attn_ext_q8_0_noalloc", "qwfn_flash_attn_ext_q8_0_append",
     "qwfn_fattn_workspace_size_seq", "qwfn_flash_attn_ext_q8_0_seq", "qwfn_state_restore",
     # include/qwfn_state.h
     "qwfn_state_config_default", "qwfn_state_create", "qwfn_state_destroy", "qwfn_state_tensor",
@@ -108,6 +108,8 @@ def load(path: str = LIB_PATH):
     L.qwfn_kv_gather_segments.argtypes = [vp, sz, i64, sz, sz, sz, i32, vp, i64, vp, sz, sz, vp]
     L.qwfn_fattn_workspace_size.argtypes = [T, T, T, T]
     L.qwfn_fattn_workspace_size.restype = sz
+    L.qwfn_flash_attn_ext_q8_0_noalloc.argtypes = [T, T, T, T, ctypes.c_float, ctypes.c_float, ctypes.c_float, T,
+                                                   ctypes.c_int, vp]
     L.qwfn_fattn_force_splits.argtypes = [i32]
     L.qwfn_fattn_force_splits.restype = None
     L.qwfn_flash_attn_ext_q8_0.argtypes = [T, T, T, T, ctypes.c_float, ctypes.c_float, ctypes.c_float, T,
