@@ -1150,10 +1150,515 @@ __global__ __launch_bounds__(256) void k_fattn_merge(fa_args a) {
     }
 }
 
+// ================================================================ decode / verify
+//
+// k_fa_dec: row groups of at most 32 query rows per KV head (decode, MTP
+// verify, batch decode), one block of 8 waves per CU. Wave (row tile t, key
+// group g) owns query rows 16t .. 16t+15 of the block and its tiles
+// g, g + KG, g + 2KG, ... of 16 keys. It streams them through a ring of two
+// stages of its own: LDS DMA that only this wave waits for (its own vmcnt), so
+// the key loop has no block barrier. Waves drift apart, and one wave's matrix
+// core work overlaps another's vector work. The RT waves of a key group each
+// load the same keys; the second load comes from L2. The arithmetic per tile
+// is that of k_fattn_q8_0's 16-key waves (exact i8 block dots, per-block
+// d_q*d_k scaling, online base-2 softmax, hi + lo f16 P*d_v).
+
+constexpr int DEC_WAVES = 8;
+constexpr int DEC_TK    = 16;                         // keys per tile
+constexpr int DEC_KB    = DEC_TK * SEG;               // 4352: one tensor's rows of a tile
+constexpr int DEC_TDMA  = (DEC_KB / 16 + 63) / 64;    // 5 wave DMAs per tensor (the last one with 16 lanes)
+constexpr int DEC_MOFF  = 2 * DEC_KB;                 // a tile's mask granules follow its K and V rows
+constexpr int DEC_MGR   = 3;                          // 16-byte granules per mask row of a tile (32 bytes, 2-byte aligned)
+constexpr int DEC_STAGE = DEC_MOFF + 1024;            // 9728 bytes
+constexpr int DEC_OBS   = D + 4;                      // merge buffer row stride (floats)
+constexpr int DEC_QROW  = 1024 + 16;                  // query row stride in the prologue's staging (bank spread)
+static_assert(DEC_KB / 16 - 64 * (DEC_TDMA - 1) == 16, "the last DMA of a tensor has 16 lanes");
+static_assert(16 * DEC_MGR <= 64, "a wave's mask rows of a tile are one DMA");
+
+template <int RT, bool MASKED, bool RG>
+__global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
+    constexpr int ROWS = 16 * RT, KG = DEC_WAVES / RT;
+    constexpr int OPS = 2 * DEC_TDMA + (MASKED ? 1 : 0);   // DMAs per tile of one wave
+    asm volatile("" :: "s"(a.q), "s"(a.k), "s"(a.v), "s"(a.mask), "s"(a.m_ne2), "s"(a.part_o));
+    // ring[stage][wave]: stage 1 of all waves is one contiguous region, which
+    // the prologue uses for the query rows and their window image
+    __shared__ __attribute__((aligned(16))) uint8_t ring[2][DEC_WAVES][DEC_STAGE];
+    __shared__ __attribute__((aligned(16))) uint16_t scl[DEC_WAVES][2][NBLK][DEC_TK];
+    static_assert(ROWS * DEC_QROW <= DEC_WAVES * DEC_STAGE, "query rows fit stage 1");
+    static_assert(ROWS * NBLK * QWIN + ROWS * NBLK * 4 <= DEC_WAVES * DEC_STAGE, "query image fits stage 1");
+    static_assert((KG - 1) * ROWS * DEC_OBS * 4 <= 2 * DEC_WAVES * DEC_STAGE, "merge buffers fit the ring");
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int ln = lane & 15, lg = lane >> 4;
+    const int tile = wave % RT, kg = wave / RT;
+
+    // ---- block -> (b, kvh, split): as k_fattn_q8_0 (one row group) ----
+    const int id = blockIdx.x;
+    const int hgn = a.nh_kv;
+    const int n_units = RG ? a.r_units : a.B * a.ns;
+    int kvh, u;
+    if (n_units >= 8) {
+        const int j = id >> 3;
+        const int jq = (int) udiv((uint32_t) j, (uint32_t) hgn, a.hgn_mul);
+        kvh = j - jq * hgn;
+        u = jq * 8 + (id & 7);
+    } else {
+        u = (int) udiv((uint32_t) id, (uint32_t) hgn, a.hgn_mul);
+        kvh = id - u * hgn;
+    }
+    if (u >= n_units) return;
+    int b, split;
+    int64_t k_lo, k_hi;
+    if constexpr (RG) {
+        int32_t us = 0, nsb = 1, slb = 0;
+        int64_t nkb = 0;
+        b = 0;
+#pragma unroll
+        for (int i = 0; i < RAGGED_MAX_B; i++)
+            if (i < a.B && u >= a.r_ustart[i]) {
+                b = i; us = a.r_ustart[i]; nsb = a.r_ns[i]; slb = a.r_split_len[i]; nkb = a.r_n_kv[i];
+            }
+        split = u - us;
+        k_lo = (int64_t) split * slb;
+        const int64_t e = k_lo + slb;
+        k_hi = split == nsb - 1 ? nkb : (nkb < e ? nkb : e);
+    } else {
+        b = (int) udiv((uint32_t) u, (uint32_t) a.ns, a.ns_mul);
+        split = u - b * a.ns;
+        k_lo = (int64_t) split * a.split_len;
+        const int64_t e = k_lo + a.split_len;
+        k_hi = split == a.ns - 1 ? a.n_kv : (a.n_kv < e ? a.n_kv : e);
+    }
+    const int span = (int) (k_hi - k_lo);
+    const int n_tiles = (span + DEC_TK - 1) / DEC_TK;
+    const int RW = a.R < ROWS ? a.R : ROWS;             // rows of this block (one row group)
+    const int wr0 = 16 * tile;                          // the wave's first row in the block
+
+    const char * kbase = a.k + (size_t) bmod(b, a.kb) * a.k_nb3 + (size_t) kvh * a.k_nb2;
+    const char * vbase = a.v + (size_t) bmod(b, a.vb) * a.v_nb3 + (size_t) kvh * a.v_nb2;
+
+    // ---- the wave's mask rows: query position for a mask shared by the heads,
+    //      query row for a per-head mask; byte offsets from the mask slice
+    //      rounded down to 16 bytes ----
+    const char * mslice = MASKED ? a.mask + (size_t) bmod(b, a.m_ne3) * a.m_nb3 : nullptr;
+    const char * mslice_al = (const char *) ((uintptr_t) mslice & ~(uintptr_t) 15);
+    const int wt0 = (int) div_gqa(a, (uint32_t) wr0);   // first query position of the wave's rows
+    auto mrow_off = [&](int mr) -> uint32_t {           // mask row mr of the wave
+        int t = wt0 + mr, hq = 0;
+        if (a.m_ne2 != 1) {
+            const int r = wr0 + mr;
+            t = (int) div_gqa(a, (uint32_t) r);
+            hq = (kvh * a.gqa + (r - t * a.gqa)) % a.m_ne2;
+        }
+        return (uint32_t) (mslice - mslice_al) + (uint32_t) ((size_t) t * a.m_nb1 + (size_t) hq * a.m_nb2);
+    };
+    int n_mrows = 0;
+    uint32_t m_goff = 0, m_lane = 0;
+    if constexpr (MASKED) {
+        const int wlast = (wr0 + 15 < RW ? wr0 + 15 : RW - 1);
+        n_mrows = wr0 >= RW ? 1 : (a.m_ne2 == 1 ? (int) div_gqa(a, (uint32_t) wlast) - wt0 + 1 : wlast - wr0 + 1);
+        // DMA lane g: granule g % 3 of mask row g / 3 (lanes past the rows re-read the last granule)
+        const int g = lane < n_mrows * DEC_MGR ? lane : n_mrows * DEC_MGR - 1;
+        m_goff = (mrow_off(g / DEC_MGR) & ~15u) + 16u * (uint32_t) (g % DEC_MGR);
+        // the lane's own row in the stage's mask area
+        const int rl = wr0 + ln < RW ? wr0 + ln : wr0;
+        const int mi = a.m_ne2 == 1 ? (int) div_gqa(a, (uint32_t) rl) - wt0 : rl - wr0;
+        m_lane = (uint32_t) (DEC_MOFF + mi * DEC_MGR * 16) + (mrow_off(mi) & 15u) + 8u * (uint32_t) lg;
+    }
+
+    // ---- per-lane DMA offsets of a tile's pieces: piece p = 64s + lane is byte
+    //      16 (p % 17) of key p / 17; the same for every tile ----
+    uint32_t koff[DEC_TDMA], voff[DEC_TDMA];
+#pragma unroll
+    for (int s = 0; s < DEC_TDMA; s++) {
+        const uint32_t p = (uint32_t) (64 * s + lane), key = p / 17u, part = p - key * 17u;
+        koff[s] = key * (uint32_t) a.k_nb1 + part * 16u;
+        voff[s] = key * (uint32_t) a.v_nb1 + part * 16u;
+    }
+    const int64_t k_bytes = k_hi * (int64_t) a.k_nb1, v_bytes = k_hi * (int64_t) a.v_nb1;
+    // tile ti of the split (keys 16 ti .. 16 ti + 15) into stage buffer st, in
+    // two halves: the K rows (free once the tile's QK is done) and the V rows
+    // with the mask granules (free once its PV is done). Keys past the split
+    // arrive as zeros (buffer bounds) and are masked.
+    auto issue_k = [&](int ti, uint8_t * st) __attribute__((always_inline)) {
+        const int64_t key0 = k_lo + (int64_t) ti * DEC_TK;
+        const int64_t kc = key0 * (int64_t) a.k_nb1;
+        const v4i rk = make_rsrc(kbase + kc, (uint32_t) std::min<int64_t>(k_bytes - kc, 0xffffffffll));
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's reads of the stage are done
+#pragma unroll
+        for (int s = 0; s < DEC_TDMA; s++)
+            if (s < DEC_TDMA - 1 || lane < 16)
+                dma16_buf(rk, koff[s], __builtin_amdgcn_readfirstlane(lds_addr(st + 1024 * s)));
+    };
+    auto issue_v = [&](int ti, uint8_t * st) __attribute__((always_inline)) {
+        const int64_t key0 = k_lo + (int64_t) ti * DEC_TK;
+        const int64_t vc = key0 * (int64_t) a.v_nb1;
+        const v4i rv = make_rsrc(vbase + vc, (uint32_t) std::min<int64_t>(v_bytes - vc, 0xffffffffll));
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+#pragma unroll
+        for (int s = 0; s < DEC_TDMA; s++)
+            if (s < DEC_TDMA - 1 || lane < 16)
+                dma16_buf(rv, voff[s], __builtin_amdgcn_readfirstlane(lds_addr(st + DEC_KB + 1024 * s)));
+        if constexpr (MASKED) {
+            const v4i rm = make_rsrc(mslice_al + key0 * 2, (uint32_t) (a.m_slice + (uint32_t) (mslice - mslice_al) - key0 * 2));
+            if (lane < n_mrows * DEC_MGR)
+                dma16_buf(rm, m_goff, __builtin_amdgcn_readfirstlane(lds_addr(st + DEC_MOFF)));
+        }
+    };
+    auto issue_tile = [&](int ti, uint8_t * st) __attribute__((always_inline)) {
+        issue_k(ti, st);
+        issue_v(ti, st);
+    };
+
+    // ---- prologue: the block's query rows (f32, one wave DMA per row) into
+    //      stage 1, then the fused append (if any), then every wave's first tile ----
+    uint8_t * qstage = &ring[1][0][0];
+    {
+        const v4i rq = make_rsrc(a.q + (size_t) b * a.q_nb3, a.q_slice);
+#pragma unroll
+        for (int j = 0; j < (ROWS + DEC_WAVES - 1) / DEC_WAVES; j++) {
+            const int rl = wave + DEC_WAVES * j;
+            if (rl >= RW) break;
+            const uint32_t r = (uint32_t) rl;
+            const uint32_t t = div_gqa(a, r), h = (uint32_t) (kvh * a.gqa) + (r - t * (uint32_t) a.gqa);
+            dma16_buf(rq, t * (uint32_t) a.q_nb1 + h * (uint32_t) a.q_nb2 + 16u * (uint32_t) lane,
+                      __builtin_amdgcn_readfirstlane(lds_addr(qstage + rl * DEC_QROW)));
+        }
+    }
+    const int first0 = kg < n_tiles ? kg : -1, first1 = kg + KG < n_tiles ? kg + KG : -1;
+    if (a.app_n > 0) {
+        // as in k_fattn_q8_0: the blocks whose keys hold appended rows quantise
+        // their KV head's part of them first, and read them back only after
+        // their own stores are done
+        const int64_t alo = std::max<int64_t>(a.app_row0, k_lo), ahi = std::min<int64_t>(a.app_row0 + a.app_n, k_hi);
+        if (alo < ahi) {
+            const int units = (int) (ahi - alo) * NBLK * 2;
+            const int sub = threadIdx.x & 7;
+            for (int u0 = 0; u0 < units; u0 += DEC_WAVES * 8) {
+                const int uu0 = u0 + (int) (threadIdx.x >> 3);
+                const bool live = uu0 < units;
+                const int uu = live ? uu0 : 0;
+                const int tensor = uu & 1, jb = (uu >> 1) % NBLK;
+                const int64_t row = alo + (uu >> 1) / NBLK;
+                const float4 xv = *(const float4 *) ((tensor ? a.app_v : a.app_k) + (size_t) (row - a.app_row0) * a.app_nb1 +
+                                                     (size_t) (kvh * D + QK * jb + 4 * sub) * 4);
+                float x[4] = {xv.x, xv.y, xv.z, xv.w};
+                uint16_t d16;
+                float dqa;
+                const uint32_t q4 = dev::q8_quantize_lane4(x, a.x86 != 0, &d16, &dqa);
+                if (live) {
+                    char * bp = (char *) (tensor ? vbase + (size_t) row * a.v_nb1 : kbase + (size_t) row * a.k_nb1) + jb * QBLOCK;
+                    uint16_t * qp = (uint16_t *) (bp + 2 + sub * 4);
+                    qp[0] = (uint16_t) (q4 & 0xffffu);
+                    qp[1] = (uint16_t) (q4 >> 16);
+                    if (sub == 0) *(uint16_t *) bp = d16;
+                }
+            }
+            wait_vmcnt<0>();
+            __syncthreads();
+        }
+    }
+    if (first0 >= 0) issue_tile(first0, &ring[0][wave][0]);
+    if (first0 >= 0) wait_vmcnt<OPS>();                 // the query DMAs have landed (the tile's may not)
+    else wait_vmcnt<0>();
+    __syncthreads();
+
+    // ---- requantisation of the query rows (ggml's quantiser): wave w takes
+    //      q8_0 block w of every row, QL lanes per (row, block) ----
+    constexpr int QL = 64 / ROWS, QV = 32 / QL;
+    static_assert(NBLK == DEC_WAVES, "one block of all rows per wave");
+    static_assert(win_off(0) == 2 && win_off(1) == 20 && win_off(2) == 6 && win_off(3) == 8 && win_off(4) == 10 &&
+                  win_off(5) == 12 && win_off(6) == 14 && win_off(7) == 32, "the packed window offsets");
+    const int qrl = lane / QL, qh = lane % QL;
+    float qx[QV];
+    {
+        const float4 * src = (const float4 *) (qstage + qrl * DEC_QROW + (QK * wave + QV * qh) * 4);
+#pragma unroll
+        for (int m = 0; m < QV / 4; m++) {
+            const float4 v = qrl < RW ? src[m] : make_float4(0.f, 0.f, 0.f, 0.f);
+            qx[4 * m] = v.x; qx[4 * m + 1] = v.y; qx[4 * m + 2] = v.z; qx[4 * m + 3] = v.w;
+        }
+    }
+    __syncthreads();   // every query value is in registers: stage 1 becomes the window image
+    // window image [block][16-byte slice][row]: the 16 rows a lane group of the
+    // MFMA operand reads are consecutive 16-byte pieces (no bank conflicts)
+    uint8_t * qwin = qstage;
+    auto qslice = [&](int bb, int sl, int row) { return qwin + ((bb * 4 + sl) * ROWS + row) * 16; };
+    float * dql = (float *) (qstage + NBLK * QWIN * ROWS);        // [ROWS][NBLK]
+    {
+#pragma unroll
+        for (int z = 0; z < 4 / QL; z++) *(uint4 *) qslice(wave, qh * (4 / QL) + z, qrl) = make_uint4(0, 0, 0, 0);
+        wave_lds_sync();
+        uint32_t w[QV / 4];
+        uint16_t d16;
+        float dqv = 0.f;
+        if (a.x86) dev::q8_quantize_lanes<QV>(qx, true, w, &d16, &dqv);
+        else       dev::q8_quantize_lanes<QV>(qx, false, w, &d16, &dqv);
+        if (qrl < RW) {
+            // win_off(wave), read from a packed table (no scalar branch chain)
+            const int woff = (int) ((0x200E0C0A08061402ull >> (8 * wave)) & 0xff);
+#pragma unroll
+            for (int m = 0; m < QV / 2; m++) {   // 2-byte pieces never straddle a slice
+                const int o = woff + QV * qh + 2 * m;
+                *(uint16_t *) (qslice(wave, o >> 4, qrl) + (o & 15)) = (uint16_t) (w[m >> 1] >> (16 * (m & 1)));
+            }
+        }
+        if (qh == 0) dql[qrl * NBLK + wave] = qrl < RW ? dqv * (a.scale * LOG2E) : 0.f;
+    }
+    __syncthreads();
+    const int rl_lane = wr0 + ln;
+    v4i qw[NBLK];
+    float dq[NBLK];
+#pragma unroll
+    for (int bb = 0; bb < NBLK; bb++) {
+        qw[bb] = *(const v4i *) qslice(bb, lg, rl_lane);
+        dq[bb] = dql[rl_lane * NBLK + bb];
+    }
+#pragma unroll
+    for (int bb = 0; bb < NBLK; bb++) asm volatile("" : "+v"(qw[bb]), "+v"(dq[bb]));
+    __syncthreads();   // every wave has its operands: stage 1 is free
+    if (first1 >= 0) issue_tile(first1, &ring[1][wave][0]);
+
+    // ---- the key loop ----
+    v4f O[NBLK][2];
+    float m_run = -INFINITY, l_run = 0.f;
+#pragma unroll
+    for (int bb = 0; bb < NBLK; bb++) { O[bb][0] = v4f{0, 0, 0, 0}; O[bb][1] = v4f{0, 0, 0, 0}; }
+    uint16_t (*sw)[NBLK][DEC_TK] = scl[wave];
+
+    // tile ti from stage st; nx >= 0: tile nx goes into the same stage, its K
+    // rows as soon as the QK is done, its V rows and mask after the PV
+    auto tile_step = [&](int ti, uint8_t * st, int nx) __attribute__((always_inline)) {
+        const int kin = ti * DEC_TK + lg * 4;   // the lane's first key, within the split
+        // the tile's block scales, transposed to [tensor][block][key]
+        {
+            const uint8_t * src = st + (lane >> 3) * SEG + (lane & 7) * QBLOCK;
+            uint16_t * dstw = &sw[0][lane & 7][lane >> 3];
+            uint16_t sv[4];
+#pragma unroll
+            for (int n = 0; n < 4; n++) sv[n] = *(const uint16_t *) (src + (n >> 1) * DEC_KB + (n & 1) * 8 * SEG);
+#pragma unroll
+            for (int n = 0; n < 4; n++) dstw[(n >> 1) * NBLK * DEC_TK + (n & 1) * 8] = sv[n];
+        }
+        wave_lds_sync();
+        // ---- S = K Q^T: keys (MFMA rows) x the wave's 16 query rows. Each
+        //      block's MFMA is issued two blocks ahead of its scaling, so the
+        //      matrix core runs while the vector unit scales ----
+        float s[4] = {0.f, 0.f, 0.f, 0.f};
+        {
+            v4i kA[NBLK];
+            uint2 dk[NBLK];
+            const uint8_t * krow = st + ln * SEG + 16 * lg;
+#pragma unroll
+            for (int bb = 0; bb < NBLK; bb++) {
+                kA[bb] = *(const v4i *) (krow + 16 * win_piece(bb));
+                dk[bb] = *(const uint2 *) &sw[0][bb][lg * 4];
+            }
+            v4i cc[NBLK];
+            cc[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kA[0], qw[0], v4i{0, 0, 0, 0}, 0, 0, 0);
+            cc[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kA[1], qw[1], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int bb = 0; bb < NBLK; bb++) {
+                if (bb + 2 < NBLK)
+                    cc[bb + 2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kA[bb + 2], qw[bb + 2], v4i{0, 0, 0, 0}, 0, 0, 0);
+                const float d = dq[bb];
+                s[0] = __builtin_fmaf((float) cc[bb][0], mul_f16lo(d, dk[bb].x), s[0]);
+                s[1] = __builtin_fmaf((float) cc[bb][1], mul_f16hi(d, dk[bb].x), s[1]);
+                s[2] = __builtin_fmaf((float) cc[bb][2], mul_f16lo(d, dk[bb].y), s[2]);
+                s[3] = __builtin_fmaf((float) cc[bb][3], mul_f16hi(d, dk[bb].y), s[3]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        if (nx >= 0) issue_k(nx, st);
+        // ---- mask, online softmax (base 2) ----
+        float p[4];
+        uint32_t p16[2];
+        {
+            float x[4];
+            if constexpr (MASKED) {
+                const uint16_t * mp = (const uint16_t *) (st + m_lane);
+#pragma unroll
+                for (int i = 0; i < 4; i++) x[i] = fma_f16lo((uint32_t) mp[i], LOG2E, s[i]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++) x[i] = s[i];
+            }
+            if ((ti + 1) * DEC_TK > span) {   // the split's last tile: keys past its end
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (kin + i >= span) x[i] = -INFINITY;
+            }
+            float mloc = vmax(vmax(x[0], x[1]), vmax(x[2], x[3]));
+            mloc = xmax_lanes16_32(mloc);
+            const bool grow = mloc > m_run + RESCALE_SLACK;
+            float alpha = 1.f;
+            if (grow) {
+                alpha = __builtin_amdgcn_exp2f(m_run - mloc);
+                m_run = mloc;
+            }
+            const float m_use = m_run == -INFINITY ? 0.f : m_run;
+            float lsum = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                p[i] = __builtin_amdgcn_exp2f(x[i] - m_use);
+                lsum += p[i];
+            }
+            l_run = l_run * alpha + lsum;
+            p16[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p[0], p[1]));
+            p16[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p[2], p[3]));
+            if (__any(grow)) {
+                // a real branch (taken when the running max moves by more than
+                // the slack): if-converted, every tile would pay the 64 multiplies
+                asm volatile("" ::: "memory");
+#pragma unroll
+                for (int bb = 0; bb < NBLK; bb++) { O[bb][0] *= alpha; O[bb][1] *= alpha; }
+            }
+        }
+        // ---- O += V^T (P d_v) per V block. All V reads first; then block b's
+        //      MFMAs are interleaved with the conversions of block b + 1, so
+        //      the matrix core runs while the vector unit converts ----
+        const uint8_t * vrow = st + DEC_KB + (lg * 4) * SEG + 2 + 2 * ln;
+        uint32_t w[NBLK][4];
+        uint2 dv2[NBLK];
+#pragma unroll
+        for (int bb = 0; bb < NBLK; bb++) {
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) w[bb][jj] = *(const uint16_t *) (vrow + jj * SEG + bb * QBLOCK);
+            dv2[bb] = *(const uint2 *) &sw[1][bb][lg * 4];
+        }
+        uint32_t a0[2], a1[2], bh[2], bl[2];
+        {
+            const uint32_t dv[2] = {dv2[0].x, dv2[0].y};
+            cvt_v_block(w[0], a0, a1);
+            pdv_hilo(p, p16, dv, bh, bl);
+        }
+#pragma unroll
+        for (int bb = 0; bb < NBLK; bb++) {
+            const v4h A0 = __builtin_bit_cast(v4h, make_uint2(a0[0], a0[1]));
+            const v4h A1 = __builtin_bit_cast(v4h, make_uint2(a1[0], a1[1]));
+            const v4h Bh = __builtin_bit_cast(v4h, make_uint2(bh[0], bh[1]));
+            const v4h Bl = __builtin_bit_cast(v4h, make_uint2(bl[0], bl[1]));
+            O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x16f16(A0, Bh, O[bb][0], 0, 0, 0);
+            O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A1, Bh, O[bb][1], 0, 0, 0);
+            if (bb + 1 < NBLK) {
+                const uint32_t dv[2] = {dv2[bb + 1].x, dv2[bb + 1].y};
+                cvt_v_block(w[bb + 1], a0, a1);
+                pdv_hilo(p, p16, dv, bh, bl);
+            }
+            O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x16f16(A0, Bl, O[bb][0], 0, 0, 0);
+            O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A1, Bl, O[bb][1], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (nx >= 0) issue_v(nx, st);
+    };
+    // key group kg takes tiles kg, kg + KG, ... in that order (a fixed order:
+    // the result is reproducible bit for bit); the two stages alternate. The
+    // DMAs of the tile after next follow each tile (its K half mid-step), so
+    // the ones issued after a tile's own are exactly the next tile's.
+    for (int j = 0; kg + j * KG < n_tiles; j += 2) {
+        const int t0 = kg + j * KG, t1 = t0 + KG, t2 = t1 + KG, t3 = t2 + KG;
+        if (t1 < n_tiles) wait_vmcnt<OPS>();
+        else wait_vmcnt<0>();
+        tile_step(t0, &ring[0][wave][0], t2 < n_tiles ? t2 : -1);
+        if (t1 < n_tiles) {
+            if (t2 < n_tiles) wait_vmcnt<OPS>();
+            else wait_vmcnt<0>();
+            tile_step(t1, &ring[1][wave][0], t3 < n_tiles ? t3 : -1);
+        }
+    }
+
+    // ---- merge the key groups of each row tile (as k_fattn_q8_0's epilogue) ----
+    {
+        const float l = sum_lanes16_32(l_run);
+        float2 * mlw = (float2 *) &scl[wave][0][0][0];
+        if (lg == 0) mlw[ln] = make_float2(m_run, l);
+    }
+    __syncthreads();   // every wave is done with its ring stages, and its (max, sum) are out
+    float M = -INFINITY, L = 0.f;
+#pragma unroll
+    for (int k2 = 0; k2 < KG; k2++) M = xmax(M, ((const float2 *) &scl[k2 * RT + tile][0][0][0])[ln].x);
+#pragma unroll
+    for (int k2 = 0; k2 < KG; k2++) {
+        const float2 e = ((const float2 *) &scl[k2 * RT + tile][0][0][0])[ln];
+        L += e.x == -INFINITY ? 0.f : e.y * exp2f(e.x - M);
+    }
+    const float fw = m_run == -INFINITY ? 0.f : exp2f(m_run - M);
+    int tid_e = (int) threadIdx.x;
+    asm volatile("" : "+v"(tid_e));
+    const int ln_e = tid_e & 15, lg_e = (tid_e >> 4) & 3;
+    const int rl = wr0 + ln_e;
+    float * ob = (float *) &ring[0][0][0];
+    const int orow = rl * DEC_OBS + 8 * lg_e;
+    float4 acc[NBLK][2];
+#pragma unroll
+    for (int bb = 0; bb < NBLK; bb++) {
+        const v4f o0 = O[bb][0] * fw, o1 = O[bb][1] * fw;
+        acc[bb][0] = make_float4(o0[0], o1[0], o0[1], o1[1]);
+        acc[bb][1] = make_float4(o0[2], o1[2], o0[3], o1[3]);
+    }
+    if (kg != 0) {
+        float * d = ob + (kg - 1) * ROWS * DEC_OBS + orow;
+#pragma unroll
+        for (int bb = 0; bb < NBLK; bb++) {
+            *(float4 *) (d + 32 * bb) = acc[bb][0];
+            *(float4 *) (d + 32 * bb + 4) = acc[bb][1];
+        }
+    }
+    __syncthreads();
+    if (kg != 0 || rl >= RW) return;
+#pragma unroll 1
+    for (int k2 = 0; k2 < KG - 1; k2++) {
+#pragma unroll
+        for (int bb = 0; bb < NBLK; bb++) {
+            const float * src = ob + k2 * ROWS * DEC_OBS + orow + 32 * bb;
+            const float4 x0 = *(const float4 *) src, x1 = *(const float4 *) (src + 4);
+            acc[bb][0].x += x0.x; acc[bb][0].y += x0.y; acc[bb][0].z += x0.z; acc[bb][0].w += x0.w;
+            acc[bb][1].x += x1.x; acc[bb][1].y += x1.y; acc[bb][1].z += x1.z; acc[bb][1].w += x1.w;
+        }
+    }
+    const size_t bh = (size_t) b * a.nh_kv + kvh;
+    const int r = rl;
+    const int tq = (int) div_gqa(a, (uint32_t) r), h = kvh * a.gqa + (r - tq * a.gqa);
+    float * out;
+    float oscale;
+    const bool nsplit = a.ns > 1;
+    if (!nsplit) {
+        out = a.dst + (((size_t) b * a.T + tq) * a.nh + h) * D + 8 * lg_e;
+        oscale = L > 0.f ? 1.f / L : 0.f;
+    } else {
+        out = a.part_o + ((bh * a.ns + split) * a.R + r) * D + 8 * lg_e;
+        oscale = 1.f;
+        if (lg_e == 0) {
+            float2 * mlp = &a.part_ml[(bh * a.ns + split) * a.R + r];
+            __builtin_nontemporal_store(M, &mlp->x);
+            __builtin_nontemporal_store(L, &mlp->y);
+        }
+    }
+#pragma unroll
+    for (int bb = 0; bb < NBLK; bb++) {
+        const float4 p0 = acc[bb][0], p1 = acc[bb][1];
+        const float4 w0 = make_float4(p0.x * oscale, p0.y * oscale, p0.z * oscale, p0.w * oscale);
+        const float4 w1 = make_float4(p1.x * oscale, p1.y * oscale, p1.z * oscale, p1.w * oscale);
+        if (nsplit) {
+            store_nt4(out + 32 * bb, w0);
+            store_nt4(out + 32 * bb + 4, w1);
+        } else if (a.dst_vec) {
+            *(float4 *) (out + 32 * bb) = w0;
+            *(float4 *) (out + 32 * bb + 4) = w1;
+        } else {
+            float * o = out + 32 * bb;
+            o[0] = w0.x; o[1] = w0.y; o[2] = w0.z; o[3] = w0.w;
+            o[4] = w1.x; o[5] = w1.y; o[6] = w1.z; o[7] = w1.w;
+        }
+    }
+}
+
 // ---------------------------------------------------------------- planning
 
 // Attention kernel shapes: waves per block, query tiles, keys per wave.
 enum fa_kind {
+    FA_DEC,       // k_fa_dec: at most 32 query rows per KV head, 8 waves, one block per CU
     FA_P4_T1,     // 4 waves, one tile, 64-key chunks, two blocks per CU
     FA_P4_T2,     // 4 waves, two tiles, 32 keys per wave, two blocks per CU; mask tiles of
                   // more than MASK_ROWS_PAIR rows go to 8 waves over the same 64-key chunks
@@ -1197,7 +1702,11 @@ uint32_t recip32(int64_t d) {
 // kernel that spills to scratch would break that count: refuse to run one.
 int check_no_scratch() {
     static const int rc = [] {
-        for (const void * f : {(const void *) k_fattn_q8_0<2, true, WAVES, 16, false>,
+        for (const void * f : {(const void *) k_fa_dec<1, false, false>, (const void *) k_fa_dec<1, true, false>,
+                               (const void *) k_fa_dec<2, false, false>, (const void *) k_fa_dec<2, true, false>,
+                               (const void *) k_fa_dec<1, false, true>, (const void *) k_fa_dec<1, true, true>,
+                               (const void *) k_fa_dec<2, false, true>, (const void *) k_fa_dec<2, true, true>,
+                               (const void *) k_fattn_q8_0<2, true, WAVES, 16, false>,
                                (const void *) k_fattn_q8_0<1, false, WAVES_PAIR, 16, false>,
                                (const void *) k_fattn_q8_0<1, true, WAVES_PAIR, 16, false>,
                                (const void *) k_fattn_q8_0<2, false, WAVES_PAIR, 32, false>,
@@ -1266,28 +1775,34 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
         if (mask_slice_bytes(*mask) >= (size_t(1) << 31))
             return set_error(QWFN_ENOTSUP, "flash_attn_ext: mask batch slices must be below 2 GiB");
     }
-    // Query rows per block: one or two 16-row tiles, in 4-wave blocks, two per
-    // CU (their prologues and phases overlap).
+    // Query rows per block: one or two 16-row tiles. Up to 32 rows per KV head
+    // (decode, verify, batch decode) take k_fa_dec, 8-wave blocks, one per CU;
+    // longer query blocks k_fattn_q8_0's 4-wave blocks, two per CU (their
+    // prologues and phases overlap).
     const int rw = R > 16 ? 32 : 16;
     const int64_t B = q->ne[3];
-    pl->kind = rw == 16 ? FA_P4_T1 : FA_P4_T2;
+    const bool dec = R <= 32;
+    pl->kind = dec ? FA_DEC : rw == 16 ? FA_P4_T1 : FA_P4_T2;
     pl->R = (int32_t) R;
     pl->rw = rw;
     pl->RT = rw / 16;
     pl->n_rg = (int32_t) ((R + rw - 1) / rw);
     pl->gqa = (int32_t) gqa;
-    const int64_t ck = pl->kind == FA_P4_T1 ? fa_cfg<1, false, WAVES_PAIR, 16>::CK : fa_cfg<2, false, WAVES_PAIR, 32>::CK;
-    // Splits: about one block per CU slot (512), each at least one chunk.
-    const int64_t target_blocks = 512;
+    // k_fa_dec: splits of whole 16-key tiles, at least one tile per key group;
+    // k_fattn_q8_0: whole chunks.
+    const int64_t ck = dec ? DEC_TK : pl->kind == FA_P4_T1 ? fa_cfg<1, false, WAVES_PAIR, 16>::CK : fa_cfg<2, false, WAVES_PAIR, 32>::CK;
+    const int64_t min_split = dec ? DEC_TK * (DEC_WAVES / pl->RT) : ck;
+    // Splits: about one block per CU slot (256 for k_fa_dec, 512 otherwise).
+    const int64_t target_blocks = dec ? 256 : 512;
     int64_t ns = std::max<int64_t>(1, target_blocks / std::max<int64_t>(1, nh_kv * B * pl->n_rg));
-    ns = std::min<int64_t>(ns, std::max<int64_t>(1, (n_kv + ck - 1) / ck));
+    ns = std::min<int64_t>(ns, std::max<int64_t>(1, (n_kv + min_split - 1) / min_split));
     if (const int32_t force = g_force_splits.load(std::memory_order_relaxed)) ns = force;
     ns = std::min<int64_t>(ns, std::max<int64_t>(1, ns_cap));
     // Splits are whole chunks. When the keys exceed two or more chunks per
     // split by less than one chunk (n_kv = 2^k + T), the last split takes the
     // rest; otherwise every split rounds up and there are fewer.
     int64_t split_len = n_kv / (ns * ck) * ck;
-    if (split_len < 2 * ck || n_kv - ns * split_len >= ck) {
+    if (split_len < (dec ? min_split : 2 * ck) || n_kv - ns * split_len >= (dec ? min_split : ck)) {
         split_len = (n_kv + ns - 1) / ns;
         split_len = std::max<int64_t>(ck, (split_len + ck - 1) / ck * ck);
         ns = std::max<int64_t>(1, (n_kv + split_len - 1) / split_len);
@@ -1314,7 +1829,7 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
         for (int64_t b = 0; b < B; b++) {
             const int64_t nk = seq_n_kv[b];
             int64_t nsb = total > 0 ? std::max<int64_t>(1, (units * nk + total / 2) / total) : 1;
-            nsb = std::min<int64_t>(nsb, std::max<int64_t>(1, (nk + ck - 1) / ck));
+            nsb = std::min<int64_t>(nsb, std::max<int64_t>(1, (nk + min_split - 1) / min_split));
             int64_t sl = (nk + nsb - 1) / nsb;
             sl = std::max<int64_t>(ck, (sl + ck - 1) / ck * ck);
             nsb = std::max<int64_t>(1, (nk + sl - 1) / sl);
@@ -1516,6 +2031,7 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
         a.app_n = (int32_t) app->src_k->ne[1];
     }
 
+    if (pl.kind == FA_DEC) a.n_rg = 1;
     const int64_t n_units = a.ragged ? (int64_t) a.r_units : (int64_t) a.B * a.ns;
     const int64_t units = n_units >= 8 ? (n_units + 7) / 8 * 8 : n_units;
     const int64_t hgn = (int64_t) a.nh_kv * a.n_rg;
@@ -1529,7 +2045,19 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
     hipStream_t st = as_stream(stream);
     const bool mt = a.mask_mode == MASK_TILE;
     const dim3 g((unsigned) grid), b8(WAVES * 64), b4(WAVES_PAIR * 64);
-    if (a.ragged) {
+    if (pl.kind == FA_DEC) {
+        const dim3 bd(DEC_WAVES * 64);
+        const bool msk = a.mask != nullptr;
+#define QWFN_DEC(RT_, M_, RG_) hipLaunchKernelGGL((k_fa_dec<RT_, M_, RG_>), g, bd, 0, st, a)
+        if (pl.RT == 1) {
+            if (a.ragged) { if (msk) QWFN_DEC(1, true, true); else QWFN_DEC(1, false, true); }
+            else          { if (msk) QWFN_DEC(1, true, false); else QWFN_DEC(1, false, false); }
+        } else {
+            if (a.ragged) { if (msk) QWFN_DEC(2, true, true); else QWFN_DEC(2, false, true); }
+            else          { if (msk) QWFN_DEC(2, true, false); else QWFN_DEC(2, false, false); }
+        }
+#undef QWFN_DEC
+    } else if (a.ragged) {
         // per-sequence splits: the 4-wave kernels (and the 8-wave mask-tile one)
         switch (pl.kind) {
             case FA_P4_T1:
@@ -1544,6 +2072,8 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
         }
     } else {
     switch (pl.kind) {
+        case FA_DEC:
+            break;
         case FA_P4_T1:
             if (mt) hipLaunchKernelGGL((k_fattn_q8_0<1, true, WAVES_PAIR, 16, false>), g, b4, 0, st, a);
             else    hipLaunchKernelGGL((k_fattn_q8_0<1, false, WAVES_PAIR, 16, false>), g, b4, 0, st, a);
