@@ -193,6 +193,33 @@ int qwfn_flash_attn_ext_q8_0_seq(const qwfn_tensor * q, const qwfn_tensor * k, c
                                  const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes,
                                  const int64_t * seq_n_kv, void * stream);
 
+/* Sparse decode attention over selected cache cells, the gather fused into
+ * the attention: replaces the raw get_rows of the selected cells' K and V
+ * words (qsa_gather, qwfn_graph.cpp:632-645), the cell mask
+ * (:668-675, padding :688-693) and the ggml_flash_attn_ext over the gathered
+ * copy (:694-699). The rows are read straight from the cache; nothing is
+ * materialised.
+ *
+ * k, v: the q8_0 cache views [256, n_rows, n_head_kv, 1] (nb1 = the cache row
+ * stride, nb2 = the head offset), n_rows * row stride < 2 GiB, 1 <= n_head_kv
+ * <= 8. cells: device int32, 16-byte aligned; KV head h attends the rows
+ * cells[h * cell_stride + j], j < n_cells[h] (n_cells: host array of
+ * n_head_kv counts). cell_stride = 0 gives every head the same list, the
+ * reference's one list shared by both KV heads; otherwise it is a multiple of
+ * 4 and at least every count. Query t (q [256, T, n_head, 1], T * n_head /
+ * n_head_kv <= 32) sees a cell only if the cell is at most pos0 + t (cells are
+ * positions, qwfn_engine.cpp:682). A cell outside [0, n_rows) is masked and
+ * sets bit 1 (get_rows index) of qwfn_device_status. Lists may repeat
+ * cells (each copy counts, as ggml's attention over a gathered copy counts
+ * it) and need no padding. A query row that sees no cell is 0. Size ws with
+ * qwfn_fattn_workspace_size_cells (ws NULL: the library's buffer). */
+size_t qwfn_fattn_workspace_size_cells(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
+                                       const int64_t * n_cells, int64_t cell_stride);
+int qwfn_flash_attn_ext_q8_0_cells(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
+                                   const int32_t * cells, const int64_t * n_cells, int64_t cell_stride, int64_t pos0,
+                                   float scale, const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes,
+                                   void * stream);
+
 /* The layer's K and V append followed by its attention, in one launch: the
  * two ggml_cpy / ggml_set_rows nodes that write the step's rows
  * (qwfn_graph.cpp:376-383, :623-624, :916-921) and the ggml_flash_attn_ext

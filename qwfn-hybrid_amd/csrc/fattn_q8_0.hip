@@ -67,6 +67,7 @@ constexpr int WAVES_PAIR = 4;          // wavefronts per block, two blocks per C
 constexpr int QWIN   = 64;             // bytes of one block's query window
 constexpr int MAX_SPLITS = 1024;       // key splits per (batch, KV head, row group)
 constexpr int RAGGED_MAX_B = 16;       // sequences of a call with per-sequence key counts
+constexpr int GATHER_MAX_HEADS = 8;    // KV heads of a call with per-head cell lists
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float RESCALE_SLACK = 8.f;   // log2 units the running max may lag the true max
 constexpr int PV_BATCH = 4;            // 16-key V block tiles whose LDS reads are issued together
@@ -156,6 +157,15 @@ struct fa_args {
     int32_t  r_ns[RAGGED_MAX_B];
     int32_t  r_split_len[RAGGED_MAX_B];
     int64_t  r_n_kv[RAGGED_MAX_B];
+    // gathered keys (k_fa_dec<.., GATHER>): KV head h attends cache rows
+    // g_cells[h * g_stride + j], j < g_n[h]; query t sees a row only if it is
+    // at most g_pos0 + t. The cache has g_rows rows.
+    const int32_t * g_cells;
+    int64_t  g_stride;
+    int64_t  g_pos0;
+    int64_t  g_rows;
+    int32_t  g_n[GATHER_MAX_HEADS];
+    uint32_t * status;     // device flags (DEVERR_GET_ROWS_INDEX: a cell outside the cache)
 };
 
 // x / d through m = ceil(2^32 / d): floor(x * m / 2^32) = floor(x / d) while
@@ -1172,10 +1182,15 @@ constexpr int DEC_MGR   = 3;                          // 16-byte granules per ma
 constexpr int DEC_STAGE = DEC_MOFF + 1024;            // 9728 bytes
 constexpr int DEC_OBS   = D + 4;                      // merge buffer row stride (floats)
 constexpr int DEC_QROW  = 1024 + 16;                  // query row stride in the prologue's staging (bank spread)
+constexpr int DEC_GATHER_SPLIT = 512;                 // cells of a block's split, at most (gathered keys)
 static_assert(DEC_KB / 16 - 64 * (DEC_TDMA - 1) == 16, "the last DMA of a tensor has 16 lanes");
 static_assert(16 * DEC_MGR <= 64, "a wave's mask rows of a tile are one DMA");
 
-template <int RT, bool MASKED, bool RG>
+// GATHER: the keys of KV head h are the cache rows its cell list names (the
+// reference's raw get_rows of the selected cells, qwfn_graph.cpp:632-651,
+// fused: the rows are DMA'd straight from the cache), and a query sees a row
+// only if it is at most its own position (the decode cell mask, :668-675)
+template <int RT, bool MASKED, bool RG, bool GATHER>
 __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
     constexpr int ROWS = 16 * RT, KG = DEC_WAVES / RT;
     constexpr int OPS = 2 * DEC_TDMA + (MASKED ? 1 : 0);   // DMAs per tile of one wave
@@ -1184,6 +1199,9 @@ __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
     // the prologue uses for the query rows and their window image
     __shared__ __attribute__((aligned(16))) uint8_t ring[2][DEC_WAVES][DEC_STAGE];
     __shared__ __attribute__((aligned(16))) uint16_t scl[DEC_WAVES][2][NBLK][DEC_TK];
+    // GATHER: the block's part of its KV head's cell list
+    __shared__ __attribute__((aligned(16))) int32_t gcell[GATHER ? DEC_GATHER_SPLIT : 4];
+    static_assert(!(GATHER && (MASKED || RG)), "gathered keys carry their own mask, one sequence");
     static_assert(ROWS * DEC_QROW <= DEC_WAVES * DEC_STAGE, "query rows fit stage 1");
     static_assert(ROWS * NBLK * QWIN + ROWS * NBLK * 4 <= DEC_WAVES * DEC_STAGE, "query image fits stage 1");
     static_assert((KG - 1) * ROWS * DEC_OBS * 4 <= 2 * DEC_WAVES * DEC_STAGE, "merge buffers fit the ring");
@@ -1229,6 +1247,15 @@ __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
         k_lo = (int64_t) split * a.split_len;
         const int64_t e = k_lo + a.split_len;
         k_hi = split == a.ns - 1 ? a.n_kv : (a.n_kv < e ? a.n_kv : e);
+    }
+    if constexpr (GATHER) {
+        // this head's own cell count (constant indices keep the table scalar)
+        int64_t nh = 0;
+#pragma unroll
+        for (int i = 0; i < GATHER_MAX_HEADS; i++)
+            if (i == kvh) nh = a.g_n[i];
+        k_hi = k_hi < nh ? k_hi : nh;
+        k_lo = k_lo < k_hi ? k_lo : k_hi;
     }
     const int span = (int) (k_hi - k_lo);
     const int n_tiles = (span + DEC_TK - 1) / DEC_TK;
@@ -1277,29 +1304,66 @@ __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
         voff[s] = key * (uint32_t) a.v_nb1 + part * 16u;
     }
     const int64_t k_bytes = k_hi * (int64_t) a.k_nb1, v_bytes = k_hi * (int64_t) a.v_nb1;
+    // GATHER: the DMA offsets of tile ti follow its cells (in LDS): piece p of
+    // slot s is byte 16 (p % 17) of row gcell[16 ti + p / 17]; a cell outside
+    // the cache, or a key past the split, gets an offset past the buffer, so
+    // its bytes arrive as zeros (and the key is masked); the cache is below
+    // 2 GiB per call, so 2^31 is past it
+    const uint32_t g_kbytes = GATHER ? (uint32_t) (a.g_rows * (int64_t) a.k_nb1) : 0u;
+    const uint32_t g_vbytes = GATHER ? (uint32_t) (a.g_rows * (int64_t) a.v_nb1) : 0u;
+    auto gather_off = [&](int ti, int s, uint32_t nb1) -> uint32_t {
+        const uint32_t p = (uint32_t) (64 * s + lane), key = p / 17u, part = p - key * 17u;
+        const int kk = ti * DEC_TK + (int) key;
+        const uint32_t row = kk < span ? (uint32_t) gcell[kk] : 0xffffffffu;
+        return row < (uint32_t) a.g_rows ? row * nb1 + part * 16u : 0x80000000u;
+    };
     // tile ti of the split (keys 16 ti .. 16 ti + 15) into stage buffer st, in
     // two halves: the K rows (free once the tile's QK is done) and the V rows
     // with the mask granules (free once its PV is done). Keys past the split
     // arrive as zeros (buffer bounds) and are masked.
     auto issue_k = [&](int ti, uint8_t * st) __attribute__((always_inline)) {
-        const int64_t key0 = k_lo + (int64_t) ti * DEC_TK;
-        const int64_t kc = key0 * (int64_t) a.k_nb1;
-        const v4i rk = make_rsrc(kbase + kc, (uint32_t) std::min<int64_t>(k_bytes - kc, 0xffffffffll));
-        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's reads of the stage are done
+        if constexpr (GATHER) {
+            uint32_t go[DEC_TDMA];
 #pragma unroll
-        for (int s = 0; s < DEC_TDMA; s++)
-            if (s < DEC_TDMA - 1 || lane < 16)
-                dma16_buf(rk, koff[s], __builtin_amdgcn_readfirstlane(lds_addr(st + 1024 * s)));
+            for (int s = 0; s < DEC_TDMA; s++) go[s] = gather_off(ti, s, (uint32_t) a.k_nb1);
+            const v4i rk = make_rsrc(kbase, g_kbytes);
+            __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the cells are read, this wave's reads of the stage are done
+#pragma unroll
+            for (int s = 0; s < DEC_TDMA; s++)
+                if (s < DEC_TDMA - 1 || lane < 16)
+                    dma16_buf(rk, go[s], __builtin_amdgcn_readfirstlane(lds_addr(st + 1024 * s)));
+        } else {
+            const int64_t key0 = k_lo + (int64_t) ti * DEC_TK;
+            const int64_t kc = key0 * (int64_t) a.k_nb1;
+            const v4i rk = make_rsrc(kbase + kc, (uint32_t) std::min<int64_t>(k_bytes - kc, 0xffffffffll));
+            __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's reads of the stage are done
+#pragma unroll
+            for (int s = 0; s < DEC_TDMA; s++)
+                if (s < DEC_TDMA - 1 || lane < 16)
+                    dma16_buf(rk, koff[s], __builtin_amdgcn_readfirstlane(lds_addr(st + 1024 * s)));
+        }
     };
     auto issue_v = [&](int ti, uint8_t * st) __attribute__((always_inline)) {
         const int64_t key0 = k_lo + (int64_t) ti * DEC_TK;
-        const int64_t vc = key0 * (int64_t) a.v_nb1;
-        const v4i rv = make_rsrc(vbase + vc, (uint32_t) std::min<int64_t>(v_bytes - vc, 0xffffffffll));
-        __builtin_amdgcn_s_waitcnt(0xC07F);
+        if constexpr (GATHER) {
+            uint32_t go[DEC_TDMA];
 #pragma unroll
-        for (int s = 0; s < DEC_TDMA; s++)
-            if (s < DEC_TDMA - 1 || lane < 16)
-                dma16_buf(rv, voff[s], __builtin_amdgcn_readfirstlane(lds_addr(st + DEC_KB + 1024 * s)));
+            for (int s = 0; s < DEC_TDMA; s++) go[s] = gather_off(ti, s, (uint32_t) a.v_nb1);
+            const v4i rv = make_rsrc(vbase, g_vbytes);
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+#pragma unroll
+            for (int s = 0; s < DEC_TDMA; s++)
+                if (s < DEC_TDMA - 1 || lane < 16)
+                    dma16_buf(rv, go[s], __builtin_amdgcn_readfirstlane(lds_addr(st + DEC_KB + 1024 * s)));
+        } else {
+            const int64_t vc = key0 * (int64_t) a.v_nb1;
+            const v4i rv = make_rsrc(vbase + vc, (uint32_t) std::min<int64_t>(v_bytes - vc, 0xffffffffll));
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+#pragma unroll
+            for (int s = 0; s < DEC_TDMA; s++)
+                if (s < DEC_TDMA - 1 || lane < 16)
+                    dma16_buf(rv, voff[s], __builtin_amdgcn_readfirstlane(lds_addr(st + DEC_KB + 1024 * s)));
+        }
         if constexpr (MASKED) {
             const v4i rm = make_rsrc(mslice_al + key0 * 2, (uint32_t) (a.m_slice + (uint32_t) (mslice - mslice_al) - key0 * 2));
             if (lane < n_mrows * DEC_MGR)
@@ -1327,6 +1391,18 @@ __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
         }
     }
     const int first0 = kg < n_tiles ? kg : -1, first1 = kg + KG < n_tiles ? kg + KG : -1;
+    __shared__ uint32_t g_bad;   // GATHER: a cell of the block lies outside the cache
+    if constexpr (GATHER) {
+        // the block's cells [k_lo, k_hi): wave w takes 256-cell pieces w, w + NW, ...
+        const int32_t * cl = a.g_cells + (size_t) kvh * a.g_stride + k_lo;
+        const v4i rc = make_rsrc(cl, (uint32_t) span * 4u);
+        for (int m = wave; m * 256 < span; m += DEC_WAVES)
+            dma16_buf(rc, (uint32_t) (m * 1024 + 16 * lane), __builtin_amdgcn_readfirstlane(lds_addr(&gcell[m * 256])));
+        if (threadIdx.x == 0) g_bad = 0;
+        wait_vmcnt<0>();   // this wave's cells (and query rows) have landed
+        __syncthreads();   // ... and every wave's: the first tiles' DMA offsets follow them
+        if ((int) threadIdx.x < span && (uint32_t) gcell[threadIdx.x] >= (uint32_t) a.g_rows) g_bad = 1;
+    }
     if (a.app_n > 0) {
         // as in k_fattn_q8_0: the blocks whose keys hold appended rows quantise
         // their KV head's part of them first, and read them back only after
@@ -1426,6 +1502,8 @@ __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
 #pragma unroll
     for (int bb = 0; bb < NBLK; bb++) { O[bb][0] = v4f{0, 0, 0, 0}; O[bb][1] = v4f{0, 0, 0, 0}; }
     uint16_t (*sw)[NBLK][DEC_TK] = scl[wave];
+    // GATHER: the position of the lane's query row
+    const int64_t q_pos = GATHER ? a.g_pos0 + (int64_t) div_gqa(a, (uint32_t) (wr0 + ln)) : 0;
 
     // tile ti from stage st; nx >= 0: tile nx goes into the same stage, its K
     // rows as soon as the QK is done, its V rows and mask after the PV
@@ -1480,6 +1558,14 @@ __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
                 const uint16_t * mp = (const uint16_t *) (st + m_lane);
 #pragma unroll
                 for (int i = 0; i < 4; i++) x[i] = fma_f16lo((uint32_t) mp[i], LOG2E, s[i]);
+            } else if constexpr (GATHER) {
+                // a cell is seen by the queries at or after its position (keys
+                // past the split read a cell that the tail check below masks)
+                const int4 c = *(const int4 *) &gcell[kin < DEC_GATHER_SPLIT - 3 ? kin : 0];
+                const int cv[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    x[i] = (uint32_t) cv[i] < (uint32_t) a.g_rows && (int64_t) cv[i] <= q_pos ? s[i] : -INFINITY;
             } else {
 #pragma unroll
                 for (int i = 0; i < 4; i++) x[i] = s[i];
@@ -1606,6 +1692,9 @@ __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
         }
     }
     __syncthreads();
+    if constexpr (GATHER) {
+        if (threadIdx.x == 0 && g_bad && a.status) atomicOr(a.status, DEVERR_GET_ROWS_INDEX);
+    }
     if (kg != 0 || rl >= RW) return;
 #pragma unroll 1
     for (int k2 = 0; k2 < KG - 1; k2++) {
@@ -1702,10 +1791,11 @@ uint32_t recip32(int64_t d) {
 // kernel that spills to scratch would break that count: refuse to run one.
 int check_no_scratch() {
     static const int rc = [] {
-        for (const void * f : {(const void *) k_fa_dec<1, false, false>, (const void *) k_fa_dec<1, true, false>,
-                               (const void *) k_fa_dec<2, false, false>, (const void *) k_fa_dec<2, true, false>,
-                               (const void *) k_fa_dec<1, false, true>, (const void *) k_fa_dec<1, true, true>,
-                               (const void *) k_fa_dec<2, false, true>, (const void *) k_fa_dec<2, true, true>,
+        for (const void * f : {(const void *) k_fa_dec<1, false, false, false>, (const void *) k_fa_dec<1, true, false, false>,
+                               (const void *) k_fa_dec<2, false, false, false>, (const void *) k_fa_dec<2, true, false, false>,
+                               (const void *) k_fa_dec<1, false, true, false>, (const void *) k_fa_dec<1, true, true, false>,
+                               (const void *) k_fa_dec<2, false, true, false>, (const void *) k_fa_dec<2, true, true, false>,
+                               (const void *) k_fa_dec<1, false, false, true>, (const void *) k_fa_dec<2, false, false, true>,
                                (const void *) k_fattn_q8_0<2, true, WAVES, 16, false>,
                                (const void *) k_fattn_q8_0<1, false, WAVES_PAIR, 16, false>,
                                (const void *) k_fattn_q8_0<1, true, WAVES_PAIR, 16, false>,
@@ -1729,7 +1819,7 @@ int check_no_scratch() {
 }
 
 int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v, const qwfn_tensor * mask,
-               fa_plan * pl, const int64_t * seq_n_kv = nullptr, int64_t ns_cap = MAX_SPLITS) {
+               fa_plan * pl, const int64_t * seq_n_kv = nullptr, int64_t ns_cap = MAX_SPLITS, bool gather = false) {
     if (!q || !k || !v) return set_error(QWFN_EINVAL, "flash_attn_ext: NULL q/k/v");
     if (q->type != QWFN_TYPE_F32) return set_error(QWFN_EINVAL, "flash_attn_ext: q must be f32");
     if (k->type != QWFN_TYPE_Q8_0 || v->type != QWFN_TYPE_Q8_0)
@@ -1801,8 +1891,13 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
     // Splits are whole chunks. When the keys exceed two or more chunks per
     // split by less than one chunk (n_kv = 2^k + T), the last split takes the
     // rest; otherwise every split rounds up and there are fewer.
+    if (gather) {
+        // gathered keys: a block's cells fit its LDS list
+        if (!dec) return set_error(QWFN_ENOTSUP, "flash_attn_ext_cells: at most 32 query rows per KV head (T * n_head / n_head_kv)");
+        ns = std::max<int64_t>(ns, (n_kv + DEC_GATHER_SPLIT - 1) / DEC_GATHER_SPLIT);
+    }
     int64_t split_len = n_kv / (ns * ck) * ck;
-    if (split_len < (dec ? min_split : 2 * ck) || n_kv - ns * split_len >= (dec ? min_split : ck)) {
+    if (gather || split_len < (dec ? min_split : 2 * ck) || n_kv - ns * split_len >= (dec ? min_split : ck)) {
         split_len = (n_kv + ns - 1) / ns;
         split_len = std::max<int64_t>(ck, (split_len + ck - 1) / ck * ck);
         ns = std::max<int64_t>(1, (n_kv + split_len - 1) / split_len);
@@ -1937,20 +2032,30 @@ int scratch_address(void ** out) {
 // buffer when ws is NULL), or the library's static scratch.
 enum ws_mode { WS_CALLER, WS_SCRATCH };
 
+// Gathered keys: per KV head a list of cache rows (qwfn_flash_attn_ext_q8_0_cells).
+struct fa_gather {
+    const int32_t * cells;
+    const int64_t * n_cells;   // host, one count per KV head
+    int64_t stride;
+    int64_t pos0;
+    int64_t n_rows;            // rows of the cache
+};
+
 int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v, const qwfn_tensor * mask, float scale,
               float max_bias, float logit_softcap, const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes,
-              void * stream, const fa_append * app, const int64_t * seq_n_kv = nullptr, ws_mode wsm = WS_CALLER) {
+              void * stream, const fa_append * app, const int64_t * seq_n_kv = nullptr, ws_mode wsm = WS_CALLER,
+              const fa_gather * gat = nullptr) {
     if (max_bias != 0.0f) return set_error(QWFN_ENOTSUP, "flash_attn_ext: max_bias (ALiBi) is not supported");
     if (logit_softcap != 0.0f) return set_error(QWFN_ENOTSUP, "flash_attn_ext: logit_softcap is not supported");
     if (!(std::isfinite(scale))) return set_error(QWFN_EINVAL, "flash_attn_ext: scale must be finite");
     if (variant != QWFN_Q8_REF && variant != QWFN_Q8_X86) return set_error(QWFN_EINVAL, "flash_attn_ext: unknown variant");
     fa_plan pl{};
-    if (int rc = plan_fattn(q, k, v, mask, &pl, seq_n_kv)) return rc;
+    if (int rc = plan_fattn(q, k, v, mask, &pl, seq_n_kv, MAX_SPLITS, gat != nullptr)) return rc;
     if (wsm == WS_SCRATCH && pl.ws_bytes > NOALLOC_SCRATCH_BYTES) {
         // fewer key splits, so that their partials fit the scratch
         const size_t per_split = (size_t) q->ne[3] * k->ne[2] * pl.R * (D * sizeof(float) + sizeof(float2));
         const int64_t cap = std::max<int64_t>(1, (int64_t) ((NOALLOC_SCRATCH_BYTES - 512) / std::max<size_t>(per_split, 1)));
-        if (int rc = plan_fattn(q, k, v, mask, &pl, seq_n_kv, cap)) return rc;
+        if (int rc = plan_fattn(q, k, v, mask, &pl, seq_n_kv, cap, gat != nullptr)) return rc;
         if (pl.ws_bytes > NOALLOC_SCRATCH_BYTES)
             return set_error(QWFN_ENOMEM, "flash_attn_ext_noalloc: the split partials need more than the 16 MiB scratch");
     }
@@ -2023,6 +2128,14 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
     a.dst_vec = is_aligned(dst->data, 16) ? 1 : 0;
     a.q_slice = (uint32_t) q_slice_bytes(*q);
     a.gqa_mul = recip32(pl.gqa);
+    if (gat) {
+        a.g_cells = gat->cells;
+        a.g_stride = gat->stride;
+        a.g_pos0 = gat->pos0;
+        a.g_rows = gat->n_rows;
+        for (int64_t h = 0; h < a.nh_kv; h++) a.g_n[h] = (int32_t) gat->n_cells[h];
+        if (int rc = status_word(&a.status)) return rc;
+    }
     if (app) {
         a.app_k = (const char *) app->src_k->data;
         a.app_v = (const char *) app->src_v->data;
@@ -2048,8 +2161,11 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
     if (pl.kind == FA_DEC) {
         const dim3 bd(DEC_WAVES * 64);
         const bool msk = a.mask != nullptr;
-#define QWFN_DEC(RT_, M_, RG_) hipLaunchKernelGGL((k_fa_dec<RT_, M_, RG_>), g, bd, 0, st, a)
-        if (pl.RT == 1) {
+#define QWFN_DEC(RT_, M_, RG_) hipLaunchKernelGGL((k_fa_dec<RT_, M_, RG_, false>), g, bd, 0, st, a)
+        if (gat) {
+            if (pl.RT == 1) hipLaunchKernelGGL((k_fa_dec<1, false, false, true>), g, bd, 0, st, a);
+            else            hipLaunchKernelGGL((k_fa_dec<2, false, false, true>), g, bd, 0, st, a);
+        } else if (pl.RT == 1) {
             if (a.ragged) { if (msk) QWFN_DEC(1, true, true); else QWFN_DEC(1, false, true); }
             else          { if (msk) QWFN_DEC(1, true, false); else QWFN_DEC(1, false, false); }
         } else {
@@ -2116,6 +2232,62 @@ extern "C" int qwfn_flash_attn_ext_q8_0_noalloc(const qwfn_tensor * q, const qwf
     return ::qwfn::abi_call("flash_attn_ext_q8_0_noalloc", [&]() -> int {
         return fattn_run(q, k, v, mask, scale, max_bias, logit_softcap, dst, variant, nullptr, 0, stream, nullptr, nullptr,
                          WS_SCRATCH);
+    });
+}
+
+namespace {
+// Checks of a gathered call; kk / vv get the longest list's length as their key count.
+int gather_args(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v, const int32_t * cells,
+                const int64_t * n_cells, int64_t cell_stride, int64_t pos0, qwfn_tensor * kk, qwfn_tensor * vv,
+                fa_gather * g) {
+    if (!q || !k || !v || !cells || !n_cells) return set_error(QWFN_EINVAL, "flash_attn_ext_cells: NULL argument");
+    if (!is_aligned(cells, 16)) return set_error(QWFN_EALIGN, "flash_attn_ext_cells: cells must be 16-byte aligned");
+    if (k->ne[2] < 1 || k->ne[2] > GATHER_MAX_HEADS)
+        return set_error(QWFN_ENOTSUP, "flash_attn_ext_cells: 1 to 8 KV heads");
+    if (q->ne[3] != 1 || k->ne[3] != 1 || v->ne[3] != 1) return set_error(QWFN_ENOTSUP, "flash_attn_ext_cells: one sequence (B = 1)");
+    if (cell_stride < 0 || cell_stride % 4)
+        return set_error(QWFN_EALIGN, "flash_attn_ext_cells: cell_stride must be 0 (one shared list) or a positive multiple of 4");
+    if (pos0 < 0) return set_error(QWFN_EINVAL, "flash_attn_ext_cells: negative pos0");
+    if (k->ne[1] != v->ne[1]) return set_error(QWFN_EINVAL, "flash_attn_ext_cells: k and v must have the same rows");
+    if ((uint64_t) k->ne[1] * std::max(k->nb[1], v->nb[1]) >= (uint64_t(1) << 31))
+        return set_error(QWFN_ENOTSUP, "flash_attn_ext_cells: the cache must be below 2 GiB (rows * row stride)");
+    int64_t mx = 0;
+    for (int64_t h = 0; h < k->ne[2]; h++) {
+        if (n_cells[h] < 0 || (cell_stride > 0 && n_cells[h] > cell_stride))
+            return set_error(QWFN_ERANGE, "flash_attn_ext_cells: each head's cell count must lie in [0, cell_stride]");
+        mx = std::max(mx, n_cells[h]);
+    }
+    *kk = *k;
+    *vv = *v;
+    kk->ne[1] = vv->ne[1] = mx;
+    *g = fa_gather{cells, n_cells, cell_stride, pos0, k->ne[1]};
+    return QWFN_OK;
+}
+}  // namespace
+
+extern "C" size_t qwfn_fattn_workspace_size_cells(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
+                                                  const int64_t * n_cells, int64_t cell_stride) {
+    return ::qwfn::abi_value<size_t>("fattn_workspace_size_cells", 0, [&]() -> size_t {
+        qwfn_tensor kk, vv;
+        fa_gather g{};
+        static const int32_t dummy[4] = {0, 0, 0, 0};
+        if (gather_args(q, k, v, dummy, n_cells, cell_stride, 0, &kk, &vv, &g)) return 0;
+        fa_plan pl{};
+        if (plan_fattn(q, &kk, &vv, nullptr, &pl, nullptr, MAX_SPLITS, true)) return 0;
+        return pl.ws_bytes;
+    });
+}
+
+extern "C" int qwfn_flash_attn_ext_q8_0_cells(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
+                                              const int32_t * cells, const int64_t * n_cells, int64_t cell_stride,
+                                              int64_t pos0, float scale, const qwfn_tensor * dst, int variant, void * ws,
+                                              size_t ws_bytes, void * stream) {
+    return ::qwfn::abi_call("flash_attn_ext_q8_0_cells", [&]() -> int {
+        qwfn_tensor kk, vv;
+        fa_gather g{};
+        if (int rc = gather_args(q, k, v, cells, n_cells, cell_stride, pos0, &kk, &vv, &g)) return rc;
+        return fattn_run(q, &kk, &vv, nullptr, scale, 0.0f, 0.0f, dst, variant, ws, ws_bytes, stream, nullptr, nullptr,
+                         WS_CALLER, &g);
     });
 }
 

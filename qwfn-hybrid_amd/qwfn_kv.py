@@ -70,6 +70,7 @@ EXPORTS = [
     "qwfn_set_rows_q8_0", "qwfn_cpy_f32_q8_0", "qwfn_set_rows_q8_0_kv", "qwfn_cpy_f32_q8_0_kv", "qwfn_get_rows_i32", "qwfn_kv_gather_segments",
     "qwfn_fattn_workspace_size", "qwfn_fattn_force_splits", "qwfn_flash_attn_ext_q8_0", "qwfn_flash_attn_ext_q8_0_noalloc", "qwfn_flash_attn_ext_q8_0_append",
     "qwfn_fattn_workspace_size_seq", "qwfn_flash_attn_ext_q8_0_seq", "qwfn_state_restore",
+    "qwfn_fattn_workspace_size_cells", "qwfn_flash_attn_ext_q8_0_cells",
     # include/qwfn_state.h
     "qwfn_state_config_default", "qwfn_state_create", "qwfn_state_destroy", "qwfn_state_tensor",
     "qwfn_state_bytes", "qwfn_state_host_bytes", "qwfn_state_rollback_bytes", "qwfn_state_n_ctx",
@@ -121,6 +122,9 @@ def load(path: str = LIB_PATH):
                                                ctypes.c_int, vp, sz, PL, vp]
     L.qwfn_flash_attn_ext_q8_0_append.argtypes = [T, T, T, T, ctypes.c_float, ctypes.c_float, ctypes.c_float, T,
                                                   ctypes.c_int, vp, sz, T, T, i64, vp]
+    L.qwfn_fattn_workspace_size_cells.argtypes = [T, T, T, PL, i64]
+    L.qwfn_fattn_workspace_size_cells.restype = sz
+    L.qwfn_flash_attn_ext_q8_0_cells.argtypes = [T, T, T, vp, PL, i64, i64, ctypes.c_float, T, ctypes.c_int, vp, sz, vp]
     L.qwfn_state_restore.argtypes = [ctypes.POINTER(vp), ctypes.POINTER(sz), ctypes.POINTER(vp), i32, i32, i32, vp]
     # include/qwfn_state.h
     u32, PV, PS = ctypes.c_uint32, ctypes.POINTER(vp), ctypes.POINTER(sz)
@@ -179,6 +183,7 @@ def load(path: str = LIB_PATH):
     L.qwfn_last_error.restype = ctypes.c_char_p
     L.qwfn_fattn_workspace_size.restype = sz
     L.qwfn_fattn_workspace_size_seq.restype = sz
+    L.qwfn_fattn_workspace_size_cells.restype = sz
     L.qwfn_qsa_select_workspace_size.restype = sz
     _lib = L
     return L
@@ -353,6 +358,29 @@ def fattn_workspace_size_seq(qv: Tensor, kv: Tensor, vv: Tensor, mv: Tensor | No
     n = (ctypes.c_int64 * len(seq_n_kv))(*[int(x) for x in seq_n_kv])
     return int(load().qwfn_fattn_workspace_size_seq(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv),
                                                     ctypes.byref(mv) if mv is not None else None, n))
+
+
+def flash_attn_ext_cells(qv: Tensor, kv: Tensor, vv: Tensor, cells, n_cells, pos0: int, scale: float, ov: Tensor,
+                         variant: int = Q8_X86, ws=None, stream=None, shared: bool = False):
+    """Attention of KV head h's query heads over the cache rows cells[h, :n_cells[h]]
+    (cells: device int32 [n_head_kv, stride]; shared: every head reads row 0, the
+    reference's one list); query t sees a row at most pos0 + t."""
+    L = load()
+    n = (ctypes.c_int64 * len(n_cells))(*[int(x) for x in n_cells])
+    ws_ptr = ws.data_ptr() if ws is not None else None
+    ws_bytes = ws.numel() * ws.element_size() if ws is not None else 0
+    if str(cells.dtype) != "torch.int32" or cells.dim() != 2 or cells.stride(1) != 1:
+        raise ValueError("cells must be an int32 [n_head_kv, stride] tensor with contiguous rows")
+    return check(L.qwfn_flash_attn_ext_q8_0_cells(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), cells.data_ptr(),
+                                                  n, 0 if shared else cells.stride(0), pos0, scale, ctypes.byref(ov),
+                                                  variant, ws_ptr,
+                                                  ws_bytes, _stream(stream)))
+
+
+def fattn_workspace_size_cells(qv: Tensor, kv: Tensor, vv: Tensor, n_cells, cell_stride: int) -> int:
+    n = (ctypes.c_int64 * len(n_cells))(*[int(x) for x in n_cells])
+    return int(load().qwfn_fattn_workspace_size_cells(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), n,
+                                                      cell_stride))
 
 
 def flash_attn_ext_append(qv: Tensor, kv: Tensor, vv: Tensor, mv: Tensor | None, scale: float, ov: Tensor,

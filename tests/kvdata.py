@@ -83,6 +83,44 @@ def oracle_attn_f64(q, kc, vc, n_kv, n_head_kv, mask, scale, quantize_q: int = 2
     return O.attn_f64(qv, kv, vv, mv, scale, (T, nh, hd), quantize_q)
 
 
+def selection_lists(seed: int = 4, n_ctx: int = 65536, blocks: int = 1024, bsz: int = 64, top: int = 128,
+                    tail: int = 512, n_head_kv: int = 2) -> list[np.ndarray]:
+    """Sparse selection per KV head: the top-`top` of `blocks` blocks of `bsz`
+    positions by seeded uniform scores (ties to the lower block) united with
+    the last `tail` positions; ascending int32 cell lists."""
+    lists = []
+    for h in range(n_head_kv):
+        u = O.uniform(O.stream_key(seed, 0, SCORE_KIND, h), blocks)
+        order = np.argsort(-u, kind="stable")[:top]
+        pos = (order[:, None] * bsz + np.arange(bsz)[None, :]).reshape(-1)
+        lists.append(np.union1d(pos, np.arange(n_ctx - tail, n_ctx)).astype(np.int32))
+    return lists
+
+
+def oracle_attn_cells(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, lists, pos0: int, scale: float,
+                      variant: int = O.Q8_X86) -> np.ndarray:
+    """ggml-cpu attention of query t (position pos0 + t) over the cache rows that
+    KV head h's list names (repeats count), those at most pos0 + t and inside
+    the cache: the gathered copy with its cell mask. q [T, nh, hd]; a query row
+    that sees no cell is 0."""
+    T, nh, hd = q.shape
+    nh_kv = len(lists)
+    g = nh // nh_kv
+    seg = hd // 32 * 34
+    out = np.zeros((T, nh, hd), np.float32)
+    for h in range(nh_kv):
+        lst = np.asarray(lists[h], np.int64)
+        for t in range(T):
+            sel = lst[(lst >= 0) & (lst < kc.shape[0]) & (lst <= pos0 + t)]
+            if len(sel) == 0:
+                continue
+            kh = np.ascontiguousarray(kc[sel][:, h * seg:(h + 1) * seg])
+            vh = np.ascontiguousarray(vc[sel][:, h * seg:(h + 1) * seg])
+            out[t, h * g:(h + 1) * g] = oracle_attn(q[t:t + 1, h * g:(h + 1) * g], kh, vh, len(sel), 1, None, scale,
+                                                    variant)[0]
+    return out
+
+
 def err_stats(got: np.ndarray, ref: np.ndarray) -> tuple[float, float]:
     d = np.abs(got.astype(np.float64) - ref.astype(np.float64))
     return float(d.max()), float(d.mean())

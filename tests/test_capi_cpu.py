@@ -176,3 +176,32 @@ def test_ragged_batch_validation():
     _err(L.qwfn_flash_attn_ext_q8_0_seq(r(q), r(k), r(k), None, 0.0625, 0.0, 0.0, r(o), 1, None, 0, seq, None),
          K.ENOTSUP, "at most 16")
     assert L.qwfn_fattn_workspace_size_seq(r(q4), r(k4), r(k4), None, None) == 0
+
+
+def test_cells_attention_validation():
+    L = K.load()
+    r = ctypes.byref
+    q, k, o = _fa_views()
+    n = (ctypes.c_int64 * 2)(8, 5)
+
+    def call(qq, kk, cells, counts, stride, pos0=50):
+        return L.qwfn_flash_attn_ext_q8_0_cells(r(qq), r(kk), r(kk), cells, counts, stride, pos0, 0.0625, r(o), 1,
+                                                None, 0, None)
+    _err(call(q, k, None, n, 8), K.EINVAL, "NULL")
+    _err(call(q, k, FAKE, None, 8), K.EINVAL, "NULL")
+    _err(call(q, k, FAKE + 4, n, 8), K.EALIGN, "16-byte")
+    _err(call(q, k, FAKE, n, 6), K.EALIGN, "cell_stride")
+    _err(call(q, k, FAKE, n, -4), K.EALIGN, "cell_stride")
+    _err(call(q, k, FAKE, (ctypes.c_int64 * 2)(9, 5), 8), K.ERANGE, "[0, cell_stride]")
+    _err(call(q, k, FAKE, (ctypes.c_int64 * 2)(-1, 5), 0), K.ERANGE, "[0, cell_stride]")
+    _err(call(q, k, FAKE, n, 8, -1), K.EINVAL, "pos0")
+    q9, k9, _ = _fa_views(nh=18, nh_kv=9)
+    _err(call(q9, k9, FAKE, (ctypes.c_int64 * 9)(*([4] * 9)), 4), K.ENOTSUP, "1 to 8 KV heads")
+    q5, k5, _ = _fa_views(T=5)
+    _err(call(q5, k5, FAKE, n, 8), K.ENOTSUP, "at most 32 query rows")
+    big = K.tensor(FAKE, K.TYPE_Q8_0, (256, 1 << 22, 2, 1), (34, 544, 272, 1 << 20))
+    _err(call(q, big, FAKE, n, 8), K.ENOTSUP, "2 GiB")
+    # sizing is host-only: one 512-cell split per block at most, partials when there are several splits
+    assert L.qwfn_fattn_workspace_size_cells(r(q5), r(k5), r(k5), n, 8) == 0
+    one = L.qwfn_fattn_workspace_size_cells(r(q), r(k), r(k), (ctypes.c_int64 * 2)(4000, 3000), 4000)
+    assert one >= 2 * 8 * 8 * 256 * 4

@@ -1,0 +1,174 @@
+"""GPU parity of sparse decode attention with the gather fused in
+(qwfn_flash_attn_ext_q8_0_cells) against the oracle's attention over the
+gathered copy with its cell mask (qwfn_graph.cpp:632-699): the full-size
+selection (per-KV-head lists of 8576 and 8640 cells of a 65536-row cache, 3
+queries), the reference's one shared list, multi-split lists of different
+lengths per head, and the edge cases: an empty list, repeated and unsorted
+cells, cells outside the cache (masked and flagged), a query that sees no
+cell. Tolerance: 2e-3 max / 1e-3 mean abs of ggml-cpu semantics, 1e-4 max
+as observed."""
+import numpy as np
+import pytest
+import torch
+
+import kvdata as KD
+from gpu_util import dev, host, say
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+TIGHT = 1e-4
+
+
+def check(got, ref, tight=TIGHT):
+    mx, mean = KD.err_stats(got, ref)
+    print(f"  max abs {mx:.3e}  mean abs {mean:.3e}", flush=True)
+    assert np.isfinite(got).all()
+    assert mx <= KD.MAX_ABS_TOL and mean <= KD.MEAN_ABS_TOL
+    assert mx <= tight
+
+
+def cells_attn(K, q, kd, vd, n_rows, lists, pos0, stride=None, variant=1, ws=False, shared=False):
+    """q [T, nh, 256] numpy; kd/vd device caches uint8 [n_ctx, 544]; returns (out, device flags)."""
+    T, nh, hd = q.shape
+    nh_kv = len(lists)
+    n = [len(x) for x in lists]
+    if shared:
+        stride = 0
+        cells = dev(np.asarray(lists[0], np.int32)[None])
+    else:
+        stride = stride or max(4, (max(n) + 3) // 4 * 4)
+        c = np.full((nh_kv, stride), -7, np.int32)
+        for h, x in enumerate(lists):
+            c[h, :len(x)] = x
+        cells = dev(c)
+    rb = kd.shape[1]
+    kv = K.tensor(kd.data_ptr(), K.TYPE_Q8_0, (hd, n_rows, nh_kv, 1), (34, rb, hd // 32 * 34, n_rows * rb))
+    vv = K.tensor(vd.data_ptr(), K.TYPE_Q8_0, (hd, n_rows, nh_kv, 1), (34, rb, hd // 32 * 34, n_rows * rb))
+    qd = dev(q[None].astype(np.float32))
+    out = torch.full((1, T, nh, hd), float("nan"), dtype=torch.float32, device="cuda")
+    wst = None
+    if ws:
+        nb = K.fattn_workspace_size_cells(K.q_view(qd), kv, vv, n, stride)
+        assert nb >= 256
+        wst = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    K.flash_attn_ext_cells(K.q_view(qd), kv, vv, cells, n, pos0, 1 / 16, K.out_view(out), variant, ws=wst,
+                           shared=shared)
+    flags = K.device_status()
+    return host(out)[0], flags
+
+
+def test_cells_full_size_selection(gpu, oracle):
+    """64K cache, the per-head top-128 blocks of 64 plus the last 512 positions, 3 queries at 65533-65535."""
+    K = gpu
+    n_ctx, T, nh = 65536, 3, 16
+    lists = KD.selection_lists(4, n_ctx)
+    assert [len(x) for x in lists] == [8576, 8640]
+    kc = KD.make_cache(KD.kv_rows(4, 0, KD.K_KIND, n_ctx), n_ctx)
+    vc = KD.make_cache(KD.kv_rows(4, 0, KD.V_KIND, n_ctx), n_ctx)
+    q = KD.q_rows(4, 1, T, nh)[0]
+    kd, vd = dev(kc), dev(vc)
+    say("cells attention: 8576 / 8640 cells of 65536, T=3")
+    got, flags = cells_attn(K, q, kd, vd, n_ctx, lists, n_ctx - T, ws=True)
+    assert flags == 0
+    check(got, KD.oracle_attn_cells(q, kc, vc, lists, n_ctx - T, 1 / 16))
+    say("cells attention: library workspace, same bits")
+    got2, _ = cells_attn(K, q, kd, vd, n_ctx, lists, n_ctx - T)
+    np.testing.assert_array_equal(got2, got)
+
+
+def test_cells_shared_list(gpu, oracle):
+    """The reference's form: one list of 2052 cells for both KV heads (2 of them past the query), T = 1."""
+    K = gpu
+    n_ctx, T, nh = 8192, 1, 16
+    u = O.uniform(O.stream_key(9, 0, KD.SCORE_KIND, 0), n_ctx)
+    sel = np.sort(np.argsort(u, kind="stable")[:2050]).astype(np.int32)
+    pos0 = 6000
+    lst = np.concatenate([sel[sel <= pos0], [pos0 + 5, pos0 + 9], sel[sel > pos0]])[:2052].astype(np.int32)
+    kc = KD.make_cache(KD.kv_rows(9, 0, KD.K_KIND, n_ctx, outliers=True), n_ctx)
+    vc = KD.make_cache(KD.kv_rows(9, 0, KD.V_KIND, n_ctx, outliers=True), n_ctx)
+    q = KD.q_rows(9, 1, T, nh)[0]
+    kd, vd = dev(kc), dev(vc)
+    say("cells attention: one shared list of 2052 cells, T=1")
+    got, flags = cells_attn(K, q, kd, vd, n_ctx, [lst, lst], pos0, shared=True)
+    assert flags == 0
+    check(got, KD.oracle_attn_cells(q, kc, vc, [lst, lst], pos0, 1 / 16))
+
+
+@pytest.mark.parametrize("variant", [0, 1])
+def test_cells_multi_split_ragged_heads(gpu, oracle, variant):
+    """1500 and 37 cells (several 512-cell splits for one head, one partial tile for the other), T = 2."""
+    K = gpu
+    n_ctx, T, nh = 4096, 2, 16
+    l0 = np.sort(np.argsort(O.uniform(O.stream_key(11, 0, KD.SCORE_KIND, 0), n_ctx), kind="stable")[:1500])
+    l1 = np.sort(np.argsort(O.uniform(O.stream_key(11, 0, KD.SCORE_KIND, 1), n_ctx), kind="stable")[:37])
+    lists = [l0.astype(np.int32), l1.astype(np.int32)]
+    kc = KD.make_cache(KD.kv_rows(11, 0, KD.K_KIND, n_ctx), n_ctx, variant)
+    vc = KD.make_cache(KD.kv_rows(11, 0, KD.V_KIND, n_ctx), n_ctx, variant)
+    q = KD.q_rows(11, 1, T, nh)[0]
+    kd, vd = dev(kc), dev(vc)
+    say(f"cells attention: 1500 / 37 cells, T=2, variant {variant}")
+    got, flags = cells_attn(K, q, kd, vd, n_ctx, lists, n_ctx - T, variant=variant)
+    assert flags == 0
+    check(got, KD.oracle_attn_cells(q, kc, vc, lists, n_ctx - T, 1 / 16, variant))
+
+
+def test_cells_edge_cases(gpu, oracle):
+    """Head 0: no cells. Head 1: unsorted, repeated cells, two outside the cache
+    (masked, flag raised) and cells that only the second query sees."""
+    K = gpu
+    n_ctx, T, nh = 1024, 2, 16
+    pos0 = 700
+    rng = np.random.default_rng(5)
+    base = rng.permutation(pos0 + 1)[:300].astype(np.int32)
+    l1 = np.concatenate([base, base[:20], [n_ctx + 3, -1], [pos0 + 1] * 3]).astype(np.int32)
+    rng.shuffle(l1)
+    lists = [np.zeros(0, np.int32), l1]
+    kc = KD.make_cache(KD.kv_rows(12, 0, KD.K_KIND, n_ctx), n_ctx)
+    vc = KD.make_cache(KD.kv_rows(12, 0, KD.V_KIND, n_ctx), n_ctx)
+    q = KD.q_rows(12, 1, T, nh)[0]
+    kd, vd = dev(kc), dev(vc)
+    say("cells attention: empty list, repeats, cells outside the cache")
+    got, flags = cells_attn(K, q, kd, vd, n_ctx, lists, pos0)
+    assert flags & 2, flags
+    assert (got[:, :8] == 0).all()
+    check(got, KD.oracle_attn_cells(q, kc, vc, lists, pos0, 1 / 16))
+    say("cells attention: a query that sees no cell")
+    late = [np.array([pos0 + 1, pos0 + 1], np.int32), np.array([pos0 + 1], np.int32)]
+    got, flags = cells_attn(K, q, kd, vd, n_ctx, late, pos0)
+    assert flags == 0
+    assert (got[0] == 0).all()
+    check(got, KD.oracle_attn_cells(q, kc, vc, late, pos0, 1 / 16))
+
+
+def test_cells_matches_gather_then_attention(gpu, oracle):
+    """The fused call against the separate path it replaces: gather the cells'
+    halves, then masked attention over the gathered copy (within float rounding)."""
+    K = gpu
+    n_ctx, T, nh, seg = 16384, 3, 16, KD.SEG
+    lists = KD.selection_lists(6, n_ctx, blocks=256, bsz=64, top=32, tail=512)
+    kc = KD.make_cache(KD.kv_rows(6, 0, KD.K_KIND, n_ctx), n_ctx)
+    vc = KD.make_cache(KD.kv_rows(6, 0, KD.V_KIND, n_ctx), n_ctx)
+    q = KD.q_rows(6, 1, T, nh)[0]
+    kd, vd = dev(kc), dev(vc)
+    say("cells attention vs gather + masked attention at 16384")
+    fused, _ = cells_attn(K, q, kd, vd, n_ctx, lists, n_ctx - T)
+    m = ((max(len(x) for x in lists) + 255) // 256) * 256
+    idx = np.stack([np.concatenate([x, np.repeat(x[-1:], m - len(x))]) for x in lists]).astype(np.int32)
+    gk = torch.zeros((2, m, seg), dtype=torch.uint8, device="cuda")
+    gv = torch.zeros((2, m, seg), dtype=torch.uint8, device="cuda")
+    idd = dev(idx)
+    K.gather_segments(kd, idd, gk, 0, seg, seg)
+    K.gather_segments(vd, idd, gv, 0, seg, seg)
+    qpos = np.arange(n_ctx - T, n_ctx)
+    mask = np.full((1, nh, T, m), O.F16_NEG_INF, np.uint16)
+    for h in range(nh):
+        lst = lists[h // 8]
+        for t in range(T):
+            mask[0, h, t, :len(lst)][lst <= qpos[t]] = 0
+    kview = K.tensor(gk.data_ptr(), K.TYPE_Q8_0, (256, m, 2, 1), (34, seg, m * seg, 2 * m * seg))
+    vview = K.tensor(gv.data_ptr(), K.TYPE_Q8_0, (256, m, 2, 1), (34, seg, m * seg, 2 * m * seg))
+    qd, md = dev(q[None].astype(np.float32)), dev(mask.view(np.float16))
+    out = torch.full((1, T, nh, 256), float("nan"), dtype=torch.float32, device="cuda")
+    K.flash_attn_ext(K.q_view(qd), kview, vview, K.mask_view(md), 1 / 16, K.out_view(out))
+    sep = host(out)[0]
+    check(fused, sep, tight=2e-5)

@@ -175,21 +175,10 @@ def test_batch_decode_restored_slots(gpu, oracle):
 
 # ------------------------------------------------------- sparse selection
 
-def _selection_lists(n_ctx=65536, blocks=1024, bsz=64, top=128, tail=512):
-    """Per KV head: top-`top` blocks by seeded uniform scores (ties to the lower block) and the last `tail` positions."""
-    lists = []
-    for h in range(2):
-        u = O.uniform(O.stream_key(4, 0, KD.SCORE_KIND, h), blocks)
-        order = np.argsort(-u, kind="stable")[:top]
-        pos = (order[:, None] * bsz + np.arange(bsz)[None, :]).reshape(-1)
-        lists.append(np.union1d(pos, np.arange(n_ctx - tail, n_ctx)).astype(np.int32))
-    return lists
-
-
 def test_sparse_selection_gather_and_attention(gpu, oracle):
     K = gpu
     n_ctx, T, nh = 65536, 3, 16
-    lists = _selection_lists(n_ctx)
+    lists = KD.selection_lists(4, n_ctx)
     assert [len(x) for x in lists] == [8576, 8640]
     kc = KD.make_cache(KD.kv_rows(4, 0, KD.K_KIND, n_ctx), n_ctx)
     vc = KD.make_cache(KD.kv_rows(4, 0, KD.V_KIND, n_ctx), n_ctx)
