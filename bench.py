@@ -60,6 +60,16 @@ def parse():
     return ap.parse_args()
 
 
+def cpu_model() -> str | None:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def timed(torch, fn, reps: int) -> float:
     """Average µs per call of fn(k) over reps back-to-back calls on the current stream."""
     stream = torch.cuda.current_stream()
@@ -239,19 +249,62 @@ def measure_rows(K, torch, np, dev, gen) -> dict:
     rows["append_kv_3_rows"] = {"us_per_launch": round(us, 3), "bytes_per_launch": 2 * 3 * (kv_dim * 4 + ROW)}
     del caches, srcs
 
-    # ---- sparse gather: per KV head, top-128 of 1024 blocks of 64 positions by uniform
-    #      scores plus the last 512 positions, as 272-byte half rows (K and V) ----
-    n_ctx = 65536
-    sets = 4
-    kvs = [(torch.randint(0, 256, (n_ctx, ROW), dtype=torch.uint8, device=dev, generator=gen),
-            torch.randint(0, 256, (n_ctx, ROW), dtype=torch.uint8, device=dev, generator=gen)) for _ in range(sets)]
+    # ---- sparse selection at 64K: per KV head, top-128 of 1024 blocks of 64 positions by
+    #      uniform scores plus the last 512 positions. (i) attention of 3 queries over the
+    #      selected cells with the gather fused in (qwfn_flash_attn_ext_q8_0_cells): 32 list
+    #      variants rotated over 4 caches, so the touched lines (32 x 9.4 MB) exceed the
+    #      Infinity Cache; (ii) the materialised per-head gather of the 272-byte half rows ----
+    n_ctx, Tq = 65536, 3
+    sets, n_lists = 4, 32
+    kvs = []
+    for _ in range(sets):
+        kc = torch.randint(-100, 100, (n_ctx, ROW), dtype=torch.int8, device=dev, generator=gen).view(torch.uint8)
+        vc = torch.randint(-100, 100, (n_ctx, ROW), dtype=torch.int8, device=dev, generator=gen).view(torch.uint8)
+        for c in (kc, vc):                       # valid fp16 scales (0x211F ~ 0.0101)
+            c.view(-1, 34)[:, 0] = 0x1F
+            c.view(-1, 34)[:, 1] = 0x21
+        kvs.append((kc, vc))
     rng = np.random.default_rng(4)
-    lists = []
-    for h in range(nh_kv):
-        sc = rng.random(1024)
-        top = np.argsort(-sc, kind="stable")[:128]
-        pos = np.unique(np.concatenate([(top[:, None] * 64 + np.arange(64)).ravel(), np.arange(n_ctx - 512, n_ctx)]))
-        lists.append(pos)
+
+    def selection():
+        out = []
+        for h in range(nh_kv):
+            sc = rng.random(1024)
+            top = np.argsort(-sc, kind="stable")[:128]
+            out.append(np.unique(np.concatenate([(top[:, None] * 64 + np.arange(64)).ravel(),
+                                                 np.arange(n_ctx - 512, n_ctx)])))
+        return out
+    sel = [selection() for _ in range(n_lists)]
+    stride = (max(len(x) for ls in sel for x in ls) + 3) // 4 * 4
+    cells = []
+    for ls in sel:
+        c = np.zeros((nh_kv, stride), np.int32)
+        for h, x in enumerate(ls):
+            c[h, :len(x)] = x
+        cells.append((torch.from_numpy(c).to(dev), [len(x) for x in ls]))
+    sq = torch.randn((1, Tq, nh, hd), generator=gen, device=dev)
+    sout = torch.zeros((1, Tq, nh, hd), dtype=torch.float32, device=dev)
+    sviews = [(K.tensor(kc.data_ptr(), K.TYPE_Q8_0, (hd, n_ctx, nh_kv, 1), (34, ROW, 272, n_ctx * ROW)),
+               K.tensor(vc.data_ptr(), K.TYPE_Q8_0, (hd, n_ctx, nh_kv, 1), (34, ROW, 272, n_ctx * ROW)))
+              for kc, vc in kvs]
+    sws = torch.empty(max(256, max(K.fattn_workspace_size_cells(K.q_view(sq), sviews[0][0], sviews[0][1], n, stride)
+                                   for _, n in cells)), dtype=torch.uint8, device=dev)
+
+    def sparse(k):
+        kv, vv = sviews[k % sets]
+        c, n = cells[k % n_lists]
+        K.flash_attn_ext_cells(K.q_view(sq), kv, vv, c, n, n_ctx - Tq, 1 / 16, K.out_view(sout), ws=sws)
+    for k in range(n_lists):
+        sparse(k)
+    us = timed(torch, sparse, 4 * n_lists)
+    n_sel = float(np.mean([sum(n) for _, n in cells]))
+    b = n_sel * 272 * 2 + n_sel * 4 + 2 * Tq * nh * hd * 4
+    rows["sparse_64k_cells_attention"] = {
+        "us_per_launch": round(us, 3), "cells_per_head": cells[0][1], "T": Tq,
+        "bytes_per_launch": int(b), "GBs": gbs(b, us), "frac": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "entry": "qwfn_flash_attn_ext_q8_0_cells (gather fused into k_fa_dec)"}
+
+    lists = sel[0]
     m = max(len(x) for x in lists)
     idx = torch.from_numpy(np.stack([np.concatenate([x, np.repeat(x[-1:], m - len(x))]) for x in lists])
                            .astype(np.int32)).to(dev)
@@ -267,7 +320,7 @@ def measure_rows(K, torch, np, dev, gen) -> dict:
     rows["gather_64k"] = {"us_per_op": round(us, 3), "positions_per_head": [len(x) for x in lists],
                           "bytes_read": moved, "bytes_written": moved, "GBs": gbs(2 * moved, us),
                           "frac": round(2 * moved / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
-    del kvs, gk, gv
+    del kvs, gk, gv, sws
 
     # ---- snapshot restore: 12 layers x 8192 rows of K and V + 36 DeltaNet states
     #      [32,128,128] f32 into 4 slots, from device memory and from pinned host memory ----
@@ -333,28 +386,29 @@ def measure_rows(K, torch, np, dev, gen) -> dict:
                              "entry": "qwfn_flash_attn_ext_q8_0_seq"}
     del bc, bws, sws
 
-    # ---- prefill chunk: 512 causal queries at depth 16384 through the same op ----
-    d0, T = 16384, 512
-    n_kv = d0 + T
-    kc = torch.randint(0, 256, (n_kv, ROW), dtype=torch.uint8, device=dev, generator=gen)
-    vc = torch.randint(0, 256, (n_kv, ROW), dtype=torch.uint8, device=dev, generator=gen)
-    for c in (kc, vc):
-        c.view(-1, 34)[:, 0] = 0x20
-        c.view(-1, 34)[:, 1] = 0x14
-    pm = np.full((T, n_kv), 0xFC00, np.uint16)
-    for i in range(T):
-        pm[i, :d0 + i + 1] = 0
-    pmask = torch.from_numpy(pm.view(np.float16)).to(dev)
-    pq = torch.randn((1, T, nh, hd), generator=gen, device=dev)
-    pout = torch.zeros((1, T, nh, hd), dtype=torch.float32, device=dev)
-    pk, pv, pmv = K.cache_attn_view(kc, n_kv, nh_kv), K.cache_attn_view(vc, n_kv, nh_kv), K.mask_view(pmask)
-    pws = torch.empty(max(256, K.fattn_workspace_size(K.q_view(pq), pk, pv, pmv)), dtype=torch.uint8, device=dev)
-    us = timed(torch, lambda k: K.flash_attn_ext(K.q_view(pq), pk, pv, pmv, 1 / 16, K.out_view(pout), ws=pws), 3)
-    flops = 4 * nh * hd * (T * d0 + T * (T + 1) // 2)      # causal count, QK^T and PV
-    rows["prefill_512_at_16k"] = {"us_per_launch": round(us, 1), "flops": flops,
-                                  "TFLOPs": round(flops / (us * 1e-6) / 1e12, 2),
-                                  "frac_of_f16_mfma_peak": round(flops / (us * 1e-6) / 2.5e15, 4)}
-    del kc, vc, pws
+    # ---- prefill chunk: 512 causal queries at depths 0, 4096 and 16384 through the same op ----
+    for d0 in (0, 4096, 16384):
+        T = 512
+        n_kv = d0 + T
+        kc = torch.randint(-100, 100, (n_kv, ROW), dtype=torch.int8, device=dev, generator=gen).view(torch.uint8)
+        vc = torch.randint(-100, 100, (n_kv, ROW), dtype=torch.int8, device=dev, generator=gen).view(torch.uint8)
+        for c in (kc, vc):
+            c.view(-1, 34)[:, 0] = 0x1F
+            c.view(-1, 34)[:, 1] = 0x21
+        pm = np.full((T, n_kv), 0xFC00, np.uint16)
+        for i in range(T):
+            pm[i, :d0 + i + 1] = 0
+        pmask = torch.from_numpy(pm.view(np.float16)).to(dev)
+        pq = torch.randn((1, T, nh, hd), generator=gen, device=dev)
+        pout = torch.zeros((1, T, nh, hd), dtype=torch.float32, device=dev)
+        pk, pv, pmv = K.cache_attn_view(kc, n_kv, nh_kv), K.cache_attn_view(vc, n_kv, nh_kv), K.mask_view(pmask)
+        pws = torch.empty(max(256, K.fattn_workspace_size(K.q_view(pq), pk, pv, pmv)), dtype=torch.uint8, device=dev)
+        us = timed(torch, lambda k: K.flash_attn_ext(K.q_view(pq), pk, pv, pmv, 1 / 16, K.out_view(pout), ws=pws), 5)
+        flops = 4 * nh * hd * (T * d0 + T * (T + 1) // 2)      # causal count, QK^T and PV
+        rows[f"prefill_512_at_{d0}"] = {"us_per_launch": round(us, 1), "flops": flops,
+                                        "TFLOPs": round(flops / (us * 1e-6) / 1e12, 2),
+                                        "frac_of_f16_mfma_peak": round(flops / (us * 1e-6) / 2.5e15, 4)}
+        del kc, vc, pws
     torch.cuda.empty_cache()
     return rows
 
@@ -570,26 +624,35 @@ def main() -> int:
         torch.cuda.synchronize()
         log(f"[bench] calibration copy of {args.calib_copy_mb} MiB done")
 
-    # ---- CPU baseline: the oracle (ggml-cpu flash_attn_ext semantics) on one layer ----
+    # ---- CPU baseline: the oracle (ggml-cpu flash_attn_ext semantics, restated in C) on
+    #      one layer; 2 warm-ups, then the median of >= 10 timed reps ----
     cpu = None
     if not args.no_cpu:
         try:
+            import statistics
+
             import kvdata as KD
+            # the host threads given to this GPU's job (at most 16, its share of the host)
             cores = min(16, len(os.sched_getaffinity(0)))
             kc, vc = caches[0][0]
             kc_h, vc_h = kc.cpu().numpy(), vc.cpu().numpy()
             q_h = q[0].cpu().numpy()[0]
-            reps, t_cpu = 0, 0.0
-            while t_cpu < args.cpu_seconds and reps < 1000:
+
+            def one():
                 t1 = time.perf_counter()
                 KD.oracle_attn(q_h, kc_h, vc_h, n_kv, nh_kv, mask_np, scale, threads=cores)
-                t_cpu += time.perf_counter() - t1
-                reps += 1
-            cpu = {"value": round(attn_bytes * reps / t_cpu / 1e9, 3), "unit": "GB/s", "cores": cores,
-                   "kind": "port",
-                   "sample": f"{reps} x one layer's verify attention (T={T}, {n_kv} q8_0 rows, 2 KV heads) "
-                             f"in the C oracle of ggml-cpu flash_attn_ext, {t_cpu:.1f}s, "
-                             f"{t_cpu / reps * 1e6:.0f} us/layer"}
+                return time.perf_counter() - t1
+            one(), one()
+            times = []
+            while len(times) < 10 or (sum(times) < args.cpu_seconds and len(times) < 200):
+                times.append(one())
+            med = statistics.median(times)
+            cpu = {"value": round(attn_bytes / med / 1e9, 3), "unit": "GB/s", "cores": cores,
+                   "kind": "port", "cpu_model": cpu_model(),
+                   "sample": f"one layer's verify attention (T={T}, {n_kv} q8_0 rows, 2 KV heads) in the C "
+                             f"restatement of ggml-cpu flash_attn_ext on {cores} threads: median of {len(times)} "
+                             f"reps after 2 warm-ups, {med * 1e6:.0f} us/layer (min {min(times) * 1e6:.0f})",
+                   "us_per_layer": round(med * 1e6, 1)}
             log(f"[bench] cpu baseline: {cpu}")
         except Exception as e:
             log(f"[bench] cpu baseline skipped: {e}")
@@ -605,7 +668,7 @@ def main() -> int:
         if w.get("depth") == depth and w.get("T") == T:
             traffic = tj["traffic_bytes"]
 
-    best_ms = graph_ms if graph_ms is not None else eager_ms
+    best_ms = min(graph_ms, eager_ms) if graph_ms is not None else eager_ms
     value = step_bytes / (best_ms * 1e-3) / 1e9
     achieved = attn_bytes / (attn_us * 1e-6) / 1e9
     res = {
@@ -631,7 +694,7 @@ def main() -> int:
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "flash_attn_ext q8_0 (k_fattn_q8_0 + k_fattn_merge)",
+                     "kernel": "flash_attn_ext q8_0 verify op: k_fa_dec (the key loop) + k_fattn_merge (split merge)",
                      "us_per_launch": round(attn_us, 3), "bytes_per_launch": attn_bytes},
         "cpu_baseline": cpu,
         "long_context": long_ctx,

@@ -168,11 +168,6 @@ struct fa_args {
     uint32_t * status;     // device flags (DEVERR_GET_ROWS_INDEX: a cell outside the cache)
 };
 
-// x / d through m = ceil(2^32 / d): floor(x * m / 2^32) = floor(x / d) while
-// x * d < 2^32 (the host checks the ranges of a call); d = 1 needs no m.
-__device__ __forceinline__ uint32_t udiv(uint32_t x, uint32_t d, uint32_t m) {
-    return d == 1 ? x : __umulhi(x, m);
-}
 __device__ __forceinline__ uint32_t div_gqa(const fa_args & a, uint32_t r) {
     return udiv(r, (uint32_t) a.gqa, a.gqa_mul);
 }
@@ -1782,10 +1777,6 @@ size_t q_slice_bytes(const qwfn_tensor & q) {
 }
 
 // ceil(2^32 / d) for d > 1 (0 for d = 1, which divides without it).
-uint32_t recip32(int64_t d) {
-    return d > 1 ? (uint32_t) (((uint64_t(1) << 32) + (uint64_t) d - 1) / (uint64_t) d) : 0u;
-}
-
 // The key loop hand-counts its outstanding vector-memory operations (the LDS
 // DMAs are inline asm the compiler does not see), so a build of the attention
 // kernel that spills to scratch would break that count: refuse to run one.

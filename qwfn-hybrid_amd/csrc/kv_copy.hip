@@ -32,41 +32,61 @@ struct gather_args {
     char *          dst;
     size_t          dst_row_stride;
     size_t          dst_seg_stride;
-    int32_t         units;     // copy units (16 or 4 bytes) per segment
-    int32_t         n_seg;
+    uint32_t        units;     // copy units (16 or 4 bytes) per segment
+    uint32_t        units_mul; // recip32(units)
+    uint32_t        rows;      // index rows per workgroup (rows * units * units < 2^32 when rows > 1)
     uint32_t *      status;
 };
 
+// Workgroup (x, y) copies index rows [x rows, (x + 1) rows) of segment y; a
+// lane's unit u of the workgroup is part u % units of row u / units (32-bit
+// reciprocal division, no 64-bit arithmetic per unit).
 template <typename U>
 __global__ __launch_bounds__(COPY_THREADS) void k_gather(gather_args a) {
-    const int64_t total = (int64_t) a.n_seg * a.n_idx * a.units;
-    for (int64_t u = (int64_t) blockIdx.x * COPY_THREADS + threadIdx.x; u < total;
-         u += (int64_t) gridDim.x * COPY_THREADS) {
-        const int64_t row = u / a.units;               // (seg, i) flattened
-        const int32_t part = (int32_t) (u - row * a.units);
-        const int64_t seg = row / a.n_idx;
-        const int64_t i = row - seg * a.n_idx;
-        const int32_t r = a.idx[row];
+    const uint32_t seg = blockIdx.y;
+    const int64_t i0 = (int64_t) blockIdx.x * a.rows;
+    const int64_t left = a.n_idx - i0;
+    const uint32_t nrow = left < (int64_t) a.rows ? (uint32_t) left : a.rows;
+    const uint32_t total = nrow * a.units;
+    const int32_t * idx = a.idx + (size_t) seg * (size_t) a.n_idx + i0;
+    const char * src = a.src + a.seg_off + (size_t) seg * a.seg_stride;
+    char * dst = a.dst + (size_t) seg * a.dst_seg_stride + (size_t) i0 * a.dst_row_stride;
+    for (uint32_t u = threadIdx.x; u < total; u += COPY_THREADS) {
+        const uint32_t row = a.rows == 1 ? 0u : udiv(u, a.units, a.units_mul);
+        const uint32_t part = u - row * a.units;
+        const int32_t r = idx[row];
         if (r < 0 || r >= a.src_rows) {
             if (part == 0) atomicOr(a.status, DEVERR_GET_ROWS_INDEX);
             continue;
         }
-        const U * s = (const U *) (a.src + (size_t) r * a.src_row_stride + a.seg_off + (size_t) seg * a.seg_stride) + part;
-        U * d = (U *) (a.dst + (size_t) seg * a.dst_seg_stride + (size_t) i * a.dst_row_stride) + part;
+        const U * s = (const U *) (src + (size_t) r * a.src_row_stride) + part;
+        U * d = (U *) (dst + (size_t) row * a.dst_row_stride) + part;
         *d = *s;
     }
 }
 
-int launch_gather(gather_args a, size_t seg_bytes, hipStream_t stream) {
+int launch_gather(gather_args a, size_t seg_bytes, int32_t n_seg, hipStream_t stream) {
     const bool v16 = seg_bytes % 16 == 0 && a.src_row_stride % 16 == 0 && a.seg_off % 16 == 0 &&
                      a.seg_stride % 16 == 0 && a.dst_row_stride % 16 == 0 && a.dst_seg_stride % 16 == 0 &&
                      is_aligned(a.src, 16) && is_aligned(a.dst, 16);
-    a.units = (int32_t) (seg_bytes / (v16 ? 16 : 4));
-    const int64_t total = (int64_t) a.n_seg * a.n_idx * a.units;
-    if (total == 0) return QWFN_OK;
-    const int64_t grid = std::min<int64_t>((total + COPY_THREADS - 1) / COPY_THREADS, 65536);
-    if (v16) hipLaunchKernelGGL(k_gather<uint4>, dim3((unsigned) grid), dim3(COPY_THREADS), 0, stream, a);
-    else     hipLaunchKernelGGL(k_gather<uint32_t>, dim3((unsigned) grid), dim3(COPY_THREADS), 0, stream, a);
+    const uint64_t units = seg_bytes / (v16 ? 16 : 4);
+    if (a.n_idx == 0) return QWFN_OK;
+    if (units >= (uint64_t(1) << 31))
+        return set_error(QWFN_ENOTSUP, "gather: rows of 8 GiB or more are not supported");
+    if (n_seg > 65535) return set_error(QWFN_ENOTSUP, "gather: at most 65535 segments");
+    // about 1024 workgroups over the whole copy, each at least one unit per lane
+    // and at most 4096 units (several rows when rows are short)
+    const uint64_t total = (uint64_t) n_seg * (uint64_t) a.n_idx * units;
+    const uint64_t per_wg = std::min<uint64_t>(4096, std::max<uint64_t>(COPY_THREADS, total / 1024));
+    const uint64_t rows = std::max<uint64_t>(1, std::min<uint64_t>(per_wg / units, (uint64_t) a.n_idx));
+    const uint64_t gx = ((uint64_t) a.n_idx + rows - 1) / rows;
+    if (gx >= (uint64_t(1) << 31)) return set_error(QWFN_ENOTSUP, "gather: too many index rows");
+    a.units = (uint32_t) units;
+    a.units_mul = recip32((int64_t) units);
+    a.rows = (uint32_t) rows;
+    const dim3 grid((unsigned) gx, (unsigned) n_seg);
+    if (v16) hipLaunchKernelGGL(k_gather<uint4>, grid, dim3(COPY_THREADS), 0, stream, a);
+    else     hipLaunchKernelGGL(k_gather<uint32_t>, grid, dim3(COPY_THREADS), 0, stream, a);
     return hip_check(hipGetLastError(), "gather launch");
 }
 
@@ -226,8 +246,8 @@ extern "C" int qwfn_get_rows_i32(const qwfn_tensor * src, const qwfn_tensor * id
         a.seg_off = 0; a.seg_stride = 0;
         a.idx = (const int32_t *) idx->data; a.n_idx = idx->ne[0];
         a.dst = (char *) dst->data; a.dst_row_stride = dst->nb[1]; a.dst_seg_stride = 0;
-        a.n_seg = 1; a.status = st;
-        return launch_gather(a, (size_t) src->ne[0] * 4, as_stream(stream));
+        a.status = st;
+        return launch_gather(a, (size_t) src->ne[0] * 4, 1, as_stream(stream));
     });
 }
 
@@ -252,8 +272,8 @@ extern "C" int qwfn_kv_gather_segments(const void * src, size_t src_row_stride, 
         a.seg_off = seg_off; a.seg_stride = seg_stride;
         a.idx = idx; a.n_idx = n_idx;
         a.dst = (char *) dst; a.dst_row_stride = dst_row_stride; a.dst_seg_stride = dst_seg_stride;
-        a.n_seg = n_seg; a.status = st;
-        return launch_gather(a, seg_bytes, as_stream(stream));
+        a.status = st;
+        return launch_gather(a, seg_bytes, n_seg, as_stream(stream));
     });
 }
 

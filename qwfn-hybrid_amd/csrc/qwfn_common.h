@@ -20,6 +20,16 @@ constexpr int QBLOCK  = 34;
 constexpr uint32_t DEVERR_SET_ROWS_INDEX = 1u << 0;
 constexpr uint32_t DEVERR_GET_ROWS_INDEX = 1u << 1;
 
+// x / d through m = ceil(2^32 / d): floor(x * m / 2^32) = floor(x / d) while
+// x * d < 2^32 (the host checks the ranges of a call); d = 1 needs no m.
+__device__ __forceinline__ uint32_t udiv(uint32_t x, uint32_t d, uint32_t m) {
+    return d == 1 ? x : __umulhi(x, m);
+}
+// the m of udiv, on the host
+inline uint32_t recip32(int64_t d) {
+    return d > 1 ? (uint32_t) (((uint64_t(1) << 32) + (uint64_t) d - 1) / (uint64_t) d) : 0u;
+}
+
 // ---- host-side error plumbing (runtime.cpp) ----
 // The message goes into a fixed thread-local buffer: recording an error never
 // allocates and never throws.
