@@ -1155,6 +1155,55 @@ __global__ __launch_bounds__(256) void k_fattn_merge(fa_args a) {
     }
 }
 
+// LSE merge for many query rows over few splits (k_fa_pre's key splits, at
+// most MERGE_ROWS_SPLITS): one 64-lane group per row, a lane per 4 dims; all
+// of a lane's partials and (max, sum) pairs are loaded before any is used.
+constexpr int MERGE_ROWS_SPLITS = 16;
+
+__global__ __launch_bounds__(256) void k_fattn_merge_rows(fa_args a) {
+    const uint32_t row = blockIdx.x * 4u + (threadIdx.x >> 6);   // (b * nh_kv + kvh) * R + r
+    const uint32_t n_rows = (uint32_t) a.B * (uint32_t) a.nh_kv * (uint32_t) a.R;
+    if (row >= n_rows) return;
+    const int q4 = threadIdx.x & 63;
+    const uint32_t bh = row / (uint32_t) a.R, r = row - bh * (uint32_t) a.R;
+    const uint32_t b = bh / (uint32_t) a.nh_kv, kvh = bh - b * (uint32_t) a.nh_kv;
+    const float2 * ml = a.part_ml + (size_t) bh * a.ns * a.R + r;
+    const float4 * po = (const float4 *) (a.part_o + ((size_t) bh * a.ns * a.R + r) * D) + q4;
+    const size_t sstride = (size_t) a.R * D / 4;
+    float2 e[MERGE_ROWS_SPLITS];
+    float4 o[MERGE_ROWS_SPLITS];
+#pragma unroll
+    for (int s = 0; s < MERGE_ROWS_SPLITS; s++) {
+        if (s < a.ns) {
+            e[s] = ml[(size_t) s * a.R];
+            o[s] = load_nt4(po + (size_t) s * sstride);
+        } else {
+            e[s] = make_float2(-INFINITY, 0.f);
+            o[s] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < MERGE_ROWS_SPLITS; s++) M = xmax(M, e[s].x);
+    float L = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int s = 0; s < MERGE_ROWS_SPLITS; s++) {
+        const float w = e[s].x == -INFINITY ? 0.f : exp2f(e[s].x - M);
+        L += w * e[s].y;
+        acc.x += w * o[s].x; acc.y += w * o[s].y; acc.z += w * o[s].z; acc.w += w * o[s].w;
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    acc.x *= inv; acc.y *= inv; acc.z *= inv; acc.w *= inv;
+    const uint32_t t = div_gqa(a, r), h = kvh * (uint32_t) a.gqa + (r - t * (uint32_t) a.gqa);
+    float * d = a.dst + (((size_t) b * a.T + t) * a.nh + h) * D + 4 * q4;
+    if (a.dst_vec) {
+        *(float4 *) d = acc;
+    } else {
+        d[0] = acc.x; d[1] = acc.y; d[2] = acc.z; d[3] = acc.w;
+    }
+}
+
 // ================================================================ decode / verify
 //
 // k_fa_dec: row groups of at most 32 query rows per KV head (decode, MTP
@@ -1738,11 +1787,480 @@ __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
     }
 }
 
+// ================================================================ prefill
+//
+// k_fa_pre: long query blocks (more than 32 query rows per KV head: prefill
+// chunks, long verify blocks) with a mask shared by the heads or none, GQA >= 4.
+// One block of 8 waves per CU holds 128 query rows of one KV head (16 rows a
+// wave: 16 tokens x 8 heads at GQA 8). Keys stream in chunks of 64 through LDS
+// DMA into a two-stage ring that the 8 waves share, so a block reads each K/V
+// row once for its 128 rows; the row groups of one (KV head, key split) are
+// placed on one XCD, whose L2 then serves the same rows to all of them. Per
+// chunk the block converts V to f16 once, transposed to [dim][key] (the PV A
+// operand of a lane is one 16-byte LDS read), repacks the K quants to
+// [block][key][32] (the QK A operand of a lane is one aligned 8-byte read),
+// and tabulates the K and V block scales; then each wave takes its 16 rows
+// over the 64 keys: exact i8 block dots (v_mfma_i32_16x16x32_i8, one q8_0
+// block each) scaled by d_q*d_k, one online-softmax step, and hi + lo f16
+// P*d_v on v_mfma_f32_16x16x32_f16 (32 keys a step). The LDS reads of the
+// next key tile (QK) and V block (PV) are issued ahead of the current one's
+// arithmetic. A wave whose rows see none of the
+// chunk's keys (a causal mask's upper triangle) skips it.
+
+constexpr int PRE_WAVES = 8;
+constexpr int PRE_ROWS  = 16 * PRE_WAVES;                 // 128 query rows per block
+constexpr int PRE_CK    = 64;                             // keys per chunk
+constexpr int PRE_KB    = PRE_CK * SEG;                   // 17408: one tensor's rows of a chunk
+constexpr int PRE_TDMA  = PRE_KB / 1024;                  // 17 wave DMAs per tensor
+constexpr int PRE_MGR   = 2 * PRE_CK / 16 + 1;            // 9 granules per mask row of a chunk
+constexpr int PRE_MROWS = PRE_ROWS / 4 + 1;               // 33 mask rows of a block at most (GQA >= 4)
+constexpr int PRE_MDMA  = (PRE_MROWS * PRE_MGR + 63) / 64;   // 5 wave DMAs for them
+constexpr int PRE_MOFF  = 2 * PRE_KB;                     // mask granules follow the K and V rows
+constexpr int PRE_STAGE = PRE_MOFF + PRE_MDMA * 1024;     // 39936 bytes
+constexpr int PRE_SLOTS = 2 * PRE_TDMA + PRE_MDMA;        // 39 DMA slots per chunk
+constexpr int PRE_SPW   = (PRE_SLOTS + PRE_WAVES - 1) / PRE_WAVES;   // 5 per wave
+constexpr int PRE_VTS   = 2 * PRE_CK + 16;                // 144: bytes per dim row of V^T (padded: no bank conflicts)
+constexpr int PRE_VT    = D * PRE_VTS;                    // 36864
+constexpr int PRE_KQ    = NBLK * PRE_CK * QK;             // 16384: a chunk's K quants [block][key][32]
+constexpr int PRE_QIMG  = NBLK * 16 * QK;                 // 4096: a wave's query quants [block][row][32]
+constexpr int PRE_QW    = PRE_QIMG + 16 * NBLK * 4;       // + d_q [row][block]
+static_assert(PRE_KB % 1024 == 0, "a tensor's rows of a chunk are whole wave DMAs");
+static_assert(PRE_WAVES * PRE_QW <= PRE_STAGE + PRE_VT, "the query images fit stage 1 and V^T");
+static_assert(PRE_CK == 64 && NBLK == PRE_WAVES, "the conversion pass: wave w takes V block w of every key");
+
+// V^T rows hold a chunk's keys in this order: key k = 32h + 16tt + 4g + i
+// (half h, key tile tt of the half, lane group g, i = 0..3) sits at position
+// 32h + 8g + 4tt + i, so the 8 keys a lane group's PV operand needs are
+// consecutive.
+
+// f16 pair (lo: byte B of s0, hi: byte B of s1) from two int8 values, exact.
+template <int B>
+__device__ __forceinline__ uint32_t cvt_i8_pair(uint32_t s0, uint32_t s1) {
+    uint32_t d;
+    if constexpr (B == 0)
+        asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+            "v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_0"
+            : "=&v"(d) : "v"(s0), "v"(s1));
+    else
+        asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
+            "v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1"
+            : "=&v"(d) : "v"(s0), "v"(s1));
+    return d;
+}
+
+template <bool MASKED>
+__global__ __launch_bounds__(PRE_WAVES * 64, 2) void k_fa_pre(fa_args a) {
+    asm volatile("" :: "s"(a.q), "s"(a.k), "s"(a.v), "s"(a.mask), "s"(a.part_o));
+    // stage 0 | stage 1 | V^T; the query images of the prologue use stage 1 and V^T
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * PRE_STAGE + PRE_VT + PRE_KQ];
+    __shared__ __attribute__((aligned(16))) uint16_t skv[2][NBLK][PRE_CK];   // [K|V][block][key] fp16 scales
+    uint8_t * const vt = lds + 2 * PRE_STAGE;
+    uint8_t * const kq = vt + PRE_VT;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int ln = lane & 15, lg = lane >> 4;
+
+    // ---- block -> (unit = (b, kvh, split), row group): the n_rg row groups of a
+    //      unit are blocks x, x + 8, ... of one XCD x ----
+    const int id = blockIdx.x;
+    const int xcd = id & 7, j = id >> 3;
+    const int ul = (int) udiv((uint32_t) j, (uint32_t) a.n_rg, a.nrg_mul);
+    const int rg = j - ul * a.n_rg;
+    const int unit = xcd + 8 * ul;
+    const int n_units = a.B * a.nh_kv * a.ns;
+    if (unit >= n_units) return;
+    const int bh = (int) udiv((uint32_t) unit, (uint32_t) a.ns, a.ns_mul);
+    const int split = unit - bh * a.ns;
+    const int b = bh / a.nh_kv, kvh = bh - b * a.nh_kv;
+    const int64_t k_lo = (int64_t) split * a.split_len;
+    const int64_t k_e = k_lo + a.split_len;
+    const int64_t k_hi = split == a.ns - 1 ? a.n_kv : (a.n_kv < k_e ? a.n_kv : k_e);
+    const int span = (int) (k_hi - k_lo);
+    const int n_chunks = (span + PRE_CK - 1) / PRE_CK;
+    const int r0 = rg * PRE_ROWS;
+    const int RW = a.R - r0 < PRE_ROWS ? a.R - r0 : PRE_ROWS;   // rows of this block
+    const int wr0 = 16 * wave;                                  // the wave's first row in the block
+    const int t0 = (int) div_gqa(a, (uint32_t) r0);
+
+    const char * kbase = a.k + (size_t) bmod(b, a.kb) * a.k_nb3 + (size_t) kvh * a.k_nb2;
+    const char * vbase = a.v + (size_t) bmod(b, a.vb) * a.v_nb3 + (size_t) kvh * a.v_nb2;
+    // mask rows: query positions t0 .. t0 + n_mrows - 1 (one row per position)
+    const char * mslice = MASKED ? a.mask + (size_t) bmod(b, a.m_ne3) * a.m_nb3 : nullptr;
+    const char * mslice_al = (const char *) ((uintptr_t) mslice & ~(uintptr_t) 15);
+    auto mrow_off = [&](int mr) -> uint32_t {
+        return (uint32_t) (mslice - mslice_al) + (uint32_t) ((size_t) (t0 + mr) * a.m_nb1);
+    };
+    const int n_mrows = MASKED ? (int) div_gqa(a, (uint32_t) (r0 + RW - 1)) - t0 + 1 : 0;
+    const int n_mdma = (n_mrows * PRE_MGR + 63) / 64;
+
+    // ---- DMA slots of a chunk: slot s lands at byte 1024 s of the stage. Slots
+    //      [0, 17) are the K rows (piece p = 64 s + lane is byte 16 (p % 17) of
+    //      key p / 17), [17, 34) the V rows, then the mask granules (granule
+    //      G = 64 m + lane is granule G % 9 of row G / 9; lanes past the rows
+    //      re-read the last one). Wave w issues slots w, w + 8, ... ----
+    uint32_t doff[PRE_SPW];
+    bool dlive[PRE_SPW];
+#pragma unroll
+    for (int s = 0; s < PRE_SPW; s++) {
+        const int slot = wave + PRE_WAVES * s;
+        uint32_t off = 0;
+        bool live = false;
+        if (slot < 2 * PRE_TDMA) {
+            const int tensor = slot >= PRE_TDMA;
+            const uint32_t p = (uint32_t) ((slot - tensor * PRE_TDMA) * 64 + lane), key = p / 17u, part = p - key * 17u;
+            off = key * (uint32_t) (tensor ? a.v_nb1 : a.k_nb1) + part * 16u;
+            live = true;
+        } else if (MASKED && slot < PRE_SLOTS && slot - 2 * PRE_TDMA < n_mdma) {
+            const int g = (slot - 2 * PRE_TDMA) * 64 + lane;
+            const int gc = g < n_mrows * PRE_MGR ? g : n_mrows * PRE_MGR - 1;
+            off = (mrow_off(gc / PRE_MGR) & ~15u) + 16u * (uint32_t) (gc % PRE_MGR);
+            live = true;
+        }
+        doff[s] = off;
+        dlive[s] = live;
+    }
+    const int64_t k_bytes = k_hi * (int64_t) a.k_nb1, v_bytes = k_hi * (int64_t) a.v_nb1;
+    // chunk c through resources based at its first key and ending at the
+    // split's end: keys past the split arrive as zeros (and are masked)
+    auto issue_chunk = [&](int c, uint8_t * st) __attribute__((always_inline)) {
+        const int64_t c0 = k_lo + (int64_t) c * PRE_CK;
+        const int64_t kc = c0 * (int64_t) a.k_nb1, vc = c0 * (int64_t) a.v_nb1;
+        const v4i rk = make_rsrc(kbase + kc, (uint32_t) std::min<int64_t>(k_bytes - kc, 0xffffffffll));
+        const v4i rv = make_rsrc(vbase + vc, (uint32_t) std::min<int64_t>(v_bytes - vc, 0xffffffffll));
+        v4i rm = rk;
+        if constexpr (MASKED)
+            rm = make_rsrc(mslice_al + c0 * 2, (uint32_t) (a.m_slice + (uint32_t) (mslice - mslice_al) - c0 * 2));
+#pragma unroll
+        for (int s = 0; s < PRE_SPW; s++) {
+            const int slot = wave + PRE_WAVES * s;
+            if (!dlive[s]) continue;
+            dma16_buf(slot < PRE_TDMA ? rk : slot < 2 * PRE_TDMA ? rv : rm, doff[s],
+                      __builtin_amdgcn_readfirstlane(lds_addr(st + slot * 1024)));
+        }
+    };
+    // fused append (as in k_fa_dec): the blocks whose keys hold appended rows
+    // quantise their KV head's part of them first, and their chunk DMAs read
+    // the rows only after these stores are done
+    if (a.app_n > 0) {
+        const int64_t alo = std::max<int64_t>(a.app_row0, k_lo), ahi = std::min<int64_t>(a.app_row0 + a.app_n, k_hi);
+        if (alo < ahi) {
+            const int units = (int) (ahi - alo) * NBLK * 2;
+            const int sub = threadIdx.x & 7;
+            for (int u0 = 0; u0 < units; u0 += PRE_WAVES * 8) {
+                const int uu0 = u0 + (int) (threadIdx.x >> 3);
+                const bool live = uu0 < units;
+                const int uu = live ? uu0 : 0;
+                const int tensor = uu & 1, jb = (uu >> 1) % NBLK;
+                const int64_t row = alo + (uu >> 1) / NBLK;
+                const float4 xv = *(const float4 *) ((tensor ? a.app_v : a.app_k) + (size_t) (row - a.app_row0) * a.app_nb1 +
+                                                     (size_t) (kvh * D + QK * jb + 4 * sub) * 4);
+                float x[4] = {xv.x, xv.y, xv.z, xv.w};
+                uint16_t d16;
+                float dqa;
+                const uint32_t q4 = dev::q8_quantize_lane4(x, a.x86 != 0, &d16, &dqa);
+                if (live) {
+                    char * bp = (char *) (tensor ? vbase + (size_t) row * a.v_nb1 : kbase + (size_t) row * a.k_nb1) + jb * QBLOCK;
+                    uint16_t * qp = (uint16_t *) (bp + 2 + sub * 4);
+                    qp[0] = (uint16_t) (q4 & 0xffffu);
+                    qp[1] = (uint16_t) (q4 >> 16);
+                    if (sub == 0) *(uint16_t *) bp = d16;
+                }
+            }
+            wait_vmcnt<0>();
+            __syncthreads();
+        }
+    }
+    if (n_chunks > 0) issue_chunk(0, lds);
+
+    // ---- prologue: each wave requantises its own 16 query rows (ggml's
+    //      quantiser; 4 lanes per (row, block)) into an image of its own, from
+    //      which lane (ln, lg) takes quants 8 lg .. 8 lg + 7 of each block of row ln ----
+    uint8_t * qimg = lds + PRE_STAGE + wave * PRE_QW;       // [block][row][32] int8
+    float * dql = (float *) (qimg + PRE_QIMG);                  // [16 rows][NBLK]
+    long qw[NBLK];
+    float dq[NBLK];
+    {
+        const int qrow = lane >> 2, ql = lane & 3;              // (row, quarter of a block)
+        const int r = r0 + wr0 + qrow;
+        const bool live = wr0 + qrow < RW;
+        const char * qp = a.q;
+        if (live) {
+            const uint32_t t = div_gqa(a, (uint32_t) r), h = (uint32_t) (kvh * a.gqa) + ((uint32_t) r - t * (uint32_t) a.gqa);
+            qp = a.q + (size_t) b * a.q_nb3 + (size_t) t * a.q_nb1 + (size_t) h * a.q_nb2 + (size_t) (8 * ql) * 4;
+        }
+        float4 xv[NBLK][2];
+#pragma unroll
+        for (int bb = 0; bb < NBLK; bb++) {
+            xv[bb][0] = live ? *(const float4 *) (qp + QK * bb * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+            xv[bb][1] = live ? *(const float4 *) (qp + QK * bb * 4 + 16) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        const float fs = a.scale * LOG2E;
+#pragma unroll
+        for (int bb = 0; bb < NBLK; bb++) {
+            float x[8] = {xv[bb][0].x, xv[bb][0].y, xv[bb][0].z, xv[bb][0].w,
+                          xv[bb][1].x, xv[bb][1].y, xv[bb][1].z, xv[bb][1].w};
+            uint32_t w[2];
+            uint16_t d16;
+            float dqv;
+            if (a.x86) dev::q8_quantize_lanes<8>(x, true, w, &d16, &dqv);
+            else       dev::q8_quantize_lanes<8>(x, false, w, &d16, &dqv);
+            // padding rows quantise zeros: all-zero quants and d_q = 0
+            *(uint2 *) (qimg + (bb * 16 + qrow) * QK + 8 * ql) = make_uint2(w[0], w[1]);
+            if (ql == 0) dql[qrow * NBLK + bb] = live ? dqv * fs : 0.f;
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int bb = 0; bb < NBLK; bb++) {
+            qw[bb] = *(const long *) (qimg + (bb * 16 + ln) * QK + 8 * lg);
+            dq[bb] = dql[ln * NBLK + bb];
+        }
+#pragma unroll
+        for (int bb = 0; bb < NBLK; bb++) asm volatile("" : "+v"(qw[bb]), "+v"(dq[bb]));
+    }
+
+    // the lane's mask row in a stage: its query position's granules, plus the
+    // row's offset within its first granule
+    const int rl_lane = wr0 + ln < RW ? wr0 + ln : 0;
+    const int mrow = MASKED ? (int) div_gqa(a, (uint32_t) (r0 + rl_lane)) - t0 : 0;
+    const uint32_t m_lane = MASKED ? (uint32_t) (PRE_MOFF + mrow * PRE_MGR * 16) + (mrow_off(mrow) & 15u) + 8u * (uint32_t) lg : 0u;
+    const bool wave_rows = wr0 < RW;   // the wave has rows of its own
+
+    v4f O[NBLK][2];
+    float m_run = -INFINITY, l_run = 0.f;
+#pragma unroll
+    for (int bb = 0; bb < NBLK; bb++) { O[bb][0] = v4f{0, 0, 0, 0}; O[bb][1] = v4f{0, 0, 0, 0}; }
+
+    // ---- the key loop: chunk c in stage c % 2; chunk c + 1 loads while chunk c
+    //      is converted and computed ----
+    for (int c = 0; c < n_chunks; c++) {
+        uint8_t * st = lds + (c & 1) * PRE_STAGE;
+        wait_vmcnt<0>();
+        __syncthreads();   // chunk c has landed; every wave is done with chunk c - 1 (and the prologue)
+        if (c + 1 < n_chunks) issue_chunk(c + 1, lds + ((c + 1) & 1) * PRE_STAGE);
+        // conversion pass: wave w takes V block w (dims 32w .. 32w+31) of the
+        // 64 keys: lane (key pair kp, half dh) converts dims 32w + 16dh .. +15 of
+        // the keys at V^T positions 2kp, 2kp + 1; lane k also tabulates the K
+        // and V scales of block w of key k
+        {
+            const int kp = lane & 31, dh = lane >> 5;
+            const int p0 = 2 * kp;
+            // the key at position p0 (its neighbour p0 + 1 is the next key)
+            const int key0 = 32 * (p0 >> 5) + 16 * ((p0 >> 2) & 1) + 4 * ((p0 >> 3) & 3) + (p0 & 3);
+            const uint8_t * src0 = st + PRE_KB + key0 * SEG + QBLOCK * wave + 2 + 16 * dh;
+            uint32_t s0[8], s1[8];
+#pragma unroll
+            for (int m = 0; m < 8; m++) {
+                s0[m] = *(const uint16_t *) (src0 + 2 * m);
+                s1[m] = *(const uint16_t *) (src0 + SEG + 2 * m);
+            }
+            const uint16_t kd = *(const uint16_t *) (st + lane * SEG + QBLOCK * wave);
+            const uint16_t vd = *(const uint16_t *) (st + PRE_KB + lane * SEG + QBLOCK * wave);
+            // K block w of key `lane`: its 32 quants to kq[w][lane]
+            {
+                const uint16_t * ks = (const uint16_t *) (st + lane * SEG + QBLOCK * wave + 2);
+                uint32_t kw[8];
+#pragma unroll
+                for (int m = 0; m < 8; m++) kw[m] = (uint32_t) ks[2 * m] | ((uint32_t) ks[2 * m + 1] << 16);
+                uint4 * kd4 = (uint4 *) (kq + (wave * PRE_CK + lane) * QK);
+                kd4[0] = make_uint4(kw[0], kw[1], kw[2], kw[3]);
+                kd4[1] = make_uint4(kw[4], kw[5], kw[6], kw[7]);
+            }
+            uint8_t * dst0 = vt + (32 * wave + 16 * dh) * PRE_VTS + 2 * p0;
+#pragma unroll
+            for (int m = 0; m < 8; m++) {
+                *(uint32_t *) (dst0 + (2 * m) * PRE_VTS) = cvt_i8_pair<0>(s0[m], s1[m]);
+                *(uint32_t *) (dst0 + (2 * m + 1) * PRE_VTS) = cvt_i8_pair<1>(s0[m], s1[m]);
+            }
+            skv[0][wave][lane] = kd;
+            skv[1][wave][lane] = vd;
+        }
+        __syncthreads();   // V^T and the scale tables of chunk c are complete
+
+        // ---- the wave's 16 rows over the chunk's keys: the lane's keys are
+        //      16 kt + 4 lg + i (key tile kt, i = 0..3) ----
+        const int kin = c * PRE_CK + 4 * lg;
+        uint32_t mv[4][4];
+        bool live = false;
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                mv[kt][i] = MASKED ? *(const uint16_t *) (st + m_lane + 32 * kt + 2 * i) : 0u;
+                live |= kin + 16 * kt + i < span && (!MASKED || mv[kt][i] != 0xFC00u);
+            }
+        if (!wave_rows || !__any(live)) continue;
+
+        // S = K Q^T per key tile (MFMA rows: keys; columns: the wave's rows);
+        // tile kt + 1's quants and scales are read while tile kt is computed
+        float s[4][4];
+        {
+            long kA[2][NBLK];
+            uint2 dk[2][NBLK];
+            auto load_tile = [&](int kt, long (&ka)[NBLK], uint2 (&dkk)[NBLK]) __attribute__((always_inline)) {
+                const uint8_t * kr = kq + (16 * kt + ln) * QK + 8 * lg;
+#pragma unroll
+                for (int bb = 0; bb < NBLK; bb++) {
+                    ka[bb] = *(const long *) (kr + bb * PRE_CK * QK);
+                    dkk[bb] = *(const uint2 *) &skv[0][bb][16 * kt + 4 * lg];
+                }
+            };
+            load_tile(0, kA[0], dk[0]);
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++) {
+                const int cb = kt & 1;
+                if (kt + 1 < 4) load_tile(kt + 1, kA[cb ^ 1], dk[cb ^ 1]);
+                v4i cc[NBLK];
+                cc[0] = __builtin_amdgcn_mfma_i32_16x16x32_i8(kA[cb][0], qw[0], v4i{0, 0, 0, 0}, 0, 0, 0);
+                cc[1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(kA[cb][1], qw[1], v4i{0, 0, 0, 0}, 0, 0, 0);
+                float sa[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int bb = 0; bb < NBLK; bb++) {
+                    if (bb + 2 < NBLK)
+                        cc[bb + 2] = __builtin_amdgcn_mfma_i32_16x16x32_i8(kA[cb][bb + 2], qw[bb + 2], v4i{0, 0, 0, 0}, 0, 0, 0);
+                    const float d = dq[bb];
+                    sa[0] = __builtin_fmaf((float) cc[bb][0], mul_f16lo(d, dk[cb][bb].x), sa[0]);
+                    sa[1] = __builtin_fmaf((float) cc[bb][1], mul_f16hi(d, dk[cb][bb].x), sa[1]);
+                    sa[2] = __builtin_fmaf((float) cc[bb][2], mul_f16lo(d, dk[cb][bb].y), sa[2]);
+                    sa[3] = __builtin_fmaf((float) cc[bb][3], mul_f16hi(d, dk[cb][bb].y), sa[3]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; i++) s[kt][i] = sa[i];
+            }
+        }
+
+        // ---- mask, online softmax (base 2) over the chunk's 64 keys ----
+        float p[4][4];
+        uint32_t p16[4][2];
+        {
+            float x[4][4];
+            float mloc = -INFINITY;
+            const bool tail = (c + 1) * PRE_CK > span;
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    x[kt][i] = MASKED ? fma_f16lo(mv[kt][i], LOG2E, s[kt][i]) : s[kt][i];
+                    if (tail && kin + 16 * kt + i >= span) x[kt][i] = -INFINITY;
+                    mloc = vmax(mloc, x[kt][i]);
+                }
+            mloc = xmax_lanes16_32(mloc);
+            const bool grow = mloc > m_run + RESCALE_SLACK;
+            float alpha = 1.f;
+            if (grow) {
+                alpha = __builtin_amdgcn_exp2f(m_run - mloc);
+                m_run = mloc;
+            }
+            const float m_use = m_run == -INFINITY ? 0.f : m_run;
+            float lsum = 0.f;
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    p[kt][i] = __builtin_amdgcn_exp2f(x[kt][i] - m_use);
+                    lsum += p[kt][i];
+                }
+                p16[kt][0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p[kt][0], p[kt][1]));
+                p16[kt][1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p[kt][2], p[kt][3]));
+            }
+            l_run = l_run * alpha + lsum;
+            if (__any(grow)) {
+                asm volatile("" ::: "memory");
+#pragma unroll
+                for (int bb = 0; bb < NBLK; bb++) { O[bb][0] *= alpha; O[bb][1] *= alpha; }
+            }
+        }
+
+        // ---- O += V^T (P d_v): per half of 32 keys (key tiles 2h, 2h + 1) and V
+        //      block, A = V^T rows 32bb + 16e + ln at the lane group's 8
+        //      positions, B = the same 8 keys' P d_v as f16 hi + lo; step n + 1's
+        //      operands are read while step n is computed ----
+        {
+            v8h A[2][2];
+            uint2 dvv[2][2];
+            auto load_step = [&](int n, v8h (&aa)[2], uint2 (&dd)[2]) __attribute__((always_inline)) {
+                const int h = n >> 3, bb = n & 7;
+                const uint8_t * va = vt + (32 * bb + ln) * PRE_VTS + (32 * h + 8 * lg) * 2;
+                aa[0] = *(const v8h *) va;
+                aa[1] = *(const v8h *) (va + 16 * PRE_VTS);
+                dd[0] = *(const uint2 *) &skv[1][bb][32 * h + 4 * lg];
+                dd[1] = *(const uint2 *) &skv[1][bb][32 * h + 16 + 4 * lg];
+            };
+            load_step(0, A[0], dvv[0]);
+#pragma unroll
+            for (int n = 0; n < 2 * NBLK; n++) {
+                const int cb = n & 1, h = n >> 3, bb = n & 7;
+                if (n + 1 < 2 * NBLK) load_step(n + 1, A[cb ^ 1], dvv[cb ^ 1]);
+                uint32_t bh0[2], bl0[2], bh1[2], bl1[2];
+                {
+                    const uint32_t dv[2] = {dvv[cb][0].x, dvv[cb][0].y};
+                    pdv_hilo(p[2 * h], p16[2 * h], dv, bh0, bl0);
+                }
+                {
+                    const uint32_t dv[2] = {dvv[cb][1].x, dvv[cb][1].y};
+                    pdv_hilo(p[2 * h + 1], p16[2 * h + 1], dv, bh1, bl1);
+                }
+                const v8h Bh = __builtin_bit_cast(v8h, make_uint4(bh0[0], bh0[1], bh1[0], bh1[1]));
+                const v8h Bl = __builtin_bit_cast(v8h, make_uint4(bl0[0], bl0[1], bl1[0], bl1[1]));
+                O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[cb][0], Bh, O[bb][0], 0, 0, 0);
+                O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[cb][1], Bh, O[bb][1], 0, 0, 0);
+                O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[cb][0], Bl, O[bb][0], 0, 0, 0);
+                O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[cb][1], Bl, O[bb][1], 0, 0, 0);
+            }
+        }
+    }
+
+    // ---- epilogue: lane (ln, lg) holds dims 32bb + 16e + 4lg + i of row ln in
+    //      O[bb][e][i] ----
+    const float L = sum_lanes16_32(l_run);
+    if (!wave_rows) return;
+    int tid_e = (int) threadIdx.x;
+    asm volatile("" : "+v"(tid_e));
+    const int ln_e = tid_e & 15, lg_e = (tid_e >> 4) & 3;
+    const int rl = wr0 + ln_e;
+    if (rl >= RW) return;
+    const int r = r0 + rl;
+    const int tq = (int) div_gqa(a, (uint32_t) r), h = kvh * a.gqa + (r - tq * a.gqa);
+    float * out;
+    float oscale;
+    const bool nsplit = a.ns > 1;
+    if (!nsplit) {
+        out = a.dst + (((size_t) b * a.T + tq) * a.nh + h) * D + 4 * lg_e;
+        oscale = L > 0.f ? 1.f / L : 0.f;
+    } else {
+        const size_t bhs = (size_t) bh * a.ns + split;
+        out = a.part_o + (bhs * a.R + r) * D + 4 * lg_e;
+        oscale = 1.f;
+        if (lg_e == 0) {
+            float2 * mlp = &a.part_ml[bhs * a.R + r];
+            __builtin_nontemporal_store(m_run, &mlp->x);
+            __builtin_nontemporal_store(L, &mlp->y);
+        }
+    }
+#pragma unroll
+    for (int bb = 0; bb < NBLK; bb++) {
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const v4f o = O[bb][e] * oscale;
+            float * op = out + 32 * bb + 16 * e;
+            if (nsplit) {
+                store_nt4(op, make_float4(o[0], o[1], o[2], o[3]));
+            } else if (a.dst_vec) {
+                *(float4 *) op = make_float4(o[0], o[1], o[2], o[3]);
+            } else {
+                op[0] = o[0]; op[1] = o[1]; op[2] = o[2]; op[3] = o[3];
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------- planning
 
 // Attention kernel shapes: waves per block, query tiles, keys per wave.
 enum fa_kind {
     FA_DEC,       // k_fa_dec: at most 32 query rows per KV head, 8 waves, one block per CU
+    FA_PRE,       // k_fa_pre: longer query blocks, mask shared by the heads (or none), GQA >= 4
     FA_P4_T1,     // 4 waves, one tile, 64-key chunks, two blocks per CU
     FA_P4_T2,     // 4 waves, two tiles, 32 keys per wave, two blocks per CU; mask tiles of
                   // more than MASK_ROWS_PAIR rows go to 8 waves over the same 64-key chunks
@@ -1787,6 +2305,7 @@ int check_no_scratch() {
                                (const void *) k_fa_dec<1, false, true, false>, (const void *) k_fa_dec<1, true, true, false>,
                                (const void *) k_fa_dec<2, false, true, false>, (const void *) k_fa_dec<2, true, true, false>,
                                (const void *) k_fa_dec<1, false, false, true>, (const void *) k_fa_dec<2, false, false, true>,
+                               (const void *) k_fa_pre<false>, (const void *) k_fa_pre<true>,
                                (const void *) k_fattn_q8_0<2, true, WAVES, 16, false>,
                                (const void *) k_fattn_q8_0<1, false, WAVES_PAIR, 16, false>,
                                (const void *) k_fattn_q8_0<1, true, WAVES_PAIR, 16, false>,
@@ -1864,6 +2383,38 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
     const int64_t B = q->ne[3];
     const bool dec = R <= 32;
     pl->kind = dec ? FA_DEC : rw == 16 ? FA_P4_T1 : FA_P4_T2;
+    if (!dec && !gather && !seq_n_kv && (!mask || mask->ne[2] == 1) && gqa >= 4) {
+        // k_fa_pre: 128-row blocks; key splits of whole 64-key chunks (at least
+        // two per split), about one block per CU; the row groups of a (batch,
+        // KV head, split) unit share an XCD
+        pl->kind = FA_PRE;
+        pl->R = (int32_t) R;
+        pl->rw = PRE_ROWS;
+        pl->RT = PRE_WAVES;
+        pl->n_rg = (int32_t) ((R + PRE_ROWS - 1) / PRE_ROWS);
+        pl->gqa = (int32_t) gqa;
+        const int64_t per = nh_kv * B * pl->n_rg;
+        int64_t ns = std::max<int64_t>(1, (256 + per - 1) / per);
+        ns = std::min<int64_t>(ns, std::max<int64_t>(1, n_kv / (2 * PRE_CK)));
+        if (const int32_t force = g_force_splits.load(std::memory_order_relaxed)) ns = force;
+        ns = std::max<int64_t>(1, std::min<int64_t>(ns, ns_cap));
+        int64_t split_len = (n_kv + ns - 1) / ns;
+        split_len = std::max<int64_t>(PRE_CK, (split_len + PRE_CK - 1) / PRE_CK * PRE_CK);
+        ns = std::max<int64_t>(1, (n_kv + split_len - 1) / split_len);
+        if (ns > MAX_SPLITS)
+            return set_error(QWFN_ENOTSUP, "flash_attn_ext: " + std::to_string(ns) + " key splits requested, at most " +
+                                               std::to_string(MAX_SPLITS) + " supported");
+        pl->ns = (int32_t) ns;
+        pl->split_len = (int32_t) split_len;
+        pl->max_span = split_len;
+        pl->ragged = 0;
+        const size_t n_part = ns > 1 ? (size_t) (B * nh_kv * ns * R) : 0;
+        size_t off = align256(n_part * D * sizeof(float));
+        pl->off_ml = off;
+        off = align256(off + n_part * sizeof(float2));
+        pl->ws_bytes = std::max<size_t>(off, 256);
+        return QWFN_OK;
+    }
     pl->R = (int32_t) R;
     pl->rw = rw;
     pl->RT = rw / 16;
@@ -2135,6 +2686,28 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
         a.app_n = (int32_t) app->src_k->ne[1];
     }
 
+    if (pl.kind == FA_PRE) {
+        const int64_t units = (int64_t) a.B * a.nh_kv * a.ns;
+        const int64_t grid = 8 * (int64_t) a.n_rg * ((units + 7) / 8);
+        if (grid >= (int64_t(1) << 31) || grid * a.n_rg >= (int64_t(1) << 32) || units * a.ns >= (int64_t(1) << 32))
+            return set_error(QWFN_ENOTSUP, "flash_attn_ext: grid too large");
+        a.ns_mul = recip32(a.ns);
+        a.nrg_mul = recip32(a.n_rg);
+        const dim3 g((unsigned) grid), bd(PRE_WAVES * 64);
+        if (a.mask) hipLaunchKernelGGL((k_fa_pre<true>), g, bd, 0, as_stream(stream), a);
+        else        hipLaunchKernelGGL((k_fa_pre<false>), g, bd, 0, as_stream(stream), a);
+        if (int rc = hip_check(hipGetLastError(), "flash_attn launch")) return rc;
+        if (a.ns > 1) {
+            const int64_t rows = (int64_t) a.B * a.nh_kv * a.R;
+            if (rows * 4 > 0x7fffffff) return set_error(QWFN_EINVAL, "flash_attn_ext: merge grid too large");
+            if (a.ns <= MERGE_ROWS_SPLITS)
+                hipLaunchKernelGGL(k_fattn_merge_rows, dim3((unsigned) ((rows + 3) / 4)), dim3(256), 0, as_stream(stream), a);
+            else
+                hipLaunchKernelGGL(k_fattn_merge<false>, dim3((unsigned) (rows * 4)), dim3(256), 0, as_stream(stream), a);
+            if (int rc = hip_check(hipGetLastError(), "flash_attn merge launch")) return rc;
+        }
+        return QWFN_OK;
+    }
     if (pl.kind == FA_DEC) a.n_rg = 1;
     const int64_t n_units = a.ragged ? (int64_t) a.r_units : (int64_t) a.B * a.ns;
     const int64_t units = n_units >= 8 ? (n_units + 7) / 8 * 8 : n_units;
@@ -2180,6 +2753,7 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
     } else {
     switch (pl.kind) {
         case FA_DEC:
+        case FA_PRE:
             break;
         case FA_P4_T1:
             if (mt) hipLaunchKernelGGL((k_fattn_q8_0<1, true, WAVES_PAIR, 16, false>), g, b4, 0, st, a);
