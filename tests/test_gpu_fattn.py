@@ -203,7 +203,7 @@ def test_batched_ragged_depths(gpu, oracle):
         check(got[s], ref)
 
 
-def test_prefill_rows_through_decode_kernel(gpu, oracle):
+def test_prefill_rows_64(gpu, oracle):
     """64 new positions at depth 1000, causal (many row groups per KV head)."""
     K = gpu
     T, n_past = 64, 1000
@@ -263,7 +263,8 @@ def test_gathered_inputs_padded(gpu, oracle):
 
 @pytest.mark.parametrize("n_past,T,nh,variant,first_off", [(100, 1, 16, O.Q8_X86, 0), (16384, 3, 16, O.Q8_X86, 0),
                                                            (16384, 3, 24, O.Q8_REF, 0), (65536, 3, 16, O.Q8_X86, 0),
-                                                           (4094, 3, 16, O.Q8_X86, -2)])
+                                                           (4094, 3, 16, O.Q8_X86, -2), (2000, 8, 16, O.Q8_X86, 0),
+                                                           (4000, 40, 24, O.Q8_REF, -5)])
 def test_fused_append_equals_separate_calls(gpu, oracle, n_past, T, nh, variant, first_off):
     """qwfn_flash_attn_ext_q8_0_append writes the same cache bytes and returns the
     same output bits as the two-tensor append followed by the attention call;
