@@ -218,6 +218,52 @@ int qwfn_qsa_select_cells(const uint16_t * pool, size_t pool_nb1, int64_t n_bloc
                           const int32_t * blk_cells, int32_t ratio, int32_t * cells, int32_t * top, void * ws,
                           size_t ws_bytes, void * stream);
 
+/* ------------------------------------------------- QSA index producer */
+
+/* The indexer's key geometry and the rope / norm constants of the model
+ * (qwfn_hparams.h:26, :34-36, :53): idx_dim = idx_key_len (128), n_dims =
+ * rope_dim (64), sections = mrope_sections {11, 11, 10, 0}, freq_base =
+ * rope_freq_base (1e7), rms_eps (1e-6). */
+typedef struct qwfn_qsa_pool_cfg {
+    int32_t idx_dim;
+    int32_t n_dims;
+    int32_t sections[4];
+    float   freq_base;
+    float   rms_eps;
+} qwfn_qsa_pool_cfg;
+void qwfn_qsa_pool_cfg_default(qwfn_qsa_pool_cfg * cfg);
+
+/* ggml_set_rows of F32 rows into an F16 tensor (IEEE round to nearest even):
+ * dst F16 [ne0, rows] (row stride nb[1]), src F32 [ne0, n], idx I32 [n]
+ * (device). An index outside [0, rows) skips its row and sets bit 0 of
+ * qwfn_device_status. The decode step's raw indexer key into the index cache
+ * (qwfn_graph.cpp:536-543) is this op with n = 1. */
+int qwfn_set_rows_f16(const qwfn_tensor * dst, const qwfn_tensor * src, const qwfn_tensor * idx, void * stream);
+
+/* qsa_dec_index (qwfn_graph.cpp:529-554) for one decode position, one launch:
+ * the raw key k_raw (F32 [idx_dim], device; NULL: no key is written) into row
+ * *write_idx of the index cache (F16 [ic_rows][idx_dim]), then the block's
+ * pooled key -- qsa_pool_blocks (:282-301): the mean of index-cache rows
+ * member_idx[0 .. ratio-1] (the new key among them read from the call's own
+ * value), RMS norm, times k_norm_w (F32 [idx_dim]), IMROPE at positions
+ * blk_pos[0..3] -- rounded to F16 into row *blk_idx of the pool cache (F16
+ * [pool_rows][idx_dim]). write_idx, member_idx, blk_pos and blk_idx are the
+ * device inputs qwfn_qsa_decode_prepare writes. Out-of-range rows are
+ * skipped and flagged in qwfn_device_status. */
+int qwfn_qsa_pool_decode(uint16_t * idx_cache, int64_t ic_rows, const float * k_raw, const int32_t * write_idx,
+                         const int32_t * member_idx, int32_t ratio, const int32_t * blk_pos, const int32_t * blk_idx,
+                         const float * k_norm_w, uint16_t * pool, int64_t pool_rows, const qwfn_qsa_pool_cfg * cfg,
+                         void * stream);
+
+/* The pooled keys of every whole block after a prefill or a restore
+ * (engine::qsa_pool_rebuild, qwfn_engine.cpp:1121-1145, through
+ * graph_builder::qsa_pool_rebuild, qwfn_graph.cpp:478-495): block b <
+ * n_past / ratio pools index-cache rows b*ratio .. b*ratio + ratio - 1 at
+ * position b*ratio into pool row b. One launch for all blocks. */
+int qwfn_qsa_pool_rebuild(const uint16_t * idx_cache, int64_t ic_rows, int64_t n_past, int32_t ratio,
+                          const float * k_norm_w, uint16_t * pool, int64_t pool_rows, const qwfn_qsa_pool_cfg * cfg,
+                          void * stream);
+
 /* ---------------------------------------------------------------- masks */
 
 /* Causal F16 mask of T query rows over n_kv keys, row i at byte i*row_stride:

@@ -411,3 +411,70 @@ int oracle_attn_f64(const oracle_view * q, const oracle_view * k, const oracle_v
     free(qrow); free(Q_q); free(kd); free(vd); free(s); free(acc);
     return 0;
 }
+
+/* ------------------------------------------------------ QSA index producer */
+
+void oracle_rms_norm_f32(const float * x, float * y, int64_t n, float eps) {
+    double sum = 0.0;
+    for (int64_t i = 0; i < n; i++) sum += (double) (x[i] * x[i]);
+    const float mean = (float) (sum / (double) n);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (int64_t i = 0; i < n; i++) y[i] = x[i] * scale;
+}
+
+void oracle_rope_multi_f32(const float * x, float * y, int64_t ne0, int n_dims, const int32_t pos[4],
+                           const int sections[4], int imrope, float freq_base) {
+    const float theta_scale = powf(freq_base, -2.0f / (float) n_dims);
+    const int sect_dims = sections[0] + sections[1] + sections[2] + sections[3];
+    const int sec_w = sections[0] + sections[1];
+    float th[4] = {(float) pos[0], (float) pos[1], (float) pos[2], (float) pos[3]};
+    for (int64_t i = n_dims; i < ne0; i++) y[i] = x[i];
+    for (int k = 0; k < n_dims / 2; k++) {
+        const int sector = k % sect_dims;
+        int s;
+        if (imrope) {
+            if (sector % 3 == 1 && sector < 3 * sections[1]) s = 1;
+            else if (sector % 3 == 2 && sector < 3 * sections[2]) s = 2;
+            else if (sector % 3 == 0 && sector < 3 * sections[0]) s = 0;
+            else s = 3;
+        } else {
+            s = sector < sections[0] ? 0 : sector < sec_w ? 1 : sector < sec_w + sections[2] ? 2 : 3;
+        }
+        const float theta = th[s];
+        const float c = cosf(theta), sn = sinf(theta);
+        const float x0 = x[k], x1 = x[k + n_dims / 2];
+        y[k] = x0 * c - x1 * sn;
+        y[k + n_dims / 2] = x0 * sn + x1 * c;
+        for (int j = 0; j < 4; j++) th[j] *= theta_scale;
+    }
+}
+
+int oracle_set_rows_f16(uint16_t * dst, int64_t dst_rows, int64_t ne0, const float * src, const int32_t * idx,
+                        int64_t n) {
+    for (int64_t i = 0; i < n; i++)
+        if (idx[i] < 0 || idx[i] >= dst_rows) return -1;
+    for (int64_t i = 0; i < n; i++)
+        for (int64_t j = 0; j < ne0; j++) dst[(size_t) idx[i] * ne0 + j] = oracle_fp32_to_fp16(src[(size_t) i * ne0 + j]);
+    return 0;
+}
+
+void oracle_qsa_pool_blocks(const uint16_t * ic, int64_t idx_dim, const int32_t * members, int64_t r, int64_t n_blk,
+                            const float * k_norm_w, const int32_t * pos4, const int sections[4], float eps,
+                            float freq_base, int n_dims, uint16_t * out) {
+    float * acc = malloc(sizeof(float) * (size_t) idx_dim * 3);
+    float * nrm = acc + idx_dim;
+    float * rot = nrm + idx_dim;
+    const float inv_r = 1.0f / (float) r;
+    for (int64_t b = 0; b < n_blk; b++) {
+        for (int64_t d = 0; d < idx_dim; d++) acc[d] = oracle_fp16_to_fp32(ic[(size_t) members[b * r] * idx_dim + d]);
+        for (int64_t m = 1; m < r; m++)
+            for (int64_t d = 0; d < idx_dim; d++)
+                acc[d] = acc[d] + oracle_fp16_to_fp32(ic[(size_t) members[b * r + m] * idx_dim + d]);
+        for (int64_t d = 0; d < idx_dim; d++) acc[d] = acc[d] * inv_r;
+        oracle_rms_norm_f32(acc, nrm, idx_dim, eps);
+        for (int64_t d = 0; d < idx_dim; d++) nrm[d] = nrm[d] * k_norm_w[d];
+        oracle_rope_multi_f32(nrm, rot, idx_dim, n_dims, pos4 + 4 * b, sections, 1, freq_base);
+        for (int64_t d = 0; d < idx_dim; d++) out[(size_t) b * idx_dim + d] = oracle_fp32_to_fp16(rot[d]);
+    }
+    free(acc);
+}

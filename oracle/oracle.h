@@ -92,6 +92,33 @@ int oracle_flash_attn_ext_q8_0(const oracle_view * q, const oracle_view * k, con
 int oracle_attn_f64(const oracle_view * q, const oracle_view * k, const oracle_view * v,
                     const oracle_view * mask, double scale, double * dst, int quantize_q);
 
+/* ---- QSA index producer (qwfn_graph.cpp:282-301 qsa_pool_blocks, :529-554
+ * qsa_dec_index, :478-495 qsa_pool_rebuild) ----
+ * ggml_rms_norm (ggml-cpu): the squares summed in double, mean = (float)
+ * (sum / n), y = x * (1.0f / sqrtf(mean + eps)).  Pinned by its closed form. */
+void oracle_rms_norm_f32(const float * x, float * y, int64_t n, float eps);
+/* ggml_rope_multi on one head of ne0 values, GGML_ROPE_TYPE_IMROPE (imrope = 1)
+ * or MROPE (imrope = 0), freq_scale 1, ext_factor 0, attn_factor 1: the first
+ * n_dims values rotate in neox pairs (i, i + n_dims/2); pair i turns by
+ * theta_s * theta_scale^i (a running float product) for the position of its
+ * section s, theta_scale = powf(freq_base, -2/n_dims); the rest pass through.
+ * pos = {t, h, w, e}.  Pinned by the reduction to standard neox rope at equal
+ * positions, norm preservation, relative-position invariance and an fp64
+ * restatement (tests). */
+void oracle_rope_multi_f32(const float * x, float * y, int64_t ne0, int n_dims, const int32_t pos[4],
+                           const int sections[4], int imrope, float freq_base);
+/* F32 rows to F16 rows (ggml_set_rows into an F16 tensor): dst row idx[i] =
+ * fp16(src row i).  Returns 0, or -1 for an index outside [0, dst_rows). */
+int oracle_set_rows_f16(uint16_t * dst, int64_t dst_rows, int64_t ne0, const float * src, const int32_t * idx,
+                        int64_t n);
+/* qsa_pool_blocks for n_blk blocks: block b pools the F16 index-cache rows
+ * members[b*r .. b*r+r-1] (mean: sequential adds, then * (1.0f/r)), RMS-norms
+ * with eps, multiplies by k_norm_w, ropes at pos4[4*b .. 4*b+3] (t, h, w, e),
+ * and stores fp16 of the result at out[b]. */
+void oracle_qsa_pool_blocks(const uint16_t * ic, int64_t idx_dim, const int32_t * members, int64_t r, int64_t n_blk,
+                            const float * k_norm_w, const int32_t * pos4, const int sections[4], float eps,
+                            float freq_base, int n_dims, uint16_t * out);
+
 #ifdef __cplusplus
 }
 #endif

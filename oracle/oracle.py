@@ -68,6 +68,11 @@ def lib():
         L.oracle_flash_attn_ext_q8_0.argtypes = [ctypes.POINTER(View)] * 4 + [
             ctypes.c_float, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int]
         L.oracle_attn_f64.argtypes = [ctypes.POINTER(View)] * 4 + [ctypes.c_double, vp, ctypes.c_int]
+        L.oracle_rms_norm_f32.argtypes = [vp, vp, i64, ctypes.c_float]
+        L.oracle_rope_multi_f32.argtypes = [vp, vp, i64, ctypes.c_int, vp, vp, ctypes.c_int, ctypes.c_float]
+        L.oracle_set_rows_f16.argtypes = [vp, i64, i64, vp, vp, i64]
+        L.oracle_qsa_pool_blocks.argtypes = [vp, i64, vp, i64, i64, vp, vp, vp, ctypes.c_float, ctypes.c_float,
+                                             ctypes.c_int, vp]
         _lib = L
     return _lib
 
@@ -247,3 +252,62 @@ def causal_mask(T: int, n_past: int, n_kv: int | None = None) -> np.ndarray:
     for i in range(T):
         m[i, :min(n_kv, n_past + i + 1)] = F16_ZERO
     return m
+
+
+# ------------------------------------------------------- QSA index producer
+
+IMROPE_SECTIONS = (11, 11, 10, 0)     # qwfn_hparams.h:36
+ROPE_FREQ_BASE = 10000000.0           # qwfn_hparams.h:34
+ROPE_DIM = 64                         # qwfn_hparams.h:35
+RMS_EPS = 1e-6                        # qwfn_hparams.h:26
+
+
+def rms_norm(x: np.ndarray, eps: float = RMS_EPS) -> np.ndarray:
+    """ggml_rms_norm over the last axis (float32)."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    n = x.shape[-1]
+    xf, yf = x.reshape(-1, n), y.reshape(-1, n)
+    for i in range(xf.shape[0]):
+        lib().oracle_rms_norm_f32(_p(xf[i]), _p(yf[i]), n, eps)
+    return y
+
+
+def rope_multi(x: np.ndarray, pos, n_dims: int = ROPE_DIM, sections=IMROPE_SECTIONS, imrope: bool = True,
+               freq_base: float = ROPE_FREQ_BASE) -> np.ndarray:
+    """ggml_rope_multi of one or more heads (last axis) at one position (t, h, w, e)."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    n = x.shape[-1]
+    p4 = np.ascontiguousarray(np.broadcast_to(np.asarray(pos, np.int32), (4,)))
+    sec = np.ascontiguousarray(np.asarray(sections, np.int32))
+    xf, yf = x.reshape(-1, n), y.reshape(-1, n)
+    for i in range(xf.shape[0]):
+        lib().oracle_rope_multi_f32(_p(xf[i]), _p(yf[i]), n, n_dims, _p(p4), _p(sec), int(imrope), freq_base)
+    return y
+
+
+def set_rows_f16(dst_bits: np.ndarray, src: np.ndarray, idx: np.ndarray) -> None:
+    """dst_bits uint16 [rows, ne0] in place: row idx[i] = fp16(src[i])."""
+    src = np.ascontiguousarray(src, np.float32)
+    idx = np.ascontiguousarray(idx, np.int32)
+    rc = lib().oracle_set_rows_f16(_p(dst_bits), dst_bits.shape[0], dst_bits.shape[1], _p(src), _p(idx), len(idx))
+    if rc:
+        raise IndexError("set_rows_f16: index out of range")
+
+
+def qsa_pool_blocks(ic_bits: np.ndarray, members: np.ndarray, r: int, k_norm_w: np.ndarray, pos4: np.ndarray,
+                    n_dims: int = ROPE_DIM, sections=IMROPE_SECTIONS, eps: float = RMS_EPS,
+                    freq_base: float = ROPE_FREQ_BASE) -> np.ndarray:
+    """Pooled F16 bits [n_blk, idx_dim]: members [n_blk * r] rows of ic_bits (uint16 [rows, idx_dim]),
+    pos4 [n_blk, 4] int32 (t, h, w, e)."""
+    ic_bits = np.ascontiguousarray(ic_bits, np.uint16)
+    members = np.ascontiguousarray(members, np.int32)
+    n_blk = len(members) // r
+    out = np.zeros((n_blk, ic_bits.shape[1]), np.uint16)
+    w = np.ascontiguousarray(k_norm_w, np.float32)
+    p4 = np.ascontiguousarray(pos4, np.int32).reshape(-1)
+    sec = np.ascontiguousarray(np.asarray(sections, np.int32))
+    lib().oracle_qsa_pool_blocks(_p(ic_bits), ic_bits.shape[1], _p(members), r, n_blk, _p(w), _p(p4), _p(sec),
+                                 eps, freq_base, n_dims, _p(out))
+    return out

@@ -1,0 +1,271 @@
+// The QSA index producer on the device: the decode step's raw indexer key into
+// the F16 index cache and the pooled key of its block into the pool cache
+// (graph_builder::qsa_dec_index, qwfn_graph.cpp:529-554), the rebuild of every
+// whole block's pooled key after a prefill or restore (engine::qsa_pool_rebuild
+// qwfn_engine.cpp:1107-1148 -> graph_builder::qsa_pool_rebuild,
+// qwfn_graph.cpp:478-495), and ggml_set_rows of F32 rows into an F16 tensor.
+//
+// A pooled key (qsa_pool_blocks, qwfn_graph.cpp:282-301): the block's r member
+// rows of the index cache (F16 -> F32) added in member order, times 1/r, RMS
+// normed (squares summed in double), times the k_norm weight, roped at the
+// block's first cell (all four sections), rounded to F16. One wave per block:
+// the block's key sits in LDS; lane k < n_dims/2 rotates pair k.
+#include "qwfn_common.h"
+#include "qwfn_state.h"
+#include "rope_device.h"
+
+#include <cmath>
+
+namespace qwfn {
+namespace {
+
+constexpr int POOL_MAX_DIM = 256;     // index key length, at most
+
+// fp16 <-> fp32 (IEEE; the f32 -> f16 conversion rounds to nearest even)
+__device__ __forceinline__ uint16_t f2h(float x) { return __builtin_bit_cast(uint16_t, (_Float16) x); }
+__device__ __forceinline__ float h2f(uint16_t h) { return (float) __builtin_bit_cast(_Float16, h); }
+constexpr int POOL_WAVES = 4;         // blocks per workgroup
+
+struct pool_args {
+    uint16_t *       ic;          // F16 [ic_rows][dim]
+    int64_t          ic_rows;
+    uint16_t *       pool;        // F16 [pool_rows][dim]
+    int64_t          pool_rows;
+    int32_t          dim;
+    int32_t          r;
+    float            inv_r;       // 1.0f / r (host float division, as ggml_scale's argument)
+    float            eps;
+    const float *    w;           // k_norm weight F32 [dim]
+    rope_params      rp;
+    int64_t          n_blk;       // rebuild: blocks 0 .. n_blk-1
+    // decode: one block from the per-token inputs (device)
+    const float *    k_raw;       // F32 [dim] or null
+    const int32_t *  write_idx;
+    const int32_t *  member_idx;  // [r]
+    const int32_t *  blk_pos;     // [4]
+    const int32_t *  blk_idx;
+    uint32_t *       status;
+};
+
+template <bool DECODE>
+__global__ __launch_bounds__(POOL_WAVES * 64) void k_qsa_pool(pool_args a) {
+    __shared__ float xs[POOL_WAVES][POOL_MAX_DIM];
+    __shared__ uint16_t key16[POOL_WAVES][POOL_MAX_DIM];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int64_t blk = (int64_t) blockIdx.x * POOL_WAVES + wv;
+    if (!DECODE && blk >= a.n_blk) return;
+    if (DECODE && blk > 0) return;
+    float * x = xs[wv];
+    const int dim = a.dim;
+
+    int32_t wrow = -1;
+    if constexpr (DECODE) {
+        // the raw key into the index cache at write_idx (F32 -> F16, RNE); the
+        // pooling below takes it from registers, not from memory
+        wrow = *a.write_idx;
+        const bool wok = wrow >= 0 && wrow < a.ic_rows;
+        if (a.k_raw) {
+            for (int d = lane; d < dim; d += 64) {
+                const uint16_t h = f2h(a.k_raw[d]);
+                key16[wv][d] = h;
+                if (wok) a.ic[(size_t) wrow * dim + d] = h;
+            }
+            if (!wok && lane == 0) atomicOr(a.status, DEVERR_SET_ROWS_INDEX);
+        } else {
+            wrow = -1;
+        }
+    }
+    // mean of the member rows, in member order
+    for (int d = lane; d < dim; d += 64) {
+        float acc = 0.f;
+        for (int m = 0; m < a.r; m++) {
+            const int64_t row = DECODE ? (int64_t) a.member_idx[m] : blk * a.r + m;
+            float v;
+            if (DECODE && row == wrow) {
+                v = h2f(key16[wv][d]);
+            } else if (row >= 0 && row < a.ic_rows) {
+                v = h2f(a.ic[(size_t) row * dim + d]);
+            } else {
+                v = 0.f;
+                if (d == lane && lane == 0) atomicOr(a.status, DEVERR_GET_ROWS_INDEX);
+            }
+            acc = m == 0 ? v : __fadd_rn(acc, v);
+        }
+        x[d] = __fmul_rn(acc, a.inv_r);
+    }
+    // RMS norm: the squares (float) summed in double across the wave
+    double sq = 0.0;
+    for (int d = lane; d < dim; d += 64) sq += (double) __fmul_rn(x[d], x[d]);
+    for (int off = 32; off >= 1; off >>= 1) sq += __shfl_xor(sq, off);
+    const float mean = (float) (sq / (double) dim);
+    const float scale = 1.0f / sqrtf(__fadd_rn(mean, a.eps));
+    for (int d = lane; d < dim; d += 64) x[d] = __fmul_rn(__fmul_rn(x[d], scale), a.w[d]);
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+
+    int32_t pos[4];
+    int64_t orow;
+    if constexpr (DECODE) {
+        for (int s = 0; s < 4; s++) pos[s] = a.blk_pos[s];
+        orow = *a.blk_idx;
+    } else {
+        for (int s = 0; s < 4; s++) pos[s] = (int32_t) (blk * a.r);
+        orow = blk;
+    }
+    const bool ook = orow >= 0 && orow < a.pool_rows;
+    if (!ook) {
+        if (lane == 0) atomicOr(a.status, DEVERR_SET_ROWS_INDEX);
+        return;
+    }
+    uint16_t * out = a.pool + (size_t) orow * dim;
+    const int half = a.rp.n_dims / 2;
+    if (lane < half) {
+        float c, s, y0, y1;
+        rope_cos_sin(a.rp, pos, lane, &c, &s);
+        rope_rotate(x[lane], x[lane + half], c, s, &y0, &y1);
+        out[lane] = f2h(y0);
+        out[lane + half] = f2h(y1);
+    }
+    for (int d = a.rp.n_dims + lane; d < dim; d += 64) out[d] = f2h(x[d]);
+}
+
+// ggml_set_rows F32 -> F16: row idx[i] of dst = fp16(row i of src)
+struct f16_rows_args {
+    uint16_t *      dst;
+    size_t          dst_nb1;   // bytes
+    int64_t         dst_rows;
+    const float *   src;
+    size_t          src_nb1;   // bytes
+    int64_t         ne0;
+    const int32_t * idx;
+    int64_t         n;
+    uint32_t *      status;
+};
+
+__global__ __launch_bounds__(256) void k_set_rows_f16(f16_rows_args a) {
+    const int64_t i = blockIdx.y;
+    const int32_t row = a.idx[i];
+    if (row < 0 || row >= a.dst_rows) {
+        if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(a.status, DEVERR_SET_ROWS_INDEX);
+        return;
+    }
+    const float * s = (const float *) ((const char *) a.src + (size_t) i * a.src_nb1);
+    uint16_t * d = (uint16_t *) ((char *) a.dst + (size_t) row * a.dst_nb1);
+    for (int64_t j = (int64_t) blockIdx.x * 256 + threadIdx.x; j < a.ne0; j += (int64_t) gridDim.x * 256)
+        d[j] = f2h(s[j]);
+}
+
+int pool_cfg_args(const qwfn_qsa_pool_cfg * cfg, int32_t ratio, const float * w, pool_args * a) {
+    if (!cfg || !w) return set_error(QWFN_EINVAL, "qsa_pool: NULL cfg or k_norm weight");
+    if (cfg->idx_dim < 2 || cfg->idx_dim > POOL_MAX_DIM || cfg->idx_dim % 2)
+        return set_error(QWFN_ENOTSUP, "qsa_pool: idx_dim must be even and at most 256");
+    if (cfg->n_dims < 2 || cfg->n_dims % 2 || cfg->n_dims > cfg->idx_dim || cfg->n_dims > 128)
+        return set_error(QWFN_EINVAL, "qsa_pool: n_dims must be even, at most idx_dim and 128");
+    int sect = 0;
+    for (int s = 0; s < 4; s++) {
+        if (cfg->sections[s] < 0) return set_error(QWFN_EINVAL, "qsa_pool: negative rope section");
+        sect += cfg->sections[s];
+    }
+    if (sect <= 0) return set_error(QWFN_EINVAL, "qsa_pool: rope sections must not all be zero");
+    if (!(cfg->freq_base > 0.f) || !std::isfinite(cfg->freq_base) || !(cfg->rms_eps >= 0.f))
+        return set_error(QWFN_EINVAL, "qsa_pool: freq_base must be positive and rms_eps non-negative");
+    if (ratio < 1 || ratio > 4096) return set_error(QWFN_EINVAL, "qsa_pool: ratio must lie in [1, 4096]");
+    a->dim = cfg->idx_dim;
+    a->r = ratio;
+    a->inv_r = 1.0f / (float) ratio;
+    a->eps = cfg->rms_eps;
+    a->w = w;
+    a->rp.n_dims = cfg->n_dims;
+    for (int s = 0; s < 4; s++) a->rp.sections[s] = cfg->sections[s];
+    a->rp.imrope = 1;
+    a->rp.theta_scale = powf(cfg->freq_base, -2.0f / (float) cfg->n_dims);
+    return QWFN_OK;
+}
+
+}  // namespace
+}  // namespace qwfn
+
+using namespace qwfn;
+
+extern "C" void qwfn_qsa_pool_cfg_default(qwfn_qsa_pool_cfg * cfg) {
+    if (!cfg) return;
+    cfg->idx_dim = 128;
+    cfg->n_dims = 64;
+    cfg->sections[0] = 11; cfg->sections[1] = 11; cfg->sections[2] = 10; cfg->sections[3] = 0;
+    cfg->freq_base = 10000000.0f;
+    cfg->rms_eps = 1e-6f;
+}
+
+extern "C" int qwfn_set_rows_f16(const qwfn_tensor * dst, const qwfn_tensor * src, const qwfn_tensor * idx,
+                                 void * stream) {
+    return ::qwfn::abi_call("set_rows_f16", [&]() -> int {
+        if (!dst || !src || !idx || !dst->data || !src->data || !idx->data)
+            return set_error(QWFN_EINVAL, "set_rows_f16: NULL tensor");
+        if (dst->type != QWFN_TYPE_F16 || src->type != QWFN_TYPE_F32 || idx->type != QWFN_TYPE_I32)
+            return set_error(QWFN_EINVAL, "set_rows_f16: dst must be f16, src f32, idx i32");
+        if (dst->nb[0] != 2 || src->nb[0] != 4 || idx->nb[0] != 4)
+            return set_error(QWFN_EINVAL, "set_rows_f16: rows must be contiguous");
+        if (dst->ne[0] != src->ne[0] || src->ne[1] != idx->ne[0] || src->ne[2] != 1 || src->ne[3] != 1 ||
+            dst->ne[2] != 1 || dst->ne[3] != 1 || idx->ne[1] != 1)
+            return set_error(QWFN_EINVAL, "set_rows_f16: dst [ne0, rows], src [ne0, n], idx [n]");
+        if (!is_aligned(dst->data, 2) || !is_aligned(src->data, 4) || !is_aligned(idx->data, 4) || dst->nb[1] % 2 ||
+            src->nb[1] % 4)
+            return set_error(QWFN_EALIGN, "set_rows_f16: element alignment");
+        if (src->ne[1] > 65535) return set_error(QWFN_ENOTSUP, "set_rows_f16: at most 65535 rows per call");
+        if (src->ne[0] == 0 || src->ne[1] == 0) return QWFN_OK;
+        f16_rows_args a{};
+        a.dst = (uint16_t *) dst->data; a.dst_nb1 = dst->nb[1]; a.dst_rows = dst->ne[1];
+        a.src = (const float *) src->data; a.src_nb1 = src->nb[1]; a.ne0 = src->ne[0];
+        a.idx = (const int32_t *) idx->data; a.n = src->ne[1];
+        if (int rc = status_word(&a.status)) return rc;
+        const unsigned gx = (unsigned) std::min<int64_t>((a.ne0 + 255) / 256, 64);
+        hipLaunchKernelGGL(k_set_rows_f16, dim3(gx, (unsigned) a.n), dim3(256), 0, as_stream(stream), a);
+        return hip_check(hipGetLastError(), "set_rows_f16 launch");
+    });
+}
+
+extern "C" int qwfn_qsa_pool_decode(uint16_t * idx_cache, int64_t ic_rows, const float * k_raw,
+                                    const int32_t * write_idx, const int32_t * member_idx, int32_t ratio,
+                                    const int32_t * blk_pos, const int32_t * blk_idx, const float * k_norm_w,
+                                    uint16_t * pool, int64_t pool_rows, const qwfn_qsa_pool_cfg * cfg, void * stream) {
+    return ::qwfn::abi_call("qsa_pool_decode", [&]() -> int {
+        pool_args a{};
+        if (int rc = pool_cfg_args(cfg, ratio, k_norm_w, &a)) return rc;
+        if (!idx_cache || !member_idx || !blk_pos || !blk_idx || !pool || (k_raw && !write_idx))
+            return set_error(QWFN_EINVAL, "qsa_pool_decode: NULL pointer");
+        if (ic_rows < 1 || pool_rows < 1) return set_error(QWFN_EINVAL, "qsa_pool_decode: empty cache");
+        if (!is_aligned(idx_cache, 2) || !is_aligned(pool, 2) || !is_aligned(k_norm_w, 4) ||
+            (k_raw && !is_aligned(k_raw, 4)))
+            return set_error(QWFN_EALIGN, "qsa_pool_decode: element alignment");
+        a.ic = idx_cache; a.ic_rows = ic_rows; a.pool = pool; a.pool_rows = pool_rows;
+        a.k_raw = k_raw; a.write_idx = write_idx; a.member_idx = member_idx; a.blk_pos = blk_pos; a.blk_idx = blk_idx;
+        a.n_blk = 1;
+        if (int rc = status_word(&a.status)) return rc;
+        hipLaunchKernelGGL(k_qsa_pool<true>, dim3(1), dim3(POOL_WAVES * 64), 0, as_stream(stream), a);
+        return hip_check(hipGetLastError(), "qsa_pool_decode launch");
+    });
+}
+
+extern "C" int qwfn_qsa_pool_rebuild(const uint16_t * idx_cache, int64_t ic_rows, int64_t n_past, int32_t ratio,
+                                     const float * k_norm_w, uint16_t * pool, int64_t pool_rows,
+                                     const qwfn_qsa_pool_cfg * cfg, void * stream) {
+    return ::qwfn::abi_call("qsa_pool_rebuild", [&]() -> int {
+        pool_args a{};
+        if (int rc = pool_cfg_args(cfg, ratio, k_norm_w, &a)) return rc;
+        if (!idx_cache || !pool) return set_error(QWFN_EINVAL, "qsa_pool_rebuild: NULL pointer");
+        if (n_past < 0) return set_error(QWFN_EINVAL, "qsa_pool_rebuild: negative n_past");
+        const int64_t n_whole = n_past / ratio;
+        if (n_whole * ratio > ic_rows) return set_error(QWFN_ERANGE, "qsa_pool_rebuild: n_past beyond the index cache");
+        if (n_whole > pool_rows) return set_error(QWFN_ERANGE, "qsa_pool_rebuild: more whole blocks than pool rows");
+        if (n_whole * ratio >= (int64_t(1) << 31)) return set_error(QWFN_ENOTSUP, "qsa_pool_rebuild: positions beyond 2^31");
+        if (!is_aligned(idx_cache, 2) || !is_aligned(pool, 2) || !is_aligned(k_norm_w, 4))
+            return set_error(QWFN_EALIGN, "qsa_pool_rebuild: element alignment");
+        if (n_whole == 0) return QWFN_OK;
+        a.ic = const_cast<uint16_t *>(idx_cache); a.ic_rows = ic_rows; a.pool = pool; a.pool_rows = pool_rows;
+        a.n_blk = n_whole;
+        if (int rc = status_word(&a.status)) return rc;
+        const int64_t grid = (n_whole + POOL_WAVES - 1) / POOL_WAVES;
+        hipLaunchKernelGGL(k_qsa_pool<false>, dim3((unsigned) grid), dim3(POOL_WAVES * 64), 0, as_stream(stream), a);
+        return hip_check(hipGetLastError(), "qsa_pool_rebuild launch");
+    });
+}

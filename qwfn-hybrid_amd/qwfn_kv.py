@@ -65,6 +65,12 @@ class QsaInputs(ctypes.Structure):
                 ("ratio", ctypes.c_int32), ("pad_", ctypes.c_int32), ("n_blocks_max", ctypes.c_int64)]
 
 
+class QsaPoolCfg(ctypes.Structure):
+    """qwfn_qsa_pool_cfg: the indexer key geometry and rope / norm constants."""
+    _fields_ = [("idx_dim", ctypes.c_int32), ("n_dims", ctypes.c_int32), ("sections", ctypes.c_int32 * 4),
+                ("freq_base", ctypes.c_float), ("rms_eps", ctypes.c_float)]
+
+
 EXPORTS = [
     "qwfn_abi_version", "qwfn_last_error", "qwfn_init", "qwfn_device_status",
     "qwfn_set_rows_q8_0", "qwfn_cpy_f32_q8_0", "qwfn_set_rows_q8_0_kv", "qwfn_cpy_f32_q8_0_kv", "qwfn_get_rows_i32", "qwfn_kv_gather_segments",
@@ -82,6 +88,7 @@ EXPORTS = [
     "qwfn_snap_pool_entry", "qwfn_snap_pool_save", "qwfn_snap_pool_best", "qwfn_snap_pool_load",
     "qwfn_snap_pool_split", "qwfn_snap_pool_restore_or_reset",
     "qwfn_qsa_select_workspace_size", "qwfn_qsa_select_cells",
+    "qwfn_qsa_pool_cfg_default", "qwfn_set_rows_f16", "qwfn_qsa_pool_decode", "qwfn_qsa_pool_rebuild",
 ]
 
 _lib = None
@@ -173,6 +180,11 @@ def load(path: str = LIB_PATH):
     L.qwfn_snap_pool_split.argtypes = [vp, PI, i32, i32, i32]
     L.qwfn_snap_pool_split.restype = i32
     L.qwfn_snap_pool_restore_or_reset.argtypes = [vp, PV, i32, PI, i32, i32, PI, i32, i32, PI, vp]
+    L.qwfn_qsa_pool_cfg_default.argtypes = [ctypes.POINTER(QsaPoolCfg)]
+    L.qwfn_qsa_pool_cfg_default.restype = None
+    L.qwfn_set_rows_f16.argtypes = [T, T, T, vp]
+    L.qwfn_qsa_pool_decode.argtypes = [vp, i64, vp, vp, vp, i32, vp, vp, vp, vp, i64, ctypes.POINTER(QsaPoolCfg), vp]
+    L.qwfn_qsa_pool_rebuild.argtypes = [vp, i64, i64, i32, vp, vp, i64, ctypes.POINTER(QsaPoolCfg), vp]
     L.qwfn_qsa_select_workspace_size.argtypes = [i64, i32]
     L.qwfn_qsa_select_workspace_size.restype = sz
     L.qwfn_qsa_select_cells.argtypes = [vp, sz, i64, vp, i32, sz, vp, sz, i32, i32, vp, i32, vp, vp, vp, sz, vp]
@@ -416,3 +428,41 @@ def device_status(stream=None) -> int:
     f = ctypes.c_uint32(0)
     check(L.qwfn_device_status(_stream(stream), ctypes.byref(f)))
     return int(f.value)
+
+
+def qsa_pool_cfg(**overrides) -> QsaPoolCfg:
+    c = QsaPoolCfg()
+    load().qwfn_qsa_pool_cfg_default(ctypes.byref(c))
+    for k, v in overrides.items():
+        if k == "sections":
+            for i in range(4):
+                c.sections[i] = int(v[i])
+        else:
+            setattr(c, k, v)
+    return c
+
+
+def set_rows_f16(dst, src, idx, stream=None):
+    """ggml_set_rows F32 -> F16: dst torch f16/uint16 [rows, ne0], src f32 [n, ne0], idx i32 [n] (device)."""
+    d = tensor(dst.data_ptr(), TYPE_F16, (dst.shape[1], dst.shape[0]), (2, dst.stride(0) * 2))
+    sv = tensor(src.data_ptr(), TYPE_F32, (src.shape[1], src.shape[0]), (4, src.stride(0) * 4))
+    iv = tensor(idx.data_ptr(), TYPE_I32, (idx.shape[0],), (4,))
+    return check(load().qwfn_set_rows_f16(ctypes.byref(d), ctypes.byref(sv), ctypes.byref(iv), _stream(stream)))
+
+
+def qsa_pool_decode(ic, k_raw, write_idx, member_idx, ratio: int, blk_pos, blk_idx, k_norm_w, pool, cfg=None,
+                    stream=None):
+    """qsa_dec_index: ic / pool torch f16 or uint16 [rows, idx_dim] (device), k_raw f32 [idx_dim] or None,
+    the i32 decode inputs on the device."""
+    cfg = cfg or qsa_pool_cfg()
+    return check(load().qwfn_qsa_pool_decode(ic.data_ptr(), ic.shape[0], k_raw.data_ptr() if k_raw is not None else None,
+                                             write_idx.data_ptr(), member_idx.data_ptr(), ratio, blk_pos.data_ptr(),
+                                             blk_idx.data_ptr(), k_norm_w.data_ptr(), pool.data_ptr(), pool.shape[0],
+                                             ctypes.byref(cfg), _stream(stream)))
+
+
+def qsa_pool_rebuild(ic, n_past: int, ratio: int, k_norm_w, pool, cfg=None, stream=None):
+    """Every whole block's pooled key: ic / pool torch f16 or uint16 [rows, idx_dim] (device)."""
+    cfg = cfg or qsa_pool_cfg()
+    return check(load().qwfn_qsa_pool_rebuild(ic.data_ptr(), ic.shape[0], n_past, ratio, k_norm_w.data_ptr(),
+                                              pool.data_ptr(), pool.shape[0], ctypes.byref(cfg), _stream(stream)))

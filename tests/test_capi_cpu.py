@@ -205,3 +205,30 @@ def test_cells_attention_validation():
     assert L.qwfn_fattn_workspace_size_cells(r(q5), r(k5), r(k5), n, 8) == 0
     one = L.qwfn_fattn_workspace_size_cells(r(q), r(k), r(k), (ctypes.c_int64 * 2)(4000, 3000), 4000)
     assert one >= 2 * 8 * 8 * 256 * 4
+
+
+def test_qsa_pool_validation():
+    L = K.load()
+    cfg = K.qsa_pool_cfg()
+    assert (cfg.idx_dim, cfg.n_dims, list(cfg.sections), cfg.freq_base, cfg.rms_eps) == (128, 64, [11, 11, 10, 0],
+                                                                                        1e7, pytest.approx(1e-6))
+    r = ctypes.byref
+    _err(L.qwfn_qsa_pool_rebuild(FAKE, 100, 64, 0, FAKE, FAKE, 10, r(cfg), None), K.EINVAL, "ratio")
+    _err(L.qwfn_qsa_pool_rebuild(FAKE, 100, 640, 32, FAKE, FAKE, 10, r(cfg), None), K.ERANGE, "index cache")
+    _err(L.qwfn_qsa_pool_rebuild(FAKE, 1000, 640, 32, FAKE, FAKE, 10, r(cfg), None), K.ERANGE, "pool rows")
+    _err(L.qwfn_qsa_pool_rebuild(FAKE, 1000, -1, 32, FAKE, FAKE, 10, r(cfg), None), K.EINVAL, "n_past")
+    bad = K.qsa_pool_cfg(n_dims=65)
+    _err(L.qwfn_qsa_pool_rebuild(FAKE, 1000, 64, 32, FAKE, FAKE, 10, r(bad), None), K.EINVAL, "n_dims")
+    bad = K.qsa_pool_cfg(idx_dim=512)
+    _err(L.qwfn_qsa_pool_rebuild(FAKE, 1000, 64, 32, FAKE, FAKE, 10, r(bad), None), K.ENOTSUP, "idx_dim")
+    bad = K.qsa_pool_cfg(sections=[0, 0, 0, 0])
+    _err(L.qwfn_qsa_pool_rebuild(FAKE, 1000, 64, 32, FAKE, FAKE, 10, r(bad), None), K.EINVAL, "sections")
+    _err(L.qwfn_qsa_pool_decode(FAKE, 100, FAKE, None, FAKE, 32, FAKE, FAKE, FAKE, FAKE, 10, r(cfg), None),
+         K.EINVAL, "NULL")
+    _err(L.qwfn_qsa_pool_decode(FAKE + 1, 100, None, None, FAKE, 32, FAKE, FAKE, FAKE, FAKE, 10, r(cfg), None),
+         K.EALIGN, "alignment")
+    d = K.tensor(FAKE, K.TYPE_F16, (128, 10), (2, 256))
+    s = K.tensor(FAKE, K.TYPE_F32, (128, 2), (4, 512))
+    i = K.tensor(FAKE, K.TYPE_I32, (2,), (4,))
+    _err(L.qwfn_set_rows_f16(r(d), r(s), r(K.tensor(FAKE, K.TYPE_I32, (3,), (4,))), None), K.EINVAL, "idx [n]")
+    _err(L.qwfn_set_rows_f16(r(s), r(s), r(i), None), K.EINVAL, "f16")
