@@ -220,6 +220,46 @@ int qwfn_flash_attn_ext_q8_0_cells(const qwfn_tensor * q, const qwfn_tensor * k,
                                    float scale, const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes,
                                    void * stream);
 
+/* Rope and norm constants of the attention layers (qwfn_hparams.h:26,
+ * :34-36): n_dims = rope_dim (64), sections = mrope_sections {11, 11, 10, 0},
+ * freq_base = rope_freq_base (1e7), rms_eps (1e-6). */
+typedef struct qwfn_rope_cfg {
+    int32_t n_dims;
+    int32_t sections[4];
+    float   freq_base;
+    float   rms_eps;
+} qwfn_rope_cfg;
+
+/* The layer's K/V producer for a decode or verify step, one launch: K =
+ * attn_k . cur and V = attn_v . cur (ggml_mul_mat with F16 weights: cur
+ * converted to F16, F16 products summed in F32), each K head RMS-normed and
+ * multiplied by k_norm_w (F32 [256]), roped (IMROPE at pos, I32 [4 * T]
+ * device: the T t positions, then h, w, e, as ggml_rope_multi reads them),
+ * then K and V quantised (q8_0, variant as in qwfn_set_rows_q8_0) into cache
+ * rows first_row .. first_row + T - 1. Replaces qwfn_graph.cpp:441-451 (the
+ * mul_mats and rms), :446-451 / :129-132 (rope) and :370-384 (kv_append).
+ * cur: F32 [n_embd, T] (T <= 16, n_embd a multiple of 8, T * n_embd <=
+ * 65536); wk, wv: F16 [n_embd, kv_dim] (kv_dim = 256 * n_head_kv <= 2048,
+ * 16-byte aligned rows); caches: q8_0 [kv_dim, n_rows]. The projected rows
+ * pass through a device-resident staging buffer of the library (one per GPU):
+ * calls that overlap on one GPU race. The K/V bytes equal ggml's quantiser on
+ * the F32 rows this kernel computes; those rows differ from ggml-cpu's only
+ * in float summation order. */
+int qwfn_kv_produce_q8_0(const qwfn_tensor * cur, const qwfn_tensor * wk, const qwfn_tensor * wv, const float * k_norm_w,
+                         const int32_t * pos, const qwfn_rope_cfg * rope, const qwfn_tensor * k_cache,
+                         const qwfn_tensor * v_cache, int64_t first_row, int variant, void * stream);
+
+/* Attention with the output gate of the reference's attention layers fused
+ * into its last store: dst = attention * sigmoid(gate), sigmoid(x) = 1 / (1 +
+ * exp(-x)) -- the ggml_sigmoid and ggml_mul after flash_attn_ext
+ * (qwfn_graph.cpp:474, :701). gate: F32 with dst's shape and strides, dst
+ * and gate contiguous and 16-byte aligned. Otherwise as
+ * qwfn_flash_attn_ext_q8_0 (same workspace). */
+int qwfn_flash_attn_ext_q8_0_gated(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
+                                   const qwfn_tensor * mask, float scale, float max_bias, float logit_softcap,
+                                   const qwfn_tensor * dst, const qwfn_tensor * gate, int variant, void * ws,
+                                   size_t ws_bytes, void * stream);
+
 /* The layer's K and V append followed by its attention, in one launch: the
  * two ggml_cpy / ggml_set_rows nodes that write the step's rows
  * (qwfn_graph.cpp:376-383, :623-624, :916-921) and the ggml_flash_attn_ext

@@ -478,3 +478,43 @@ void oracle_qsa_pool_blocks(const uint16_t * ic, int64_t idx_dim, const int32_t 
     }
     free(acc);
 }
+
+/* ----------------------------------------------------- K/V producer */
+
+void oracle_kv_produce_q8_0(const float * cur, int64_t E, int64_t T, const uint16_t * wk, const uint16_t * wv,
+                            int64_t kv_dim, const float * k_norm_w, const int32_t * pos, const int sections[4],
+                            int n_dims, float freq_base, float eps, void * k_rows, void * v_rows, float * k_f32,
+                            float * v_f32, int variant) {
+    const int64_t hd = 256;
+    const size_t row_bytes = (size_t) (kv_dim / ORACLE_QK8_0) * 34;
+    float * c16 = malloc(sizeof(float) * (size_t) E);
+    float * k = malloc(sizeof(float) * (size_t) kv_dim * 2);
+    float * v = k + kv_dim;
+    float * tmp = malloc(sizeof(float) * (size_t) hd * 2);
+    for (int64_t t = 0; t < T; t++) {
+        for (int64_t e = 0; e < E; e++) c16[e] = oracle_fp16_to_fp32(oracle_fp32_to_fp16(cur[t * E + e]));
+        for (int64_t o = 0; o < kv_dim; o++) {
+            double sk = 0.0, sv = 0.0;
+            for (int64_t e = 0; e < E; e++) {
+                sk += (double) oracle_fp16_to_fp32(wk[o * E + e]) * (double) c16[e];
+                sv += (double) oracle_fp16_to_fp32(wv[o * E + e]) * (double) c16[e];
+            }
+            k[o] = (float) sk;
+            v[o] = (float) sv;
+        }
+        const int32_t p4[4] = {pos[t], pos[T + t], pos[2 * T + t], pos[3 * T + t]};
+        for (int64_t h = 0; h < kv_dim / hd; h++) {
+            float * kh = k + h * hd;
+            oracle_rms_norm_f32(kh, tmp, hd, eps);
+            for (int64_t d = 0; d < hd; d++) tmp[d] = tmp[d] * k_norm_w[d];
+            oracle_rope_multi_f32(tmp, kh, hd, n_dims, p4, sections, 1, freq_base);
+        }
+        if (k_f32) memcpy(k_f32 + t * kv_dim, k, sizeof(float) * (size_t) kv_dim);
+        if (v_f32) memcpy(v_f32 + t * kv_dim, v, sizeof(float) * (size_t) kv_dim);
+        oracle_quantize_row_q8_0(k, (char *) k_rows + (size_t) t * row_bytes, kv_dim, variant);
+        oracle_quantize_row_q8_0(v, (char *) v_rows + (size_t) t * row_bytes, kv_dim, variant);
+    }
+    free(c16);
+    free(k);
+    free(tmp);
+}

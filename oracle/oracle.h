@@ -119,6 +119,19 @@ void oracle_qsa_pool_blocks(const uint16_t * ic, int64_t idx_dim, const int32_t 
                             const float * k_norm_w, const int32_t * pos4, const int sections[4], float eps,
                             float freq_base, int n_dims, uint16_t * out);
 
+/* The attention layer's K/V producer (qwfn_graph.cpp:441-451, :129-132,
+ * :370-384) for T tokens: K = attn_k . cur, V = attn_v . cur with F16
+ * weights [kv_dim][E] and cur rounded to F16 (ggml_mul_mat's conversion of
+ * src1), the products summed in double and rounded to float (ggml-cpu sums in
+ * float lanes: the difference is float rounding); each 256-value K head RMS
+ * normed, times k_norm_w, IMROPE at pos[s*T + t]; then both quantised (q8_0,
+ * variant) into k_rows / v_rows (T rows of kv_dim/32*34 bytes). k_f32 / v_f32
+ * (may be NULL) receive the float rows before quantisation. */
+void oracle_kv_produce_q8_0(const float * cur, int64_t E, int64_t T, const uint16_t * wk, const uint16_t * wv,
+                            int64_t kv_dim, const float * k_norm_w, const int32_t * pos, const int sections[4],
+                            int n_dims, float freq_base, float eps, void * k_rows, void * v_rows, float * k_f32,
+                            float * v_f32, int variant);
+
 #ifdef __cplusplus
 }
 #endif

@@ -71,6 +71,8 @@ def lib():
         L.oracle_rms_norm_f32.argtypes = [vp, vp, i64, ctypes.c_float]
         L.oracle_rope_multi_f32.argtypes = [vp, vp, i64, ctypes.c_int, vp, vp, ctypes.c_int, ctypes.c_float]
         L.oracle_set_rows_f16.argtypes = [vp, i64, i64, vp, vp, i64]
+        L.oracle_kv_produce_q8_0.argtypes = [vp, i64, i64, vp, vp, i64, vp, vp, vp, ctypes.c_int, ctypes.c_float,
+                                             ctypes.c_float, vp, vp, vp, vp, ctypes.c_int]
         L.oracle_qsa_pool_blocks.argtypes = [vp, i64, vp, i64, i64, vp, vp, vp, ctypes.c_float, ctypes.c_float,
                                              ctypes.c_int, vp]
         _lib = L
@@ -311,3 +313,24 @@ def qsa_pool_blocks(ic_bits: np.ndarray, members: np.ndarray, r: int, k_norm_w: 
     lib().oracle_qsa_pool_blocks(_p(ic_bits), ic_bits.shape[1], _p(members), r, n_blk, _p(w), _p(p4), _p(sec),
                                  eps, freq_base, n_dims, _p(out))
     return out
+
+
+def kv_produce(cur: np.ndarray, wk_bits: np.ndarray, wv_bits: np.ndarray, k_norm_w: np.ndarray, pos: np.ndarray,
+               variant: int = Q8_X86, n_dims: int = ROPE_DIM, sections=IMROPE_SECTIONS, freq_base: float = ROPE_FREQ_BASE,
+               eps: float = RMS_EPS):
+    """cur f32 [T, E]; w*_bits uint16 [kv_dim, E]; pos int32 [4*T]. Returns (k_rows, v_rows, k_f32, v_f32):
+    q8_0 rows uint8 [T, kv_dim/32*34] and the float rows before quantisation [T, kv_dim]."""
+    cur = np.ascontiguousarray(cur, np.float32)
+    T, E = cur.shape
+    kv_dim = wk_bits.shape[0]
+    rb = kv_dim // QK8_0 * Q8_0_BLOCK_BYTES
+    k_rows = np.zeros((T, rb), np.uint8)
+    v_rows = np.zeros((T, rb), np.uint8)
+    k_f = np.zeros((T, kv_dim), np.float32)
+    v_f = np.zeros((T, kv_dim), np.float32)
+    sec = np.ascontiguousarray(np.asarray(sections, np.int32))
+    lib().oracle_kv_produce_q8_0(_p(cur), E, T, _p(np.ascontiguousarray(wk_bits, np.uint16)),
+                                 _p(np.ascontiguousarray(wv_bits, np.uint16)), kv_dim,
+                                 _p(np.ascontiguousarray(k_norm_w, np.float32)), _p(np.ascontiguousarray(pos, np.int32)),
+                                 _p(sec), n_dims, freq_base, eps, _p(k_rows), _p(v_rows), _p(k_f), _p(v_f), variant)
+    return k_rows, v_rows, k_f, v_f

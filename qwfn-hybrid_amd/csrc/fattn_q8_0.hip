@@ -166,10 +166,24 @@ struct fa_args {
     int64_t  g_rows;
     int32_t  g_n[GATHER_MAX_HEADS];
     uint32_t * status;     // device flags (DEVERR_GET_ROWS_INDEX: a cell outside the cache)
+    // output gate (or null): dst = attention * sigmoid(gate), gate laid out as dst
+    const float * gate;
 };
 
 __device__ __forceinline__ uint32_t div_gqa(const fa_args & a, uint32_t r) {
     return udiv(r, (uint32_t) a.gqa, a.gqa_mul);
+}
+// v * sigmoid(gate) for the 4 dst values at d (16-byte aligned), sigmoid(x) =
+// 1 / (1 + exp(-x)) as ggml_sigmoid, then ggml_mul's product; v as is
+// without a gate
+__device__ __forceinline__ float4 apply_gate(const fa_args & a, const float * d, float4 v) {
+    if (!a.gate) return v;
+    const float4 g = *(const float4 *) (a.gate + (d - a.dst));
+    v.x = __fmul_rn(v.x, 1.0f / (1.0f + expf(-g.x)));
+    v.y = __fmul_rn(v.y, 1.0f / (1.0f + expf(-g.y)));
+    v.z = __fmul_rn(v.z, 1.0f / (1.0f + expf(-g.z)));
+    v.w = __fmul_rn(v.w, 1.0f / (1.0f + expf(-g.w)));
+    return v;
 }
 // b % n for a batch index b and a broadcast extent n (n is 1 or B in practice)
 __device__ __forceinline__ int bmod(int b, int n) {
@@ -1027,8 +1041,8 @@ __global__ __launch_bounds__(NW * 64, NW / 4 > 2 ? NW / 4 : 2) void k_fattn_q8_0
             store_nt4(out + 32 * bb, w0);
             store_nt4(out + 32 * bb + 4, w1);
         } else if (vec) {
-            *(float4 *) (out + 32 * bb) = w0;
-            *(float4 *) (out + 32 * bb + 4) = w1;
+            *(float4 *) (out + 32 * bb) = apply_gate(a, out + 32 * bb, w0);
+            *(float4 *) (out + 32 * bb + 4) = apply_gate(a, out + 32 * bb + 4, w1);
         } else {
             float * o = out + 32 * bb;
             o[0] = w0.x; o[1] = w0.y; o[2] = w0.z; o[3] = w0.w;
@@ -1148,7 +1162,7 @@ __global__ __launch_bounds__(256) void k_fattn_merge(fa_args a) {
         const int t = (int) div_gqa(a, (uint32_t) r), h = kvh * a.gqa + (r - t * a.gqa);
         float * d = a.dst + (((size_t) b * a.T + t) * a.nh + h) * D + 64 * quarter + 4 * q;
         if (a.dst_vec) {
-            *(float4 *) d = o;
+            *(float4 *) d = apply_gate(a, d, o);
         } else {
             d[0] = o.x; d[1] = o.y; d[2] = o.z; d[3] = o.w;
         }
@@ -1198,7 +1212,7 @@ __global__ __launch_bounds__(256) void k_fattn_merge_rows(fa_args a) {
     const uint32_t t = div_gqa(a, r), h = kvh * (uint32_t) a.gqa + (r - t * (uint32_t) a.gqa);
     float * d = a.dst + (((size_t) b * a.T + t) * a.nh + h) * D + 4 * q4;
     if (a.dst_vec) {
-        *(float4 *) d = acc;
+        *(float4 *) d = apply_gate(a, d, acc);
     } else {
         d[0] = acc.x; d[1] = acc.y; d[2] = acc.z; d[3] = acc.w;
     }
@@ -1777,8 +1791,8 @@ __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
             store_nt4(out + 32 * bb, w0);
             store_nt4(out + 32 * bb + 4, w1);
         } else if (a.dst_vec) {
-            *(float4 *) (out + 32 * bb) = w0;
-            *(float4 *) (out + 32 * bb + 4) = w1;
+            *(float4 *) (out + 32 * bb) = apply_gate(a, out + 32 * bb, w0);
+            *(float4 *) (out + 32 * bb + 4) = apply_gate(a, out + 32 * bb + 4, w1);
         } else {
             float * o = out + 32 * bb;
             o[0] = w0.x; o[1] = w0.y; o[2] = w0.z; o[3] = w0.w;
@@ -2247,7 +2261,7 @@ __global__ __launch_bounds__(PRE_WAVES * 64, 2) void k_fa_pre(fa_args a) {
             if (nsplit) {
                 store_nt4(op, make_float4(o[0], o[1], o[2], o[3]));
             } else if (a.dst_vec) {
-                *(float4 *) op = make_float4(o[0], o[1], o[2], o[3]);
+                *(float4 *) op = apply_gate(a, op, make_float4(o[0], o[1], o[2], o[3]));
             } else {
                 op[0] = o[0]; op[1] = o[1]; op[2] = o[2]; op[3] = o[3];
             }
@@ -2586,7 +2600,7 @@ struct fa_gather {
 int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v, const qwfn_tensor * mask, float scale,
               float max_bias, float logit_softcap, const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes,
               void * stream, const fa_append * app, const int64_t * seq_n_kv = nullptr, ws_mode wsm = WS_CALLER,
-              const fa_gather * gat = nullptr) {
+              const fa_gather * gat = nullptr, const qwfn_tensor * gate = nullptr) {
     if (max_bias != 0.0f) return set_error(QWFN_ENOTSUP, "flash_attn_ext: max_bias (ALiBi) is not supported");
     if (logit_softcap != 0.0f) return set_error(QWFN_ENOTSUP, "flash_attn_ext: logit_softcap is not supported");
     if (!(std::isfinite(scale))) return set_error(QWFN_EINVAL, "flash_attn_ext: scale must be finite");
@@ -2668,6 +2682,17 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
     }
     a.scale = scale; a.x86 = variant == QWFN_Q8_X86;
     a.dst_vec = is_aligned(dst->data, 16) ? 1 : 0;
+    if (gate) {
+        if (!gate->data || gate->type != QWFN_TYPE_F32) return set_error(QWFN_EINVAL, "flash_attn_ext_gated: gate must be f32");
+        for (int i = 0; i < 4; i++)
+            if (gate->ne[i] != dst->ne[i] || gate->nb[i] != dst->nb[i])
+                return set_error(QWFN_EINVAL, "flash_attn_ext_gated: gate must have dst's shape and strides");
+        const bool contiguous = dst->nb[0] == 4 && dst->nb[1] == (size_t) D * 4 && dst->nb[2] == dst->nb[1] * dst->ne[1] &&
+                                dst->nb[3] == dst->nb[2] * dst->ne[2];
+        if (!contiguous || !is_aligned(dst->data, 16) || !is_aligned(gate->data, 16))
+            return set_error(QWFN_EALIGN, "flash_attn_ext_gated: dst and gate must be contiguous and 16-byte aligned");
+        a.gate = (const float *) gate->data;
+    }
     a.q_slice = (uint32_t) q_slice_bytes(*q);
     a.gqa_mul = recip32(pl.gqa);
     if (gat) {
@@ -2853,6 +2878,17 @@ extern "C" int qwfn_flash_attn_ext_q8_0_cells(const qwfn_tensor * q, const qwfn_
         if (int rc = gather_args(q, k, v, cells, n_cells, cell_stride, pos0, &kk, &vv, &g)) return rc;
         return fattn_run(q, &kk, &vv, nullptr, scale, 0.0f, 0.0f, dst, variant, ws, ws_bytes, stream, nullptr, nullptr,
                          WS_CALLER, &g);
+    });
+}
+
+extern "C" int qwfn_flash_attn_ext_q8_0_gated(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
+                                              const qwfn_tensor * mask, float scale, float max_bias, float logit_softcap,
+                                              const qwfn_tensor * dst, const qwfn_tensor * gate, int variant, void * ws,
+                                              size_t ws_bytes, void * stream) {
+    return ::qwfn::abi_call("flash_attn_ext_q8_0_gated", [&]() -> int {
+        if (!gate) return set_error(QWFN_EINVAL, "flash_attn_ext_gated: NULL gate");
+        return fattn_run(q, k, v, mask, scale, max_bias, logit_softcap, dst, variant, ws, ws_bytes, stream, nullptr,
+                         nullptr, WS_CALLER, nullptr, gate);
     });
 }
 

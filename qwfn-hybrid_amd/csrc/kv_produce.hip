@@ -1,0 +1,288 @@
+// The attention layer's K/V producer, one launch for a decode or verify step:
+// the K and V projections of the step's hidden rows, RMS norm of each K head
+// times attn_k_norm, IMROPE at the tokens' positions, and the q8_0 append of
+// both into the caches -- the ops qwfn_graph.cpp:441-451 (attn_k / attn_v
+// mul_mat, rms), :129-132 / :446-451 (rope) and :370-384 (kv_append: cpy
+// F32 -> q8_0) emit one by one.
+//
+// Projection: ggml_mul_mat with F16 weights converts the F32 hidden rows to
+// F16 and sums the F16 products in F32. Each wave computes 4 output rows for
+// all T tokens: 16-byte weight loads along n_embd, the hidden rows (F16) in
+// LDS, per-lane F32 partial sums, a wave reduction. The rows land in a
+// device-resident staging buffer; the workgroup that finishes last (a ticket
+// counter, reset by that workgroup) runs the epilogue for every (token, head):
+// K heads are normed, weighted and roped (rope_device.h, ggml-cpu's float
+// order), then quantised with the cache quantiser (q8_device.h) into row
+// first_row + t; V heads are quantised as they are.
+#include "q8_device.h"
+#include "qwfn_common.h"
+#include "qwfn_state.h"
+#include "rope_device.h"
+
+#include <cmath>
+#include <mutex>
+
+namespace qwfn {
+namespace {
+
+constexpr int KVP_MAX_T = 16;            // tokens per call
+constexpr int KVP_MAX_HKV = 8;           // KV heads
+constexpr int KVP_HD = 256;              // head size
+constexpr int KVP_ROWS_W = 4;            // output rows per wave
+constexpr int KVP_WAVES = 4;
+constexpr int KVP_MAX_EMBD = 8192;       // hidden size, at most (the F16 rows of all tokens fit LDS)
+constexpr int KVP_STAGE = KVP_MAX_T * 2 * KVP_MAX_HKV * KVP_HD;   // F32 projected rows
+
+// projected rows of the current call ([t][K rows | V rows]) and the ticket;
+// one set per device: calls that overlap on one device race
+__device__ float g_kvp_rows[KVP_STAGE];
+__device__ unsigned g_kvp_ticket = 0;
+
+struct kvp_args {
+    const float *    cur;         // F32 [n_embd] per token, token stride cur_nb1 bytes
+    size_t           cur_nb1;
+    int32_t          n_embd;
+    int32_t          T;
+    const uint16_t * wk;          // F16 [n_embd] per output row (kv_dim rows), row stride w_nb1 bytes
+    const uint16_t * wv;
+    size_t           wk_nb1, wv_nb1;
+    int32_t          nh_kv;
+    int32_t          kv_dim;      // nh_kv * 256
+    const float *    k_norm_w;    // F32 [256]
+    float            eps;
+    rope_params      rp;
+    const int32_t *  pos;         // I32 [4 * T]: t positions, then h, w, e (ggml_rope_multi's layout)
+    char *           kc;          // q8_0 caches, row stride k_nb1 / v_nb1 bytes
+    char *           vc;
+    size_t           k_nb1, v_nb1;
+    int64_t          first_row;
+    int32_t          x86;
+    float *          rows;        // g_kvp_rows
+    unsigned *       ticket;      // g_kvp_ticket
+};
+
+__device__ __forceinline__ float h2f(uint16_t h) { return (float) __builtin_bit_cast(_Float16, h); }
+
+__device__ __forceinline__ float wave_sum(float x) {
+    for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+    return x;
+}
+
+__global__ __launch_bounds__(KVP_WAVES * 64) void k_kv_produce(kvp_args a) {
+    extern __shared__ uint16_t cur16[];          // [T][n_embd] F16 hidden rows
+    __shared__ float head[KVP_WAVES][KVP_HD];    // epilogue: one head row per wave
+    __shared__ unsigned last;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int T = a.T, E = a.n_embd;
+
+    // ---- the hidden rows, F32 -> F16 (ggml's conversion of src1) ----
+    for (int i = threadIdx.x; i < T * E; i += KVP_WAVES * 64) {
+        const int t = i / E, e = i - t * E;
+        const float x = *(const float *) ((const char *) a.cur + (size_t) t * a.cur_nb1 + (size_t) e * 4);
+        cur16[i] = __builtin_bit_cast(uint16_t, (_Float16) x);
+    }
+    __syncthreads();
+
+    // ---- projection: wave w of block b takes output rows 4 (4b + w) .. +3 of
+    //      [K rows | V rows]; lane l takes the 8 hidden values 8 l + 512 j ----
+    const int n_out = 2 * a.kv_dim;
+    const int o0 = (blockIdx.x * KVP_WAVES + wv) * KVP_ROWS_W;
+    if (o0 < n_out) {
+        float acc[KVP_ROWS_W][KVP_MAX_T];
+#pragma unroll
+        for (int r = 0; r < KVP_ROWS_W; r++)
+#pragma unroll
+            for (int t = 0; t < KVP_MAX_T; t++) acc[r][t] = 0.f;
+        const uint16_t * wrow[KVP_ROWS_W];
+#pragma unroll
+        for (int r = 0; r < KVP_ROWS_W; r++) {
+            const int o = o0 + r < n_out ? o0 + r : o0;
+            wrow[r] = o < a.kv_dim ? (const uint16_t *) ((const char *) a.wk + (size_t) o * a.wk_nb1)
+                                   : (const uint16_t *) ((const char *) a.wv + (size_t) (o - a.kv_dim) * a.wv_nb1);
+        }
+        for (int e0 = 8 * lane; e0 < E; e0 += 512) {
+            uint4 wq[KVP_ROWS_W];
+#pragma unroll
+            for (int r = 0; r < KVP_ROWS_W; r++) wq[r] = *(const uint4 *) (wrow[r] + e0);
+#pragma unroll
+            for (int t = 0; t < KVP_MAX_T; t++) {
+                if (t >= T) continue;
+                const uint4 cq = *(const uint4 *) &cur16[t * E + e0];
+                const uint32_t cw[4] = {cq.x, cq.y, cq.z, cq.w};
+#pragma unroll
+                for (int r = 0; r < KVP_ROWS_W; r++) {
+                    const uint32_t ww[4] = {wq[r].x, wq[r].y, wq[r].z, wq[r].w};
+                    float s = acc[r][t];
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        s = __fmaf_rn(h2f((uint16_t) ww[q]), h2f((uint16_t) cw[q]), s);
+                        s = __fmaf_rn(h2f((uint16_t) (ww[q] >> 16)), h2f((uint16_t) (cw[q] >> 16)), s);
+                    }
+                    acc[r][t] = s;
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < KVP_ROWS_W; r++)
+#pragma unroll
+            for (int t = 0; t < KVP_MAX_T; t++) {
+                if (t >= T) continue;
+                const float v = wave_sum(acc[r][t]);
+                if (lane == 0 && o0 + r < n_out) a.rows[t * n_out + o0 + r] = v;
+            }
+    }
+
+    // ---- the last workgroup to finish runs the epilogue ----
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) last = atomicAdd(a.ticket, 1u) == gridDim.x - 1 ? 1u : 0u;
+    __syncthreads();
+    if (!last) return;
+    if (threadIdx.x == 0) atomicExch(a.ticket, 0u);
+    __threadfence();
+
+    const int n_tasks = T * 2 * a.nh_kv;                 // (token, K heads then V heads)
+    float * hx = head[wv];
+    for (int task = wv; task < n_tasks; task += KVP_WAVES) {
+        const int t = task / (2 * a.nh_kv), hh = task - t * 2 * a.nh_kv;
+        const bool is_k = hh < a.nh_kv;
+        const int h = is_k ? hh : hh - a.nh_kv;
+        const volatile float * src = a.rows + t * n_out + (is_k ? 0 : a.kv_dim) + h * KVP_HD;
+        float x[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) x[i] = src[4 * lane + i];
+        if (is_k) {
+            // RMS norm (squares summed in double), times the weight
+            double sq = 0.0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) sq += (double) __fmul_rn(x[i], x[i]);
+            for (int off = 32; off >= 1; off >>= 1) sq += __shfl_xor(sq, off);
+            const float mean = (float) (sq / (double) KVP_HD);
+            const float scale = 1.0f / sqrtf(__fadd_rn(mean, a.eps));
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                x[i] = __fmul_rn(__fmul_rn(x[i], scale), a.k_norm_w[4 * lane + i]);
+                hx[4 * lane + i] = x[i];
+            }
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            // rope: the lane's values 4 lane + i that lie in the first n_dims
+            int32_t pos[4];
+            for (int s = 0; s < 4; s++) pos[s] = a.pos[s * T + t];
+            const int half = a.rp.n_dims / 2;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int d = 4 * lane + i;
+                if (d < a.rp.n_dims) {
+                    const int k = d < half ? d : d - half;
+                    float c, s, y0, y1;
+                    rope_cos_sin(a.rp, pos, k, &c, &s);
+                    rope_rotate(hx[k], hx[k + half], c, s, &y0, &y1);
+                    x[i] = d < half ? y0 : y1;
+                }
+            }
+        }
+        // q8_0 of the head row: 8 lanes per block
+        uint16_t d16;
+        float dqa;
+        const uint32_t q4 = dev::q8_quantize_lane4(x, a.x86 != 0, &d16, &dqa);
+        char * row = (is_k ? a.kc + (size_t) (a.first_row + t) * a.k_nb1 : a.vc + (size_t) (a.first_row + t) * a.v_nb1) +
+                     (size_t) h * (KVP_HD / QK) * QBLOCK;
+        char * bp = row + (lane >> 3) * QBLOCK;
+        uint16_t * qp = (uint16_t *) (bp + 2 + (lane & 7) * 4);
+        qp[0] = (uint16_t) (q4 & 0xffffu);
+        qp[1] = (uint16_t) (q4 >> 16);
+        if ((lane & 7) == 0) *(uint16_t *) bp = d16;
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");   // hx is reused by the next task
+    }
+}
+
+}  // namespace
+}  // namespace qwfn
+
+using namespace qwfn;
+
+extern "C" int qwfn_kv_produce_q8_0(const qwfn_tensor * cur, const qwfn_tensor * wk, const qwfn_tensor * wv,
+                                    const float * k_norm_w, const int32_t * pos, const qwfn_rope_cfg * rope,
+                                    const qwfn_tensor * k_cache, const qwfn_tensor * v_cache, int64_t first_row,
+                                    int variant, void * stream) {
+    return ::qwfn::abi_call("kv_produce_q8_0", [&]() -> int {
+        if (!cur || !wk || !wv || !k_norm_w || !pos || !rope || !k_cache || !v_cache || !cur->data || !wk->data ||
+            !wv->data || !k_cache->data || !v_cache->data)
+            return set_error(QWFN_EINVAL, "kv_produce: NULL argument");
+        if (cur->type != QWFN_TYPE_F32 || wk->type != QWFN_TYPE_F16 || wv->type != QWFN_TYPE_F16 ||
+            k_cache->type != QWFN_TYPE_Q8_0 || v_cache->type != QWFN_TYPE_Q8_0)
+            return set_error(QWFN_EINVAL, "kv_produce: cur f32, weights f16, caches q8_0");
+        if (variant != QWFN_Q8_REF && variant != QWFN_Q8_X86) return set_error(QWFN_EINVAL, "kv_produce: unknown variant");
+        const int64_t E = cur->ne[0], T = cur->ne[1];
+        if (cur->nb[0] != 4 || wk->nb[0] != 2 || wv->nb[0] != 2) return set_error(QWFN_EINVAL, "kv_produce: rows must be contiguous");
+        if (E < 8 || E % 8 || E > KVP_MAX_EMBD) return set_error(QWFN_ENOTSUP, "kv_produce: n_embd must be a multiple of 8, at most 8192");
+        if (T < 1 || T > KVP_MAX_T) return set_error(QWFN_ENOTSUP, "kv_produce: 1 to 16 tokens per call");
+        if (T * E * 2 > 128 * 1024) return set_error(QWFN_ENOTSUP, "kv_produce: T * n_embd must be at most 65536");
+        if (wk->ne[0] != E || wv->ne[0] != E || wk->ne[1] != wv->ne[1])
+            return set_error(QWFN_EINVAL, "kv_produce: weights must be [n_embd, kv_dim] for K and V alike");
+        const int64_t kv_dim = wk->ne[1];
+        if (kv_dim % KVP_HD || kv_dim / KVP_HD < 1 || kv_dim / KVP_HD > KVP_MAX_HKV)
+            return set_error(QWFN_ENOTSUP, "kv_produce: kv_dim must be 256 * n_head_kv, 1 to 8 heads");
+        if (k_cache->ne[0] != kv_dim || v_cache->ne[0] != kv_dim || k_cache->nb[0] != QBLOCK || v_cache->nb[0] != QBLOCK)
+            return set_error(QWFN_EINVAL, "kv_produce: caches must be q8_0 rows of kv_dim values");
+        if (k_cache->nb[1] < (size_t) kv_dim / QK * QBLOCK || v_cache->nb[1] < (size_t) kv_dim / QK * QBLOCK)
+            return set_error(QWFN_EINVAL, "kv_produce: cache rows overlap");
+        if (first_row < 0 || first_row + T > k_cache->ne[1] || first_row + T > v_cache->ne[1])
+            return set_error(QWFN_ERANGE, "kv_produce: rows first_row .. first_row + T - 1 must lie in the caches");
+        if (rope->n_dims < 2 || rope->n_dims % 2 || rope->n_dims > KVP_HD || !(rope->freq_base > 0.f) ||
+            !(rope->rms_eps >= 0.f))
+            return set_error(QWFN_EINVAL, "kv_produce: rope n_dims must be even and at most 256, freq_base positive");
+        int sect = 0;
+        for (int s = 0; s < 4; s++) {
+            if (rope->sections[s] < 0) return set_error(QWFN_EINVAL, "kv_produce: negative rope section");
+            sect += rope->sections[s];
+        }
+        if (sect <= 0) return set_error(QWFN_EINVAL, "kv_produce: rope sections must not all be zero");
+        if (!is_aligned(cur->data, 4) || cur->nb[1] % 4 || !is_aligned(wk->data, 16) || !is_aligned(wv->data, 16) ||
+            wk->nb[1] % 16 || wv->nb[1] % 16 || !is_aligned(k_norm_w, 4) || !is_aligned(pos, 4) ||
+            !is_aligned(k_cache->data, 2) || !is_aligned(v_cache->data, 2) || k_cache->nb[1] % 2 || v_cache->nb[1] % 2)
+            return set_error(QWFN_EALIGN, "kv_produce: weights 16-byte aligned rows, 4-byte f32 / i32, 2-byte cache rows");
+        kvp_args a{};
+        a.cur = (const float *) cur->data; a.cur_nb1 = cur->nb[1]; a.n_embd = (int32_t) E; a.T = (int32_t) T;
+        a.wk = (const uint16_t *) wk->data; a.wv = (const uint16_t *) wv->data; a.wk_nb1 = wk->nb[1]; a.wv_nb1 = wv->nb[1];
+        a.nh_kv = (int32_t) (kv_dim / KVP_HD); a.kv_dim = (int32_t) kv_dim;
+        a.k_norm_w = k_norm_w; a.eps = rope->rms_eps;
+        a.rp.n_dims = rope->n_dims;
+        for (int s = 0; s < 4; s++) a.rp.sections[s] = rope->sections[s];
+        a.rp.imrope = 1;
+        a.rp.theta_scale = powf(rope->freq_base, -2.0f / (float) rope->n_dims);
+        a.pos = pos;
+        a.kc = (char *) k_cache->data; a.vc = (char *) v_cache->data; a.k_nb1 = k_cache->nb[1]; a.v_nb1 = v_cache->nb[1];
+        a.first_row = first_row; a.x86 = variant == QWFN_Q8_X86;
+        // the staging buffer and the ticket, per device (their addresses, not the symbols)
+        int dev = 0;
+        if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
+        static float * rows_ptr[64];
+        static unsigned * ticket_ptr[64];
+        static std::mutex mu;
+        if (dev < 0 || dev >= 64) return set_error(QWFN_ENOTSUP, "kv_produce: device index beyond 63");
+        std::lock_guard<std::mutex> lock(mu);
+        if (!rows_ptr[dev]) {
+            void * p = nullptr;
+            void * q = nullptr;
+            if (int rc = hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(g_kvp_rows)), "hipGetSymbolAddress")) return rc;
+            if (int rc = hip_check(hipGetSymbolAddress(&q, HIP_SYMBOL(g_kvp_ticket)), "hipGetSymbolAddress")) return rc;
+            // the hidden rows of up to 16 tokens take more than 64 KB of LDS
+            if (int rc = hip_check(hipFuncSetAttribute((const void *) k_kv_produce,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024),
+                                   "hipFuncSetAttribute"))
+                return rc;
+            ticket_ptr[dev] = (unsigned *) q;
+            rows_ptr[dev] = (float *) p;
+        }
+        a.rows = rows_ptr[dev];
+        a.ticket = ticket_ptr[dev];
+        const int64_t n_out = 2 * kv_dim;
+        const int64_t blocks = (n_out + KVP_WAVES * KVP_ROWS_W - 1) / (KVP_WAVES * KVP_ROWS_W);
+        const size_t lds = (size_t) T * E * 2;
+        hipLaunchKernelGGL(k_kv_produce, dim3((unsigned) blocks), dim3(KVP_WAVES * 64), lds, as_stream(stream), a);
+        return hip_check(hipGetLastError(), "kv_produce launch");
+    });
+}

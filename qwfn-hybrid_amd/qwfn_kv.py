@@ -65,6 +65,21 @@ class QsaInputs(ctypes.Structure):
                 ("ratio", ctypes.c_int32), ("pad_", ctypes.c_int32), ("n_blocks_max", ctypes.c_int64)]
 
 
+class RopeCfg(ctypes.Structure):
+    """qwfn_rope_cfg: rope and norm constants of the attention layers."""
+    _fields_ = [("n_dims", ctypes.c_int32), ("sections", ctypes.c_int32 * 4), ("freq_base", ctypes.c_float),
+                ("rms_eps", ctypes.c_float)]
+
+
+def rope_cfg(n_dims: int = 64, sections=(11, 11, 10, 0), freq_base: float = 1e7, rms_eps: float = 1e-6) -> RopeCfg:
+    c = RopeCfg()
+    c.n_dims = n_dims
+    for i in range(4):
+        c.sections[i] = int(sections[i])
+    c.freq_base, c.rms_eps = freq_base, rms_eps
+    return c
+
+
 class QsaPoolCfg(ctypes.Structure):
     """qwfn_qsa_pool_cfg: the indexer key geometry and rope / norm constants."""
     _fields_ = [("idx_dim", ctypes.c_int32), ("n_dims", ctypes.c_int32), ("sections", ctypes.c_int32 * 4),
@@ -76,7 +91,8 @@ EXPORTS = [
     "qwfn_set_rows_q8_0", "qwfn_cpy_f32_q8_0", "qwfn_set_rows_q8_0_kv", "qwfn_cpy_f32_q8_0_kv", "qwfn_get_rows_i32", "qwfn_kv_gather_segments",
     "qwfn_fattn_workspace_size", "qwfn_fattn_force_splits", "qwfn_flash_attn_ext_q8_0", "qwfn_flash_attn_ext_q8_0_noalloc", "qwfn_flash_attn_ext_q8_0_append",
     "qwfn_fattn_workspace_size_seq", "qwfn_flash_attn_ext_q8_0_seq", "qwfn_state_restore",
-    "qwfn_fattn_workspace_size_cells", "qwfn_flash_attn_ext_q8_0_cells",
+    "qwfn_fattn_workspace_size_cells", "qwfn_flash_attn_ext_q8_0_cells", "qwfn_kv_produce_q8_0",
+    "qwfn_flash_attn_ext_q8_0_gated",
     # include/qwfn_state.h
     "qwfn_state_config_default", "qwfn_state_create", "qwfn_state_destroy", "qwfn_state_tensor",
     "qwfn_state_bytes", "qwfn_state_host_bytes", "qwfn_state_rollback_bytes", "qwfn_state_n_ctx",
@@ -132,6 +148,9 @@ def load(path: str = LIB_PATH):
     L.qwfn_fattn_workspace_size_cells.argtypes = [T, T, T, PL, i64]
     L.qwfn_fattn_workspace_size_cells.restype = sz
     L.qwfn_flash_attn_ext_q8_0_cells.argtypes = [T, T, T, vp, PL, i64, i64, ctypes.c_float, T, ctypes.c_int, vp, sz, vp]
+    L.qwfn_kv_produce_q8_0.argtypes = [T, T, T, vp, vp, ctypes.POINTER(RopeCfg), T, T, i64, ctypes.c_int, vp]
+    L.qwfn_flash_attn_ext_q8_0_gated.argtypes = [T, T, T, T, ctypes.c_float, ctypes.c_float, ctypes.c_float, T, T,
+                                                 ctypes.c_int, vp, sz, vp]
     L.qwfn_state_restore.argtypes = [ctypes.POINTER(vp), ctypes.POINTER(sz), ctypes.POINTER(vp), i32, i32, i32, vp]
     # include/qwfn_state.h
     u32, PV, PS = ctypes.c_uint32, ctypes.POINTER(vp), ctypes.POINTER(sz)
@@ -466,3 +485,33 @@ def qsa_pool_rebuild(ic, n_past: int, ratio: int, k_norm_w, pool, cfg=None, stre
     cfg = cfg or qsa_pool_cfg()
     return check(load().qwfn_qsa_pool_rebuild(ic.data_ptr(), ic.shape[0], n_past, ratio, k_norm_w.data_ptr(),
                                               pool.data_ptr(), pool.shape[0], ctypes.byref(cfg), _stream(stream)))
+
+
+def kv_produce(cur, wk, wv, k_norm_w, pos, kcache, vcache, first_row: int, variant: int = Q8_X86, rope=None,
+               stream=None):
+    """K/V producer: cur torch f32 [T, n_embd]; wk, wv torch f16 [kv_dim, n_embd]; k_norm_w f32 [256];
+    pos i32 [4 * T]; caches uint8 [n_rows, kv_dim/32*34] (all on the device)."""
+    T, E = cur.shape
+    kv_dim = wk.shape[0]
+    cv = tensor(cur.data_ptr(), TYPE_F32, (E, T), (4, cur.stride(0) * 4))
+    wkv = tensor(wk.data_ptr(), TYPE_F16, (E, kv_dim), (2, wk.stride(0) * 2))
+    wvv = tensor(wv.data_ptr(), TYPE_F16, (E, kv_dim), (2, wv.stride(0) * 2))
+    kcv = tensor(kcache.data_ptr(), TYPE_Q8_0, (kv_dim, kcache.shape[0]), (34, kcache.stride(0)))
+    vcv = tensor(vcache.data_ptr(), TYPE_Q8_0, (kv_dim, vcache.shape[0]), (34, vcache.stride(0)))
+    rope = rope or rope_cfg()
+    return check(load().qwfn_kv_produce_q8_0(ctypes.byref(cv), ctypes.byref(wkv), ctypes.byref(wvv),
+                                             k_norm_w.data_ptr(), pos.data_ptr(), ctypes.byref(rope), ctypes.byref(kcv),
+                                             ctypes.byref(vcv), first_row, variant, _stream(stream)))
+
+
+def flash_attn_ext_gated(qv: Tensor, kv: Tensor, vv: Tensor, mv: Tensor | None, scale: float, ov: Tensor, gate,
+                         variant: int = Q8_X86, ws=None, stream=None):
+    """Attention times sigmoid(gate): gate a torch f32 tensor laid out as the output."""
+    L = load()
+    gv = out_view(gate)
+    ws_ptr = ws.data_ptr() if ws is not None else None
+    ws_bytes = ws.numel() * ws.element_size() if ws is not None else 0
+    return check(L.qwfn_flash_attn_ext_q8_0_gated(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv),
+                                                  ctypes.byref(mv) if mv is not None else None, scale, 0.0, 0.0,
+                                                  ctypes.byref(ov), ctypes.byref(gv), variant, ws_ptr, ws_bytes,
+                                                  _stream(stream)))
