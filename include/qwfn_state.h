@@ -218,6 +218,30 @@ int qwfn_qsa_select_cells(const uint16_t * pool, size_t pool_nb1, int64_t n_bloc
                           const int32_t * blk_cells, int32_t ratio, int32_t * cells, int32_t * top, void * ws,
                           size_t ws_bytes, void * stream);
 
+/* ------------------------------------------------- Gated DeltaNet state */
+
+/* The recurrent update of a DeltaNet layer for T tokens with its rollback
+ * snapshots, one launch: ggml_gated_delta_net (qwfn_graph.cpp:258, inside
+ * graph_builder::deltanet :240-278) and the state copies of
+ * deltanet_write_state (:208-238). Per value head h (key head
+ * h / (n_v_heads / n_k_heads)), state S [head_dim][head_dim] (the second index
+ * contiguous), token t:
+ *   S = S * exp(g[t][h]);  m[c] = sum_r S[r][c] k[r]
+ *   S[r][c] += k[r] * (v[c] - m[c]) * beta[t][h]
+ *   out[t][h][c] = sum_r S[r][c] * q[r] * scale
+ * (the gated delta rule; q and k L2-normed by the caller as the reference's
+ * deltanet_conv_qkv does, scale 1/sqrt(head_dim)). q, k: F32 [n_k][head_dim]
+ * per token at q_token_stride / k_token_stride floats (the views of the conv
+ * output), v: [n_v][head_dim] per token at v_token_stride; g (log decay) and
+ * beta: F32 [T][n_v]; state: F32 [n_v][head_dim][head_dim], updated in place
+ * (rs_state); out: F32 [T][n_v][head_dim]; snap: n_snap <= T-1 slots at
+ * snap_stride_bytes, slot s-1 receiving the state s tokens back (the
+ * rollback slots rb_rs_). head_dim = 128. Device memory throughout. */
+int qwfn_gated_delta_net(const float * q, int64_t q_token_stride, const float * k, int64_t k_token_stride,
+                         const float * v, int64_t v_token_stride, const float * g, const float * beta, int32_t T,
+                         int32_t n_k_heads, int32_t n_v_heads, int32_t head_dim, float scale, float * state, float * out,
+                         float * snap, size_t snap_stride_bytes, int32_t n_snap, void * stream);
+
 /* ------------------------------------------------- QSA index producer */
 
 /* The indexer's key geometry and the rope / norm constants of the model

@@ -518,3 +518,42 @@ void oracle_kv_produce_q8_0(const float * cur, int64_t E, int64_t T, const uint1
     free(k);
     free(tmp);
 }
+
+/* ----------------------------------------------------- gated delta rule */
+
+void oracle_gated_delta_net(const float * q, int64_t q_ts, const float * k, int64_t k_ts, const float * v, int64_t v_ts,
+                            const float * g, const float * beta, float * state, float * out, float * snap,
+                            int64_t n_snap, int64_t T, int64_t n_k, int64_t n_v, int64_t dk, int64_t dv, float scale) {
+    const int64_t rep = n_v / n_k;
+    float * m = malloc(sizeof(float) * (size_t) dv);
+    for (int64_t h = 0; h < n_v; h++) {
+        float * S = state + (size_t) h * dk * dv;
+        const int64_t hk = h / rep;
+        for (int64_t t = 0; t < T; t++) {
+            const float * qt = q + t * q_ts + hk * dk;
+            const float * kt = k + t * k_ts + hk * dk;
+            const float * vt = v + t * v_ts + h * dv;
+            const float a = expf(g[t * n_v + h]);
+            const float b = beta[t * n_v + h];
+            for (int64_t i = 0; i < dk * dv; i++) S[i] = S[i] * a;
+            for (int64_t c = 0; c < dv; c++) {
+                float acc = 0.0f;
+                for (int64_t r = 0; r < dk; r++) acc = acc + S[r * dv + c] * kt[r];
+                m[c] = acc;
+            }
+            for (int64_t c = 0; c < dv; c++) {
+                const float d = (vt[c] - m[c]) * b;
+                for (int64_t r = 0; r < dk; r++) S[r * dv + c] = S[r * dv + c] + kt[r] * d;
+            }
+            for (int64_t c = 0; c < dv; c++) {
+                float acc = 0.0f;
+                for (int64_t r = 0; r < dk; r++) acc = acc + S[r * dv + c] * (qt[r] * scale);
+                out[(t * n_v + h) * dv + c] = acc;
+            }
+            const int64_t sb = T - 1 - t;
+            if (snap && sb >= 1 && sb <= n_snap)
+                memcpy(snap + ((size_t) (sb - 1) * n_v + h) * dk * dv, S, sizeof(float) * (size_t) dk * dv);
+        }
+    }
+    free(m);
+}

@@ -132,6 +132,24 @@ void oracle_kv_produce_q8_0(const float * cur, int64_t E, int64_t T, const uint1
                             int n_dims, float freq_base, float eps, void * k_rows, void * v_rows, float * k_f32,
                             float * v_f32, int variant);
 
+/* Gated delta rule (ggml_gated_delta_net as qwfn_graph.cpp:258 calls it; the
+ * op lives in the reference's llama.cpp fork, absent here, so this restates
+ * the published recurrence of Gated DeltaNet -- Yang, Kautz, Hatamizadeh
+ * 2024, as HF Qwen3-Next's recurrent form writes it): per value head h
+ * (key head h / (n_v / n_k)), state S [dk][dv] (dv contiguous), token t:
+ *   S = S * exp(g[t][h]);  m[c] = sum_r S[r][c] k[r]
+ *   S[r][c] += k[r] * (v[c] - m[c]) * beta[t][h]
+ *   out[t][h][c] = sum_r S[r][c] * q[r] * scale
+ * q, k: [T][n_k][dk] at token strides q_ts / k_ts floats; v: [T][n_v][dv] at
+ * v_ts; g, beta: [T][n_v]; state [n_v][dk][dv] in/out (the final state);
+ * snap (may be NULL): n_snap slots of [n_v][dk][dv], slot s-1 the state s
+ * tokens back (after token T-1-s), s = 1 .. n_snap <= T-1 (the rollback
+ * snapshots of deltanet_write_state, :208-238). Sums run over r in order, in
+ * float. */
+void oracle_gated_delta_net(const float * q, int64_t q_ts, const float * k, int64_t k_ts, const float * v, int64_t v_ts,
+                            const float * g, const float * beta, float * state, float * out, float * snap,
+                            int64_t n_snap, int64_t T, int64_t n_k, int64_t n_v, int64_t dk, int64_t dv, float scale);
+
 #ifdef __cplusplus
 }
 #endif

@@ -73,6 +73,8 @@ def lib():
         L.oracle_set_rows_f16.argtypes = [vp, i64, i64, vp, vp, i64]
         L.oracle_kv_produce_q8_0.argtypes = [vp, i64, i64, vp, vp, i64, vp, vp, vp, ctypes.c_int, ctypes.c_float,
                                              ctypes.c_float, vp, vp, vp, vp, ctypes.c_int]
+        L.oracle_gated_delta_net.argtypes = [vp, i64, vp, i64, vp, i64, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64,
+                                             i64, ctypes.c_float]
         L.oracle_qsa_pool_blocks.argtypes = [vp, i64, vp, i64, i64, vp, vp, vp, ctypes.c_float, ctypes.c_float,
                                              ctypes.c_int, vp]
         _lib = L
@@ -334,3 +336,22 @@ def kv_produce(cur: np.ndarray, wk_bits: np.ndarray, wv_bits: np.ndarray, k_norm
                                  _p(np.ascontiguousarray(k_norm_w, np.float32)), _p(np.ascontiguousarray(pos, np.int32)),
                                  _p(sec), n_dims, freq_base, eps, _p(k_rows), _p(v_rows), _p(k_f), _p(v_f), variant)
     return k_rows, v_rows, k_f, v_f
+
+
+def gated_delta_net(q: np.ndarray, k: np.ndarray, v: np.ndarray, g: np.ndarray, beta: np.ndarray, state: np.ndarray,
+                    n_snap: int = 0, scale: float | None = None):
+    """q, k f32 [T, n_k, dk]; v [T, n_v, dv]; g, beta [T, n_v]; state [n_v, dk, dv] (not modified).
+    Returns (out [T, n_v, dv], final state, snapshots [n_snap, n_v, dk, dv])."""
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    T, n_k, dk = q.shape
+    n_v, dv = v.shape[1], v.shape[2]
+    st = np.ascontiguousarray(state, np.float32).copy()
+    out = np.zeros((T, n_v, dv), np.float32)
+    snap = np.zeros((max(n_snap, 1), n_v, dk, dv), np.float32)
+    scale = float(1.0 / np.sqrt(dk)) if scale is None else scale
+    lib().oracle_gated_delta_net(_p(q), n_k * dk, _p(k), n_k * dk, _p(v), n_v * dv,
+                                 _p(np.ascontiguousarray(g, np.float32)), _p(np.ascontiguousarray(beta, np.float32)),
+                                 _p(st), _p(out), _p(snap) if n_snap else None, n_snap, T, n_k, n_v, dk, dv, scale)
+    return out, st, snap[:n_snap]

@@ -105,6 +105,7 @@ EXPORTS = [
     "qwfn_snap_pool_split", "qwfn_snap_pool_restore_or_reset",
     "qwfn_qsa_select_workspace_size", "qwfn_qsa_select_cells",
     "qwfn_qsa_pool_cfg_default", "qwfn_set_rows_f16", "qwfn_qsa_pool_decode", "qwfn_qsa_pool_rebuild",
+    "qwfn_gated_delta_net",
 ]
 
 _lib = None
@@ -204,6 +205,8 @@ def load(path: str = LIB_PATH):
     L.qwfn_set_rows_f16.argtypes = [T, T, T, vp]
     L.qwfn_qsa_pool_decode.argtypes = [vp, i64, vp, vp, vp, i32, vp, vp, vp, vp, i64, ctypes.POINTER(QsaPoolCfg), vp]
     L.qwfn_qsa_pool_rebuild.argtypes = [vp, i64, i64, i32, vp, vp, i64, ctypes.POINTER(QsaPoolCfg), vp]
+    L.qwfn_gated_delta_net.argtypes = [vp, i64, vp, i64, vp, i64, vp, vp, i32, i32, i32, i32, ctypes.c_float, vp, vp,
+                                       vp, sz, i32, vp]
     L.qwfn_qsa_select_workspace_size.argtypes = [i64, i32]
     L.qwfn_qsa_select_workspace_size.restype = sz
     L.qwfn_qsa_select_cells.argtypes = [vp, sz, i64, vp, i32, sz, vp, sz, i32, i32, vp, i32, vp, vp, vp, sz, vp]
@@ -515,3 +518,18 @@ def flash_attn_ext_gated(qv: Tensor, kv: Tensor, vv: Tensor, mv: Tensor | None, 
                                                   ctypes.byref(mv) if mv is not None else None, scale, 0.0, 0.0,
                                                   ctypes.byref(ov), ctypes.byref(gv), variant, ws_ptr, ws_bytes,
                                                   _stream(stream)))
+
+
+def gated_delta_net(q, k, v, g, beta, state, out, n_k: int, snap=None, n_snap: int = 0, scale: float | None = None,
+                    stream=None):
+    """The gated delta rule over T tokens. q, k: torch f32 [T, >= n_k*128] (token stride = row stride);
+    v: [T, >= n_v*128]; g, beta: [T, n_v]; state [n_v, 128, 128] in place; out [T, n_v, 128];
+    snap [>= n_snap, n_v, 128, 128] or None."""
+    T = q.shape[0]
+    n_v, hd = state.shape[0], state.shape[1]
+    scale = 1.0 / hd ** 0.5 if scale is None else scale
+    return check(load().qwfn_gated_delta_net(q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), v.data_ptr(),
+                                             v.stride(0), g.data_ptr(), beta.data_ptr(), T, n_k, n_v, hd, scale,
+                                             state.data_ptr(), out.data_ptr(),
+                                             snap.data_ptr() if snap is not None else None,
+                                             snap.stride(0) * 4 if snap is not None else 0, n_snap, _stream(stream)))
