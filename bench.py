@@ -220,6 +220,56 @@ def measure_state_rows(K, torch, np, dev, gbs) -> dict:
     del pool, qsel, bsel, bcells, csel, wsel
     rows["decode_step_inputs"] = {"us_per_step": round(us, 2), "launches": 3,
                                   "what": "qsa_decode_prepare, qsa_decode_prepare_k (18432-block bias), cell mask 2052->2304"}
+
+    # ---- the QSA index producer: one decode step's raw key + pooled block key, and the
+    #      pool rebuild after a 65536-position prefill (16384 blocks of 4) ----
+    n_ctx, ratio = 73728, 4
+    ic = (torch.randn((n_ctx, 128), generator=gsel, device=dev)).to(torch.float16)
+    kpool = torch.zeros((n_ctx // ratio, 128), dtype=torch.float16, device=dev)
+    knw = torch.rand(128, generator=gsel, device=dev) + 0.5
+    kraw = torch.randn(128, generator=gsel, device=dev)
+    us = timed_graph(torch, lambda k: K.qsa_pool_decode(ic, kraw, qd.write_idx, qd.member_idx, ratio, qd.blk_pos,
+                                                         qd.blk_idx, knw, kpool), 16, 10)
+    rows["qsa_pool_decode"] = {"us_per_call": round(us, 2), "ratio": ratio,
+                               "what": "raw key F16 set_rows + mean-pool, RMS norm, IMROPE of its block (one launch)"}
+    n_past = 65536
+    us = timed(torch, lambda k: K.qsa_pool_rebuild(ic, n_past, ratio, knw, kpool), 20)
+    rb = n_past * 128 * 2 + (n_past // ratio) * 128 * 2
+    rows["qsa_pool_rebuild_64k"] = {"us_per_call": round(us, 2), "blocks": n_past // ratio, "bytes": rb,
+                                    "GBs": gbs(rb, us), "frac": frac(rb, us)}
+    del ic, kpool
+
+    # ---- the K/V producer of a 3-token verify step (F16 weights 2 x 512 x 2560) ----
+    E, kv_dim, T3 = 2560, 512, 3
+    wk = (torch.randn((kv_dim, E), generator=gsel, device=dev) * 0.02).to(torch.float16)
+    wv = (torch.randn((kv_dim, E), generator=gsel, device=dev) * 0.02).to(torch.float16)
+    hid = torch.randn((T3, E), generator=gsel, device=dev)
+    kpos = torch.arange(16384, 16384 + T3, dtype=torch.int32, device=dev).repeat(4)
+    kcp = torch.zeros((16400, 544), dtype=torch.uint8, device=dev)
+    vcp = torch.zeros((16400, 544), dtype=torch.uint8, device=dev)
+    knw256 = torch.rand(256, generator=gsel, device=dev) + 0.5
+    us = timed_graph(torch, lambda k: K.kv_produce(hid, wk, wv, knw256, kpos, kcp, vcp, 16384), 16, 10)
+    pb = 2 * kv_dim * E * 2 + T3 * E * 4 + 2 * T3 * 544
+    rows["kv_produce_T3"] = {"us_per_call": round(us, 2), "bytes": pb, "GBs": gbs(pb, us), "frac": frac(pb, us),
+                             "what": "attn_k/attn_v projections + K RMS norm + IMROPE + q8_0 append, two launches"}
+    del wk, wv, kcp, vcp
+
+    # ---- one DeltaNet layer's recurrent update for a 3-token verify step with 2
+    #      rollback snapshots (48 value heads of 128: 3.1 MB of state) ----
+    conv = torch.randn((T3, 10240), generator=gsel, device=dev)
+    conv[:, :4096] = torch.nn.functional.normalize(conv[:, :4096].view(T3, 32, 128), dim=-1).view(T3, 4096)
+    dg = -torch.rand((T3, 48), generator=gsel, device=dev)
+    db = torch.rand((T3, 48), generator=gsel, device=dev)
+    dstates = [torch.randn((48, 128, 128), generator=gsel, device=dev) * 0.05 for _ in range(8)]
+    dout = torch.empty((T3, 48, 128), dtype=torch.float32, device=dev)
+    dsnap = torch.empty((2, 48, 128, 128), dtype=torch.float32, device=dev)
+    us = timed_graph(torch, lambda k: K.gated_delta_net(conv[:, :2048], conv[:, 2048:4096], conv[:, 4096:], dg, db,
+                                                        dstates[k % 8], dout, 16, dsnap, 2), 16, 10)
+    sb = 48 * 128 * 128 * 4
+    db_ = 2 * sb + 2 * sb + T3 * 10240 * 4 + T3 * 48 * 128 * 4
+    rows["gated_delta_net_T3"] = {"us_per_call": round(us, 2), "bytes": db_, "GBs": gbs(db_, us), "frac": frac(db_, us),
+                                  "what": "state read + written, 2 rollback snapshots written, q/k/v/out"}
+    del conv, dstates, dsnap
     torch.cuda.empty_cache()
     return rows
 

@@ -230,7 +230,8 @@ typedef struct qwfn_rope_cfg {
     float   rms_eps;
 } qwfn_rope_cfg;
 
-/* The layer's K/V producer for a decode or verify step, one launch: K =
+/* The layer's K/V producer for a decode or verify step (two launches: the
+ * projections, then norm, rope and quantisation): K =
  * attn_k . cur and V = attn_v . cur (ggml_mul_mat with F16 weights: cur
  * converted to F16, F16 products summed in F32), each K head RMS-normed and
  * multiplied by k_norm_w (F32 [256]), roped (IMROPE at pos, I32 [4 * T]
@@ -239,8 +240,8 @@ typedef struct qwfn_rope_cfg {
  * rows first_row .. first_row + T - 1. Replaces qwfn_graph.cpp:441-451 (the
  * mul_mats and rms), :446-451 / :129-132 (rope) and :370-384 (kv_append).
  * cur: F32 [n_embd, T] (T <= 16, n_embd a multiple of 8, T * n_embd <=
- * 65536); wk, wv: F16 [n_embd, kv_dim] (kv_dim = 256 * n_head_kv <= 2048,
- * 16-byte aligned rows); caches: q8_0 [kv_dim, n_rows]. The projected rows
+ * 65536, 16-byte aligned rows); wk, wv: F16 [n_embd, kv_dim] (kv_dim = 256 *
+ * n_head_kv <= 2048, 16-byte aligned rows); caches: q8_0 [kv_dim, n_rows]. The projected rows
  * pass through a device-resident staging buffer of the library (one per GPU):
  * calls that overlap on one GPU race. The K/V bytes equal ggml's quantiser on
  * the F32 rows this kernel computes; those rows differ from ggml-cpu's only

@@ -1,4 +1,4 @@
-// The attention layer's K/V producer, one launch for a decode or verify step:
+// The attention layer's K/V producer for a decode or verify step, two launches:
 // the K and V projections of the step's hidden rows, RMS norm of each K head
 // times attn_k_norm, IMROPE at the tokens' positions, and the q8_0 append of
 // both into the caches -- the ops qwfn_graph.cpp:441-451 (attn_k / attn_v
@@ -6,14 +6,17 @@
 // F32 -> q8_0) emit one by one.
 //
 // Projection: ggml_mul_mat with F16 weights converts the F32 hidden rows to
-// F16 and sums the F16 products in F32. Each wave computes 4 output rows for
-// all T tokens: 16-byte weight loads along n_embd, the hidden rows (F16) in
-// LDS, per-lane F32 partial sums, a wave reduction. The rows land in a
-// device-resident staging buffer; the workgroup that finishes last (a ticket
-// counter, reset by that workgroup) runs the epilogue for every (token, head):
-// K heads are normed, weighted and roped (rope_device.h, ggml-cpu's float
-// order), then quantised with the cache quantiser (q8_device.h) into row
-// first_row + t; V heads are quantised as they are.
+// F16 and sums the F16 products in F32. Each wave computes one output row for
+// all T tokens: the row's 16-byte weight loads are issued before the block
+// stages the hidden rows (F16) in LDS, then per-lane F32 partial sums and a
+// wave reduction. The rows land in a device-resident staging buffer. The
+// second launch takes one (token, head) per wave: K heads are normed, weighted
+// and roped (rope_device.h, ggml-cpu's float order; one lane per rope pair
+// computes its cos / sin), then quantised with the cache quantiser
+// (q8_device.h) into row first_row + t; V heads are quantised as they are. (A single launch whose
+// last workgroup runs the epilogue needs a device-scope release per
+// workgroup, an L2 write-back each: measured 13 us more than the second
+// launch.)
 #include "q8_device.h"
 #include "qwfn_common.h"
 #include "qwfn_state.h"
@@ -28,15 +31,14 @@ namespace {
 constexpr int KVP_MAX_T = 16;            // tokens per call
 constexpr int KVP_MAX_HKV = 8;           // KV heads
 constexpr int KVP_HD = 256;              // head size
-constexpr int KVP_ROWS_W = 4;            // output rows per wave
 constexpr int KVP_WAVES = 4;
 constexpr int KVP_MAX_EMBD = 8192;       // hidden size, at most (the F16 rows of all tokens fit LDS)
+constexpr int KVP_MAX_PAIRS = 128;       // rope pairs per head, at most
 constexpr int KVP_STAGE = KVP_MAX_T * 2 * KVP_MAX_HKV * KVP_HD;   // F32 projected rows
 
-// projected rows of the current call ([t][K rows | V rows]) and the ticket;
-// one set per device: calls that overlap on one device race
+// projected rows of the current call ([t][K rows | V rows]), one buffer per
+// device: calls that overlap on one device race
 __device__ float g_kvp_rows[KVP_STAGE];
-__device__ unsigned g_kvp_ticket = 0;
 
 struct kvp_args {
     const float *    cur;         // F32 [n_embd] per token, token stride cur_nb1 bytes
@@ -58,7 +60,6 @@ struct kvp_args {
     int64_t          first_row;
     int32_t          x86;
     float *          rows;        // g_kvp_rows
-    unsigned *       ticket;      // g_kvp_ticket
 };
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float) __builtin_bit_cast(_Float16, h); }
@@ -68,86 +69,102 @@ __device__ __forceinline__ float wave_sum(float x) {
     return x;
 }
 
-__global__ __launch_bounds__(KVP_WAVES * 64) void k_kv_produce(kvp_args a) {
+__global__ __launch_bounds__(KVP_WAVES * 64) void k_kv_project(kvp_args a) {
     extern __shared__ uint16_t cur16[];          // [T][n_embd] F16 hidden rows
-    __shared__ float head[KVP_WAVES][KVP_HD];    // epilogue: one head row per wave
-    __shared__ unsigned last;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int T = a.T, E = a.n_embd;
-
-    // ---- the hidden rows, F32 -> F16 (ggml's conversion of src1) ----
-    for (int i = threadIdx.x; i < T * E; i += KVP_WAVES * 64) {
-        const int t = i / E, e = i - t * E;
-        const float x = *(const float *) ((const char *) a.cur + (size_t) t * a.cur_nb1 + (size_t) e * 4);
-        cur16[i] = __builtin_bit_cast(uint16_t, (_Float16) x);
-    }
-    __syncthreads();
-
-    // ---- projection: wave w of block b takes output rows 4 (4b + w) .. +3 of
-    //      [K rows | V rows]; lane l takes the 8 hidden values 8 l + 512 j ----
     const int n_out = 2 * a.kv_dim;
-    const int o0 = (blockIdx.x * KVP_WAVES + wv) * KVP_ROWS_W;
-    if (o0 < n_out) {
-        float acc[KVP_ROWS_W][KVP_MAX_T];
+
+    // ---- wave w of block b takes output row 4b + w of [K rows | V rows];
+    //      lane l takes the 8 hidden values 8 l + 512 j: its weight loads go
+    //      out first, so that they overlap the staging below ----
+    const int o = blockIdx.x * KVP_WAVES + wv;
+    const int oc = o < n_out ? o : n_out - 1;
+    const uint16_t * wrow = oc < a.kv_dim ? (const uint16_t *) ((const char *) a.wk + (size_t) oc * a.wk_nb1)
+                                          : (const uint16_t *) ((const char *) a.wv + (size_t) (oc - a.kv_dim) * a.wv_nb1);
+    uint4 wq[KVP_MAX_EMBD / 512];
 #pragma unroll
-        for (int r = 0; r < KVP_ROWS_W; r++)
+    for (int j = 0; j < KVP_MAX_EMBD / 512; j++)
+        if (512 * j < E) wq[j] = *(const uint4 *) (wrow + (512 * j + 8 * lane < E ? 512 * j + 8 * lane : 0));
+
+    // ---- the hidden rows, F32 -> F16 (ggml's conversion of src1): 4 values a
+    //      lane, 4 loads in flight before any conversion ----
+    {
+        const int n4 = T * E / 4;
+        const uint32_t e4_mul = (uint32_t) (((uint64_t(1) << 32) + (uint64_t) (E / 4) - 1) / (uint64_t) (E / 4));
+        for (int i0 = threadIdx.x; i0 < n4; i0 += KVP_WAVES * 64 * 4) {
+            float4 x[4];
+            int idx[4];
 #pragma unroll
-            for (int t = 0; t < KVP_MAX_T; t++) acc[r][t] = 0.f;
-        const uint16_t * wrow[KVP_ROWS_W];
+            for (int u = 0; u < 4; u++) {
+                const int i = i0 + KVP_WAVES * 64 * u;
+                const int ii = i < n4 ? i : n4 - 1;
+                const int t = E / 4 == 1 ? ii : (int) __umulhi((uint32_t) ii, e4_mul);
+                const int e = 4 * (ii - t * (E / 4));
+                x[u] = *(const float4 *) ((const char *) a.cur + (size_t) t * a.cur_nb1 + (size_t) e * 4);
+                idx[u] = i < n4 ? 4 * i : -1;
+            }
 #pragma unroll
-        for (int r = 0; r < KVP_ROWS_W; r++) {
-            const int o = o0 + r < n_out ? o0 + r : o0;
-            wrow[r] = o < a.kv_dim ? (const uint16_t *) ((const char *) a.wk + (size_t) o * a.wk_nb1)
-                                   : (const uint16_t *) ((const char *) a.wv + (size_t) (o - a.kv_dim) * a.wv_nb1);
-        }
-        for (int e0 = 8 * lane; e0 < E; e0 += 512) {
-            uint4 wq[KVP_ROWS_W];
-#pragma unroll
-            for (int r = 0; r < KVP_ROWS_W; r++) wq[r] = *(const uint4 *) (wrow[r] + e0);
-#pragma unroll
-            for (int t = 0; t < KVP_MAX_T; t++) {
-                if (t >= T) continue;
-                const uint4 cq = *(const uint4 *) &cur16[t * E + e0];
-                const uint32_t cw[4] = {cq.x, cq.y, cq.z, cq.w};
-#pragma unroll
-                for (int r = 0; r < KVP_ROWS_W; r++) {
-                    const uint32_t ww[4] = {wq[r].x, wq[r].y, wq[r].z, wq[r].w};
-                    float s = acc[r][t];
-#pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        s = __fmaf_rn(h2f((uint16_t) ww[q]), h2f((uint16_t) cw[q]), s);
-                        s = __fmaf_rn(h2f((uint16_t) (ww[q] >> 16)), h2f((uint16_t) (cw[q] >> 16)), s);
-                    }
-                    acc[r][t] = s;
-                }
+            for (int u = 0; u < 4; u++) {
+                if (idx[u] < 0) continue;
+                const uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16) x[u].x) |
+                                    ((uint32_t) __builtin_bit_cast(uint16_t, (_Float16) x[u].y) << 16);
+                const uint32_t hi = __builtin_bit_cast(uint16_t, (_Float16) x[u].z) |
+                                    ((uint32_t) __builtin_bit_cast(uint16_t, (_Float16) x[u].w) << 16);
+                *(uint2 *) &cur16[idx[u]] = make_uint2(lo, hi);
             }
         }
-#pragma unroll
-        for (int r = 0; r < KVP_ROWS_W; r++)
-#pragma unroll
-            for (int t = 0; t < KVP_MAX_T; t++) {
-                if (t >= T) continue;
-                const float v = wave_sum(acc[r][t]);
-                if (lane == 0 && o0 + r < n_out) a.rows[t * n_out + o0 + r] = v;
-            }
     }
-
-    // ---- the last workgroup to finish runs the epilogue ----
-    __threadfence();
     __syncthreads();
-    if (threadIdx.x == 0) last = atomicAdd(a.ticket, 1u) == gridDim.x - 1 ? 1u : 0u;
-    __syncthreads();
-    if (!last) return;
-    if (threadIdx.x == 0) atomicExch(a.ticket, 0u);
-    __threadfence();
 
+    // ---- projection ----
+    float acc[KVP_MAX_T];
+#pragma unroll
+    for (int t = 0; t < KVP_MAX_T; t++) acc[t] = 0.f;
+#pragma clang loop unroll(full)
+    for (int j = 0; j < KVP_MAX_EMBD / 512; j++) {
+        const int e0 = 512 * j + 8 * lane;
+        if (e0 >= E) continue;
+        const uint32_t ww[4] = {wq[j].x, wq[j].y, wq[j].z, wq[j].w};
+#pragma unroll
+        for (int t = 0; t < KVP_MAX_T; t++) {
+            if (t >= T) continue;
+            const uint4 cq = *(const uint4 *) &cur16[t * E + e0];
+            const uint32_t cw[4] = {cq.x, cq.y, cq.z, cq.w};
+            float s = acc[t];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                s = __fmaf_rn(h2f((uint16_t) ww[q]), h2f((uint16_t) cw[q]), s);
+                s = __fmaf_rn(h2f((uint16_t) (ww[q] >> 16)), h2f((uint16_t) (cw[q] >> 16)), s);
+            }
+            acc[t] = s;
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < KVP_MAX_T; t++) {
+        if (t >= T) continue;
+        const float v = wave_sum(acc[t]);
+        if (lane == 0 && o < n_out) a.rows[t * n_out + o] = v;
+    }
+}
+
+// The epilogue: wave w of block b takes (token, head) task 4b + w (K heads,
+// then V heads, of each token).
+__global__ __launch_bounds__(KVP_WAVES * 64) void k_kv_epilogue(kvp_args a) {
+    __shared__ float head[KVP_WAVES][KVP_HD];
+    __shared__ float csw[KVP_WAVES][2][KVP_MAX_PAIRS];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int T = a.T;
+    const int n_out = 2 * a.kv_dim;
+    const int half = a.rp.n_dims / 2;
     const int n_tasks = T * 2 * a.nh_kv;                 // (token, K heads then V heads)
     float * hx = head[wv];
-    for (int task = wv; task < n_tasks; task += KVP_WAVES) {
+    const int task = blockIdx.x * KVP_WAVES + wv;
+    if (task < n_tasks) {
         const int t = task / (2 * a.nh_kv), hh = task - t * 2 * a.nh_kv;
         const bool is_k = hh < a.nh_kv;
         const int h = is_k ? hh : hh - a.nh_kv;
-        const volatile float * src = a.rows + t * n_out + (is_k ? 0 : a.kv_dim) + h * KVP_HD;
+        const float * src = a.rows + t * n_out + (is_k ? 0 : a.kv_dim) + h * KVP_HD;
         float x[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) x[i] = src[4 * lane + i];
@@ -166,18 +183,20 @@ __global__ __launch_bounds__(KVP_WAVES * 64) void k_kv_produce(kvp_args a) {
             }
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-            // rope: the lane's values 4 lane + i that lie in the first n_dims
+            // rope: lane k computes pair k's cos / sin, then each lane rotates
+            // its values 4 lane + i that lie in the first n_dims
             int32_t pos[4];
             for (int s = 0; s < 4; s++) pos[s] = a.pos[s * T + t];
-            const int half = a.rp.n_dims / 2;
+            for (int k = lane; k < half; k += 64) rope_cos_sin(a.rp, pos, k, &csw[wv][0][k], &csw[wv][1][k]);
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int d = 4 * lane + i;
                 if (d < a.rp.n_dims) {
                     const int k = d < half ? d : d - half;
-                    float c, s, y0, y1;
-                    rope_cos_sin(a.rp, pos, k, &c, &s);
-                    rope_rotate(hx[k], hx[k + half], c, s, &y0, &y1);
+                    float y0, y1;
+                    rope_rotate(hx[k], hx[k + half], csw[wv][0][k], csw[wv][1][k], &y0, &y1);
                     x[i] = d < half ? y0 : y1;
                 }
             }
@@ -193,8 +212,6 @@ __global__ __launch_bounds__(KVP_WAVES * 64) void k_kv_produce(kvp_args a) {
         qp[0] = (uint16_t) (q4 & 0xffffu);
         qp[1] = (uint16_t) (q4 >> 16);
         if ((lane & 7) == 0) *(uint16_t *) bp = d16;
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");   // hx is reused by the next task
     }
 }
 
@@ -231,7 +248,7 @@ extern "C" int qwfn_kv_produce_q8_0(const qwfn_tensor * cur, const qwfn_tensor *
             return set_error(QWFN_EINVAL, "kv_produce: cache rows overlap");
         if (first_row < 0 || first_row + T > k_cache->ne[1] || first_row + T > v_cache->ne[1])
             return set_error(QWFN_ERANGE, "kv_produce: rows first_row .. first_row + T - 1 must lie in the caches");
-        if (rope->n_dims < 2 || rope->n_dims % 2 || rope->n_dims > KVP_HD || !(rope->freq_base > 0.f) ||
+        if (rope->n_dims < 2 || rope->n_dims % 2 || rope->n_dims > 2 * KVP_MAX_PAIRS || !(rope->freq_base > 0.f) ||
             !(rope->rms_eps >= 0.f))
             return set_error(QWFN_EINVAL, "kv_produce: rope n_dims must be even and at most 256, freq_base positive");
         int sect = 0;
@@ -240,10 +257,10 @@ extern "C" int qwfn_kv_produce_q8_0(const qwfn_tensor * cur, const qwfn_tensor *
             sect += rope->sections[s];
         }
         if (sect <= 0) return set_error(QWFN_EINVAL, "kv_produce: rope sections must not all be zero");
-        if (!is_aligned(cur->data, 4) || cur->nb[1] % 4 || !is_aligned(wk->data, 16) || !is_aligned(wv->data, 16) ||
+        if (!is_aligned(cur->data, 16) || cur->nb[1] % 16 || !is_aligned(wk->data, 16) || !is_aligned(wv->data, 16) ||
             wk->nb[1] % 16 || wv->nb[1] % 16 || !is_aligned(k_norm_w, 4) || !is_aligned(pos, 4) ||
             !is_aligned(k_cache->data, 2) || !is_aligned(v_cache->data, 2) || k_cache->nb[1] % 2 || v_cache->nb[1] % 2)
-            return set_error(QWFN_EALIGN, "kv_produce: weights 16-byte aligned rows, 4-byte f32 / i32, 2-byte cache rows");
+            return set_error(QWFN_EALIGN, "kv_produce: cur and weights 16-byte aligned rows, 4-byte i32 / weight, 2-byte cache rows");
         kvp_args a{};
         a.cur = (const float *) cur->data; a.cur_nb1 = cur->nb[1]; a.n_embd = (int32_t) E; a.T = (int32_t) T;
         a.wk = (const uint16_t *) wk->data; a.wv = (const uint16_t *) wv->data; a.wk_nb1 = wk->nb[1]; a.wv_nb1 = wv->nb[1];
@@ -256,33 +273,32 @@ extern "C" int qwfn_kv_produce_q8_0(const qwfn_tensor * cur, const qwfn_tensor *
         a.pos = pos;
         a.kc = (char *) k_cache->data; a.vc = (char *) v_cache->data; a.k_nb1 = k_cache->nb[1]; a.v_nb1 = v_cache->nb[1];
         a.first_row = first_row; a.x86 = variant == QWFN_Q8_X86;
-        // the staging buffer and the ticket, per device (their addresses, not the symbols)
+        // the staging buffer, per device (its address, not the symbol)
         int dev = 0;
         if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
         static float * rows_ptr[64];
-        static unsigned * ticket_ptr[64];
         static std::mutex mu;
         if (dev < 0 || dev >= 64) return set_error(QWFN_ENOTSUP, "kv_produce: device index beyond 63");
         std::lock_guard<std::mutex> lock(mu);
         if (!rows_ptr[dev]) {
             void * p = nullptr;
-            void * q = nullptr;
             if (int rc = hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(g_kvp_rows)), "hipGetSymbolAddress")) return rc;
-            if (int rc = hip_check(hipGetSymbolAddress(&q, HIP_SYMBOL(g_kvp_ticket)), "hipGetSymbolAddress")) return rc;
             // the hidden rows of up to 16 tokens take more than 64 KB of LDS
-            if (int rc = hip_check(hipFuncSetAttribute((const void *) k_kv_produce,
+            if (int rc = hip_check(hipFuncSetAttribute((const void *) k_kv_project,
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024),
                                    "hipFuncSetAttribute"))
                 return rc;
-            ticket_ptr[dev] = (unsigned *) q;
             rows_ptr[dev] = (float *) p;
         }
         a.rows = rows_ptr[dev];
-        a.ticket = ticket_ptr[dev];
         const int64_t n_out = 2 * kv_dim;
-        const int64_t blocks = (n_out + KVP_WAVES * KVP_ROWS_W - 1) / (KVP_WAVES * KVP_ROWS_W);
+        const int64_t blocks = (n_out + KVP_WAVES - 1) / KVP_WAVES;
         const size_t lds = (size_t) T * E * 2;
-        hipLaunchKernelGGL(k_kv_produce, dim3((unsigned) blocks), dim3(KVP_WAVES * 64), lds, as_stream(stream), a);
-        return hip_check(hipGetLastError(), "kv_produce launch");
+        hipLaunchKernelGGL(k_kv_project, dim3((unsigned) blocks), dim3(KVP_WAVES * 64), lds, as_stream(stream), a);
+        if (int rc = hip_check(hipGetLastError(), "kv_produce launch")) return rc;
+        const int64_t tasks = T * 2 * (kv_dim / KVP_HD);
+        hipLaunchKernelGGL(k_kv_epilogue, dim3((unsigned) ((tasks + KVP_WAVES - 1) / KVP_WAVES)), dim3(KVP_WAVES * 64), 0,
+                           as_stream(stream), a);
+        return hip_check(hipGetLastError(), "kv_produce epilogue launch");
     });
 }
