@@ -711,7 +711,7 @@ def main() -> int:
     # rocprofv3 --pmc passes summarised under profiles/ (FETCH_SIZE, WRITE_SIZE,
     # each scaled by what the counter reads for a plain copy of known size)
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", "fattn_q8_0.mtp_verify_16k.traffic.json")
+    tpath = os.path.join(ROOT, "profiles", "fa_dec.verify_16k.traffic.json")
     if os.path.exists(tpath):
         tj = json.load(open(tpath))
         w = tj.get("workload", {})
