@@ -7,7 +7,10 @@
  * licence; not present in the reference tree or in this image) for:
  *   block_q8_0, quantize_row_q8_0[_ref], dequantize_row_q8_0,
  *   ggml_vec_dot_q8_0_q8_0, set_rows/cpy F32->Q8_0, get_rows (I32),
- *   flash_attn_ext one-chunk CPU loop.
+ *   flash_attn_ext one-chunk CPU loop, rms_norm, rope_multi (IMROPE),
+ *   set_rows F32->F16, the QSA block pooling, the attention layer's K/V
+ *   producer and the gated delta rule (ggml_gated_delta_net, an op of the
+ *   reference's ggml fork: parity unpinned, see oracle_gated_delta_net).
  * The reference's use of them: qwfn_graph.cpp:370-384 (cpy append),
  * :612-628 (set_rows append), :632-645 (raw get_rows gather), :458-475 and
  * :697-701 (flash_attn_ext), qwfn_state.cpp:48-91 (cache layout).
@@ -414,6 +417,9 @@ int oracle_attn_f64(const oracle_view * q, const oracle_view * k, const oracle_v
 
 /* ------------------------------------------------------ QSA index producer */
 
+/* ggml_rms_norm (then the caller's ggml_mul by the weight): the squares summed
+ * in double, the mean rounded to float, scale = 1 / sqrtf(mean + eps).
+ * Used at qwfn_graph.cpp:124-126 (rms), :443 (attn_k_norm), :295 (pooled keys). */
 void oracle_rms_norm_f32(const float * x, float * y, int64_t n, float eps) {
     double sum = 0.0;
     for (int64_t i = 0; i < n; i++) sum += (double) (x[i] * x[i]);
@@ -422,6 +428,10 @@ void oracle_rms_norm_f32(const float * x, float * y, int64_t n, float eps) {
     for (int64_t i = 0; i < n; i++) y[i] = x[i] * scale;
 }
 
+/* ggml_rope_multi, neox pairs (k, k + n_dims/2), GGML_ROPE_TYPE_IMROPE sections
+ * interleaved t, h, w over the pairs (qwfn_graph.cpp:128-131, :297-299,
+ * :911-913); the angle is pos * theta_scale^k as a running float product,
+ * theta_scale = powf(freq_base, -2 / n_dims), cos / sin of the float angle. */
 void oracle_rope_multi_f32(const float * x, float * y, int64_t ne0, int n_dims, const int32_t pos[4],
                            const int sections[4], int imrope, float freq_base) {
     const float theta_scale = powf(freq_base, -2.0f / (float) n_dims);
@@ -481,6 +491,14 @@ void oracle_qsa_pool_blocks(const uint16_t * ic, int64_t idx_dim, const int32_t 
 
 /* ----------------------------------------------------- K/V producer */
 
+/* The attention layer's K/V producer for T tokens (qwfn_graph.cpp:441-451 for
+ * the projections, attn_k_norm and rope; :370-384 / :623-624 for the q8_0
+ * append): ggml_mul_mat with F16 weights (the F32 rows converted to F16, the
+ * F16 products summed; summed in double here, which ggml's F32 accumulation
+ * order matches to within a float rounding: parity of the projection is to a
+ * tolerance, of everything after it bit for bit), K rms-normed times the
+ * weight and roped, then both quantised with quantize_row_q8_0 (variant). */
+
 void oracle_kv_produce_q8_0(const float * cur, int64_t E, int64_t T, const uint16_t * wk, const uint16_t * wv,
                             int64_t kv_dim, const float * k_norm_w, const int32_t * pos, const int sections[4],
                             int n_dims, float freq_base, float eps, void * k_rows, void * v_rows, float * k_f32,
@@ -520,6 +538,16 @@ void oracle_kv_produce_q8_0(const float * cur, int64_t E, int64_t T, const uint1
 }
 
 /* ----------------------------------------------------- gated delta rule */
+
+/* The recurrence of ggml_gated_delta_net as the reference calls it
+ * (qwfn_graph.cpp:240-278; snapshots for rollback :210-238): per value head h
+ * (key head h / (n_v / n_k)), per token, S *= exp(g); m = S^T k;
+ * S += k (v - m)^T beta; out = S^T q * scale; snapshot s = the state after
+ * token T - 1 - s. The op belongs to the reference's ggml fork, which is not in
+ * the reference tree or this image: the head broadcast rule and the float
+ * order are restated from its call site and the gated delta rule's published
+ * definition (parity unpinned beyond the fp64 brute force and closed forms of
+ * tests/test_oracle_deltanet.py). */
 
 void oracle_gated_delta_net(const float * q, int64_t q_ts, const float * k, int64_t k_ts, const float * v, int64_t v_ts,
                             const float * g, const float * beta, float * state, float * out, float * snap,

@@ -267,7 +267,7 @@ RMS_EPS = 1e-6                        # qwfn_hparams.h:26
 
 
 def rms_norm(x: np.ndarray, eps: float = RMS_EPS) -> np.ndarray:
-    """ggml_rms_norm over the last axis (float32)."""
+    """ggml_rms_norm over the last axis (float32); qwfn_graph.cpp:124-126, :443, :295."""
     x = np.ascontiguousarray(x, np.float32)
     y = np.empty_like(x)
     n = x.shape[-1]
@@ -279,7 +279,8 @@ def rms_norm(x: np.ndarray, eps: float = RMS_EPS) -> np.ndarray:
 
 def rope_multi(x: np.ndarray, pos, n_dims: int = ROPE_DIM, sections=IMROPE_SECTIONS, imrope: bool = True,
                freq_base: float = ROPE_FREQ_BASE) -> np.ndarray:
-    """ggml_rope_multi of one or more heads (last axis) at one position (t, h, w, e)."""
+    """ggml_rope_multi (IMROPE) of one or more heads (last axis) at one position (t, h, w, e);
+    qwfn_graph.cpp:128-131, :297-299, :911-913."""
     x = np.ascontiguousarray(x, np.float32)
     y = np.empty_like(x)
     n = x.shape[-1]
@@ -292,7 +293,8 @@ def rope_multi(x: np.ndarray, pos, n_dims: int = ROPE_DIM, sections=IMROPE_SECTI
 
 
 def set_rows_f16(dst_bits: np.ndarray, src: np.ndarray, idx: np.ndarray) -> None:
-    """dst_bits uint16 [rows, ne0] in place: row idx[i] = fp16(src[i])."""
+    """ggml_set_rows F32 -> F16 (qwfn_graph.cpp:543, the raw indexer key):
+    dst_bits uint16 [rows, ne0] in place, row idx[i] = fp16(src[i])."""
     src = np.ascontiguousarray(src, np.float32)
     idx = np.ascontiguousarray(idx, np.int32)
     rc = lib().oracle_set_rows_f16(_p(dst_bits), dst_bits.shape[0], dst_bits.shape[1], _p(src), _p(idx), len(idx))
@@ -303,7 +305,8 @@ def set_rows_f16(dst_bits: np.ndarray, src: np.ndarray, idx: np.ndarray) -> None
 def qsa_pool_blocks(ic_bits: np.ndarray, members: np.ndarray, r: int, k_norm_w: np.ndarray, pos4: np.ndarray,
                     n_dims: int = ROPE_DIM, sections=IMROPE_SECTIONS, eps: float = RMS_EPS,
                     freq_base: float = ROPE_FREQ_BASE) -> np.ndarray:
-    """Pooled F16 bits [n_blk, idx_dim]: members [n_blk * r] rows of ic_bits (uint16 [rows, idx_dim]),
+    """qsa_pool_blocks (qwfn_graph.cpp:282-301; decode :544-549, rebuild qwfn_engine.cpp:1121-1145):
+    pooled F16 bits [n_blk, idx_dim] from members [n_blk * r] rows of ic_bits (uint16 [rows, idx_dim]),
     pos4 [n_blk, 4] int32 (t, h, w, e)."""
     ic_bits = np.ascontiguousarray(ic_bits, np.uint16)
     members = np.ascontiguousarray(members, np.int32)
@@ -320,7 +323,8 @@ def qsa_pool_blocks(ic_bits: np.ndarray, members: np.ndarray, r: int, k_norm_w: 
 def kv_produce(cur: np.ndarray, wk_bits: np.ndarray, wv_bits: np.ndarray, k_norm_w: np.ndarray, pos: np.ndarray,
                variant: int = Q8_X86, n_dims: int = ROPE_DIM, sections=IMROPE_SECTIONS, freq_base: float = ROPE_FREQ_BASE,
                eps: float = RMS_EPS):
-    """cur f32 [T, E]; w*_bits uint16 [kv_dim, E]; pos int32 [4*T]. Returns (k_rows, v_rows, k_f32, v_f32):
+    """The K/V producer (qwfn_graph.cpp:441-451, then the append of :370-384 / :623-624):
+    cur f32 [T, E]; w*_bits uint16 [kv_dim, E]; pos int32 [4*T]. Returns (k_rows, v_rows, k_f32, v_f32):
     q8_0 rows uint8 [T, kv_dim/32*34] and the float rows before quantisation [T, kv_dim]."""
     cur = np.ascontiguousarray(cur, np.float32)
     T, E = cur.shape
@@ -340,7 +344,9 @@ def kv_produce(cur: np.ndarray, wk_bits: np.ndarray, wv_bits: np.ndarray, k_norm
 
 def gated_delta_net(q: np.ndarray, k: np.ndarray, v: np.ndarray, g: np.ndarray, beta: np.ndarray, state: np.ndarray,
                     n_snap: int = 0, scale: float | None = None):
-    """q, k f32 [T, n_k, dk]; v [T, n_v, dv]; g, beta [T, n_v]; state [n_v, dk, dv] (not modified).
+    """The gated delta rule of ggml_gated_delta_net (qwfn_graph.cpp:240-278, snapshots :210-238; an op of
+    the reference's ggml fork, parity unpinned beyond the fp64 brute force and closed forms):
+    q, k f32 [T, n_k, dk]; v [T, n_v, dv]; g, beta [T, n_v]; state [n_v, dk, dv] (not modified).
     Returns (out [T, n_v, dv], final state, snapshots [n_snap, n_v, dk, dv])."""
     q = np.ascontiguousarray(q, np.float32)
     k = np.ascontiguousarray(k, np.float32)

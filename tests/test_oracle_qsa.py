@@ -135,3 +135,31 @@ def test_pool_blocks_composition(r):
         n = m / np.sqrt((m ** 2).mean() + O.RMS_EPS) * w
         ref = _neox(n, _angles_f32(b * r, N_DIMS // 2))
         np.testing.assert_allclose(got[b], ref, rtol=2e-3, atol=1e-4)
+
+
+@pytest.mark.parametrize("T,variant", [(1, O.Q8_X86), (3, O.Q8_REF)])
+def test_kv_produce_composition(T, variant):
+    """The oracle's K/V producer (qwfn_graph.cpp:441-451, then the q8_0 append)
+    against the same steps done independently: the projection in fp64 numpy of
+    the F16 weights and the F16-rounded hidden rows (ggml_mul_mat's conversion
+    of src1), the K heads through the pinned rms_norm x weight and rope_multi,
+    both tensors through the pinned quantiser."""
+    rng = np.random.default_rng(40 + T)
+    E, kv_dim = 96, 512
+    cur = rng.standard_normal((T, E)).astype(np.float32)
+    wk = (rng.standard_normal((kv_dim, E)) * 0.1).astype(np.float16)
+    wv = (rng.standard_normal((kv_dim, E)) * 0.1).astype(np.float16)
+    knw = rng.uniform(0.5, 1.5, 256).astype(np.float32)
+    pos = np.tile(np.arange(700, 700 + T, dtype=np.int32), 4)
+    k_rows, v_rows, k_f, v_f = O.kv_produce(cur, wk.view(np.uint16), wv.view(np.uint16), knw, pos, variant)
+    c16 = cur.astype(np.float16).astype(np.float64)
+    kp = c16 @ wk.astype(np.float64).T
+    vp = c16 @ wv.astype(np.float64).T
+    np.testing.assert_allclose(v_f, vp, rtol=1e-6, atol=1e-6)
+    for t in range(T):
+        heads = kp[t].astype(np.float32).reshape(2, 256)
+        kn = O.rms_norm(heads) * knw
+        ref_k = O.rope_multi(kn, int(pos[t])).reshape(-1)
+        np.testing.assert_allclose(k_f[t], ref_k, rtol=1e-5, atol=1e-5)
+        np.testing.assert_array_equal(k_rows[t], O.quantize(k_f[t], variant).reshape(-1))
+        np.testing.assert_array_equal(v_rows[t], O.quantize(v_f[t], variant).reshape(-1))
