@@ -1812,7 +1812,7 @@ __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
 // placed on one XCD, whose L2 then serves the same rows to all of them. Per
 // chunk the block converts V to f16 once, transposed to [dim][key] (the PV A
 // operand of a lane is one 16-byte LDS read), repacks the K quants to
-// [block][key][32] (the QK A operand of a lane is one aligned 8-byte read),
+// [block][key][32 + 8 padding] (the QK A operand of a lane is one aligned 8-byte read),
 // and tabulates the K and V block scales; then each wave takes its 16 rows
 // over the 64 keys: exact i8 block dots (v_mfma_i32_16x16x32_i8, one q8_0
 // block each) scaled by d_q*d_k, one online-softmax step, and hi + lo f16
@@ -1833,9 +1833,14 @@ constexpr int PRE_MOFF  = 2 * PRE_KB;                     // mask granules follo
 constexpr int PRE_STAGE = PRE_MOFF + PRE_MDMA * 1024;     // 39936 bytes
 constexpr int PRE_SLOTS = 2 * PRE_TDMA + PRE_MDMA;        // 39 DMA slots per chunk
 constexpr int PRE_SPW   = (PRE_SLOTS + PRE_WAVES - 1) / PRE_WAVES;   // 5 per wave
-constexpr int PRE_VTS   = 2 * PRE_CK + 16;                // 144: bytes per dim row of V^T (padded: no bank conflicts)
-constexpr int PRE_VT    = D * PRE_VTS;                    // 36864
-constexpr int PRE_KQ    = NBLK * PRE_CK * QK;             // 16384: a chunk's K quants [block][key][32]
+// LDS rows are padded so that the wave-wide operand reads meet no bank
+// conflict on gfx950 (measured): 16-byte reads of 16 rows need a row stride of
+// 16 bytes times 2 mod 4, 8-byte reads of 16 rows one of 8 bytes times an odd
+// number (the unpadded 128- and 32-byte strides ran 1.8x and 3.8x slower)
+constexpr int PRE_VTS   = 2 * PRE_CK + 32;                // 160: bytes per dim row of V^T
+constexpr int PRE_VT    = D * PRE_VTS;                    // 40960
+constexpr int PRE_KQS   = QK + 8;                         // 40: bytes per key row of the repacked K quants
+constexpr int PRE_KQ    = NBLK * PRE_CK * PRE_KQS;        // 20480: a chunk's K quants [block][key][32 + 8]
 constexpr int PRE_QIMG  = NBLK * 16 * QK;                 // 4096: a wave's query quants [block][row][32]
 constexpr int PRE_QW    = PRE_QIMG + 16 * NBLK * 4;       // + d_q [row][block]
 static_assert(PRE_KB % 1024 == 0, "a tensor's rows of a chunk are whole wave DMAs");
@@ -1855,11 +1860,25 @@ __device__ __forceinline__ uint32_t cvt_i8_pair(uint32_t s0, uint32_t s1) {
         asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
             "v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_0"
             : "=&v"(d) : "v"(s0), "v"(s1));
-    else
+    else if constexpr (B == 1)
         asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
             "v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1"
             : "=&v"(d) : "v"(s0), "v"(s1));
+    else if constexpr (B == 2)
+        asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
+            "v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_2"
+            : "=&v"(d) : "v"(s0), "v"(s1));
+    else
+        asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_3\n\t"
+            "v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_3"
+            : "=&v"(d) : "v"(s0), "v"(s1));
     return d;
+}
+
+// The 4 quant bytes that start 2 bytes into the 4-byte-aligned word at p
+// (q8_0 blocks of even index start 2 bytes past a word boundary).
+__device__ __forceinline__ uint32_t quads_at_plus2(const uint8_t * p) {
+    return __builtin_amdgcn_alignbyte(*(const uint32_t *) (p + 4), *(const uint32_t *) p, 2);
 }
 
 template <bool MASKED>
@@ -2054,40 +2073,54 @@ __global__ __launch_bounds__(PRE_WAVES * 64, 2) void k_fa_pre(fa_args a) {
         if (c + 1 < n_chunks) issue_chunk(c + 1, lds + ((c + 1) & 1) * PRE_STAGE);
         // conversion pass: wave w takes V block w (dims 32w .. 32w+31) of the
         // 64 keys: lane (key pair kp, half dh) converts dims 32w + 16dh .. +15 of
-        // the keys at V^T positions 2kp, 2kp + 1; lane k also tabulates the K
-        // and V scales of block w of key k
+        // the keys at V^T positions 2kp, 2kp + 1, and K block w of key `lane`
+        // into the repacked quants; lane k also tabulates the K and V scales of
+        // block w of key k. Rows sit 272 bytes (68 words, 4 banks mod 32) apart,
+        // so reads of one offset in many rows would meet in 8 banks: the reads
+        // are whole words, and each lane starts its run of words at a rotated
+        // word, so that one read's lanes cover every bank.
         {
             const int kp = lane & 31, dh = lane >> 5;
             const int p0 = 2 * kp;
             // the key at position p0 (its neighbour p0 + 1 is the next key)
             const int key0 = 32 * (p0 >> 5) + 16 * ((p0 >> 2) & 1) + 4 * ((p0 >> 3) & 3) + (p0 & 3);
-            const uint8_t * src0 = st + PRE_KB + key0 * SEG + QBLOCK * wave + 2 + 16 * dh;
-            uint32_t s0[8], s1[8];
-#pragma unroll
-            for (int m = 0; m < 8; m++) {
-                s0[m] = *(const uint16_t *) (src0 + 2 * m);
-                s1[m] = *(const uint16_t *) (src0 + SEG + 2 * m);
-            }
-            const uint16_t kd = *(const uint16_t *) (st + lane * SEG + QBLOCK * wave);
-            const uint16_t vd = *(const uint16_t *) (st + PRE_KB + lane * SEG + QBLOCK * wave);
-            // K block w of key `lane`: its 32 quants to kq[w][lane]
+            const bool odd = (wave & 1) != 0;          // block w's quants start on a word boundary (34w + 2 = 0 mod 4)
+            // V: word t of the lane's 16 bytes holds dims 16dh + 4t .. + 3 of keys key0 / key0 + 1
             {
-                const uint16_t * ks = (const uint16_t *) (st + lane * SEG + QBLOCK * wave + 2);
-                uint32_t kw[8];
+                const uint8_t * v0 = st + PRE_KB + key0 * SEG + QBLOCK * wave + 16 * dh + (odd ? 2 : 0);
+                uint8_t * vrow = vt + (32 * wave + 16 * dh) * PRE_VTS + 2 * p0;
+                const int rot = (kp >> 3) & 3;
 #pragma unroll
-                for (int m = 0; m < 8; m++) kw[m] = (uint32_t) ks[2 * m] | ((uint32_t) ks[2 * m + 1] << 16);
-                uint4 * kd4 = (uint4 *) (kq + (wave * PRE_CK + lane) * QK);
-                kd4[0] = make_uint4(kw[0], kw[1], kw[2], kw[3]);
-                kd4[1] = make_uint4(kw[4], kw[5], kw[6], kw[7]);
+                for (int i = 0; i < 4; i++) {
+                    const int t = (i + rot) & 3;
+                    uint32_t x, y;
+                    if (odd) {
+                        x = *(const uint32_t *) (v0 + 4 * t);
+                        y = *(const uint32_t *) (v0 + SEG + 4 * t);
+                    } else {
+                        x = quads_at_plus2(v0 + 4 * t);
+                        y = quads_at_plus2(v0 + SEG + 4 * t);
+                    }
+                    uint8_t * d = vrow + 4 * t * PRE_VTS;
+                    *(uint32_t *) (d) = cvt_i8_pair<0>(x, y);
+                    *(uint32_t *) (d + PRE_VTS) = cvt_i8_pair<1>(x, y);
+                    *(uint32_t *) (d + 2 * PRE_VTS) = cvt_i8_pair<2>(x, y);
+                    *(uint32_t *) (d + 3 * PRE_VTS) = cvt_i8_pair<3>(x, y);
+                }
             }
-            uint8_t * dst0 = vt + (32 * wave + 16 * dh) * PRE_VTS + 2 * p0;
+            // K: word j of block w of key `lane` (quants 4j .. 4j + 3) to kq[w][lane]
+            {
+                const uint8_t * k0 = st + lane * SEG + QBLOCK * wave + (odd ? 2 : 0);
+                uint8_t * kd = kq + (wave * PRE_CK + lane) * PRE_KQS;
+                const int rot = (lane >> 3) & 7;
 #pragma unroll
-            for (int m = 0; m < 8; m++) {
-                *(uint32_t *) (dst0 + (2 * m) * PRE_VTS) = cvt_i8_pair<0>(s0[m], s1[m]);
-                *(uint32_t *) (dst0 + (2 * m + 1) * PRE_VTS) = cvt_i8_pair<1>(s0[m], s1[m]);
+                for (int i = 0; i < 8; i++) {
+                    const int jw = (i + rot) & 7;
+                    *(uint32_t *) (kd + 4 * jw) = odd ? *(const uint32_t *) (k0 + 4 * jw) : quads_at_plus2(k0 + 4 * jw);
+                }
             }
-            skv[0][wave][lane] = kd;
-            skv[1][wave][lane] = vd;
+            skv[0][wave][lane] = *(const uint16_t *) (st + lane * SEG + QBLOCK * wave);
+            skv[1][wave][lane] = *(const uint16_t *) (st + PRE_KB + lane * SEG + QBLOCK * wave);
         }
         __syncthreads();   // V^T and the scale tables of chunk c are complete
 
@@ -2112,10 +2145,10 @@ __global__ __launch_bounds__(PRE_WAVES * 64, 2) void k_fa_pre(fa_args a) {
             long kA[2][NBLK];
             uint2 dk[2][NBLK];
             auto load_tile = [&](int kt, long (&ka)[NBLK], uint2 (&dkk)[NBLK]) __attribute__((always_inline)) {
-                const uint8_t * kr = kq + (16 * kt + ln) * QK + 8 * lg;
+                const uint8_t * kr = kq + (16 * kt + ln) * PRE_KQS + 8 * lg;
 #pragma unroll
                 for (int bb = 0; bb < NBLK; bb++) {
-                    ka[bb] = *(const long *) (kr + bb * PRE_CK * QK);
+                    ka[bb] = *(const long *) (kr + bb * PRE_CK * PRE_KQS);
                     dkk[bb] = *(const uint2 *) &skv[0][bb][16 * kt + 4 * lg];
                 }
             };
