@@ -1841,10 +1841,16 @@ constexpr int PRE_VTS   = 2 * PRE_CK + 32;                // 160: bytes per dim 
 constexpr int PRE_VT    = D * PRE_VTS;                    // 40960
 constexpr int PRE_KQS   = QK + 8;                         // 40: bytes per key row of the repacked K quants
 constexpr int PRE_KQ    = NBLK * PRE_CK * PRE_KQS;        // 20480: a chunk's K quants [block][key][32 + 8]
+constexpr int PRE_SKV   = 2 * NBLK * PRE_CK * 2;          // 2048: K and V scales [K|V][block][key] fp16
 constexpr int PRE_QIMG  = NBLK * 16 * QK;                 // 4096: a wave's query quants [block][row][32]
 constexpr int PRE_QW    = PRE_QIMG + 16 * NBLK * 4;       // + d_q [row][block]
+// LDS: V^T | K quants | scales | stage 0 | stage 1. The regions the key loop
+// reads most end below 64 KB, so that their offsets fit the 16-bit offset of
+// an LDS instruction and one base register serves many accesses.
+constexpr int PRE_LDS   = PRE_VT + PRE_KQ + PRE_SKV + 2 * PRE_STAGE;   // 143360
+static_assert(PRE_VT + PRE_KQ + PRE_SKV <= 65536, "V^T, K quants and scales sit below 64 KB");
 static_assert(PRE_KB % 1024 == 0, "a tensor's rows of a chunk are whole wave DMAs");
-static_assert(PRE_WAVES * PRE_QW <= PRE_STAGE + PRE_VT, "the query images fit stage 1 and V^T");
+static_assert(PRE_WAVES * PRE_QW <= PRE_VT + PRE_KQ, "the query images fit V^T and the K quants");
 static_assert(PRE_CK == 64 && NBLK == PRE_WAVES, "the conversion pass: wave w takes V block w of every key");
 
 // V^T rows hold a chunk's keys in this order: key k = 32h + 16tt + 4g + i
@@ -1875,20 +1881,16 @@ __device__ __forceinline__ uint32_t cvt_i8_pair(uint32_t s0, uint32_t s1) {
     return d;
 }
 
-// The 4 quant bytes that start 2 bytes into the 4-byte-aligned word at p
-// (q8_0 blocks of even index start 2 bytes past a word boundary).
-__device__ __forceinline__ uint32_t quads_at_plus2(const uint8_t * p) {
-    return __builtin_amdgcn_alignbyte(*(const uint32_t *) (p + 4), *(const uint32_t *) p, 2);
-}
-
 template <bool MASKED>
 __global__ __launch_bounds__(PRE_WAVES * 64, 2) void k_fa_pre(fa_args a) {
     asm volatile("" :: "s"(a.q), "s"(a.k), "s"(a.v), "s"(a.mask), "s"(a.part_o));
-    // stage 0 | stage 1 | V^T; the query images of the prologue use stage 1 and V^T
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * PRE_STAGE + PRE_VT + PRE_KQ];
-    __shared__ __attribute__((aligned(16))) uint16_t skv[2][NBLK][PRE_CK];   // [K|V][block][key] fp16 scales
-    uint8_t * const vt = lds + 2 * PRE_STAGE;
+    // V^T | K quants | scales | stage 0 | stage 1; the query images of the
+    // prologue use V^T and the K quants
+    __shared__ __attribute__((aligned(16))) uint8_t lds[PRE_LDS];
+    uint8_t * const vt = lds;
     uint8_t * const kq = vt + PRE_VT;
+    uint16_t (* const skv)[NBLK][PRE_CK] = (uint16_t (*)[NBLK][PRE_CK]) (kq + PRE_KQ);   // [K|V][block][key] fp16 scales
+    uint8_t * const stg = kq + PRE_KQ + PRE_SKV;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -2004,12 +2006,12 @@ __global__ __launch_bounds__(PRE_WAVES * 64, 2) void k_fa_pre(fa_args a) {
             __syncthreads();
         }
     }
-    if (n_chunks > 0) issue_chunk(0, lds);
+    if (n_chunks > 0) issue_chunk(0, stg);
 
     // ---- prologue: each wave requantises its own 16 query rows (ggml's
     //      quantiser; 4 lanes per (row, block)) into an image of its own, from
     //      which lane (ln, lg) takes quants 8 lg .. 8 lg + 7 of each block of row ln ----
-    uint8_t * qimg = lds + PRE_STAGE + wave * PRE_QW;       // [block][row][32] int8
+    uint8_t * qimg = lds + wave * PRE_QW;                   // [block][row][32] int8
     float * dql = (float *) (qimg + PRE_QIMG);                  // [16 rows][NBLK]
     long qw[NBLK];
     float dq[NBLK];
@@ -2067,75 +2069,96 @@ __global__ __launch_bounds__(PRE_WAVES * 64, 2) void k_fa_pre(fa_args a) {
     // ---- the key loop: chunk c in stage c % 2; chunk c + 1 loads while chunk c
     //      is converted and computed ----
     for (int c = 0; c < n_chunks; c++) {
-        uint8_t * st = lds + (c & 1) * PRE_STAGE;
+        uint8_t * st = stg + (c & 1) * PRE_STAGE;
         wait_vmcnt<0>();
         __syncthreads();   // chunk c has landed; every wave is done with chunk c - 1 (and the prologue)
-        if (c + 1 < n_chunks) issue_chunk(c + 1, lds + ((c + 1) & 1) * PRE_STAGE);
+        if (c + 1 < n_chunks) issue_chunk(c + 1, stg + ((c + 1) & 1) * PRE_STAGE);
         // conversion pass: wave w takes V block w (dims 32w .. 32w+31) of the
         // 64 keys: lane (key pair kp, half dh) converts dims 32w + 16dh .. +15 of
         // the keys at V^T positions 2kp, 2kp + 1, and K block w of key `lane`
         // into the repacked quants; lane k also tabulates the K and V scales of
-        // block w of key k. Rows sit 272 bytes (68 words, 4 banks mod 32) apart,
-        // so reads of one offset in many rows would meet in 8 banks: the reads
-        // are whole words, and each lane starts its run of words at a rotated
-        // word, so that one read's lanes cover every bank.
+        // block w of key k. Block w's quants start 2 bytes into a word when w
+        // is even and on a word boundary when w is odd (34w + 2 = 0 mod 4): the
+        // lanes read whole words from the word at or before them and realign
+        // them with alignbyte (shift 2 or 0), with no branch on the parity.
+        // Rows sit 272 bytes (68 words, 4 banks mod 32) apart, so reads of one
+        // offset in many rows would meet in 8 banks: each lane reads its run of
+        // words starting at a rotated word (slot i holds word (i + rot) mod n,
+        // the word past the run sits in slot n), so that one read's lanes cover
+        // every bank. Every read is issued before the first conversion.
         {
             const int kp = lane & 31, dh = lane >> 5;
             const int p0 = 2 * kp;
             // the key at position p0 (its neighbour p0 + 1 is the next key)
             const int key0 = 32 * (p0 >> 5) + 16 * ((p0 >> 2) & 1) + 4 * ((p0 >> 3) & 3) + (p0 & 3);
-            const bool odd = (wave & 1) != 0;          // block w's quants start on a word boundary (34w + 2 = 0 mod 4)
-            // V: word t of the lane's 16 bytes holds dims 16dh + 4t .. + 3 of keys key0 / key0 + 1
-            {
-                const uint8_t * v0 = st + PRE_KB + key0 * SEG + QBLOCK * wave + 16 * dh + (odd ? 2 : 0);
-                uint8_t * vrow = vt + (32 * wave + 16 * dh) * PRE_VTS + 2 * p0;
-                const int rot = (kp >> 3) & 3;
+            const int odd = wave & 1;
+            const uint32_t sh = odd ? 0u : 2u;
+            const uint8_t * v0 = st + PRE_KB + key0 * SEG + QBLOCK * wave + 16 * dh + 2 * odd;
+            const uint8_t * k0 = st + lane * SEG + QBLOCK * wave + 2 * odd;
+            const int vrot = (kp >> 3) & 3, krot = (lane >> 3) & 7;
+            uint32_t x[5], y[5], kw[9];
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int t = (i + rot) & 3;
-                    uint32_t x, y;
-                    if (odd) {
-                        x = *(const uint32_t *) (v0 + 4 * t);
-                        y = *(const uint32_t *) (v0 + SEG + 4 * t);
-                    } else {
-                        x = quads_at_plus2(v0 + 4 * t);
-                        y = quads_at_plus2(v0 + SEG + 4 * t);
-                    }
-                    uint8_t * d = vrow + 4 * t * PRE_VTS;
-                    *(uint32_t *) (d) = cvt_i8_pair<0>(x, y);
-                    *(uint32_t *) (d + PRE_VTS) = cvt_i8_pair<1>(x, y);
-                    *(uint32_t *) (d + 2 * PRE_VTS) = cvt_i8_pair<2>(x, y);
-                    *(uint32_t *) (d + 3 * PRE_VTS) = cvt_i8_pair<3>(x, y);
-                }
+            for (int i = 0; i < 4; i++) {
+                const int t = (i + vrot) & 3;
+                x[i] = *(const uint32_t *) (v0 + 4 * t);
+                y[i] = *(const uint32_t *) (v0 + SEG + 4 * t);
+            }
+            x[4] = *(const uint32_t *) (v0 + 16);
+            y[4] = *(const uint32_t *) (v0 + SEG + 16);
+#pragma unroll
+            for (int i = 0; i < 8; i++) kw[i] = *(const uint32_t *) (k0 + 4 * ((i + krot) & 7));
+            kw[8] = *(const uint32_t *) (k0 + 32);
+            const uint16_t dk16 = *(const uint16_t *) (st + lane * SEG + QBLOCK * wave);
+            const uint16_t dv16 = *(const uint16_t *) (st + PRE_KB + lane * SEG + QBLOCK * wave);
+            // V: word t of the lane's 16 bytes holds dims 16dh + 4t .. + 3 of keys key0 / key0 + 1
+            uint8_t * vrow = vt + (32 * wave + 16 * dh) * PRE_VTS + 2 * p0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int t = (i + vrot) & 3;
+                const uint32_t xa = __builtin_amdgcn_alignbyte(t == 3 ? x[4] : x[(i + 1) & 3], x[i], sh);
+                const uint32_t ya = __builtin_amdgcn_alignbyte(t == 3 ? y[4] : y[(i + 1) & 3], y[i], sh);
+                uint8_t * d = vrow + 4 * t * PRE_VTS;
+                *(uint32_t *) (d) = cvt_i8_pair<0>(xa, ya);
+                *(uint32_t *) (d + PRE_VTS) = cvt_i8_pair<1>(xa, ya);
+                *(uint32_t *) (d + 2 * PRE_VTS) = cvt_i8_pair<2>(xa, ya);
+                *(uint32_t *) (d + 3 * PRE_VTS) = cvt_i8_pair<3>(xa, ya);
             }
             // K: word j of block w of key `lane` (quants 4j .. 4j + 3) to kq[w][lane]
-            {
-                const uint8_t * k0 = st + lane * SEG + QBLOCK * wave + (odd ? 2 : 0);
-                uint8_t * kd = kq + (wave * PRE_CK + lane) * PRE_KQS;
-                const int rot = (lane >> 3) & 7;
+            uint8_t * kd = kq + (wave * PRE_CK + lane) * PRE_KQS;
 #pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    const int jw = (i + rot) & 7;
-                    *(uint32_t *) (kd + 4 * jw) = odd ? *(const uint32_t *) (k0 + 4 * jw) : quads_at_plus2(k0 + 4 * jw);
-                }
+            for (int i = 0; i < 8; i++) {
+                const int t = (i + krot) & 7;
+                *(uint32_t *) (kd + 4 * t) = __builtin_amdgcn_alignbyte(t == 7 ? kw[8] : kw[(i + 1) & 7], kw[i], sh);
             }
-            skv[0][wave][lane] = *(const uint16_t *) (st + lane * SEG + QBLOCK * wave);
-            skv[1][wave][lane] = *(const uint16_t *) (st + PRE_KB + lane * SEG + QBLOCK * wave);
+            skv[0][wave][lane] = dk16;
+            skv[1][wave][lane] = dv16;
         }
         __syncthreads();   // V^T and the scale tables of chunk c are complete
 
         // ---- the wave's 16 rows over the chunk's keys: the lane's keys are
         //      16 kt + 4 lg + i (key tile kt, i = 0..3) ----
+        // mask pairs: mv[kt][j] holds the f16 mask of keys 16 kt + 4 lg + 2j (low
+        // half) and + 1 (high half); a pair of two -inf is 0xFC00FC00. Keys past
+        // the split (the last chunk only) arrive as zeros and are not live.
         const int kin = c * PRE_CK + 4 * lg;
-        uint32_t mv[4][4];
-        bool live = false;
+        const bool tail = (c + 1) * PRE_CK > span;
+        uint32_t mv[4][2];
+        bool live = !MASKED;
 #pragma unroll
         for (int kt = 0; kt < 4; kt++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                mv[kt][i] = MASKED ? *(const uint16_t *) (st + m_lane + 32 * kt + 2 * i) : 0u;
-                live |= kin + 16 * kt + i < span && (!MASKED || mv[kt][i] != 0xFC00u);
+            for (int j = 0; j < 2; j++) {
+                mv[kt][j] = MASKED ? *(const uint32_t *) (st + m_lane + 32 * kt + 4 * j) : 0u;
+                if (MASKED) live |= mv[kt][j] != 0xFC00FC00u;
             }
+        if (tail) {
+            live = false;
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    live |= kin + 16 * kt + i < span && (!MASKED || ((mv[kt][i >> 1] >> (16 * (i & 1))) & 0xffffu) != 0xFC00u);
+        }
         if (!wave_rows || !__any(live)) continue;
 
         // S = K Q^T per key tile (MFMA rows: keys; columns: the wave's rows);
@@ -2183,15 +2206,23 @@ __global__ __launch_bounds__(PRE_WAVES * 64, 2) void k_fa_pre(fa_args a) {
         {
             float x[4][4];
             float mloc = -INFINITY;
-            const bool tail = (c + 1) * PRE_CK > span;
 #pragma unroll
             for (int kt = 0; kt < 4; kt++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    x[kt][i] = MASKED ? fma_f16lo(mv[kt][i], LOG2E, s[kt][i]) : s[kt][i];
-                    if (tail && kin + 16 * kt + i >= span) x[kt][i] = -INFINITY;
-                    mloc = vmax(mloc, x[kt][i]);
-                }
+                for (int i = 0; i < 4; i++)
+                    x[kt][i] = !MASKED ? s[kt][i]
+                             : (i & 1) ? fma_f16hi(mv[kt][i >> 1], LOG2E, s[kt][i]) : fma_f16lo(mv[kt][i >> 1], LOG2E, s[kt][i]);
+            if (tail) {
+#pragma unroll
+                for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        if (kin + 16 * kt + i >= span) x[kt][i] = -INFINITY;
+            }
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) mloc = vmax(mloc, x[kt][i]);
             mloc = xmax_lanes16_32(mloc);
             const bool grow = mloc > m_run + RESCALE_SLACK;
             float alpha = 1.f;
@@ -2239,6 +2270,8 @@ __global__ __launch_bounds__(PRE_WAVES * 64, 2) void k_fa_pre(fa_args a) {
             for (int n = 0; n < 2 * NBLK; n++) {
                 const int cb = n & 1, h = n >> 3, bb = n & 7;
                 if (n + 1 < 2 * NBLK) load_step(n + 1, A[cb ^ 1], dvv[cb ^ 1]);
+                // the next step's reads are issued before this step's arithmetic
+                __builtin_amdgcn_sched_barrier(0);
                 uint32_t bh0[2], bl0[2], bh1[2], bl1[2];
                 {
                     const uint32_t dv[2] = {dvv[cb][0].x, dvv[cb][0].y};
@@ -2254,6 +2287,7 @@ __global__ __launch_bounds__(PRE_WAVES * 64, 2) void k_fa_pre(fa_args a) {
                 O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[cb][1], Bh, O[bb][1], 0, 0, 0);
                 O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[cb][0], Bl, O[bb][0], 0, 0, 0);
                 O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[cb][1], Bl, O[bb][1], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
     }
