@@ -345,6 +345,23 @@ __device__ __forceinline__ void dma16_buf(v4i rsrc, uint32_t off, uint32_t lds_b
                  :: "v"(off), "s"(rsrc), "s"(lds_base) : "memory");
 }
 
+// The same with the LDS destination lds_base + lds_off, lds_off an immediate:
+// M0 comes from one scalar add.
+template <uint32_t LDS_OFF>
+__device__ __forceinline__ void dma16_buf_at(v4i rsrc, uint32_t off, uint32_t lds_base) {
+    asm volatile("s_add_u32 m0, %2, %3\n\t"
+                 "s_nop 0\n\t"
+                 "buffer_load_dwordx4 %0, %1, 0 offen lds"
+                 :: "v"(off), "s"(rsrc), "s"(lds_base), "i"(LDS_OFF) : "memory");
+}
+
+// num_records of a buffer resource for `rem` bytes (at most 2^32 - 1).
+__device__ __forceinline__ uint32_t rsrc_bytes(int64_t rem) {
+    uint32_t hi = (uint32_t) ((uint64_t) rem >> 32);
+    asm("" : "+s"(hi));   // a 32-bit scalar test (the 64-bit compare it would fold into is a vector one)
+    return hi ? 0xffffffffu : (uint32_t) rem;
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const void * p) {
     return (uint32_t) (uintptr_t) (const __attribute__((address_space(3))) void *) p;
 }
@@ -1362,6 +1379,22 @@ __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
         voff[s] = key * (uint32_t) a.v_nb1 + part * 16u;
     }
     const int64_t k_bytes = k_hi * (int64_t) a.k_nb1, v_bytes = k_hi * (int64_t) a.v_nb1;
+    // LDS addresses of the wave's two stages, in 32-bit arithmetic from the
+    // ring's own address (casting a computed generic pointer tests it for null
+    // at every use)
+    const uint32_t stl0 = lds_addr(&ring[0][0][0]) + (uint32_t) wave * DEC_STAGE;
+    const uint32_t stl1 = stl0 + DEC_WAVES * DEC_STAGE;
+    // the wave's tiles kg, kg + KG, ... are issued in that order, each once:
+    // their K, V and mask resources start where the previous one's did plus
+    // a stride of KG tiles, and what is left of the split shrinks by as much
+    const int64_t key_first = k_lo + (int64_t) kg * DEC_TK;
+    const char * k_next = kbase + key_first * (int64_t) a.k_nb1;
+    const char * v_next = vbase + key_first * (int64_t) a.v_nb1;
+    const char * m_next = mslice_al + key_first * 2;
+    int64_t k_rem = k_bytes - key_first * (int64_t) a.k_nb1, v_rem = v_bytes - key_first * (int64_t) a.v_nb1;
+    int64_t m_rem = (int64_t) a.m_slice + (mslice - mslice_al) - key_first * 2;
+    const int64_t k_step = (int64_t) (KG * DEC_TK) * a.k_nb1, v_step = (int64_t) (KG * DEC_TK) * a.v_nb1;
+    constexpr int64_t m_step = KG * DEC_TK * 2;
     // GATHER: the DMA offsets of tile ti follow its cells (in LDS): piece p of
     // slot s is byte 16 (p % 17) of row gcell[16 ti + p / 17]; a cell outside
     // the cache, or a key past the split, gets an offset past the buffer, so
@@ -1379,58 +1412,58 @@ __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
     // two halves: the K rows (free once the tile's QK is done) and the V rows
     // with the mask granules (free once its PV is done). Keys past the split
     // arrive as zeros (buffer bounds) and are masked.
-    auto issue_k = [&](int ti, uint8_t * st) __attribute__((always_inline)) {
+    auto issue_k = [&](int ti, uint32_t stl) __attribute__((always_inline)) {
+        v4i rk;
+        uint32_t o[DEC_TDMA];
         if constexpr (GATHER) {
-            uint32_t go[DEC_TDMA];
 #pragma unroll
-            for (int s = 0; s < DEC_TDMA; s++) go[s] = gather_off(ti, s, (uint32_t) a.k_nb1);
-            const v4i rk = make_rsrc(kbase, g_kbytes);
-            __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the cells are read, this wave's reads of the stage are done
-#pragma unroll
-            for (int s = 0; s < DEC_TDMA; s++)
-                if (s < DEC_TDMA - 1 || lane < 16)
-                    dma16_buf(rk, go[s], __builtin_amdgcn_readfirstlane(lds_addr(st + 1024 * s)));
+            for (int s = 0; s < DEC_TDMA; s++) o[s] = gather_off(ti, s, (uint32_t) a.k_nb1);
+            rk = make_rsrc(kbase, g_kbytes);
         } else {
-            const int64_t key0 = k_lo + (int64_t) ti * DEC_TK;
-            const int64_t kc = key0 * (int64_t) a.k_nb1;
-            const v4i rk = make_rsrc(kbase + kc, (uint32_t) std::min<int64_t>(k_bytes - kc, 0xffffffffll));
-            __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's reads of the stage are done
 #pragma unroll
-            for (int s = 0; s < DEC_TDMA; s++)
-                if (s < DEC_TDMA - 1 || lane < 16)
-                    dma16_buf(rk, koff[s], __builtin_amdgcn_readfirstlane(lds_addr(st + 1024 * s)));
+            for (int s = 0; s < DEC_TDMA; s++) o[s] = koff[s];
+            rk = make_rsrc(k_next, rsrc_bytes(k_rem));
+            k_next += k_step;
+            k_rem -= k_step;
         }
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): (the cells are read and) this wave's reads of the stage are done
+        dma16_buf_at<0>(rk, o[0], stl);
+        dma16_buf_at<1024>(rk, o[1], stl);
+        dma16_buf_at<2048>(rk, o[2], stl);
+        dma16_buf_at<3072>(rk, o[3], stl);
+        static_assert(DEC_TDMA == 5, "five DMAs per tensor");
+        if (lane < 16) dma16_buf_at<4096>(rk, o[4], stl);
     };
-    auto issue_v = [&](int ti, uint8_t * st) __attribute__((always_inline)) {
-        const int64_t key0 = k_lo + (int64_t) ti * DEC_TK;
+    auto issue_v = [&](int ti, uint32_t stl) __attribute__((always_inline)) {
+        v4i rv;
+        uint32_t o[DEC_TDMA];
         if constexpr (GATHER) {
-            uint32_t go[DEC_TDMA];
 #pragma unroll
-            for (int s = 0; s < DEC_TDMA; s++) go[s] = gather_off(ti, s, (uint32_t) a.v_nb1);
-            const v4i rv = make_rsrc(vbase, g_vbytes);
-            __builtin_amdgcn_s_waitcnt(0xC07F);
-#pragma unroll
-            for (int s = 0; s < DEC_TDMA; s++)
-                if (s < DEC_TDMA - 1 || lane < 16)
-                    dma16_buf(rv, go[s], __builtin_amdgcn_readfirstlane(lds_addr(st + DEC_KB + 1024 * s)));
+            for (int s = 0; s < DEC_TDMA; s++) o[s] = gather_off(ti, s, (uint32_t) a.v_nb1);
+            rv = make_rsrc(vbase, g_vbytes);
         } else {
-            const int64_t vc = key0 * (int64_t) a.v_nb1;
-            const v4i rv = make_rsrc(vbase + vc, (uint32_t) std::min<int64_t>(v_bytes - vc, 0xffffffffll));
-            __builtin_amdgcn_s_waitcnt(0xC07F);
 #pragma unroll
-            for (int s = 0; s < DEC_TDMA; s++)
-                if (s < DEC_TDMA - 1 || lane < 16)
-                    dma16_buf(rv, voff[s], __builtin_amdgcn_readfirstlane(lds_addr(st + DEC_KB + 1024 * s)));
+            for (int s = 0; s < DEC_TDMA; s++) o[s] = voff[s];
+            rv = make_rsrc(v_next, rsrc_bytes(v_rem));
+            v_next += v_step;
+            v_rem -= v_step;
         }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        dma16_buf_at<DEC_KB>(rv, o[0], stl);
+        dma16_buf_at<DEC_KB + 1024>(rv, o[1], stl);
+        dma16_buf_at<DEC_KB + 2048>(rv, o[2], stl);
+        dma16_buf_at<DEC_KB + 3072>(rv, o[3], stl);
+        if (lane < 16) dma16_buf_at<DEC_KB + 4096>(rv, o[4], stl);
         if constexpr (MASKED) {
-            const v4i rm = make_rsrc(mslice_al + key0 * 2, (uint32_t) (a.m_slice + (uint32_t) (mslice - mslice_al) - key0 * 2));
-            if (lane < n_mrows * DEC_MGR)
-                dma16_buf(rm, m_goff, __builtin_amdgcn_readfirstlane(lds_addr(st + DEC_MOFF)));
+            const v4i rm = make_rsrc(m_next, (uint32_t) m_rem);
+            m_next += m_step;
+            m_rem -= m_step;
+            if (lane < n_mrows * DEC_MGR) dma16_buf_at<DEC_MOFF>(rm, m_goff, stl);
         }
     };
-    auto issue_tile = [&](int ti, uint8_t * st) __attribute__((always_inline)) {
-        issue_k(ti, st);
-        issue_v(ti, st);
+    auto issue_tile = [&](int ti, uint32_t stl) __attribute__((always_inline)) {
+        issue_k(ti, stl);
+        issue_v(ti, stl);
     };
 
     // ---- prologue: the block's query rows (f32, one wave DMA per row) into
@@ -1493,7 +1526,7 @@ __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
             __syncthreads();
         }
     }
-    if (first0 >= 0) issue_tile(first0, &ring[0][wave][0]);
+    if (first0 >= 0) issue_tile(first0, stl0);
     if (first0 >= 0) wait_vmcnt<OPS>();                 // the query DMAs have landed (the tile's may not)
     else wait_vmcnt<0>();
     __syncthreads();
@@ -1552,7 +1585,7 @@ __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
 #pragma unroll
     for (int bb = 0; bb < NBLK; bb++) asm volatile("" : "+v"(qw[bb]), "+v"(dq[bb]));
     __syncthreads();   // every wave has its operands: stage 1 is free
-    if (first1 >= 0) issue_tile(first1, &ring[1][wave][0]);
+    if (first1 >= 0) issue_tile(first1, stl1);
 
     // ---- the key loop ----
     v4f O[NBLK][2];
@@ -1565,7 +1598,7 @@ __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
 
     // tile ti from stage st; nx >= 0: tile nx goes into the same stage, its K
     // rows as soon as the QK is done, its V rows and mask after the PV
-    auto tile_step = [&](int ti, uint8_t * st, int nx) __attribute__((always_inline)) {
+    auto tile_step = [&](int ti, uint8_t * st, uint32_t stl, int nx) __attribute__((always_inline)) {
         const int kin = ti * DEC_TK + lg * 4;   // the lane's first key, within the split
         // the tile's block scales, transposed to [tensor][block][key]
         {
@@ -1606,7 +1639,7 @@ __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-        if (nx >= 0) issue_k(nx, st);
+        if (nx >= 0) issue_k(nx, stl);
         // ---- mask, online softmax (base 2) ----
         float p[4];
         uint32_t p16[2];
@@ -1694,7 +1727,7 @@ __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
             O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A1, Bl, O[bb][1], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
-        if (nx >= 0) issue_v(nx, st);
+        if (nx >= 0) issue_v(nx, stl);
     };
     // key group kg takes tiles kg, kg + KG, ... in that order (a fixed order:
     // the result is reproducible bit for bit); the two stages alternate. The
@@ -1704,11 +1737,11 @@ __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
         const int t0 = kg + j * KG, t1 = t0 + KG, t2 = t1 + KG, t3 = t2 + KG;
         if (t1 < n_tiles) wait_vmcnt<OPS>();
         else wait_vmcnt<0>();
-        tile_step(t0, &ring[0][wave][0], t2 < n_tiles ? t2 : -1);
+        tile_step(t0, &ring[0][wave][0], stl0, t2 < n_tiles ? t2 : -1);
         if (t1 < n_tiles) {
             if (t2 < n_tiles) wait_vmcnt<OPS>();
             else wait_vmcnt<0>();
-            tile_step(t1, &ring[1][wave][0], t3 < n_tiles ? t3 : -1);
+            tile_step(t1, &ring[1][wave][0], stl1, t3 < n_tiles ? t3 : -1);
         }
     }
 
