@@ -2220,6 +2220,7 @@ __global__ __launch_bounds__(PRE_WAVES * 64, 2) void k_fa_pre(fa_args a) {
 #pragma unroll
             for (int kt = 0; kt < 4; kt++) {
                 const int cb = kt & 1;
+                if (cb) __builtin_amdgcn_s_setprio(0); else __builtin_amdgcn_s_setprio(1);
                 if (kt + 1 < 4) load_tile(kt + 1, kA[cb ^ 1], dk[cb ^ 1]);
                 v4i cc[NBLK];
                 cc[0] = __builtin_amdgcn_mfma_i32_16x16x32_i8(kA[cb][0], qw[0], v4i{0, 0, 0, 0}, 0, 0, 0);
@@ -2310,6 +2311,7 @@ __global__ __launch_bounds__(PRE_WAVES * 64, 2) void k_fa_pre(fa_args a) {
 #pragma unroll
             for (int n = 0; n < 2 * NBLK; n++) {
                 const int cb = n & 1, h = n >> 3, bb = n & 7;
+                if (cb) __builtin_amdgcn_s_setprio(0); else __builtin_amdgcn_s_setprio(1);
                 if (n + 1 < 2 * NBLK) load_step(n + 1, A[cb ^ 1], dvv[cb ^ 1]);
                 // the next step's reads are issued before this step's arithmetic
                 __builtin_amdgcn_sched_barrier(0);
@@ -2330,6 +2332,7 @@ __global__ __launch_bounds__(PRE_WAVES * 64, 2) void k_fa_pre(fa_args a) {
                 O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[cb][1], Bl, O[bb][1], 0, 0, 0);
                 __builtin_amdgcn_sched_barrier(0);
             }
+            __builtin_amdgcn_s_setprio(0);
         }
     }
 
