@@ -74,10 +74,12 @@ int launch_gather(gather_args a, size_t seg_bytes, int32_t n_seg, hipStream_t st
     if (units >= (uint64_t(1) << 31))
         return set_error(QWFN_ENOTSUP, "gather: rows of 8 GiB or more are not supported");
     if (n_seg > 65535) return set_error(QWFN_ENOTSUP, "gather: at most 65535 segments");
-    // about 1024 workgroups over the whole copy, each at least one unit per lane
-    // and at most 4096 units (several rows when rows are short)
-    const uint64_t total = (uint64_t) n_seg * (uint64_t) a.n_idx * units;
-    const uint64_t per_wg = std::min<uint64_t>(4096, std::max<uint64_t>(COPY_THREADS, total / 1024));
+    // one unit per lane (whole rows per workgroup when rows are short): a
+    // lane's copy is one index load, one data load and one store, so the
+    // workgroups' loads are all in flight at once (several units per lane
+    // chain them: 4.24 us against 3.64 us in the kernel for the 64K gather of
+    // K and V)
+    const uint64_t per_wg = COPY_THREADS;
     const uint64_t rows = std::max<uint64_t>(1, std::min<uint64_t>(per_wg / units, (uint64_t) a.n_idx));
     const uint64_t gx = ((uint64_t) a.n_idx + rows - 1) / rows;
     if (gx >= (uint64_t(1) << 31)) return set_error(QWFN_ENOTSUP, "gather: too many index rows");
