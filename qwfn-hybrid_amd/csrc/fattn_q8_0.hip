@@ -1733,21 +1733,23 @@ __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
     // the result is reproducible bit for bit); the two stages alternate. The
     // DMAs of the tile after next follow each tile (its K half mid-step), so
     // the ones issued after a tile's own are exactly the next tile's.
-    // Two waves share a SIMD and the older one wins its issue slots, so it
-    // would finish its tiles long before the other, which then runs alone at
-    // half the vector rate: a wave takes the higher priority for its
-    // even-numbered tiles and drops it for its odd ones, so the wave that
-    // falls a tile behind is the one served first.
+    // Two waves share a SIMD (waves w and w + 4) and the older one wins its
+    // issue slots, so it would finish its tiles long before the other, which
+    // then runs alone at half the vector rate: the wave priority alternates
+    // with the tile count, in opposite phase for the two waves of a SIMD, so
+    // that on the same tile the two take turns and a wave that falls a tile
+    // behind is served first.
+    const bool young = wave >= DEC_WAVES / 2;
     for (int j = 0; kg + j * KG < n_tiles; j += 2) {
         const int t0 = kg + j * KG, t1 = t0 + KG, t2 = t1 + KG, t3 = t2 + KG;
         if (t1 < n_tiles) wait_vmcnt<OPS>();
         else wait_vmcnt<0>();
-        __builtin_amdgcn_s_setprio(1);
+        if (young) __builtin_amdgcn_s_setprio(0); else __builtin_amdgcn_s_setprio(1);
         tile_step(t0, &ring[0][wave][0], stl0, t2 < n_tiles ? t2 : -1);
         if (t1 < n_tiles) {
             if (t2 < n_tiles) wait_vmcnt<OPS>();
             else wait_vmcnt<0>();
-            __builtin_amdgcn_s_setprio(0);
+            if (young) __builtin_amdgcn_s_setprio(1); else __builtin_amdgcn_s_setprio(0);
             tile_step(t1, &ring[1][wave][0], stl1, t3 < n_tiles ? t3 : -1);
         }
     }
