@@ -85,6 +85,24 @@ def test_prefill_general_mask(gpu, oracle):
     assert not got[17].any()
 
 
+def test_prefill_odd_mask_rows(gpu, oracle):
+    """An odd key count: the unpadded mask's rows start 2 bytes into a word on
+    every other row (the kernel reads them as f16 pairs), and the split's last
+    chunk holds a single key."""
+    K = gpu
+    T, n_kv, nh = 40, 1473, 16
+    kc, vc = layer(47, n_kv)
+    q = KD.q_rows(47, 0, T, nh)[0]
+    rng = np.random.default_rng(47)
+    m = rng.uniform(-5, 1, (T, n_kv)).astype(np.float16).view(np.uint16)
+    m[:, 3::5] = O.F16_NEG_INF
+    m[5, :] = O.F16_NEG_INF
+    say("k_fa_pre odd mask rows n_kv=1473")
+    got = gpu_attn(K, q, kc, vc, n_kv, 2, m, 1 / 16)
+    check(got, KD.oracle_attn(q, kc, vc, n_kv, 2, m, 1 / 16))
+    assert not got[5].any()
+
+
 def test_prefill_split_invariance(gpu, oracle):
     """The same call with 1, 2, 5 and 13 key splits agrees with the oracle and across splits."""
     K = gpu
