@@ -2296,42 +2296,60 @@ __global__ __launch_bounds__(PRE_WAVES * 64, 2) void k_fa_pre(fa_args a) {
 
         // ---- O += V^T (P d_v): per half of 32 keys (key tiles 2h, 2h + 1) and V
         //      block, A = V^T rows 32bb + 16e + ln at the lane group's 8
-        //      positions, B = the same 8 keys' P d_v as f16 hi + lo; step n + 1's
-        //      operands are read while step n is computed ----
+        //      positions, B = the same 8 keys' P d_v as f16 hi + lo. A step's
+        //      lo MFMAs accumulate into what its hi MFMAs just wrote, and an
+        //      MFMA whose accumulator was written a few MFMAs before stalls for
+        //      the result: the next step's B operands are formed between the
+        //      two pairs. Step n + 1's V^T and step n + 2's d_v are read while
+        //      step n is computed ----
         {
             v8h A[2][2];
-            uint2 dvv[2][2];
-            auto load_step = [&](int n, v8h (&aa)[2], uint2 (&dd)[2]) __attribute__((always_inline)) {
+            uint2 dvv[3][2];
+            v8h Bh[2], Bl[2];
+            auto load_a = [&](int n, v8h (&aa)[2]) __attribute__((always_inline)) {
                 const int h = n >> 3, bb = n & 7;
                 const uint8_t * va = vt + (32 * bb + ln) * PRE_VTS + (32 * h + 8 * lg) * 2;
                 aa[0] = *(const v8h *) va;
                 aa[1] = *(const v8h *) (va + 16 * PRE_VTS);
+            };
+            auto load_dv = [&](int n, uint2 (&dd)[2]) __attribute__((always_inline)) {
+                const int h = n >> 3, bb = n & 7;
                 dd[0] = *(const uint2 *) &skv[1][bb][32 * h + 4 * lg];
                 dd[1] = *(const uint2 *) &skv[1][bb][32 * h + 16 + 4 * lg];
             };
-            load_step(0, A[0], dvv[0]);
-#pragma unroll
-            for (int n = 0; n < 2 * NBLK; n++) {
-                const int cb = n & 1, h = n >> 3, bb = n & 7;
-                if (cb) __builtin_amdgcn_s_setprio(0); else __builtin_amdgcn_s_setprio(1);
-                if (n + 1 < 2 * NBLK) load_step(n + 1, A[cb ^ 1], dvv[cb ^ 1]);
-                // the next step's reads are issued before this step's arithmetic
-                __builtin_amdgcn_sched_barrier(0);
+            auto form_b = [&](int n, const uint2 (&dd)[2], v8h & bh, v8h & bl) __attribute__((always_inline)) {
+                const int h = n >> 3;
                 uint32_t bh0[2], bl0[2], bh1[2], bl1[2];
                 {
-                    const uint32_t dv[2] = {dvv[cb][0].x, dvv[cb][0].y};
+                    const uint32_t dv[2] = {dd[0].x, dd[0].y};
                     pdv_hilo(p[2 * h], p16[2 * h], dv, bh0, bl0);
                 }
                 {
-                    const uint32_t dv[2] = {dvv[cb][1].x, dvv[cb][1].y};
+                    const uint32_t dv[2] = {dd[1].x, dd[1].y};
                     pdv_hilo(p[2 * h + 1], p16[2 * h + 1], dv, bh1, bl1);
                 }
-                const v8h Bh = __builtin_bit_cast(v8h, make_uint4(bh0[0], bh0[1], bh1[0], bh1[1]));
-                const v8h Bl = __builtin_bit_cast(v8h, make_uint4(bl0[0], bl0[1], bl1[0], bl1[1]));
-                O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[cb][0], Bh, O[bb][0], 0, 0, 0);
-                O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[cb][1], Bh, O[bb][1], 0, 0, 0);
-                O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[cb][0], Bl, O[bb][0], 0, 0, 0);
-                O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[cb][1], Bl, O[bb][1], 0, 0, 0);
+                bh = __builtin_bit_cast(v8h, make_uint4(bh0[0], bh0[1], bh1[0], bh1[1]));
+                bl = __builtin_bit_cast(v8h, make_uint4(bl0[0], bl0[1], bl1[0], bl1[1]));
+            };
+            load_a(0, A[0]);
+            load_dv(0, dvv[0]);
+            load_dv(1, dvv[1]);
+            form_b(0, dvv[0], Bh[0], Bl[0]);
+#pragma unroll
+            for (int n = 0; n < 2 * NBLK; n++) {
+                const int cb = n & 1, bb = n & 7;
+                if (cb) __builtin_amdgcn_s_setprio(0); else __builtin_amdgcn_s_setprio(1);
+                if (n + 1 < 2 * NBLK) load_a(n + 1, A[cb ^ 1]);
+                if (n + 2 < 2 * NBLK) load_dv(n + 2, dvv[(n + 2) % 3]);
+                // the next reads are issued before this step's arithmetic
+                __builtin_amdgcn_sched_barrier(0);
+                O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[cb][0], Bh[cb], O[bb][0], 0, 0, 0);
+                O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[cb][1], Bh[cb], O[bb][1], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (n + 1 < 2 * NBLK) form_b(n + 1, dvv[(n + 1) % 3], Bh[cb ^ 1], Bl[cb ^ 1]);
+                __builtin_amdgcn_sched_barrier(0);
+                O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[cb][0], Bl[cb], O[bb][0], 0, 0, 0);
+                O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[cb][1], Bl[cb], O[bb][1], 0, 0, 0);
                 __builtin_amdgcn_sched_barrier(0);
             }
             __builtin_amdgcn_s_setprio(0);
