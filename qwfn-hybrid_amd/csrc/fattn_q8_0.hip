@@ -339,20 +339,21 @@ __device__ __forceinline__ v4i make_rsrc(const void * base, uint32_t bytes) {
 // are, so the explicit counts are exact.
 __device__ __forceinline__ void dma16_buf(v4i rsrc, uint32_t off, uint32_t lds_base) {
     // an LDS DMA reads M0 one wait state after the SALU write at the earliest
+    // the asm writes M0 only: no instruction in it touches SCC, so the compiler
+    // may keep a carry or a branch condition live across it
     asm volatile("s_mov_b32 m0, %2\n\t"
                  "s_nop 0\n\t"
                  "buffer_load_dwordx4 %0, %1, 0 offen lds"
-                 :: "v"(off), "s"(rsrc), "s"(lds_base) : "memory");
+                 :: "v"(off), "s"(rsrc), "s"(lds_base) : "memory", "m0");
 }
 
-// The same with the LDS destination lds_base + lds_off, lds_off an immediate:
-// M0 comes from one scalar add.
+// The same with the LDS destination lds_base + lds_off, lds_off a constant.
+// The addition is the compiler's: a scalar add in the asm would overwrite SCC,
+// which the compiler may hold across the asm (the carry of a 64-bit pointer
+// increment split around it), and a lost carry moves a buffer base by 4 GiB.
 template <uint32_t LDS_OFF>
 __device__ __forceinline__ void dma16_buf_at(v4i rsrc, uint32_t off, uint32_t lds_base) {
-    asm volatile("s_add_u32 m0, %2, %3\n\t"
-                 "s_nop 0\n\t"
-                 "buffer_load_dwordx4 %0, %1, 0 offen lds"
-                 :: "v"(off), "s"(rsrc), "s"(lds_base), "i"(LDS_OFF) : "memory");
+    dma16_buf(rsrc, off, lds_base + LDS_OFF);
 }
 
 // num_records of a buffer resource for `rem` bytes (at most 2^32 - 1).
