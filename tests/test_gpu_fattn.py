@@ -71,6 +71,47 @@ def test_verify_causal(gpu, oracle, n_past, outliers):
     check(got, ref)
 
 
+@pytest.mark.parametrize("crossing", ["k", "v"])
+def test_cache_across_4gib_boundary(gpu, oracle, crossing):
+    """Verify at depth 16384 with the K (or V) cache placed across a 4 GiB address
+    boundary inside one allocation: the DMA resources of the tiles past the
+    boundary carry into the high half of their 64-bit base."""
+    K = gpu
+    import torch
+    T, n_past = 3, 16384
+    n_kv = n_past + T
+    kc, vc = layer(5, n_kv)
+    q = KD.q_rows(5, 0, T, 16)[0]
+    mask = O.causal_mask(T, n_past)
+    rb = kc.shape[1]
+    nbytes = n_kv * rb
+    buf = torch.empty((5 << 30) + 2 * nbytes + 4096, dtype=torch.uint8, device="cuda")
+    base = buf.data_ptr()
+    boundary = ((base >> 32) + 1) << 32
+    if boundary - base < nbytes:
+        boundary += 1 << 32
+    # the crossing cache has half its rows below the boundary (rows start on
+    # 256-byte boundaries); the other cache follows it
+    cross_off = (boundary - base - nbytes // 2) // 256 * 256
+    assert 0 < cross_off < boundary - base < cross_off + nbytes
+    other_off = (cross_off + nbytes + 255) // 256 * 256
+    assert other_off + nbytes <= buf.numel()
+    k_off, v_off = (cross_off, other_off) if crossing == "k" else (other_off, cross_off)
+    kd = buf[k_off:k_off + nbytes].view(n_kv, rb)
+    vd = buf[v_off:v_off + nbytes].view(n_kv, rb)
+    kd.copy_(torch.from_numpy(kc))
+    vd.copy_(torch.from_numpy(vc))
+    qd = dev(q[None].astype(np.float32))
+    md = dev(mask.view(np.float16))
+    out = torch.full((1, T, 16, 256), float("nan"), dtype=torch.float32, device="cuda")
+    say(f"verify T=3 n_past={n_past} with the {crossing.upper()} cache across a 4 GiB boundary")
+    K.flash_attn_ext(K.q_view(qd), K.cache_attn_view(kd, n_kv, 2), K.cache_attn_view(vd, n_kv, 2), K.mask_view(md),
+                     1 / 16, K.out_view(out))
+    got = host(out)[0]
+    del buf, kd, vd
+    check(got, KD.oracle_attn(q, kc, vc, n_kv, 2, mask, 1 / 16))
+
+
 @pytest.mark.parametrize("n_kv", [1, 2, 33, 130])
 def test_few_keys_with_outliers(gpu, oracle, n_kv):
     """Worst case for the f16 P*d_v rounding: a handful of keys dominate and the
