@@ -339,12 +339,13 @@ __device__ __forceinline__ v4i make_rsrc(const void * base, uint32_t bytes) {
 // are, so the explicit counts are exact.
 __device__ __forceinline__ void dma16_buf(v4i rsrc, uint32_t off, uint32_t lds_base) {
     // an LDS DMA reads M0 one wait state after the SALU write at the earliest
-    // the asm writes M0 only: no instruction in it touches SCC, so the compiler
-    // may keep a carry or a branch condition live across it
+    // The asm writes M0 only (a reserved register that the compiler uses for
+    // nothing else in these kernels): no instruction in it touches SCC, so the
+    // compiler may keep a carry or a branch condition live across it.
     asm volatile("s_mov_b32 m0, %2\n\t"
                  "s_nop 0\n\t"
                  "buffer_load_dwordx4 %0, %1, 0 offen lds"
-                 :: "v"(off), "s"(rsrc), "s"(lds_base) : "memory", "m0");
+                 :: "v"(off), "s"(rsrc), "s"(lds_base) : "memory");
 }
 
 // The same with the LDS destination lds_base + lds_off, lds_off a constant.
