@@ -57,15 +57,17 @@ int launch_zero(void * p, size_t bytes, hipStream_t stream) {
 
 // Causal mask: thread = (row, group of 8 keys). A group wholly inside the row
 // and 16-byte aligned is one store, otherwise 2-byte stores.
-__global__ __launch_bounds__(FILL_THREADS) void k_causal_mask(char * mask, int64_t n_kv, int64_t T, int64_t n_past,
-                                                             size_t row_stride, int64_t groups_per_row) {
-    const int64_t total = T * groups_per_row;
+// Row i0 + blockIdx.y (query i), 16-byte groups blockIdx.x * FILL_THREADS + tid
+// and on in steps of the grid: a 2-D grid, so no 64-bit division splits a flat
+// index.
+__global__ __launch_bounds__(FILL_THREADS) void k_causal_mask(char * mask, int64_t n_kv, int64_t n_past, size_t row_stride,
+                                                             int64_t groups_per_row, int64_t i0) {
+    const int64_t i = i0 + blockIdx.y;
     const int64_t row_elems = (int64_t) (row_stride / 2);
-    for (int64_t u = (int64_t) blockIdx.x * FILL_THREADS + threadIdx.x; u < total; u += (int64_t) gridDim.x * FILL_THREADS) {
-        const int64_t i = u / groups_per_row;
-        const int64_t j0 = (u - i * groups_per_row) * 8;
-        const int64_t vis = n_past + i;   // last visible key
-        uint16_t * row = (uint16_t *) (mask + (size_t) i * row_stride);
+    const int64_t vis = n_past + i;   // last visible key
+    uint16_t * row = (uint16_t *) (mask + (size_t) i * row_stride);
+    for (int64_t g = (int64_t) blockIdx.x * FILL_THREADS + threadIdx.x; g < groups_per_row; g += (int64_t) gridDim.x * FILL_THREADS) {
+        const int64_t j0 = g * 8;
         uint16_t v[8];
 #pragma unroll
         for (int e = 0; e < 8; e++) {
@@ -610,10 +612,13 @@ int qwfn_causal_mask_f16(uint16_t * mask, int64_t n_kv, int64_t T, int64_t n_pas
         if (row_stride % 2 || row_stride < (size_t) n_kv * 2 || !is_aligned(mask, 2))
             return set_error(QWFN_EALIGN, "causal_mask: row_stride must be even and hold n_kv keys");
         const int64_t groups = (int64_t) ((row_stride / 2 + 7) / 8);
-        const int64_t total = T * groups;
-        if (total == 0) return QWFN_OK;
-        hipLaunchKernelGGL(k_causal_mask, dim3(grid_for(total)), dim3(FILL_THREADS), 0, as_stream(stream), (char *) mask, n_kv, T,
-                           n_past, row_stride, groups);
+        if (T == 0 || groups == 0) return QWFN_OK;
+        const int64_t gx = std::min<int64_t>((groups + FILL_THREADS - 1) / FILL_THREADS, 1024);
+        for (int64_t i0 = 0; i0 < T; i0 += 65535) {   // grid rows: at most 65535 a launch
+            const int64_t nr = std::min<int64_t>(T - i0, 65535);
+            hipLaunchKernelGGL(k_causal_mask, dim3((unsigned) gx, (unsigned) nr), dim3(FILL_THREADS), 0, as_stream(stream),
+                               (char *) mask, n_kv, n_past, row_stride, groups, i0);
+        }
         return hip_check(hipGetLastError(), "causal_mask launch");
     });
 }

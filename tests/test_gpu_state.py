@@ -264,7 +264,8 @@ def test_state_caches_feed_attention(gpu):
 
 
 @pytest.mark.parametrize("n_kv,T,n_past,row", [(19, 3, 16, 19), (1027, 5, 1022, 1088), (4608, 512, 4096, 4608),
-                                               (16387, 3, 16384, 16387), (8, 1, 7, 8), (40, 2, 0, 64)])
+                                               (16387, 3, 16384, 16387), (8, 1, 7, 8), (40, 2, 0, 64),
+                                               (8, 65540, 0, 8)])
 def test_causal_mask_matches_oracle(gpu, n_kv, T, n_past, row):
     import torch
     m = torch.full((T, row), 0x1234, dtype=torch.int16, device="cuda")
