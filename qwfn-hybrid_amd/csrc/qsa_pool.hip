@@ -129,6 +129,88 @@ __global__ __launch_bounds__(POOL_WAVES * 64) void k_qsa_pool(pool_args a) {
     for (int d = a.rp.n_dims + lane; d < dim; d += 64) out[d] = f2h(x[d]);
 }
 
+// The rebuild with 16-byte lanes, for dim / 8 a power of two and 16-byte
+// aligned caches: a lane holds 8 dims of one block, summed over the block's r
+// member rows in member order, and a wave holds 64 / (dim / 8) blocks (4 at
+// dim 128). The normalised keys pass through LDS so that the rotation takes
+// one (block, pair) per lane: the wave's fp64 sin / cos work is shared by all
+// of its blocks (2 blocks per pass at n_dims 64) instead of one block leaving
+// half the lanes idle. Per value the arithmetic is k_qsa_pool's.
+constexpr int RB_WAVES = 4;
+
+__global__ __launch_bounds__(RB_WAVES * 64) void k_qsa_pool_rebuild(pool_args a) {
+    __shared__ __align__(16) float xs[RB_WAVES][512];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int dim = a.dim, lpb = dim >> 3, bpw = 64 / lpb;
+    const int lb = lane / lpb, lj = lane % lpb;
+    const int64_t blk0 = ((int64_t) blockIdx.x * RB_WAVES + wv) * bpw;
+    if (blk0 >= a.n_blk) return;   // wave-uniform
+    const int64_t blk = blk0 + lb;
+    const bool live = blk < a.n_blk;
+    float x[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) x[i] = 0.f;
+    if (live) {
+        const uint16_t * src = a.ic + (size_t) blk * (size_t) a.r * (size_t) dim + 8 * lj;
+#pragma unroll 4
+        for (int m = 0; m < a.r; m++) {
+            const uint4 u = *(const uint4 *) (src + (size_t) m * dim);
+            const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float v = h2f((uint16_t) (w4[i >> 1] >> (16 * (i & 1))));
+                x[i] = m == 0 ? v : __fadd_rn(x[i], v);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) x[i] = __fmul_rn(x[i], a.inv_r);
+    }
+    // RMS norm over the block's lpb lanes: the squares (float) summed in double
+    double sq = 0.0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) sq += (double) __fmul_rn(x[i], x[i]);
+    for (int off = lpb >> 1; off >= 1; off >>= 1) sq += __shfl_xor(sq, off);
+    const float mean = (float) (sq / (double) dim);
+    const float scale = 1.0f / sqrtf(__fadd_rn(mean, a.eps));
+    float * xw = xs[wv] + lb * dim + 8 * lj;
+#pragma unroll
+    for (int i = 0; i < 8; i++) x[i] = __fmul_rn(__fmul_rn(x[i], scale), a.w[8 * lj + i]);
+    *(float4 *) xw = make_float4(x[0], x[1], x[2], x[3]);
+    *(float4 *) (xw + 4) = make_float4(x[4], x[5], x[6], x[7]);
+    // the dims past the rotated ones go out from registers
+    if (live) {
+        uint16_t * out = a.pool + (size_t) blk * dim + 8 * lj;
+        if (8 * lj >= a.rp.n_dims) {
+            uint32_t o[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) o[i] = (uint32_t) f2h(x[2 * i]) | ((uint32_t) f2h(x[2 * i + 1]) << 16);
+            *(uint4 *) out = make_uint4(o[0], o[1], o[2], o[3]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                if (8 * lj + i >= a.rp.n_dims) out[i] = f2h(x[i]);
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    // rotation: lane -> (block, pair), the wave's blocks in turn
+    const int half = a.rp.n_dims / 2;
+    for (int idx = lane; idx < bpw * half; idx += 64) {
+        const int b = idx / half, k = idx - b * half;
+        const int64_t bk = blk0 + b;
+        if (bk >= a.n_blk) break;   // idx only grows: every later pair is past the end too
+        const int32_t p = (int32_t) (bk * a.r);
+        const int32_t pos[4] = {p, p, p, p};
+        float c, s, y0, y1;
+        rope_cos_sin(a.rp, pos, k, &c, &s);
+        const float * xb = xs[wv] + b * dim;
+        rope_rotate(xb[k], xb[k + half], c, s, &y0, &y1);
+        uint16_t * out = a.pool + (size_t) bk * dim;
+        out[k] = f2h(y0);
+        out[k + half] = f2h(y1);
+    }
+}
+
 // ggml_set_rows F32 -> F16: row idx[i] of dst = fp16(row i of src)
 struct f16_rows_args {
     uint16_t *      dst;
@@ -264,6 +346,13 @@ extern "C" int qwfn_qsa_pool_rebuild(const uint16_t * idx_cache, int64_t ic_rows
         a.ic = const_cast<uint16_t *>(idx_cache); a.ic_rows = ic_rows; a.pool = pool; a.pool_rows = pool_rows;
         a.n_blk = n_whole;
         if (int rc = status_word(&a.status)) return rc;
+        const int lpb = a.dim / 8;
+        if (a.dim % 8 == 0 && (lpb & (lpb - 1)) == 0 && is_aligned(idx_cache, 16) && is_aligned(pool, 16)) {
+            const int64_t waves = (n_whole + 64 / lpb - 1) / (64 / lpb);
+            const int64_t grid = (waves + RB_WAVES - 1) / RB_WAVES;
+            hipLaunchKernelGGL(k_qsa_pool_rebuild, dim3((unsigned) grid), dim3(RB_WAVES * 64), 0, as_stream(stream), a);
+            return hip_check(hipGetLastError(), "qsa_pool_rebuild launch");
+        }
         const int64_t grid = (n_whole + POOL_WAVES - 1) / POOL_WAVES;
         hipLaunchKernelGGL(k_qsa_pool<false>, dim3((unsigned) grid), dim3(POOL_WAVES * 64), 0, as_stream(stream), a);
         return hip_check(hipGetLastError(), "qsa_pool_rebuild launch");
