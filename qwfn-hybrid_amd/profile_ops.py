@@ -25,7 +25,7 @@ ROW = 544
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("op", choices=["verify", "prefill", "cells", "append", "gather", "restore", "produce", "deltanet",
-                                   "pool", "copy"])
+                                   "pool", "select", "copy"])
     ap.add_argument("--depth", type=int, default=16384)
     ap.add_argument("--T", type=int, default=3)
     ap.add_argument("--reps", type=int, default=10)
@@ -140,6 +140,18 @@ def main() -> int:
         snap = torch.empty((max(1, n_snap), 48, 128, 128), dtype=torch.float32, device=dev)
         run = lambda i: K.gated_delta_net(conv[:, :2048], conv[:, 2048:4096], conv[:, 4096:], g, beta,
                                           states[i % a.sets], out, 16, snap if n_snap else None, n_snap)
+    elif a.op == "select":
+        # the decode step's block selection for a 3-position verify step at 73728
+        # positions: 18432 pooled f16 keys, 4 indexer heads, top 513 blocks of 4 cells
+        import qwfn_state as S
+        nb, kb = 73728 // 4, 513
+        pool = (torch.randn((nb, 128), generator=gen, device=dev) * 0.5).to(torch.float16)
+        qsel = torch.randn((3, 4, 128), generator=gen, device=dev)
+        bsel = torch.zeros((3, nb), dtype=torch.float32, device=dev)
+        bcells = torch.arange(nb * 4, dtype=torch.int32, device=dev)
+        csel = torch.empty((3, kb * 4), dtype=torch.int32, device=dev)
+        wsel = torch.empty(K.load().qwfn_qsa_select_workspace_size(nb, 3), dtype=torch.uint8, device=dev)
+        run = lambda i: S.qsa_select_cells(pool, qsel, bsel, kb, bcells, 4, csel, ws=wsel)
     else:  # pool: rebuild after a prefill of `depth` positions, ratio 4
         ic = torch.randn((a.depth + 64, 128), generator=gen, device=dev).to(torch.float16)
         pool = torch.zeros((a.depth // 4 + 16, 128), dtype=torch.float16, device=dev)
