@@ -64,9 +64,70 @@ struct kvp_args {
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float) __builtin_bit_cast(_Float16, h); }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// x + the value of the lane that a permlane16 / permlane32 swap brings
+template <bool P32>
+__device__ __forceinline__ float swap_add(float x) {
+    const unsigned u = __builtin_bit_cast(unsigned, x);
+    const auto r = P32 ? __builtin_amdgcn_permlane32_swap(u, u, false, false) : __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    unsigned p = r[0], q = r[1];
+    asm volatile("" : "+v"(p), "+v"(q));
+    return __builtin_bit_cast(float, p) + __builtin_bit_cast(float, q);
+}
+
+// sum over the wave, in every lane: within each row of 16 (quad swaps, the
+// mirrored half-row, the mirrored row), then across rows (permlane swaps)
 __device__ __forceinline__ float wave_sum(float x) {
-    for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
-    return x;
+    x += dpp_f<0xB1>(x);    // quad_perm [1,0,3,2]
+    x += dpp_f<0x4E>(x);    // quad_perm [2,3,0,1]
+    x += dpp_f<0x141>(x);   // row_half_mirror
+    x += dpp_f<0x140>(x);   // row_mirror
+    x = swap_add<false>(x);
+    return swap_add<true>(x);
+}
+
+// c + a * b for the low (or high) f16 halves of a and b, in f32 with one
+// rounding: f16 values are exact in f32, so this is fmaf(float(a), float(b), c)
+__device__ __forceinline__ float fma_mix_lo(uint32_t a, uint32_t b, float c) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,0,0] op_sel_hi:[1,1,0]" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+__device__ __forceinline__ float fma_mix_hi(uint32_t a, uint32_t b, float c) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,1,0] op_sel_hi:[1,1,0]" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
+// the same for a double: both halves move with the same pattern
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t) __builtin_amdgcn_update_dpp(0, (int) (uint32_t) u, CTRL, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t) __builtin_amdgcn_update_dpp(0, (int) (uint32_t) (u >> 32), CTRL, 0xF, 0xF, false);
+    return __builtin_bit_cast(double, ((uint64_t) hi << 32) | lo);
+}
+template <bool P32>
+__device__ __forceinline__ double swap_add_d(double x) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, x);
+    const unsigned lo = (unsigned) u, hi = (unsigned) (u >> 32);
+    const auto rl = P32 ? __builtin_amdgcn_permlane32_swap(lo, lo, false, false) : __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const auto rh = P32 ? __builtin_amdgcn_permlane32_swap(hi, hi, false, false) : __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    unsigned l0 = rl[0], l1 = rl[1], h0 = rh[0], h1 = rh[1];
+    asm volatile("" : "+v"(l0), "+v"(l1), "+v"(h0), "+v"(h1));
+    return __builtin_bit_cast(double, ((uint64_t) h0 << 32) | l0) + __builtin_bit_cast(double, ((uint64_t) h1 << 32) | l1);
+}
+__device__ __forceinline__ double wave_sum_d(double x) {
+    x += dpp_d<0xB1>(x);
+    x += dpp_d<0x4E>(x);
+    x += dpp_d<0x141>(x);
+    x += dpp_d<0x140>(x);
+    x = swap_add_d<false>(x);
+    return swap_add_d<true>(x);
 }
 
 __global__ __launch_bounds__(KVP_WAVES * 64) void k_kv_project(kvp_args a) {
@@ -88,15 +149,16 @@ __global__ __launch_bounds__(KVP_WAVES * 64) void k_kv_project(kvp_args a) {
         if (512 * j < E) wq[j] = *(const uint4 *) (wrow + (512 * j + 8 * lane < E ? 512 * j + 8 * lane : 0));
 
     // ---- the hidden rows, F32 -> F16 (ggml's conversion of src1): 4 values a
-    //      lane, 4 loads in flight before any conversion ----
+    //      lane, 8 loads in flight before any conversion (one round for up to
+    //      8192 values) ----
     {
         const int n4 = T * E / 4;
         const uint32_t e4_mul = (uint32_t) (((uint64_t(1) << 32) + (uint64_t) (E / 4) - 1) / (uint64_t) (E / 4));
-        for (int i0 = threadIdx.x; i0 < n4; i0 += KVP_WAVES * 64 * 4) {
-            float4 x[4];
-            int idx[4];
+        for (int i0 = threadIdx.x; i0 < n4; i0 += KVP_WAVES * 64 * 8) {
+            float4 x[8];
+            int idx[8];
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
+            for (int u = 0; u < 8; u++) {
                 const int i = i0 + KVP_WAVES * 64 * u;
                 const int ii = i < n4 ? i : n4 - 1;
                 const int t = E / 4 == 1 ? ii : (int) __umulhi((uint32_t) ii, e4_mul);
@@ -105,7 +167,7 @@ __global__ __launch_bounds__(KVP_WAVES * 64) void k_kv_project(kvp_args a) {
                 idx[u] = i < n4 ? 4 * i : -1;
             }
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
+            for (int u = 0; u < 8; u++) {
                 if (idx[u] < 0) continue;
                 const uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16) x[u].x) |
                                     ((uint32_t) __builtin_bit_cast(uint16_t, (_Float16) x[u].y) << 16);
@@ -134,8 +196,8 @@ __global__ __launch_bounds__(KVP_WAVES * 64) void k_kv_project(kvp_args a) {
             float s = acc[t];
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                s = __fmaf_rn(h2f((uint16_t) ww[q]), h2f((uint16_t) cw[q]), s);
-                s = __fmaf_rn(h2f((uint16_t) (ww[q] >> 16)), h2f((uint16_t) (cw[q] >> 16)), s);
+                s = fma_mix_lo(ww[q], cw[q], s);
+                s = fma_mix_hi(ww[q], cw[q], s);
             }
             acc[t] = s;
         }
@@ -173,7 +235,7 @@ __global__ __launch_bounds__(KVP_WAVES * 64) void k_kv_epilogue(kvp_args a) {
             double sq = 0.0;
 #pragma unroll
             for (int i = 0; i < 4; i++) sq += (double) __fmul_rn(x[i], x[i]);
-            for (int off = 32; off >= 1; off >>= 1) sq += __shfl_xor(sq, off);
+            sq = wave_sum_d(sq);
             const float mean = (float) (sq / (double) KVP_HD);
             const float scale = 1.0f / sqrtf(__fadd_rn(mean, a.eps));
 #pragma unroll
