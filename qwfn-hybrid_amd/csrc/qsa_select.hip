@@ -12,11 +12,12 @@
 // Two kernels. k_qsa_score reads the pool cache (n_blocks x 128 f16, 4.7 MB
 // at 18432 blocks) once for up to 8 queries and computes the dot products on
 // the matrix cores, one wave per 16 blocks; the scores land in a workspace.
-// k_qsa_topk, one workgroup per query, holds the scores in registers, finds
-// the k-th largest by a radix select over order-preserving keys of the float
-// bits (histograms in LDS), keeps the blocks above it and as many equal to it
-// as needed, lowest block first, orders those by score, best first (ties:
-// lower block first), and writes their cells.
+// k_qsa_topk, one workgroup per query, holds the scores in registers as
+// order-preserving keys of the float bits, and writes the cells of the k
+// best blocks, best first (ties: lower block first). Usually a threshold
+// from a sample of the scores leaves under 1024 candidates, which one
+// bitonic sort orders; otherwise a radix select (histograms in LDS) finds the
+// k-th largest and the k are placed and sorted.
 #include "qwfn_common.h"
 #include "qwfn_state.h"
 
@@ -179,74 +180,62 @@ __device__ __forceinline__ void block_scan2(uint32_t x, uint32_t y, uint32_t & e
     ey = by + iy - y;
 }
 
-// One workgroup per query. Thread i holds scores [i * KPT, i * KPT + KPT) as
-// order-preserving keys in registers. A radix select (8-bit digits, most
-// significant first) finds the k-th largest key `kth` and how many keys equal
-// to it are kept (`keep`, the lowest blocks). Each pass counts digits into 32
-// sub-histograms, one per lane mod 32, whose rows are SUBH_LD words apart: lanes
-// with the same digit hit distinct banks, so clustered digits (the exponent
-// byte of similar scores) cost no serialised atomics. A pass whose boundary
-// bin is kept whole ends the select early. Keys above kth, then the kept equal
-// keys, are placed by an exclusive scan of per-thread counts (block order),
-// packed with their block as (key << 32 | ~block), so the larger packed value
-// comes first, and sorted: runs of 64 per wave, then merged by rank.
-template <int KPT>
-__global__ __launch_bounds__(TOPK_THREADS) void k_qsa_topk(topk_args a) {
-    __shared__ __align__(16) uint32_t sub_hist[(1 << RADIX_BITS) * SUBH_LD];
-    __shared__ uint32_t hist[1 << RADIX_BITS];
-    __shared__ uint32_t s_digit, s_need, s_done;
-    __shared__ __align__(16) uint2 wsum[TOPK_THREADS / 64];
-    __shared__ __align__(16) uint64_t sel[TOPK_MAX];
-    __shared__ int32_t order[TOPK_MAX];
+constexpr int CAND_MAX = 2 * TOPK_THREADS;   // LDS words of the candidates (the sort's two buffers)
+
+struct topk_lds {
+    uint32_t sub_hist[(1 << RADIX_BITS) * SUBH_LD];
+    uint64_t sel[TOPK_MAX];
+    uint64_t cand[CAND_MAX];
+    uint2    wsum[TOPK_THREADS / 64];
+    uint32_t hist[1 << RADIX_BITS];
+    int32_t  order[TOPK_MAX];
+    uint32_t s_digit, s_need, s_done, n_cand;
+};
+
+// Radix select over the keys key[j] (j < nv) of every thread, most significant
+// 8-bit digit first, for the need-th largest, down to the digit at bit
+// last_shift at most. Each pass counts digits into 32 sub-histograms, one per
+// lane mod 32, whose rows are SUBH_LD words apart: lanes with the same digit
+// hit distinct banks, so clustered digits (the exponent byte of similar
+// scores) cost no serialised atomics. A pass whose boundary bin is kept whole
+// ends the select early (done). Out: the digits found (prefix, the bits below
+// them zero) and the need left within the boundary bin. sub_hist is all
+// zeros at entry and at exit.
+template <int KK>
+__device__ __forceinline__ void radix_passes(const uint32_t (&key)[KK], int nv, uint32_t need, int last_shift, topk_lds & L,
+                                             uint32_t & prefix_out, uint32_t & need_out, bool & done_out) {
     const int tid = threadIdx.x, lane = tid & 63;
-    const int64_t n = a.n_blocks;
-    const int k = a.k;
-    const int64_t base = (int64_t) tid * KPT;
-    const float * sc = a.score + (size_t) blockIdx.x * score_ld(n);
-
-    for (int i = tid; i < (1 << RADIX_BITS) * SUBH_LD / 4; i += TOPK_THREADS)
-        ((uint4 *) sub_hist)[i] = make_uint4(0u, 0u, 0u, 0u);
-    uint32_t key[KPT];
-#pragma unroll
-    for (int j = 0; j < KPT; j += 4) {
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (base + j < n) v = *(const float4 *) (sc + base + j);   // score_ld keeps the float4 inside the row
-        key[j] = okey(v.x); key[j + 1] = okey(v.y); key[j + 2] = okey(v.z); key[j + 3] = okey(v.w);
-    }
-    const int nv = base >= n ? 0 : (n - base < KPT ? (int) (n - base) : KPT);   // valid keys of this thread
-    __syncthreads();
-
-    uint32_t prefix = 0, mask = 0, need = (uint32_t) k;
-    uint32_t kth = 0, keep = 0;
+    uint32_t prefix = 0, mask = 0;
+    bool done = false;
 #pragma unroll 1
-    for (int shift = 32 - RADIX_BITS; shift >= 0; shift -= RADIX_BITS) {
-        uint32_t * mine = sub_hist + (lane & 31);
+    for (int shift = 32 - RADIX_BITS; shift >= last_shift; shift -= RADIX_BITS) {
+        uint32_t * mine = L.sub_hist + (lane & 31);
 #pragma unroll
-        for (int j = 0; j < KPT; j++)
+        for (int j = 0; j < KK; j++)
             if (j < nv && (key[j] & mask) == prefix)
                 atomicAdd(&mine[((key[j] >> shift) & ((1u << RADIX_BITS) - 1)) * SUBH_LD], 1u);
         __syncthreads();
         {
             // 4 threads per bin sum its 32 counts and clear them for the next pass
             const int bin = tid >> 2, qq = tid & 3;
-            uint4 * p = (uint4 *) (sub_hist + bin * SUBH_LD + qq * 8);
+            uint4 * p = (uint4 *) (L.sub_hist + bin * SUBH_LD + qq * 8);
             const uint4 x = p[0], y = p[1];
             p[0] = make_uint4(0u, 0u, 0u, 0u);
             p[1] = make_uint4(0u, 0u, 0u, 0u);
             uint32_t c = x.x + x.y + x.z + x.w + y.x + y.y + y.z + y.w;
             c += dpp_u<0xB1>(c);                          // quad_perm 1,0,3,2
             c += dpp_u<0x4E>(c);                          // quad_perm 2,3,0,1
-            if (qq == 0) hist[bin] = c;
+            if (qq == 0) L.hist[bin] = c;
         }
         __syncthreads();
         if (tid < 64) {
             // lane l holds bins 255-4l down to 252-4l; s = keys in bins >= 252-4l
             const int top = 255 - 4 * lane;
-            const uint32_t c3 = hist[top], c2 = hist[top - 1], c1 = hist[top - 2], c0 = hist[top - 3];
+            const uint32_t c3 = L.hist[top], c2 = L.hist[top - 1], c1 = L.hist[top - 2], c0 = L.hist[top - 3];
             const uint32_t tot = c0 + c1 + c2 + c3;
-            const uint32_t s = wave_incl_scan(tot);
-            const uint32_t above = s - tot;           // keys in bins above this lane's
-            if (above < need && need <= s) {          // the one lane whose bins hold the need-th key
+            const uint32_t sc = wave_incl_scan(tot);
+            const uint32_t above = sc - tot;          // keys in bins above this lane's
+            if (above < need && need <= sc) {         // the one lane whose bins hold the need-th key
                 uint32_t acc = above, d, cd;
                 if (acc + c3 >= need) { d = 3; cd = c3; }
                 else {
@@ -258,45 +247,214 @@ __global__ __launch_bounds__(TOPK_THREADS) void k_qsa_topk(topk_args a) {
                         else { acc += c1; d = 0; cd = c0; }
                     }
                 }
-                s_digit = (uint32_t) (top - 3) + d;
-                s_need = need - acc;
-                s_done = (need - acc == cd) ? 1u : 0u;   // the whole bin is kept
+                L.s_digit = (uint32_t) (top - 3) + d;
+                L.s_need = need - acc;
+                L.s_done = (need - acc == cd) ? 1u : 0u;   // the whole bin is kept
             }
         }
         __syncthreads();
-        prefix |= s_digit << shift;
-        need = s_need;
+        prefix |= L.s_digit << shift;
+        need = L.s_need;
         mask |= ((1u << RADIX_BITS) - 1) << shift;
-        if (s_done) {
-            // keep every key >= prefix (the bin's keys have prefix's top bits and
-            // any low bits): the keys above prefix - 1, and none equal to it;
-            // valid keys are never 0, so prefix 0 keeps them all
-            kth = prefix ? prefix - 1 : 0u;
-            keep = 0;
-            break;
-        }
-        kth = prefix;
-        keep = need;
+        done = L.s_done != 0;
+        if (done) break;   // (the next pass writes the result words only after two more barriers)
     }
+    prefix_out = prefix;
+    need_out = need;
+    done_out = done;
+}
+
+// The k-th largest key `kth` and how many keys equal to it are kept (`keep`)
+// from a full radix select: a select that ended on a bin kept whole keeps
+// every key >= prefix (the bin's keys have prefix's top bits and any low
+// bits): the keys above prefix - 1, and none equal to it; valid keys are
+// never 0, so prefix 0 keeps them all.
+__device__ __forceinline__ void kth_keep(uint32_t prefix, uint32_t need, bool done, uint32_t & kth, uint32_t & keep) {
+    if (done) { kth = prefix ? prefix - 1 : 0u; keep = 0; }
+    else      { kth = prefix; keep = need; }
+}
+
+// Keys above kth, then the kept equal keys (the lowest blocks: threads and
+// their keys are in block order), into sel[0, k) by an exclusive scan of
+// per-thread counts, packed with their block as (key << 32 | ~block), so that
+// the larger packed value comes first (ties: the lower block).
+template <int KK, typename Blk>
+__device__ __forceinline__ void place(const uint32_t (&key)[KK], Blk blk, int nv, uint32_t kth, uint32_t keep, int k,
+                                      topk_lds & L) {
     uint32_t na = 0, ne = 0;
 #pragma unroll
-    for (int j = 0; j < KPT; j++) {
+    for (int j = 0; j < KK; j++) {
         na += (j < nv && key[j] > kth) ? 1u : 0u;
         ne += (j < nv && key[j] == kth) ? 1u : 0u;
     }
     uint32_t pa, pe;
-    block_scan2(na, ne, pa, pe, wsum);
+    block_scan2(na, ne, pa, pe, L.wsum);
     const uint32_t first_equal = (uint32_t) k - keep;        // the keys above take the slots before
 #pragma unroll
-    for (int j = 0; j < KPT; j++) {
-        const uint64_t packed = ((uint64_t) key[j] << 32) | (uint32_t) ~(uint32_t) (base + j);
+    for (int j = 0; j < KK; j++) {
+        const uint64_t packed = ((uint64_t) key[j] << 32) | (uint32_t) ~blk(j);
         if (j < nv && key[j] > kth) {
-            if (pa < first_equal) sel[pa] = packed;
+            if (pa < first_equal) L.sel[pa] = packed;
             pa++;
         } else if (j < nv && key[j] == kth) {
-            if (pe < keep && first_equal + pe < (uint32_t) k) sel[first_equal + pe] = packed;
+            if (pe < keep && first_equal + pe < (uint32_t) k) L.sel[first_equal + pe] = packed;
             pe++;
         }
+    }
+}
+
+// One compare-exchange step of a bitonic sort with the element of lane ^ D
+// (D < 64, in the wave): every lane gets max or min of the pair. The pair
+// comes back as {a, b} = {own, partner} in either order (the permlane swaps
+// return it so); the larger is taken iff take_max.
+template <int D>
+__device__ __forceinline__ uint64_t bitonic_lane_step(uint64_t v, bool take_max) {
+    const uint32_t lo = (uint32_t) v, hi = (uint32_t) (v >> 32);
+    uint32_t alo = lo, ahi = hi, blo, bhi;
+    if constexpr (D == 1 || D == 2 || D == 8) {
+        constexpr int CTRL = D == 1 ? 0xB1 : D == 2 ? 0x4E : 0x128;   // quad_perm [1,0,3,2], [2,3,0,1], row_ror:8
+        blo = (uint32_t) __builtin_amdgcn_update_dpp(0, (int) lo, CTRL, 0xF, 0xF, false);
+        bhi = (uint32_t) __builtin_amdgcn_update_dpp(0, (int) hi, CTRL, 0xF, 0xF, false);
+    } else if constexpr (D == 16 || D == 32) {
+        const auto rl = D == 16 ? __builtin_amdgcn_permlane16_swap(lo, lo, false, false)
+                                : __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+        const auto rh = D == 16 ? __builtin_amdgcn_permlane16_swap(hi, hi, false, false)
+                                : __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+        alo = rl[0]; blo = rl[1]; ahi = rh[0]; bhi = rh[1];
+    } else {
+        blo = (uint32_t) __shfl_xor((int) lo, D);
+        bhi = (uint32_t) __shfl_xor((int) hi, D);
+    }
+    const uint64_t a = ((uint64_t) ahi << 32) | alo, b = ((uint64_t) bhi << 32) | blo;
+    return (take_max == (a > b)) ? a : b;
+}
+
+// Bitonic sort, largest first, of the TOPK_THREADS values v (one a thread,
+// element tid): strides below 64 exchange within the wave, larger ones
+// through the two LDS buffers buf[0 .. 2 * TOPK_THREADS), one barrier a step.
+// Returns the element of rank tid.
+__device__ __forceinline__ uint64_t bitonic_sort_block(uint64_t v, uint64_t * buf) {
+    const int tid = threadIdx.x;
+    int cur = 0;
+#pragma unroll
+    for (int size = 2; size <= TOPK_THREADS; size <<= 1) {
+        const bool up = (tid & size) == 0;   // this run of `size` is sorted largest first
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            const bool take_max = up == ((tid & stride) == 0);
+            if (stride >= 64) {
+                buf[cur * TOPK_THREADS + tid] = v;
+                __syncthreads();
+                const uint64_t o = buf[cur * TOPK_THREADS + (tid ^ stride)];
+                v = (take_max == (v > o)) ? v : o;
+                cur ^= 1;
+            } else if (stride == 32) v = bitonic_lane_step<32>(v, take_max);
+            else if (stride == 16)   v = bitonic_lane_step<16>(v, take_max);
+            else if (stride == 8)    v = bitonic_lane_step<8>(v, take_max);
+            else if (stride == 4)    v = bitonic_lane_step<4>(v, take_max);
+            else if (stride == 2)    v = bitonic_lane_step<2>(v, take_max);
+            else                     v = bitonic_lane_step<1>(v, take_max);
+        }
+    }
+    return v;
+}
+
+// One workgroup per query. Thread i holds scores [i * KPT, i * KPT + KPT) as
+// order-preserving keys in registers, packed with their block as
+// (key << 32 | ~block): the larger packed value comes first, ties to the
+// lower block, and no two are equal. Fast path: a threshold tau such that
+// between k and TOPK_THREADS keys are >= tau -- every key when there are at
+// most TOPK_THREADS, else the 16-bit digits of the sample key (two a thread)
+// ranked to leave about (k + TOPK_THREADS) / 2 keys in expectation -- the
+// keys >= tau gathered into LDS (in any order), one bitonic sort of them, and
+// thread i holds rank i. Otherwise (the sample missed, k above 3/4 of
+// TOPK_THREADS, or more than 32 keys a thread): a radix select over every key
+// finds the k-th largest, the keys above it and the lowest-block equal ones
+// are placed by a scan, and those k are sorted in runs of 64 per wave, then
+// merged by rank.
+template <int KPT>
+__global__ __launch_bounds__(TOPK_THREADS) void k_qsa_topk(topk_args a) {
+    __shared__ __align__(16) topk_lds L;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int64_t n = a.n_blocks;
+    const int k = a.k;
+    const int64_t base = (int64_t) tid * KPT;
+    const float * sc = a.score + (size_t) blockIdx.x * score_ld(n);
+
+    for (int i = tid; i < (1 << RADIX_BITS) * SUBH_LD / 4; i += TOPK_THREADS)
+        ((uint4 *) L.sub_hist)[i] = make_uint4(0u, 0u, 0u, 0u);
+    if (tid == 0) L.n_cand = 0;
+    uint32_t key[KPT];
+#pragma unroll
+    for (int j = 0; j < KPT; j += 4) {
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (base + j < n) v = *(const float4 *) (sc + base + j);   // score_ld keeps the float4 inside the row
+        key[j] = okey(v.x); key[j + 1] = okey(v.y); key[j + 2] = okey(v.z); key[j + 3] = okey(v.w);
+    }
+    const int nv = base >= n ? 0 : (n - base < KPT ? (int) (n - base) : KPT);   // valid keys of this thread
+    __syncthreads();
+
+    bool sorted_all = false;
+    uint64_t mine = 0;                                          // fast path: the element of rank tid
+    if (KPT <= 32 && (n <= TOPK_THREADS || 4 * k <= 3 * TOPK_THREADS)) {   // (barriers: the conditions are uniform)
+        uint32_t tau = 0;                                       // valid keys are never 0: all of them
+        if (n > TOPK_THREADS) {
+            constexpr int J2 = KPT / 2;
+            const int64_t m0 = (n + KPT - 1) / KPT, m1 = n > J2 ? (n - J2 + KPT - 1) / KPT : 0;
+            const int64_t m = m0 + m1;                          // sample keys: key[0] and key[KPT / 2] of each thread
+            const int64_t want = ((int64_t) k + TOPK_THREADS) / 2;
+            uint32_t S = (uint32_t) ((want * m + n - 1) / n);
+            S = S < 1 ? 1u : (S > (uint32_t) m ? (uint32_t) m : S);
+            const uint32_t sk[2] = {key[0], key[J2]};
+            uint32_t nd;
+            bool dn;
+            radix_passes<2>(sk, nv > J2 ? 2 : (nv > 0 ? 1 : 0), S, 16, L, tau, nd, dn);
+        }
+        // the keys >= tau into L.cand, each wave's at an offset it takes with one atomic
+        uint32_t c = 0;
+#pragma unroll
+        for (int j = 0; j < KPT; j++) c += (j < nv && key[j] >= tau) ? 1u : 0u;
+        const uint32_t incl = wave_incl_scan(c);
+        uint32_t wbase = 0;
+        if (lane == 63) wbase = atomicAdd(&L.n_cand, incl);
+        wbase = (uint32_t) __builtin_amdgcn_readlane((int) wbase, 63);
+        uint32_t pos = wbase + incl - c;
+#pragma unroll
+        for (int j = 0; j < KPT; j++)
+            if (j < nv && key[j] >= tau) {
+                if (pos < (uint32_t) TOPK_THREADS) L.cand[pos] = ((uint64_t) key[j] << 32) | (uint32_t) ~(uint32_t) (base + j);
+                pos++;
+            }
+        __syncthreads();
+        const uint32_t total = L.n_cand;
+        if (total >= (uint32_t) k && total <= (uint32_t) TOPK_THREADS) {
+            sorted_all = true;
+            uint64_t v = (uint32_t) tid < total ? L.cand[tid] : 0ull;   // 0: below every packed key
+            __syncthreads();                                    // L.cand becomes the sort's buffers
+            mine = bitonic_sort_block(v, L.cand);
+        }
+    }
+    if (sorted_all) {
+        if (tid < k) {
+            const int32_t ix = (int32_t) ~(uint32_t) mine;
+            const size_t o = (size_t) blockIdx.x * k + tid;
+            const bool ok = ix >= 0 && ix < n;
+            int32_t cv[RATIO_MAX];
+#pragma unroll
+            for (int m = 0; m < RATIO_MAX; m++) cv[m] = (ok && m < a.ratio) ? a.blk_cells[(size_t) ix * a.ratio + m] : -1;
+            if (a.top) a.top[o] = ok ? ix : -1;
+#pragma unroll
+            for (int m = 0; m < RATIO_MAX; m++)
+                if (m < a.ratio) a.cells[o * a.ratio + m] = cv[m];
+        }
+        return;
+    }
+    {
+        uint32_t pfx, need, kth, keep;
+        bool done;
+        radix_passes<KPT>(key, nv, (uint32_t) k, 0, L, pfx, need, done);
+        kth_keep(pfx, need, done, kth, keep);
+        place<KPT>(key, [&](int j) { return (uint32_t) (base + j); }, nv, kth, keep, k, L);
     }
     // order: every wave sorts a run of 64 values in registers (bitonic over
     // lane swaps, best first); then each value's place is its index in its
@@ -304,11 +462,11 @@ __global__ __launch_bounds__(TOPK_THREADS) void k_qsa_topk(topk_args a) {
     // (a binary search). Padding (0) sorts last and is never placed.
     const int kpad = (k + 63) & ~63;
     const int n_runs = kpad >> 6;
-    for (int j = k + tid; j < kpad; j += TOPK_THREADS) sel[j] = 0;
+    for (int j = k + tid; j < kpad; j += TOPK_THREADS) L.sel[j] = 0;
     __syncthreads();
     const int wv = tid >> 6;
     if (wv < n_runs) {                                            // wave-uniform
-        uint64_t x = sel[tid];
+        uint64_t x = L.sel[tid];
 #pragma unroll
         for (int size = 2; size <= 64; size <<= 1) {
 #pragma unroll
@@ -320,15 +478,15 @@ __global__ __launch_bounds__(TOPK_THREADS) void k_qsa_topk(topk_args a) {
                 x = take_max ? (x > y ? x : y) : (x < y ? x : y);
             }
         }
-        sel[tid] = x;
+        L.sel[tid] = x;
     }
     __syncthreads();
     if (wv < n_runs) {
-        const uint64_t v = sel[tid];
+        const uint64_t v = L.sel[tid];
         uint32_t rank = (uint32_t) lane;
         for (int r = 0; r < n_runs; r++) {
             if (r == wv) continue;
-            const uint64_t * run = sel + 64 * r;
+            const uint64_t * run = L.sel + 64 * r;
             int pos = 0;
 #pragma unroll
             for (int step = 32; step >= 1; step >>= 1)
@@ -336,11 +494,11 @@ __global__ __launch_bounds__(TOPK_THREADS) void k_qsa_topk(topk_args a) {
             pos += run[pos] > v ? 1 : 0;                          // pos <= 63 here: all 64 above
             rank += (uint32_t) pos;
         }
-        if (v != 0 && rank < (uint32_t) k) order[rank] = (int32_t) ~(uint32_t) v;
+        if (v != 0 && rank < (uint32_t) k) L.order[rank] = (int32_t) ~(uint32_t) v;
     }
     __syncthreads();
     if (tid < k) {
-        const int32_t ix = order[tid];
+        const int32_t ix = L.order[tid];
         const size_t o = (size_t) blockIdx.x * k + tid;
         const bool ok = ix >= 0 && ix < n;                      // always, for distinct ranks; never read outside blk_cells
         // all of the block's cells are loaded before any is stored (cells may alias blk_cells)

@@ -422,6 +422,73 @@ def _bias(nb, n_past, ratio):
     return SO.qsa_pool_rebuild_bias(nb, n_past, ratio)
 
 
+def _exact_top(scores, k):
+    """The k best blocks of one query's f32 scores: score descending, ties to
+    the lower block (stable sort of the negated scores)."""
+    return np.argsort(-scores.astype(np.float64), kind="stable")[:k].astype(np.int32)
+
+
+@pytest.mark.parametrize("case", ["random", "all_equal", "few_values", "mostly_masked", "k1024", "just_above_2048",
+                                  "two_tied_bins", "ties_in_candidates", "small"])
+def test_qsa_topk_exact_on_device_scores(gpu, case):
+    """The selection alone, bit for bit: the kernel's own scores are read back
+    from the workspace and the expected blocks are an exact sort of them. The
+    cases reach both the fast path (a threshold from a sample of the scores,
+    or none at 1024 blocks or fewer, then one sort of the keys above it) and
+    the full select it falls back to: all scores tied, a few distinct values,
+    most blocks masked, k above 768, ties around the k-th place."""
+    import torch
+    rng = np.random.default_rng(sum(map(ord, case)))
+    nb, k, T, ratio = 18432, 513, 3, 4
+    pool = (rng.standard_normal((nb, 128)) * 0.5).astype(np.float16)
+    q = rng.standard_normal((T, 4, 128)).astype(np.float32)
+    bias = np.zeros((T, nb), np.float32)
+    if case == "all_equal":
+        pool[:] = 0
+    elif case == "few_values":
+        pool[:] = 0
+        pool[:, 0] = rng.integers(0, 6, nb) / 4.0
+        q[:] = 0
+        q[:, 0, 0] = 1.0
+    elif case == "mostly_masked":
+        bias[:, 3000:] = -np.inf
+    elif case == "k1024":
+        k = 1024
+    elif case == "just_above_2048":
+        nb = 2049
+        pool, bias = pool[:nb], bias[:, :nb]
+    elif case == "ties_in_candidates":
+        # about 9 blocks per distinct score: ties at the k-th place among the candidates
+        pool[:] = 0
+        pool[:, 0] = rng.integers(0, 2048, nb) / 64.0
+        q[:] = 0
+        q[:, 0, 0] = 1.0
+    elif case == "small":
+        nb, k = 1000, 100
+        pool, bias = pool[:nb], bias[:, :nb]
+    elif case == "two_tied_bins":
+        # every score one of two values, the better one held by exactly k - 1 blocks
+        pool[:] = 0
+        pool[:, 0] = 0.25
+        pool[rng.choice(nb, k - 1, replace=False), 0] = 0.5
+        q[:] = 0
+        q[:, 0, 0] = 1.0
+    blk_cells, _, _ = SO.qsa_tables(nb, ratio, 1, 0)
+    pd = dev(pool.view(np.uint16))
+    qd, bd, cd = dev(q), dev(bias), dev(blk_cells.astype(np.int32))
+    cells = torch.full((T, k * ratio), -1, dtype=torch.int32, device="cuda")
+    top = torch.full((T, k), -1, dtype=torch.int32, device="cuda")
+    ws = torch.zeros(K.load().qwfn_qsa_select_workspace_size(nb, T), dtype=torch.uint8, device="cuda")
+    say(f"qsa top-k exact: {case} nb={nb} k={k}")
+    S.qsa_select_cells(pd, qd, bd, k, cd, ratio, cells, top, ws=ws)
+    ld = (nb + 63) // 64 * 64
+    sc = host(ws).view(np.float32)[:T * ld].reshape(T, ld)[:, :nb]
+    got = host(top)
+    for t in range(T):
+        np.testing.assert_array_equal(got[t], _exact_top(sc[t], k))
+    np.testing.assert_array_equal(host(cells), np.stack([SO.qsa_cells(got[t], blk_cells, ratio) for t in range(T)]))
+
+
 def test_qsa_select_closed_forms(gpu):
     rng = np.random.default_rng(70)
     nb, ratio, k = 768, 4, 513
