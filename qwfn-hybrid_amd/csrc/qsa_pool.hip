@@ -13,6 +13,7 @@
 #include "qwfn_common.h"
 #include "qwfn_state.h"
 #include "rope_device.h"
+#include "wave_ops.h"
 
 #include <cmath>
 
@@ -96,7 +97,7 @@ __global__ __launch_bounds__(POOL_WAVES * 64) void k_qsa_pool(pool_args a) {
     // RMS norm: the squares (float) summed in double across the wave
     double sq = 0.0;
     for (int d = lane; d < dim; d += 64) sq += (double) __fmul_rn(x[d], x[d]);
-    for (int off = 32; off >= 1; off >>= 1) sq += __shfl_xor(sq, off);
+    sq = wave::wave_sum_d(sq);
     const float mean = (float) (sq / (double) dim);
     const float scale = 1.0f / sqrtf(__fadd_rn(mean, a.eps));
     for (int d = lane; d < dim; d += 64) x[d] = __fmul_rn(__fmul_rn(x[d], scale), a.w[d]);
@@ -169,7 +170,9 @@ __global__ __launch_bounds__(RB_WAVES * 64) void k_qsa_pool_rebuild(pool_args a)
     double sq = 0.0;
 #pragma unroll
     for (int i = 0; i < 8; i++) sq += (double) __fmul_rn(x[i], x[i]);
-    for (int off = lpb >> 1; off >= 1; off >>= 1) sq += __shfl_xor(sq, off);
+    if (lpb == 16) sq = wave::row16_sum_d(sq);   // a block's lanes are one DPP row
+    else
+        for (int off = lpb >> 1; off >= 1; off >>= 1) sq += __shfl_xor(sq, off);
     const float mean = (float) (sq / (double) dim);
     const float scale = 1.0f / sqrtf(__fadd_rn(mean, a.eps));
     float * xw = xs[wv] + lb * dim + 8 * lj;
