@@ -400,10 +400,12 @@ __global__ __launch_bounds__(TOPK_THREADS) void k_qsa_topk(topk_args a) {
         uint32_t tau = 0;                                       // valid keys are never 0: all of them
         if (n > TOPK_THREADS) {
             constexpr int J2 = KPT / 2;
-            const int64_t m0 = (n + KPT - 1) / KPT, m1 = n > J2 ? (n - J2 + KPT - 1) / KPT : 0;
-            const int64_t m = m0 + m1;                          // sample keys: key[0] and key[KPT / 2] of each thread
-            const int64_t want = ((int64_t) k + TOPK_THREADS) / 2;
-            uint32_t S = (uint32_t) ((want * m + n - 1) / n);
+            const int nn = (int) n;                             // at most 32 * 1024 here
+            const int m = (nn + KPT - 1) / KPT + (nn > J2 ? (nn - J2 + KPT - 1) / KPT : 0);   // sample keys: key[0] and key[KPT / 2] of each thread
+            // the sample rank, in float (an estimate serves: any tau with between
+            // k and TOPK_THREADS keys at or above it gives the exact answer)
+            const float want = 0.5f * (float) (k + TOPK_THREADS);
+            uint32_t S = (uint32_t) ceilf(want * (float) m / (float) nn);
             S = S < 1 ? 1u : (S > (uint32_t) m ? (uint32_t) m : S);
             const uint32_t sk[2] = {key[0], key[J2]};
             uint32_t nd;
