@@ -429,7 +429,7 @@ def _exact_top(scores, k):
 
 
 @pytest.mark.parametrize("case", ["random", "all_equal", "few_values", "mostly_masked", "k1024", "just_above_2048",
-                                  "two_tied_bins", "ties_in_candidates", "small"])
+                                  "two_tied_bins", "ties_in_candidates", "small", "kpt12", "kpt32", "kpt40"])
 def test_qsa_topk_exact_on_device_scores(gpu, case):
     """The selection alone, bit for bit: the kernel's own scores are read back
     from the workspace and the expected blocks are an exact sort of them. The
@@ -466,6 +466,11 @@ def test_qsa_topk_exact_on_device_scores(gpu, case):
     elif case == "small":
         nb, k = 1000, 100
         pool, bias = pool[:nb], bias[:, :nb]
+    elif case in ("kpt12", "kpt32", "kpt40"):
+        # 12 and 32 scores a thread take the sampled path, 40 the full select
+        nb = {"kpt12": 10000, "kpt32": 30000, "kpt40": 36000}[case]
+        pool = (rng.standard_normal((nb, 128)) * 0.5).astype(np.float16)
+        bias = np.zeros((T, nb), np.float32)
     elif case == "two_tied_bins":
         # every score one of two values, the better one held by exactly k - 1 blocks
         pool[:] = 0
