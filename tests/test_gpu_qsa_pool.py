@@ -74,6 +74,30 @@ def test_pool_rebuild_matches_oracle(gpu, oracle, n_past, ratio):
     _ulp_check(got[:n_whole], ref)
 
 
+@pytest.mark.parametrize("dim,n_dims", [(96, 64), (256, 128), (64, 48)])
+def test_pool_rebuild_other_dims(gpu, oracle, dim, n_dims):
+    """Index keys of other lengths: 96 takes the one-block-per-wave kernel (96 / 8
+    is not a power of two), 256 and 64 the 16-byte-lane kernel with 2 and 8
+    blocks a wave (64 with a rotated part that is not a whole lane's 8 dims)."""
+    K = gpu
+    rng = np.random.default_rng(dim)
+    n_past, ratio = 4099, 4
+    ic = (rng.standard_normal((n_past + 5, dim)) * 2).astype(np.float16)
+    w = rng.uniform(0.6, 1.4, dim).astype(np.float32)
+    n_whole = n_past // ratio
+    pool = torch.zeros((n_whole + 3, dim), dtype=torch.float16, device="cuda")
+    cfg = K.qsa_pool_cfg(idx_dim=dim, n_dims=n_dims)
+    say(f"pool rebuild dim={dim} n_dims={n_dims}")
+    K.qsa_pool_rebuild(dev(ic), n_past, ratio, dev(w), pool, cfg=cfg)
+    got = host(pool).view(np.uint16)
+    assert K.device_status() == 0
+    assert not got[n_whole:].any()
+    members = np.arange(n_whole * ratio, dtype=np.int32)
+    pos4 = np.repeat((np.arange(n_whole) * ratio)[:, None], 4, axis=1).astype(np.int32)
+    ref = O.qsa_pool_blocks(ic.view(np.uint16), members, ratio, w, pos4, n_dims=n_dims)
+    _ulp_check(got[:n_whole], ref)
+
+
 def test_pool_decode_chain_across_a_block_edge(gpu, oracle):
     """Three chained positions 8190, 8191, 8192 (ratio 32): the raw key of each
     goes to its row, its block's key is re-pooled (the first two block 255,
