@@ -32,6 +32,7 @@ def main() -> int:
     ap.add_argument("--sets", type=int, default=4)
     ap.add_argument("--mb", type=int, default=1024)
     ap.add_argument("--lib", default=None, help="library path (default: the package's build)")
+    ap.add_argument("--append", action="store_true", help="verify: append the T new K/V rows in the same launch")
     a = ap.parse_args()
     import numpy as np
     import torch
@@ -64,6 +65,11 @@ def main() -> int:
                          dtype=torch.uint8, device=dev)
         run = lambda i: K.flash_attn_ext(K.q_view(q), views[i % a.sets][0], views[i % a.sets][1], K.mask_view(mask),
                                          1 / 16, K.out_view(out), ws=ws)
+        if a.append and a.op == "verify":
+            newk = torch.randn((T, 512), generator=gen, device=dev)
+            newv = torch.randn((T, 512), generator=gen, device=dev)
+            run = lambda i: K.flash_attn_ext_append(K.q_view(q), views[i % a.sets][0], views[i % a.sets][1],
+                                                    K.mask_view(mask), 1 / 16, K.out_view(out), newk, newv, a.depth, ws=ws)
     elif a.op == "cells":
         n_ctx = 65536
         sets = [(cache(n_ctx), cache(n_ctx)) for _ in range(a.sets)]
