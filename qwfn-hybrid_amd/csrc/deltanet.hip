@@ -13,7 +13,8 @@
 // wave covers two whole 128-byte row pieces. A column stays in registers for
 // the whole step and the state is read and written once. The sums over r
 // are finished across the two halves of the wave (permlane32 swap) and then
-// across the 8 waves through LDS, in a fixed order. The inputs of up to DN_TC
+// across the 8 waves through LDS, in a fixed order; one barrier a token (a
+// token's output sums share the next token's barrier) and one at the end. The inputs of up to DN_TC
 // tokens (k and q of the key head in LDS, v, the decay and beta in registers)
 // are loaded together with the state. After token T-1-s the state is also
 // stored to rollback slot s-1 (s = 1 .. n_snap): the state s tokens back.
@@ -73,7 +74,9 @@ __device__ __forceinline__ float red_sum(const float (*red)[DN_COLS], int cl) {
 
 __global__ __launch_bounds__(DN_WAVES * 64) void k_gated_delta_net(dn_args a) {
     __shared__ float4 kq[DN_TC][2][DN_D / 4];   // [token][k, q][rows / 4]
-    __shared__ float red_m[DN_WAVES][DN_COLS], red_o[DN_WAVES][DN_COLS];
+    // the waves' partial sums, two buffers each by token parity: token t's
+    // output sums are read after token t + 1's first barrier (or the last one)
+    __shared__ float red_m[2][DN_WAVES][DN_COLS], red_o[2][DN_WAVES][DN_COLS];
     const int h = blockIdx.x / (DN_D / DN_COLS), cb = blockIdx.x % (DN_D / DN_COLS);
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int cl = lane & 31;
@@ -123,9 +126,11 @@ __global__ __launch_bounds__(DN_WAVES * 64) void k_gated_delta_net(dn_args a) {
                 m = __fmaf_rn(S[i], kk[i], m);
             }
             m = sum_halves(m);
-            if (lane < 32) red_m[w][cl] = m;
+            if (lane < 32) red_m[t & 1][w][cl] = m;
             __syncthreads();
-            m = red_sum(red_m, cl);
+            if (t > 0 && w == 0 && lane < 32)
+                a.out[((int64_t) (t - 1) * a.n_v + h) * DN_D + c] = red_sum(red_o[(t - 1) & 1], cl);
+            m = red_sum(red_m[t & 1], cl);
             const float d = (vc - m) * b;
             float o = 0.f;
 #pragma unroll
@@ -134,10 +139,7 @@ __global__ __launch_bounds__(DN_WAVES * 64) void k_gated_delta_net(dn_args a) {
                 o = __fmaf_rn(S[i], qq[i] * a.scale, o);
             }
             o = sum_halves(o);
-            if (lane < 32) red_o[w][cl] = o;
-            __syncthreads();
-            if (w == 0 && lane < 32)
-                a.out[((int64_t) t * a.n_v + h) * DN_D + c] = red_sum(red_o, cl);
+            if (lane < 32) red_o[t & 1][w][cl] = o;
             const int sb = a.T - 1 - t;
             if (sb >= 1 && sb <= a.n_snap) {
                 float * sp = a.snap + (sb - 1) * a.snap_stride + (size_t) h * DN_D * DN_D;
@@ -148,6 +150,9 @@ __global__ __launch_bounds__(DN_WAVES * 64) void k_gated_delta_net(dn_args a) {
     }
 #pragma unroll
     for (int i = 0; i < DN_RPS; i++) Sg[(size_t) (r0 + i) * DN_D + c] = S[i];
+    __syncthreads();
+    if (w == 0 && lane < 32)
+        a.out[((int64_t) (a.T - 1) * a.n_v + h) * DN_D + c] = red_sum(red_o[(a.T - 1) & 1], cl);
 }
 
 }  // namespace
