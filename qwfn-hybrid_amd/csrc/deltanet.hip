@@ -144,12 +144,12 @@ __global__ __launch_bounds__(DN_WAVES * 64) void k_gated_delta_net(dn_args a) {
             if (sb >= 1 && sb <= a.n_snap) {
                 float * sp = a.snap + (sb - 1) * a.snap_stride + (size_t) h * DN_D * DN_D;
 #pragma unroll
-                for (int i = 0; i < DN_RPS; i++) sp[(size_t) (r0 + i) * DN_D + c] = S[i];
+                for (int i = 0; i < DN_RPS; i++) __builtin_nontemporal_store(S[i], &sp[(size_t) (r0 + i) * DN_D + c]);
             }
         }
     }
 #pragma unroll
-    for (int i = 0; i < DN_RPS; i++) Sg[(size_t) (r0 + i) * DN_D + c] = S[i];
+    for (int i = 0; i < DN_RPS; i++) __builtin_nontemporal_store(S[i], &Sg[(size_t) (r0 + i) * DN_D + c]);
     __syncthreads();
     if (w == 0 && lane < 32)
         a.out[((int64_t) (a.T - 1) * a.n_v + h) * DN_D + c] = red_sum(red_o[(a.T - 1) & 1], cl);
