@@ -138,6 +138,7 @@ __global__ __launch_bounds__(POOL_WAVES * 64) void k_qsa_pool(pool_args a) {
 // of its blocks (2 blocks per pass at n_dims 64) instead of one block leaving
 // half the lanes idle. Per value the arithmetic is k_qsa_pool's.
 constexpr int RB_WAVES = 4;
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(RB_WAVES * 64) void k_qsa_pool_rebuild(pool_args a) {
     __shared__ __align__(16) float xs[RB_WAVES][512];
@@ -187,7 +188,7 @@ __global__ __launch_bounds__(RB_WAVES * 64) void k_qsa_pool_rebuild(pool_args a)
             uint32_t o[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) o[i] = (uint32_t) f2h(x[2 * i]) | ((uint32_t) f2h(x[2 * i + 1]) << 16);
-            *(uint4 *) out = make_uint4(o[0], o[1], o[2], o[3]);
+            __builtin_nontemporal_store(v4u{o[0], o[1], o[2], o[3]}, (v4u *) out);
         } else {
 #pragma unroll
             for (int i = 0; i < 8; i++)
