@@ -467,7 +467,9 @@ def main() -> int:
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this path has no multi-GPU form to run (asked for --gpus {args.gpus}); "
-              "see DESIGN.md for how it would shard.", file=sys.stderr)
+              "across GPUs it would shard by KV head and by key-position range, each GPU running these kernels on "
+              "its share and the split partials merged across GPUs.",
+              file=sys.stderr)
         return 2
     import numpy as np
     import torch
