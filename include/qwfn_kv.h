@@ -177,6 +177,34 @@ int qwfn_flash_attn_ext_q8_0_noalloc(const qwfn_tensor * q, const qwfn_tensor * 
  * partition). */
 void qwfn_fattn_force_splits(int32_t n_splits);
 
+/* Force the attention kernel family of later calls in this process (any
+ * thread): QWFN_FA_KERNEL_AUTO returns to the planner's choice. A call whose
+ * shape the forced family cannot take returns QWFN_ENOTSUP. For parity tests
+ * that reach every kernel family on the same inputs, and for A/B timing; the
+ * results do not depend on it beyond float rounding. No counterpart in the
+ * reference (ggml picks its own kernel).
+ *   VD:      at most 24 query rows per KV head, a mask shared by the heads
+ *            over at most 4 query positions (or none)
+ *   DEC:     at most 32 query rows per KV head
+ *   GENERAL: any shape but gathered cells
+ *   PRE:     more than 32 query rows per KV head, a mask shared by the heads
+ *            (or none), n_head / n_head_kv >= 4, one batch, no cells */
+enum {
+    QWFN_FA_KERNEL_AUTO    = 0,
+    QWFN_FA_KERNEL_VD      = 1,
+    QWFN_FA_KERNEL_DEC     = 2,
+    QWFN_FA_KERNEL_GENERAL = 3,
+    QWFN_FA_KERNEL_PRE     = 4
+};
+void qwfn_fattn_force_kernel(int32_t kind);
+
+/* The attention kernel that the calling thread's last attention call launched,
+ * as its template instantiation ("k_fa_vd<1, 1, true, false, false>"), or ""
+ * before the first launch; the string lives as long as the library. For the
+ * tests that check that every kernel instantiation is reached. No counterpart
+ * in the reference. */
+const char * qwfn_fattn_last_kernel(void);
+
 /* Batched decode over sequences of different depths: as
  * qwfn_flash_attn_ext_q8_0, except that sequence b (q batch index) attends
  * only keys [0, seq_n_kv[b]) -- the same result as masking its later keys with

@@ -357,6 +357,15 @@ __device__ __forceinline__ void dma16_buf_at(v4i rsrc, uint32_t off, uint32_t ld
     dma16_buf(rsrc, off, lds_base + LDS_OFF);
 }
 
+// r with every component read from the first lane: a resource that the
+// compiler cannot prove uniform (a value merged across branches, at low
+// optimisation levels) is moved to scalar registers for the DMA asm; where it
+// is already scalar, nothing is emitted.
+__device__ __forceinline__ v4i uniform_rsrc(v4i r) {
+    return v4i{__builtin_amdgcn_readfirstlane(r[0]), __builtin_amdgcn_readfirstlane(r[1]),
+               __builtin_amdgcn_readfirstlane(r[2]), __builtin_amdgcn_readfirstlane(r[3])};
+}
+
 // num_records of a buffer resource for `rem` bytes (at most 2^32 - 1).
 __device__ __forceinline__ uint32_t rsrc_bytes(int64_t rem) {
     uint32_t hi = (uint32_t) ((uint64_t) rem >> 32);
@@ -1846,6 +1855,860 @@ __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
     }
 }
 
+// ================================================================ decode / verify in 32-key steps
+//
+// k_fa_vd<NF, PK, MASKED, RG, GATHER>: at most 24 query rows per KV head
+// (decode, MTP verify, batch decode, sparse cells), one block of 8 waves per
+// CU. Every wave holds all of the block's query rows and takes its own steps
+// of 32 keys: two 16-key sub-tiles, one per stage of a private two-stage ring
+// filled by LDS DMA. Each K/V row of the block is therefore DMA'd, its block
+// scales tabulated and its V quants converted once (k_fa_dec does all three
+// once per 16-row tile). The rows sit in up to two MFMA tiles:
+//   full tile (NF = 1): query rows 0..15, one 16x16 score tile per sub-tile;
+//   packed tile (PK = 1): the next 8 rows. Its score tile holds each of them
+//     twice: column r for the keys of sub-tile 0, column r + 8 for sub-tile 1.
+//     Its QK^T is two MFMAs, one per sub-tile, whose query operand is zero in
+//     the other half's columns; its PV operand holds P*d_v of the column's
+//     own sub-tile and zeros for the other. The two columns of a row share one
+//     running max (a lane swap across the halves) and add up in the epilogue.
+// 24 rows (3 tokens x 8 heads) take one tile of each kind, and no vector
+// instruction works on a padding column. PV runs on v_mfma_f32_16x16x32_f16:
+// the reduction index 8g + 4u + i of lane group g is key 4g + i of sub-tile u,
+// in the V^T operand and in P*d_v alike. The arithmetic per score is
+// k_fa_dec's: exact i8 block dots of the requantised query, d_q*d_k scaling
+// per block, online base-2 softmax, P*d_v as f16 hi + lo.
+// Sub-tiles go to the waves round robin (wave w takes sub-tiles w, w + 8,
+// w + 16, ...) and a step pairs two of a wave's sub-tiles, 8 apart. A wave
+// left with one sub-tile runs a half step: one 16-key sub-tile, PV on
+// v_mfma_f32_16x16x16_f16, about 55% of a step's vector work. So a split of
+// 16 keys more than 8 steps' worth costs one half step, not one step, and a
+// split of 128 keys keeps all 8 waves busy.
+
+constexpr int VD_WAVES  = 8;
+constexpr int VD_STEP   = 32;                                   // keys of a step: two 16-key sub-tiles
+constexpr int VD_GAP    = VD_WAVES;                             // sub-tiles from a step's first to its second
+constexpr int VD_MROWS  = 4;                                    // mask rows (query positions) of a block, at most
+constexpr int VD_MBYTES = 2 * VD_MROWS * DEC_MGR * 16;          // a wave's mask granules of one step
+constexpr int VD_OBS    = D + 4;                                // epilogue buffer row stride (floats)
+constexpr int VD_OBUF   = 32 * VD_OBS;                          // one epilogue buffer: 32 rows (floats)
+constexpr int VD_QROW   = 1024;                                 // f32 query row in the prologue's staging
+constexpr int VD_ROWS   = 24;                                   // query rows per KV head, at most
+static_assert(VD_ROWS * VD_QROW <= VD_WAVES * DEC_KB, "the query rows fit sub-tile 1's V region");
+static_assert(4 * VD_OBUF * 4 <= 2 * 2 * VD_WAVES * DEC_KB, "the epilogue buffers fit the ring");
+
+// DPP row_ror:8: lane i of each 16-lane row reads lane i ^ 8 of the same row
+__device__ __forceinline__ float swap_halves8(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x128, 0xF, 0xF, false));
+}
+
+template <int NF, int PK, bool MASKED, bool RG, bool GATHER>
+__global__ __launch_bounds__(VD_WAVES * 64, 2) void k_fa_vd(fa_args a) {
+    static_assert(NF >= 0 && NF <= 1 && PK >= 0 && PK <= 1 && NF + PK >= 1, "a full tile, a packed tile or both");
+    static_assert(!(GATHER && (MASKED || RG)), "gathered keys carry their own mask, one sequence");
+    constexpr int IR  = 16 * NF + 8 * PK;                  // query rows of the block, at most
+    constexpr int NKD = 2 * DEC_TDMA;                      // K DMAs of a step
+    constexpr int NVD = 2 * DEC_TDMA + (MASKED ? 1 : 0);   // V and mask DMAs of a step
+    asm volatile("" :: "s"(a.q), "s"(a.k), "s"(a.v), "s"(a.mask), "s"(a.m_ne2), "s"(a.part_o));
+
+    // kvr[tensor][u][wave]: sub-tile u's K (tensor 0) or V rows of a wave's
+    // step (sub-tile 1 at a fixed offset below 64 KB from sub-tile 0, so one
+    // address register serves both). The V rows of sub-tile 1 of all waves are
+    // one contiguous region, which holds the block's f32 query rows during the
+    // prologue.
+    __shared__ __attribute__((aligned(16))) uint8_t kvr[2][2][VD_WAVES][DEC_KB];
+    __shared__ __attribute__((aligned(16))) uint8_t mgr[MASKED ? VD_WAVES : 1][MASKED ? VD_MBYTES : 16];
+    // query window images [block][16-byte slice][row] of the full tile and of
+    // the packed tile; qzero has the packed image's layout and holds zeros
+    __shared__ __attribute__((aligned(16))) uint8_t qimf[NF ? NBLK : 1][4][16][16];
+    __shared__ __attribute__((aligned(16))) uint8_t qimp[PK ? NBLK : 1][4][8][16];
+    __shared__ __attribute__((aligned(16))) uint8_t qzero[PK ? NBLK : 1][4][8][16];
+    // one tensor's block scales of a wave's step, [block][key]; after the key
+    // loop each wave's (max, sum) per row
+    __shared__ __attribute__((aligned(16))) uint16_t stab[VD_WAVES][NBLK][VD_STEP];
+    // the query rows' d_q * scale * log2(e), [row][block]
+    __shared__ __attribute__((aligned(16))) float dqs[IR][NBLK];
+    __shared__ __attribute__((aligned(16))) int32_t gcell[GATHER ? DEC_GATHER_SPLIT : 4];
+    __shared__ uint32_t g_bad;   // GATHER: a cell of the block lies outside the cache
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int ln = lane & 15, lg = lane >> 4;
+    const int hs = ln >> 3;                                // packed tile: the column's sub-tile
+
+    // ---- block -> (b, kvh, split), as k_fa_dec ----
+    const int id = blockIdx.x;
+    const int hgn = a.nh_kv;
+    const int n_units = RG ? a.r_units : a.B * a.ns;
+    int kvh, unit;
+    if (n_units >= 8) {
+        const int j = id >> 3;
+        const int jq = (int) udiv((uint32_t) j, (uint32_t) hgn, a.hgn_mul);
+        kvh = j - jq * hgn;
+        unit = jq * 8 + (id & 7);
+    } else {
+        unit = (int) udiv((uint32_t) id, (uint32_t) hgn, a.hgn_mul);
+        kvh = id - unit * hgn;
+    }
+    if (unit >= n_units) return;
+    int b, split;
+    int64_t k_lo, k_hi;
+    if constexpr (RG) {
+        int32_t us = 0, nsb = 1, slb = 0;
+        int64_t nkb = 0;
+        b = 0;
+#pragma unroll
+        for (int i = 0; i < RAGGED_MAX_B; i++)
+            if (i < a.B && unit >= a.r_ustart[i]) {
+                b = i; us = a.r_ustart[i]; nsb = a.r_ns[i]; slb = a.r_split_len[i]; nkb = a.r_n_kv[i];
+            }
+        split = unit - us;
+        k_lo = (int64_t) split * slb;
+        const int64_t e = k_lo + slb;
+        k_hi = split == nsb - 1 ? nkb : (nkb < e ? nkb : e);
+    } else {
+        b = (int) udiv((uint32_t) unit, (uint32_t) a.ns, a.ns_mul);
+        split = unit - b * a.ns;
+        k_lo = (int64_t) split * a.split_len;
+        const int64_t e = k_lo + a.split_len;
+        k_hi = split == a.ns - 1 ? a.n_kv : (a.n_kv < e ? a.n_kv : e);
+    }
+    if constexpr (GATHER) {
+        int64_t nh = 0;
+#pragma unroll
+        for (int i = 0; i < GATHER_MAX_HEADS; i++)
+            if (i == kvh) nh = a.g_n[i];
+        k_hi = k_hi < nh ? k_hi : nh;
+        k_lo = k_lo < k_hi ? k_lo : k_hi;
+    }
+    const int span = (int) (k_hi - k_lo);
+    const int n_sub = (span + DEC_TK - 1) / DEC_TK;         // 16-key sub-tiles of the split
+    const int RW = a.R;                                    // the block's rows: all of the KV head's
+
+    const char * kbase = a.k + (size_t) bmod(b, a.kb) * a.k_nb3 + (size_t) kvh * a.k_nb2;
+    const char * vbase = a.v + (size_t) bmod(b, a.vb) * a.v_nb3 + (size_t) kvh * a.v_nb2;
+
+    // ---- mask (shared by the heads): n_mr query positions. One DMA a step
+    //      brings 3 granules of 16 bytes per (sub-tile, position) from the
+    //      16-byte aligned address at or below the sub-tile's first key; the
+    //      lane's keys 4lg.. of a sub-tile then sit at m_lf (full tile,
+    //      sub-tile 0; + 48 n_mr for sub-tile 1) or m_lp (packed tile) ----
+    const char * mslice = MASKED ? a.mask + (size_t) bmod(b, a.m_ne3) * a.m_nb3 : nullptr;
+    const char * mslice_al = (const char *) ((uintptr_t) mslice & ~(uintptr_t) 15);
+    const uint32_t mb_off = (uint32_t) (mslice - mslice_al);
+    int n_mr = 1;
+    uint32_t m_goff = 0, m_lf = 0, m_lp = 0;
+    if constexpr (MASKED) {
+        n_mr = (int) div_gqa(a, (uint32_t) (RW - 1)) + 1;
+        const int gmax = 2 * n_mr * DEC_MGR;
+        const int g = lane < gmax ? lane : gmax - 1;
+        const int su = g / (n_mr * DEC_MGR), mr = (g / DEC_MGR) % n_mr;
+        m_goff = ((mb_off + (uint32_t) mr * (uint32_t) a.m_nb1) & ~15u) + (uint32_t) (VD_GAP * DEC_TK * 2) * (uint32_t) su +
+                 16u * (uint32_t) (g % DEC_MGR);
+        auto lane_at = [&](int row, int su2) -> uint32_t {
+            const int mr2 = (int) div_gqa(a, (uint32_t) (row < RW ? row : RW - 1));
+            return (uint32_t) ((su2 * n_mr + mr2) * DEC_MGR * 16) + ((mb_off + (uint32_t) mr2 * (uint32_t) a.m_nb1) & 15u) +
+                   8u * (uint32_t) lg;
+        };
+        if constexpr (NF) m_lf = lane_at(ln, 0);
+        if constexpr (PK) m_lp = lane_at(16 * NF + (ln & 7), hs);
+    }
+
+    // ---- per-lane DMA offsets of a sub-tile's pieces: piece p = 64s + lane is
+    //      byte 16 (p % 17) of key p / 17 ----
+    //      (K and V rows have the same stride: one table serves both)
+    uint32_t koff[DEC_TDMA];
+#pragma unroll
+    for (int s = 0; s < DEC_TDMA; s++) {
+        const uint32_t p = (uint32_t) (64 * s + lane), key = p / 17u, part = p - key * 17u;
+        koff[s] = key * (uint32_t) a.k_nb1 + part * 16u;
+    }
+    const uint32_t k_sub = (uint32_t) (VD_GAP * DEC_TK) * (uint32_t) a.k_nb1;   // sub-tile 1 of a step
+    // the wave's steps start at sub-tiles wave, wave + 16, ... : resources
+    // start at the step's first key and end at the split's end (keys past it
+    // arrive as zeros, without memory traffic)
+    const int64_t key_first = k_lo + (int64_t) wave * DEC_TK;
+    const char * k_next = kbase + key_first * (int64_t) a.k_nb1;
+    const char * v_next = vbase + key_first * (int64_t) a.v_nb1;
+    const char * m_next = mslice_al + key_first * 2;
+    int64_t k_rem = (k_hi - key_first) * (int64_t) a.k_nb1, v_rem = (k_hi - key_first) * (int64_t) a.v_nb1;
+    int64_t m_rem = (int64_t) a.m_slice + mb_off - key_first * 2;
+    const int64_t k_step = (int64_t) (2 * VD_GAP * DEC_TK) * a.k_nb1, v_step = (int64_t) (2 * VD_GAP * DEC_TK) * a.v_nb1;
+    constexpr int64_t m_step = 2 * VD_GAP * DEC_TK * 2;
+    // GATHER: the DMA offsets of sub-tile ti follow its cells (as k_fa_dec)
+    const uint32_t g_kbytes = GATHER ? (uint32_t) (a.g_rows * (int64_t) a.k_nb1) : 0u;
+    const uint32_t g_vbytes = GATHER ? (uint32_t) (a.g_rows * (int64_t) a.v_nb1) : 0u;
+    auto gather_off = [&](int ti, int s, uint32_t nb1) -> uint32_t {
+        const uint32_t p = (uint32_t) (64 * s + lane), key = p / 17u, part = p - key * 17u;
+        const int kk = ti * DEC_TK + (int) key;
+        const uint32_t row = kk < span ? (uint32_t) gcell[kk] : 0xffffffffu;
+        return row < (uint32_t) a.g_rows ? row * nb1 + part * 16u : 0x80000000u;
+    };
+    const uint32_t l_kv = lds_addr(&kvr[0][0][0][0]);
+    const uint32_t l_k0 = l_kv + (uint32_t) (0 * VD_WAVES + wave) * DEC_KB, l_k1 = l_kv + (uint32_t) (1 * VD_WAVES + wave) * DEC_KB;
+    const uint32_t l_v0 = l_kv + (uint32_t) (2 * VD_WAVES + wave) * DEC_KB, l_v1 = l_kv + (uint32_t) (3 * VD_WAVES + wave) * DEC_KB;
+    const uint32_t l_m = lds_addr(&mgr[0][0]) + (uint32_t) (MASKED ? wave * VD_MBYTES : 0);
+
+    auto rsrc_k = [&]() __attribute__((always_inline)) -> v4i {
+        if constexpr (GATHER) return make_rsrc(kbase, g_kbytes);
+        const v4i r = make_rsrc(k_next, rsrc_bytes(k_rem));
+        k_next += k_step;
+        k_rem -= k_step;
+        return r;
+    };
+    auto rsrc_v = [&]() __attribute__((always_inline)) -> v4i {
+        if constexpr (GATHER) return make_rsrc(vbase, g_vbytes);
+        const v4i r = make_rsrc(v_next, rsrc_bytes(v_rem));
+        v_next += v_step;
+        v_rem -= v_step;
+        return r;
+    };
+    // K rows of the two sub-tiles of the step that starts at sub-tile t0 (10 DMAs)
+    auto issue_k = [&](int t0, v4i rk) __attribute__((always_inline)) {
+        rk = uniform_rsrc(rk);
+        uint32_t o0[DEC_TDMA], o1[DEC_TDMA];
+#pragma unroll
+        for (int s = 0; s < DEC_TDMA; s++) {
+            if constexpr (GATHER) {
+                o0[s] = gather_off(t0, s, (uint32_t) a.k_nb1);
+                o1[s] = gather_off(t0 + VD_GAP, s, (uint32_t) a.k_nb1);
+            } else {
+                o0[s] = koff[s];
+                o1[s] = koff[s] + k_sub;
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's reads of the regions are done
+        static_assert(DEC_TDMA == 5, "five DMAs per sub-tile and tensor");
+        dma16_buf_at<0>(rk, o0[0], l_k0);
+        dma16_buf_at<1024>(rk, o0[1], l_k0);
+        dma16_buf_at<2048>(rk, o0[2], l_k0);
+        dma16_buf_at<3072>(rk, o0[3], l_k0);
+        if (lane < 16) dma16_buf_at<4096>(rk, o0[4], l_k0);
+        dma16_buf_at<0>(rk, o1[0], l_k1);
+        dma16_buf_at<1024>(rk, o1[1], l_k1);
+        dma16_buf_at<2048>(rk, o1[2], l_k1);
+        dma16_buf_at<3072>(rk, o1[3], l_k1);
+        if (lane < 16) dma16_buf_at<4096>(rk, o1[4], l_k1);
+    };
+    // V rows of sub-tile su of the step that starts at sub-tile t0 (5 DMAs)
+    auto issue_vs = [&](int t0, int su, v4i rv) __attribute__((always_inline)) {
+        rv = uniform_rsrc(rv);
+        uint32_t o[DEC_TDMA];
+#pragma unroll
+        for (int s = 0; s < DEC_TDMA; s++) {
+            if constexpr (GATHER) o[s] = gather_off(t0 + (su ? VD_GAP : 0), s, (uint32_t) a.v_nb1);
+            else o[s] = koff[s] + (su ? k_sub : 0u);
+        }
+        const uint32_t lv = su ? l_v1 : l_v0;
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        dma16_buf_at<0>(rv, o[0], lv);
+        dma16_buf_at<1024>(rv, o[1], lv);
+        dma16_buf_at<2048>(rv, o[2], lv);
+        dma16_buf_at<3072>(rv, o[3], lv);
+        if (lane < 16) dma16_buf_at<4096>(rv, o[4], lv);
+    };
+    // mask granules of a step (one DMA), the next step's resource after it
+    auto issue_m = [&]() __attribute__((always_inline)) {
+        if constexpr (MASKED) {
+            const v4i rm = uniform_rsrc(make_rsrc(m_next, (uint32_t) m_rem));
+            m_next += m_step;
+            m_rem -= m_step;
+            if (lane < 2 * n_mr * DEC_MGR) dma16_buf(rm, m_goff, l_m);
+        }
+    };
+
+    // ---- prologue: the block's f32 query rows (one wave DMA per row, wave w
+    //      takes rows w, w + 8, w + 16) and the cell list (GATHER) first, and
+    //      waited for before any K/V DMA: queued behind the K/V requests of
+    //      every CU they would arrive microseconds later. Then the fused
+    //      append, the first step's K rows, sub-tile 0's V rows and the mask,
+    //      which load while the query rows are requantised; sub-tile 1's V
+    //      region holds the query rows until then, its DMA follows. ----
+    uint8_t * qst = &kvr[1][1][0][0];
+    const int first = wave < n_sub ? wave : -1;
+    if constexpr (GATHER) {
+        const int32_t * cl = a.g_cells + (size_t) kvh * a.g_stride + k_lo;
+        const v4i rc = make_rsrc(cl, (uint32_t) span * 4u);
+        for (int m = wave; m * 256 < span; m += VD_WAVES)
+            dma16_buf(rc, (uint32_t) (m * 1024 + 16 * lane), __builtin_amdgcn_readfirstlane(lds_addr(&gcell[m * 256])));
+        if (threadIdx.x == 0) g_bad = 0;
+    }
+    {
+        const v4i rq = make_rsrc(a.q + (size_t) b * a.q_nb3, a.q_slice);
+#pragma unroll
+        for (int j = 0; j < (IR + VD_WAVES - 1) / VD_WAVES; j++) {
+            const int rl = wave + VD_WAVES * j;
+            if (rl >= RW) break;
+            const uint32_t r = (uint32_t) rl;
+            const uint32_t t = div_gqa(a, r), h = (uint32_t) (kvh * a.gqa) + (r - t * (uint32_t) a.gqa);
+            dma16_buf(rq, t * (uint32_t) a.q_nb1 + h * (uint32_t) a.q_nb2 + 16u * (uint32_t) lane,
+                      __builtin_amdgcn_readfirstlane(lds_addr(qst + rl * VD_QROW)));
+        }
+    }
+    if (a.app_n > 0) {
+        // as in k_fa_dec: the blocks whose keys hold appended rows quantise
+        // their KV head's part of them first, and read them back only after
+        // their own stores are done
+        const int64_t alo = std::max<int64_t>(a.app_row0, k_lo), ahi = std::min<int64_t>(a.app_row0 + a.app_n, k_hi);
+        if (alo < ahi) {
+            const int units = (int) (ahi - alo) * NBLK * 2;
+            const int sub = threadIdx.x & 7;
+            for (int u0 = 0; u0 < units; u0 += VD_WAVES * 8) {
+                const int uu0 = u0 + (int) (threadIdx.x >> 3);
+                const bool live = uu0 < units;
+                const int uu = live ? uu0 : 0;
+                const int tensor = uu & 1, jb = (uu >> 1) % NBLK;
+                const int64_t row = alo + (uu >> 1) / NBLK;
+                const float4 xv = *(const float4 *) ((tensor ? a.app_v : a.app_k) + (size_t) (row - a.app_row0) * a.app_nb1 +
+                                                     (size_t) (kvh * D + QK * jb + 4 * sub) * 4);
+                float x[4] = {xv.x, xv.y, xv.z, xv.w};
+                uint16_t d16;
+                float dqa;
+                const uint32_t q4 = dev::q8_quantize_lane4(x, a.x86 != 0, &d16, &dqa);
+                if (live) {
+                    char * bp = (char *) (tensor ? vbase + (size_t) row * a.v_nb1 : kbase + (size_t) row * a.k_nb1) + jb * QBLOCK;
+                    uint16_t * qp = (uint16_t *) (bp + 2 + sub * 4);
+                    qp[0] = (uint16_t) (q4 & 0xffffu);
+                    qp[1] = (uint16_t) (q4 >> 16);
+                    if (sub == 0) *(uint16_t *) bp = d16;
+                }
+            }
+        }
+    }
+    wait_vmcnt<0>();   // this wave's query rows (cells, appended rows) have landed
+    __syncthreads();   // ... and every wave's
+    if constexpr (GATHER) {
+        if ((int) threadIdx.x < span && (uint32_t) gcell[threadIdx.x] >= (uint32_t) a.g_rows) g_bad = 1;
+    }
+    v4i rv_first{0, 0, 0, 0};
+    if (first >= 0) {
+        issue_k(first, rsrc_k());
+        rv_first = rsrc_v();
+        issue_vs(first, 0, rv_first);
+        issue_m();
+    }
+
+    // ---- requantisation of the query rows (ggml's quantiser): wave w takes
+    //      q8_0 block w of every row, two lanes per row ----
+    static_assert(NBLK == VD_WAVES, "one block of all rows per wave");
+    const int qrow = lane >> 1, qh = lane & 1;
+    float qx[16];
+    {
+        const float4 * src = (const float4 *) (qst + qrow * VD_QROW + (QK * wave + 16 * qh) * 4);
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const float4 v = qrow < RW ? src[m] : make_float4(0.f, 0.f, 0.f, 0.f);
+            qx[4 * m] = v.x; qx[4 * m + 1] = v.y; qx[4 * m + 2] = v.z; qx[4 * m + 3] = v.w;
+        }
+    }
+    __syncthreads();   // every query value is in registers: the staging region becomes sub-tile 1's V rows
+    if (first >= 0) issue_vs(first, 1, rv_first);
+    {
+        // zero this wave's block of both images and its share of the zero image
+        if constexpr (NF) *(uint4 *) &qimf[wave][lane >> 4][lane & 15][0] = make_uint4(0, 0, 0, 0);
+        if constexpr (PK) {
+            if (lane < 32) *(uint4 *) &qimp[wave][lane >> 3][lane & 7][0] = make_uint4(0, 0, 0, 0);
+            else           *(uint4 *) &qzero[wave][(lane - 32) >> 3][lane & 7][0] = make_uint4(0, 0, 0, 0);
+        }
+        wave_lds_sync();
+        uint32_t w[4];
+        uint16_t d16;
+        float dqv = 0.f;
+        if (a.x86) dev::q8_quantize_lanes<16>(qx, true, w, &d16, &dqv);
+        else       dev::q8_quantize_lanes<16>(qx, false, w, &d16, &dqv);
+        if (qrow < RW) {
+            const int woff = (int) ((0x200E0C0A08061402ull >> (8 * wave)) & 0xff);   // win_off(wave)
+            const bool full = qrow < 16 * NF;
+            uint8_t * s0 = full ? &qimf[wave][0][NF ? qrow : 0][0] : &qimp[wave][0][PK ? qrow - 16 * NF : 0][0];
+            const int sstride = full ? 16 * 16 : 8 * 16;    // bytes between the slices of a row
+#pragma unroll
+            for (int m = 0; m < 8; m++) {   // 2-byte pieces never straddle a slice
+                const int o = woff + 16 * qh + 2 * m;
+                *(uint16_t *) (s0 + (o >> 4) * sstride + (o & 15)) = (uint16_t) (w[m >> 1] >> (16 * (m & 1)));
+            }
+        }
+        if (qh == 0 && qrow < IR) dqs[qrow][wave] = qrow < RW ? dqv * (a.scale * LOG2E) : 0.f;
+    }
+    __syncthreads();   // the images and the d_q table are complete
+
+    // ---- the key loop ----
+    v4f Of[NF ? NBLK : 1][2], Op[PK ? NBLK : 1][2];
+#pragma unroll
+    for (int bb = 0; bb < (NF ? NBLK : 1); bb++) { Of[bb][0] = v4f{0, 0, 0, 0}; Of[bb][1] = v4f{0, 0, 0, 0}; }
+#pragma unroll
+    for (int bb = 0; bb < (PK ? NBLK : 1); bb++) { Op[bb][0] = v4f{0, 0, 0, 0}; Op[bb][1] = v4f{0, 0, 0, 0}; }
+    float mfr = -INFINITY, lfr = 0.f, mpr = -INFINITY, lpr = 0.f;
+    // per-lane LDS addresses (block bb at + bb * stride)
+    constexpr int SUB1 = VD_WAVES * DEC_KB;                                  // sub-tile 1's region from sub-tile 0's
+    const uint8_t * kr0 = &kvr[0][0][wave][0] + ln * SEG + 16 * lg;         // K window slices of key ln
+    const uint8_t * vr0 = &kvr[1][0][wave][0] + (4 * lg) * SEG + 2 + 2 * ln;   // V dims 2ln, 2ln+1 of keys 4lg..
+    const float * dqf_l = &dqs[NF ? ln : 0][0];                             // the full tile's row
+    const float * dqp_l = &dqs[PK ? 16 * NF + (ln & 7) : 0][0];             // the packed tile's row
+    const uint8_t * qf_l = &qimf[0][lg][NF ? ln : 0][0];                   // + 1024 bb
+    const uint8_t * qp0_l = hs == 0 ? &qimp[0][lg][ln & 7][0] : &qzero[0][lg][ln & 7][0];   // + 512 bb
+    const uint8_t * qp1_l = hs == 1 ? &qimp[0][lg][ln & 7][0] : &qzero[0][lg][ln & 7][0];
+    const uint8_t * tab = (const uint8_t *) &stab[wave][0][0];
+    const uint8_t * tf_l = tab + 8 * lg;                                    // keys 4lg.. of sub-tile 0; + 64 bb (+ 32: sub-tile 1)
+    const uint8_t * tp_l = tab + 32 * hs + 8 * lg;                          // the packed column's sub-tile
+    const uint8_t * tz = &qzero[0][0][0][0];
+    const uint8_t * tpv0_l = hs == 0 ? tp_l : tz;                           // d_v of the packed columns, zero for
+    const uint8_t * tpv1_l = hs == 1 ? tp_l : tz;                           // the other half's sub-tile
+    const uint8_t * mg = &mgr[MASKED ? wave : 0][0];
+    // GATHER: the position of the lane's query rows
+    const int64_t qpos_f = GATHER ? a.g_pos0 + (int64_t) div_gqa(a, (uint32_t) (NF ? ln : 0)) : 0;
+    const int64_t qpos_p = GATHER ? a.g_pos0 + (int64_t) div_gqa(a, (uint32_t) (16 * NF + (ln & 7))) : 0;
+
+    // one tensor's block scales of the step into the wave's table [block][key]
+    auto tab_fill = [&](int tensor, auto half_tag) __attribute__((always_inline)) {
+        constexpr bool HALF = decltype(half_tag)::value;
+        const int bq = lane & 7, kq = lane >> 3;
+        constexpr int NN = HALF ? 2 : 4;
+        uint16_t sv[4];
+#pragma unroll
+        for (int n = 0; n < NN; n++)
+            sv[n] = *(const uint16_t *) (&kvr[tensor][n >> 1][wave][0] + (kq + 8 * (n & 1)) * SEG + bq * QBLOCK);
+#pragma unroll
+        for (int n = 0; n < NN; n++) stab[wave][bq][16 * (n >> 1) + kq + 8 * (n & 1)] = sv[n];
+    };
+
+    // one step from the sub-tiles t0 and t0 + 8 (HALF: t0 only); the next
+    // step of the wave starts at sub-tile tn
+    auto step = [&](int t0, int tn, auto half_tag) __attribute__((always_inline)) {
+        constexpr bool HALF = decltype(half_tag)::value;
+        constexpr int NU = HALF ? 1 : 2;                   // sub-tiles of the step
+        const bool nx = tn < n_sub;
+        wait_vmcnt<NVD>();   // the step's K rows have landed
+        tab_fill(0, half_tag);
+        wave_lds_sync();
+
+        // ---- S = K Q^T per sub-tile: MFMA rows are keys, columns the rows of
+        //      the tile. Each block's MFMAs are issued one block ahead of its
+        //      scaling ----
+        float sf[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}}, sp[4] = {0.f, 0.f, 0.f, 0.f};
+        {
+            v4i cf[2][2], cp[2];
+            float4 dq4f[2], dq4p[2];
+            auto qk_mfma = [&](int bb) __attribute__((always_inline)) {
+                const int sl = bb & 1;
+                const v4i a0 = *(const v4i *) (kr0 + 16 * win_piece(bb));
+                v4i a1{0, 0, 0, 0};
+                if constexpr (!HALF) a1 = *(const v4i *) (kr0 + SUB1 + 16 * win_piece(bb));
+                if constexpr (NF) {
+                    const v4i qv = *(const v4i *) (qf_l + bb * 1024);
+                    cf[sl][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, qv, v4i{0, 0, 0, 0}, 0, 0, 0);
+                    if constexpr (!HALF) cf[sl][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, qv, v4i{0, 0, 0, 0}, 0, 0, 0);
+                }
+                if constexpr (PK) {
+                    const v4i q0 = *(const v4i *) (qp0_l + bb * 512);
+                    cp[sl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, q0, v4i{0, 0, 0, 0}, 0, 0, 0);
+                    if constexpr (!HALF) {
+                        const v4i q1 = *(const v4i *) (qp1_l + bb * 512);
+                        cp[sl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, q1, cp[sl], 0, 0, 0);
+                    }
+                }
+            };
+            auto dq_at = [](const float4 & v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; };
+            auto qk_scale = [&](int bb) __attribute__((always_inline)) {
+                const int sl = bb & 1;
+                if constexpr (NF) {
+                    const float d = dq_at(dq4f[bb >> 2], bb & 3);
+#pragma unroll
+                    for (int su = 0; su < NU; su++) {
+                        const uint2 dk = *(const uint2 *) (tf_l + bb * 64 + 32 * su);
+                        sf[su][0] = __builtin_fmaf((float) cf[sl][su][0], mul_f16lo(d, dk.x), sf[su][0]);
+                        sf[su][1] = __builtin_fmaf((float) cf[sl][su][1], mul_f16hi(d, dk.x), sf[su][1]);
+                        sf[su][2] = __builtin_fmaf((float) cf[sl][su][2], mul_f16lo(d, dk.y), sf[su][2]);
+                        sf[su][3] = __builtin_fmaf((float) cf[sl][su][3], mul_f16hi(d, dk.y), sf[su][3]);
+                    }
+                }
+                if constexpr (PK) {
+                    const uint2 dk = *(const uint2 *) (tp_l + bb * 64);
+                    const float d = dq_at(dq4p[bb >> 2], bb & 3);
+                    sp[0] = __builtin_fmaf((float) cp[sl][0], mul_f16lo(d, dk.x), sp[0]);
+                    sp[1] = __builtin_fmaf((float) cp[sl][1], mul_f16hi(d, dk.x), sp[1]);
+                    sp[2] = __builtin_fmaf((float) cp[sl][2], mul_f16lo(d, dk.y), sp[2]);
+                    sp[3] = __builtin_fmaf((float) cp[sl][3], mul_f16hi(d, dk.y), sp[3]);
+                }
+            };
+            if constexpr (NF) { dq4f[0] = *(const float4 *) dqf_l; dq4f[1] = *(const float4 *) (dqf_l + 4); }
+            if constexpr (PK) { dq4p[0] = *(const float4 *) dqp_l; dq4p[1] = *(const float4 *) (dqp_l + 4); }
+            qk_mfma(0);
+#pragma unroll
+            for (int bb = 0; bb < NBLK; bb++) {
+                if (bb + 1 < NBLK) qk_mfma(bb + 1);
+                qk_scale(bb);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        // the scores are complete here: otherwise the compiler sinks the
+        // scaling past the DMA branch below, keeping every block's integer
+        // dots and scale products live at once
+#pragma unroll
+        for (int i = 0; i < 4; i++) asm volatile("" : "+v"(sf[0][i]), "+v"(sf[1][i]), "+v"(sp[i]));
+        if (nx) {
+            issue_k(tn, rsrc_k());
+            wait_vmcnt<NKD>();   // the step's V rows and mask have landed
+        } else {
+            wait_vmcnt<0>();
+        }
+        tab_fill(1, half_tag);
+        wave_lds_sync();
+
+        // ---- mask, online softmax (base 2) over the step's keys; sub-tile u
+        //      starts at key kb[u] of the split ----
+        const int kb0 = DEC_TK * t0, kb1 = DEC_TK * (t0 + VD_GAP);
+        auto kb = [&](int su) { return su ? kb1 : kb0; };
+        float pf[2][4], pp[4];
+        uint32_t pf16[2][2], pp16[2];
+        if constexpr (NF) {
+            float x[2][4];
+#pragma unroll
+            for (int su = 0; su < NU; su++) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) x[su][i] = sf[su][i];
+                if constexpr (MASKED) {
+                    const uint8_t * mp = mg + m_lf + su * (n_mr * DEC_MGR * 16);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) x[su][i] = fma_f16lo((uint32_t) *(const uint16_t *) (mp + 2 * i), LOG2E, x[su][i]);
+                } else if constexpr (GATHER) {
+                    const int kin = kb(su) + 4 * lg;
+                    const int4 c = *(const int4 *) &gcell[kin < DEC_GATHER_SPLIT - 3 ? kin : 0];
+                    const int cv[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        x[su][i] = (uint32_t) cv[i] < (uint32_t) a.g_rows && (int64_t) cv[i] <= qpos_f ? x[su][i] : -INFINITY;
+                }
+                if (kb(su) + DEC_TK > span) {   // the split's last sub-tile: keys past its end
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        if (kb(su) + 4 * lg + i >= span) x[su][i] = -INFINITY;
+                }
+            }
+            float mloc = vmax(vmax(x[0][0], x[0][1]), vmax(x[0][2], x[0][3]));
+            if constexpr (!HALF) mloc = vmax(mloc, vmax(vmax(x[1][0], x[1][1]), vmax(x[1][2], x[1][3])));
+            mloc = xmax_lanes16_32(mloc);
+            const bool grow = mloc > mfr + RESCALE_SLACK;
+            const bool rescale = grow && mfr != -INFINITY;   // the accumulators hold something to rescale
+            float alpha = 1.f;
+            if (grow) {
+                alpha = __builtin_amdgcn_exp2f(mfr - mloc);
+                mfr = mloc;
+            }
+            const float m_use = mfr == -INFINITY ? 0.f : mfr;
+            float lsum = 0.f;
+#pragma unroll
+            for (int su = 0; su < NU; su++) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    pf[su][i] = __builtin_amdgcn_exp2f(x[su][i] - m_use);
+                    lsum += pf[su][i];
+                }
+                pf16[su][0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(pf[su][0], pf[su][1]));
+                pf16[su][1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(pf[su][2], pf[su][3]));
+            }
+            lfr = lfr * alpha + lsum;
+            if (__any(rescale)) {
+                asm volatile("" ::: "memory");
+#pragma unroll
+                for (int bb = 0; bb < NBLK; bb++) { Of[bb][0] *= alpha; Of[bb][1] *= alpha; }
+            }
+        }
+        if constexpr (PK) {
+            float x[4];
+            const int kbp = HALF || hs == 0 ? kb0 : kb1;   // the packed column's sub-tile (HALF: only sub-tile 0 has keys)
+#pragma unroll
+            for (int i = 0; i < 4; i++) x[i] = sp[i];
+            if constexpr (MASKED) {
+                const uint8_t * mp = mg + m_lp;
+#pragma unroll
+                for (int i = 0; i < 4; i++) x[i] = fma_f16lo((uint32_t) *(const uint16_t *) (mp + 2 * i), LOG2E, x[i]);
+            } else if constexpr (GATHER) {
+                const int kin = kbp + 4 * lg;
+                const int4 c = *(const int4 *) &gcell[kin < DEC_GATHER_SPLIT - 3 ? kin : 0];
+                const int cv[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    x[i] = (uint32_t) cv[i] < (uint32_t) a.g_rows && (int64_t) cv[i] <= qpos_p ? x[i] : -INFINITY;
+            }
+            if (HALF && hs) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) x[i] = -INFINITY;   // no sub-tile 1 in a half step
+            } else if (kbp + DEC_TK > span) {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (kbp + 4 * lg + i >= span) x[i] = -INFINITY;
+            }
+            float mloc = vmax(vmax(x[0], x[1]), vmax(x[2], x[3]));
+            mloc = xmax_lanes16_32(mloc);
+            mloc = vmax(mloc, swap_halves8(mloc));      // both sub-tiles of the row
+            const bool grow = mloc > mpr + RESCALE_SLACK;
+            const bool rescale = grow && mpr != -INFINITY;
+            float alpha = 1.f;
+            if (grow) {
+                alpha = __builtin_amdgcn_exp2f(mpr - mloc);
+                mpr = mloc;
+            }
+            const float m_use = mpr == -INFINITY ? 0.f : mpr;
+            float lsum = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                pp[i] = __builtin_amdgcn_exp2f(x[i] - m_use);
+                lsum += pp[i];
+            }
+            pp16[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(pp[0], pp[1]));
+            pp16[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(pp[2], pp[3]));
+            lpr = lpr * alpha + lsum;
+            if (__any(rescale)) {
+                asm volatile("" ::: "memory");
+#pragma unroll
+                for (int bb = 0; bb < NBLK; bb++) { Op[bb][0] *= alpha; Op[bb][1] *= alpha; }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) asm volatile("" : "+v"(pf[0][i]), "+v"(pf[1][i]), "+v"(pp[i]));
+        asm volatile("" : "+v"(pf16[0][0]), "+v"(pf16[0][1]), "+v"(pf16[1][0]), "+v"(pf16[1][1]), "+v"(pp16[0]), "+v"(pp16[1]));
+
+        // ---- O += V^T (P d_v) per V block over the step's keys. Block bb + 1's
+        //      V quants are read while bb is computed ----
+        {
+            uint32_t w[2][2][4];
+            auto load_v = [&](int bb, uint32_t (&ww)[2][4]) __attribute__((always_inline)) {
+#pragma unroll
+                for (int jv = 0; jv < 4; jv++) {
+                    ww[0][jv] = *(const uint16_t *) (vr0 + jv * SEG + bb * QBLOCK);
+                    if constexpr (!HALF) ww[1][jv] = *(const uint16_t *) (vr0 + SUB1 + jv * SEG + bb * QBLOCK);
+                }
+            };
+            load_v(0, w[0]);
+#pragma unroll
+            for (int bb = 0; bb < NBLK; bb++) {
+                const int cb = bb & 1;
+                if (bb + 1 < NBLK) load_v(bb + 1, w[cb ^ 1]);
+                uint32_t a00[2], a10[2], a01[2], a11[2];
+                cvt_v_block(w[cb][0], a00, a10);
+                if constexpr (!HALF) cvt_v_block(w[cb][1], a01, a11);
+                if constexpr (NF) {
+                    uint32_t bh[2][2], bl[2][2];
+#pragma unroll
+                    for (int su = 0; su < NU; su++) {
+                        const uint2 d = *(const uint2 *) (tf_l + bb * 64 + 32 * su);
+                        const uint32_t dv[2] = {d.x, d.y};
+                        pdv_hilo(pf[su], pf16[su], dv, bh[su], bl[su]);
+                    }
+                    if constexpr (HALF) {
+                        const v4h A0 = __builtin_bit_cast(v4h, make_uint2(a00[0], a00[1]));
+                        const v4h A1 = __builtin_bit_cast(v4h, make_uint2(a10[0], a10[1]));
+                        const v4h Bh = __builtin_bit_cast(v4h, make_uint2(bh[0][0], bh[0][1]));
+                        const v4h Bl = __builtin_bit_cast(v4h, make_uint2(bl[0][0], bl[0][1]));
+                        Of[bb][0] = __builtin_amdgcn_mfma_f32_16x16x16f16(A0, Bh, Of[bb][0], 0, 0, 0);
+                        Of[bb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A1, Bh, Of[bb][1], 0, 0, 0);
+                        Of[bb][0] = __builtin_amdgcn_mfma_f32_16x16x16f16(A0, Bl, Of[bb][0], 0, 0, 0);
+                        Of[bb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A1, Bl, Of[bb][1], 0, 0, 0);
+                    } else {
+                        const v8h A0 = __builtin_bit_cast(v8h, make_uint4(a00[0], a00[1], a01[0], a01[1]));
+                        const v8h A1 = __builtin_bit_cast(v8h, make_uint4(a10[0], a10[1], a11[0], a11[1]));
+                        const v8h Bh = __builtin_bit_cast(v8h, make_uint4(bh[0][0], bh[0][1], bh[1][0], bh[1][1]));
+                        const v8h Bl = __builtin_bit_cast(v8h, make_uint4(bl[0][0], bl[0][1], bl[1][0], bl[1][1]));
+                        Of[bb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, Bh, Of[bb][0], 0, 0, 0);
+                        Of[bb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, Bh, Of[bb][1], 0, 0, 0);
+                        Of[bb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, Bl, Of[bb][0], 0, 0, 0);
+                        Of[bb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, Bl, Of[bb][1], 0, 0, 0);
+                    }
+                }
+                if constexpr (PK) {
+                    uint32_t bh[2][2], bl[2][2];
+#pragma unroll
+                    for (int su = 0; su < NU; su++) {
+                        const uint2 e = *(const uint2 *) ((su ? tpv1_l : tpv0_l) + bb * 64);
+                        const uint32_t dv[2] = {e.x, e.y};
+                        pdv_hilo(pp, pp16, dv, bh[su], bl[su]);
+                    }
+                    if constexpr (HALF) {
+                        const v4h A0 = __builtin_bit_cast(v4h, make_uint2(a00[0], a00[1]));
+                        const v4h A1 = __builtin_bit_cast(v4h, make_uint2(a10[0], a10[1]));
+                        const v4h Bh = __builtin_bit_cast(v4h, make_uint2(bh[0][0], bh[0][1]));
+                        const v4h Bl = __builtin_bit_cast(v4h, make_uint2(bl[0][0], bl[0][1]));
+                        Op[bb][0] = __builtin_amdgcn_mfma_f32_16x16x16f16(A0, Bh, Op[bb][0], 0, 0, 0);
+                        Op[bb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A1, Bh, Op[bb][1], 0, 0, 0);
+                        Op[bb][0] = __builtin_amdgcn_mfma_f32_16x16x16f16(A0, Bl, Op[bb][0], 0, 0, 0);
+                        Op[bb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A1, Bl, Op[bb][1], 0, 0, 0);
+                    } else {
+                        const v8h A0 = __builtin_bit_cast(v8h, make_uint4(a00[0], a00[1], a01[0], a01[1]));
+                        const v8h A1 = __builtin_bit_cast(v8h, make_uint4(a10[0], a10[1], a11[0], a11[1]));
+                        const v8h Bh = __builtin_bit_cast(v8h, make_uint4(bh[0][0], bh[0][1], bh[1][0], bh[1][1]));
+                        const v8h Bl = __builtin_bit_cast(v8h, make_uint4(bl[0][0], bl[0][1], bl[1][0], bl[1][1]));
+                        Op[bb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, Bh, Op[bb][0], 0, 0, 0);
+                        Op[bb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, Bh, Op[bb][1], 0, 0, 0);
+                        Op[bb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, Bl, Op[bb][0], 0, 0, 0);
+                        Op[bb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, Bl, Op[bb][1], 0, 0, 0);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        if (nx) {
+            const v4i rv = rsrc_v();
+            issue_vs(tn, 0, rv);
+            issue_vs(tn, 1, rv);
+            issue_m();
+        }
+    };
+
+    // The wave's steps. Two waves share a SIMD (waves w and w + 4) and the
+    // older one wins its issue slots: the wave priority alternates with the
+    // step count, in opposite phase for the two waves of a SIMD.
+    const bool young = wave >= VD_WAVES / 2;
+    int jj = 0, t0 = first;
+    for (; t0 >= 0 && t0 + VD_GAP < n_sub; t0 += 2 * VD_GAP, jj++) {
+        if (young == (bool) (jj & 1)) __builtin_amdgcn_s_setprio(1); else __builtin_amdgcn_s_setprio(0);
+        step(t0, t0 + 2 * VD_GAP, std::false_type{});
+    }
+    if (t0 >= 0 && t0 < n_sub) {   // the wave's last sub-tile alone
+        if (young == (bool) (jj & 1)) __builtin_amdgcn_s_setprio(1); else __builtin_amdgcn_s_setprio(0);
+        step(t0, t0 + 2 * VD_GAP, std::true_type{});
+    }
+    __builtin_amdgcn_s_setprio(0);
+
+    // ---- epilogue: the waves' (max, sum) per row, each wave's O scaled to the
+    //      block max, then summed in two rounds through LDS (waves 4..7 into
+    //      0..3, then 0..3 into four buffers that every thread reads) ----
+    {
+        float2 * mlw = (float2 *) &stab[wave][0][0];           // [row]
+        if constexpr (NF) {
+            const float l = sum_lanes16_32(lfr);
+            if (lg == 0) mlw[ln] = make_float2(mfr, l);
+        }
+        if constexpr (PK) {
+            float l = sum_lanes16_32(lpr);
+            l += swap_halves8(l);
+            if (lg == 0 && hs == 0) mlw[16 * NF + ln] = make_float2(mpr, l);
+        }
+    }
+    __syncthreads();   // every wave is done with its ring stages, and its (max, sum) are out
+    auto block_ml = [&](int row, float & M, float & L) __attribute__((always_inline)) {
+        M = -INFINITY;
+        L = 0.f;
+#pragma unroll
+        for (int w2 = 0; w2 < VD_WAVES; w2++) M = xmax(M, ((const float2 *) &stab[w2][0][0])[row].x);
+#pragma unroll
+        for (int w2 = 0; w2 < VD_WAVES; w2++) {
+            const float2 e = ((const float2 *) &stab[w2][0][0])[row];
+            L += e.x == -INFINITY ? 0.f : e.y * __builtin_amdgcn_exp2f(e.x - M);
+        }
+    };
+    if constexpr (NF) {
+        float M, L;
+        block_ml(ln, M, L);
+        const float fw = mfr == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mfr - M);
+#pragma unroll
+        for (int bb = 0; bb < NBLK; bb++) { Of[bb][0] *= fw; Of[bb][1] *= fw; }
+    }
+    if constexpr (PK) {
+        float M, L;
+        block_ml(16 * NF + (ln & 7), M, L);
+        const float fw = mpr == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mpr - M);
+#pragma unroll
+        for (int bb = 0; bb < NBLK; bb++) { Op[bb][0] *= fw; Op[bb][1] *= fw; }
+    }
+    // buffer rows: the full tile's column c at row c, the packed tile's at 16 NF + c
+    float * ob = (float *) &kvr[0][0][0][0];
+    int tid_e = (int) threadIdx.x;
+    asm volatile("" : "+v"(tid_e));
+    const int ln_e = tid_e & 15, lg_e = (tid_e >> 4) & 3;
+    auto dump = [&](float * buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int bb = 0; bb < NBLK; bb++) {
+            if constexpr (NF) {
+                float * d = buf + ln_e * VD_OBS + 32 * bb + 8 * lg_e;
+                *(float4 *) d = make_float4(Of[bb][0][0], Of[bb][1][0], Of[bb][0][1], Of[bb][1][1]);
+                *(float4 *) (d + 4) = make_float4(Of[bb][0][2], Of[bb][1][2], Of[bb][0][3], Of[bb][1][3]);
+            }
+            if constexpr (PK) {
+                float * d = buf + (16 * NF + ln_e) * VD_OBS + 32 * bb + 8 * lg_e;
+                *(float4 *) d = make_float4(Op[bb][0][0], Op[bb][1][0], Op[bb][0][1], Op[bb][1][1]);
+                *(float4 *) (d + 4) = make_float4(Op[bb][0][2], Op[bb][1][2], Op[bb][0][3], Op[bb][1][3]);
+            }
+        }
+    };
+    auto add = [&](const float * buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int bb = 0; bb < NBLK; bb++) {
+            if constexpr (NF) {
+                const float * d = buf + ln_e * VD_OBS + 32 * bb + 8 * lg_e;
+                const float4 x0 = *(const float4 *) d, x1 = *(const float4 *) (d + 4);
+                Of[bb][0][0] += x0.x; Of[bb][1][0] += x0.y; Of[bb][0][1] += x0.z; Of[bb][1][1] += x0.w;
+                Of[bb][0][2] += x1.x; Of[bb][1][2] += x1.y; Of[bb][0][3] += x1.z; Of[bb][1][3] += x1.w;
+            }
+            if constexpr (PK) {
+                const float * d = buf + (16 * NF + ln_e) * VD_OBS + 32 * bb + 8 * lg_e;
+                const float4 x0 = *(const float4 *) d, x1 = *(const float4 *) (d + 4);
+                Op[bb][0][0] += x0.x; Op[bb][1][0] += x0.y; Op[bb][0][1] += x0.z; Op[bb][1][1] += x0.w;
+                Op[bb][0][2] += x1.x; Op[bb][1][2] += x1.y; Op[bb][0][3] += x1.z; Op[bb][1][3] += x1.w;
+            }
+        }
+    };
+    if (wave >= VD_WAVES / 2) dump(ob + (wave - VD_WAVES / 2) * VD_OBUF);
+    __syncthreads();
+    if (wave < VD_WAVES / 2) {
+        add(ob + wave * VD_OBUF);
+        dump(ob + wave * VD_OBUF);
+    }
+    __syncthreads();
+    if constexpr (GATHER) {
+        if (threadIdx.x == 0 && g_bad && a.status) atomicOr(a.status, DEVERR_GET_ROWS_INDEX);
+    }
+    // ---- the block's rows: thread (row, q) adds dims 16q .. 16q + 15 of the
+    //      four buffers (and both columns of a packed row) ----
+    const int frow = tid_e >> 4, fq = tid_e & 15;
+    if (frow >= RW) return;
+    const bool prow = frow >= 16 * NF;
+    const int br = prow ? 16 * NF + (frow - 16 * NF) : frow;
+    float4 acc[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) acc[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int w4 = 0; w4 < VD_WAVES / 2; w4++) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float4 x = *(const float4 *) (ob + w4 * VD_OBUF + br * VD_OBS + 16 * fq + 4 * c);
+            acc[c].x += x.x; acc[c].y += x.y; acc[c].z += x.z; acc[c].w += x.w;
+        }
+        if (prow) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const float4 x = *(const float4 *) (ob + w4 * VD_OBUF + (br + 8) * VD_OBS + 16 * fq + 4 * c);
+                acc[c].x += x.x; acc[c].y += x.y; acc[c].z += x.z; acc[c].w += x.w;
+            }
+        }
+    }
+    float M, L;
+    block_ml(frow, M, L);
+    const size_t bh = (size_t) b * a.nh_kv + kvh;
+    const int tq = (int) div_gqa(a, (uint32_t) frow), h = kvh * a.gqa + (frow - tq * a.gqa);
+    if (a.ns > 1) {
+        float * out = a.part_o + ((bh * a.ns + split) * a.R + frow) * D + 16 * fq;
+#pragma unroll
+        for (int c = 0; c < 4; c++) store_nt4(out + 4 * c, acc[c]);
+        if (fq == 0) {
+            float2 * mlp = &a.part_ml[(bh * a.ns + split) * a.R + frow];
+            __builtin_nontemporal_store(M, &mlp->x);
+            __builtin_nontemporal_store(L, &mlp->y);
+        }
+    } else {
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        float * out = a.dst + (((size_t) b * a.T + tq) * a.nh + h) * D + 16 * fq;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float4 o = make_float4(acc[c].x * inv, acc[c].y * inv, acc[c].z * inv, acc[c].w * inv);
+            if (a.dst_vec) {
+                *(float4 *) (out + 4 * c) = apply_gate(a, out + 4 * c, o);
+            } else {
+                float * p = out + 4 * c;
+                p[0] = o.x; p[1] = o.y; p[2] = o.z; p[3] = o.w;
+            }
+        }
+    }
+}
+
 // ================================================================ prefill
 //
 // k_fa_pre: long query blocks (more than 32 query rows per KV head: prefill
@@ -2406,6 +3269,7 @@ __global__ __launch_bounds__(PRE_WAVES * 64, 2) void k_fa_pre(fa_args a) {
 
 // Attention kernel shapes: waves per block, query tiles, keys per wave.
 enum fa_kind {
+    FA_VD,        // k_fa_vd: at most 24 query rows per KV head, 8 waves, one block per CU, 32-key steps
     FA_DEC,       // k_fa_dec: at most 32 query rows per KV head, 8 waves, one block per CU
     FA_PRE,       // k_fa_pre: longer query blocks, mask shared by the heads (or none), GQA >= 4
     FA_P4_T1,     // 4 waves, one tile, 64-key chunks, two blocks per CU
@@ -2428,6 +3292,12 @@ struct fa_plan {
 // A forced key-split count for later calls (0: the planner's choice); set by
 // qwfn_fattn_force_splits, read once per call.
 std::atomic<int32_t> g_force_splits{0};
+// A forced kernel family (QWFN_FA_KERNEL_*, 0: the planner's choice); set by
+// qwfn_fattn_force_kernel, read once per call.
+std::atomic<int32_t> g_force_kernel{0};
+// The attention kernel the calling thread's last attention call launched
+// (qwfn_fattn_last_kernel).
+thread_local const char * g_last_kernel = "";
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
@@ -2452,6 +3322,15 @@ int check_no_scratch() {
                                (const void *) k_fa_dec<1, false, true, false>, (const void *) k_fa_dec<1, true, true, false>,
                                (const void *) k_fa_dec<2, false, true, false>, (const void *) k_fa_dec<2, true, true, false>,
                                (const void *) k_fa_dec<1, false, false, true>, (const void *) k_fa_dec<2, false, false, true>,
+                               (const void *) k_fa_vd<0, 1, false, false, false>, (const void *) k_fa_vd<0, 1, true, false, false>,
+                               (const void *) k_fa_vd<0, 1, false, true, false>, (const void *) k_fa_vd<0, 1, true, true, false>,
+                               (const void *) k_fa_vd<0, 1, false, false, true>,
+                               (const void *) k_fa_vd<1, 0, false, false, false>, (const void *) k_fa_vd<1, 0, true, false, false>,
+                               (const void *) k_fa_vd<1, 0, false, true, false>, (const void *) k_fa_vd<1, 0, true, true, false>,
+                               (const void *) k_fa_vd<1, 0, false, false, true>,
+                               (const void *) k_fa_vd<1, 1, false, false, false>, (const void *) k_fa_vd<1, 1, true, false, false>,
+                               (const void *) k_fa_vd<1, 1, false, true, false>, (const void *) k_fa_vd<1, 1, true, true, false>,
+                               (const void *) k_fa_vd<1, 1, false, false, true>,
                                (const void *) k_fa_pre<false>, (const void *) k_fa_pre<true>,
                                (const void *) k_fattn_q8_0<2, true, WAVES, 16, false>,
                                (const void *) k_fattn_q8_0<1, false, WAVES_PAIR, 16, false>,
@@ -2530,7 +3409,35 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
     const int64_t B = q->ne[3];
     const bool dec = R <= 32;
     pl->kind = dec ? FA_DEC : rw == 16 ? FA_P4_T1 : FA_P4_T2;
-    if (!dec && !gather && !seq_n_kv && (!mask || mask->ne[2] == 1) && gqa >= 4) {
+    // k_fa_vd: up to 24 rows (a full and a packed tile), K and V rows of one
+    // stride, and a mask shared by the heads over at most VD_MROWS query
+    // positions (its granules travel with each step)
+    const bool vd_ok = dec && R <= VD_ROWS && k->nb[1] == v->nb[1] &&
+                       (!mask || (mask->ne[2] == 1 && (R - 1) / gqa + 1 <= VD_MROWS));
+    const bool pre_ok = !dec && !gather && !seq_n_kv && (!mask || mask->ne[2] == 1) && gqa >= 4;
+    const int32_t fk = g_force_kernel.load(std::memory_order_relaxed);
+    switch (fk) {
+        case QWFN_FA_KERNEL_VD:
+            if (!vd_ok) return set_error(QWFN_ENOTSUP, "flash_attn_ext: the forced VD kernel cannot take this shape");
+            break;
+        case QWFN_FA_KERNEL_DEC:
+            if (!dec) return set_error(QWFN_ENOTSUP, "flash_attn_ext: the forced DEC kernel takes at most 32 rows per KV head");
+            break;
+        case QWFN_FA_KERNEL_GENERAL:
+            if (gather) return set_error(QWFN_ENOTSUP, "flash_attn_ext: the forced GENERAL kernel takes no cell lists");
+            pl->kind = rw == 16 ? FA_P4_T1 : FA_P4_T2;
+            break;
+        case QWFN_FA_KERNEL_PRE:
+            if (!pre_ok) return set_error(QWFN_ENOTSUP, "flash_attn_ext: the forced PRE kernel cannot take this shape");
+            break;
+        default:
+            break;
+    }
+    // k_fa_vd measures slower than k_fa_dec at every depth so far (its
+    // prologue and epilogue cost more than its steps save): callers reach it
+    // only by forcing it
+    if (vd_ok && fk == QWFN_FA_KERNEL_VD) pl->kind = FA_VD;
+    if (pre_ok && (fk == QWFN_FA_KERNEL_AUTO || fk == QWFN_FA_KERNEL_PRE)) {
         // k_fa_pre: 128-row blocks; key splits of whole 64-key chunks (at least
         // two per split), about one block per CU; the row groups of a (batch,
         // KV head, split) unit share an XCD
@@ -2562,34 +3469,60 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
         pl->ws_bytes = std::max<size_t>(off, 256);
         return QWFN_OK;
     }
+    const bool vd = pl->kind == FA_VD, kdec = pl->kind == FA_DEC;
     pl->R = (int32_t) R;
-    pl->rw = rw;
-    pl->RT = rw / 16;
-    pl->n_rg = (int32_t) ((R + rw - 1) / rw);
+    pl->rw = vd ? VD_ROWS : rw;
+    pl->RT = vd ? 1 : rw / 16;
+    pl->n_rg = vd ? 1 : (int32_t) ((R + rw - 1) / rw);
     pl->gqa = (int32_t) gqa;
-    // k_fa_dec: splits of whole 16-key tiles, at least one tile per key group;
+    // k_fa_vd: splits of whole 16-key sub-tiles, at least one per wave;
+    // k_fa_dec: whole 16-key tiles, at least one tile per key group;
     // k_fattn_q8_0: whole chunks.
-    const int64_t ck = dec ? DEC_TK : pl->kind == FA_P4_T1 ? fa_cfg<1, false, WAVES_PAIR, 16>::CK : fa_cfg<2, false, WAVES_PAIR, 32>::CK;
-    const int64_t min_split = dec ? DEC_TK * (DEC_WAVES / pl->RT) : ck;
-    // Splits: about one block per CU slot (256 for k_fa_dec, 512 otherwise).
-    const int64_t target_blocks = dec ? 256 : 512;
+    const int64_t ck = vd ? DEC_TK : kdec ? DEC_TK
+                     : pl->kind == FA_P4_T1 ? fa_cfg<1, false, WAVES_PAIR, 16>::CK : fa_cfg<2, false, WAVES_PAIR, 32>::CK;
+    const int64_t min_split = vd ? DEC_TK * VD_WAVES : kdec ? DEC_TK * (DEC_WAVES / pl->RT) : ck;
+    // Splits: about one block per CU slot (256 for the one-block-per-CU
+    // kernels, 512 otherwise).
+    const int64_t target_blocks = vd || kdec ? 256 : 512;
     int64_t ns = std::max<int64_t>(1, target_blocks / std::max<int64_t>(1, nh_kv * B * pl->n_rg));
-    ns = std::min<int64_t>(ns, std::max<int64_t>(1, (n_kv + min_split - 1) / min_split));
-    if (const int32_t force = g_force_splits.load(std::memory_order_relaxed)) ns = force;
+    if (vd) ns = std::min<int64_t>(ns, std::max<int64_t>(1, n_kv / min_split));
+    else    ns = std::min<int64_t>(ns, std::max<int64_t>(1, (n_kv + min_split - 1) / min_split));
+    const int32_t forced_ns = g_force_splits.load(std::memory_order_relaxed);
+    if (forced_ns) ns = forced_ns;
     ns = std::min<int64_t>(ns, std::max<int64_t>(1, ns_cap));
-    // Splits are whole chunks. When the keys exceed two or more chunks per
-    // split by less than one chunk (n_kv = 2^k + T), the last split takes the
-    // rest; otherwise every split rounds up and there are fewer.
     if (gather) {
         // gathered keys: a block's cells fit its LDS list
-        if (!dec) return set_error(QWFN_ENOTSUP, "flash_attn_ext_cells: at most 32 query rows per KV head (T * n_head / n_head_kv)");
+        if (!vd && !kdec) return set_error(QWFN_ENOTSUP, "flash_attn_ext_cells: at most 32 query rows per KV head (T * n_head / n_head_kv)");
         ns = std::max<int64_t>(ns, (n_kv + DEC_GATHER_SPLIT - 1) / DEC_GATHER_SPLIT);
     }
-    int64_t split_len = n_kv / (ns * ck) * ck;
-    if (gather || split_len < (dec ? min_split : 2 * ck) || n_kv - ns * split_len >= (dec ? min_split : ck)) {
-        split_len = (n_kv + ns - 1) / ns;
-        split_len = std::max<int64_t>(ck, (split_len + ck - 1) / ck * ck);
+    int64_t split_len;
+    if (vd && !gather) {
+        // The slowest wave of a split of s sub-tiles takes ceil(s / 8) of
+        // them: pairs as steps, an odd one as a half step. The fewest
+        // sub-tiles per split with every block on a CU of its own (the last
+        // split takes what is left, fewer keys) give the shortest slowest
+        // wave; a forced split count takes the sub-tiles that it implies.
+        const int64_t per = std::max<int64_t>(1, nh_kv * B);
+        int64_t sub = std::max<int64_t>(VD_WAVES, (n_kv + ck * ns - 1) / (ck * ns));
+        if (!forced_ns)
+            while ((n_kv + ck * sub - 1) / (ck * sub) * per > target_blocks) sub++;
+        split_len = ck * sub;
         ns = std::max<int64_t>(1, (n_kv + split_len - 1) / split_len);
+        if (ns > ns_cap) {
+            split_len = (n_kv + ns_cap - 1) / ns_cap;
+            split_len = (split_len + ck - 1) / ck * ck;
+            ns = std::max<int64_t>(1, (n_kv + split_len - 1) / split_len);
+        }
+    } else {
+        // Splits are whole chunks. When the keys exceed two or more chunks per
+        // split by less than one chunk (n_kv = 2^k + T), the last split takes the
+        // rest; otherwise every split rounds up and there are fewer.
+        split_len = n_kv / (ns * ck) * ck;
+        if (gather || split_len < (kdec ? min_split : 2 * ck) || n_kv - ns * split_len >= (kdec ? min_split : ck)) {
+            split_len = (n_kv + ns - 1) / ns;
+            split_len = std::max<int64_t>(ck, (split_len + ck - 1) / ck * ck);
+            ns = std::max<int64_t>(1, (n_kv + split_len - 1) / split_len);
+        }
     }
     // keys of the longest split (the last may be longer), rounded up to whole chunks
     pl->max_span = std::max<int64_t>(split_len, n_kv - (ns - 1) * split_len);
@@ -2607,7 +3540,9 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
                 return set_error(QWFN_ERANGE, "flash_attn_ext_seq: sequence key counts must lie in [0, n_kv]");
             total += seq_n_kv[b];
         }
-        const int64_t units = std::max<int64_t>(1, std::min<int64_t>(target_blocks / std::max<int64_t>(1, nh_kv * pl->n_rg),
+        // (a forced split count asks for that many splits per sequence on average)
+        const int64_t units = std::max<int64_t>(1, std::min<int64_t>(forced_ns ? forced_ns * B
+                                                                               : target_blocks / std::max<int64_t>(1, nh_kv * pl->n_rg),
                                                                      ns_cap * B));
         int64_t ns_max = 1, span = ck, ustart = 0;
         for (int64_t b = 0; b < B; b++) {
@@ -2729,6 +3664,31 @@ struct fa_gather {
     int64_t pos0;
     int64_t n_rows;            // rows of the cache
 };
+
+// Launch of an attention kernel of the fa_args `a` in scope, recording its
+// name for qwfn_fattn_last_kernel.
+#define QWFN_FA_LAUNCH(G, BD, ST, ...)                              \
+    do {                                                            \
+        g_last_kernel = #__VA_ARGS__;                               \
+        hipLaunchKernelGGL((__VA_ARGS__), G, BD, 0, ST, a);         \
+    } while (0)
+
+// k_fa_vd with NF full and PK packed tiles, by mask, per-sequence counts and cell lists
+template <int NF, int PK, bool M, bool RG, bool G>
+void launch_vd1(const fa_args & a, dim3 g, hipStream_t st) {
+    static const std::string name = "k_fa_vd<" + std::to_string(NF) + ", " + std::to_string(PK) + ", " +
+                                    (M ? "true" : "false") + ", " + (RG ? "true" : "false") + ", " + (G ? "true" : "false") + ">";
+    g_last_kernel = name.c_str();
+    hipLaunchKernelGGL((k_fa_vd<NF, PK, M, RG, G>), g, dim3(VD_WAVES * 64), 0, st, a);
+}
+template <int NF, int PK>
+void launch_vd(const fa_args & a, bool msk, bool rg, bool gat, dim3 g, hipStream_t st) {
+    if (gat)      launch_vd1<NF, PK, false, false, true>(a, g, st);
+    else if (rg)  { if (msk) launch_vd1<NF, PK, true, true, false>(a, g, st);
+                    else     launch_vd1<NF, PK, false, true, false>(a, g, st); }
+    else          { if (msk) launch_vd1<NF, PK, true, false, false>(a, g, st);
+                    else     launch_vd1<NF, PK, false, false, false>(a, g, st); }
+}
 
 int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v, const qwfn_tensor * mask, float scale,
               float max_bias, float logit_softcap, const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes,
@@ -2852,8 +3812,8 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
         a.ns_mul = recip32(a.ns);
         a.nrg_mul = recip32(a.n_rg);
         const dim3 g((unsigned) grid), bd(PRE_WAVES * 64);
-        if (a.mask) hipLaunchKernelGGL((k_fa_pre<true>), g, bd, 0, as_stream(stream), a);
-        else        hipLaunchKernelGGL((k_fa_pre<false>), g, bd, 0, as_stream(stream), a);
+        if (a.mask) QWFN_FA_LAUNCH(g, bd, as_stream(stream), k_fa_pre<true>);
+        else        QWFN_FA_LAUNCH(g, bd, as_stream(stream), k_fa_pre<false>);
         if (int rc = hip_check(hipGetLastError(), "flash_attn launch")) return rc;
         if (a.ns > 1) {
             const int64_t rows = (int64_t) a.B * a.nh_kv * a.R;
@@ -2866,7 +3826,7 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
         }
         return QWFN_OK;
     }
-    if (pl.kind == FA_DEC) a.n_rg = 1;
+    if (pl.kind == FA_DEC || pl.kind == FA_VD) a.n_rg = 1;
     const int64_t n_units = a.ragged ? (int64_t) a.r_units : (int64_t) a.B * a.ns;
     const int64_t units = n_units >= 8 ? (n_units + 7) / 8 * 8 : n_units;
     const int64_t hgn = (int64_t) a.nh_kv * a.n_rg;
@@ -2880,13 +3840,19 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
     hipStream_t st = as_stream(stream);
     const bool mt = a.mask_mode == MASK_TILE;
     const dim3 g((unsigned) grid), b8(WAVES * 64), b4(WAVES_PAIR * 64);
-    if (pl.kind == FA_DEC) {
+    if (pl.kind == FA_VD) {
+        // tiles: a packed one for up to 8 rows, a full one for up to 16, both for up to 24
+        const bool msk = a.mask != nullptr;
+        if (a.R <= 8)       launch_vd<0, 1>(a, msk, a.ragged != 0, gat != nullptr, g, st);
+        else if (a.R <= 16) launch_vd<1, 0>(a, msk, a.ragged != 0, gat != nullptr, g, st);
+        else                launch_vd<1, 1>(a, msk, a.ragged != 0, gat != nullptr, g, st);
+    } else if (pl.kind == FA_DEC) {
         const dim3 bd(DEC_WAVES * 64);
         const bool msk = a.mask != nullptr;
-#define QWFN_DEC(RT_, M_, RG_) hipLaunchKernelGGL((k_fa_dec<RT_, M_, RG_, false>), g, bd, 0, st, a)
+#define QWFN_DEC(RT_, M_, RG_) QWFN_FA_LAUNCH(g, bd, st, k_fa_dec<RT_, M_, RG_, false>)
         if (gat) {
-            if (pl.RT == 1) hipLaunchKernelGGL((k_fa_dec<1, false, false, true>), g, bd, 0, st, a);
-            else            hipLaunchKernelGGL((k_fa_dec<2, false, false, true>), g, bd, 0, st, a);
+            if (pl.RT == 1) QWFN_FA_LAUNCH(g, bd, st, k_fa_dec<1, false, false, true>);
+            else            QWFN_FA_LAUNCH(g, bd, st, k_fa_dec<2, false, false, true>);
         } else if (pl.RT == 1) {
             if (a.ragged) { if (msk) QWFN_DEC(1, true, true); else QWFN_DEC(1, false, true); }
             else          { if (msk) QWFN_DEC(1, true, false); else QWFN_DEC(1, false, false); }
@@ -2899,13 +3865,13 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
         // per-sequence splits: the 4-wave kernels (and the 8-wave mask-tile one)
         switch (pl.kind) {
             case FA_P4_T1:
-                if (mt) hipLaunchKernelGGL((k_fattn_q8_0<1, true, WAVES_PAIR, 16, true>), g, b4, 0, st, a);
-                else    hipLaunchKernelGGL((k_fattn_q8_0<1, false, WAVES_PAIR, 16, true>), g, b4, 0, st, a);
+                if (mt) QWFN_FA_LAUNCH(g, b4, st, k_fattn_q8_0<1, true, WAVES_PAIR, 16, true>);
+                else    QWFN_FA_LAUNCH(g, b4, st, k_fattn_q8_0<1, false, WAVES_PAIR, 16, true>);
                 break;
             default:
-                if (mt && mrows > MASK_ROWS_PAIR) hipLaunchKernelGGL((k_fattn_q8_0<2, true, WAVES, 16, true>), g, b8, 0, st, a);
-                else if (mt) hipLaunchKernelGGL((k_fattn_q8_0<2, true, WAVES_PAIR, 32, true>), g, b4, 0, st, a);
-                else    hipLaunchKernelGGL((k_fattn_q8_0<2, false, WAVES_PAIR, 32, true>), g, b4, 0, st, a);
+                if (mt && mrows > MASK_ROWS_PAIR) QWFN_FA_LAUNCH(g, b8, st, k_fattn_q8_0<2, true, WAVES, 16, true>);
+                else if (mt) QWFN_FA_LAUNCH(g, b4, st, k_fattn_q8_0<2, true, WAVES_PAIR, 32, true>);
+                else    QWFN_FA_LAUNCH(g, b4, st, k_fattn_q8_0<2, false, WAVES_PAIR, 32, true>);
                 break;
         }
     } else {
@@ -2914,16 +3880,16 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
         case FA_PRE:
             break;
         case FA_P4_T1:
-            if (mt) hipLaunchKernelGGL((k_fattn_q8_0<1, true, WAVES_PAIR, 16, false>), g, b4, 0, st, a);
-            else    hipLaunchKernelGGL((k_fattn_q8_0<1, false, WAVES_PAIR, 16, false>), g, b4, 0, st, a);
+            if (mt) QWFN_FA_LAUNCH(g, b4, st, k_fattn_q8_0<1, true, WAVES_PAIR, 16, false>);
+            else    QWFN_FA_LAUNCH(g, b4, st, k_fattn_q8_0<1, false, WAVES_PAIR, 16, false>);
             break;
         case FA_P4_T2:
             // mask tiles of at most MASK_ROWS_PAIR rows fit next to two stages;
             // more rows (per-head masks, small gqa) take the 8-wave kernel over
             // the same 64-key chunks
-            if (mt && mrows > MASK_ROWS_PAIR) hipLaunchKernelGGL((k_fattn_q8_0<2, true, WAVES, 16, false>), g, b8, 0, st, a);
-            else if (mt) hipLaunchKernelGGL((k_fattn_q8_0<2, true, WAVES_PAIR, 32, false>), g, b4, 0, st, a);
-            else    hipLaunchKernelGGL((k_fattn_q8_0<2, false, WAVES_PAIR, 32, false>), g, b4, 0, st, a);
+            if (mt && mrows > MASK_ROWS_PAIR) QWFN_FA_LAUNCH(g, b8, st, k_fattn_q8_0<2, true, WAVES, 16, false>);
+            else if (mt) QWFN_FA_LAUNCH(g, b4, st, k_fattn_q8_0<2, true, WAVES_PAIR, 32, false>);
+            else    QWFN_FA_LAUNCH(g, b4, st, k_fattn_q8_0<2, false, WAVES_PAIR, 32, false>);
             break;
     }
     }
@@ -3057,4 +4023,13 @@ extern "C" int qwfn_flash_attn_ext_q8_0_append(const qwfn_tensor * q, const qwfn
 
 extern "C" void qwfn_fattn_force_splits(int32_t n_splits) {
     g_force_splits.store(n_splits > 0 ? std::min<int32_t>(n_splits, MAX_SPLITS) : 0, std::memory_order_relaxed);
+}
+
+extern "C" void qwfn_fattn_force_kernel(int32_t kind) {
+    g_force_kernel.store(kind >= QWFN_FA_KERNEL_AUTO && kind <= QWFN_FA_KERNEL_PRE ? kind : QWFN_FA_KERNEL_AUTO,
+                         std::memory_order_relaxed);
+}
+
+extern "C" const char * qwfn_fattn_last_kernel(void) {
+    return g_last_kernel;
 }

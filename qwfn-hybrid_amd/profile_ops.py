@@ -33,12 +33,18 @@ def main() -> int:
     ap.add_argument("--mb", type=int, default=1024)
     ap.add_argument("--lib", default=None, help="library path (default: the package's build)")
     ap.add_argument("--append", action="store_true", help="verify: append the T new K/V rows in the same launch")
+    ap.add_argument("--kernel", choices=["auto", "vd", "dec", "general"], default="auto",
+                    help="attention ops: the kernel family to force (qwfn_fattn_force_kernel)")
+    ap.add_argument("--splits", type=int, default=0, help="attention ops: a forced key-split count (0: the planner's)")
     a = ap.parse_args()
     import numpy as np
     import torch
 
     import qwfn_kv as K
     K.check((K.load(a.lib) if a.lib else K.load()).qwfn_init(0))
+    K.load().qwfn_fattn_force_kernel({"auto": K.FA_KERNEL_AUTO, "vd": K.FA_KERNEL_VD, "dec": K.FA_KERNEL_DEC,
+                                      "general": K.FA_KERNEL_GENERAL}[a.kernel])
+    K.load().qwfn_fattn_force_splits(a.splits)
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev)
     gen.manual_seed(5)
@@ -165,10 +171,15 @@ def main() -> int:
         run = lambda i: K.qsa_pool_rebuild(ic, a.depth, 4, knw, pool)
     run(0)
     torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
     for i in range(a.reps):
         run(i + 1)
+    e1.record()
     torch.cuda.synchronize()
-    print(f"{a.op}: {a.reps} launches done", flush=True)
+    kname = K.last_kernel() if a.op in ("verify", "prefill", "cells") else ""
+    print(f"{a.op}: {a.reps} launches done, {e0.elapsed_time(e1) * 1e3 / a.reps:.2f} us per launch (event time) {kname}",
+          flush=True)
     return 0
 
 

@@ -29,6 +29,29 @@ OK, EINVAL, ERANGE, EALIGN, ENOTSUP, EDEVICE, ENOMEM, ESIZE = 0, -1, -2, -3, -4,
 DEVERR_SET_ROWS_INDEX = 1
 DEVERR_GET_ROWS_INDEX = 2
 
+# attention kernel families (qwfn_fattn_force_kernel)
+FA_KERNEL_AUTO, FA_KERNEL_VD, FA_KERNEL_DEC, FA_KERNEL_GENERAL, FA_KERNEL_PRE = 0, 1, 2, 3, 4
+
+
+def last_kernel() -> str:
+    """The attention kernel instantiation this thread's last attention call launched."""
+    return load().qwfn_fattn_last_kernel().decode()
+
+
+class forced_kernel:
+    """Context manager: later attention calls in this process use kernel family `kind`
+    (FA_KERNEL_*) while it is active."""
+    def __init__(self, kind: int):
+        self.kind = kind
+
+    def __enter__(self):
+        load().qwfn_fattn_force_kernel(self.kind)
+        return self
+
+    def __exit__(self, *exc):
+        load().qwfn_fattn_force_kernel(FA_KERNEL_AUTO)
+        return False
+
 
 class QwfnError(RuntimeError):
     def __init__(self, code: int, msg: str):
@@ -89,7 +112,7 @@ class QsaPoolCfg(ctypes.Structure):
 EXPORTS = [
     "qwfn_abi_version", "qwfn_last_error", "qwfn_init", "qwfn_device_status",
     "qwfn_set_rows_q8_0", "qwfn_cpy_f32_q8_0", "qwfn_set_rows_q8_0_kv", "qwfn_cpy_f32_q8_0_kv", "qwfn_get_rows_i32", "qwfn_kv_gather_segments",
-    "qwfn_fattn_workspace_size", "qwfn_fattn_force_splits", "qwfn_flash_attn_ext_q8_0", "qwfn_flash_attn_ext_q8_0_noalloc", "qwfn_flash_attn_ext_q8_0_append",
+    "qwfn_fattn_workspace_size", "qwfn_fattn_force_splits", "qwfn_fattn_force_kernel", "qwfn_fattn_last_kernel", "qwfn_flash_attn_ext_q8_0", "qwfn_flash_attn_ext_q8_0_noalloc", "qwfn_flash_attn_ext_q8_0_append",
     "qwfn_fattn_workspace_size_seq", "qwfn_flash_attn_ext_q8_0_seq", "qwfn_state_restore",
     "qwfn_fattn_workspace_size_cells", "qwfn_flash_attn_ext_q8_0_cells", "qwfn_kv_produce_q8_0",
     "qwfn_flash_attn_ext_q8_0_gated",
@@ -137,6 +160,10 @@ def load(path: str = LIB_PATH):
                                                    ctypes.c_int, vp]
     L.qwfn_fattn_force_splits.argtypes = [i32]
     L.qwfn_fattn_force_splits.restype = None
+    L.qwfn_fattn_force_kernel.argtypes = [i32]
+    L.qwfn_fattn_force_kernel.restype = None
+    L.qwfn_fattn_last_kernel.argtypes = []
+    L.qwfn_fattn_last_kernel.restype = ctypes.c_char_p
     L.qwfn_flash_attn_ext_q8_0.argtypes = [T, T, T, T, ctypes.c_float, ctypes.c_float, ctypes.c_float, T,
                                            ctypes.c_int, vp, sz, vp]
     PL = ctypes.POINTER(i64)
@@ -212,9 +239,10 @@ def load(path: str = LIB_PATH):
     L.qwfn_qsa_select_cells.argtypes = [vp, sz, i64, vp, i32, sz, vp, sz, i32, i32, vp, i32, vp, vp, vp, sz, vp]
     for name in EXPORTS:
         if name not in ("qwfn_state_config_default", "qwfn_state_destroy", "qwfn_snap_pool_destroy",
-                        "qwfn_fattn_force_splits"):
+                        "qwfn_fattn_force_splits", "qwfn_fattn_force_kernel", "qwfn_fattn_last_kernel"):
             getattr(L, name).restype = getattr(L, name).restype or ctypes.c_int
     L.qwfn_last_error.restype = ctypes.c_char_p
+    L.qwfn_fattn_last_kernel.restype = ctypes.c_char_p
     L.qwfn_fattn_workspace_size.restype = sz
     L.qwfn_fattn_workspace_size_seq.restype = sz
     L.qwfn_fattn_workspace_size_cells.restype = sz
