@@ -205,6 +205,25 @@ void qwfn_fattn_force_kernel(int32_t kind);
  * in the reference. */
 const char * qwfn_fattn_last_kernel(void);
 
+/* Force how later calls merge their key splits (any thread): AUTO lets the
+ * planner choose (today the merge launch, which measures faster), FUSED
+ * merges inside k_fa_dec / k_fa_vd (the last blocks of each (batch, KV head)
+ * to finish fold all of its splits; other kernels, and batches of several
+ * depths, still use a merge launch), KERNEL always launches the separate
+ * merge kernel. qwfn_fattn_last_merge reports what the
+ * calling thread's last attention call did (NONE: one split, nothing to
+ * merge). For parity tests of both merge paths and for A/B timing; results
+ * do not depend on it beyond float rounding. No counterpart in the reference
+ * (ggml's CPU kernel keeps one partial per thread chunk). */
+enum {
+    QWFN_FA_MERGE_AUTO   = 0,
+    QWFN_FA_MERGE_FUSED  = 1,
+    QWFN_FA_MERGE_KERNEL = 2,
+    QWFN_FA_MERGE_NONE   = 3
+};
+void    qwfn_fattn_force_merge(int32_t mode);
+int32_t qwfn_fattn_last_merge(void);
+
 /* Batched decode over sequences of different depths: as
  * qwfn_flash_attn_ext_q8_0, except that sequence b (q batch index) attends
  * only keys [0, seq_n_kv[b]) -- the same result as masking its later keys with

@@ -168,6 +168,13 @@ struct fa_args {
     uint32_t * status;     // device flags (DEVERR_GET_ROWS_INDEX: a cell outside the cache)
     // output gate (or null): dst = attention * sigmoid(gate), gate laid out as dst
     const float * gate;
+    // split merge inside the attention kernel (k_fa_dec, k_fa_vd; null: a
+    // k_fattn_merge launch follows): per (batch, KV head) group two words,
+    // [arrived splits] and [claimed rows], each (call epoch << 16) | count;
+    // m_ebase = this call's epoch << 16; the last m_nm splits to arrive may merge
+    unsigned long long * mctr;
+    unsigned long long m_ebase;
+    int32_t  m_nm;
 };
 
 __device__ __forceinline__ uint32_t div_gqa(const fa_args & a, uint32_t r) {
@@ -393,6 +400,34 @@ __device__ __forceinline__ void store_nt4(float * p, float4 v) {
 __device__ __forceinline__ float4 load_nt4(const float4 * p) {
     const v4f v = __builtin_nontemporal_load((const v4f *) p);
     return make_float4(v[0], v[1], v[2], v[3]);
+}
+
+// Device-scope (sc1) access to the split partials of an in-kernel merge
+// (fa_merge_tail): the cache policy of the compiler's agent-scope relaxed
+// atomics, under which a store is written through to where the loads of every
+// XCD read and a load never returns another XCD's stale L2 copy. So the
+// partials need no L2 write-back on the writer's side and no L2 invalidate on
+// the merger's. Offsets are bytes from the resource's base (below 4 GiB: the
+// host checks the partials' extent).
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+constexpr int CPOL_DEV = 16;   // sc1
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const void * base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, -1, 0x00020000);
+}
+__device__ __forceinline__ void store_dev4(__amdgpu_buffer_rsrc_t r, uint32_t off, float4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v4f{v.x, v.y, v.z, v.w}), r, (int) off, 0, CPOL_DEV);
+}
+__device__ __forceinline__ void store_dev2(__amdgpu_buffer_rsrc_t r, uint32_t off, float2 v) {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u, v), r, (int) off, 0, CPOL_DEV);
+}
+__device__ __forceinline__ float4 load_dev4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const v4f v = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(r, (int) off, 0, CPOL_DEV));
+    return make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ float2 load_dev2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, (int) off, 0, CPOL_DEV));
 }
 
 // f[0 .. n) = 0 (dst is only 4-byte aligned, so plain f32 stores).
@@ -1246,6 +1281,163 @@ __global__ __launch_bounds__(256) void k_fattn_merge_rows(fa_args a) {
     }
 }
 
+// ================================================================ split merge inside the attention kernel
+//
+// Every block of a (batch, KV head) group writes its split's partials, then
+// takes a ticket from the group's arrival word. The block with the last ticket
+// knows that every split is written; it claims rows of the group one at a
+// time from the group's claim word and merges each (the same LSE merge as
+// k_fattn_merge) until none is left. The blocks with the m_nm - 1 tickets
+// before it poll the arrival word for a bounded time: one that sees every
+// split arrive claims rows too, one that does not simply leaves. So no block
+// ever waits for a block that may not be resident, every row is merged once,
+// and the merge costs no launch.
+// Ordering across XCDs: the partials are written and read with device-scope
+// accesses (store_dev4 and friends), and each writer waits until its stores
+// have completed before the block arrives; a merger reads them only after it
+// has seen the last arrival.
+// Counters: one library-owned array (g_merge_ctr), zero when loaded. A call
+// takes consecutive slots of it (one per group) and an epoch from a 48-bit
+// per-device sequence; each word holds (epoch << 16) | count, and the call's
+// first atomic max on a word installs its epoch with count 0, so no word is
+// ever reset. Calls in flight at once get disjoint slots unless more than
+// MERGE_SLOTS groups are in flight.
+
+constexpr int      MERGE_SLOTS    = 16384;            // (batch, KV head) groups in flight at once, at most
+constexpr uint32_t MERGE_SPIN_MAX = 1u << 13;         // polls of a waiting merger (s_sleep 2 each): ~0.4 ms
+__device__ __align__(256) static unsigned long long g_merge_ctr[2 * MERGE_SLOTS];
+
+// LDS of the fused merge (floats): 16 words of tickets, the split weights, a
+// reduction row and 8 x 64 float4 column sums
+constexpr int FMERGE_LDS = 16 + MAX_SPLITS + 16 + 8 * 64 * 4;
+
+// One row r of group (b, kvh) by a block of NT threads: thread t folds
+// float4 column t % 64 of splits t / 64 + (NT / 64) i, 16 partials in flight
+// per batch (the first batch is issued with the (max, sum) loads).
+template <int NT>
+__device__ __forceinline__ void fa_merge_row(const fa_args & a, int b, int kvh, int r, float * sm) {
+    constexpr int NG = NT / 64, MB = 16, MLJ = (MAX_SPLITS + NT - 1) / NT;
+    static_assert(NG <= 8, "column sums hold 8 groups");
+    const int S = a.ns;
+    const int t = (int) threadIdx.x, sg = t >> 6, c = t & 63;
+    const size_t bh = (size_t) b * a.nh_kv + kvh;
+    // the group's partials: (max, sum) of split s at 8 (s R + r), its O row at 4 D (s R + r)
+    const __amdgpu_buffer_rsrc_t mr = dev_rsrc(a.part_ml + bh * a.ns * a.R);
+    const __amdgpu_buffer_rsrc_t orr = dev_rsrc(a.part_o + bh * a.ns * a.R * D);
+    const uint32_t mst = 8u * (uint32_t) a.R, ost = 4u * D * (uint32_t) a.R;
+    const uint32_t m0 = 8u * (uint32_t) r, o0 = 4u * D * (uint32_t) r + 16u * (uint32_t) c;
+    float * wsh = sm + 16;
+    float * red = wsh + MAX_SPLITS;
+    float4 * colsum = (float4 *) (red + 16);
+    float2 e[MLJ];
+#pragma unroll
+    for (int j = 0; j < MLJ; j++) e[j] = load_dev2(mr, m0 + mst * (uint32_t) std::min(t + NT * j, S - 1));
+    float4 ob[MB];
+#pragma unroll
+    for (int i = 0; i < MB; i++) ob[i] = load_dev4(orr, o0 + ost * (uint32_t) std::min(sg + NG * i, S - 1));
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < MLJ; j++) {
+        if (t + NT * j >= S) e[j] = make_float2(-INFINITY, 0.f);
+        mloc = xmax(mloc, e[j].x);
+    }
+    mloc = wave_reduce(mloc, [](float x, float y) { return xmax(x, y); });
+    if ((t & 63) == 0) red[sg] = mloc;
+    __syncthreads();
+    float M = red[0];
+#pragma unroll
+    for (int g = 1; g < NG; g++) M = xmax(M, red[g]);
+    float lpart = 0.f;
+#pragma unroll
+    for (int j = 0; j < MLJ; j++) {
+        const int s = t + NT * j;
+        const float w = e[j].x == -INFINITY ? 0.f : exp2f(e[j].x - M);
+        lpart += w * e[j].y;
+        if (s < S) wsh[s] = w;
+    }
+    lpart = wave_reduce(lpart, [](float x, float y) { return x + y; });
+    if ((t & 63) == 0) red[8 + sg] = lpart;
+    __syncthreads();
+    float L = 0.f;
+#pragma unroll
+    for (int g = 0; g < NG; g++) L += red[8 + g];
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = 0; s0 < S; s0 += NG * MB) {
+        if (s0 > 0) {
+#pragma unroll
+            for (int i = 0; i < MB; i++) ob[i] = load_dev4(orr, o0 + ost * (uint32_t) std::min(s0 + sg + NG * i, S - 1));
+        }
+#pragma unroll
+        for (int i = 0; i < MB; i++) {
+            const int s = s0 + sg + NG * i;
+            const float w = s < S ? wsh[s] : 0.f;
+            acc.x += w * ob[i].x; acc.y += w * ob[i].y; acc.z += w * ob[i].z; acc.w += w * ob[i].w;
+        }
+    }
+    colsum[sg * 64 + c] = acc;
+    __syncthreads();
+    if (sg == 0) {
+        float4 o = colsum[c];
+#pragma unroll
+        for (int g = 1; g < NG; g++) {
+            const float4 x = colsum[g * 64 + c];
+            o.x += x.x; o.y += x.y; o.z += x.z; o.w += x.w;
+        }
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        o.x *= inv; o.y *= inv; o.z *= inv; o.w *= inv;
+        const int tq = (int) div_gqa(a, (uint32_t) r), h = kvh * a.gqa + (r - tq * a.gqa);
+        float * d = a.dst + (((size_t) b * a.T + tq) * a.nh + h) * D + 4 * c;
+        if (a.dst_vec) {
+            *(float4 *) d = apply_gate(a, d, o);
+        } else {
+            d[0] = o.x; d[1] = o.y; d[2] = o.z; d[3] = o.w;
+        }
+    }
+    __syncthreads();   // wsh, red and colsum are the next row's
+}
+
+// The tail of a k_fa_dec / k_fa_vd block of NT threads once its partials are
+// stored (every thread of the block calls it); sm: FMERGE_LDS floats of LDS
+// the block no longer uses.
+template <int NT>
+__device__ void fa_merge_tail(const fa_args & a, int b, int kvh, float * sm) {
+    unsigned long long * arrive = a.mctr + 2 * ((size_t) b * a.nh_kv + kvh);
+    unsigned long long * claim = arrive + 1;
+    const unsigned long long e = a.m_ebase;
+    const int S = a.ns;
+    int * si = (int *) sm;
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);   // this wave's device-scope partial stores have completed
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __hip_atomic_fetch_max(arrive, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int tk = (int) (__hip_atomic_fetch_add(arrive, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 0xFFFFu);
+        int go = tk == S - 1;
+        if (!go && tk >= S - a.m_nm) {
+            for (uint32_t polls = 0; polls < MERGE_SPIN_MAX; polls++) {
+                if (__hip_atomic_load(arrive, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (e | (unsigned) S)) {
+                    go = 1;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+        }
+        if (go) __hip_atomic_fetch_max(claim, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        si[0] = go;
+    }
+    __syncthreads();
+    if (!si[0]) return;
+    for (;;) {
+        __syncthreads();   // every thread has read si[1]
+        if (threadIdx.x == 0)
+            si[1] = (int) (__hip_atomic_fetch_add(claim, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 0xFFFFu);
+        __syncthreads();
+        const int r = si[1];
+        if (r >= a.R) break;
+        fa_merge_row<NT>(a, b, kvh, r, sm);
+    }
+}
+
 // ================================================================ decode / verify
 //
 // k_fa_dec: row groups of at most 32 query rows per KV head (decode, MTP
@@ -1807,52 +1999,64 @@ __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
     if constexpr (GATHER) {
         if (threadIdx.x == 0 && g_bad && a.status) atomicOr(a.status, DEVERR_GET_ROWS_INDEX);
     }
-    if (kg != 0 || rl >= RW) return;
+    if (kg == 0 && rl < RW) {
 #pragma unroll 1
-    for (int k2 = 0; k2 < KG - 1; k2++) {
+        for (int k2 = 0; k2 < KG - 1; k2++) {
+#pragma unroll
+            for (int bb = 0; bb < NBLK; bb++) {
+                const float * src = ob + k2 * ROWS * DEC_OBS + orow + 32 * bb;
+                const float4 x0 = *(const float4 *) src, x1 = *(const float4 *) (src + 4);
+                acc[bb][0].x += x0.x; acc[bb][0].y += x0.y; acc[bb][0].z += x0.z; acc[bb][0].w += x0.w;
+                acc[bb][1].x += x1.x; acc[bb][1].y += x1.y; acc[bb][1].z += x1.z; acc[bb][1].w += x1.w;
+            }
+        }
+        const size_t bh = (size_t) b * a.nh_kv + kvh;
+        const int r = rl;
+        const int tq = (int) div_gqa(a, (uint32_t) r), h = kvh * a.gqa + (r - tq * a.gqa);
+        float * out;
+        float oscale;
+        const bool nsplit = a.ns > 1;
+        if (!nsplit) {
+            out = a.dst + (((size_t) b * a.T + tq) * a.nh + h) * D + 8 * lg_e;
+            oscale = L > 0.f ? 1.f / L : 0.f;
+        } else {
+            out = a.part_o + ((bh * a.ns + split) * a.R + r) * D + 8 * lg_e;
+            oscale = 1.f;
+            if (lg_e == 0) {
+                float2 * mlp = &a.part_ml[(bh * a.ns + split) * a.R + r];
+                if (a.mctr) {
+                    store_dev2(dev_rsrc(a.part_ml), (uint32_t) ((const char *) mlp - (const char *) a.part_ml),
+                               make_float2(M, L));
+                } else {
+                    __builtin_nontemporal_store(M, &mlp->x);
+                    __builtin_nontemporal_store(L, &mlp->y);
+                }
+            }
+        }
+        const __amdgpu_buffer_rsrc_t prs = dev_rsrc(a.part_o);
+        const uint32_t poff = (uint32_t) ((const char *) out - (const char *) a.part_o);
 #pragma unroll
         for (int bb = 0; bb < NBLK; bb++) {
-            const float * src = ob + k2 * ROWS * DEC_OBS + orow + 32 * bb;
-            const float4 x0 = *(const float4 *) src, x1 = *(const float4 *) (src + 4);
-            acc[bb][0].x += x0.x; acc[bb][0].y += x0.y; acc[bb][0].z += x0.z; acc[bb][0].w += x0.w;
-            acc[bb][1].x += x1.x; acc[bb][1].y += x1.y; acc[bb][1].z += x1.z; acc[bb][1].w += x1.w;
+            const float4 p0 = acc[bb][0], p1 = acc[bb][1];
+            const float4 w0 = make_float4(p0.x * oscale, p0.y * oscale, p0.z * oscale, p0.w * oscale);
+            const float4 w1 = make_float4(p1.x * oscale, p1.y * oscale, p1.z * oscale, p1.w * oscale);
+            if (nsplit && a.mctr) {
+                store_dev4(prs, poff + 128 * bb, w0);
+                store_dev4(prs, poff + 128 * bb + 16, w1);
+            } else if (nsplit) {
+                store_nt4(out + 32 * bb, w0);
+                store_nt4(out + 32 * bb + 4, w1);
+            } else if (a.dst_vec) {
+                *(float4 *) (out + 32 * bb) = apply_gate(a, out + 32 * bb, w0);
+                *(float4 *) (out + 32 * bb + 4) = apply_gate(a, out + 32 * bb + 4, w1);
+            } else {
+                float * o = out + 32 * bb;
+                o[0] = w0.x; o[1] = w0.y; o[2] = w0.z; o[3] = w0.w;
+                o[4] = w1.x; o[5] = w1.y; o[6] = w1.z; o[7] = w1.w;
+            }
         }
     }
-    const size_t bh = (size_t) b * a.nh_kv + kvh;
-    const int r = rl;
-    const int tq = (int) div_gqa(a, (uint32_t) r), h = kvh * a.gqa + (r - tq * a.gqa);
-    float * out;
-    float oscale;
-    const bool nsplit = a.ns > 1;
-    if (!nsplit) {
-        out = a.dst + (((size_t) b * a.T + tq) * a.nh + h) * D + 8 * lg_e;
-        oscale = L > 0.f ? 1.f / L : 0.f;
-    } else {
-        out = a.part_o + ((bh * a.ns + split) * a.R + r) * D + 8 * lg_e;
-        oscale = 1.f;
-        if (lg_e == 0) {
-            float2 * mlp = &a.part_ml[(bh * a.ns + split) * a.R + r];
-            __builtin_nontemporal_store(M, &mlp->x);
-            __builtin_nontemporal_store(L, &mlp->y);
-        }
-    }
-#pragma unroll
-    for (int bb = 0; bb < NBLK; bb++) {
-        const float4 p0 = acc[bb][0], p1 = acc[bb][1];
-        const float4 w0 = make_float4(p0.x * oscale, p0.y * oscale, p0.z * oscale, p0.w * oscale);
-        const float4 w1 = make_float4(p1.x * oscale, p1.y * oscale, p1.z * oscale, p1.w * oscale);
-        if (nsplit) {
-            store_nt4(out + 32 * bb, w0);
-            store_nt4(out + 32 * bb + 4, w1);
-        } else if (a.dst_vec) {
-            *(float4 *) (out + 32 * bb) = apply_gate(a, out + 32 * bb, w0);
-            *(float4 *) (out + 32 * bb + 4) = apply_gate(a, out + 32 * bb + 4, w1);
-        } else {
-            float * o = out + 32 * bb;
-            o[0] = w0.x; o[1] = w0.y; o[2] = w0.z; o[3] = w0.w;
-            o[4] = w1.x; o[5] = w1.y; o[6] = w1.z; o[7] = w1.w;
-        }
-    }
+    if (a.mctr) fa_merge_tail<DEC_WAVES * 64>(a, b, kvh, (float *) &ring[0][0][0]);
 }
 
 // ================================================================ decode / verify in 32-key steps
@@ -2659,54 +2863,66 @@ __global__ __launch_bounds__(VD_WAVES * 64, 2) void k_fa_vd(fa_args a) {
     // ---- the block's rows: thread (row, q) adds dims 16q .. 16q + 15 of the
     //      four buffers (and both columns of a packed row) ----
     const int frow = tid_e >> 4, fq = tid_e & 15;
-    if (frow >= RW) return;
-    const bool prow = frow >= 16 * NF;
-    const int br = prow ? 16 * NF + (frow - 16 * NF) : frow;
-    float4 acc[4];
+    if (frow < RW) {
+        const bool prow = frow >= 16 * NF;
+        const int br = prow ? 16 * NF + (frow - 16 * NF) : frow;
+        float4 acc[4];
 #pragma unroll
-    for (int c = 0; c < 4; c++) acc[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int c = 0; c < 4; c++) acc[c] = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int w4 = 0; w4 < VD_WAVES / 2; w4++) {
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const float4 x = *(const float4 *) (ob + w4 * VD_OBUF + br * VD_OBS + 16 * fq + 4 * c);
-            acc[c].x += x.x; acc[c].y += x.y; acc[c].z += x.z; acc[c].w += x.w;
-        }
-        if (prow) {
+        for (int w4 = 0; w4 < VD_WAVES / 2; w4++) {
 #pragma unroll
             for (int c = 0; c < 4; c++) {
-                const float4 x = *(const float4 *) (ob + w4 * VD_OBUF + (br + 8) * VD_OBS + 16 * fq + 4 * c);
+                const float4 x = *(const float4 *) (ob + w4 * VD_OBUF + br * VD_OBS + 16 * fq + 4 * c);
                 acc[c].x += x.x; acc[c].y += x.y; acc[c].z += x.z; acc[c].w += x.w;
             }
-        }
-    }
-    float M, L;
-    block_ml(frow, M, L);
-    const size_t bh = (size_t) b * a.nh_kv + kvh;
-    const int tq = (int) div_gqa(a, (uint32_t) frow), h = kvh * a.gqa + (frow - tq * a.gqa);
-    if (a.ns > 1) {
-        float * out = a.part_o + ((bh * a.ns + split) * a.R + frow) * D + 16 * fq;
+            if (prow) {
 #pragma unroll
-        for (int c = 0; c < 4; c++) store_nt4(out + 4 * c, acc[c]);
-        if (fq == 0) {
+                for (int c = 0; c < 4; c++) {
+                    const float4 x = *(const float4 *) (ob + w4 * VD_OBUF + (br + 8) * VD_OBS + 16 * fq + 4 * c);
+                    acc[c].x += x.x; acc[c].y += x.y; acc[c].z += x.z; acc[c].w += x.w;
+                }
+            }
+        }
+        float M, L;
+        block_ml(frow, M, L);
+        const size_t bh = (size_t) b * a.nh_kv + kvh;
+        const int tq = (int) div_gqa(a, (uint32_t) frow), h = kvh * a.gqa + (frow - tq * a.gqa);
+        if (a.ns > 1) {
+            float * out = a.part_o + ((bh * a.ns + split) * a.R + frow) * D + 16 * fq;
             float2 * mlp = &a.part_ml[(bh * a.ns + split) * a.R + frow];
-            __builtin_nontemporal_store(M, &mlp->x);
-            __builtin_nontemporal_store(L, &mlp->y);
-        }
-    } else {
-        const float inv = L > 0.f ? 1.f / L : 0.f;
-        float * out = a.dst + (((size_t) b * a.T + tq) * a.nh + h) * D + 16 * fq;
+            if (a.mctr) {
+                const __amdgpu_buffer_rsrc_t prs = dev_rsrc(a.part_o);
+                const uint32_t poff = (uint32_t) ((const char *) out - (const char *) a.part_o);
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const float4 o = make_float4(acc[c].x * inv, acc[c].y * inv, acc[c].z * inv, acc[c].w * inv);
-            if (a.dst_vec) {
-                *(float4 *) (out + 4 * c) = apply_gate(a, out + 4 * c, o);
+                for (int c = 0; c < 4; c++) store_dev4(prs, poff + 16 * c, acc[c]);
+                if (fq == 0)
+                    store_dev2(dev_rsrc(a.part_ml), (uint32_t) ((const char *) mlp - (const char *) a.part_ml),
+                               make_float2(M, L));
             } else {
-                float * p = out + 4 * c;
-                p[0] = o.x; p[1] = o.y; p[2] = o.z; p[3] = o.w;
+#pragma unroll
+                for (int c = 0; c < 4; c++) store_nt4(out + 4 * c, acc[c]);
+                if (fq == 0) {
+                    __builtin_nontemporal_store(M, &mlp->x);
+                    __builtin_nontemporal_store(L, &mlp->y);
+                }
+            }
+        } else {
+            const float inv = L > 0.f ? 1.f / L : 0.f;
+            float * out = a.dst + (((size_t) b * a.T + tq) * a.nh + h) * D + 16 * fq;
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const float4 o = make_float4(acc[c].x * inv, acc[c].y * inv, acc[c].z * inv, acc[c].w * inv);
+                if (a.dst_vec) {
+                    *(float4 *) (out + 4 * c) = apply_gate(a, out + 4 * c, o);
+                } else {
+                    float * p = out + 4 * c;
+                    p[0] = o.x; p[1] = o.y; p[2] = o.z; p[3] = o.w;
+                }
             }
         }
     }
+    if (a.mctr) fa_merge_tail<VD_WAVES * 64>(a, b, kvh, ob);
 }
 
 // ================================================================ prefill
@@ -3298,6 +3514,46 @@ std::atomic<int32_t> g_force_kernel{0};
 // The attention kernel the calling thread's last attention call launched
 // (qwfn_fattn_last_kernel).
 thread_local const char * g_last_kernel = "";
+// A forced split-merge path (QWFN_FA_MERGE_*, 0: the planner's choice); set by
+// qwfn_fattn_force_merge, read once per call; and the path the calling
+// thread's last call took (qwfn_fattn_last_merge).
+std::atomic<int32_t> g_force_merge{0};
+thread_local int32_t g_last_merge = QWFN_FA_MERGE_NONE;
+
+// The fused merge's counter slots on each device: g_merge_ctr's address there
+// (hipGetSymbolAddress, once per device, with the device current) and the next
+// free slot. A call takes one slot per (batch, KV head) group, consecutive and
+// not wrapping round the end; calls in flight at once (on several streams)
+// get disjoint slots unless more than MERGE_SLOTS groups are in flight.
+constexpr int MERGE_MAX_DEVICES = 64;
+std::mutex            g_merge_mu;
+unsigned long long *  g_merge_addr[MERGE_MAX_DEVICES];
+std::atomic<uint64_t> g_merge_next[MERGE_MAX_DEVICES];
+std::atomic<uint64_t> g_merge_epoch[MERGE_MAX_DEVICES];   // the last epoch handed out (48 bits, from 1)
+
+int merge_slots(int64_t groups, unsigned long long ** out, unsigned long long * ebase) {
+    int dev = 0;
+    QWFN_HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= MERGE_MAX_DEVICES) return set_error(QWFN_ENOTSUP, "flash_attn_ext: device index beyond the merge table");
+    if (groups < 1 || groups > MERGE_SLOTS) return set_error(QWFN_EINVAL, "flash_attn_ext: merge groups out of range");
+    unsigned long long * base = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_merge_mu);
+        if (!g_merge_addr[dev]) {
+            void * p = nullptr;
+            QWFN_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(g_merge_ctr)));
+            if (!p) return set_error(QWFN_EDEVICE, "flash_attn_ext: merge counters have no device address");
+            g_merge_addr[dev] = (unsigned long long *) p;
+        }
+        base = g_merge_addr[dev];
+    }
+    uint64_t first = g_merge_next[dev].fetch_add((uint64_t) groups, std::memory_order_relaxed) % MERGE_SLOTS;
+    if (first + (uint64_t) groups > (uint64_t) MERGE_SLOTS) first = 0;
+    *out = base + 2 * first;
+    const uint64_t ep = (g_merge_epoch[dev].fetch_add(1, std::memory_order_relaxed) + 1) & ((uint64_t(1) << 48) - 1);
+    *ebase = (unsigned long long) ep << 16;
+    return QWFN_OK;
+}
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
@@ -3814,6 +4070,7 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
         const dim3 g((unsigned) grid), bd(PRE_WAVES * 64);
         if (a.mask) QWFN_FA_LAUNCH(g, bd, as_stream(stream), k_fa_pre<true>);
         else        QWFN_FA_LAUNCH(g, bd, as_stream(stream), k_fa_pre<false>);
+        g_last_merge = a.ns > 1 ? QWFN_FA_MERGE_KERNEL : QWFN_FA_MERGE_NONE;
         if (int rc = hip_check(hipGetLastError(), "flash_attn launch")) return rc;
         if (a.ns > 1) {
             const int64_t rows = (int64_t) a.B * a.nh_kv * a.R;
@@ -3827,6 +4084,21 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
         return QWFN_OK;
     }
     if (pl.kind == FA_DEC || pl.kind == FA_VD) a.n_rg = 1;
+    // the split merge: a k_fattn_merge launch unless the in-kernel merge is
+    // forced. The launch measures faster (16384 keys, T = 3: 20.0 against
+    // 27.1 us per op; 65536: 33.2 against 39.1): after the last split, the
+    // in-kernel merge waits out a chain of device-scope round trips (the
+    // partials' store completion, the arrival, a row claim, the partials'
+    // loads) that costs more than the launch boundary it replaces
+    const int32_t fm = g_force_merge.load(std::memory_order_relaxed);
+    const int64_t groups = (int64_t) a.B * a.nh_kv;
+    const bool fuse = (pl.kind == FA_DEC || pl.kind == FA_VD) && !a.ragged && a.ns > 1 && groups <= MERGE_SLOTS &&
+                      pl.off_ml < (size_t(1) << 32) && fm == QWFN_FA_MERGE_FUSED;
+    if (fuse) {
+        if (int rc = merge_slots(groups, &a.mctr, &a.m_ebase)) return rc;
+        a.m_nm = std::min<int32_t>(a.R, a.ns);
+    }
+    g_last_merge = a.ns <= 1 ? QWFN_FA_MERGE_NONE : fuse ? QWFN_FA_MERGE_FUSED : QWFN_FA_MERGE_KERNEL;
     const int64_t n_units = a.ragged ? (int64_t) a.r_units : (int64_t) a.B * a.ns;
     const int64_t units = n_units >= 8 ? (n_units + 7) / 8 * 8 : n_units;
     const int64_t hgn = (int64_t) a.nh_kv * a.n_rg;
@@ -3894,7 +4166,7 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
     }
     }
     if (int rc = hip_check(hipGetLastError(), "flash_attn launch")) return rc;
-    if (a.ns > 1) {
+    if (a.ns > 1 && !a.mctr) {
         const int64_t blocks = (int64_t) a.B * a.nh_kv * a.R * 4;
         if (blocks > 0x7fffffff) return set_error(QWFN_EINVAL, "flash_attn_ext: merge grid too large");
         if (a.ragged) hipLaunchKernelGGL(k_fattn_merge<true>, dim3((unsigned) blocks), dim3(256), 0, st, a);
@@ -4032,4 +4304,13 @@ extern "C" void qwfn_fattn_force_kernel(int32_t kind) {
 
 extern "C" const char * qwfn_fattn_last_kernel(void) {
     return g_last_kernel;
+}
+
+extern "C" void qwfn_fattn_force_merge(int32_t mode) {
+    g_force_merge.store(mode == QWFN_FA_MERGE_FUSED || mode == QWFN_FA_MERGE_KERNEL ? mode : QWFN_FA_MERGE_AUTO,
+                        std::memory_order_relaxed);
+}
+
+extern "C" int32_t qwfn_fattn_last_merge(void) {
+    return g_last_merge;
 }

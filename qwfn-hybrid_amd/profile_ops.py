@@ -36,6 +36,8 @@ def main() -> int:
     ap.add_argument("--kernel", choices=["auto", "vd", "dec", "general"], default="auto",
                     help="attention ops: the kernel family to force (qwfn_fattn_force_kernel)")
     ap.add_argument("--splits", type=int, default=0, help="attention ops: a forced key-split count (0: the planner's)")
+    ap.add_argument("--merge", choices=["auto", "fused", "kernel"], default="auto",
+                    help="attention ops: merge the key splits inside the kernel or with a merge launch")
     a = ap.parse_args()
     import numpy as np
     import torch
@@ -45,6 +47,8 @@ def main() -> int:
     K.load().qwfn_fattn_force_kernel({"auto": K.FA_KERNEL_AUTO, "vd": K.FA_KERNEL_VD, "dec": K.FA_KERNEL_DEC,
                                       "general": K.FA_KERNEL_GENERAL}[a.kernel])
     K.load().qwfn_fattn_force_splits(a.splits)
+    K.load().qwfn_fattn_force_merge({"auto": K.FA_MERGE_AUTO, "fused": K.FA_MERGE_FUSED,
+                                     "kernel": K.FA_MERGE_KERNEL}[a.merge])
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev)
     gen.manual_seed(5)
@@ -178,6 +182,8 @@ def main() -> int:
     e1.record()
     torch.cuda.synchronize()
     kname = K.last_kernel() if a.op in ("verify", "prefill", "cells") else ""
+    if kname:
+        kname += {K.FA_MERGE_FUSED: " + fused merge", K.FA_MERGE_KERNEL: " + k_fattn_merge"}.get(K.last_merge(), "")
     print(f"{a.op}: {a.reps} launches done, {e0.elapsed_time(e1) * 1e3 / a.reps:.2f} us per launch (event time) {kname}",
           flush=True)
     return 0

@@ -38,6 +38,30 @@ def last_kernel() -> str:
     return load().qwfn_fattn_last_kernel().decode()
 
 
+# split-merge paths (qwfn_fattn_force_merge, qwfn_fattn_last_merge)
+FA_MERGE_AUTO, FA_MERGE_FUSED, FA_MERGE_KERNEL, FA_MERGE_NONE = 0, 1, 2, 3
+
+
+def last_merge() -> int:
+    """How this thread's last attention call merged its key splits (FA_MERGE_*)."""
+    return int(load().qwfn_fattn_last_merge())
+
+
+class forced_merge:
+    """Context manager: later attention calls in this process merge their key splits
+    by path `mode` (FA_MERGE_*) while it is active."""
+    def __init__(self, mode: int):
+        self.mode = mode
+
+    def __enter__(self):
+        load().qwfn_fattn_force_merge(self.mode)
+        return self
+
+    def __exit__(self, *exc):
+        load().qwfn_fattn_force_merge(FA_MERGE_AUTO)
+        return False
+
+
 class forced_kernel:
     """Context manager: later attention calls in this process use kernel family `kind`
     (FA_KERNEL_*) while it is active."""
@@ -112,7 +136,7 @@ class QsaPoolCfg(ctypes.Structure):
 EXPORTS = [
     "qwfn_abi_version", "qwfn_last_error", "qwfn_init", "qwfn_device_status",
     "qwfn_set_rows_q8_0", "qwfn_cpy_f32_q8_0", "qwfn_set_rows_q8_0_kv", "qwfn_cpy_f32_q8_0_kv", "qwfn_get_rows_i32", "qwfn_kv_gather_segments",
-    "qwfn_fattn_workspace_size", "qwfn_fattn_force_splits", "qwfn_fattn_force_kernel", "qwfn_fattn_last_kernel", "qwfn_flash_attn_ext_q8_0", "qwfn_flash_attn_ext_q8_0_noalloc", "qwfn_flash_attn_ext_q8_0_append",
+    "qwfn_fattn_workspace_size", "qwfn_fattn_force_splits", "qwfn_fattn_force_kernel", "qwfn_fattn_last_kernel", "qwfn_fattn_force_merge", "qwfn_fattn_last_merge", "qwfn_flash_attn_ext_q8_0", "qwfn_flash_attn_ext_q8_0_noalloc", "qwfn_flash_attn_ext_q8_0_append",
     "qwfn_fattn_workspace_size_seq", "qwfn_flash_attn_ext_q8_0_seq", "qwfn_state_restore",
     "qwfn_fattn_workspace_size_cells", "qwfn_flash_attn_ext_q8_0_cells", "qwfn_kv_produce_q8_0",
     "qwfn_flash_attn_ext_q8_0_gated",
@@ -164,6 +188,10 @@ def load(path: str = LIB_PATH):
     L.qwfn_fattn_force_kernel.restype = None
     L.qwfn_fattn_last_kernel.argtypes = []
     L.qwfn_fattn_last_kernel.restype = ctypes.c_char_p
+    L.qwfn_fattn_force_merge.argtypes = [i32]
+    L.qwfn_fattn_force_merge.restype = None
+    L.qwfn_fattn_last_merge.argtypes = []
+    L.qwfn_fattn_last_merge.restype = i32
     L.qwfn_flash_attn_ext_q8_0.argtypes = [T, T, T, T, ctypes.c_float, ctypes.c_float, ctypes.c_float, T,
                                            ctypes.c_int, vp, sz, vp]
     PL = ctypes.POINTER(i64)
@@ -239,7 +267,8 @@ def load(path: str = LIB_PATH):
     L.qwfn_qsa_select_cells.argtypes = [vp, sz, i64, vp, i32, sz, vp, sz, i32, i32, vp, i32, vp, vp, vp, sz, vp]
     for name in EXPORTS:
         if name not in ("qwfn_state_config_default", "qwfn_state_destroy", "qwfn_snap_pool_destroy",
-                        "qwfn_fattn_force_splits", "qwfn_fattn_force_kernel", "qwfn_fattn_last_kernel"):
+                        "qwfn_fattn_force_splits", "qwfn_fattn_force_kernel", "qwfn_fattn_last_kernel",
+                        "qwfn_fattn_force_merge", "qwfn_fattn_last_merge"):
             getattr(L, name).restype = getattr(L, name).restype or ctypes.c_int
     L.qwfn_last_error.restype = ctypes.c_char_p
     L.qwfn_fattn_last_kernel.restype = ctypes.c_char_p
