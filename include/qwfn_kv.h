@@ -267,6 +267,34 @@ int qwfn_flash_attn_ext_q8_0_cells(const qwfn_tensor * q, const qwfn_tensor * k,
                                    float scale, const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes,
                                    void * stream);
 
+/* The attention of the reference's default verify step (QSA on), one list of
+ * cells per query position: engine::attn_decode (qwfn_engine.cpp:2259-2280)
+ * chains T sparse_attn_decode calls, and call k attends the k_blocks * ratio
+ * cells its own top-k selected (qwfn_graph.cpp:653-705) through a raw gather
+ * of whole cache rows (both KV heads read the same list, :694-699), masked to
+ * cells at most the query's position (:668-675), scaled by 1/sqrt(256), and
+ * multiplies the result by sigmoid(gate) (:701). Here all T positions run in
+ * one launch and one merge: query t (position pos0 + t) attends cache rows
+ * cells[t * cell_stride + j], j < n_cells[t] (n_cells: host array of T
+ * counts), those at most pos0 + t; cell_stride = 0 gives every position the
+ * same list. Lists may repeat cells and need no padding (the reference pads
+ * to a multiple of 256 with masked duplicates, which add nothing). q: F32
+ * [256, T, n_head, 1]; k, v: the q8_0 cache views [256, n_rows, n_head_kv, 1]
+ * (nb1 the row stride, nb2 the head offset), n_rows * row stride < 2 GiB,
+ * T * n_head_kv <= 32; cells: device int32, 16-byte aligned, cell_stride a
+ * multiple of 4 and at least every count; dst: contiguous F32 [256, n_head,
+ * T, 1]; gate: NULL or F32 of dst's shape and strides (then dst = attention *
+ * sigmoid(gate), both 16-byte aligned). A cell outside [0, n_rows) is masked
+ * and sets bit 1 of qwfn_device_status; a query that sees no cell gets 0.
+ * Size ws with qwfn_fattn_workspace_size_query_cells (ws NULL: the library's
+ * buffer). */
+size_t qwfn_fattn_workspace_size_query_cells(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
+                                             const int64_t * n_cells, int64_t cell_stride);
+int qwfn_flash_attn_ext_q8_0_query_cells(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
+                                         const int32_t * cells, const int64_t * n_cells, int64_t cell_stride,
+                                         int64_t pos0, float scale, const qwfn_tensor * gate, const qwfn_tensor * dst,
+                                         int variant, void * ws, size_t ws_bytes, void * stream);
+
 /* Rope and norm constants of the attention layers (qwfn_hparams.h:26,
  * :34-36): n_dims = rope_dim (64), sections = mrope_sections {11, 11, 10, 0},
  * freq_base = rope_freq_base (1e7), rms_eps (1e-6). */

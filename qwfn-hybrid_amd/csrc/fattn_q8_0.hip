@@ -67,7 +67,8 @@ constexpr int WAVES_PAIR = 4;          // wavefronts per block, two blocks per C
 constexpr int QWIN   = 64;             // bytes of one block's query window
 constexpr int MAX_SPLITS = 1024;       // key splits per (batch, KV head, row group)
 constexpr int RAGGED_MAX_B = 16;       // sequences of a call with per-sequence key counts
-constexpr int GATHER_MAX_HEADS = 8;    // KV heads of a call with per-head cell lists
+constexpr int GATHER_MAX_HEADS = 8;    // KV heads of a call with cell lists
+constexpr int GATHER_MAX_LISTS = 32;   // (sequence, KV head) cell lists of a call
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float RESCALE_SLACK = 8.f;   // log2 units the running max may lag the true max
 constexpr int PV_BATCH = 4;            // 16-key V block tiles whose LDS reads are issued together
@@ -157,14 +158,17 @@ struct fa_args {
     int32_t  r_ns[RAGGED_MAX_B];
     int32_t  r_split_len[RAGGED_MAX_B];
     int64_t  r_n_kv[RAGGED_MAX_B];
-    // gathered keys (k_fa_dec<.., GATHER>): KV head h attends cache rows
-    // g_cells[h * g_stride + j], j < g_n[h]; query t sees a row only if it is
-    // at most g_pos0 + t. The cache has g_rows rows.
+    // gathered keys (k_fa_dec / k_fa_vd <.., GATHER>): KV head h of sequence b
+    // attends cache rows g_cells[b * g_bstride + h * g_hstride + j],
+    // j < g_n[b * nh_kv + h]; query t of sequence b sees a row only if it is
+    // at most g_pos0 + b + t (one list per KV head: B = 1; one list per query
+    // position: each position is a sequence of one query, T = 1). The cache
+    // has g_rows rows.
     const int32_t * g_cells;
-    int64_t  g_stride;
+    int64_t  g_bstride, g_hstride;
     int64_t  g_pos0;
     int64_t  g_rows;
-    int32_t  g_n[GATHER_MAX_HEADS];
+    int32_t  g_n[GATHER_MAX_LISTS];
     uint32_t * status;     // device flags (DEVERR_GET_ROWS_INDEX: a cell outside the cache)
     // output gate (or null): dst = attention * sigmoid(gate), gate laid out as dst
     const float * gate;
@@ -1527,11 +1531,12 @@ __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
         k_hi = split == a.ns - 1 ? a.n_kv : (a.n_kv < e ? a.n_kv : e);
     }
     if constexpr (GATHER) {
-        // this head's own cell count (constant indices keep the table scalar)
+        // this list's own cell count (constant indices keep the table scalar)
+        const int li = b * a.nh_kv + kvh;
         int64_t nh = 0;
 #pragma unroll
-        for (int i = 0; i < GATHER_MAX_HEADS; i++)
-            if (i == kvh) nh = a.g_n[i];
+        for (int i = 0; i < GATHER_MAX_LISTS; i++)
+            if (i == li) nh = a.g_n[i];
         k_hi = k_hi < nh ? k_hi : nh;
         k_lo = k_lo < k_hi ? k_lo : k_hi;
     }
@@ -1688,7 +1693,7 @@ __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
     __shared__ uint32_t g_bad;   // GATHER: a cell of the block lies outside the cache
     if constexpr (GATHER) {
         // the block's cells [k_lo, k_hi): wave w takes 256-cell pieces w, w + NW, ...
-        const int32_t * cl = a.g_cells + (size_t) kvh * a.g_stride + k_lo;
+        const int32_t * cl = a.g_cells + (size_t) b * a.g_bstride + (size_t) kvh * a.g_hstride + k_lo;
         const v4i rc = make_rsrc(cl, (uint32_t) span * 4u);
         for (int m = wave; m * 256 < span; m += DEC_WAVES)
             dma16_buf(rc, (uint32_t) (m * 1024 + 16 * lane), __builtin_amdgcn_readfirstlane(lds_addr(&gcell[m * 256])));
@@ -1797,7 +1802,7 @@ __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
     for (int bb = 0; bb < NBLK; bb++) { O[bb][0] = v4f{0, 0, 0, 0}; O[bb][1] = v4f{0, 0, 0, 0}; }
     uint16_t (*sw)[NBLK][DEC_TK] = scl[wave];
     // GATHER: the position of the lane's query row
-    const int64_t q_pos = GATHER ? a.g_pos0 + (int64_t) div_gqa(a, (uint32_t) (wr0 + ln)) : 0;
+    const int64_t q_pos = GATHER ? a.g_pos0 + b + (int64_t) div_gqa(a, (uint32_t) (wr0 + ln)) : 0;
 
     // tile ti from stage st; nx >= 0: tile nx goes into the same stage, its K
     // rows as soon as the QK is done, its V rows and mask after the PV
@@ -2177,10 +2182,11 @@ __global__ __launch_bounds__(VD_WAVES * 64, 2) void k_fa_vd(fa_args a) {
         k_hi = split == a.ns - 1 ? a.n_kv : (a.n_kv < e ? a.n_kv : e);
     }
     if constexpr (GATHER) {
+        const int li = b * a.nh_kv + kvh;
         int64_t nh = 0;
 #pragma unroll
-        for (int i = 0; i < GATHER_MAX_HEADS; i++)
-            if (i == kvh) nh = a.g_n[i];
+        for (int i = 0; i < GATHER_MAX_LISTS; i++)
+            if (i == li) nh = a.g_n[i];
         k_hi = k_hi < nh ? k_hi : nh;
         k_lo = k_lo < k_hi ? k_lo : k_hi;
     }
@@ -2330,7 +2336,7 @@ __global__ __launch_bounds__(VD_WAVES * 64, 2) void k_fa_vd(fa_args a) {
     uint8_t * qst = &kvr[1][1][0][0];
     const int first = wave < n_sub ? wave : -1;
     if constexpr (GATHER) {
-        const int32_t * cl = a.g_cells + (size_t) kvh * a.g_stride + k_lo;
+        const int32_t * cl = a.g_cells + (size_t) b * a.g_bstride + (size_t) kvh * a.g_hstride + k_lo;
         const v4i rc = make_rsrc(cl, (uint32_t) span * 4u);
         for (int m = wave; m * 256 < span; m += VD_WAVES)
             dma16_buf(rc, (uint32_t) (m * 1024 + 16 * lane), __builtin_amdgcn_readfirstlane(lds_addr(&gcell[m * 256])));
@@ -2458,8 +2464,8 @@ __global__ __launch_bounds__(VD_WAVES * 64, 2) void k_fa_vd(fa_args a) {
     const uint8_t * tpv1_l = hs == 1 ? tp_l : tz;                           // the other half's sub-tile
     const uint8_t * mg = &mgr[MASKED ? wave : 0][0];
     // GATHER: the position of the lane's query rows
-    const int64_t qpos_f = GATHER ? a.g_pos0 + (int64_t) div_gqa(a, (uint32_t) (NF ? ln : 0)) : 0;
-    const int64_t qpos_p = GATHER ? a.g_pos0 + (int64_t) div_gqa(a, (uint32_t) (16 * NF + (ln & 7))) : 0;
+    const int64_t qpos_f = GATHER ? a.g_pos0 + b + (int64_t) div_gqa(a, (uint32_t) (NF ? ln : 0)) : 0;
+    const int64_t qpos_p = GATHER ? a.g_pos0 + b + (int64_t) div_gqa(a, (uint32_t) (16 * NF + (ln & 7))) : 0;
 
     // one tensor's block scales of the step into the wave's table [block][key]
     auto tab_fill = [&](int tensor, auto half_tag) __attribute__((always_inline)) {
@@ -3915,10 +3921,11 @@ enum ws_mode { WS_CALLER, WS_SCRATCH };
 // Gathered keys: per KV head a list of cache rows (qwfn_flash_attn_ext_q8_0_cells).
 struct fa_gather {
     const int32_t * cells;
-    const int64_t * n_cells;   // host, one count per KV head
-    int64_t stride;
+    const int64_t * n_cells;   // host: one count per KV head, or per query position (per_query)
+    int64_t stride;            // between the lists of consecutive heads, or positions (per_query)
     int64_t pos0;
     int64_t n_rows;            // rows of the cache
+    bool    per_query = false; // one list per query position, shared by the KV heads
 };
 
 // Launch of an attention kernel of the fa_args `a` in scope, recording its
@@ -4046,10 +4053,13 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
     a.gqa_mul = recip32(pl.gqa);
     if (gat) {
         a.g_cells = gat->cells;
-        a.g_stride = gat->stride;
+        a.g_bstride = gat->per_query ? gat->stride : 0;
+        a.g_hstride = gat->per_query ? 0 : gat->stride;
         a.g_pos0 = gat->pos0;
         a.g_rows = gat->n_rows;
-        for (int64_t h = 0; h < a.nh_kv; h++) a.g_n[h] = (int32_t) gat->n_cells[h];
+        for (int64_t b = 0; b < a.B; b++)
+            for (int64_t h = 0; h < a.nh_kv; h++)
+                a.g_n[b * a.nh_kv + h] = (int32_t) gat->n_cells[gat->per_query ? b : h];
         if (int rc = status_word(&a.status)) return rc;
     }
     if (app) {
@@ -4249,6 +4259,92 @@ extern "C" int qwfn_flash_attn_ext_q8_0_cells(const qwfn_tensor * q, const qwfn_
         if (int rc = gather_args(q, k, v, cells, n_cells, cell_stride, pos0, &kk, &vv, &g)) return rc;
         return fattn_run(q, &kk, &vv, nullptr, scale, 0.0f, 0.0f, dst, variant, ws, ws_bytes, stream, nullptr, nullptr,
                          WS_CALLER, &g);
+    });
+}
+
+namespace {
+// Checks of a call with one cell list per query position, and the views that
+// present position t as sequence t of one query: q [256, 1, n_head, T], dst
+// and gate [256, n_head, 1, T] over the same memory; kk / vv get the longest
+// list's length as their key count.
+int query_cells_args(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v, const int32_t * cells,
+                     const int64_t * n_cells, int64_t cell_stride, int64_t pos0, const qwfn_tensor * dst,
+                     const qwfn_tensor * gate, qwfn_tensor * qq, qwfn_tensor * kk, qwfn_tensor * vv, qwfn_tensor * dd,
+                     qwfn_tensor * gg, fa_gather * g) {
+    if (!q || !k || !v || !cells || !n_cells) return set_error(QWFN_EINVAL, "flash_attn_ext_query_cells: NULL argument");
+    if (!is_aligned(cells, 16)) return set_error(QWFN_EALIGN, "flash_attn_ext_query_cells: cells must be 16-byte aligned");
+    if (k->ne[2] < 1 || k->ne[2] > GATHER_MAX_HEADS)
+        return set_error(QWFN_ENOTSUP, "flash_attn_ext_query_cells: 1 to 8 KV heads");
+    if (q->ne[3] != 1 || k->ne[3] != 1 || v->ne[3] != 1)
+        return set_error(QWFN_ENOTSUP, "flash_attn_ext_query_cells: one sequence (q, k and v with ne[3] = 1)");
+    const int64_t T = q->ne[1];
+    if (T < 1 || T * k->ne[2] > GATHER_MAX_LISTS)
+        return set_error(QWFN_ENOTSUP, "flash_attn_ext_query_cells: T * n_head_kv must lie in [1, 32]");
+    if (cell_stride < 0 || cell_stride % 4)
+        return set_error(QWFN_EALIGN, "flash_attn_ext_query_cells: cell_stride must be 0 (one list for every position) or a positive multiple of 4");
+    if (pos0 < 0) return set_error(QWFN_EINVAL, "flash_attn_ext_query_cells: negative pos0");
+    if (k->ne[1] != v->ne[1]) return set_error(QWFN_EINVAL, "flash_attn_ext_query_cells: k and v must have the same rows");
+    if ((uint64_t) k->ne[1] * std::max(k->nb[1], v->nb[1]) >= (uint64_t(1) << 31))
+        return set_error(QWFN_ENOTSUP, "flash_attn_ext_query_cells: the cache must be below 2 GiB (rows * row stride)");
+    int64_t mx = 0;
+    for (int64_t t = 0; t < T; t++) {
+        if (n_cells[t] < 0 || (cell_stride > 0 && n_cells[t] > cell_stride))
+            return set_error(QWFN_ERANGE, "flash_attn_ext_query_cells: each position's cell count must lie in [0, cell_stride]");
+        mx = std::max(mx, n_cells[t]);
+    }
+    if (!dst || dst->ne[0] != D || dst->ne[1] != q->ne[2] || dst->ne[2] != T || dst->ne[3] != 1 || dst->nb[0] != 4 ||
+        dst->nb[1] != (size_t) D * 4 || dst->nb[2] != dst->nb[1] * (size_t) dst->ne[1])
+        return set_error(QWFN_EINVAL, "flash_attn_ext_query_cells: dst must be contiguous f32 [256, n_head, T, 1]");
+    *qq = *q;
+    qq->ne[1] = 1; qq->ne[3] = T; qq->nb[3] = q->nb[1];
+    *kk = *k;
+    *vv = *v;
+    kk->ne[1] = vv->ne[1] = mx;
+    *dd = *dst;
+    dd->ne[2] = 1; dd->ne[3] = T; dd->nb[3] = dst->nb[2];
+    if (gate) {
+        *gg = *gate;
+        if (gate->ne[2] != T || gate->ne[3] != 1 || gate->nb[2] != dst->nb[2])
+            return set_error(QWFN_EINVAL, "flash_attn_ext_query_cells: gate must have dst's shape and strides");
+        gg->ne[2] = 1; gg->ne[3] = T; gg->nb[3] = gate->nb[2];
+    }
+    *g = fa_gather{cells, n_cells, cell_stride, pos0, k->ne[1], true};
+    return QWFN_OK;
+}
+}  // namespace
+
+extern "C" size_t qwfn_fattn_workspace_size_query_cells(const qwfn_tensor * q, const qwfn_tensor * k,
+                                                        const qwfn_tensor * v, const int64_t * n_cells,
+                                                        int64_t cell_stride) {
+    return ::qwfn::abi_value<size_t>("fattn_workspace_size_query_cells", 0, [&]() -> size_t {
+        if (!q) return 0;
+        qwfn_tensor qq, kk, vv, dd, gg;
+        fa_gather g{};
+        static const int32_t dummy[4] = {0, 0, 0, 0};
+        qwfn_tensor dst = *q;   // a contiguous [256, n_head, T, 1] stand-in: only the plan is wanted
+        dst.type = QWFN_TYPE_F32;
+        dst.ne[0] = D; dst.ne[1] = q->ne[2]; dst.ne[2] = q->ne[1]; dst.ne[3] = 1;
+        dst.nb[0] = 4; dst.nb[1] = (size_t) D * 4; dst.nb[2] = dst.nb[1] * (size_t) dst.ne[1]; dst.nb[3] = dst.nb[2] * (size_t) dst.ne[2];
+        if (query_cells_args(q, k, v, dummy, n_cells, cell_stride, 0, &dst, nullptr, &qq, &kk, &vv, &dd, &gg, &g))
+            return 0;
+        fa_plan pl{};
+        if (plan_fattn(&qq, &kk, &vv, nullptr, &pl, nullptr, MAX_SPLITS, true)) return 0;
+        return pl.ws_bytes;
+    });
+}
+
+extern "C" int qwfn_flash_attn_ext_q8_0_query_cells(const qwfn_tensor * q, const qwfn_tensor * k,
+                                                    const qwfn_tensor * v, const int32_t * cells,
+                                                    const int64_t * n_cells, int64_t cell_stride, int64_t pos0,
+                                                    float scale, const qwfn_tensor * gate, const qwfn_tensor * dst,
+                                                    int variant, void * ws, size_t ws_bytes, void * stream) {
+    return ::qwfn::abi_call("flash_attn_ext_q8_0_query_cells", [&]() -> int {
+        qwfn_tensor qq, kk, vv, dd, gg;
+        fa_gather g{};
+        if (int rc = query_cells_args(q, k, v, cells, n_cells, cell_stride, pos0, dst, gate, &qq, &kk, &vv, &dd, &gg, &g))
+            return rc;
+        return fattn_run(&qq, &kk, &vv, nullptr, scale, 0.0f, 0.0f, &dd, variant, ws, ws_bytes, stream, nullptr, nullptr,
+                         WS_CALLER, &g, gate ? &gg : nullptr);
     });
 }
 

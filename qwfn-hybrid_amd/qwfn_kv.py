@@ -139,6 +139,7 @@ EXPORTS = [
     "qwfn_fattn_workspace_size", "qwfn_fattn_force_splits", "qwfn_fattn_force_kernel", "qwfn_fattn_last_kernel", "qwfn_fattn_force_merge", "qwfn_fattn_last_merge", "qwfn_flash_attn_ext_q8_0", "qwfn_flash_attn_ext_q8_0_noalloc", "qwfn_flash_attn_ext_q8_0_append",
     "qwfn_fattn_workspace_size_seq", "qwfn_flash_attn_ext_q8_0_seq", "qwfn_state_restore",
     "qwfn_fattn_workspace_size_cells", "qwfn_flash_attn_ext_q8_0_cells", "qwfn_kv_produce_q8_0",
+    "qwfn_fattn_workspace_size_query_cells", "qwfn_flash_attn_ext_q8_0_query_cells",
     "qwfn_flash_attn_ext_q8_0_gated",
     # include/qwfn_state.h
     "qwfn_state_config_default", "qwfn_state_create", "qwfn_state_destroy", "qwfn_state_tensor",
@@ -204,6 +205,10 @@ def load(path: str = LIB_PATH):
     L.qwfn_fattn_workspace_size_cells.argtypes = [T, T, T, PL, i64]
     L.qwfn_fattn_workspace_size_cells.restype = sz
     L.qwfn_flash_attn_ext_q8_0_cells.argtypes = [T, T, T, vp, PL, i64, i64, ctypes.c_float, T, ctypes.c_int, vp, sz, vp]
+    L.qwfn_fattn_workspace_size_query_cells.argtypes = [T, T, T, PL, i64]
+    L.qwfn_fattn_workspace_size_query_cells.restype = sz
+    L.qwfn_flash_attn_ext_q8_0_query_cells.argtypes = [T, T, T, vp, PL, i64, i64, ctypes.c_float, T, T, ctypes.c_int,
+                                                       vp, sz, vp]
     L.qwfn_kv_produce_q8_0.argtypes = [T, T, T, vp, vp, ctypes.POINTER(RopeCfg), T, T, i64, ctypes.c_int, vp]
     L.qwfn_flash_attn_ext_q8_0_gated.argtypes = [T, T, T, T, ctypes.c_float, ctypes.c_float, ctypes.c_float, T, T,
                                                  ctypes.c_int, vp, sz, vp]
@@ -466,6 +471,31 @@ def flash_attn_ext_cells(qv: Tensor, kv: Tensor, vv: Tensor, cells, n_cells, pos
                                                   n, 0 if shared else cells.stride(0), pos0, scale, ctypes.byref(ov),
                                                   variant, ws_ptr,
                                                   ws_bytes, _stream(stream)))
+
+
+def flash_attn_ext_query_cells(qv: Tensor, kv: Tensor, vv: Tensor, cells, n_cells, pos0: int, scale: float,
+                               ov: Tensor, gate=None, variant: int = Q8_X86, ws=None, stream=None):
+    """Attention of query position t over the cache rows cells[t, :n_cells[t]] (cells:
+    device int32 [T, stride] with contiguous rows, read by every KV head; a [1, stride]
+    list serves every position), the rows at most pos0 + t; times sigmoid(gate) when
+    gate (a torch f32 tensor laid out as the output) is given."""
+    L = load()
+    gv = out_view(gate) if gate is not None else None
+    n = (ctypes.c_int64 * len(n_cells))(*[int(x) for x in n_cells])
+    ws_ptr = ws.data_ptr() if ws is not None else None
+    ws_bytes = ws.numel() * ws.element_size() if ws is not None else 0
+    if str(cells.dtype) != "torch.int32" or cells.dim() != 2 or cells.stride(1) != 1 or not cells.is_cuda:
+        raise ValueError("cells must be a device int32 [T, stride] tensor with contiguous rows")
+    stride = 0 if cells.shape[0] == 1 else cells.stride(0)
+    return check(L.qwfn_flash_attn_ext_q8_0_query_cells(
+        ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), cells.data_ptr(), n, stride, pos0, scale,
+        ctypes.byref(gv) if gv is not None else None, ctypes.byref(ov), variant, ws_ptr, ws_bytes, _stream(stream)))
+
+
+def fattn_workspace_size_query_cells(qv: Tensor, kv: Tensor, vv: Tensor, n_cells, cell_stride: int) -> int:
+    n = (ctypes.c_int64 * len(n_cells))(*[int(x) for x in n_cells])
+    return int(load().qwfn_fattn_workspace_size_query_cells(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), n,
+                                                            cell_stride))
 
 
 def fattn_workspace_size_cells(qv: Tensor, kv: Tensor, vv: Tensor, n_cells, cell_stride: int) -> int:

@@ -172,3 +172,118 @@ def test_cells_matches_gather_then_attention(gpu, oracle):
     K.flash_attn_ext(K.q_view(qd), kview, vview, K.mask_view(md), 1 / 16, K.out_view(out))
     sep = host(out)[0]
     check(fused, sep, tight=2e-5)
+
+
+def query_cells_attn(K, q, kd, vd, n_rows, lists, pos0, gate=None, ws=False):
+    """One list per query position (qwfn_flash_attn_ext_q8_0_query_cells); lists: T arrays,
+    or one array that every position reads."""
+    T, nh, hd = q.shape
+    n = [len(x) for x in lists]
+    stride = max(4, (max(n) + 3) // 4 * 4)
+    c = np.full((len(lists), stride), -7, np.int32)
+    for t, x in enumerate(lists):
+        c[t, :len(x)] = x
+    rb = kd.shape[1]
+    kv = K.tensor(kd.data_ptr(), K.TYPE_Q8_0, (hd, n_rows, 2, 1), (34, rb, hd // 32 * 34, n_rows * rb))
+    vv = K.tensor(vd.data_ptr(), K.TYPE_Q8_0, (hd, n_rows, 2, 1), (34, rb, hd // 32 * 34, n_rows * rb))
+    qd = dev(q[None].astype(np.float32))
+    out = torch.full((1, T, nh, hd), float("nan"), dtype=torch.float32, device="cuda")
+    wst = None
+    if ws:
+        nb = K.fattn_workspace_size_query_cells(K.q_view(qd), kv, vv, n if len(lists) == T else n * T,
+                                                0 if len(lists) == 1 else stride)
+        assert nb >= 256
+        wst = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    cnt = n if len(lists) == T else n * T
+    K.flash_attn_ext_query_cells(K.q_view(qd), kv, vv, dev(c), cnt, pos0, 1 / 16, K.out_view(out),
+                                 gate=dev(gate[None]) if gate is not None else None, ws=wst)
+    flags = K.device_status()
+    return host(out)[0], flags
+
+
+def _query_lists(seed, n_rows, pos0, T, n_cells):
+    """T lists in the reference's shape: the top blocks of 4 cells of position pos0 + t (a
+    random ranking that changes a little from one position to the next), the block of
+    pos0 + t among them."""
+    rng = np.random.default_rng(seed)
+    nb = (pos0 + T + 3) // 4
+    base = rng.permutation(nb)
+    lists = []
+    for t in range(T):
+        order = base.copy()
+        swap = rng.choice(nb, 40, replace=False)
+        order[swap] = order[rng.permutation(swap)]
+        own = (pos0 + t) // 4
+        top = [own] + [b for b in order if b != own][:n_cells // 4 - 1]
+        lists.append((np.asarray(top, np.int64)[:, None] * 4 + np.arange(4)).reshape(-1).astype(np.int32))
+    return lists
+
+
+@pytest.mark.parametrize("gated", [False, True])
+def test_query_cells_reference_shape(gpu, oracle, gated):
+    """The reference's verify step: T = 3 positions, each with its own 2052 cells (513
+    blocks of 4, its own block among them, cells past it masked), in one launch."""
+    K = gpu
+    n_rows, T, nh = 20000, 3, 16
+    pos0 = n_rows - 8
+    lists = _query_lists(11, n_rows, pos0, T, 2052)
+    kc = KD.make_cache(KD.kv_rows(11, 0, KD.K_KIND, n_rows, outliers=True), n_rows)
+    vc = KD.make_cache(KD.kv_rows(11, 0, KD.V_KIND, n_rows, outliers=True), n_rows)
+    q = KD.q_rows(11, 1, T, nh)[0]
+    gate = (np.random.default_rng(12).standard_normal((T, nh, 256)) * 3).astype(np.float32) if gated else None
+    kd, vd = dev(kc), dev(vc)
+    say(f"query cells T=3 x 2052 gated={gated}")
+    got, flags = query_cells_attn(K, q, kd, vd, n_rows, lists, pos0, gate=gate, ws=True)
+    assert flags == 0
+    ref = np.stack([KD.oracle_attn_cells(q[t:t + 1], kc, vc, [lists[t], lists[t]], pos0 + t, 1 / 16)[0]
+                    for t in range(T)])
+    if gated:
+        ref = ref * (1.0 / (1.0 + np.exp(-gate.astype(np.float64)))).astype(np.float32)
+    check(got, ref)
+
+
+def test_query_cells_agree_with_the_shared_list_forms(gpu, oracle):
+    """One position: identical bits to the shared-list cells call. Three positions reading
+    one list (cell_stride 0): the shared-list cells call to float rounding."""
+    K = gpu
+    n_rows, nh = 9000, 16
+    pos0 = 8990
+    lst = _query_lists(13, n_rows, pos0, 1, 2052)[0]
+    kc = KD.make_cache(KD.kv_rows(13, 0, KD.K_KIND, n_rows, outliers=True), n_rows)
+    vc = KD.make_cache(KD.kv_rows(13, 0, KD.V_KIND, n_rows, outliers=True), n_rows)
+    kd, vd = dev(kc), dev(vc)
+    q1 = KD.q_rows(13, 1, 1, nh)[0]
+    say("query cells T=1 against the cells call")
+    a, _ = query_cells_attn(K, q1, kd, vd, n_rows, [lst], pos0)
+    b, _ = cells_attn(K, q1, kd, vd, n_rows, [lst, lst], pos0, shared=True)
+    np.testing.assert_array_equal(a, b)
+    q3 = KD.q_rows(13, 2, 3, nh)[0]
+    say("query cells T=3, one list for every position")
+    a3, _ = query_cells_attn(K, q3, kd, vd, n_rows, [lst], pos0)
+    b3, _ = cells_attn(K, q3, kd, vd, n_rows, [lst, lst], pos0, shared=True)
+    np.testing.assert_allclose(a3, b3, rtol=1e-5, atol=1e-6)
+    check(a3, KD.oracle_attn_cells(q3, kc, vc, [lst, lst], pos0, 1 / 16))
+
+
+def test_query_cells_edges(gpu, oracle):
+    """Lists of different lengths (one empty: its query gets 0), repeats, unsorted cells,
+    a cell outside the cache (masked, flagged), and a split count that differs per list."""
+    K = gpu
+    n_rows, T, nh = 5000, 4, 16
+    pos0 = 4000
+    rng = np.random.default_rng(14)
+    lists = [rng.choice(pos0, 1500, replace=False).astype(np.int32),
+             np.array([], np.int32),
+             np.concatenate([rng.choice(n_rows, 37), [3, 3, 3]]).astype(np.int32),
+             np.concatenate([rng.choice(pos0, 700, replace=False), [n_rows + 5]]).astype(np.int32)]
+    kc = KD.make_cache(KD.kv_rows(14, 0, KD.K_KIND, n_rows), n_rows)
+    vc = KD.make_cache(KD.kv_rows(14, 0, KD.V_KIND, n_rows), n_rows)
+    q = KD.q_rows(14, 1, T, nh)[0]
+    kd, vd = dev(kc), dev(vc)
+    say("query cells edges")
+    got, flags = query_cells_attn(K, q, kd, vd, n_rows, lists, pos0)
+    assert flags & 2
+    ref = np.stack([KD.oracle_attn_cells(q[t:t + 1], kc, vc, [lists[t], lists[t]], pos0 + t, 1 / 16)[0]
+                    for t in range(T)])
+    assert not got[1].any()
+    check(got, ref)
