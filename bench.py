@@ -274,6 +274,117 @@ def measure_state_rows(K, torch, np, dev, gbs) -> dict:
     return rows
 
 
+def measure_qsa_step_rows(K, torch, np, dev, gen, n_layers: int = 12) -> dict:
+    """The reference's default verify step with QSA on (qwfn_engine.cpp:2259-2280 ->
+    qwfn_graph.cpp:653-705) for one attention layer, T = 3 positions at 73700 of a
+    73728-position context (18432 pooled blocks of 4), composed as
+    tests/test_gpu_qsa_verify_step.py composes it: prepare / prepare_k x3, pool decode x3,
+    one top-513 selection for the 3 queries, the K/V producer (F16 weights), one gated
+    attention launch over the 3 lists of 2052 cells and its merge. 12 layers' states (index
+    cache, pool, K/V caches, weights: 1.3 GB) are rotated so each layer's reads come from
+    HBM; one step of the 12 layers is captured in a HIP graph and replayed. Also the
+    attention alone at the reference's shape: 3 per-position lists (one launch) and one
+    shared list at T = 1 (decode)."""
+    import qwfn_state as S
+    rows = {}
+    n_ctx, ratio, nbm, T, nh, nh_kv, kb, E = 73728, 4, 18432, 3, 24, 2, 513, 2560
+    n_past, nc = 73700, 513 * 4
+    frac = lambda b, us: round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+    gbs = lambda b, us: round(b / (us * 1e-6) / 1e9, 1)
+
+    def cache():
+        c = torch.randint(-100, 100, (n_ctx, ROW), dtype=torch.int8, device=dev, generator=gen).view(torch.uint8)
+        c.view(-1, 34)[:, 0] = 0x1F
+        c.view(-1, 34)[:, 1] = 0x21
+        return c
+    layers = []
+    for _ in range(n_layers):
+        kc, vc = cache(), cache()
+        layers.append(dict(
+            ic=torch.randn((n_ctx, 128), generator=gen, device=dev).to(torch.float16),
+            pool=(torch.randn((nbm, 128), generator=gen, device=dev) * 0.5).to(torch.float16),
+            kc=kc, vc=vc,
+            kv=K.tensor(kc.data_ptr(), K.TYPE_Q8_0, (256, n_ctx, nh_kv, 1), (34, ROW, 272, n_ctx * ROW)),
+            vv=K.tensor(vc.data_ptr(), K.TYPE_Q8_0, (256, n_ctx, nh_kv, 1), (34, ROW, 272, n_ctx * ROW)),
+            wk=(torch.randn((512, E), generator=gen, device=dev) * 0.02).to(torch.float16),
+            wv=(torch.randn((512, E), generator=gen, device=dev) * 0.02).to(torch.float16),
+            knw=torch.rand(256, generator=gen, device=dev) + 0.5,
+            knw_idx=torch.rand(128, generator=gen, device=dev) + 0.5))
+    bias = torch.empty((T, nbm), dtype=torch.float32, device=dev)
+    qds = []
+    for t in range(T):
+        qd = S.QsaDecodeInputs(ratio, nbm)
+        qd.bias = bias[t]
+        qds.append(qd)
+    qds[0].rebuild_bias(n_past)
+    blk_cells = torch.empty(nbm * ratio, dtype=torch.int32, device=dev)
+    S.qsa_tables(blk_cells, ratio)
+    k_raw = torch.randn((T, 128), generator=gen, device=dev)
+    q_idx = torch.randn((T, 4, 128), generator=gen, device=dev)
+    cur = torch.randn((T, E), generator=gen, device=dev)
+    pos = torch.arange(n_past, n_past + T, dtype=torch.int32, device=dev).repeat(4)
+    cells = torch.empty((T, nc), dtype=torch.int32, device=dev)
+    wsel = torch.empty(K.load().qwfn_qsa_select_workspace_size(nbm, T), dtype=torch.uint8, device=dev)
+    q = torch.randn((1, T, nh, 256), generator=gen, device=dev)
+    gate = torch.randn((1, T, nh, 256), generator=gen, device=dev)
+    out = torch.empty((1, T, nh, 256), dtype=torch.float32, device=dev)
+    q1, out1 = q[:, :1].contiguous(), torch.empty((1, 1, nh, 256), dtype=torch.float32, device=dev)
+    aws = torch.empty(max(256, K.fattn_workspace_size_query_cells(K.q_view(q), layers[0]["kv"], layers[0]["vv"],
+                                                                  [nc] * T, nc),
+                          K.fattn_workspace_size_cells(K.q_view(q1), layers[0]["kv"], layers[0]["vv"], [nc, nc], 0)),
+                      dtype=torch.uint8, device=dev)
+
+    def step(k):
+        L = layers[k % n_layers]
+        for t in range(T):
+            qds[t].prepare(n_past + t, prev=qds[t - 1] if t else None)
+        for t in range(T):
+            K.qsa_pool_decode(L["ic"], k_raw[t], qds[t].write_idx, qds[t].member_idx, ratio, qds[t].blk_pos,
+                              qds[t].blk_idx, L["knw_idx"], L["pool"])
+        S.qsa_select_cells(L["pool"], q_idx, bias, kb, blk_cells, ratio, cells, ws=wsel)
+        K.kv_produce(cur, L["wk"], L["wv"], L["knw"], pos, L["kc"], L["vc"], n_past)
+        K.flash_attn_ext_query_cells(K.q_view(q), L["kv"], L["vv"], cells, [nc] * T, n_past, 1 / 16, K.out_view(out),
+                                     gate=gate, ws=aws)
+    us = timed_graph(torch, step, n_layers, 10)
+    lists = cells.cpu().numpy()
+    union = int(np.unique(lists).size)
+    # compulsory bytes per layer: the pool once (select), the bias rows, the K/V weights
+    # (producer), the K/V rows of the union of the three lists, the produced rows, q / gate / out
+    step_bytes = (nbm * 128 * 2 + T * nbm * 4 + 2 * 512 * E * 2 + union * ROW + 2 * T * ROW + 3 * T * nh * 256 * 4)
+    rows["qsa_verify_step_T3"] = {
+        "us_per_layer": round(us, 2), "bytes_per_layer": step_bytes, "GBs": gbs(step_bytes, us),
+        "frac": frac(step_bytes, us), "blocks": nbm, "k_blocks": kb, "cells_per_position": nc,
+        "union_cells": union, "launches_per_layer": 3 + 3 + 1 + 2 + 2,
+        "what": "prepare x3, pool decode x3, select (3 queries), K/V produce, gated query-cells attention + merge"}
+
+    # ---- the attention alone at the reference's decode shape ----
+    sel = cells.clone()
+
+    def attn3(k):
+        L = layers[k % n_layers]
+        K.flash_attn_ext_query_cells(K.q_view(q), L["kv"], L["vv"], sel, [nc] * T, n_past, 1 / 16, K.out_view(out),
+                                     gate=gate, ws=aws)
+    us = timed_graph(torch, attn3, n_layers, 10)
+    ab = union * ROW + 3 * T * nh * 256 * 4
+    rows["query_cells_2052_T3"] = {"us_per_launch": round(us, 3), "union_cells": union, "bytes": ab,
+                                   "GBs": gbs(ab, us), "frac": frac(ab, us),
+                                   "entry": "qwfn_flash_attn_ext_q8_0_query_cells (3 lists of 2052, gated) + merge"}
+    sel1 = sel[:1].contiguous()
+
+    def attn1(k):
+        L = layers[k % n_layers]
+        K.flash_attn_ext_cells(K.q_view(q1), L["kv"], L["vv"], sel1, [nc, nc], n_past, 1 / 16, K.out_view(out1),
+                               ws=aws, shared=True)
+    us = timed_graph(torch, attn1, n_layers, 10)
+    ab1 = nc * ROW + 2 * nh * 256 * 4
+    rows["shared_cells_2052_T1"] = {"us_per_launch": round(us, 3), "cells": nc, "bytes": ab1, "GBs": gbs(ab1, us),
+                                    "frac": frac(ab1, us),
+                                    "entry": "qwfn_flash_attn_ext_q8_0_cells (one list shared by both KV heads) + merge"}
+    del layers
+    torch.cuda.empty_cache()
+    return rows
+
+
 def measure_rows(K, torch, np, dev, gen) -> dict:
     """The other rows of the path on their own workloads: append of a 512-row prefill chunk,
     the per-KV-head sparse gather at 64K, snapshot restore into 4 slots, batch-4 ragged decode
@@ -397,6 +508,7 @@ def measure_rows(K, torch, np, dev, gen) -> dict:
     del src, kv_dst, dn_dst, host
 
     rows.update(measure_state_rows(K, torch, np, dev, gbs))
+    rows.update(measure_qsa_step_rows(K, torch, np, dev, gen))
 
     # ---- batch-4 ragged decode: one query per slot at depths 8192..65536 (mask [n_kv,1,1,4]) ----
     depths = [8192, 16384, 32768, 65536]
