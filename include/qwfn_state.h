@@ -307,6 +307,36 @@ int qwfn_causal_mask_f16(uint16_t * mask, int64_t n_kv, int64_t T, int64_t n_pas
 int qwfn_cell_mask_f16(const int32_t * cells, int64_t n_cells, int64_t n_pad, int32_t n_past,
                        uint16_t * mask, int32_t * gcells, void * stream);
 
+/* The prefill chunk's sparse-attention inputs, engine::fill_chunk_qsa
+ * (qwfn_engine.cpp:1276-1320), written on the device in one launch. n_kv =
+ * n_past_c + Tc keys, n_blocks = ceil(n_kv / ratio) blocks, n_bid = n_kv /
+ * ratio whole ones; the dead block is the partial tail block n_bid when there
+ * is one, else the last. Any pointer may be NULL.
+ *   cell_blk  I32 [n_kv]:          j / ratio for the cells of whole blocks, dead after
+ *   blk_cells I32 [n_blocks*ratio]: b*ratio + k; the tail block's real cells,
+ *                                   the last one repeated
+ *   blk_pos   I32 [4*n_blocks]:    b*ratio in each of the 4 rope sections
+ *   bias      F32 [Tc][n_blocks] (rows bias_nb1 bytes apart), row i for query
+ *             q = n_past_c + i: 0 for whole blocks ending at or before q, 1e9
+ *             for the block holding q when q is not its last cell and for the
+ *             dead block unless it lies wholly after q, -1e9 for blocks wholly
+ *             after q, -inf for none (every block is one of the above).
+ * Tc <= 65534, n_kv < 2^31. */
+int qwfn_qsa_chunk_inputs(int64_t n_past_c, int64_t Tc, int32_t ratio, int32_t * cell_blk, int32_t * blk_cells,
+                          int32_t * blk_pos, float * bias, size_t bias_nb1, void * stream);
+
+/* The prefill's selection mask, graph_builder::qsa_mask (qwfn_graph.cpp:
+ * 388-414): F16 mask [T rows of mask_nb1 bytes] = -inf everywhere, then 0 at
+ * the cells query t selected (cells: I32 [T][width], rows cells_nb1 bytes
+ * apart: the qsa_top_k output), plus the causal mask (F16 [T][>= n_kv], rows
+ * causal_nb1 bytes apart). So key j < n_kv of row t is causal[t][j] where
+ * selected, -inf elsewhere; the row's padding past n_kv is -inf. Repeated
+ * cells are harmless; a cell outside [0, n_kv) is skipped and sets bit 0 of
+ * qwfn_device_status. mask must not overlap causal (the reference adds in
+ * place into a separate selection tensor). n_kv <= 524288. */
+int qwfn_qsa_mask_f16(const int32_t * cells, int64_t width, size_t cells_nb1, const uint16_t * causal,
+                      size_t causal_nb1, int64_t n_kv, int64_t T, uint16_t * mask, size_t mask_nb1, void * stream);
+
 /* ------------------------------------------- decode-time sparse-attention inputs */
 
 /* qsa_decode_inputs (qwfn_graph.h:71-84): device tensors written per token. */

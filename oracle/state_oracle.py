@@ -12,6 +12,8 @@ Each function follows the reference file:line named in its docstring:
 * masks                          qwfn_engine.cpp:1261-1271, :2093-2098, :3415-3421;
                                  qwfn_graph.cpp:668-675, :681-693 (cell mask, padding)
 * saved-sequence pool            tools/qwfn_server.cpp:767-793, :1380-1424
+* prefill sparse-attention inputs qwfn_engine.cpp:1276-1320 (fill_chunk_qsa);
+                                 qwfn_graph.cpp:388-414 (qsa_mask)
 
 How each is pinned (tests/test_state_cpu.py): the layout and summary by the
 summary line the reference's own runs logged at 73728 positions and by the
@@ -21,7 +23,12 @@ three causal-mask builders by their agreement with each other; the cell mask's
 ggml op chain (float arithmetic) by the integer comparison it reduces to; the
 pool by scripted cases whose outcomes follow from the server's rules (count
 and byte caps, replacement of an equal sequence, strict extension, the split
-conditions) and by the invariants the server asserts.
+conditions) and by the invariants the server asserts; the prefill chunk's
+tables and bias by the per-block closed form (whole block ending at or before
+the query: 0; the block holding it mid-block, or the partial tail block at or
+before it: 1e9; a block wholly after it: -1e9); the selection mask by its
+limits (every cell selected: the causal mask; none: all -inf) and the set of
+zeros it must hold (selected and causally visible).
 """
 from __future__ import annotations
 
@@ -363,3 +370,65 @@ def qsa_top_k(score: np.ndarray, k: int) -> np.ndarray:
 def qsa_cells(top: np.ndarray, blk_cells: np.ndarray, ratio: int) -> np.ndarray:
     """get_rows(blk_cells, top) reshaped to [k * ratio] (qwfn_graph.cpp:578-579)."""
     return np.concatenate([blk_cells[b * ratio:(b + 1) * ratio] for b in top]).astype(np.int32)
+
+
+# ------------------------------------------------- prefill sparse-attention inputs
+
+def fill_chunk_qsa(n_past_c: int, Tc: int, ratio: int) -> dict:
+    """engine::fill_chunk_qsa (qwfn_engine.cpp:1276-1320) step by step: n_kv =
+    n_past_c + Tc keys in n_blocks = ceil(n_kv / ratio) blocks (ai.qsa.n_blocks,
+    :1247), n_bid whole ones; cell_blk [n_kv], blk_cells [n_blocks * ratio],
+    blk_pos [4 * n_blocks] and the bias [Tc, n_blocks] (row i for query
+    n_past_c + i): filled 0 / 1e9 / -inf around tail_b, the dead block set to
+    1e9, then positive entries of blocks wholly after the query set to -1e9."""
+    n_kv = n_past_c + Tc
+    n_blocks = (n_kv + ratio - 1) // ratio
+    n_bid = n_kv // ratio
+    have_dead = n_bid < n_blocks
+    dead = n_bid if have_dead else n_blocks - 1
+    cb = np.empty(n_kv, np.int32)
+    cb[:n_bid * ratio] = np.arange(n_bid * ratio) // ratio
+    cb[n_bid * ratio:] = dead
+    bc = np.zeros(ratio * n_blocks, np.int32)
+    bp = np.zeros(4 * n_blocks, np.int32)
+    bc[:n_bid * ratio] = np.arange(n_bid * ratio)
+    for sec in range(4):
+        bp[sec * n_blocks:sec * n_blocks + n_bid] = np.arange(n_bid) * ratio
+    if n_bid < n_blocks:
+        bc[n_bid * ratio:(n_bid + 1) * ratio] = np.minimum(n_bid * ratio + np.arange(ratio), n_kv - 1)
+        for sec in range(4):
+            bp[sec * n_blocks + n_bid] = n_bid * ratio
+    bi = np.empty((Tc, n_blocks), np.float32)
+    blocks = np.arange(n_blocks)
+    for i in range(Tc):
+        row = bi[i]
+        q = n_past_c + i
+        tail_b = min(n_bid, (q + 1) // ratio)
+        row[:tail_b] = 0.0
+        row[tail_b:n_bid] = 1e9
+        row[n_bid:] = -np.inf
+        if have_dead:
+            row[dead] = 1e9
+        flip = (blocks >= tail_b) & (row > 0.0) & (blocks * ratio > q)
+        row[flip] = -1e9
+    return dict(n_blocks=n_blocks, cell_blk=cb, blk_cells=bc, blk_pos=bp, bias=bi)
+
+
+def qsa_mask(cells: np.ndarray, causal_bits: np.ndarray, n_kv: int, row_len: int) -> np.ndarray:
+    """graph_builder::qsa_mask (qwfn_graph.cpp:388-414): an F16 [n_kv, T] tensor
+    filled with -inf, 0 written at each query's selected cells (ggml_set_rows
+    of an F32 zero: +0), then the causal mask added in place (ggml's F16 add:
+    f16(f32(a) + f32(b))). cells: int32 [T, width]; causal_bits: uint16
+    [T, >= n_kv]. Returned as uint16 rows of row_len values, the padding past
+    n_kv -inf as the kernel writes it."""
+    cells = np.asarray(cells, np.int64)
+    T = cells.shape[0]
+    sel = np.full((T, n_kv), -np.inf, np.float32)
+    for t in range(T):
+        sel[t, cells[t]] = 0.0
+    causal = np.ascontiguousarray(causal_bits[:, :n_kv]).view(np.float16).astype(np.float32)
+    with np.errstate(invalid="ignore"):
+        out = _f16_bits(sel + causal)
+    res = np.full((T, row_len), F16_NEG_INF, np.uint16)
+    res[:, :n_kv] = out
+    return res

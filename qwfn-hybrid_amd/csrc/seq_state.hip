@@ -172,6 +172,112 @@ __global__ __launch_bounds__(FILL_THREADS) void k_qsa_tables(qsa_tables_args a) 
         for (int64_t i = t0; i < 4 * a.n_whole; i += stride) a.blk_pos_all[i] = (int32_t) ((i % a.n_whole) * a.ratio);
 }
 
+// ---- the prefill chunk's sparse-attention inputs (engine::fill_chunk_qsa,
+//      qwfn_engine.cpp:1276-1320), closed form per element. n_kv = n_past_c +
+//      Tc, n_blocks = ceil(n_kv / ratio), n_bid = n_kv / ratio whole blocks,
+//      dead = the partial tail block (n_bid) if there is one, else the last.
+struct qsa_chunk_args {
+    int32_t * cell_blk;    // [n_kv] or null
+    int32_t * blk_cells;   // [n_blocks * ratio] or null
+    int32_t * blk_pos;     // [4 * n_blocks] or null
+    float *   bias;        // [Tc][n_blocks], rows bias_ld floats apart, or null
+    int64_t   bias_ld;
+    int64_t   n_past_c, Tc, n_blocks;
+    int32_t   ratio;
+};
+
+// Row i (query q = n_past_c + i) of the bias at block b: the reference's fills
+// (0 before tail_b = min(n_bid, (q+1)/ratio), 1e9 up to n_bid, -inf after, the
+// dead block 1e9) followed by its -1e9 for positive entries of blocks wholly
+// after q.
+__device__ __forceinline__ float chunk_bias(int64_t b, int64_t q, int64_t r, int64_t n_bid, int64_t dead, bool have_dead) {
+    const int64_t tail_b = (q + 1) / r < n_bid ? (q + 1) / r : n_bid;
+    float v = b < tail_b ? 0.0f : (b < n_bid ? 1e9f : -INFINITY);
+    if (have_dead && b == dead) v = 1e9f;
+    if (b >= tail_b && v > 0.0f && b * r > q) v = -1e9f;
+    return v;
+}
+
+// blockIdx.y < Tc: bias row blockIdx.y; blockIdx.y == Tc: the three tables.
+__global__ __launch_bounds__(FILL_THREADS) void k_qsa_chunk(qsa_chunk_args a) {
+    const int64_t r = a.ratio, n_kv = a.n_past_c + a.Tc, n_bid = n_kv / r;
+    const bool have_dead = n_bid < a.n_blocks;
+    const int64_t dead = have_dead ? n_bid : a.n_blocks - 1;
+    const int64_t t0 = (int64_t) blockIdx.x * FILL_THREADS + threadIdx.x;
+    const int64_t stride = (int64_t) gridDim.x * FILL_THREADS;
+    if ((int64_t) blockIdx.y < a.Tc) {
+        if (!a.bias) return;
+        const int64_t q = a.n_past_c + blockIdx.y;
+        float * row = a.bias + (size_t) blockIdx.y * (size_t) a.bias_ld;
+        for (int64_t b = t0; b < a.n_blocks; b += stride) row[b] = chunk_bias(b, q, r, n_bid, dead, have_dead);
+        return;
+    }
+    if (a.cell_blk)
+        for (int64_t j = t0; j < n_kv; j += stride) a.cell_blk[j] = (int32_t) (j < n_bid * r ? j / r : dead);
+    if (a.blk_cells)
+        for (int64_t i = t0; i < a.n_blocks * r; i += stride) {
+            const int64_t b = i / r;
+            // whole blocks: their own cells; the partial tail block: its real
+            // cells, the last one repeated (n_blocks = ceil(n_kv / ratio), so no
+            // block lies past it)
+            a.blk_cells[i] = (int32_t) (b < n_bid ? i : (i < n_kv - 1 ? i : n_kv - 1));
+        }
+    if (a.blk_pos)
+        for (int64_t i = t0; i < 4 * a.n_blocks; i += stride) a.blk_pos[i] = (int32_t) ((i % a.n_blocks) * r);
+}
+
+// ---- the prefill's selection mask (graph_builder::qsa_mask, qwfn_graph.cpp:
+//      388-414): -inf everywhere, 0 at the query's selected cells, plus the
+//      causal mask. Block = query row t: its selected cells become a bitmap in
+//      LDS, then every 8-key group of the row is written once: the causal
+//      value where the key is selected, -inf elsewhere (and in the padding
+//      past n_kv). Cells outside [0, n_kv) are skipped and flagged.
+__global__ __launch_bounds__(FILL_THREADS) void k_qsa_mask(const int32_t * cells, int64_t width, int64_t cells_ld,
+                                                          const uint16_t * causal, int64_t causal_ld, int64_t n_kv,
+                                                          uint16_t * mask, int64_t mask_ld, uint32_t * status) {
+    extern __shared__ uint32_t sel[];   // ceil(n_kv / 32) words
+    const int64_t t = blockIdx.x;
+    const int64_t n_words = (n_kv + 31) / 32;
+    for (int64_t w = threadIdx.x; w < n_words; w += FILL_THREADS) sel[w] = 0u;
+    __syncthreads();
+    const int32_t * crow = cells + (size_t) t * (size_t) cells_ld;
+    bool bad = false;
+    for (int64_t j = threadIdx.x; j < width; j += FILL_THREADS) {
+        const int64_t c = crow[j];
+        if (c < 0 || c >= n_kv) { bad = true; continue; }
+        atomicOr(&sel[c >> 5], 1u << (c & 31));
+    }
+    if (__any(bad) && (threadIdx.x & 63) == 0 && status) atomicOr(status, DEVERR_SET_ROWS_INDEX);
+    __syncthreads();
+    const uint16_t * src = causal + (size_t) t * (size_t) causal_ld;
+    uint16_t * dst = mask + (size_t) t * (size_t) mask_ld;
+    const int64_t groups = (mask_ld + 7) / 8;
+    for (int64_t g = threadIdx.x; g < groups; g += FILL_THREADS) {
+        const int64_t j0 = g * 8;
+        uint16_t v[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int64_t j = j0 + e;
+            const bool on = j < n_kv && ((sel[j >> 5] >> (j & 31)) & 1u);
+            // selected: f16(+0 + c), which is c except that -0 becomes +0
+            const uint16_t c = on ? src[j] : F16_NINF;
+            v[e] = c == 0x8000u ? F16_ZERO : c;
+        }
+        if (j0 + 8 <= mask_ld && ((uintptr_t) (dst + j0) & 15) == 0) {
+            uint4 w;
+            w.x = v[0] | ((uint32_t) v[1] << 16);
+            w.y = v[2] | ((uint32_t) v[3] << 16);
+            w.z = v[4] | ((uint32_t) v[5] << 16);
+            w.w = v[6] | ((uint32_t) v[7] << 16);
+            store_nt16(dst + j0, w);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                if (j0 + e < mask_ld) dst[j0 + e] = v[e];
+        }
+    }
+}
+
 unsigned grid_for(int64_t n) {
     return (unsigned) std::max<int64_t>(1, std::min<int64_t>((n + FILL_THREADS - 1) / FILL_THREADS, 4096));
 }
@@ -643,6 +749,56 @@ int qwfn_cell_mask_f16(const int32_t * cells, int64_t n_cells, int64_t n_pad, in
         hipLaunchKernelGGL(k_cell_mask, dim3(grid_for(n_pad)), dim3(FILL_THREADS), 0, as_stream(stream), cells, n_cells, n_pad,
                            n_past, mask, gcells);
         return hip_check(hipGetLastError(), "cell_mask launch");
+    });
+}
+
+int qwfn_qsa_chunk_inputs(int64_t n_past_c, int64_t Tc, int32_t ratio, int32_t * cell_blk, int32_t * blk_cells,
+                          int32_t * blk_pos, float * bias, size_t bias_nb1, void * stream) {
+    return ::qwfn::abi_call("qsa_chunk_inputs", [&]() -> int {
+        if (n_past_c < 0 || Tc < 1 || ratio < 1) return set_error(QWFN_EINVAL, "qsa_chunk_inputs: need n_past_c >= 0, Tc >= 1, ratio >= 1");
+        if (Tc > 65535 - 1) return set_error(QWFN_ENOTSUP, "qsa_chunk_inputs: at most 65534 queries per chunk");
+        const int64_t n_kv = n_past_c + Tc;
+        if (n_kv >= (int64_t(1) << 31)) return set_error(QWFN_ENOTSUP, "qsa_chunk_inputs: n_kv must fit int32");
+        const int64_t n_blocks = (n_kv + ratio - 1) / ratio;
+        if (bias && (bias_nb1 % 4 || bias_nb1 < (size_t) n_blocks * 4))
+            return set_error(QWFN_EINVAL, "qsa_chunk_inputs: bias rows must be float [n_blocks] at a 4-byte multiple stride");
+        if ((cell_blk && !is_aligned(cell_blk, 4)) || (blk_cells && !is_aligned(blk_cells, 4)) ||
+            (blk_pos && !is_aligned(blk_pos, 4)) || (bias && !is_aligned(bias, 4)))
+            return set_error(QWFN_EALIGN, "qsa_chunk_inputs: misaligned pointer");
+        qsa_chunk_args a{};
+        a.cell_blk = cell_blk; a.blk_cells = blk_cells; a.blk_pos = blk_pos; a.bias = bias;
+        a.bias_ld = (int64_t) (bias_nb1 / 4);
+        a.n_past_c = n_past_c; a.Tc = Tc; a.n_blocks = n_blocks; a.ratio = ratio;
+        const int64_t n = std::max<int64_t>({n_kv, n_blocks * ratio, 4 * n_blocks});
+        const dim3 g(grid_for(std::max<int64_t>(n, n_blocks)), (unsigned) (Tc + 1));
+        hipLaunchKernelGGL(k_qsa_chunk, g, dim3(FILL_THREADS), 0, as_stream(stream), a);
+        return hip_check(hipGetLastError(), "qsa_chunk_inputs launch");
+    });
+}
+
+int qwfn_qsa_mask_f16(const int32_t * cells, int64_t width, size_t cells_nb1, const uint16_t * causal,
+                      size_t causal_nb1, int64_t n_kv, int64_t T, uint16_t * mask, size_t mask_nb1, void * stream) {
+    return ::qwfn::abi_call("qsa_mask_f16", [&]() -> int {
+        if (!cells || !causal || !mask) return set_error(QWFN_EINVAL, "qsa_mask: NULL pointer");
+        if (width < 0 || n_kv < 1 || T < 1) return set_error(QWFN_EINVAL, "qsa_mask: need width >= 0, n_kv >= 1, T >= 1");
+        if (cells_nb1 % 4 || cells_nb1 < (size_t) width * 4 || causal_nb1 % 2 || causal_nb1 < (size_t) n_kv * 2 ||
+            mask_nb1 % 2 || mask_nb1 < (size_t) n_kv * 2)
+            return set_error(QWFN_EINVAL, "qsa_mask: rows must hold width cells, n_kv causal values and n_kv mask values");
+        if (!is_aligned(cells, 4) || !is_aligned(causal, 2) || !is_aligned(mask, 2))
+            return set_error(QWFN_EALIGN, "qsa_mask: misaligned pointer");
+        if (T > 0x7fffffff) return set_error(QWFN_ENOTSUP, "qsa_mask: too many rows");
+        const size_t lds = (size_t) ((n_kv + 31) / 32) * 4;
+        if (lds > 64 * 1024) return set_error(QWFN_ENOTSUP, "qsa_mask: n_kv beyond 524288 keys");
+        // the output (T whole rows) must not overlap the causal mask it reads
+        const char * m0 = (const char *) mask, * m1 = m0 + (size_t) T * mask_nb1;
+        const char * c0 = (const char *) causal, * c1 = c0 + (size_t) (T - 1) * causal_nb1 + (size_t) n_kv * 2;
+        if (m0 < c1 && c0 < m1) return set_error(QWFN_EINVAL, "qsa_mask: mask and causal overlap");
+        uint32_t * status = nullptr;
+        if (int rc = status_word(&status)) return rc;
+        hipLaunchKernelGGL(k_qsa_mask, dim3((unsigned) T), dim3(FILL_THREADS), lds, as_stream(stream), cells, width,
+                           (int64_t) (cells_nb1 / 4), causal, (int64_t) (causal_nb1 / 2), n_kv, mask,
+                           (int64_t) (mask_nb1 / 2), status);
+        return hip_check(hipGetLastError(), "qsa_mask launch");
     });
 }
 

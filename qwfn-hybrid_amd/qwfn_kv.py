@@ -146,7 +146,8 @@ EXPORTS = [
     "qwfn_state_bytes", "qwfn_state_host_bytes", "qwfn_state_rollback_bytes", "qwfn_state_n_ctx",
     "qwfn_state_summary", "qwfn_state_n_past", "qwfn_state_rollback_depth", "qwfn_state_step_done",
     "qwfn_state_reset", "qwfn_state_rollback", "qwfn_snapshot_parts", "qwfn_snapshot_save", "qwfn_snapshot_load",
-    "qwfn_causal_mask_f16", "qwfn_cell_mask_f16", "qwfn_qsa_bucket", "qwfn_qsa_decode_prepare",
+    "qwfn_causal_mask_f16", "qwfn_cell_mask_f16", "qwfn_qsa_chunk_inputs", "qwfn_qsa_mask_f16",
+    "qwfn_qsa_bucket", "qwfn_qsa_decode_prepare",
     "qwfn_qsa_bias_rebuild", "qwfn_qsa_tables",
     "qwfn_snap_pool_create", "qwfn_snap_pool_destroy", "qwfn_snap_pool_count", "qwfn_snap_pool_bytes",
     "qwfn_snap_pool_entry", "qwfn_snap_pool_save", "qwfn_snap_pool_best", "qwfn_snap_pool_load",
@@ -239,6 +240,8 @@ def load(path: str = LIB_PATH):
     L.qwfn_snapshot_load.argtypes = [PV, i32, i32, PV, PS, i32, i32, vp]
     L.qwfn_causal_mask_f16.argtypes = [vp, i64, i64, i64, sz, vp]
     L.qwfn_cell_mask_f16.argtypes = [vp, i64, i64, i32, vp, vp, vp]
+    L.qwfn_qsa_chunk_inputs.argtypes = [i64, i64, i32, vp, vp, vp, vp, sz, vp]
+    L.qwfn_qsa_mask_f16.argtypes = [vp, i64, sz, vp, sz, i64, i64, vp, sz, vp]
     L.qwfn_qsa_bucket.argtypes = [i32, i32, i64]
     L.qwfn_qsa_bucket.restype = i64
     L.qwfn_qsa_decode_prepare.argtypes = [ctypes.POINTER(QsaInputs), vp, i32, vp]

@@ -215,6 +215,51 @@ def cell_mask_f16(cells, n_past: int, n_pad: int, mask, gcells=None, stream=None
                                         gcells.data_ptr() if gcells is not None else None, K._stream(stream)))
 
 
+def _dev_check(name, **tensors):
+    for k, t in tensors.items():
+        if t is not None and not t.is_cuda:
+            raise ValueError(f"{name}: {k} must be device memory")
+
+
+def qsa_chunk_inputs(n_past_c: int, Tc: int, ratio: int, cell_blk=None, blk_cells=None, blk_pos=None, bias=None,
+                     stream=None) -> int:
+    """engine::fill_chunk_qsa on the device; returns n_blocks = ceil((n_past_c + Tc) / ratio).
+    cell_blk: i32 [n_kv]; blk_cells: i32 [n_blocks * ratio]; blk_pos: i32 [4 * n_blocks];
+    bias: f32 [Tc, >= n_blocks] with contiguous rows. Any may be None."""
+    import torch
+    n_kv = n_past_c + Tc
+    nb = -(-n_kv // ratio)
+    _dev_check("qsa_chunk_inputs", cell_blk=cell_blk, blk_cells=blk_cells, blk_pos=blk_pos, bias=bias)
+    for name, t, n in (("cell_blk", cell_blk, n_kv), ("blk_cells", blk_cells, nb * ratio), ("blk_pos", blk_pos, 4 * nb)):
+        if t is not None and (t.dtype != torch.int32 or not t.is_contiguous() or t.numel() < n):
+            raise ValueError(f"qsa_chunk_inputs: {name} must be contiguous i32 with at least {n} entries")
+    if bias is not None and (bias.dtype != torch.float32 or bias.dim() != 2 or bias.shape[0] < Tc
+                             or bias.shape[1] < nb or bias.stride(1) != 1):
+        raise ValueError("qsa_chunk_inputs: bias must be f32 [Tc, >= n_blocks] with contiguous rows")
+    p = lambda t: t.data_ptr() if t is not None else None
+    K.check(K.load().qwfn_qsa_chunk_inputs(n_past_c, Tc, ratio, p(cell_blk), p(blk_cells), p(blk_pos), p(bias),
+                                           bias.stride(0) * 4 if bias is not None else 0, K._stream(stream)))
+    return nb
+
+
+def qsa_mask_f16(cells, causal, n_kv: int, mask, stream=None):
+    """graph_builder::qsa_mask on the device: cells i32 [T, width] (contiguous rows), causal
+    f16 [T, >= n_kv] and mask f16 [T, row] (2-byte elements, contiguous rows); row t of mask
+    becomes causal where selected, -inf elsewhere (padding included)."""
+    import torch
+    _dev_check("qsa_mask_f16", cells=cells, causal=causal, mask=mask)
+    f16 = (torch.float16,) + ((torch.uint16,) if hasattr(torch, "uint16") else ())
+    if cells.dtype != torch.int32 or cells.dim() != 2 or cells.stride(1) != 1:
+        raise ValueError("qsa_mask_f16: cells must be i32 [T, width] with contiguous rows")
+    for name, t in (("causal", causal), ("mask", mask)):
+        if t.dim() != 2 or t.dtype not in f16 or t.stride(1) != 1 or t.shape[1] < n_kv or t.shape[0] < cells.shape[0]:
+            raise ValueError(f"qsa_mask_f16: {name} must be f16 [T, >= n_kv] with contiguous rows")
+    T = cells.shape[0]
+    K.check(K.load().qwfn_qsa_mask_f16(cells.data_ptr(), cells.shape[1], cells.stride(0) * 4, causal.data_ptr(),
+                                       causal.stride(0) * 2, n_kv, T, mask.data_ptr(), mask.stride(0) * 2,
+                                       K._stream(stream)))
+
+
 # ------------------------------------------- decode-time sparse-attention inputs
 
 class QsaDecodeInputs:

@@ -478,3 +478,66 @@ def test_qsa_select_wrapper_checks_shapes():
     # well-shaped host tensors: the kernels would read host addresses, so the wrapper refuses them
     with pytest.raises(ValueError, match="GPU tensor"):
         S.qsa_select_cells(pool=pool, q=q, bias=bias, k_blocks=k, blk_cells=blk, ratio=ratio, cells=cells, stream=0)
+
+
+# ---- the prefill chunk's sparse-attention inputs (fill_chunk_qsa, qsa_mask)
+
+@pytest.mark.parametrize("n_past_c,Tc,ratio", [(0, 512, 4), (16384, 512, 4), (16385, 510, 4), (7, 1, 4), (0, 3, 4),
+                                               (100, 37, 32), (5, 9, 1), (4093, 512, 4), (0, 1, 4), (31, 64, 32)])
+def test_fill_chunk_qsa_closed_form(n_past_c, Tc, ratio):
+    """The reference's procedural fills against the per-block closed form: a whole
+    block that ends at or before the query scores on its merit (0), the block that
+    holds the query mid-block and the partial tail block at or before it are forced
+    (1e9), a block wholly after the query is pushed out (-1e9); no block is -inf
+    since n_blocks = ceil(n_kv / ratio). The tables: every cell's block, each
+    block's cells (the tail block's last real cell repeated), each block's first
+    position in all four rope sections."""
+    o = SO.fill_chunk_qsa(n_past_c, Tc, ratio)
+    n_kv = n_past_c + Tc
+    nb = -(-n_kv // ratio)
+    assert o["n_blocks"] == nb
+    np.testing.assert_array_equal(o["cell_blk"], np.arange(n_kv) // ratio)
+    np.testing.assert_array_equal(o["blk_cells"], np.minimum(np.arange(nb * ratio), n_kv - 1))
+    np.testing.assert_array_equal(o["blk_pos"], np.tile(np.arange(nb) * ratio, 4))
+    b = np.arange(nb)
+    start, last = b * ratio, np.minimum((b + 1) * ratio, n_kv) - 1
+    whole = (b + 1) * ratio <= n_kv
+    for i in range(Tc):
+        q = n_past_c + i
+        want = np.where(start > q, -1e9, np.where(whole & (last <= q), 0.0, 1e9)).astype(np.float32)
+        np.testing.assert_array_equal(o["bias"][i], want, err_msg=f"row {i}")
+        assert (o["bias"][i] == 1e9).sum() == (0 if (q + 1) % ratio == 0 and q + 1 <= (n_kv // ratio) * ratio else 1)
+
+
+def _causal_bits(T, n_past, row_len):
+    m = np.full((T, row_len), SO.F16_NEG_INF, np.uint16)
+    for t in range(T):
+        m[t, :n_past + t + 1] = SO.F16_ZERO
+    return m
+
+
+def test_qsa_mask_limits_and_zeros():
+    """Every cell selected gives the causal mask; none gives -inf; otherwise the
+    zeros are exactly the selected cells the query may see, repeats changing
+    nothing; the padding past n_kv is -inf; a selected -0 becomes +0 (f16 add)."""
+    rng = np.random.default_rng(3)
+    T, n_past, row_len = 6, 290, 304
+    n_kv = n_past + T
+    causal = _causal_bits(T, n_past, row_len)
+    every = np.tile(np.arange(n_kv, dtype=np.int32), (T, 1))
+    got = SO.qsa_mask(every, causal, n_kv, row_len)
+    np.testing.assert_array_equal(got[:, :n_kv], causal[:, :n_kv])
+    assert (got[:, n_kv:] == SO.F16_NEG_INF).all()
+    none = np.zeros((T, 0), np.int32)
+    assert (SO.qsa_mask(none, causal, n_kv, row_len) == SO.F16_NEG_INF).all()
+    cells = rng.integers(0, n_kv, (T, 120)).astype(np.int32)
+    cells[:, 60:70] = cells[:, :10]                                  # repeats
+    got = SO.qsa_mask(cells, causal, n_kv, row_len)
+    for t in range(T):
+        want = {int(c) for c in cells[t] if c <= n_past + t}
+        assert set(np.flatnonzero(got[t] == SO.F16_ZERO).tolist()) == want
+        assert (got[t][got[t] != SO.F16_ZERO] == SO.F16_NEG_INF).all()
+    negz = causal.copy()
+    negz[:, 5] = 0x8000
+    got = SO.qsa_mask(every, negz, n_kv, row_len)
+    assert (got[:, 5] == SO.F16_ZERO).all()
