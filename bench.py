@@ -572,7 +572,62 @@ def measure_rows(K, torch, np, dev, gen) -> dict:
                                         "frac_of_f16_mfma_peak": round(flops / (us * 1e-6) / 2.5e15, 4)}
         del kc, vc, pws
     torch.cuda.empty_cache()
+    rows.update(measure_qsa_prefill_row(K, torch, np, dev, gen))
     return rows
+
+
+def measure_qsa_prefill_row(K, torch, np, dev, gen) -> dict:
+    """The reference's default prefill with QSA on (qwfn_graph.cpp:313-414, :466) for a
+    512-query chunk at depth 16384, 16 heads over 2 KV heads: the chunk's block tables
+    and bias, the pooled keys of its 4224 blocks of 4, each query's top 513 blocks
+    (indexer: 4 heads of 128), the causal and the selection masks, and flash attention
+    over the selection mask; also the attention alone. As the GPU test composes it."""
+    import qwfn_state as S
+    d0, T, ratio, nh, nh_kv, hd, kb = 16384, 512, 4, 16, 2, 256, 513
+    n_kv = d0 + T
+    nb = n_kv // ratio
+    row = (n_kv + 63) // 64 * 64
+
+    def cache():
+        c = torch.randint(-100, 100, (n_kv, ROW), dtype=torch.int8, device=dev, generator=gen).view(torch.uint8)
+        c.view(-1, 34)[:, 0] = 0x1F
+        c.view(-1, 34)[:, 1] = 0x21
+        return c
+    kc, vc = cache(), cache()
+    ic = torch.randn((n_kv, 128), generator=gen, device=dev).to(torch.float16)
+    knw = torch.rand(128, generator=gen, device=dev) + 0.5
+    q_idx = torch.randn((T, 4, 128), generator=gen, device=dev)
+    bc = torch.empty(nb * ratio, dtype=torch.int32, device=dev)
+    bp = torch.empty(4 * nb, dtype=torch.int32, device=dev)
+    bias = torch.empty((T, nb), dtype=torch.float32, device=dev)
+    pool = torch.empty((nb, 128), dtype=torch.float16, device=dev)
+    cells = torch.empty((T, kb * ratio), dtype=torch.int32, device=dev)
+    wsel = torch.empty(K.load().qwfn_qsa_select_workspace_size(nb, T), dtype=torch.uint8, device=dev)
+    causal = torch.empty((T, row), dtype=torch.float16, device=dev)
+    qmask = torch.empty((T, row), dtype=torch.float16, device=dev)
+    pq = torch.randn((1, T, nh, hd), generator=gen, device=dev)
+    pout = torch.empty((1, T, nh, hd), dtype=torch.float32, device=dev)
+    pk, pv, pmv = K.cache_attn_view(kc, n_kv, nh_kv), K.cache_attn_view(vc, n_kv, nh_kv), K.mask_view(qmask)
+    pws = torch.empty(max(256, K.fattn_workspace_size(K.q_view(pq), pk, pv, pmv)), dtype=torch.uint8, device=dev)
+
+    def chain(k):
+        S.qsa_chunk_inputs(d0, T, ratio, None, bc, bp, bias)
+        K.qsa_pool_rebuild(ic, n_kv, ratio, knw, pool)
+        S.qsa_select_cells(pool, q_idx, bias, kb, bc, ratio, cells, ws=wsel)
+        S.causal_mask_f16(causal, n_kv, T, d0)
+        S.qsa_mask_f16(cells, causal, n_kv, qmask)
+        K.flash_attn_ext(K.q_view(pq), pk, pv, pmv, 1 / 16, K.out_view(pout), ws=pws)
+    us_chain = timed(torch, chain, 5)
+    us_attn = timed(torch, lambda k: K.flash_attn_ext(K.q_view(pq), pk, pv, pmv, 1 / 16, K.out_view(pout), ws=pws), 5)
+    visible = int((qmask[:, :n_kv] == 0).sum().item())
+    flops = 4 * nh * hd * visible                               # QK^T and PV over the visible keys
+    return {"prefill_512_at_16384_qsa": {
+        "us_per_layer": round(us_chain, 1), "us_attention": round(us_attn, 1), "us_inputs": round(us_chain - us_attn, 1),
+        "blocks": nb, "k_blocks": kb, "visible_keys_per_query": round(visible / T, 1), "flops": flops,
+        "TFLOPs": round(flops / (us_attn * 1e-6) / 1e12, 2),
+        "frac_of_f16_mfma_peak": round(flops / (us_attn * 1e-6) / 2.5e15, 4),
+        "what": "chunk tables + pool of 4224 blocks + top-513 select for 512 queries + causal and selection masks "
+                "+ k_fa_pre over the selection mask"}}
 
 
 def main() -> int:
