@@ -61,13 +61,25 @@ def parse():
 
 
 def cpu_model() -> str | None:
+    """The host CPU: model name, family / model / stepping, and the widest x86 vector
+    extension it reports (what a -march=native build can use)."""
+    info = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            k, _, v = line.partition(":")
+            k = k.strip()
+            if k in ("model name", "cpu family", "model", "stepping", "flags") and k not in info:
+                info[k] = v.strip()
+            if len(info) == 5:
+                break
     except OSError:
-        pass
-    return None
+        return None
+    if "model name" not in info:
+        return None
+    flags = set(info.get("flags", "").split())
+    vec = next((f for f in ("avx512f", "avx2", "avx", "sse4_2") if f in flags), "none")
+    return (f"{info['model name']} (family {info.get('cpu family', '?')}, model {info.get('model', '?')}, "
+            f"stepping {info.get('stepping', '?')}; widest vector ISA: {vec})")
 
 
 def timed(torch, fn, reps: int) -> float:
@@ -794,7 +806,7 @@ def main() -> int:
     if args.long_depth:
         ld = args.long_depth
         n_kv_l = ld + T
-        n_sets_l = 4                                   # 4 x 71 MB: more than the Infinity Cache holds
+        n_sets_l = 8                                   # 8 x 71.8 MB = 574 MB: over twice the 256 MB Infinity Cache
         lcaches = []
         for s in range(n_sets_l):
             kc = torch.zeros((n_kv_l, ROW), dtype=torch.uint8, device=dev)
@@ -851,26 +863,35 @@ def main() -> int:
             import statistics
 
             import kvdata as KD
-            # the host threads given to this GPU's job (at most 16, its share of the host)
-            cores = min(16, len(os.sched_getaffinity(0)))
+            # every core the job may use: the affinity set, capped at the 16 cores that
+            # are one GPU's share of the host
+            affinity = len(os.sched_getaffinity(0))
+            cores = min(16, affinity)
             kc, vc = caches[0][0]
             kc_h, vc_h = kc.cpu().numpy(), vc.cpu().numpy()
             q_h = q[0].cpu().numpy()[0]
 
             def one():
                 t1 = time.perf_counter()
-                KD.oracle_attn(q_h, kc_h, vc_h, n_kv, nh_kv, mask_np, scale, threads=cores)
+                KD.oracle_attn(q_h, kc_h, vc_h, n_kv, nh_kv, mask_np, scale, threads=cores, native=True)
                 return time.perf_counter() - t1
+            # the native build computes what the checker build does, bit for bit
+            chk = KD.oracle_attn(q_h, kc_h, vc_h, n_kv, nh_kv, mask_np, scale, threads=cores)
+            nat = KD.oracle_attn(q_h, kc_h, vc_h, n_kv, nh_kv, mask_np, scale, threads=cores, native=True)
+            if not np.array_equal(chk, nat):
+                raise RuntimeError("the -march=native oracle build differs from the checker build")
             one(), one()
             times = []
             while len(times) < 10 or (sum(times) < args.cpu_seconds and len(times) < 200):
                 times.append(one())
             med = statistics.median(times)
             cpu = {"value": round(attn_bytes / med / 1e9, 3), "unit": "GB/s", "cores": cores,
-                   "kind": "port", "cpu_model": cpu_model(),
-                   "sample": f"one layer's verify attention (T={T}, {n_kv} q8_0 rows, 2 KV heads) in the C "
-                             f"restatement of ggml-cpu flash_attn_ext on {cores} threads: median of {len(times)} "
-                             f"reps after 2 warm-ups, {med * 1e6:.0f} us/layer (min {min(times) * 1e6:.0f})",
+                   "affinity_cores": affinity, "kind": "port", "cpu_model": cpu_model(),
+                   "build": "gcc -O3 -march=native -ffp-contract=off (oracle/Makefile liboracle_native.so)",
+                   "sample": f"one layer's verify attention (T={T}, {n_kv} q8_0 rows, 2 KV heads) in the scalar C "
+                             f"restatement of ggml-cpu flash_attn_ext, built -O3 -march=native for this host, on "
+                             f"{cores} threads: median of {len(times)} reps after 2 warm-ups, {med * 1e6:.0f} "
+                             f"us/layer (min {min(times) * 1e6:.0f})",
                    "us_per_layer": round(med * 1e6, 1)}
             log(f"[bench] cpu baseline: {cpu}")
         except Exception as e:

@@ -202,12 +202,33 @@ def view(data: np.ndarray, ne, nb) -> View:
     return v
 
 
+NATIVE_PATH = os.path.join(HERE, "liboracle_native.so")
+_native = None
+
+
+def native_lib():
+    """The same C source built with -march=native (`make -C oracle native`): a separate
+    library used only to time the CPU baseline; the tests check against lib()."""
+    global _native
+    if _native is None:
+        # built on first use in each process, for the host it runs on (a build
+        # shipped from another machine might use instructions this CPU lacks)
+        subprocess.run(["make", "-B", "-s", "-C", HERE, "liboracle_native.so"], check=True)
+        L = ctypes.CDLL(NATIVE_PATH)
+        L.oracle_flash_attn_ext_q8_0.argtypes = lib().oracle_flash_attn_ext_q8_0.argtypes
+        L.oracle_flash_attn_ext_q8_0.restype = lib().oracle_flash_attn_ext_q8_0.restype
+        _native = L
+    return _native
+
+
 def flash_attn_ext(qv: View, kv: View, vv: View, mv: View | None, scale: float, out_shape,
-                   q_variant: int = Q8_X86, dot_variant: int = Q8_X86, n_threads: int = 1) -> np.ndarray:
+                   q_variant: int = Q8_X86, dot_variant: int = Q8_X86, n_threads: int = 1,
+                   native: bool = False) -> np.ndarray:
     dst = np.zeros(out_shape, dtype=np.float32)
-    rc = lib().oracle_flash_attn_ext_q8_0(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv),
-                                          ctypes.byref(mv) if mv is not None else None, scale, _p(dst),
-                                          q_variant, dot_variant, n_threads)
+    L = native_lib() if native else lib()
+    rc = L.oracle_flash_attn_ext_q8_0(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv),
+                                      ctypes.byref(mv) if mv is not None else None, scale, _p(dst),
+                                      q_variant, dot_variant, n_threads)
     if rc:
         raise ValueError(f"oracle flash_attn_ext failed ({rc})")
     return dst

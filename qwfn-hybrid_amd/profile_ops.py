@@ -29,7 +29,7 @@ def main() -> int:
     ap.add_argument("--depth", type=int, default=16384)
     ap.add_argument("--T", type=int, default=3)
     ap.add_argument("--reps", type=int, default=10)
-    ap.add_argument("--sets", type=int, default=4)
+    ap.add_argument("--sets", type=int, default=8)
     ap.add_argument("--mb", type=int, default=1024)
     ap.add_argument("--lib", default=None, help="library path (default: the package's build)")
     ap.add_argument("--append", action="store_true", help="verify: append the T new K/V rows in the same launch")

@@ -65,14 +65,15 @@ def make_cache(rows_f32: np.ndarray, n_ctx: int, variant: int = O.Q8_X86, first_
 
 
 def oracle_attn(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, n_kv: int, n_head_kv: int,
-                mask: np.ndarray | None, scale: float, variant: int = O.Q8_X86, threads: int = 8) -> np.ndarray:
+                mask: np.ndarray | None, scale: float, variant: int = O.Q8_X86, threads: int = 8,
+                native: bool = False) -> np.ndarray:
     """ggml-cpu flash_attn_ext over a token-major cache. q [T, nh, hd]; mask F16 bits [T, n_kv] or None.
-    Returns [T, nh, hd] float32."""
+    Returns [T, nh, hd] float32. native: the -march=native build of the same C (CPU timing only)."""
     T, nh, hd = q.shape
     q = np.ascontiguousarray(q, np.float32)
     qv, kv, vv = O.cache_views(q, kc, vc, n_kv, n_head_kv, hd)
     mv = O.mask_view(mask) if mask is not None else None
-    return O.flash_attn_ext(qv, kv, vv, mv, scale, (T, nh, hd), variant, variant, threads)
+    return O.flash_attn_ext(qv, kv, vv, mv, scale, (T, nh, hd), variant, variant, threads, native=native)
 
 
 def oracle_attn_f64(q, kc, vc, n_kv, n_head_kv, mask, scale, quantize_q: int = 2) -> np.ndarray:
