@@ -45,6 +45,7 @@ enum qwfn_type {
     QWFN_TYPE_F16  = 1,
     QWFN_TYPE_Q8_0 = 8,
     QWFN_TYPE_I32  = 26,
+    QWFN_TYPE_BF16 = 30,
 };
 
 enum qwfn_status {
@@ -308,15 +309,23 @@ typedef struct qwfn_rope_cfg {
 /* The layer's K/V producer for a decode or verify step (two launches: the
  * projections, then norm, rope and quantisation): K =
  * attn_k . cur and V = attn_v . cur (ggml_mul_mat with F16 weights: cur
- * converted to F16, F16 products summed in F32), each K head RMS-normed and
+ * converted to F16, F16 products summed in F32; with BF16 weights: cur
+ * converted to BF16, round to nearest even, BF16 products summed in F32),
+ * each K head RMS-normed and
  * multiplied by k_norm_w (F32 [256]), roped (IMROPE at pos, I32 [4 * T]
  * device: the T t positions, then h, w, e, as ggml_rope_multi reads them),
  * then K and V quantised (q8_0, variant as in qwfn_set_rows_q8_0) into cache
  * rows first_row .. first_row + T - 1. Replaces qwfn_graph.cpp:441-451 (the
  * mul_mats and rms), :446-451 / :129-132 (rope) and :370-384 (kv_append).
  * cur: F32 [n_embd, T] (T <= 16, n_embd a multiple of 8, T * n_embd <=
- * 65536, 16-byte aligned rows); wk, wv: F16 [n_embd, kv_dim] (kv_dim = 256 *
- * n_head_kv <= 2048, 16-byte aligned rows); caches: q8_0 [kv_dim, n_rows]. The projected rows
+ * 65536, 16-byte aligned rows); wk, wv: both F16 or both BF16 [n_embd,
+ * kv_dim] (kv_dim = 256 * n_head_kv <= 2048, 16-byte aligned rows). Weights
+ * stored quantised (the reference model's GGUF holds one F16 tensor, 484 BF16
+ * and the rest in k-quant / i-quant types; which of these attn_k and attn_v
+ * are is not recorded in its logs) must be converted by the caller to F16
+ * (or BF16) once at load: ggml would instead quantise cur to q8_K for them,
+ * so for such weights parity with ggml's projection is unpinned.
+ * caches: q8_0 [kv_dim, n_rows]. The projected rows
  * pass through a device-resident staging buffer of the library (one per GPU):
  * calls that overlap on one GPU race. The K/V bytes equal ggml's quantiser on
  * the F32 rows this kernel computes; those rows differ from ggml-cpu's only

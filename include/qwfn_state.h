@@ -273,7 +273,8 @@ int qwfn_set_rows_f16(const qwfn_tensor * dst, const qwfn_tensor * src, const qw
  * blk_pos[0..3] -- rounded to F16 into row *blk_idx of the pool cache (F16
  * [pool_rows][idx_dim]). write_idx, member_idx, blk_pos and blk_idx are the
  * device inputs qwfn_qsa_decode_prepare writes. Out-of-range rows are
- * skipped and flagged in qwfn_device_status. */
+ * skipped and flagged in qwfn_device_status. Both caches are rows packed at
+ * idx_dim values (row r at element r * idx_dim): there is no row stride. */
 int qwfn_qsa_pool_decode(uint16_t * idx_cache, int64_t ic_rows, const float * k_raw, const int32_t * write_idx,
                          const int32_t * member_idx, int32_t ratio, const int32_t * blk_pos, const int32_t * blk_idx,
                          const float * k_norm_w, uint16_t * pool, int64_t pool_rows, const qwfn_qsa_pool_cfg * cfg,
@@ -283,7 +284,8 @@ int qwfn_qsa_pool_decode(uint16_t * idx_cache, int64_t ic_rows, const float * k_
  * (engine::qsa_pool_rebuild, qwfn_engine.cpp:1121-1145, through
  * graph_builder::qsa_pool_rebuild, qwfn_graph.cpp:478-495): block b <
  * n_past / ratio pools index-cache rows b*ratio .. b*ratio + ratio - 1 at
- * position b*ratio into pool row b. One launch for all blocks. */
+ * position b*ratio into pool row b. One launch for all blocks. Rows packed
+ * at idx_dim values, as in qwfn_qsa_pool_decode. */
 int qwfn_qsa_pool_rebuild(const uint16_t * idx_cache, int64_t ic_rows, int64_t n_past, int32_t ratio,
                           const float * k_norm_w, uint16_t * pool, int64_t pool_rows, const qwfn_qsa_pool_cfg * cfg,
                           void * stream);

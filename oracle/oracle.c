@@ -494,15 +494,33 @@ void oracle_qsa_pool_blocks(const uint16_t * ic, int64_t idx_dim, const int32_t 
 /* The attention layer's K/V producer for T tokens (qwfn_graph.cpp:441-451 for
  * the projections, attn_k_norm and rope; :370-384 / :623-624 for the q8_0
  * append): ggml_mul_mat with F16 weights (the F32 rows converted to F16, the
- * F16 products summed; summed in double here, which ggml's F32 accumulation
+ * F16 products summed) or BF16 weights (w_bf16: the rows converted to BF16;
+ * the products summed; summed in double here, which ggml's F32 accumulation
  * order matches to within a float rounding: parity of the projection is to a
  * tolerance, of everything after it bit for bit), K rms-normed times the
  * weight and roped, then both quantised with quantize_row_q8_0 (variant). */
 
+/* F32 -> BF16: the upper 16 bits after rounding to nearest, ties to even; a
+ * NaN keeps its sign and top payload bits and is made quiet. BF16 -> F32 is
+ * the exact inverse placement of the 16 bits. */
+uint16_t oracle_fp32_to_bf16(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t) ((u >> 16) | 0x40u);
+    return (uint16_t) ((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+float oracle_bf16_to_fp32(uint16_t h) {
+    const uint32_t u = (uint32_t) h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
 void oracle_kv_produce_q8_0(const float * cur, int64_t E, int64_t T, const uint16_t * wk, const uint16_t * wv,
                             int64_t kv_dim, const float * k_norm_w, const int32_t * pos, const int sections[4],
                             int n_dims, float freq_base, float eps, void * k_rows, void * v_rows, float * k_f32,
-                            float * v_f32, int variant) {
+                            float * v_f32, int variant, int w_bf16) {
     const int64_t hd = 256;
     const size_t row_bytes = (size_t) (kv_dim / ORACLE_QK8_0) * 34;
     float * c16 = malloc(sizeof(float) * (size_t) E);
@@ -510,12 +528,17 @@ void oracle_kv_produce_q8_0(const float * cur, int64_t E, int64_t T, const uint1
     float * v = k + kv_dim;
     float * tmp = malloc(sizeof(float) * (size_t) hd * 2);
     for (int64_t t = 0; t < T; t++) {
-        for (int64_t e = 0; e < E; e++) c16[e] = oracle_fp16_to_fp32(oracle_fp32_to_fp16(cur[t * E + e]));
+        /* ggml_mul_mat converts src1 to the weights' vec_dot type: F16 or BF16 */
+        for (int64_t e = 0; e < E; e++)
+            c16[e] = w_bf16 ? oracle_bf16_to_fp32(oracle_fp32_to_bf16(cur[t * E + e]))
+                            : oracle_fp16_to_fp32(oracle_fp32_to_fp16(cur[t * E + e]));
         for (int64_t o = 0; o < kv_dim; o++) {
             double sk = 0.0, sv = 0.0;
             for (int64_t e = 0; e < E; e++) {
-                sk += (double) oracle_fp16_to_fp32(wk[o * E + e]) * (double) c16[e];
-                sv += (double) oracle_fp16_to_fp32(wv[o * E + e]) * (double) c16[e];
+                const float a = w_bf16 ? oracle_bf16_to_fp32(wk[o * E + e]) : oracle_fp16_to_fp32(wk[o * E + e]);
+                const float b = w_bf16 ? oracle_bf16_to_fp32(wv[o * E + e]) : oracle_fp16_to_fp32(wv[o * E + e]);
+                sk += (double) a * (double) c16[e];
+                sv += (double) b * (double) c16[e];
             }
             k[o] = (float) sk;
             v[o] = (float) sv;

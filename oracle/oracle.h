@@ -130,7 +130,11 @@ void oracle_qsa_pool_blocks(const uint16_t * ic, int64_t idx_dim, const int32_t 
 void oracle_kv_produce_q8_0(const float * cur, int64_t E, int64_t T, const uint16_t * wk, const uint16_t * wv,
                             int64_t kv_dim, const float * k_norm_w, const int32_t * pos, const int sections[4],
                             int n_dims, float freq_base, float eps, void * k_rows, void * v_rows, float * k_f32,
-                            float * v_f32, int variant);
+                            float * v_f32, int variant, int w_bf16);
+/* w_bf16: the weights are BF16 bits and the rows are rounded to BF16 (round
+ * to nearest even) instead of F16. */
+uint16_t oracle_fp32_to_bf16(float f);
+float    oracle_bf16_to_fp32(uint16_t h);
 
 /* Gated delta rule (ggml_gated_delta_net as qwfn_graph.cpp:258 calls it; the
  * op lives in the reference's llama.cpp fork, absent here, so this restates

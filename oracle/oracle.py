@@ -72,7 +72,11 @@ def lib():
         L.oracle_rope_multi_f32.argtypes = [vp, vp, i64, ctypes.c_int, vp, vp, ctypes.c_int, ctypes.c_float]
         L.oracle_set_rows_f16.argtypes = [vp, i64, i64, vp, vp, i64]
         L.oracle_kv_produce_q8_0.argtypes = [vp, i64, i64, vp, vp, i64, vp, vp, vp, ctypes.c_int, ctypes.c_float,
-                                             ctypes.c_float, vp, vp, vp, vp, ctypes.c_int]
+                                             ctypes.c_float, vp, vp, vp, vp, ctypes.c_int, ctypes.c_int]
+        L.oracle_fp32_to_bf16.argtypes = [ctypes.c_float]
+        L.oracle_fp32_to_bf16.restype = ctypes.c_uint16
+        L.oracle_bf16_to_fp32.argtypes = [ctypes.c_uint16]
+        L.oracle_bf16_to_fp32.restype = ctypes.c_float
         L.oracle_gated_delta_net.argtypes = [vp, i64, vp, i64, vp, i64, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64,
                                              i64, ctypes.c_float]
         L.oracle_qsa_pool_blocks.argtypes = [vp, i64, vp, i64, i64, vp, vp, vp, ctypes.c_float, ctypes.c_float,
@@ -341,12 +345,20 @@ def qsa_pool_blocks(ic_bits: np.ndarray, members: np.ndarray, r: int, k_norm_w: 
     return out
 
 
+def fp32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """F32 -> BF16 bits, round to nearest even (the conversion of ggml_mul_mat's src1 for BF16 weights)."""
+    L = lib()
+    return np.array([L.oracle_fp32_to_bf16(float(v)) for v in np.asarray(x, np.float32).ravel()],
+                    np.uint16).reshape(np.shape(x))
+
+
 def kv_produce(cur: np.ndarray, wk_bits: np.ndarray, wv_bits: np.ndarray, k_norm_w: np.ndarray, pos: np.ndarray,
                variant: int = Q8_X86, n_dims: int = ROPE_DIM, sections=IMROPE_SECTIONS, freq_base: float = ROPE_FREQ_BASE,
-               eps: float = RMS_EPS):
+               eps: float = RMS_EPS, w_bf16: bool = False):
     """The K/V producer (qwfn_graph.cpp:441-451, then the append of :370-384 / :623-624):
-    cur f32 [T, E]; w*_bits uint16 [kv_dim, E]; pos int32 [4*T]. Returns (k_rows, v_rows, k_f32, v_f32):
-    q8_0 rows uint8 [T, kv_dim/32*34] and the float rows before quantisation [T, kv_dim]."""
+    cur f32 [T, E]; w*_bits uint16 [kv_dim, E] (F16 bits, or BF16 bits with w_bf16); pos int32 [4*T].
+    Returns (k_rows, v_rows, k_f32, v_f32): q8_0 rows uint8 [T, kv_dim/32*34] and the float rows
+    before quantisation [T, kv_dim]."""
     cur = np.ascontiguousarray(cur, np.float32)
     T, E = cur.shape
     kv_dim = wk_bits.shape[0]
@@ -359,7 +371,8 @@ def kv_produce(cur: np.ndarray, wk_bits: np.ndarray, wv_bits: np.ndarray, k_norm
     lib().oracle_kv_produce_q8_0(_p(cur), E, T, _p(np.ascontiguousarray(wk_bits, np.uint16)),
                                  _p(np.ascontiguousarray(wv_bits, np.uint16)), kv_dim,
                                  _p(np.ascontiguousarray(k_norm_w, np.float32)), _p(np.ascontiguousarray(pos, np.int32)),
-                                 _p(sec), n_dims, freq_base, eps, _p(k_rows), _p(v_rows), _p(k_f), _p(v_f), variant)
+                                 _p(sec), n_dims, freq_base, eps, _p(k_rows), _p(v_rows), _p(k_f), _p(v_f), variant,
+                                 1 if w_bf16 else 0)
     return k_rows, v_rows, k_f, v_f
 
 

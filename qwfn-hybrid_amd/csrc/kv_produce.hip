@@ -6,7 +6,9 @@
 // F32 -> q8_0) emit one by one.
 //
 // Projection: ggml_mul_mat with F16 weights converts the F32 hidden rows to
-// F16 and sums the F16 products in F32. Each wave computes one output row for
+// F16 and sums the F16 products in F32; with BF16 weights it converts them to
+// BF16 (round to nearest even) and sums the BF16 products in F32 (both kinds
+// of products are exact in F32). Each wave computes one output row for
 // all T tokens: the row's 16-byte weight loads are issued before the block
 // stages the hidden rows (F16) in LDS, then per-lane F32 partial sums and a
 // wave reduction. The rows land in a device-resident staging buffer. The
@@ -49,7 +51,7 @@ struct kvp_args {
     size_t           cur_nb1;
     int32_t          n_embd;
     int32_t          T;
-    const uint16_t * wk;          // F16 [n_embd] per output row (kv_dim rows), row stride w_nb1 bytes
+    const uint16_t * wk;          // F16 or BF16 [n_embd] per output row (kv_dim rows), row stride w_nb1 bytes
     const uint16_t * wv;
     size_t           wk_nb1, wv_nb1;
     int32_t          nh_kv;
@@ -81,8 +83,25 @@ __device__ __forceinline__ float fma_mix_hi(uint32_t a, uint32_t b, float c) {
     return r;
 }
 
+// F32 -> BF16, round to nearest even (a NaN stays a quiet NaN)
+__device__ __forceinline__ uint32_t f32_to_bf16(float x) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+// c + a * b for the low (or high) BF16 halves of a and b: a BF16 value is the
+// upper half of an F32, and the product of two is exact in F32
+__device__ __forceinline__ float fma_bf16_lo(uint32_t a, uint32_t b, float c) {
+    return __builtin_fmaf(__builtin_bit_cast(float, a << 16), __builtin_bit_cast(float, b << 16), c);
+}
+__device__ __forceinline__ float fma_bf16_hi(uint32_t a, uint32_t b, float c) {
+    return __builtin_fmaf(__builtin_bit_cast(float, a & 0xffff0000u), __builtin_bit_cast(float, b & 0xffff0000u), c);
+}
+
+template <bool BF16>
 __global__ __launch_bounds__(KVP_WAVES * 64) void k_kv_project(kvp_args a) {
-    extern __shared__ uint16_t cur16[];          // [T][n_embd] F16 hidden rows
+    extern __shared__ uint16_t cur16[];          // [T][n_embd] F16 (or BF16) hidden rows
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int T = a.T, E = a.n_embd;
     const int n_out = 2 * a.kv_dim;
@@ -120,10 +139,16 @@ __global__ __launch_bounds__(KVP_WAVES * 64) void k_kv_project(kvp_args a) {
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 if (idx[u] < 0) continue;
-                const uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16) x[u].x) |
-                                    ((uint32_t) __builtin_bit_cast(uint16_t, (_Float16) x[u].y) << 16);
-                const uint32_t hi = __builtin_bit_cast(uint16_t, (_Float16) x[u].z) |
-                                    ((uint32_t) __builtin_bit_cast(uint16_t, (_Float16) x[u].w) << 16);
+                uint32_t lo, hi;
+                if constexpr (BF16) {
+                    lo = f32_to_bf16(x[u].x) | (f32_to_bf16(x[u].y) << 16);
+                    hi = f32_to_bf16(x[u].z) | (f32_to_bf16(x[u].w) << 16);
+                } else {
+                    lo = __builtin_bit_cast(uint16_t, (_Float16) x[u].x) |
+                         ((uint32_t) __builtin_bit_cast(uint16_t, (_Float16) x[u].y) << 16);
+                    hi = __builtin_bit_cast(uint16_t, (_Float16) x[u].z) |
+                         ((uint32_t) __builtin_bit_cast(uint16_t, (_Float16) x[u].w) << 16);
+                }
                 *(uint2 *) &cur16[idx[u]] = make_uint2(lo, hi);
             }
         }
@@ -147,8 +172,13 @@ __global__ __launch_bounds__(KVP_WAVES * 64) void k_kv_project(kvp_args a) {
             float s = acc[t];
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                s = fma_mix_lo(ww[q], cw[q], s);
-                s = fma_mix_hi(ww[q], cw[q], s);
+                if constexpr (BF16) {
+                    s = fma_bf16_lo(ww[q], cw[q], s);
+                    s = fma_bf16_hi(ww[q], cw[q], s);
+                } else {
+                    s = fma_mix_lo(ww[q], cw[q], s);
+                    s = fma_mix_hi(ww[q], cw[q], s);
+                }
             }
             acc[t] = s;
         }
@@ -241,9 +271,10 @@ extern "C" int qwfn_kv_produce_q8_0(const qwfn_tensor * cur, const qwfn_tensor *
         if (!cur || !wk || !wv || !k_norm_w || !pos || !rope || !k_cache || !v_cache || !cur->data || !wk->data ||
             !wv->data || !k_cache->data || !v_cache->data)
             return set_error(QWFN_EINVAL, "kv_produce: NULL argument");
-        if (cur->type != QWFN_TYPE_F32 || wk->type != QWFN_TYPE_F16 || wv->type != QWFN_TYPE_F16 ||
-            k_cache->type != QWFN_TYPE_Q8_0 || v_cache->type != QWFN_TYPE_Q8_0)
-            return set_error(QWFN_EINVAL, "kv_produce: cur f32, weights f16, caches q8_0");
+        const bool bf16 = wk->type == QWFN_TYPE_BF16;
+        if (cur->type != QWFN_TYPE_F32 || (wk->type != QWFN_TYPE_F16 && wk->type != QWFN_TYPE_BF16) ||
+            wv->type != wk->type || k_cache->type != QWFN_TYPE_Q8_0 || v_cache->type != QWFN_TYPE_Q8_0)
+            return set_error(QWFN_EINVAL, "kv_produce: cur f32, weights both f16 or both bf16, caches q8_0");
         if (variant != QWFN_Q8_REF && variant != QWFN_Q8_X86) return set_error(QWFN_EINVAL, "kv_produce: unknown variant");
         const int64_t E = cur->ne[0], T = cur->ne[1];
         if (cur->nb[0] != 4 || wk->nb[0] != 2 || wv->nb[0] != 2) return set_error(QWFN_EINVAL, "kv_produce: rows must be contiguous");
@@ -297,17 +328,18 @@ extern "C" int qwfn_kv_produce_q8_0(const qwfn_tensor * cur, const qwfn_tensor *
             void * p = nullptr;
             if (int rc = hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(g_kvp_rows)), "hipGetSymbolAddress")) return rc;
             // the hidden rows of up to 16 tokens take more than 64 KB of LDS
-            if (int rc = hip_check(hipFuncSetAttribute((const void *) k_kv_project,
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024),
-                                   "hipFuncSetAttribute"))
-                return rc;
+            for (const void * f : {(const void *) k_kv_project<false>, (const void *) k_kv_project<true>})
+                if (int rc = hip_check(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024),
+                                       "hipFuncSetAttribute"))
+                    return rc;
             rows_ptr[dev] = (float *) p;
         }
         a.rows = rows_ptr[dev];
         const int64_t n_out = 2 * kv_dim;
         const int64_t blocks = (n_out + KVP_WAVES - 1) / KVP_WAVES;
         const size_t lds = (size_t) T * E * 2;
-        hipLaunchKernelGGL(k_kv_project, dim3((unsigned) blocks), dim3(KVP_WAVES * 64), lds, as_stream(stream), a);
+        if (bf16) hipLaunchKernelGGL(k_kv_project<true>, dim3((unsigned) blocks), dim3(KVP_WAVES * 64), lds, as_stream(stream), a);
+        else      hipLaunchKernelGGL(k_kv_project<false>, dim3((unsigned) blocks), dim3(KVP_WAVES * 64), lds, as_stream(stream), a);
         if (int rc = hip_check(hipGetLastError(), "kv_produce launch")) return rc;
         const int64_t tasks = T * 2 * (kv_dim / KVP_HD);
         hipLaunchKernelGGL(k_kv_epilogue, dim3((unsigned) ((tasks + KVP_WAVES - 1) / KVP_WAVES)), dim3(KVP_WAVES * 64), 0,

@@ -71,26 +71,32 @@ bool extends(const std::vector<int32_t> & t, const int32_t * tok, int32_t n) {
 
 // Copies the live entries contiguously into the other half and swaps halves.
 // Allocates nothing (at most MAX_ENTRIES entries).
+// The bookkeeping moves to the other half only once the copy is launched: a
+// launch that fails leaves the pool as it was.
 int compact(qwfn_snap_pool & P, hipStream_t stream) {
     const int to = 1 - P.half;
     const char * src[MAX_ENTRIES];
     char * dst[MAX_ENTRIES];
     size_t bytes[MAX_ENTRIES];
+    size_t off[MAX_ENTRIES];
     int n = 0;
     size_t cur = 0;
-    for (auto & e : P.saved) {
+    for (size_t k = 0; k < P.saved.size(); k++) {
+        const auto & e = P.saved[k];
         if (P.arena) {
             src[n] = P.base(P.half) + e.off;
             dst[n] = P.base(to) + cur;
             bytes[n] = e.span;
             n++;
         }
-        e.off = cur;
+        off[k] = cur;
         cur += e.span;
     }
+    if (n > 0)
+        if (int rc = restore_device(src, bytes, dst, n, 1, 0, stream)) return rc;
+    for (size_t k = 0; k < P.saved.size(); k++) P.saved[k].off = off[k];
     P.half = to;
-    if (n == 0) return QWFN_OK;
-    return restore_device(src, bytes, dst, n, 1, 0, stream);
+    return QWFN_OK;
 }
 
 // First fit of `span` bytes in the current half; compacts when fragmented.
@@ -205,7 +211,12 @@ int qwfn_snap_pool_save(qwfn_snap_pool * P, const qwfn_state * const * sts, int3
         if (e.bytes > P->cap) return 0;                  // larger than the cap: not kept
         // Which entries stay: an equal token sequence is replaced, then the
         // oldest go until within the limits. Nothing changes until the
-        // snapshot is known to fit the arena and every host allocation is done.
+        // snapshot is known to fit the arena and every host allocation is
+        // done, so a host allocation failure leaves the pool as it was. A
+        // device error after that point (the launch of the compaction copy or
+        // of the snapshot's copy) returns with the evicted entries dropped and
+        // the new snapshot not added; the entries kept stay valid (a
+        // compaction whose launch fails moves nothing).
         const size_t n_old = P->saved.size();
         bool drop[MAX_ENTRIES] = {};
         for (size_t k = 0; k < n_old; k++)

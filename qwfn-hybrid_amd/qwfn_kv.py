@@ -17,7 +17,7 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libqwfn_kv.so")
 
-TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_I32 = 0, 1, 8, 26
+TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_I32, TYPE_BF16 = 0, 1, 8, 26, 30
 Q8_REF, Q8_X86 = 0, 1
 SRC_DEVICE, SRC_HOST = 0, 1
 
@@ -562,11 +562,33 @@ def set_rows_f16(dst, src, idx, stream=None):
     return check(load().qwfn_set_rows_f16(ctypes.byref(d), ctypes.byref(sv), ctypes.byref(iv), _stream(stream)))
 
 
+def _check_pool_args(name, cfg, ic, pool, k_norm_w, k_raw=None, **i32):
+    """What the C ABI cannot see: the caches are 2-byte rows packed at idx_dim (the kernels
+    index row * idx_dim), everything lives on one device, the vectors are contiguous."""
+    import torch
+    two = (torch.float16, torch.int16) + ((torch.uint16,) if hasattr(torch, "uint16") else ())
+    dev_ = ic.device
+    for nm, t in (("ic", ic), ("pool", pool)):
+        if t.dim() != 2 or t.dtype not in two or t.shape[1] != cfg.idx_dim or t.stride(1) != 1 \
+                or t.stride(0) != cfg.idx_dim:
+            raise ValueError(f"{name}: {nm} must be a 2-byte [rows, {cfg.idx_dim}] tensor with rows packed at idx_dim")
+    vecs = [("k_norm_w", k_norm_w, torch.float32), ("k_raw", k_raw, torch.float32)]
+    vecs += [(k, v, torch.int32) for k, v in i32.items()]
+    for nm, t, dt in vecs:
+        if t is not None and (t.dtype != dt or not t.is_contiguous()):
+            raise ValueError(f"{name}: {nm} must be contiguous {dt}")
+    for nm, t in [("ic", ic), ("pool", pool)] + [(n, t) for n, t, _ in vecs]:
+        if t is not None and (not t.is_cuda or t.device != dev_):
+            raise ValueError(f"{name}: {nm} must be on {dev_}")
+
+
 def qsa_pool_decode(ic, k_raw, write_idx, member_idx, ratio: int, blk_pos, blk_idx, k_norm_w, pool, cfg=None,
                     stream=None):
     """qsa_dec_index: ic / pool torch f16 or uint16 [rows, idx_dim] (device), k_raw f32 [idx_dim] or None,
     the i32 decode inputs on the device."""
     cfg = cfg or qsa_pool_cfg()
+    _check_pool_args("qsa_pool_decode", cfg, ic, pool, k_norm_w, k_raw=k_raw, write_idx=write_idx,
+                     member_idx=member_idx, blk_pos=blk_pos, blk_idx=blk_idx)
     return check(load().qwfn_qsa_pool_decode(ic.data_ptr(), ic.shape[0], k_raw.data_ptr() if k_raw is not None else None,
                                              write_idx.data_ptr(), member_idx.data_ptr(), ratio, blk_pos.data_ptr(),
                                              blk_idx.data_ptr(), k_norm_w.data_ptr(), pool.data_ptr(), pool.shape[0],
@@ -576,19 +598,24 @@ def qsa_pool_decode(ic, k_raw, write_idx, member_idx, ratio: int, blk_pos, blk_i
 def qsa_pool_rebuild(ic, n_past: int, ratio: int, k_norm_w, pool, cfg=None, stream=None):
     """Every whole block's pooled key: ic / pool torch f16 or uint16 [rows, idx_dim] (device)."""
     cfg = cfg or qsa_pool_cfg()
+    _check_pool_args("qsa_pool_rebuild", cfg, ic, pool, k_norm_w)
     return check(load().qwfn_qsa_pool_rebuild(ic.data_ptr(), ic.shape[0], n_past, ratio, k_norm_w.data_ptr(),
                                               pool.data_ptr(), pool.shape[0], ctypes.byref(cfg), _stream(stream)))
 
 
 def kv_produce(cur, wk, wv, k_norm_w, pos, kcache, vcache, first_row: int, variant: int = Q8_X86, rope=None,
                stream=None):
-    """K/V producer: cur torch f32 [T, n_embd]; wk, wv torch f16 [kv_dim, n_embd]; k_norm_w f32 [256];
+    """K/V producer: cur torch f32 [T, n_embd]; wk, wv torch f16 or bf16 [kv_dim, n_embd]; k_norm_w f32 [256];
     pos i32 [4 * T]; caches uint8 [n_rows, kv_dim/32*34] (all on the device)."""
     T, E = cur.shape
     kv_dim = wk.shape[0]
     cv = tensor(cur.data_ptr(), TYPE_F32, (E, T), (4, cur.stride(0) * 4))
-    wkv = tensor(wk.data_ptr(), TYPE_F16, (E, kv_dim), (2, wk.stride(0) * 2))
-    wvv = tensor(wv.data_ptr(), TYPE_F16, (E, kv_dim), (2, wv.stride(0) * 2))
+    import torch
+    wt = TYPE_BF16 if wk.dtype == torch.bfloat16 else TYPE_F16
+    if wv.dtype != wk.dtype or wk.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("kv_produce: wk and wv must both be float16 or both bfloat16")
+    wkv = tensor(wk.data_ptr(), wt, (E, kv_dim), (2, wk.stride(0) * 2))
+    wvv = tensor(wv.data_ptr(), wt, (E, kv_dim), (2, wv.stride(0) * 2))
     kcv = tensor(kcache.data_ptr(), TYPE_Q8_0, (kv_dim, kcache.shape[0]), (34, kcache.stride(0)))
     vcv = tensor(vcache.data_ptr(), TYPE_Q8_0, (kv_dim, vcache.shape[0]), (34, vcache.stride(0)))
     rope = rope or rope_cfg()

@@ -10,7 +10,8 @@
 // turns a host allocation failure into QWFN_ENOMEM instead of letting the
 // exception cross the C boundary (the reference's engine::snapshot_save
 // returns false on std::bad_alloc, qwfn_engine.cpp:1022-1025), and that a
-// failed pool save leaves the pool exactly as it was.
+// pool save that fails on a host allocation leaves the pool exactly as it was
+// (device errors after the last allocation are outside what this checks).
 #include "qwfn_kv.h"
 #include "qwfn_state.h"
 

@@ -76,6 +76,30 @@ def test_kv_produce_matches_oracle(gpu, oracle, T, n_past, variant):
     _compare_rows(vg[n_past:n_past + T], v_rows, v_f)
 
 
+@pytest.mark.parametrize("T,n_past", [(1, 5000), (3, 16384), (16, 700)])
+def test_kv_produce_bf16_weights(gpu, oracle, T, n_past):
+    """BF16 attn_k / attn_v weights: the hidden rows rounded to BF16 on the device,
+    the same tolerance on the q8_0 bytes as for F16 weights."""
+    K = gpu
+    rng = np.random.default_rng(100 + T)
+    wk = torch.from_numpy((rng.standard_normal((KV_DIM, E)) * 0.02).astype(np.float32)).to(torch.bfloat16)
+    wv = torch.from_numpy((rng.standard_normal((KV_DIM, E)) * 0.02).astype(np.float32)).to(torch.bfloat16)
+    knw = rng.uniform(0.5, 1.5, 256).astype(np.float32)
+    cur = KD.normal(80 + T, 0, KD.Q_KIND, T * E).reshape(T, E)
+    pos = np.tile(np.arange(n_past, n_past + T, dtype=np.int32), 4)
+    n_rows = n_past + T + 8
+    kd = torch.zeros((n_rows, 544), dtype=torch.uint8, device="cuda")
+    vd = torch.zeros((n_rows, 544), dtype=torch.uint8, device="cuda")
+    say(f"kv_produce bf16 T={T} first_row={n_past}")
+    K.kv_produce(dev(cur), wk.cuda(), wv.cuda(), dev(knw), dev(pos), kd, vd, n_past)
+    wk_bits = wk.view(torch.int16).numpy().view(np.uint16)
+    wv_bits = wv.view(torch.int16).numpy().view(np.uint16)
+    k_rows, v_rows, k_f, v_f = O.kv_produce(cur, wk_bits, wv_bits, knw, pos, O.Q8_X86, w_bf16=True)
+    _compare_rows(host(kd)[n_past:n_past + T], k_rows, k_f)
+    _compare_rows(host(vd)[n_past:n_past + T], v_rows, v_f)
+    assert not host(kd)[:n_past].any() and not host(kd)[n_past + T:].any()
+
+
 def test_kv_produce_then_attention(gpu, oracle):
     """The produced rows feed the verify attention like appended ones: decode over
     the cache after a 3-token producer step matches the oracle on the same cache."""

@@ -163,3 +163,47 @@ def test_kv_produce_composition(T, variant):
         np.testing.assert_allclose(k_f[t], ref_k, rtol=1e-5, atol=1e-5)
         np.testing.assert_array_equal(k_rows[t], O.quantize(k_f[t], variant).reshape(-1))
         np.testing.assert_array_equal(v_rows[t], O.quantize(v_f[t], variant).reshape(-1))
+
+
+def test_fp32_to_bf16_is_rne():
+    """The oracle's F32 -> BF16 (src1 of a BF16 mul_mat) against torch's round to
+    nearest even: ties both ways, values just off a tie, overflow to inf, signed
+    zero, subnormals, inf; a NaN stays a NaN."""
+    import torch
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal(4000) * np.exp(rng.uniform(-90, 88, 4000))).astype(np.float32)
+    u = x.view(np.uint32)
+    u[:16] = (u[:16] & 0xFFFF0000) | 0x8000                       # exact ties
+    u[16:32] = (u[16:32] & 0xFFFF0000) | 0x7FFF                   # just below a tie
+    u[32:48] = (u[32:48] & 0xFFFF0000) | 0x8001                   # just above
+    x[48:53] = [3.4028235e38, -0.0, 1e-45, -1e-41, np.inf]
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(O.fp32_to_bf16_bits(x), want)
+    nan = O.fp32_to_bf16_bits(np.array([np.nan], np.float32))[0]
+    assert (nan & 0x7F80) == 0x7F80 and (nan & 0x007F) != 0
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_kv_produce_composition_bf16(T):
+    """The producer with BF16 weights: the hidden rows rounded to BF16 (pinned above),
+    the projection in fp64 of the BF16 values, then the same norm / rope / quantiser."""
+    import torch
+    rng = np.random.default_rng(60 + T)
+    E, kv_dim = 96, 512
+    cur = rng.standard_normal((T, E)).astype(np.float32)
+    wk = torch.from_numpy((rng.standard_normal((kv_dim, E)) * 0.1).astype(np.float32)).to(torch.bfloat16)
+    wv = torch.from_numpy((rng.standard_normal((kv_dim, E)) * 0.1).astype(np.float32)).to(torch.bfloat16)
+    wk_bits = wk.view(torch.int16).numpy().view(np.uint16)
+    wv_bits = wv.view(torch.int16).numpy().view(np.uint16)
+    knw = rng.uniform(0.5, 1.5, 256).astype(np.float32)
+    pos = np.tile(np.arange(900, 900 + T, dtype=np.int32), 4)
+    k_rows, v_rows, k_f, v_f = O.kv_produce(cur, wk_bits, wv_bits, knw, pos, O.Q8_X86, w_bf16=True)
+    cb = torch.from_numpy(cur).to(torch.bfloat16).to(torch.float64).numpy()
+    kp = cb @ wk.to(torch.float64).numpy().T
+    vp = cb @ wv.to(torch.float64).numpy().T
+    np.testing.assert_allclose(v_f, vp, rtol=1e-6, atol=1e-6)
+    for t in range(T):
+        kn = O.rms_norm(kp[t].astype(np.float32).reshape(2, 256)) * knw
+        np.testing.assert_allclose(k_f[t], O.rope_multi(kn, int(pos[t])).reshape(-1), rtol=1e-5, atol=1e-5)
+        np.testing.assert_array_equal(k_rows[t], O.quantize(k_f[t], O.Q8_X86).reshape(-1))
+        np.testing.assert_array_equal(v_rows[t], O.quantize(v_f[t], O.Q8_X86).reshape(-1))
