@@ -189,13 +189,15 @@ void qwfn_fattn_force_splits(int32_t n_splits);
  *   DEC:     at most 32 query rows per KV head
  *   GENERAL: any shape but gathered cells
  *   PRE:     more than 32 query rows per KV head, a mask shared by the heads
- *            (or none), n_head / n_head_kv >= 4, one batch, no cells */
+ *            (or none), n_head / n_head_kv >= 4, one batch, no cells
+ *   VS:      the shapes of VD (the value dims split across the waves) */
 enum {
     QWFN_FA_KERNEL_AUTO    = 0,
     QWFN_FA_KERNEL_VD      = 1,
     QWFN_FA_KERNEL_DEC     = 2,
     QWFN_FA_KERNEL_GENERAL = 3,
-    QWFN_FA_KERNEL_PRE     = 4
+    QWFN_FA_KERNEL_PRE     = 4,
+    QWFN_FA_KERNEL_VS      = 5
 };
 void qwfn_fattn_force_kernel(int32_t kind);
 

@@ -2931,6 +2931,669 @@ __global__ __launch_bounds__(VD_WAVES * 64, 2) void k_fa_vd(fa_args a) {
     if (a.mctr) fa_merge_tail<VD_WAVES * 64>(a, b, kvh, ob);
 }
 
+// ================================================================ decode / verify, value dims split across the waves
+//
+// k_fa_vs<NF, PK, MASKED, RG, GATHER>: the shapes of k_fa_vd (at most 24
+// query rows per KV head, one block of 8 waves per CU), with the work of a
+// block split so that no wave holds O for all 256 dims. The keys go in rounds
+// of 128: in a round, wave w computes the scores of sub-tile w (16 keys) for
+// all rows, the waves agree on each row's running max through LDS, wave w
+// publishes its P (its lanes' values are already in the layout the PV
+// operand wants, so the exchange is one float4 per lane), and then wave w
+// computes O for its own V block (32 dims) over all 128 keys of the round.
+// So O is 16 registers a lane instead of 96, no cross-wave reduction of O is
+// needed at the end, and each K/V row is still read from HBM once. K and V
+// go through two-stage rings (the next round's DMAs are issued as soon as
+// every wave has finished the previous round), and the requantised query
+// rows stay in registers. The arithmetic per score is k_fa_vd's: exact i8
+// block dots, d_q*d_k per block, online base-2 softmax with the running max
+// allowed to lag by RESCALE_SLACK (the same decision in every wave: they see
+// the same block max), P*d_v as f16 hi + lo. The packed tile (rows 16..23)
+// covers one sub-tile per wave: its columns 8..15 are empty in the scores,
+// and in PV they carry the odd sub-tiles of each 32-key pair (column c + 8
+// for rows of sub-tile 2j+1), which a lane swap adds at the end.
+
+constexpr int VS_WAVES = 8;
+constexpr int VS_ROUND = VS_WAVES * DEC_TK;               // 128 keys: one sub-tile per wave
+constexpr int VS_MG    = VD_MROWS * DEC_MGR * 16;         // a wave's mask granules of a round
+constexpr int VS_QROW  = 1024;                            // f32 query row in the prologue's staging
+constexpr int64_t VS_AUTO_MAX_KEYS = 36864;               // the planner's k_fa_vs range (8 rows, one sequence)
+static_assert(VD_ROWS * VS_QROW <= VS_WAVES * DEC_KB, "the query rows fit V stage 1");
+
+template <int NF, int PK, bool MASKED, bool RG, bool GATHER>
+__global__ __launch_bounds__(VS_WAVES * 64, 2) void k_fa_vs(fa_args a) {
+    static_assert(NF >= 0 && NF <= 1 && PK >= 0 && PK <= 1 && NF + PK >= 1, "a full tile, a packed tile or both");
+    static_assert(!(GATHER && (MASKED || RG)), "gathered keys carry their own mask, one sequence");
+    static_assert(NBLK == VS_WAVES, "one V block per wave");
+    constexpr int IR  = 16 * NF + 8 * PK;                  // query rows of the block, at most
+    constexpr int NKD = DEC_TDMA + (MASKED ? 1 : 0);       // K and mask DMAs of a wave's round
+    constexpr int NVD = DEC_TDMA;                          // V DMAs of a wave's round
+    asm volatile("" :: "s"(a.q), "s"(a.k), "s"(a.v), "s"(a.mask), "s"(a.m_ne2), "s"(a.part_o));
+
+    // kr / vr[stage][wave]: sub-tile `wave`'s K (V) rows of a round. V stage 1
+    // holds the f32 query rows in the prologue.
+    __shared__ __attribute__((aligned(16))) uint8_t kr[2][VS_WAVES][DEC_KB];
+    __shared__ __attribute__((aligned(16))) uint8_t vr[2][VS_WAVES][DEC_KB];
+    __shared__ __attribute__((aligned(16))) uint8_t mgr[MASKED ? 2 : 1][MASKED ? VS_WAVES : 1][MASKED ? VS_MG : 16];
+    // P of a round by sub-tile: the full tile's lanes, the packed tile's lanes
+    // with a row (hs = 0) at 8 lg + c
+    __shared__ __attribute__((aligned(16))) float4 pxf[NF ? VS_WAVES : 1][NF ? 64 : 1];
+    __shared__ __attribute__((aligned(16))) float4 pxp[PK ? VS_WAVES : 1][PK ? 32 : 1];
+    __shared__ __attribute__((aligned(16))) uint16_t ktab[VS_WAVES][NBLK][DEC_TK];   // a wave's d_k [block][key]
+    __shared__ __attribute__((aligned(16))) uint16_t vtab[VS_WAVES][NBLK][DEC_TK];   // a sub-tile's d_v [block][key]
+    __shared__ __attribute__((aligned(16))) float mx[IR][VS_WAVES];   // the waves' row maxima (row sums at the end)
+    __shared__ __attribute__((aligned(16))) float dqs[IR][NBLK];      // d_q * scale * log2(e) [row][block]
+    __shared__ __attribute__((aligned(16))) int32_t gcell[GATHER ? DEC_GATHER_SPLIT : 4];
+    __shared__ uint32_t g_bad;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int ln = lane & 15, lg = lane >> 4;
+    const int hs = ln >> 3;
+
+    // ---- block -> (b, kvh, split), as k_fa_vd ----
+    const int id = blockIdx.x;
+    const int hgn = a.nh_kv;
+    const int n_units = RG ? a.r_units : a.B * a.ns;
+    int kvh, unit;
+    if (n_units >= 8) {
+        const int j = id >> 3;
+        const int jq = (int) udiv((uint32_t) j, (uint32_t) hgn, a.hgn_mul);
+        kvh = j - jq * hgn;
+        unit = jq * 8 + (id & 7);
+    } else {
+        unit = (int) udiv((uint32_t) id, (uint32_t) hgn, a.hgn_mul);
+        kvh = id - unit * hgn;
+    }
+    if (unit >= n_units) return;
+    int b, split;
+    int64_t k_lo, k_hi;
+    if constexpr (RG) {
+        int32_t us = 0, nsb = 1, slb = 0;
+        int64_t nkb = 0;
+        b = 0;
+#pragma unroll
+        for (int i = 0; i < RAGGED_MAX_B; i++)
+            if (i < a.B && unit >= a.r_ustart[i]) {
+                b = i; us = a.r_ustart[i]; nsb = a.r_ns[i]; slb = a.r_split_len[i]; nkb = a.r_n_kv[i];
+            }
+        split = unit - us;
+        k_lo = (int64_t) split * slb;
+        const int64_t e = k_lo + slb;
+        k_hi = split == nsb - 1 ? nkb : (nkb < e ? nkb : e);
+    } else {
+        b = (int) udiv((uint32_t) unit, (uint32_t) a.ns, a.ns_mul);
+        split = unit - b * a.ns;
+        k_lo = (int64_t) split * a.split_len;
+        const int64_t e = k_lo + a.split_len;
+        k_hi = split == a.ns - 1 ? a.n_kv : (a.n_kv < e ? a.n_kv : e);
+    }
+    if constexpr (GATHER) {
+        const int li = b * a.nh_kv + kvh;
+        int64_t nh = 0;
+#pragma unroll
+        for (int i = 0; i < GATHER_MAX_LISTS; i++)
+            if (i == li) nh = a.g_n[i];
+        k_hi = k_hi < nh ? k_hi : nh;
+        k_lo = k_lo < k_hi ? k_lo : k_hi;
+    }
+    const int span = (int) (k_hi - k_lo);
+    const int n_sub = (span + DEC_TK - 1) / DEC_TK;          // 16-key sub-tiles of the split
+    const int n_rounds = (n_sub + VS_WAVES - 1) / VS_WAVES;  // block-uniform
+    const int RW = a.R;
+
+    const char * kbase = a.k + (size_t) bmod(b, a.kb) * a.k_nb3 + (size_t) kvh * a.k_nb2;
+    const char * vbase = a.v + (size_t) bmod(b, a.vb) * a.v_nb3 + (size_t) kvh * a.v_nb2;
+
+    // ---- mask (shared by the heads): n_mr query positions; one DMA a round
+    //      brings 3 granules of 16 bytes per position from the 16-byte aligned
+    //      address at or below the sub-tile's first key ----
+    const char * mslice = MASKED ? a.mask + (size_t) bmod(b, a.m_ne3) * a.m_nb3 : nullptr;
+    const char * mslice_al = (const char *) ((uintptr_t) mslice & ~(uintptr_t) 15);
+    const uint32_t mb_off = (uint32_t) (mslice - mslice_al);
+    int n_mr = 1;
+    uint32_t m_goff = 0, m_lf = 0, m_lp = 0;
+    if constexpr (MASKED) {
+        n_mr = (int) div_gqa(a, (uint32_t) (RW - 1)) + 1;
+        const int gmax = n_mr * DEC_MGR;
+        const int g = lane < gmax ? lane : gmax - 1;
+        const int mr = g / DEC_MGR;
+        m_goff = ((mb_off + (uint32_t) mr * (uint32_t) a.m_nb1) & ~15u) + 16u * (uint32_t) (g % DEC_MGR);
+        auto lane_at = [&](int row) -> uint32_t {
+            const int mr2 = (int) div_gqa(a, (uint32_t) (row < RW ? row : RW - 1));
+            return (uint32_t) (mr2 * DEC_MGR * 16) + ((mb_off + (uint32_t) mr2 * (uint32_t) a.m_nb1) & 15u) + 8u * (uint32_t) lg;
+        };
+        if constexpr (NF) m_lf = lane_at(ln);
+        if constexpr (PK) m_lp = lane_at(16 * NF + (ln & 7));
+    }
+
+    // ---- DMA: piece p = 64 s + lane of a sub-tile is byte 16 (p % 17) of key
+    //      p / 17 (K and V rows have the same stride) ----
+    uint32_t koff[DEC_TDMA];
+#pragma unroll
+    for (int s = 0; s < DEC_TDMA; s++) {
+        const uint32_t p = (uint32_t) (64 * s + lane), key = p / 17u, part = p - key * 17u;
+        koff[s] = key * (uint32_t) a.k_nb1 + part * 16u;
+    }
+    // the wave's sub-tiles are wave, wave + 8, ...: resources start at the
+    // sub-tile's first key and end at the split's end (keys past it arrive as
+    // zeros); a sub-tile past the split issues nothing
+    const int64_t key_first = k_lo + (int64_t) wave * DEC_TK;
+    const char * k_next = kbase + key_first * (int64_t) a.k_nb1;
+    const char * v_next = vbase + key_first * (int64_t) a.v_nb1;
+    const char * m_next = mslice_al + key_first * 2;
+    int64_t k_rem = (k_hi - key_first) * (int64_t) a.k_nb1, v_rem = (k_hi - key_first) * (int64_t) a.v_nb1;
+    int64_t m_rem = (int64_t) a.m_slice + mb_off - key_first * 2;
+    const int64_t k_step = (int64_t) VS_ROUND * a.k_nb1, v_step = (int64_t) VS_ROUND * a.v_nb1;
+    constexpr int64_t m_step = VS_ROUND * 2;
+    const uint32_t g_kbytes = GATHER ? (uint32_t) (a.g_rows * (int64_t) a.k_nb1) : 0u;
+    const uint32_t g_vbytes = GATHER ? (uint32_t) (a.g_rows * (int64_t) a.v_nb1) : 0u;
+    auto gather_off = [&](int ti, int s, uint32_t nb1) -> uint32_t {
+        const uint32_t p = (uint32_t) (64 * s + lane), key = p / 17u, part = p - key * 17u;
+        const int kk = ti * DEC_TK + (int) key;
+        const uint32_t row = kk < span ? (uint32_t) gcell[kk] : 0xffffffffu;
+        return row < (uint32_t) a.g_rows ? row * nb1 + part * 16u : 0x80000000u;
+    };
+    // sub-tile ti's K rows, mask granules and V rows into stage st (11 DMAs at most)
+    // sub-tile ti's K rows and mask granules into stage st (6 DMAs at most),
+    // then the resources of the wave's next sub-tile
+    auto issue_km = [&](int ti, int st) __attribute__((always_inline)) {
+        v4i rk;
+        if constexpr (GATHER) rk = make_rsrc(kbase, g_kbytes);
+        else                  rk = make_rsrc(k_next, rsrc_bytes(k_rem));
+        rk = uniform_rsrc(rk);
+        uint32_t ok[DEC_TDMA];
+#pragma unroll
+        for (int s = 0; s < DEC_TDMA; s++) {
+            if constexpr (GATHER) ok[s] = gather_off(ti, s, (uint32_t) a.k_nb1);
+            else                  ok[s] = koff[s];
+        }
+        const uint32_t lk = __builtin_amdgcn_readfirstlane(lds_addr(&kr[st][wave][0]));
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's reads of the stage are done
+        static_assert(DEC_TDMA == 5, "five DMAs per sub-tile and tensor");
+        dma16_buf_at<0>(rk, ok[0], lk);
+        dma16_buf_at<1024>(rk, ok[1], lk);
+        dma16_buf_at<2048>(rk, ok[2], lk);
+        dma16_buf_at<3072>(rk, ok[3], lk);
+        if (lane < 16) dma16_buf_at<4096>(rk, ok[4], lk);
+        if constexpr (MASKED) {
+            const v4i rm = uniform_rsrc(make_rsrc(m_next, (uint32_t) m_rem));
+            if (lane < n_mr * DEC_MGR) dma16_buf(rm, m_goff, __builtin_amdgcn_readfirstlane(lds_addr(&mgr[st][wave][0])));
+        }
+        k_next += k_step; k_rem -= k_step;
+        m_next += m_step; m_rem -= m_step;
+    };
+    // sub-tile ti's V rows into stage st (5 DMAs), then the next sub-tile's resource
+    auto issue_v = [&](int ti, int st) __attribute__((always_inline)) {
+        v4i rv;
+        if constexpr (GATHER) rv = make_rsrc(vbase, g_vbytes);
+        else                  rv = make_rsrc(v_next, rsrc_bytes(v_rem));
+        rv = uniform_rsrc(rv);
+        uint32_t ov[DEC_TDMA];
+#pragma unroll
+        for (int s = 0; s < DEC_TDMA; s++) {
+            if constexpr (GATHER) ov[s] = gather_off(ti, s, (uint32_t) a.v_nb1);
+            else                  ov[s] = koff[s];
+        }
+        const uint32_t lv = __builtin_amdgcn_readfirstlane(lds_addr(&vr[st][wave][0]));
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        dma16_buf_at<0>(rv, ov[0], lv);
+        dma16_buf_at<1024>(rv, ov[1], lv);
+        dma16_buf_at<2048>(rv, ov[2], lv);
+        dma16_buf_at<3072>(rv, ov[3], lv);
+        if (lane < 16) dma16_buf_at<4096>(rv, ov[4], lv);
+        v_next += v_step; v_rem -= v_step;
+    };
+
+    // ---- prologue: the cell list (GATHER) and the query rows (V stage 1),
+    //      the fused append; then round 0's K, mask and V rows and round 1's K
+    //      and mask, which load while the rows are requantised into images
+    //      (in the P exchange buffers) and from there into registers ----
+    uint8_t * qst = &vr[1][0][0];
+    if constexpr (GATHER) {
+        const int32_t * cl = a.g_cells + (size_t) b * a.g_bstride + (size_t) kvh * a.g_hstride + k_lo;
+        const v4i rc = make_rsrc(cl, (uint32_t) span * 4u);
+        for (int m = wave; m * 256 < span; m += VS_WAVES)
+            dma16_buf(rc, (uint32_t) (m * 1024 + 16 * lane), __builtin_amdgcn_readfirstlane(lds_addr(&gcell[m * 256])));
+        if (threadIdx.x == 0) g_bad = 0;
+    }
+    {
+        const v4i rq = make_rsrc(a.q + (size_t) b * a.q_nb3, a.q_slice);
+#pragma unroll
+        for (int j = 0; j < (IR + VS_WAVES - 1) / VS_WAVES; j++) {
+            const int rl = wave + VS_WAVES * j;
+            if (rl >= RW) break;
+            const uint32_t r = (uint32_t) rl;
+            const uint32_t t = div_gqa(a, r), h = (uint32_t) (kvh * a.gqa) + (r - t * (uint32_t) a.gqa);
+            dma16_buf(rq, t * (uint32_t) a.q_nb1 + h * (uint32_t) a.q_nb2 + 16u * (uint32_t) lane,
+                      __builtin_amdgcn_readfirstlane(lds_addr(qst + rl * VS_QROW)));
+        }
+    }
+    if (a.app_n > 0) {
+        // as in k_fa_vd: the blocks whose keys hold appended rows quantise
+        // their KV head's part of them first, and read them back only after
+        // their own stores are done
+        const int64_t alo = std::max<int64_t>(a.app_row0, k_lo), ahi = std::min<int64_t>(a.app_row0 + a.app_n, k_hi);
+        if (alo < ahi) {
+            const int units = (int) (ahi - alo) * NBLK * 2;
+            const int sub = threadIdx.x & 7;
+            for (int u0 = 0; u0 < units; u0 += VS_WAVES * 8) {
+                const int uu0 = u0 + (int) (threadIdx.x >> 3);
+                const bool live = uu0 < units;
+                const int uu = live ? uu0 : 0;
+                const int tensor = uu & 1, jb = (uu >> 1) % NBLK;
+                const int64_t row = alo + (uu >> 1) / NBLK;
+                const float4 xv = *(const float4 *) ((tensor ? a.app_v : a.app_k) + (size_t) (row - a.app_row0) * a.app_nb1 +
+                                                     (size_t) (kvh * D + QK * jb + 4 * sub) * 4);
+                float x[4] = {xv.x, xv.y, xv.z, xv.w};
+                uint16_t d16;
+                float dqa;
+                const uint32_t q4 = dev::q8_quantize_lane4(x, a.x86 != 0, &d16, &dqa);
+                if (live) {
+                    char * bp = (char *) (tensor ? vbase + (size_t) row * a.v_nb1 : kbase + (size_t) row * a.k_nb1) + jb * QBLOCK;
+                    uint16_t * qp = (uint16_t *) (bp + 2 + sub * 4);
+                    qp[0] = (uint16_t) (q4 & 0xffffu);
+                    qp[1] = (uint16_t) (q4 >> 16);
+                    if (sub == 0) *(uint16_t *) bp = d16;
+                }
+            }
+        }
+    }
+    wait_vmcnt<0>();   // this wave's query rows (cells, appended rows) have landed
+    __syncthreads();   // ... and every wave's
+    if constexpr (GATHER) {
+        if ((int) threadIdx.x < span && (uint32_t) gcell[threadIdx.x] >= (uint32_t) a.g_rows) g_bad = 1;
+    }
+    if (wave < n_sub) {
+        issue_km(wave, 0);
+        issue_v(wave, 0);
+    }
+    if (wave + VS_WAVES < n_sub) issue_km(wave + VS_WAVES, 1);
+
+    // requantisation (ggml's quantiser): wave w takes q8_0 block w of every
+    // row, two lanes per row; the images [block][16-byte slice][row] of the
+    // full tile go to pxf, the packed tile's to pxp
+    uint8_t * qimf = (uint8_t *) &pxf[0][0];
+    uint8_t * qimp = (uint8_t *) &pxp[0][0];
+    static_assert(!NF || NBLK * 4 * 16 * 16 <= (int) sizeof(pxf), "the full tile's image fits pxf");
+    static_assert(!PK || NBLK * 4 * 8 * 16 <= (int) sizeof(pxp), "the packed tile's image fits pxp");
+    const int qrow = lane >> 1, qh = lane & 1;
+    {
+        float qx[16];
+        const float4 * src = (const float4 *) (qst + qrow * VS_QROW + (QK * wave + 16 * qh) * 4);
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const float4 v = qrow < RW ? src[m] : make_float4(0.f, 0.f, 0.f, 0.f);
+            qx[4 * m] = v.x; qx[4 * m + 1] = v.y; qx[4 * m + 2] = v.z; qx[4 * m + 3] = v.w;
+        }
+        // zero this wave's block of both images
+        if constexpr (NF) *(uint4 *) (qimf + wave * 1024 + lane * 16) = make_uint4(0, 0, 0, 0);
+        if constexpr (PK) if (lane < 32) *(uint4 *) (qimp + wave * 512 + lane * 16) = make_uint4(0, 0, 0, 0);
+        wave_lds_sync();
+        uint32_t w[4];
+        uint16_t d16;
+        float dqv = 0.f;
+        if (a.x86) dev::q8_quantize_lanes<16>(qx, true, w, &d16, &dqv);
+        else       dev::q8_quantize_lanes<16>(qx, false, w, &d16, &dqv);
+        if (qrow < RW) {
+            const int woff = (int) ((0x200E0C0A08061402ull >> (8 * wave)) & 0xff);   // win_off(wave)
+            const bool full = qrow < 16 * NF;
+            uint8_t * s0 = full ? qimf + wave * 1024 + (NF ? qrow : 0) * 16 : qimp + wave * 512 + (PK ? qrow - 16 * NF : 0) * 16;
+            const int sstride = full ? 16 * 16 : 8 * 16;    // bytes between the slices of a row
+#pragma unroll
+            for (int m = 0; m < 8; m++) {   // 2-byte pieces never straddle a slice
+                const int o = woff + 16 * qh + 2 * m;
+                *(uint16_t *) (s0 + (o >> 4) * sstride + (o & 15)) = (uint16_t) (w[m >> 1] >> (16 * (m & 1)));
+            }
+        }
+        if (qh == 0 && qrow < IR) dqs[qrow][wave] = qrow < RW ? dqv * (a.scale * LOG2E) : 0.f;
+    }
+    __syncthreads();   // the images and the d_q table are complete
+    // the query operands in registers (read before the first round's barrier,
+    // after which pxf and pxp carry P): the full tile's row ln, the packed
+    // tile's row 16 + (ln & 7) in columns 0..7 (zeros in 8..15)
+    v4i qf[NF ? NBLK : 1], qp[PK ? NBLK : 1];
+    float dqf[NF ? NBLK : 1], dqp[PK ? NBLK : 1];
+#pragma unroll
+    for (int bb = 0; bb < NBLK; bb++) {
+        if constexpr (NF) {
+            qf[bb] = *(const v4i *) (qimf + bb * 1024 + lg * 256 + ln * 16);
+            dqf[bb] = dqs[ln][bb];
+        }
+        if constexpr (PK) {
+            const v4i v = *(const v4i *) (qimp + bb * 512 + lg * 128 + (ln & 7) * 16);
+            qp[bb] = hs == 0 ? v : v4i{0, 0, 0, 0};
+            dqp[bb] = dqs[16 * NF + (ln & 7)][bb];
+        }
+    }
+
+    // ---- the rounds ----
+    v4f Of[2] = {v4f{0, 0, 0, 0}, v4f{0, 0, 0, 0}}, Op[2] = {v4f{0, 0, 0, 0}, v4f{0, 0, 0, 0}};
+    float mfr = -INFINITY, lfr = 0.f, mpr = -INFINITY, lpr = 0.f;
+    const int64_t qpos_f = GATHER ? a.g_pos0 + b + (int64_t) div_gqa(a, (uint32_t) (NF ? ln : 0)) : 0;
+    const int64_t qpos_p = GATHER ? a.g_pos0 + b + (int64_t) div_gqa(a, (uint32_t) (16 * NF + (ln & 7))) : 0;
+    const int prow = 16 * NF + (ln & 7);                 // the packed tile's row of the lane
+#pragma unroll 1
+    for (int r = 0; r < n_rounds; r++) {
+        const int st = r & 1;
+        const int sub = VS_WAVES * r + wave;             // this wave's sub-tile
+        const int kb0 = DEC_TK * sub;                    // its first key in the split
+        const bool mine = sub < n_sub;
+        const bool mine_nx = sub + VS_WAVES < n_sub;        // the wave's sub-tile of the next round
+        const bool mine_nx2 = sub + 2 * VS_WAVES < n_sub;   // ... and of the one after
+        // The wave issues K and mask rows two rounds ahead (after its scores
+        // of a round, into the stage they leave) and V rows one round ahead
+        // (after the round's first barrier, when every wave is done with the
+        // stage): K0 M0 V0 K1 M1 | K2 M2 V1 | K3 M3 V2 | ... The sub-tile's K
+        // rows and mask have landed once at most the next round's K, mask and
+        // this round's V rows are in flight.
+        if (mine_nx) wait_vmcnt<NKD + NVD>();
+        else         wait_vmcnt<NVD>();
+
+        // the sub-tile's K block scales, [block][key]
+        {
+            const int bq = lane & 7, kq = lane >> 3;
+            const uint16_t s0 = *(const uint16_t *) (&kr[st][wave][0] + kq * SEG + bq * QBLOCK);
+            const uint16_t s1 = *(const uint16_t *) (&kr[st][wave][0] + (kq + 8) * SEG + bq * QBLOCK);
+            ktab[wave][bq][kq] = s0;
+            ktab[wave][bq][kq + 8] = s1;
+        }
+        wave_lds_sync();
+
+        // ---- S = K Q^T for the sub-tile: MFMA rows are keys, columns rows;
+        //      block bb + 1's MFMAs are issued while bb is scaled ----
+        float sf[4] = {0.f, 0.f, 0.f, 0.f}, sp[4] = {0.f, 0.f, 0.f, 0.f};
+        {
+            // every block's K window and scales first: one LDS latency a round
+            const uint8_t * kr0 = &kr[st][wave][0] + ln * SEG + 16 * lg;
+            const uint8_t * tk = (const uint8_t *) &ktab[wave][0][0] + 8 * lg;   // + 32 bb
+            v4i kw[NBLK];
+            uint2 dkw[NBLK];
+#pragma unroll
+            for (int bb = 0; bb < NBLK; bb++) kw[bb] = *(const v4i *) (kr0 + 16 * win_piece(bb));
+#pragma unroll
+            for (int bb = 0; bb < NBLK; bb++) dkw[bb] = *(const uint2 *) (tk + 32 * bb);
+            v4i cf[2], cp[2];
+            auto qk_mfma = [&](int bb) __attribute__((always_inline)) {
+                if constexpr (NF) cf[bb & 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kw[bb], qf[bb], v4i{0, 0, 0, 0}, 0, 0, 0);
+                if constexpr (PK) cp[bb & 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kw[bb], qp[bb], v4i{0, 0, 0, 0}, 0, 0, 0);
+            };
+            qk_mfma(0);
+#pragma unroll
+            for (int bb = 0; bb < NBLK; bb++) {
+                if (bb + 1 < NBLK) qk_mfma(bb + 1);
+                const uint2 dk = dkw[bb];
+                if constexpr (NF) {
+                    const float d = dqf[bb];
+                    const v4i c = cf[bb & 1];
+                    sf[0] = __builtin_fmaf((float) c[0], mul_f16lo(d, dk.x), sf[0]);
+                    sf[1] = __builtin_fmaf((float) c[1], mul_f16hi(d, dk.x), sf[1]);
+                    sf[2] = __builtin_fmaf((float) c[2], mul_f16lo(d, dk.y), sf[2]);
+                    sf[3] = __builtin_fmaf((float) c[3], mul_f16hi(d, dk.y), sf[3]);
+                }
+                if constexpr (PK) {
+                    const float d = dqp[bb];
+                    const v4i c = cp[bb & 1];
+                    sp[0] = __builtin_fmaf((float) c[0], mul_f16lo(d, dk.x), sp[0]);
+                    sp[1] = __builtin_fmaf((float) c[1], mul_f16hi(d, dk.x), sp[1]);
+                    sp[2] = __builtin_fmaf((float) c[2], mul_f16lo(d, dk.y), sp[2]);
+                    sp[3] = __builtin_fmaf((float) c[3], mul_f16hi(d, dk.y), sp[3]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) asm volatile("" : "+v"(sf[i]), "+v"(sp[i]));
+
+        // ---- mask; the sub-tile's maxima per row out to LDS ----
+        float xf[4], xp[4];
+        const uint8_t * mg = &mgr[MASKED ? st : 0][MASKED ? wave : 0][0];
+        if constexpr (NF) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) xf[i] = sf[i];
+            if constexpr (MASKED) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) xf[i] = fma_f16lo((uint32_t) *(const uint16_t *) (mg + m_lf + 2 * i), LOG2E, xf[i]);
+            } else if constexpr (GATHER) {
+                const int kin = kb0 + 4 * lg;
+                const int4 c = *(const int4 *) &gcell[kin < DEC_GATHER_SPLIT - 3 ? kin : 0];
+                const int cv[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    xf[i] = (uint32_t) cv[i] < (uint32_t) a.g_rows && (int64_t) cv[i] <= qpos_f ? xf[i] : -INFINITY;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (!mine || kb0 + 4 * lg + i >= span) xf[i] = -INFINITY;
+            float m = vmax(vmax(xf[0], xf[1]), vmax(xf[2], xf[3]));
+            m = xmax_lanes16_32(m);
+            if (lg == 0) mx[ln][wave] = m;
+        }
+        if constexpr (PK) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) xp[i] = sp[i];
+            if constexpr (MASKED) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) xp[i] = fma_f16lo((uint32_t) *(const uint16_t *) (mg + m_lp + 2 * i), LOG2E, xp[i]);
+            } else if constexpr (GATHER) {
+                const int kin = kb0 + 4 * lg;
+                const int4 c = *(const int4 *) &gcell[kin < DEC_GATHER_SPLIT - 3 ? kin : 0];
+                const int cv[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    xp[i] = (uint32_t) cv[i] < (uint32_t) a.g_rows && (int64_t) cv[i] <= qpos_p ? xp[i] : -INFINITY;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (hs || !mine || kb0 + 4 * lg + i >= span) xp[i] = -INFINITY;   // columns 8..15 hold no row
+            float m = vmax(vmax(xp[0], xp[1]), vmax(xp[2], xp[3]));
+            m = xmax_lanes16_32(m);
+            if (lg == 0 && hs == 0) mx[prow][wave] = m;
+        }
+        if (mine_nx2) issue_km(sub + 2 * VS_WAVES, st);   // the stage's K rows and mask are used
+        __syncthreads();   // B1: the maxima are out; every wave is done with the previous round
+        if (mine_nx) issue_v(sub + VS_WAVES, st ^ 1);
+
+        // ---- the block's max per row (the same in every wave), P, the
+        //      running sums; P out to LDS ----
+        if constexpr (NF) {
+            const float4 m0 = *(const float4 *) &mx[ln][0], m1 = *(const float4 *) &mx[ln][4];
+            const float mloc = vmax(vmax(vmax(m0.x, m0.y), vmax(m0.z, m0.w)), vmax(vmax(m1.x, m1.y), vmax(m1.z, m1.w)));
+            const bool grow = mloc > mfr + RESCALE_SLACK;
+            const bool rescale = grow && mfr != -INFINITY;
+            float alpha = 1.f;
+            if (grow) {
+                alpha = __builtin_amdgcn_exp2f(mfr - mloc);
+                mfr = mloc;
+            }
+            const float m_use = mfr == -INFINITY ? 0.f : mfr;
+            float p[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) p[i] = __builtin_amdgcn_exp2f(xf[i] - m_use);
+            lfr = lfr * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+            if (__any(rescale)) { Of[0] *= alpha; Of[1] *= alpha; }
+            pxf[wave][lane] = make_float4(p[0], p[1], p[2], p[3]);
+        }
+        if constexpr (PK) {
+            const float4 m0 = *(const float4 *) &mx[prow][0], m1 = *(const float4 *) &mx[prow][4];
+            const float mloc = vmax(vmax(vmax(m0.x, m0.y), vmax(m0.z, m0.w)), vmax(vmax(m1.x, m1.y), vmax(m1.z, m1.w)));
+            const bool grow = mloc > mpr + RESCALE_SLACK;
+            const bool rescale = grow && mpr != -INFINITY;
+            float alpha = 1.f;
+            if (grow) {
+                alpha = __builtin_amdgcn_exp2f(mpr - mloc);
+                mpr = mloc;
+            }
+            const float m_use = mpr == -INFINITY ? 0.f : mpr;
+            float p[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) p[i] = __builtin_amdgcn_exp2f(xp[i] - m_use);
+            lpr = lpr * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+            if (__any(rescale)) { Op[0] *= alpha; Op[1] *= alpha; }
+            if (hs == 0) pxp[wave][8 * lg + ln] = make_float4(p[0], p[1], p[2], p[3]);
+        }
+        // this round's V rows have landed: after them come K and mask two
+        // rounds ahead and V one round ahead
+        if (mine_nx2)     wait_vmcnt<NKD + NVD>();
+        else if (mine_nx) wait_vmcnt<NVD>();
+        else              wait_vmcnt<0>();
+        // the sub-tile's V block scales, [block][key]: zeros for a sub-tile
+        // past the split (its ring stage holds an older round's rows); keys
+        // past the split's end arrived as zero rows
+        {
+            const int bq = lane & 7, kq = lane >> 3;
+            const uint16_t s0 = *(const uint16_t *) (&vr[st][wave][0] + kq * SEG + bq * QBLOCK);
+            const uint16_t s1 = *(const uint16_t *) (&vr[st][wave][0] + (kq + 8) * SEG + bq * QBLOCK);
+            vtab[wave][bq][kq] = mine ? s0 : (uint16_t) 0;
+            vtab[wave][bq][kq + 8] = mine ? s1 : (uint16_t) 0;
+        }
+        __syncthreads();   // B2: every wave's P, V rows and V scales of the round
+
+        // ---- O += V^T (P d_v) over the round's keys, two sub-tiles a step;
+        //      a step's LDS operands are read one step ahead ----
+        {
+            const uint8_t * tv = (const uint8_t *) &vtab[0][wave][0] + 8 * lg;   // keys 4lg.. of sub-tile u: + 256 u
+            const uint8_t * vb = &vr[st][0][0] + (4 * lg) * SEG + 2 + 2 * ln + wave * QBLOCK;   // + DEC_KB u
+            struct pv_ops {
+                uint32_t w0[4], w1[4];   // V dims 2ln, 2ln+1 of keys 4lg.. of the two sub-tiles
+                uint2 d0, d1;            // their d_v
+                float4 f0, f1;           // the full tile's P
+                float4 pq;               // the packed tile's P (the column's sub-tile)
+            };
+            auto pv_load = [&](int j, pv_ops & x) __attribute__((always_inline)) {
+                const int u0 = 2 * j, u1 = 2 * j + 1;
+#pragma unroll
+                for (int jv = 0; jv < 4; jv++) {
+                    x.w0[jv] = *(const uint16_t *) (vb + u0 * DEC_KB + jv * SEG);
+                    x.w1[jv] = *(const uint16_t *) (vb + u1 * DEC_KB + jv * SEG);
+                }
+                x.d0 = *(const uint2 *) (tv + 256 * u0);
+                x.d1 = *(const uint2 *) (tv + 256 * u1);
+                if constexpr (NF) {
+                    x.f0 = pxf[u0][lane];
+                    x.f1 = pxf[u1][lane];
+                }
+                if constexpr (PK) x.pq = pxp[hs ? u1 : u0][8 * lg + (ln & 7)];
+            };
+            pv_ops cur, nxt;
+            pv_load(0, cur);
+#pragma unroll
+            for (int j = 0; j < VS_WAVES / 2; j++) {
+                if (j + 1 < VS_WAVES / 2) pv_load(j + 1, nxt);
+                uint32_t a00[2], a10[2], a01[2], a11[2];
+                cvt_v_block(cur.w0, a00, a10);
+                cvt_v_block(cur.w1, a01, a11);
+                const v8h A0 = __builtin_bit_cast(v8h, make_uint4(a00[0], a00[1], a01[0], a01[1]));
+                const v8h A1 = __builtin_bit_cast(v8h, make_uint4(a10[0], a10[1], a11[0], a11[1]));
+                const uint32_t dv0[2] = {cur.d0.x, cur.d0.y}, dv1[2] = {cur.d1.x, cur.d1.y};
+                if constexpr (NF) {
+                    const float p0[4] = {cur.f0.x, cur.f0.y, cur.f0.z, cur.f0.w}, p1[4] = {cur.f1.x, cur.f1.y, cur.f1.z, cur.f1.w};
+                    const uint32_t p016[2] = {__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p0[0], p0[1])),
+                                              __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p0[2], p0[3]))};
+                    const uint32_t p116[2] = {__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p1[0], p1[1])),
+                                              __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p1[2], p1[3]))};
+                    uint32_t bh0[2], bl0[2], bh1[2], bl1[2];
+                    pdv_hilo(p0, p016, dv0, bh0, bl0);
+                    pdv_hilo(p1, p116, dv1, bh1, bl1);
+                    const v8h Bh = __builtin_bit_cast(v8h, make_uint4(bh0[0], bh0[1], bh1[0], bh1[1]));
+                    const v8h Bl = __builtin_bit_cast(v8h, make_uint4(bl0[0], bl0[1], bl1[0], bl1[1]));
+                    Of[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, Bh, Of[0], 0, 0, 0);
+                    Of[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, Bh, Of[1], 0, 0, 0);
+                    Of[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, Bl, Of[0], 0, 0, 0);
+                    Of[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, Bl, Of[1], 0, 0, 0);
+                }
+                if constexpr (PK) {
+                    // column c < 8: row 16 + c over sub-tile u0's keys; c >= 8: over u1's
+                    const float pz[4] = {0.f, 0.f, 0.f, 0.f};
+                    const float pq[4] = {cur.pq.x, cur.pq.y, cur.pq.z, cur.pq.w};
+                    const uint32_t pq16[2] = {__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(pq[0], pq[1])),
+                                              __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(pq[2], pq[3]))};
+                    const uint32_t z16[2] = {0u, 0u};
+                    uint32_t bh0[2], bl0[2], bh1[2], bl1[2];
+                    pdv_hilo(hs ? pz : pq, hs ? z16 : pq16, dv0, bh0, bl0);
+                    pdv_hilo(hs ? pq : pz, hs ? pq16 : z16, dv1, bh1, bl1);
+                    const v8h Bh = __builtin_bit_cast(v8h, make_uint4(bh0[0], bh0[1], bh1[0], bh1[1]));
+                    const v8h Bl = __builtin_bit_cast(v8h, make_uint4(bl0[0], bl0[1], bl1[0], bl1[1]));
+                    Op[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, Bh, Op[0], 0, 0, 0);
+                    Op[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, Bh, Op[1], 0, 0, 0);
+                    Op[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, Bl, Op[0], 0, 0, 0);
+                    Op[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, Bl, Op[1], 0, 0, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                cur = nxt;
+            }
+        }
+    }
+
+    // ---- epilogue: the row sums over the waves; the packed columns c and
+    //      c + 8 of a row added; O of the wave's V block written ----
+    __syncthreads();   // every wave is done with the round maxima
+    if constexpr (NF) {
+        const float l = sum_lanes16_32(lfr);
+        if (lg == 0) mx[ln][wave] = l;
+    }
+    if constexpr (PK) {
+        float l = sum_lanes16_32(lpr);
+        if (lg == 0 && hs == 0) mx[prow][wave] = l;
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            Op[0][v] += swap_halves8(Op[0][v]);
+            Op[1][v] += swap_halves8(Op[1][v]);
+        }
+    }
+    __syncthreads();
+    if constexpr (GATHER) {
+        if (threadIdx.x == 0 && g_bad && a.status) atomicOr(a.status, DEVERR_GET_ROWS_INDEX);
+    }
+    const size_t bh = (size_t) b * a.nh_kv + kvh;
+    auto store_row = [&](int row, float M, const v4f & o0, const v4f & o1) __attribute__((always_inline)) {
+        const float4 l0 = *(const float4 *) &mx[row][0], l1 = *(const float4 *) &mx[row][4];
+        const float L = ((l0.x + l0.y) + (l0.z + l0.w)) + ((l1.x + l1.y) + (l1.z + l1.w));
+        const int dim0 = QK * wave + 8 * lg;
+        float4 w0 = make_float4(o0[0], o1[0], o0[1], o1[1]), w1 = make_float4(o0[2], o1[2], o0[3], o1[3]);
+        if (a.ns > 1) {
+            float * out = a.part_o + ((bh * a.ns + split) * a.R + row) * D + dim0;
+            if (a.mctr) {
+                const __amdgpu_buffer_rsrc_t prs = dev_rsrc(a.part_o);
+                const uint32_t poff = (uint32_t) ((const char *) out - (const char *) a.part_o);
+                store_dev4(prs, poff, w0);
+                store_dev4(prs, poff + 16, w1);
+                if (wave == 0 && lg == 0)
+                    store_dev2(dev_rsrc(a.part_ml),
+                               (uint32_t) (((bh * a.ns + split) * a.R + row) * sizeof(float2)), make_float2(M, L));
+            } else {
+                store_nt4(out, w0);
+                store_nt4(out + 4, w1);
+                if (wave == 0 && lg == 0) {
+                    float2 * mlp = &a.part_ml[(bh * a.ns + split) * a.R + row];
+                    __builtin_nontemporal_store(M, &mlp->x);
+                    __builtin_nontemporal_store(L, &mlp->y);
+                }
+            }
+        } else {
+            const float inv = L > 0.f ? 1.f / L : 0.f;
+            w0.x *= inv; w0.y *= inv; w0.z *= inv; w0.w *= inv;
+            w1.x *= inv; w1.y *= inv; w1.z *= inv; w1.w *= inv;
+            const int tq = (int) div_gqa(a, (uint32_t) row), h = kvh * a.gqa + (row - tq * a.gqa);
+            float * out = a.dst + (((size_t) b * a.T + tq) * a.nh + h) * D + dim0;
+            if (a.dst_vec) {
+                *(float4 *) out = apply_gate(a, out, w0);
+                *(float4 *) (out + 4) = apply_gate(a, out + 4, w1);
+            } else {
+                out[0] = w0.x; out[1] = w0.y; out[2] = w0.z; out[3] = w0.w;
+                out[4] = w1.x; out[5] = w1.y; out[6] = w1.z; out[7] = w1.w;
+            }
+        }
+    };
+    if constexpr (NF) {
+        if (ln < RW) store_row(ln, mfr, Of[0], Of[1]);
+    }
+    if constexpr (PK) {
+        if (hs == 0 && prow < RW) store_row(prow, mpr, Op[0], Op[1]);
+    }
+    if (a.mctr) fa_merge_tail<VS_WAVES * 64>(a, b, kvh, (float *) &kr[0][0][0]);
+}
+
 // ================================================================ prefill
 //
 // k_fa_pre: long query blocks (more than 32 query rows per KV head: prefill
@@ -3492,6 +4155,7 @@ __global__ __launch_bounds__(PRE_WAVES * 64, 2) void k_fa_pre(fa_args a) {
 // Attention kernel shapes: waves per block, query tiles, keys per wave.
 enum fa_kind {
     FA_VD,        // k_fa_vd: at most 24 query rows per KV head, 8 waves, one block per CU, 32-key steps
+    FA_VS,        // k_fa_vs: the shapes of k_fa_vd, 128-key rounds, each wave one V block (32 dims)
     FA_DEC,       // k_fa_dec: at most 32 query rows per KV head, 8 waves, one block per CU
     FA_PRE,       // k_fa_pre: longer query blocks, mask shared by the heads (or none), GQA >= 4
     FA_P4_T1,     // 4 waves, one tile, 64-key chunks, two blocks per CU
@@ -3593,6 +4257,15 @@ int check_no_scratch() {
                                (const void *) k_fa_vd<1, 1, false, false, false>, (const void *) k_fa_vd<1, 1, true, false, false>,
                                (const void *) k_fa_vd<1, 1, false, true, false>, (const void *) k_fa_vd<1, 1, true, true, false>,
                                (const void *) k_fa_vd<1, 1, false, false, true>,
+                               (const void *) k_fa_vs<0, 1, false, false, false>, (const void *) k_fa_vs<0, 1, true, false, false>,
+                               (const void *) k_fa_vs<0, 1, false, true, false>, (const void *) k_fa_vs<0, 1, true, true, false>,
+                               (const void *) k_fa_vs<0, 1, false, false, true>,
+                               (const void *) k_fa_vs<1, 0, false, false, false>, (const void *) k_fa_vs<1, 0, true, false, false>,
+                               (const void *) k_fa_vs<1, 0, false, true, false>, (const void *) k_fa_vs<1, 0, true, true, false>,
+                               (const void *) k_fa_vs<1, 0, false, false, true>,
+                               (const void *) k_fa_vs<1, 1, false, false, false>, (const void *) k_fa_vs<1, 1, true, false, false>,
+                               (const void *) k_fa_vs<1, 1, false, true, false>, (const void *) k_fa_vs<1, 1, true, true, false>,
+                               (const void *) k_fa_vs<1, 1, false, false, true>,
                                (const void *) k_fa_pre<false>, (const void *) k_fa_pre<true>,
                                (const void *) k_fattn_q8_0<2, true, WAVES, 16, false>,
                                (const void *) k_fattn_q8_0<1, false, WAVES_PAIR, 16, false>,
@@ -3682,6 +4355,9 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
         case QWFN_FA_KERNEL_VD:
             if (!vd_ok) return set_error(QWFN_ENOTSUP, "flash_attn_ext: the forced VD kernel cannot take this shape");
             break;
+        case QWFN_FA_KERNEL_VS:
+            if (!vd_ok) return set_error(QWFN_ENOTSUP, "flash_attn_ext: the forced VS kernel cannot take this shape");
+            break;
         case QWFN_FA_KERNEL_DEC:
             if (!dec) return set_error(QWFN_ENOTSUP, "flash_attn_ext: the forced DEC kernel takes at most 32 rows per KV head");
             break;
@@ -3697,8 +4373,16 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
     }
     // k_fa_vd measures slower than k_fa_dec at every depth so far (its
     // prologue and epilogue cost more than its steps save): callers reach it
-    // only by forcing it
+    // only by forcing it. k_fa_vs measures faster than k_fa_dec for one
+    // sequence of at most 8 rows per KV head (one position, GQA 8) up to
+    // 32K keys (kernel + merge, 2 KV heads: 1K 14.9 against 15.3 us, 16K
+    // 16.5 against 17.3, 32K 21.0 against 21.4), slower past it (64K 28.5
+    // against 27.0) and slower for 24 rows at every depth (16K 19.5
+    // against 18.9)
     if (vd_ok && fk == QWFN_FA_KERNEL_VD) pl->kind = FA_VD;
+    if (vd_ok && fk == QWFN_FA_KERNEL_VS) pl->kind = FA_VS;
+    if (vd_ok && fk == QWFN_FA_KERNEL_AUTO && R <= 8 && B == 1 && !seq_n_kv && !gather && n_kv <= VS_AUTO_MAX_KEYS)
+        pl->kind = FA_VS;
     if (pre_ok && (fk == QWFN_FA_KERNEL_AUTO || fk == QWFN_FA_KERNEL_PRE)) {
         // k_fa_pre: 128-row blocks; key splits of whole 64-key chunks (at least
         // two per split), about one block per CU; the row groups of a (batch,
@@ -3731,7 +4415,8 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
         pl->ws_bytes = std::max<size_t>(off, 256);
         return QWFN_OK;
     }
-    const bool vd = pl->kind == FA_VD, kdec = pl->kind == FA_DEC;
+    const bool vs = pl->kind == FA_VS;
+    const bool vd = pl->kind == FA_VD || vs, kdec = pl->kind == FA_DEC;
     pl->R = (int32_t) R;
     pl->rw = vd ? VD_ROWS : rw;
     pl->RT = vd ? 1 : rw / 16;
@@ -3759,17 +4444,32 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
     }
     int64_t split_len;
     if (vd && !gather) {
-        // The slowest wave of a split of s sub-tiles takes ceil(s / 8) of
-        // them: pairs as steps, an odd one as a half step. The fewest
-        // sub-tiles per split with every block on a CU of its own (the last
-        // split takes what is left, fewer keys) give the shortest slowest
-        // wave; a forced split count takes the sub-tiles that it implies.
         const int64_t per = std::max<int64_t>(1, nh_kv * B);
-        int64_t sub = std::max<int64_t>(VD_WAVES, (n_kv + ck * ns - 1) / (ck * ns));
-        if (!forced_ns)
-            while ((n_kv + ck * sub - 1) / (ck * sub) * per > target_blocks) sub++;
-        split_len = ck * sub;
-        ns = std::max<int64_t>(1, (n_kv + split_len - 1) / split_len);
+        if (vs) {
+            // Every wave of a k_fa_vs block takes ceil(s / 8) rounds for a
+            // split of s sub-tiles, so splits are whole rounds of 128 keys,
+            // as many as fill one block per CU, and the last split takes the
+            // keys past the others' (n_kv = 2^k + T: one short round more in
+            // one block, rather than a block more than the CUs)
+            const int64_t rk = DEC_TK * VS_WAVES;
+            const int64_t want = forced_ns ? (int64_t) forced_ns : std::max<int64_t>(1, target_blocks / per);
+            const int64_t rounds = std::max<int64_t>(1, n_kv / rk);
+            split_len = (rounds + want - 1) / want * rk;
+            ns = forced_ns ? (n_kv + split_len - 1) / split_len : n_kv / split_len;
+            ns = std::max<int64_t>(1, ns);
+        } else {
+            // The slowest wave of a split of s sub-tiles takes ceil(s / 8) of
+            // them: pairs as steps, an odd one as a half step. The fewest
+            // sub-tiles per split with every block on a CU of its own (the
+            // last split takes what is left, fewer keys) give the shortest
+            // slowest wave; a forced split count takes the sub-tiles that it
+            // implies.
+            int64_t sub = std::max<int64_t>(VD_WAVES, (n_kv + ck * ns - 1) / (ck * ns));
+            if (!forced_ns)
+                while ((n_kv + ck * sub - 1) / (ck * sub) * per > target_blocks) sub++;
+            split_len = ck * sub;
+            ns = std::max<int64_t>(1, (n_kv + split_len - 1) / split_len);
+        }
         if (ns > ns_cap) {
             split_len = (n_kv + ns_cap - 1) / ns_cap;
             split_len = (split_len + ck - 1) / ck * ck;
@@ -3952,6 +4652,22 @@ void launch_vd(const fa_args & a, bool msk, bool rg, bool gat, dim3 g, hipStream
     else          { if (msk) launch_vd1<NF, PK, true, false, false>(a, g, st);
                     else     launch_vd1<NF, PK, false, false, false>(a, g, st); }
 }
+// k_fa_vs, likewise
+template <int NF, int PK, bool M, bool RG, bool G>
+void launch_vs1(const fa_args & a, dim3 g, hipStream_t st) {
+    static const std::string name = "k_fa_vs<" + std::to_string(NF) + ", " + std::to_string(PK) + ", " +
+                                    (M ? "true" : "false") + ", " + (RG ? "true" : "false") + ", " + (G ? "true" : "false") + ">";
+    g_last_kernel = name.c_str();
+    hipLaunchKernelGGL((k_fa_vs<NF, PK, M, RG, G>), g, dim3(VS_WAVES * 64), 0, st, a);
+}
+template <int NF, int PK>
+void launch_vs(const fa_args & a, bool msk, bool rg, bool gat, dim3 g, hipStream_t st) {
+    if (gat)      launch_vs1<NF, PK, false, false, true>(a, g, st);
+    else if (rg)  { if (msk) launch_vs1<NF, PK, true, true, false>(a, g, st);
+                    else     launch_vs1<NF, PK, false, true, false>(a, g, st); }
+    else          { if (msk) launch_vs1<NF, PK, true, false, false>(a, g, st);
+                    else     launch_vs1<NF, PK, false, false, false>(a, g, st); }
+}
 
 int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v, const qwfn_tensor * mask, float scale,
               float max_bias, float logit_softcap, const qwfn_tensor * dst, int variant, void * ws, size_t ws_bytes,
@@ -4093,7 +4809,7 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
         }
         return QWFN_OK;
     }
-    if (pl.kind == FA_DEC || pl.kind == FA_VD) a.n_rg = 1;
+    if (pl.kind == FA_DEC || pl.kind == FA_VD || pl.kind == FA_VS) a.n_rg = 1;
     // the split merge: a k_fattn_merge launch unless the in-kernel merge is
     // forced. The launch measures faster (16384 keys, T = 3: 20.0 against
     // 27.1 us per op; 65536: 33.2 against 39.1): after the last split, the
@@ -4102,7 +4818,7 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
     // loads) that costs more than the launch boundary it replaces
     const int32_t fm = g_force_merge.load(std::memory_order_relaxed);
     const int64_t groups = (int64_t) a.B * a.nh_kv;
-    const bool fuse = (pl.kind == FA_DEC || pl.kind == FA_VD) && !a.ragged && a.ns > 1 && groups <= MERGE_SLOTS &&
+    const bool fuse = (pl.kind == FA_DEC || pl.kind == FA_VD || pl.kind == FA_VS) && !a.ragged && a.ns > 1 && groups <= MERGE_SLOTS &&
                       pl.off_ml < (size_t(1) << 32) && fm == QWFN_FA_MERGE_FUSED;
     if (fuse) {
         if (int rc = merge_slots(groups, &a.mctr, &a.m_ebase)) return rc;
@@ -4128,6 +4844,11 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
         if (a.R <= 8)       launch_vd<0, 1>(a, msk, a.ragged != 0, gat != nullptr, g, st);
         else if (a.R <= 16) launch_vd<1, 0>(a, msk, a.ragged != 0, gat != nullptr, g, st);
         else                launch_vd<1, 1>(a, msk, a.ragged != 0, gat != nullptr, g, st);
+    } else if (pl.kind == FA_VS) {
+        const bool msk = a.mask != nullptr;
+        if (a.R <= 8)       launch_vs<0, 1>(a, msk, a.ragged != 0, gat != nullptr, g, st);
+        else if (a.R <= 16) launch_vs<1, 0>(a, msk, a.ragged != 0, gat != nullptr, g, st);
+        else                launch_vs<1, 1>(a, msk, a.ragged != 0, gat != nullptr, g, st);
     } else if (pl.kind == FA_DEC) {
         const dim3 bd(DEC_WAVES * 64);
         const bool msk = a.mask != nullptr;
@@ -4394,7 +5115,7 @@ extern "C" void qwfn_fattn_force_splits(int32_t n_splits) {
 }
 
 extern "C" void qwfn_fattn_force_kernel(int32_t kind) {
-    g_force_kernel.store(kind >= QWFN_FA_KERNEL_AUTO && kind <= QWFN_FA_KERNEL_PRE ? kind : QWFN_FA_KERNEL_AUTO,
+    g_force_kernel.store(kind >= QWFN_FA_KERNEL_AUTO && kind <= QWFN_FA_KERNEL_VS ? kind : QWFN_FA_KERNEL_AUTO,
                          std::memory_order_relaxed);
 }
 

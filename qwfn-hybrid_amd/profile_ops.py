@@ -33,7 +33,7 @@ def main() -> int:
     ap.add_argument("--mb", type=int, default=1024)
     ap.add_argument("--lib", default=None, help="library path (default: the package's build)")
     ap.add_argument("--append", action="store_true", help="verify: append the T new K/V rows in the same launch")
-    ap.add_argument("--kernel", choices=["auto", "vd", "dec", "general"], default="auto",
+    ap.add_argument("--kernel", choices=["auto", "vd", "vs", "dec", "general"], default="auto",
                     help="attention ops: the kernel family to force (qwfn_fattn_force_kernel)")
     ap.add_argument("--splits", type=int, default=0, help="attention ops: a forced key-split count (0: the planner's)")
     ap.add_argument("--merge", choices=["auto", "fused", "kernel"], default="auto",
@@ -45,7 +45,7 @@ def main() -> int:
     import qwfn_kv as K
     K.check((K.load(a.lib) if a.lib else K.load()).qwfn_init(0))
     K.load().qwfn_fattn_force_kernel({"auto": K.FA_KERNEL_AUTO, "vd": K.FA_KERNEL_VD, "dec": K.FA_KERNEL_DEC,
-                                      "general": K.FA_KERNEL_GENERAL}[a.kernel])
+                                      "general": K.FA_KERNEL_GENERAL, "vs": K.FA_KERNEL_VS}[a.kernel])
     K.load().qwfn_fattn_force_splits(a.splits)
     K.load().qwfn_fattn_force_merge({"auto": K.FA_MERGE_AUTO, "fused": K.FA_MERGE_FUSED,
                                      "kernel": K.FA_MERGE_KERNEL}[a.merge])

@@ -30,7 +30,7 @@ DEVERR_SET_ROWS_INDEX = 1
 DEVERR_GET_ROWS_INDEX = 2
 
 # attention kernel families (qwfn_fattn_force_kernel)
-FA_KERNEL_AUTO, FA_KERNEL_VD, FA_KERNEL_DEC, FA_KERNEL_GENERAL, FA_KERNEL_PRE = 0, 1, 2, 3, 4
+FA_KERNEL_AUTO, FA_KERNEL_VD, FA_KERNEL_DEC, FA_KERNEL_GENERAL, FA_KERNEL_PRE, FA_KERNEL_VS = 0, 1, 2, 3, 4, 5
 
 
 def last_kernel() -> str:

@@ -1,4 +1,4 @@
-"""The key-split merge inside k_fa_dec and k_fa_vd, through the C ABI.
+"""The key-split merge inside k_fa_dec, k_fa_vd and k_fa_vs, through the C ABI.
 
 A call with several key splits either merges them in the attention kernel
 itself (the last blocks of each (batch, KV head) group to finish claim its
@@ -69,13 +69,14 @@ def run(K, q, kd, vd, n_kv, md):
     return host(out), K.last_kernel(), K.last_merge()
 
 
-FAMILIES = {"vd": KK.FA_KERNEL_VD, "dec": KK.FA_KERNEL_DEC}
+FAMILIES = {"vd": KK.FA_KERNEL_VD, "vs": KK.FA_KERNEL_VS, "dec": KK.FA_KERNEL_DEC}
 
 
 @pytest.mark.parametrize("fam,n_past,T,causal", [
     ("dec", 16384, 3, True), ("vd", 16384, 3, True),
     ("dec", 4096, 1, False), ("vd", 4096, 1, False),
     ("dec", 3000, 2, True), ("vd", 3000, 2, True),
+    ("vs", 16384, 3, True), ("vs", 4096, 1, False), ("vs", 3000, 2, True),
 ])
 def test_fused_merge_matches_kernel_merge(gpu, oracle, fam, n_past, T, causal):
     K = gpu
@@ -98,7 +99,7 @@ def test_fused_merge_matches_kernel_merge(gpu, oracle, fam, n_past, T, causal):
     np.testing.assert_allclose(outs[KK.FA_MERGE_FUSED], outs[KK.FA_MERGE_KERNEL], rtol=1e-5, atol=1e-6)
 
 
-@pytest.mark.parametrize("fam", ["dec", "vd"])
+@pytest.mark.parametrize("fam", ["dec", "vd", "vs"])
 def test_fused_merge_repeats_bit_identical(gpu, oracle, fam):
     K = gpu
     nh, T, n_past = 16, 3, 8192
@@ -141,7 +142,7 @@ def test_fused_merge_grid_beyond_the_gpu(gpu, oracle):
         check(got[0], ref)
 
 
-@pytest.mark.parametrize("fam", ["dec", "vd"])
+@pytest.mark.parametrize("fam", ["dec", "vd", "vs"])
 def test_fused_merge_batch_of_sequences(gpu, oracle, fam):
     """Four query sequences over one cache (B = 4, the cache broadcast): eight merge
     groups in one launch."""
@@ -196,7 +197,7 @@ def test_fused_merge_cells(gpu, oracle):
         np.testing.assert_allclose(outs[KK.FA_MERGE_FUSED], outs[KK.FA_MERGE_KERNEL], rtol=1e-5, atol=1e-6)
 
 
-@pytest.mark.parametrize("fam", ["dec", "vd"])
+@pytest.mark.parametrize("fam", ["dec", "vd", "vs"])
 def test_fused_merge_alternating_calls(gpu, oracle, fam):
     """Calls on the library's workspace that alternate between two layers (other
     queries, other caches): each call's mergers must read that call's partials,

@@ -2,9 +2,9 @@
 the C ABI and checked against the oracle's ggml-cpu flash_attn_ext on the same
 inputs.
 
-The planner picks one kernel family per call (k_fa_vd for up to 24 query rows
-per KV head, k_fa_dec up to 32, k_fa_pre for prefill blocks, k_fattn_q8_0 for
-the rest); qwfn_fattn_force_kernel makes a family take a call it can serve, so
+The planner picks one kernel family per call (k_fa_dec for up to 32 query
+rows per KV head, k_fa_pre for prefill blocks, k_fattn_q8_0 for the rest;
+k_fa_vd and k_fa_vs, up to 24 rows, when forced); qwfn_fattn_force_kernel makes a family take a call it can serve, so
 the same shapes run through each of them, and qwfn_fattn_last_kernel names
 the instantiation that ran. Forms: dense (qwfn_flash_attn_ext_q8_0),
 per-sequence key counts (_seq), gathered cells (_cells), the fused append and
@@ -27,7 +27,7 @@ HD = 256
 
 # every attention kernel instantiation of the library (its scratch check list)
 ALL_KERNELS = (
-    [f"k_fa_vd<{nf}, {pk}, {m}, {rg}, {g}>" for nf, pk in ((0, 1), (1, 0), (1, 1))
+    [f"k_fa_{f}<{nf}, {pk}, {m}, {rg}, {g}>" for f in ("vd", "vs") for nf, pk in ((0, 1), (1, 0), (1, 1))
      for m, rg, g in (("false", "false", "false"), ("true", "false", "false"), ("false", "true", "false"),
                       ("true", "true", "false"), ("false", "false", "true"))]
     + [f"k_fa_dec<{rt}, {m}, {rg}, false>" for rt in (1, 2) for m in ("false", "true") for rg in ("false", "true")]
@@ -144,7 +144,8 @@ def forced(kind, splits=0):
     return _F()
 
 
-FAMILY = {"vd": KK.FA_KERNEL_VD, "dec": KK.FA_KERNEL_DEC, "general": KK.FA_KERNEL_GENERAL, "auto": KK.FA_KERNEL_AUTO}
+FAMILY = {"vd": KK.FA_KERNEL_VD, "vs": KK.FA_KERNEL_VS, "dec": KK.FA_KERNEL_DEC, "general": KK.FA_KERNEL_GENERAL,
+          "auto": KK.FA_KERNEL_AUTO}
 
 # (family, T, mask, forced splits, expected instantiation) over a dense layer of 3000 keys
 DENSE = [
@@ -155,7 +156,16 @@ DENSE = [
     ("vd", 3, None, 0, "k_fa_vd<1, 1, false, false, false>"),
     ("vd", 3, "causal", 0, "k_fa_vd<1, 1, true, false, false>"),
     ("vd", 3, "finite", 3, "k_fa_vd<1, 1, true, false, false>"),
+    ("vs", 1, None, 0, "k_fa_vs<0, 1, false, false, false>"),
+    ("vs", 1, "finite", 0, "k_fa_vs<0, 1, true, false, false>"),
+    ("vs", 1, None, 1, "k_fa_vs<0, 1, false, false, false>"),
+    ("vs", 2, None, 0, "k_fa_vs<1, 0, false, false, false>"),
+    ("vs", 2, "causal", 0, "k_fa_vs<1, 0, true, false, false>"),
+    ("vs", 3, None, 0, "k_fa_vs<1, 1, false, false, false>"),
+    ("vs", 3, "causal", 0, "k_fa_vs<1, 1, true, false, false>"),
+    ("vs", 3, "finite", 3, "k_fa_vs<1, 1, true, false, false>"),
     ("auto", 3, "causal", 0, "k_fa_dec<2, true, false, false>"),
+    ("auto", 1, "finite", 0, "k_fa_vs<0, 1, true, false, false>"),
     ("dec", 2, None, 0, "k_fa_dec<1, false, false, false>"),
     ("dec", 2, "causal", 0, "k_fa_dec<1, true, false, false>"),
     ("dec", 3, None, 0, "k_fa_dec<2, false, false, false>"),
@@ -192,6 +202,12 @@ SEQ = [
     ("vd", 2, True, 0, "k_fa_vd<1, 0, true, true, false>"),
     ("vd", 3, False, 0, "k_fa_vd<1, 1, false, true, false>"),
     ("vd", 3, True, 0, "k_fa_vd<1, 1, true, true, false>"),
+    ("vs", 1, False, 0, "k_fa_vs<0, 1, false, true, false>"),
+    ("vs", 1, True, 0, "k_fa_vs<0, 1, true, true, false>"),
+    ("vs", 2, False, 0, "k_fa_vs<1, 0, false, true, false>"),
+    ("vs", 2, True, 0, "k_fa_vs<1, 0, true, true, false>"),
+    ("vs", 3, False, 0, "k_fa_vs<1, 1, false, true, false>"),
+    ("vs", 3, True, 0, "k_fa_vs<1, 1, true, true, false>"),
     ("dec", 2, False, 0, "k_fa_dec<1, false, true, false>"),
     ("dec", 2, True, 0, "k_fa_dec<1, true, true, false>"),
     ("dec", 3, False, 0, "k_fa_dec<2, false, true, false>"),
@@ -255,6 +271,9 @@ CELLS = [
     ("vd", 1, "k_fa_vd<0, 1, false, false, true>"),
     ("vd", 2, "k_fa_vd<1, 0, false, false, true>"),
     ("vd", 3, "k_fa_vd<1, 1, false, false, true>"),
+    ("vs", 1, "k_fa_vs<0, 1, false, false, true>"),
+    ("vs", 2, "k_fa_vs<1, 0, false, false, true>"),
+    ("vs", 3, "k_fa_vs<1, 1, false, false, true>"),
     ("dec", 2, "k_fa_dec<1, false, false, true>"),
     ("dec", 3, "k_fa_dec<2, false, false, true>"),
 ]
@@ -330,6 +349,28 @@ def test_gqa2_causal_block_gated(gpu, oracle):
     check(host(out)[0], ref * sig)
 
 
+@pytest.mark.parametrize("fam,splits", [("vs", 1), ("vs", 0), ("vd", 1)])
+def test_gated_verify_family(gpu, oracle, fam, splits):
+    """The output gate on the verify kernels: with one split the kernel writes the gated
+    rows itself, with several the merge launch does."""
+    K = gpu
+    T, nh, n_kv = 3, 16, 2500
+    kc, vc = layer(103, n_kv)
+    q = KD.q_rows(103, 1, T, nh)[0]
+    mask = O.causal_mask(T, n_kv - T)
+    gate = (np.random.default_rng(103).standard_normal((1, T, nh, HD)) * 2).astype(np.float32)
+    qd, kd, vd, md, gd = dev(q[None].astype(np.float32)), dev(kc), dev(vc), dev(mask.view(np.float16)), dev(gate)
+    out = torch.full((1, T, nh, HD), float("nan"), dtype=torch.float32, device="cuda")
+    say(f"gated {fam} splits={splits}")
+    with forced(FAMILY[fam], splits):
+        K.flash_attn_ext_gated(K.q_view(qd), K.cache_attn_view(kd, n_kv, 2), K.cache_attn_view(vd, n_kv, 2),
+                               K.mask_view(md), 1 / 16, K.out_view(out), gd)
+        name = K.last_kernel()
+    assert name == f"k_fa_{fam}<1, 1, true, false, false>"
+    sig = (1.0 / (1.0 + np.exp(-gate[0].astype(np.float64)))).astype(np.float32)
+    check(host(out)[0], ref_dense(q, kc, vc, n_kv, mask, nh) * sig)
+
+
 def test_seq_long_block(gpu, oracle):
     """Per-sequence counts with 8 positions per sequence (64 rows per KV head)."""
     K = gpu
@@ -345,7 +386,7 @@ def test_seq_long_block(gpu, oracle):
         check(got[s], KD.oracle_attn(q[s], kcs[s], vcs[s], dpt, 2, None, 1 / 16))
 
 
-@pytest.mark.parametrize("fam,T", [("vd", 3), ("dec", 3), ("general", 3), ("auto", 8)])
+@pytest.mark.parametrize("fam,T", [("vd", 3), ("vs", 3), ("dec", 3), ("general", 3), ("auto", 8)])
 def test_append_family(gpu, oracle, fam, T):
     """The fused K/V append on each family: cache bytes are the oracle's quantisation of
     the new rows, and the output is the oracle's attention over the appended cache."""
@@ -379,7 +420,7 @@ def test_forced_family_refuses_shapes_it_cannot_take(gpu):
     T, nh, n_kv = 8, 16, 600
     kc, vc = layer(102, n_kv)
     q = KD.q_rows(102, 1, T, nh)[0]
-    for fam in ("vd", "dec"):
+    for fam in ("vd", "vs", "dec"):
         with forced(FAMILY[fam]):
             with pytest.raises(K.QwfnError) as e:
                 run_dense(K, q, kc, vc, n_kv, None)
