@@ -429,14 +429,17 @@ def _exact_top(scores, k):
 
 
 @pytest.mark.parametrize("case", ["random", "all_equal", "few_values", "mostly_masked", "k1024", "just_above_2048",
-                                  "two_tied_bins", "ties_in_candidates", "small", "kpt12", "kpt32", "kpt40"])
+                                  "two_tied_bins", "ties_in_candidates", "small", "kpt12", "kpt32", "kpt40", "rising",
+                                  "t1", "t16", "t17"])
 def test_qsa_topk_exact_on_device_scores(gpu, case):
     """The selection alone, bit for bit: the kernel's own scores are read back
     from the workspace and the expected blocks are an exact sort of them. The
     cases reach both the fast path (a threshold from a sample of the scores,
     or none at 1024 blocks or fewer, then one sort of the keys above it) and
     the full select it falls back to: all scores tied, a few distinct values,
-    most blocks masked, k above 768, ties around the k-th place."""
+    most blocks masked, k above 768, ties around the k-th place, every kept
+    block in the last part of the pool ("rising"), and 1, 16 and 17 queries
+    in one call."""
     import torch
     rng = np.random.default_rng(sum(map(ord, case)))
     nb, k, T, ratio = 18432, 513, 3, 4
@@ -470,6 +473,15 @@ def test_qsa_topk_exact_on_device_scores(gpu, case):
         # 12 and 32 scores a thread take the sampled path, 40 the full select
         nb = {"kpt12": 10000, "kpt32": 30000, "kpt40": 36000}[case]
         pool = (rng.standard_normal((nb, 128)) * 0.5).astype(np.float16)
+        bias = np.zeros((T, nb), np.float32)
+    elif case == "rising":
+        pool[:] = 0
+        pool[:, 0] = (np.arange(nb) / nb).astype(np.float16)
+        q[:] = 0
+        q[:, 0, 0] = 1.0
+    elif case in ("t1", "t16", "t17"):
+        T = int(case[1:])
+        q = rng.standard_normal((T, 4, 128)).astype(np.float32)
         bias = np.zeros((T, nb), np.float32)
     elif case == "two_tied_bins":
         # every score one of two values, the better one held by exactly k - 1 blocks
