@@ -346,17 +346,29 @@ def measure_qsa_step_rows(K, torch, np, dev, gen, n_layers: int = 12) -> dict:
                           K.fattn_workspace_size_cells(K.q_view(q1), layers[0]["kv"], layers[0]["vv"], [nc, nc], 0)),
                       dtype=torch.uint8, device=dev)
 
-    def step(k):
+    def tail(L):
+        S.qsa_select_cells(L["pool"], q_idx, bias, kb, blk_cells, ratio, cells, ws=wsel)
+        K.kv_produce(cur, L["wk"], L["wv"], L["knw"], pos, L["kc"], L["vc"], n_past)
+        K.flash_attn_ext_query_cells(K.q_view(q), L["kv"], L["vv"], cells, [nc] * T, n_past, 1 / 16, K.out_view(out),
+                                     gate=gate, ws=aws)
+
+    def step_chained(k):
+        # the reference's order: prepare and pool decode one position a call
         L = layers[k % n_layers]
         for t in range(T):
             qds[t].prepare(n_past + t, prev=qds[t - 1] if t else None)
         for t in range(T):
             K.qsa_pool_decode(L["ic"], k_raw[t], qds[t].write_idx, qds[t].member_idx, ratio, qds[t].blk_pos,
                               qds[t].blk_idx, L["knw_idx"], L["pool"])
-        S.qsa_select_cells(L["pool"], q_idx, bias, kb, blk_cells, ratio, cells, ws=wsel)
-        K.kv_produce(cur, L["wk"], L["wv"], L["knw"], pos, L["kc"], L["vc"], n_past)
-        K.flash_attn_ext_query_cells(K.q_view(q), L["kv"], L["vv"], cells, [nc] * T, n_past, 1 / 16, K.out_view(out),
-                                     gate=gate, ws=aws)
+        tail(L)
+
+    def step(k):
+        # the step's positions batched: one prepare launch, one pool-decode launch
+        L = layers[k % n_layers]
+        S.qsa_decode_prepare_steps(qds, n_past)
+        K.qsa_pool_decode_steps(L["ic"], k_raw, qds, L["knw_idx"], L["pool"])
+        tail(L)
+    us_chained = timed_graph(torch, step_chained, n_layers, 10)
     us = timed_graph(torch, step, n_layers, 10)
     lists = cells.cpu().numpy()
     union = int(np.unique(lists).size)
@@ -366,8 +378,11 @@ def measure_qsa_step_rows(K, torch, np, dev, gen, n_layers: int = 12) -> dict:
     rows["qsa_verify_step_T3"] = {
         "us_per_layer": round(us, 2), "bytes_per_layer": step_bytes, "GBs": gbs(step_bytes, us),
         "frac": frac(step_bytes, us), "blocks": nbm, "k_blocks": kb, "cells_per_position": nc,
-        "union_cells": union, "launches_per_layer": 3 + 3 + 1 + 2 + 2,
-        "what": "prepare x3, pool decode x3, select (3 queries), K/V produce, gated query-cells attention + merge"}
+        "union_cells": union, "launches_per_layer": 1 + 1 + 2 + 2 + 2,
+        "us_per_layer_positions_one_a_call": round(us_chained, 2),
+        "what": "prepare steps, pool decode steps (one launch each for the 3 positions), select (3 queries), "
+                "K/V produce, gated query-cells attention + merge; us_per_layer_positions_one_a_call: prepare x3 "
+                "and pool decode x3 as the reference issues them"}
 
     # ---- the attention alone at the reference's decode shape ----
     sel = cells.clone()

@@ -367,6 +367,31 @@ int64_t qwfn_qsa_bucket(int32_t n_past, int32_t ratio, int64_t n_blocks_max);
  * 1e9 for the incomplete block of n_past, -inf past it. */
 int qwfn_qsa_decode_prepare(const qwfn_qsa_inputs * qd, const float * prev_bias, int32_t n_past, void * stream);
 
+/* The inputs of a verify step's T positions n_past .. n_past + T - 1 in one
+ * launch (engine::attn_decode's T chained preparations, qwfn_engine.cpp:
+ * 2259-2280 through :1072-1105 and :3582-3614): the same values as
+ * qwfn_qsa_decode_prepare(&qd[0], NULL, n_past) followed by
+ * qwfn_qsa_decode_prepare(&qd[t], qd[t-1].bias, n_past + t) for t = 1 ..
+ * T-1. qd: host array of T input sets with the same ratio and n_blocks_max
+ * and bias rows that do not overlap; qd[0].bias holds the running bias.
+ * T <= 16. No counterpart in the reference, which prepares one position a
+ * call; for engines that batch the step's positions. */
+int qwfn_qsa_decode_prepare_steps(const qwfn_qsa_inputs * qd, int32_t T, int32_t n_past, void * stream);
+
+/* qsa_dec_index for the T positions of a verify step in one launch (the T
+ * chained sparse_attn_decode calls of engine::attn_decode, qwfn_engine.cpp:
+ * 2259-2280, each through qwfn_graph.cpp:529-554): the same index cache and
+ * pool as qwfn_qsa_pool_decode for position 0, 1, .. T-1 in order, with
+ * position t's raw key in row t of k_raw (F32, rows k_raw_nb1 bytes apart;
+ * NULL: no keys are written) and its device inputs in qd[t] (host array, as
+ * qwfn_qsa_decode_prepare or _steps wrote them; qd[t].bias is not read).
+ * Only the last position of each block pools it, with the keys of this call
+ * taken from k_raw. T <= 16. No counterpart in the reference, which runs one
+ * position a call; for engines that batch the step's positions. */
+int qwfn_qsa_pool_decode_steps(uint16_t * idx_cache, int64_t ic_rows, const float * k_raw, size_t k_raw_nb1,
+                               const qwfn_qsa_inputs * qd, int32_t T, const float * k_norm_w, uint16_t * pool,
+                               int64_t pool_rows, const qwfn_qsa_pool_cfg * cfg, void * stream);
+
 /* The full bias rewrite of qsa_pool_rebuild (qwfn_engine.cpp:1115-1120):
  * 0 for blocks < (n_past+1)/ratio, the block of n_past 0 or 1e9, -inf after.
  * n_past = -1 writes -inf everywhere (engine::reset, init_qsa_tables). */

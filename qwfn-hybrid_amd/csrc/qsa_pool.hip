@@ -48,6 +48,36 @@ struct pool_args {
     uint32_t *       status;
 };
 
+// The pooled block's tail, for the mean x[0 .. dim) of its member rows (one
+// wave): RMS norm (the squares in float, summed in double across the wave),
+// times the weight, IMROPE at positions pos[0..3], F16 into pool row orow.
+__device__ __forceinline__ void pool_finish(const pool_args & a, float * x, int lane, const int32_t (&pos)[4], int64_t orow) {
+    const int dim = a.dim;
+    double sq = 0.0;
+    for (int d = lane; d < dim; d += 64) sq += (double) __fmul_rn(x[d], x[d]);
+    sq = wave::wave_sum_d(sq);
+    const float mean = (float) (sq / (double) dim);
+    const float scale = 1.0f / sqrtf(__fadd_rn(mean, a.eps));
+    for (int d = lane; d < dim; d += 64) x[d] = __fmul_rn(__fmul_rn(x[d], scale), a.w[d]);
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    const bool ook = orow >= 0 && orow < a.pool_rows;
+    if (!ook) {
+        if (lane == 0) atomicOr(a.status, DEVERR_SET_ROWS_INDEX);
+        return;
+    }
+    uint16_t * out = a.pool + (size_t) orow * dim;
+    const int half = a.rp.n_dims / 2;
+    if (lane < half) {
+        float c, s, y0, y1;
+        rope_cos_sin(a.rp, pos, lane, &c, &s);
+        rope_rotate(x[lane], x[lane + half], c, s, &y0, &y1);
+        out[lane] = f2h(y0);
+        out[lane + half] = f2h(y1);
+    }
+    for (int d = a.rp.n_dims + lane; d < dim; d += 64) out[d] = f2h(x[d]);
+}
+
 template <bool DECODE>
 __global__ __launch_bounds__(POOL_WAVES * 64) void k_qsa_pool(pool_args a) {
     __shared__ float xs[POOL_WAVES][POOL_MAX_DIM];
@@ -94,16 +124,6 @@ __global__ __launch_bounds__(POOL_WAVES * 64) void k_qsa_pool(pool_args a) {
         }
         x[d] = __fmul_rn(acc, a.inv_r);
     }
-    // RMS norm: the squares (float) summed in double across the wave
-    double sq = 0.0;
-    for (int d = lane; d < dim; d += 64) sq += (double) __fmul_rn(x[d], x[d]);
-    sq = wave::wave_sum_d(sq);
-    const float mean = (float) (sq / (double) dim);
-    const float scale = 1.0f / sqrtf(__fadd_rn(mean, a.eps));
-    for (int d = lane; d < dim; d += 64) x[d] = __fmul_rn(__fmul_rn(x[d], scale), a.w[d]);
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-
     int32_t pos[4];
     int64_t orow;
     if constexpr (DECODE) {
@@ -113,21 +133,77 @@ __global__ __launch_bounds__(POOL_WAVES * 64) void k_qsa_pool(pool_args a) {
         for (int s = 0; s < 4; s++) pos[s] = (int32_t) (blk * a.r);
         orow = blk;
     }
-    const bool ook = orow >= 0 && orow < a.pool_rows;
-    if (!ook) {
-        if (lane == 0) atomicOr(a.status, DEVERR_SET_ROWS_INDEX);
-        return;
+    pool_finish(a, x, lane, pos, orow);
+}
+
+// qsa_dec_index for the T positions of a step, one wave each (wave w of
+// workgroup g: position 4 g + w): the same caches as T k_qsa_pool<true>
+// calls in position order. Every position writes its raw key; only the last
+// position of each block pools it, since an earlier position's pooled row
+// would be overwritten by the later one's. A member row that a position of
+// this call at or before the pooling one writes is taken from that
+// position's key (rounded to F16, as written), never from memory; a block's
+// members never include a later position (they are cells of the block up to
+// its position).
+constexpr int POOL_MAX_T = 16;
+struct pool_steps_args {
+    pool_args       p;                        // caches, geometry, norm and rope constants, status
+    const float *   k_raw;                    // F32 [T][dim], rows k_ld floats apart, or null (no keys)
+    int64_t         k_ld;
+    const int32_t * write_idx[POOL_MAX_T];
+    const int32_t * member_idx[POOL_MAX_T];
+    const int32_t * blk_pos[POOL_MAX_T];
+    const int32_t * blk_idx[POOL_MAX_T];
+    int32_t         T;
+};
+
+__global__ __launch_bounds__(POOL_WAVES * 64) void k_qsa_pool_steps(pool_steps_args s) {
+    __shared__ float xs[POOL_WAVES][POOL_MAX_DIM];
+    const pool_args & a = s.p;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int t = (int) blockIdx.x * POOL_WAVES + wv;
+    if (t >= s.T) return;
+    const int dim = a.dim;
+    // every position's write row and block: lane u holds position u's
+    int32_t wi = -1, bi = -1;
+    if (lane < s.T) {
+        wi = s.k_raw ? *s.write_idx[lane] : -1;
+        bi = *s.blk_idx[lane];
     }
-    uint16_t * out = a.pool + (size_t) orow * dim;
-    const int half = a.rp.n_dims / 2;
-    if (lane < half) {
-        float c, s, y0, y1;
-        rope_cos_sin(a.rp, pos, lane, &c, &s);
-        rope_rotate(x[lane], x[lane + half], c, s, &y0, &y1);
-        out[lane] = f2h(y0);
-        out[lane + half] = f2h(y1);
+    const int32_t wrow = __shfl(wi, t), blk = __shfl(bi, t);
+    if (s.k_raw) {
+        const bool wok = wrow >= 0 && wrow < a.ic_rows;
+        for (int d = lane; d < dim; d += 64)
+            if (wok) a.ic[(size_t) wrow * dim + d] = f2h(s.k_raw[(size_t) t * s.k_ld + d]);
+        if (!wok && lane == 0) atomicOr(a.status, DEVERR_SET_ROWS_INDEX);
     }
-    for (int d = a.rp.n_dims + lane; d < dim; d += 64) out[d] = f2h(x[d]);
+    bool last = true;
+    for (int u = t + 1; u < s.T; u++) last &= __shfl(bi, u) != blk;
+    if (!last) return;
+    float * x = xs[wv];
+    const int32_t * mem = s.member_idx[t];
+    for (int d = lane; d < dim; d += 64) {
+        float acc = 0.f;
+        for (int m = 0; m < a.r; m++) {
+            const int64_t row = mem[m];
+            int src = -1;                              // the latest position at or before t writing this row
+            for (int u = 0; u <= t; u++) src = __shfl(wi, u) == row ? u : src;
+            float v;
+            if (src >= 0) {
+                v = h2f(f2h(s.k_raw[(size_t) src * s.k_ld + d]));
+            } else if (row >= 0 && row < a.ic_rows) {
+                v = h2f(a.ic[(size_t) row * dim + d]);
+            } else {
+                v = 0.f;
+                if (d == lane && lane == 0) atomicOr(a.status, DEVERR_GET_ROWS_INDEX);
+            }
+            acc = m == 0 ? v : __fadd_rn(acc, v);
+        }
+        x[d] = __fmul_rn(acc, a.inv_r);
+    }
+    int32_t pos[4];
+    for (int q = 0; q < 4; q++) pos[q] = s.blk_pos[t][q];
+    pool_finish(a, x, lane, pos, blk);
 }
 
 // The rebuild with 16-byte lanes, for dim / 8 a power of two and 16-byte
@@ -329,6 +405,39 @@ extern "C" int qwfn_qsa_pool_decode(uint16_t * idx_cache, int64_t ic_rows, const
         if (int rc = status_word(&a.status)) return rc;
         hipLaunchKernelGGL(k_qsa_pool<true>, dim3(1), dim3(POOL_WAVES * 64), 0, as_stream(stream), a);
         return hip_check(hipGetLastError(), "qsa_pool_decode launch");
+    });
+}
+
+extern "C" int qwfn_qsa_pool_decode_steps(uint16_t * idx_cache, int64_t ic_rows, const float * k_raw, size_t k_raw_nb1,
+                                          const qwfn_qsa_inputs * qd, int32_t T, const float * k_norm_w, uint16_t * pool,
+                                          int64_t pool_rows, const qwfn_qsa_pool_cfg * cfg, void * stream) {
+    return ::qwfn::abi_call("qsa_pool_decode_steps", [&]() -> int {
+        if (!qd) return set_error(QWFN_EINVAL, "qsa_pool_decode_steps: NULL inputs");
+        if (T < 1 || T > POOL_MAX_T) return set_error(QWFN_ENOTSUP, "qsa_pool_decode_steps: 1 to 16 positions");
+        pool_steps_args sa{};
+        if (int rc = pool_cfg_args(cfg, qd[0].ratio, k_norm_w, &sa.p)) return rc;
+        if (!idx_cache || !pool) return set_error(QWFN_EINVAL, "qsa_pool_decode_steps: NULL pointer");
+        if (ic_rows < 1 || pool_rows < 1) return set_error(QWFN_EINVAL, "qsa_pool_decode_steps: empty cache");
+        if (!is_aligned(idx_cache, 2) || !is_aligned(pool, 2) || !is_aligned(k_norm_w, 4) ||
+            (k_raw && (!is_aligned(k_raw, 4) || k_raw_nb1 % 4 || k_raw_nb1 < (size_t) sa.p.dim * 4)))
+            return set_error(QWFN_EALIGN, "qsa_pool_decode_steps: element alignment, or k_raw rows shorter than idx_dim");
+        for (int t = 0; t < T; t++) {
+            if (qd[t].ratio != qd[0].ratio) return set_error(QWFN_EINVAL, "qsa_pool_decode_steps: positions of different ratios");
+            if (!qd[t].member_idx || !qd[t].blk_pos || !qd[t].blk_idx || (k_raw && !qd[t].write_idx))
+                return set_error(QWFN_EINVAL, "qsa_pool_decode_steps: NULL tensor");
+            sa.write_idx[t] = qd[t].write_idx;
+            sa.member_idx[t] = qd[t].member_idx;
+            sa.blk_pos[t] = qd[t].blk_pos;
+            sa.blk_idx[t] = qd[t].blk_idx;
+        }
+        sa.p.ic = idx_cache; sa.p.ic_rows = ic_rows; sa.p.pool = pool; sa.p.pool_rows = pool_rows;
+        sa.k_raw = k_raw;
+        sa.k_ld = (int64_t) (k_raw_nb1 / 4);
+        sa.T = T;
+        if (int rc = status_word(&sa.p.status)) return rc;
+        hipLaunchKernelGGL(k_qsa_pool_steps, dim3((unsigned) ((T + POOL_WAVES - 1) / POOL_WAVES)), dim3(POOL_WAVES * 64), 0,
+                           as_stream(stream), sa);
+        return hip_check(hipGetLastError(), "qsa_pool_decode_steps launch");
     });
 }
 

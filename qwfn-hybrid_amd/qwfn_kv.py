@@ -147,7 +147,7 @@ EXPORTS = [
     "qwfn_state_summary", "qwfn_state_n_past", "qwfn_state_rollback_depth", "qwfn_state_step_done",
     "qwfn_state_reset", "qwfn_state_rollback", "qwfn_snapshot_parts", "qwfn_snapshot_save", "qwfn_snapshot_load",
     "qwfn_causal_mask_f16", "qwfn_cell_mask_f16", "qwfn_qsa_chunk_inputs", "qwfn_qsa_mask_f16",
-    "qwfn_qsa_bucket", "qwfn_qsa_decode_prepare",
+    "qwfn_qsa_bucket", "qwfn_qsa_decode_prepare", "qwfn_qsa_decode_prepare_steps", "qwfn_qsa_pool_decode_steps",
     "qwfn_qsa_bias_rebuild", "qwfn_qsa_tables",
     "qwfn_snap_pool_create", "qwfn_snap_pool_destroy", "qwfn_snap_pool_count", "qwfn_snap_pool_bytes",
     "qwfn_snap_pool_entry", "qwfn_snap_pool_save", "qwfn_snap_pool_best", "qwfn_snap_pool_load",
@@ -245,6 +245,7 @@ def load(path: str = LIB_PATH):
     L.qwfn_qsa_bucket.argtypes = [i32, i32, i64]
     L.qwfn_qsa_bucket.restype = i64
     L.qwfn_qsa_decode_prepare.argtypes = [ctypes.POINTER(QsaInputs), vp, i32, vp]
+    L.qwfn_qsa_decode_prepare_steps.argtypes = [ctypes.POINTER(QsaInputs), i32, i32, vp]
     L.qwfn_qsa_bias_rebuild.argtypes = [vp, i64, i32, i32, vp]
     L.qwfn_qsa_tables.argtypes = [vp, i64, i32, vp, i64, vp, i64, vp]
     PI = ctypes.POINTER(i32)
@@ -267,6 +268,8 @@ def load(path: str = LIB_PATH):
     L.qwfn_qsa_pool_cfg_default.restype = None
     L.qwfn_set_rows_f16.argtypes = [T, T, T, vp]
     L.qwfn_qsa_pool_decode.argtypes = [vp, i64, vp, vp, vp, i32, vp, vp, vp, vp, i64, ctypes.POINTER(QsaPoolCfg), vp]
+    L.qwfn_qsa_pool_decode_steps.argtypes = [vp, i64, vp, sz, ctypes.POINTER(QsaInputs), i32, vp, vp, i64,
+                                             ctypes.POINTER(QsaPoolCfg), vp]
     L.qwfn_qsa_pool_rebuild.argtypes = [vp, i64, i64, i32, vp, vp, i64, ctypes.POINTER(QsaPoolCfg), vp]
     L.qwfn_gated_delta_net.argtypes = [vp, i64, vp, i64, vp, i64, vp, vp, i32, i32, i32, i32, ctypes.c_float, vp, vp,
                                        vp, sz, i32, vp]
@@ -593,6 +596,24 @@ def qsa_pool_decode(ic, k_raw, write_idx, member_idx, ratio: int, blk_pos, blk_i
                                              write_idx.data_ptr(), member_idx.data_ptr(), ratio, blk_pos.data_ptr(),
                                              blk_idx.data_ptr(), k_norm_w.data_ptr(), pool.data_ptr(), pool.shape[0],
                                              ctypes.byref(cfg), _stream(stream)))
+
+
+def qsa_pool_decode_steps(ic, k_raw, qds, k_norm_w, pool, cfg=None, stream=None):
+    """qsa_dec_index for a step's T positions in one launch: k_raw f32 [T, idx_dim] (rows may be strided) or None;
+    qds: the positions' QsaDecodeInputs (qwfn_state), as prepared."""
+    cfg = cfg or qsa_pool_cfg()
+    T = len(qds)
+    _check_pool_args("qsa_pool_decode_steps", cfg, ic, pool, k_norm_w, k_raw=k_raw[0] if k_raw is not None else None,
+                     write_idx=qds[0].write_idx, member_idx=qds[0].member_idx, blk_pos=qds[0].blk_pos,
+                     blk_idx=qds[0].blk_idx)
+    if k_raw is not None and (k_raw.dim() != 2 or k_raw.shape[0] != T or k_raw.stride(1) != 1):
+        raise ValueError("qsa_pool_decode_steps: k_raw must be [T, idx_dim] with contiguous rows")
+    arr = (QsaInputs * T)(*[q._c() for q in qds])
+    return check(load().qwfn_qsa_pool_decode_steps(ic.data_ptr(), ic.shape[0],
+                                                   k_raw.data_ptr() if k_raw is not None else None,
+                                                   k_raw.stride(0) * 4 if k_raw is not None else 0, arr, T,
+                                                   k_norm_w.data_ptr(), pool.data_ptr(), pool.shape[0],
+                                                   ctypes.byref(cfg), _stream(stream)))
 
 
 def qsa_pool_rebuild(ic, n_past: int, ratio: int, k_norm_w, pool, cfg=None, stream=None):

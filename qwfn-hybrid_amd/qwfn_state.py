@@ -302,6 +302,16 @@ class QsaDecodeInputs:
                                                K._stream(stream)))
 
 
+def qsa_decode_prepare_steps(qds, n_past: int, stream=None):
+    """The inputs of positions n_past .. n_past + T - 1 in one launch: the same as qds[0].prepare(n_past)
+    followed by qds[t].prepare(n_past + t, prev=qds[t - 1])."""
+    arr = (K.QsaInputs * len(qds))(*[q._c() for q in qds])
+    K.check(K.load().qwfn_qsa_decode_prepare_steps(arr, len(qds), n_past, K._stream(stream)))
+    nb = max(q.bucket(n_past + t) for t, q in enumerate(qds))
+    for q in qds:
+        q.n_bucket = nb
+
+
 def qsa_tables(blk_cells, ratio: int, cell_pos=None, blk_pos_all=None, n_whole: int = 0, stream=None):
     n_blocks_max = blk_cells.numel() // ratio if blk_cells is not None else 0
     K.check(K.load().qwfn_qsa_tables(blk_cells.data_ptr() if blk_cells is not None else None, n_blocks_max, ratio,

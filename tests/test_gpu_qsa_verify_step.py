@@ -13,9 +13,11 @@ sparse_attn_decode calls (qwfn_graph.cpp:653-705); call k
   - attends its cells masked to positions at most its own, times
     sigmoid(gate) (:662-701).
 The device runs the same chain batched the way the library offers it:
-prepare x3, pool decode x3, ONE selection over the three queries, ONE K/V
-producer call for the three rows, ONE attention launch over the three lists
-(qwfn_flash_attn_ext_q8_0_query_cells) with the gate. The oracle runs the
+prepare x3, pool decode x3 (or each in one launch for the three positions:
+qwfn_qsa_decode_prepare_steps, qwfn_qsa_pool_decode_steps), ONE selection
+over the three queries, ONE K/V producer call for the three rows, ONE
+attention launch over the three lists (qwfn_flash_attn_ext_q8_0_query_cells)
+with the gate. The oracle runs the
 chain position by position, so the test also shows that batching the pool
 writes ahead of the selection changes nothing: a later position only touches
 its own block, which an earlier query either keeps by the 1e9 bias of its
@@ -54,8 +56,8 @@ def _ulp_ok(got_bits, ref_bits):
     assert int((d != 0).sum()) <= max(1, d.size // 1000)
 
 
-@pytest.mark.parametrize("n_past", [73700, 73702])
-def test_qsa_verify_step_composed(gpu, oracle, n_past):
+@pytest.mark.parametrize("n_past,batched", [(73700, False), (73702, False), (73700, True), (73702, True)])
+def test_qsa_verify_step_composed(gpu, oracle, n_past, batched):
     K = gpu
     rng = np.random.default_rng(n_past)
     # ---- the layer's state after a prefill to n_past
@@ -89,11 +91,16 @@ def test_qsa_verify_step_composed(gpu, oracle, n_past):
         qds.append(qd)
     qds[0].rebuild_bias(n_past)
     pool0 = host(pool).view(np.uint16).copy()     # the oracle chain starts from the device's rebuilt pool
-    say("prepare / prepare_k, pool decode x3")
-    for k in range(T):
-        qds[k].prepare(n_past + k, prev=qds[k - 1] if k else None)
-        K.qsa_pool_decode(ic_d, dev(k_raw[k]), qds[k].write_idx, qds[k].member_idx, RATIO, qds[k].blk_pos,
-                          qds[k].blk_idx, knw_idx_d, pool)
+    if batched:
+        say("prepare steps, pool decode steps (one launch each)")
+        S.qsa_decode_prepare_steps(qds, n_past)
+        K.qsa_pool_decode_steps(ic_d, dev(k_raw), qds, knw_idx_d, pool)
+    else:
+        say("prepare / prepare_k, pool decode x3")
+        for k in range(T):
+            qds[k].prepare(n_past + k, prev=qds[k - 1] if k else None)
+            K.qsa_pool_decode(ic_d, dev(k_raw[k]), qds[k].write_idx, qds[k].member_idx, RATIO, qds[k].blk_pos,
+                              qds[k].blk_idx, knw_idx_d, pool)
     nb = qds[-1].n_bucket
     assert nb == NB_MAX
     cells = torch.full((T, K_BLOCKS * RATIO), -1, dtype=torch.int32, device="cuda")

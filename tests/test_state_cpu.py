@@ -245,6 +245,28 @@ def test_step_input_validation():
         setattr(q, f, FAKE)
     q.ratio, q.n_blocks_max = 0, 16
     err(L.qwfn_qsa_decode_prepare(ctypes.byref(q), None, 0, None), K.EINVAL, "ratio")
+    # the step forms: 1 to 16 positions, one ratio, bias rows apart, k_raw rows of idx_dim floats
+    arr = (K.QsaInputs * 2)()
+    for qq in arr:
+        for f in ("bias", "write_idx", "member_idx", "blk_pos", "blk_idx", "npast_f"):
+            setattr(qq, f, FAKE)
+        qq.ratio, qq.n_blocks_max = 4, 16
+    err(L.qwfn_qsa_decode_prepare_steps(arr, 0, 5, None), K.ENOTSUP, "1 to 16")
+    err(L.qwfn_qsa_decode_prepare_steps(arr, 17, 5, None), K.ENOTSUP, "1 to 16")
+    err(L.qwfn_qsa_decode_prepare_steps(arr, 2, -1, None), K.EINVAL, "positions")
+    err(L.qwfn_qsa_decode_prepare_steps(arr, 2, 5, None), K.EINVAL, "overlap")
+    arr[1].bias, arr[1].ratio = FAKE + 4096, 8
+    err(L.qwfn_qsa_decode_prepare_steps(arr, 2, 5, None), K.EINVAL, "same ratio")
+    arr[1].ratio = 4
+    cfg = K.QsaPoolCfg()
+    L.qwfn_qsa_pool_cfg_default(ctypes.byref(cfg))
+    err(L.qwfn_qsa_pool_decode_steps(FAKE, 100, FAKE, 512, arr, 17, FAKE, FAKE, 10, ctypes.byref(cfg), None),
+        K.ENOTSUP, "1 to 16")
+    err(L.qwfn_qsa_pool_decode_steps(FAKE, 100, FAKE, 256, arr, 2, FAKE, FAKE, 10, ctypes.byref(cfg), None),
+        K.EALIGN, "shorter")
+    arr[1].ratio = 8
+    err(L.qwfn_qsa_pool_decode_steps(FAKE, 100, FAKE, 512, arr, 2, FAKE, FAKE, 10, ctypes.byref(cfg), None),
+        K.EINVAL, "ratios")
     err(L.qwfn_qsa_bias_rebuild(FAKE, 16, -2, 4, None), K.EINVAL, "sizes")
     err(L.qwfn_qsa_tables(FAKE, 1 << 30, 4, None, 0, None, 0, None), K.ERANGE, "int32")
     # snapshot calls need states with memory
