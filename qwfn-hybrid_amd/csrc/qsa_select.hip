@@ -11,7 +11,8 @@
 //
 // Two kernels. k_qsa_score reads the pool cache (n_blocks x 128 f16, 4.7 MB
 // at 18432 blocks) once for up to 8 queries and computes the dot products on
-// the matrix cores, one wave per 16 blocks; the scores land in a workspace.
+// the matrix cores, one wave per 16 blocks (per 32 to 128 blocks when many
+// queries keep the grid full); the scores land in a workspace.
 // k_qsa_topk, one workgroup per query, holds the scores in registers as
 // order-preserving keys of the float bits, and writes the cells of the k
 // best blocks, best first (ties: lower block first). Usually a threshold
@@ -52,6 +53,7 @@ struct score_args {
     const float *    bias;        // F32 [n_blocks] per query, query stride bias_nb1 bytes
     size_t           bias_nb1;
     float *          score;       // [T][score_ld(n_blocks)]
+    int32_t          mb;          // 16-block tiles per wave
 };
 
 // sum over the 16 lanes of a DPP row, the same tree as butterflies over lane
@@ -83,67 +85,89 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float    v4f __attribute__((ext_vector_type(4)));
 
 // Scores as a GEMM on the matrix cores: D[block][col] = pool[block] . q16[col]
-// with v_mfma_f32_16x16x32_f16, one wave per 16 blocks. The columns of a tile
-// are (query, head) pairs, 2^head_bits columns per query (heads past n_heads
-// are zero), so a query's heads are adjacent lanes of a DPP row. A (the keys)
-// comes from global memory straight into registers: lane (lg, ln) holds dims
-// [32 s + 8 lg, +8) of block ln for k-step s; B (the query heads, rounded to
-// f16) likewise for column ln. D: lane (lg, ln) holds blocks 4 lg + r of
-// column ln. relu, then the sum over a query's heads across its lanes; the
-// first lane of each query adds the bias and writes 4 scores. No LDS, no
-// barriers: a wave past the last block leaves at once.
+// with v_mfma_f32_16x16x32_f16, one wave per a.mb tiles of 16 blocks. The
+// columns of a tile are (query, head) pairs, 2^head_bits columns per query
+// (heads past n_heads are zero), so a query's heads are adjacent lanes of a
+// DPP row. B (the query heads, rounded to f16) is loaded once per wave into
+// registers, all of the workgroup's queries: lane (lg, ln) holds dims
+// [32 s + 8 lg, +8) of column ln for k-step s. A (the keys) likewise for block
+// ln of each 16-block tile, the next tile's keys loaded while the current one
+// is scored. D: lane (lg, ln) holds blocks 4 lg + r of column ln. relu, then
+// the sum over a query's heads across its lanes; the first lane of each query
+// adds the bias and writes 4 scores. No LDS, no barriers: a wave past the
+// last block leaves at once.
+// 16-column tiles of a pass's query columns, at most: 8 queries of 8 columns
+constexpr int SCORE_MAX_QT = SCORE_T * MAX_IDX_HEADS / 16;
+
+__device__ __forceinline__ void score_keys(const score_args & a, int64_t blk, int lg, v8h (&kr)[4]) {
+#pragma unroll
+    for (int st = 0; st < 4; st++) {
+        uint4 raw = make_uint4(0u, 0u, 0u, 0u);
+        if (blk < a.n_blocks) raw = *(const uint4 *) ((const char *) a.pool + (size_t) blk * a.pool_nb1 + (32 * st + 8 * lg) * 2);
+        kr[st] = __builtin_bit_cast(v8h, raw);
+    }
+}
+
 __global__ __launch_bounds__(SCORE_THREADS) void k_qsa_score(score_args a) {
     const int lane = threadIdx.x & 63;
     const int ln = lane & 15, lg = lane >> 4;
     const int64_t n = a.n_blocks;
-    const int64_t m0 = ((int64_t) blockIdx.x * (SCORE_THREADS / 64) + (threadIdx.x >> 6)) * 16;
-    if (m0 >= n) return;
+    const int64_t tile0 = ((int64_t) blockIdx.x * (SCORE_THREADS / 64) + (threadIdx.x >> 6)) * a.mb;
+    if (tile0 * 16 >= n) return;
     const int t0 = blockIdx.y * SCORE_T;
     const int nt = a.T - t0 < SCORE_T ? a.T - t0 : SCORE_T;
     const int hb = a.head_bits, Hp = 1 << hb;
     const int QT = 16 >> hb;                                      // queries per tile of 16 columns
     const int n_tiles = (nt + QT - 1) / QT;
-    const int64_t blk = m0 + ln;
-    v8h kr[4];
+    const int h = ln & (Hp - 1);
+    v8h qb[SCORE_MAX_QT][4];
 #pragma unroll
-    for (int st = 0; st < 4; st++) {
-        uint4 raw = make_uint4(0u, 0u, 0u, 0u);
-        if (blk < n) raw = *(const uint4 *) ((const char *) a.pool + (size_t) blk * a.pool_nb1 + (32 * st + 8 * lg) * 2);
-        kr[st] = __builtin_bit_cast(v8h, raw);
-    }
-    const int64_t ld = score_ld(n);
-    const int64_t ob = m0 + 4 * lg;                               // blocks ob .. ob + 3 of this lane's D rows
-    for (int tile = 0; tile < n_tiles; tile++) {
+    for (int tile = 0; tile < SCORE_MAX_QT; tile++) {
         const int tl = tile * QT + (ln >> hb);                    // query of this lane's column
-        const int h = ln & (Hp - 1);
-        const bool colv = tl < nt && h < a.n_heads;
-        const bool writer = h == 0 && tl < nt;
-        const float * qp = (const float *) ((const char *) a.q + (size_t) (t0 + (tl < nt ? tl : 0)) * a.q_nb2)
-                           + h * IDX_DIM + 8 * lg;
-        v8h qb[4];
+        const bool colv = tile < n_tiles && tl < nt && h < a.n_heads;
+        const float * qp = (const float *) ((const char *) a.q + (size_t) (t0 + (colv ? tl : 0)) * a.q_nb2)
+                           + (colv ? h : 0) * IDX_DIM + 8 * lg;
 #pragma unroll
         for (int st = 0; st < 4; st++) {
             float4 x = make_float4(0.f, 0.f, 0.f, 0.f), y = x;
             if (colv) { x = *(const float4 *) (qp + 32 * st); y = *(const float4 *) (qp + 32 * st + 4); }
-            qb[st] = v8h{(_Float16) x.x, (_Float16) x.y, (_Float16) x.z, (_Float16) x.w,
-                         (_Float16) y.x, (_Float16) y.y, (_Float16) y.z, (_Float16) y.w};   // round to nearest even
+            qb[tile][st] = v8h{(_Float16) x.x, (_Float16) x.y, (_Float16) x.z, (_Float16) x.w,
+                               (_Float16) y.x, (_Float16) y.y, (_Float16) y.z, (_Float16) y.w};   // round to nearest even
         }
-        float bias4[4];
-        const char * brow = (const char *) a.bias + (size_t) (t0 + (tl < nt ? tl : 0)) * a.bias_nb1;
+    }
+    const int64_t ld = score_ld(n);
+    v8h kr[4];
+    score_keys(a, tile0 * 16 + ln, lg, kr);
+    for (int mt = 0; mt < a.mb; mt++) {
+        const int64_t m0 = (tile0 + mt) * 16;
+        if (m0 >= n) break;
+        v8h kn[4];
+        score_keys(a, m0 + 16 + ln, lg, kn);                      // past the wave's last tile: not used
+        const int64_t ob = m0 + 4 * lg;                           // blocks ob .. ob + 3 of this lane's D rows
 #pragma unroll
-        for (int r = 0; r < 4; r++)
-            bias4[r] = (writer && ob + r < n) ? *(const float *) (brow + (size_t) (ob + r) * 4) : 0.f;
-        v4f acc = {0.f, 0.f, 0.f, 0.f};
+        for (int tile = 0; tile < SCORE_MAX_QT; tile++) {
+            if (tile >= n_tiles) break;
+            const int tl = tile * QT + (ln >> hb);
+            const bool writer = h == 0 && tl < nt;
+            const char * brow = (const char *) a.bias + (size_t) (t0 + (tl < nt ? tl : 0)) * a.bias_nb1;
+            float bias4[4];
 #pragma unroll
-        for (int st = 0; st < 4; st++) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr[st], qb[st], acc, 0, 0, 0);
+            for (int r = 0; r < 4; r++)
+                bias4[r] = (writer && ob + r < n) ? *(const float *) (brow + (size_t) (ob + r) * 4) : 0.f;
+            v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            float v = acc[r] > 0.f ? acc[r] : 0.f;                // relu per head
-            if (hb >= 1) v += dpp_f<0xB1>(v);                     // quad_perm 1,0,3,2
-            if (hb >= 2) v += dpp_f<0x4E>(v);                     // quad_perm 2,3,0,1
-            if (hb >= 3) v += dpp_f<0x141>(v);                    // row_half_mirror
-            if (writer && ob + r < n) a.score[(size_t) (t0 + tl) * ld + ob + r] = v + bias4[r];
+            for (int st = 0; st < 4; st++) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr[st], qb[tile][st], acc, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                float v = acc[r] > 0.f ? acc[r] : 0.f;            // relu per head
+                if (hb >= 1) v += dpp_f<0xB1>(v);                 // quad_perm 1,0,3,2
+                if (hb >= 2) v += dpp_f<0x4E>(v);                 // quad_perm 2,3,0,1
+                if (hb >= 3) v += dpp_f<0x141>(v);                // row_half_mirror
+                if (writer && ob + r < n) a.score[(size_t) (t0 + tl) * ld + ob + r] = v + bias4[r];
+            }
         }
+#pragma unroll
+        for (int st = 0; st < 4; st++) kr[st] = kn[st];
     }
 }
 
@@ -549,10 +573,16 @@ extern "C" int qwfn_qsa_select_cells(const uint16_t * pool, size_t pool_nb1, int
         hipStream_t st = as_stream(stream);
         int head_bits = 0;
         while ((1 << head_bits) < n_heads) head_bits++;
-        score_args sa{pool, pool_nb1, n_blocks, q, q_nb2, n_heads, head_bits, T, bias, bias_nb1, (float *) ws};
-        const int64_t per = SCORE_THREADS / 64 * 16;                 // blocks per workgroup: 16 per wave
+        // tiles per wave: a wave's query loads are shared by its tiles; more
+        // than one only while the grid keeps at least 2048 waves (a prefill
+        // chunk: 512 queries over 4224 blocks take 8)
+        const int64_t n_tile = (n_blocks + 15) / 16, ny = (T + SCORE_T - 1) / SCORE_T;
+        int32_t mb = 1;
+        while (mb < 8 && n_tile * ny / (2 * mb) >= 2048) mb *= 2;
+        score_args sa{pool, pool_nb1, n_blocks, q, q_nb2, n_heads, head_bits, T, bias, bias_nb1, (float *) ws, mb};
+        const int64_t per = SCORE_THREADS / 64 * 16 * mb;            // blocks per workgroup: 16 mb per wave
         const unsigned gx = (unsigned) ((n_blocks + per - 1) / per);
-        hipLaunchKernelGGL(k_qsa_score, dim3(gx, (unsigned) ((T + SCORE_T - 1) / SCORE_T)), dim3(SCORE_THREADS), 0, st, sa);
+        hipLaunchKernelGGL(k_qsa_score, dim3(gx, (unsigned) ny), dim3(SCORE_THREADS), 0, st, sa);
         if (int rc = hip_check(hipGetLastError(), "qsa score launch")) return rc;
         topk_args ta{(const float *) ws, n_blocks, k_blocks, blk_cells, ratio, cells, top};
         const int64_t kpt = (n_blocks + TOPK_THREADS - 1) / TOPK_THREADS;

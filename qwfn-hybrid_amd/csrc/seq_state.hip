@@ -234,8 +234,9 @@ struct qsa_chunk_args {
 // (0 before tail_b = min(n_bid, (q+1)/ratio), 1e9 up to n_bid, -inf after, the
 // dead block 1e9) followed by its -1e9 for positive entries of blocks wholly
 // after q.
-__device__ __forceinline__ float chunk_bias(int64_t b, int64_t q, int64_t r, int64_t n_bid, int64_t dead, bool have_dead) {
-    const int64_t tail_b = (q + 1) / r < n_bid ? (q + 1) / r : n_bid;
+// tail_b = min((q + 1) / r, n_bid): the whole blocks that end at or before q
+__device__ __forceinline__ float chunk_bias(int64_t b, int64_t q, int64_t r, int64_t tail_b, int64_t n_bid, int64_t dead,
+                                            bool have_dead) {
     float v = b < tail_b ? 0.0f : (b < n_bid ? 1e9f : -INFINITY);
     if (have_dead && b == dead) v = 1e9f;
     if (b >= tail_b && v > 0.0f && b * r > q) v = -1e9f;
@@ -252,8 +253,9 @@ __global__ __launch_bounds__(FILL_THREADS) void k_qsa_chunk(qsa_chunk_args a) {
     if ((int64_t) blockIdx.y < a.Tc) {
         if (!a.bias) return;
         const int64_t q = a.n_past_c + blockIdx.y;
+        const int64_t tail_b = (q + 1) / r < n_bid ? (q + 1) / r : n_bid;
         float * row = a.bias + (size_t) blockIdx.y * (size_t) a.bias_ld;
-        for (int64_t b = t0; b < a.n_blocks; b += stride) row[b] = chunk_bias(b, q, r, n_bid, dead, have_dead);
+        for (int64_t b = t0; b < a.n_blocks; b += stride) row[b] = chunk_bias(b, q, r, tail_b, n_bid, dead, have_dead);
         return;
     }
     if (a.cell_blk)
@@ -296,28 +298,49 @@ __global__ __launch_bounds__(FILL_THREADS) void k_qsa_mask(const int32_t * cells
     const uint16_t * src = causal + (size_t) t * (size_t) causal_ld;
     uint16_t * dst = mask + (size_t) t * (size_t) mask_ld;
     const int64_t groups = (mask_ld + 7) / 8;
-    for (int64_t g = threadIdx.x; g < groups; g += FILL_THREADS) {
-        const int64_t j0 = g * 8;
-        uint16_t v[8];
+    const bool src_al = ((uintptr_t) src & 15) == 0;
+    // a thread's groups in batches of MB: their causal values are loaded as
+    // 16-byte vectors (where the group lies inside the row, is aligned and
+    // holds a selected key) before any is used, so a batch waits for one
+    // round of loads
+    constexpr int MB = 8;
+    for (int64_t gb = threadIdx.x; gb < groups; gb += (int64_t) FILL_THREADS * MB) {
+        uint4 cw[MB];
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const int64_t j = j0 + e;
-            const bool on = j < n_kv && ((sel[j >> 5] >> (j & 31)) & 1u);
-            // selected: f16(+0 + c), which is c except that -0 becomes +0
-            const uint16_t c = on ? src[j] : F16_NINF;
-            v[e] = c == 0x8000u ? F16_ZERO : c;
+        for (int u = 0; u < MB; u++) {
+            const int64_t j0 = (gb + (int64_t) u * FILL_THREADS) * 8;
+            // only groups holding a selected key are read
+            const bool any = j0 + 8 <= n_kv && ((sel[j0 >> 5] >> (j0 & 31)) & 0xffu) != 0u;
+            cw[u] = (src_al && any) ? *(const uint4 *) (src + j0) : make_uint4(0u, 0u, 0u, 0u);
         }
-        if (j0 + 8 <= mask_ld && ((uintptr_t) (dst + j0) & 15) == 0) {
-            uint4 w;
-            w.x = v[0] | ((uint32_t) v[1] << 16);
-            w.y = v[2] | ((uint32_t) v[3] << 16);
-            w.z = v[4] | ((uint32_t) v[5] << 16);
-            w.w = v[6] | ((uint32_t) v[7] << 16);
-            store_nt16(dst + j0, w);
-        } else {
 #pragma unroll
-            for (int e = 0; e < 8; e++)
-                if (j0 + e < mask_ld) dst[j0 + e] = v[e];
+        for (int u = 0; u < MB; u++) {
+            const int64_t g = gb + (int64_t) u * FILL_THREADS;
+            if (g >= groups) break;
+            const int64_t j0 = g * 8;
+            const bool vec = src_al && j0 + 8 <= n_kv;
+            const uint32_t cwv[4] = {cw[u].x, cw[u].y, cw[u].z, cw[u].w};
+            uint16_t v[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int64_t j = j0 + e;
+                const bool on = j < n_kv && ((sel[j >> 5] >> (j & 31)) & 1u);
+                // selected: f16(+0 + c), which is c except that -0 becomes +0
+                const uint16_t c = on ? (vec ? (uint16_t) (cwv[e >> 1] >> (16 * (e & 1))) : src[j]) : F16_NINF;
+                v[e] = c == 0x8000u ? F16_ZERO : c;
+            }
+            if (j0 + 8 <= mask_ld && ((uintptr_t) (dst + j0) & 15) == 0) {
+                uint4 w;
+                w.x = v[0] | ((uint32_t) v[1] << 16);
+                w.y = v[2] | ((uint32_t) v[3] << 16);
+                w.z = v[4] | ((uint32_t) v[5] << 16);
+                w.w = v[6] | ((uint32_t) v[7] << 16);
+                store_nt16(dst + j0, w);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    if (j0 + e < mask_ld) dst[j0 + e] = v[e];
+            }
         }
     }
 }
@@ -813,8 +836,8 @@ int qwfn_qsa_chunk_inputs(int64_t n_past_c, int64_t Tc, int32_t ratio, int32_t *
         a.cell_blk = cell_blk; a.blk_cells = blk_cells; a.blk_pos = blk_pos; a.bias = bias;
         a.bias_ld = (int64_t) (bias_nb1 / 4);
         a.n_past_c = n_past_c; a.Tc = Tc; a.n_blocks = n_blocks; a.ratio = ratio;
-        const int64_t n = std::max<int64_t>({n_kv, n_blocks * ratio, 4 * n_blocks});
-        const dim3 g(grid_for(std::max<int64_t>(n, n_blocks)), (unsigned) (Tc + 1));
+        // sized for a bias row: the table row (blockIdx.y == Tc) strides over its longer tables
+        const dim3 g(grid_for(n_blocks), (unsigned) (Tc + 1));
         hipLaunchKernelGGL(k_qsa_chunk, g, dim3(FILL_THREADS), 0, as_stream(stream), a);
         return hip_check(hipGetLastError(), "qsa_chunk_inputs launch");
     });
