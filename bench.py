@@ -646,6 +646,22 @@ def measure_qsa_prefill_row(K, torch, np, dev, gen) -> dict:
         K.flash_attn_ext(K.q_view(pq), pk, pv, pmv, 1 / 16, K.out_view(pout), ws=pws)
     us_chain = timed(torch, chain, 5)
     us_attn = timed(torch, lambda k: K.flash_attn_ext(K.q_view(pq), pk, pv, pmv, 1 / 16, K.out_view(pout), ws=pws), 5)
+    # the same keys as lists: each query's visible cells (no causal or selection mask),
+    # then attention over them
+    lists = torch.empty((T, kb * ratio), dtype=torch.int32, device=dev)
+    counts = torch.empty((T,), dtype=torch.int32, device=dev)
+    lout = torch.empty((1, T, nh, hd), dtype=torch.float32, device=dev)
+
+    def chain_lists(k):
+        S.qsa_chunk_inputs(d0, T, ratio, None, bc, bp, bias)
+        K.qsa_pool_rebuild(ic, n_kv, ratio, knw, pool)
+        S.qsa_select_cells(pool, q_idx, bias, kb, bc, ratio, cells, ws=wsel)
+        S.qsa_visible_cells(cells, n_kv, d0, lists, counts)
+        K.flash_attn_ext_query_cells_dev(K.q_view(pq), pk, pv, lists, counts, d0, 1 / 16, K.out_view(lout))
+    us_lists = timed(torch, chain_lists, 5)
+    us_lattn = timed(torch, lambda k: K.flash_attn_ext_query_cells_dev(K.q_view(pq), pk, pv, lists, counts, d0, 1 / 16,
+                                                                        K.out_view(lout)), 5)
+    lerr = float((lout - pout).abs().max().item())
     visible = int((qmask[:, :n_kv] == 0).sum().item())
     flops = 4 * nh * hd * visible                               # QK^T and PV over the visible keys
     return {"prefill_512_at_16384_qsa": {
@@ -653,6 +669,9 @@ def measure_qsa_prefill_row(K, torch, np, dev, gen) -> dict:
         "blocks": nb, "k_blocks": kb, "visible_keys_per_query": round(visible / T, 1), "flops": flops,
         "TFLOPs": round(flops / (us_attn * 1e-6) / 1e12, 2),
         "frac_of_f16_mfma_peak": round(flops / (us_attn * 1e-6) / 2.5e15, 4),
+        "us_per_layer_lists": round(us_lists, 1), "us_attention_lists": round(us_lattn, 1),
+        "lists_gathered_bytes": int(counts.sum().item()) * nh_kv * 2 * 272,
+        "lists_max_abs_diff_vs_mask": lerr,
         "what": "chunk tables + pool of 4224 blocks + top-513 select for 512 queries + causal and selection masks "
                 "+ k_fa_pre over the selection mask"}}
 

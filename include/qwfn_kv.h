@@ -291,6 +291,28 @@ int qwfn_flash_attn_ext_q8_0_cells(const qwfn_tensor * q, const qwfn_tensor * k,
  * and sets bit 1 of qwfn_device_status; a query that sees no cell gets 0.
  * Size ws with qwfn_fattn_workspace_size_query_cells (ws NULL: the library's
  * buffer). */
+/* Many query positions, each over its own cell list, the list lengths on
+ * the device: the attention of the reference's QSA-on prefill chunk
+ * (ggml_flash_attn_ext over the selection mask, qwfn_graph.cpp:466-471)
+ * given the keys each query sees as lists (qwfn_qsa_visible_cells), and, with
+ * gate, the ggml_mul by sigmoid(gate) after it (:474). Query t (position
+ * pos0 + t) attends cache rows cells[t * cell_stride + j], j < counts[t]
+ * (counts: device int32 [T]), those at most pos0 + t, scaled by `scale`; a
+ * cell outside [0, n_rows) is masked and sets bit 1 of qwfn_device_status, a
+ * count outside [0, cell_stride] is clipped to it and sets the same bit, and a
+ * query that sees no cell gets 0. Lists may repeat cells (each copy counts).
+ * q: F32 [256, T, n_head, 1], 16-byte aligned strides; k, v: the q8_0 cache
+ * views [256, n_rows, n_head_kv, 1] (nb1 the row stride, nb2 the head
+ * offset), n_rows * row stride < 2 GiB, n_head / n_head_kv <= 16; cells:
+ * device int32, 16-byte aligned, cell_stride a positive multiple of 4; dst:
+ * contiguous F32 [256, n_head, T, 1], 16-byte aligned; gate: NULL or F32 of
+ * dst's shape and strides. No workspace: every list is one unit of k_fa_qc,
+ * with no key splits. */
+int qwfn_flash_attn_ext_q8_0_query_cells_dev(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
+                                             const int32_t * cells, const int32_t * counts, int64_t cell_stride,
+                                             int64_t pos0, float scale, const qwfn_tensor * gate,
+                                             const qwfn_tensor * dst, int variant, void * stream);
+
 size_t qwfn_fattn_workspace_size_query_cells(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,
                                              const int64_t * n_cells, int64_t cell_stride);
 int qwfn_flash_attn_ext_q8_0_query_cells(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * v,

@@ -339,6 +339,21 @@ int qwfn_qsa_chunk_inputs(int64_t n_past_c, int64_t Tc, int32_t ratio, int32_t *
 int qwfn_qsa_mask_f16(const int32_t * cells, int64_t width, size_t cells_nb1, const uint16_t * causal,
                       size_t causal_nb1, int64_t n_kv, int64_t T, uint16_t * mask, size_t mask_nb1, void * stream);
 
+/* The keys each query of a QSA-on prefill chunk sees, as lists: the zeros of
+ * qwfn_qsa_mask_f16's mask over the chunk's causal mask (qwfn_graph.cpp:
+ * 388-414 over the mask of qwfn_engine.cpp:1261-1270, 0 up to the query's
+ * position). Row t of lists (lists_nb1 bytes apart) gets the distinct cells
+ * of cells row t (I32 [T][width], rows cells_nb1 bytes apart: the
+ * qsa_top_k output) that are at most n_past + t, ascending; counts[t] their
+ * number (device int32). With qwfn_flash_attn_ext_q8_0_query_cells_dev over
+ * them (pos0 = n_past) it replaces qsa_mask and the flash attention over it:
+ * the same keys, no mask. A cell outside [0, n_kv) is skipped and sets bit 0
+ * of qwfn_device_status. No counterpart in the reference: its callers build
+ * the dense mask. lists_nb1 >= width * 4; cells, lists and counts must not
+ * overlap; n_kv <= 524288. */
+int qwfn_qsa_visible_cells(const int32_t * cells, int64_t width, size_t cells_nb1, int64_t n_kv, int64_t T,
+                           int64_t n_past, int32_t * lists, size_t lists_nb1, int32_t * counts, void * stream);
+
 /* ------------------------------------------- decode-time sparse-attention inputs */
 
 /* qsa_decode_inputs (qwfn_graph.h:71-84): device tensors written per token. */

@@ -432,3 +432,14 @@ def qsa_mask(cells: np.ndarray, causal_bits: np.ndarray, n_kv: int, row_len: int
     res = np.full((T, row_len), F16_NEG_INF, np.uint16)
     res[:, :n_kv] = out
     return res
+
+
+def visible_cells(cells_row: np.ndarray, n_kv: int, pos: int) -> np.ndarray:
+    """The keys a query at position pos of a QSA-on prefill chunk sees: the zero entries
+    of qsa_mask (qwfn_graph.cpp:388-414) over the chunk's causal row (0 at keys <= pos,
+    -inf after, qwfn_engine.cpp:1261-1270), ascending. cells_row: the query's selected
+    cells, all in [0, n_kv)."""
+    causal = np.full((1, n_kv), F16_NEG_INF, np.uint16)
+    causal[0, :min(n_kv, pos + 1)] = F16_ZERO
+    m = qsa_mask(np.asarray(cells_row, np.int64)[None], causal, n_kv, n_kv)
+    return np.flatnonzero(m[0] == F16_ZERO).astype(np.int32)

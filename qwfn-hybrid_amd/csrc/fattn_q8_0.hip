@@ -2064,6 +2064,421 @@ __global__ __launch_bounds__(DEC_WAVES * 64, 2) void k_fa_dec(fa_args a) {
     if (a.mctr) fa_merge_tail<DEC_WAVES * 64>(a, b, kvh, (float *) &ring[0][0][0]);
 }
 
+// ================================================================ many per-position cell lists
+//
+// k_fa_qc<KG> (KG = 2, 4, 8): attention of many query positions, each over its own list of
+// cache cells (the keys a query of a QSA-on prefill chunk sees: its selected
+// cells at or before its position, qwfn_graph.cpp:388-414 and :466-471), with
+// the list lengths on the device. A unit is one (position, KV head) list and
+// its n_head / n_head_kv query rows (at most 16: one MFMA tile, rows past the
+// group zero). A block of 8 waves takes 8 / KG units of one KV head; the KG
+// waves of a unit take its 16-key tiles round robin, each through a private
+// two-stage LDS-DMA ring as k_fa_dec's waves do, with the same arithmetic per
+// tile (exact i8 block dots of the requantised query, d_q*d_k per block,
+// online base-2 softmax, P*d_v as f16 hi + lo). No key splits: the KG waves
+// merge in LDS and the unit's rows go straight to dst (times sigmoid(gate)).
+// Blocks alternate over the KV heads, so with 2 KV heads each XCD's L2 serves
+// one head's rows.
+//
+// The tile's cells come by LDS DMA too, into four slots per wave, so every
+// vector-memory load of the key loop is a DMA and the explicit counts stay
+// exact: a step issues the K and V rows of the wave's tile two ahead (5 DMAs
+// each) and the cells of the tile four ahead (1 DMA), 11 in all, including
+// tiles past the list (their offsets lie past the buffers: zeros, no memory
+// access). So when step j starts, the ops issued after tile j's V rows are
+// the cells of tile j + 2, tile j + 1's K and V and the cells of tile j + 3:
+// vmcnt <= 12 means tile j has landed, and <= 11 that tile j + 2's cells have.
+
+constexpr int QC_WAVES  = 8;
+constexpr int QC_STAGE  = 2 * DEC_KB;                 // 8704: a tile's K and V rows
+constexpr int QC_SLOTS  = 4;                          // cell slots of a wave (16 cells each)
+constexpr int QC_AHEAD  = 2 * DEC_TDMA + 2;           // 12: DMAs issued after a tile's V rows when its step starts
+
+struct qc_args {
+    const char *    q;            // F32 [256, T, n_head]: position stride q_nb1, head stride q_nb2
+    uint32_t        q_nb1, q_nb2, q_bytes;
+    const char *    k;            // q8_0 cache rows: row stride k_nb1, KV head offset k_nb2
+    const char *    v;
+    uint32_t        k_nb1, v_nb1, k_nb2, v_nb2;
+    uint32_t        k_bytes, v_bytes;   // n_rows * row stride
+    int64_t         n_rows;
+    const int32_t * cells;        // list of position t at cells + t * cell_stride
+    int64_t         cell_stride;
+    const int32_t * counts;       // [T] list lengths (device)
+    int64_t         pos0;         // position of query 0
+    int32_t         T, nh, nh_kv, gqa;
+    float           scale_log2;   // scale * log2(e)
+    int32_t         x86;
+    float *         dst;          // F32 [256, n_head, T] contiguous
+    const float *   gate;         // null or dst's layout
+    uint32_t *      status;
+};
+
+template <int KG>
+__global__ __launch_bounds__(QC_WAVES * 64, 1) void k_fa_qc(qc_args a) {
+    constexpr int UPB = QC_WAVES / KG;                 // units of a block
+    constexpr int QR = 16 * UPB;                       // query rows staged by the block
+    constexpr int OPS = 2 * DEC_TDMA + 1;              // DMAs of a step
+    static_assert(QC_AHEAD == OPS + 1, "a step's DMAs and the cells issued before the next tile");
+    __shared__ __attribute__((aligned(16))) uint8_t ring[2][QC_WAVES][QC_STAGE];
+    __shared__ __attribute__((aligned(16))) uint16_t scl[QC_WAVES][2][NBLK][DEC_TK];
+    __shared__ __attribute__((aligned(16))) int32_t cslot[QC_WAVES][QC_SLOTS][DEC_TK];
+    static_assert(QR * DEC_QROW <= QC_WAVES * QC_STAGE, "query rows fit stage 1");
+    static_assert(QR * NBLK * QWIN + QR * NBLK * 4 <= QC_WAVES * QC_STAGE, "query image fits stage 1");
+    static_assert((KG - 1) * QR * DEC_OBS * 4 <= 2 * QC_WAVES * QC_STAGE, "merge buffers fit the ring");
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int ln = lane & 15, lg = lane >> 4;
+    const int unit = wave / KG, kg = wave % KG;
+    const int kvh = (int) (blockIdx.x % (unsigned) a.nh_kv);
+    const int t0 = (int) (blockIdx.x / (unsigned) a.nh_kv) * UPB;   // the block's first position
+    const int t = t0 + unit;
+    const bool live = t < a.T;
+    const int tq = live ? t : a.T - 1;                 // a unit past the last position reads its rows, stores nothing
+    int64_t n = live ? (int64_t) a.counts[t] : 0;
+    bool bad = n < 0 || n > a.cell_stride;             // a count outside [0, cell_stride] is clipped and flagged
+    n = n < 0 ? 0 : (n > a.cell_stride ? a.cell_stride : n);
+    const int span = (int) n;
+    const int n_tiles = (span + DEC_TK - 1) / DEC_TK;
+    const int J = kg < n_tiles ? (n_tiles - kg + KG - 1) / KG : 0;   // the wave's tiles kg, kg + KG, ...
+    const char * kbase = a.k + (size_t) kvh * a.k_nb2;
+    const char * vbase = a.v + (size_t) kvh * a.v_nb2;
+    const v4i rk = make_rsrc(kbase, a.k_bytes), rv = make_rsrc(vbase, a.v_bytes);
+    const v4i rc = make_rsrc(a.cells + (size_t) tq * (size_t) a.cell_stride, (uint32_t) span * 4u);
+    const int64_t q_pos = a.pos0 + tq;
+
+    // ---- DMA issue: piece p = 64 s + lane of a tile is byte 16 (p % 17) of
+    //      the row of its key p / 17; keys past the list, and cells outside
+    //      the cache, get an offset past the buffer (zeros, and the key is
+    //      masked) ----
+    const uint32_t stl0 = lds_addr(&ring[0][0][0]) + (uint32_t) wave * QC_STAGE;
+    const uint32_t stl1 = stl0 + QC_WAVES * QC_STAGE;
+    const uint32_t csl = lds_addr(&cslot[wave][0][0]);
+    auto gather_off = [&](int j, int s, uint32_t nb1) -> uint32_t {
+        const uint32_t p = (uint32_t) (64 * s + lane), key = p / 17u, part = p - key * 17u;
+        const int kk = (kg + j * KG) * DEC_TK + (int) key;
+        const uint32_t row = kk < span ? (uint32_t) cslot[wave][j & (QC_SLOTS - 1)][key < DEC_TK ? key : 0] : 0xffffffffu;
+        return row < (uint32_t) a.n_rows ? row * nb1 + part * 16u : 0x80000000u;
+    };
+    auto issue_rows = [&](int j, uint32_t stl, v4i r, uint32_t nb1, auto base_c) __attribute__((always_inline)) {
+        constexpr uint32_t B = decltype(base_c)::value;
+        uint32_t o[DEC_TDMA];
+#pragma unroll
+        for (int s = 0; s < DEC_TDMA; s++) o[s] = gather_off(j, s, nb1);
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the cells are read and this wave's reads of the stage are done
+        dma16_buf_at<B>(r, o[0], stl);
+        dma16_buf_at<B + 1024>(r, o[1], stl);
+        dma16_buf_at<B + 2048>(r, o[2], stl);
+        dma16_buf_at<B + 3072>(r, o[3], stl);
+        static_assert(DEC_TDMA == 5, "five DMAs per tensor");
+        if (lane < 16) dma16_buf_at<B + 4096>(r, o[4], stl);
+    };
+    auto issue_k = [&](int j, uint32_t stl) __attribute__((always_inline)) {
+        issue_rows(j, stl, rk, a.k_nb1, std::integral_constant<uint32_t, 0>{});
+    };
+    auto issue_v = [&](int j, uint32_t stl) __attribute__((always_inline)) {
+        issue_rows(j, stl, rv, a.v_nb1, std::integral_constant<uint32_t, DEC_KB>{});
+    };
+    // the 16 cells of the wave's tile j into slot j % 4 (lanes 0-3, 16 bytes each)
+    auto issue_cells = [&](int j) __attribute__((always_inline)) {
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // this wave's reads of the slot are done
+        if (lane < 4)
+            dma16_buf(rc, (uint32_t) (((kg + j * KG) * DEC_TK + 4 * lane) * 4),
+                      csl + (uint32_t) ((j & (QC_SLOTS - 1)) * DEC_TK * 4));
+    };
+
+    // ---- prologue: the block's query rows (one wave DMA per row) into stage 1
+    //      and the cells of the wave's first four tiles; then tile 0 ----
+    uint8_t * qstage = &ring[1][0][0];
+    {
+        const v4i rq = make_rsrc(a.q, a.q_bytes);
+#pragma unroll
+        for (int jr = 0; jr < QR / QC_WAVES; jr++) {
+            const int rl = wave + QC_WAVES * jr, U = rl / 16, r = rl % 16;
+            const int tU = t0 + U < a.T ? t0 + U : a.T - 1;
+            if (r < a.gqa)
+                dma16_buf(rq, (uint32_t) tU * a.q_nb1 + (uint32_t) (kvh * a.gqa + r) * a.q_nb2 + 16u * (uint32_t) lane,
+                          __builtin_amdgcn_readfirstlane(lds_addr(qstage + rl * DEC_QROW)));
+        }
+        // own tiles 0..3: lane l takes piece l % 4 of tile l / 4
+        if (lane < 16)
+            dma16_buf(rc, (uint32_t) (((kg + (lane >> 2) * KG) * DEC_TK + 4 * (lane & 3)) * 4), csl);
+    }
+    wait_vmcnt<0>();
+    issue_k(0, stl0);
+    issue_v(0, stl0);
+
+    // ---- requantisation of the query rows (ggml's quantiser): wave w takes
+    //      q8_0 block w of every row, QL lanes per row ----
+    constexpr int QL = 64 / QR, QV = 32 / QL;
+    static_assert(NBLK == QC_WAVES, "one block of all rows per wave");
+    static_assert(QR * QL == 64, "QL lanes per row");
+    const int qrow = lane / QL, qh = lane % QL;
+    const bool qv = (qrow % 16) < a.gqa;               // rows past the head group stay zero
+    float qx[QV];
+    {
+        const float4 * src = (const float4 *) (qstage + qrow * DEC_QROW + (QK * wave + QV * qh) * 4);
+#pragma unroll
+        for (int m = 0; m < QV / 4; m++) {
+            const float4 v = qv ? src[m] : make_float4(0.f, 0.f, 0.f, 0.f);
+            qx[4 * m] = v.x; qx[4 * m + 1] = v.y; qx[4 * m + 2] = v.z; qx[4 * m + 3] = v.w;
+        }
+    }
+    __syncthreads();   // every query value is in registers: stage 1 becomes the window image
+    uint8_t * qwin = qstage;
+    auto qslice = [&](int bb, int sl, int row) { return qwin + ((bb * 4 + sl) * QR + row) * 16; };
+    float * dql = (float *) (qstage + NBLK * QWIN * QR);          // [QR][NBLK]
+    {
+#pragma unroll
+        for (int z = 0; z < 4 / QL; z++) *(uint4 *) qslice(wave, qh * (4 / QL) + z, qrow) = make_uint4(0, 0, 0, 0);
+        wave_lds_sync();
+        uint32_t w[QV / 4];
+        uint16_t d16;
+        float dqv = 0.f;
+        if (a.x86) dev::q8_quantize_lanes<QV>(qx, true, w, &d16, &dqv);
+        else       dev::q8_quantize_lanes<QV>(qx, false, w, &d16, &dqv);
+        if (qv) {
+            const int woff = (int) ((0x200E0C0A08061402ull >> (8 * wave)) & 0xff);   // win_off(wave)
+#pragma unroll
+            for (int m = 0; m < QV / 2; m++) {   // 2-byte pieces never straddle a slice
+                const int o = woff + QV * qh + 2 * m;
+                *(uint16_t *) (qslice(wave, o >> 4, qrow) + (o & 15)) = (uint16_t) (w[m >> 1] >> (16 * (m & 1)));
+            }
+        }
+        if (qh == 0) dql[qrow * NBLK + wave] = qv ? dqv * a.scale_log2 : 0.f;
+    }
+    static_assert(win_off(0) == 2 && win_off(1) == 20 && win_off(2) == 6 && win_off(3) == 8 && win_off(4) == 10 &&
+                  win_off(5) == 12 && win_off(6) == 14 && win_off(7) == 32, "the packed window offsets");
+    __syncthreads();
+    const int rl_lane = unit * 16 + ln;
+    v4i qw[NBLK];
+    float dq[NBLK];
+#pragma unroll
+    for (int bb = 0; bb < NBLK; bb++) {
+        qw[bb] = *(const v4i *) qslice(bb, lg, rl_lane);
+        dq[bb] = dql[rl_lane * NBLK + bb];
+    }
+#pragma unroll
+    for (int bb = 0; bb < NBLK; bb++) asm volatile("" : "+v"(qw[bb]), "+v"(dq[bb]));
+    __syncthreads();   // every wave has its operands: stage 1 is free
+    // the order of a steady step (tile 0's V rows, then tile 2's cells, tile
+    // 1's K and V, tile 3's cells): tiles 2 and 3's cells are already in
+    // their slots and arrive again, unchanged
+    issue_cells(2);
+    issue_k(1, stl1);
+    issue_v(1, stl1);
+    issue_cells(3);
+
+    // ---- the key loop ----
+    v4f O[NBLK][2];
+    float m_run = -INFINITY, l_run = 0.f;
+#pragma unroll
+    for (int bb = 0; bb < NBLK; bb++) { O[bb][0] = v4f{0, 0, 0, 0}; O[bb][1] = v4f{0, 0, 0, 0}; }
+    uint16_t (*sw)[NBLK][DEC_TK] = scl[wave];
+
+    // the wave's tile j from stage st; then tile j + 2 into the same stage
+    // (its K rows once the QK is done, its V rows after the PV) and tile j +
+    // 4's cells into tile j's slot
+    auto tile_step = [&](int j, uint8_t * st, uint32_t stl) __attribute__((always_inline)) {
+        const int kin = (kg + j * KG) * DEC_TK + lg * 4;   // the lane's first key, within the list
+        {
+            const uint8_t * src = st + (lane >> 3) * SEG + (lane & 7) * QBLOCK;
+            uint16_t * dstw = &sw[0][lane & 7][lane >> 3];
+            uint16_t sv[4];
+#pragma unroll
+            for (int nn = 0; nn < 4; nn++) sv[nn] = *(const uint16_t *) (src + (nn >> 1) * DEC_KB + (nn & 1) * 8 * SEG);
+#pragma unroll
+            for (int nn = 0; nn < 4; nn++) dstw[(nn >> 1) * NBLK * DEC_TK + (nn & 1) * 8] = sv[nn];
+        }
+        wave_lds_sync();
+        float s[4] = {0.f, 0.f, 0.f, 0.f};
+        {
+            v4i kA[NBLK];
+            uint2 dk[NBLK];
+            const uint8_t * krow = st + ln * SEG + 16 * lg;
+#pragma unroll
+            for (int bb = 0; bb < NBLK; bb++) {
+                kA[bb] = *(const v4i *) (krow + 16 * win_piece(bb));
+                dk[bb] = *(const uint2 *) &sw[0][bb][lg * 4];
+            }
+            v4i cc[NBLK];
+            cc[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kA[0], qw[0], v4i{0, 0, 0, 0}, 0, 0, 0);
+            cc[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kA[1], qw[1], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int bb = 0; bb < NBLK; bb++) {
+                if (bb + 2 < NBLK)
+                    cc[bb + 2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kA[bb + 2], qw[bb + 2], v4i{0, 0, 0, 0}, 0, 0, 0);
+                const float d = dq[bb];
+                s[0] = __builtin_fmaf((float) cc[bb][0], mul_f16lo(d, dk[bb].x), s[0]);
+                s[1] = __builtin_fmaf((float) cc[bb][1], mul_f16hi(d, dk[bb].x), s[1]);
+                s[2] = __builtin_fmaf((float) cc[bb][2], mul_f16lo(d, dk[bb].y), s[2]);
+                s[3] = __builtin_fmaf((float) cc[bb][3], mul_f16hi(d, dk[bb].y), s[3]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        wait_vmcnt<QC_AHEAD - 1>();   // tile j + 2's cells have landed
+        issue_k(j + 2, stl);
+        float p[4];
+        uint32_t p16[2];
+        {
+            // a cell is seen by the queries at or after its position; keys
+            // past the list and cells outside the cache are masked (and the
+            // latter flagged)
+            const int4 c = *(const int4 *) &cslot[wave][j & (QC_SLOTS - 1)][lg * 4];
+            const int cv[4] = {c.x, c.y, c.z, c.w};
+            float x[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const bool in = kin + i < span;
+                const bool row_ok = (uint32_t) cv[i] < (uint32_t) a.n_rows;
+                bad |= in && !row_ok;
+                x[i] = in && row_ok && (int64_t) cv[i] <= q_pos ? s[i] : -INFINITY;
+            }
+            float mloc = vmax(vmax(x[0], x[1]), vmax(x[2], x[3]));
+            mloc = xmax_lanes16_32(mloc);
+            const bool grow = mloc > m_run + RESCALE_SLACK;
+            float alpha = 1.f;
+            if (grow) {
+                alpha = __builtin_amdgcn_exp2f(m_run - mloc);
+                m_run = mloc;
+            }
+            const float m_use = m_run == -INFINITY ? 0.f : m_run;
+            float lsum = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                p[i] = __builtin_amdgcn_exp2f(x[i] - m_use);
+                lsum += p[i];
+            }
+            l_run = l_run * alpha + lsum;
+            p16[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p[0], p[1]));
+            p16[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p[2], p[3]));
+            if (__any(grow)) {
+                asm volatile("" ::: "memory");
+#pragma unroll
+                for (int bb = 0; bb < NBLK; bb++) { O[bb][0] *= alpha; O[bb][1] *= alpha; }
+            }
+        }
+        const uint8_t * vrow = st + DEC_KB + (lg * 4) * SEG + 2 + 2 * ln;
+        uint32_t w[NBLK][4];
+        uint2 dv2[NBLK];
+#pragma unroll
+        for (int bb = 0; bb < NBLK; bb++) {
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) w[bb][jj] = *(const uint16_t *) (vrow + jj * SEG + bb * QBLOCK);
+            dv2[bb] = *(const uint2 *) &sw[1][bb][lg * 4];
+        }
+        uint32_t a0[2], a1[2], bh[2], bl[2];
+        {
+            const uint32_t dv[2] = {dv2[0].x, dv2[0].y};
+            cvt_v_block(w[0], a0, a1);
+            pdv_hilo(p, p16, dv, bh, bl);
+        }
+#pragma unroll
+        for (int bb = 0; bb < NBLK; bb++) {
+            const v4h A0 = __builtin_bit_cast(v4h, make_uint2(a0[0], a0[1]));
+            const v4h A1 = __builtin_bit_cast(v4h, make_uint2(a1[0], a1[1]));
+            const v4h Bh = __builtin_bit_cast(v4h, make_uint2(bh[0], bh[1]));
+            const v4h Bl = __builtin_bit_cast(v4h, make_uint2(bl[0], bl[1]));
+            O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x16f16(A0, Bh, O[bb][0], 0, 0, 0);
+            O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A1, Bh, O[bb][1], 0, 0, 0);
+            if (bb + 1 < NBLK) {
+                const uint32_t dv[2] = {dv2[bb + 1].x, dv2[bb + 1].y};
+                cvt_v_block(w[bb + 1], a0, a1);
+                pdv_hilo(p, p16, dv, bh, bl);
+            }
+            O[bb][0] = __builtin_amdgcn_mfma_f32_16x16x16f16(A0, Bl, O[bb][0], 0, 0, 0);
+            O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A1, Bl, O[bb][1], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        issue_v(j + 2, stl);
+        issue_cells(j + 4);
+    };
+    for (int j = 0; j < J; j += 2) {
+        wait_vmcnt<QC_AHEAD>();
+        tile_step(j, &ring[0][wave][0], stl0);
+        if (j + 1 < J) {
+            wait_vmcnt<QC_AHEAD>();
+            tile_step(j + 1, &ring[1][wave][0], stl1);
+        }
+    }
+    wait_vmcnt<0>();   // every DMA of the wave has landed (those past the list included)
+
+    // ---- merge the KG waves of each unit ----
+    {
+        const float l = sum_lanes16_32(l_run);
+        float2 * mlw = (float2 *) &scl[wave][0][0][0];   // the wave's own scale table, done with
+        if (lg == 0) mlw[ln] = make_float2(m_run, l);
+    }
+    if (__any(bad) && lane == 0 && a.status) atomicOr(a.status, DEVERR_GET_ROWS_INDEX);
+    __syncthreads();   // every wave is done with its ring stages, and its (max, sum) are out
+    float M = -INFINITY, L = 0.f;
+#pragma unroll
+    for (int k2 = 0; k2 < KG; k2++) M = xmax(M, ((const float2 *) &scl[unit * KG + k2][0][0][0])[ln].x);
+#pragma unroll
+    for (int k2 = 0; k2 < KG; k2++) {
+        const float2 e = ((const float2 *) &scl[unit * KG + k2][0][0][0])[ln];
+        L += e.x == -INFINITY ? 0.f : e.y * exp2f(e.x - M);
+    }
+    const float fw = m_run == -INFINITY ? 0.f : exp2f(m_run - M);
+    int tid_e = (int) threadIdx.x;
+    asm volatile("" : "+v"(tid_e));
+    const int ln_e = tid_e & 15, lg_e = (tid_e >> 4) & 3;
+    float * ob = (float *) &ring[0][0][0];
+    const int orow = ln_e * DEC_OBS + 8 * lg_e;
+    float4 acc[NBLK][2];
+#pragma unroll
+    for (int bb = 0; bb < NBLK; bb++) {
+        const v4f o0 = O[bb][0] * fw, o1 = O[bb][1] * fw;
+        acc[bb][0] = make_float4(o0[0], o1[0], o0[1], o1[1]);
+        acc[bb][1] = make_float4(o0[2], o1[2], o0[3], o1[3]);
+    }
+    if (KG > 1 && kg != 0) {
+        float * d = ob + (unit * (KG - 1) + kg - 1) * 16 * DEC_OBS + orow;
+#pragma unroll
+        for (int bb = 0; bb < NBLK; bb++) {
+            *(float4 *) (d + 32 * bb) = acc[bb][0];
+            *(float4 *) (d + 32 * bb + 4) = acc[bb][1];
+        }
+    }
+    __syncthreads();
+    if (kg == 0 && live && ln_e < a.gqa) {
+#pragma unroll 1
+        for (int k2 = 0; k2 < KG - 1; k2++) {
+#pragma unroll
+            for (int bb = 0; bb < NBLK; bb++) {
+                const float * src = ob + (unit * (KG - 1) + k2) * 16 * DEC_OBS + orow + 32 * bb;
+                const float4 x0 = *(const float4 *) src, x1 = *(const float4 *) (src + 4);
+                acc[bb][0].x += x0.x; acc[bb][0].y += x0.y; acc[bb][0].z += x0.z; acc[bb][0].w += x0.w;
+                acc[bb][1].x += x1.x; acc[bb][1].y += x1.y; acc[bb][1].z += x1.z; acc[bb][1].w += x1.w;
+            }
+        }
+        const int h = kvh * a.gqa + ln_e;
+        const size_t o = ((size_t) t * (size_t) a.nh + (size_t) h) * D + 8 * lg_e;
+        float * out = a.dst + o;
+        const float oscale = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+        for (int bb = 0; bb < NBLK; bb++) {
+            const float4 p0 = acc[bb][0], p1 = acc[bb][1];
+            float4 w0 = make_float4(p0.x * oscale, p0.y * oscale, p0.z * oscale, p0.w * oscale);
+            float4 w1 = make_float4(p1.x * oscale, p1.y * oscale, p1.z * oscale, p1.w * oscale);
+            if (a.gate) {
+                const float4 g0 = *(const float4 *) (a.gate + o + 32 * bb), g1 = *(const float4 *) (a.gate + o + 32 * bb + 4);
+                w0.x = __fmul_rn(w0.x, 1.0f / (1.0f + expf(-g0.x)));
+                w0.y = __fmul_rn(w0.y, 1.0f / (1.0f + expf(-g0.y)));
+                w0.z = __fmul_rn(w0.z, 1.0f / (1.0f + expf(-g0.z)));
+                w0.w = __fmul_rn(w0.w, 1.0f / (1.0f + expf(-g0.w)));
+                w1.x = __fmul_rn(w1.x, 1.0f / (1.0f + expf(-g1.x)));
+                w1.y = __fmul_rn(w1.y, 1.0f / (1.0f + expf(-g1.y)));
+                w1.z = __fmul_rn(w1.z, 1.0f / (1.0f + expf(-g1.z)));
+                w1.w = __fmul_rn(w1.w, 1.0f / (1.0f + expf(-g1.w)));
+            }
+            *(float4 *) (out + 32 * bb) = w0;
+            *(float4 *) (out + 32 * bb + 4) = w1;
+        }
+    }
+}
+
 // ================================================================ decode / verify in 32-key steps
 //
 // k_fa_vd<NF, PK, MASKED, RG, GATHER>: at most 24 query rows per KV head
@@ -4267,6 +4682,7 @@ int check_no_scratch() {
                                (const void *) k_fa_vs<1, 1, false, true, false>, (const void *) k_fa_vs<1, 1, true, true, false>,
                                (const void *) k_fa_vs<1, 1, false, false, true>,
                                (const void *) k_fa_pre<false>, (const void *) k_fa_pre<true>,
+                               (const void *) k_fa_qc<2>, (const void *) k_fa_qc<4>, (const void *) k_fa_qc<8>,
                                (const void *) k_fattn_q8_0<2, true, WAVES, 16, false>,
                                (const void *) k_fattn_q8_0<1, false, WAVES_PAIR, 16, false>,
                                (const void *) k_fattn_q8_0<1, true, WAVES_PAIR, 16, false>,
@@ -5066,6 +5482,75 @@ extern "C" int qwfn_flash_attn_ext_q8_0_query_cells(const qwfn_tensor * q, const
             return rc;
         return fattn_run(&qq, &kk, &vv, nullptr, scale, 0.0f, 0.0f, &dd, variant, ws, ws_bytes, stream, nullptr, nullptr,
                          WS_CALLER, &g, gate ? &gg : nullptr);
+    });
+}
+
+extern "C" int qwfn_flash_attn_ext_q8_0_query_cells_dev(const qwfn_tensor * q, const qwfn_tensor * k,
+                                                        const qwfn_tensor * v, const int32_t * cells,
+                                                        const int32_t * counts, int64_t cell_stride, int64_t pos0,
+                                                        float scale, const qwfn_tensor * gate, const qwfn_tensor * dst,
+                                                        int variant, void * stream) {
+    return ::qwfn::abi_call("flash_attn_ext_q8_0_query_cells_dev", [&]() -> int {
+        const char * fn = "flash_attn_ext_query_cells_dev: ";
+        auto fail = [&](int code, const char * what) { return set_error(code, std::string(fn) + what); };
+        if (!q || !k || !v || !cells || !counts || !dst) return fail(QWFN_EINVAL, "NULL argument");
+        if (q->type != QWFN_TYPE_F32 || q->ne[0] != D || q->nb[0] != 4) return fail(QWFN_EINVAL, "q must be F32 [256, T, n_head, 1]");
+        if (k->type != QWFN_TYPE_Q8_0 || v->type != QWFN_TYPE_Q8_0) return fail(QWFN_ENOTSUP, "k and v must be q8_0");
+        if (k->ne[0] != D || v->ne[0] != D || k->nb[0] != QBLOCK || v->nb[0] != QBLOCK)
+            return fail(QWFN_ENOTSUP, "k and v rows must be 256 q8_0 values");
+        if (q->ne[3] != 1 || k->ne[3] != 1 || v->ne[3] != 1) return fail(QWFN_ENOTSUP, "one sequence (ne[3] = 1)");
+        if (k->ne[1] != v->ne[1] || k->ne[2] != v->ne[2]) return fail(QWFN_EINVAL, "k and v must have the same rows and KV heads");
+        const int64_t T = q->ne[1], nh = q->ne[2], nh_kv = k->ne[2], n_rows = k->ne[1];
+        if (T < 1 || nh < 1 || nh_kv < 1 || n_rows < 1) return fail(QWFN_EINVAL, "empty q or cache");
+        if (nh % nh_kv || nh / nh_kv > 16) return fail(QWFN_ENOTSUP, "n_head must be a multiple of n_head_kv, at most 16 times it");
+        if (T > INT32_MAX / 2) return fail(QWFN_ENOTSUP, "too many positions");
+        if (!is_aligned(q->data, 16) || q->nb[1] % 16 || q->nb[2] % 16)
+            return fail(QWFN_EALIGN, "q data and strides must be 16-byte aligned");
+        const uint64_t q_bytes = (uint64_t) (T - 1) * q->nb[1] + (uint64_t) (nh - 1) * q->nb[2] + (uint64_t) D * 4;
+        if (q_bytes >= (uint64_t(1) << 32)) return fail(QWFN_ENOTSUP, "q must span below 4 GiB");
+        if (!is_aligned(k->data, 16) || !is_aligned(v->data, 16) || k->nb[1] % 16 || v->nb[1] % 16 || k->nb[2] % 16 ||
+            v->nb[2] % 16)
+            return fail(QWFN_EALIGN, "k/v data and strides must be 16-byte aligned");
+        if ((uint64_t) (nh_kv - 1) * k->nb[2] + SEG > k->nb[1] || (uint64_t) (nh_kv - 1) * v->nb[2] + SEG > v->nb[1])
+            return fail(QWFN_EINVAL, "the KV heads must lie within a cache row");
+        if ((uint64_t) n_rows * std::max(k->nb[1], v->nb[1]) >= (uint64_t(1) << 31))
+            return fail(QWFN_ENOTSUP, "the cache must be below 2 GiB (rows * row stride)");
+        if (!is_aligned(cells, 16) || cell_stride < 4 || cell_stride % 4 || cell_stride > (int64_t(1) << 28))
+            return fail(QWFN_EALIGN, "cells must be 16-byte aligned rows of cell_stride int32, a positive multiple of 4");
+        if (!is_aligned(counts, 4)) return fail(QWFN_EALIGN, "counts must be int32");
+        if (pos0 < 0) return fail(QWFN_EINVAL, "negative pos0");
+        if (dst->type != QWFN_TYPE_F32 || dst->ne[0] != D || dst->ne[1] != nh || dst->ne[2] != T || dst->ne[3] != 1 ||
+            dst->nb[0] != 4 || dst->nb[1] != (size_t) D * 4 || dst->nb[2] != dst->nb[1] * (size_t) nh || !is_aligned(dst->data, 16))
+            return fail(QWFN_EINVAL, "dst must be contiguous 16-byte aligned F32 [256, n_head, T, 1]");
+        if (gate && (gate->type != QWFN_TYPE_F32 || gate->ne[0] != D || gate->ne[1] != nh || gate->ne[2] != T ||
+                     gate->nb[0] != 4 || gate->nb[1] != dst->nb[1] || gate->nb[2] != dst->nb[2] || !is_aligned(gate->data, 16)))
+            return fail(QWFN_EINVAL, "gate must have dst's shape and strides, 16-byte aligned");
+        if (int rc = check_no_scratch()) return rc;
+        qc_args a{};
+        a.q = (const char *) q->data; a.q_nb1 = (uint32_t) q->nb[1]; a.q_nb2 = (uint32_t) q->nb[2];
+        a.q_bytes = (uint32_t) q_bytes;
+        a.k = (const char *) k->data; a.v = (const char *) v->data;
+        a.k_nb1 = (uint32_t) k->nb[1]; a.v_nb1 = (uint32_t) v->nb[1];
+        a.k_nb2 = (uint32_t) k->nb[2]; a.v_nb2 = (uint32_t) v->nb[2];
+        a.k_bytes = (uint32_t) ((uint64_t) n_rows * k->nb[1]); a.v_bytes = (uint32_t) ((uint64_t) n_rows * v->nb[1]);
+        a.n_rows = n_rows;
+        a.cells = cells; a.cell_stride = cell_stride; a.counts = counts; a.pos0 = pos0;
+        a.T = (int32_t) T; a.nh = (int32_t) nh; a.nh_kv = (int32_t) nh_kv; a.gqa = (int32_t) (nh / nh_kv);
+        a.scale_log2 = scale * LOG2E;
+        a.x86 = variant == QWFN_Q8_X86;
+        a.dst = (float *) dst->data;
+        a.gate = gate ? (const float *) gate->data : nullptr;
+        if (int rc = status_word(&a.status)) return rc;
+        // waves per list: the (position, KV head) lists over about 256 blocks
+        // of 8 waves (one a CU), at least 2 waves a list
+        const int64_t lists = T * nh_kv;
+        const int kg = lists >= 1024 ? 2 : lists >= 512 ? 4 : 8;
+        const int64_t upb = QC_WAVES / kg;
+        const int64_t blocks = (T + upb - 1) / upb * nh_kv;
+        if (blocks > INT32_MAX) return fail(QWFN_ENOTSUP, "too many positions");
+        auto kern = kg == 2 ? k_fa_qc<2> : kg == 4 ? k_fa_qc<4> : k_fa_qc<8>;
+        hipLaunchKernelGGL(kern, dim3((unsigned) blocks), dim3(QC_WAVES * 64), 0, as_stream(stream), a);
+        return hip_check(hipGetLastError(), "flash_attn_ext_query_cells_dev launch");
     });
 }
 

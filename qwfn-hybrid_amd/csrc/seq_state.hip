@@ -345,6 +345,65 @@ __global__ __launch_bounds__(FILL_THREADS) void k_qsa_mask(const int32_t * cells
     }
 }
 
+// ---- the keys each query of a QSA-on prefill chunk sees: the zeros of the
+//      selection mask (graph_builder::qsa_mask, qwfn_graph.cpp:388-414) over
+//      the chunk's causal mask (0 up to the query's position, -inf after,
+//      qwfn_engine.cpp:1261-1270), as a list: the distinct cells query t
+//      selected at or before its position n_past + t, ascending. Block =
+//      query row t: its cells become a bitmap in LDS; thread i counts the set
+//      bits of its run of words, the counts are scanned across the block, and
+//      each thread writes its cells from its offset on. ----
+__global__ __launch_bounds__(FILL_THREADS) void k_qsa_visible(const int32_t * cells, int64_t width, int64_t cells_ld,
+                                                             int64_t n_kv, int64_t n_past, int32_t * lists,
+                                                             int64_t lists_ld, int32_t * counts, uint32_t * status) {
+    extern __shared__ uint32_t vis[];   // ceil(n_vis / 32) words
+    __shared__ uint32_t wsum[FILL_THREADS / 64];
+    const int64_t t = blockIdx.x;
+    const int64_t n_vis = n_past + t + 1 < n_kv ? n_past + t + 1 : n_kv;   // keys at or before the position
+    const int64_t n_words = (n_vis + 31) / 32;
+    for (int64_t w = threadIdx.x; w < n_words; w += FILL_THREADS) vis[w] = 0u;
+    __syncthreads();
+    const int32_t * crow = cells + (size_t) t * (size_t) cells_ld;
+    bool bad = false;
+    for (int64_t j = threadIdx.x; j < width; j += FILL_THREADS) {
+        const int64_t c = crow[j];
+        if (c < 0 || c >= n_kv) { bad = true; continue; }
+        if (c < n_vis) atomicOr(&vis[c >> 5], 1u << (c & 31));
+    }
+    if (__any(bad) && (threadIdx.x & 63) == 0 && status) atomicOr(status, DEVERR_SET_ROWS_INDEX);
+    __syncthreads();
+    const int64_t per = (n_words + FILL_THREADS - 1) / FILL_THREADS;
+    const int64_t w0 = (int64_t) threadIdx.x * per, w1 = w0 + per < n_words ? w0 + per : n_words;
+    uint32_t cnt = 0;
+    for (int64_t w = w0; w < w1; w++) cnt += (uint32_t) __popc(vis[w]);
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    uint32_t inc = cnt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = __shfl_up(inc, o);
+        if (lane >= o) inc += y;
+    }
+    if (lane == 63) wsum[wv] = inc;
+    __syncthreads();
+    uint32_t base = 0, total = 0;
+#pragma unroll
+    for (int k = 0; k < FILL_THREADS / 64; k++) {
+        if (k < wv) base += wsum[k];
+        total += wsum[k];
+    }
+    int32_t * orow = lists + (size_t) t * (size_t) lists_ld;
+    uint32_t off = base + inc - cnt;
+    for (int64_t w = w0; w < w1; w++) {
+        uint32_t bits = vis[w];
+        while (bits) {
+            const int b = __ffs((int) bits) - 1;
+            orow[off++] = (int32_t) (w * 32 + b);
+            bits &= bits - 1u;
+        }
+    }
+    if (threadIdx.x == 0) counts[t] = (int32_t) total;
+}
+
 unsigned grid_for(int64_t n) {
     return (unsigned) std::max<int64_t>(1, std::min<int64_t>((n + FILL_THREADS - 1) / FILL_THREADS, 4096));
 }
@@ -866,6 +925,33 @@ int qwfn_qsa_mask_f16(const int32_t * cells, int64_t width, size_t cells_nb1, co
                            (int64_t) (cells_nb1 / 4), causal, (int64_t) (causal_nb1 / 2), n_kv, mask,
                            (int64_t) (mask_nb1 / 2), status);
         return hip_check(hipGetLastError(), "qsa_mask launch");
+    });
+}
+
+int qwfn_qsa_visible_cells(const int32_t * cells, int64_t width, size_t cells_nb1, int64_t n_kv, int64_t T,
+                           int64_t n_past, int32_t * lists, size_t lists_nb1, int32_t * counts, void * stream) {
+    return ::qwfn::abi_call("qsa_visible_cells", [&]() -> int {
+        if (!cells || !lists || !counts) return set_error(QWFN_EINVAL, "qsa_visible_cells: NULL pointer");
+        if (width < 0 || n_kv < 1 || T < 1 || n_past < 0)
+            return set_error(QWFN_EINVAL, "qsa_visible_cells: need width >= 0, n_kv >= 1, T >= 1, n_past >= 0");
+        if (cells_nb1 % 4 || cells_nb1 < (size_t) width * 4 || lists_nb1 % 4 || lists_nb1 < (size_t) width * 4)
+            return set_error(QWFN_EINVAL, "qsa_visible_cells: rows of cells and lists must hold width int32");
+        if (!is_aligned(cells, 4) || !is_aligned(lists, 4) || !is_aligned(counts, 4))
+            return set_error(QWFN_EALIGN, "qsa_visible_cells: misaligned pointer");
+        if (T > 0x7fffffff || n_kv > 0x7fffffff) return set_error(QWFN_ENOTSUP, "qsa_visible_cells: too many rows or keys");
+        const size_t lds = (size_t) ((n_kv + 31) / 32) * 4;
+        if (lds > 64 * 1024) return set_error(QWFN_ENOTSUP, "qsa_visible_cells: n_kv beyond 524288 keys");
+        // the lists (T whole rows) and counts must not overlap the cells they read
+        const char * c0 = (const char *) cells, * c1 = c0 + (size_t) (T - 1) * cells_nb1 + (size_t) width * 4;
+        const char * l0 = (const char *) lists, * l1 = l0 + (size_t) (T - 1) * lists_nb1 + (size_t) width * 4;
+        const char * n0 = (const char *) counts, * n1 = n0 + (size_t) T * 4;
+        if ((width > 0 && l0 < c1 && c0 < l1) || (n0 < c1 && c0 < n1) || (width > 0 && n0 < l1 && l0 < n1))
+            return set_error(QWFN_EINVAL, "qsa_visible_cells: cells, lists and counts must not overlap");
+        uint32_t * status = nullptr;
+        if (int rc = status_word(&status)) return rc;
+        hipLaunchKernelGGL(k_qsa_visible, dim3((unsigned) T), dim3(FILL_THREADS), lds, as_stream(stream), cells, width,
+                           (int64_t) (cells_nb1 / 4), n_kv, n_past, lists, (int64_t) (lists_nb1 / 4), counts, status);
+        return hip_check(hipGetLastError(), "qsa_visible_cells launch");
     });
 }
 

@@ -140,6 +140,7 @@ EXPORTS = [
     "qwfn_fattn_workspace_size_seq", "qwfn_flash_attn_ext_q8_0_seq", "qwfn_state_restore",
     "qwfn_fattn_workspace_size_cells", "qwfn_flash_attn_ext_q8_0_cells", "qwfn_kv_produce_q8_0",
     "qwfn_fattn_workspace_size_query_cells", "qwfn_flash_attn_ext_q8_0_query_cells",
+    "qwfn_flash_attn_ext_q8_0_query_cells_dev", "qwfn_qsa_visible_cells",
     "qwfn_flash_attn_ext_q8_0_gated",
     # include/qwfn_state.h
     "qwfn_state_config_default", "qwfn_state_create", "qwfn_state_destroy", "qwfn_state_tensor",
@@ -208,6 +209,9 @@ def load(path: str = LIB_PATH):
     L.qwfn_flash_attn_ext_q8_0_cells.argtypes = [T, T, T, vp, PL, i64, i64, ctypes.c_float, T, ctypes.c_int, vp, sz, vp]
     L.qwfn_fattn_workspace_size_query_cells.argtypes = [T, T, T, PL, i64]
     L.qwfn_fattn_workspace_size_query_cells.restype = sz
+    L.qwfn_flash_attn_ext_q8_0_query_cells_dev.argtypes = [T, T, T, vp, vp, i64, i64, ctypes.c_float, T, T, ctypes.c_int,
+                                                          vp]
+    L.qwfn_qsa_visible_cells.argtypes = [vp, i64, sz, i64, i64, i64, vp, sz, vp, vp]
     L.qwfn_flash_attn_ext_q8_0_query_cells.argtypes = [T, T, T, vp, PL, i64, i64, ctypes.c_float, T, T, ctypes.c_int,
                                                        vp, sz, vp]
     L.qwfn_kv_produce_q8_0.argtypes = [T, T, T, vp, vp, ctypes.POINTER(RopeCfg), T, T, i64, ctypes.c_int, vp]
@@ -496,6 +500,24 @@ def flash_attn_ext_query_cells(qv: Tensor, kv: Tensor, vv: Tensor, cells, n_cell
     return check(L.qwfn_flash_attn_ext_q8_0_query_cells(
         ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), cells.data_ptr(), n, stride, pos0, scale,
         ctypes.byref(gv) if gv is not None else None, ctypes.byref(ov), variant, ws_ptr, ws_bytes, _stream(stream)))
+
+
+def flash_attn_ext_query_cells_dev(qv: Tensor, kv: Tensor, vv: Tensor, cells, counts, pos0: int, scale: float,
+                                   ov: Tensor, gate=None, variant: int = Q8_X86, stream=None):
+    """Attention of query position t over the cache rows cells[t, :counts[t]] (cells: device
+    int32 [T, stride] with contiguous rows, stride a multiple of 4; counts: device int32
+    [T]), the rows at most pos0 + t; times sigmoid(gate) when gate (a torch f32 tensor laid
+    out as the output) is given. No workspace."""
+    L = load()
+    gv = out_view(gate) if gate is not None else None
+    for name, x in (("cells", cells), ("counts", counts)):
+        if str(x.dtype) != "torch.int32" or not x.is_cuda:
+            raise ValueError(f"{name} must be a device int32 tensor")
+    if cells.dim() != 2 or cells.stride(1) != 1 or counts.dim() != 1 or not counts.is_contiguous():
+        raise ValueError("cells must be [T, stride] with contiguous rows and counts a contiguous [T]")
+    return check(L.qwfn_flash_attn_ext_q8_0_query_cells_dev(
+        ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), cells.data_ptr(), counts.data_ptr(), cells.stride(0),
+        pos0, scale, ctypes.byref(gv) if gv is not None else None, ctypes.byref(ov), variant, _stream(stream)))
 
 
 def fattn_workspace_size_query_cells(qv: Tensor, kv: Tensor, vv: Tensor, n_cells, cell_stride: int) -> int:

@@ -260,6 +260,25 @@ def qsa_mask_f16(cells, causal, n_kv: int, mask, stream=None):
                                        K._stream(stream)))
 
 
+def qsa_visible_cells(cells, n_kv: int, n_past: int, lists, counts, stream=None):
+    """The keys each query of a QSA-on prefill chunk sees: row t of lists (i32 [T, >= width],
+    contiguous rows) gets the distinct cells of cells row t (i32 [T, width]) at most n_past
+    + t, ascending, and counts[t] (i32 [T]) their number."""
+    import torch
+    _dev_check("qsa_visible_cells", cells=cells, lists=lists, counts=counts)
+    for name, t in (("cells", cells), ("lists", lists)):
+        if t.dtype != torch.int32 or t.dim() != 2 or t.stride(1) != 1:
+            raise ValueError(f"qsa_visible_cells: {name} must be i32 [T, width] with contiguous rows")
+    T, width = cells.shape
+    if lists.shape[0] < T or lists.shape[1] < width:
+        raise ValueError("qsa_visible_cells: lists must be at least [T, width]")
+    if counts.dtype != torch.int32 or counts.dim() != 1 or counts.shape[0] < T or not counts.is_contiguous():
+        raise ValueError("qsa_visible_cells: counts must be a contiguous i32 [T]")
+    K.check(K.load().qwfn_qsa_visible_cells(cells.data_ptr(), width, cells.stride(0) * 4, n_kv, T, n_past,
+                                            lists.data_ptr(), lists.stride(0) * 4, counts.data_ptr(),
+                                            K._stream(stream)))
+
+
 # ------------------------------------------- decode-time sparse-attention inputs
 
 class QsaDecodeInputs:

@@ -287,3 +287,108 @@ def test_query_cells_edges(gpu, oracle):
                     for t in range(T)])
     assert not got[1].any()
     check(got, ref)
+
+
+def query_cells_dev_attn(K, q, kd, vd, n_rows, lists, pos0, gate=None, counts=None, stride=None):
+    """qwfn_flash_attn_ext_q8_0_query_cells_dev: list t for position t, the counts on the
+    device (default: the list lengths); returns (out, device flags)."""
+    T, nh, hd = q.shape
+    n = [len(x) for x in lists]
+    stride = stride or max(4, (max(n) + 3) // 4 * 4)
+    c = np.full((T, stride), -7, np.int32)
+    for t, x in enumerate(lists):
+        c[t, :len(x)] = x[:stride]
+    cnt = np.asarray(n if counts is None else counts, np.int32)
+    rb = kd.shape[1]
+    kv = K.tensor(kd.data_ptr(), K.TYPE_Q8_0, (hd, n_rows, 2, 1), (34, rb, hd // 32 * 34, n_rows * rb))
+    vv = K.tensor(vd.data_ptr(), K.TYPE_Q8_0, (hd, n_rows, 2, 1), (34, rb, hd // 32 * 34, n_rows * rb))
+    qd = dev(q[None].astype(np.float32))
+    out = torch.full((1, T, nh, hd), float("nan"), dtype=torch.float32, device="cuda")
+    K.flash_attn_ext_query_cells_dev(K.q_view(qd), kv, vv, dev(c), dev(cnt), pos0, 1 / 16, K.out_view(out),
+                                     gate=dev(gate[None]) if gate is not None else None)
+    flags = K.device_status()
+    return host(out)[0], flags
+
+
+def _oracle_per_position(q, kc, vc, lists, pos0):
+    return np.stack([KD.oracle_attn_cells(q[t:t + 1], kc, vc, [lists[t], lists[t]], pos0 + t, 1 / 16)[0]
+                     for t in range(q.shape[0])])
+
+
+@pytest.mark.parametrize("T,n_cells", [(37, 2052), (256, 516), (512, 260)])
+def test_query_cells_dev_many_positions(gpu, oracle, T, n_cells):
+    """Many positions, each over its own list in the reference's shape (blocks of 4, the
+    position's own block among them, cells past it masked), the counts on the device: 2, 4
+    and 8 waves a list (512, 256 and 37 positions over 2 KV heads)."""
+    K = gpu
+    n_rows, nh = 6000, 16
+    pos0 = n_rows - T - 3
+    lists = _query_lists(20 + T, n_rows, pos0, T, n_cells)
+    kc = KD.make_cache(KD.kv_rows(20 + T, 0, KD.K_KIND, n_rows, outliers=True), n_rows)
+    vc = KD.make_cache(KD.kv_rows(20 + T, 0, KD.V_KIND, n_rows, outliers=True), n_rows)
+    q = KD.q_rows(20 + T, 1, T, nh)[0]
+    kd, vd = dev(kc), dev(vc)
+    say(f"query cells (device counts) T={T} x {n_cells}")
+    got, flags = query_cells_dev_attn(K, q, kd, vd, n_rows, lists, pos0)
+    assert flags == 0
+    check(got, _oracle_per_position(q, kc, vc, lists, pos0))
+
+
+@pytest.mark.parametrize("nh", [8, 16, 32])
+def test_query_cells_dev_edges(gpu, oracle, nh):
+    """Head groups of 4, 8 and 16 rows; lists of different lengths (one empty: its query
+    gets 0; one whose length is not a multiple of 16), repeats, unsorted cells, cells past
+    the position, a cell outside the cache (masked, flagged), a count above the row stride
+    (clipped, flagged), and the gate."""
+    K = gpu
+    n_rows, T = 3000, 9
+    pos0 = 2500
+    rng = np.random.default_rng(30 + nh)
+    lists = [rng.choice(pos0, 700, replace=False).astype(np.int32),
+             np.array([], np.int32),
+             np.concatenate([rng.choice(n_rows, 37), [3, 3, 3]]).astype(np.int32),
+             np.concatenate([rng.choice(pos0, 300, replace=False), [n_rows + 5]]).astype(np.int32),
+             rng.choice(n_rows, 17).astype(np.int32),
+             np.arange(pos0, pos0 + 9, dtype=np.int32),
+             rng.choice(pos0, 1, replace=False).astype(np.int32),
+             rng.choice(pos0 + 8, 64, replace=False).astype(np.int32),
+             rng.choice(pos0, 650, replace=False).astype(np.int32)]
+    stride = 704
+    counts = [len(x) for x in lists]
+    counts[8] = stride + 40                                       # past the row: clipped to the stride
+    kc = KD.make_cache(KD.kv_rows(30 + nh, 0, KD.K_KIND, n_rows), n_rows)
+    vc = KD.make_cache(KD.kv_rows(30 + nh, 0, KD.V_KIND, n_rows), n_rows)
+    q = KD.q_rows(30 + nh, 1, T, nh)[0]
+    gate = (rng.standard_normal((T, nh, 256)) * 3).astype(np.float32)
+    kd, vd = dev(kc), dev(vc)
+    say(f"query cells (device counts) edges nh={nh}")
+    got, flags = query_cells_dev_attn(K, q, kd, vd, n_rows, lists, pos0, gate=gate, counts=counts, stride=stride)
+    assert flags & 2
+    ref_lists = [x[:stride] for x in lists]
+    ref = _oracle_per_position(q, kc, vc, ref_lists, pos0)
+    ref = ref * (1.0 / (1.0 + np.exp(-gate.astype(np.float64)))).astype(np.float32)
+    assert not got[1].any()
+    check(got, ref)
+    say("the same without the out-of-range cell and count: no flag")
+    lists[3] = lists[3][:-1]
+    counts = [min(len(x), stride) for x in lists]
+    got2, flags2 = query_cells_dev_attn(K, q, kd, vd, n_rows, lists, pos0, counts=counts, stride=stride)
+    assert flags2 == 0
+    check(got2, _oracle_per_position(q, kc, vc, [x[:stride] for x in lists], pos0))
+
+
+def test_query_cells_dev_agrees_with_query_cells(gpu, oracle):
+    """Three positions of the reference's verify shape: the device-count call and the
+    host-count call (k_fa_dec with key splits) agree to float rounding."""
+    K = gpu
+    n_rows, T, nh = 20000, 3, 16
+    pos0 = n_rows - 8
+    lists = _query_lists(41, n_rows, pos0, T, 2052)
+    kc = KD.make_cache(KD.kv_rows(41, 0, KD.K_KIND, n_rows, outliers=True), n_rows)
+    vc = KD.make_cache(KD.kv_rows(41, 0, KD.V_KIND, n_rows, outliers=True), n_rows)
+    q = KD.q_rows(41, 1, T, nh)[0]
+    kd, vd = dev(kc), dev(vc)
+    say("query cells: device counts against host counts")
+    a, _ = query_cells_dev_attn(K, q, kd, vd, n_rows, lists, pos0)
+    b, _ = query_cells_attn(K, q, kd, vd, n_rows, lists, pos0)
+    np.testing.assert_allclose(a, b, rtol=1e-5, atol=2e-6)

@@ -47,6 +47,38 @@ def test_chunk_inputs_match_oracle(gpu, n_past_c, Tc, ratio):
     assert (b[:, nb:] == 7.0).all()
 
 
+def test_visible_cells_match_oracle(gpu):
+    """The keys each query sees, as sorted lists: the distinct selected cells at or before
+    the query's position (the zeros of the selection mask over the causal mask), bit for
+    bit; a cell outside the keys is skipped and flagged."""
+    K = gpu
+    rng = np.random.default_rng(6)
+    for T, n_past, width in ((64, 5000, 300), (7, 0, 40), (33, 100000, 2052)):
+        n_kv = n_past + T
+        cells = rng.integers(0, n_kv, (T, width)).astype(np.int32)
+        cells[:, width // 2:width // 2 + 10] = cells[:, :10]     # repeats
+        lists = torch.full((T, width + 4), -7, dtype=torch.int32, device="cuda")
+        counts = torch.full((T,), -7, dtype=torch.int32, device="cuda")
+        say(f"visible cells T={T} n_past={n_past} width={width}")
+        S.qsa_visible_cells(dev(cells), n_kv, n_past, lists, counts)
+        assert K.device_status() == 0
+        g_l, g_n = host(lists), host(counts)
+        for t in range(T):
+            want = SO.visible_cells(cells[t], n_kv, n_past + t)
+            assert g_n[t] == len(want), f"row {t}"
+            np.testing.assert_array_equal(g_l[t, :len(want)], want)
+            assert (g_l[t, len(want):] == -7).all()
+    say("visible cells with a cell outside the keys")
+    cells[5, 7] = n_kv + 3
+    cells[6, 1] = -1
+    S.qsa_visible_cells(dev(cells), n_kv, n_past, lists, counts)
+    assert K.device_status() & 1
+    for t in (5, 6):
+        want = SO.visible_cells(cells[t][(cells[t] >= 0) & (cells[t] < n_kv)], n_kv, n_past + t)
+        np.testing.assert_array_equal(host(lists)[t, :len(want)], want)
+        assert host(counts)[t] == len(want)
+
+
 def test_qsa_mask_matches_oracle(gpu):
     K = gpu
     rng = np.random.default_rng(5)
@@ -161,3 +193,25 @@ def test_qsa_prefill_chunk_chain(gpu, oracle, n_past_c, Tc):
     print(f"  max abs {mx:.3e}  mean abs {mean:.3e}", flush=True)
     assert np.isfinite(g_out).all()
     assert mx <= 1e-4 and mean <= KD.MEAN_ABS_TOL
+
+    # ---- the same keys as lists: visible cells, then attention over them (no mask)
+    say("visible cells and attention over the lists")
+    lists = torch.full((Tc, cells.shape[1]), -7, dtype=torch.int32, device="cuda")
+    counts = torch.empty((Tc,), dtype=torch.int32, device="cuda")
+    S.qsa_visible_cells(cells, n_kv, n_past_c, lists, counts)
+    out2 = torch.full((1, Tc, nh, 256), float("nan"), dtype=torch.float32, device="cuda")
+    K.flash_attn_ext_query_cells_dev(K.q_view(qd), K.cache_attn_view(kd, n_kv, 2), K.cache_attn_view(vd, n_kv, 2),
+                                     lists, counts, n_past_c, 1 / 16, K.out_view(out2))
+    assert K.device_status() == 0
+    g_lists, g_counts = host(lists), host(counts)
+    for t in range(Tc):
+        want = np.flatnonzero(g_mask[t, :n_kv] == SO.F16_ZERO).astype(np.int32)
+        assert g_counts[t] == len(want), f"query {t}"
+        np.testing.assert_array_equal(g_lists[t, :len(want)], want)
+    g_out2 = host(out2)[0]
+    mx, mean = KD.err_stats(g_out2, ref)
+    print(f"  lists: max abs {mx:.3e}  mean abs {mean:.3e}", flush=True)
+    assert np.isfinite(g_out2).all()
+    assert mx <= 1e-4 and mean <= KD.MEAN_ABS_TOL
+    # each within 1e-4 of the oracle, so within 2e-4 of each other (9.2e-5 observed)
+    np.testing.assert_allclose(g_out2, g_out, rtol=0, atol=2e-4)

@@ -563,3 +563,33 @@ def test_qsa_mask_limits_and_zeros():
     negz[:, 5] = 0x8000
     got = SO.qsa_mask(every, negz, n_kv, row_len)
     assert (got[:, 5] == SO.F16_ZERO).all()
+
+
+def test_visible_cells_closed_forms():
+    """The keys a query sees: its distinct selected cells at or before its position,
+    ascending (the position itself included, the one after it not); none for an empty
+    selection; every key up to the position when every cell is selected."""
+    np.testing.assert_array_equal(SO.visible_cells(np.array([5, 3, 3, 9, 8, 100]), 200, 8), [3, 5, 8])
+    np.testing.assert_array_equal(SO.visible_cells(np.array([9]), 200, 8), np.zeros(0, np.int32))
+    assert len(SO.visible_cells(np.zeros(0, np.int32), 50, 49)) == 0
+    np.testing.assert_array_equal(SO.visible_cells(np.arange(40)[::-1], 40, 17), np.arange(18))
+    rng = np.random.default_rng(9)
+    for pos in (0, 77, 299):
+        c = rng.integers(0, 300, 150)
+        np.testing.assert_array_equal(SO.visible_cells(c, 300, pos), sorted({int(x) for x in c if x <= pos}))
+
+
+def test_visible_cells_and_query_cells_dev_validation():
+    """Host checks of the prefill-list entry points (nothing reaches a device)."""
+    import ctypes
+    L = K.load()
+    buf = (ctypes.c_int32 * 64)()
+    p = ctypes.addressof(buf)
+    # NULL pointers, negative sizes, short rows, overlapping outputs
+    assert L.qwfn_qsa_visible_cells(None, 4, 16, 10, 1, 0, p, 16, p + 128, None) == K.EINVAL
+    assert L.qwfn_qsa_visible_cells(p, -1, 16, 10, 1, 0, p + 64, 16, p + 128, None) == K.EINVAL
+    assert L.qwfn_qsa_visible_cells(p, 4, 12, 10, 1, 0, p + 64, 16, p + 128, None) == K.EINVAL
+    assert L.qwfn_qsa_visible_cells(p, 4, 16, 10, 1, 0, p + 8, 16, p + 128, None) == K.EINVAL
+    assert L.qwfn_qsa_visible_cells(p, 4, 16, 600000, 1, 0, p + 64, 16, p + 128, None) == K.ENOTSUP
+    assert L.qwfn_flash_attn_ext_q8_0_query_cells_dev(None, None, None, None, None, 4, 0, 1.0, None, None, 1,
+                                                      None) == K.EINVAL
