@@ -2146,7 +2146,8 @@ __global__ __launch_bounds__(QC_WAVES * 64, 1) void k_fa_qc(qc_args a) {
     const char * vbase = a.v + (size_t) kvh * a.v_nb2;
     const v4i rk = make_rsrc(kbase, a.k_bytes), rv = make_rsrc(vbase, a.v_bytes);
     const v4i rc = make_rsrc(a.cells + (size_t) tq * (size_t) a.cell_stride, (uint32_t) span * 4u);
-    const int64_t q_pos = a.pos0 + tq;
+    // the query's position, clipped to int32 (cells are int32)
+    const int32_t q_pos = a.pos0 + tq < INT32_MAX ? (int32_t) (a.pos0 + tq) : INT32_MAX;
 
     // ---- DMA issue: piece p = 64 s + lane of a tile is byte 16 (p % 17) of
     //      the row of its key p / 17; keys past the list, and cells outside
@@ -2155,17 +2156,32 @@ __global__ __launch_bounds__(QC_WAVES * 64, 1) void k_fa_qc(qc_args a) {
     const uint32_t stl0 = lds_addr(&ring[0][0][0]) + (uint32_t) wave * QC_STAGE;
     const uint32_t stl1 = stl0 + QC_WAVES * QC_STAGE;
     const uint32_t csl = lds_addr(&cslot[wave][0][0]);
-    auto gather_off = [&](int j, int s, uint32_t nb1) -> uint32_t {
-        const uint32_t p = (uint32_t) (64 * s + lane), key = p / 17u, part = p - key * 17u;
-        const int kk = (kg + j * KG) * DEC_TK + (int) key;
-        const uint32_t row = kk < span ? (uint32_t) cslot[wave][j & (QC_SLOTS - 1)][key < DEC_TK ? key : 0] : 0xffffffffu;
-        return row < (uint32_t) a.n_rows ? row * nb1 + part * 16u : 0x80000000u;
+    // per lane and DMA slot s: the key (p / 17) and the byte within its row
+    uint32_t skey[DEC_TDMA], spart[DEC_TDMA];
+#pragma unroll
+    for (int s = 0; s < DEC_TDMA; s++) {
+        const uint32_t p = (uint32_t) (64 * s + lane), key = p / 17u;
+        skey[s] = (key < DEC_TK ? key : 0u) * 4u;          // byte offset in the slot (lanes past the tile: key 0)
+        spart[s] = (p - key * 17u) * 16u;
+    }
+    // the rows of the wave's tile j: a key past the list reads a cell that is
+    // 0 or another cell of the list (the DMA of the cells zero-fills past the
+    // list) and is masked by the key check; a cell outside the cache gets
+    // offsets past the buffer (zeros, no memory access)
+    uint32_t srow[DEC_TDMA];
+    auto load_rows = [&](int j) __attribute__((always_inline)) {
+        const uint8_t * sl = (const uint8_t *) &cslot[wave][j & (QC_SLOTS - 1)][0];
+#pragma unroll
+        for (int s = 0; s < DEC_TDMA; s++) {
+            const uint32_t row = *(const uint32_t *) (sl + skey[s]);
+            srow[s] = row < (uint32_t) a.n_rows ? row : 0xffffffffu;
+        }
     };
-    auto issue_rows = [&](int j, uint32_t stl, v4i r, uint32_t nb1, auto base_c) __attribute__((always_inline)) {
+    auto issue_rows = [&](uint32_t stl, v4i r, uint32_t nb1, auto base_c) __attribute__((always_inline)) {
         constexpr uint32_t B = decltype(base_c)::value;
         uint32_t o[DEC_TDMA];
 #pragma unroll
-        for (int s = 0; s < DEC_TDMA; s++) o[s] = gather_off(j, s, nb1);
+        for (int s = 0; s < DEC_TDMA; s++) o[s] = srow[s] != 0xffffffffu ? srow[s] * nb1 + spart[s] : 0x80000000u;
         __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the cells are read and this wave's reads of the stage are done
         dma16_buf_at<B>(r, o[0], stl);
         dma16_buf_at<B + 1024>(r, o[1], stl);
@@ -2174,11 +2190,13 @@ __global__ __launch_bounds__(QC_WAVES * 64, 1) void k_fa_qc(qc_args a) {
         static_assert(DEC_TDMA == 5, "five DMAs per tensor");
         if (lane < 16) dma16_buf_at<B + 4096>(r, o[4], stl);
     };
+    // K rows of tile j (reads its cells), then V rows of the same tile
     auto issue_k = [&](int j, uint32_t stl) __attribute__((always_inline)) {
-        issue_rows(j, stl, rk, a.k_nb1, std::integral_constant<uint32_t, 0>{});
+        load_rows(j);
+        issue_rows(stl, rk, a.k_nb1, std::integral_constant<uint32_t, 0>{});
     };
-    auto issue_v = [&](int j, uint32_t stl) __attribute__((always_inline)) {
-        issue_rows(j, stl, rv, a.v_nb1, std::integral_constant<uint32_t, DEC_KB>{});
+    auto issue_v = [&](uint32_t stl) __attribute__((always_inline)) {
+        issue_rows(stl, rv, a.v_nb1, std::integral_constant<uint32_t, DEC_KB>{});
     };
     // the 16 cells of the wave's tile j into slot j % 4 (lanes 0-3, 16 bytes each)
     auto issue_cells = [&](int j) __attribute__((always_inline)) {
@@ -2205,9 +2223,10 @@ __global__ __launch_bounds__(QC_WAVES * 64, 1) void k_fa_qc(qc_args a) {
         if (lane < 16)
             dma16_buf(rc, (uint32_t) (((kg + (lane >> 2) * KG) * DEC_TK + 4 * (lane & 3)) * 4), csl);
     }
-    wait_vmcnt<0>();
+    wait_vmcnt<0>();   // this wave's query rows and cells have landed
+    __syncthreads();   // ... and every wave's: the query rows are read across the block
     issue_k(0, stl0);
-    issue_v(0, stl0);
+    issue_v(stl0);
 
     // ---- requantisation of the query rows (ggml's quantiser): wave w takes
     //      q8_0 block w of every row, QL lanes per row ----
@@ -2267,7 +2286,7 @@ __global__ __launch_bounds__(QC_WAVES * 64, 1) void k_fa_qc(qc_args a) {
     // their slots and arrive again, unchanged
     issue_cells(2);
     issue_k(1, stl1);
-    issue_v(1, stl1);
+    issue_v(stl1);
     issue_cells(3);
 
     // ---- the key loop ----
@@ -2333,7 +2352,7 @@ __global__ __launch_bounds__(QC_WAVES * 64, 1) void k_fa_qc(qc_args a) {
                 const bool in = kin + i < span;
                 const bool row_ok = (uint32_t) cv[i] < (uint32_t) a.n_rows;
                 bad |= in && !row_ok;
-                x[i] = in && row_ok && (int64_t) cv[i] <= q_pos ? s[i] : -INFINITY;
+                x[i] = in && row_ok && cv[i] <= q_pos ? s[i] : -INFINITY;
             }
             float mloc = vmax(vmax(x[0], x[1]), vmax(x[2], x[3]));
             mloc = xmax_lanes16_32(mloc);
@@ -2391,17 +2410,24 @@ __global__ __launch_bounds__(QC_WAVES * 64, 1) void k_fa_qc(qc_args a) {
             O[bb][1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A1, Bl, O[bb][1], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
-        issue_v(j + 2, stl);
+        issue_v(stl);                  // the rows issue_k(j + 2) read
         issue_cells(j + 4);
     };
+    // Waves w and w + 4 share a SIMD: their priorities alternate with the tile,
+    // in opposite phase, so that neither runs its tiles ahead of the other
+    // and then finishes alone at half the vector rate.
+    const bool young = wave >= QC_WAVES / 2;
     for (int j = 0; j < J; j += 2) {
         wait_vmcnt<QC_AHEAD>();
+        if (young) __builtin_amdgcn_s_setprio(0); else __builtin_amdgcn_s_setprio(1);
         tile_step(j, &ring[0][wave][0], stl0);
         if (j + 1 < J) {
             wait_vmcnt<QC_AHEAD>();
+            if (young) __builtin_amdgcn_s_setprio(1); else __builtin_amdgcn_s_setprio(0);
             tile_step(j + 1, &ring[1][wave][0], stl1);
         }
     }
+    __builtin_amdgcn_s_setprio(0);
     wait_vmcnt<0>();   // every DMA of the wave has landed (those past the list included)
 
     // ---- merge the KG waves of each unit ----
