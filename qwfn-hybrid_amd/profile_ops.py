@@ -5,6 +5,7 @@ after one warm-up; nothing else runs on the GPU besides the input set-up.
   python3 qwfn-hybrid_amd/profile_ops.py verify --depth 16384 --T 3
   python3 qwfn-hybrid_amd/profile_ops.py prefill --depth 16384
   python3 qwfn-hybrid_amd/profile_ops.py cells | append | gather | restore | produce | deltanet | pool
+  python3 qwfn-hybrid_amd/profile_ops.py qsaprefill --depth 16384  (QSA-on prefill chunk over cell lists)
   python3 qwfn-hybrid_amd/profile_ops.py copy --mb 1024        (a plain device copy: counter calibration)
 
 Cache sets are rotated (--sets) so that a repeated launch does not find its
@@ -25,7 +26,7 @@ ROW = 544
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("op", choices=["verify", "prefill", "cells", "append", "gather", "restore", "produce", "deltanet",
-                                   "pool", "select", "copy"])
+                                   "pool", "select", "qsaprefill", "copy"])
     ap.add_argument("--depth", type=int, default=16384)
     ap.add_argument("--T", type=int, default=3)
     ap.add_argument("--reps", type=int, default=10)
@@ -168,6 +169,37 @@ def main() -> int:
         csel = torch.empty((3, kb * 4), dtype=torch.int32, device=dev)
         wsel = torch.empty(K.load().qwfn_qsa_select_workspace_size(nb, 3), dtype=torch.uint8, device=dev)
         run = lambda i: S.qsa_select_cells(pool, qsel, bsel, kb, bcells, 4, csel, ws=wsel)
+    elif a.op == "qsaprefill":
+        # the reference's default prefill (QSA on) for a 512-query chunk at `depth`:
+        # chunk tables and bias, the pool rebuild, top-513 selection of blocks of 4,
+        # each query's visible cells, and the attention over those lists (k_fa_qc)
+        import qwfn_state as S
+        T, ratio, kb = 512, 4, 513
+        n_kv = a.depth + T
+        nb = n_kv // ratio
+        sets = [(cache(n_kv), cache(n_kv)) for _ in range(a.sets)]
+        ic = torch.randn((n_kv, 128), generator=gen, device=dev).to(torch.float16)
+        knw = torch.rand(128, generator=gen, device=dev) + 0.5
+        q_idx = torch.randn((T, 4, 128), generator=gen, device=dev)
+        bc = torch.empty(nb * ratio, dtype=torch.int32, device=dev)
+        bp = torch.empty(4 * nb, dtype=torch.int32, device=dev)
+        bias = torch.empty((T, nb), dtype=torch.float32, device=dev)
+        pool = torch.empty((nb, 128), dtype=torch.float16, device=dev)
+        cells = torch.empty((T, kb * ratio), dtype=torch.int32, device=dev)
+        lists = torch.empty((T, kb * ratio), dtype=torch.int32, device=dev)
+        counts = torch.empty((T,), dtype=torch.int32, device=dev)
+        wsel = torch.empty(K.load().qwfn_qsa_select_workspace_size(nb, T), dtype=torch.uint8, device=dev)
+        q = torch.randn((1, T, nh, hd), generator=gen, device=dev)
+        out = torch.zeros((1, T, nh, hd), dtype=torch.float32, device=dev)
+        views = [(K.cache_attn_view(k, n_kv, 2), K.cache_attn_view(v, n_kv, 2)) for k, v in sets]
+
+        def run(i):
+            S.qsa_chunk_inputs(a.depth, T, ratio, None, bc, bp, bias)
+            K.qsa_pool_rebuild(ic, n_kv, ratio, knw, pool)
+            S.qsa_select_cells(pool, q_idx, bias, kb, bc, ratio, cells, ws=wsel)
+            S.qsa_visible_cells(cells, n_kv, a.depth, lists, counts)
+            K.flash_attn_ext_query_cells_dev(K.q_view(q), views[i % a.sets][0], views[i % a.sets][1], lists, counts,
+                                             a.depth, 1 / 16, K.out_view(out))
     else:  # pool: rebuild after a prefill of `depth` positions, ratio 4
         ic = torch.randn((a.depth + 64, 128), generator=gen, device=dev).to(torch.float16)
         pool = torch.zeros((a.depth // 4 + 16, 128), dtype=torch.float16, device=dev)
