@@ -211,7 +211,8 @@ int     qwfn_snap_pool_restore_or_reset(qwfn_snap_pool * pool, qwfn_state * cons
  * [T][k_blocks]. k_blocks <= min(n_blocks, 1024), n_blocks <= 49152. Equal
  * scores keep the lower block first. ws: at least
  * qwfn_qsa_select_workspace_size(n_blocks, T) bytes of 16-byte aligned device
- * memory (the scores). All pointers are device memory. */
+ * memory (the scores; for more than 8 queries without the bias, which the
+ * top-k adds). All pointers are device memory. */
 size_t qwfn_qsa_select_workspace_size(int64_t n_blocks, int32_t T);
 int qwfn_qsa_select_cells(const uint16_t * pool, size_t pool_nb1, int64_t n_blocks, const float * q, int32_t n_heads,
                           size_t q_nb2, const float * bias, size_t bias_nb1, int32_t T, int32_t k_blocks,

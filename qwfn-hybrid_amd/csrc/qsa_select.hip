@@ -12,8 +12,9 @@
 // Two kernels. k_qsa_score reads the pool cache (n_blocks x 128 f16, 4.7 MB
 // at 18432 blocks) once for up to 8 queries and computes the dot products on
 // the matrix cores, one wave per 16 blocks (per 32 to 128 blocks when many
-// queries keep the grid full); the scores land in a workspace.
-// k_qsa_topk, one workgroup per query, holds the scores in registers as
+// queries keep the grid full); the scores land in a workspace, the bias
+// added there for up to 8 queries and by k_qsa_topk as it loads them for
+// more. k_qsa_topk, one workgroup per query, holds the scores in registers as
 // order-preserving keys of the float bits, and writes the cells of the k
 // best blocks, best first (ties: lower block first). Usually a threshold
 // from a sample of the scores leaves under 1024 candidates, which one
@@ -50,8 +51,8 @@ struct score_args {
     int32_t          n_heads;
     int32_t          head_bits;   // columns per query: 2^head_bits >= n_heads
     int32_t          T;
-    const float *    bias;        // F32 [n_blocks] per query, query stride bias_nb1 bytes
-    size_t           bias_nb1;
+    const float *    bias;        // null: the sums over heads alone (k_qsa_topk adds the bias), else F32
+    size_t           bias_nb1;    // [n_blocks] per query, query stride bias_nb1 bytes
     float *          score;       // [T][score_ld(n_blocks)]
     int32_t          mb;          // 16-block tiles per wave
 };
@@ -149,21 +150,33 @@ __global__ __launch_bounds__(SCORE_THREADS) void k_qsa_score(score_args a) {
             if (tile >= n_tiles) break;
             const int tl = tile * QT + (ln >> hb);
             const bool writer = h == 0 && tl < nt;
-            const char * brow = (const char *) a.bias + (size_t) (t0 + (tl < nt ? tl : 0)) * a.bias_nb1;
-            float bias4[4];
+            float bias4[4] = {0.f, 0.f, 0.f, 0.f};
+            if (a.bias) {
+                const char * brow = (const char *) a.bias + (size_t) (t0 + (writer ? tl : 0)) * a.bias_nb1;
 #pragma unroll
-            for (int r = 0; r < 4; r++)
-                bias4[r] = (writer && ob + r < n) ? *(const float *) (brow + (size_t) (ob + r) * 4) : 0.f;
+                for (int r = 0; r < 4; r++)
+                    if (writer && ob + r < n) bias4[r] = *(const float *) (brow + (size_t) (ob + r) * 4);
+            }
             v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int st = 0; st < 4; st++) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr[st], qb[tile][st], acc, 0, 0, 0);
+            float v[4];
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                float v = acc[r] > 0.f ? acc[r] : 0.f;            // relu per head
-                if (hb >= 1) v += dpp_f<0xB1>(v);                 // quad_perm 1,0,3,2
-                if (hb >= 2) v += dpp_f<0x4E>(v);                 // quad_perm 2,3,0,1
-                if (hb >= 3) v += dpp_f<0x141>(v);                // row_half_mirror
-                if (writer && ob + r < n) a.score[(size_t) (t0 + tl) * ld + ob + r] = v + bias4[r];
+                v[r] = acc[r] > 0.f ? acc[r] : 0.f;               // relu per head
+                if (hb >= 1) v[r] += dpp_f<0xB1>(v[r]);           // quad_perm 1,0,3,2
+                if (hb >= 2) v[r] += dpp_f<0x4E>(v[r]);           // quad_perm 2,3,0,1
+                if (hb >= 3) v[r] += dpp_f<0x141>(v[r]);          // row_half_mirror
+                if (a.bias) v[r] += bias4[r];
+            }
+            // score rows are 64 floats apart in a 16-byte aligned workspace
+            float * srow = a.score + (size_t) (t0 + (writer ? tl : 0)) * ld;
+            if (writer && ob + 3 < n) {
+                *(float4 *) (srow + ob) = make_float4(v[0], v[1], v[2], v[3]);
+            } else if (writer) {
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    if (ob + r < n) srow[ob + r] = v[r];
             }
         }
 #pragma unroll
@@ -172,7 +185,10 @@ __global__ __launch_bounds__(SCORE_THREADS) void k_qsa_score(score_args a) {
 }
 
 struct topk_args {
-    const float *   score;        // [T][score_ld(n_blocks)]
+    const float *   score;        // [T][score_ld(n_blocks)]: the sums over heads
+    const float *   bias;         // null: the scores are complete; else F32 [n_blocks] per query
+    size_t          bias_nb1;     // (query stride bias_nb1 bytes), added as the scores load
+    int32_t         bias_vec;     // bias and bias_nb1 16-byte aligned
     int64_t         n_blocks;
     int32_t         k;            // blocks kept
     const int32_t * blk_cells;    // [n_blocks_max * ratio]
@@ -404,6 +420,7 @@ __global__ __launch_bounds__(TOPK_THREADS) void k_qsa_topk(topk_args a) {
     const int k = a.k;
     const int64_t base = (int64_t) tid * KPT;
     const float * sc = a.score + (size_t) blockIdx.x * score_ld(n);
+    const float * br = a.bias ? (const float *) ((const char *) a.bias + (size_t) blockIdx.x * a.bias_nb1) : nullptr;
 
     for (int i = tid; i < (1 << RADIX_BITS) * SUBH_LD / 4; i += TOPK_THREADS)
         ((uint4 *) L.sub_hist)[i] = make_uint4(0u, 0u, 0u, 0u);
@@ -411,8 +428,20 @@ __global__ __launch_bounds__(TOPK_THREADS) void k_qsa_topk(topk_args a) {
     uint32_t key[KPT];
 #pragma unroll
     for (int j = 0; j < KPT; j += 4) {
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f), bv = v;
         if (base + j < n) v = *(const float4 *) (sc + base + j);   // score_ld keeps the float4 inside the row
+        if (br) {
+            if (a.bias_vec && base + j + 3 < n) {
+                bv = *(const float4 *) (br + base + j);
+            } else {
+                if (base + j < n) bv.x = br[base + j];
+                if (base + j + 1 < n) bv.y = br[base + j + 1];
+                if (base + j + 2 < n) bv.z = br[base + j + 2];
+                if (base + j + 3 < n) bv.w = br[base + j + 3];
+            }
+            // score = the sum over heads + the bias, one f32 addition
+            v.x += bv.x; v.y += bv.y; v.z += bv.z; v.w += bv.w;
+        }
         key[j] = okey(v.x); key[j + 1] = okey(v.y); key[j + 2] = okey(v.z); key[j + 3] = okey(v.w);
     }
     const int nv = base >= n ? 0 : (n - base < KPT ? (int) (n - base) : KPT);   // valid keys of this thread
@@ -579,12 +608,22 @@ extern "C" int qwfn_qsa_select_cells(const uint16_t * pool, size_t pool_nb1, int
         const int64_t n_tile = (n_blocks + 15) / 16, ny = (T + SCORE_T - 1) / SCORE_T;
         int32_t mb = 1;
         while (mb < 8 && n_tile * ny / (2 * mb) >= 2048) mb *= 2;
-        score_args sa{pool, pool_nb1, n_blocks, q, q_nb2, n_heads, head_bits, T, bias, bias_nb1, (float *) ws, mb};
+        // the bias: added by the score kernel for one pass over the pool (up to 8
+        // queries: decode, verify), whose top-k then reads only scores it has just
+        // written; by the top-k for more (a prefill chunk), which keeps the score
+        // kernel's tile loop free of dependent loads (8 tiles a wave at 512
+        // queries x 4224 blocks: 32.0 -> 24.0 us, the top-k 14.9 -> 16.3 us; at
+        // 3 queries x 18432 blocks the top-k took 13.3 -> 15.4 us)
+        const bool bias_in_score = ny == 1;
+        score_args sa{pool, pool_nb1, n_blocks, q, q_nb2, n_heads, head_bits, T, bias_in_score ? bias : nullptr,
+                      bias_nb1, (float *) ws, mb};
         const int64_t per = SCORE_THREADS / 64 * 16 * mb;            // blocks per workgroup: 16 mb per wave
         const unsigned gx = (unsigned) ((n_blocks + per - 1) / per);
         hipLaunchKernelGGL(k_qsa_score, dim3(gx, (unsigned) ny), dim3(SCORE_THREADS), 0, st, sa);
         if (int rc = hip_check(hipGetLastError(), "qsa score launch")) return rc;
-        topk_args ta{(const float *) ws, n_blocks, k_blocks, blk_cells, ratio, cells, top};
+        const int32_t bias_vec = is_aligned(bias, 16) && bias_nb1 % 16 == 0;
+        topk_args ta{(const float *) ws, bias_in_score ? nullptr : bias, bias_nb1, bias_vec, n_blocks, k_blocks,
+                     blk_cells, ratio, cells, top};
         const int64_t kpt = (n_blocks + TOPK_THREADS - 1) / TOPK_THREADS;
         // the smallest multiple of 4 that holds n_blocks / 1024 (18432 blocks: 20)
         auto topk = kpt <= 8 ? k_qsa_topk<8> : kpt <= 12 ? k_qsa_topk<12> : kpt <= 16 ? k_qsa_topk<16>
