@@ -600,17 +600,19 @@ def measure_rows(K, torch, np, dev, gen) -> dict:
         del kc, vc, pws
     torch.cuda.empty_cache()
     rows.update(measure_qsa_prefill_row(K, torch, np, dev, gen))
+    rows.update(measure_qsa_prefill_row(K, torch, np, dev, gen, d0=65536))
     return rows
 
 
-def measure_qsa_prefill_row(K, torch, np, dev, gen) -> dict:
+def measure_qsa_prefill_row(K, torch, np, dev, gen, d0: int = 16384) -> dict:
     """The reference's default prefill with QSA on (qwfn_graph.cpp:313-414, :466) for a
-    512-query chunk at depth 16384, 16 heads over 2 KV heads: the chunk's block tables
-    and bias, the pooled keys of its 4224 blocks of 4, each query's top 513 blocks
-    (indexer: 4 heads of 128), the causal and the selection masks, and flash attention
-    over the selection mask; also the attention alone. As the GPU test composes it."""
+    512-query chunk at depth d0 (16384: 4224 blocks of 4), 16 heads over 2 KV heads: the
+    chunk's block tables and bias, the pooled keys of its blocks, each query's top 513
+    blocks (indexer: 4 heads of 128), the causal and the selection masks, and flash
+    attention over the selection mask; also the attention alone, and the same keys as
+    lists (qwfn_qsa_visible_cells, then k_fa_qc). As the GPU test composes it."""
     import qwfn_state as S
-    d0, T, ratio, nh, nh_kv, hd, kb = 16384, 512, 4, 16, 2, 256, 513
+    T, ratio, nh, nh_kv, hd, kb = 512, 4, 16, 2, 256, 513
     n_kv = d0 + T
     nb = n_kv // ratio
     row = (n_kv + 63) // 64 * 64
@@ -664,7 +666,7 @@ def measure_qsa_prefill_row(K, torch, np, dev, gen) -> dict:
     lerr = float((lout - pout).abs().max().item())
     visible = int((qmask[:, :n_kv] == 0).sum().item())
     flops = 4 * nh * hd * visible                               # QK^T and PV over the visible keys
-    return {"prefill_512_at_16384_qsa": {
+    return {f"prefill_512_at_{d0}_qsa": {
         "us_per_layer": round(us_chain, 1), "us_attention": round(us_attn, 1), "us_inputs": round(us_chain - us_attn, 1),
         "blocks": nb, "k_blocks": kb, "visible_keys_per_query": round(visible / T, 1), "flops": flops,
         "TFLOPs": round(flops / (us_attn * 1e-6) / 1e12, 2),
@@ -672,8 +674,8 @@ def measure_qsa_prefill_row(K, torch, np, dev, gen) -> dict:
         "us_per_layer_lists": round(us_lists, 1), "us_attention_lists": round(us_lattn, 1),
         "lists_gathered_bytes": int(counts.sum().item()) * nh_kv * 2 * 272,
         "lists_max_abs_diff_vs_mask": lerr,
-        "what": "chunk tables + pool of 4224 blocks + top-513 select for 512 queries + causal and selection masks "
-                "+ k_fa_pre over the selection mask"}}
+        "what": f"chunk tables + pool of {nb} blocks + top-513 select for 512 queries + causal and selection masks "
+                "+ k_fa_pre over the selection mask; _lists: the same selection, visible cells, k_fa_qc"}}
 
 
 def main() -> int:

@@ -184,6 +184,106 @@ __global__ __launch_bounds__(SCORE_THREADS) void k_qsa_score(score_args a) {
     }
 }
 
+// Many queries (a prefill chunk): the same scores as k_qsa_score, tiled as a
+// GEMM so that the pool and the queries are each read a few times instead of
+// once per 8 queries. A workgroup holds QBW = 256 / 2^head_bits queries (64 at
+// 4 heads), rounded to f16, in LDS ([query][head][128 dims], rows padded to 272
+// bytes so that the 16 columns of an operand read hit distinct banks), and its
+// 8 waves take mb tiles of 16 blocks each; per tile a wave keeps the keys in
+// registers and runs the workgroup's 16-column tiles past them. The operand
+// layout per lane and k-step is k_qsa_score's, so the scores are the same bits.
+// The bias is left to the top-k.
+constexpr int SQ_COLS = 256;                          // (query, head) columns of a workgroup
+constexpr int SQ_ROWB = IDX_DIM * 2 + 16;             // 272: LDS bytes per column
+constexpr int SQ_THREADS = 512;                       // 8 waves: two workgroups a CU hold 4 waves a SIMD
+
+__global__ __launch_bounds__(SQ_THREADS) void k_qsa_score_tiled(score_args a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t sq_lds[];   // SQ_COLS * SQ_ROWB
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int ln = lane & 15, lg = lane >> 4;
+    const int64_t n = a.n_blocks;
+    const int hb = a.head_bits, Hp = 1 << hb;
+    const int QBW = SQ_COLS >> hb;                       // queries of the workgroup
+    const int t0 = blockIdx.y * QBW;
+    const int nt = a.T - t0 < QBW ? a.T - t0 : QBW;
+    // ---- the workgroup's queries into LDS as f16: column c = query c >> hb,
+    //      head c & (Hp - 1) (heads past n_heads and queries past T: zeros);
+    //      thread i takes 8-dim pieces i, i + 256, ... ----
+    // in two rounds of 8 pieces a thread, every load of a round issued before
+    // any of its conversions and stores
+    constexpr int SQ_PIECES = SQ_COLS * (IDX_DIM / 8) / SQ_THREADS;   // 8
+    constexpr int SQ_ROUND = 8;
+#pragma unroll
+    for (int r0 = 0; r0 < SQ_PIECES; r0 += SQ_ROUND) {
+        float4 x[SQ_ROUND], y[SQ_ROUND];
+#pragma unroll
+        for (int u = 0; u < SQ_ROUND; u++) {
+            const int pc = (r0 + u) * SQ_THREADS + threadIdx.x;
+            const int c = pc >> 4, d8 = (pc & 15) * 8;
+            const int tl = c >> hb, hh = c & (Hp - 1);
+            x[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            y[u] = x[u];
+            if (tl < nt && hh < a.n_heads) {
+                const float * qp = (const float *) ((const char *) a.q + (size_t) (t0 + tl) * a.q_nb2) + hh * IDX_DIM + d8;
+                x[u] = *(const float4 *) qp;
+                y[u] = *(const float4 *) (qp + 4);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < SQ_ROUND; u++) {
+            const int pc = (r0 + u) * SQ_THREADS + threadIdx.x;
+            const int c = pc >> 4, d8 = (pc & 15) * 8;
+            const v8h hv = v8h{(_Float16) x[u].x, (_Float16) x[u].y, (_Float16) x[u].z, (_Float16) x[u].w,
+                               (_Float16) y[u].x, (_Float16) y[u].y, (_Float16) y[u].z, (_Float16) y[u].w};   // round to nearest even
+            *(v8h *) (sq_lds + c * SQ_ROWB + d8 * 2) = hv;
+        }
+    }
+    static_assert(SQ_PIECES % SQ_ROUND == 0, "whole rounds");
+    __syncthreads();
+    const int QT = 16 >> hb;                              // queries per 16-column tile
+    const int n_ct = (nt * Hp + 15) / 16;                 // the workgroup's column tiles holding a query
+    const int h = ln & (Hp - 1);
+    const int64_t ld = score_ld(n);
+    const int64_t tile0 = ((int64_t) blockIdx.x * (SQ_THREADS / 64) + wave) * a.mb;
+    v8h kr[4];
+    score_keys(a, tile0 * 16 + ln, lg, kr);
+    for (int mt = 0; mt < a.mb; mt++) {
+        const int64_t m0 = (tile0 + mt) * 16;
+        if (m0 >= n) break;
+        v8h kn[4];
+        score_keys(a, m0 + 16 + ln, lg, kn);              // the next tile's keys (past the wave's last: unused)
+        const int64_t ob = m0 + 4 * lg;
+#pragma unroll 2
+        for (int ct = 0; ct < n_ct; ct++) {
+            const int tl = ct * QT + (ln >> hb);          // query of this lane's column
+            const bool writer = h == 0 && tl < nt;
+            const uint8_t * qc = sq_lds + (ct * 16 + ln) * SQ_ROWB + 16 * lg;
+            v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < 4; st++)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr[st], *(const v8h *) (qc + 64 * st), acc, 0, 0, 0);
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                v[r] = acc[r] > 0.f ? acc[r] : 0.f;       // relu per head
+                if (hb >= 1) v[r] += dpp_f<0xB1>(v[r]);   // quad_perm 1,0,3,2
+                if (hb >= 2) v[r] += dpp_f<0x4E>(v[r]);   // quad_perm 2,3,0,1
+                if (hb >= 3) v[r] += dpp_f<0x141>(v[r]);  // row_half_mirror
+            }
+            float * srow = a.score + (size_t) (t0 + (writer ? tl : 0)) * ld;
+            if (writer && ob + 3 < n) {
+                *(float4 *) (srow + ob) = make_float4(v[0], v[1], v[2], v[3]);
+            } else if (writer) {
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    if (ob + r < n) srow[ob + r] = v[r];
+            }
+        }
+#pragma unroll
+        for (int st = 0; st < 4; st++) kr[st] = kn[st];
+    }
+}
+
 struct topk_args {
     const float *   score;        // [T][score_ld(n_blocks)]: the sums over heads
     const float *   bias;         // null: the scores are complete; else F32 [n_blocks] per query
@@ -314,32 +414,66 @@ __device__ __forceinline__ void kth_keep(uint32_t prefix, uint32_t need, bool do
     else      { kth = prefix; keep = need; }
 }
 
-// Keys above kth, then the kept equal keys (the lowest blocks: threads and
-// their keys are in block order), into sel[0, k) by an exclusive scan of
-// per-thread counts, packed with their block as (key << 32 | ~block), so that
-// the larger packed value comes first (ties: the lower block).
+// Keys above kth, then the kept equal keys (the lowest blocks), into
+// sel[0, k), packed with their block as (key << 32 | ~block), so that the
+// larger packed value comes first (ties: the lower block). Key j of thread
+// tid is block blk(j), and blocks rise in the order (j / 4, tid, j % 4) (the
+// top-k's interleaved layout). The keys above kth go in thread order (one
+// exclusive scan: their order is the sort's business); the equal ones one
+// group of 4 keys at a time, a scan per group, so that the first `keep` of
+// them in block order are the ones kept.
 template <int KK, typename Blk>
 __device__ __forceinline__ void place(const uint32_t (&key)[KK], Blk blk, int nv, uint32_t kth, uint32_t keep, int k,
                                       topk_lds & L) {
-    uint32_t na = 0, ne = 0;
+    static_assert(KK % 4 == 0, "groups of 4 keys");
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    // exclusive prefix of x over the workgroup in thread order, and the total
+    auto scan_total = [&](uint32_t x, uint32_t & ex) -> uint32_t {
+        const uint32_t ix = wave_incl_scan(x);
+        __syncthreads();                                 // the previous scan's readers are done with wsum
+        if (lane == 63) L.wsum[w].x = ix;
+        __syncthreads();
+        uint32_t bx = 0, tot = 0;
 #pragma unroll
-    for (int j = 0; j < KK; j++) {
-        na += (j < nv && key[j] > kth) ? 1u : 0u;
-        ne += (j < nv && key[j] == kth) ? 1u : 0u;
-    }
-    uint32_t pa, pe;
-    block_scan2(na, ne, pa, pe, L.wsum);
+        for (int w2 = 0; w2 < TOPK_THREADS / 64; w2++) {
+            const uint32_t t = L.wsum[w2].x;
+            if (w2 < w) bx += t;
+            tot += t;
+        }
+        ex = bx + ix - x;
+        return tot;
+    };
+    uint32_t na = 0;
+#pragma unroll
+    for (int j = 0; j < KK; j++) na += (j < nv && key[j] > kth) ? 1u : 0u;
+    uint32_t pa;
+    scan_total(na, pa);
     const uint32_t first_equal = (uint32_t) k - keep;        // the keys above take the slots before
 #pragma unroll
-    for (int j = 0; j < KK; j++) {
-        const uint64_t packed = ((uint64_t) key[j] << 32) | (uint32_t) ~blk(j);
+    for (int j = 0; j < KK; j++)
         if (j < nv && key[j] > kth) {
-            if (pa < first_equal) L.sel[pa] = packed;
+            if (pa < first_equal) L.sel[pa] = ((uint64_t) key[j] << 32) | (uint32_t) ~blk(j);
             pa++;
-        } else if (j < nv && key[j] == kth) {
-            if (pe < keep && first_equal + pe < (uint32_t) k) L.sel[first_equal + pe] = packed;
-            pe++;
         }
+    uint32_t placed = 0;                                     // equal keys of the groups before (uniform)
+#pragma unroll
+    for (int g = 0; g < KK / 4; g++) {
+        if (placed >= keep) break;
+        uint32_t ne = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) ne += (4 * g + e < nv && key[4 * g + e] == kth) ? 1u : 0u;
+        uint32_t pe;
+        const uint32_t tot = scan_total(ne, pe);
+        pe += placed;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int j = 4 * g + e;
+            if (j < nv && key[j] == kth) {
+                if (pe < keep && first_equal + pe < (uint32_t) k) L.sel[first_equal + pe] = ((uint64_t) key[j] << 32) | (uint32_t) ~blk(j);
+                pe++;
+            }
+        }
+        placed += tot;
     }
 }
 
@@ -413,12 +547,15 @@ __device__ __forceinline__ uint64_t bitonic_sort_block(uint64_t v, uint64_t * bu
 // are placed by a scan, and those k are sorted in runs of 64 per wave, then
 // merged by rank.
 template <int KPT>
-__global__ __launch_bounds__(TOPK_THREADS) void k_qsa_topk(topk_args a) {
+__global__ __launch_bounds__(TOPK_THREADS, KPT <= 16 ? 8 : 1) void k_qsa_topk(topk_args a) {
     __shared__ __align__(16) topk_lds L;
     const int tid = threadIdx.x, lane = tid & 63;
     const int64_t n = a.n_blocks;
     const int k = a.k;
-    const int64_t base = (int64_t) tid * KPT;
+    // key j of this thread is block kidx(j) = 4 tid + 4096 (j / 4) + j % 4: a
+    // wave's float4 loads cover 1 KB runs, and a thread's valid keys are a
+    // prefix of its j (the blocks rise with j)
+    auto kidx = [&](int j) -> int64_t { return 4 * (int64_t) tid + 4 * TOPK_THREADS * (int64_t) (j >> 2) + (j & 3); };
     const float * sc = a.score + (size_t) blockIdx.x * score_ld(n);
     const float * br = a.bias ? (const float *) ((const char *) a.bias + (size_t) blockIdx.x * a.bias_nb1) : nullptr;
 
@@ -428,23 +565,29 @@ __global__ __launch_bounds__(TOPK_THREADS) void k_qsa_topk(topk_args a) {
     uint32_t key[KPT];
 #pragma unroll
     for (int j = 0; j < KPT; j += 4) {
+        const int64_t b0 = kidx(j);
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f), bv = v;
-        if (base + j < n) v = *(const float4 *) (sc + base + j);   // score_ld keeps the float4 inside the row
+        if (b0 < n) v = *(const float4 *) (sc + b0);             // score_ld keeps the float4 inside the row
         if (br) {
-            if (a.bias_vec && base + j + 3 < n) {
-                bv = *(const float4 *) (br + base + j);
+            if (a.bias_vec && b0 + 3 < n) {
+                bv = *(const float4 *) (br + b0);
             } else {
-                if (base + j < n) bv.x = br[base + j];
-                if (base + j + 1 < n) bv.y = br[base + j + 1];
-                if (base + j + 2 < n) bv.z = br[base + j + 2];
-                if (base + j + 3 < n) bv.w = br[base + j + 3];
+                if (b0 < n) bv.x = br[b0];
+                if (b0 + 1 < n) bv.y = br[b0 + 1];
+                if (b0 + 2 < n) bv.z = br[b0 + 2];
+                if (b0 + 3 < n) bv.w = br[b0 + 3];
             }
             // score = the sum over heads + the bias, one f32 addition
             v.x += bv.x; v.y += bv.y; v.z += bv.z; v.w += bv.w;
         }
         key[j] = okey(v.x); key[j + 1] = okey(v.y); key[j + 2] = okey(v.z); key[j + 3] = okey(v.w);
     }
-    const int nv = base >= n ? 0 : (n - base < KPT ? (int) (n - base) : KPT);   // valid keys of this thread
+    int nv = 0;                                                 // valid keys of this thread: j < nv
+#pragma unroll
+    for (int j = 0; j < KPT; j += 4) {
+        const int64_t r = n - kidx(j);
+        nv += r <= 0 ? 0 : (r < 4 ? (int) r : 4);
+    }
     __syncthreads();
 
     bool sorted_all = false;
@@ -452,18 +595,34 @@ __global__ __launch_bounds__(TOPK_THREADS) void k_qsa_topk(topk_args a) {
     if (KPT <= 32 && (n <= TOPK_THREADS || 4 * k <= 3 * TOPK_THREADS)) {   // (barriers: the conditions are uniform)
         uint32_t tau = 0;                                       // valid keys are never 0: all of them
         if (n > TOPK_THREADS) {
-            constexpr int J2 = KPT / 2;
+            // the sample: keys j1 = tid % KPT and j2 = (tid + KPT / 2) % KPT of
+            // each thread, so that it spreads over every part of the pool
             const int nn = (int) n;                             // at most 32 * 1024 here
-            const int m = (nn + KPT - 1) / KPT + (nn > J2 ? (nn - J2 + KPT - 1) / KPT : 0);   // sample keys: key[0] and key[KPT / 2] of each thread
+            const int j1 = tid % KPT, j2 = (tid + KPT / 2) % KPT;
+            uint32_t k1 = key[0], k2 = key[0];
+#pragma unroll
+            for (int j = 1; j < KPT; j++) {
+                k1 = j == j1 ? key[j] : k1;
+                k2 = j == j2 ? key[j] : k2;
+            }
+            const bool v1 = j1 < nv, v2 = j2 < nv;
+            // the valid sample keys, counted with a ballot per wave
+            const uint32_t c1 = (uint32_t) __popcll(__ballot(v1)), c2 = (uint32_t) __popcll(__ballot(v2));
+            if (lane == 0) L.wsum[tid >> 6] = make_uint2(c1, c2);
+            __syncthreads();
+            int m = 0;
+#pragma unroll
+            for (int w2 = 0; w2 < TOPK_THREADS / 64; w2++) m += (int) (L.wsum[w2].x + L.wsum[w2].y);
+            __syncthreads();                                    // wsum is free again
             // the sample rank, in float (an estimate serves: any tau with between
             // k and TOPK_THREADS keys at or above it gives the exact answer)
             const float want = 0.5f * (float) (k + TOPK_THREADS);
             uint32_t S = (uint32_t) ceilf(want * (float) m / (float) nn);
             S = S < 1 ? 1u : (S > (uint32_t) m ? (uint32_t) m : S);
-            const uint32_t sk[2] = {key[0], key[J2]};
+            const uint32_t sk[2] = {v1 ? k1 : k2, v1 ? k2 : k1};   // the valid ones first
             uint32_t nd;
             bool dn;
-            radix_passes<2>(sk, nv > J2 ? 2 : (nv > 0 ? 1 : 0), S, 16, L, tau, nd, dn);
+            radix_passes<2>(sk, (v1 ? 1 : 0) + (v2 ? 1 : 0), S, 16, L, tau, nd, dn);
         }
         // the keys >= tau into L.cand, each wave's at an offset it takes with one atomic
         uint32_t c = 0;
@@ -477,7 +636,7 @@ __global__ __launch_bounds__(TOPK_THREADS) void k_qsa_topk(topk_args a) {
 #pragma unroll
         for (int j = 0; j < KPT; j++)
             if (j < nv && key[j] >= tau) {
-                if (pos < (uint32_t) TOPK_THREADS) L.cand[pos] = ((uint64_t) key[j] << 32) | (uint32_t) ~(uint32_t) (base + j);
+                if (pos < (uint32_t) TOPK_THREADS) L.cand[pos] = ((uint64_t) key[j] << 32) | (uint32_t) ~(uint32_t) kidx(j);
                 pos++;
             }
         __syncthreads();
@@ -509,7 +668,7 @@ __global__ __launch_bounds__(TOPK_THREADS) void k_qsa_topk(topk_args a) {
         bool done;
         radix_passes<KPT>(key, nv, (uint32_t) k, 0, L, pfx, need, done);
         kth_keep(pfx, need, done, kth, keep);
-        place<KPT>(key, [&](int j) { return (uint32_t) (base + j); }, nv, kth, keep, k, L);
+        place<KPT>(key, [&](int j) { return (uint32_t) kidx(j); }, nv, kth, keep, k, L);
     }
     // order: every wave sorts a run of 64 values in registers (bitonic over
     // lane swaps, best first); then each value's place is its index in its
@@ -602,12 +761,9 @@ extern "C" int qwfn_qsa_select_cells(const uint16_t * pool, size_t pool_nb1, int
         hipStream_t st = as_stream(stream);
         int head_bits = 0;
         while ((1 << head_bits) < n_heads) head_bits++;
-        // tiles per wave: a wave's query loads are shared by its tiles; more
-        // than one only while the grid keeps at least 2048 waves (a prefill
-        // chunk: 512 queries over 4224 blocks take 8)
+        // one pass over the pool (up to 8 queries): one 16-block tile a wave
         const int64_t n_tile = (n_blocks + 15) / 16, ny = (T + SCORE_T - 1) / SCORE_T;
-        int32_t mb = 1;
-        while (mb < 8 && n_tile * ny / (2 * mb) >= 2048) mb *= 2;
+        const int32_t mb = 1;
         // the bias: added by the score kernel for one pass over the pool (up to 8
         // queries: decode, verify), whose top-k then reads only scores it has just
         // written; by the top-k for more (a prefill chunk), which keeps the score
@@ -617,9 +773,20 @@ extern "C" int qwfn_qsa_select_cells(const uint16_t * pool, size_t pool_nb1, int
         const bool bias_in_score = ny == 1;
         score_args sa{pool, pool_nb1, n_blocks, q, q_nb2, n_heads, head_bits, T, bias_in_score ? bias : nullptr,
                       bias_nb1, (float *) ws, mb};
-        const int64_t per = SCORE_THREADS / 64 * 16 * mb;            // blocks per workgroup: 16 mb per wave
-        const unsigned gx = (unsigned) ((n_blocks + per - 1) / per);
-        hipLaunchKernelGGL(k_qsa_score, dim3(gx, (unsigned) ny), dim3(SCORE_THREADS), 0, st, sa);
+        if (bias_in_score) {
+            const int64_t per = SCORE_THREADS / 64 * 16 * mb;        // blocks per workgroup: 16 mb per wave
+            const unsigned gx = (unsigned) ((n_blocks + per - 1) / per);
+            hipLaunchKernelGGL(k_qsa_score, dim3(gx, (unsigned) ny), dim3(SCORE_THREADS), 0, st, sa);
+        } else {
+            // more than 8 queries: the tiled kernel, 256 >> head_bits queries a
+            // workgroup; tiles a wave so that the grid holds about 512 workgroups
+            // (two a CU)
+            const int64_t nyq = (T + (SQ_COLS >> head_bits) - 1) / (SQ_COLS >> head_bits);
+            sa.mb = (int32_t) std::max<int64_t>(1, std::min<int64_t>(64, n_tile * nyq / (8 * 512)));
+            const int64_t per = SQ_THREADS / 64 * 16 * (int64_t) sa.mb;
+            const unsigned gx = (unsigned) ((n_blocks + per - 1) / per);
+            hipLaunchKernelGGL(k_qsa_score_tiled, dim3(gx, (unsigned) nyq), dim3(SQ_THREADS), SQ_COLS * SQ_ROWB, st, sa);
+        }
         if (int rc = hip_check(hipGetLastError(), "qsa score launch")) return rc;
         const int32_t bias_vec = is_aligned(bias, 16) && bias_nb1 % 16 == 0;
         topk_args ta{(const float *) ws, bias_in_score ? nullptr : bias, bias_nb1, bias_vec, n_blocks, k_blocks,

@@ -226,6 +226,7 @@ struct qsa_chunk_args {
     int32_t * blk_pos;     // [4 * n_blocks] or null
     float *   bias;        // [Tc][n_blocks], rows bias_ld floats apart, or null
     int64_t   bias_ld;
+    int32_t   bias_vec;    // bias and bias_ld 16-byte aligned: 4 blocks a thread, one 16-byte store
     int64_t   n_past_c, Tc, n_blocks;
     int32_t   ratio;
 };
@@ -255,7 +256,20 @@ __global__ __launch_bounds__(FILL_THREADS) void k_qsa_chunk(qsa_chunk_args a) {
         const int64_t q = a.n_past_c + blockIdx.y;
         const int64_t tail_b = (q + 1) / r < n_bid ? (q + 1) / r : n_bid;
         float * row = a.bias + (size_t) blockIdx.y * (size_t) a.bias_ld;
-        for (int64_t b = t0; b < a.n_blocks; b += stride) row[b] = chunk_bias(b, q, r, tail_b, n_bid, dead, have_dead);
+        if (a.bias_vec) {
+            for (int64_t b = 4 * t0; b < a.n_blocks; b += 4 * stride) {
+                if (b + 4 <= a.n_blocks) {
+                    *(float4 *) (row + b) = make_float4(chunk_bias(b, q, r, tail_b, n_bid, dead, have_dead),
+                                                        chunk_bias(b + 1, q, r, tail_b, n_bid, dead, have_dead),
+                                                        chunk_bias(b + 2, q, r, tail_b, n_bid, dead, have_dead),
+                                                        chunk_bias(b + 3, q, r, tail_b, n_bid, dead, have_dead));
+                } else {
+                    for (int64_t e = b; e < a.n_blocks; e++) row[e] = chunk_bias(e, q, r, tail_b, n_bid, dead, have_dead);
+                }
+            }
+        } else {
+            for (int64_t b = t0; b < a.n_blocks; b += stride) row[b] = chunk_bias(b, q, r, tail_b, n_bid, dead, have_dead);
+        }
         return;
     }
     if (a.cell_blk)
@@ -894,9 +908,11 @@ int qwfn_qsa_chunk_inputs(int64_t n_past_c, int64_t Tc, int32_t ratio, int32_t *
         qsa_chunk_args a{};
         a.cell_blk = cell_blk; a.blk_cells = blk_cells; a.blk_pos = blk_pos; a.bias = bias;
         a.bias_ld = (int64_t) (bias_nb1 / 4);
+        a.bias_vec = bias && is_aligned(bias, 16) && bias_nb1 % 16 == 0;
         a.n_past_c = n_past_c; a.Tc = Tc; a.n_blocks = n_blocks; a.ratio = ratio;
-        // sized for a bias row: the table row (blockIdx.y == Tc) strides over its longer tables
-        const dim3 g(grid_for(n_blocks), (unsigned) (Tc + 1));
+        // sized for a bias row (4 blocks a thread when aligned): the table row
+        // (blockIdx.y == Tc) strides over its longer tables
+        const dim3 g(grid_for(a.bias_vec ? (n_blocks + 3) / 4 : n_blocks), (unsigned) (Tc + 1));
         hipLaunchKernelGGL(k_qsa_chunk, g, dim3(FILL_THREADS), 0, as_stream(stream), a);
         return hip_check(hipGetLastError(), "qsa_chunk_inputs launch");
     });
