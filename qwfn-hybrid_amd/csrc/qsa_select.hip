@@ -215,26 +215,28 @@ __global__ __launch_bounds__(SQ_THREADS) void k_qsa_score_tiled(score_args a) {
     constexpr int SQ_ROUND = 8;
 #pragma unroll
     for (int r0 = 0; r0 < SQ_PIECES; r0 += SQ_ROUND) {
+        // unconditional loads (a piece past the queries or the heads reads
+        // query 0, head 0 and is zeroed after): no branch holds a wait
         float4 x[SQ_ROUND], y[SQ_ROUND];
+        bool ok[SQ_ROUND];
 #pragma unroll
         for (int u = 0; u < SQ_ROUND; u++) {
             const int pc = (r0 + u) * SQ_THREADS + threadIdx.x;
             const int c = pc >> 4, d8 = (pc & 15) * 8;
             const int tl = c >> hb, hh = c & (Hp - 1);
-            x[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-            y[u] = x[u];
-            if (tl < nt && hh < a.n_heads) {
-                const float * qp = (const float *) ((const char *) a.q + (size_t) (t0 + tl) * a.q_nb2) + hh * IDX_DIM + d8;
-                x[u] = *(const float4 *) qp;
-                y[u] = *(const float4 *) (qp + 4);
-            }
+            ok[u] = tl < nt && hh < a.n_heads;
+            const float * qp = (const float *) ((const char *) a.q + (size_t) (t0 + (ok[u] ? tl : 0)) * a.q_nb2) +
+                               (ok[u] ? hh : 0) * IDX_DIM + d8;
+            x[u] = *(const float4 *) qp;
+            y[u] = *(const float4 *) (qp + 4);
         }
 #pragma unroll
         for (int u = 0; u < SQ_ROUND; u++) {
             const int pc = (r0 + u) * SQ_THREADS + threadIdx.x;
             const int c = pc >> 4, d8 = (pc & 15) * 8;
-            const v8h hv = v8h{(_Float16) x[u].x, (_Float16) x[u].y, (_Float16) x[u].z, (_Float16) x[u].w,
-                               (_Float16) y[u].x, (_Float16) y[u].y, (_Float16) y[u].z, (_Float16) y[u].w};   // round to nearest even
+            const float4 xx = ok[u] ? x[u] : make_float4(0.f, 0.f, 0.f, 0.f), yy = ok[u] ? y[u] : make_float4(0.f, 0.f, 0.f, 0.f);
+            const v8h hv = v8h{(_Float16) xx.x, (_Float16) xx.y, (_Float16) xx.z, (_Float16) xx.w,
+                               (_Float16) yy.x, (_Float16) yy.y, (_Float16) yy.z, (_Float16) yy.w};   // round to nearest even
             *(v8h *) (sq_lds + c * SQ_ROWB + d8 * 2) = hv;
         }
     }
@@ -253,30 +255,41 @@ __global__ __launch_bounds__(SQ_THREADS) void k_qsa_score_tiled(score_args a) {
         v8h kn[4];
         score_keys(a, m0 + 16 + ln, lg, kn);              // the next tile's keys (past the wave's last: unused)
         const int64_t ob = m0 + 4 * lg;
-#pragma unroll 2
-        for (int ct = 0; ct < n_ct; ct++) {
-            const int tl = ct * QT + (ln >> hb);          // query of this lane's column
-            const bool writer = h == 0 && tl < nt;
-            const uint8_t * qc = sq_lds + (ct * 16 + ln) * SQ_ROWB + 16 * lg;
-            v4f acc = {0.f, 0.f, 0.f, 0.f};
+        // 4 column tiles at a time: their 16 MFMAs interleave (each accumulator
+        // still takes the k-steps 0..3 in order: the same bits)
+        for (int ct0 = 0; ct0 < n_ct; ct0 += 4) {
+            v4f acc[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-            for (int st = 0; st < 4; st++)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr[st], *(const v8h *) (qc + 64 * st), acc, 0, 0, 0);
-            float v[4];
+            for (int st = 0; st < 4; st++) {
+                v8h bq[4];
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                v[r] = acc[r] > 0.f ? acc[r] : 0.f;       // relu per head
-                if (hb >= 1) v[r] += dpp_f<0xB1>(v[r]);   // quad_perm 1,0,3,2
-                if (hb >= 2) v[r] += dpp_f<0x4E>(v[r]);   // quad_perm 2,3,0,1
-                if (hb >= 3) v[r] += dpp_f<0x141>(v[r]);  // row_half_mirror
+                for (int c = 0; c < 4; c++)   // columns past n_ct read other LDS columns: unused
+                    bq[c] = *(const v8h *) (sq_lds + ((ct0 + c) * 16 + ln) * SQ_ROWB + 16 * lg + 64 * st);
+#pragma unroll
+                for (int c = 0; c < 4; c++) acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr[st], bq[c], acc[c], 0, 0, 0);
             }
-            float * srow = a.score + (size_t) (t0 + (writer ? tl : 0)) * ld;
-            if (writer && ob + 3 < n) {
-                *(float4 *) (srow + ob) = make_float4(v[0], v[1], v[2], v[3]);
-            } else if (writer) {
 #pragma unroll
-                for (int r = 0; r < 4; r++)
-                    if (ob + r < n) srow[ob + r] = v[r];
+            for (int c = 0; c < 4; c++) {
+                const int ct = ct0 + c;
+                if (ct >= n_ct) break;
+                const int tl = ct * QT + (ln >> hb);      // query of this lane's column
+                const bool writer = h == 0 && tl < nt;
+                float v[4];
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    v[r] = acc[c][r] > 0.f ? acc[c][r] : 0.f;   // relu per head
+                    if (hb >= 1) v[r] += dpp_f<0xB1>(v[r]);     // quad_perm 1,0,3,2
+                    if (hb >= 2) v[r] += dpp_f<0x4E>(v[r]);     // quad_perm 2,3,0,1
+                    if (hb >= 3) v[r] += dpp_f<0x141>(v[r]);    // row_half_mirror
+                }
+                float * srow = a.score + (size_t) (t0 + (writer ? tl : 0)) * ld;
+                if (writer && ob + 3 < n) {
+                    *(float4 *) (srow + ob) = make_float4(v[0], v[1], v[2], v[3]);
+                } else if (writer) {
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        if (ob + r < n) srow[ob + r] = v[r];
+                }
             }
         }
 #pragma unroll
@@ -779,10 +792,12 @@ extern "C" int qwfn_qsa_select_cells(const uint16_t * pool, size_t pool_nb1, int
             hipLaunchKernelGGL(k_qsa_score, dim3(gx, (unsigned) ny), dim3(SCORE_THREADS), 0, st, sa);
         } else {
             // more than 8 queries: the tiled kernel, 256 >> head_bits queries a
-            // workgroup; tiles a wave so that the grid holds about 512 workgroups
-            // (two a CU)
+            // workgroup; tiles a wave so that the grid fits in one round of two
+            // workgroups a CU (512): 520 workgroups at 16512 blocks x 512
+            // queries took 44 us, the 8 past the round costing a whole wave
+            // lifetime
             const int64_t nyq = (T + (SQ_COLS >> head_bits) - 1) / (SQ_COLS >> head_bits);
-            sa.mb = (int32_t) std::max<int64_t>(1, std::min<int64_t>(64, n_tile * nyq / (8 * 512)));
+            sa.mb = (int32_t) std::max<int64_t>(1, std::min<int64_t>(64, (n_tile * nyq + 8 * 512 - 1) / (8 * 512)));
             const int64_t per = SQ_THREADS / 64 * 16 * (int64_t) sa.mb;
             const unsigned gx = (unsigned) ((n_blocks + per - 1) / per);
             hipLaunchKernelGGL(k_qsa_score_tiled, dim3(gx, (unsigned) nyq), dim3(SQ_THREADS), SQ_COLS * SQ_ROWB, st, sa);
