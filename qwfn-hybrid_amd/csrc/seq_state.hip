@@ -33,6 +33,7 @@ namespace {
 
 constexpr size_t ARENA_ALIGN = 256;
 constexpr int    FILL_THREADS = 256;
+constexpr int    CELL_BATCH = 8;     // cells a thread loads before it sets their bits (one round of loads)
 constexpr uint16_t F16_ZERO = 0x0000u;
 constexpr uint16_t F16_NINF = 0xFC00u;
 
@@ -302,10 +303,21 @@ __global__ __launch_bounds__(FILL_THREADS) void k_qsa_mask(const int32_t * cells
     __syncthreads();
     const int32_t * crow = cells + (size_t) t * (size_t) cells_ld;
     bool bad = false;
-    for (int64_t j = threadIdx.x; j < width; j += FILL_THREADS) {
-        const int64_t c = crow[j];
-        if (c < 0 || c >= n_kv) { bad = true; continue; }
-        atomicOr(&sel[c >> 5], 1u << (c & 31));
+    // a thread's cells 8 at a time, all 8 loaded before any atomic
+    for (int64_t j0 = threadIdx.x; j0 < width; j0 += (int64_t) FILL_THREADS * CELL_BATCH) {
+        int32_t cb[CELL_BATCH];
+#pragma unroll
+        for (int u = 0; u < CELL_BATCH; u++) {
+            const int64_t j = j0 + (int64_t) u * FILL_THREADS;
+            cb[u] = j < width ? crow[j] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < CELL_BATCH; u++) {
+            if (j0 + (int64_t) u * FILL_THREADS >= width) break;
+            const int64_t c = cb[u];
+            if (c < 0 || c >= n_kv) { bad = true; continue; }
+            atomicOr(&sel[c >> 5], 1u << (c & 31));
+        }
     }
     if (__any(bad) && (threadIdx.x & 63) == 0 && status) atomicOr(status, DEVERR_SET_ROWS_INDEX);
     __syncthreads();
@@ -379,10 +391,21 @@ __global__ __launch_bounds__(FILL_THREADS) void k_qsa_visible(const int32_t * ce
     __syncthreads();
     const int32_t * crow = cells + (size_t) t * (size_t) cells_ld;
     bool bad = false;
-    for (int64_t j = threadIdx.x; j < width; j += FILL_THREADS) {
-        const int64_t c = crow[j];
-        if (c < 0 || c >= n_kv) { bad = true; continue; }
-        if (c < n_vis) atomicOr(&vis[c >> 5], 1u << (c & 31));
+    // a thread's cells 8 at a time, all 8 loaded before any atomic
+    for (int64_t j0 = threadIdx.x; j0 < width; j0 += (int64_t) FILL_THREADS * CELL_BATCH) {
+        int32_t cb[CELL_BATCH];
+#pragma unroll
+        for (int u = 0; u < CELL_BATCH; u++) {
+            const int64_t j = j0 + (int64_t) u * FILL_THREADS;
+            cb[u] = j < width ? crow[j] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < CELL_BATCH; u++) {
+            if (j0 + (int64_t) u * FILL_THREADS >= width) break;
+            const int64_t c = cb[u];
+            if (c < 0 || c >= n_kv) { bad = true; continue; }
+            if (c < n_vis) atomicOr(&vis[c >> 5], 1u << (c & 31));
+        }
     }
     if (__any(bad) && (threadIdx.x & 63) == 0 && status) atomicOr(status, DEVERR_SET_ROWS_INDEX);
     __syncthreads();
