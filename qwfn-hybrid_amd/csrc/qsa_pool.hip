@@ -53,12 +53,20 @@ struct pool_args {
 // times the weight, IMROPE at positions pos[0..3], F16 into pool row orow.
 __device__ __forceinline__ void pool_finish(const pool_args & a, float * x, int lane, const int32_t (&pos)[4], int64_t orow) {
     const int dim = a.dim;
+    // the weights first: their loads overlap the sum of squares
+    float wr[POOL_MAX_DIM / 64];
+#pragma unroll
+    for (int i = 0; i < POOL_MAX_DIM / 64; i++) wr[i] = lane + 64 * i < dim ? a.w[lane + 64 * i] : 0.f;
     double sq = 0.0;
     for (int d = lane; d < dim; d += 64) sq += (double) __fmul_rn(x[d], x[d]);
     sq = wave::wave_sum_d(sq);
     const float mean = (float) (sq / (double) dim);
     const float scale = 1.0f / sqrtf(__fadd_rn(mean, a.eps));
-    for (int d = lane; d < dim; d += 64) x[d] = __fmul_rn(__fmul_rn(x[d], scale), a.w[d]);
+#pragma unroll
+    for (int i = 0; i < POOL_MAX_DIM / 64; i++) {
+        const int d = lane + 64 * i;
+        if (d < dim) x[d] = __fmul_rn(__fmul_rn(x[d], scale), wr[i]);
+    }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     const bool ook = orow >= 0 && orow < a.pool_rows;
@@ -157,6 +165,7 @@ struct pool_steps_args {
     int32_t         T;
 };
 
+template <int NI>        // dim <= 64 * NI
 __global__ __launch_bounds__(POOL_WAVES * 64) void k_qsa_pool_steps(pool_steps_args s) {
     __shared__ float xs[POOL_WAVES][POOL_MAX_DIM];
     const pool_args & a = s.p;
@@ -165,11 +174,21 @@ __global__ __launch_bounds__(POOL_WAVES * 64) void k_qsa_pool_steps(pool_steps_a
     if (t >= s.T) return;
     const int dim = a.dim;
     // every position's write row and block: lane u holds position u's
+    // (both pointers, then both values: two round trips)
     int32_t wi = -1, bi = -1;
     if (lane < s.T) {
-        wi = s.k_raw ? *s.write_idx[lane] : -1;
-        bi = *s.blk_idx[lane];
+        const int32_t * pb = s.blk_idx[lane];
+        const int32_t * pw = s.k_raw ? s.write_idx[lane] : pb;
+        const int32_t w = *pw;
+        bi = *pb;
+        wi = s.k_raw ? w : -1;
     }
+    // this position's members (lane m holds member m's row) and block
+    // positions, fetched before the write so that their loads overlap it
+    const int32_t * mem = s.member_idx[t];
+    const int32_t my_row = lane < a.r ? mem[lane & 63] : -1;
+    int32_t pos[4];
+    for (int q = 0; q < 4; q++) pos[q] = s.blk_pos[t][q];
     const int32_t wrow = __shfl(wi, t), blk = __shfl(bi, t);
     if (s.k_raw) {
         const bool wok = wrow >= 0 && wrow < a.ic_rows;
@@ -181,28 +200,81 @@ __global__ __launch_bounds__(POOL_WAVES * 64) void k_qsa_pool_steps(pool_steps_a
     for (int u = t + 1; u < s.T; u++) last &= __shfl(bi, u) != blk;
     if (!last) return;
     float * x = xs[wv];
-    const int32_t * mem = s.member_idx[t];
-    for (int d = lane; d < dim; d += 64) {
-        float acc = 0.f;
-        for (int m = 0; m < a.r; m++) {
-            const int64_t row = mem[m];
-            int src = -1;                              // the latest position at or before t writing this row
-            for (int u = 0; u <= t; u++) src = __shfl(wi, u) == row ? u : src;
-            float v;
-            if (src >= 0) {
-                v = h2f(f2h(s.k_raw[(size_t) src * s.k_ld + d]));
-            } else if (row >= 0 && row < a.ic_rows) {
-                v = h2f(a.ic[(size_t) row * dim + d]);
-            } else {
-                v = 0.f;
-                if (d == lane && lane == 0) atomicOr(a.status, DEVERR_GET_ROWS_INDEX);
+    if (a.r <= 64) {
+        // lane m holds member m's row and the latest position at or before t
+        // that writes it; then every member's values are loaded, 8 members a
+        // round, before they are summed in member order (one round trip a
+        // round, not one a member)
+        int my_src = -1;
+        if (s.k_raw)
+            for (int u = 0; u <= t; u++) my_src = __shfl(wi, u) == my_row ? u : my_src;
+        // src >= 0 only with k_raw; otherwise the loads below read the norm
+        // weights' first word, which is discarded
+        const float * kr = s.k_raw ? s.k_raw : a.w;
+        float acc[NI];
+        bool bad_row = false;
+        for (int m0 = 0; m0 < a.r; m0 += 8) {
+            uint16_t vi[8][NI];
+            float vr[8][NI];
+            int src[8];
+            bool rok[8];
+#pragma unroll
+            for (int mm = 0; mm < 8; mm++) {
+                const int m = m0 + mm;
+                const bool mok = m < a.r;
+                const int32_t row = __shfl(my_row, m & 63);
+                src[mm] = __shfl(my_src, m & 63);
+                rok[mm] = row >= 0 && row < a.ic_rows;
+                bad_row |= mok && src[mm] < 0 && !rok[mm];
+#pragma unroll
+                for (int i = 0; i < NI; i++) {
+                    const int d = lane + 64 * i;
+                    const bool dok = mok && d < dim;
+                    // unconditional loads at a valid address (row 0, dim 0 otherwise)
+                    vi[mm][i] = a.ic[(dok && rok[mm]) ? (size_t) row * dim + d : 0];
+                    vr[mm][i] = kr[(dok && src[mm] >= 0) ? (size_t) src[mm] * s.k_ld + d : 0];
+                }
             }
-            acc = m == 0 ? v : __fadd_rn(acc, v);
+            // every load of the round is issued before the first sum waits;
+            // selects, not a break: a branch would put each member's loads
+            // behind the previous member's wait
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int mm = 0; mm < 8; mm++) {
+                const int m = m0 + mm;
+#pragma unroll
+                for (int i = 0; i < NI; i++) {
+                    const float v = src[mm] >= 0 ? h2f(f2h(vr[mm][i])) : (rok[mm] ? h2f(vi[mm][i]) : 0.f);
+                    const float sum = __fadd_rn(acc[i], v);
+                    acc[i] = m == 0 ? v : (m < a.r ? sum : acc[i]);
+                }
+            }
         }
-        x[d] = __fmul_rn(acc, a.inv_r);
+        if (bad_row && lane == 0) atomicOr(a.status, DEVERR_GET_ROWS_INDEX);
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+            if (lane + 64 * i < dim) x[lane + 64 * i] = __fmul_rn(acc[i], a.inv_r);
+    } else {
+        for (int d = lane; d < dim; d += 64) {
+            float acc = 0.f;
+            for (int m = 0; m < a.r; m++) {
+                const int64_t row = mem[m];
+                int src = -1;                              // the latest position at or before t writing this row
+                for (int u = 0; u <= t; u++) src = __shfl(wi, u) == row ? u : src;
+                float v;
+                if (src >= 0) {
+                    v = h2f(f2h(s.k_raw[(size_t) src * s.k_ld + d]));
+                } else if (row >= 0 && row < a.ic_rows) {
+                    v = h2f(a.ic[(size_t) row * dim + d]);
+                } else {
+                    v = 0.f;
+                    if (d == lane && lane == 0) atomicOr(a.status, DEVERR_GET_ROWS_INDEX);
+                }
+                acc = m == 0 ? v : __fadd_rn(acc, v);
+            }
+            x[d] = __fmul_rn(acc, a.inv_r);
+        }
     }
-    int32_t pos[4];
-    for (int q = 0; q < 4; q++) pos[q] = s.blk_pos[t][q];
     pool_finish(a, x, lane, pos, blk);
 }
 
@@ -435,8 +507,11 @@ extern "C" int qwfn_qsa_pool_decode_steps(uint16_t * idx_cache, int64_t ic_rows,
         sa.k_ld = (int64_t) (k_raw_nb1 / 4);
         sa.T = T;
         if (int rc = status_word(&sa.p.status)) return rc;
-        hipLaunchKernelGGL(k_qsa_pool_steps, dim3((unsigned) ((T + POOL_WAVES - 1) / POOL_WAVES)), dim3(POOL_WAVES * 64), 0,
-                           as_stream(stream), sa);
+        const dim3 grid((unsigned) ((T + POOL_WAVES - 1) / POOL_WAVES));
+        if (sa.p.dim <= 128)
+            hipLaunchKernelGGL(k_qsa_pool_steps<2>, grid, dim3(POOL_WAVES * 64), 0, as_stream(stream), sa);
+        else
+            hipLaunchKernelGGL(k_qsa_pool_steps<POOL_MAX_DIM / 64>, grid, dim3(POOL_WAVES * 64), 0, as_stream(stream), sa);
         return hip_check(hipGetLastError(), "qsa_pool_decode_steps launch");
     });
 }
