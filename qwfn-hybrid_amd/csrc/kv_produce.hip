@@ -99,58 +99,70 @@ __device__ __forceinline__ float fma_bf16_hi(uint32_t a, uint32_t b, float c) {
     return __builtin_fmaf(__builtin_bit_cast(float, a & 0xffff0000u), __builtin_bit_cast(float, b & 0xffff0000u), c);
 }
 
+// the hidden values 4 i .. 4 i + 3 of the call's rows, F32 -> F16 (or BF16),
+// into LDS
 template <bool BF16>
+__device__ __forceinline__ void stage_hidden4(uint16_t * cur16, int idx, const float4 & x) {
+    uint32_t lo, hi;
+    if constexpr (BF16) {
+        lo = f32_to_bf16(x.x) | (f32_to_bf16(x.y) << 16);
+        hi = f32_to_bf16(x.z) | (f32_to_bf16(x.w) << 16);
+    } else {
+        lo = __builtin_bit_cast(uint16_t, (_Float16) x.x) | ((uint32_t) __builtin_bit_cast(uint16_t, (_Float16) x.y) << 16);
+        hi = __builtin_bit_cast(uint16_t, (_Float16) x.z) | ((uint32_t) __builtin_bit_cast(uint16_t, (_Float16) x.w) << 16);
+    }
+    *(uint2 *) &cur16[idx] = make_uint2(lo, hi);
+}
+
+template <bool BF16, int NJ>      // NJ = ceil(n_embd / 512) weight loads a lane
 __global__ __launch_bounds__(KVP_WAVES * 64) void k_kv_project(kvp_args a) {
     extern __shared__ uint16_t cur16[];          // [T][n_embd] F16 (or BF16) hidden rows
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int T = a.T, E = a.n_embd;
     const int n_out = 2 * a.kv_dim;
+    constexpr int NT = KVP_WAVES * 64;
+    const int n4 = T * E / 4;
+    const uint32_t e4_mul = (uint32_t) (((uint64_t(1) << 32) + (uint64_t) (E / 4) - 1) / (uint64_t) (E / 4));
+    auto hidden4 = [&](int i) -> float4 {          // values 4 i .. 4 i + 3 (i < n4)
+        const int t = E / 4 == 1 ? i : (int) __umulhi((uint32_t) i, e4_mul);
+        const int e = 4 * (i - t * (E / 4));
+        return *(const float4 *) ((const char *) a.cur + (size_t) t * a.cur_nb1 + (size_t) e * 4);
+    };
 
-    // ---- wave w of block b takes output row 4b + w of [K rows | V rows];
-    //      lane l takes the 8 hidden values 8 l + 512 j: its weight loads go
-    //      out first, so that they overlap the staging below ----
+    // ---- the first 8 hidden loads a thread go out first (one round for up
+    //      to 8192 values), then the weights: wave w of block b takes output
+    //      row 4b + w of [K rows | V rows], lane l the 8 hidden values
+    //      8 l + 512 j. Loads return in order, so the conversion below waits
+    //      only for the hidden rows (mostly L2 hits) while the weights stream ----
+    float4 x[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        const int i = threadIdx.x + NT * u;
+        x[u] = hidden4(i < n4 ? i : n4 - 1);
+    }
     const int o = blockIdx.x * KVP_WAVES + wv;
     const int oc = o < n_out ? o : n_out - 1;
     const uint16_t * wrow = oc < a.kv_dim ? (const uint16_t *) ((const char *) a.wk + (size_t) oc * a.wk_nb1)
                                           : (const uint16_t *) ((const char *) a.wv + (size_t) (oc - a.kv_dim) * a.wv_nb1);
-    uint4 wq[KVP_MAX_EMBD / 512];
+    uint4 wq[NJ];
 #pragma unroll
-    for (int j = 0; j < KVP_MAX_EMBD / 512; j++)
-        if (512 * j < E) wq[j] = *(const uint4 *) (wrow + (512 * j + 8 * lane < E ? 512 * j + 8 * lane : 0));
-
-    // ---- the hidden rows, F32 -> F16 (ggml's conversion of src1): 4 values a
-    //      lane, 8 loads in flight before any conversion (one round for up to
-    //      8192 values) ----
-    {
-        const int n4 = T * E / 4;
-        const uint32_t e4_mul = (uint32_t) (((uint64_t(1) << 32) + (uint64_t) (E / 4) - 1) / (uint64_t) (E / 4));
-        for (int i0 = threadIdx.x; i0 < n4; i0 += KVP_WAVES * 64 * 8) {
-            float4 x[8];
-            int idx[8];
+    for (int j = 0; j < NJ; j++) wq[j] = *(const uint4 *) (wrow + (512 * j + 8 * lane < E ? 512 * j + 8 * lane : 0));
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const int i = i0 + KVP_WAVES * 64 * u;
-                const int ii = i < n4 ? i : n4 - 1;
-                const int t = E / 4 == 1 ? ii : (int) __umulhi((uint32_t) ii, e4_mul);
-                const int e = 4 * (ii - t * (E / 4));
-                x[u] = *(const float4 *) ((const char *) a.cur + (size_t) t * a.cur_nb1 + (size_t) e * 4);
-                idx[u] = i < n4 ? 4 * i : -1;
-            }
+    for (int u = 0; u < 8; u++) {
+        const int i = threadIdx.x + NT * u;
+        if (i < n4) stage_hidden4<BF16>(cur16, 4 * i, x[u]);
+    }
+    // more than 8192 values: the rest, 8 loads in flight at a time
+    for (int i0 = threadIdx.x + NT * 8; i0 < n4; i0 += NT * 8) {
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                if (idx[u] < 0) continue;
-                uint32_t lo, hi;
-                if constexpr (BF16) {
-                    lo = f32_to_bf16(x[u].x) | (f32_to_bf16(x[u].y) << 16);
-                    hi = f32_to_bf16(x[u].z) | (f32_to_bf16(x[u].w) << 16);
-                } else {
-                    lo = __builtin_bit_cast(uint16_t, (_Float16) x[u].x) |
-                         ((uint32_t) __builtin_bit_cast(uint16_t, (_Float16) x[u].y) << 16);
-                    hi = __builtin_bit_cast(uint16_t, (_Float16) x[u].z) |
-                         ((uint32_t) __builtin_bit_cast(uint16_t, (_Float16) x[u].w) << 16);
-                }
-                *(uint2 *) &cur16[idx[u]] = make_uint2(lo, hi);
-            }
+        for (int u = 0; u < 8; u++) {
+            const int i = i0 + NT * u;
+            x[u] = hidden4(i < n4 ? i : n4 - 1);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = i0 + NT * u;
+            if (i < n4) stage_hidden4<BF16>(cur16, 4 * i, x[u]);
         }
     }
     __syncthreads();
@@ -159,8 +171,8 @@ __global__ __launch_bounds__(KVP_WAVES * 64) void k_kv_project(kvp_args a) {
     float acc[KVP_MAX_T];
 #pragma unroll
     for (int t = 0; t < KVP_MAX_T; t++) acc[t] = 0.f;
-#pragma clang loop unroll(full)
-    for (int j = 0; j < KVP_MAX_EMBD / 512; j++) {
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
         const int e0 = 512 * j + 8 * lane;
         if (e0 >= E) continue;
         const uint32_t ww[4] = {wq[j].x, wq[j].y, wq[j].z, wq[j].w};
@@ -196,7 +208,9 @@ __global__ __launch_bounds__(KVP_WAVES * 64) void k_kv_project(kvp_args a) {
 __global__ __launch_bounds__(KVP_WAVES * 64) void k_kv_epilogue(kvp_args a) {
     __shared__ float head[KVP_WAVES][KVP_HD];
     __shared__ float csw[KVP_WAVES][2][KVP_MAX_PAIRS];
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    // wv through readfirstlane: the task, and so the position loads, are
+    // scalar, and the cos / sin need not wait for the vector loads
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int T = a.T;
     const int n_out = 2 * a.kv_dim;
     const int half = a.rp.n_dims / 2;
@@ -208,10 +222,19 @@ __global__ __launch_bounds__(KVP_WAVES * 64) void k_kv_epilogue(kvp_args a) {
         const bool is_k = hh < a.nh_kv;
         const int h = is_k ? hh : hh - a.nh_kv;
         const float * src = a.rows + t * n_out + (is_k ? 0 : a.kv_dim) + h * KVP_HD;
-        float x[4];
+        // every load first (the row, the norm weight, the positions), then the
+        // rope's cos / sin while they are in flight: one round trip, not three
+        float x[4], nw[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) x[i] = src[4 * lane + i];
+#pragma unroll
+        for (int i = 0; i < 4; i++) nw[i] = a.k_norm_w[4 * lane + i];
+        int32_t pos[4];
+#pragma unroll
+        for (int s = 0; s < 4; s++) pos[s] = a.pos[s * T + t];
         if (is_k) {
+            // lane k computes pair k's cos / sin
+            for (int k = lane; k < half; k += 64) rope_cos_sin(a.rp, pos, k, &csw[wv][0][k], &csw[wv][1][k]);
             // RMS norm (squares summed in double), times the weight
             double sq = 0.0;
 #pragma unroll
@@ -221,18 +244,12 @@ __global__ __launch_bounds__(KVP_WAVES * 64) void k_kv_epilogue(kvp_args a) {
             const float scale = 1.0f / sqrtf(__fadd_rn(mean, a.eps));
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                x[i] = __fmul_rn(__fmul_rn(x[i], scale), a.k_norm_w[4 * lane + i]);
+                x[i] = __fmul_rn(__fmul_rn(x[i], scale), nw[i]);
                 hx[4 * lane + i] = x[i];
             }
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-            // rope: lane k computes pair k's cos / sin, then each lane rotates
-            // its values 4 lane + i that lie in the first n_dims
-            int32_t pos[4];
-            for (int s = 0; s < 4; s++) pos[s] = a.pos[s * T + t];
-            for (int k = lane; k < half; k += 64) rope_cos_sin(a.rp, pos, k, &csw[wv][0][k], &csw[wv][1][k]);
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            // each lane rotates its values 4 lane + i that lie in the first n_dims
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int d = 4 * lane + i;
@@ -256,6 +273,30 @@ __global__ __launch_bounds__(KVP_WAVES * 64) void k_kv_epilogue(kvp_args a) {
         qp[1] = (uint16_t) (q4 >> 16);
         if ((lane & 7) == 0) *(uint16_t *) bp = d16;
     }
+}
+
+constexpr int KVP_MAX_NJ = KVP_MAX_EMBD / 512;
+
+// k_kv_project<BF16, nj> for nj = NJ .. KVP_MAX_NJ
+template <bool BF16, int NJ = 1>
+void launch_project(int nj, dim3 grid, size_t lds, hipStream_t stream, const kvp_args & a) {
+    if constexpr (NJ <= KVP_MAX_NJ) {
+        if (nj == NJ) hipLaunchKernelGGL((k_kv_project<BF16, NJ>), grid, dim3(KVP_WAVES * 64), lds, stream, a);
+        else          launch_project<BF16, NJ + 1>(nj, grid, lds, stream, a);
+    }
+}
+
+// the hidden rows of up to 16 tokens take more than 64 KB of LDS
+template <bool BF16, int NJ = 1>
+int allow_project_lds() {
+    if constexpr (NJ <= KVP_MAX_NJ) {
+        if (int rc = hip_check(hipFuncSetAttribute((const void *) k_kv_project<BF16, NJ>,
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024),
+                               "hipFuncSetAttribute"))
+            return rc;
+        return allow_project_lds<BF16, NJ + 1>();
+    }
+    return 0;
 }
 
 }  // namespace
@@ -327,19 +368,17 @@ extern "C" int qwfn_kv_produce_q8_0(const qwfn_tensor * cur, const qwfn_tensor *
         if (!rows_ptr[dev]) {
             void * p = nullptr;
             if (int rc = hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(g_kvp_rows)), "hipGetSymbolAddress")) return rc;
-            // the hidden rows of up to 16 tokens take more than 64 KB of LDS
-            for (const void * f : {(const void *) k_kv_project<false>, (const void *) k_kv_project<true>})
-                if (int rc = hip_check(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024),
-                                       "hipFuncSetAttribute"))
-                    return rc;
+            if (int rc = allow_project_lds<false>()) return rc;
+            if (int rc = allow_project_lds<true>()) return rc;
             rows_ptr[dev] = (float *) p;
         }
         a.rows = rows_ptr[dev];
         const int64_t n_out = 2 * kv_dim;
         const int64_t blocks = (n_out + KVP_WAVES - 1) / KVP_WAVES;
         const size_t lds = (size_t) T * E * 2;
-        if (bf16) hipLaunchKernelGGL(k_kv_project<true>, dim3((unsigned) blocks), dim3(KVP_WAVES * 64), lds, as_stream(stream), a);
-        else      hipLaunchKernelGGL(k_kv_project<false>, dim3((unsigned) blocks), dim3(KVP_WAVES * 64), lds, as_stream(stream), a);
+        const int nj = (int) ((E + 511) / 512);
+        if (bf16) launch_project<true>(nj, dim3((unsigned) blocks), lds, as_stream(stream), a);
+        else      launch_project<false>(nj, dim3((unsigned) blocks), lds, as_stream(stream), a);
         if (int rc = hip_check(hipGetLastError(), "kv_produce launch")) return rc;
         const int64_t tasks = T * 2 * (kv_dim / KVP_HD);
         hipLaunchKernelGGL(k_kv_epilogue, dim3((unsigned) ((tasks + KVP_WAVES - 1) / KVP_WAVES)), dim3(KVP_WAVES * 64), 0,
