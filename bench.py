@@ -362,13 +362,20 @@ def measure_qsa_step_rows(K, torch, np, dev, gen, n_layers: int = 12) -> dict:
                               qds[t].blk_idx, L["knw_idx"], L["pool"])
         tail(L)
 
-    def step(k):
+    def step_two(k):
         # the step's positions batched: one prepare launch, one pool-decode launch
         L = layers[k % n_layers]
         S.qsa_decode_prepare_steps(qds, n_past)
         K.qsa_pool_decode_steps(L["ic"], k_raw, qds, L["knw_idx"], L["pool"])
         tail(L)
+
+    def step(k):
+        # the step's preparation and pooling in one launch
+        L = layers[k % n_layers]
+        S.qsa_decode_prepare_pool_steps(qds, n_past, L["ic"], k_raw, L["knw_idx"], L["pool"])
+        tail(L)
     us_chained = timed_graph(torch, step_chained, n_layers, 10)
+    us_two = timed_graph(torch, step_two, n_layers, 10)
     us = timed_graph(torch, step, n_layers, 10)
     lists = cells.cpu().numpy()
     union = int(np.unique(lists).size)
@@ -378,11 +385,13 @@ def measure_qsa_step_rows(K, torch, np, dev, gen, n_layers: int = 12) -> dict:
     rows["qsa_verify_step_T3"] = {
         "us_per_layer": round(us, 2), "bytes_per_layer": step_bytes, "GBs": gbs(step_bytes, us),
         "frac": frac(step_bytes, us), "blocks": nbm, "k_blocks": kb, "cells_per_position": nc,
-        "union_cells": union, "launches_per_layer": 1 + 1 + 2 + 2 + 2,
+        "union_cells": union, "launches_per_layer": 1 + 2 + 2 + 2,
+        "us_per_layer_prepare_then_pool": round(us_two, 2),
         "us_per_layer_positions_one_a_call": round(us_chained, 2),
-        "what": "prepare steps, pool decode steps (one launch each for the 3 positions), select (3 queries), "
-                "K/V produce, gated query-cells attention + merge; us_per_layer_positions_one_a_call: prepare x3 "
-                "and pool decode x3 as the reference issues them"}
+        "what": "the 3 positions' inputs and index pooling (one launch), select (3 queries), K/V produce, gated "
+                "query-cells attention + merge; us_per_layer_prepare_then_pool: the inputs and the pooling in a "
+                "launch each; us_per_layer_positions_one_a_call: prepare x3 and pool decode x3 as the reference "
+                "issues them"}
 
     # ---- the attention alone at the reference's decode shape ----
     sel = cells.clone()

@@ -408,6 +408,20 @@ int qwfn_qsa_pool_decode_steps(uint16_t * idx_cache, int64_t ic_rows, const floa
                                const qwfn_qsa_inputs * qd, int32_t T, const float * k_norm_w, uint16_t * pool,
                                int64_t pool_rows, const qwfn_qsa_pool_cfg * cfg, void * stream);
 
+/* qwfn_qsa_decode_prepare_steps(qd, T, n_past) followed by
+ * qwfn_qsa_pool_decode_steps(idx_cache, ic_rows, k_raw, k_raw_nb1, qd, T,
+ * k_norm_w, pool, pool_rows, cfg), in one launch: the same bias rows, small
+ * inputs, index cache rows and pooled rows. The pooling takes its indices in
+ * the closed forms the preparation writes (position p = n_past + t writes
+ * index row p of block p / ratio, whose members are the rows
+ * (p / ratio) ratio + m) instead of reading them back. No counterpart in the
+ * reference, whose engine fills these inputs on the host (qwfn_engine.cpp:
+ * 1072-1105) before the graph pools (qwfn_graph.cpp:529-554); for engines
+ * that run the step's preparation and pooling back to back. */
+int qwfn_qsa_decode_prepare_pool_steps(const qwfn_qsa_inputs * qd, int32_t T, int32_t n_past, uint16_t * idx_cache,
+                                       int64_t ic_rows, const float * k_raw, size_t k_raw_nb1, const float * k_norm_w,
+                                       uint16_t * pool, int64_t pool_rows, const qwfn_qsa_pool_cfg * cfg, void * stream);
+
 /* The full bias rewrite of qsa_pool_rebuild (qwfn_engine.cpp:1115-1120):
  * 0 for blocks < (n_past+1)/ratio, the block of n_past 0 or 1e9, -inf after.
  * n_past = -1 writes -inf everywhere (engine::reset, init_qsa_tables). */

@@ -10,11 +10,13 @@
 // normed (squares summed in double), times the k_norm weight, roped at the
 // block's first cell (all four sections), rounded to F16. One wave per block:
 // the block's key sits in LDS; lane k < n_dims/2 rotates pair k.
+#include "qsa_steps.h"
 #include "qwfn_common.h"
 #include "qwfn_state.h"
 #include "rope_device.h"
 #include "wave_ops.h"
 
+#include <algorithm>
 #include <cmath>
 
 namespace qwfn {
@@ -48,15 +50,26 @@ struct pool_args {
     uint32_t *       status;
 };
 
+// What the pooled block's tail needs besides the member mean, which a caller
+// may fetch while the members load: the norm weights (lane + 64 i) and the
+// cos / sin of rope pair `lane` at positions pos[0..3] (lanes past the pairs:
+// pair 0's, unused).
+struct pool_tail_in {
+    float wr[POOL_MAX_DIM / 64];
+    float c, s;
+};
+__device__ __forceinline__ void pool_prefetch(const pool_args & a, int lane, const int32_t (&pos)[4], pool_tail_in & in) {
+#pragma unroll
+    for (int i = 0; i < POOL_MAX_DIM / 64; i++) in.wr[i] = lane + 64 * i < a.dim ? a.w[lane + 64 * i] : 0.f;
+    rope_cos_sin(a.rp, pos, lane < a.rp.n_dims / 2 ? lane : 0, &in.c, &in.s);
+}
+
 // The pooled block's tail, for the mean x[0 .. dim) of its member rows (one
 // wave): RMS norm (the squares in float, summed in double across the wave),
-// times the weight, IMROPE at positions pos[0..3], F16 into pool row orow.
-__device__ __forceinline__ void pool_finish(const pool_args & a, float * x, int lane, const int32_t (&pos)[4], int64_t orow) {
+// times the weight, IMROPE, F16 into pool row orow.
+__device__ __forceinline__ void pool_finish_with(const pool_args & a, float * x, int lane, int64_t orow,
+                                                 const pool_tail_in & in) {
     const int dim = a.dim;
-    // the weights first: their loads overlap the sum of squares
-    float wr[POOL_MAX_DIM / 64];
-#pragma unroll
-    for (int i = 0; i < POOL_MAX_DIM / 64; i++) wr[i] = lane + 64 * i < dim ? a.w[lane + 64 * i] : 0.f;
     double sq = 0.0;
     for (int d = lane; d < dim; d += 64) sq += (double) __fmul_rn(x[d], x[d]);
     sq = wave::wave_sum_d(sq);
@@ -65,7 +78,7 @@ __device__ __forceinline__ void pool_finish(const pool_args & a, float * x, int 
 #pragma unroll
     for (int i = 0; i < POOL_MAX_DIM / 64; i++) {
         const int d = lane + 64 * i;
-        if (d < dim) x[d] = __fmul_rn(__fmul_rn(x[d], scale), wr[i]);
+        if (d < dim) x[d] = __fmul_rn(__fmul_rn(x[d], scale), in.wr[i]);
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
@@ -77,13 +90,18 @@ __device__ __forceinline__ void pool_finish(const pool_args & a, float * x, int 
     uint16_t * out = a.pool + (size_t) orow * dim;
     const int half = a.rp.n_dims / 2;
     if (lane < half) {
-        float c, s, y0, y1;
-        rope_cos_sin(a.rp, pos, lane, &c, &s);
-        rope_rotate(x[lane], x[lane + half], c, s, &y0, &y1);
+        float y0, y1;
+        rope_rotate(x[lane], x[lane + half], in.c, in.s, &y0, &y1);
         out[lane] = f2h(y0);
         out[lane + half] = f2h(y1);
     }
     for (int d = a.rp.n_dims + lane; d < dim; d += 64) out[d] = f2h(x[d]);
+}
+
+__device__ __forceinline__ void pool_finish(const pool_args & a, float * x, int lane, const int32_t (&pos)[4], int64_t orow) {
+    pool_tail_in in;
+    pool_prefetch(a, lane, pos, in);
+    pool_finish_with(a, x, lane, orow, in);
 }
 
 template <bool DECODE>
@@ -165,59 +183,86 @@ struct pool_steps_args {
     int32_t         T;
 };
 
-template <int NI>        // dim <= 64 * NI
-__global__ __launch_bounds__(POOL_WAVES * 64) void k_qsa_pool_steps(pool_steps_args s) {
-    __shared__ float xs[POOL_WAVES][POOL_MAX_DIM];
+// One position's wave of the step's pooling (position t, lane `lane`, x its
+// LDS row of dim floats). The indices come from the device inputs that the
+// preparation wrote (CLOSED false) or from their closed forms of n_past
+// (CLOSED true, qsa_steps.h: position p = n_past + t writes row p into block
+// p / r, whose members are the rows (p / r) r + m and whose rope positions
+// are (p / r) r), the same values without the round trips that read them.
+template <int NI, bool CLOSED>      // dim <= 64 * NI
+__device__ __forceinline__ void pool_step_wave(const pool_steps_args & s, int32_t n_past, float * x, int t, int lane) {
     const pool_args & a = s.p;
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int t = (int) blockIdx.x * POOL_WAVES + wv;
-    if (t >= s.T) return;
     const int dim = a.dim;
-    // every position's write row and block: lane u holds position u's
-    // (both pointers, then both values: two round trips)
+    // every position's write row and block (lane u holds position u's), this
+    // position's members (lane m holds member m's row) and block positions,
+    // all before the write so that their loads overlap it
     int32_t wi = -1, bi = -1;
-    if (lane < s.T) {
-        const int32_t * pb = s.blk_idx[lane];
-        const int32_t * pw = s.k_raw ? s.write_idx[lane] : pb;
-        const int32_t w = *pw;
-        bi = *pb;
-        wi = s.k_raw ? w : -1;
-    }
-    // this position's members (lane m holds member m's row) and block
-    // positions, fetched before the write so that their loads overlap it
-    const int32_t * mem = s.member_idx[t];
-    const int32_t my_row = lane < a.r ? mem[lane & 63] : -1;
+    int32_t my_row = -1;
     int32_t pos[4];
-    for (int q = 0; q < 4; q++) pos[q] = s.blk_pos[t][q];
-    const int32_t wrow = __shfl(wi, t), blk = __shfl(bi, t);
-    if (s.k_raw) {
-        const bool wok = wrow >= 0 && wrow < a.ic_rows;
-        for (int d = lane; d < dim; d += 64)
-            if (wok) a.ic[(size_t) wrow * dim + d] = f2h(s.k_raw[(size_t) t * s.k_ld + d]);
-        if (!wok && lane == 0) atomicOr(a.status, DEVERR_SET_ROWS_INDEX);
+    const int32_t * mem = nullptr;
+    int64_t mem0 = 0;                   // CLOSED: member m is row mem0 + m
+    if constexpr (CLOSED) {
+        if (lane < s.T) {
+            wi = s.k_raw ? n_past + lane : -1;
+            bi = (int32_t) (((int64_t) n_past + lane) / a.r);
+        }
+        mem0 = (((int64_t) n_past + t) / a.r) * a.r;
+        my_row = lane < a.r ? (int32_t) (mem0 + lane) : -1;
+        for (int q = 0; q < 4; q++) pos[q] = (int32_t) mem0;
+    } else {
+        // both pointers, then both values: two round trips
+        if (lane < s.T) {
+            const int32_t * pb = s.blk_idx[lane];
+            const int32_t * pw = s.k_raw ? s.write_idx[lane] : pb;
+            const int32_t w = *pw;
+            bi = *pb;
+            wi = s.k_raw ? w : -1;
+        }
+        mem = s.member_idx[t];
+        my_row = lane < a.r ? mem[lane & 63] : -1;
+        for (int q = 0; q < 4; q++) pos[q] = s.blk_pos[t][q];
     }
+    const int32_t wrow = __shfl(wi, t), blk = __shfl(bi, t);
+    // src >= 0 only with k_raw; otherwise the loads from kr read the norm
+    // weights' first word, which is discarded
+    const auto kr = gptr(s.k_raw ? s.k_raw : a.w);
+    const auto ic = gptr(a.ic);
+    // the written key row, loaded first
+    float kv[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) kv[i] = kr[(s.k_raw && lane + 64 * i < dim) ? (size_t) t * s.k_ld + lane + 64 * i : 0];
+    auto write_row = [&]() {
+        if (!s.k_raw) return;
+        const bool wok = wrow >= 0 && wrow < a.ic_rows;
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+            if (wok && lane + 64 * i < dim) ic[(size_t) wrow * dim + lane + 64 * i] = f2h(kv[i]);
+        if (!wok && lane == 0) atomicOr(a.status, DEVERR_SET_ROWS_INDEX);
+    };
     bool last = true;
     for (int u = t + 1; u < s.T; u++) last &= __shfl(bi, u) != blk;
-    if (!last) return;
-    float * x = xs[wv];
+    if (!last) {
+        write_row();
+        return;
+    }
     if (a.r <= 64) {
         // lane m holds member m's row and the latest position at or before t
         // that writes it; then every member's values are loaded, 8 members a
         // round, before they are summed in member order (one round trip a
-        // round, not one a member)
+        // round, not one a member). The first round's loads go out before the
+        // write, the tail's weights and cos / sin are fetched behind them: a
+        // member row that this call writes is taken from k_raw, so the order of
+        // the write and these reads does not matter.
         int my_src = -1;
         if (s.k_raw)
             for (int u = 0; u <= t; u++) my_src = __shfl(wi, u) == my_row ? u : my_src;
-        // src >= 0 only with k_raw; otherwise the loads below read the norm
-        // weights' first word, which is discarded
-        const float * kr = s.k_raw ? s.k_raw : a.w;
         float acc[NI];
         bool bad_row = false;
-        for (int m0 = 0; m0 < a.r; m0 += 8) {
-            uint16_t vi[8][NI];
-            float vr[8][NI];
-            int src[8];
-            bool rok[8];
+        uint16_t vi[8][NI];
+        float vr[8][NI];
+        int src[8];
+        bool rok[8];
+        auto load_round = [&](int m0) {
 #pragma unroll
             for (int mm = 0; mm < 8; mm++) {
                 const int m = m0 + mm;
@@ -231,14 +276,14 @@ __global__ __launch_bounds__(POOL_WAVES * 64) void k_qsa_pool_steps(pool_steps_a
                     const int d = lane + 64 * i;
                     const bool dok = mok && d < dim;
                     // unconditional loads at a valid address (row 0, dim 0 otherwise)
-                    vi[mm][i] = a.ic[(dok && rok[mm]) ? (size_t) row * dim + d : 0];
+                    vi[mm][i] = ic[(dok && rok[mm]) ? (size_t) row * dim + d : 0];
                     vr[mm][i] = kr[(dok && src[mm] >= 0) ? (size_t) src[mm] * s.k_ld + d : 0];
                 }
             }
-            // every load of the round is issued before the first sum waits;
-            // selects, not a break: a branch would put each member's loads
-            // behind the previous member's wait
-            __builtin_amdgcn_sched_barrier(0);
+        };
+        // selects, not a break: a branch would put each member's loads behind
+        // the previous member's wait
+        auto sum_round = [&](int m0) {
 #pragma unroll
             for (int mm = 0; mm < 8; mm++) {
                 const int m = m0 + mm;
@@ -249,16 +294,30 @@ __global__ __launch_bounds__(POOL_WAVES * 64) void k_qsa_pool_steps(pool_steps_a
                     acc[i] = m == 0 ? v : (m < a.r ? sum : acc[i]);
                 }
             }
+        };
+        load_round(0);
+        pool_tail_in in;
+        pool_prefetch(a, lane, pos, in);
+        write_row();
+        __builtin_amdgcn_sched_barrier(0);
+        sum_round(0);
+        for (int m0 = 8; m0 < a.r; m0 += 8) {
+            load_round(m0);
+            __builtin_amdgcn_sched_barrier(0);        // every load of the round before the first sum waits
+            sum_round(m0);
         }
         if (bad_row && lane == 0) atomicOr(a.status, DEVERR_GET_ROWS_INDEX);
 #pragma unroll
         for (int i = 0; i < NI; i++)
             if (lane + 64 * i < dim) x[lane + 64 * i] = __fmul_rn(acc[i], a.inv_r);
+        pool_finish_with(a, x, lane, blk, in);
+        return;
     } else {
+        write_row();
         for (int d = lane; d < dim; d += 64) {
             float acc = 0.f;
             for (int m = 0; m < a.r; m++) {
-                const int64_t row = mem[m];
+                const int64_t row = CLOSED ? mem0 + m : (int64_t) mem[m];
                 int src = -1;                              // the latest position at or before t writing this row
                 for (int u = 0; u <= t; u++) src = __shfl(wi, u) == row ? u : src;
                 float v;
@@ -276,6 +335,38 @@ __global__ __launch_bounds__(POOL_WAVES * 64) void k_qsa_pool_steps(pool_steps_a
         }
     }
     pool_finish(a, x, lane, pos, blk);
+}
+
+template <int NI>
+__global__ __launch_bounds__(POOL_WAVES * 64) void k_qsa_pool_steps(pool_steps_args s) {
+    __shared__ float xs[POOL_WAVES][POOL_MAX_DIM];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int t = (int) blockIdx.x * POOL_WAVES + wv;
+    if (t < s.T) pool_step_wave<NI, false>(s, 0, xs[wv], t, lane);
+}
+
+// The step's preparation and pooling in one launch: workgroups below
+// pool_blocks pool (4 positions each, indices in closed form), the others
+// write the bias rows and the small inputs (prepare_steps_range). Neither
+// part reads what the other writes.
+struct prep_pool_args {
+    pool_steps_args     s;
+    qsa_prep_steps_args prep;
+    int32_t             pool_blocks;
+};
+
+template <int NI>
+__global__ __launch_bounds__(POOL_WAVES * 64) void k_qsa_prepare_pool_steps(prep_pool_args a) {
+    __shared__ float xs[POOL_WAVES][POOL_MAX_DIM];
+    if ((int) blockIdx.x < a.pool_blocks) {
+        const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+        const int t = (int) blockIdx.x * POOL_WAVES + wv;
+        if (t < a.s.T) pool_step_wave<NI, true>(a.s, a.prep.n_past, xs[wv], t, lane);
+        return;
+    }
+    constexpr int64_t NT = POOL_WAVES * 64;
+    prepare_steps_range(a.prep, (int64_t) (blockIdx.x - a.pool_blocks) * NT + threadIdx.x,
+                        (int64_t) (gridDim.x - a.pool_blocks) * NT);
 }
 
 // The rebuild with 16-byte lanes, for dim / 8 a power of two and 16-byte
@@ -480,39 +571,81 @@ extern "C" int qwfn_qsa_pool_decode(uint16_t * idx_cache, int64_t ic_rows, const
     });
 }
 
+namespace qwfn {
+namespace {
+
+// Checks the pooling arguments of a step (qwfn_qsa_pool_decode_steps) and
+// fills the kernel arguments; `who` names the entry point in the messages,
+// `pointers`: the kernel reads the indices from qd (else their closed forms).
+int pool_steps_fill(uint16_t * idx_cache, int64_t ic_rows, const float * k_raw, size_t k_raw_nb1, const qwfn_qsa_inputs * qd,
+                    int32_t T, const float * k_norm_w, uint16_t * pool, int64_t pool_rows, const qwfn_qsa_pool_cfg * cfg,
+                    const char * who, bool pointers, pool_steps_args * sa) {
+    if (!qd) return set_error2(QWFN_EINVAL, who, ": NULL inputs");
+    if (T < 1 || T > POOL_MAX_T) return set_error2(QWFN_ENOTSUP, who, ": 1 to 16 positions");
+    *sa = pool_steps_args{};
+    if (int rc = pool_cfg_args(cfg, qd[0].ratio, k_norm_w, &sa->p)) return rc;
+    if (!idx_cache || !pool) return set_error2(QWFN_EINVAL, who, ": NULL pointer");
+    if (ic_rows < 1 || pool_rows < 1) return set_error2(QWFN_EINVAL, who, ": empty cache");
+    if (!is_aligned(idx_cache, 2) || !is_aligned(pool, 2) || !is_aligned(k_norm_w, 4) ||
+        (k_raw && (!is_aligned(k_raw, 4) || k_raw_nb1 % 4 || k_raw_nb1 < (size_t) sa->p.dim * 4)))
+        return set_error2(QWFN_EALIGN, who, ": element alignment, or k_raw rows shorter than idx_dim");
+    for (int t = 0; t < T; t++) {
+        if (qd[t].ratio != qd[0].ratio) return set_error2(QWFN_EINVAL, who, ": positions of different ratios");
+        if (!pointers) continue;
+        if (!qd[t].member_idx || !qd[t].blk_pos || !qd[t].blk_idx || (k_raw && !qd[t].write_idx))
+            return set_error2(QWFN_EINVAL, who, ": NULL tensor");
+        sa->write_idx[t] = qd[t].write_idx;
+        sa->member_idx[t] = qd[t].member_idx;
+        sa->blk_pos[t] = qd[t].blk_pos;
+        sa->blk_idx[t] = qd[t].blk_idx;
+    }
+    sa->p.ic = idx_cache; sa->p.ic_rows = ic_rows; sa->p.pool = pool; sa->p.pool_rows = pool_rows;
+    sa->k_raw = k_raw;
+    sa->k_ld = (int64_t) (k_raw_nb1 / 4);
+    sa->T = T;
+    return status_word(&sa->p.status);
+}
+
+}  // namespace
+}  // namespace qwfn
+
 extern "C" int qwfn_qsa_pool_decode_steps(uint16_t * idx_cache, int64_t ic_rows, const float * k_raw, size_t k_raw_nb1,
                                           const qwfn_qsa_inputs * qd, int32_t T, const float * k_norm_w, uint16_t * pool,
                                           int64_t pool_rows, const qwfn_qsa_pool_cfg * cfg, void * stream) {
     return ::qwfn::abi_call("qsa_pool_decode_steps", [&]() -> int {
-        if (!qd) return set_error(QWFN_EINVAL, "qsa_pool_decode_steps: NULL inputs");
-        if (T < 1 || T > POOL_MAX_T) return set_error(QWFN_ENOTSUP, "qsa_pool_decode_steps: 1 to 16 positions");
-        pool_steps_args sa{};
-        if (int rc = pool_cfg_args(cfg, qd[0].ratio, k_norm_w, &sa.p)) return rc;
-        if (!idx_cache || !pool) return set_error(QWFN_EINVAL, "qsa_pool_decode_steps: NULL pointer");
-        if (ic_rows < 1 || pool_rows < 1) return set_error(QWFN_EINVAL, "qsa_pool_decode_steps: empty cache");
-        if (!is_aligned(idx_cache, 2) || !is_aligned(pool, 2) || !is_aligned(k_norm_w, 4) ||
-            (k_raw && (!is_aligned(k_raw, 4) || k_raw_nb1 % 4 || k_raw_nb1 < (size_t) sa.p.dim * 4)))
-            return set_error(QWFN_EALIGN, "qsa_pool_decode_steps: element alignment, or k_raw rows shorter than idx_dim");
-        for (int t = 0; t < T; t++) {
-            if (qd[t].ratio != qd[0].ratio) return set_error(QWFN_EINVAL, "qsa_pool_decode_steps: positions of different ratios");
-            if (!qd[t].member_idx || !qd[t].blk_pos || !qd[t].blk_idx || (k_raw && !qd[t].write_idx))
-                return set_error(QWFN_EINVAL, "qsa_pool_decode_steps: NULL tensor");
-            sa.write_idx[t] = qd[t].write_idx;
-            sa.member_idx[t] = qd[t].member_idx;
-            sa.blk_pos[t] = qd[t].blk_pos;
-            sa.blk_idx[t] = qd[t].blk_idx;
-        }
-        sa.p.ic = idx_cache; sa.p.ic_rows = ic_rows; sa.p.pool = pool; sa.p.pool_rows = pool_rows;
-        sa.k_raw = k_raw;
-        sa.k_ld = (int64_t) (k_raw_nb1 / 4);
-        sa.T = T;
-        if (int rc = status_word(&sa.p.status)) return rc;
+        pool_steps_args sa;
+        if (int rc = pool_steps_fill(idx_cache, ic_rows, k_raw, k_raw_nb1, qd, T, k_norm_w, pool, pool_rows, cfg,
+                                     "qsa_pool_decode_steps", true, &sa))
+            return rc;
         const dim3 grid((unsigned) ((T + POOL_WAVES - 1) / POOL_WAVES));
         if (sa.p.dim <= 128)
             hipLaunchKernelGGL(k_qsa_pool_steps<2>, grid, dim3(POOL_WAVES * 64), 0, as_stream(stream), sa);
         else
             hipLaunchKernelGGL(k_qsa_pool_steps<POOL_MAX_DIM / 64>, grid, dim3(POOL_WAVES * 64), 0, as_stream(stream), sa);
         return hip_check(hipGetLastError(), "qsa_pool_decode_steps launch");
+    });
+}
+
+extern "C" int qwfn_qsa_decode_prepare_pool_steps(const qwfn_qsa_inputs * qd, int32_t T, int32_t n_past, uint16_t * idx_cache,
+                                                  int64_t ic_rows, const float * k_raw, size_t k_raw_nb1,
+                                                  const float * k_norm_w, uint16_t * pool, int64_t pool_rows,
+                                                  const qwfn_qsa_pool_cfg * cfg, void * stream) {
+    return ::qwfn::abi_call("qsa_decode_prepare_pool_steps", [&]() -> int {
+        prep_pool_args a{};
+        if (int rc = prep_steps_args(qd, T, n_past, "qsa_decode_prepare_pool_steps", &a.prep)) return rc;
+        if (int rc = pool_steps_fill(idx_cache, ic_rows, k_raw, k_raw_nb1, qd, T, k_norm_w, pool, pool_rows, cfg,
+                                     "qsa_decode_prepare_pool_steps", false, &a.s))
+            return rc;
+        a.pool_blocks = (T + POOL_WAVES - 1) / POOL_WAVES;
+        const int64_t n = std::max<int64_t>(qd[0].n_blocks_max, T);
+        const int64_t prep_blocks = std::max<int64_t>(1, std::min<int64_t>((n + POOL_WAVES * 64 - 1) / (POOL_WAVES * 64), 4096));
+        const dim3 grid((unsigned) (a.pool_blocks + prep_blocks));
+        if (a.s.p.dim <= 128)
+            hipLaunchKernelGGL(k_qsa_prepare_pool_steps<2>, grid, dim3(POOL_WAVES * 64), 0, as_stream(stream), a);
+        else
+            hipLaunchKernelGGL(k_qsa_prepare_pool_steps<POOL_MAX_DIM / 64>, grid, dim3(POOL_WAVES * 64), 0,
+                               as_stream(stream), a);
+        return hip_check(hipGetLastError(), "qsa_decode_prepare_pool_steps launch");
     });
 }
 

@@ -25,6 +25,14 @@ constexpr uint32_t DEVERR_GET_ROWS_INDEX = 1u << 1;
 __device__ __forceinline__ uint32_t udiv(uint32_t x, uint32_t d, uint32_t m) {
     return d == 1 ? x : __umulhi(x, m);
 }
+// A pointer the compiler cannot place (one held in a struct of pointers, or
+// a select of two) is accessed with flat instructions, which also count on
+// the LDS counter, so that an LDS wait (a lane shuffle) waits for them too.
+// gptr states that it points to global memory.
+template <class T>
+__device__ __forceinline__ __attribute__((address_space(1))) T * gptr(T * p) {
+    return (__attribute__((address_space(1))) T *) p;
+}
 // the m of udiv, on the host
 inline uint32_t recip32(int64_t d) {
     return d > 1 ? (uint32_t) (((uint64_t(1) << 32) + (uint64_t) d - 1) / (uint64_t) d) : 0u;

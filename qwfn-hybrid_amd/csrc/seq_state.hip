@@ -19,6 +19,7 @@
 // kernel arguments, so a decode step sends nothing over the host link.
 #include "qwfn_common.h"
 #include "qwfn_state.h"
+#include "qsa_steps.h"
 #include "state_internal.h"
 
 #include <algorithm>
@@ -109,13 +110,6 @@ __global__ __launch_bounds__(FILL_THREADS) void k_cell_mask(const int32_t * cell
     }
 }
 
-// The decode bias of block b at n_past (b_last = n_past / ratio, n_bid =
-// (n_past + 1) / ratio): 0 whole block, 1e9 the incomplete block of n_past,
-// -inf beyond (qwfn_engine.cpp:1093-1096 for the window, :1115-1120 for all).
-__device__ __forceinline__ float bias_of(int64_t b, int64_t b_last, int64_t n_bid) {
-    return b < n_bid ? 0.0f : (b == b_last ? 1e9f : -INFINITY);
-}
-
 struct qsa_prep_args {
     qwfn_qsa_inputs qd;
     const float *   prev;    // previous position's bias, or null (window in place)
@@ -146,47 +140,10 @@ __global__ __launch_bounds__(FILL_THREADS) void k_qsa_prepare(qsa_prep_args a) {
 }
 
 // The inputs of T consecutive positions n_past .. n_past + T - 1 in one
-// launch: the same values as k_qsa_prepare for position n_past (its window in
-// place in qd[0].bias) followed by k_qsa_prepare of each later position from
-// the previous one's bias. Row t's block b is the value of the latest window
-// at or before t that holds b, else the running bias qd[0].bias[b], which the
-// thread reads before it writes.
-constexpr int PREP_MAX_T = 16;
-struct qsa_prep_steps_args {
-    qwfn_qsa_inputs qd[PREP_MAX_T];
-    int32_t         T;
-    int32_t         n_past;
-};
-
+// launch: k_qsa_prepare for position n_past, then for each later position
+// from the previous one's bias (prepare_steps_range, qsa_steps.h).
 __global__ __launch_bounds__(FILL_THREADS) void k_qsa_prepare_steps(qsa_prep_steps_args a) {
-    const int64_t r = a.qd[0].ratio, nbm = a.qd[0].n_blocks_max;
-    const int64_t t0 = (int64_t) blockIdx.x * FILL_THREADS + threadIdx.x;
-    const int64_t stride = (int64_t) gridDim.x * FILL_THREADS;
-    for (int64_t b = t0; b < nbm; b += stride) {
-        float v = a.qd[0].bias[b];
-        for (int t = 0; t < a.T; t++) {
-            const int64_t p = (int64_t) a.n_past + t, b_last = p / r, n_bid = (p + 1) / r;
-            const int64_t lo = b_last > 0 ? b_last - 1 : 0;
-            const bool win = b >= lo && b <= b_last + 1;
-            if (win) v = bias_of(b, b_last, n_bid);
-            if (t == 0) {
-                if (win) a.qd[0].bias[b] = v;
-            } else {
-                a.qd[t].bias[b] = v;
-            }
-        }
-    }
-    // position t's small inputs: one thread each
-    if (t0 < a.T) {
-        const int t = (int) t0;
-        const int64_t p = (int64_t) a.n_past + t, b_last = p / r;
-        const qwfn_qsa_inputs & q = a.qd[t];
-        for (int64_t m = 0; m < r; m++) q.member_idx[m] = (int32_t) (b_last * r + m);
-        for (int i = 0; i < 4; i++) q.blk_pos[i] = (int32_t) (b_last * r);
-        *q.write_idx = (int32_t) p;
-        *q.blk_idx = (int32_t) b_last;
-        *q.npast_f = (float) p;
-    }
+    prepare_steps_range(a, (int64_t) blockIdx.x * FILL_THREADS + threadIdx.x, (int64_t) gridDim.x * FILL_THREADS);
 }
 
 __global__ __launch_bounds__(FILL_THREADS) void k_qsa_bias(float * bias, int64_t nb_max, int32_t n_past, int32_t ratio) {
@@ -1024,26 +981,8 @@ int qwfn_qsa_decode_prepare(const qwfn_qsa_inputs * qd, const float * prev_bias,
 
 int qwfn_qsa_decode_prepare_steps(const qwfn_qsa_inputs * qd, int32_t T, int32_t n_past, void * stream) {
     return ::qwfn::abi_call("qsa_decode_prepare_steps", [&]() -> int {
-        if (!qd) return set_error(QWFN_EINVAL, "qsa_decode_prepare_steps: NULL inputs");
-        if (T < 1 || T > PREP_MAX_T) return set_error(QWFN_ENOTSUP, "qsa_decode_prepare_steps: 1 to 16 positions");
-        if (n_past < 0 || (int64_t) n_past + T - 1 > INT32_MAX)
-            return set_error(QWFN_EINVAL, "qsa_decode_prepare_steps: positions outside [0, 2^31)");
-        qsa_prep_steps_args a{};
-        for (int t = 0; t < T; t++) {
-            const qwfn_qsa_inputs & q = qd[t];
-            if (!q.bias || !q.write_idx || !q.member_idx || !q.blk_pos || !q.blk_idx || !q.npast_f)
-                return set_error(QWFN_EINVAL, "qsa_decode_prepare_steps: NULL tensor");
-            if (q.ratio < 1 || q.n_blocks_max < 1 || q.ratio != qd[0].ratio || q.n_blocks_max != qd[0].n_blocks_max)
-                return set_error(QWFN_EINVAL, "qsa_decode_prepare_steps: every position needs the same ratio >= 1 and n_blocks_max >= 1");
-            for (int u = 0; u < t; u++) {
-                const char * x0 = (const char *) q.bias, * x1 = x0 + q.n_blocks_max * 4;
-                const char * y0 = (const char *) qd[u].bias, * y1 = y0 + q.n_blocks_max * 4;
-                if (x0 < y1 && y0 < x1) return set_error(QWFN_EINVAL, "qsa_decode_prepare_steps: bias rows overlap");
-            }
-            a.qd[t] = q;
-        }
-        a.T = T;
-        a.n_past = n_past;
+        qsa_prep_steps_args a;
+        if (int rc = prep_steps_args(qd, T, n_past, "qsa_decode_prepare_steps", &a)) return rc;
         const int64_t n = std::max<int64_t>(qd[0].n_blocks_max, T);
         hipLaunchKernelGGL(k_qsa_prepare_steps, dim3(grid_for(n)), dim3(FILL_THREADS), 0, as_stream(stream), a);
         return hip_check(hipGetLastError(), "qsa_decode_prepare_steps launch");

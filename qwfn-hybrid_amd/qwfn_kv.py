@@ -149,6 +149,7 @@ EXPORTS = [
     "qwfn_state_reset", "qwfn_state_rollback", "qwfn_snapshot_parts", "qwfn_snapshot_save", "qwfn_snapshot_load",
     "qwfn_causal_mask_f16", "qwfn_cell_mask_f16", "qwfn_qsa_chunk_inputs", "qwfn_qsa_mask_f16",
     "qwfn_qsa_bucket", "qwfn_qsa_decode_prepare", "qwfn_qsa_decode_prepare_steps", "qwfn_qsa_pool_decode_steps",
+    "qwfn_qsa_decode_prepare_pool_steps",
     "qwfn_qsa_bias_rebuild", "qwfn_qsa_tables",
     "qwfn_snap_pool_create", "qwfn_snap_pool_destroy", "qwfn_snap_pool_count", "qwfn_snap_pool_bytes",
     "qwfn_snap_pool_entry", "qwfn_snap_pool_save", "qwfn_snap_pool_best", "qwfn_snap_pool_load",
@@ -274,6 +275,8 @@ def load(path: str = LIB_PATH):
     L.qwfn_qsa_pool_decode.argtypes = [vp, i64, vp, vp, vp, i32, vp, vp, vp, vp, i64, ctypes.POINTER(QsaPoolCfg), vp]
     L.qwfn_qsa_pool_decode_steps.argtypes = [vp, i64, vp, sz, ctypes.POINTER(QsaInputs), i32, vp, vp, i64,
                                              ctypes.POINTER(QsaPoolCfg), vp]
+    L.qwfn_qsa_decode_prepare_pool_steps.argtypes = [ctypes.POINTER(QsaInputs), i32, i32, vp, i64, vp, sz, vp, vp, i64,
+                                                     ctypes.POINTER(QsaPoolCfg), vp]
     L.qwfn_qsa_pool_rebuild.argtypes = [vp, i64, i64, i32, vp, vp, i64, ctypes.POINTER(QsaPoolCfg), vp]
     L.qwfn_gated_delta_net.argtypes = [vp, i64, vp, i64, vp, i64, vp, vp, i32, i32, i32, i32, ctypes.c_float, vp, vp,
                                        vp, sz, i32, vp]

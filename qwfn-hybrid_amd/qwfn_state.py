@@ -331,6 +331,26 @@ def qsa_decode_prepare_steps(qds, n_past: int, stream=None):
         q.n_bucket = nb
 
 
+def qsa_decode_prepare_pool_steps(qds, n_past: int, ic, k_raw, k_norm_w, pool, cfg=None, stream=None):
+    """qsa_decode_prepare_steps(qds, n_past) then qwfn_kv.qsa_pool_decode_steps(ic, k_raw, qds, k_norm_w, pool)
+    in one launch, the pooling's indices in their closed forms."""
+    cfg = cfg or K.qsa_pool_cfg()
+    T = len(qds)
+    K._check_pool_args("qsa_decode_prepare_pool_steps", cfg, ic, pool, k_norm_w,
+                       k_raw=k_raw[0] if k_raw is not None else None)
+    if k_raw is not None and (k_raw.dim() != 2 or k_raw.shape[0] != T or k_raw.stride(1) != 1):
+        raise ValueError("qsa_decode_prepare_pool_steps: k_raw must be [T, idx_dim] with contiguous rows")
+    arr = (K.QsaInputs * T)(*[q._c() for q in qds])
+    K.check(K.load().qwfn_qsa_decode_prepare_pool_steps(arr, T, n_past, ic.data_ptr(), ic.shape[0],
+                                                        k_raw.data_ptr() if k_raw is not None else None,
+                                                        k_raw.stride(0) * 4 if k_raw is not None else 0,
+                                                        k_norm_w.data_ptr(), pool.data_ptr(), pool.shape[0],
+                                                        ctypes.byref(cfg), K._stream(stream)))
+    nb = max(q.bucket(n_past + t) for t, q in enumerate(qds))
+    for q in qds:
+        q.n_bucket = nb
+
+
 def qsa_tables(blk_cells, ratio: int, cell_pos=None, blk_pos_all=None, n_whole: int = 0, stream=None):
     n_blocks_max = blk_cells.numel() // ratio if blk_cells is not None else 0
     K.check(K.load().qwfn_qsa_tables(blk_cells.data_ptr() if blk_cells is not None else None, n_blocks_max, ratio,

@@ -90,3 +90,48 @@ def test_pool_decode_steps_matches_chained_calls(gpu, ratio, n_past, T):
     pool_n = dev(pool0)
     K.qsa_pool_decode_steps(ic_b, None, qds, w_d, pool_n)
     np.testing.assert_array_equal(host(pool_n).view(np.uint16), host(pool_s).view(np.uint16))
+
+
+@pytest.mark.parametrize("ratio,n_past,T,dim,keys", [(4, 73700, 3, 128, True), (4, 73703, 3, 128, True),
+                                                     (4, 73701, 16, 128, True), (1, 500, 3, 128, True),
+                                                     (16, 4095, 16, 128, True), (32, 8190, 3, 128, False),
+                                                     (128, 1000, 5, 128, True), (4, 4097, 3, 256, True),
+                                                     (4, 0, 1, 128, True)])
+def test_prepare_pool_steps_matches_separate_calls(gpu, ratio, n_past, T, dim, keys):
+    """qwfn_qsa_decode_prepare_pool_steps == qwfn_qsa_decode_prepare_steps then
+    qwfn_qsa_pool_decode_steps: bias rows, small inputs, index cache and pool, bit for bit
+    (ratio 128: members past one wave's lanes; idx_dim 256; no keys)."""
+    K = gpu
+    rng = np.random.default_rng(n_past * 7 + T + dim)
+    cfg = K.qsa_pool_cfg(idx_dim=dim)
+    n_ctx = (n_past + T) // ratio * ratio + 2 * ratio + 64        # every member row of the step's blocks
+    nb = n_ctx // ratio + 8
+    base = _running_bias(nb, max(n_past, 1), ratio, rng)
+    ic = rng.standard_normal((n_ctx, dim)).astype(np.float16)
+    pool0 = (rng.standard_normal((nb, dim)) * 0.3).astype(np.float16)
+    w = rng.uniform(0.6, 1.4, dim).astype(np.float32)
+    kr_d = dev(rng.standard_normal((T, dim)).astype(np.float32)) if keys else None
+    w_d = dev(w)
+    sets = []
+    for _ in range(2):
+        qds = [S.QsaDecodeInputs(ratio, nb) for _ in range(T)]
+        qds[0].bias.copy_(dev(base))
+        for t in range(1, T):
+            qds[t].bias.fill_(5.0)
+        sets.append(qds)
+    seq, fused = sets
+    ic_s, pool_s = dev(ic), dev(pool0)
+    say(f"prepare + pool x{T} at {n_past}, ratio {ratio}, dim {dim}: two launches")
+    S.qsa_decode_prepare_steps(seq, n_past)
+    K.qsa_pool_decode_steps(ic_s, kr_d, seq, w_d, pool_s, cfg=cfg)
+    ic_f, pool_f = dev(ic), dev(pool0)
+    say("one launch")
+    S.qsa_decode_prepare_pool_steps(fused, n_past, ic_f, kr_d, w_d, pool_f, cfg=cfg)
+    assert K.device_status() == 0
+    for t in range(T):
+        for f in ("bias", "write_idx", "member_idx", "blk_pos", "blk_idx", "npast_f"):
+            np.testing.assert_array_equal(host(getattr(fused[t], f)), host(getattr(seq[t], f)), err_msg=f"{f} at {t}")
+        assert fused[t].n_bucket == seq[t].n_bucket
+    np.testing.assert_array_equal(host(ic_f).view(np.uint16), host(ic_s).view(np.uint16))
+    np.testing.assert_array_equal(host(pool_f).view(np.uint16), host(pool_s).view(np.uint16))
+    assert not np.array_equal(host(pool_f).view(np.uint16), pool0.view(np.uint16))

@@ -14,7 +14,8 @@ sparse_attn_decode calls (qwfn_graph.cpp:653-705); call k
     sigmoid(gate) (:662-701).
 The device runs the same chain batched the way the library offers it:
 prepare x3, pool decode x3 (or each in one launch for the three positions:
-qwfn_qsa_decode_prepare_steps, qwfn_qsa_pool_decode_steps), ONE selection
+qwfn_qsa_decode_prepare_steps, qwfn_qsa_pool_decode_steps; or both in one
+launch: qwfn_qsa_decode_prepare_pool_steps), ONE selection
 over the three queries, ONE K/V producer call for the three rows, ONE
 attention launch over the three lists (qwfn_flash_attn_ext_q8_0_query_cells)
 with the gate. The oracle runs the
@@ -56,7 +57,8 @@ def _ulp_ok(got_bits, ref_bits):
     assert int((d != 0).sum()) <= max(1, d.size // 1000)
 
 
-@pytest.mark.parametrize("n_past,batched", [(73700, False), (73702, False), (73700, True), (73702, True)])
+@pytest.mark.parametrize("n_past,batched", [(73700, ""), (73702, ""), (73700, "steps"), (73702, "steps"),
+                                            (73700, "fused"), (73703, "fused")])
 def test_qsa_verify_step_composed(gpu, oracle, n_past, batched):
     K = gpu
     rng = np.random.default_rng(n_past)
@@ -91,7 +93,10 @@ def test_qsa_verify_step_composed(gpu, oracle, n_past, batched):
         qds.append(qd)
     qds[0].rebuild_bias(n_past)
     pool0 = host(pool).view(np.uint16).copy()     # the oracle chain starts from the device's rebuilt pool
-    if batched:
+    if batched == "fused":
+        say("prepare and pool decode steps, one launch")
+        S.qsa_decode_prepare_pool_steps(qds, n_past, ic_d, dev(k_raw), knw_idx_d, pool)
+    elif batched:
         say("prepare steps, pool decode steps (one launch each)")
         S.qsa_decode_prepare_steps(qds, n_past)
         K.qsa_pool_decode_steps(ic_d, dev(k_raw), qds, knw_idx_d, pool)

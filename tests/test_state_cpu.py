@@ -264,9 +264,19 @@ def test_step_input_validation():
         K.ENOTSUP, "1 to 16")
     err(L.qwfn_qsa_pool_decode_steps(FAKE, 100, FAKE, 256, arr, 2, FAKE, FAKE, 10, ctypes.byref(cfg), None),
         K.EALIGN, "shorter")
+    # the fused form checks both sets of arguments, the preparation's first
+    PP = L.qwfn_qsa_decode_prepare_pool_steps
+    err(PP(None, 2, 5, FAKE, 100, FAKE, 512, FAKE, FAKE, 10, ctypes.byref(cfg), None), K.EINVAL, "NULL inputs")
+    err(PP(arr, 17, 5, FAKE, 100, FAKE, 512, FAKE, FAKE, 10, ctypes.byref(cfg), None), K.ENOTSUP, "1 to 16")
+    err(PP(arr, 2, -1, FAKE, 100, FAKE, 512, FAKE, FAKE, 10, ctypes.byref(cfg), None), K.EINVAL, "positions")
+    err(PP(arr, 2, 5, FAKE, 100, FAKE, 256, FAKE, FAKE, 10, ctypes.byref(cfg), None), K.EALIGN, "shorter")
+    err(PP(arr, 2, 5, None, 100, FAKE, 512, FAKE, FAKE, 10, ctypes.byref(cfg), None), K.EINVAL, "NULL pointer")
+    err(PP(arr, 2, 5, FAKE, 100, FAKE, 512, None, FAKE, 10, ctypes.byref(cfg), None), K.EINVAL, "k_norm")
+    assert L.qwfn_last_error().decode().startswith("qsa_pool"), L.qwfn_last_error()
     arr[1].ratio = 8
     err(L.qwfn_qsa_pool_decode_steps(FAKE, 100, FAKE, 512, arr, 2, FAKE, FAKE, 10, ctypes.byref(cfg), None),
         K.EINVAL, "ratios")
+    err(PP(arr, 2, 5, FAKE, 100, FAKE, 512, FAKE, FAKE, 10, ctypes.byref(cfg), None), K.EINVAL, "same ratio")
     err(L.qwfn_qsa_bias_rebuild(FAKE, 16, -2, 4, None), K.EINVAL, "sizes")
     err(L.qwfn_qsa_tables(FAKE, 1 << 30, 4, None, 0, None, 0, None), K.ERANGE, "int32")
     # snapshot calls need states with memory
