@@ -510,13 +510,21 @@ def measure_rows(K, torch, np, dev, gen) -> dict:
 
     def gather(k):
         kc, vc = kvs[k % sets]
+        K.gather_segments_kv(kc, vc, idx, gk, gv, 0, 272, 272)
+
+    def gather_two(k):
+        kc, vc = kvs[k % sets]
         K.gather_segments(kc, idx, gk, 0, 272, 272)
         K.gather_segments(vc, idx, gv, 0, 272, 272)
+    us_two = timed_graph(torch, gather_two, 16, 10)
     us = timed_graph(torch, gather, 16, 10)
     moved = sum(len(x) for x in lists) * 272 * 2
     rows["gather_64k"] = {"us_per_op": round(us, 3), "positions_per_head": [len(x) for x in lists],
                           "bytes_read": moved, "bytes_written": moved, "GBs": gbs(2 * moved, us),
-                          "frac": round(2 * moved / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+                          "frac": round(2 * moved / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                          "us_per_op_two_launches": round(us_two, 3),
+                          "entry": "qwfn_kv_gather_segments_kv (K and V in one launch); us_per_op_two_launches: "
+                                   "qwfn_kv_gather_segments for K, then for V"}
     del kvs, gk, gv, sws
 
     # ---- snapshot restore: 12 layers x 8192 rows of K and V + 36 DeltaNet states

@@ -128,6 +128,16 @@ int qwfn_kv_gather_segments(const void * src, size_t src_row_stride, int64_t src
                             const int32_t * idx, int64_t n_idx,
                             void * dst, size_t dst_row_stride, size_t dst_seg_stride, void * stream);
 
+/* qwfn_kv_gather_segments of the K cache into dst_k and of the V cache into
+ * dst_v with the same indices and geometry, in one launch: the reference's
+ * qsa_gather gathers K and V with the same index (qwfn_graph.cpp:632-645),
+ * two get_rows; the same bytes as the two calls. dst_k and dst_v must not
+ * overlap. */
+int qwfn_kv_gather_segments_kv(const void * src_k, const void * src_v, size_t src_row_stride, int64_t src_rows,
+                               size_t seg_off, size_t seg_stride, size_t seg_bytes, int32_t n_seg,
+                               const int32_t * idx, int64_t n_idx, void * dst_k, void * dst_v,
+                               size_t dst_row_stride, size_t dst_seg_stride, void * stream);
+
 /* ------------------------------------------------------- flash attention */
 
 /* ggml_flash_attn_ext(q, k, v, mask, scale, max_bias, logit_softcap) with F32

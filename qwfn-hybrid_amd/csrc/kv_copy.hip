@@ -23,6 +23,8 @@ constexpr int COPY_THREADS = 256;
 
 struct gather_args {
     const char *    src;
+    const char *    src2;      // blockIdx.z 1: the second tensor of a pair (V of K and V), same geometry
+    char *          dst2;
     size_t          src_row_stride;
     int64_t         src_rows;
     size_t          seg_off;
@@ -47,9 +49,10 @@ __device__ __forceinline__ void store_nt(uint4 * p, uint4 v) {
 }
 
 
-// Workgroup (x, y) copies index rows [x rows, (x + 1) rows) of segment y; a
-// lane's unit u of the workgroup is part u % units of row u / units (32-bit
-// reciprocal division, no 64-bit arithmetic per unit).
+// Workgroup (x, y, z) copies index rows [x rows, (x + 1) rows) of segment y
+// of tensor z (src / dst, or src2 / dst2 for a pair); a lane's unit u of the
+// workgroup is part u % units of row u / units (32-bit reciprocal division,
+// no 64-bit arithmetic per unit).
 template <typename U>
 __global__ __launch_bounds__(COPY_THREADS) void k_gather(gather_args a) {
     const uint32_t seg = blockIdx.y;
@@ -58,8 +61,8 @@ __global__ __launch_bounds__(COPY_THREADS) void k_gather(gather_args a) {
     const uint32_t nrow = left < (int64_t) a.rows ? (uint32_t) left : a.rows;
     const uint32_t total = nrow * a.units;
     const int32_t * idx = a.idx + (size_t) seg * (size_t) a.n_idx + i0;
-    const char * src = a.src + a.seg_off + (size_t) seg * a.seg_stride;
-    char * dst = a.dst + (size_t) seg * a.dst_seg_stride + (size_t) i0 * a.dst_row_stride;
+    const char * src = (blockIdx.z ? a.src2 : a.src) + a.seg_off + (size_t) seg * a.seg_stride;
+    char * dst = (blockIdx.z ? a.dst2 : a.dst) + (size_t) seg * a.dst_seg_stride + (size_t) i0 * a.dst_row_stride;
     for (uint32_t u = threadIdx.x; u < total; u += COPY_THREADS) {
         const uint32_t row = a.rows == 1 ? 0u : udiv(u, a.units, a.units_mul);
         const uint32_t part = u - row * a.units;
@@ -74,10 +77,12 @@ __global__ __launch_bounds__(COPY_THREADS) void k_gather(gather_args a) {
     }
 }
 
-int launch_gather(gather_args a, size_t seg_bytes, int32_t n_seg, hipStream_t stream) {
+// n_t: 1, or 2 for a pair (src2 / dst2 set)
+int launch_gather(gather_args a, size_t seg_bytes, int32_t n_seg, int n_t, hipStream_t stream) {
     const bool v16 = seg_bytes % 16 == 0 && a.src_row_stride % 16 == 0 && a.seg_off % 16 == 0 &&
                      a.seg_stride % 16 == 0 && a.dst_row_stride % 16 == 0 && a.dst_seg_stride % 16 == 0 &&
-                     is_aligned(a.src, 16) && is_aligned(a.dst, 16);
+                     is_aligned(a.src, 16) && is_aligned(a.dst, 16) &&
+                     (n_t == 1 || (is_aligned(a.src2, 16) && is_aligned(a.dst2, 16)));
     const uint64_t units = seg_bytes / (v16 ? 16 : 4);
     if (a.n_idx == 0) return QWFN_OK;
     if (units >= (uint64_t(1) << 31))
@@ -95,7 +100,7 @@ int launch_gather(gather_args a, size_t seg_bytes, int32_t n_seg, hipStream_t st
     a.units = (uint32_t) units;
     a.units_mul = recip32((int64_t) units);
     a.rows = (uint32_t) rows;
-    const dim3 grid((unsigned) gx, (unsigned) n_seg);
+    const dim3 grid((unsigned) gx, (unsigned) n_seg, (unsigned) n_t);
     if (v16) hipLaunchKernelGGL(k_gather<uint4>, grid, dim3(COPY_THREADS), 0, stream, a);
     else     hipLaunchKernelGGL(k_gather<uint32_t>, grid, dim3(COPY_THREADS), 0, stream, a);
     return hip_check(hipGetLastError(), "gather launch");
@@ -258,7 +263,7 @@ extern "C" int qwfn_get_rows_i32(const qwfn_tensor * src, const qwfn_tensor * id
         a.idx = (const int32_t *) idx->data; a.n_idx = idx->ne[0];
         a.dst = (char *) dst->data; a.dst_row_stride = dst->nb[1]; a.dst_seg_stride = 0;
         a.status = st;
-        return launch_gather(a, (size_t) src->ne[0] * 4, 1, as_stream(stream));
+        return launch_gather(a, (size_t) src->ne[0] * 4, 1, 1, as_stream(stream));
     });
 }
 
@@ -284,7 +289,40 @@ extern "C" int qwfn_kv_gather_segments(const void * src, size_t src_row_stride, 
         a.idx = idx; a.n_idx = n_idx;
         a.dst = (char *) dst; a.dst_row_stride = dst_row_stride; a.dst_seg_stride = dst_seg_stride;
         a.status = st;
-        return launch_gather(a, seg_bytes, n_seg, as_stream(stream));
+        return launch_gather(a, seg_bytes, n_seg, 1, as_stream(stream));
+    });
+}
+
+extern "C" int qwfn_kv_gather_segments_kv(const void * src_k, const void * src_v, size_t src_row_stride, int64_t src_rows,
+                                          size_t seg_off, size_t seg_stride, size_t seg_bytes, int32_t n_seg,
+                                          const int32_t * idx, int64_t n_idx, void * dst_k, void * dst_v,
+                                          size_t dst_row_stride, size_t dst_seg_stride, void * stream) {
+    return ::qwfn::abi_call("kv_gather_segments_kv", [&]() -> int {
+        if (!src_k || !src_v || !idx || !dst_k || !dst_v) return set_error(QWFN_EINVAL, "gather_segments_kv: NULL pointer");
+        if (n_seg < 1 || n_idx < 0 || src_rows < 0 || seg_bytes == 0)
+            return set_error(QWFN_EINVAL, "gather_segments_kv: empty or negative sizes");
+        if (seg_bytes % 4 || seg_off % 4 || seg_stride % 4 || src_row_stride % 4 || dst_row_stride % 4 ||
+            dst_seg_stride % 4 || !is_aligned(src_k, 4) || !is_aligned(src_v, 4) || !is_aligned(dst_k, 4) ||
+            !is_aligned(dst_v, 4) || !is_aligned(idx, 4))
+            return set_error(QWFN_EALIGN, "gather_segments_kv: sizes, offsets and strides must be multiples of 4");
+        if (seg_off + (size_t) (n_seg - 1) * seg_stride + seg_bytes > src_row_stride)
+            return set_error(QWFN_ERANGE, "gather_segments_kv: segments extend past the source row");
+        if (dst_row_stride < seg_bytes) return set_error(QWFN_EINVAL, "gather_segments_kv: dst rows overlap");
+        // the two destinations' extents must not overlap each other
+        const size_t ext = n_idx == 0 ? 0 : (size_t) (n_seg - 1) * dst_seg_stride + (size_t) (n_idx - 1) * dst_row_stride + seg_bytes;
+        const char * k0 = (const char *) dst_k, * v0 = (const char *) dst_v;
+        if (ext && k0 < v0 + ext && v0 < k0 + ext) return set_error(QWFN_EINVAL, "gather_segments_kv: dst_k and dst_v overlap");
+        uint32_t * st = nullptr;
+        if (int rc = status_word(&st)) return rc;
+        gather_args a{};
+        a.src = (const char *) src_k; a.src2 = (const char *) src_v;
+        a.src_row_stride = src_row_stride; a.src_rows = src_rows;
+        a.seg_off = seg_off; a.seg_stride = seg_stride;
+        a.idx = idx; a.n_idx = n_idx;
+        a.dst = (char *) dst_k; a.dst2 = (char *) dst_v;
+        a.dst_row_stride = dst_row_stride; a.dst_seg_stride = dst_seg_stride;
+        a.status = st;
+        return launch_gather(a, seg_bytes, n_seg, 2, as_stream(stream));
     });
 }
 

@@ -135,7 +135,7 @@ class QsaPoolCfg(ctypes.Structure):
 
 EXPORTS = [
     "qwfn_abi_version", "qwfn_last_error", "qwfn_init", "qwfn_device_status",
-    "qwfn_set_rows_q8_0", "qwfn_cpy_f32_q8_0", "qwfn_set_rows_q8_0_kv", "qwfn_cpy_f32_q8_0_kv", "qwfn_get_rows_i32", "qwfn_kv_gather_segments",
+    "qwfn_set_rows_q8_0", "qwfn_cpy_f32_q8_0", "qwfn_set_rows_q8_0_kv", "qwfn_cpy_f32_q8_0_kv", "qwfn_get_rows_i32", "qwfn_kv_gather_segments", "qwfn_kv_gather_segments_kv",
     "qwfn_fattn_workspace_size", "qwfn_fattn_force_splits", "qwfn_fattn_force_kernel", "qwfn_fattn_last_kernel", "qwfn_fattn_force_merge", "qwfn_fattn_last_merge", "qwfn_flash_attn_ext_q8_0", "qwfn_flash_attn_ext_q8_0_noalloc", "qwfn_flash_attn_ext_q8_0_append",
     "qwfn_fattn_workspace_size_seq", "qwfn_flash_attn_ext_q8_0_seq", "qwfn_state_restore",
     "qwfn_fattn_workspace_size_cells", "qwfn_flash_attn_ext_q8_0_cells", "qwfn_kv_produce_q8_0",
@@ -182,6 +182,7 @@ def load(path: str = LIB_PATH):
     L.qwfn_cpy_f32_q8_0_kv.argtypes = [T, T, T, T, ctypes.c_int, vp]
     L.qwfn_get_rows_i32.argtypes = [T, T, T, vp]
     L.qwfn_kv_gather_segments.argtypes = [vp, sz, i64, sz, sz, sz, i32, vp, i64, vp, sz, sz, vp]
+    L.qwfn_kv_gather_segments_kv.argtypes = [vp, vp, sz, i64, sz, sz, sz, i32, vp, i64, vp, vp, sz, sz, vp]
     L.qwfn_fattn_workspace_size.argtypes = [T, T, T, T]
     L.qwfn_fattn_workspace_size.restype = sz
     L.qwfn_flash_attn_ext_q8_0_noalloc.argtypes = [T, T, T, T, ctypes.c_float, ctypes.c_float, ctypes.c_float, T,
@@ -439,6 +440,20 @@ def gather_segments(cache, idx, out, seg_off: int, seg_stride: int, seg_bytes: i
     return check(L.qwfn_kv_gather_segments(cache.data_ptr(), cache.stride(0), cache.shape[0], seg_off, seg_stride,
                                            seg_bytes, n_seg, idx.data_ptr(), n_idx, out.data_ptr(), out.stride(1),
                                            out.stride(0), _stream(stream)))
+
+
+def gather_segments_kv(kcache, vcache, idx, out_k, out_v, seg_off: int, seg_stride: int, seg_bytes: int, stream=None):
+    """gather_segments of the K and the V cache with the same idx, one launch; the caches share their
+    geometry, as do out_k and out_v."""
+    L = load()
+    n_seg, n_idx = idx.shape
+    if kcache.shape != vcache.shape or kcache.stride() != vcache.stride() or out_k.shape != out_v.shape \
+            or out_k.stride() != out_v.stride():
+        raise ValueError("gather_segments_kv: K and V caches (and outputs) must share shape and strides")
+    return check(L.qwfn_kv_gather_segments_kv(kcache.data_ptr(), vcache.data_ptr(), kcache.stride(0), kcache.shape[0],
+                                              seg_off, seg_stride, seg_bytes, n_seg, idx.data_ptr(), n_idx,
+                                              out_k.data_ptr(), out_v.data_ptr(), out_k.stride(1), out_k.stride(0),
+                                              _stream(stream)))
 
 
 def flash_attn_ext(qv: Tensor, kv: Tensor, vv: Tensor, mv: Tensor | None, scale: float, ov: Tensor,

@@ -97,6 +97,14 @@ def test_get_rows_and_gather_validation():
          K.EALIGN, "multiples of 4")
     _err(L.qwfn_kv_gather_segments(FAKE, 544, 100, 0, 272, 276, 2, FAKE, 10, FAKE, 276, 2760, None),
          K.ERANGE, "past the source row")
+    G2 = L.qwfn_kv_gather_segments_kv
+    _err(G2(FAKE, None, 544, 100, 0, 272, 272, 2, FAKE, 10, FAKE, FAKE + 8192, 272, 2720, None), K.EINVAL, "NULL")
+    _err(G2(FAKE, FAKE, 544, 100, 2, 272, 272, 2, FAKE, 10, FAKE, FAKE + 8192, 272, 2720, None),
+         K.EALIGN, "multiples of 4")
+    _err(G2(FAKE, FAKE, 544, 100, 0, 272, 276, 2, FAKE, 10, FAKE, FAKE + 8192, 276, 2760, None),
+         K.ERANGE, "past the source row")
+    _err(G2(FAKE, FAKE, 544, 100, 0, 272, 272, 2, FAKE, 10, FAKE, FAKE + 4096, 272, 2720, None),
+         K.EINVAL, "overlap")
 
 
 def _fa_views(hd=256, T=1, nh=16, nh_kv=2, n_kv=100, qtype=K.TYPE_F32):

@@ -179,6 +179,27 @@ def test_gather_segments_per_head(gpu, oracle):
         np.testing.assert_array_equal(got[h], O.get_rows(cache, idx[h], 272, 272 * h))
 
 
+@pytest.mark.parametrize("seg,m", [(272, 8704), (136, 100), (4, 1)])
+def test_gather_segments_kv_pair(gpu, oracle, seg, m):
+    """K and V gathered in one launch: the same bytes as the oracle's get_rows of each
+    (16-byte units at 272 / 136, 4-byte units at 4); the outputs keep no stale bytes."""
+    K = gpu
+    import torch
+    n_ctx = 65536
+    rng = np.random.default_rng(seg + m)
+    kc = rng.integers(0, 256, (n_ctx, 544), dtype=np.uint8)
+    vc = rng.integers(0, 256, (n_ctx, 544), dtype=np.uint8)
+    idx = np.stack([np.sort(rng.choice(n_ctx, m, replace=False)) for _ in range(2)]).astype(np.int32)
+    say(f"gather_segments_kv 2 x {m} x {seg} B")
+    gk = torch.full((2, m, seg), 7, dtype=torch.uint8, device="cuda")
+    gv = torch.full((2, m, seg), 9, dtype=torch.uint8, device="cuda")
+    K.gather_segments_kv(dev(kc), dev(vc), dev(idx), gk, gv, 0, 272, seg)
+    assert K.device_status() == 0
+    for h in range(2):
+        np.testing.assert_array_equal(host(gk)[h], O.get_rows(kc, idx[h], seg, 272 * h))
+        np.testing.assert_array_equal(host(gv)[h], O.get_rows(vc, idx[h], seg, 272 * h))
+
+
 def test_gather_out_of_range_flagged(gpu, oracle):
     K = gpu
     import torch
