@@ -377,6 +377,8 @@ __global__ __launch_bounds__(POOL_WAVES * 64) void k_qsa_prepare_pool_steps(prep
 // of its blocks (2 blocks per pass at n_dims 64) instead of one block leaving
 // half the lanes idle. Per value the arithmetic is k_qsa_pool's.
 constexpr int RB_WAVES = 4;
+constexpr int RB_PRE = 4;       // member rows loaded ahead of the rope's cos / sin
+constexpr int RB_TASKS = 4;     // rotation tasks a lane: bpw * n_dims / 2 <= 256
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(RB_WAVES * 64) void k_qsa_pool_rebuild(pool_args a) {
@@ -391,18 +393,41 @@ __global__ __launch_bounds__(RB_WAVES * 64) void k_qsa_pool_rebuild(pool_args a)
     float x[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) x[i] = 0.f;
+    // the first RB_PRE member rows' loads go out first (unconditional, at
+    // block 0 / member 0 where there is no such row); the rope's cos / sin,
+    // which depend on the block positions alone, are computed while they land
+    const uint16_t * src = a.ic + (size_t) (live ? blk : 0) * (size_t) a.r * (size_t) dim + 8 * lj;
+    uint4 u[RB_PRE];
+#pragma unroll
+    for (int m = 0; m < RB_PRE; m++) u[m] = *(const uint4 *) (src + (size_t) (m < a.r ? m : 0) * dim);
+    // lane task q: (block, pair) lane + 64 q of the wave's bpw blocks (at most
+    // 4: bpw * n_dims / 2 <= 256); unused tasks keep cos 1, sin 0
+    const int half = a.rp.n_dims / 2;
+    float cq[RB_TASKS], sq4[RB_TASKS];
+#pragma unroll
+    for (int q = 0; q < RB_TASKS; q++) {
+        const int idx = lane + 64 * q, b = idx / half, k = idx - b * half;
+        cq[q] = 1.f;
+        sq4[q] = 0.f;
+        if (idx < bpw * half && blk0 + b < a.n_blk) {
+            const int32_t p = (int32_t) ((blk0 + b) * a.r);
+            const int32_t pos[4] = {p, p, p, p};
+            rope_cos_sin(a.rp, pos, k, &cq[q], &sq4[q]);
+        }
+    }
     if (live) {
-        const uint16_t * src = a.ic + (size_t) blk * (size_t) a.r * (size_t) dim + 8 * lj;
-#pragma unroll 4
-        for (int m = 0; m < a.r; m++) {
-            const uint4 u = *(const uint4 *) (src + (size_t) m * dim);
-            const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+        auto add_row = [&](const uint4 & w, int m) {
+            const uint32_t w4[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const float v = h2f((uint16_t) (w4[i >> 1] >> (16 * (i & 1))));
                 x[i] = m == 0 ? v : __fadd_rn(x[i], v);
             }
-        }
+        };
+#pragma unroll
+        for (int m = 0; m < RB_PRE; m++)
+            if (m < a.r) add_row(u[m], m);
+        for (int m = RB_PRE; m < a.r; m++) add_row(*(const uint4 *) (src + (size_t) m * dim), m);
 #pragma unroll
         for (int i = 0; i < 8; i++) x[i] = __fmul_rn(x[i], a.inv_r);
     }
@@ -437,17 +462,14 @@ __global__ __launch_bounds__(RB_WAVES * 64) void k_qsa_pool_rebuild(pool_args a)
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     // rotation: lane -> (block, pair), the wave's blocks in turn
-    const int half = a.rp.n_dims / 2;
-    for (int idx = lane; idx < bpw * half; idx += 64) {
-        const int b = idx / half, k = idx - b * half;
+#pragma unroll
+    for (int q = 0; q < RB_TASKS; q++) {
+        const int idx = lane + 64 * q, b = idx / half, k = idx - b * half;
         const int64_t bk = blk0 + b;
-        if (bk >= a.n_blk) break;   // idx only grows: every later pair is past the end too
-        const int32_t p = (int32_t) (bk * a.r);
-        const int32_t pos[4] = {p, p, p, p};
-        float c, s, y0, y1;
-        rope_cos_sin(a.rp, pos, k, &c, &s);
+        if (idx >= bpw * half || bk >= a.n_blk) break;   // idx only grows: every later task is past the end too
+        float y0, y1;
         const float * xb = xs[wv] + b * dim;
-        rope_rotate(xb[k], xb[k + half], c, s, &y0, &y1);
+        rope_rotate(xb[k], xb[k + half], cq[q], sq4[q], &y0, &y1);
         uint16_t * out = a.pool + (size_t) bk * dim;
         out[k] = f2h(y0);
         out[k + half] = f2h(y1);
