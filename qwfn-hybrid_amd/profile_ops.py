@@ -4,7 +4,7 @@ after one warm-up; nothing else runs on the GPU besides the input set-up.
 
   python3 qwfn-hybrid_amd/profile_ops.py verify --depth 16384 --T 3
   python3 qwfn-hybrid_amd/profile_ops.py prefill --depth 16384
-  python3 qwfn-hybrid_amd/profile_ops.py cells | append | gather | restore | produce | deltanet | pool
+  python3 qwfn-hybrid_amd/profile_ops.py cells | append | gather [--pair] | restore | produce | deltanet | pool
   python3 qwfn-hybrid_amd/profile_ops.py qsaprefill --depth 16384  (QSA-on prefill chunk over cell lists)
   python3 qwfn-hybrid_amd/profile_ops.py copy --mb 1024        (a plain device copy: counter calibration)
 
@@ -34,6 +34,7 @@ def main() -> int:
     ap.add_argument("--mb", type=int, default=1024)
     ap.add_argument("--lib", default=None, help="library path (default: the package's build)")
     ap.add_argument("--append", action="store_true", help="verify: append the T new K/V rows in the same launch")
+    ap.add_argument("--pair", action="store_true", help="gather: the K and the V cache with one index in one launch")
     ap.add_argument("--kernel", choices=["auto", "vd", "vs", "dec", "general"], default="auto",
                     help="attention ops: the kernel family to force (qwfn_fattn_force_kernel)")
     ap.add_argument("--splits", type=int, default=0, help="attention ops: a forced key-split count (0: the planner's)")
@@ -121,7 +122,11 @@ def main() -> int:
         idx = torch.from_numpy(np.stack([np.concatenate([x, np.repeat(x[-1:], mlen - len(x))]) for x in lists])
                                .astype(np.int32)).to(dev)
         gk = torch.zeros((2, mlen, 272), dtype=torch.uint8, device=dev)
-        run = lambda i: K.gather_segments(sets[i % a.sets][i % 2], idx, gk, 0, 272, 272)
+        gv = torch.zeros((2, mlen, 272), dtype=torch.uint8, device=dev)
+        if a.pair:
+            run = lambda i: K.gather_segments_kv(sets[i % a.sets][0], sets[i % a.sets][1], idx, gk, gv, 0, 272, 272)
+        else:
+            run = lambda i: K.gather_segments(sets[i % a.sets][i % 2], idx, gk, 0, 272, 272)
     elif a.op in ("restore", "copy"):
         if a.op == "copy":
             nbytes = [a.mb << 20]
