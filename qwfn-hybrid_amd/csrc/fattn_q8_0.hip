@@ -4869,7 +4869,14 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
     // k_fattn_q8_0: whole chunks.
     const int64_t ck = vd ? DEC_TK : kdec ? DEC_TK
                      : pl->kind == FA_P4_T1 ? fa_cfg<1, false, WAVES_PAIR, 16>::CK : fa_cfg<2, false, WAVES_PAIR, 32>::CK;
-    const int64_t min_split = vd ? DEC_TK * VD_WAVES : kdec ? DEC_TK * (DEC_WAVES / pl->RT) : ck;
+    // (gathered cells with one row tile, T <= 2 at GQA 8: splits down to one
+    // 16-key tile, so that the grid reaches a block per CU although most
+    // waves of a block then idle; shared list, T = 1, kernel + merge: 1024
+    // cells 13.8 -> 12.9 us, 2052 14.1 -> 13.1, 4096 15.0 -> 13.9, 8192 15.6 ->
+    // 14.3. With two row tiles the same grid is slower: 3 x 2052, 64 splits
+    // 22.6 against 16.3 us)
+    const int64_t min_split = vd ? DEC_TK * VD_WAVES
+                            : kdec ? (gather && pl->RT == 1 ? DEC_TK : DEC_TK * (DEC_WAVES / pl->RT)) : ck;
     // Splits: about one block per CU slot (256 for the one-block-per-CU
     // kernels, 512 otherwise).
     const int64_t target_blocks = vd || kdec ? 256 : 512;
