@@ -6,6 +6,7 @@ after one warm-up; nothing else runs on the GPU besides the input set-up.
   python3 qwfn-hybrid_amd/profile_ops.py prefill --depth 16384
   python3 qwfn-hybrid_amd/profile_ops.py cells | append | gather [--pair] | restore | produce | deltanet | pool
   python3 qwfn-hybrid_amd/profile_ops.py qsaprefill --depth 16384  (QSA-on prefill chunk over cell lists)
+  python3 qwfn-hybrid_amd/profile_ops.py qsastep  (QSA-on 3-position verify step of one layer at 73700)
   python3 qwfn-hybrid_amd/profile_ops.py copy --mb 1024        (a plain device copy: counter calibration)
 
 Cache sets are rotated (--sets) so that a repeated launch does not find its
@@ -26,7 +27,7 @@ ROW = 544
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("op", choices=["verify", "prefill", "cells", "append", "gather", "restore", "produce", "deltanet",
-                                   "pool", "select", "qsaprefill", "copy"])
+                                   "pool", "select", "qsaprefill", "qsastep", "copy"])
     ap.add_argument("--depth", type=int, default=16384)
     ap.add_argument("--T", type=int, default=3)
     ap.add_argument("--reps", type=int, default=10)
@@ -205,6 +206,50 @@ def main() -> int:
             S.qsa_visible_cells(cells, n_kv, a.depth, lists, counts)
             K.flash_attn_ext_query_cells_dev(K.q_view(q), views[i % a.sets][0], views[i % a.sets][1], lists, counts,
                                              a.depth, 1 / 16, K.out_view(out))
+    elif a.op == "qsastep":
+        # the reference's default verify step (QSA on) for one attention layer: the 3
+        # positions' inputs and index pooling (one launch), top-513 selection of 18432
+        # blocks for the 3 queries, the K/V producer, the gated per-position cells
+        # attention over 3 lists of 2052 and its merge
+        import qwfn_state as S
+        n_ctx, ratio, nbm, T, kb, E, nh = 73728, 4, 18432, 3, 513, 2560, 24
+        n_past, nc = 73700, kb * 4
+        sets = [(cache(n_ctx), cache(n_ctx)) for _ in range(a.sets)]
+        views = [(K.cache_attn_view(k, n_ctx, 2), K.cache_attn_view(v, n_ctx, 2)) for k, v in sets]
+        ic = torch.randn((n_ctx, 128), generator=gen, device=dev).to(torch.float16)
+        pool = (torch.randn((nbm, 128), generator=gen, device=dev) * 0.5).to(torch.float16)
+        wk = (torch.randn((512, E), generator=gen, device=dev) * 0.02).to(torch.float16)
+        wv = (torch.randn((512, E), generator=gen, device=dev) * 0.02).to(torch.float16)
+        knw = torch.rand(256, generator=gen, device=dev) + 0.5
+        knw_idx = torch.rand(128, generator=gen, device=dev) + 0.5
+        bias = torch.empty((T, nbm), dtype=torch.float32, device=dev)
+        qds = []
+        for t in range(T):
+            qd = S.QsaDecodeInputs(ratio, nbm)
+            qd.bias = bias[t]
+            qds.append(qd)
+        qds[0].rebuild_bias(n_past)
+        blk_cells = torch.empty(nbm * ratio, dtype=torch.int32, device=dev)
+        S.qsa_tables(blk_cells, ratio)
+        k_raw = torch.randn((T, 128), generator=gen, device=dev)
+        q_idx = torch.randn((T, 4, 128), generator=gen, device=dev)
+        cur = torch.randn((T, E), generator=gen, device=dev)
+        pos = torch.arange(n_past, n_past + T, dtype=torch.int32, device=dev).repeat(4)
+        cells = torch.empty((T, nc), dtype=torch.int32, device=dev)
+        wsel = torch.empty(K.load().qwfn_qsa_select_workspace_size(nbm, T), dtype=torch.uint8, device=dev)
+        q = torch.randn((1, T, nh, 256), generator=gen, device=dev)
+        gate = torch.randn((1, T, nh, 256), generator=gen, device=dev)
+        out = torch.empty((1, T, nh, 256), dtype=torch.float32, device=dev)
+        aws = torch.empty(max(256, K.fattn_workspace_size_query_cells(K.q_view(q), views[0][0], views[0][1], [nc] * T, nc)),
+                          dtype=torch.uint8, device=dev)
+
+        def run(i):
+            kc, vc = sets[i % a.sets]
+            S.qsa_decode_prepare_pool_steps(qds, n_past, ic, k_raw, knw_idx, pool)
+            S.qsa_select_cells(pool, q_idx, bias, kb, blk_cells, ratio, cells, ws=wsel)
+            K.kv_produce(cur, wk, wv, knw, pos, kc, vc, n_past)
+            K.flash_attn_ext_query_cells(K.q_view(q), views[i % a.sets][0], views[i % a.sets][1], cells, [nc] * T, n_past,
+                                         1 / 16, K.out_view(out), gate=gate, ws=aws)
     else:  # pool: rebuild after a prefill of `depth` positions, ratio 4
         ic = torch.randn((a.depth + 64, 128), generator=gen, device=dev).to(torch.float16)
         pool = torch.zeros((a.depth // 4 + 16, 128), dtype=torch.float16, device=dev)
