@@ -509,8 +509,16 @@ __device__ __forceinline__ uint64_t bitonic_lane_step(uint64_t v, bool take_max)
                                 : __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
         alo = rl[0]; blo = rl[1]; ahi = rh[0]; bhi = rh[1];
     } else {
-        blo = (uint32_t) __shfl_xor((int) lo, D);
-        bhi = (uint32_t) __shfl_xor((int) hi, D);
+        static_assert(D == 4, "lane strides 1 to 32");
+        // lane ^ 4 within a row of 16: row_ror:12 brings lane + 4 (lanes with
+        // bit 2 clear), row_ror:4 lane - 4 (bit 2 set)
+        const bool up = (threadIdx.x & 4) != 0;
+        const uint32_t l4 = (uint32_t) __builtin_amdgcn_update_dpp(0, (int) lo, 0x124, 0xF, 0xF, false);
+        const uint32_t l12 = (uint32_t) __builtin_amdgcn_update_dpp(0, (int) lo, 0x12C, 0xF, 0xF, false);
+        const uint32_t h4 = (uint32_t) __builtin_amdgcn_update_dpp(0, (int) hi, 0x124, 0xF, 0xF, false);
+        const uint32_t h12 = (uint32_t) __builtin_amdgcn_update_dpp(0, (int) hi, 0x12C, 0xF, 0xF, false);
+        blo = up ? l4 : l12;
+        bhi = up ? h4 : h12;
     }
     const uint64_t a = ((uint64_t) ahi << 32) | alo, b = ((uint64_t) bhi << 32) | blo;
     return (take_max == (a > b)) ? a : b;
