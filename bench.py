@@ -801,7 +801,7 @@ def main() -> int:
                              scale, threads=min(16, len(os.sched_getaffinity(0))))
         parity = KD.err_stats(got, ref)
         log(f"[bench] parity vs oracle (layer 0): max abs {parity[0]:.2e} mean abs {parity[1]:.2e}")
-    except Exception as e:  # the oracle is a checker; never part of the timed work
+    except Exception as e:  # the oracle only checks results; never part of the timed work
         log(f"[bench] parity check skipped: {e}")
 
     stream = torch.cuda.current_stream()
@@ -928,11 +928,11 @@ def main() -> int:
                 t1 = time.perf_counter()
                 KD.oracle_attn(q_h, kc_h, vc_h, n_kv, nh_kv, mask_np, scale, threads=cores, native=True)
                 return time.perf_counter() - t1
-            # the native build computes what the checker build does, bit for bit
+            # the native build computes what the portable build does, bit for bit
             chk = KD.oracle_attn(q_h, kc_h, vc_h, n_kv, nh_kv, mask_np, scale, threads=cores)
             nat = KD.oracle_attn(q_h, kc_h, vc_h, n_kv, nh_kv, mask_np, scale, threads=cores, native=True)
             if not np.array_equal(chk, nat):
-                raise RuntimeError("the -march=native oracle build differs from the checker build")
+                raise RuntimeError("the -march=native oracle build differs from the portable build")
             one(), one()
             times = []
             while len(times) < 10 or (sum(times) < args.cpu_seconds and len(times) < 200):

@@ -1,6 +1,6 @@
 /*
  * CPU oracle for the q8_0 KV-cache path. TEST INFRASTRUCTURE ONLY: loaded by
- * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg as the checker,
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg to check results,
  * never by the product library.
  *
  * Restates ggml-cpu semantics (ggml from unslothai/llama.cpp @ ca1426903, MIT

@@ -1,7 +1,7 @@
 """ctypes binding of the CPU oracle (liboracle.so). TEST INFRASTRUCTURE ONLY.
 
 Only tests/, ``__graft_entry__.smoke()`` and bench.py's cpu_baseline leg import
-this module, and only as the checker. The product library never loads it.
+this module, and only to check results. The product library never loads it.
 
 The C sources restate ggml-cpu semantics for the q8_0 KV-cache path; see the
 header of oracle.c for the ggml functions and reference call sites they follow.

@@ -105,7 +105,7 @@ def test_m0_only_in_dma_asm(fattn_asm):
 
 
 def test_scan_finds_a_split_carry():
-    """The checker itself: a 64-bit add split around an SCC-writing asm block is found."""
+    """The scan itself: a 64-bit add split around an SCC-writing asm block is found."""
     lines = ["\ts_add_u32 s16, s16, s18", "\t;;#ASMSTART", "\ts_add_u32 m0, s47, 0x1900",
              "\tbuffer_load_dwordx4 v150, s[4:7], 0 offen lds", "\t;;#ASMEND", "\ts_addc_u32 s17, s17, s19"]
     assert len(scc_carried_across(lines, asm_blocks(lines))) == 1
