@@ -141,6 +141,11 @@ struct fa_args {
     int32_t  m_gran;       // MASK_SPLIT: 16-byte granules per mask row of a split (split_len / 8 + 1)
     uint32_t m_gran_mul;   // ceil(2^32 / m_gran)
     uint32_t ns_mul, hgn_mul, nrg_mul;   // ceil(2^32 / d) for ns, nh_kv * n_rg, n_rg
+    // k_fa_pre block order: 0 puts the row groups of a (batch, KV head,
+    // split) unit on one XCD (they share its K/V rows), 1 puts the splits of
+    // a (batch, KV head, row group) on one XCD (they share its query rows)
+    int32_t  pre_rgmap;
+    uint32_t nbh_mul;      // ceil(2^32 / (B * nh_kv))
     // fused append (app_n > 0): F32 rows [nh_kv * D] of K and V quantised into
     // cache rows app_row0 .. app_row0 + app_n - 1 before they are attended
     const char * app_k;
@@ -1237,8 +1242,10 @@ __global__ __launch_bounds__(256) void k_fattn_merge(fa_args a) {
 }
 
 // LSE merge for many query rows over few splits (k_fa_pre's key splits, at
-// most MERGE_ROWS_SPLITS): one 64-lane group per row, a lane per 4 dims; all
-// of a lane's partials and (max, sum) pairs are loaded before any is used.
+// most MERGE_ROWS_SPLITS): one 64-lane group (one wave) per row, a lane per 4
+// dims. The (max, sum) pairs are loaded first; a split in which the row saw
+// no key (max -inf) has no O partial (k_fa_pre does not write it), so only
+// the live splits' partials are loaded, all before any is used.
 constexpr int MERGE_ROWS_SPLITS = 16;
 
 __global__ __launch_bounds__(256) void k_fattn_merge_rows(fa_args a) {
@@ -1254,15 +1261,10 @@ __global__ __launch_bounds__(256) void k_fattn_merge_rows(fa_args a) {
     float2 e[MERGE_ROWS_SPLITS];
     float4 o[MERGE_ROWS_SPLITS];
 #pragma unroll
-    for (int s = 0; s < MERGE_ROWS_SPLITS; s++) {
-        if (s < a.ns) {
-            e[s] = ml[(size_t) s * a.R];
-            o[s] = load_nt4(po + (size_t) s * sstride);
-        } else {
-            e[s] = make_float2(-INFINITY, 0.f);
-            o[s] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    }
+    for (int s = 0; s < MERGE_ROWS_SPLITS; s++) e[s] = s < a.ns ? ml[(size_t) s * a.R] : make_float2(-INFINITY, 0.f);
+#pragma unroll
+    for (int s = 0; s < MERGE_ROWS_SPLITS; s++)
+        o[s] = e[s].x != -INFINITY ? load_nt4(po + (size_t) s * sstride) : make_float4(0.f, 0.f, 0.f, 0.f);
     float M = -INFINITY;
 #pragma unroll
     for (int s = 0; s < MERGE_ROWS_SPLITS; s++) M = xmax(M, e[s].x);
@@ -4130,17 +4132,30 @@ __global__ __launch_bounds__(PRE_WAVES * 64, 2) void k_fa_pre(fa_args a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int ln = lane & 15, lg = lane >> 4;
 
-    // ---- block -> (unit = (b, kvh, split), row group): the n_rg row groups of a
-    //      unit are blocks x, x + 8, ... of one XCD x ----
+    // ---- block -> (b, kvh, split, row group), blocks x, x + 8, ... on XCD x.
+    //      pre_rgmap 0: unit (b, kvh, split) = x + 8 u, its n_rg row groups
+    //      consecutive; 1: row group unit (rg, b, kvh) = x + 8 u (bh fastest, so
+    //      an XCD holds one KV head when B * nh_kv divides 8), its ns splits
+    //      consecutive ----
     const int id = blockIdx.x;
     const int xcd = id & 7, j = id >> 3;
-    const int ul = (int) udiv((uint32_t) j, (uint32_t) a.n_rg, a.nrg_mul);
-    const int rg = j - ul * a.n_rg;
-    const int unit = xcd + 8 * ul;
-    const int n_units = a.B * a.nh_kv * a.ns;
-    if (unit >= n_units) return;
-    const int bh = (int) udiv((uint32_t) unit, (uint32_t) a.ns, a.ns_mul);
-    const int split = unit - bh * a.ns;
+    const int nbh = a.B * a.nh_kv;
+    int bh, split, rg;
+    if (a.pre_rgmap) {
+        const int ul = (int) udiv((uint32_t) j, (uint32_t) a.ns, a.ns_mul);
+        split = j - ul * a.ns;
+        const int rgu = xcd + 8 * ul;
+        if (rgu >= nbh * a.n_rg) return;
+        rg = (int) udiv((uint32_t) rgu, (uint32_t) nbh, a.nbh_mul);
+        bh = rgu - rg * nbh;
+    } else {
+        const int ul = (int) udiv((uint32_t) j, (uint32_t) a.n_rg, a.nrg_mul);
+        rg = j - ul * a.n_rg;
+        const int unit = xcd + 8 * ul;
+        if (unit >= nbh * a.ns) return;
+        bh = (int) udiv((uint32_t) unit, (uint32_t) a.ns, a.ns_mul);
+        split = unit - bh * a.ns;
+    }
     const int b = bh / a.nh_kv, kvh = bh - b * a.nh_kv;
     const int64_t k_lo = (int64_t) split * a.split_len;
     const int64_t k_e = k_lo + a.split_len;
@@ -4573,6 +4588,11 @@ __global__ __launch_bounds__(PRE_WAVES * 64, 2) void k_fa_pre(fa_args a) {
             __builtin_nontemporal_store(m_run, &mlp->x);
             __builtin_nontemporal_store(L, &mlp->y);
         }
+        // a row that saw no key of this split (a causal split above its
+        // diagonal) leaves its O partial unwritten: k_fattn_merge_rows loads
+        // only the partials whose max is finite (k_fattn_merge, for more
+        // splits, reads them all)
+        if (m_run == -INFINITY && a.ns <= MERGE_ROWS_SPLITS) return;
     }
 #pragma unroll
     for (int bb = 0; bb < NBLK; bb++) {
@@ -4607,6 +4627,7 @@ enum fa_kind {
 struct fa_plan {
     int32_t R, RT, gqa, rw, n_rg, ns, split_len;
     int32_t max_span;                 // keys of the longest split, whole chunks
+    int32_t pre_rgmap;                // k_fa_pre block order (fa_args::pre_rgmap)
     fa_kind kind;
     size_t  off_ml;                   // workspace section of the split (max, sum) pairs (bytes)
     size_t  ws_bytes;
@@ -4850,6 +4871,13 @@ int plan_fattn(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor *
         pl->split_len = (int32_t) split_len;
         pl->max_span = split_len;
         pl->ragged = 0;
+        // block order: the bytes an XCD's L2 cannot share. Units on an XCD read
+        // each KV head's f32 query rows once per split; row groups on an XCD
+        // (one KV head an XCD) read its K/V rows once per XCD holding its rows
+        const int64_t nbh = B * nh_kv;
+        const double q_rep = (double) R * D * 4 * (double) (ns - 1);
+        const double kv_rep = (double) n_kv * (2.0 * (D / 32) * 34) * (double) (std::max<int64_t>(1, 8 / nbh) - 1);
+        pl->pre_rgmap = ns > 1 && q_rep > kv_rep ? 1 : 0;
         const size_t n_part = ns > 1 ? (size_t) (B * nh_kv * ns * R) : 0;
         size_t off = align256(n_part * D * sizeof(float));
         pl->off_ml = off;
@@ -5193,6 +5221,7 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
     a.gqa = pl.gqa; a.R = pl.R; a.B = (int32_t) q->ne[3];
     a.kb = (int32_t) k->ne[3]; a.vb = (int32_t) v->ne[3];
     a.ns = pl.ns; a.split_len = pl.split_len; a.rw = pl.rw; a.n_rg = pl.n_rg;
+    a.pre_rgmap = pl.kind == FA_PRE ? pl.pre_rgmap : 0;
     a.ragged = pl.ragged;
     if (pl.ragged) {
         for (int b = 0; b <= a.B; b++) a.r_ustart[b] = pl.r_ustart[b];
@@ -5237,11 +5266,13 @@ int fattn_run(const qwfn_tensor * q, const qwfn_tensor * k, const qwfn_tensor * 
 
     if (pl.kind == FA_PRE) {
         const int64_t units = (int64_t) a.B * a.nh_kv * a.ns;
-        const int64_t grid = 8 * (int64_t) a.n_rg * ((units + 7) / 8);
+        const int64_t rgus = (int64_t) a.B * a.nh_kv * a.n_rg;
+        const int64_t grid = a.pre_rgmap ? 8 * (int64_t) a.ns * ((rgus + 7) / 8) : 8 * (int64_t) a.n_rg * ((units + 7) / 8);
         if (grid >= (int64_t(1) << 31) || grid * a.n_rg >= (int64_t(1) << 32) || units * a.ns >= (int64_t(1) << 32))
             return set_error(QWFN_ENOTSUP, "flash_attn_ext: grid too large");
         a.ns_mul = recip32(a.ns);
         a.nrg_mul = recip32(a.n_rg);
+        a.nbh_mul = recip32(a.B * a.nh_kv);
         const dim3 g((unsigned) grid), bd(PRE_WAVES * 64);
         if (a.mask) QWFN_FA_LAUNCH(g, bd, as_stream(stream), k_fa_pre<true>);
         else        QWFN_FA_LAUNCH(g, bd, as_stream(stream), k_fa_pre<false>);
