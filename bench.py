@@ -609,7 +609,7 @@ def measure_rows(K, torch, np, dev, gen) -> dict:
         pout = torch.zeros((1, T, nh, hd), dtype=torch.float32, device=dev)
         pk, pv, pmv = K.cache_attn_view(kc, n_kv, nh_kv), K.cache_attn_view(vc, n_kv, nh_kv), K.mask_view(pmask)
         pws = torch.empty(max(256, K.fattn_workspace_size(K.q_view(pq), pk, pv, pmv)), dtype=torch.uint8, device=dev)
-        us = timed(torch, lambda k: K.flash_attn_ext(K.q_view(pq), pk, pv, pmv, 1 / 16, K.out_view(pout), ws=pws), 5)
+        us = timed(torch, lambda k: K.flash_attn_ext(K.q_view(pq), pk, pv, pmv, 1 / 16, K.out_view(pout), ws=pws), 20)
         flops = 4 * nh * hd * (T * d0 + T * (T + 1) // 2)      # causal count, QK^T and PV
         rows[f"prefill_512_at_{d0}"] = {"us_per_launch": round(us, 1), "flops": flops,
                                         "TFLOPs": round(flops / (us * 1e-6) / 1e12, 2),
